@@ -1,0 +1,138 @@
+/* linuxformer on MI355X: the chip layers' persistent greedy-decode kernel, C ABI.
+ *
+ * The drop-in boundary for lx.mega's native library. The reference binds its CUDA library with
+ * ctypes (lx/lx/mk_build.py:40-57, lx/lx/mega.py:202) and calls five entry points
+ * (lx/csrc/mega.cu:864-893); each has a counterpart here with the same role and error
+ * convention (a hipError_t returned as int, 0 on success). All buffers belong to the caller
+ * (torch tensors on the Python side); the library allocates nothing.
+ *
+ * Entry formats in the packed tables ("e4", always for bf16 models, and for fp32 models whose
+ * packed values are all exact in bf16): one uint32, index (16 bits) | bf16 value bits << 16,
+ * norm weights as their bf16 bits; otherwise two uint32, index then the float's bits, norm
+ * weights as 1 + w in fp32.
+ */
+#ifndef LXM_H
+#define LXM_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define LXM_NT 512          /* threads per workgroup */
+#define LXM_MAXH 4096       /* hidden size limit */
+#define LXM_KD 256          /* key head dim (the chip's, and the padded text layers') */
+#define LXM_VD 128          /* value head dim */
+#define LXM_RMAX 8          /* value heads per key head */
+#define LXM_MAXU 2048       /* MLP units per layer */
+#define LXM_MAXQK 1024      /* live query/key channels, all layers */
+#define LXM_MAXQKL 512      /* live query/key channels of one layer */
+#define LXM_MAXDEC 512      /* decaying value heads of one layer */
+#define LXM_HOT_MAX 65536   /* bytes of one layer's resident tables */
+#define LXM_NSYNC 256       /* uint32 words of the sync area */
+
+/* One layer's resident tables (the "hot" blob the chain workgroup stages in LDS). All offsets
+   are bytes from the start of the hot blob, 16-byte aligned. */
+typedef struct lxm_hot {
+  int32_t n_units, n_qk, n_dec, qk_base; /* qk_base: the layer's first q/k history slot */
+  int32_t w1_in, w1_post;  /* norm weights: e4 raw w (bf16 bits, uint16), else 1 + w (fp32) */
+  int32_t unit;            /* uint32 per unit: entry start (16 bits) | gate count (8) | up (8) */
+  int32_t gu_ent;          /* gate then up entries of each unit (column) */
+  int32_t down_ptr;        /* uint16 per residual row + 1: down entries of the row */
+  int32_t down_ent;        /* entries (unit) */
+  int32_t qk;              /* lxm_qkc[n_qk] */
+  int32_t dec;             /* lxm_dec[n_dec] */
+  int32_t ent;             /* entries of the q/k and decay rows (column) */
+  int32_t size;            /* bytes */
+  float eps, geps;
+} lxm_hot;
+
+typedef struct lxm_qkc {   /* a live query/key channel (its conv taps are not all zero) */
+  int32_t slot;            /* key head * 512 + (0 query | 256 key) + position */
+  int32_t chan;            /* conv channel */
+  int32_t start, len;      /* in_proj_qkv row: entries in the hot blob */
+  float taps[4];
+} lxm_qkc;
+
+typedef struct lxm_dec {   /* a value head whose decay can be nonzero */
+  int32_t vh, start, len;  /* in_proj_a row: entries in the hot blob */
+  float dt_bias, A_log;
+  int32_t pad[3];
+} lxm_dec;
+
+typedef struct lxm_chan {  /* a conv channel: in_proj_qkv row (cold entries) and taps */
+  int32_t start, len;
+  float taps[4];
+} lxm_chan;
+
+typedef struct lxm_row { int32_t start, len; } lxm_row;
+
+/* One layer: byte offsets into the packed blob. */
+typedef struct lxm_layer {
+  int64_t hot;             /* lxm_hot + its tables, hot.size bytes */
+  int64_t chan;            /* lxm_chan[n_conv] */
+  int64_t qkv_ent;         /* entries (column) */
+  int64_t b_row, b_ent;    /* lxm_row[nv], entries (column) */
+  int64_t z_row, z_ent;    /* lxm_row[nv * vd], entries (column) */
+  int64_t out_ptr;         /* per key head int32[hidden + 1] (nk of them) */
+  int64_t out_ent;         /* entries (dim within the key head's value dims) */
+  int64_t gnorm;           /* float[vd] */
+} lxm_layer;
+
+typedef struct lxm_params {
+  int32_t hidden, n_layers, nk, kd, nv, vd, n_conv, vocab, bf16, n_blocks;
+  float rms_eps;
+  int32_t head_lds;        /* bytes of head tables a helper workgroup stages */
+  int32_t e4, pad1;        /* the entry format (above) */
+  const lxm_layer* layers; /* device, n_layers */
+  const uint8_t* blob;     /* device */
+  float* const* rec;       /* device array of n_layers pointers: (nv, kd, vd) float */
+  void* const* conv;       /* device array of n_layers pointers: (n_conv, 4) model dtype */
+  const int64_t* emb_ptr;  /* (vocab + 1): the embedding rows (all columns) */
+  const uint32_t* emb_ent;
+  const float* w1_final;   /* (hidden): 1 + the final norm's weight */
+  const int32_t* head_rows;/* (n_blocks + 1): block b's vocabulary rows */
+  const int64_t* head_ptr; /* (vocab + 1): head entries (columns with nonzero final weight) */
+  const uint32_t* head_ent;
+  const int32_t* forced;
+  int32_t n_forced, n_tokens;
+  int32_t* preds;          /* (n_tokens) */
+  int32_t* inputs;         /* (n_tokens) or null: each step's input as embedded */
+  float* trace;            /* (n_tokens, n_layers, hidden) or null: residual after each layer */
+  float* ring;             /* (4, n_layers, hidden): recent GDN norm outputs */
+  float* hn;               /* (hidden): the head's normed input, chain -> helpers */
+  uint32_t* sync;          /* LXM_NSYNC words, zero at launch */
+  unsigned long long* keys;/* (2), zero at launch */
+  int32_t* err;            /* (1), zero at launch; nonzero: a spin timed out (1..) */
+  int32_t n_qk_total, pad;
+} lxm_params;
+
+/* mk_run (lx/csrc/mega.cu:867-874): launch the persistent decode, cooperatively, n_blocks
+   workgroups of LXM_NT threads with lds_bytes of LDS each, on stream (a hipStream_t). p_host
+   is the parameter block in host memory, p_dev the same bytes in device memory (the kernel
+   reads its parameters from there). Returns a hipError_t. */
+int lxm_run(const lxm_params* p_host, const lxm_params* p_dev, int n_blocks, int lds_bytes,
+            void* stream);
+/* mk_smem_base (mega.cu:865): LDS bytes the kernel needs besides the staged head tables. */
+int lxm_lds_base(void);
+/* mk_max_ctas (mega.cu:876-883): co-resident workgroups at lds_bytes (occupancy x CUs). */
+int lxm_max_blocks(int lds_bytes);
+/* mk_max_smem (mega.cu:885-890): LDS bytes a workgroup may use. */
+int lxm_max_lds(void);
+/* mk_last_error (mega.cu:892). */
+int lxm_last_error(void);
+/* the device's compute units */
+int lxm_device_cus(void);
+
+/* Test exports (mk_test.cu:136-160's roles): the kernels' own arithmetic on device arrays.
+   fn: 0 exp, 1 silu, 2 sigmoid, 3 softplus, 4 rsqrt, 5 log1p, 6 bf16 rounding. */
+int lxm_t_elem(int fn, const float* x, float* y, long n, void* stream);
+/* kind 0: the 512-lane hidden sum, kind 1: the 64-lane head sum, of each of rows rows of n
+   values (x row-major); out (rows). */
+int lxm_t_sum(int kind, const float* x, int n, int rows, float* out, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

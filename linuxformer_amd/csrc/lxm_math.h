@@ -1,0 +1,123 @@
+// The decode's float arithmetic on gfx950, one rounding at a time.
+//
+// Every op is a single IEEE binary32 op rounded to nearest even; the library is built with
+// -ffp-contract=off, so a*b+c is never fused, and without fast-math, so nothing is reordered;
+// f32 division and sqrt are the correctly rounded sequences (clang's HIP default). exp and
+// log1p are evaluated in binary64 and rounded once to binary32: exp by a Cody-Waite reduction
+// with ln 2 split in two and a degree-13 Taylor polynomial for exp(r), |r| <= ln2/2; log by
+// f in [sqrt(1/2), sqrt(2)] and the series 2 atanh(s) = 2 (s + s^3/3 + ... + s^23/23). The
+// compositions silu(x) = x / (1 + exp(-x)), sigmoid(x) = 1 / (1 + exp(-x)),
+// softplus(x) = x > 20 ? x : log1p(exp(x)) and rsqrt(x) = 1 / sqrt(x) are those of ATen's CPU
+// kernels for torch.nn.functional.silu/sigmoid/softplus and torch.rsqrt, which the stock
+// forward (transformers/models/qwen3_5/modeling_qwen3_5.py:168-184, :242-245, :497-499,
+// :727) calls; the results agree with ATen's on every bf16 input.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace lxm {
+
+__device__ __forceinline__ float bitsf(uint32_t u) { return __uint_as_float(u); }
+__device__ __forceinline__ uint32_t fbits(float x) { return __float_as_uint(x); }
+
+// round to bf16, nearest even (NaN -> 0x7fc0, as c10::BFloat16); returned widened to f32
+__device__ __forceinline__ float bf16r(float x) {
+  uint32_t u = fbits(x);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return bitsf(0x7fc00000u);
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return bitsf(u & 0xffff0000u);
+}
+__device__ __forceinline__ float bf16f(uint32_t hi16) { return bitsf(hi16 << 16); }
+
+// the model dtype's rounding
+template <bool BF>
+__device__ __forceinline__ float rd(float x) {
+  if constexpr (BF) return bf16r(x);
+  else return x;
+}
+
+__device__ __forceinline__ double pow2i(int k) {
+  return __longlong_as_double((long long)(k + 1023) << 52);
+}
+
+__device__ __forceinline__ float cr_exp(float x) {
+  if (x != x) return x;
+  if (x > 89.0f) return __builtin_inff();
+  if (x < -110.0f) return 0.0f;
+  const double xd = (double)x;
+  const double kd = __builtin_floor(xd * 0x1.71547652b82fep+0 + 0.5);
+  const double r = (xd - kd * 0x1.62e42fee00000p-1) - kd * 0x1.a39ef35793c76p-33;
+  double p = 0x1.6124613a86d09p-33;
+  p = p * r + 0x1.1eed8eff8d898p-29;
+  p = p * r + 0x1.ae64567f544e4p-26;
+  p = p * r + 0x1.27e4fb7789f5cp-22;
+  p = p * r + 0x1.71de3a556c734p-19;
+  p = p * r + 0x1.a01a01a01a01ap-16;
+  p = p * r + 0x1.a01a01a01a01ap-13;
+  p = p * r + 0x1.6c16c16c16c17p-10;
+  p = p * r + 0x1.1111111111111p-7;
+  p = p * r + 0x1.5555555555555p-5;
+  p = p * r + 0x1.5555555555555p-3;
+  p = p * r + 0x1.0000000000000p-1;
+  p = p * r + 1.0;
+  p = p * r + 1.0;
+  return (float)(p * pow2i((int)kd));
+}
+
+__device__ __forceinline__ double log_ge1(double u) {
+  long long b = __double_as_longlong(u);
+  int m = (int)((b >> 52) & 0x7ff) - 1023;
+  double f = __longlong_as_double((b & 0x000fffffffffffffll) | 0x3ff0000000000000ll);
+  if (f > 0x1.6a09e667f3bcdp+0) {
+    f = f * 0.5;
+    m += 1;
+  }
+  const double s = (f - 1.0) / (f + 1.0);
+  const double s2 = s * s;
+  double p = 0x1.642c8590b2164p-5;
+  p = p * s2 + 0x1.8618618618618p-5;
+  p = p * s2 + 0x1.af286bca1af28p-5;
+  p = p * s2 + 0x1.e1e1e1e1e1e1ep-5;
+  p = p * s2 + 0x1.1111111111111p-4;
+  p = p * s2 + 0x1.3b13b13b13b14p-4;
+  p = p * s2 + 0x1.745d1745d1746p-4;
+  p = p * s2 + 0x1.c71c71c71c71cp-4;
+  p = p * s2 + 0x1.2492492492492p-3;
+  p = p * s2 + 0x1.999999999999ap-3;
+  p = p * s2 + 0x1.5555555555555p-2;
+  p = p * s2 + 1.0;
+  const double lf = (2.0 * s) * p;
+  return (double)m * 0x1.62e42fee00000p-1 + ((double)m * 0x1.a39ef35793c76p-33 + lf);
+}
+
+// log1p(y), y >= 0
+__device__ __forceinline__ float cr_log1p(float y) {
+  if (y != y) return y;
+  if (y == __builtin_inff()) return y;
+  const double yd = (double)y;
+  if (yd < 0x1p-29) return (float)(yd - (yd * yd) * 0.5);
+  return (float)log_ge1(1.0 + yd);
+}
+
+__device__ __forceinline__ float silu(float x) { return x / (1.0f + cr_exp(-x)); }
+__device__ __forceinline__ float sigmoid(float x) { return 1.0f / (1.0f + cr_exp(-x)); }
+__device__ __forceinline__ float softplus(float x) { return x > 20.0f ? x : cr_log1p(cr_exp(x)); }
+__device__ __forceinline__ float rsqrt_(float x) { return 1.0f / __builtin_sqrtf(x); }
+
+// (value, index) -> one key whose unsigned maximum is torch.argmax's pick: the larger value,
+// then the lower index; NaN above everything; -0 counted as +0
+__device__ __forceinline__ unsigned long long argmax_key(float v, int idx) {
+  uint32_t u = fbits(v);
+  uint32_t o;
+  if ((u & 0x7fffffffu) > 0x7f800000u) o = 0xffffffffu;
+  else {
+    if ((u & 0x7fffffffu) == 0) u = 0;
+    o = (u >> 31) ? ~u : (u | 0x80000000u);
+  }
+  return ((unsigned long long)o << 32) | (unsigned long long)(0xffffffffu - (uint32_t)idx);
+}
+__device__ __forceinline__ int argmax_idx(unsigned long long key) {
+  return (int)(0xffffffffu - (uint32_t)(key & 0xffffffffull));
+}
+
+}  // namespace lxm

@@ -1,0 +1,97 @@
+"""The chip layers without the zeros (lx/lx/fast.py's role): which rows, columns, units and heads
+of the checkpoint tensors are live, and the tables the decode kernel is packed from.
+
+    f = Fast(model, n_chip, rows)    # model: a transformers Qwen3_5ForCausalLM, or a SparseModel
+    m = Mega(f, model, cache, offset)
+
+What is skipped, and why that changes nothing (lx/lx/fast.py:8-19): weight rows and columns that
+are all zero (a dead output is exactly 0, a dead input contributes exactly 0), MLP units whose
+gate row, up row or down column is zero (lx/lx/fast.py:242-248), head columns the final norm
+zeroes, and key heads whose query, key and decay are all zero at a step (their state stays as it
+is and their output is exactly 0).
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import torch
+
+from . import synth
+
+
+class Rows:
+    """CSR rows (ptr, cols, vals) of a Coo's row range."""
+
+    def __init__(self, coo, lo: int = 0, hi: int | None = None):
+        hi = coo.shape[0] if hi is None else hi
+        sel = (coo.rows >= lo) & (coo.rows < hi)
+        rows, self.cols, self.vals = coo.rows[sel] - lo, coo.cols[sel], coo.vals[sel]
+        self.n = hi - lo
+        self.ptr = np.zeros(self.n + 1, np.int64)
+        np.cumsum(np.bincount(rows, minlength=self.n), out=self.ptr[1:])
+
+
+class Fast:
+    """lx.fast.Fast (lx/lx/fast.py:172-185): built once from the model's tensors."""
+
+    def __init__(self, model, n_chip: int | None = None, rows: slice | None = None):
+        self.model = model
+        self.sm = model if isinstance(model, synth.SparseModel) else synth.from_hf(model, n_chip)
+        d = self.sm.dims
+        self.n_chip = d.n_layers
+        self.nk, self.nv, self.kd, self.vd = d.nk, d.nv, d.kd, d.vd
+        self.r = d.nv // d.nk
+        self.rows = rows
+        lo = 0 if rows is None else (rows.start or 0)
+        hi = d.vocab if rows is None or rows.stop is None else rows.stop
+        self.head_range = (lo, hi)
+        w1 = np.float32(1.0) + np.asarray(self.sm.norm, np.float32)
+        self.head_cols = np.nonzero(w1 != 0)[0]
+        self.dec = [self._live(L) for L in range(self.n_chip)]
+
+    def _live(self, L: int) -> dict:
+        """A layer's live parts (lx/lx/fast.py:187-248): key heads with a live query or key
+        channel, value heads that can decay, MLP units, out_proj rows."""
+        ly, d = self.sm.layers[L], self.sm.dims
+        taps = np.asarray(ly.conv1d)
+        live = (taps != 0).any(1)
+        nq = d.nk * d.kd
+        kh = np.nonzero(live[:nq].reshape(d.nk, d.kd).any(1) |
+                        live[nq:2 * nq].reshape(d.nk, d.kd).any(1))[0]
+        g = np.bincount(ly.gate_proj.rows, minlength=d.inter) > 0
+        u = np.bincount(ly.up_proj.rows, minlength=d.inter) > 0
+        dn = np.bincount(ly.down_proj.cols, minlength=d.inter) > 0
+        return {"kh": kh, "units": np.nonzero(g & u & dn)[0],
+                "decays": np.unique(ly.in_proj_a.rows),
+                "out_rows": np.unique(ly.out_proj.rows)}
+
+    def embed_rows(self, offset: int = 0) -> Rows:
+        """The embedding rows of chip tokens offset .. offset + vocab (all columns)."""
+        lo, hi = self.head_range
+        return Rows(self.sm.embed, offset + lo if self.rows is None else lo,
+                    (offset + hi) if self.rows is None else hi)
+
+
+class _CacheLayer:
+    def __init__(self, conv: torch.Tensor, rec: torch.Tensor):
+        self.conv_states = {0: conv}
+        self.recurrent_states = {0: rec}
+
+
+class StateCache:
+    """The chip layers' states in transformers' LinearAttentionLayer layout
+    (transformers/cache_utils.py:998-1080): layers[L].conv_states[0] (1, n_conv, 4) in the model
+    dtype, layers[L].recurrent_states[0] (1, nv, kd, vd) float32."""
+
+    def __init__(self, conv: np.ndarray, rec: np.ndarray, dtype: str, device):
+        dt = torch.bfloat16 if dtype == "bf16" else torch.float32
+        self.layers = [
+            _CacheLayer(torch.from_numpy(np.ascontiguousarray(conv[L]))[None].to(device=device, dtype=dt),
+                        torch.from_numpy(np.ascontiguousarray(rec[L]))[None].to(device=device))
+            for L in range(conv.shape[0])]
+
+    def conv_numpy(self) -> np.ndarray:
+        return np.stack([l.conv_states[0][0].float().cpu().numpy() for l in self.layers])
+
+    def rec_numpy(self) -> np.ndarray:
+        return np.stack([l.recurrent_states[0][0].cpu().numpy() for l in self.layers])

@@ -1,0 +1,427 @@
+"""The chip layers' decode as one persistent HIP kernel (csrc/lxm_decode.hip) on MI355X.
+
+The drop-in for lx.mega (lx/lx/mega.py): the same class, constructor and ``run`` signature,
+the same cache tensors updated in place, the same predictions.
+
+    m = Mega(fast, model, cache, offset)
+    preds = m.run(forced, n)   # n steps: inputs forced[0..], then each step's own prediction
+
+The packer here turns the model's sparse tensors (from ``Fast``) into one byte blob of tables the
+kernel reads: per layer a "hot" blob (norm weights, MLP rows, the gates' query/key/decay rows)
+that the chain workgroup streams into LDS one layer ahead, and "cold" tables (value rows, z,
+beta, out_proj by residual row, per key head) read only when a head is active; the head's rows
+split over the helper workgroups, each staging its own in LDS.
+"""
+
+from __future__ import annotations
+
+import ctypes
+
+import numpy as np
+import torch
+
+from . import mk_build
+
+NT, MAXH, KD, VD, RMAX = 512, 4096, 256, 128, 8
+MAXU, MAXQK, MAXQKL, MAXDEC, HOT_MAX, NSYNC = 2048, 1024, 512, 512, 65536, 256
+
+I32, I64, F32, PTR = ctypes.c_int32, ctypes.c_int64, ctypes.c_float, ctypes.c_void_p
+
+
+class Hot(ctypes.Structure):
+    _fields_ = [(n, I32) for n in ("n_units", "n_qk", "n_dec", "qk_base", "w1_in", "w1_post",
+                                   "unit", "gu_ent", "down_ptr", "down_ent", "qk", "dec", "ent",
+                                   "size")] + [("eps", F32), ("geps", F32)]
+
+
+class QkC(ctypes.Structure):
+    _fields_ = [("slot", I32), ("chan", I32), ("start", I32), ("len", I32), ("taps", F32 * 4)]
+
+
+class Dec(ctypes.Structure):
+    _fields_ = [("vh", I32), ("start", I32), ("len", I32), ("dt_bias", F32), ("A_log", F32),
+                ("pad", I32 * 3)]
+
+
+class Chan(ctypes.Structure):
+    _fields_ = [("start", I32), ("len", I32), ("taps", F32 * 4)]
+
+
+class LayerDesc(ctypes.Structure):
+    _fields_ = [(n, I64) for n in ("hot", "chan", "qkv_ent", "b_row", "b_ent", "z_row", "z_ent",
+                                   "out_ptr", "out_ent", "gnorm")]
+
+
+class Params(ctypes.Structure):
+    _fields_ = [(n, I32) for n in ("hidden", "n_layers", "nk", "kd", "nv", "vd", "n_conv",
+                                   "vocab", "bf16", "n_blocks")] + \
+        [("rms_eps", F32), ("head_lds", I32), ("e4", I32), ("pad1", I32)] + \
+        [(n, PTR) for n in ("layers", "blob", "rec", "conv", "emb_ptr", "emb_ent", "w1_final",
+                            "head_rows", "head_ptr", "head_ent", "forced")] + \
+        [("n_forced", I32), ("n_tokens", I32)] + \
+        [(n, PTR) for n in ("preds", "inputs", "trace", "ring", "hn", "sync", "keys", "err")] + \
+        [("n_qk_total", I32), ("pad", I32)]
+
+
+assert ctypes.sizeof(Hot) == 64 and ctypes.sizeof(QkC) == 32 and ctypes.sizeof(Dec) == 32
+assert ctypes.sizeof(Chan) == 24 and ctypes.sizeof(LayerDesc) == 80
+
+
+def _bf16_bits(v: np.ndarray) -> np.ndarray:
+    """float32 values exactly representable in bf16 -> their 16 bits (uint32)."""
+    u = np.ascontiguousarray(v, np.float32).view(np.uint32)
+    assert np.all((u & 0xffff) == 0), "a value is not exact in bf16"
+    return u >> 16
+
+
+class _Blob:
+    """A growing byte buffer with 16-byte aligned sections."""
+
+    def __init__(self):
+        self.parts, self.n = [], 0
+
+    def add(self, b: bytes) -> int:
+        off = self.n
+        b = bytes(b)
+        pad = -len(b) % 16
+        self.parts.append(b + bytes(pad))
+        self.n += len(b) + pad
+        return off
+
+    def bytes(self) -> bytes:
+        return b"".join(self.parts)
+
+
+class _Csr:
+    """Rows of a Coo (sorted by row, then column): ptr, cols, vals."""
+
+    def __init__(self, coo, keep_rows=None):
+        rows, cols, vals = coo.rows, coo.cols, coo.vals
+        self.n = coo.shape[0]
+        self.ptr = np.zeros(self.n + 1, np.int64)
+        np.cumsum(np.bincount(rows, minlength=self.n), out=self.ptr[1:])
+        self.cols, self.vals = cols, vals
+
+    def row(self, r):
+        a, b = self.ptr[r], self.ptr[r + 1]
+        return self.cols[a:b], self.vals[a:b]
+
+    def count(self, r):
+        return int(self.ptr[r + 1] - self.ptr[r])
+
+
+def _bf16_exact(v) -> bool:
+    return bool(np.all((np.ascontiguousarray(v, np.float32).view(np.uint32) & 0xffff) == 0))
+
+
+def model_e4(sm) -> bool:
+    """Whether every value the packer stores is exact in bf16 (the 4-byte entry format)."""
+    if sm.dims.dtype == "bf16":
+        return True
+    for ly in sm.layers:
+        for c in (ly.in_proj_qkv, ly.in_proj_z, ly.in_proj_b, ly.in_proj_a, ly.out_proj,
+                  ly.gate_proj, ly.up_proj, ly.down_proj):
+            if not _bf16_exact(c.vals):
+                return False
+        if not (_bf16_exact(ly.input_layernorm) and _bf16_exact(ly.post_attention_layernorm)):
+            return False
+    return _bf16_exact(sm.embed.vals)
+
+
+class Packer:
+    def __init__(self, e4: bool):
+        self.bf16 = e4
+
+    def ent(self, idx: np.ndarray, vals: np.ndarray) -> bytes:
+        """Entries: e4 one uint32 (index | bf16 << 16), else two uint32 (index, float)."""
+        idx = np.asarray(idx, np.int64)
+        if self.bf16:
+            assert len(idx) == 0 or idx.max() < 1 << 16
+            return (idx.astype(np.uint32) | (_bf16_bits(vals) << 16)).astype(np.uint32).tobytes()
+        out = np.empty((len(idx), 2), np.uint32)
+        out[:, 0] = idx
+        out[:, 1] = np.asarray(vals, np.float32).view(np.uint32)
+        return out.tobytes()
+
+    @property
+    def esz(self) -> int:
+        return 4 if self.bf16 else 8
+
+    def w1(self, w: np.ndarray) -> bytes:
+        """A norm's weights: bf16 models the raw weight's bits (the kernel adds 1 in fp32, as
+        (1.0 + weight.float()) does), fp32 models 1 + w in fp32."""
+        w = np.asarray(w, np.float32)
+        if self.bf16:
+            return _bf16_bits(w).astype(np.uint16).tobytes()
+        return (np.float32(1.0) + w).astype(np.float32).tobytes()
+
+
+class Mega:
+    """lx.mega.Mega (lx/lx/mega.py:198-574) on MI355X.
+
+    fast: a ``linuxformer_amd.fast.Fast``; model: the model it was built from (unused beyond
+    what Fast holds, kept for the signature); cache: per layer ``conv_states[0]`` (1, n_conv, 4)
+    in the model dtype and ``recurrent_states[0]`` (1, nv, kd, vd) float32 on the device,
+    updated in place; offset: the first chip token's row in the embedding. ``spec`` and
+    ``pair_layers`` are accepted for compatibility: this kernel computes each layer's gates
+    before its MLP, so it never speculates and never redoes work.
+    """
+
+    def __init__(self, fast, model=None, cache=None, offset: int = 0, ncta: int | None = None,
+                 subprof: bool = False, spec: bool = True, pair_layers=None, device=None):
+        self.lib = mk_build.load()
+        self.fast, self.model, self.cache, self.offset = fast, model, cache, offset
+        sm = fast.sm
+        d = sm.dims
+        self.dims = d
+        dev = torch.device(device) if device is not None else torch.device("cuda")
+        if dev.type == "cuda" and dev.index is None:
+            dev = torch.device("cuda", torch.cuda.current_device())
+        self.dev = dev
+        cus = int(self.lib.lxm_device_cus())
+        self.ncta = ncta or cus
+        assert self.ncta >= 2, "the decode needs the chain workgroup and at least one helper"
+        assert d.kd == KD and d.vd == VD and d.conv == 4, "key dim 256, value dim 128, conv 4"
+        assert d.nv % d.nk == 0 and d.nv // d.nk <= RMAX and d.hidden <= MAXH
+        assert d.nv <= 256 and d.nk <= 64 and d.n_layers <= 64
+        self.bf = d.dtype == "bf16"
+        self.e4 = model_e4(sm)
+        pk = Packer(self.e4)
+        blob = _Blob()
+        descs = (LayerDesc * d.n_layers)()
+        H, R, C = d.hidden, d.nv // d.nk, d.n_conv
+        qk_total = 0
+        self.stats = {"layers": d.n_layers, "hot_bytes": [], "units": [], "qk": [], "dec": []}
+        for L, ly in enumerate(sm.layers):
+            # ---- live MLP units (gate row, up row and down column nonzero; lx/lx/fast.py:242-248)
+            g, u, dn = _Csr(ly.gate_proj), _Csr(ly.up_proj), _Csr(ly.down_proj.transpose())
+            gc = np.diff(g.ptr)
+            uc = np.diff(u.ptr)
+            dc = np.diff(dn.ptr)
+            units = np.nonzero((gc > 0) & (uc > 0) & (dc > 0))[0]
+            assert len(units) <= MAXU, f"layer {L}: {len(units)} live MLP units > {MAXU}"
+            uidx = np.full(d.inter, -1, np.int64)
+            uidx[units] = np.arange(len(units))
+            gu_parts, meta, pos = [], [], 0
+            for uu in units:
+                c1, v1 = g.row(uu)
+                c2, v2 = u.row(uu)
+                assert len(c1) < 256 and len(c2) < 256
+                meta.append(pos | (len(c1) << 16) | (len(c2) << 24))
+                gu_parts.append(pk.ent(c1, v1))
+                gu_parts.append(pk.ent(c2, v2))
+                pos += len(c1) + len(c2)
+            assert pos < 1 << 16
+            # down_proj by residual row over the live units (ascending unit order)
+            dcoo = ly.down_proj
+            keep = uidx[dcoo.cols] >= 0
+            drows, dunits, dvals = dcoo.rows[keep], uidx[dcoo.cols[keep]], dcoo.vals[keep]
+            order = np.lexsort((dunits, drows))
+            drows, dunits, dvals = drows[order], dunits[order], dvals[order]
+            dptr = np.zeros(H + 1, np.int64)
+            np.cumsum(np.bincount(drows, minlength=H), out=dptr[1:])
+            assert dptr[-1] < 1 << 16
+            # ---- the gates: live query/key channels (nonzero conv taps) and decaying heads
+            qkv = _Csr(ly.in_proj_qkv)
+            taps = np.asarray(ly.conv1d, np.float32)
+            ent_parts, epos = [], 0
+            qks = []
+            for c in np.nonzero((taps[:2 * d.nk * KD] != 0).any(1))[0]:
+                kh, rem = divmod(int(c) % (d.nk * KD), KD)
+                isk = int(c) >= d.nk * KD
+                cols, vals = qkv.row(c)
+                q = QkC(slot=kh * 512 + (256 if isk else 0) + rem, chan=int(c), start=epos,
+                        len=len(cols))
+                q.taps[:] = [float(x) for x in taps[c]]
+                qks.append(q)
+                ent_parts.append(pk.ent(cols, vals))
+                epos += len(cols)
+            assert len(qks) <= MAXQKL, f"layer {L}: {len(qks)} live query/key channels"
+            acsr = _Csr(ly.in_proj_a)
+            decs = []
+            for vh in range(d.nv):
+                cols, vals = acsr.row(vh)
+                # softplus(dt_bias) is exactly 0 only when exp(dt_bias) underflows (< -103.97)
+                if len(cols) == 0 and not float(ly.dt_bias[vh]) > -103.9:
+                    continue
+                decs.append(Dec(vh=vh, start=epos, len=len(cols), dt_bias=float(ly.dt_bias[vh]),
+                                A_log=float(ly.A_log[vh])))
+                ent_parts.append(pk.ent(cols, vals))
+                epos += len(cols)
+            assert len(decs) <= MAXDEC
+            # ---- the hot blob
+            hb = _Blob()
+            hb.add(bytes(64))
+            o_w1in = hb.add(pk.w1(ly.input_layernorm))
+            o_w1post = hb.add(pk.w1(ly.post_attention_layernorm))
+            o_unit = hb.add(np.asarray(meta, np.uint32).tobytes())
+            o_gu = hb.add(b"".join(gu_parts))
+            o_dptr = hb.add(dptr.astype(np.uint16).tobytes())
+            o_dent = hb.add(pk.ent(dunits, dvals))
+            o_qk = hb.add(b"".join(bytes(q) for q in qks))
+            o_dec = hb.add(b"".join(bytes(x) for x in decs))
+            o_ent = hb.add(b"".join(ent_parts))
+            hot = Hot(n_units=len(units), n_qk=len(qks), n_dec=len(decs), qk_base=qk_total,
+                      w1_in=o_w1in, w1_post=o_w1post, unit=o_unit, gu_ent=o_gu, down_ptr=o_dptr,
+                      down_ent=o_dent, qk=o_qk, dec=o_dec, ent=o_ent, size=hb.n,
+                      eps=d.rms_eps, geps=d.geps)
+            hb.parts[0] = bytes(hot)
+            assert hb.n <= HOT_MAX, f"layer {L}: resident tables {hb.n} B > {HOT_MAX}"
+            qk_total += len(qks)
+            desc = descs[L]
+            desc.hot = blob.add(hb.bytes())
+            # ---- cold tables
+            chans = np.zeros(C, dtype=[("start", "<i4"), ("len", "<i4"), ("taps", "<f4", (4,))])
+            chans["start"] = qkv.ptr[:-1]
+            chans["len"] = np.diff(qkv.ptr)
+            chans["taps"] = taps
+            desc.chan = blob.add(chans.tobytes())
+            desc.qkv_ent = blob.add(pk.ent(qkv.cols, qkv.vals))
+            b = _Csr(ly.in_proj_b)
+            desc.b_row = blob.add(np.stack([b.ptr[:-1], np.diff(b.ptr)], 1).astype(np.int32).tobytes())
+            desc.b_ent = blob.add(pk.ent(b.cols, b.vals))
+            z = _Csr(ly.in_proj_z)
+            desc.z_row = blob.add(np.stack([z.ptr[:-1], np.diff(z.ptr)], 1).astype(np.int32).tobytes())
+            desc.z_ent = blob.add(pk.ent(z.cols, z.vals))
+            # out_proj by residual row, per key head, columns local to the head's value dims
+            oc = ly.out_proj
+            head_of = oc.cols // (R * VD)
+            optr = np.zeros((d.nk, H + 1), np.int64)
+            oent = []
+            base = 0
+            for kh in range(d.nk):
+                sel = head_of == kh
+                rr, cc, vv = oc.rows[sel], oc.cols[sel] - kh * R * VD, oc.vals[sel]
+                order = np.lexsort((cc, rr))
+                rr, cc, vv = rr[order], cc[order], vv[order]
+                optr[kh, 1:] = np.cumsum(np.bincount(rr, minlength=H)) + base
+                optr[kh, 0] = base
+                base += len(rr)
+                oent.append(pk.ent(cc, vv))
+            desc.out_ptr = blob.add(optr.astype(np.int32).tobytes())
+            desc.out_ent = blob.add(b"".join(oent))
+            desc.gnorm = blob.add(np.asarray(ly.norm, np.float32).tobytes())
+            self.stats["hot_bytes"].append(hb.n)
+            self.stats["units"].append(len(units))
+            self.stats["qk"].append(len(qks))
+            self.stats["dec"].append(len(decs))
+        assert qk_total <= MAXQK, f"{qk_total} live query/key channels > {MAXQK}"
+        blob.add(bytes(HOT_MAX))  # padding past the last table
+        self.blob = torch.frombuffer(bytearray(blob.bytes()), dtype=torch.uint8).to(dev)
+        self.layers_d = torch.frombuffer(bytearray(bytes(descs)), dtype=torch.uint8).to(dev)
+        self.n_qk_total = qk_total
+        # ---- embedding (rows offset .. offset + vocab, all columns) and the head
+        emb = fast.embed_rows(offset)
+        self.emb_ptr = torch.from_numpy(emb.ptr).to(dev)
+        self.emb_ent = torch.frombuffer(bytearray(pk.ent(emb.cols, emb.vals)),
+                                        dtype=torch.uint8).to(dev)
+        w1f = (np.float32(1.0) + np.asarray(sm.norm, np.float32)).astype(np.float32)
+        self.w1_final = torch.from_numpy(w1f).to(dev)
+        hcols = np.nonzero(w1f != 0)[0]  # a column whose (1 + w) is 0 adds only zeros
+        hmask = np.zeros(H, bool)
+        hmask[hcols] = True
+        keep = hmask[emb.cols]
+        hrows = np.repeat(np.arange(emb.n), np.diff(emb.ptr))[keep]
+        hptr = np.zeros(emb.n + 1, np.int64)
+        np.cumsum(np.bincount(hrows, minlength=emb.n), out=hptr[1:])
+        self.head_ptr = torch.from_numpy(hptr).to(dev)
+        self.head_ent = torch.frombuffer(bytearray(pk.ent(emb.cols[keep], emb.vals[keep]) + bytes(16)),
+                                         dtype=torch.uint8).to(dev)
+        V = emb.n
+        nh = self.ncta - 1
+        # block 0 is the chain (no head rows); helper b covers cuts[b - 1] .. cuts[b]
+        cuts = np.linspace(0, V, nh + 1).round().astype(np.int64)
+        bounds = np.concatenate([[0], cuts])
+        self.head_rows = torch.from_numpy(bounds.astype(np.int32)).to(dev)
+        need = 0
+        for b in range(1, self.ncta):
+            r0, r1 = bounds[b], bounds[b + 1]
+            ne = hptr[r1] - hptr[r0]
+            need = max(need, ((r1 - r0 + 1) * 4 + 15) // 16 * 16 + ne * pk.esz)
+        self.head_lds = int((need + 15) // 16 * 16)
+        base = int(self.lib.lxm_lds_base())
+        self.lds = max(base, self.head_lds + 4 * MAXH + 128)
+        self.lds = (self.lds + 255) // 256 * 256
+        maxlds = int(self.lib.lxm_max_lds())
+        assert self.lds <= maxlds, (self.lds, maxlds)
+        assert int(self.lib.lxm_max_blocks(self.lds)) >= self.ncta, "the grid is not co-resident"
+        self.vocab = V
+        # ---- run buffers (the library allocates nothing)
+        self.ring = torch.zeros(4 * d.n_layers * H, dtype=torch.float32, device=dev)
+        self.hn = torch.zeros(MAXH, dtype=torch.float32, device=dev)
+        self.sync = torch.zeros(NSYNC, dtype=torch.int32, device=dev)
+        self.keys = torch.zeros(2, dtype=torch.int64, device=dev)
+        self.err = torch.zeros(1, dtype=torch.int32, device=dev)
+        self.stats.update({"ctas": self.ncta, "lds": self.lds, "head_lds": self.head_lds,
+                           "blob_bytes": int(self.blob.numel()), "qk_total": qk_total,
+                           "head_nnz": int(hptr[-1]), "vocab": V})
+
+    def _state_ptrs(self):
+        rs, cs = [], []
+        d = self.dims
+        for L in range(d.n_layers):
+            cl = self.cache.layers[L]
+            r, c = cl.recurrent_states[0], cl.conv_states[0]
+            assert r.is_contiguous() and c.is_contiguous() and r.dtype == torch.float32
+            assert tuple(r.shape[-3:]) == (d.nv, KD, VD) and c.shape[-1] == 4
+            assert c.dtype == (torch.bfloat16 if self.bf else torch.float32)
+            assert r.device == self.dev and c.device == self.dev
+            rs.append(r.data_ptr())
+            cs.append(c.data_ptr())
+        return (torch.tensor(rs, dtype=torch.int64, device=self.dev),
+                torch.tensor(cs, dtype=torch.int64, device=self.dev))
+
+    def sync_bitmaps(self) -> None:
+        """lx.mega's nonzero-row bitmaps are not used: decays scale the whole state tile."""
+
+    @torch.no_grad()
+    def run(self, forced, n: int, dbg=None, dbg_tok: int = 0, dbg_items=None, prof=None,
+            inputs: torch.Tensor | None = None, trace: torch.Tensor | None = None) -> list:
+        """n steps; step i's input is forced[i] (i < len(forced)) or step i - 1's prediction.
+        Returns the n predictions (chip token ids). inputs (n,) int32: each step's input as the
+        kernel embedded it. trace (n, n_layers, hidden) float32: the residual after each
+        layer of each step."""
+        assert len(forced) >= 1 and n >= 1
+        f = np.asarray(forced, np.int64)
+        if f.min() < 0 or f.max() >= self.vocab:
+            raise ValueError("forced token out of range")
+        d = self.dims
+        rs, cs = self._state_ptrs()
+        ft = torch.tensor(f.astype(np.int32), device=self.dev)
+        preds = torch.zeros(n, dtype=torch.int32, device=self.dev)
+        if inputs is not None:
+            assert inputs.dtype == torch.int32 and inputs.numel() >= n and inputs.device == self.dev
+        if trace is not None:
+            assert trace.dtype == torch.float32 and trace.is_contiguous()
+            assert trace.numel() >= n * d.n_layers * d.hidden and trace.device == self.dev
+        self.sync.zero_()
+        self.keys.zero_()
+        self.err.zero_()
+        p = Params(hidden=d.hidden, n_layers=d.n_layers, nk=d.nk, kd=KD, nv=d.nv, vd=VD,
+                   n_conv=d.n_conv, vocab=self.vocab, bf16=int(self.bf), n_blocks=self.ncta,
+                   rms_eps=d.rms_eps, head_lds=self.head_lds, e4=int(self.e4),
+                   layers=self.layers_d.data_ptr(), blob=self.blob.data_ptr(),
+                   rec=rs.data_ptr(), conv=cs.data_ptr(), emb_ptr=self.emb_ptr.data_ptr(),
+                   emb_ent=self.emb_ent.data_ptr(), w1_final=self.w1_final.data_ptr(),
+                   head_rows=self.head_rows.data_ptr(), head_ptr=self.head_ptr.data_ptr(),
+                   head_ent=self.head_ent.data_ptr(), forced=ft.data_ptr(), n_forced=len(f),
+                   n_tokens=n, preds=preds.data_ptr(),
+                   inputs=inputs.data_ptr() if inputs is not None else None,
+                   trace=trace.data_ptr() if trace is not None else None,
+                   ring=self.ring.data_ptr(), hn=self.hn.data_ptr(), sync=self.sync.data_ptr(),
+                   keys=self.keys.data_ptr(), err=self.err.data_ptr(), n_qk_total=self.n_qk_total)
+        pd = torch.frombuffer(bytearray(bytes(p)), dtype=torch.uint8).to(self.dev)
+        self._keep = (rs, cs, ft, pd)
+        st = ctypes.c_void_p(torch.cuda.current_stream(self.dev).cuda_stream)
+        e = self.lib.lxm_run(ctypes.byref(p), ctypes.c_void_p(pd.data_ptr()), self.ncta,
+                             self.lds, st)
+        if e:
+            raise RuntimeError(f"mega launch failed: hipError {e}")
+        out = preds.tolist()  # syncs
+        e = self.lib.lxm_last_error()
+        if e:
+            raise RuntimeError(f"mega failed: hipError {e}")
+        err = int(self.err.item())
+        if err:
+            raise RuntimeError(f"mega failed: a grid wait timed out (code {err})")
+        return out

@@ -1,0 +1,71 @@
+"""Build and load the native library (lx/lx/mk_build.py's role: nvcc + ctypes there, hipcc for
+gfx950 here). The library is built in-tree, so it travels with the repository to the GPU box;
+loading never compiles, and a missing library is an error, never a fallback."""
+
+from __future__ import annotations
+
+import ctypes
+import os
+import subprocess
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+CSRC = os.path.join(HERE, "csrc")
+LIBDIR = os.path.join(HERE, "_lib")
+LIB = os.path.join(LIBDIR, "liblxm.so")
+SOURCES = ["lxm_decode.hip"]
+HEADERS = ["lxm_math.h", os.path.join("..", "..", "include", "lxm.h")]
+# -ffp-contract=off: no a*b+c is fused (the rounding contract); packed fp32 ops disabled
+FLAGS = ["--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC", "-shared", "-ffp-contract=off",
+         "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops"]
+
+
+def hipcc() -> str:
+    for c in (os.environ.get("HIPCC"), "/opt/rocm/bin/hipcc", "hipcc"):
+        if c and (os.path.isabs(c) and os.path.exists(c) or not os.path.isabs(c)):
+            return c
+    return "hipcc"
+
+
+def build(verbose: bool = False) -> str:
+    """Compile the library for gfx950 (always compiles)."""
+    os.makedirs(LIBDIR, exist_ok=True)
+    tmp = LIB + ".tmp"
+    cmd = [hipcc(), *FLAGS, "-o", tmp, *[os.path.join(CSRC, s) for s in SOURCES]]
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError(f"hipcc failed ({r.returncode}):\n{r.stderr[-4000:]}")
+    if verbose and r.stderr:
+        print(r.stderr)
+    os.replace(tmp, LIB)
+    return LIB
+
+
+_lib = None
+
+
+def load() -> ctypes.CDLL:
+    """The built library (ctypes). Raises if it has not been built."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB):
+            raise RuntimeError(f"{LIB} is missing: run linuxformer_amd.mk_build.build() (or "
+                               "__graft_entry__.build()) first")
+        lib = ctypes.CDLL(LIB)
+        P, I = ctypes.c_void_p, ctypes.c_int
+        lib.lxm_run.argtypes = [P, P, I, I, P]
+        lib.lxm_run.restype = I
+        for n in ("lxm_lds_base", "lxm_max_lds", "lxm_last_error", "lxm_device_cus"):
+            getattr(lib, n).restype = I
+            getattr(lib, n).argtypes = []
+        lib.lxm_max_blocks.argtypes = [I]
+        lib.lxm_max_blocks.restype = I
+        lib.lxm_t_elem.argtypes = [I, P, P, ctypes.c_long, P]
+        lib.lxm_t_elem.restype = I
+        lib.lxm_t_sum.argtypes = [I, P, I, I, P, P]
+        lib.lxm_t_sum.restype = I
+        _lib = lib
+    return _lib
+
+
+EXPORTS = ("lxm_run", "lxm_lds_base", "lxm_max_blocks", "lxm_max_lds", "lxm_last_error",
+           "lxm_device_cus", "lxm_t_elem", "lxm_t_sum")

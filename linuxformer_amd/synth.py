@@ -1,0 +1,438 @@
+"""Seeded synthetic chip stacks (the benchmark's configurations) as sparse checkpoint tensors.
+
+The reference measures only the real chip, whose 32 GB checkpoint is not available offline, so
+every workload here is synthetic and fully determined by a seed. A ``SparseModel`` holds the
+same tensors a stock ``Qwen3_5ForCausalLM`` chip model carries (the names of
+transformers/models/qwen3_5/modeling_qwen3_5.py:387-430 and :704-793; the tied embedding/head of
+lx/lx/hf.py:179-184), but in coordinate form, so that a 37-layer stack at 0.08 % density costs
+megabytes instead of the 16 GB its dense bf16 tensors would. ``to_hf`` materialises small
+models as a real transformers model (the stock forward used to pin the oracle).
+
+Write gates. Most chip layer-steps leave the recurrent state and the residual stream alone: the
+real chip's decode touches ~4.5 state rows per token (lx/results/head_activity.json). The
+synthetic stacks reproduce that with one *gate column* per layer at the top of the residual
+stream: a layer's query, key and decay projections read only its gate column, no projection
+writes gate columns, and a token's embedding row sets the gate column of layer L with
+probability ``p_gate`` (seeded). A layer-step therefore has a nonzero query, key or decay only
+when its input tokens carry that layer's gate, i.e. on about ``p_gate`` of layer-steps whatever
+the greedy stream does (the final norm weight is -1 on gate columns, so the head's argmax never
+sees them). Everything else is uniform at the configured density, except that a SwiGLU unit's
+up_proj row reads the same (seeded, uniform) columns as its gate_proj row, so that units fire
+and the residual stream mixes across layers.
+"""
+
+from __future__ import annotations
+
+from dataclasses import dataclass, field, replace
+
+import numpy as np
+
+VALS = np.array([-2.0, -1.0, -0.5, 0.5, 1.0, 2.0], dtype=np.float32)
+
+# component ids for per-(layer, component) seeds
+_QKV, _Z, _B, _A, _OUT, _CONV, _GATE, _UP, _DOWN, _LIVE, _EMB, _GEMB, _FN, _STATE, _START = range(15)
+
+
+@dataclass
+class Coo:
+    """A sparse matrix: rows, cols (int64), vals (float32, exact in the model dtype), sorted by
+    row then column, no duplicates."""
+    shape: tuple
+    rows: np.ndarray
+    cols: np.ndarray
+    vals: np.ndarray
+
+    @staticmethod
+    def build(shape, rows, cols, vals) -> "Coo":
+        rows = np.asarray(rows, np.int64)
+        cols = np.asarray(cols, np.int64)
+        vals = np.asarray(vals, np.float32)
+        keep = vals != 0
+        rows, cols, vals = rows[keep], cols[keep], vals[keep]
+        key = rows * shape[1] + cols
+        order = np.argsort(key, kind="stable")
+        key = key[order]
+        assert len(key) < 2 or np.all(np.diff(key) > 0), "duplicate entries"
+        return Coo(tuple(shape), rows[order], cols[order], vals[order])
+
+    @staticmethod
+    def from_dense(w) -> "Coo":
+        w = np.asarray(w, np.float32)
+        r, c = np.nonzero(w)
+        return Coo(tuple(w.shape), r.astype(np.int64), c.astype(np.int64), w[r, c])
+
+    @property
+    def nnz(self) -> int:
+        return len(self.vals)
+
+    def dense(self) -> np.ndarray:
+        out = np.zeros(self.shape, np.float32)
+        out[self.rows, self.cols] = self.vals
+        return out
+
+    def transpose(self) -> "Coo":
+        return Coo.build((self.shape[1], self.shape[0]), self.cols, self.rows, self.vals)
+
+
+@dataclass
+class Dims:
+    hidden: int
+    n_layers: int
+    nk: int = 16
+    kd: int = 256
+    nv: int = 128
+    vd: int = 128
+    conv: int = 4
+    inter: int = 1024
+    vocab: int = 4096
+    dtype: str = "bf16"  # model dtype: "bf16" or "fp32"
+    rms_eps: float = 1e-6
+    gated_eps: float | None = None  # the gated norm's eps (None: rms_eps, as the stock layer)
+
+    @property
+    def geps(self) -> float:
+        return self.rms_eps if self.gated_eps is None else self.gated_eps
+
+    @property
+    def n_conv(self) -> int:
+        return 2 * self.nk * self.kd + self.nv * self.vd
+
+
+@dataclass
+class Layer:
+    in_proj_qkv: Coo
+    in_proj_z: Coo
+    in_proj_b: Coo
+    in_proj_a: Coo
+    out_proj: Coo
+    conv1d: np.ndarray  # (n_conv, conv) float32
+    A_log: np.ndarray  # (nv,)
+    dt_bias: np.ndarray  # (nv,)
+    norm: np.ndarray  # (vd,) the gated norm's weight
+    input_layernorm: np.ndarray  # (hidden,) raw weight w (the module scales by 1 + w)
+    post_attention_layernorm: np.ndarray
+    gate_proj: Coo
+    up_proj: Coo
+    down_proj: Coo
+
+
+@dataclass
+class SparseModel:
+    dims: Dims
+    layers: list
+    embed: Coo  # (vocab, hidden), tied to the output head
+    norm: np.ndarray  # (hidden,) final norm weight
+    meta: dict = field(default_factory=dict)
+
+
+@dataclass
+class Spec:
+    """A synthetic stack: shapes, density, gates and seeds (2 and 5)."""
+    name: str
+    dims: Dims
+    seed: int = 0
+    density: float = 0.0008
+    p_gate: float = 0.02  # per (token, layer): the token's embedding sets the layer's gate
+    p_live: float = 0.25  # per key head: reads the gate (query/key rows)
+    p_decay: float = 0.25  # per value head of a live key head: in_proj_a reads the gate
+    p_tap: float = 0.1  # per earlier conv tap of a live channel
+    gate_gain: float = 64.0  # 1 + input_layernorm weight on gate columns
+    dt_bias: float = -112.0  # softplus(dt_bias) == 0 in fp32: no decay without the gate
+    emb_nnz: int = 3  # nonzeros per embedding row outside the gate columns
+    state: str = "normal"  # initial recurrent state: "normal" (N(0,1)) or "zero"
+    n_steps: int = 256
+
+
+def config1(seed: int = 1) -> Spec:
+    """one chip-shaped GDN + SwiGLU layer, fp32, zero state, 4,096 tokens.
+    A single layer at 0.08 % density barely mixes the residual stream, so a quarter of its
+    layer-steps are gated on (the delta rule, its writes into the zero state and their reads)."""
+    return Spec("c1", Dims(hidden=3572, n_layers=1, vocab=4096, dtype="fp32"), seed=seed,
+                state="zero", n_steps=256, p_gate=0.25)
+
+
+def config2(seed: int = 2) -> Spec:
+    """the 37-layer synthetic chip stack, bf16, N(0,1) state, 2% gates."""
+    return Spec("c2", Dims(hidden=3572, n_layers=37, vocab=459_982, dtype="bf16"), seed=seed,
+                state="normal", n_steps=262_144)
+
+
+def config5(seed: int = 2) -> Spec:
+    """config 2's stack with gates on for half of the layer-steps."""
+    s = config2(seed)
+    return replace(s, name="c5", p_gate=0.5, n_steps=65_536)
+
+
+def small(seed: int = 7, n_layers: int = 3, hidden: int = 192, vocab: int = 512,
+          dtype: str = "bf16", p_gate: float = 0.3, density: float = 0.05,
+          state: str = "normal") -> Spec:
+    """A small stack of the chip's head shapes (KD 256, VD 128) for fast parity tests."""
+    return Spec("small", Dims(hidden=hidden, n_layers=n_layers, nk=2, nv=8, inter=48,
+                              vocab=vocab, dtype=dtype), seed=seed, density=density,
+                p_gate=p_gate, p_live=1.0, p_decay=0.5, p_tap=0.3, emb_nnz=6, state=state,
+                n_steps=64)
+
+
+def _rng(seed: int, *k: int) -> np.random.Generator:
+    return np.random.default_rng([seed, *k])
+
+
+def _uniform(rng, rows: np.ndarray, cols: np.ndarray, density: float, shape) -> Coo:
+    """Nonzeros at round(density * n) seeded uniform positions of the submatrix rows x cols,
+    values uniform over VALS."""
+    n = len(rows) * len(cols)
+    k = int(round(density * n))
+    if k == 0 or n == 0:
+        return Coo.build(shape, [], [], [])
+    pos = rng.choice(n, size=k, replace=False)
+    return Coo.build(shape, rows[pos // len(cols)], cols[pos % len(cols)],
+                     rng.choice(VALS, size=k))
+
+
+def _layer(spec: Spec, L: int) -> Layer:
+    d, s = spec.dims, spec.seed
+    H, nk, kd, nv, vd, R = d.hidden, d.nk, d.kd, d.nv, d.vd, d.nv // d.nk
+    C = d.n_conv
+    ng = np.arange(H - d.n_layers)  # columns (rows) that are not gate columns
+    gcol = H - d.n_layers + L
+    # live key heads: their query and key rows read the gate column
+    rl = _rng(s, L, _LIVE)
+    live = rl.random(nk) < spec.p_live
+    if not live.any():
+        live[rl.integers(nk)] = True
+    qr, qc, qv = [], [], []
+    for kh in np.nonzero(live)[0]:
+        for base, lo, hi in ((kh * kd, 1, 5), (nk * kd + kh * kd, 1, 3)):
+            n = int(rl.integers(lo, hi))
+            rows = base + rl.choice(kd, size=n, replace=False)
+            qr += list(rows)
+            qc += [gcol] * n
+            qv += list(rl.choice(VALS, size=n))
+    qk = Coo.build((C, H), qr, qc, qv)
+    v_rows = np.arange(2 * nk * kd, C)
+    v = _uniform(_rng(s, L, _QKV), v_rows, ng, spec.density, (C, H))
+    qkv = Coo.build((C, H), np.concatenate([qk.rows, v.rows]), np.concatenate([qk.cols, v.cols]),
+                    np.concatenate([qk.vals, v.vals]))
+    # conv taps: tap conv-1 (the current input) on every channel with a projection row, earlier
+    # taps seeded
+    rc = _rng(s, L, _CONV)
+    has_row = np.zeros(C, bool)
+    has_row[qkv.rows] = True
+    conv = np.zeros((C, d.conv), np.float32)
+    conv[has_row, d.conv - 1] = rc.choice(VALS, size=int(has_row.sum()))
+    extra = (rc.random((C, d.conv - 1)) < spec.p_tap) & has_row[:, None]
+    conv[:, :d.conv - 1] = np.where(extra, rc.choice(VALS, size=(C, d.conv - 1)), 0.0)
+    # decay projections: some value heads of live key heads read the gate
+    ra = _rng(s, L, _A)
+    vh_live = np.repeat(live, R)
+    dec = vh_live & (ra.random(nv) < spec.p_decay)
+    a = Coo.build((nv, H), np.nonzero(dec)[0], np.full(int(dec.sum()), gcol),
+                  ra.choice(VALS, size=int(dec.sum())))
+    vrows_h = np.arange(nv * vd)
+    # SwiGLU units: up_proj's row reads the columns its gate_proj row reads (seeded uniform
+    # positions, independent values), so a unit fires whenever its inputs are nonzero
+    gate = _uniform(_rng(s, L, _GATE), np.arange(d.inter), ng, spec.density, (d.inter, H))
+    lay = Layer(
+        in_proj_qkv=qkv,
+        in_proj_z=_uniform(_rng(s, L, _Z), vrows_h, ng, spec.density, (nv * vd, H)),
+        in_proj_b=_uniform(_rng(s, L, _B), np.arange(nv), ng, spec.density, (nv, H)),
+        in_proj_a=a,
+        out_proj=_uniform(_rng(s, L, _OUT), ng, np.arange(nv * vd), spec.density, (H, nv * vd)),
+        conv1d=conv,
+        A_log=np.zeros(nv, np.float32),
+        dt_bias=np.full(nv, spec.dt_bias, np.float32),
+        norm=np.ones(vd, np.float32),
+        input_layernorm=np.zeros(H, np.float32),
+        post_attention_layernorm=np.zeros(H, np.float32),
+        gate_proj=gate,
+        up_proj=Coo.build(gate.shape, gate.rows, gate.cols,
+                          _rng(s, L, _UP).choice(VALS, size=gate.nnz)),
+        down_proj=_uniform(_rng(s, L, _DOWN), ng, np.arange(d.inter), spec.density, (H, d.inter)),
+    )
+    lay.input_layernorm[H - d.n_layers:] = spec.gate_gain - 1.0
+    lay.post_attention_layernorm[H - d.n_layers:] = -1.0
+    return lay
+
+
+def build(spec: Spec) -> SparseModel:
+    """The seeded stack of ``spec`` (weights only; see ``init_state`` for the caches)."""
+    d, s = spec.dims, spec.seed
+    H, V = d.hidden, d.vocab
+    assert d.nv % d.nk == 0 and H > d.n_layers
+    layers = [_layer(spec, L) for L in range(d.n_layers)]
+    # embedding: emb_nnz distinct non-gate columns per row, plus each layer's gate at p_gate
+    re = _rng(s, 0, _EMB)
+    hng = H - d.n_layers
+    k = min(spec.emb_nnz, hng)
+    cols = np.stack([re.choice(hng, size=k, replace=False) for _ in range(min(V, 4096))]) \
+        if V <= 4096 else _distinct_cols(re, V, hng, k)
+    rows = np.repeat(np.arange(V), k)
+    vals = re.choice(VALS, size=V * k)
+    rg = _rng(s, 0, _GEMB)
+    gr, gc = [], []
+    for L in range(d.n_layers):
+        on = np.nonzero(rg.random(V) < spec.p_gate)[0]
+        gr.append(on)
+        gc.append(np.full(len(on), hng + L))
+    gr = np.concatenate(gr) if gr else np.zeros(0, np.int64)
+    gc = np.concatenate(gc) if gc else np.zeros(0, np.int64)
+    embed = Coo.build((V, H), np.concatenate([rows, gr]), np.concatenate([cols.reshape(-1), gc]),
+                      np.concatenate([vals, rg.choice(VALS, size=len(gr))]))
+    # final norm: weight 0 or -2 (1 + w = +-1) outside the gates, -1 on them (the head ignores
+    # the gates)
+    rf = _rng(s, 0, _FN)
+    norm = np.where(rf.random(H) < 0.5, -2.0, 0.0).astype(np.float32)
+    norm[hng:] = -1.0
+    return SparseModel(d, layers, embed, norm, meta={"spec": spec})
+
+
+def _distinct_cols(rng, V: int, n: int, k: int) -> np.ndarray:
+    cols = rng.integers(0, n, size=(V, k))
+    while True:
+        s = np.sort(cols, axis=1)
+        bad = np.nonzero((np.diff(s, axis=1) == 0).any(1))[0]
+        if len(bad) == 0:
+            return cols
+        cols[bad] = rng.integers(0, n, size=(len(bad), k))
+
+
+def init_state(model: SparseModel, kind: str | None = None, seed: int | None = None):
+    """The initial caches: conv windows (n_layers, n_conv, conv) zero and recurrent states
+    (n_layers, nv, kd, vd) float32, N(0,1) (seeded per layer, row by row) or zero. Returns
+    numpy arrays; conv windows hold values exact in the model dtype."""
+    d = model.dims
+    spec = model.meta.get("spec")
+    kind = kind or (spec.state if spec else "zero")
+    seed = seed if seed is not None else (spec.seed if spec else 0)
+    conv = np.zeros((d.n_layers, d.n_conv, d.conv), np.float32)
+    rec = np.zeros((d.n_layers, d.nv, d.kd, d.vd), np.float32)
+    if kind == "normal":
+        for L in range(d.n_layers):
+            rec[L] = _rng(seed, L, _STATE).standard_normal((d.nv, d.kd, d.vd), np.float32)
+    return conv, rec
+
+
+def start_token(spec: Spec) -> int:
+    return int(_rng(spec.seed, 0, _START).integers(0, spec.dims.vocab))
+
+
+def tiny_dense(seed: int = 0, dtype: str = "fp32", hidden: int = 64, n_layers: int = 2,
+               nk: int = 4, nv: int = 32, inter: int = 64, vocab: int = 96,
+               scale: float = 0.08) -> SparseModel:
+    """A small dense random stack (every weight nonzero, N(0, scale) rounded to the dtype):
+    every head is live at every step, so every sum of the step has its full length. Used to
+    pin the oracle against the stock transformers forward."""
+    d = Dims(hidden=hidden, n_layers=n_layers, nk=nk, nv=nv, inter=inter, vocab=vocab,
+             dtype=dtype)
+    rng = np.random.default_rng([seed, 99])
+
+    def w(*shape, s=scale):
+        return _round(rng.standard_normal(shape).astype(np.float32) * s, dtype)
+
+    H, C = hidden, d.n_conv
+    layers = []
+    for _ in range(n_layers):
+        layers.append(Layer(
+            in_proj_qkv=Coo.from_dense(w(C, H)), in_proj_z=Coo.from_dense(w(nv * d.vd, H)),
+            in_proj_b=Coo.from_dense(w(nv, H, s=0.5)), in_proj_a=Coo.from_dense(w(nv, H, s=0.5)),
+            out_proj=Coo.from_dense(w(H, nv * d.vd)),
+            conv1d=w(C, d.conv, s=0.5), A_log=w(nv, s=0.5), dt_bias=w(nv, s=0.5),
+            norm=1.0 + w(d.vd, s=0.1), input_layernorm=w(H, s=0.1),
+            post_attention_layernorm=w(H, s=0.1), gate_proj=Coo.from_dense(w(inter, H, s=0.3)),
+            up_proj=Coo.from_dense(w(inter, H, s=0.3)), down_proj=Coo.from_dense(w(H, inter)),
+        ))
+    embed = Coo.from_dense(w(vocab, H, s=1.0))
+    return SparseModel(d, layers, embed, w(H, s=0.1), meta={"tiny": seed})
+
+
+def _round(x: np.ndarray, dtype: str) -> np.ndarray:
+    """float32 values rounded to the model dtype (bf16: round to nearest even), as float32."""
+    if dtype == "fp32":
+        return x.astype(np.float32)
+    u = x.astype(np.float32).view(np.uint32).astype(np.uint64)
+    u = ((u + 0x7FFF + ((u >> 16) & 1)) >> 16) << 16
+    return u.astype(np.uint32).view(np.float32)
+
+
+def to_hf(model: SparseModel, dev: str = "cpu"):
+    """The model as a stock transformers Qwen3_5ForCausalLM (dense tensors; small models only):
+    n_layers linear-attention layers, the tied head, the final norm."""
+    import torch
+    from transformers import Qwen3_5ForCausalLM, Qwen3_5TextConfig
+
+    d = model.dims
+    dt = torch.bfloat16 if d.dtype == "bf16" else torch.float32
+    cfg = Qwen3_5TextConfig(
+        vocab_size=d.vocab, hidden_size=d.hidden, intermediate_size=d.inter,
+        num_hidden_layers=d.n_layers, layer_types=["linear_attention"] * d.n_layers,
+        linear_key_head_dim=d.kd, linear_value_head_dim=d.vd, linear_num_key_heads=d.nk,
+        linear_num_value_heads=d.nv, linear_conv_kernel_dim=d.conv, rms_norm_eps=d.rms_eps,
+        tie_word_embeddings=True, hidden_act="silu", num_attention_heads=4,
+        num_key_value_heads=1, head_dim=64,
+        rope_parameters={"rope_type": "default", "rope_theta": 10000.0,
+                         "partial_rotary_factor": 0.25})
+    with torch.device("meta"):
+        m = Qwen3_5ForCausalLM(cfg)
+    sd = {}
+    t = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(dt)  # noqa: E731
+    for L, lay in enumerate(model.layers):
+        p = f"model.layers.{L}."
+        ga = p + "linear_attn."
+        sd[ga + "in_proj_qkv.weight"] = t(lay.in_proj_qkv.dense())
+        sd[ga + "in_proj_z.weight"] = t(lay.in_proj_z.dense())
+        sd[ga + "in_proj_b.weight"] = t(lay.in_proj_b.dense())
+        sd[ga + "in_proj_a.weight"] = t(lay.in_proj_a.dense())
+        sd[ga + "out_proj.weight"] = t(lay.out_proj.dense())
+        sd[ga + "conv1d.weight"] = t(lay.conv1d[:, None, :])
+        sd[ga + "A_log"] = t(lay.A_log)
+        sd[ga + "dt_bias"] = t(lay.dt_bias)
+        sd[ga + "norm.weight"] = t(lay.norm)
+        sd[p + "input_layernorm.weight"] = t(lay.input_layernorm)
+        sd[p + "post_attention_layernorm.weight"] = t(lay.post_attention_layernorm)
+        sd[p + "mlp.gate_proj.weight"] = t(lay.gate_proj.dense())
+        sd[p + "mlp.up_proj.weight"] = t(lay.up_proj.dense())
+        sd[p + "mlp.down_proj.weight"] = t(lay.down_proj.dense())
+    sd["model.embed_tokens.weight"] = t(model.embed.dense())
+    sd["model.norm.weight"] = t(model.norm)
+    missing, unexpected = m.load_state_dict(sd, strict=False, assign=True)
+    assert not unexpected and set(missing) <= {"lm_head.weight"}, (missing[:4], unexpected[:4])
+    m.tie_weights()
+    from transformers.models.qwen3_5 import modeling_qwen3_5 as q
+    m.model.rotary_emb = q.Qwen3_5TextRotaryEmbedding(config=cfg)
+    return m.to(device=dev, dtype=dt).eval()
+
+
+def from_hf(m, n_chip: int | None = None) -> SparseModel:
+    """A transformers Qwen3_5 chip model's tensors (its first n_chip layers) in coordinate form."""
+    import torch
+
+    cfg = m.config
+    n = n_chip if n_chip is not None else cfg.num_hidden_layers
+    dtype = "bf16" if m.dtype == torch.bfloat16 else "fp32"
+    d = Dims(hidden=cfg.hidden_size, n_layers=n, nk=cfg.linear_num_key_heads,
+             kd=cfg.linear_key_head_dim, nv=cfg.linear_num_value_heads,
+             vd=cfg.linear_value_head_dim, conv=cfg.linear_conv_kernel_dim,
+             inter=cfg.intermediate_size, vocab=m.lm_head.weight.shape[0], dtype=dtype,
+             rms_eps=cfg.rms_norm_eps,
+             gated_eps=float(m.model.layers[0].linear_attn.norm.variance_epsilon) if n else None)
+
+    def f(x):
+        return x.detach().float().cpu().numpy()
+
+    def coo(x):
+        return Coo.from_dense(f(x))
+
+    layers = []
+    for L in range(n):
+        lay = m.model.layers[L]
+        ga = lay.linear_attn
+        layers.append(Layer(
+            in_proj_qkv=coo(ga.in_proj_qkv.weight), in_proj_z=coo(ga.in_proj_z.weight),
+            in_proj_b=coo(ga.in_proj_b.weight), in_proj_a=coo(ga.in_proj_a.weight),
+            out_proj=coo(ga.out_proj.weight), conv1d=f(ga.conv1d.weight[:, 0]),
+            A_log=f(ga.A_log), dt_bias=f(ga.dt_bias), norm=f(ga.norm.weight),
+            input_layernorm=f(lay.input_layernorm.weight),
+            post_attention_layernorm=f(lay.post_attention_layernorm.weight),
+            gate_proj=coo(lay.mlp.gate_proj.weight), up_proj=coo(lay.mlp.up_proj.weight),
+            down_proj=coo(lay.mlp.down_proj.weight)))
+    return SparseModel(d, layers, coo(m.lm_head.weight), f(m.model.norm.weight))

@@ -1,0 +1,491 @@
+/* TEST INFRASTRUCTURE ONLY -- the checker, never the product.
+ *
+ * A CPU restatement, in plain C, of the stock decode of linuxformer's chip layers: the
+ * transformers Qwen3_5 decoder layer run token by token in the "chip view"
+ * (lx/lx/hf.py:169-176: no positions, no masks), then the tied output head's argmax
+ * (lx/lx/hf.py:179-184), with the next input fed back as lx.mega runs it (lx/csrc/mega.cu:852-858,
+ * lx/lx/mega.py:529-535). Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline may
+ * load this library; the HIP product path never does.
+ *
+ * Each step follows, op for op, the stock module it restates (TF = transformers 5.15
+ * models/qwen3_5/modeling_qwen3_5.py):
+ *   Qwen3_5RMSNorm                TF:720-737   x * rsqrt(mean(x^2) + eps), * (1 + w), to dtype
+ *   Qwen3_5GatedDeltaNet.forward  TF:432-543   projections, causal_conv1d_update (TF:199-216),
+ *                                              beta = sigmoid(b), g = -exp(A_log) softplus(a + dt)
+ *   torch_recurrent_gated_delta_rule TF:330-380 with l2norm (TF:242-245) in the input dtype
+ *   Qwen3_5RMSNormGated           TF:168-184
+ *   Qwen3_5MLP                    TF:704-717
+ *   Qwen3_5DecoderLayer.forward   TF:753-793
+ *
+ * The rounding contract (what "bit-exact" means between this file and the HIP kernels):
+ *   - every elementary op is one IEEE binary32 op, rounded to nearest even, never contracted
+ *     into an fma (built with -ffp-contract=off); "D(x)" rounds to the model dtype (bf16: round
+ *     to nearest even with NaN -> 0x7fc0, as c10::BFloat16 does; fp32: identity);
+ *   - exp, log1p are this file's own functions: evaluated in binary64 (exp: Cody-Waite reduction
+ *     by ln 2 and a degree-13 Taylor polynomial; log1p: 2 atanh series) and rounded once to
+ *     binary32 (correctly rounded except within ~1e-15 relative of a rounding boundary);
+ *     silu(x) = x / (1 + exp(-x)), sigmoid(x) = 1 / (1 + exp(-x)), softplus(x) = x > 20 ? x :
+ *     log1p(exp(x)), rsqrt(x) = 1 / sqrt(x) -- the compositions ATen's CPU kernels use;
+ *   - dot products and row sums add their terms in ascending index order, from +0; a term
+ *     whose factor is an exact zero is skipped (it can change only the sign of a zero sum);
+ *   - the delta rule's sums over the state's rows (kv and o, TF:372 and :375, torch's .sum(-2))
+ *     follow ATen's CPU cascade for a reduction over a non-contiguous dimension: rows in blocks
+ *     of 16, each block summed in order from +0, the block sums added in order from +0 (this
+ *     order does not depend on the CPU's vector width, and torch's sum matches it bit for bit);
+ *   - sums over a hidden vector (RMSNorm's sum of squares) use 512 lanes: lane l adds
+ *     x[l], x[l + 512], ... in order from +0; the lanes of each group of 64 are combined by a
+ *     pairwise tree at offsets 32, 16, 8, 4, 2, 1 (lane i takes i + off); the 8 group totals by
+ *     a tree at offsets 4, 2, 1. Sums over a head (128 or 256 values) use one group of 64 lanes.
+ *     Means divide the sum by the count (ATen's CPU mean is sum().div_(n)).
+ */
+#include <math.h>
+#include <stdint.h>
+#include <stdlib.h>
+#include <string.h>
+
+/* ------------------------------------------------------------------ rounding primitives */
+
+static inline uint32_t fbits(float x) { uint32_t u; memcpy(&u, &x, 4); return u; }
+static inline float bitsf(uint32_t u) { float x; memcpy(&x, &u, 4); return x; }
+
+static inline float bf16r(float x) {
+  uint32_t u = fbits(x);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return bitsf(0x7fc00000u);
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return bitsf(u & 0xffff0000u);
+}
+
+static int g_bf16 = 1; /* model dtype of the current call */
+static inline float D(float x) { return g_bf16 ? bf16r(x) : x; }
+
+static inline double pow2i(int k) { /* 2^k, -1022 <= k <= 1023 */
+  uint64_t u = (uint64_t)(k + 1023) << 52;
+  double d; memcpy(&d, &u, 8); return d;
+}
+
+/* exp(x) in binary64 for -110 <= x <= 89 (relative error ~5e-16) */
+static double exp_d(double x) {
+  const double LOG2E = 0x1.71547652b82fep+0;
+  const double LN2_HI = 0x1.62e42fee00000p-1, LN2_LO = 0x1.a39ef35793c76p-33;
+  double kd = floor(x * LOG2E + 0.5);
+  double r = (x - kd * LN2_HI) - kd * LN2_LO;
+  double p = 0x1.6124613a86d09p-33;
+  p = p * r + 0x1.1eed8eff8d898p-29;
+  p = p * r + 0x1.ae64567f544e4p-26;
+  p = p * r + 0x1.27e4fb7789f5cp-22;
+  p = p * r + 0x1.71de3a556c734p-19;
+  p = p * r + 0x1.a01a01a01a01ap-16;
+  p = p * r + 0x1.a01a01a01a01ap-13;
+  p = p * r + 0x1.6c16c16c16c17p-10;
+  p = p * r + 0x1.1111111111111p-7;
+  p = p * r + 0x1.5555555555555p-5;
+  p = p * r + 0x1.5555555555555p-3;
+  p = p * r + 0x1.0000000000000p-1;
+  p = p * r + 1.0;
+  p = p * r + 1.0;
+  return p * pow2i((int)kd);
+}
+
+float ox_expf(float x) {
+  if (x != x) return x;
+  if (x > 89.0f) return INFINITY;
+  if (x < -110.0f) return 0.0f;
+  return (float)exp_d((double)x);
+}
+
+/* log(u) in binary64 for finite u >= 1 */
+static double log_d(double u) {
+  const double LN2_HI = 0x1.62e42fee00000p-1, LN2_LO = 0x1.a39ef35793c76p-33;
+  uint64_t b; memcpy(&b, &u, 8);
+  int m = (int)((b >> 52) & 0x7ff) - 1023;
+  b = (b & 0x000fffffffffffffull) | 0x3ff0000000000000ull; /* f in [1, 2) */
+  double f; memcpy(&f, &b, 8);
+  if (f > 0x1.6a09e667f3bcdp+0) { f = f * 0.5; m += 1; } /* f in [sqrt(1/2), sqrt(2)] */
+  double s = (f - 1.0) / (f + 1.0);
+  double s2 = s * s;
+  double p = 0x1.642c8590b2164p-5;
+  p = p * s2 + 0x1.8618618618618p-5;
+  p = p * s2 + 0x1.af286bca1af28p-5;
+  p = p * s2 + 0x1.e1e1e1e1e1e1ep-5;
+  p = p * s2 + 0x1.1111111111111p-4;
+  p = p * s2 + 0x1.3b13b13b13b14p-4;
+  p = p * s2 + 0x1.745d1745d1746p-4;
+  p = p * s2 + 0x1.c71c71c71c71cp-4;
+  p = p * s2 + 0x1.2492492492492p-3;
+  p = p * s2 + 0x1.999999999999ap-3;
+  p = p * s2 + 0x1.5555555555555p-2;
+  p = p * s2 + 1.0;
+  double lf = (2.0 * s) * p;
+  return (double)m * LN2_HI + ((double)m * LN2_LO + lf);
+}
+
+/* log1p(y) for y >= 0 (the only arguments softplus gives it) */
+float ox_log1pf(float y) {
+  if (y != y) return y;
+  if (y == INFINITY) return y;
+  double yd = (double)y;
+  if (yd < 0x1p-29) return (float)(yd - (yd * yd) * 0.5);
+  return (float)log_d(1.0 + yd);
+}
+
+float ox_silu(float x) { return x / (1.0f + ox_expf(-x)); }
+float ox_sigmoid(float x) { return 1.0f / (1.0f + ox_expf(-x)); }
+float ox_softplus(float x) { return x > 20.0f ? x : ox_log1pf(ox_expf(x)); }
+float ox_rsqrt(float x) { return 1.0f / sqrtf(x); }
+
+/* elementwise exports for the tests: fn 0 exp, 1 silu, 2 sigmoid, 3 softplus, 4 rsqrt,
+   5 log1p, 6 bf16 rounding */
+void ox_elem(int fn, const float* x, float* y, long n) {
+  for (long i = 0; i < n; i++) {
+    float v = x[i];
+    switch (fn) {
+      case 0: y[i] = ox_expf(v); break;
+      case 1: y[i] = ox_silu(v); break;
+      case 2: y[i] = ox_sigmoid(v); break;
+      case 3: y[i] = ox_softplus(v); break;
+      case 4: y[i] = ox_rsqrt(v); break;
+      case 5: y[i] = ox_log1pf(v); break;
+      default: y[i] = bf16r(v); break;
+    }
+  }
+}
+
+/* ------------------------------------------------------------------ canonical sums */
+
+/* the 512-lane sum of n values (n <= 512 * 64 is plenty for hidden sizes) */
+float ox_sum_h(const float* x, int n) {
+  float p[512], w[8];
+  for (int l = 0; l < 512; l++) {
+    float s = 0.0f;
+    for (int i = l; i < n; i += 512) s = s + x[i];
+    p[l] = s;
+  }
+  for (int g = 0; g < 8; g++) {
+    float* q = p + 64 * g;
+    for (int off = 32; off >= 1; off >>= 1)
+      for (int i = 0; i < off; i++) q[i] = q[i] + q[i + off];
+    w[g] = q[0];
+  }
+  for (int off = 4; off >= 1; off >>= 1)
+    for (int i = 0; i < off; i++) w[i] = w[i] + w[i + off];
+  return w[0];
+}
+
+/* the 64-lane sum of n values (a head's 128 or 256) */
+float ox_sum_64(const float* x, int n) {
+  float q[64];
+  for (int l = 0; l < 64; l++) {
+    float s = 0.0f;
+    for (int i = l; i < n; i += 64) s = s + x[i];
+    q[l] = s;
+  }
+  for (int off = 32; off >= 1; off >>= 1)
+    for (int i = 0; i < off; i++) q[i] = q[i] + q[i + off];
+  return q[0];
+}
+
+/* ------------------------------------------------------------------ the model */
+
+typedef struct {
+  int hidden, n_layers, nk, kd, nv, vd, conv, inter, vocab, bf16;
+  float rms_eps, gated_eps;
+} ox_dims;
+
+typedef struct { /* CSR: row r's entries ptr[r] .. ptr[r + 1] - 1, columns ascending */
+  int nrows, ncols;
+  const int64_t* ptr;
+  const int32_t* col;
+  const float* val;
+} ox_csr;
+
+typedef struct {
+  ox_csr qkv, z, b, a, out, gate, up, down;
+  const float* conv_w;  /* (n_conv, conv) */
+  const float* A_log;   /* (nv,) */
+  const float* dt_bias; /* (nv,) */
+  const float* gnorm;   /* (vd,) */
+  const float* ln_in;   /* (hidden,) raw weights w */
+  const float* ln_post;
+} ox_layer;
+
+typedef struct {
+  ox_dims d;
+  const ox_layer* layers;
+  ox_csr embed;             /* (vocab, hidden): the embedding, also the tied output head */
+  const float* final_norm;  /* (hidden,) */
+} ox_model;
+
+typedef struct {
+  float *xn, *P, *z, *b, *a, *y, *beta, *g, *qn, *kn, *o, *on, *out, *sq, *kv, *delta, *act,
+      *gt, *up, *logits;
+  int *proc;
+} ox_ws;
+
+static void* xalloc(size_t n) { void* p = calloc(n ? n : 1, 1); if (!p) abort(); return p; }
+
+static void ws_init(ox_ws* w, const ox_dims* d) {
+  int C = 2 * d->nk * d->kd + d->nv * d->vd;
+  w->xn = xalloc(4 * (size_t)d->hidden);
+  w->P = xalloc(4 * (size_t)C);
+  w->y = xalloc(4 * (size_t)C);
+  w->z = xalloc(4 * (size_t)d->nv * d->vd);
+  w->b = xalloc(4 * (size_t)d->nv);
+  w->a = xalloc(4 * (size_t)d->nv);
+  w->beta = xalloc(4 * (size_t)d->nv);
+  w->g = xalloc(4 * (size_t)d->nv);
+  w->qn = xalloc(4 * (size_t)d->nk * d->kd);
+  w->kn = xalloc(4 * (size_t)d->nk * d->kd);
+  w->o = xalloc(4 * (size_t)d->vd);
+  w->on = xalloc(4 * (size_t)d->nv * d->vd);
+  w->out = xalloc(4 * (size_t)d->hidden);
+  w->sq = xalloc(4 * (size_t)(d->kd > d->vd ? d->kd : d->vd));
+  w->kv = xalloc(4 * (size_t)d->vd);
+  w->delta = xalloc(4 * (size_t)d->vd);
+  w->act = xalloc(4 * (size_t)d->inter);
+  w->gt = xalloc(4 * (size_t)d->inter);
+  w->up = xalloc(4 * (size_t)d->inter);
+  w->logits = xalloc(4 * (size_t)d->vocab);
+  w->proc = xalloc(4 * (size_t)d->nv);
+}
+
+static void ws_free(ox_ws* w) {
+  void* ps[] = {w->xn, w->P, w->y, w->z, w->b, w->a, w->beta, w->g, w->qn, w->kn, w->o, w->on,
+                w->out, w->sq, w->kv, w->delta, w->act, w->gt, w->up, w->logits, w->proc};
+  for (size_t i = 0; i < sizeof(ps) / sizeof(ps[0]); i++) free(ps[i]);
+}
+
+/* out[r] = D(sum over row r's entries of x[col] * w), ascending columns, from +0 */
+static void csr_mv(const ox_csr* m, const float* x, float* out) {
+  for (int r = 0; r < m->nrows; r++) {
+    float s = 0.0f;
+    for (int64_t e = m->ptr[r]; e < m->ptr[r + 1]; e++) {
+      float xv = x[m->col[e]];
+      if (xv == 0.0f) continue;
+      s = s + xv * m->val[e];
+    }
+    out[r] = D(s);
+  }
+}
+
+/* Qwen3_5RMSNorm(h) (TF:720-737): r = rsqrt(mean(h^2) + eps); xn = D((h * r) * (1 + w)) */
+static void rms_norm(const float* h, int H, float eps, const float* w, float* sq, float* xn) {
+  for (int i = 0; i < H; i++) sq[i] = h[i] * h[i];
+  float ss = ox_sum_h(sq, H);
+  float r = ox_rsqrt(ss / (float)H + eps);
+  for (int i = 0; i < H; i++) xn[i] = D((h[i] * r) * (1.0f + w[i]));
+}
+
+/* sum over rows i of col[i * stride] * f[i] (f[i] != 0 only), in ATen's outer-sum cascade:
+   blocks of 16 rows, each from +0 in order, the block sums from +0 in order */
+static float row_sum(const float* col, int stride, const float* f, int n) {
+  float tot = 0.0f;
+  for (int b = 0; b < n; b += 16) {
+    float s = 0.0f;
+    int any = 0;
+    for (int i = b; i < b + 16 && i < n; i++) {
+      if (f[i] == 0.0f) continue;
+      s = s + col[(size_t)i * stride] * f[i];
+      any = 1;
+    }
+    if (any) tot = tot + s;
+  }
+  return tot;
+}
+
+/* l2norm(x) (TF:242-245) in the model dtype: x * rsqrt(sum(x * x) + 1e-6), each op rounded */
+static void l2norm_D(const float* x, int n, float* sq, float* out) {
+  for (int i = 0; i < n; i++) sq[i] = D(x[i] * x[i]);
+  float s = D(ox_sum_64(sq, n));
+  float inv = D(ox_rsqrt(D(s + 1e-6f)));
+  for (int i = 0; i < n; i++) out[i] = D(x[i] * inv);
+}
+
+/* one chip layer's decode step on the residual h (TF:753-793), updating its conv window cs
+   (n_conv, conv) and recurrent state S (nv, kd, vd) in place */
+static void layer_step(const ox_model* m, int L, float* h, float* cs, float* S, ox_ws* w,
+                       float* hsq) {
+  const ox_dims* d = &m->d;
+  const ox_layer* ly = &m->layers[L];
+  const int H = d->hidden, K = d->conv, kd = d->kd, vd = d->vd, nk = d->nk, nv = d->nv;
+  const int R = nv / nk, C = 2 * nk * kd + nv * vd;
+
+  /* ---- linear attention (TF:432-543) */
+  rms_norm(h, H, d->rms_eps, ly->ln_in, hsq, w->xn);
+  csr_mv(&ly->qkv, w->xn, w->P);
+  csr_mv(&ly->b, w->xn, w->b);
+  csr_mv(&ly->a, w->xn, w->a);
+  /* causal_conv1d_update (TF:199-216): window <- [window[1:], P]; y = silu(D(sum w_i x_i)) */
+  for (int c = 0; c < C; c++) {
+    float* win = cs + (size_t)c * K;
+    for (int i = 0; i + 1 < K; i++) win[i] = win[i + 1];
+    win[K - 1] = w->P[c];
+    const float* tw = ly->conv_w + (size_t)c * K;
+    float s = 0.0f;
+    for (int i = 0; i < K; i++) s = s + tw[i] * win[i];
+    w->y[c] = D(ox_silu(D(s)));
+  }
+  for (int v = 0; v < nv; v++) {
+    w->beta[v] = D(ox_sigmoid(w->b[v]));
+    float sp = ox_softplus(w->a[v] + ly->dt_bias[v]);
+    w->g[v] = (-ox_expf(ly->A_log[v])) * sp;
+  }
+  /* the recurrent step per value head (TF:330-380); query and key heads repeat R times */
+  int any_proc = 0;
+  for (int kh = 0; kh < nk; kh++) {
+    const float* q = w->y + (size_t)kh * kd;
+    const float* k = w->y + (size_t)nk * kd + (size_t)kh * kd;
+    int live = 0;
+    for (int i = 0; i < kd; i++) live |= (q[i] != 0.0f) | (k[i] != 0.0f);
+    float* qn = w->qn + (size_t)kh * kd;
+    float* kn = w->kn + (size_t)kh * kd;
+    if (live) {
+      l2norm_D(q, kd, w->sq, qn);
+      l2norm_D(k, kd, w->sq, kn);
+      for (int i = 0; i < kd; i++) qn[i] = qn[i] * 0.0625f; /* 1 / sqrt(256) */
+    }
+    for (int r = 0; r < R; r++) {
+      const int vh = kh * R + r;
+      float* Sv = S + (size_t)vh * kd * vd;
+      float* on = w->on + (size_t)vh * vd;
+      const float e = ox_expf(w->g[vh]);
+      w->proc[vh] = live || e != 1.0f;
+      for (int j = 0; j < vd; j++) on[j] = 0.0f;
+      if (!w->proc[vh]) continue; /* exp(g) = 1, q = k = 0: state and output unchanged */
+      if (e != 1.0f)
+        for (size_t i = 0; i < (size_t)kd * vd; i++) Sv[i] = Sv[i] * e;
+      if (!live) continue; /* q = 0: output exactly 0 */
+      const float* v = w->y + (size_t)2 * nk * kd + (size_t)vh * vd;
+      const float beta = w->beta[vh];
+      for (int j = 0; j < vd; j++) {
+        float s = row_sum(Sv + j, vd, kn, kd);
+        w->kv[j] = s;
+        w->delta[j] = (v[j] - s) * beta;
+      }
+      for (int i = 0; i < kd; i++) {
+        if (kn[i] == 0.0f) continue;
+        for (int j = 0; j < vd; j++) Sv[(size_t)i * vd + j] = Sv[(size_t)i * vd + j] + kn[i] * w->delta[j];
+      }
+      for (int j = 0; j < vd; j++) w->o[j] = D(row_sum(Sv + j, vd, qn, kd));
+      any_proc = 1;
+      /* Qwen3_5RMSNormGated (TF:168-184) on this value head, gate z */
+      w->proc[vh] = 2;
+      for (int j = 0; j < vd; j++) w->sq[j] = w->o[j] * w->o[j];
+      float ss = ox_sum_64(w->sq, vd);
+      float rr = ox_rsqrt(ss / (float)vd + d->gated_eps);
+      float zrow[256];
+      for (int j = 0; j < vd; j++) { /* in_proj_z rows of this head */
+        const ox_csr* zm = &ly->z;
+        int row = vh * vd + j;
+        float s = 0.0f;
+        for (int64_t e2 = zm->ptr[row]; e2 < zm->ptr[row + 1]; e2++) {
+          float xv = w->xn[zm->col[e2]];
+          if (xv == 0.0f) continue;
+          s = s + xv * zm->val[e2];
+        }
+        zrow[j] = D(s);
+      }
+      for (int j = 0; j < vd; j++) {
+        float t1 = D(w->o[j] * rr);
+        float t2 = D(ly->gnorm[j] * t1);
+        on[j] = D(t2 * ox_silu(zrow[j]));
+      }
+    }
+  }
+  /* out_proj, then the residual add (all rows: a row with no term adds +0) */
+  if (any_proc) {
+    csr_mv(&ly->out, w->on, w->out);
+  } else {
+    for (int i = 0; i < H; i++) w->out[i] = 0.0f;
+  }
+  for (int i = 0; i < H; i++) h[i] = D(h[i] + w->out[i]);
+
+  /* ---- MLP (TF:704-717) */
+  rms_norm(h, H, d->rms_eps, ly->ln_post, hsq, w->xn);
+  csr_mv(&ly->gate, w->xn, w->gt);
+  csr_mv(&ly->up, w->xn, w->up);
+  for (int u = 0; u < d->inter; u++) w->act[u] = D(D(ox_silu(w->gt[u])) * w->up[u]);
+  csr_mv(&ly->down, w->act, w->out);
+  for (int i = 0; i < H; i++) h[i] = D(h[i] + w->out[i]);
+}
+
+/* the final norm and the tied head's first maximum (NaN counts as the maximum, as
+   torch.argmax takes it) */
+static int head_argmax(const ox_model* m, const float* h, ox_ws* w, float* hsq) {
+  const ox_dims* d = &m->d;
+  rms_norm(h, d->hidden, d->rms_eps, m->final_norm, hsq, w->xn);
+  csr_mv(&m->embed, w->xn, w->logits);
+  int best = 0;
+  float bv = w->logits[0];
+  for (int v = 1; v < d->vocab; v++) {
+    float x = w->logits[v];
+    if (bv != bv) break;
+    if (x != x || x > bv) { bv = x; best = v; }
+  }
+  return best;
+}
+
+/* The residual stream of token tok: its embedding row (D values). */
+static void embed_row(const ox_model* m, int tok, float* h) {
+  const ox_csr* e = &m->embed;
+  for (int i = 0; i < m->d.hidden; i++) h[i] = 0.0f;
+  for (int64_t k = e->ptr[tok]; k < e->ptr[tok + 1]; k++) h[e->col[k]] = e->val[k];
+}
+
+/* n greedy decode steps: step i's input is forced[i] (i < n_forced) or step i - 1's
+   prediction (lx/lx/mega.py:529-535). conv (n_layers, n_conv, conv) and rec (n_layers, nv, kd,
+   vd) are updated in place. trace (optional, n x n_layers x hidden): the residual after each
+   layer. Returns 0, or -1 on a token id out of range. */
+int ox_decode(const ox_model* m, float* conv, float* rec, const int* forced, int n_forced, int n,
+              int* preds, int* inputs, float* trace) {
+  const ox_dims* d = &m->d;
+  g_bf16 = d->bf16;
+  const int H = d->hidden, C = 2 * d->nk * d->kd + d->nv * d->vd;
+  ox_ws w;
+  ws_init(&w, d);
+  float* h = xalloc(4 * (size_t)H);
+  float* hsq = xalloc(4 * (size_t)H);
+  int tok = n_forced > 0 ? forced[0] : 0, rc = 0;
+  for (int i = 0; i < n; i++) {
+    if (tok < 0 || tok >= d->vocab) { rc = -1; break; }
+    if (inputs) inputs[i] = tok;
+    embed_row(m, tok, h);
+    for (int L = 0; L < d->n_layers; L++) {
+      layer_step(m, L, h, conv + (size_t)L * C * d->conv, rec + (size_t)L * d->nv * d->kd * d->vd,
+                 &w, hsq);
+      if (trace) memcpy(trace + ((size_t)i * d->n_layers + L) * H, h, 4 * (size_t)H);
+    }
+    int p = head_argmax(m, h, &w, hsq);
+    preds[i] = p;
+    tok = i + 1 < n_forced ? forced[i + 1] : p;
+  }
+  free(h);
+  free(hsq);
+  ws_free(&w);
+  return rc;
+}
+
+/* One layer's step on a given residual h (in place) -- the per-layer comparison against the
+   stock decoder layer. */
+void ox_layer_step(const ox_model* m, int L, float* h, float* conv_L, float* rec_L) {
+  g_bf16 = m->d.bf16;
+  ox_ws w;
+  ws_init(&w, &m->d);
+  float* hsq = xalloc(4 * (size_t)m->d.hidden);
+  layer_step(m, L, h, conv_L, rec_L, &w, hsq);
+  free(hsq);
+  ws_free(&w);
+}
+
+/* The head on residual rows h (T, hidden): logits (T, vocab) if given, and the argmax. */
+void ox_head(const ox_model* m, const float* h, int T, float* logits, int* pred) {
+  g_bf16 = m->d.bf16;
+  ox_ws w;
+  ws_init(&w, &m->d);
+  float* hsq = xalloc(4 * (size_t)m->d.hidden);
+  for (int t = 0; t < T; t++) {
+    pred[t] = head_argmax(m, h + (size_t)t * m->d.hidden, &w, hsq);
+    if (logits) memcpy(logits + (size_t)t * m->d.vocab, w.logits, 4 * (size_t)m->d.vocab);
+  }
+  free(hsq);
+  ws_free(&w);
+}
