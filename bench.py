@@ -1,0 +1,167 @@
+"""Benchmark: greedy decode tok/s of the 37-layer synthetic sparse chip stack on one MI355X.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--tokens T] [--config c2]
+
+A step is one launch of the persistent decode kernel over one chunk of T tokens (default
+262,144), continuing the same greedy stream launch after launch, as
+lx/tools/mega_boot.py runs the boot in 262,144-token launches. The model is the seeded synthetic
+stack (synth.config2: 37 layers, hidden 3572, bf16, 0.08 % density, N(0,1) state); it is built
+and packed on the host, then every input is resident in HBM before the timed region.
+
+One JSON line on stdout (the driver's contract); everything else goes to stderr.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, HERE)
+
+METRIC = "greedy decode tok/s, 37-layer sparse chip stack, 1 MI355X"
+HBM_PEAK_GBS = 8000.0
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def survey_bytes_per_token(model, f_out: float) -> float:
+    """The algorithmic bytes of one decoded token, SURVEY 8(d)'s formula for config 2:
+    sum over layers of 4 B per nonzero of in_proj_qkv, b, a, gate, up, down, plus 4 B x the
+    fraction of layer-steps with output x (in_proj_z + out_proj nonzeros), plus 16 B per live
+    conv channel (window read + write), plus 4 B per head nonzero, plus the 2 B x hidden
+    embedding row. (The recurrent-state term is left out: at ~2 % activity it is < 1 %.)"""
+    import numpy as np
+
+    tot = 0.0
+    w1 = np.float32(1.0) + np.asarray(model.norm, np.float32)
+    for ly in model.layers:
+        tot += 4 * (ly.in_proj_qkv.nnz + ly.in_proj_b.nnz + ly.in_proj_a.nnz +
+                    ly.gate_proj.nnz + ly.up_proj.nnz + ly.down_proj.nnz)
+        tot += 4 * f_out * (ly.in_proj_z.nnz + ly.out_proj.nnz)
+        live = int((np.asarray(ly.conv1d) != 0).any(1).sum())
+        tot += 16 * live
+    hk = np.nonzero(w1 != 0)[0]
+    mask = np.zeros(model.dims.hidden, bool)
+    mask[hk] = True
+    tot += 4 * int(mask[model.embed.cols].sum())
+    tot += 2 * model.dims.hidden
+    return tot
+
+
+def cpu_baseline(model, conv0, rec0, start: int, n: int):
+    """The C oracle (a single-threaded port of the stock decode) on the first n tokens."""
+    from oracle import oracle as ox
+
+    ox.build()
+    om = ox.OracleModel(model)
+    c, r = conv0.copy(), rec0.copy()
+    om.decode(c, r, [start], 2)  # warm-up (page-in)
+    c, r = conv0.copy(), rec0.copy()
+    t = time.perf_counter()
+    preds, _, _ = om.decode(c, r, [start], n)
+    dt = time.perf_counter() - t
+    return n / dt, preds
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=1)
+    ap.add_argument("--warmup", type=int, default=1)
+    ap.add_argument("--tokens", type=int, default=262_144)
+    ap.add_argument("--warmup-tokens", type=int, default=4096)
+    ap.add_argument("--config", default="c2", choices=["c1", "c2", "c5", "small"])
+    ap.add_argument("--cpu-tokens", type=int, default=128, help="CPU baseline sample (0: skip)")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU: the decode is one sequential chain per stream and this "
+              f"build runs on a single MI355X (asked for --gpus {args.gpus}).", file=sys.stderr)
+        return 2
+
+    import numpy as np
+    import torch
+
+    from linuxformer_amd import fast, mega, synth
+
+    spec = {"c1": synth.config1(), "c2": synth.config2(), "c5": synth.config5(),
+            "small": synth.small()}[args.config]
+    t0 = time.time()
+    model = synth.build(spec)
+    conv0, rec0 = synth.init_state(model)
+    start = synth.start_token(spec)
+    f = fast.Fast(model)
+    dev = torch.device("cuda", 0)
+    cache = fast.StateCache(conv0, rec0, model.dims.dtype, dev)
+    mg = mega.Mega(f, model, cache, 0)
+    torch.cuda.synchronize()
+    log(f"[bench] {spec.name}: built and packed in {time.time() - t0:.1f}s; "
+        f"{json.dumps({k: v for k, v in mg.stats.items() if not isinstance(v, list)})}")
+
+    stream = torch.cuda.current_stream(dev)
+    # warm-up launches continue the stream from the start token; their first predictions are
+    # checked against the CPU oracle below
+    tok = start
+    first_preds = None
+    for w in range(args.warmup):
+        preds = mg.run([tok], args.warmup_tokens)
+        if first_preds is None:
+            first_preds = preds
+        tok = preds[-1]
+        log(f"[bench] warm-up launch {w + 1}/{args.warmup}: {args.warmup_tokens} tokens")
+    torch.cuda.synchronize()
+    # timed: K launches of T tokens, events on the launch stream around each
+    evs = []
+    t_start = time.perf_counter()
+    for k in range(args.steps):
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        preds = mg.run([tok], args.tokens)
+        e1.record(stream)
+        evs.append((e0, e1))
+        tok = preds[-1]
+        log(f"[bench] timed launch {k + 1}/{args.steps}: {args.tokens} tokens, "
+            f"distinct predictions {len(set(preds))}")
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t_start
+    kern_ms = sum(a.elapsed_time(b) for a, b in evs) / len(evs)
+    n_tok = args.steps * args.tokens
+    value = n_tok / wall
+    # roofline: SURVEY 8(d)'s algorithmic bytes per token x tokens per launch / launch time
+    b_tok = survey_bytes_per_token(model, spec.p_gate)
+    achieved = b_tok * args.tokens / (kern_ms * 1e-3) / 1e9
+    out = {
+        "metric": METRIC, "value": round(value, 1), "unit": "tok/s", "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(wall * 1e3 / args.steps, 3),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16" if model.dims.dtype == "bf16" else "fp32",
+        "data": "synthetic (seeded config stack, random weights and state; no checkpoint)",
+        "config": {"workload": f"{spec.name}: {model.dims.n_layers}-layer synthetic sparse chip stack, "
+                               f"hidden {model.dims.hidden}, vocab {model.dims.vocab}, greedy decode "
+                               f"chunks of {args.tokens} tokens at batch 1",
+                   "tokens_per_step": args.tokens, "batch": 1, "p_gate": spec.p_gate,
+                   "density": spec.density, "parallelism": "single GPU (one chain workgroup + "
+                   f"{mg.ncta - 1} head workgroups)"},
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 5), "traffic": None,
+                     "bytes_per_token": round(b_tok), "kernel_ms_per_launch": round(kern_ms, 3)},
+    }
+    if args.cpu_tokens > 0:
+        cps, cpreds = cpu_baseline(model, conv0, rec0, start, args.cpu_tokens)
+        m = min(len(cpreds), len(first_preds or []))
+        match = bool(m > 0 and list(cpreds[:m]) == list(first_preds[:m]))
+        out["cpu_baseline"] = {"value": round(cps, 2), "unit": "tok/s", "cores": 1, "kind": "port",
+                               "sample": f"first {args.cpu_tokens} tokens of the {spec.name} stream "
+                                         f"(C oracle, one thread)"}
+        out["check"] = {"oracle_tokens": m, "preds_match": match}
+    print(json.dumps(out), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -105,6 +105,7 @@ typedef struct lxm_params {
   uint32_t* sync;          /* LXM_NSYNC words, zero at launch */
   unsigned long long* keys;/* (2), zero at launch */
   int32_t* err;            /* (1), zero at launch; nonzero: a spin timed out (1..) */
+  unsigned long long* prof; /* null, or 32 + 2 x n_blocks counters (phase cycles, see the kernel) */
   int32_t n_qk_total, pad;
 } lxm_params;
 

@@ -64,7 +64,8 @@ using namespace lxm;
 #define L_BETA (L_EV + 4 * 256)
 #define L_WSUM (L_BETA + 4 * RMAX)
 #define L_FLAGS (L_WSUM + 4 * 32)
-#define L_CHAIN_END (L_FLAGS + 4 * 256)
+#define L_PROF (L_FLAGS + 4 * 256)
+#define L_CHAIN_END (L_PROF + 8 * 32)
 // flags (int): [0] any head active, [1] any output, [2] nq, [3] nk, [4] scratch, [8] token
 // [16 + kh] per key head: bit 0 query nonzero, bit 1 key nonzero, bit 2 decay
 #define F_ANY 0
@@ -121,6 +122,14 @@ __device__ __forceinline__ void lds_barrier() {
   __builtin_amdgcn_s_barrier();
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
 }
+
+// In-kernel phase counters (lx/csrc/mega.cu's prof buffer and MK_SUBPROF checkpoints): with
+// p.prof set, thread 0 of the chain adds the shader-clock cycles of each phase into an LDS
+// slot; the slots are written to p.prof at the end. Phases: 0 embedding, 1 layer staging,
+// 2 GDN norm + gates, 3 active heads, 4 MLP, 5 trace, 6 final norm + publish, 7 waiting for the
+// head's argmax; counters 16 active layer-steps, 17 tokens.
+#define PROF_ON (p.prof != nullptr)
+__device__ __forceinline__ uint64_t cycles() { return __builtin_readcyclecounter(); }
 
 // spin (one thread) until *p >= target; false on timeout or another block's error
 __device__ bool spin_ge(const uint32_t* p, uint32_t target, int32_t* err, int code) {
@@ -382,9 +391,21 @@ __device__ __forceinline__ float layer(const lxm_params& p, int L, int step, flo
   lds_barrier();
   if (t < p.nk && flags[F_KH + t]) atomicOr(&flags[F_ANY], 1);
   lds_barrier();
+  uint64_t* pa = reinterpret_cast<uint64_t*>(smem + L_PROF);
+  uint64_t c0 = 0;
+  if (PROF_ON && t == 0) {
+    c0 = cycles();
+    pa[2] += c0 - pa[15];
+  }
   if (flags[F_ANY]) {
     gdn_active<BF, E4>(p, L, step, r1);
     if (flags[F_OUT]) ss = hidden_ss(H);
+    if (PROF_ON && t == 0) {
+      const uint64_t c1 = cycles();
+      pa[3] += c1 - c0;
+      pa[16] += 1;
+      c0 = c1;
+    }
   }
   // ---- MLP (:788-791; Qwen3_5MLP :715)
   const float r2 = norm_r(ss, H, hd.eps);
@@ -413,7 +434,13 @@ __device__ __forceinline__ float layer(const lxm_params& p, int L, int step, flo
       s2 = s2 + hv * hv;
     }
   }
-  return sum512(s2, LF(L_WSUM));
+  const float ssn = sum512(s2, LF(L_WSUM));
+  if (PROF_ON && t == 0) {
+    const uint64_t c1 = cycles();
+    pa[4] += c1 - c0;
+    pa[15] = c1;
+  }
+  return ssn;
 }
 
 // The delta rule for the layer's active key heads (torch_recurrent_gated_delta_rule :330-380
@@ -536,7 +563,13 @@ __device__ void gdn_active(const lxm_params& p, int L, int step, float r1) {
       float* S = S0 + (size_t)vh * KD * VD;
       const float e = ev[vh];
       if (e != 1.0f)
-        for (int i = 0; i < KD; i++) S[(size_t)i * VD + j] = S[(size_t)i * VD + j] * e;
+        for (int i0 = 0; i0 < KD; i0 += 16) {  // 16 loads in flight, then the stores
+          float v[16];
+#pragma unroll
+          for (int k = 0; k < 16; k++) v[k] = S[(size_t)(i0 + k) * VD + j];
+#pragma unroll
+          for (int k = 0; k < 16; k++) S[(size_t)(i0 + k) * VD + j] = v[k] * e;
+        }
       if (nk > 0) {
         const float kv = row_cascade(S, j, nzk, nk, kn);
         const float dl = (vb[r * VD + j] - kv) * beta[r];
@@ -618,11 +651,15 @@ __device__ void run_chain(const lxm_params& p) {
     n16s[L] = reinterpret_cast<const lxm_hot*>(p.blob + p.layers[L].hot)->size / 16;
   __syncthreads();
   Pf pf = fetch(p, 0, n16s[0]);
+  uint64_t* pa = reinterpret_cast<uint64_t*>(smem + L_PROF);
+  if (t < 32) pa[t] = 0;
+  __syncthreads();
   int tok = p.forced[0];
   const uint32_t nh = (uint32_t)(p.n_blocks - 1);
   for (int i = 0; i < p.n_tokens; i++) {
     if (tok < 0 || tok >= p.vocab) tok = 0;  // the host checks forced tokens; preds are in range
     if (t == 0 && p.inputs) p.inputs[i] = tok;
+    if (PROF_ON && t == 0) pa[15] = cycles();
     // the input's embedding row
     for (int c = t; c < H; c += NT) h[c] = 0.0f;
     lds_barrier();
@@ -637,17 +674,32 @@ __device__ void run_chain(const lxm_params& p) {
     }
     lds_barrier();
     float ss = hidden_ss(H);
+    if (PROF_ON && t == 0) {
+      const uint64_t c = cycles();
+      pa[0] += c - pa[15];
+      pa[15] = c;
+    }
     for (int L = 0; L < p.n_layers; L++) {
       stage(n16s[L], pf);
       lds_barrier();
       const int Ln = L + 1 < p.n_layers ? L + 1 : 0;
       pf = fetch(p, Ln, n16s[Ln]);
+      if (PROF_ON && t == 0) {
+        const uint64_t c = cycles();
+        pa[1] += c - pa[15];
+        pa[15] = c;
+      }
       ss = layer<BF, E4>(p, L, i, ss);
       if (p.trace) {
         float* tr = p.trace + ((size_t)i * p.n_layers + L) * H;
         for (int c = t; c < H; c += NT) tr[c] = h[c];
       }
       lds_barrier();
+      if (PROF_ON && t == 0) {
+        const uint64_t c = cycles();
+        pa[5] += c - pa[15];
+        pa[15] = c;
+      }
     }
     // the final norm (lx/lx/hf.py:179-184: model.norm then the tied head), to the helpers
     {
@@ -656,6 +708,11 @@ __device__ void run_chain(const lxm_params& p) {
     }
     drain();
     __syncthreads();
+    if (PROF_ON && t == 0) {
+      const uint64_t c = cycles();
+      pa[6] += c - pa[15];
+      pa[15] = c;
+    }
     if (t == 0) {
       st_rlx(p.sync + S_TOKFLAG, (uint32_t)(i + 1));
       bool ok = spin_ge(p.sync + S_COUNT, nh * (uint32_t)(i + 1), p.err, 1);
@@ -669,11 +726,18 @@ __device__ void run_chain(const lxm_params& p) {
       }
       flags[F_OK] = ok;
       flags[F_TOK] = pred;
+      if (PROF_ON) {
+        const uint64_t c = cycles();
+        pa[7] += c - pa[15];
+        pa[15] = c;
+        pa[17] += 1;
+      }
     }
     __syncthreads();
     if (!flags[F_OK]) return;
     tok = i + 1 < p.n_forced ? p.forced[i + 1] : flags[F_TOK];
   }
+  if (PROF_ON && t < 32) p.prof[t] = pa[t];
   // every ring write visible to the other blocks, then let them write the conv windows
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
   __syncthreads();
@@ -698,10 +762,16 @@ __device__ void run_helper(const lxm_params& p) {
     for (int64_t k = t; k < ne * (Ent<E4>::SZ / 4); k += NT) dst[k] = src[k];
   }
   __syncthreads();
+  uint64_t hw = 0, hc = 0, hc0 = 0;
   for (int i = 0; i < p.n_tokens; i++) {
+    const uint64_t w0 = (PROF_ON && t == 0) ? cycles() : 0;
     if (t == 0) *ok = spin_ge(p.sync + S_TOKFLAG, (uint32_t)(i + 1), p.err, 2);
     __syncthreads();
     if (!*ok) return;
+    if (PROF_ON && t == 0) {
+      hc0 = cycles();
+      hw += hc0 - w0;
+    }
     for (int c = t; c < H; c += NT) hn[c] = ld_rlxf(p.hn + c);
     __syncthreads();
     unsigned long long best = 0;
@@ -721,7 +791,12 @@ __device__ void run_helper(const lxm_params& p) {
       __hip_atomic_fetch_max(p.keys + (i & 1), best, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       drain();
       __hip_atomic_fetch_add(p.sync + S_COUNT, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if (PROF_ON) hc += cycles() - hc0;
     }
+  }
+  if (PROF_ON && t == 0) {
+    p.prof[32 + 2 * blockIdx.x] = hw;
+    p.prof[33 + 2 * blockIdx.x] = hc;
   }
   if (t == 0) *ok = spin_ge(p.sync + S_DONE, 1u, p.err, 3);
   __syncthreads();

@@ -59,7 +59,8 @@ class Params(ctypes.Structure):
         [(n, PTR) for n in ("layers", "blob", "rec", "conv", "emb_ptr", "emb_ent", "w1_final",
                             "head_rows", "head_ptr", "head_ent", "forced")] + \
         [("n_forced", I32), ("n_tokens", I32)] + \
-        [(n, PTR) for n in ("preds", "inputs", "trace", "ring", "hn", "sync", "keys", "err")] + \
+        [(n, PTR) for n in ("preds", "inputs", "trace", "ring", "hn", "sync", "keys", "err",
+                            "prof")] + \
         [("n_qk_total", I32), ("pad", I32)]
 
 
@@ -356,6 +357,24 @@ class Mega:
                            "blob_bytes": int(self.blob.numel()), "qk_total": qk_total,
                            "head_nnz": int(hptr[-1]), "vocab": V})
 
+    PHASES = ("embedding", "layer staging", "GDN norm + gates", "active heads", "MLP", "trace",
+              "final norm + publish", "head argmax wait")
+
+    def phase_report(self, prof: torch.Tensor) -> dict:
+        """prof counters -> cycles per token of each chain phase, and the helpers' mean cycles
+        per token waiting for the flag and computing their rows."""
+        c = prof.cpu().tolist()
+        n = max(c[17], 1)
+        out = {name: round(c[k] / n, 1) for k, name in enumerate(self.PHASES)}
+        out["active layer-steps per token"] = round(c[16] / n, 3)
+        hw = [c[32 + 2 * b] for b in range(1, self.ncta)]
+        hc = [c[33 + 2 * b] for b in range(1, self.ncta)]
+        out["helper wait"] = round(sum(hw) / len(hw) / n, 1)
+        out["helper compute"] = round(sum(hc) / len(hc) / n, 1)
+        out["helper compute max"] = round(max(hc) / n, 1)
+        out["tokens"] = n
+        return out
+
     def _state_ptrs(self):
         rs, cs = [], []
         d = self.dims
@@ -380,7 +399,8 @@ class Mega:
         """n steps; step i's input is forced[i] (i < len(forced)) or step i - 1's prediction.
         Returns the n predictions (chip token ids). inputs (n,) int32: each step's input as the
         kernel embedded it. trace (n, n_layers, hidden) float32: the residual after each
-        layer of each step."""
+        layer of each step. prof (32 + 2 x ncta) int64: phase cycle counters (see
+        ``phase_report``)."""
         assert len(forced) >= 1 and n >= 1
         f = np.asarray(forced, np.int64)
         if f.min() < 0 or f.max() >= self.vocab:
@@ -391,6 +411,9 @@ class Mega:
         preds = torch.zeros(n, dtype=torch.int32, device=self.dev)
         if inputs is not None:
             assert inputs.dtype == torch.int32 and inputs.numel() >= n and inputs.device == self.dev
+        if prof is not None:
+            assert prof.dtype == torch.int64 and prof.numel() >= 32 + 2 * self.ncta
+            assert prof.device == self.dev
         if trace is not None:
             assert trace.dtype == torch.float32 and trace.is_contiguous()
             assert trace.numel() >= n * d.n_layers * d.hidden and trace.device == self.dev
@@ -409,7 +432,9 @@ class Mega:
                    inputs=inputs.data_ptr() if inputs is not None else None,
                    trace=trace.data_ptr() if trace is not None else None,
                    ring=self.ring.data_ptr(), hn=self.hn.data_ptr(), sync=self.sync.data_ptr(),
-                   keys=self.keys.data_ptr(), err=self.err.data_ptr(), n_qk_total=self.n_qk_total)
+                   keys=self.keys.data_ptr(), err=self.err.data_ptr(),
+                   prof=prof.data_ptr() if prof is not None else None,
+                   n_qk_total=self.n_qk_total)
         pd = torch.frombuffer(bytearray(bytes(p)), dtype=torch.uint8).to(self.dev)
         self._keep = (rs, cs, ft, pd)
         st = ctypes.c_void_p(torch.cuda.current_stream(self.dev).cuda_stream)

@@ -12,10 +12,10 @@ Write gates. Most chip layer-steps leave the recurrent state and the residual st
 real chip's decode touches ~4.5 state rows per token (lx/results/head_activity.json). The
 synthetic stacks reproduce that with one *gate column* per layer at the top of the residual
 stream: a layer's query, key and decay projections read only its gate column, no projection
-writes gate columns, and a token's embedding row sets the gate column of layer L with
-probability ``p_gate`` (seeded). A layer-step therefore has a nonzero query, key or decay only
-when its input tokens carry that layer's gate, i.e. on about ``p_gate`` of layer-steps whatever
-the greedy stream does (the final norm weight is -1 on gate columns, so the head's argmax never
+writes gate columns, and a token's embedding row sets the gate columns of p_gate x n_layers
+seeded layers (config 2: exactly one). A layer-step therefore has a nonzero query, key or decay
+only when its input tokens carry that layer's gate, i.e. on about ``p_gate`` of layer-steps
+whatever tokens the greedy stream visits (the final norm weight is -1 on gate columns, so the head's argmax never
 sees them). Everything else is uniform at the configured density, except that a SwiGLU unit's
 up_proj row reads the same (seeded, uniform) columns as its gate_proj row, so that units fire
 and the residual stream mixes across layers.
@@ -132,7 +132,8 @@ class Spec:
     dims: Dims
     seed: int = 0
     density: float = 0.0008
-    p_gate: float = 0.02  # per (token, layer): the token's embedding sets the layer's gate
+    p_gate: float = 0.02  # gated fraction of (token, layer) pairs; each token gates p_gate x
+    # n_layers layers (rounded up or down at random), so config 2's tokens gate one layer each
     p_live: float = 0.25  # per key head: reads the gate (query/key rows)
     p_decay: float = 0.25  # per value head of a live key head: in_proj_a reads the gate
     p_tap: float = 0.1  # per earlier conv tap of a live channel
@@ -152,9 +153,10 @@ def config1(seed: int = 1) -> Spec:
 
 
 def config2(seed: int = 2) -> Spec:
-    """the 37-layer synthetic chip stack, bf16, N(0,1) state, 2% gates."""
+    """the 37-layer synthetic chip stack, bf16, N(0,1) state; every token
+    gates exactly one layer (1/37 = 2.7 % of layer-steps, BASELINE's "about 2 %")."""
     return Spec("c2", Dims(hidden=3572, n_layers=37, vocab=459_982, dtype="bf16"), seed=seed,
-                state="normal", n_steps=262_144)
+                state="normal", n_steps=262_144, p_gate=1.0 / 37)
 
 
 def config5(seed: int = 2) -> Spec:
@@ -268,14 +270,16 @@ def build(spec: Spec) -> SparseModel:
         if V <= 4096 else _distinct_cols(re, V, hng, k)
     rows = np.repeat(np.arange(V), k)
     vals = re.choice(VALS, size=V * k)
+    # gates: token v sets the gate columns of k_v seeded layers, k_v = floor(g) or floor(g) + 1
+    # with mean g = p_gate * n_layers, so every token carries (almost) the same number of gates
+    # and the stream's gate rate is p_gate whatever tokens the greedy decode visits
     rg = _rng(s, 0, _GEMB)
-    gr, gc = [], []
-    for L in range(d.n_layers):
-        on = np.nonzero(rg.random(V) < spec.p_gate)[0]
-        gr.append(on)
-        gc.append(np.full(len(on), hng + L))
-    gr = np.concatenate(gr) if gr else np.zeros(0, np.int64)
-    gc = np.concatenate(gc) if gc else np.zeros(0, np.int64)
+    g = spec.p_gate * d.n_layers
+    k = np.floor(g).astype(np.int64) + (rg.random(V) < g - np.floor(g))
+    order = np.argsort(rg.random((V, d.n_layers)), axis=1)
+    on = np.arange(d.n_layers)[None, :] < k[:, None]
+    gr = np.repeat(np.arange(V), on.sum(1))
+    gc = hng + order[on]
     embed = Coo.build((V, H), np.concatenate([rows, gr]), np.concatenate([cols.reshape(-1), gc]),
                       np.concatenate([vals, rg.choice(VALS, size=len(gr))]))
     # final norm: weight 0 or -2 (1 + w = +-1) outside the gates, -1 on them (the head ignores

@@ -235,7 +235,7 @@ static void ws_init(ox_ws* w, const ox_dims* d) {
   w->g = xalloc(4 * (size_t)d->nv);
   w->qn = xalloc(4 * (size_t)d->nk * d->kd);
   w->kn = xalloc(4 * (size_t)d->nk * d->kd);
-  w->o = xalloc(4 * (size_t)d->vd);
+  w->o = xalloc(4 * (size_t)d->nv * d->vd);
   w->on = xalloc(4 * (size_t)d->nv * d->vd);
   w->out = xalloc(4 * (size_t)d->hidden);
   w->sq = xalloc(4 * (size_t)(d->kd > d->vd ? d->kd : d->vd));
@@ -300,6 +300,58 @@ static void l2norm_D(const float* x, int n, float* sq, float* out) {
   for (int i = 0; i < n; i++) out[i] = D(x[i] * inv);
 }
 
+/* torch_recurrent_gated_delta_rule (TF:330-380) for one token, use_qk_l2norm_in_kernel: q, k
+   (nk, kd) and v (nv, vd) in the model dtype, g (nv) fp32, beta (nv) model dtype, the state S
+   (nv, kd, vd) fp32 updated in place; value head vh reads key head vh / (nv / nk) (the stock
+   repeat_interleave). Outputs o (nv, vd) in the model dtype into w->o; w->proc[vh] is 0 for a
+   head the step leaves alone (exp(g) = 1, q = k = 0: state unchanged, output exactly 0), 1 for a
+   decay only, 2 for a head with a live query or key. Returns whether any head had one. */
+static int rec_heads(const ox_dims* d, const float* qall, const float* kall, const float* vall,
+                     const float* g, const float* betas, float* S, ox_ws* w) {
+  const int kd = d->kd, vd = d->vd, nk = d->nk, nv = d->nv, R = nv / nk;
+  int any = 0;
+  for (int kh = 0; kh < nk; kh++) {
+    const float* q = qall + (size_t)kh * kd;
+    const float* k = kall + (size_t)kh * kd;
+    int live = 0;
+    for (int i = 0; i < kd; i++) live |= (q[i] != 0.0f) | (k[i] != 0.0f);
+    float* qn = w->qn + (size_t)kh * kd;
+    float* kn = w->kn + (size_t)kh * kd;
+    if (live) {
+      l2norm_D(q, kd, w->sq, qn);
+      l2norm_D(k, kd, w->sq, kn);
+      for (int i = 0; i < kd; i++) qn[i] = qn[i] * 0.0625f; /* 1 / sqrt(256) */
+    }
+    for (int r = 0; r < R; r++) {
+      const int vh = kh * R + r;
+      float* Sv = S + (size_t)vh * kd * vd;
+      float* o = w->o + (size_t)vh * vd;
+      const float e = ox_expf(g[vh]);
+      w->proc[vh] = live || e != 1.0f;
+      for (int j = 0; j < vd; j++) o[j] = 0.0f;
+      if (!w->proc[vh]) continue;
+      if (e != 1.0f)
+        for (size_t i = 0; i < (size_t)kd * vd; i++) Sv[i] = Sv[i] * e;
+      if (!live) continue; /* q = 0: output exactly 0 */
+      const float* v = vall + (size_t)vh * vd;
+      const float beta = betas[vh];
+      for (int j = 0; j < vd; j++) {
+        float s = row_sum(Sv + j, vd, kn, kd);
+        w->kv[j] = s;
+        w->delta[j] = (v[j] - s) * beta;
+      }
+      for (int i = 0; i < kd; i++) {
+        if (kn[i] == 0.0f) continue;
+        for (int j = 0; j < vd; j++) Sv[(size_t)i * vd + j] = Sv[(size_t)i * vd + j] + kn[i] * w->delta[j];
+      }
+      for (int j = 0; j < vd; j++) o[j] = D(row_sum(Sv + j, vd, qn, kd));
+      w->proc[vh] = 2;
+      any = 1;
+    }
+  }
+  return any;
+}
+
 /* one chip layer's decode step on the residual h (TF:753-793), updating its conv window cs
    (n_conv, conv) and recurrent state S (nv, kd, vd) in place */
 static void layer_step(const ox_model* m, int L, float* h, float* cs, float* S, ox_ws* w,
@@ -307,7 +359,7 @@ static void layer_step(const ox_model* m, int L, float* h, float* cs, float* S, 
   const ox_dims* d = &m->d;
   const ox_layer* ly = &m->layers[L];
   const int H = d->hidden, K = d->conv, kd = d->kd, vd = d->vd, nk = d->nk, nv = d->nv;
-  const int R = nv / nk, C = 2 * nk * kd + nv * vd;
+  const int C = 2 * nk * kd + nv * vd;
 
   /* ---- linear attention (TF:432-543) */
   rms_norm(h, H, d->rms_eps, ly->ln_in, hsq, w->xn);
@@ -330,65 +382,35 @@ static void layer_step(const ox_model* m, int L, float* h, float* cs, float* S, 
     w->g[v] = (-ox_expf(ly->A_log[v])) * sp;
   }
   /* the recurrent step per value head (TF:330-380); query and key heads repeat R times */
-  int any_proc = 0;
-  for (int kh = 0; kh < nk; kh++) {
-    const float* q = w->y + (size_t)kh * kd;
-    const float* k = w->y + (size_t)nk * kd + (size_t)kh * kd;
-    int live = 0;
-    for (int i = 0; i < kd; i++) live |= (q[i] != 0.0f) | (k[i] != 0.0f);
-    float* qn = w->qn + (size_t)kh * kd;
-    float* kn = w->kn + (size_t)kh * kd;
-    if (live) {
-      l2norm_D(q, kd, w->sq, qn);
-      l2norm_D(k, kd, w->sq, kn);
-      for (int i = 0; i < kd; i++) qn[i] = qn[i] * 0.0625f; /* 1 / sqrt(256) */
-    }
-    for (int r = 0; r < R; r++) {
-      const int vh = kh * R + r;
-      float* Sv = S + (size_t)vh * kd * vd;
-      float* on = w->on + (size_t)vh * vd;
-      const float e = ox_expf(w->g[vh]);
-      w->proc[vh] = live || e != 1.0f;
+  int any_proc = rec_heads(d, w->y, w->y + (size_t)nk * kd, w->y + (size_t)2 * nk * kd, w->g,
+                           w->beta, S, w);
+  for (int vh = 0; vh < nv; vh++) {
+    float* on = w->on + (size_t)vh * vd;
+    if (w->proc[vh] != 2) {
       for (int j = 0; j < vd; j++) on[j] = 0.0f;
-      if (!w->proc[vh]) continue; /* exp(g) = 1, q = k = 0: state and output unchanged */
-      if (e != 1.0f)
-        for (size_t i = 0; i < (size_t)kd * vd; i++) Sv[i] = Sv[i] * e;
-      if (!live) continue; /* q = 0: output exactly 0 */
-      const float* v = w->y + (size_t)2 * nk * kd + (size_t)vh * vd;
-      const float beta = w->beta[vh];
-      for (int j = 0; j < vd; j++) {
-        float s = row_sum(Sv + j, vd, kn, kd);
-        w->kv[j] = s;
-        w->delta[j] = (v[j] - s) * beta;
+      continue;
+    }
+    const float* o = w->o + (size_t)vh * vd;
+    /* Qwen3_5RMSNormGated (TF:168-184) on this value head, gate z */
+    for (int j = 0; j < vd; j++) w->sq[j] = o[j] * o[j];
+    float ss = ox_sum_64(w->sq, vd);
+    float rr = ox_rsqrt(ss / (float)vd + d->gated_eps);
+    float zrow[256];
+    for (int j = 0; j < vd; j++) { /* in_proj_z rows of this head */
+      const ox_csr* zm = &ly->z;
+      int row = vh * vd + j;
+      float s = 0.0f;
+      for (int64_t e2 = zm->ptr[row]; e2 < zm->ptr[row + 1]; e2++) {
+        float xv = w->xn[zm->col[e2]];
+        if (xv == 0.0f) continue;
+        s = s + xv * zm->val[e2];
       }
-      for (int i = 0; i < kd; i++) {
-        if (kn[i] == 0.0f) continue;
-        for (int j = 0; j < vd; j++) Sv[(size_t)i * vd + j] = Sv[(size_t)i * vd + j] + kn[i] * w->delta[j];
-      }
-      for (int j = 0; j < vd; j++) w->o[j] = D(row_sum(Sv + j, vd, qn, kd));
-      any_proc = 1;
-      /* Qwen3_5RMSNormGated (TF:168-184) on this value head, gate z */
-      w->proc[vh] = 2;
-      for (int j = 0; j < vd; j++) w->sq[j] = w->o[j] * w->o[j];
-      float ss = ox_sum_64(w->sq, vd);
-      float rr = ox_rsqrt(ss / (float)vd + d->gated_eps);
-      float zrow[256];
-      for (int j = 0; j < vd; j++) { /* in_proj_z rows of this head */
-        const ox_csr* zm = &ly->z;
-        int row = vh * vd + j;
-        float s = 0.0f;
-        for (int64_t e2 = zm->ptr[row]; e2 < zm->ptr[row + 1]; e2++) {
-          float xv = w->xn[zm->col[e2]];
-          if (xv == 0.0f) continue;
-          s = s + xv * zm->val[e2];
-        }
-        zrow[j] = D(s);
-      }
-      for (int j = 0; j < vd; j++) {
-        float t1 = D(w->o[j] * rr);
-        float t2 = D(ly->gnorm[j] * t1);
-        on[j] = D(t2 * ox_silu(zrow[j]));
-      }
+      zrow[j] = D(s);
+    }
+    for (int j = 0; j < vd; j++) {
+      float t1 = D(o[j] * rr);
+      float t2 = D(ly->gnorm[j] * t1);
+      on[j] = D(t2 * ox_silu(zrow[j]));
     }
   }
   /* out_proj, then the residual add (all rows: a row with no term adds +0) */
@@ -487,5 +509,22 @@ void ox_head(const ox_model* m, const float* h, int T, float* logits, int* pred)
     if (logits) memcpy(logits + (size_t)t * m->d.vocab, w.logits, 4 * (size_t)m->d.vocab);
   }
   free(hsq);
+  ws_free(&w);
+}
+
+/* torch_recurrent_gated_delta_rule for one token (the test of the delta rule alone): q, k
+   (nk, kd), v (nv, vd), beta (nv) in the model dtype (bf16 != 0), g (nv) fp32; S (nv, kd, vd)
+   updated in place; o (nv, vd) written. */
+void ox_rec_step(int nk, int nv, int bf16, const float* q, const float* k, const float* v,
+                 const float* g, const float* beta, float* S, float* o) {
+  ox_dims d;
+  memset(&d, 0, sizeof d);
+  d.nk = nk; d.nv = nv; d.kd = 256; d.vd = 128; d.hidden = 1; d.n_layers = 1; d.conv = 4;
+  d.inter = 1; d.vocab = 1; d.bf16 = bf16;
+  g_bf16 = bf16;
+  ox_ws w;
+  ws_init(&w, &d);
+  rec_heads(&d, q, k, v, g, beta, S, &w);
+  memcpy(o, w.o, 4 * (size_t)nv * 128);
   ws_free(&w);
 }

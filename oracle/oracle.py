@@ -69,6 +69,7 @@ def lib():
         _lib.ox_decode.argtypes = [PTR, PTR, PTR, PTR, I32, I32, PTR, PTR, PTR]
         _lib.ox_layer_step.argtypes = [PTR, I32, PTR, PTR, PTR]
         _lib.ox_head.argtypes = [PTR, PTR, I32, PTR, PTR]
+        _lib.ox_rec_step.argtypes = [I32, I32, I32] + [PTR] * 7
     return _lib
 
 
@@ -91,6 +92,17 @@ def sum_h(x) -> np.float32:
 def sum_64(x) -> np.float32:
     x = np.ascontiguousarray(x, np.float32)
     return np.float32(lib().ox_sum_64(_p(x), len(x)))
+
+
+def rec_step(q, k, v, g, beta, S, bf16: bool):
+    """One token of torch_recurrent_gated_delta_rule (q, k (nk, 256); v (nv, 128); g, beta (nv);
+    S (nv, 256, 128) updated in place). Returns o (nv, 128)."""
+    q, k, v, g, beta = (np.ascontiguousarray(a, np.float32) for a in (q, k, v, g, beta))
+    assert S.dtype == np.float32 and S.flags.c_contiguous
+    o = np.zeros((v.shape[0], 128), np.float32)
+    lib().ox_rec_step(q.shape[0], v.shape[0], int(bf16), _p(q), _p(k), _p(v), _p(g), _p(beta),
+                      _p(S), _p(o))
+    return o
 
 
 class OracleModel:

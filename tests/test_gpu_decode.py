@@ -1,0 +1,197 @@
+"""Parity of the HIP decode kernel with the oracle, on an MI355X, through the C ABI.
+
+Bit-exact: predictions, each step's input, every layer's residual after every step, the conv
+windows and the recurrent states (compared bit for bit). The oracle runs the same seeded inputs
+on the CPU; the configs are BASELINE's (config 1, 2, 5) and a small stack of the chip's head
+shapes. Full-size runs are checked by properties the decode must keep.
+"""
+
+import ctypes
+
+import numpy as np
+import pytest
+import torch
+
+from linuxformer_amd import fast, mega, mk_build, synth
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def cuda():
+    assert torch.cuda.is_available(), "the gpu tests need an MI355X"
+    mk_build.load()  # the native library, never a fallback
+    return torch.device("cuda", 0)
+
+
+def _specs():
+    return {"small": synth.small(), "small_fp32": synth.small(dtype="fp32", seed=3),
+            "c1": synth.config1(), "c2": synth.config2(), "c5": synth.config5()}
+
+
+_MODELS = {}
+
+
+def model(name):
+    if name not in _MODELS:
+        spec = _specs()[name]
+        m = synth.build(spec)
+        conv0, rec0 = synth.init_state(m)
+        _MODELS[name] = (spec, m, conv0, rec0)
+    return _MODELS[name]
+
+
+def bits(a):
+    return np.ascontiguousarray(a, np.float32).view(np.uint32)
+
+
+def check(name, n, forced=None, launches=None, conv0=None, trace=True):
+    """Run the kernel and the oracle from the same state; compare everything bit for bit."""
+    from oracle import oracle as ox
+
+    spec, m, c0, r0 = model(name)
+    conv0 = c0 if conv0 is None else conv0
+    print(f"[gpu-test] {name}: n={n} forced={None if forced is None else len(forced)} "
+          f"launches={launches}", flush=True)
+    forced = [synth.start_token(spec)] if forced is None else list(forced)
+    cache = fast.StateCache(conv0, r0, m.dims.dtype, "cuda")
+    mg = mega.Mega(fast.Fast(m), m, cache, 0)
+    d = m.dims
+    tr = torch.zeros(n, d.n_layers, d.hidden, device="cuda") if trace else None
+    inp = torch.zeros(n, dtype=torch.int32, device="cuda")
+    preds = []
+    done = 0
+    for k in launches or [n]:
+        f = forced[done:] if done < len(forced) else [preds[-1]]
+        sub_tr = tr[done:done + k] if trace else None
+        sub_in = inp[done:done + k]
+        preds += mg.run(f, k, inputs=sub_in, trace=sub_tr)
+        done += k
+    om = ox.OracleModel(m)
+    c, r = conv0.copy(), r0.copy()
+    po, io, tro = om.decode(c, r, forced, n, trace=trace)
+    assert preds == po.tolist()
+    assert inp.cpu().numpy().tolist() == io.tolist()
+    if trace:
+        assert (bits(tr.cpu().numpy()) == bits(tro)).all()
+    assert (bits(cache.conv_numpy()) == bits(c)).all()
+    assert (bits(cache.rec_numpy()) == bits(r)).all()
+    return preds
+
+
+def test_device_math_matches_oracle(cuda):
+    """The kernels' exp, log1p, silu, sigmoid, softplus, rsqrt and bf16 rounding equal the
+    oracle's on every bf16 value and on 1M random floats per function."""
+    from oracle import oracle as ox
+
+    lib = mk_build.load()
+    rng = np.random.default_rng(3)
+    allb = (np.arange(65536, dtype=np.uint32) << 16).view(np.float32)
+    st = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    for fn, code in ox.ELEM.items():
+        lo, hi = (0.0, 1e9) if fn in ("log1p", "rsqrt") else (-120.0, 100.0)
+        x = np.concatenate([allb, rng.uniform(lo, hi, 1 << 20).astype(np.float32)])
+        if fn == "log1p":
+            x = np.abs(x)
+        xd = torch.from_numpy(x).to(cuda)
+        yd = torch.empty_like(xd)
+        assert lib.lxm_t_elem(code, ctypes.c_void_p(xd.data_ptr()), ctypes.c_void_p(yd.data_ptr()),
+                              x.size, st) == 0
+        y = yd.cpu().numpy()
+        ref = ox.elem(fn, x)
+        same = (bits(y) == bits(ref)) | (np.isnan(y) & np.isnan(ref))
+        assert same.all(), (fn, int((~same).sum()))
+
+
+@pytest.mark.parametrize("kind,n", [(0, 3572), (0, 192), (1, 128), (1, 256)])
+def test_device_sums_match_oracle(cuda, kind, n):
+    from oracle import oracle as ox
+
+    lib = mk_build.load()
+    rng = np.random.default_rng(kind * 1000 + n)
+    rows = 64
+    x = (rng.standard_normal((rows, n)) * np.exp(rng.uniform(-8, 8, (rows, n)))).astype(np.float32)
+    xd = torch.from_numpy(x).to(cuda)
+    out = torch.zeros(rows, device=cuda)
+    st = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    assert lib.lxm_t_sum(kind, ctypes.c_void_p(xd.data_ptr()), n, rows,
+                         ctypes.c_void_p(out.data_ptr()), st) == 0
+    ref = [ox.sum_h(x[i]) if kind == 0 else ox.sum_64(x[i]) for i in range(rows)]
+    assert (bits(out.cpu().numpy()) == bits(np.array(ref, np.float32))).all()
+
+
+def test_small_stack(cuda):
+    check("small", 64)
+
+
+def test_small_stack_fp32(cuda):
+    check("small_fp32", 48)
+
+
+def test_config1_greedy(cuda):
+    """256 greedy steps of one chip-shaped fp32 layer."""
+    check("c1", 256)
+
+
+def test_config1_forced_inputs(cuda):
+    """Config 1 driven by 256 seeded inputs (a quarter of its layer-steps gated)."""
+    rng = np.random.default_rng(5)
+    check("c1", 256, forced=rng.integers(0, 4096, 256).tolist())
+
+
+def test_config2(cuda):
+    """BASELINE config 2 (37 layers, bf16, N(0,1) state): 20 steps, every layer's residual."""
+    check("c2", 20)
+
+
+def test_config5(cuda):
+    """BASELINE config 5 (half of the layer-steps gated): 8 steps."""
+    check("c5", 8)
+
+
+def test_launches_continue_the_stream(cuda):
+    """Three launches (5, 3 and 40 steps, each fed the last prediction) leave the same stream
+    and states as one launch of 48: the windows written at a launch's end are the next's."""
+    check("small", 48, launches=[5, 3, 40])
+
+
+def test_short_launch_with_live_windows(cuda):
+    """A launch shorter than the conv window, from nonzero windows on every channel (dead ones
+    included): the first steps read the windows left before the launch."""
+    spec, m, c0, r0 = model("small")
+    rng = np.random.default_rng(9)
+    conv0 = synth._round(rng.standard_normal(c0.shape).astype(np.float32), "bf16")
+    check("small", 2, conv0=conv0)
+    check("small", 9, launches=[1, 1, 1, 6], conv0=conv0)
+
+
+def test_forced_token_out_of_range(cuda):
+    spec, m, c0, r0 = model("small")
+    cache = fast.StateCache(c0, r0, m.dims.dtype, "cuda")
+    mg = mega.Mega(fast.Fast(m), m, cache, 0)
+    with pytest.raises(ValueError):
+        mg.run([m.dims.vocab], 4)
+
+
+def test_config2_long_run_properties(cuda):
+    """4,096 steps of config 2: every input is the previous prediction (input purity), every
+    prediction is a token, and the state of value heads no live gate reaches is untouched."""
+    spec, m, c0, r0 = model("c2")
+    cache = fast.StateCache(c0, r0, "bf16", "cuda")
+    f = fast.Fast(m)
+    mg = mega.Mega(f, m, cache, 0)
+    n = 4096
+    inp = torch.zeros(n, dtype=torch.int32, device="cuda")
+    preds = mg.run([synth.start_token(spec)], n, inputs=inp)
+    inp = inp.cpu().numpy()
+    assert (inp[1:] == np.array(preds[:-1])).all()
+    assert min(preds) >= 0 and max(preds) < m.dims.vocab
+    rec = cache.rec_numpy()
+    R = m.dims.nv // m.dims.nk
+    for L in (0, 18, 36):
+        touched = set()
+        for kh in f.dec[L]["kh"]:
+            touched.update(range(kh * R, kh * R + R))
+        touched.update(int(v) for v in f.dec[L]["decays"])
+        idle = [v for v in range(m.dims.nv) if v not in touched]
+        assert idle and (bits(rec[L][idle]) == bits(r0[L][idle])).all()

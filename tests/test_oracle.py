@@ -1,0 +1,244 @@
+"""The oracle (oracle/lx_oracle.c) pinned: its elementary functions against float64 and against
+torch's own bf16 kernels, its sum orders against constructed cancellations, and its decode
+against the stock forward's golden vectors (tests/golden, written from transformers' Qwen3_5
+layers by tests/golden/make_golden.py)."""
+
+import os
+
+import numpy as np
+import pytest
+import torch
+
+from linuxformer_amd import synth
+
+GOLD = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
+
+
+def bf16_all():
+    return (np.arange(65536, dtype=np.uint32) << 16).view(np.float32)
+
+
+def bits(a):
+    return np.ascontiguousarray(a, np.float32).view(np.uint32)
+
+
+def test_exp_log1p_correctly_rounded(oracle_lib):
+    """exp and log1p against float64 rounded once to float32 (the double reference is 2^29
+    times finer than a float ulp, so a mismatch would mean a misrounded result)."""
+    ox = oracle_lib
+    rng = np.random.default_rng(0)
+    x = rng.uniform(-103.0, 88.7, 1 << 20).astype(np.float32)
+    ref = np.exp(x.astype(np.float64)).astype(np.float32)
+    assert (bits(ox.elem("exp", x)) != bits(ref)).sum() == 0
+    y = np.exp(rng.uniform(np.log(1e-30), np.log(1e9), 1 << 20)).astype(np.float32)
+    ref = np.log1p(y.astype(np.float64)).astype(np.float32)
+    assert (bits(ox.elem("log1p", y)) != bits(ref)).sum() == 0
+
+
+def test_special_values(oracle_lib):
+    ox = oracle_lib
+    x = np.array([0.0, -0.0, 1.0, 88.72, 89.5, -103.9, -104.0, -200.0, np.inf, -np.inf], np.float32)
+    e = ox.elem("exp", x)
+    assert e[0] == 1.0 and e[1] == 1.0 and e[2] == np.float32(np.e)
+    assert np.isfinite(e[3]) and e[4] == np.inf and e[5] > 0 and e[6] == 0 and e[7] == 0
+    assert e[8] == np.inf and e[9] == 0
+    sp = ox.elem("softplus", np.array([21.0, 20.0, -200.0, 0.0], np.float32))
+    assert sp[0] == 21.0 and sp[1] == np.float32(np.log1p(np.exp(20.0))) and sp[2] == 0.0
+    assert sp[3] == np.float32(np.log(2.0))
+    si = ox.elem("silu", np.array([0.0, -0.0, -200.0, 100.0], np.float32))
+    assert bits(si[:2]).tolist() == [0, 0x80000000] and si[2] == 0.0 and si[3] == 100.0
+    assert ox.elem("rsqrt", np.array([4.0], np.float32))[0] == 0.5
+    b = ox.elem("bf16", np.array([1.0 + 2 ** -8, 1.0 + 3 * 2 ** -8, np.nan], np.float32))
+    assert b[0] == 1.0 and b[1] == 1.0 + 2 ** -6 and bits(b[2:]).tolist() == [0x7FC00000]
+
+
+def test_bf16_elementwise_equals_torch(oracle_lib):
+    """On every bf16 input, the oracle's silu, sigmoid, exp and rsqrt rounded to bf16 equal
+    torch's bf16 kernels (the vectorised path the chip's 128-head tensors take)."""
+    ox = oracle_lib
+    x = bf16_all()
+    fin = np.isfinite(x)
+    xb = torch.from_numpy(x.copy()).to(torch.bfloat16)
+    for name, fn in (("silu", torch.nn.functional.silu), ("sigmoid", torch.sigmoid),
+                     ("exp", torch.exp), ("rsqrt", torch.rsqrt)):
+        mine = ox.elem("bf16", ox.elem(name, x))
+        ref = fn(xb).float().numpy()
+        same = (bits(mine) == bits(ref)) | (np.isnan(mine) & np.isnan(ref))
+        assert (~same & fin).sum() == 0, name
+
+
+def test_hidden_sum_order(oracle_lib):
+    """The 512-lane tree: lane l adds x[l], x[l + 512], ... in order; lanes pair at offsets
+    32..1 within a group of 64, then the 8 group totals at 4, 2, 1. Big values placed where the
+    documented pairing cancels them first keep the small terms; any other order loses them."""
+    ox = oracle_lib
+    x = np.zeros(3572, np.float32)
+    x[0], x[32] = 1e8, -1e8          # paired at offset 32 inside group 0
+    x[1] = 1.0                        # meets the pair's exact 0 later
+    x[64 * 3], x[64 * 7] = 3e8, -3e8  # groups 3 and 7 pair at offset 4
+    x[64 * 5 + 7] = 0.5
+    assert ox.sum_h(x) == 1.5
+    y = np.zeros(3572, np.float32)
+    y[5], y[5 + 512] = 1e8, 1.0       # one lane, in order: 1e8 + 1 rounds to 1e8
+    y[5 + 1024] = -1e8
+    assert ox.sum_h(y) == 0.0
+    z = np.arange(1, 3573, dtype=np.float32)
+    assert ox.sum_h(z) == float(z.astype(np.float64).sum())
+    h = np.zeros(256, np.float32)
+    h[0], h[32], h[1], h[3] = 1e8, -1e8, 1.0, 0.25  # lanes 0 and 32 cancel first
+    assert ox.sum_64(h) == 1.25
+    h[64] = 1.0  # lane 0 again, after its 1e8: absorbed
+    assert ox.sum_64(h) == 1.25
+
+
+def _load(name):
+    return dict(np.load(os.path.join(GOLD, name + ".npz")))
+
+
+@pytest.mark.parametrize("name,exact,tol", [
+    ("c1_64", True, 0.0),            # the chip's shape: bit for bit
+    ("small_fp32_32", False, 1e-6),  # dense-ish rows, 8 value heads: per-layer 1e-6 relative
+    ("tiny_fp32_8", False, 1e-5),    # dense layers: per-step 1e-6 errors carried 8 steps in the state
+])
+def test_oracle_matches_stock_fp32(oracle_lib, name, exact, tol):
+    from golden.make_golden import model_of, sha
+
+    g = _load(name)
+    m, conv0, rec0, start = model_of(name)
+    om = oracle_lib.OracleModel(m)
+    c, r = conv0.copy(), rec0.copy()
+    preds, _, tr = om.decode(c, r, [int(g["start"])], int(g["n"]), trace=True)
+    assert preds.tolist() == g["preds"].tolist()
+    if exact:
+        assert sha(tr) == str(g["trace_sha"])
+        assert sha(c) == str(g["conv_sha"]) and sha(r) == str(g["rec_sha"])
+    else:
+        ref = g["trace"]
+        rel = np.abs(tr - ref).max(-1) / np.maximum(np.abs(ref).max(-1), 1e-30)
+        assert rel.max() <= tol, rel.max()
+        rs = r.reshape(-1)[g["rec_idx"]]
+        assert np.abs(rs - g["rec_sample"]).max() <= tol * max(1.0, np.abs(g["rec_sample"]).max())
+
+
+@pytest.mark.parametrize("name", ["small_bf16_32", "tiny_bf16_8"])
+def test_oracle_matches_stock_bf16(oracle_lib, name):
+    """bf16 stacks with long dense sums: torch's summation orders (oneDNN's GEMV, ATen's
+    vectorised inner sums) differ from the contract's, so single fp32 roundings can flip a bf16
+    result; the stream is identical and most residual values are bit-equal."""
+    from golden.make_golden import model_of
+
+    g = _load(name)
+    m, conv0, rec0, start = model_of(name)
+    om = oracle_lib.OracleModel(m)
+    c, r = conv0.copy(), rec0.copy()
+    preds, _, tr = om.decode(c, r, [int(g["start"])], int(g["n"]), trace=True)
+    assert preds.tolist() == g["preds"].tolist()
+    ref = g["trace"]
+    assert (tr == ref).mean() >= 0.2
+    rel = np.abs(tr - ref).max(-1) / np.maximum(np.abs(ref).max(-1), 1e-30)
+    assert rel.max() <= 0.03, rel.max()
+
+
+def test_layer_step_matches_stock_decoder_layer(oracle_lib):
+    """One fully dense decoder layer (fp32) from identical random inputs, against transformers'
+    Qwen3_5DecoderLayer: the output within 5e-6 relative -- its out_proj adds 4,096 dense
+    terms, which oneDNN sums in its own order (two orders spread by ~sqrt(4096) x 2^-24 =
+    3.8e-6) -- and the state and conv window within 1e-6. (The sparse, chip-shaped config 1 is
+    bit-identical: test_oracle_matches_stock_fp32; the delta rule alone is bit-identical:
+    test_recurrent_step_bit_exact.)"""
+    import stock
+
+    torch.set_grad_enabled(False)
+    m = synth.tiny_dense(seed=11, dtype="fp32")
+    hf = synth.to_hf(m)
+    d = m.dims
+    rng = np.random.default_rng(2)
+    conv0 = rng.standard_normal((d.n_layers, d.n_conv, 4)).astype(np.float32)
+    rec0 = rng.standard_normal((d.n_layers, d.nv, d.kd, d.vd)).astype(np.float32)
+    h = rng.standard_normal(d.hidden).astype(np.float32)
+    cache = stock.make_cache(hf, conv0, rec0)
+    out = hf.model.layers[0](torch.from_numpy(h)[None, None], position_embeddings=None,
+                             attention_mask=None, position_ids=None, past_key_values=cache)
+    out = (out[0] if isinstance(out, tuple) else out)[0, 0].numpy()
+    om = oracle_lib.OracleModel(m)
+    hx, c, r = h.copy(), conv0[0].copy(), rec0[0].copy()
+    om.layer_step(0, hx, c, r)
+    R = cache.layers[0].recurrent_states[0][0].numpy()
+    Cs = cache.layers[0].conv_states[0][0].numpy()
+    assert np.abs(hx - out).max() / np.abs(out).max() <= 5e-6
+    assert np.abs(r - R).max() <= 1e-6 * np.abs(R).max()
+    assert np.abs(c - Cs).max() <= 1e-6 * np.abs(Cs).max()
+
+
+def _rec_inputs(dtype, dense, chip, seed):
+    rng = np.random.default_rng(seed)
+    nk, nv = 16, 128
+    tdt = torch.bfloat16 if dtype == "bf16" else torch.float32
+
+    def rnd(shape, p):
+        if chip:  # dyadic values, as the chip's circuit values are
+            x = rng.choice(synth.VALS, shape).astype(np.float32)
+        else:
+            x = rng.standard_normal(shape).astype(np.float32)
+        x[rng.random(shape) > p] = 0
+        return torch.from_numpy(x).to(tdt).float().numpy()
+
+    qv = rnd((nk, 256), 1.0 if dense else 0.02)
+    kv = rnd((nk, 256), 1.0 if dense else 0.01)
+    qv[3] = 0
+    kv[3] = 0  # an idle head
+    vv = torch.from_numpy(rng.standard_normal((nv, 128)).astype(np.float32)).to(tdt).float().numpy()
+    beta = torch.from_numpy(rng.random(nv).astype(np.float32)).to(tdt).float().numpy()
+    if chip:  # decays exp(g) in {1, 1/2, 0}
+        g = rng.choice(np.array([0.0, -np.log(2.0), -200.0], np.float32), nv).astype(np.float32)
+    else:
+        g = np.where(rng.random(nv) < 0.3, -rng.random(nv), 0.0).astype(np.float32)
+    S0 = rng.standard_normal((nv, 256, 128)).astype(np.float32)
+    return qv, kv, vv, g, beta, S0, tdt
+
+
+def _stock_rec(qv, kv, vv, g, beta, S0, tdt):
+    from transformers.models.qwen3_5 import modeling_qwen3_5 as q
+
+    R = vv.shape[0] // qv.shape[0]
+    T = lambda a: torch.from_numpy(a).to(tdt)  # noqa: E731
+    o, S = q.torch_recurrent_gated_delta_rule(
+        T(qv)[None, None].repeat_interleave(R, dim=2), T(kv)[None, None].repeat_interleave(R, dim=2),
+        T(vv)[None, None], g=torch.from_numpy(g)[None, None], beta=T(beta)[None, None],
+        initial_state=torch.from_numpy(S0.copy())[None], output_final_state=True,
+        use_qk_l2norm_in_kernel=True)
+    return o[0, 0].float().numpy(), S[0].numpy()
+
+
+@pytest.mark.parametrize("dtype", ["fp32", "bf16"])
+@pytest.mark.parametrize("dense", [False, True])
+def test_recurrent_step_bit_exact(oracle_lib, dtype, dense):
+    """The delta rule (l2norm in the model dtype, decay, kv, delta, write, output) equals
+    transformers' torch_recurrent_gated_delta_rule bit for bit at the chip's 16 key x 8 value
+    heads, in the chip's regime (dyadic query/key values, decays exp(g) in {1, 1/2, 0}) with
+    random state, values and betas; sparse (as the chip's) or dense queries and keys."""
+    torch.set_grad_enabled(False)
+    qv, kv, vv, g, beta, S0, tdt = _rec_inputs(dtype, dense, True, 7 + dense)
+    o_t, S_t = _stock_rec(qv, kv, vv, g, beta, S0, tdt)
+    S = S0.copy()
+    o = oracle_lib.rec_step(qv, kv, vv, g, beta, S, dtype == "bf16")
+    assert (o == o_t).all()
+    assert (S == S_t).all()
+
+
+@pytest.mark.parametrize("dtype", ["fp32", "bf16"])
+def test_recurrent_step_generic_inputs(oracle_lib, dtype):
+    """Random (non-dyadic) inputs: torch's fp32 l2norm sums 256 terms in its vector-width order
+    and its Sleef exp is 1 ulp off on ~1 % of decays, so fp32 results agree within 1e-6
+    relative; in bf16 the outputs are bit-identical and the state differs only on heads whose
+    exp(g) torch rounds differently."""
+    torch.set_grad_enabled(False)
+    qv, kv, vv, g, beta, S0, tdt = _rec_inputs(dtype, True, False, 21)
+    o_t, S_t = _stock_rec(qv, kv, vv, g, beta, S0, tdt)
+    S = S0.copy()
+    o = oracle_lib.rec_step(qv, kv, vv, g, beta, S, dtype == "bf16")
+    same_e = oracle_lib.elem("exp", g) == torch.exp(torch.from_numpy(g)).numpy()
+    assert np.abs(o - o_t).max() <= 1e-6 * np.abs(o_t).max() + (0 if dtype == "fp32" else 1e-2)
+    assert np.abs(S - S_t).max() <= 1e-6 * np.abs(S_t).max()
+    if dtype == "bf16":
+        assert (S[same_e] == S_t[same_e]).all()
