@@ -65,7 +65,8 @@ using namespace lxm;
 #define L_WSUM (L_BETA + 4 * RMAX)
 #define L_FLAGS (L_WSUM + 4 * 32)
 #define L_PROF (L_FLAGS + 4 * 256)
-#define L_CHAIN_END (L_PROF + 8 * 32)
+#define L_XG (L_PROF + 8 * 32)
+#define L_CHAIN_END (L_XG + 4 * MAXH)
 // flags (int): [0] any head active, [1] any output, [2] nq, [3] nk, [4] scratch, [8] token
 // [16 + kh] per key head: bit 0 query nonzero, bit 1 key nonzero, bit 2 decay
 #define F_ANY 0
@@ -125,9 +126,10 @@ __device__ __forceinline__ void lds_barrier() {
 
 // In-kernel phase counters (lx/csrc/mega.cu's prof buffer and MK_SUBPROF checkpoints): with
 // p.prof set, thread 0 of the chain adds the shader-clock cycles of each phase into an LDS
-// slot; the slots are written to p.prof at the end. Phases: 0 embedding, 1 layer staging,
-// 2 GDN norm + gates, 3 active heads, 4 MLP, 5 trace, 6 final norm + publish, 7 waiting for the
-// head's argmax; counters 16 active layer-steps, 17 tokens.
+// slot; the slots are written to p.prof at the end. Phases: 0 embedding, 1 layer staging (and
+// the trace), 2 the norms (stage A), 3 the gates and the MLP units (stage B), 4 active heads
+// and the MLP's redo, 5 down_proj and the next norm's sums (stage C), 6 final norm + publish,
+// 7 waiting for the head's argmax; counters 16 active layer-steps, 17 tokens.
 #define PROF_ON (p.prof != nullptr)
 __device__ __forceinline__ uint64_t cycles() { return __builtin_readcyclecounter(); }
 
@@ -261,12 +263,6 @@ extern __shared__ __align__(16) uint8_t smem[];
 __device__ __forceinline__ float norm_r(float ss, int H, float eps) {
   return rsqrt_(ss / (float)H + eps);
 }
-// the normed input of column c: D((h * r) * (1 + w)) (:729-734)
-template <bool BF, bool E4>
-__device__ __forceinline__ float xnorm(int off, int c, float r) {
-  return rd<BF>((LF(L_H)[c] * r) * w1_at<E4>(smem + L_HOT, off, c));
-}
-
 __device__ __forceinline__ float hidden_ss(int H) {
   const float* h = LF(L_H);
   float s = 0.0f;
@@ -315,7 +311,140 @@ __device__ __forceinline__ void stage(int n16, const Pf& r) {
 }
 
 template <bool BF, bool E4>
-__device__ void gdn_active(const lxm_params& p, int L, int step, float r1);
+__device__ void gdn_active(const lxm_params& p, int L, int step);
+
+// One chunk of up to 4 entries of a row (entries k0 .. k0 + 3 of start .. start + n): the sum
+// continues in entry order; all loads of the chunk are issued together.
+template <bool E4>
+__device__ __forceinline__ float chunk4(const uint8_t* ent, int start, int n, int k0,
+                                        const float* x, float s) {
+  int i[4];
+  float w[4], xv[4];
+#pragma unroll
+  for (int j = 0; j < 4; j++) {
+    i[j] = 0;
+    w[j] = 0.0f;
+    if (k0 + j < n) Ent<E4>::at(ent, start + k0 + j, i[j], w[j]);
+  }
+#pragma unroll
+  for (int j = 0; j < 4; j++) xv[j] = x[i[j]];
+#pragma unroll
+  for (int j = 0; j < 4; j++)
+    if (k0 + j < n && xv[j] != 0.0f) s = s + xv[j] * w[j];
+  return s;
+}
+template <bool E4>
+__device__ __forceinline__ float rest4(const uint8_t* ent, int start, int n, const float* x,
+                                       float s) {
+  for (int k0 = 4; k0 < n; k0 += 4) s = chunk4<E4>(ent, start, n, k0, x, s);
+  return s;
+}
+
+// silu and the MLP product for one unit (Qwen3_5MLP :715): D(D(silu(D(g))) * D(u))
+template <bool BF>
+__device__ __forceinline__ float swiglu(float gs, float us) {
+  const float g = rd<BF>(gs), up = rd<BF>(us);
+  const float sg = g == 0.0f ? g : silu(g);  // silu(+-0) = +-0 / 2 = +-0
+  return rd<BF>(rd<BF>(sg) * up);
+}
+
+// The MLP's gate and up rows of every unit: act[u]. Two units a thread, their first chunks
+// issued together.
+template <bool BF, bool E4>
+__device__ __forceinline__ void mlp_units(const lxm_hot& hd, const uint8_t* hot) {
+  const int t = threadIdx.x;
+  const float* xm = LF(L_XM);
+  float* act = LF(L_ACT);
+  const uint32_t* um = reinterpret_cast<const uint32_t*>(hot + hd.unit);
+  const uint8_t* gu = hot + hd.gu_ent;
+  for (int u = t; u < hd.n_units; u += 2 * NT) {
+    const int u2 = u + NT;
+    const bool two = u2 < hd.n_units;
+    const uint32_t m1 = um[u], m2 = two ? um[u2] : 0u;
+    const int s1 = (int)(m1 & 0xffffu), g1 = (int)((m1 >> 16) & 255), n1 = (int)(m1 >> 24);
+    const int s2 = (int)(m2 & 0xffffu), g2 = (int)((m2 >> 16) & 255), n2 = (int)(m2 >> 24);
+    float ag = chunk4<E4>(gu, s1, g1, 0, xm, 0.0f);
+    float au = chunk4<E4>(gu, s1 + g1, n1, 0, xm, 0.0f);
+    float bg = chunk4<E4>(gu, s2, g2, 0, xm, 0.0f);
+    float bu = chunk4<E4>(gu, s2 + g2, n2, 0, xm, 0.0f);
+    ag = rest4<E4>(gu, s1, g1, xm, ag);
+    au = rest4<E4>(gu, s1 + g1, n1, xm, au);
+    bg = rest4<E4>(gu, s2, g2, xm, bg);
+    bu = rest4<E4>(gu, s2 + g2, n2, xm, bu);
+    act[u] = swiglu<BF>(ag, au);
+    if (two) act[u2] = swiglu<BF>(bg, bu);
+  }
+}
+
+// The gates: the live query/key channels' projections, conv windows (history in LDS) and silu
+// (causal_conv1d_update :199-216), and the decays g = -exp(A_log) softplus(a + dt_bias) (:499).
+// Flags per key head: 1 query nonzero, 2 key nonzero, 4 a decay exp(g) != 1. Items run on the
+// threads from the top down (the units take them from the bottom up).
+template <bool BF, bool E4>
+__device__ __forceinline__ void gates(const lxm_params& p, const lxm_hot& hd, const uint8_t* hot) {
+  const int tt = NT - 1 - (int)threadIdx.x;
+  const float* xg = LF(L_XG);
+  float* hist = LF(L_HIST);
+  float* qkcur = LF(L_QKCUR);
+  float* ev = LF(L_EV);
+  int* flags = LI(L_FLAGS);
+  const lxm_qkc* qk = reinterpret_cast<const lxm_qkc*>(hot + hd.qk);
+  const uint8_t* ent = hot + hd.ent;
+  for (int j = tt; j < hd.n_qk; j += NT) {
+    const lxm_qkc c = qk[j];
+    const float P = rd<BF>(rest4<E4>(ent, c.start, c.len, xg, chunk4<E4>(ent, c.start, c.len, 0, xg, 0.0f)));
+    float* hs = hist + 3 * (hd.qk_base + j);
+    float y = 0.0f;
+    y = y + c.taps[0] * hs[0];
+    y = y + c.taps[1] * hs[1];
+    y = y + c.taps[2] * hs[2];
+    y = y + c.taps[3] * P;
+    hs[0] = hs[1];
+    hs[1] = hs[2];
+    hs[2] = P;
+    const float yr = rd<BF>(y);
+    const float v = yr == 0.0f ? yr : rd<BF>(silu(yr));
+    qkcur[j] = v;
+    if (v != 0.0f) atomicOr(&flags[F_KH + (c.slot >> 9)], (c.slot & 256) ? 2 : 1);
+  }
+  const lxm_dec* dc = reinterpret_cast<const lxm_dec*>(hot + hd.dec);
+  for (int j = ((tt - hd.n_qk) % NT + NT) % NT; j < hd.n_dec; j += NT) {
+    const lxm_dec d = dc[j];
+    const float a = rd<BF>(rest4<E4>(ent, d.start, d.len, xg, chunk4<E4>(ent, d.start, d.len, 0, xg, 0.0f)));
+    const float x = a + d.dt_bias;
+    float e;
+    if (x < -104.0f && d.A_log <= 88.0f) {
+      e = 1.0f;  // exp(x) rounds to 0, so softplus is 0 and g = -exp(A_log) * 0 = -0
+    } else {
+      const float g = (-cr_exp(d.A_log)) * softplus(x);
+      e = cr_exp(g);
+    }
+    ev[d.vh] = e;
+    if (e != 1.0f) atomicOr(&flags[F_KH + d.vh / (p.nv / p.nk)], 4);
+  }
+}
+
+// stage A's norm: r = rsqrt(mean(h^2) + eps) (transformers qwen3_5 :727, mean = sum / n); both
+// norms' inputs D((h * r) * (1 + w)) (:729-734) from one h * r; the GDN norm's output also to the
+// ring. Only the MLP's when gdn is false (the redo after a delta rule that wrote h).
+template <bool BF, bool E4>
+__device__ __forceinline__ void norms(const lxm_params& p, const lxm_hot& hd, const uint8_t* hot,
+                                      int L, int step, float r, bool gdn) {
+  const int H = p.hidden;
+  const float* h = LF(L_H);
+  float* xg = LF(L_XG);
+  float* xm = LF(L_XM);
+  GAS float* ring = gp(p.ring + ((size_t)(step & 3) * p.n_layers + L) * H);
+  for (int c = threadIdx.x; c < H; c += NT) {
+    const float hr = h[c] * r;
+    xm[c] = rd<BF>(hr * w1_at<E4>(hot, hd.w1_post, c));
+    if (gdn) {
+      const float g = rd<BF>(hr * w1_at<E4>(hot, hd.w1_in, c));
+      xg[c] = g;
+      ring[c] = g;
+    }
+  }
+}
 
 // One layer. ss: the sum of squares of h on entry; returns it for the layer's output.
 template <bool BF, bool E4>
@@ -324,120 +453,85 @@ __device__ __forceinline__ float layer(const lxm_params& p, int L, int step, flo
   const uint8_t* hot = smem + L_HOT;
   const lxm_hot hd = *reinterpret_cast<const lxm_hot*>(hot);
   float* h = LF(L_H);
-  float* xm = LF(L_XM);
   float* act = LF(L_ACT);
-  float* hist = LF(L_HIST);
-  float* qkcur = LF(L_QKCUR);
   float* ev = LF(L_EV);
   int* flags = LI(L_FLAGS);
-  using E = Ent<E4>;
-  // ---- GDN norm (transformers qwen3_5 :764 input_layernorm) and the ring of its outputs
-  const float r1 = norm_r(ss, H, hd.eps);
-  {
-    float* ring = p.ring + ((size_t)(step & 3) * p.n_layers + L) * H;
-    for (int c = t; c < H; c += NT) ring[c] = xnorm<BF, E4>(hd.w1_in, c, r1);
-  }
+  uint64_t* pa = reinterpret_cast<uint64_t*>(smem + L_PROF);
+  // ---- stage A: both norms (the GDN's input_layernorm :764 and the MLP's
+  // post_attention_layernorm :789 read the same h when the GDN leaves it alone)
+  const float r = norm_r(ss, H, hd.eps);
+  norms<BF, E4>(p, hd, hot, L, step, r, true);
   if (t < p.nk) flags[F_KH + t] = 0;
   if (t < p.nv) ev[t] = 1.0f;
   if (t == 0) flags[F_ANY] = 0;
   lds_barrier();
-  // ---- the gates: live query/key channels (projection, conv window, silu) and decays
-  // (causal_conv1d_update :199-216; g = -exp(A_log) softplus(a + dt_bias) :499)
-  {
-    const lxm_qkc* qk = reinterpret_cast<const lxm_qkc*>(hot + hd.qk);
-    const uint8_t* ent = hot + hd.ent;
-    for (int j = t; j < hd.n_qk; j += NT) {
-      const lxm_qkc c = qk[j];
-      float s = 0.0f;
-      for (int k = 0; k < c.len; k++) {
-        int col;
-        float w;
-        E::at(ent, c.start + k, col, w);
-        const float xv = xnorm<BF, E4>(hd.w1_in, col, r1);
-        if (xv != 0.0f) s = s + xv * w;
-      }
-      const float P = rd<BF>(s);
-      float* hs = hist + 3 * (hd.qk_base + j);
-      float y = 0.0f;
-      y = y + c.taps[0] * hs[0];
-      y = y + c.taps[1] * hs[1];
-      y = y + c.taps[2] * hs[2];
-      y = y + c.taps[3] * P;
-      hs[0] = hs[1];
-      hs[1] = hs[2];
-      hs[2] = P;
-      const float v = rd<BF>(silu(rd<BF>(y)));
-      qkcur[j] = v;
-      if (v != 0.0f) atomicOr(&flags[F_KH + (c.slot >> 9)], (c.slot & 256) ? 2 : 1);
-    }
-    const lxm_dec* dc = reinterpret_cast<const lxm_dec*>(hot + hd.dec);
-    for (int j = t; j < hd.n_dec; j += NT) {
-      const lxm_dec d = dc[j];
-      float s = 0.0f;
-      for (int k = 0; k < d.len; k++) {
-        int col;
-        float w;
-        E::at(ent, d.start + k, col, w);
-        const float xv = xnorm<BF, E4>(hd.w1_in, col, r1);
-        if (xv != 0.0f) s = s + xv * w;
-      }
-      const float a = rd<BF>(s);
-      const float g = (-cr_exp(d.A_log)) * softplus(a + d.dt_bias);
-      const float e = cr_exp(g);
-      ev[d.vh] = e;
-      if (e != 1.0f) atomicOr(&flags[F_KH + d.vh / (p.nv / p.nk)], 4);
-    }
-  }
-  lds_barrier();
-  if (t < p.nk && flags[F_KH + t]) atomicOr(&flags[F_ANY], 1);
-  lds_barrier();
-  uint64_t* pa = reinterpret_cast<uint64_t*>(smem + L_PROF);
   uint64_t c0 = 0;
   if (PROF_ON && t == 0) {
     c0 = cycles();
     pa[2] += c0 - pa[15];
   }
+  // ---- stage B: the gates and, speculatively (the GDN leaves h alone on most steps), the MLP
+  mlp_units<BF, E4>(hd, hot);
+  gates<BF, E4>(p, hd, hot);
+  lds_barrier();
+  if (t < p.nk && flags[F_KH + t]) atomicOr(&flags[F_ANY], 1);
+  lds_barrier();
+  if (PROF_ON && t == 0) {
+    const uint64_t c1 = cycles();
+    pa[3] += c1 - c0;
+    c0 = c1;
+  }
   if (flags[F_ANY]) {
-    gdn_active<BF, E4>(p, L, step, r1);
-    if (flags[F_OUT]) ss = hidden_ss(H);
+    gdn_active<BF, E4>(p, L, step);
+    if (flags[F_OUT]) {  // h changed: the MLP again, on the new h
+      ss = hidden_ss(H);
+      norms<BF, E4>(p, hd, hot, L, step, norm_r(ss, H, hd.eps), false);
+      lds_barrier();
+      mlp_units<BF, E4>(hd, hot);
+      lds_barrier();
+    }
     if (PROF_ON && t == 0) {
       const uint64_t c1 = cycles();
-      pa[3] += c1 - c0;
+      pa[4] += c1 - c0;
       pa[16] += 1;
       c0 = c1;
     }
   }
-  // ---- MLP (:788-791; Qwen3_5MLP :715)
-  const float r2 = norm_r(ss, H, hd.eps);
-  for (int c = t; c < H; c += NT) xm[c] = xnorm<BF, E4>(hd.w1_post, c, r2);
-  lds_barrier();
-  {
-    const uint32_t* um = reinterpret_cast<const uint32_t*>(hot + hd.unit);
-    const uint8_t* gu = hot + hd.gu_ent;
-    for (int u = t; u < hd.n_units; u += NT) {
-      const uint32_t m = um[u];
-      const int st = (int)(m & 0xffffu), ng = (int)((m >> 16) & 255), nu = (int)(m >> 24);
-      const float g = rd<BF>(dot_row<E4>(gu, st, ng, xm));
-      const float up = rd<BF>(dot_row<E4>(gu, st + ng, nu, xm));
-      act[u] = rd<BF>(rd<BF>(silu(g)) * up);
-    }
-  }
-  lds_barrier();
+  // ---- stage C: down_proj by residual row (units ascending), the residual add on every row
+  // (:791), and this thread's terms of the next sum of squares (rows t, t + 512, ... in order)
   float s2 = 0.0f;
   {
     const uint16_t* dp = reinterpret_cast<const uint16_t*>(hot + hd.down_ptr);
     const uint8_t* de = hot + hd.down_ent;
-    for (int i = t; i < H; i += NT) {
-      const float d = rd<BF>(dot_row<E4>(de, dp[i], (int)dp[i + 1] - (int)dp[i], act));
-      const float hv = rd<BF>(h[i] + d);
-      h[i] = hv;
-      s2 = s2 + hv * hv;
+    int a[8], n[8];
+    float d[8];
+#pragma unroll
+    for (int k = 0; k < 8; k++) {
+      const int i = t + k * NT;
+      a[k] = 0;
+      n[k] = 0;
+      if (i < H) {
+        a[k] = dp[i];
+        n[k] = (int)dp[i + 1] - a[k];
+      }
+    }
+#pragma unroll
+    for (int k = 0; k < 8; k++) d[k] = chunk4<E4>(de, a[k], n[k], 0, act, 0.0f);
+#pragma unroll
+    for (int k = 0; k < 8; k++) {
+      const int i = t + k * NT;
+      if (i < H) {
+        const float dk = rd<BF>(rest4<E4>(de, a[k], n[k], act, d[k]));
+        const float hv = rd<BF>(h[i] + dk);
+        h[i] = hv;
+        s2 = s2 + hv * hv;
+      }
     }
   }
   const float ssn = sum512(s2, LF(L_WSUM));
   if (PROF_ON && t == 0) {
     const uint64_t c1 = cycles();
-    pa[4] += c1 - c0;
+    pa[5] += c1 - c0;
     pa[15] = c1;
   }
   return ssn;
@@ -448,7 +542,7 @@ __device__ __forceinline__ float layer(const lxm_params& p, int L, int step, flo
 // out_proj's output into h. Uniform control flow: every condition is read from LDS after a
 // barrier.
 template <bool BF, bool E4>
-__device__ void gdn_active(const lxm_params& p, int L, int step, float r1) {
+__device__ void gdn_active(const lxm_params& p, int L, int step) {
   using E = Ent<E4>;
   const int t = threadIdx.x, H = p.hidden;
   const uint8_t* hot = smem + L_HOT;
@@ -476,9 +570,7 @@ __device__ void gdn_active(const lxm_params& p, int L, int step, float r1) {
   const void* cs = p.conv[L];
   const lxm_chan* chans = reinterpret_cast<const lxm_chan*>(blob + ly.chan);
   const uint8_t* qent = blob + ly.qkv_ent;
-  // the GDN norm's output, from the ring (this step's slot, written by this workgroup)
-  const float* xg = p.ring + ((size_t)(step & 3) * p.n_layers + L) * H;
-  (void)r1;
+  const float* xg = LF(L_XG);  // the GDN norm's output (stage A)
   if (t == 0) flags[F_OUT] = 0;
   for (int c = t; c < H; c += NT) xm[c] = 0.0f;  // out_proj's running sums
   __syncthreads();  // and the ring's stores of this step, visible to every thread
@@ -563,12 +655,12 @@ __device__ void gdn_active(const lxm_params& p, int L, int step, float r1) {
       float* S = S0 + (size_t)vh * KD * VD;
       const float e = ev[vh];
       if (e != 1.0f)
-        for (int i0 = 0; i0 < KD; i0 += 16) {  // 16 loads in flight, then the stores
-          float v[16];
+        for (int i0 = 0; i0 < KD; i0 += 64) {  // 64 loads in flight, then the stores
+          float v[64];
 #pragma unroll
-          for (int k = 0; k < 16; k++) v[k] = S[(size_t)(i0 + k) * VD + j];
+          for (int k = 0; k < 64; k++) v[k] = S[(size_t)(i0 + k) * VD + j];
 #pragma unroll
-          for (int k = 0; k < 16; k++) S[(size_t)(i0 + k) * VD + j] = v[k] * e;
+          for (int k = 0; k < 64; k++) S[(size_t)(i0 + k) * VD + j] = v[k] * e;
         }
       if (nk > 0) {
         const float kv = row_cascade(S, j, nzk, nk, kn);
@@ -697,7 +789,7 @@ __device__ void run_chain(const lxm_params& p) {
       lds_barrier();
       if (PROF_ON && t == 0) {
         const uint64_t c = cycles();
-        pa[5] += c - pa[15];
+        pa[1] += c - pa[15];
         pa[15] = c;
       }
     }

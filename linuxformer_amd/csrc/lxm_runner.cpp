@@ -1,0 +1,179 @@
+// lxm_runner: replay a packed decode (written by linuxformer_amd.mega.Mega.dump) through the C ABI
+// of liblxm.so, without Python: the binding a foreign host (C, Go via cgo, ...) would use, and the
+// process rocprofv3 profiles.
+//
+//   lxm_runner <dump dir> <launches> [tokens per launch]
+//
+// The dump's manifest lists each lxm_params pointer field with the file holding its device
+// buffer ("buf"), a zeroed buffer size ("zero"), or a list of files whose device copies form a
+// pointer array ("ptrs", the per-layer states). Every launch continues the stream from the last
+// prediction of the one before. Prints one JSON line: tokens, per-launch kernel milliseconds
+// (hipEvent), tok/s, the last prediction.
+#include <dlfcn.h>
+#include <hip/hip_runtime.h>
+
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <fstream>
+#include <map>
+#include <sstream>
+#include <string>
+#include <vector>
+
+#include "../../include/lxm.h"
+
+#define CK(x)                                                                    \
+  do {                                                                           \
+    hipError_t e_ = (x);                                                         \
+    if (e_ != hipSuccess) {                                                      \
+      fprintf(stderr, "%s:%d %s\n", __FILE__, __LINE__, hipGetErrorString(e_)); \
+      exit(1);                                                                   \
+    }                                                                            \
+  } while (0)
+
+static std::vector<char> slurp(const std::string& path) {
+  std::ifstream f(path, std::ios::binary);
+  if (!f) {
+    fprintf(stderr, "cannot read %s\n", path.c_str());
+    exit(1);
+  }
+  return std::vector<char>((std::istreambuf_iterator<char>(f)), std::istreambuf_iterator<char>());
+}
+
+static void* upload(const std::string& path, size_t* n = nullptr) {
+  std::vector<char> b = slurp(path);
+  void* d = nullptr;
+  CK(hipMalloc(&d, b.size() + 256));
+  CK(hipMemcpy(d, b.data(), b.size(), hipMemcpyHostToDevice));
+  if (n) *n = b.size();
+  return d;
+}
+
+int main(int argc, char** argv) {
+  if (argc < 3) {
+    fprintf(stderr, "usage: %s <dump dir> <launches> [tokens]\n", argv[0]);
+    return 2;
+  }
+  const std::string dir = argv[1];
+  const int launches = atoi(argv[2]);
+  std::string libpath = std::string(getenv("LXM_LIB") ? getenv("LXM_LIB") : "");
+  if (libpath.empty()) {
+    std::ifstream lf(dir + "/lib.txt");
+    std::getline(lf, libpath);
+  }
+  void* h = dlopen(libpath.c_str(), RTLD_NOW);
+  if (!h) {
+    fprintf(stderr, "dlopen %s: %s\n", libpath.c_str(), dlerror());
+    return 1;
+  }
+  auto run = (int (*)(const lxm_params*, const lxm_params*, int, int, void*))dlsym(h, "lxm_run");
+  auto last = (int (*)(void))dlsym(h, "lxm_last_error");
+  if (!run || !last) return 1;
+
+  std::vector<char> pb = slurp(dir + "/params.bin");
+  if (pb.size() != sizeof(lxm_params)) {
+    fprintf(stderr, "params.bin: %zu bytes, lxm_params is %zu\n", pb.size(), sizeof(lxm_params));
+    return 1;
+  }
+  lxm_params p;
+  memcpy(&p, pb.data(), sizeof p);
+  std::map<std::string, void**> field = {
+      {"layers", (void**)&p.layers},     {"blob", (void**)&p.blob},
+      {"rec", (void**)&p.rec},           {"conv", (void**)&p.conv},
+      {"emb_ptr", (void**)&p.emb_ptr},   {"emb_ent", (void**)&p.emb_ent},
+      {"w1_final", (void**)&p.w1_final}, {"head_rows", (void**)&p.head_rows},
+      {"head_ptr", (void**)&p.head_ptr}, {"head_ent", (void**)&p.head_ent},
+      {"forced", (void**)&p.forced},     {"preds", (void**)&p.preds},
+      {"inputs", (void**)&p.inputs},     {"trace", (void**)&p.trace},
+      {"ring", (void**)&p.ring},         {"hn", (void**)&p.hn},
+      {"sync", (void**)&p.sync},         {"keys", (void**)&p.keys},
+      {"err", (void**)&p.err},           {"prof", (void**)&p.prof}};
+  for (auto& kv : field) *kv.second = nullptr;
+  int n_blocks = 0, lds = 0;
+  std::ifstream mf(dir + "/manifest.txt");
+  std::string line;
+  std::vector<std::pair<void*, size_t>> zeroed;
+  while (std::getline(mf, line)) {
+    std::istringstream ss(line);
+    std::string kind, name;
+    ss >> kind >> name;
+    if (kind == "launch") {
+      ss >> n_blocks >> lds;
+    } else if (kind == "buf") {
+      std::string file;
+      ss >> file;
+      *field.at(name) = upload(dir + "/" + file);
+    } else if (kind == "zero") {
+      size_t n;
+      ss >> n;
+      void* d;
+      CK(hipMalloc(&d, n));
+      CK(hipMemset(d, 0, n));
+      zeroed.push_back({d, n});
+      *field.at(name) = d;
+    } else if (kind == "ptrs") {
+      int n;
+      ss >> n;
+      std::vector<void*> ptrs(n);
+      for (int i = 0; i < n; i++) {
+        std::string file;
+        ss >> file;
+        ptrs[i] = upload(dir + "/" + file);
+      }
+      void* d;
+      CK(hipMalloc(&d, sizeof(void*) * n));
+      CK(hipMemcpy(d, ptrs.data(), sizeof(void*) * n, hipMemcpyHostToDevice));
+      *field.at(name) = d;
+    }
+  }
+  if (argc > 3) p.n_tokens = atoi(argv[3]);
+  int* forced_d = (int*)p.forced;
+  int* preds_d = p.preds;
+  lxm_params* pd;
+  CK(hipMalloc(&pd, sizeof p));
+  hipStream_t st;
+  CK(hipStreamCreate(&st));
+  hipEvent_t e0, e1;
+  CK(hipEventCreate(&e0));
+  CK(hipEventCreate(&e1));
+  std::vector<float> ms;
+  int tok = 0;
+  CK(hipMemcpy(&tok, forced_d, 4, hipMemcpyDeviceToHost));
+  for (int k = 0; k < launches; k++) {
+    // sync words, keys and the error flag start at zero; the stream continues from `tok`
+    CK(hipMemsetAsync(p.sync, 0, LXM_NSYNC * 4, st));
+    CK(hipMemsetAsync(p.keys, 0, 16, st));
+    CK(hipMemsetAsync(p.err, 0, 4, st));
+    CK(hipMemcpyAsync(forced_d, &tok, 4, hipMemcpyHostToDevice, st));
+    p.n_forced = 1;
+    CK(hipMemcpyAsync(pd, &p, sizeof p, hipMemcpyHostToDevice, st));
+    CK(hipEventRecord(e0, st));
+    int rc = run(&p, pd, n_blocks, lds, st);
+    if (rc) {
+      fprintf(stderr, "lxm_run: hipError %d\n", rc);
+      return 1;
+    }
+    CK(hipEventRecord(e1, st));
+    CK(hipStreamSynchronize(st));
+    float t = 0;
+    CK(hipEventElapsedTime(&t, e0, e1));
+    ms.push_back(t);
+    int err = 0;
+    CK(hipMemcpy(&err, p.err, 4, hipMemcpyDeviceToHost));
+    if (err || last()) {
+      fprintf(stderr, "decode failed: err %d\n", err);
+      return 1;
+    }
+    CK(hipMemcpy(&tok, preds_d + p.n_tokens - 1, 4, hipMemcpyDeviceToHost));
+    fprintf(stderr, "[lxm_runner] launch %d/%d: %d tokens in %.3f ms\n", k + 1, launches,
+            p.n_tokens, t);
+  }
+  double tot = 0;
+  for (float t : ms) tot += t;
+  printf("{\"tokens_per_launch\": %d, \"launches\": %d, \"kernel_ms\": [", p.n_tokens, launches);
+  for (size_t i = 0; i < ms.size(); i++) printf("%s%.3f", i ? ", " : "", ms[i]);
+  printf("], \"tok_per_s\": %.1f, \"last_pred\": %d}\n", p.n_tokens * launches / (tot * 1e-3), tok);
+  fflush(stdout);
+  return 0;
+}

@@ -357,7 +357,8 @@ class Mega:
                            "blob_bytes": int(self.blob.numel()), "qk_total": qk_total,
                            "head_nnz": int(hptr[-1]), "vocab": V})
 
-    PHASES = ("embedding", "layer staging", "GDN norm + gates", "active heads", "MLP", "trace",
+    PHASES = ("embedding", "layer staging (+trace)", "norms (stage A)",
+              "gates + MLP units (stage B)", "active heads + MLP redo", "down_proj + next norm (stage C)",
               "final norm + publish", "head argmax wait")
 
     def phase_report(self, prof: torch.Tensor) -> dict:
@@ -374,6 +375,51 @@ class Mega:
         out["helper compute max"] = round(max(hc) / n, 1)
         out["tokens"] = n
         return out
+
+    def dump(self, path: str, forced, n: int, prof: bool = False) -> None:
+        """Write everything a launch needs (tables, states, parameter block, manifest) to path,
+        for csrc/lxm_runner.cpp to replay through the C ABI without Python."""
+        import os
+
+        os.makedirs(path, exist_ok=True)
+        d = self.dims
+        lines = [f"launch x {self.ncta} {self.lds}"]
+
+        def buf(name, t):
+            fn = name + ".bin"
+            with open(os.path.join(path, fn), "wb") as f:
+                f.write(t.detach().cpu().contiguous().view(torch.uint8).numpy().tobytes())
+            lines.append(f"buf {name} {fn}")
+
+        for name in ("layers_d", "blob", "emb_ptr", "emb_ent", "w1_final", "head_rows",
+                     "head_ptr", "head_ent"):
+            buf({"layers_d": "layers"}.get(name, name), getattr(self, name))
+        buf("forced", torch.tensor([int(forced[0])], dtype=torch.int32))
+        for field, attr in (("rec", "recurrent_states"), ("conv", "conv_states")):
+            files = []
+            for L in range(d.n_layers):
+                fn = f"{field}{L}.bin"
+                t = getattr(self.cache.layers[L], attr)[0]
+                with open(os.path.join(path, fn), "wb") as f:
+                    f.write(t.detach().cpu().contiguous().view(torch.uint8).numpy().tobytes())
+                files.append(fn)
+            lines.append(f"ptrs {field} {d.n_layers} " + " ".join(files))
+        for name, nbytes in (("preds", 4 * n), ("ring", self.ring.numel() * 4),
+                             ("hn", self.hn.numel() * 4), ("sync", NSYNC * 4), ("keys", 16),
+                             ("err", 4)):
+            lines.append(f"zero {name} {nbytes}")
+        if prof:
+            lines.append(f"zero prof {8 * (32 + 2 * self.ncta)}")
+        p = Params(hidden=d.hidden, n_layers=d.n_layers, nk=d.nk, kd=KD, nv=d.nv, vd=VD,
+                   n_conv=d.n_conv, vocab=self.vocab, bf16=int(self.bf), n_blocks=self.ncta,
+                   rms_eps=d.rms_eps, head_lds=self.head_lds, e4=int(self.e4), n_forced=1,
+                   n_tokens=n, n_qk_total=self.n_qk_total)
+        with open(os.path.join(path, "params.bin"), "wb") as f:
+            f.write(bytes(p))
+        with open(os.path.join(path, "manifest.txt"), "w") as f:
+            f.write("\n".join(lines) + "\n")
+        with open(os.path.join(path, "lib.txt"), "w") as f:
+            f.write(mk_build.LIB + "\n")
 
     def _state_ptrs(self):
         rs, cs = [], []

@@ -12,6 +12,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
 LIBDIR = os.path.join(HERE, "_lib")
 LIB = os.path.join(LIBDIR, "liblxm.so")
+RUNNER = os.path.join(LIBDIR, "lxm_runner")
 SOURCES = ["lxm_decode.hip"]
 HEADERS = ["lxm_math.h", os.path.join("..", "..", "include", "lxm.h")]
 # -ffp-contract=off: no a*b+c is fused (the rounding contract); packed fp32 ops disabled
@@ -37,6 +38,11 @@ def build(verbose: bool = False) -> str:
     if verbose and r.stderr:
         print(r.stderr)
     os.replace(tmp, LIB)
+    r = subprocess.run([hipcc(), "-O2", "-std=c++17", "-o", RUNNER + ".tmp",
+                        os.path.join(CSRC, "lxm_runner.cpp"), "-ldl"], capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError(f"hipcc (runner) failed ({r.returncode}):\n{r.stderr[-4000:]}")
+    os.replace(RUNNER + ".tmp", RUNNER)
     return LIB
 
 
