@@ -31,6 +31,7 @@ extern "C" {
 #define LXM_MAXDEC 512      /* decaying value heads of one layer */
 #define LXM_HOT_MAX 65536   /* bytes of one layer's resident tables */
 #define LXM_NSYNC 256       /* uint32 words of the sync area */
+#define LXM_OUT_MAX 1024    /* out_proj entries of the rows one helper workgroup computes */
 
 /* One layer's resident tables (the "hot" blob the chain workgroup stages in LDS). All offsets
    are bytes from the start of the hot blob, 16-byte aligned. */
@@ -75,8 +76,8 @@ typedef struct lxm_layer {
   int64_t qkv_ent;         /* entries (column) */
   int64_t b_row, b_ent;    /* lxm_row[nv], entries (column) */
   int64_t z_row, z_ent;    /* lxm_row[nv * vd], entries (column) */
-  int64_t out_ptr;         /* per key head int32[hidden + 1] (nk of them) */
-  int64_t out_ent;         /* entries (dim within the key head's value dims) */
+  int64_t out_ptr;         /* int32[hidden + 1]: out_proj by residual row */
+  int64_t out_ent;         /* entries (value dim, all heads: vh * vd + j), ascending per row */
   int64_t gnorm;           /* float[vd] */
 } lxm_layer;
 
@@ -100,12 +101,17 @@ typedef struct lxm_params {
   int32_t* preds;          /* (n_tokens) */
   int32_t* inputs;         /* (n_tokens) or null: each step's input as embedded */
   float* trace;            /* (n_tokens, n_layers, hidden) or null: residual after each layer */
-  float* ring;             /* (4, n_layers, hidden): recent GDN norm outputs */
+  float* ring;             /* (4, n_layers, LXM_MAXH): recent GDN norm outputs */
   float* hn;               /* (hidden): the head's normed input, chain -> helpers */
   uint32_t* sync;          /* LXM_NSYNC words, zero at launch */
   unsigned long long* keys;/* (2), zero at launch */
   int32_t* err;            /* (1), zero at launch; nonzero: a spin timed out (1..) */
-  unsigned long long* prof; /* null, or 32 + 2 x n_blocks counters (phase cycles, see the kernel) */
+  unsigned long long* prof; /* null, or 32 + 4 x n_blocks counters (phase cycles, see the kernel) */
+  uint32_t* mb_task;       /* (nv): a GDN event's task per value head, chain -> helpers */
+  float* mb_e;             /* (nv): its decay factor exp(g) */
+  float* mb_qk;            /* (LXM_MAXQKL): the layer's live query/key channel values */
+  float* ybuf;             /* (nv, vd): each value head's gated-norm output */
+  float* xo;               /* (LXM_MAXH): out_proj's rows, rounded, helpers -> chain */
   int32_t n_qk_total, pad;
 } lxm_params;
 
@@ -117,6 +123,9 @@ int lxm_run(const lxm_params* p_host, const lxm_params* p_dev, int n_blocks, int
             void* stream);
 /* mk_smem_base (mega.cu:865): LDS bytes the kernel needs besides the staged head tables. */
 int lxm_lds_base(void);
+/* LDS bytes a helper workgroup needs with head_lds bytes of head tables (the launch's LDS is
+   the larger of this and lxm_lds_base()). */
+int lxm_helper_lds(int head_lds);
 /* mk_max_ctas (mega.cu:876-883): co-resident workgroups at lds_bytes (occupancy x CUs). */
 int lxm_max_blocks(int lds_bytes);
 /* mk_max_smem (mega.cu:885-890): LDS bytes a workgroup may use. */

@@ -5,26 +5,30 @@
 // argmax, fed back as the next input on the GPU; conv windows and recurrent states updated in
 // place. How it computes it is MI355X's own design:
 //
-// * The dependent chain of a token (37 layers, each: RMSNorm, the write gates' check, the MLP,
-//   and rarely the delta rule) runs inside ONE workgroup (block 0, "the chain"): the residual
-//   stream lives in its LDS and every layer's resident tables (norm weights, MLP rows, the
-//   query/key/decay rows the gates read) are streamed into LDS one layer ahead through
-//   registers. A grid barrier costs ~4 us across MI355X's 8 XCDs (measured), so the reference's
-//   ~38 barriered phases per token would cost more than its whole H100 step; here a token
-//   crosses the grid once.
-// * The output head (459,982 rows) is spread over the other 255 workgroups ("helpers"), each
-//   holding its rows' sparse entries in LDS for the whole launch. The chain publishes the
-//   final normed residual (agent-scope atomic stores, then a relaxed flag), every helper
-//   reduces its rows to one argmax key and folds it into a 64-bit atomicMax, then counts
-//   itself done; the chain waits for the count. Keys order by (value, lower index) as
-//   torch.argmax breaks ties.
+// * The dependent chain of a token (37 layers, each: RMSNorm, the write gates, the MLP) runs
+//   inside ONE workgroup (block 0, "the chain"): the residual stream lives in its LDS and every
+//   layer's resident tables (norm weights, MLP rows, the query/key/decay rows the gates read)
+//   are streamed into LDS one layer ahead through registers. A grid-wide round trip costs
+//   ~4 us across MI355X's 8 XCDs (measured), so the reference's ~38 barriered phases per token
+//   would cost more than its whole H100 step; here a token crosses the grid once, plus once
+//   per layer whose write gates open.
+// * The other workgroups ("helpers") serve events the chain posts in one 32-bit word:
+//   - HEAD (once per token): each helper holds a slice of the output head (459,982 rows) in
+//     LDS for the whole launch, reduces its rows to one argmax key and folds it into a 64-bit
+//     atomicMax. Keys order by (value, lower index) as torch.argmax breaks ties.
+//   - GDN (a layer whose gates opened): helper 1 + vh owns value head vh's recurrent state (of
+//     every layer: one owner, so the state never needs cross-XCD coherence) and runs its delta
+//     rule, gated norm and output; then every helper computes a slice of out_proj's rows from
+//     all heads' outputs. The chain adds the rows to the residual.
+//   Cross-block data moves through agent-scope atomic loads and stores (sc1 on gfx950) and
+//   two monotone counters; a counter's target is known to every party, so nothing is reset.
 // * Gates instead of speculation: the chain computes, for each layer, the query/key channels'
 //   conv outputs and the decays first (a few rows), so it knows exactly whether the layer's
-//   delta rule runs and whether it changes the residual. Nothing is ever redone. The conv
-//   windows are not shifted channel by channel every step: the chain keeps the last four
-//   tokens' GDN norm outputs per layer (a ring in HBM), recomputes the few windows an active
-//   head needs from them, keeps its query/key channels' windows in LDS, and writes every
-//   window once at the end of the launch.
+//   delta rule runs and whether it can change the residual; the MLP is computed alongside and
+//   redone only when it did. The conv windows are not shifted channel by channel every step:
+//   the chain keeps the last four tokens' GDN norm outputs per layer (a ring in HBM), the
+//   helpers rebuild the few windows an active head needs from it, the chain keeps its
+//   query/key channels' windows in LDS, and every window is written once at the launch's end.
 //
 // Arithmetic: the rounding contract of lxm_math.h; sums in the orders documented per site.
 #include <hip/hip_runtime.h>
@@ -42,70 +46,56 @@ using namespace lxm;
 #define VD LXM_VD
 #define RMAX LXM_RMAX
 #define TIMEOUT_TICKS 300000000ull  // 3 s of the 100 MHz wall clock
+static_assert(MAXH == 8 * NT, "eight residual rows per thread cover any hidden size");
 
 // ---------------------------------------------------------------------------------------------
 // LDS layout of the chain workgroup (bytes)
 #define L_HOT 0
 #define L_H (L_HOT + LXM_HOT_MAX)
 #define L_XM (L_H + 4 * MAXH)
-#define L_ACT (L_XM + 4 * MAXH)
+#define L_XG (L_XM + 4 * MAXH)
+#define L_ACT (L_XG + 4 * MAXH)
 #define L_HIST (L_ACT + 4 * LXM_MAXU)
 #define L_QKCUR (L_HIST + 4 * 3 * LXM_MAXQK)
-#define L_QD (L_QKCUR + 4 * LXM_MAXQKL)
-#define L_KDV (L_QD + 4 * KD)
-#define L_QN (L_KDV + 4 * KD)
-#define L_KN (L_QN + 4 * KD)
-#define L_NZQ (L_KN + 4 * KD)
-#define L_NZK (L_NZQ + 4 * KD)
-#define L_VB (L_NZK + 4 * KD)
-#define L_OB (L_VB + 4 * RMAX * VD)
-#define L_ZB (L_OB + 4 * RMAX * VD)
-#define L_EV (L_ZB + 4 * RMAX * VD)
-#define L_BETA (L_EV + 4 * 256)
-#define L_WSUM (L_BETA + 4 * RMAX)
+#define L_EV (L_QKCUR + 4 * LXM_MAXQKL)
+#define L_WSUM (L_EV + 4 * 256)
 #define L_FLAGS (L_WSUM + 4 * 32)
 #define L_PROF (L_FLAGS + 4 * 256)
-#define L_XG (L_PROF + 8 * 32)
-#define L_CHAIN_END (L_XG + 4 * MAXH)
-// flags (int): [0] any head active, [1] any output, [2] nq, [3] nk, [4] scratch, [8] token
-// [16 + kh] per key head: bit 0 query nonzero, bit 1 key nonzero, bit 2 decay
+#define L_LT (L_PROF + 8 * 32)
+#define L_CHAIN_END (L_LT + 16 * 64)
+// flags (int): [0] any head active, [1] any query live (the residual may change), [4] ok,
+// [8] token, [16 + kh] per key head: bit 0 query nonzero, bit 1 key nonzero, bit 2 a decay
 #define F_ANY 0
 #define F_OUT 1
-#define F_NQ 2
-#define F_NK 3
 #define F_OK 4
 #define F_TOK 8
 #define F_KH 16
 
-// sync words (uint32, 128-byte apart groups)
-#define S_TOKFLAG 0
-#define S_COUNT 32
-#define S_DONE 64
-#define S_ERRSEEN 96
+// LDS layout of a helper workgroup, after its head tables (p.head_lds bytes)
+#define HX_X 0                        // hidden: the head's normed input, or a task's GDN norm
+#define HX_QD (HX_X + 4 * MAXH)       // dense query / key of the task's key head, raw
+#define HX_KD (HX_QD + 4 * KD)
+#define HX_QN (HX_KD + 4 * KD)        // the same after l2norm (query scaled by 1/16)
+#define HX_KN (HX_QN + 4 * KD)
+#define HX_V (HX_KN + 4 * KD)         // value channels' conv outputs
+#define HX_Z (HX_V + 4 * VD)          // in_proj_z rows
+#define HX_O (HX_Z + 4 * VD)          // the head's output o
+#define HX_DL (HX_O + 4 * VD)         // delta = (v - kv) beta
+#define HX_BS (HX_DL + 4 * VD)        // per row block (16 rows) partial sums, [16][VD]
+#define HX_MISC (HX_BS + 4 * 16 * VD) // ints: [0] nq, [1] nk, [2] beta bits, [4] event, [5] ok
+#define HX_OP (HX_MISC + 256)         // out_proj: the helper's row pointers (32 ints)
+#define HX_OE (HX_OP + 4 * 32)        // its entries (LXM_OUT_MAX, 8 bytes each at most)
+#define HX_OY (HX_OE + 8 * LXM_OUT_MAX)  // the head outputs each entry reads
+#define HX_END (HX_OY + 4 * LXM_OUT_MAX)
 
-__device__ __forceinline__ uint32_t ld_rlx(const uint32_t* p) {
-  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ void st_rlx(uint32_t* p, uint32_t v) {
-  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ float ld_rlxf(const float* p) {
-  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ void st_rlxf(float* p, float v) {
-  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-// every earlier memory op of this wave has completed (its stores are visible at agent scope
-// when they were agent-scope atomics)
-__device__ __forceinline__ void drain() {
-  __atomic_signal_fence(__ATOMIC_SEQ_CST);
-  __builtin_amdgcn_s_waitcnt(0);
-  __atomic_signal_fence(__ATOMIC_SEQ_CST);
-}
-__device__ __forceinline__ uint64_t wall() { return __builtin_amdgcn_s_memrealtime(); }
+// sync words (uint32 indices into p.sync, groups 128 bytes apart)
+#define S_EV 0     // the event word: seq << 8 | layer << 2 | out << 1 | kind (0 head, 1 gdn)
+#define S_CALL 32  // helpers done with an event (each helper, each event)
+#define S_CVH 64   // value-head helpers done with a GDN event's heads (each, each GDN event)
+#define S_DONE 96
+#define EV_GDN 1u
+#define EV_OUT 2u
 
-// global-address-space views of generic pointers: loads and stores through them are
-// global_load/global_store (flat ones would also count against lgkmcnt, i.e. LDS waits)
 #define GAS __attribute__((address_space(1)))
 template <class T>
 __device__ __forceinline__ GAS T* gp(T* q) {
@@ -115,6 +105,44 @@ template <class T>
 __device__ __forceinline__ const GAS T* gp(const T* q) {
   return (const GAS T*)q;
 }
+
+// a struct from global memory through global loads (a generic copy would be flat loads)
+template <class T>
+__device__ __forceinline__ T ldg(const T* q) {
+  static_assert(sizeof(T) % 4 == 0, "whole words");
+  T r;
+  const GAS uint32_t* src = gp(reinterpret_cast<const uint32_t*>(q));
+  uint32_t* dst = reinterpret_cast<uint32_t*>(&r);
+#pragma unroll
+  for (int i = 0; i < (int)(sizeof(T) / 4); i++) dst[i] = src[i];
+  return r;
+}
+typedef float v4f __attribute__((ext_vector_type(4)));
+
+// agent-scope relaxed atomics: sc1 loads and stores on gfx950, coherent across the XCDs
+__device__ __forceinline__ uint32_t ld_rlx(const uint32_t* p) {
+  return __hip_atomic_load(gp(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void st_rlx(uint32_t* p, uint32_t v) {
+  __hip_atomic_store(gp(p), v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float ld_rlxf(const float* p) {
+  return __hip_atomic_load(gp(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void st_rlxf(float* p, float v) {
+  __hip_atomic_store(gp(p), v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void add_rlx(uint32_t* p, uint32_t v) {
+  __hip_atomic_fetch_add(gp(p), v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+// every earlier memory op of this wave has completed (its stores are visible at agent scope
+// when they were agent-scope atomics)
+__device__ __forceinline__ void drain() {
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+  __builtin_amdgcn_s_waitcnt(0);
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+}
+__device__ __forceinline__ uint64_t wall() { return __builtin_amdgcn_s_memrealtime(); }
 
 // a workgroup barrier ordering LDS only: global loads in flight (the next layer's tables)
 // stay in flight across it
@@ -127,35 +155,58 @@ __device__ __forceinline__ void lds_barrier() {
 // In-kernel phase counters (lx/csrc/mega.cu's prof buffer and MK_SUBPROF checkpoints): with
 // p.prof set, thread 0 of the chain adds the shader-clock cycles of each phase into an LDS
 // slot; the slots are written to p.prof at the end. Phases: 0 embedding, 1 layer staging (and
-// the trace), 2 the norms (stage A), 3 the gates and the MLP units (stage B), 4 active heads
+// the trace), 2 the norms (stage A), 3 the gates and the MLP units (stage B), 4 a GDN event
 // and the MLP's redo, 5 down_proj and the next norm's sums (stage C), 6 final norm + publish,
-// 7 waiting for the head's argmax; counters 16 active layer-steps, 17 tokens.
+// 7 waiting for the head's argmax; counters 16 GDN events, 17 tokens. Helper b adds at
+// 32 + 4b: 0 waiting for events, 1 head rows, 2 its value head's delta rule, 3 out_proj rows
+// (with the wait for every head's output).
 #define PROF_ON (p.prof != nullptr)
 __device__ __forceinline__ uint64_t cycles() { return __builtin_readcyclecounter(); }
 
-// spin (one thread) until *p >= target; false on timeout or another block's error
+// spin (one thread) until the counter reaches target (modulo 2^32); false on timeout or
+// another block's error
 __device__ bool spin_ge(const uint32_t* p, uint32_t target, int32_t* err, int code) {
   const uint64_t t0 = wall();
-  while (ld_rlx(p) < target) {
+  while ((int32_t)(ld_rlx(p) - target) < 0) {
     __builtin_amdgcn_s_sleep(1);
-    if (__hip_atomic_load(err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) return false;
+    if (__hip_atomic_load(gp(err), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) return false;
     if (wall() - t0 > TIMEOUT_TICKS) {
-      __hip_atomic_fetch_max(err, code, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __hip_atomic_fetch_max(gp(err), code, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       return false;
     }
   }
   return true;
 }
+// spin (one thread) until the word differs from last; 0 on timeout or another block's error
+__device__ bool spin_ne(const uint32_t* p, uint32_t last, uint32_t* out, int32_t* err, int code) {
+  const uint64_t t0 = wall();
+  uint32_t v;
+  while ((v = ld_rlx(p)) == last) {
+    __builtin_amdgcn_s_sleep(1);
+    if (__hip_atomic_load(gp(err), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) return false;
+    if (wall() - t0 > TIMEOUT_TICKS) {
+      __hip_atomic_fetch_max(gp(err), code, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      return false;
+    }
+  }
+  *out = v;
+  return true;
+}
 
 // ---------------------------------------------------------------------------------------------
-// packed entries
-template <bool BF>
+// packed entries (LDS or global)
+template <bool E4>
 struct Ent;
 template <>
 struct Ent<true> {
   static constexpr int SZ = 4;
   __device__ static __forceinline__ void at(const uint8_t* base, int64_t e, int& idx, float& v) {
     const uint32_t w = reinterpret_cast<const uint32_t*>(base)[e];
+    idx = (int)(w & 0xffffu);
+    v = bf16f(w >> 16);
+  }
+  __device__ static __forceinline__ void gat(const uint8_t* base, int64_t e, int& idx, float& v) {
+    const uint32_t w = gp(reinterpret_cast<const uint32_t*>(base))[e];
     idx = (int)(w & 0xffffu);
     v = bf16f(w >> 16);
   }
@@ -168,30 +219,123 @@ struct Ent<false> {
     idx = (int)w.x;
     v = __uint_as_float(w.y);
   }
+  __device__ static __forceinline__ void gat(const uint8_t* base, int64_t e, int& idx, float& v) {
+    typedef uint32_t v2u __attribute__((ext_vector_type(2)));
+    const v2u w = gp(reinterpret_cast<const v2u*>(base))[e];
+    idx = (int)w.x;
+    v = __uint_as_float(w.y);
+  }
 };
 
-// sum over a row's entries of x[idx] * w, in entry order from +0 (terms with x == 0 skipped,
-// which leaves the sum's bits unchanged: a sum from +0 never yields -0)
-template <bool E4>
-__device__ __forceinline__ float dot_row(const uint8_t* ent, int64_t start, int len, const float* x) {
-  float s = 0.0f;
-  for (int k = 0; k < len; k++) {
-    int i;
-    float w;
-    Ent<E4>::at(ent, start + k, i, w);
-    const float xv = x[i];
-    if (xv != 0.0f) s = s + xv * w;
+// Dot products of a sparse row with x, in entry order from +0, terms with x == 0 skipped
+// (which leaves the sum's bits unchanged: a sum from +0 never yields -0). A chunk issues the
+// loads of N entries at once, unconditionally (every table is followed by at least N entries'
+// worth of bytes, so they stay inside the LDS region or the blob), and drops the terms past the
+// row's end by selects, so the code has no branches. Where: 0 x in LDS, 1 entries in global
+// memory and x in LDS, 2 entries in global memory and x in global memory (agent-scope loads).
+template <bool E4, int N, int WHERE>
+__device__ __forceinline__ float chunk(const uint8_t* ent, int64_t start, int n, int k0,
+                                       const float* x, float s) {
+  int i[N];
+  float w[N], xv[N];
+#pragma unroll
+  for (int j = 0; j < N; j++) {
+    if constexpr (WHERE == 0) Ent<E4>::at(ent, start + k0 + j, i[j], w[j]);
+    else Ent<E4>::gat(ent, start + k0 + j, i[j], w[j]);
   }
+#pragma unroll
+  for (int j = 0; j < N; j++) i[j] = k0 + j < n ? i[j] : 0;
+#pragma unroll
+  for (int j = 0; j < N; j++) {
+    if constexpr (WHERE == 2) xv[j] = ld_rlxf(x + i[j]);
+    else xv[j] = x[i[j]];
+  }
+#pragma unroll
+  for (int j = 0; j < N; j++) s = (k0 + j < n && xv[j] != 0.0f) ? s + xv[j] * w[j] : s;
+  return s;
+}
+template <bool E4, int N, int WHERE>
+__device__ __forceinline__ float rest(const uint8_t* ent, int64_t start, int n, const float* x,
+                                      float s) {
+  for (int k0 = N; k0 < n; k0 += N) s = chunk<E4, N, WHERE>(ent, start, n, k0, x, s);
+  return s;
+}
+template <bool E4, int N, int WHERE>
+__device__ __forceinline__ float dot(const uint8_t* ent, int64_t start, int n, const float* x) {
+  return rest<E4, N, WHERE>(ent, start, n, x, chunk<E4, N, WHERE>(ent, start, n, 0, x, 0.0f));
+}
+// R rows at once: the first N entries of every row, then N more of every row while any row of
+// this thread has more (a row past its end adds nothing). Each round loads all rows' entries,
+// then all their x values, so a round is two LDS round trips. Entry reads run up to the
+// longest row's length past a shorter row's start: the tables sit inside the 64 KB hot region,
+// followed by other LDS arrays.
+template <bool E4, int N, int R>
+__device__ __forceinline__ void dots_round(const uint8_t* ent, const int (&st)[R],
+                                           const int (&n)[R], int k0, const float* x,
+                                           float (&s)[R]) {
+  int i[R][N];
+  float w[R][N], xv[R][N];
+#pragma unroll
+  for (int r = 0; r < R; r++)
+#pragma unroll
+    for (int j = 0; j < N; j++) Ent<E4>::at(ent, st[r] + k0 + j, i[r][j], w[r][j]);
+#pragma unroll
+  for (int r = 0; r < R; r++)
+#pragma unroll
+    for (int j = 0; j < N; j++) i[r][j] = k0 + j < n[r] ? i[r][j] : 0;
+#pragma unroll
+  for (int r = 0; r < R; r++)
+#pragma unroll
+    for (int j = 0; j < N; j++) xv[r][j] = x[i[r][j]];
+#pragma unroll
+  for (int r = 0; r < R; r++)
+#pragma unroll
+    for (int j = 0; j < N; j++)
+      s[r] = (k0 + j < n[r] && xv[r][j] != 0.0f) ? s[r] + xv[r][j] * w[r][j] : s[r];
+}
+template <bool E4, int N, int R>
+__device__ __forceinline__ void dots(const uint8_t* ent, const int (&st)[R], const int (&n)[R],
+                                     const float* x, float (&s)[R]) {
+  int m = 0;
+#pragma unroll
+  for (int r = 0; r < R; r++) {
+    s[r] = 0.0f;
+    m = n[r] > m ? n[r] : m;
+  }
+  dots_round<E4, N, R>(ent, st, n, 0, x, s);
+  for (int k0 = N; k0 < m; k0 += N) dots_round<E4, N, R>(ent, st, n, k0, x, s);
+}
+
+// A wave's tree sum: lane 0 ends with the sum that __shfl_down at offsets 32, 16, ..., 1
+// leaves there (lane l adds lane l + off). Offsets 32 and 16 by gfx950's permlane swaps, 8..1
+// by DPP row shifts; no LDS round trips.
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float x) {
+  return __builtin_bit_cast(
+      float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), CTRL, 0xf, 0xf, true));
+}
+__device__ __forceinline__ float wave_tree(float s) {
+  const uint32_t u = __float_as_uint(s);
+  s = s + __uint_as_float(__builtin_amdgcn_permlane32_swap(u, u, false, false)[1]);
+  const uint32_t v = __float_as_uint(s);
+  s = s + __uint_as_float(__builtin_amdgcn_permlane16_swap(v, v, false, false)[1]);
+  s = s + dpp_f<0x108>(s);  // row_shl:8
+  s = s + dpp_f<0x104>(s);
+  s = s + dpp_f<0x102>(s);
+  s = s + dpp_f<0x101>(s);
   return s;
 }
 
-// the 512-lane hidden sum: lane t's partial (its elements t, t + 512, ... in order), combined
-// within each wave at offsets 32..1, the 8 wave totals at offsets 4, 2, 1. All threads call;
-// all get the sum.
-__device__ __forceinline__ float sum512(float s, float* wsum) {
-  for (int off = 32; off >= 1; off >>= 1) s = s + __shfl_down(s, off, 64);
+// the 512-lane hidden sum: lane t's partial (its elements 4t..4t+3, then 2048+4t..2048+4t+3,
+// in order), combined within each wave at offsets 32..1, the 8 wave totals at offsets 4, 2, 1.
+// All threads call; all get the sum. In two halves, so a caller can put LDS writes between
+// the halves' barriers (the second orders them).
+__device__ __forceinline__ void sum512_begin(float s, float* wsum) {
+  s = wave_tree(s);
   if ((threadIdx.x & 63) == 0) wsum[threadIdx.x >> 6] = s;
   lds_barrier();
+}
+__device__ __forceinline__ float sum512_end(const float* wsum) {
   float w[NW];
 #pragma unroll
   for (int i = 0; i < NW; i++) w[i] = wsum[i];
@@ -202,31 +346,16 @@ __device__ __forceinline__ float sum512(float s, float* wsum) {
     for (int i = 0; i < off; i++) w[i] = w[i] + w[i + off];
   return w[0];
 }
+__device__ __forceinline__ float sum512(float s, float* wsum) {
+  sum512_begin(s, wsum);
+  return sum512_end(wsum);
+}
 
 // the 64-lane head sum over one wave: lane l's partial (elements l, l + 64, ...), offsets
 // 32..1; every lane gets the sum
 __device__ __forceinline__ float sum64(float s) {
-  for (int off = 32; off >= 1; off >>= 1) s = s + __shfl_down(s, off, 64);
-  return __shfl(s, 0, 64);
-}
-
-// ATen's CPU order for a sum over the state's rows (torch .sum(-2)): blocks of 16 rows, each
-// block in order from +0, the block sums in order from +0; rows given ascending
-__device__ __forceinline__ float row_cascade(const float* S, int j, const int* rows, int n,
-                                             const float* f) {
-  float tot = 0.0f, bs = 0.0f;
-  int blk = -1;
-  for (int a = 0; a < n; a++) {
-    const int r = rows[a];
-    if ((r >> 4) != blk) {
-      if (blk >= 0) tot = tot + bs;
-      bs = 0.0f;
-      blk = r >> 4;
-    }
-    bs = bs + S[(size_t)r * VD + j] * f[r];
-  }
-  if (blk >= 0) tot = tot + bs;
-  return tot;
+  return __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(
+                                       __builtin_bit_cast(int, wave_tree(s))));
 }
 
 // ---------------------------------------------------------------------------------------------
@@ -243,13 +372,18 @@ __device__ __forceinline__ float w1_at(const uint8_t* hot, int off, int c) {
 // a conv state value (model dtype) as float
 template <bool BF>
 __device__ __forceinline__ float conv_at(const void* cs, int64_t i) {
-  if constexpr (BF) return bf16f(reinterpret_cast<const uint16_t*>(cs)[i]);
-  else return reinterpret_cast<const float*>(cs)[i];
+  if constexpr (BF) return bf16f(gp(reinterpret_cast<const uint16_t*>(cs))[i]);
+  else return gp(reinterpret_cast<const float*>(cs))[i];
 }
 template <bool BF>
 __device__ __forceinline__ void conv_put(void* cs, int64_t i, float v) {
-  if constexpr (BF) reinterpret_cast<uint16_t*>(cs)[i] = (uint16_t)(__float_as_uint(v) >> 16);
-  else reinterpret_cast<float*>(cs)[i] = v;
+  if constexpr (BF) gp(reinterpret_cast<uint16_t*>(cs))[i] = (uint16_t)(__float_as_uint(v) >> 16);
+  else gp(reinterpret_cast<float*>(cs))[i] = v;
+}
+
+// the ring of GDN norm outputs: slot (step & 3), layer L, MAXH floats each
+__device__ __forceinline__ float* ring_at(const lxm_params& p, int step, int L) {
+  return p.ring + ((size_t)(step & 3) * p.n_layers + L) * MAXH;
 }
 
 // ---------------------------------------------------------------------------------------------
@@ -263,12 +397,31 @@ extern __shared__ __align__(16) uint8_t smem[];
 __device__ __forceinline__ float norm_r(float ss, int H, float eps) {
   return rsqrt_(ss / (float)H + eps);
 }
-__device__ __forceinline__ float hidden_ss(int H) {
-  const float* h = LF(L_H);
+// The residual rows of thread t: 4t..4t+3 and 2048+4t..2048+4t+3 (two 16-byte words of each
+// hidden-sized LDS array). Rows >= H hold +0, and +0 terms leave each lane's sum unchanged.
+__device__ __forceinline__ float sq_terms(const v4f& a, const v4f& b) {
   float s = 0.0f;
-  for (int c = threadIdx.x; c < H; c += NT) s = s + h[c] * h[c];
-  return sum512(s, LF(L_WSUM));
+  s = s + a.x * a.x;
+  s = s + a.y * a.y;
+  s = s + a.z * a.z;
+  s = s + a.w * a.w;
+  s = s + b.x * b.x;
+  s = s + b.y * b.y;
+  s = s + b.z * b.z;
+  s = s + b.w * b.w;
+  return s;
 }
+__device__ __forceinline__ float hidden_ss() {
+  const v4f* h4 = reinterpret_cast<const v4f*>(smem + L_H);
+  const v4f a = h4[threadIdx.x], b = h4[NT + threadIdx.x];
+  return sum512(sq_terms(a, b), LF(L_WSUM));
+}
+
+// The layer table in LDS: each layer's hot blob address and its 16-byte words
+struct LtEnt {
+  const uint8_t* hot;
+  int32_t n16, pad;
+};
 
 // stage layer L's hot blob: global -> registers (fetch, one layer ahead) -> LDS (stage); eight
 // 16-byte words per thread, kept in named registers
@@ -277,10 +430,11 @@ typedef uint32_t v4u __attribute__((ext_vector_type(4)));
 struct Pf {
   v4u w0, w1, w2, w3, w4, w5, w6, w7;
 };
-__device__ __forceinline__ Pf fetch(const lxm_params& p, int L, int n16) {
-  const GAS v4u* src = gp(reinterpret_cast<const v4u*>(p.blob + p.layers[L].hot));
-  const int t = threadIdx.x;
-  // words past the blob: a duplicate of word 0, never staged
+__device__ __forceinline__ Pf fetch(int L) {
+  const LtEnt le = reinterpret_cast<const LtEnt*>(smem + L_LT)[L];
+  const GAS v4u* src = gp(reinterpret_cast<const v4u*>(le.hot));
+  const int t = threadIdx.x, n16 = le.n16;
+  // words past the blob: a duplicate of word 0 (staged, never read as a table)
 #define PF_LD(k) src[t + (k) * NT < n16 ? t + (k) * NT : 0]
   Pf r;
   r.w0 = PF_LD(0);
@@ -294,50 +448,16 @@ __device__ __forceinline__ Pf fetch(const lxm_params& p, int L, int n16) {
 #undef PF_LD
   return r;
 }
-__device__ __forceinline__ void stage(int n16, const Pf& r) {
-  v4u* dst = reinterpret_cast<v4u*>(smem + L_HOT);
-  const int t = threadIdx.x;
-#define PF_ST(k, w) \
-  if (t + (k) * NT < n16) dst[t + (k) * NT] = r.w
-  PF_ST(0, w0);
-  PF_ST(1, w1);
-  PF_ST(2, w2);
-  PF_ST(3, w3);
-  PF_ST(4, w4);
-  PF_ST(5, w5);
-  PF_ST(6, w6);
-  PF_ST(7, w7);
-#undef PF_ST
-}
-
-template <bool BF, bool E4>
-__device__ void gdn_active(const lxm_params& p, int L, int step);
-
-// One chunk of up to 4 entries of a row (entries k0 .. k0 + 3 of start .. start + n): the sum
-// continues in entry order; all loads of the chunk are issued together.
-template <bool E4>
-__device__ __forceinline__ float chunk4(const uint8_t* ent, int start, int n, int k0,
-                                        const float* x, float s) {
-  int i[4];
-  float w[4], xv[4];
-#pragma unroll
-  for (int j = 0; j < 4; j++) {
-    i[j] = 0;
-    w[j] = 0.0f;
-    if (k0 + j < n) Ent<E4>::at(ent, start + k0 + j, i[j], w[j]);
-  }
-#pragma unroll
-  for (int j = 0; j < 4; j++) xv[j] = x[i[j]];
-#pragma unroll
-  for (int j = 0; j < 4; j++)
-    if (k0 + j < n && xv[j] != 0.0f) s = s + xv[j] * w[j];
-  return s;
-}
-template <bool E4>
-__device__ __forceinline__ float rest4(const uint8_t* ent, int start, int n, const float* x,
-                                       float s) {
-  for (int k0 = 4; k0 < n; k0 += 4) s = chunk4<E4>(ent, start, n, k0, x, s);
-  return s;
+__device__ __forceinline__ void stage(const Pf& r) {
+  v4u* dst = reinterpret_cast<v4u*>(smem + L_HOT) + threadIdx.x;
+  dst[0 * NT] = r.w0;
+  dst[1 * NT] = r.w1;
+  dst[2 * NT] = r.w2;
+  dst[3 * NT] = r.w3;
+  dst[4 * NT] = r.w4;
+  dst[5 * NT] = r.w5;
+  dst[6 * NT] = r.w6;
+  dst[7 * NT] = r.w7;
 }
 
 // silu and the MLP product for one unit (Qwen3_5MLP :715): D(D(silu(D(g))) * D(u))
@@ -360,26 +480,23 @@ __device__ __forceinline__ void mlp_units(const lxm_hot& hd, const uint8_t* hot)
   for (int u = t; u < hd.n_units; u += 2 * NT) {
     const int u2 = u + NT;
     const bool two = u2 < hd.n_units;
-    const uint32_t m1 = um[u], m2 = two ? um[u2] : 0u;
+    const uint32_t m1 = um[u], m2 = um[two ? u2 : u];
     const int s1 = (int)(m1 & 0xffffu), g1 = (int)((m1 >> 16) & 255), n1 = (int)(m1 >> 24);
-    const int s2 = (int)(m2 & 0xffffu), g2 = (int)((m2 >> 16) & 255), n2 = (int)(m2 >> 24);
-    float ag = chunk4<E4>(gu, s1, g1, 0, xm, 0.0f);
-    float au = chunk4<E4>(gu, s1 + g1, n1, 0, xm, 0.0f);
-    float bg = chunk4<E4>(gu, s2, g2, 0, xm, 0.0f);
-    float bu = chunk4<E4>(gu, s2 + g2, n2, 0, xm, 0.0f);
-    ag = rest4<E4>(gu, s1, g1, xm, ag);
-    au = rest4<E4>(gu, s1 + g1, n1, xm, au);
-    bg = rest4<E4>(gu, s2, g2, xm, bg);
-    bu = rest4<E4>(gu, s2 + g2, n2, xm, bu);
-    act[u] = swiglu<BF>(ag, au);
-    if (two) act[u2] = swiglu<BF>(bg, bu);
+    const int s2 = (int)(m2 & 0xffffu);
+    const int g2 = two ? (int)((m2 >> 16) & 255) : 0, n2 = two ? (int)(m2 >> 24) : 0;
+    const int st[4] = {s1, s1 + g1, s2, s2 + g2}, n[4] = {g1, n1, g2, n2};
+    float v[4];
+    dots<E4, 4, 4>(gu, st, n, xm, v);
+    act[u] = swiglu<BF>(v[0], v[1]);
+    if (two) act[u2] = swiglu<BF>(v[2], v[3]);
   }
 }
 
 // The gates: the live query/key channels' projections, conv windows (history in LDS) and silu
 // (causal_conv1d_update :199-216), and the decays g = -exp(A_log) softplus(a + dt_bias) (:499).
-// Flags per key head: 1 query nonzero, 2 key nonzero, 4 a decay exp(g) != 1. Items run on the
-// threads from the top down (the units take them from the bottom up).
+// Flags per key head: 1 query nonzero, 2 key nonzero, 4 a decay exp(g) != 1; F_ANY and F_OUT
+// directly. Items run on the threads from the top down (the units take them from the bottom
+// up).
 template <bool BF, bool E4>
 __device__ __forceinline__ void gates(const lxm_params& p, const lxm_hot& hd, const uint8_t* hot) {
   const int tt = NT - 1 - (int)threadIdx.x;
@@ -392,25 +509,31 @@ __device__ __forceinline__ void gates(const lxm_params& p, const lxm_hot& hd, co
   const uint8_t* ent = hot + hd.ent;
   for (int j = tt; j < hd.n_qk; j += NT) {
     const lxm_qkc c = qk[j];
-    const float P = rd<BF>(rest4<E4>(ent, c.start, c.len, xg, chunk4<E4>(ent, c.start, c.len, 0, xg, 0.0f)));
     float* hs = hist + 3 * (hd.qk_base + j);
+    const float h0 = hs[0], h1 = hs[1], h2 = hs[2];
+    const float P = rd<BF>(dot<E4, 4, 0>(ent, c.start, c.len, xg));
     float y = 0.0f;
-    y = y + c.taps[0] * hs[0];
-    y = y + c.taps[1] * hs[1];
-    y = y + c.taps[2] * hs[2];
+    y = y + c.taps[0] * h0;
+    y = y + c.taps[1] * h1;
+    y = y + c.taps[2] * h2;
     y = y + c.taps[3] * P;
-    hs[0] = hs[1];
-    hs[1] = hs[2];
+    hs[0] = h1;
+    hs[1] = h2;
     hs[2] = P;
     const float yr = rd<BF>(y);
     const float v = yr == 0.0f ? yr : rd<BF>(silu(yr));
     qkcur[j] = v;
-    if (v != 0.0f) atomicOr(&flags[F_KH + (c.slot >> 9)], (c.slot & 256) ? 2 : 1);
+    if (v != 0.0f) {
+      const bool isk = (c.slot & 256) != 0;
+      atomicOr(&flags[F_KH + (c.slot >> 9)], isk ? 2 : 1);
+      atomicOr(&flags[F_ANY], 1);
+      if (!isk) atomicOr(&flags[F_OUT], 1);
+    }
   }
   const lxm_dec* dc = reinterpret_cast<const lxm_dec*>(hot + hd.dec);
   for (int j = ((tt - hd.n_qk) % NT + NT) % NT; j < hd.n_dec; j += NT) {
     const lxm_dec d = dc[j];
-    const float a = rd<BF>(rest4<E4>(ent, d.start, d.len, xg, chunk4<E4>(ent, d.start, d.len, 0, xg, 0.0f)));
+    const float a = rd<BF>(dot<E4, 4, 0>(ent, d.start, d.len, xg));
     const float x = a + d.dt_bias;
     float e;
     if (x < -104.0f && d.A_log <= 88.0f) {
@@ -420,35 +543,119 @@ __device__ __forceinline__ void gates(const lxm_params& p, const lxm_hot& hd, co
       e = cr_exp(g);
     }
     ev[d.vh] = e;
-    if (e != 1.0f) atomicOr(&flags[F_KH + d.vh / (p.nv / p.nk)], 4);
+    if (e != 1.0f) {
+      atomicOr(&flags[F_KH + d.vh / (p.nv / p.nk)], 4);
+      atomicOr(&flags[F_ANY], 1);
+    }
   }
 }
 
 // stage A's norm: r = rsqrt(mean(h^2) + eps) (transformers qwen3_5 :727, mean = sum / n); both
 // norms' inputs D((h * r) * (1 + w)) (:729-734) from one h * r; the GDN norm's output also to the
-// ring. Only the MLP's when gdn is false (the redo after a delta rule that wrote h).
+// ring. Only the MLP's when gdn is false (the redo after a delta rule that wrote h). Rows past
+// H compute from +0 and a clamped weight; nothing reads them.
+// four norm weights 1 + w of rows c..c+3 (c a multiple of 4); rows >= H get 1
+template <bool E4>
+__device__ __forceinline__ v4f w1x4(const uint8_t* hot, int off, int c, int H) {
+  v4f w;
+  if constexpr (E4) {
+    typedef uint16_t v4h __attribute__((ext_vector_type(4)));
+    const v4h b = reinterpret_cast<const v4h*>(hot + off)[c >> 2];
+    w = v4f{1.0f + bf16f(b.x), 1.0f + bf16f(b.y), 1.0f + bf16f(b.z), 1.0f + bf16f(b.w)};
+  } else {
+    w = reinterpret_cast<const v4f*>(hot + off)[c >> 2];
+  }
+  w.x = c < H ? w.x : 1.0f;
+  w.y = c + 1 < H ? w.y : 1.0f;
+  w.z = c + 2 < H ? w.z : 1.0f;
+  w.w = c + 3 < H ? w.w : 1.0f;
+  return w;
+}
+template <bool BF>
+__device__ __forceinline__ v4f norm4(const v4f& h, float r, const v4f& w) {
+  return v4f{rd<BF>((h.x * r) * w.x), rd<BF>((h.y * r) * w.y), rd<BF>((h.z * r) * w.z),
+             rd<BF>((h.w * r) * w.w)};
+}
 template <bool BF, bool E4>
 __device__ __forceinline__ void norms(const lxm_params& p, const lxm_hot& hd, const uint8_t* hot,
                                       int L, int step, float r, bool gdn) {
-  const int H = p.hidden;
-  const float* h = LF(L_H);
-  float* xg = LF(L_XG);
-  float* xm = LF(L_XM);
-  GAS float* ring = gp(p.ring + ((size_t)(step & 3) * p.n_layers + L) * H);
-  for (int c = threadIdx.x; c < H; c += NT) {
-    const float hr = h[c] * r;
-    xm[c] = rd<BF>(hr * w1_at<E4>(hot, hd.w1_post, c));
-    if (gdn) {
-      const float g = rd<BF>(hr * w1_at<E4>(hot, hd.w1_in, c));
-      xg[c] = g;
-      ring[c] = g;
-    }
+  const int t = threadIdx.x, H = p.hidden;
+  const v4f* h4 = reinterpret_cast<const v4f*>(smem + L_H);
+  v4f* xm4 = reinterpret_cast<v4f*>(smem + L_XM);
+  v4f* xg4 = reinterpret_cast<v4f*>(smem + L_XG);
+  const int c0 = 4 * t, c1 = 2048 + 4 * t;
+  const v4f ha = h4[t], hb = h4[NT + t];
+  const v4f pa = w1x4<E4>(hot, hd.w1_post, c0, H), pb = w1x4<E4>(hot, hd.w1_post, c1, H);
+  xm4[t] = norm4<BF>(ha, r, pa);
+  xm4[NT + t] = norm4<BF>(hb, r, pb);
+  if (gdn) {
+    const v4f ia = w1x4<E4>(hot, hd.w1_in, c0, H), ib = w1x4<E4>(hot, hd.w1_in, c1, H);
+    const v4f ga = norm4<BF>(ha, r, ia), gb = norm4<BF>(hb, r, ib);
+    xg4[t] = ga;
+    xg4[NT + t] = gb;
+    float* ring = ring_at(p, step, L);
+    st_rlxf(ring + c0, ga.x);
+    st_rlxf(ring + c0 + 1, ga.y);
+    st_rlxf(ring + c0 + 2, ga.z);
+    st_rlxf(ring + c0 + 3, ga.w);
+    st_rlxf(ring + c1, gb.x);
+    st_rlxf(ring + c1 + 1, gb.y);
+    st_rlxf(ring + c1 + 2, gb.z);
+    st_rlxf(ring + c1 + 3, gb.w);
   }
 }
 
-// One layer. ss: the sum of squares of h on entry; returns it for the layer's output.
+// A GDN event for layer L (the chain's side): publish the value heads' tasks (bit 0 the key
+// head's query or key is live, bit 2 the head decays), their decays and the layer's live
+// query/key channel values; post the event; wait for every helper; add out_proj's rows
+// (already rounded) to the residual when a query was live. Returns false on an error.
 template <bool BF, bool E4>
-__device__ __forceinline__ float layer(const lxm_params& p, int L, int step, float ss) {
+__device__ bool gdn_event(const lxm_params& p, int L, uint32_t& seq, uint32_t& target) {
+  const int t = threadIdx.x, H = p.hidden;
+  const lxm_hot& hd = *reinterpret_cast<const lxm_hot*>(smem + L_HOT);
+  int* flags = LI(L_FLAGS);
+  const float* ev = LF(L_EV);
+  const bool out = flags[F_OUT] != 0;
+  if (t < p.nv) {
+    const int f = flags[F_KH + t / (p.nv / p.nk)];
+    const float e = ev[t];
+    st_rlx(p.mb_task + t, ((f & 3) ? 1u : 0u) | (e != 1.0f ? 4u : 0u));
+    st_rlxf(p.mb_e + t, e);
+  }
+  for (int j = t; j < hd.n_qk; j += NT) st_rlxf(p.mb_qk + j, LF(L_QKCUR)[j]);
+  drain();  // these and stage A's ring stores, visible at agent scope
+  __syncthreads();
+  if (t == 0) {
+    seq++;
+    st_rlx(p.sync + S_EV, (seq << 8) | ((uint32_t)L << 2) | (out ? EV_OUT : 0u) | EV_GDN);
+    target += (uint32_t)(p.n_blocks - 1);
+    flags[F_OK] = spin_ge(p.sync + S_CALL, target, p.err, 4);
+  }
+  __syncthreads();
+  if (!flags[F_OK]) return false;
+  if (out) {
+    float* h = LF(L_H);
+    float xo[8];
+#pragma unroll
+    for (int k = 0; k < 8; k++) {
+      const int i = t + k * NT;
+      xo[k] = i < H ? ld_rlxf(p.xo + i) : 0.0f;
+    }
+#pragma unroll
+    for (int k = 0; k < 8; k++) {
+      const int i = t + k * NT;
+      if (i < H) h[i] = rd<BF>(h[i] + xo[k]);
+    }
+  }
+  __syncthreads();
+  return true;
+}
+
+// One layer. ss: the sum of squares of h on entry. Ends inside the sum of squares of its output
+// (sum512_begin): the caller finishes it. False on an error.
+template <bool BF, bool E4>
+__device__ __forceinline__ bool layer(const lxm_params& p, int L, int step, float ss,
+                                      uint32_t& seq, uint32_t& target) {
   const int t = threadIdx.x, H = p.hidden;
   const uint8_t* hot = smem + L_HOT;
   const lxm_hot hd = *reinterpret_cast<const lxm_hot*>(hot);
@@ -463,7 +670,7 @@ __device__ __forceinline__ float layer(const lxm_params& p, int L, int step, flo
   norms<BF, E4>(p, hd, hot, L, step, r, true);
   if (t < p.nk) flags[F_KH + t] = 0;
   if (t < p.nv) ev[t] = 1.0f;
-  if (t == 0) flags[F_ANY] = 0;
+  if (t < 2) flags[F_ANY + t] = 0;
   lds_barrier();
   uint64_t c0 = 0;
   if (PROF_ON && t == 0) {
@@ -474,17 +681,15 @@ __device__ __forceinline__ float layer(const lxm_params& p, int L, int step, flo
   mlp_units<BF, E4>(hd, hot);
   gates<BF, E4>(p, hd, hot);
   lds_barrier();
-  if (t < p.nk && flags[F_KH + t]) atomicOr(&flags[F_ANY], 1);
-  lds_barrier();
   if (PROF_ON && t == 0) {
     const uint64_t c1 = cycles();
     pa[3] += c1 - c0;
     c0 = c1;
   }
   if (flags[F_ANY]) {
-    gdn_active<BF, E4>(p, L, step);
-    if (flags[F_OUT]) {  // h changed: the MLP again, on the new h
-      ss = hidden_ss(H);
+    if (!gdn_event<BF, E4>(p, L, seq, target)) return false;
+    if (flags[F_OUT]) {  // h may have changed: the MLP again, on the new h
+      ss = hidden_ss();
       norms<BF, E4>(p, hd, hot, L, step, norm_r(ss, H, hd.eps), false);
       lds_barrier();
       mlp_units<BF, E4>(hd, hot);
@@ -498,229 +703,35 @@ __device__ __forceinline__ float layer(const lxm_params& p, int L, int step, flo
     }
   }
   // ---- stage C: down_proj by residual row (units ascending), the residual add on every row
-  // (:791), and this thread's terms of the next sum of squares (rows t, t + 512, ... in order)
-  float s2 = 0.0f;
+  // (:791), and this thread's terms of the next sum of squares (rows past H stay +0)
   {
+    // the row pointers are padded to LXM_MAXH + 8 entries (rows past H have none)
+    typedef uint16_t v4h __attribute__((ext_vector_type(4)));
     const uint16_t* dp = reinterpret_cast<const uint16_t*>(hot + hd.down_ptr);
     const uint8_t* de = hot + hd.down_ent;
-    int a[8], n[8];
+    v4f* h4 = reinterpret_cast<v4f*>(smem + L_H);
+    const v4h pa4 = reinterpret_cast<const v4h*>(dp)[t], pb4 = reinterpret_cast<const v4h*>(dp + 2048)[t];
+    const int ea = dp[4 * t + 4], eb = dp[2048 + 4 * t + 4];
+    const int st[8] = {pa4.x, pa4.y, pa4.z, pa4.w, pb4.x, pb4.y, pb4.z, pb4.w};
+    const int n[8] = {pa4.y - pa4.x, pa4.z - pa4.y, pa4.w - pa4.z, ea - pa4.w,
+                      pb4.y - pb4.x, pb4.z - pb4.y, pb4.w - pb4.z, eb - pb4.w};
+    const v4f ha = h4[t], hb = h4[NT + t];
     float d[8];
-#pragma unroll
-    for (int k = 0; k < 8; k++) {
-      const int i = t + k * NT;
-      a[k] = 0;
-      n[k] = 0;
-      if (i < H) {
-        a[k] = dp[i];
-        n[k] = (int)dp[i + 1] - a[k];
-      }
-    }
-#pragma unroll
-    for (int k = 0; k < 8; k++) d[k] = chunk4<E4>(de, a[k], n[k], 0, act, 0.0f);
-#pragma unroll
-    for (int k = 0; k < 8; k++) {
-      const int i = t + k * NT;
-      if (i < H) {
-        const float dk = rd<BF>(rest4<E4>(de, a[k], n[k], act, d[k]));
-        const float hv = rd<BF>(h[i] + dk);
-        h[i] = hv;
-        s2 = s2 + hv * hv;
-      }
-    }
+    dots<E4, 2, 8>(de, st, n, act, d);
+    const v4f na = v4f{rd<BF>(ha.x + rd<BF>(d[0])), rd<BF>(ha.y + rd<BF>(d[1])),
+                       rd<BF>(ha.z + rd<BF>(d[2])), rd<BF>(ha.w + rd<BF>(d[3]))};
+    const v4f nb = v4f{rd<BF>(hb.x + rd<BF>(d[4])), rd<BF>(hb.y + rd<BF>(d[5])),
+                       rd<BF>(hb.z + rd<BF>(d[6])), rd<BF>(hb.w + rd<BF>(d[7]))};
+    h4[t] = na;
+    h4[NT + t] = nb;
+    sum512_begin(sq_terms(na, nb), LF(L_WSUM));
   }
-  const float ssn = sum512(s2, LF(L_WSUM));
   if (PROF_ON && t == 0) {
     const uint64_t c1 = cycles();
     pa[5] += c1 - c0;
     pa[15] = c1;
   }
-  return ssn;
-}
-
-// The delta rule for the layer's active key heads (torch_recurrent_gated_delta_rule :330-380
-// with l2norm :242-245 in the model dtype; Qwen3_5RMSNormGated :175-184; out_proj), adding
-// out_proj's output into h. Uniform control flow: every condition is read from LDS after a
-// barrier.
-template <bool BF, bool E4>
-__device__ void gdn_active(const lxm_params& p, int L, int step) {
-  using E = Ent<E4>;
-  const int t = threadIdx.x, H = p.hidden;
-  const uint8_t* hot = smem + L_HOT;
-  const lxm_hot hd = *reinterpret_cast<const lxm_hot*>(hot);
-  float* h = LF(L_H);
-  float* xm = LF(L_XM);
-  float* qkcur = LF(L_QKCUR);
-  float* qd = LF(L_QD);
-  float* kdv = LF(L_KDV);
-  float* qn = LF(L_QN);
-  float* kn = LF(L_KN);
-  int* nzq = LI(L_NZQ);
-  int* nzk = LI(L_NZK);
-  float* vb = LF(L_VB);
-  float* ob = LF(L_OB);
-  float* zb = LF(L_ZB);
-  float* ev = LF(L_EV);
-  float* beta = LF(L_BETA);
-  int* flags = LI(L_FLAGS);
-  const lxm_layer ly = p.layers[L];
-  const uint8_t* blob = p.blob;
-  const int R = p.nv / p.nk;
-  const int wv = t >> 6, lane = t & 63;
-  float* S0 = p.rec[L];
-  const void* cs = p.conv[L];
-  const lxm_chan* chans = reinterpret_cast<const lxm_chan*>(blob + ly.chan);
-  const uint8_t* qent = blob + ly.qkv_ent;
-  const float* xg = LF(L_XG);  // the GDN norm's output (stage A)
-  if (t == 0) flags[F_OUT] = 0;
-  for (int c = t; c < H; c += NT) xm[c] = 0.0f;  // out_proj's running sums
-  __syncthreads();  // and the ring's stores of this step, visible to every thread
-  for (int kh = 0; kh < p.nk; kh++) {
-    const int fk = flags[F_KH + kh];
-    if (!fk) continue;
-    // dense query and key of this head (the live channels' conv outputs, zeros elsewhere)
-    for (int i = t; i < KD; i += NT) {
-      qd[i] = 0.0f;
-      kdv[i] = 0.0f;
-    }
-    __syncthreads();
-    {
-      const lxm_qkc* qk = reinterpret_cast<const lxm_qkc*>(hot + hd.qk);
-      for (int j = t; j < hd.n_qk; j += NT) {
-        const int sl = qk[j].slot;
-        if ((sl >> 9) != kh) continue;
-        ((sl & 256) ? kdv : qd)[sl & 255] = qkcur[j];
-      }
-    }
-    __syncthreads();
-    // l2norm in the model dtype: D(x * D(rsqrt(D(D(sum D(x*x)) + 1e-6)))); query scaled by
-    // 1/sqrt(256) in fp32 (:352-353); then the nonzero rows in ascending order
-    if (wv < 2) {
-      const float* x = wv ? kdv : qd;
-      float s = 0.0f;
-      for (int i = lane; i < KD; i += 64) s = s + rd<BF>(x[i] * x[i]);
-      s = rd<BF>(sum64(s));
-      const float inv = rd<BF>(rsqrt_(rd<BF>(s + 1e-6f)));
-      float* o = wv ? kn : qn;
-      int* nz = wv ? nzk : nzq;
-      int n = 0;
-      for (int b = 0; b < KD; b += 64) {
-        float v = rd<BF>(x[b + lane] * inv);
-        if (!wv) v = v * 0.0625f;
-        o[b + lane] = v;
-        const unsigned long long m = __ballot(v != 0.0f);
-        if (v != 0.0f) nz[n + __popcll(m & ((1ull << lane) - 1))] = b + lane;
-        n += __popcll(m);
-      }
-      if (lane == 0) flags[wv ? F_NK : F_NQ] = n;
-    }
-    // beta = sigmoid(b) (:497) for this head's value heads
-    if (t >= 128 && t < 128 + R) {
-      const int r = t - 128, vh = kh * R + r;
-      const lxm_row br = reinterpret_cast<const lxm_row*>(blob + ly.b_row)[vh];
-      const float b = rd<BF>(dot_row<E4>(blob + ly.b_ent, br.start, br.len, xg));
-      beta[r] = rd<BF>(sigmoid(b));
-    }
-    __syncthreads();
-    const int nq = flags[F_NQ], nk = flags[F_NK];
-    // v: this head's value channels' conv outputs; the window's earlier inputs recomputed from
-    // the ring (or read from the conv state before this launch)
-    if (nk > 0) {
-      for (int c = t; c < R * VD; c += NT) {
-        const int chan = 2 * p.nk * KD + (kh * R) * VD + c;
-        const lxm_chan ch = chans[chan];
-        float win[4];
-        win[3] = rd<BF>(dot_row<E4>(qent, ch.start, ch.len, xg));
-#pragma unroll
-        for (int s = 1; s <= 3; s++) {
-          win[3 - s] = 0.0f;
-          if (ch.taps[3 - s] == 0.0f) continue;
-          if (step - s >= 0) {
-            const float* xo = p.ring + ((size_t)((step - s) & 3) * p.n_layers + L) * H;
-            win[3 - s] = rd<BF>(dot_row<E4>(qent, ch.start, ch.len, xo));
-          } else {
-            win[3 - s] = conv_at<BF>(cs, (int64_t)chan * 4 + 4 - (s - step));
-          }
-        }
-        float y = 0.0f;
-#pragma unroll
-        for (int k = 0; k < 4; k++)
-          if (ch.taps[k] != 0.0f) y = y + ch.taps[k] * win[k];
-        vb[c] = rd<BF>(silu(rd<BF>(y)));
-      }
-    }
-    __syncthreads();
-    // the recurrent step, one state column per thread: decay, kv, delta, write, output
-    for (int r = t >> 7; r < R; r += NT / VD) {
-      const int j = t & (VD - 1), vh = kh * R + r;
-      float* S = S0 + (size_t)vh * KD * VD;
-      const float e = ev[vh];
-      if (e != 1.0f)
-        for (int i0 = 0; i0 < KD; i0 += 64) {  // 64 loads in flight, then the stores
-          float v[64];
-#pragma unroll
-          for (int k = 0; k < 64; k++) v[k] = S[(size_t)(i0 + k) * VD + j];
-#pragma unroll
-          for (int k = 0; k < 64; k++) S[(size_t)(i0 + k) * VD + j] = v[k] * e;
-        }
-      if (nk > 0) {
-        const float kv = row_cascade(S, j, nzk, nk, kn);
-        const float dl = (vb[r * VD + j] - kv) * beta[r];
-        for (int a = 0; a < nk; a++) {
-          const int i = nzk[a];
-          S[(size_t)i * VD + j] = S[(size_t)i * VD + j] + kn[i] * dl;
-        }
-      }
-      ob[r * VD + j] = nq > 0 ? rd<BF>(row_cascade(S, j, nzq, nq, qn)) : 0.0f;
-    }
-    __syncthreads();
-    if (nq == 0) continue;  // no query: the head's output is exactly zero
-    // z = in_proj_z, then the gated norm per value head (one wave each)
-    for (int c = t; c < R * VD; c += NT) {
-      const lxm_row zr = reinterpret_cast<const lxm_row*>(blob + ly.z_row)[(kh * R) * VD + c];
-      zb[c] = rd<BF>(dot_row<E4>(blob + ly.z_ent, zr.start, zr.len, xg));
-    }
-    __syncthreads();
-    {
-      const float* gw = reinterpret_cast<const float*>(blob + ly.gnorm);
-      for (int r = wv; r < R; r += NW) {
-        float s = 0.0f;
-        for (int j = lane; j < VD; j += 64) s = s + ob[r * VD + j] * ob[r * VD + j];
-        s = sum64(s);
-        const float rr = rsqrt_(s / (float)VD + hd.geps);
-        for (int j = lane; j < VD; j += 64) {
-          const float t1 = rd<BF>(ob[r * VD + j] * rr);
-          const float t2 = rd<BF>(gw[j] * t1);
-          zb[r * VD + j] = rd<BF>(t2 * silu(zb[r * VD + j]));
-        }
-      }
-    }
-    __syncthreads();
-    // out_proj rows touched by this head: the running sums continue in ascending dim order
-    {
-      const int32_t* op = reinterpret_cast<const int32_t*>(blob + ly.out_ptr) + (size_t)kh * (H + 1);
-      const uint8_t* oe = blob + ly.out_ent;
-      for (int i = t; i < H; i += NT) {
-        const int a = op[i], b = op[i + 1];
-        if (a == b) continue;
-        float s = xm[i];
-        for (int k = a; k < b; k++) {
-          int d;
-          float w;
-          E::at(oe, k, d, w);
-          const float x = zb[d];
-          if (x != 0.0f) s = s + x * w;
-        }
-        xm[i] = s;
-      }
-    }
-    if (t == 0) flags[F_OUT] = 1;
-    __syncthreads();
-  }
-  // the residual add (all rows; a row with no term adds +0)
-  if (flags[F_OUT]) {
-    for (int i = t; i < H; i += NT) h[i] = rd<BF>(h[i] + rd<BF>(xm[i]));
-  }
-  __syncthreads();
+  return true;
 }
 
 // ---------------------------------------------------------------------------------------------
@@ -730,6 +741,7 @@ __device__ void run_chain(const lxm_params& p) {
   int* flags = LI(L_FLAGS);
   float* h = LF(L_H);
   float* hist = LF(L_HIST);
+  LtEnt* lt = reinterpret_cast<LtEnt*>(smem + L_LT);
   // the live query/key channels' windows from the conv state (positions 1..3)
   for (int L = 0; L < p.n_layers; L++) {
     const lxm_hot* hd = reinterpret_cast<const lxm_hot*>(p.blob + p.layers[L].hot);
@@ -738,21 +750,26 @@ __device__ void run_chain(const lxm_params& p) {
       for (int s = 0; s < 3; s++)
         hist[3 * (hd->qk_base + j) + s] = conv_at<BF>(p.conv[L], (int64_t)qk[j].chan * 4 + 1 + s);
   }
-  int* n16s = flags + 128;  // per layer (< 64): its hot blob's 16-byte words
-  for (int L = t; L < p.n_layers; L += NT)
-    n16s[L] = reinterpret_cast<const lxm_hot*>(p.blob + p.layers[L].hot)->size / 16;
+  for (int L = t; L < p.n_layers; L += NT) {
+    const uint8_t* hb = p.blob + p.layers[L].hot;
+    lt[L].hot = hb;
+    lt[L].n16 = reinterpret_cast<const lxm_hot*>(hb)->size / 16;
+  }
+  for (int c = t; c < MAXH; c += NT) h[c] = 0.0f;
   __syncthreads();
-  Pf pf = fetch(p, 0, n16s[0]);
+  stage(fetch(0));
+  Pf pf = fetch(p.n_layers > 1 ? 1 : 0);  // always one layer ahead of the staged one
   uint64_t* pa = reinterpret_cast<uint64_t*>(smem + L_PROF);
   if (t < 32) pa[t] = 0;
   __syncthreads();
   int tok = p.forced[0];
+  uint32_t seq = 0, target = 0;
   const uint32_t nh = (uint32_t)(p.n_blocks - 1);
   for (int i = 0; i < p.n_tokens; i++) {
     if (tok < 0 || tok >= p.vocab) tok = 0;  // the host checks forced tokens; preds are in range
     if (t == 0 && p.inputs) p.inputs[i] = tok;
     if (PROF_ON && t == 0) pa[15] = cycles();
-    // the input's embedding row
+    // the input's embedding row (the rows past it are +0 already, and stay so)
     for (int c = t; c < H; c += NT) h[c] = 0.0f;
     lds_barrier();
     {
@@ -760,33 +777,30 @@ __device__ void run_chain(const lxm_params& p) {
       for (int64_t e = a + t; e < b; e += NT) {
         int col;
         float w;
-        Ent<E4>::at(reinterpret_cast<const uint8_t*>(p.emb_ent), e, col, w);
+        Ent<E4>::gat(reinterpret_cast<const uint8_t*>(p.emb_ent), e, col, w);
         h[col] = w;
       }
     }
     lds_barrier();
-    float ss = hidden_ss(H);
+    float ss = hidden_ss();
     if (PROF_ON && t == 0) {
       const uint64_t c = cycles();
       pa[0] += c - pa[15];
       pa[15] = c;
     }
     for (int L = 0; L < p.n_layers; L++) {
-      stage(n16s[L], pf);
-      lds_barrier();
-      const int Ln = L + 1 < p.n_layers ? L + 1 : 0;
-      pf = fetch(p, Ln, n16s[Ln]);
-      if (PROF_ON && t == 0) {
-        const uint64_t c = cycles();
-        pa[1] += c - pa[15];
-        pa[15] = c;
-      }
-      ss = layer<BF, E4>(p, L, i, ss);
+      if (!layer<BF, E4>(p, L, i, ss, seq, target)) return;
+      // the next layer's tables into LDS between the two barriers of the sum of squares (stage
+      // C's reads of this layer's tables are before the first)
       if (p.trace) {
         float* tr = p.trace + ((size_t)i * p.n_layers + L) * H;
         for (int c = t; c < H; c += NT) tr[c] = h[c];
       }
-      lds_barrier();
+      stage(pf);
+      ss = sum512_end(LF(L_WSUM));
+      int L2 = L + 2;
+      while (L2 >= p.n_layers) L2 -= p.n_layers;
+      pf = fetch(L2);
       if (PROF_ON && t == 0) {
         const uint64_t c = cycles();
         pa[1] += c - pa[15];
@@ -806,14 +820,17 @@ __device__ void run_chain(const lxm_params& p) {
       pa[15] = c;
     }
     if (t == 0) {
-      st_rlx(p.sync + S_TOKFLAG, (uint32_t)(i + 1));
-      bool ok = spin_ge(p.sync + S_COUNT, nh * (uint32_t)(i + 1), p.err, 1);
+      seq++;
+      st_rlx(p.sync + S_EV, seq << 8);
+      target += nh;
+      bool ok = spin_ge(p.sync + S_CALL, target, p.err, 1);
       int pred = 0;
       if (ok) {
-        const unsigned long long key =
-            __hip_atomic_load(p.keys + (i & 1), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        const unsigned long long key = __hip_atomic_load(gp(p.keys + (i & 1)), __ATOMIC_RELAXED,
+                                                         __HIP_MEMORY_SCOPE_AGENT);
         pred = argmax_idx(key);
-        __hip_atomic_store(p.keys + ((i + 1) & 1), 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(gp(p.keys + ((i + 1) & 1)), 0ull, __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_AGENT);
         p.preds[i] = pred;
       }
       flags[F_OK] = ok;
@@ -833,66 +850,361 @@ __device__ void run_chain(const lxm_params& p) {
   // every ring write visible to the other blocks, then let them write the conv windows
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
   __syncthreads();
-  if (t == 0) __hip_atomic_store(p.sync + S_DONE, 1u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
+  if (t == 0) __hip_atomic_store(gp(p.sync + S_DONE), 1u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// ---------------------------------------------------------------------------------------------
+// The helpers.
+
+// HEAD: this helper's vocabulary rows against the final normed residual; its best key into the
+// token's atomicMax slot.
+template <bool BF, bool E4>
+__device__ void head_rows(const lxm_params& p, int step, const int32_t* lptr, const uint8_t* lent,
+                          int r0, int nr, uint8_t* hx) {
+  const int t = threadIdx.x, H = p.hidden;
+  float* hn = reinterpret_cast<float*>(hx + HX_X);
+  unsigned long long* wk = reinterpret_cast<unsigned long long*>(hx + HX_BS);
+  for (int c = t; c < H; c += NT) hn[c] = ld_rlxf(p.hn + c);
+  __syncthreads();
+  unsigned long long best = 0;
+  for (int k = t; k < nr; k += NT) {
+    const float v = rd<BF>(dot<E4, 4, 0>(lent, lptr[k], lptr[k + 1] - lptr[k], hn));
+    const unsigned long long key = argmax_key(v, r0 + k);
+    best = key > best ? key : best;
+  }
+  for (int off = 32; off >= 1; off >>= 1) {
+    const unsigned long long o = __shfl_xor(best, off, 64);
+    best = o > best ? o : best;
+  }
+  if ((t & 63) == 0) wk[t >> 6] = best;
+  __syncthreads();
+  if (t == 0) {
+    for (int w = 1; w < NW; w++) best = wk[w] > best ? wk[w] : best;
+    __hip_atomic_fetch_max(gp(p.keys + (step & 1)), best, __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_AGENT);
+  }
+}
+
+// GDN, first part: value head vh of layer L at this step (torch_recurrent_gated_delta_rule
+// :330-380 with l2norm :242-245 in the model dtype, Qwen3_5RMSNormGated :168-184), by the
+// head's owner. Writes the head's gated-norm output (zeros when it has none) to p.ybuf.
+template <bool BF, bool E4>
+__device__ void gdn_head(const lxm_params& p, int L, int step, int vh, bool out, uint8_t* hx) {
+  const int t = threadIdx.x, H = p.hidden, R = p.nv / p.nk, kh = vh / R;
+  const int wv = t >> 6, lane = t & 63;
+  float* xg = reinterpret_cast<float*>(hx + HX_X);
+  float* qd = reinterpret_cast<float*>(hx + HX_QD);
+  float* kd = reinterpret_cast<float*>(hx + HX_KD);
+  float* qn = reinterpret_cast<float*>(hx + HX_QN);
+  float* kn = reinterpret_cast<float*>(hx + HX_KN);
+  float* vb = reinterpret_cast<float*>(hx + HX_V);
+  float* zb = reinterpret_cast<float*>(hx + HX_Z);
+  float* ob = reinterpret_cast<float*>(hx + HX_O);
+  float* dl = reinterpret_cast<float*>(hx + HX_DL);
+  float* bs = reinterpret_cast<float*>(hx + HX_BS);
+  int* misc = reinterpret_cast<int*>(hx + HX_MISC);
+  float* y = p.ybuf + (size_t)vh * VD;
+  const uint32_t tf = ld_rlx(p.mb_task + vh);
+  if (tf == 0) {  // the step leaves this head alone: state unchanged, output exactly 0
+    if (out && t < VD) st_rlxf(y + t, 0.0f);
+    return;
+  }
+  const float e = ld_rlxf(p.mb_e + vh);
+  const bool live = (tf & 1) != 0, dec = (tf & 4) != 0;
+  const lxm_layer ly = p.layers[L];
+  const uint8_t* hot = p.blob + ly.hot;
+  const lxm_hot hd = *reinterpret_cast<const lxm_hot*>(hot);
+  // the step's GDN norm output, and this key head's dense query and key
+  {
+    const float* ring = ring_at(p, step, L);
+    for (int c = t; c < H; c += NT) xg[c] = ld_rlxf(ring + c);
+  }
+  if (t < KD) {
+    qd[t] = 0.0f;
+    kd[t] = 0.0f;
+  }
+  __syncthreads();
+  if (live) {
+    const lxm_qkc* qk = reinterpret_cast<const lxm_qkc*>(hot + hd.qk);
+    for (int j = t; j < hd.n_qk; j += NT) {
+      const int sl = gp(&qk[j].slot)[0];
+      if ((sl >> 9) == kh) ((sl & 256) ? kd : qd)[sl & 255] = ld_rlxf(p.mb_qk + j);
+    }
+  }
+  __syncthreads();
+  // l2norm in the model dtype: D(x * D(rsqrt(D(D(sum D(x*x)) + 1e-6)))); the query scaled by
+  // 1/sqrt(256) in fp32 (:352-353). Without a live query or key both stay 0.
+  if (wv < 2) {
+    const float* x = wv ? kd : qd;
+    float* o = wv ? kn : qn;
+    int n = 0;
+    if (live) {
+      float s = 0.0f;
+      for (int i = lane; i < KD; i += 64) s = s + rd<BF>(x[i] * x[i]);
+      s = rd<BF>(sum64(s));
+      const float inv = rd<BF>(rsqrt_(rd<BF>(s + 1e-6f)));
+      for (int b = 0; b < KD; b += 64) {
+        float v = rd<BF>(x[b + lane] * inv);
+        if (!wv) v = v * 0.0625f;
+        o[b + lane] = v;
+        n += __popcll(__ballot(v != 0.0f));
+      }
+    } else {
+      for (int b = 0; b < KD; b += 64) o[b + lane] = 0.0f;
+    }
+    if (lane == 0) misc[wv] = n;
+  }
+  // the value channels' conv outputs (the window's earlier inputs from the ring, or from the
+  // conv state before this launch), the in_proj_z rows and beta = sigmoid(b) (:497)
+  if (live) {
+    const uint8_t* qent = p.blob + ly.qkv_ent;
+    if (t < VD) {
+      const int chan = 2 * p.nk * KD + vh * VD + t;
+      const lxm_chan ch = ldg(reinterpret_cast<const lxm_chan*>(p.blob + ly.chan) + chan);
+      float win[4];
+      win[3] = rd<BF>(dot<E4, 4, 1>(qent, ch.start, ch.len, xg));
+#pragma unroll
+      for (int s = 1; s <= 3; s++) {
+        win[3 - s] = 0.0f;
+        if (ch.taps[3 - s] == 0.0f) continue;
+        if (step - s >= 0)
+          win[3 - s] = rd<BF>(dot<E4, 4, 2>(qent, ch.start, ch.len, ring_at(p, step - s, L)));
+        else
+          win[3 - s] = conv_at<BF>(p.conv[L], (int64_t)chan * 4 + 4 - (s - step));
+      }
+      float yv = 0.0f;
+#pragma unroll
+      for (int k = 0; k < 4; k++)
+        if (ch.taps[k] != 0.0f) yv = yv + ch.taps[k] * win[k];
+      vb[t] = rd<BF>(silu(rd<BF>(yv)));
+    } else if (t < 2 * VD) {
+      const int j = t - VD;
+      const lxm_row zr = ldg(reinterpret_cast<const lxm_row*>(p.blob + ly.z_row) + vh * VD + j);
+      zb[j] = rd<BF>(dot<E4, 4, 1>(p.blob + ly.z_ent, zr.start, zr.len, xg));
+    } else if (t == 2 * VD) {
+      const lxm_row br = ldg(reinterpret_cast<const lxm_row*>(p.blob + ly.b_row) + vh);
+      const float b = rd<BF>(dot<E4, 4, 1>(p.blob + ly.b_ent, br.start, br.len, xg));
+      misc[2] = (int)__float_as_uint(rd<BF>(sigmoid(b)));
+    }
+  }
+  __syncthreads();
+  const int nq = misc[0], nk = misc[1];
+  const float beta = __uint_as_float((uint32_t)misc[2]);
+  // The state tile: thread (cg, rb) holds columns 4cg..4cg+3 of rows 16rb..16rb+15, i.e. one
+  // of ATen's 16-row cascade blocks (torch .sum(-2) on the CPU: blocks of 16 rows, each from +0
+  // in order, the block sums from +0 in order; only rows with a nonzero factor add terms).
+  {
+    const int cg = t & 31, rb = t >> 5;
+    GAS v4f* S4 = gp(reinterpret_cast<v4f*>(p.rec[L] + (size_t)vh * KD * VD));
+    v4f s[16];
+#pragma unroll
+    for (int i = 0; i < 16; i++) {
+      const int r = rb * 16 + i;
+      s[i] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+      if (dec || kn[r] != 0.0f || qn[r] != 0.0f) s[i] = S4[r * (VD / 4) + cg];
+    }
+    if (dec) {
+#pragma unroll
+      for (int i = 0; i < 16; i++) {
+        s[i].x = s[i].x * e;
+        s[i].y = s[i].y * e;
+        s[i].z = s[i].z * e;
+        s[i].w = s[i].w * e;
+      }
+    }
+    if (nk > 0) {
+      v4f a = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+      for (int i = 0; i < 16; i++) {
+        const float f = kn[rb * 16 + i];
+        if (f != 0.0f) {
+          a.x = a.x + s[i].x * f;
+          a.y = a.y + s[i].y * f;
+          a.z = a.z + s[i].z * f;
+          a.w = a.w + s[i].w * f;
+        }
+      }
+      reinterpret_cast<v4f*>(bs + rb * VD)[cg] = a;
+      __syncthreads();
+      if (t < VD) {
+        float kv = 0.0f;
+#pragma unroll
+        for (int b = 0; b < 16; b++) kv = kv + bs[b * VD + t];
+        dl[t] = (vb[t] - kv) * beta;
+      }
+      __syncthreads();
+      const v4f d = reinterpret_cast<const v4f*>(dl)[cg];
+#pragma unroll
+      for (int i = 0; i < 16; i++) {
+        const float f = kn[rb * 16 + i];
+        if (f != 0.0f) {
+          s[i].x = s[i].x + f * d.x;
+          s[i].y = s[i].y + f * d.y;
+          s[i].z = s[i].z + f * d.z;
+          s[i].w = s[i].w + f * d.w;
+        }
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < 16; i++) {
+      const int r = rb * 16 + i;
+      if (dec || kn[r] != 0.0f) S4[r * (VD / 4) + cg] = s[i];
+    }
+    if (nq > 0) {
+      v4f a = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+      for (int i = 0; i < 16; i++) {
+        const float f = qn[rb * 16 + i];
+        if (f != 0.0f) {
+          a.x = a.x + s[i].x * f;
+          a.y = a.y + s[i].y * f;
+          a.z = a.z + s[i].z * f;
+          a.w = a.w + s[i].w * f;
+        }
+      }
+      __syncthreads();  // the kv sums above have read bs
+      reinterpret_cast<v4f*>(bs + rb * VD)[cg] = a;
+      __syncthreads();
+      if (t < VD) {
+        float o = 0.0f;
+#pragma unroll
+        for (int b = 0; b < 16; b++) o = o + bs[b * VD + t];
+        ob[t] = rd<BF>(o);
+      }
+    }
+  }
+  if (!out) return;
+  __syncthreads();
+  // the gated norm on this value head (one wave), gate z: y = D(D(w * D(o * r)) * silu(z))
+  if (wv == 0) {
+    const float* gw = reinterpret_cast<const float*>(p.blob + ly.gnorm);
+    if (nq > 0) {
+      float s = 0.0f;
+      for (int j = lane; j < VD; j += 64) s = s + ob[j] * ob[j];
+      s = sum64(s);
+      const float rr = rsqrt_(s / (float)VD + hd.geps);
+      for (int j = lane; j < VD; j += 64) {
+        const float t1 = rd<BF>(ob[j] * rr);
+        const float t2 = rd<BF>(gp(gw)[j] * t1);
+        st_rlxf(y + j, rd<BF>(t2 * silu(zb[j])));
+      }
+    } else {  // no live query: o = 0, and so is every term the head gives out_proj
+      for (int j = lane; j < VD; j += 64) st_rlxf(y + j, 0.0f);
+    }
+  }
+}
+
+// GDN, second part: out_proj rows ra..rb (all value heads' outputs, ascending dims, from +0),
+// rounded once, to p.xo.
+template <bool BF, bool E4>
+__device__ void out_rows(const lxm_params& p, int L, int ra, int rb, uint8_t* hx) {
+  const int t = threadIdx.x;
+  int* op = reinterpret_cast<int*>(hx + HX_OP);
+  uint8_t* oe = hx + HX_OE;
+  float* oy = reinterpret_cast<float*>(hx + HX_OY);
+  const lxm_layer ly = p.layers[L];
+  const GAS int32_t* gptr = gp(reinterpret_cast<const int32_t*>(p.blob + ly.out_ptr));
+  const int e0 = gptr[ra], ne = gptr[rb] - e0;  // the packer keeps ne <= LXM_OUT_MAX
+  if (t <= rb - ra) op[t] = gptr[ra + t] - e0;
+  for (int k = t; k < ne; k += NT) {
+    int d;
+    float w;
+    Ent<E4>::gat(p.blob + ly.out_ent, e0 + k, d, w);
+    if constexpr (E4) reinterpret_cast<uint32_t*>(oe)[k] = (uint32_t)d | (__float_as_uint(w) & 0xffff0000u);
+    else reinterpret_cast<uint2*>(oe)[k] = make_uint2((uint32_t)d, __float_as_uint(w));
+    oy[k] = ld_rlxf(p.ybuf + d);
+  }
+  __syncthreads();
+  if (t < rb - ra) {
+    float s = 0.0f;
+    for (int k = op[t]; k < op[t + 1]; k++) {
+      int d;
+      float w;
+      Ent<E4>::at(oe, k, d, w);
+      const float x = oy[k];
+      if (x != 0.0f) s = s + x * w;
+    }
+    st_rlxf(p.xo + ra + t, rd<BF>(s));
+  }
 }
 
 template <bool BF, bool E4>
 __device__ void run_helper(const lxm_params& p) {
   uint8_t* lds = smem;
-  const int t = threadIdx.x, H = p.hidden, b = blockIdx.x;
+  const int t = threadIdx.x, H = p.hidden, b = blockIdx.x, nh = p.n_blocks - 1;
   const int r0 = p.head_rows[b], r1 = p.head_rows[b + 1], nr = r1 - r0;
   const int64_t e0 = p.head_ptr[r0], ne = p.head_ptr[r1] - e0;
   int32_t* lptr = reinterpret_cast<int32_t*>(lds);
   uint8_t* lent = lds + (((size_t)(nr + 1) * 4 + 15) & ~(size_t)15);
-  float* hn = reinterpret_cast<float*>(lds + p.head_lds);
-  unsigned long long* wk = reinterpret_cast<unsigned long long*>(lds + p.head_lds + 4 * MAXH);
-  int* ok = reinterpret_cast<int*>(wk + NW);
+  uint8_t* hx = lds + p.head_lds;
+  int* misc = reinterpret_cast<int*>(hx + HX_MISC);
   for (int k = t; k <= nr; k += NT) lptr[k] = (int32_t)(p.head_ptr[r0 + k] - e0);
   {
     const uint32_t* src = p.head_ent + e0 * (Ent<E4>::SZ / 4);
     uint32_t* dst = reinterpret_cast<uint32_t*>(lent);
     for (int64_t k = t; k < ne * (Ent<E4>::SZ / 4); k += NT) dst[k] = src[k];
   }
+  // out_proj rows of this helper: an even split of the residual rows
+  const int rp = (H + nh - 1) / nh;
+  const int ra = (b - 1) * rp < H ? (b - 1) * rp : H, rb = ra + rp < H ? ra + rp : H;
+  const int vh = b - 1;
+  const bool owner = vh < p.nv;
   __syncthreads();
-  uint64_t hw = 0, hc = 0, hc0 = 0;
-  for (int i = 0; i < p.n_tokens; i++) {
-    const uint64_t w0 = (PROF_ON && t == 0) ? cycles() : 0;
-    if (t == 0) *ok = spin_ge(p.sync + S_TOKFLAG, (uint32_t)(i + 1), p.err, 2);
-    __syncthreads();
-    if (!*ok) return;
-    if (PROF_ON && t == 0) {
-      hc0 = cycles();
-      hw += hc0 - w0;
-    }
-    for (int c = t; c < H; c += NT) hn[c] = ld_rlxf(p.hn + c);
-    __syncthreads();
-    unsigned long long best = 0;
-    for (int k = t; k < nr; k += NT) {
-      const float v = rd<BF>(dot_row<E4>(lent, lptr[k], lptr[k + 1] - lptr[k], hn));
-      const unsigned long long key = argmax_key(v, r0 + k);
-      best = key > best ? key : best;
-    }
-    for (int off = 32; off >= 1; off >>= 1) {
-      const unsigned long long o = __shfl_xor(best, off, 64);
-      best = o > best ? o : best;
-    }
-    if ((t & 63) == 0) wk[t >> 6] = best;
-    __syncthreads();
+  uint64_t pr[4] = {0, 0, 0, 0};
+  uint32_t last = 0, ngdn = 0;
+  int step = 0;
+  while (step < p.n_tokens) {
+    const uint64_t w0 = PROF_ON ? cycles() : 0;
     if (t == 0) {
-      for (int w = 1; w < NW; w++) best = wk[w] > best ? wk[w] : best;
-      __hip_atomic_fetch_max(p.keys + (i & 1), best, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      drain();
-      __hip_atomic_fetch_add(p.sync + S_COUNT, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      if (PROF_ON) hc += cycles() - hc0;
+      uint32_t w = 0;
+      misc[5] = spin_ne(p.sync + S_EV, last, &w, p.err, 2);
+      misc[4] = (int)w;
     }
+    __syncthreads();
+    if (!misc[5]) return;
+    const uint32_t w = (uint32_t)misc[4];
+    last = w;
+    uint64_t w1 = 0;
+    if (PROF_ON) {
+      w1 = cycles();
+      pr[0] += w1 - w0;
+    }
+    if (!(w & EV_GDN)) {
+      head_rows<BF, E4>(p, step, lptr, lent, r0, nr, hx);
+      if (PROF_ON) pr[1] += cycles() - w1;
+      step++;
+    } else {
+      const int L = (int)((w >> 2) & 63);
+      const bool out = (w & EV_OUT) != 0;
+      ngdn++;
+      if (owner) {
+        gdn_head<BF, E4>(p, L, step, vh, out, hx);
+        drain();
+        __syncthreads();
+        if (t == 0) add_rlx(p.sync + S_CVH, 1u);
+      }
+      uint64_t w2 = 0;
+      if (PROF_ON) {
+        w2 = cycles();
+        pr[2] += w2 - w1;
+      }
+      if (out) {
+        if (t == 0) misc[5] = spin_ge(p.sync + S_CVH, (uint32_t)p.nv * ngdn, p.err, 5);
+        __syncthreads();
+        if (!misc[5]) return;
+        if (rb > ra) out_rows<BF, E4>(p, L, ra, rb, hx);
+      }
+      if (PROF_ON) pr[3] += cycles() - w2;
+    }
+    drain();
+    __syncthreads();
+    if (t == 0) add_rlx(p.sync + S_CALL, 1u);
   }
-  if (PROF_ON && t == 0) {
-    p.prof[32 + 2 * blockIdx.x] = hw;
-    p.prof[33 + 2 * blockIdx.x] = hc;
-  }
-  if (t == 0) *ok = spin_ge(p.sync + S_DONE, 1u, p.err, 3);
+  if (PROF_ON && t == 0)
+    for (int k = 0; k < 4; k++) p.prof[32 + 4 * b + k] = pr[k];
+  if (t == 0) misc[5] = spin_ge(p.sync + S_DONE, 1u, p.err, 3);
   __syncthreads();
-  if (*ok) __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+  if (misc[5]) __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
 }
 
 // Every conv window once, at the end: [P(n-4), P(n-3), P(n-2), P(n-1)] per channel, P(s) the
@@ -903,22 +1215,20 @@ __device__ void write_windows(const lxm_params& p) {
   const int64_t total = (int64_t)p.n_layers * p.n_conv;
   const int64_t per = (total + p.n_blocks - 1) / p.n_blocks;
   const int64_t a = (int64_t)blockIdx.x * per, b = a + per < total ? a + per : total;
-  const int n = p.n_tokens, H = p.hidden;
+  const int n = p.n_tokens;
   for (int64_t g = a + threadIdx.x; g < b; g += NT) {
     const int L = (int)(g / p.n_conv), c = (int)(g % p.n_conv);
     const lxm_layer ly = p.layers[L];
-    const lxm_chan ch = reinterpret_cast<const lxm_chan*>(p.blob + ly.chan)[c];
+    const lxm_chan ch = ldg(reinterpret_cast<const lxm_chan*>(p.blob + ly.chan) + c);
     void* cs = p.conv[L];
     float w[4];
 #pragma unroll
     for (int k = 0; k < 4; k++) {
       const int s = n - 4 + k;
-      if (s >= 0) {
-        const float* xo = p.ring + ((size_t)(s & 3) * p.n_layers + L) * H;
-        w[k] = rd<BF>(dot_row<E4>(p.blob + ly.qkv_ent, ch.start, ch.len, xo));
-      } else {
+      if (s >= 0)
+        w[k] = rd<BF>(dot<E4, 4, 2>(p.blob + ly.qkv_ent, ch.start, ch.len, ring_at(p, s, L)));
+      else
         w[k] = conv_at<BF>(cs, (int64_t)c * 4 + 4 + s);
-      }
     }
 #pragma unroll
     for (int k = 0; k < 4; k++) conv_put<BF>(cs, (int64_t)c * 4 + k, w[k]);
@@ -931,7 +1241,7 @@ __global__ void __launch_bounds__(NT, 1) lxm_decode(const lxm_params* __restrict
   if (blockIdx.x == 0) run_chain<BF, E4>(p);
   else run_helper<BF, E4>(p);
   __syncthreads();
-  if (__hip_atomic_load(p.err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) return;
+  if (__hip_atomic_load(gp(p.err), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) return;
   write_windows<BF, E4>(p);
 }
 
@@ -959,7 +1269,11 @@ __global__ void __launch_bounds__(NT) k_sum(int kind, const float* x, int n, flo
   const float* row = x + (size_t)blockIdx.x * n;
   if (kind == 0) {
     float s = 0.0f;
-    for (int i = threadIdx.x; i < n; i += NT) s = s + row[i];
+    for (int part = 0; part < 2; part++)
+      for (int j = 0; j < 4; j++) {
+        const int i = 2048 * part + 4 * (int)threadIdx.x + j;
+        if (i < n) s = s + row[i];
+      }
     s = sum512(s, wsum);
     if (threadIdx.x == 0) out[blockIdx.x] = s;
   } else if (threadIdx.x < 64) {
@@ -974,6 +1288,8 @@ __global__ void __launch_bounds__(NT) k_sum(int kind, const float* x, int n, flo
 extern "C" {
 
 int lxm_lds_base(void) { return L_CHAIN_END; }
+
+int lxm_helper_lds(int head_lds) { return head_lds + HX_END; }
 
 int lxm_run(const lxm_params* p_host, const lxm_params* p_dev, int n_blocks, int lds_bytes,
             void* stream) {

@@ -20,13 +20,11 @@ namespace lxm {
 __device__ __forceinline__ float bitsf(uint32_t u) { return __uint_as_float(u); }
 __device__ __forceinline__ uint32_t fbits(float x) { return __float_as_uint(x); }
 
-// round to bf16, nearest even (NaN -> 0x7fc0, as c10::BFloat16); returned widened to f32
-__device__ __forceinline__ float bf16r(float x) {
-  uint32_t u = fbits(x);
-  if ((u & 0x7fffffffu) > 0x7f800000u) return bitsf(0x7fc00000u);
-  u += 0x7fffu + ((u >> 16) & 1u);
-  return bitsf(u & 0xffff0000u);
-}
+// round to bf16, nearest even, by gfx950's v_cvt_pk_bf16_f32; returned widened to f32. Equal to
+// c10::BFloat16's rounding on every non-NaN input, denormals included; a NaN stays a NaN (the
+// hardware keeps its sign and leading payload bits where c10 returns 0x7fc0; no NaN arises
+// from finite inputs in the decode)
+__device__ __forceinline__ float bf16r(float x) { return (float)(__bf16)x; }
 __device__ __forceinline__ float bf16f(uint32_t hi16) { return bitsf(hi16 << 16); }
 
 // the model dtype's rounding

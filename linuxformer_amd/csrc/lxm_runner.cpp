@@ -88,7 +88,10 @@ int main(int argc, char** argv) {
       {"inputs", (void**)&p.inputs},     {"trace", (void**)&p.trace},
       {"ring", (void**)&p.ring},         {"hn", (void**)&p.hn},
       {"sync", (void**)&p.sync},         {"keys", (void**)&p.keys},
-      {"err", (void**)&p.err},           {"prof", (void**)&p.prof}};
+      {"err", (void**)&p.err},           {"prof", (void**)&p.prof},
+      {"mb_task", (void**)&p.mb_task},   {"mb_e", (void**)&p.mb_e},
+      {"mb_qk", (void**)&p.mb_qk},       {"ybuf", (void**)&p.ybuf},
+      {"xo", (void**)&p.xo}};
   for (auto& kv : field) *kv.second = nullptr;
   int n_blocks = 0, lds = 0;
   std::ifstream mf(dir + "/manifest.txt");

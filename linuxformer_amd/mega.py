@@ -23,7 +23,7 @@ import torch
 from . import mk_build
 
 NT, MAXH, KD, VD, RMAX = 512, 4096, 256, 128, 8
-MAXU, MAXQK, MAXQKL, MAXDEC, HOT_MAX, NSYNC = 2048, 1024, 512, 512, 65536, 256
+MAXU, MAXQK, MAXQKL, MAXDEC, HOT_MAX, NSYNC, OUT_MAX = 2048, 1024, 512, 512, 65536, 256, 1024
 
 I32, I64, F32, PTR = ctypes.c_int32, ctypes.c_int64, ctypes.c_float, ctypes.c_void_p
 
@@ -60,7 +60,7 @@ class Params(ctypes.Structure):
                             "head_rows", "head_ptr", "head_ent", "forced")] + \
         [("n_forced", I32), ("n_tokens", I32)] + \
         [(n, PTR) for n in ("preds", "inputs", "trace", "ring", "hn", "sync", "keys", "err",
-                            "prof")] + \
+                            "prof", "mb_task", "mb_e", "mb_qk", "ybuf", "xo")] + \
         [("n_qk_total", I32), ("pad", I32)]
 
 
@@ -182,6 +182,9 @@ class Mega:
         cus = int(self.lib.lxm_device_cus())
         self.ncta = ncta or cus
         assert self.ncta >= 2, "the decode needs the chain workgroup and at least one helper"
+        nh = self.ncta - 1
+        assert d.nv <= nh, "each value head needs its own helper workgroup"
+        assert -(-d.hidden // nh) <= 31, "a helper workgroup computes at most 31 out_proj rows"
         assert d.kd == KD and d.vd == VD and d.conv == 4, "key dim 256, value dim 128, conv 4"
         assert d.nv % d.nk == 0 and d.nv // d.nk <= RMAX and d.hidden <= MAXH
         assert d.nv <= 256 and d.nk <= 64 and d.n_layers <= 64
@@ -257,7 +260,10 @@ class Mega:
             o_w1post = hb.add(pk.w1(ly.post_attention_layernorm))
             o_unit = hb.add(np.asarray(meta, np.uint32).tobytes())
             o_gu = hb.add(b"".join(gu_parts))
-            o_dptr = hb.add(dptr.astype(np.uint16).tobytes())
+            # padded to MAXH + 8 rows (the kernel reads four rows' pointers at once)
+            dpad = np.full(MAXH + 8, dptr[-1], np.int64)
+            dpad[:H + 1] = dptr
+            o_dptr = hb.add(dpad.astype(np.uint16).tobytes())
             o_dent = hb.add(pk.ent(dunits, dvals))
             o_qk = hb.add(b"".join(bytes(q) for q in qks))
             o_dec = hb.add(b"".join(bytes(x) for x in decs))
@@ -284,23 +290,16 @@ class Mega:
             z = _Csr(ly.in_proj_z)
             desc.z_row = blob.add(np.stack([z.ptr[:-1], np.diff(z.ptr)], 1).astype(np.int32).tobytes())
             desc.z_ent = blob.add(pk.ent(z.cols, z.vals))
-            # out_proj by residual row, per key head, columns local to the head's value dims
-            oc = ly.out_proj
-            head_of = oc.cols // (R * VD)
-            optr = np.zeros((d.nk, H + 1), np.int64)
-            oent = []
-            base = 0
-            for kh in range(d.nk):
-                sel = head_of == kh
-                rr, cc, vv = oc.rows[sel], oc.cols[sel] - kh * R * VD, oc.vals[sel]
-                order = np.lexsort((cc, rr))
-                rr, cc, vv = rr[order], cc[order], vv[order]
-                optr[kh, 1:] = np.cumsum(np.bincount(rr, minlength=H)) + base
-                optr[kh, 0] = base
-                base += len(rr)
-                oent.append(pk.ent(cc, vv))
+            # out_proj by residual row over all value dims (vh * vd + j), ascending; each
+            # helper workgroup stages the entries of its slice of rows
+            oc = _Csr(ly.out_proj)
+            optr = oc.ptr
+            rp = -(-H // nh)
+            for r0 in range(0, H, rp):
+                n_e = int(optr[min(r0 + rp, H)] - optr[r0])
+                assert n_e <= OUT_MAX, f"layer {L}: {n_e} out_proj entries in {rp} rows > {OUT_MAX}"
             desc.out_ptr = blob.add(optr.astype(np.int32).tobytes())
-            desc.out_ent = blob.add(b"".join(oent))
+            desc.out_ent = blob.add(pk.ent(oc.cols, oc.vals))
             desc.gnorm = blob.add(np.asarray(ly.norm, np.float32).tobytes())
             self.stats["hot_bytes"].append(hb.n)
             self.stats["units"].append(len(units))
@@ -329,7 +328,6 @@ class Mega:
         self.head_ent = torch.frombuffer(bytearray(pk.ent(emb.cols[keep], emb.vals[keep]) + bytes(16)),
                                          dtype=torch.uint8).to(dev)
         V = emb.n
-        nh = self.ncta - 1
         # block 0 is the chain (no head rows); helper b covers cuts[b - 1] .. cuts[b]
         cuts = np.linspace(0, V, nh + 1).round().astype(np.int64)
         bounds = np.concatenate([[0], cuts])
@@ -341,14 +339,19 @@ class Mega:
             need = max(need, ((r1 - r0 + 1) * 4 + 15) // 16 * 16 + ne * pk.esz)
         self.head_lds = int((need + 15) // 16 * 16)
         base = int(self.lib.lxm_lds_base())
-        self.lds = max(base, self.head_lds + 4 * MAXH + 128)
+        self.lds = max(base, int(self.lib.lxm_helper_lds(self.head_lds)))
         self.lds = (self.lds + 255) // 256 * 256
         maxlds = int(self.lib.lxm_max_lds())
         assert self.lds <= maxlds, (self.lds, maxlds)
         assert int(self.lib.lxm_max_blocks(self.lds)) >= self.ncta, "the grid is not co-resident"
         self.vocab = V
         # ---- run buffers (the library allocates nothing)
-        self.ring = torch.zeros(4 * d.n_layers * H, dtype=torch.float32, device=dev)
+        self.ring = torch.zeros(4 * d.n_layers * MAXH, dtype=torch.float32, device=dev)
+        self.mb_task = torch.zeros(d.nv, dtype=torch.int32, device=dev)
+        self.mb_e = torch.zeros(d.nv, dtype=torch.float32, device=dev)
+        self.mb_qk = torch.zeros(MAXQKL, dtype=torch.float32, device=dev)
+        self.ybuf = torch.zeros(d.nv * VD, dtype=torch.float32, device=dev)
+        self.xo = torch.zeros(MAXH, dtype=torch.float32, device=dev)
         self.hn = torch.zeros(MAXH, dtype=torch.float32, device=dev)
         self.sync = torch.zeros(NSYNC, dtype=torch.int32, device=dev)
         self.keys = torch.zeros(2, dtype=torch.int64, device=dev)
@@ -358,23 +361,34 @@ class Mega:
                            "head_nnz": int(hptr[-1]), "vocab": V})
 
     PHASES = ("embedding", "layer staging (+trace)", "norms (stage A)",
-              "gates + MLP units (stage B)", "active heads + MLP redo", "down_proj + next norm (stage C)",
-              "final norm + publish", "head argmax wait")
+              "gates + MLP units (stage B)", "GDN events + MLP redo",
+              "down_proj + next norm (stage C)", "final norm + publish", "head argmax wait")
+    HELPER = ("wait", "head rows", "value head", "out_proj rows")
+
+    @property
+    def prof_size(self) -> int:
+        return 32 + 4 * self.ncta
 
     def phase_report(self, prof: torch.Tensor) -> dict:
-        """prof counters -> cycles per token of each chain phase, and the helpers' mean cycles
-        per token waiting for the flag and computing their rows."""
+        """prof counters -> cycles per token of each chain phase, and the helpers' mean (and
+        max) cycles per token in each of their parts."""
         c = prof.cpu().tolist()
         n = max(c[17], 1)
         out = {name: round(c[k] / n, 1) for k, name in enumerate(self.PHASES)}
-        out["active layer-steps per token"] = round(c[16] / n, 3)
-        hw = [c[32 + 2 * b] for b in range(1, self.ncta)]
-        hc = [c[33 + 2 * b] for b in range(1, self.ncta)]
-        out["helper wait"] = round(sum(hw) / len(hw) / n, 1)
-        out["helper compute"] = round(sum(hc) / len(hc) / n, 1)
-        out["helper compute max"] = round(max(hc) / n, 1)
+        out["GDN events per token"] = round(c[16] / n, 3)
+        for k, name in enumerate(self.HELPER):
+            v = [c[32 + 4 * b + k] for b in range(1, self.ncta)]
+            out[f"helper {name}"] = round(sum(v) / len(v) / n, 1)
+            out[f"helper {name} max"] = round(max(v) / n, 1)
         out["tokens"] = n
         return out
+
+    def _bufs(self) -> dict:
+        return dict(ring=self.ring.data_ptr(), hn=self.hn.data_ptr(), sync=self.sync.data_ptr(),
+                    keys=self.keys.data_ptr(), err=self.err.data_ptr(),
+                    mb_task=self.mb_task.data_ptr(), mb_e=self.mb_e.data_ptr(),
+                    mb_qk=self.mb_qk.data_ptr(), ybuf=self.ybuf.data_ptr(),
+                    xo=self.xo.data_ptr())
 
     def dump(self, path: str, forced, n: int, prof: bool = False) -> None:
         """Write everything a launch needs (tables, states, parameter block, manifest) to path,
@@ -406,10 +420,12 @@ class Mega:
             lines.append(f"ptrs {field} {d.n_layers} " + " ".join(files))
         for name, nbytes in (("preds", 4 * n), ("ring", self.ring.numel() * 4),
                              ("hn", self.hn.numel() * 4), ("sync", NSYNC * 4), ("keys", 16),
-                             ("err", 4)):
+                             ("err", 4), ("mb_task", self.mb_task.numel() * 4),
+                             ("mb_e", self.mb_e.numel() * 4), ("mb_qk", self.mb_qk.numel() * 4),
+                             ("ybuf", self.ybuf.numel() * 4), ("xo", self.xo.numel() * 4)):
             lines.append(f"zero {name} {nbytes}")
         if prof:
-            lines.append(f"zero prof {8 * (32 + 2 * self.ncta)}")
+            lines.append(f"zero prof {8 * self.prof_size}")
         p = Params(hidden=d.hidden, n_layers=d.n_layers, nk=d.nk, kd=KD, nv=d.nv, vd=VD,
                    n_conv=d.n_conv, vocab=self.vocab, bf16=int(self.bf), n_blocks=self.ncta,
                    rms_eps=d.rms_eps, head_lds=self.head_lds, e4=int(self.e4), n_forced=1,
@@ -445,7 +461,7 @@ class Mega:
         """n steps; step i's input is forced[i] (i < len(forced)) or step i - 1's prediction.
         Returns the n predictions (chip token ids). inputs (n,) int32: each step's input as the
         kernel embedded it. trace (n, n_layers, hidden) float32: the residual after each
-        layer of each step. prof (32 + 2 x ncta) int64: phase cycle counters (see
+        layer of each step. prof (``prof_size``) int64: phase cycle counters (see
         ``phase_report``)."""
         assert len(forced) >= 1 and n >= 1
         f = np.asarray(forced, np.int64)
@@ -458,7 +474,7 @@ class Mega:
         if inputs is not None:
             assert inputs.dtype == torch.int32 and inputs.numel() >= n and inputs.device == self.dev
         if prof is not None:
-            assert prof.dtype == torch.int64 and prof.numel() >= 32 + 2 * self.ncta
+            assert prof.dtype == torch.int64 and prof.numel() >= self.prof_size
             assert prof.device == self.dev
         if trace is not None:
             assert trace.dtype == torch.float32 and trace.is_contiguous()
@@ -477,10 +493,8 @@ class Mega:
                    n_tokens=n, preds=preds.data_ptr(),
                    inputs=inputs.data_ptr() if inputs is not None else None,
                    trace=trace.data_ptr() if trace is not None else None,
-                   ring=self.ring.data_ptr(), hn=self.hn.data_ptr(), sync=self.sync.data_ptr(),
-                   keys=self.keys.data_ptr(), err=self.err.data_ptr(),
                    prof=prof.data_ptr() if prof is not None else None,
-                   n_qk_total=self.n_qk_total)
+                   n_qk_total=self.n_qk_total, **self._bufs())
         pd = torch.frombuffer(bytearray(bytes(p)), dtype=torch.uint8).to(self.dev)
         self._keep = (rs, cs, ft, pd)
         st = ctypes.c_void_p(torch.cuda.current_stream(self.dev).cuda_stream)

@@ -73,5 +73,5 @@ def load() -> ctypes.CDLL:
     return _lib
 
 
-EXPORTS = ("lxm_run", "lxm_lds_base", "lxm_max_blocks", "lxm_max_lds", "lxm_last_error",
-           "lxm_device_cus", "lxm_t_elem", "lxm_t_sum")
+EXPORTS = ("lxm_run", "lxm_lds_base", "lxm_helper_lds", "lxm_max_blocks", "lxm_max_lds",
+           "lxm_last_error", "lxm_device_cus", "lxm_t_elem", "lxm_t_sum")

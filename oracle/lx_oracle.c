@@ -152,12 +152,19 @@ void ox_elem(int fn, const float* x, float* y, long n) {
 
 /* ------------------------------------------------------------------ canonical sums */
 
-/* the 512-lane sum of n values (n <= 512 * 64 is plenty for hidden sizes) */
+/* the 512-lane sum of n <= 4096 values: lane l adds x[4l .. 4l+3] then x[2048+4l .. 2048+4l+3]
+   (those < n) in order from +0; lanes pair within groups of 64 at offsets 32..1, the 8 group
+   totals at offsets 4, 2, 1 */
 float ox_sum_h(const float* x, int n) {
   float p[512], w[8];
+  if (n > 4096) return __builtin_nanf("");
   for (int l = 0; l < 512; l++) {
     float s = 0.0f;
-    for (int i = l; i < n; i += 512) s = s + x[i];
+    for (int part = 0; part < 2; part++)
+      for (int j = 0; j < 4; j++) {
+        const int i = 2048 * part + 4 * l + j;
+        if (i < n) s = s + x[i];
+      }
     p[l] = s;
   }
   for (int g = 0; g < 8; g++) {

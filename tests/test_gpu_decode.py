@@ -91,6 +91,9 @@ def test_device_math_matches_oracle(cuda):
     for fn, code in ox.ELEM.items():
         lo, hi = (0.0, 1e9) if fn in ("log1p", "rsqrt") else (-120.0, 100.0)
         x = np.concatenate([allb, rng.uniform(lo, hi, 1 << 20).astype(np.float32)])
+        if fn == "bf16":  # every exponent: denormals, rounding into infinity, NaNs
+            x = np.concatenate([x, rng.integers(0, 1 << 32, 1 << 20, dtype=np.uint64)
+                                .astype(np.uint32).view(np.float32)])
         if fn == "log1p":
             x = np.abs(x)
         xd = torch.from_numpy(x).to(cuda)

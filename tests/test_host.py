@@ -69,6 +69,9 @@ class _FakeLib:
     def lxm_max_lds(self):
         return 163_840
 
+    def lxm_helper_lds(self, head_lds):
+        return head_lds + 43_392
+
     def lxm_max_blocks(self, lds):
         return 256
 
@@ -116,6 +119,15 @@ def test_packer_tables_decode_to_the_model(packed):
             want = [(uidx[int(c)], float(v)) for c, v in zip(dn.cols[dn.rows == i], dn.vals[dn.rows == i])
                     if int(c) in uidx]
             got = [_ent(blob, base + hot.down_ent, k) for k in range(dptr[i], dptr[i + 1])]
+            assert [(int(c), float(v)) for c, v in got] == want
+        # out_proj by residual row over every value dim, ascending
+        oc = ly.out_proj
+        optr = np.frombuffer(blob[descs[L].out_ptr:descs[L].out_ptr + 4 * (m.dims.hidden + 1)], np.int32)
+        for i in range(m.dims.hidden):
+            sel = oc.rows == i
+            order = np.argsort(oc.cols[sel], kind="stable")
+            want = list(zip(oc.cols[sel][order].tolist(), oc.vals[sel][order].tolist()))
+            got = [_ent(blob, descs[L].out_ent, k) for k in range(optr[i], optr[i + 1])]
             assert [(int(c), float(v)) for c, v in got] == want
     # head: rows x columns with a nonzero final weight
     hptr = mg.head_ptr.numpy()

@@ -68,19 +68,20 @@ def test_bf16_elementwise_equals_torch(oracle_lib):
 
 
 def test_hidden_sum_order(oracle_lib):
-    """The 512-lane tree: lane l adds x[l], x[l + 512], ... in order; lanes pair at offsets
-    32..1 within a group of 64, then the 8 group totals at 4, 2, 1. Big values placed where the
-    documented pairing cancels them first keep the small terms; any other order loses them."""
+    """The 512-lane tree: lane l adds x[4l..4l+3] then x[2048+4l..2048+4l+3] in order; lanes
+    pair at offsets 32..1 within a group of 64, then the 8 group totals at 4, 2, 1. Big values
+    placed where the documented pairing cancels them first keep the small terms; any other
+    order loses them."""
     ox = oracle_lib
     x = np.zeros(3572, np.float32)
-    x[0], x[32] = 1e8, -1e8          # paired at offset 32 inside group 0
-    x[1] = 1.0                        # meets the pair's exact 0 later
-    x[64 * 3], x[64 * 7] = 3e8, -3e8  # groups 3 and 7 pair at offset 4
-    x[64 * 5 + 7] = 0.5
+    x[0], x[4 * 32] = 1e8, -1e8            # lanes 0 and 32: paired at offset 32 in group 0
+    x[4] = 1.0                              # lane 1 meets the pair's exact 0 later
+    x[256 * 3], x[256 * 7] = 3e8, -3e8      # groups 3 and 7 (their lane 0) pair at offset 4
+    x[2048 + 256 * 5 + 28] = 0.5            # lane 327 (group 5), second part
     assert ox.sum_h(x) == 1.5
     y = np.zeros(3572, np.float32)
-    y[5], y[5 + 512] = 1e8, 1.0       # one lane, in order: 1e8 + 1 rounds to 1e8
-    y[5 + 1024] = -1e8
+    y[20], y[21] = 1e8, 1.0                 # lane 5, in order: 1e8 + 1 rounds to 1e8
+    y[2048 + 20] = -1e8                     # lane 5's fifth term
     assert ox.sum_h(y) == 0.0
     z = np.arange(1, 3573, dtype=np.float32)
     assert ox.sum_h(z) == float(z.astype(np.float64).sum())
