@@ -101,7 +101,8 @@ typedef struct lxm_params {
   int32_t* preds;          /* (n_tokens) */
   int32_t* inputs;         /* (n_tokens) or null: each step's input as embedded */
   float* trace;            /* (n_tokens, n_layers, hidden) or null: residual after each layer */
-  float* ring;             /* (4, n_layers, LXM_MAXH): recent GDN norm outputs */
+  float* ring;             /* (4, n_layers, LXM_MAXH): the last 4 steps' layer inputs */
+  float* rring;            /* (4, n_layers): their norm factors r */
   float* hn;               /* (hidden): the head's normed input, chain -> helpers */
   uint32_t* sync;          /* LXM_NSYNC words, zero at launch */
   unsigned long long* keys;/* (2), zero at launch */

@@ -53,8 +53,7 @@ static_assert(MAXH == 8 * NT, "eight residual rows per thread cover any hidden s
 #define L_HOT 0
 #define L_H (L_HOT + LXM_HOT_MAX)
 #define L_XM (L_H + 4 * MAXH)
-#define L_XG (L_XM + 4 * MAXH)
-#define L_ACT (L_XG + 4 * MAXH)
+#define L_ACT (L_XM + 4 * MAXH)
 #define L_HIST (L_ACT + 4 * LXM_MAXU)
 #define L_QKCUR (L_HIST + 4 * 3 * LXM_MAXQK)
 #define L_EV (L_QKCUR + 4 * LXM_MAXQKL)
@@ -73,7 +72,8 @@ static_assert(MAXH == 8 * NT, "eight residual rows per thread cover any hidden s
 
 // LDS layout of a helper workgroup, after its head tables (p.head_lds bytes)
 #define HX_X 0                        // hidden: the head's normed input, or a task's GDN norm
-#define HX_QD (HX_X + 4 * MAXH)       // dense query / key of the task's key head, raw
+#define HX_XW (HX_X + 4 * MAXH)       // the GDN norm's output 1, 2 and 3 steps back
+#define HX_QD (HX_XW + 3 * 4 * MAXH)  // dense query / key of the task's key head, raw
 #define HX_KD (HX_QD + 4 * KD)
 #define HX_QN (HX_KD + 4 * KD)        // the same after l2norm (query scaled by 1/16)
 #define HX_KN (HX_QN + 4 * KD)
@@ -227,12 +227,15 @@ struct Ent<false> {
   }
 };
 
-// Dot products of a sparse row with x, in entry order from +0, terms with x == 0 skipped
-// (which leaves the sum's bits unchanged: a sum from +0 never yields -0). A chunk issues the
-// loads of N entries at once, unconditionally (every table is followed by at least N entries'
-// worth of bytes, so they stay inside the LDS region or the blob), and drops the terms past the
-// row's end by selects, so the code has no branches. Where: 0 x in LDS, 1 entries in global
-// memory and x in LDS, 2 entries in global memory and x in global memory (agent-scope loads).
+// Dot products of a sparse row with x (a hidden-sized or unit-sized vector), in entry order
+// from +0. A chunk issues the loads of N entries at once, unconditionally (every table is
+// followed by at least N entries' worth of bytes, so they stay inside the LDS region or the
+// blob), keeps the index inside the vector's MAXH slots (index & (MAXH - 1)) and gives the
+// slots past the row's end weight 0, so the code has no branches. Every x the slots can reach
+// is finite (LDS starts zeroed; the ring starts zeroed), so a weight-0 term, like a term with
+// x == 0, adds +-0 to a sum that started from +0 and is never -0: the sum's bits are those of
+// the row's own terms, in order (the oracle skips x == 0 terms; same bits). Where: 0 x in LDS,
+// 1 entries in global memory and x in LDS.
 template <bool E4, int N, int WHERE>
 __device__ __forceinline__ float chunk(const uint8_t* ent, int64_t start, int n, int k0,
                                        const float* x, float s) {
@@ -244,14 +247,14 @@ __device__ __forceinline__ float chunk(const uint8_t* ent, int64_t start, int n,
     else Ent<E4>::gat(ent, start + k0 + j, i[j], w[j]);
   }
 #pragma unroll
-  for (int j = 0; j < N; j++) i[j] = k0 + j < n ? i[j] : 0;
-#pragma unroll
   for (int j = 0; j < N; j++) {
-    if constexpr (WHERE == 2) xv[j] = ld_rlxf(x + i[j]);
-    else xv[j] = x[i[j]];
+    i[j] &= MAXH - 1;
+    w[j] = k0 + j < n ? w[j] : 0.0f;
   }
 #pragma unroll
-  for (int j = 0; j < N; j++) s = (k0 + j < n && xv[j] != 0.0f) ? s + xv[j] * w[j] : s;
+  for (int j = 0; j < N; j++) xv[j] = x[i[j]];
+#pragma unroll
+  for (int j = 0; j < N; j++) s = s + xv[j] * w[j];
   return s;
 }
 template <bool E4, int N, int WHERE>
@@ -264,11 +267,11 @@ template <bool E4, int N, int WHERE>
 __device__ __forceinline__ float dot(const uint8_t* ent, int64_t start, int n, const float* x) {
   return rest<E4, N, WHERE>(ent, start, n, x, chunk<E4, N, WHERE>(ent, start, n, 0, x, 0.0f));
 }
-// R rows at once: the first N entries of every row, then N more of every row while any row of
-// this thread has more (a row past its end adds nothing). Each round loads all rows' entries,
-// then all their x values, so a round is two LDS round trips. Entry reads run up to the
-// longest row's length past a shorter row's start: the tables sit inside the 64 KB hot region,
-// followed by other LDS arrays.
+// R rows at once (chunk's rules): the first N entries of every row, then N more of every row
+// while any row of this thread has more. Each round loads all rows' entries, then all their x
+// values, so a round is two LDS round trips. Entry reads run up to the longest row's length
+// past a shorter row's start: the tables sit inside the 64 KB hot region, followed by other
+// LDS arrays.
 template <bool E4, int N, int R>
 __device__ __forceinline__ void dots_round(const uint8_t* ent, const int (&st)[R],
                                            const int (&n)[R], int k0, const float* x,
@@ -282,7 +285,10 @@ __device__ __forceinline__ void dots_round(const uint8_t* ent, const int (&st)[R
 #pragma unroll
   for (int r = 0; r < R; r++)
 #pragma unroll
-    for (int j = 0; j < N; j++) i[r][j] = k0 + j < n[r] ? i[r][j] : 0;
+    for (int j = 0; j < N; j++) {
+      i[r][j] &= MAXH - 1;
+      w[r][j] = k0 + j < n[r] ? w[r][j] : 0.0f;
+    }
 #pragma unroll
   for (int r = 0; r < R; r++)
 #pragma unroll
@@ -290,8 +296,7 @@ __device__ __forceinline__ void dots_round(const uint8_t* ent, const int (&st)[R
 #pragma unroll
   for (int r = 0; r < R; r++)
 #pragma unroll
-    for (int j = 0; j < N; j++)
-      s[r] = (k0 + j < n[r] && xv[r][j] != 0.0f) ? s[r] + xv[r][j] * w[r][j] : s[r];
+    for (int j = 0; j < N; j++) s[r] = s[r] + xv[r][j] * w[r][j];
 }
 template <bool E4, int N, int R>
 __device__ __forceinline__ void dots(const uint8_t* ent, const int (&st)[R], const int (&n)[R],
@@ -381,9 +386,41 @@ __device__ __forceinline__ void conv_put(void* cs, int64_t i, float v) {
   else gp(reinterpret_cast<float*>(cs))[i] = v;
 }
 
-// the ring of GDN norm outputs: slot (step & 3), layer L, MAXH floats each
+// The ring of the last four steps' layer inputs (the residual before the GDN's norm): slot
+// (step & 3), layer L, MAXH floats each, and each entry's norm factor r (rring). The GDN norm's
+// output of a step is D((h * r) * (1 + w_in)) from them.
 __device__ __forceinline__ float* ring_at(const lxm_params& p, int step, int L) {
   return p.ring + ((size_t)(step & 3) * p.n_layers + L) * MAXH;
+}
+__device__ __forceinline__ float* rr_at(const lxm_params& p, int step, int L) {
+  return p.rring + (size_t)(step & 3) * p.n_layers + L;
+}
+// 16 bytes to global memory at agent scope (a buffer store with the sc1 policy: written through
+// to the coherence point, like the relaxed atomic stores)
+__device__ __forceinline__ void st4_rlx(float* base, int idx, v4f v) {
+  const __amdgpu_buffer_rsrc_t r = __builtin_amdgcn_make_buffer_rsrc(base, 0, 0x7fffffff, 0x00020000);
+  typedef uint32_t v4u_ __attribute__((ext_vector_type(4)));
+  __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(v4u_, v), r, idx * 4, 0, 16);
+}
+// one norm weight 1 + w of column c from a layer's w1 table (LDS or global)
+template <bool E4, bool GLOBAL>
+__device__ __forceinline__ float w1_one(const uint8_t* tab, int c) {
+  if constexpr (E4) {
+    const uint16_t b = GLOBAL ? gp(reinterpret_cast<const uint16_t*>(tab))[c]
+                              : reinterpret_cast<const uint16_t*>(tab)[c];
+    return 1.0f + bf16f(b);
+  } else {
+    return GLOBAL ? gp(reinterpret_cast<const float*>(tab))[c] : reinterpret_cast<const float*>(tab)[c];
+  }
+}
+// the GDN norm's output of (step, L) for every column, into LDS out (rows past H: 0)
+template <bool BF, bool E4>
+__device__ __forceinline__ void ring_norm(const lxm_params& p, int step, int L, const uint8_t* w1in,
+                                          float* out) {
+  const float r = ld_rlxf(rr_at(p, step, L));
+  const float* hs = ring_at(p, step, L);
+  for (int c = threadIdx.x; c < p.hidden; c += NT)
+    out[c] = rd<BF>((ld_rlxf(hs + c) * r) * w1_one<E4, true>(w1in, c));
 }
 
 // ---------------------------------------------------------------------------------------------
@@ -497,10 +534,34 @@ __device__ __forceinline__ void mlp_units(const lxm_hot& hd, const uint8_t* hot)
 // Flags per key head: 1 query nonzero, 2 key nonzero, 4 a decay exp(g) != 1; F_ANY and F_OUT
 // directly. Items run on the threads from the top down (the units take them from the bottom
 // up).
+// a gate row's dot product with the GDN norm's output D((h * r) * (1 + w_in)), formed per entry
 template <bool BF, bool E4>
-__device__ __forceinline__ void gates(const lxm_params& p, const lxm_hot& hd, const uint8_t* hot) {
+__device__ __forceinline__ float ndot(const uint8_t* ent, int start, int n, float r,
+                                      const uint8_t* w1in) {
+  const float* h = LF(L_H);
+  float s = 0.0f;
+  for (int k0 = 0; k0 < n; k0 += 4) {
+    int i[4];
+    float w[4], xv[4];
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+      Ent<E4>::at(ent, start + k0 + j, i[j], w[j]);
+      i[j] &= MAXH - 1;
+      w[j] = k0 + j < n ? w[j] : 0.0f;
+    }
+#pragma unroll
+    for (int j = 0; j < 4; j++) xv[j] = rd<BF>((h[i[j]] * r) * w1_one<E4, false>(w1in, i[j]));
+#pragma unroll
+    for (int j = 0; j < 4; j++) s = s + xv[j] * w[j];
+  }
+  return s;
+}
+
+template <bool BF, bool E4>
+__device__ __forceinline__ void gates(const lxm_params& p, const lxm_hot& hd, const uint8_t* hot,
+                                      float r) {
   const int tt = NT - 1 - (int)threadIdx.x;
-  const float* xg = LF(L_XG);
+  const uint8_t* w1in = hot + hd.w1_in;
   float* hist = LF(L_HIST);
   float* qkcur = LF(L_QKCUR);
   float* ev = LF(L_EV);
@@ -511,7 +572,7 @@ __device__ __forceinline__ void gates(const lxm_params& p, const lxm_hot& hd, co
     const lxm_qkc c = qk[j];
     float* hs = hist + 3 * (hd.qk_base + j);
     const float h0 = hs[0], h1 = hs[1], h2 = hs[2];
-    const float P = rd<BF>(dot<E4, 4, 0>(ent, c.start, c.len, xg));
+    const float P = rd<BF>(ndot<BF, E4>(ent, c.start, c.len, r, w1in));
     float y = 0.0f;
     y = y + c.taps[0] * h0;
     y = y + c.taps[1] * h1;
@@ -533,7 +594,7 @@ __device__ __forceinline__ void gates(const lxm_params& p, const lxm_hot& hd, co
   const lxm_dec* dc = reinterpret_cast<const lxm_dec*>(hot + hd.dec);
   for (int j = ((tt - hd.n_qk) % NT + NT) % NT; j < hd.n_dec; j += NT) {
     const lxm_dec d = dc[j];
-    const float a = rd<BF>(dot<E4, 4, 0>(ent, d.start, d.len, xg));
+    const float a = rd<BF>(ndot<BF, E4>(ent, d.start, d.len, r, w1in));
     const float x = a + d.dt_bias;
     float e;
     if (x < -104.0f && d.A_log <= 88.0f) {
@@ -550,10 +611,10 @@ __device__ __forceinline__ void gates(const lxm_params& p, const lxm_hot& hd, co
   }
 }
 
-// stage A's norm: r = rsqrt(mean(h^2) + eps) (transformers qwen3_5 :727, mean = sum / n); both
-// norms' inputs D((h * r) * (1 + w)) (:729-734) from one h * r; the GDN norm's output also to the
-// ring. Only the MLP's when gdn is false (the redo after a delta rule that wrote h). Rows past
-// H compute from +0 and a clamped weight; nothing reads them.
+// stage A's norm: r = rsqrt(mean(h^2) + eps) (transformers qwen3_5 :727, mean = sum / n); the
+// MLP's input D((h * r) * (1 + w)) (:729-734) for every row; with gdn, h and r to the ring (the
+// GDN norm's output, the same expression with its own weights, is formed where it is read).
+// Rows past H compute from +0 and weight 1; nothing reads them.
 // four norm weights 1 + w of rows c..c+3 (c a multiple of 4); rows >= H get 1
 template <bool E4>
 __device__ __forceinline__ v4f w1x4(const uint8_t* hot, int off, int c, int H) {
@@ -582,26 +643,16 @@ __device__ __forceinline__ void norms(const lxm_params& p, const lxm_hot& hd, co
   const int t = threadIdx.x, H = p.hidden;
   const v4f* h4 = reinterpret_cast<const v4f*>(smem + L_H);
   v4f* xm4 = reinterpret_cast<v4f*>(smem + L_XM);
-  v4f* xg4 = reinterpret_cast<v4f*>(smem + L_XG);
   const int c0 = 4 * t, c1 = 2048 + 4 * t;
   const v4f ha = h4[t], hb = h4[NT + t];
   const v4f pa = w1x4<E4>(hot, hd.w1_post, c0, H), pb = w1x4<E4>(hot, hd.w1_post, c1, H);
   xm4[t] = norm4<BF>(ha, r, pa);
   xm4[NT + t] = norm4<BF>(hb, r, pb);
   if (gdn) {
-    const v4f ia = w1x4<E4>(hot, hd.w1_in, c0, H), ib = w1x4<E4>(hot, hd.w1_in, c1, H);
-    const v4f ga = norm4<BF>(ha, r, ia), gb = norm4<BF>(hb, r, ib);
-    xg4[t] = ga;
-    xg4[NT + t] = gb;
     float* ring = ring_at(p, step, L);
-    st_rlxf(ring + c0, ga.x);
-    st_rlxf(ring + c0 + 1, ga.y);
-    st_rlxf(ring + c0 + 2, ga.z);
-    st_rlxf(ring + c0 + 3, ga.w);
-    st_rlxf(ring + c1, gb.x);
-    st_rlxf(ring + c1 + 1, gb.y);
-    st_rlxf(ring + c1 + 2, gb.z);
-    st_rlxf(ring + c1 + 3, gb.w);
+    st4_rlx(ring, c0, ha);
+    st4_rlx(ring, c1, hb);
+    if (t == 0) st_rlxf(rr_at(p, step, L), r);
   }
 }
 
@@ -679,7 +730,7 @@ __device__ __forceinline__ bool layer(const lxm_params& p, int L, int step, floa
   }
   // ---- stage B: the gates and, speculatively (the GDN leaves h alone on most steps), the MLP
   mlp_units<BF, E4>(hd, hot);
-  gates<BF, E4>(p, hd, hot);
+  gates<BF, E4>(p, hd, hot, r);
   lds_barrier();
   if (PROF_ON && t == 0) {
     const uint64_t c1 = cycles();
@@ -742,6 +793,9 @@ __device__ void run_chain(const lxm_params& p) {
   float* h = LF(L_H);
   float* hist = LF(L_HIST);
   LtEnt* lt = reinterpret_cast<LtEnt*>(smem + L_LT);
+  // every LDS word starts finite (zero): gathers may read slots no table names
+  for (int k = t; k < L_CHAIN_END / 16; k += NT) reinterpret_cast<v4u*>(smem)[k] = v4u{0, 0, 0, 0};
+  __syncthreads();
   // the live query/key channels' windows from the conv state (positions 1..3)
   for (int L = 0; L < p.n_layers; L++) {
     const lxm_hot* hd = reinterpret_cast<const lxm_hot*>(p.blob + p.layers[L].hot);
@@ -755,8 +809,7 @@ __device__ void run_chain(const lxm_params& p) {
     lt[L].hot = hb;
     lt[L].n16 = reinterpret_cast<const lxm_hot*>(hb)->size / 16;
   }
-  for (int c = t; c < MAXH; c += NT) h[c] = 0.0f;
-  __syncthreads();
+  __syncthreads();  // the layer table, before any thread's fetch reads it
   stage(fetch(0));
   Pf pf = fetch(p.n_layers > 1 ? 1 : 0);  // always one layer ahead of the staged one
   uint64_t* pa = reinterpret_cast<uint64_t*>(smem + L_PROF);
@@ -911,13 +964,15 @@ __device__ void gdn_head(const lxm_params& p, int L, int step, int vh, bool out,
   }
   const float e = ld_rlxf(p.mb_e + vh);
   const bool live = (tf & 1) != 0, dec = (tf & 4) != 0;
-  const lxm_layer ly = p.layers[L];
+  const lxm_layer ly = ldg(p.layers + L);
   const uint8_t* hot = p.blob + ly.hot;
-  const lxm_hot hd = *reinterpret_cast<const lxm_hot*>(hot);
-  // the step's GDN norm output, and this key head's dense query and key
-  {
-    const float* ring = ring_at(p, step, L);
-    for (int c = t; c < H; c += NT) xg[c] = ld_rlxf(ring + c);
+  const lxm_hot hd = ldg(reinterpret_cast<const lxm_hot*>(hot));
+  // the GDN norm's output of this step and the three before (the conv windows' inputs), and
+  // this key head's dense query and key
+  if (live) {
+    ring_norm<BF, E4>(p, step, L, hot + hd.w1_in, xg);
+    for (int s = 1; s <= 3 && step - s >= 0; s++)
+      ring_norm<BF, E4>(p, step - s, L, hot + hd.w1_in, xg + s * MAXH);
   }
   if (t < KD) {
     qd[t] = 0.0f;
@@ -968,7 +1023,7 @@ __device__ void gdn_head(const lxm_params& p, int L, int step, int vh, bool out,
         win[3 - s] = 0.0f;
         if (ch.taps[3 - s] == 0.0f) continue;
         if (step - s >= 0)
-          win[3 - s] = rd<BF>(dot<E4, 4, 2>(qent, ch.start, ch.len, ring_at(p, step - s, L)));
+          win[3 - s] = rd<BF>(dot<E4, 4, 1>(qent, ch.start, ch.len, xg + s * MAXH));
         else
           win[3 - s] = conv_at<BF>(p.conv[L], (int64_t)chan * 4 + 4 - (s - step));
       }
@@ -1138,6 +1193,10 @@ __device__ void run_helper(const lxm_params& p) {
   uint8_t* lent = lds + (((size_t)(nr + 1) * 4 + 15) & ~(size_t)15);
   uint8_t* hx = lds + p.head_lds;
   int* misc = reinterpret_cast<int*>(hx + HX_MISC);
+  // every LDS word starts finite (zero): gathers may read slots no table names
+  for (int k = t; k < (p.head_lds + HX_END) / 16; k += NT)
+    reinterpret_cast<v4u*>(lds)[k] = v4u{0, 0, 0, 0};
+  __syncthreads();
   for (int k = t; k <= nr; k += NT) lptr[k] = (int32_t)(p.head_ptr[r0 + k] - e0);
   {
     const uint32_t* src = p.head_ent + e0 * (Ent<E4>::SZ / 4);
@@ -1218,17 +1277,30 @@ __device__ void write_windows(const lxm_params& p) {
   const int n = p.n_tokens;
   for (int64_t g = a + threadIdx.x; g < b; g += NT) {
     const int L = (int)(g / p.n_conv), c = (int)(g % p.n_conv);
-    const lxm_layer ly = p.layers[L];
+    const lxm_layer ly = ldg(p.layers + L);
     const lxm_chan ch = ldg(reinterpret_cast<const lxm_chan*>(p.blob + ly.chan) + c);
     void* cs = p.conv[L];
     float w[4];
 #pragma unroll
     for (int k = 0; k < 4; k++) {
       const int s = n - 4 + k;
-      if (s >= 0)
-        w[k] = rd<BF>(dot<E4, 4, 2>(p.blob + ly.qkv_ent, ch.start, ch.len, ring_at(p, s, L)));
-      else
+      if (s >= 0) {
+        // the channel's projection of step s's GDN norm output, formed per entry from the ring
+        const uint8_t* w1in = p.blob + ly.hot + ldg(reinterpret_cast<const lxm_hot*>(p.blob + ly.hot)).w1_in;
+        const float r = ld_rlxf(rr_at(p, s, L));
+        const float* hs = ring_at(p, s, L);
+        float acc = 0.0f;
+        for (int e = 0; e < ch.len; e++) {
+          int col;
+          float wt;
+          Ent<E4>::gat(p.blob + ly.qkv_ent, ch.start + e, col, wt);
+          const float xv = rd<BF>((ld_rlxf(hs + col) * r) * w1_one<E4, true>(w1in, col));
+          acc = acc + xv * wt;
+        }
+        w[k] = rd<BF>(acc);
+      } else {
         w[k] = conv_at<BF>(cs, (int64_t)c * 4 + 4 + s);
+      }
     }
 #pragma unroll
     for (int k = 0; k < 4; k++) conv_put<BF>(cs, (int64_t)c * 4 + k, w[k]);

@@ -87,6 +87,7 @@ int main(int argc, char** argv) {
       {"forced", (void**)&p.forced},     {"preds", (void**)&p.preds},
       {"inputs", (void**)&p.inputs},     {"trace", (void**)&p.trace},
       {"ring", (void**)&p.ring},         {"hn", (void**)&p.hn},
+      {"rring", (void**)&p.rring},
       {"sync", (void**)&p.sync},         {"keys", (void**)&p.keys},
       {"err", (void**)&p.err},           {"prof", (void**)&p.prof},
       {"mb_task", (void**)&p.mb_task},   {"mb_e", (void**)&p.mb_e},

@@ -59,7 +59,7 @@ class Params(ctypes.Structure):
         [(n, PTR) for n in ("layers", "blob", "rec", "conv", "emb_ptr", "emb_ent", "w1_final",
                             "head_rows", "head_ptr", "head_ent", "forced")] + \
         [("n_forced", I32), ("n_tokens", I32)] + \
-        [(n, PTR) for n in ("preds", "inputs", "trace", "ring", "hn", "sync", "keys", "err",
+        [(n, PTR) for n in ("preds", "inputs", "trace", "ring", "rring", "hn", "sync", "keys", "err",
                             "prof", "mb_task", "mb_e", "mb_qk", "ybuf", "xo")] + \
         [("n_qk_total", I32), ("pad", I32)]
 
@@ -347,6 +347,7 @@ class Mega:
         self.vocab = V
         # ---- run buffers (the library allocates nothing)
         self.ring = torch.zeros(4 * d.n_layers * MAXH, dtype=torch.float32, device=dev)
+        self.rring = torch.zeros(4 * d.n_layers, dtype=torch.float32, device=dev)
         self.mb_task = torch.zeros(d.nv, dtype=torch.int32, device=dev)
         self.mb_e = torch.zeros(d.nv, dtype=torch.float32, device=dev)
         self.mb_qk = torch.zeros(MAXQKL, dtype=torch.float32, device=dev)
@@ -384,7 +385,8 @@ class Mega:
         return out
 
     def _bufs(self) -> dict:
-        return dict(ring=self.ring.data_ptr(), hn=self.hn.data_ptr(), sync=self.sync.data_ptr(),
+        return dict(ring=self.ring.data_ptr(), rring=self.rring.data_ptr(),
+                    hn=self.hn.data_ptr(), sync=self.sync.data_ptr(),
                     keys=self.keys.data_ptr(), err=self.err.data_ptr(),
                     mb_task=self.mb_task.data_ptr(), mb_e=self.mb_e.data_ptr(),
                     mb_qk=self.mb_qk.data_ptr(), ybuf=self.ybuf.data_ptr(),
@@ -419,6 +421,7 @@ class Mega:
                 files.append(fn)
             lines.append(f"ptrs {field} {d.n_layers} " + " ".join(files))
         for name, nbytes in (("preds", 4 * n), ("ring", self.ring.numel() * 4),
+                             ("rring", self.rring.numel() * 4),
                              ("hn", self.hn.numel() * 4), ("sync", NSYNC * 4), ("keys", 16),
                              ("err", 4), ("mb_task", self.mb_task.numel() * 4),
                              ("mb_e", self.mb_e.numel() * 4), ("mb_qk", self.mb_qk.numel() * 4),
