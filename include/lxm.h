@@ -32,6 +32,8 @@ extern "C" {
 #define LXM_HOT_MAX 65536   /* bytes of one layer's resident tables */
 #define LXM_NSYNC 256       /* uint32 words of the sync area */
 #define LXM_OUT_MAX 1024    /* out_proj entries of the rows one helper workgroup computes */
+#define LXM_OUT_HELPERS 64  /* helper workgroups that compute out_proj's rows */
+#define LXM_OUT_ROWS 64     /* out_proj rows one of them computes, at most */
 
 /* One layer's resident tables (the "hot" blob the chain workgroup stages in LDS). All offsets
    are bytes from the start of the hot blob, 16-byte aligned. */

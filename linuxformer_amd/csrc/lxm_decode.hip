@@ -71,9 +71,8 @@ static_assert(MAXH == 8 * NT, "eight residual rows per thread cover any hidden s
 #define F_KH 16
 
 // LDS layout of a helper workgroup, after its head tables (p.head_lds bytes)
-#define HX_X 0                        // hidden: the head's normed input, or a task's GDN norm
-#define HX_XW (HX_X + 4 * MAXH)       // the GDN norm's output 1, 2 and 3 steps back
-#define HX_QD (HX_XW + 3 * 4 * MAXH)  // dense query / key of the task's key head, raw
+#define HX_X 0                        // hidden: the head's normed input
+#define HX_QD (HX_X + 4 * MAXH)       // dense query / key of the task's key head, raw
 #define HX_KD (HX_QD + 4 * KD)
 #define HX_QN (HX_KD + 4 * KD)        // the same after l2norm (query scaled by 1/16)
 #define HX_KN (HX_QN + 4 * KD)
@@ -83,10 +82,10 @@ static_assert(MAXH == 8 * NT, "eight residual rows per thread cover any hidden s
 #define HX_DL (HX_O + 4 * VD)         // delta = (v - kv) beta
 #define HX_BS (HX_DL + 4 * VD)        // per row block (16 rows) partial sums, [16][VD]
 #define HX_MISC (HX_BS + 4 * 16 * VD) // ints: [0] nq, [1] nk, [2] beta bits, [4] event, [5] ok
-#define HX_OP (HX_MISC + 256)         // out_proj: the helper's row pointers (32 ints)
-#define HX_OE (HX_OP + 4 * 32)        // its entries (LXM_OUT_MAX, 8 bytes each at most)
+#define HX_OP (HX_MISC + 256)         // out_proj: the helper's row pointers (LXM_OUT_ROWS + 1)
+#define HX_OE (HX_OP + 4 * (LXM_OUT_ROWS + 4))  // its entries (LXM_OUT_MAX, 8 bytes at most)
 #define HX_OY (HX_OE + 8 * LXM_OUT_MAX)  // the head outputs each entry reads
-#define HX_END (HX_OY + 4 * LXM_OUT_MAX)
+#define HX_END (HX_OY + 4 * LXM_OUT_MAX + 64)  // (reads run up to 3 slots past the end)
 
 // sync words (uint32 indices into p.sync, groups 128 bytes apart)
 #define S_EV 0     // the event word: seq << 8 | layer << 2 | out << 1 | kind (0 head, 1 gdn)
@@ -413,14 +412,31 @@ __device__ __forceinline__ float w1_one(const uint8_t* tab, int c) {
     return GLOBAL ? gp(reinterpret_cast<const float*>(tab))[c] : reinterpret_cast<const float*>(tab)[c];
   }
 }
-// the GDN norm's output of (step, L) for every column, into LDS out (rows past H: 0)
+// A row's dot product (entries in global memory, chunk's rules) with the GDN norm's output of
+// a step, formed per entry from the ring: x[c] = D((h[c] * r) * (1 + w_in[c])), h by agent-
+// scope loads. Only the columns the row names are read.
 template <bool BF, bool E4>
-__device__ __forceinline__ void ring_norm(const lxm_params& p, int step, int L, const uint8_t* w1in,
-                                          float* out) {
-  const float r = ld_rlxf(rr_at(p, step, L));
-  const float* hs = ring_at(p, step, L);
-  for (int c = threadIdx.x; c < p.hidden; c += NT)
-    out[c] = rd<BF>((ld_rlxf(hs + c) * r) * w1_one<E4, true>(w1in, c));
+__device__ __forceinline__ float rdot(const uint8_t* ent, int64_t start, int n, const float* hs,
+                                      float r, const uint8_t* w1in) {
+  float s = 0.0f;
+  for (int k0 = 0; k0 < n; k0 += 4) {
+    int i[4];
+    float w[4], hv[4], wi[4];
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+      Ent<E4>::gat(ent, start + k0 + j, i[j], w[j]);
+      i[j] &= MAXH - 1;
+      w[j] = k0 + j < n ? w[j] : 0.0f;
+    }
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+      hv[j] = ld_rlxf(hs + i[j]);
+      wi[j] = w1_one<E4, true>(w1in, i[j]);
+    }
+#pragma unroll
+    for (int j = 0; j < 4; j++) s = s + rd<BF>((hv[j] * r) * wi[j]) * w[j];
+  }
+  return s;
 }
 
 // ---------------------------------------------------------------------------------------------
@@ -945,7 +961,6 @@ template <bool BF, bool E4>
 __device__ void gdn_head(const lxm_params& p, int L, int step, int vh, bool out, uint8_t* hx) {
   const int t = threadIdx.x, H = p.hidden, R = p.nv / p.nk, kh = vh / R;
   const int wv = t >> 6, lane = t & 63;
-  float* xg = reinterpret_cast<float*>(hx + HX_X);
   float* qd = reinterpret_cast<float*>(hx + HX_QD);
   float* kd = reinterpret_cast<float*>(hx + HX_KD);
   float* qn = reinterpret_cast<float*>(hx + HX_QN);
@@ -967,13 +982,7 @@ __device__ void gdn_head(const lxm_params& p, int L, int step, int vh, bool out,
   const lxm_layer ly = ldg(p.layers + L);
   const uint8_t* hot = p.blob + ly.hot;
   const lxm_hot hd = ldg(reinterpret_cast<const lxm_hot*>(hot));
-  // the GDN norm's output of this step and the three before (the conv windows' inputs), and
   // this key head's dense query and key
-  if (live) {
-    ring_norm<BF, E4>(p, step, L, hot + hd.w1_in, xg);
-    for (int s = 1; s <= 3 && step - s >= 0; s++)
-      ring_norm<BF, E4>(p, step - s, L, hot + hd.w1_in, xg + s * MAXH);
-  }
   if (t < KD) {
     qd[t] = 0.0f;
     kd[t] = 0.0f;
@@ -1013,17 +1022,21 @@ __device__ void gdn_head(const lxm_params& p, int L, int step, int vh, bool out,
   // conv state before this launch), the in_proj_z rows and beta = sigmoid(b) (:497)
   if (live) {
     const uint8_t* qent = p.blob + ly.qkv_ent;
+    const uint8_t* w1in = hot + hd.w1_in;
+    const float* h0 = ring_at(p, step, L);
+    const float r0 = ld_rlxf(rr_at(p, step, L));
     if (t < VD) {
       const int chan = 2 * p.nk * KD + vh * VD + t;
       const lxm_chan ch = ldg(reinterpret_cast<const lxm_chan*>(p.blob + ly.chan) + chan);
       float win[4];
-      win[3] = rd<BF>(dot<E4, 4, 1>(qent, ch.start, ch.len, xg));
+      win[3] = rd<BF>(rdot<BF, E4>(qent, ch.start, ch.len, h0, r0, w1in));
 #pragma unroll
       for (int s = 1; s <= 3; s++) {
         win[3 - s] = 0.0f;
         if (ch.taps[3 - s] == 0.0f) continue;
         if (step - s >= 0)
-          win[3 - s] = rd<BF>(dot<E4, 4, 1>(qent, ch.start, ch.len, xg + s * MAXH));
+          win[3 - s] = rd<BF>(rdot<BF, E4>(qent, ch.start, ch.len, ring_at(p, step - s, L),
+                                            ld_rlxf(rr_at(p, step - s, L)), w1in));
         else
           win[3 - s] = conv_at<BF>(p.conv[L], (int64_t)chan * 4 + 4 - (s - step));
       }
@@ -1035,10 +1048,10 @@ __device__ void gdn_head(const lxm_params& p, int L, int step, int vh, bool out,
     } else if (t < 2 * VD) {
       const int j = t - VD;
       const lxm_row zr = ldg(reinterpret_cast<const lxm_row*>(p.blob + ly.z_row) + vh * VD + j);
-      zb[j] = rd<BF>(dot<E4, 4, 1>(p.blob + ly.z_ent, zr.start, zr.len, xg));
+      zb[j] = rd<BF>(rdot<BF, E4>(p.blob + ly.z_ent, zr.start, zr.len, h0, r0, w1in));
     } else if (t == 2 * VD) {
       const lxm_row br = ldg(reinterpret_cast<const lxm_row*>(p.blob + ly.b_row) + vh);
-      const float b = rd<BF>(dot<E4, 4, 1>(p.blob + ly.b_ent, br.start, br.len, xg));
+      const float b = rd<BF>(rdot<BF, E4>(p.blob + ly.b_ent, br.start, br.len, h0, r0, w1in));
       misc[2] = (int)__float_as_uint(rd<BF>(sigmoid(b)));
     }
   }
@@ -1171,13 +1184,20 @@ __device__ void out_rows(const lxm_params& p, int L, int ra, int rb, uint8_t* hx
   }
   __syncthreads();
   if (t < rb - ra) {
+    // the row's entries in order, four at a time (slots past the row weigh 0; oy is finite)
+    const int a = op[t], n = op[t + 1] - a;
     float s = 0.0f;
-    for (int k = op[t]; k < op[t + 1]; k++) {
-      int d;
-      float w;
-      Ent<E4>::at(oe, k, d, w);
-      const float x = oy[k];
-      if (x != 0.0f) s = s + x * w;
+    for (int k0 = 0; k0 < n; k0 += 4) {
+      float w[4], x[4];
+#pragma unroll
+      for (int j = 0; j < 4; j++) {
+        int d;
+        Ent<E4>::at(oe, a + k0 + j, d, w[j]);
+        w[j] = k0 + j < n ? w[j] : 0.0f;
+        x[j] = oy[a + k0 + j];
+      }
+#pragma unroll
+      for (int j = 0; j < 4; j++) s = s + x[j] * w[j];
     }
     st_rlxf(p.xo + ra + t, rd<BF>(s));
   }
@@ -1203,8 +1223,10 @@ __device__ void run_helper(const lxm_params& p) {
     uint32_t* dst = reinterpret_cast<uint32_t*>(lent);
     for (int64_t k = t; k < ne * (Ent<E4>::SZ / 4); k += NT) dst[k] = src[k];
   }
-  // out_proj rows of this helper: an even split of the residual rows
-  const int rp = (H + nh - 1) / nh;
+  // out_proj rows of this helper: an even split of the residual rows over the first
+  // LXM_OUT_HELPERS helpers
+  const int no = nh < LXM_OUT_HELPERS ? nh : LXM_OUT_HELPERS;
+  const int rp = (H + no - 1) / no;
   const int ra = (b - 1) * rp < H ? (b - 1) * rp : H, rb = ra + rp < H ? ra + rp : H;
   const int vh = b - 1;
   const bool owner = vh < p.nv;
@@ -1287,17 +1309,8 @@ __device__ void write_windows(const lxm_params& p) {
       if (s >= 0) {
         // the channel's projection of step s's GDN norm output, formed per entry from the ring
         const uint8_t* w1in = p.blob + ly.hot + ldg(reinterpret_cast<const lxm_hot*>(p.blob + ly.hot)).w1_in;
-        const float r = ld_rlxf(rr_at(p, s, L));
-        const float* hs = ring_at(p, s, L);
-        float acc = 0.0f;
-        for (int e = 0; e < ch.len; e++) {
-          int col;
-          float wt;
-          Ent<E4>::gat(p.blob + ly.qkv_ent, ch.start + e, col, wt);
-          const float xv = rd<BF>((ld_rlxf(hs + col) * r) * w1_one<E4, true>(w1in, col));
-          acc = acc + xv * wt;
-        }
-        w[k] = rd<BF>(acc);
+        w[k] = rd<BF>(rdot<BF, E4>(p.blob + ly.qkv_ent, ch.start, ch.len, ring_at(p, s, L),
+                                   ld_rlxf(rr_at(p, s, L)), w1in));
       } else {
         w[k] = conv_at<BF>(cs, (int64_t)c * 4 + 4 + s);
       }

@@ -24,6 +24,7 @@ from . import mk_build
 
 NT, MAXH, KD, VD, RMAX = 512, 4096, 256, 128, 8
 MAXU, MAXQK, MAXQKL, MAXDEC, HOT_MAX, NSYNC, OUT_MAX = 2048, 1024, 512, 512, 65536, 256, 1024
+OUT_HELPERS, OUT_ROWS = 64, 64
 
 I32, I64, F32, PTR = ctypes.c_int32, ctypes.c_int64, ctypes.c_float, ctypes.c_void_p
 
@@ -184,7 +185,7 @@ class Mega:
         assert self.ncta >= 2, "the decode needs the chain workgroup and at least one helper"
         nh = self.ncta - 1
         assert d.nv <= nh, "each value head needs its own helper workgroup"
-        assert -(-d.hidden // nh) <= 31, "a helper workgroup computes at most 31 out_proj rows"
+        assert -(-d.hidden // min(nh, OUT_HELPERS)) <= OUT_ROWS, "too many out_proj rows per helper"
         assert d.kd == KD and d.vd == VD and d.conv == 4, "key dim 256, value dim 128, conv 4"
         assert d.nv % d.nk == 0 and d.nv // d.nk <= RMAX and d.hidden <= MAXH
         assert d.nv <= 256 and d.nk <= 64 and d.n_layers <= 64
@@ -294,7 +295,7 @@ class Mega:
             # helper workgroup stages the entries of its slice of rows
             oc = _Csr(ly.out_proj)
             optr = oc.ptr
-            rp = -(-H // nh)
+            rp = -(-H // min(nh, OUT_HELPERS))
             for r0 in range(0, H, rp):
                 n_e = int(optr[min(r0 + rp, H)] - optr[r0])
                 assert n_e <= OUT_MAX, f"layer {L}: {n_e} out_proj entries in {rp} rows > {OUT_MAX}"

@@ -13,10 +13,12 @@ real chip's decode touches ~4.5 state rows per token (lx/results/head_activity.j
 synthetic stacks reproduce that with one *gate column* per layer at the top of the residual
 stream: a layer's query, key and decay projections read only its gate column, no projection
 writes gate columns, and a token's embedding row sets the gate columns of p_gate x n_layers
-seeded layers (config 2: exactly one). A layer-step therefore has a nonzero query, key or decay
-only when its input tokens carry that layer's gate, i.e. on about ``p_gate`` of layer-steps
-whatever tokens the greedy stream visits (the final norm weight is -1 on gate columns, so the head's argmax never
-sees them). Everything else is uniform at the configured density, except that a SwiGLU unit's
+seeded layers (config 2: exactly one). The query/key channels of the benchmark stacks convolve
+only the current token (their earlier taps are 0; ``qk_window``), so a layer-step has a nonzero
+query, key or decay exactly when its own input token carries that layer's gate, i.e. on
+``p_gate`` of layer-steps whatever tokens the greedy stream visits (with earlier taps a gate
+would stay open for the following three tokens too). The final norm weight is -1 on gate
+columns, so the head's argmax never sees them. Everything else is uniform at the configured density, except that a SwiGLU unit's
 up_proj row reads the same (seeded, uniform) columns as its gate_proj row, so that units fire
 and the residual stream mixes across layers.
 """
@@ -137,6 +139,7 @@ class Spec:
     p_live: float = 0.25  # per key head: reads the gate (query/key rows)
     p_decay: float = 0.25  # per value head of a live key head: in_proj_a reads the gate
     p_tap: float = 0.1  # per earlier conv tap of a live channel
+    qk_window: bool = False  # query/key channels get earlier taps too (gates stay open 3 more steps)
     gate_gain: float = 64.0  # 1 + input_layernorm weight on gate columns
     dt_bias: float = -112.0  # softplus(dt_bias) == 0 in fp32: no decay without the gate
     emb_nnz: int = 3  # nonzeros per embedding row outside the gate columns
@@ -172,7 +175,7 @@ def small(seed: int = 7, n_layers: int = 3, hidden: int = 192, vocab: int = 512,
     return Spec("small", Dims(hidden=hidden, n_layers=n_layers, nk=2, nv=8, inter=48,
                               vocab=vocab, dtype=dtype), seed=seed, density=density,
                 p_gate=p_gate, p_live=1.0, p_decay=0.5, p_tap=0.3, emb_nnz=6, state=state,
-                n_steps=64)
+                n_steps=64, qk_window=True)
 
 
 def _rng(seed: int, *k: int) -> np.random.Generator:
@@ -224,6 +227,8 @@ def _layer(spec: Spec, L: int) -> Layer:
     conv[has_row, d.conv - 1] = rc.choice(VALS, size=int(has_row.sum()))
     extra = (rc.random((C, d.conv - 1)) < spec.p_tap) & has_row[:, None]
     conv[:, :d.conv - 1] = np.where(extra, rc.choice(VALS, size=(C, d.conv - 1)), 0.0)
+    if not spec.qk_window:
+        conv[:2 * nk * kd, :d.conv - 1] = 0.0
     # decay projections: some value heads of live key heads read the gate
     ra = _rng(s, L, _A)
     vh_live = np.repeat(live, R)

@@ -70,7 +70,7 @@ class _FakeLib:
         return 163_840
 
     def lxm_helper_lds(self, head_lds):
-        return head_lds + 92_544
+        return head_lds + 43_600
 
     def lxm_max_blocks(self, lds):
         return 256
