@@ -30,7 +30,7 @@ extern "C" {
 #define LXM_MAXQKL 512      /* live query/key channels of one layer */
 #define LXM_MAXDEC 512      /* decaying value heads of one layer */
 #define LXM_HOT_MAX 65536   /* bytes of one layer's resident tables */
-#define LXM_NSYNC 256       /* uint32 words of the sync area */
+#define LXM_NSYNC 1024      /* uint32 words of the sync area */
 #define LXM_OUT_MAX 1024    /* out_proj entries of the rows one helper workgroup computes */
 #define LXM_OUT_HELPERS 64  /* helper workgroups that compute out_proj's rows */
 #define LXM_OUT_ROWS 64     /* out_proj rows one of them computes, at most */

@@ -87,11 +87,15 @@ static_assert(MAXH == 8 * NT, "eight residual rows per thread cover any hidden s
 #define HX_OY (HX_OE + 8 * LXM_OUT_MAX)  // the head outputs each entry reads
 #define HX_END (HX_OY + 4 * LXM_OUT_MAX + 64)  // (reads run up to 3 slots past the end)
 
-// sync words (uint32 indices into p.sync, groups 128 bytes apart)
-#define S_EV 0     // the event word: seq << 8 | layer << 2 | out << 1 | kind (0 head, 1 gdn)
-#define S_CALL 32  // helpers done with an event (each helper, each event)
-#define S_CVH 64   // value-head helpers done with a GDN event's heads (each, each GDN event)
-#define S_DONE 96
+// sync words (uint32 indices into p.sync). The event word and both counters have one copy per
+// group of helpers (group = block index mod 8, the XCD a block lands on when blocks are dealt
+// round-robin), each on its own 128-byte line, so at most 32 workgroups poll or count on one
+// line; a counter's value is the sum of its 8 copies.
+#define NGRP 8
+#define S_EV 0       // + 32 g: seq << 8 | layer << 2 | out << 1 | kind (0 head, 1 gdn)
+#define S_CALL 256   // + 32 g: helpers done with an event (each helper, each event)
+#define S_CVH 512    // + 32 g: value-head helpers done with a GDN event's heads
+#define S_DONE 768
 #define EV_GDN 1u
 #define EV_OUT 2u
 
@@ -167,7 +171,7 @@ __device__ __forceinline__ uint64_t cycles() { return __builtin_readcyclecounter
 __device__ bool spin_ge(const uint32_t* p, uint32_t target, int32_t* err, int code) {
   const uint64_t t0 = wall();
   while ((int32_t)(ld_rlx(p) - target) < 0) {
-    __builtin_amdgcn_s_sleep(1);
+    __builtin_amdgcn_s_sleep(2);
     if (__hip_atomic_load(gp(err), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) return false;
     if (wall() - t0 > TIMEOUT_TICKS) {
       __hip_atomic_fetch_max(gp(err), code, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -176,12 +180,30 @@ __device__ bool spin_ge(const uint32_t* p, uint32_t target, int32_t* err, int co
   }
   return true;
 }
+// spin (one thread) until the sum of a counter's NGRP copies reaches target (modulo 2^32)
+__device__ bool spin_sum_ge(const uint32_t* p, uint32_t target, int32_t* err, int code) {
+  const uint64_t t0 = wall();
+  for (;;) {
+    uint32_t v[NGRP], sum = 0;
+#pragma unroll
+    for (int g = 0; g < NGRP; g++) v[g] = ld_rlx(p + 32 * g);
+#pragma unroll
+    for (int g = 0; g < NGRP; g++) sum += v[g];
+    if ((int32_t)(sum - target) >= 0) return true;
+    __builtin_amdgcn_s_sleep(2);
+    if (__hip_atomic_load(gp(err), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) return false;
+    if (wall() - t0 > TIMEOUT_TICKS) {
+      __hip_atomic_fetch_max(gp(err), code, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      return false;
+    }
+  }
+}
 // spin (one thread) until the word differs from last; 0 on timeout or another block's error
 __device__ bool spin_ne(const uint32_t* p, uint32_t last, uint32_t* out, int32_t* err, int code) {
   const uint64_t t0 = wall();
   uint32_t v;
   while ((v = ld_rlx(p)) == last) {
-    __builtin_amdgcn_s_sleep(1);
+    __builtin_amdgcn_s_sleep(2);
     if (__hip_atomic_load(gp(err), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) return false;
     if (wall() - t0 > TIMEOUT_TICKS) {
       __hip_atomic_fetch_max(gp(err), code, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -692,12 +714,11 @@ __device__ bool gdn_event(const lxm_params& p, int L, uint32_t& seq, uint32_t& t
   for (int j = t; j < hd.n_qk; j += NT) st_rlxf(p.mb_qk + j, LF(L_QKCUR)[j]);
   drain();  // these and stage A's ring stores, visible at agent scope
   __syncthreads();
-  if (t == 0) {
-    seq++;
-    st_rlx(p.sync + S_EV, (seq << 8) | ((uint32_t)L << 2) | (out ? EV_OUT : 0u) | EV_GDN);
-    target += (uint32_t)(p.n_blocks - 1);
-    flags[F_OK] = spin_ge(p.sync + S_CALL, target, p.err, 4);
-  }
+  seq++;
+  if (t < NGRP)
+    st_rlx(p.sync + S_EV + 32 * t, (seq << 8) | ((uint32_t)L << 2) | (out ? EV_OUT : 0u) | EV_GDN);
+  target += (uint32_t)(p.n_blocks - 1);
+  if (t == 0) flags[F_OK] = spin_sum_ge(p.sync + S_CALL, target, p.err, 4);
   __syncthreads();
   if (!flags[F_OK]) return false;
   if (out) {
@@ -888,11 +909,11 @@ __device__ void run_chain(const lxm_params& p) {
       pa[6] += c - pa[15];
       pa[15] = c;
     }
+    seq++;
+    target += nh;
+    if (t < NGRP) st_rlx(p.sync + S_EV + 32 * t, seq << 8);
     if (t == 0) {
-      seq++;
-      st_rlx(p.sync + S_EV, seq << 8);
-      target += nh;
-      bool ok = spin_ge(p.sync + S_CALL, target, p.err, 1);
+      bool ok = spin_sum_ge(p.sync + S_CALL, target, p.err, 1);
       int pred = 0;
       if (ok) {
         const unsigned long long key = __hip_atomic_load(gp(p.keys + (i & 1)), __ATOMIC_RELAXED,
@@ -1230,6 +1251,7 @@ __device__ void run_helper(const lxm_params& p) {
   const int ra = (b - 1) * rp < H ? (b - 1) * rp : H, rb = ra + rp < H ? ra + rp : H;
   const int vh = b - 1;
   const bool owner = vh < p.nv;
+  const int grp = b % NGRP;
   __syncthreads();
   uint64_t pr[4] = {0, 0, 0, 0};
   uint32_t last = 0, ngdn = 0;
@@ -1238,7 +1260,7 @@ __device__ void run_helper(const lxm_params& p) {
     const uint64_t w0 = PROF_ON ? cycles() : 0;
     if (t == 0) {
       uint32_t w = 0;
-      misc[5] = spin_ne(p.sync + S_EV, last, &w, p.err, 2);
+      misc[5] = spin_ne(p.sync + S_EV + 32 * grp, last, &w, p.err, 2);
       misc[4] = (int)w;
     }
     __syncthreads();
@@ -1262,24 +1284,24 @@ __device__ void run_helper(const lxm_params& p) {
         gdn_head<BF, E4>(p, L, step, vh, out, hx);
         drain();
         __syncthreads();
-        if (t == 0) add_rlx(p.sync + S_CVH, 1u);
+        if (t == 0) add_rlx(p.sync + S_CVH + 32 * grp, 1u);
       }
       uint64_t w2 = 0;
       if (PROF_ON) {
         w2 = cycles();
         pr[2] += w2 - w1;
       }
-      if (out) {
-        if (t == 0) misc[5] = spin_ge(p.sync + S_CVH, (uint32_t)p.nv * ngdn, p.err, 5);
+      if (out && rb > ra) {  // only the helpers with out_proj rows wait for every head
+        if (t == 0) misc[5] = spin_sum_ge(p.sync + S_CVH, (uint32_t)p.nv * ngdn, p.err, 5);
         __syncthreads();
         if (!misc[5]) return;
-        if (rb > ra) out_rows<BF, E4>(p, L, ra, rb, hx);
+        out_rows<BF, E4>(p, L, ra, rb, hx);
       }
       if (PROF_ON) pr[3] += cycles() - w2;
     }
     drain();
     __syncthreads();
-    if (t == 0) add_rlx(p.sync + S_CALL, 1u);
+    if (t == 0) add_rlx(p.sync + S_CALL + 32 * grp, 1u);
   }
   if (PROF_ON && t == 0)
     for (int k = 0; k < 4; k++) p.prof[32 + 4 * b + k] = pr[k];

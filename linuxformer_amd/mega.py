@@ -23,7 +23,7 @@ import torch
 from . import mk_build
 
 NT, MAXH, KD, VD, RMAX = 512, 4096, 256, 128, 8
-MAXU, MAXQK, MAXQKL, MAXDEC, HOT_MAX, NSYNC, OUT_MAX = 2048, 1024, 512, 512, 65536, 256, 1024
+MAXU, MAXQK, MAXQKL, MAXDEC, HOT_MAX, NSYNC, OUT_MAX = 2048, 1024, 512, 512, 65536, 1024, 1024
 OUT_HELPERS, OUT_ROWS = 64, 64
 
 I32, I64, F32, PTR = ctypes.c_int32, ctypes.c_int64, ctypes.c_float, ctypes.c_void_p
