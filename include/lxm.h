@@ -39,8 +39,11 @@ extern "C" {
    are bytes from the start of the hot blob, 16-byte aligned. */
 typedef struct lxm_hot {
   int32_t n_units, n_qk, n_dec, qk_base; /* qk_base: the layer's first q/k history slot */
-  int32_t w1_in, w1_post;  /* norm weights: e4 raw w (bf16 bits, uint16), else 1 + w (fp32) */
-  int32_t unit;            /* uint32 per unit: entry start (16 bits) | gate count (8) | up (8) */
+  int32_t ent_w1;          /* the GDN norm's weight at each `ent` entry's column (format below) */
+  int32_t w1_post;         /* the MLP norm's weights, LXM_MAXH rows: e4 raw w (bf16 bits, uint16),
+                              else 1 + w (fp32); rows past hidden hold w = 0 */
+  int32_t unit;            /* uint32 per unit (units by row length): entry start (16 bits) |
+                              gate count (8) | up count (8) */
   int32_t gu_ent;          /* gate then up entries of each unit (column) */
   int32_t down_ptr;        /* uint16 per residual row + 1: down entries of the row */
   int32_t down_ent;        /* entries (unit) */
@@ -81,6 +84,7 @@ typedef struct lxm_layer {
   int64_t out_ptr;         /* int32[hidden + 1]: out_proj by residual row */
   int64_t out_ent;         /* entries (value dim, all heads: vh * vd + j), ascending per row */
   int64_t gnorm;           /* float[vd] */
+  int64_t w1_in;           /* the GDN norm's weights (hidden), w1_post's format */
 } lxm_layer;
 
 typedef struct lxm_params {

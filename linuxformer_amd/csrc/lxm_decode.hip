@@ -50,18 +50,21 @@ static_assert(MAXH == 8 * NT, "eight residual rows per thread cover any hidden s
 
 // ---------------------------------------------------------------------------------------------
 // LDS layout of the chain workgroup (bytes)
-#define L_HOT 0
-#define L_H (L_HOT + LXM_HOT_MAX)
-#define L_XM (L_H + 4 * MAXH)
-#define L_ACT (L_XM + 4 * MAXH)
-#define L_HIST (L_ACT + 4 * LXM_MAXU)
+// (the vectors the sparse rows gather from sit below 64 KB, so a gather's base folds into the
+// ds_read's 16-bit offset)
+#define L_ACT 0
+#define L_XM (L_ACT + 4 * LXM_MAXU)
+#define L_H (L_XM + 4 * MAXH)
+#define L_HIST (L_H + 4 * MAXH)
 #define L_QKCUR (L_HIST + 4 * 3 * LXM_MAXQK)
 #define L_EV (L_QKCUR + 4 * LXM_MAXQKL)
 #define L_WSUM (L_EV + 4 * 256)
 #define L_FLAGS (L_WSUM + 4 * 32)
 #define L_PROF (L_FLAGS + 4 * 256)
 #define L_LT (L_PROF + 8 * 32)
-#define L_CHAIN_END (L_LT + 16 * 64)
+#define L_HOT (L_LT + 16 * 64)
+#define L_CHAIN_END (L_HOT + LXM_HOT_MAX + 2048)  // (gathers read up to ~1 KB past a table)
+static_assert(L_H + 4 * MAXH <= 65536, "gathered vectors below 64 KB");
 // flags (int): [0] any head active, [1] any query live (the residual may change), [4] ok,
 // [8] token, [16 + kh] per key head: bit 0 query nonzero, bit 1 key nonzero, bit 2 a decay
 #define F_ANY 0
@@ -70,7 +73,7 @@ static_assert(MAXH == 8 * NT, "eight residual rows per thread cover any hidden s
 #define F_TOK 8
 #define F_KH 16
 
-// LDS layout of a helper workgroup, after its head tables (p.head_lds bytes)
+// LDS layout of a helper workgroup, before its head tables (p.head_lds bytes, from HX_END)
 #define HX_X 0                        // hidden: the head's normed input
 #define HX_QD (HX_X + 4 * MAXH)       // dense query / key of the task's key head, raw
 #define HX_KD (HX_QD + 4 * KD)
@@ -248,8 +251,21 @@ struct Ent<false> {
   }
 };
 
+// s + x * w, rounded once as the oracle's s + D(x * w): for bf16 models x and w are bf16
+// values, whose product is exact in fp32, so one fused op gives the same bits
+template <bool BF>
+__device__ __forceinline__ float acc(float s, float x, float w) {
+  if constexpr (BF) return __builtin_fmaf(x, w, s);
+  else return s + x * w;
+}
+// the float at byte offset off of vector x
+__device__ __forceinline__ float at_b(const float* x, int off) {
+  return *reinterpret_cast<const float*>(reinterpret_cast<const uint8_t*>(x) + off);
+}
+#define OFF_MASK (4 * MAXH - 4)
+
 // Dot products of a sparse row with x (a hidden-sized or unit-sized vector), in entry order
-// from +0. A chunk issues the loads of N entries at once, unconditionally (every table is
+// from +0. Entries store the column as a byte offset into x. A chunk issues the loads of N entries at once, unconditionally (every table is
 // followed by at least N entries' worth of bytes, so they stay inside the LDS region or the
 // blob), keeps the index inside the vector's MAXH slots (index & (MAXH - 1)) and gives the
 // slots past the row's end weight 0, so the code has no branches. Every x the slots can reach
@@ -257,7 +273,7 @@ struct Ent<false> {
 // x == 0, adds +-0 to a sum that started from +0 and is never -0: the sum's bits are those of
 // the row's own terms, in order (the oracle skips x == 0 terms; same bits). Where: 0 x in LDS,
 // 1 entries in global memory and x in LDS.
-template <bool E4, int N, int WHERE>
+template <bool BF, bool E4, int N, int WHERE>
 __device__ __forceinline__ float chunk(const uint8_t* ent, int64_t start, int n, int k0,
                                        const float* x, float s) {
   int i[N];
@@ -269,31 +285,31 @@ __device__ __forceinline__ float chunk(const uint8_t* ent, int64_t start, int n,
   }
 #pragma unroll
   for (int j = 0; j < N; j++) {
-    i[j] &= MAXH - 1;
+    i[j] &= OFF_MASK;
     w[j] = k0 + j < n ? w[j] : 0.0f;
   }
 #pragma unroll
-  for (int j = 0; j < N; j++) xv[j] = x[i[j]];
+  for (int j = 0; j < N; j++) xv[j] = at_b(x, i[j]);
 #pragma unroll
-  for (int j = 0; j < N; j++) s = s + xv[j] * w[j];
+  for (int j = 0; j < N; j++) s = acc<BF>(s, xv[j], w[j]);
   return s;
 }
-template <bool E4, int N, int WHERE>
+template <bool BF, bool E4, int N, int WHERE>
 __device__ __forceinline__ float rest(const uint8_t* ent, int64_t start, int n, const float* x,
                                       float s) {
-  for (int k0 = N; k0 < n; k0 += N) s = chunk<E4, N, WHERE>(ent, start, n, k0, x, s);
+  for (int k0 = N; k0 < n; k0 += N) s = chunk<BF, E4, N, WHERE>(ent, start, n, k0, x, s);
   return s;
 }
-template <bool E4, int N, int WHERE>
+template <bool BF, bool E4, int N, int WHERE>
 __device__ __forceinline__ float dot(const uint8_t* ent, int64_t start, int n, const float* x) {
-  return rest<E4, N, WHERE>(ent, start, n, x, chunk<E4, N, WHERE>(ent, start, n, 0, x, 0.0f));
+  return rest<BF, E4, N, WHERE>(ent, start, n, x, chunk<BF, E4, N, WHERE>(ent, start, n, 0, x, 0.0f));
 }
 // R rows at once (chunk's rules): the first N entries of every row, then N more of every row
 // while any row of this thread has more. Each round loads all rows' entries, then all their x
 // values, so a round is two LDS round trips. Entry reads run up to the longest row's length
 // past a shorter row's start: the tables sit inside the 64 KB hot region, followed by other
 // LDS arrays.
-template <bool E4, int N, int R>
+template <bool BF, bool E4, int N, int R>
 __device__ __forceinline__ void dots_round(const uint8_t* ent, const int (&st)[R],
                                            const int (&n)[R], int k0, const float* x,
                                            float (&s)[R]) {
@@ -307,19 +323,19 @@ __device__ __forceinline__ void dots_round(const uint8_t* ent, const int (&st)[R
   for (int r = 0; r < R; r++)
 #pragma unroll
     for (int j = 0; j < N; j++) {
-      i[r][j] &= MAXH - 1;
+      i[r][j] &= OFF_MASK;
       w[r][j] = k0 + j < n[r] ? w[r][j] : 0.0f;
     }
 #pragma unroll
   for (int r = 0; r < R; r++)
 #pragma unroll
-    for (int j = 0; j < N; j++) xv[r][j] = x[i[r][j]];
+    for (int j = 0; j < N; j++) xv[r][j] = at_b(x, i[r][j]);
 #pragma unroll
   for (int r = 0; r < R; r++)
 #pragma unroll
-    for (int j = 0; j < N; j++) s[r] = s[r] + xv[r][j] * w[r][j];
+    for (int j = 0; j < N; j++) s[r] = acc<BF>(s[r], xv[r][j], w[r][j]);
 }
-template <bool E4, int N, int R>
+template <bool BF, bool E4, int N, int R>
 __device__ __forceinline__ void dots(const uint8_t* ent, const int (&st)[R], const int (&n)[R],
                                      const float* x, float (&s)[R]) {
   int m = 0;
@@ -328,8 +344,8 @@ __device__ __forceinline__ void dots(const uint8_t* ent, const int (&st)[R], con
     s[r] = 0.0f;
     m = n[r] > m ? n[r] : m;
   }
-  dots_round<E4, N, R>(ent, st, n, 0, x, s);
-  for (int k0 = N; k0 < m; k0 += N) dots_round<E4, N, R>(ent, st, n, k0, x, s);
+  dots_round<BF, E4, N, R>(ent, st, n, 0, x, s);
+  for (int k0 = N; k0 < m; k0 += N) dots_round<BF, E4, N, R>(ent, st, n, k0, x, s);
 }
 
 // A wave's tree sum: lane 0 ends with the sum that __shfl_down at offsets 32, 16, ..., 1
@@ -447,16 +463,17 @@ __device__ __forceinline__ float rdot(const uint8_t* ent, int64_t start, int n, 
 #pragma unroll
     for (int j = 0; j < 4; j++) {
       Ent<E4>::gat(ent, start + k0 + j, i[j], w[j]);
-      i[j] &= MAXH - 1;
-      w[j] = k0 + j < n ? w[j] : 0.0f;
+      i[j] &= OFF_MASK;
     }
 #pragma unroll
     for (int j = 0; j < 4; j++) {
-      hv[j] = ld_rlxf(hs + i[j]);
-      wi[j] = w1_one<E4, true>(w1in, i[j]);
+      hv[j] = ld_rlxf(reinterpret_cast<const float*>(reinterpret_cast<const uint8_t*>(hs) + i[j]));
+      wi[j] = w1_one<E4, true>(w1in, i[j] >> 2);
     }
+    // (a slot past the row may name a column past the weights: its term is dropped, not
+    // weighted by 0)
 #pragma unroll
-    for (int j = 0; j < 4; j++) s = s + rd<BF>((hv[j] * r) * wi[j]) * w[j];
+    for (int j = 0; j < 4; j++) s = k0 + j < n ? acc<BF>(s, rd<BF>((hv[j] * r) * wi[j]), w[j]) : s;
   }
   return s;
 }
@@ -543,7 +560,8 @@ __device__ __forceinline__ float swiglu(float gs, float us) {
   return rd<BF>(rd<BF>(sg) * up);
 }
 
-// The MLP's gate and up rows of every unit: act[u]. Two units a thread, their first chunks
+// The MLP's gate and up rows of every unit: act[u]. Units 2t and 2t + 1 on thread t (the packer
+// orders units by row length, so a wave's rows are about equally long), their rows' rounds
 // issued together.
 template <bool BF, bool E4>
 __device__ __forceinline__ void mlp_units(const lxm_hot& hd, const uint8_t* hot) {
@@ -552,8 +570,8 @@ __device__ __forceinline__ void mlp_units(const lxm_hot& hd, const uint8_t* hot)
   float* act = LF(L_ACT);
   const uint32_t* um = reinterpret_cast<const uint32_t*>(hot + hd.unit);
   const uint8_t* gu = hot + hd.gu_ent;
-  for (int u = t; u < hd.n_units; u += 2 * NT) {
-    const int u2 = u + NT;
+  for (int u = 2 * t; u < hd.n_units; u += 2 * NT) {
+    const int u2 = u + 1;
     const bool two = u2 < hd.n_units;
     const uint32_t m1 = um[u], m2 = um[two ? u2 : u];
     const int s1 = (int)(m1 & 0xffffu), g1 = (int)((m1 >> 16) & 255), n1 = (int)(m1 >> 24);
@@ -561,7 +579,7 @@ __device__ __forceinline__ void mlp_units(const lxm_hot& hd, const uint8_t* hot)
     const int g2 = two ? (int)((m2 >> 16) & 255) : 0, n2 = two ? (int)(m2 >> 24) : 0;
     const int st[4] = {s1, s1 + g1, s2, s2 + g2}, n[4] = {g1, n1, g2, n2};
     float v[4];
-    dots<E4, 4, 4>(gu, st, n, xm, v);
+    dots<BF, E4, 4, 4>(gu, st, n, xm, v);
     act[u] = swiglu<BF>(v[0], v[1]);
     if (two) act[u2] = swiglu<BF>(v[2], v[3]);
   }
@@ -573,9 +591,10 @@ __device__ __forceinline__ void mlp_units(const lxm_hot& hd, const uint8_t* hot)
 // directly. Items run on the threads from the top down (the units take them from the bottom
 // up).
 // a gate row's dot product with the GDN norm's output D((h * r) * (1 + w_in)), formed per entry
+// (w1e: the norm weight at each entry's column); slots past the row add nothing
 template <bool BF, bool E4>
 __device__ __forceinline__ float ndot(const uint8_t* ent, int start, int n, float r,
-                                      const uint8_t* w1in) {
+                                      const uint8_t* w1e) {
   const float* h = LF(L_H);
   float s = 0.0f;
   for (int k0 = 0; k0 < n; k0 += 4) {
@@ -584,13 +603,13 @@ __device__ __forceinline__ float ndot(const uint8_t* ent, int start, int n, floa
 #pragma unroll
     for (int j = 0; j < 4; j++) {
       Ent<E4>::at(ent, start + k0 + j, i[j], w[j]);
-      i[j] &= MAXH - 1;
-      w[j] = k0 + j < n ? w[j] : 0.0f;
+      i[j] &= OFF_MASK;
     }
 #pragma unroll
-    for (int j = 0; j < 4; j++) xv[j] = rd<BF>((h[i[j]] * r) * w1_one<E4, false>(w1in, i[j]));
+    for (int j = 0; j < 4; j++)
+      xv[j] = rd<BF>((at_b(h, i[j]) * r) * w1_one<E4, false>(w1e, start + k0 + j));
 #pragma unroll
-    for (int j = 0; j < 4; j++) s = s + xv[j] * w[j];
+    for (int j = 0; j < 4; j++) s = k0 + j < n ? acc<BF>(s, xv[j], w[j]) : s;
   }
   return s;
 }
@@ -599,7 +618,7 @@ template <bool BF, bool E4>
 __device__ __forceinline__ void gates(const lxm_params& p, const lxm_hot& hd, const uint8_t* hot,
                                       float r) {
   const int tt = NT - 1 - (int)threadIdx.x;
-  const uint8_t* w1in = hot + hd.w1_in;
+  const uint8_t* w1in = hot + hd.ent_w1;
   float* hist = LF(L_HIST);
   float* qkcur = LF(L_QKCUR);
   float* ev = LF(L_EV);
@@ -653,22 +672,16 @@ __device__ __forceinline__ void gates(const lxm_params& p, const lxm_hot& hd, co
 // MLP's input D((h * r) * (1 + w)) (:729-734) for every row; with gdn, h and r to the ring (the
 // GDN norm's output, the same expression with its own weights, is formed where it is read).
 // Rows past H compute from +0 and weight 1; nothing reads them.
-// four norm weights 1 + w of rows c..c+3 (c a multiple of 4); rows >= H get 1
+// four norm weights 1 + w of rows c..c+3 (c a multiple of 4; the table covers MAXH rows)
 template <bool E4>
-__device__ __forceinline__ v4f w1x4(const uint8_t* hot, int off, int c, int H) {
-  v4f w;
+__device__ __forceinline__ v4f w1x4(const uint8_t* hot, int off, int c) {
   if constexpr (E4) {
     typedef uint16_t v4h __attribute__((ext_vector_type(4)));
     const v4h b = reinterpret_cast<const v4h*>(hot + off)[c >> 2];
-    w = v4f{1.0f + bf16f(b.x), 1.0f + bf16f(b.y), 1.0f + bf16f(b.z), 1.0f + bf16f(b.w)};
+    return v4f{1.0f + bf16f(b.x), 1.0f + bf16f(b.y), 1.0f + bf16f(b.z), 1.0f + bf16f(b.w)};
   } else {
-    w = reinterpret_cast<const v4f*>(hot + off)[c >> 2];
+    return reinterpret_cast<const v4f*>(hot + off)[c >> 2];
   }
-  w.x = c < H ? w.x : 1.0f;
-  w.y = c + 1 < H ? w.y : 1.0f;
-  w.z = c + 2 < H ? w.z : 1.0f;
-  w.w = c + 3 < H ? w.w : 1.0f;
-  return w;
 }
 template <bool BF>
 __device__ __forceinline__ v4f norm4(const v4f& h, float r, const v4f& w) {
@@ -683,7 +696,7 @@ __device__ __forceinline__ void norms(const lxm_params& p, const lxm_hot& hd, co
   v4f* xm4 = reinterpret_cast<v4f*>(smem + L_XM);
   const int c0 = 4 * t, c1 = 2048 + 4 * t;
   const v4f ha = h4[t], hb = h4[NT + t];
-  const v4f pa = w1x4<E4>(hot, hd.w1_post, c0, H), pb = w1x4<E4>(hot, hd.w1_post, c1, H);
+  const v4f pa = w1x4<E4>(hot, hd.w1_post, c0), pb = w1x4<E4>(hot, hd.w1_post, c1);
   xm4[t] = norm4<BF>(ha, r, pa);
   xm4[NT + t] = norm4<BF>(hb, r, pb);
   if (gdn) {
@@ -805,7 +818,7 @@ __device__ __forceinline__ bool layer(const lxm_params& p, int L, int step, floa
                       pb4.y - pb4.x, pb4.z - pb4.y, pb4.w - pb4.z, eb - pb4.w};
     const v4f ha = h4[t], hb = h4[NT + t];
     float d[8];
-    dots<E4, 2, 8>(de, st, n, act, d);
+    dots<BF, E4, 2, 8>(de, st, n, act, d);
     const v4f na = v4f{rd<BF>(ha.x + rd<BF>(d[0])), rd<BF>(ha.y + rd<BF>(d[1])),
                        rd<BF>(ha.z + rd<BF>(d[2])), rd<BF>(ha.w + rd<BF>(d[3]))};
     const v4f nb = v4f{rd<BF>(hb.x + rd<BF>(d[4])), rd<BF>(hb.y + rd<BF>(d[5])),
@@ -868,7 +881,7 @@ __device__ void run_chain(const lxm_params& p) {
         int col;
         float w;
         Ent<E4>::gat(reinterpret_cast<const uint8_t*>(p.emb_ent), e, col, w);
-        h[col] = w;
+        *reinterpret_cast<float*>(reinterpret_cast<uint8_t*>(h) + (col & OFF_MASK)) = w;
       }
     }
     lds_barrier();
@@ -958,7 +971,7 @@ __device__ void head_rows(const lxm_params& p, int step, const int32_t* lptr, co
   __syncthreads();
   unsigned long long best = 0;
   for (int k = t; k < nr; k += NT) {
-    const float v = rd<BF>(dot<E4, 4, 0>(lent, lptr[k], lptr[k + 1] - lptr[k], hn));
+    const float v = rd<BF>(dot<BF, E4, 4, 0>(lent, lptr[k], lptr[k + 1] - lptr[k], hn));
     const unsigned long long key = argmax_key(v, r0 + k);
     best = key > best ? key : best;
   }
@@ -1043,7 +1056,7 @@ __device__ void gdn_head(const lxm_params& p, int L, int step, int vh, bool out,
   // conv state before this launch), the in_proj_z rows and beta = sigmoid(b) (:497)
   if (live) {
     const uint8_t* qent = p.blob + ly.qkv_ent;
-    const uint8_t* w1in = hot + hd.w1_in;
+    const uint8_t* w1in = p.blob + ly.w1_in;
     const float* h0 = ring_at(p, step, L);
     const float r0 = ld_rlxf(rr_at(p, step, L));
     if (t < VD) {
@@ -1218,7 +1231,7 @@ __device__ void out_rows(const lxm_params& p, int L, int ra, int rb, uint8_t* hx
         x[j] = oy[a + k0 + j];
       }
 #pragma unroll
-      for (int j = 0; j < 4; j++) s = s + x[j] * w[j];
+      for (int j = 0; j < 4; j++) s = acc<BF>(s, x[j], w[j]);
     }
     st_rlxf(p.xo + ra + t, rd<BF>(s));
   }
@@ -1230,12 +1243,14 @@ __device__ void run_helper(const lxm_params& p) {
   const int t = threadIdx.x, H = p.hidden, b = blockIdx.x, nh = p.n_blocks - 1;
   const int r0 = p.head_rows[b], r1 = p.head_rows[b + 1], nr = r1 - r0;
   const int64_t e0 = p.head_ptr[r0], ne = p.head_ptr[r1] - e0;
-  int32_t* lptr = reinterpret_cast<int32_t*>(lds);
-  uint8_t* lent = lds + (((size_t)(nr + 1) * 4 + 15) & ~(size_t)15);
-  uint8_t* hx = lds + p.head_lds;
+  // the scratch regions first (constant offsets: the head's normed input at 0), the head
+  // tables after them
+  uint8_t* hx = lds;
+  int32_t* lptr = reinterpret_cast<int32_t*>(lds + HX_END);
+  uint8_t* lent = lds + HX_END + (((size_t)(nr + 1) * 4 + 15) & ~(size_t)15);
   int* misc = reinterpret_cast<int*>(hx + HX_MISC);
   // every LDS word starts finite (zero): gathers may read slots no table names
-  for (int k = t; k < (p.head_lds + HX_END) / 16; k += NT)
+  for (int k = t; k < (HX_END + p.head_lds + 256) / 16; k += NT)
     reinterpret_cast<v4u*>(lds)[k] = v4u{0, 0, 0, 0};
   __syncthreads();
   for (int k = t; k <= nr; k += NT) lptr[k] = (int32_t)(p.head_ptr[r0 + k] - e0);
@@ -1330,7 +1345,7 @@ __device__ void write_windows(const lxm_params& p) {
       const int s = n - 4 + k;
       if (s >= 0) {
         // the channel's projection of step s's GDN norm output, formed per entry from the ring
-        const uint8_t* w1in = p.blob + ly.hot + ldg(reinterpret_cast<const lxm_hot*>(p.blob + ly.hot)).w1_in;
+        const uint8_t* w1in = p.blob + ly.w1_in;
         w[k] = rd<BF>(rdot<BF, E4>(p.blob + ly.qkv_ent, ch.start, ch.len, ring_at(p, s, L),
                                    ld_rlxf(rr_at(p, s, L)), w1in));
       } else {
@@ -1396,7 +1411,7 @@ extern "C" {
 
 int lxm_lds_base(void) { return L_CHAIN_END; }
 
-int lxm_helper_lds(int head_lds) { return head_lds + HX_END; }
+int lxm_helper_lds(int head_lds) { return HX_END + head_lds + 256; }  // (reads past the tables)
 
 int lxm_run(const lxm_params* p_host, const lxm_params* p_dev, int n_blocks, int lds_bytes,
             void* stream) {

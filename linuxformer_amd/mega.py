@@ -30,7 +30,7 @@ I32, I64, F32, PTR = ctypes.c_int32, ctypes.c_int64, ctypes.c_float, ctypes.c_vo
 
 
 class Hot(ctypes.Structure):
-    _fields_ = [(n, I32) for n in ("n_units", "n_qk", "n_dec", "qk_base", "w1_in", "w1_post",
+    _fields_ = [(n, I32) for n in ("n_units", "n_qk", "n_dec", "qk_base", "ent_w1", "w1_post",
                                    "unit", "gu_ent", "down_ptr", "down_ent", "qk", "dec", "ent",
                                    "size")] + [("eps", F32), ("geps", F32)]
 
@@ -50,7 +50,7 @@ class Chan(ctypes.Structure):
 
 class LayerDesc(ctypes.Structure):
     _fields_ = [(n, I64) for n in ("hot", "chan", "qkv_ent", "b_row", "b_ent", "z_row", "z_ent",
-                                   "out_ptr", "out_ent", "gnorm")]
+                                   "out_ptr", "out_ent", "gnorm", "w1_in")]
 
 
 class Params(ctypes.Structure):
@@ -66,7 +66,7 @@ class Params(ctypes.Structure):
 
 
 assert ctypes.sizeof(Hot) == 64 and ctypes.sizeof(QkC) == 32 and ctypes.sizeof(Dec) == 32
-assert ctypes.sizeof(Chan) == 24 and ctypes.sizeof(LayerDesc) == 80
+assert ctypes.sizeof(Chan) == 24 and ctypes.sizeof(LayerDesc) == 88
 
 
 def _bf16_bits(v: np.ndarray) -> np.ndarray:
@@ -134,9 +134,11 @@ class Packer:
     def __init__(self, e4: bool):
         self.bf16 = e4
 
-    def ent(self, idx: np.ndarray, vals: np.ndarray) -> bytes:
-        """Entries: e4 one uint32 (index | bf16 << 16), else two uint32 (index, float)."""
-        idx = np.asarray(idx, np.int64)
+    def ent(self, idx: np.ndarray, vals: np.ndarray, scale: int = 4) -> bytes:
+        """Entries: e4 one uint32 (index | bf16 << 16), else two uint32 (index, float). The index
+        is stored times ``scale``: 4 (a byte offset into the float vector the row is applied to,
+        which the kernel adds to the vector's base) for every table but out_proj's."""
+        idx = np.asarray(idx, np.int64) * scale
         if self.bf16:
             assert len(idx) == 0 or idx.max() < 1 << 16
             return (idx.astype(np.uint32) | (_bf16_bits(vals) << 16)).astype(np.uint32).tobytes()
@@ -197,6 +199,7 @@ class Mega:
         H, R, C = d.hidden, d.nv // d.nk, d.n_conv
         qk_total = 0
         self.stats = {"layers": d.n_layers, "hot_bytes": [], "units": [], "qk": [], "dec": []}
+        self.unit_order = []  # per layer: the model's unit index of each packed unit
         for L, ly in enumerate(sm.layers):
             # ---- live MLP units (gate row, up row and down column nonzero; lx/lx/fast.py:242-248)
             g, u, dn = _Csr(ly.gate_proj), _Csr(ly.up_proj), _Csr(ly.down_proj.transpose())
@@ -205,6 +208,11 @@ class Mega:
             dc = np.diff(dn.ptr)
             units = np.nonzero((gc > 0) & (uc > 0) & (dc > 0))[0]
             assert len(units) <= MAXU, f"layer {L}: {len(units)} live MLP units > {MAXU}"
+            # by row length, longest first (stable): a wave's units have rows of about one length,
+            # so the kernel's 4-entry rounds over a thread's rows rarely run for a few long ones,
+            # and the shortest rows share the top wave with the gates
+            units = units[np.argsort(-np.maximum(gc[units], uc[units]), kind="stable")]
+            self.unit_order.append(units)
             uidx = np.full(d.inter, -1, np.int64)
             uidx[units] = np.arange(len(units))
             gu_parts, meta, pos = [], [], 0
@@ -217,11 +225,12 @@ class Mega:
                 gu_parts.append(pk.ent(c2, v2))
                 pos += len(c1) + len(c2)
             assert pos < 1 << 16
-            # down_proj by residual row over the live units (ascending unit order)
+            # down_proj by residual row over the live units, in the model's unit order (the sum's
+            # order), each entry naming the unit's packed index
             dcoo = ly.down_proj
             keep = uidx[dcoo.cols] >= 0
             drows, dunits, dvals = dcoo.rows[keep], uidx[dcoo.cols[keep]], dcoo.vals[keep]
-            order = np.lexsort((dunits, drows))
+            order = np.lexsort((dcoo.cols[keep], drows))
             drows, dunits, dvals = drows[order], dunits[order], dvals[order]
             dptr = np.zeros(H + 1, np.int64)
             np.cumsum(np.bincount(drows, minlength=H), out=dptr[1:])
@@ -229,8 +238,9 @@ class Mega:
             # ---- the gates: live query/key channels (nonzero conv taps) and decaying heads
             qkv = _Csr(ly.in_proj_qkv)
             taps = np.asarray(ly.conv1d, np.float32)
-            ent_parts, epos = [], 0
+            ent_parts, ent_w1, epos = [], [], 0
             qks = []
+            w1in = np.asarray(ly.input_layernorm, np.float32)
             for c in np.nonzero((taps[:2 * d.nk * KD] != 0).any(1))[0]:
                 kh, rem = divmod(int(c) % (d.nk * KD), KD)
                 isk = int(c) >= d.nk * KD
@@ -240,6 +250,7 @@ class Mega:
                 q.taps[:] = [float(x) for x in taps[c]]
                 qks.append(q)
                 ent_parts.append(pk.ent(cols, vals))
+                ent_w1.append(w1in[cols])
                 epos += len(cols)
             assert len(qks) <= MAXQKL, f"layer {L}: {len(qks)} live query/key channels"
             acsr = _Csr(ly.in_proj_a)
@@ -252,13 +263,16 @@ class Mega:
                 decs.append(Dec(vh=vh, start=epos, len=len(cols), dt_bias=float(ly.dt_bias[vh]),
                                 A_log=float(ly.A_log[vh])))
                 ent_parts.append(pk.ent(cols, vals))
+                ent_w1.append(w1in[cols])
                 epos += len(cols)
             assert len(decs) <= MAXDEC
             # ---- the hot blob
             hb = _Blob()
             hb.add(bytes(64))
-            o_w1in = hb.add(pk.w1(ly.input_layernorm))
-            o_w1post = hb.add(pk.w1(ly.post_attention_layernorm))
+            # the MLP norm's weights, padded with 0 (1 + w = 1) to MAXH rows
+            wpost = np.zeros(MAXH, np.float32)
+            wpost[:H] = ly.post_attention_layernorm
+            o_w1post = hb.add(pk.w1(wpost))
             o_unit = hb.add(np.asarray(meta, np.uint32).tobytes())
             o_gu = hb.add(b"".join(gu_parts))
             # padded to MAXH + 8 rows (the kernel reads four rows' pointers at once)
@@ -269,8 +283,10 @@ class Mega:
             o_qk = hb.add(b"".join(bytes(q) for q in qks))
             o_dec = hb.add(b"".join(bytes(x) for x in decs))
             o_ent = hb.add(b"".join(ent_parts))
+            # the GDN norm's weight at each of those entries' columns
+            o_entw = hb.add(pk.w1(np.concatenate(ent_w1)) if ent_w1 else b"")
             hot = Hot(n_units=len(units), n_qk=len(qks), n_dec=len(decs), qk_base=qk_total,
-                      w1_in=o_w1in, w1_post=o_w1post, unit=o_unit, gu_ent=o_gu, down_ptr=o_dptr,
+                      ent_w1=o_entw, w1_post=o_w1post, unit=o_unit, gu_ent=o_gu, down_ptr=o_dptr,
                       down_ent=o_dent, qk=o_qk, dec=o_dec, ent=o_ent, size=hb.n,
                       eps=d.rms_eps, geps=d.geps)
             hb.parts[0] = bytes(hot)
@@ -300,8 +316,9 @@ class Mega:
                 n_e = int(optr[min(r0 + rp, H)] - optr[r0])
                 assert n_e <= OUT_MAX, f"layer {L}: {n_e} out_proj entries in {rp} rows > {OUT_MAX}"
             desc.out_ptr = blob.add(optr.astype(np.int32).tobytes())
-            desc.out_ent = blob.add(pk.ent(oc.cols, oc.vals))
+            desc.out_ent = blob.add(pk.ent(oc.cols, oc.vals, scale=1))
             desc.gnorm = blob.add(np.asarray(ly.norm, np.float32).tobytes())
+            desc.w1_in = blob.add(pk.w1(ly.input_layernorm))
             self.stats["hot_bytes"].append(hb.n)
             self.stats["units"].append(len(units))
             self.stats["qk"].append(len(qks))

@@ -70,7 +70,7 @@ class _FakeLib:
         return 163_840
 
     def lxm_helper_lds(self, head_lds):
-        return head_lds + 43_600
+        return head_lds + 43_856
 
     def lxm_max_blocks(self, lds):
         return 256
@@ -86,9 +86,11 @@ def packed(monkeypatch):
     return make
 
 
-def _ent(blob: bytes, off: int, i: int):
+def _ent(blob: bytes, off: int, i: int, scale: int = 4):
+    """A packed e4 entry: (index, value); gather tables store the index as a byte offset."""
     w = int.from_bytes(blob[off + 4 * i:off + 4 * i + 4], "little")
-    return w & 0xffff, np.uint32((w >> 16) << 16).view(np.float32)
+    assert (w & 0xffff) % scale == 0
+    return (w & 0xffff) // scale, np.uint32((w >> 16) << 16).view(np.float32)
 
 
 def test_packer_tables_decode_to_the_model(packed):
@@ -101,7 +103,8 @@ def test_packer_tables_decode_to_the_model(packed):
         base = descs[L].hot
         hot = mega.Hot.from_buffer_copy(blob[base:base + 64])
         assert hot.size <= mega.HOT_MAX
-        units = fast.Fast(m).dec[L]["units"]
+        units = mg.unit_order[L]  # the live units (lx/lx/fast.py:242-248), by row length
+        assert sorted(units.tolist()) == sorted(np.asarray(fast.Fast(m).dec[L]["units"]).tolist())
         assert hot.n_units == len(units)
         meta = np.frombuffer(blob[base + hot.unit:base + hot.unit + 4 * hot.n_units], np.uint32)
         for j, u in enumerate(units):
@@ -127,7 +130,7 @@ def test_packer_tables_decode_to_the_model(packed):
             sel = oc.rows == i
             order = np.argsort(oc.cols[sel], kind="stable")
             want = list(zip(oc.cols[sel][order].tolist(), oc.vals[sel][order].tolist()))
-            got = [_ent(blob, descs[L].out_ent, k) for k in range(optr[i], optr[i + 1])]
+            got = [_ent(blob, descs[L].out_ent, k, 1) for k in range(optr[i], optr[i + 1])]
             assert [(int(c), float(v)) for c, v in got] == want
     # head: rows x columns with a nonzero final weight
     hptr = mg.head_ptr.numpy()
