@@ -54,6 +54,19 @@ def survey_bytes_per_token(model, f_out: float) -> float:
     return tot
 
 
+def measured_traffic(config: str):
+    """HBM bytes per decoded token of the decode kernel, from the committed rocprofv3 counter
+    summary (profiles/pmc_lxm_decode_<config>.txt: FETCH_SIZE and WRITE_SIZE per dispatch,
+    each scaled by the same counter's reading for a plain copy of known size), or None."""
+    path = os.path.join(HERE, "profiles", f"pmc_lxm_decode_{config}.txt")
+    if not os.path.exists(path):
+        return None
+    for line in open(path):
+        if line.startswith("hbm_bytes_per_token:"):
+            return float(line.split(":", 1)[1])
+    return None
+
+
 def cpu_baseline(model, conv0, rec0, start: int, n: int):
     """The C oracle (a single-threaded port of the stock decode) on the first n tokens."""
     from oracle import oracle as ox
@@ -77,7 +90,7 @@ def main() -> int:
     ap.add_argument("--tokens", type=int, default=262_144)
     ap.add_argument("--warmup-tokens", type=int, default=4096)
     ap.add_argument("--config", default="c2", choices=["c1", "c2", "c5", "small"])
-    ap.add_argument("--cpu-tokens", type=int, default=128, help="CPU baseline sample (0: skip)")
+    ap.add_argument("--cpu-tokens", type=int, default=256, help="CPU baseline sample (0: skip)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: the decode is one sequential chain per stream and this "
@@ -136,6 +149,7 @@ def main() -> int:
     # roofline: SURVEY 8(d)'s algorithmic bytes per token x tokens per launch / launch time
     b_tok = survey_bytes_per_token(model, spec.p_gate)
     achieved = b_tok * args.tokens / (kern_ms * 1e-3) / 1e9
+    t_tok = measured_traffic(spec.name)
     out = {
         "metric": METRIC, "value": round(value, 1), "unit": "tok/s", "n_gpus": 1,
         "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(wall * 1e3 / args.steps, 3),
@@ -148,7 +162,8 @@ def main() -> int:
                    "density": spec.density, "parallelism": "single GPU (one chain workgroup + "
                    f"{mg.ncta - 1} head workgroups)"},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS,
-                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 5), "traffic": None,
+                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 5),
+                     "traffic": None if t_tok is None else round(t_tok * args.tokens),
                      "bytes_per_token": round(b_tok), "kernel_ms_per_launch": round(kern_ms, 3)},
     }
     if args.cpu_tokens > 0:

@@ -3,6 +3,8 @@
 // process rocprofv3 profiles.
 //
 //   lxm_runner <dump dir> <launches> [tokens per launch]
+//   lxm_runner --copy <MiB>     (one plain device copy kernel of that size: the calibration run
+//                                for the HBM byte counters FETCH_SIZE and WRITE_SIZE)
 //
 // The dump's manifest lists each lxm_params pointer field with the file holding its device
 // buffer ("buf"), a zeroed buffer size ("zero"), or a list of files whose device copies form a
@@ -50,7 +52,31 @@ static void* upload(const std::string& path, size_t* n = nullptr) {
   return d;
 }
 
+// a grid-stride copy of n 16-byte words
+__global__ void copy16(const uint4* __restrict__ src, uint4* __restrict__ dst, size_t n) {
+  for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x)
+    dst[i] = src[i];
+}
+
+static int copy_run(size_t mib) {
+  const size_t bytes = mib << 20, n = bytes / 16;
+  void *a = nullptr, *b = nullptr;
+  CK(hipMalloc(&a, bytes));
+  CK(hipMalloc(&b, bytes));
+  CK(hipMemset(a, 1, bytes));
+  CK(hipDeviceSynchronize());
+  hipLaunchKernelGGL(copy16, dim3(4096), dim3(256), 0, 0, (const uint4*)a, (uint4*)b, n);
+  CK(hipGetLastError());
+  CK(hipDeviceSynchronize());
+  printf("{\"copy_bytes_read\": %zu, \"copy_bytes_written\": %zu}\n", bytes, bytes);
+  fflush(stdout);
+  CK(hipFree(a));
+  CK(hipFree(b));
+  return 0;
+}
+
 int main(int argc, char** argv) {
+  if (argc == 3 && std::string(argv[1]) == "--copy") return copy_run((size_t)atol(argv[2]));
   if (argc < 3) {
     fprintf(stderr, "usage: %s <dump dir> <launches> [tokens]\n", argv[0]);
     return 2;

@@ -38,7 +38,9 @@ def build(verbose: bool = False) -> str:
     if verbose and r.stderr:
         print(r.stderr)
     os.replace(tmp, LIB)
-    r = subprocess.run([hipcc(), "-O2", "-std=c++17", "-o", RUNNER + ".tmp",
+    # the runner has a kernel of its own (the copy that calibrates the byte counters): gfx950
+    r = subprocess.run([hipcc(), "--offload-arch=gfx950", "-O2", "-std=c++17", "-Xclang",
+                        "-target-feature", "-Xclang", "-packed-fp32-ops", "-o", RUNNER + ".tmp",
                         os.path.join(CSRC, "lxm_runner.cpp"), "-ldl"], capture_output=True, text=True)
     if r.returncode != 0:
         raise RuntimeError(f"hipcc (runner) failed ({r.returncode}):\n{r.stderr[-4000:]}")
