@@ -359,6 +359,7 @@ class Mega:
         base = int(self.lib.lxm_lds_base())
         self.lds = max(base, int(self.lib.lxm_helper_lds(self.head_lds)))
         self.lds = (self.lds + 255) // 256 * 256
+        self.smem = self.lds  # lx.mega.Mega's name for the launch's dynamic shared memory
         maxlds = int(self.lib.lxm_max_lds())
         assert self.lds <= maxlds, (self.lds, maxlds)
         assert int(self.lib.lxm_max_blocks(self.lds)) >= self.ncta, "the grid is not co-resident"
