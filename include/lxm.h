@@ -29,40 +29,52 @@ extern "C" {
 #define LXM_MAXQK 1024      /* live query/key channels, all layers */
 #define LXM_MAXQKL 512      /* live query/key channels of one layer */
 #define LXM_MAXDEC 512      /* decaying value heads of one layer */
-#define LXM_HOT_MAX 65536   /* bytes of one layer's resident tables */
+#define LXM_GATE_MAX 65536  /* bytes of the gate section (resident in the chain's LDS) */
 #define LXM_NSYNC 1024      /* uint32 words of the sync area */
 #define LXM_OUT_MAX 1024    /* out_proj entries of the rows one helper workgroup computes */
 #define LXM_OUT_HELPERS 64  /* helper workgroups that compute out_proj's rows */
 #define LXM_OUT_ROWS 64     /* out_proj rows one of them computes, at most */
 
-/* One layer's resident tables (the "hot" blob the chain workgroup stages in LDS). All offsets
-   are bytes from the start of the hot blob, 16-byte aligned. */
-typedef struct lxm_hot {
-  int32_t n_units, n_qk, n_dec, qk_base; /* qk_base: the layer's first q/k history slot */
-  int32_t ent_w1;          /* the GDN norm's weight at each `ent` entry's column (format below) */
-  int32_t w1_post;         /* the MLP norm's weights, LXM_MAXH rows: e4 raw w (bf16 bits, uint16),
-                              else 1 + w (fp32); rows past hidden hold w = 0 */
-  int32_t unit;            /* uint32 per unit (units by row length): entry start (16 bits) |
-                              gate count (8) | up count (8) */
-  int32_t gu_ent;          /* gate then up entries of each unit (column) */
-  int32_t down_ptr;        /* uint16 per residual row + 1: down entries of the row */
-  int32_t down_ent;        /* entries (unit) */
+/* The chain workgroup's per-thread table of one layer (packed by linuxformer_amd/chain.py):
+   LXM_PT_WORDS x LXM_NT 16-byte words, word j of thread t at (j * LXM_NT + t) * 16, prefetched
+   into the thread's registers one layer ahead. Slots (uint32) in a fixed layout: the MLP norm's
+   weights of the thread's residual rows (4t..4t+3, 2048+4t..2048+4t+3), meta words, two unit
+   passes (gate/up entries interleaved) and down-row passes; see the kernel's PT<E4>. */
+#define LXM_PT_WORDS 16
+
+/* One layer's gate tables: the live query/key channels and the decaying value heads, and the
+   long units and rows of the chain's per-thread table (resident in the chain's LDS for a launch;
+   the helpers read the gate tables from global memory). Offsets are bytes
+   from the start of this header, 16-byte aligned. */
+typedef struct lxm_gate {
+  int32_t n_qk, n_dec, qk_base; /* qk_base: the layer's first q/k history slot */
   int32_t qk;              /* lxm_qkc[n_qk] */
   int32_t dec;             /* lxm_dec[n_dec] */
-  int32_t ent;             /* entries of the q/k and decay rows (column) */
+  int32_t ent;             /* entries of the q/k and decay rows (column byte offsets) */
+  int32_t ent_w1;          /* the GDN norm's weight at each entry's column (e4 bf16 bits,
+                              else 1 + w as fp32) */
   int32_t size;            /* bytes */
   float eps, geps;
-} lxm_hot;
+  int32_t long_u, long_r;  /* lxm_longu[n_long_u], lxm_longr[n_long_r] */
+  int32_t long_ent;        /* their entries */
+  int32_t n_long_u, n_long_r, pad;
+} lxm_gate;
+
+/* A unit too long for the chain's register passes: its rows' entries (column byte offsets into
+   the MLP norm's output) in the layer's long entries. */
+typedef struct lxm_longu { int32_t act, gs, gn, us, un, pad[3]; } lxm_longu;
+/* A residual row too long for the down passes: entries are unit byte offsets into act. */
+typedef struct lxm_longr { int32_t row, start, len, pad; } lxm_longr;
 
 typedef struct lxm_qkc {   /* a live query/key channel (its conv taps are not all zero) */
   int32_t slot;            /* key head * 512 + (0 query | 256 key) + position */
   int32_t chan;            /* conv channel */
-  int32_t start, len;      /* in_proj_qkv row: entries in the hot blob */
+  int32_t start, len;      /* in_proj_qkv row: entries in the gate tables */
   float taps[4];
 } lxm_qkc;
 
 typedef struct lxm_dec {   /* a value head whose decay can be nonzero */
-  int32_t vh, start, len;  /* in_proj_a row: entries in the hot blob */
+  int32_t vh, start, len;  /* in_proj_a row: entries in the gate tables */
   float dt_bias, A_log;
   int32_t pad[3];
 } lxm_dec;
@@ -76,7 +88,8 @@ typedef struct lxm_row { int32_t start, len; } lxm_row;
 
 /* One layer: byte offsets into the packed blob. */
 typedef struct lxm_layer {
-  int64_t hot;             /* lxm_hot + its tables, hot.size bytes */
+  int64_t ptt;             /* the chain's per-thread table */
+  int64_t gate;            /* lxm_gate + its tables (inside the gate section) */
   int64_t chan;            /* lxm_chan[n_conv] */
   int64_t qkv_ent;         /* entries (column) */
   int64_t b_row, b_ent;    /* lxm_row[nv], entries (column) */
@@ -91,9 +104,11 @@ typedef struct lxm_params {
   int32_t hidden, n_layers, nk, kd, nv, vd, n_conv, vocab, bf16, n_blocks;
   float rms_eps;
   int32_t head_lds;        /* bytes of head tables a helper workgroup stages */
-  int32_t e4, pad1;        /* the entry format (above) */
+  int32_t e4;              /* the entry format (above) */
+  int32_t gate_bytes;      /* bytes of the gate section (every layer's lxm_gate tables) */
   const lxm_layer* layers; /* device, n_layers */
   const uint8_t* blob;     /* device */
+  const uint8_t* gates;    /* device: the gate section, inside blob */
   float* const* rec;       /* device array of n_layers pointers: (nv, kd, vd) float */
   void* const* conv;       /* device array of n_layers pointers: (n_conv, 4) model dtype */
   const int64_t* emb_ptr;  /* (vocab + 1): the embedding rows (all columns) */
@@ -143,7 +158,8 @@ int lxm_last_error(void);
 int lxm_device_cus(void);
 
 /* Test exports (mk_test.cu:136-160's roles): the kernels' own arithmetic on device arrays.
-   fn: 0 exp, 1 silu, 2 sigmoid, 3 softplus, 4 rsqrt, 5 log1p, 6 bf16 rounding. */
+   fn: 0 exp, 1 silu, 2 sigmoid, 3 softplus, 4 rsqrt, 5 log1p, 6 bf16 rounding, 7 silu of the
+   input rounded to bf16, rounded to bf16 (the decode's fast path for bf16 models). */
 int lxm_t_elem(int fn, const float* x, float* y, long n, void* stream);
 /* kind 0: the 512-lane hidden sum, kind 1: the 64-lane head sum, of each of rows rows of n
    values (x row-major); out (rows). */

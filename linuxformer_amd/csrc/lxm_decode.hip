@@ -49,21 +49,28 @@ using namespace lxm;
 static_assert(MAXH == 8 * NT, "eight residual rows per thread cover any hidden size");
 
 // ---------------------------------------------------------------------------------------------
-// LDS layout of the chain workgroup (bytes)
-// (the vectors the sparse rows gather from sit below 64 KB, so a gather's base folds into the
-// ds_read's 16-bit offset)
-#define L_ACT 0
-#define L_XM (L_ACT + 4 * LXM_MAXU)
-#define L_H (L_XM + 4 * MAXH)
-#define L_HIST (L_H + 4 * MAXH)
+// LDS layout of the chain workgroup (bytes). The vectors rows gather from (act, xm, h) sit
+// below 64 KB, so a gather's base folds into the ds_read's 16-bit offset.
+#define L_ACT 0                       // float[MAXU]: the MLP units' outputs
+#define L_XM (L_ACT + 4 * LXM_MAXU)   // float[MAXH]: the MLP norm's output
+#define L_H (L_XM + 4 * MAXH)         // float[MAXH]: the residual (the gates gather from it)
+#define L_DSUM (L_H + 4 * MAXH)       // float[MAXH]: down_proj's row sums
+#define L_DUMMY (L_DSUM + 4 * MAXH)   // float[NT]: where a lane with no row in a pass writes
+#define L_HIST (L_DUMMY + 4 * NT)     // the live q/k channels' conv history, 3 per channel
 #define L_QKCUR (L_HIST + 4 * 3 * LXM_MAXQK)
 #define L_EV (L_QKCUR + 4 * LXM_MAXQKL)
-#define L_WSUM (L_EV + 4 * 256)
+#define L_WSUM (L_EV + 4 * 256)       // float[3][8]: wave totals of the hidden sums
 #define L_FLAGS (L_WSUM + 4 * 32)
 #define L_PROF (L_FLAGS + 4 * 256)
-#define L_LT (L_PROF + 8 * 32)
-#define L_HOT (L_LT + 16 * 64)
-#define L_CHAIN_END (L_HOT + LXM_HOT_MAX + 2048)  // (gathers read up to ~1 KB past a table)
+#define L_LT (L_PROF + 8 * 32)        // the layer table (LtEnt[64])
+#define L_PARAMS (L_LT + 16 * 64)     // the chain's copy of the parameter block
+#define L_GATES (L_PARAMS + 512)      // the gate section, resident for the launch
+#define L_SUBP (L_GATES + LXM_GATE_MAX + 64)  // (gate gathers read up to 4 entries past a row)
+#ifdef LXM_SUBPROF
+#define L_CHAIN_END (L_SUBP + 8 * (16 * SP_NS + 16))
+#else
+#define L_CHAIN_END L_SUBP
+#endif
 static_assert(L_H + 4 * MAXH <= 65536, "gathered vectors below 64 KB");
 // flags (int): [0] any head active, [1] any query live (the residual may change), [4] ok,
 // [8] token, [16 + kh] per key head: bit 0 query nonzero, bit 1 key nonzero, bit 2 a decay
@@ -158,16 +165,54 @@ __device__ __forceinline__ void lds_barrier() {
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
 }
 
+extern __shared__ __align__(16) uint8_t smem[];
+
 // In-kernel phase counters (lx/csrc/mega.cu's prof buffer and MK_SUBPROF checkpoints): with
 // p.prof set, thread 0 of the chain adds the shader-clock cycles of each phase into an LDS
-// slot; the slots are written to p.prof at the end. Phases: 0 embedding, 1 layer staging (and
-// the trace), 2 the norms (stage A), 3 the gates and the MLP units (stage B), 4 a GDN event
-// and the MLP's redo, 5 down_proj and the next norm's sums (stage C), 6 final norm + publish,
+// slot; the slots are written to p.prof at the end. Phases: 0 embedding, 1 the residual add
+// and the next norm's sums (stage C2, and the trace), 2 the norms (stage A), 3 the gates and
+// the MLP units (stage B), 4 a GDN event and the MLP's redo, 5 down_proj's rows (stage C1),
+// 6 final norm + publish,
 // 7 waiting for the head's argmax; counters 16 GDN events, 17 tokens. Helper b adds at
 // 32 + 4b: 0 waiting for events, 1 head rows, 2 its value head's delta rule, 3 out_proj rows
 // (with the wait for every head's output).
 #define PROF_ON (p.prof != nullptr)
 __device__ __forceinline__ uint64_t cycles() { return __builtin_readcyclecounter(); }
+
+// Sub-phase profile (built with -DLXM_SUBPROF, lx.mega's MK_SUBPROF): per wave of the chain and
+// per stage s (0 stage A, 1 stage B, 2 stage C1, 3 stage C2), the cycles the wave works before
+// the stage's closing barrier (busy) and the cycles it then waits in the barrier (wait). The
+// counters follow the helpers' in p.prof: [32 + 4 n_blocks + 16 s + w] busy, [.. + 8 + w] wait.
+// GDN events, the embedding and the head are outside every stage (their time is skipped).
+#define SP_NS 4
+#ifdef LXM_SUBPROF
+__device__ __forceinline__ uint64_t* sp_base() { return reinterpret_cast<uint64_t*>(smem + L_SUBP); }
+__device__ __forceinline__ void sp_arrive(int s) {
+  if ((threadIdx.x & 63) == 0) {
+    uint64_t* sp = sp_base();
+    const int w = threadIdx.x >> 6;
+    const uint64_t now = cycles();
+    sp[16 * s + w] += now - sp[16 * SP_NS + w];
+    sp[16 * SP_NS + 8 + w] = now;
+  }
+}
+__device__ __forceinline__ void sp_depart(int s) {
+  if ((threadIdx.x & 63) == 0) {
+    uint64_t* sp = sp_base();
+    const int w = threadIdx.x >> 6;
+    const uint64_t now = cycles();
+    sp[16 * s + 8 + w] += now - sp[16 * SP_NS + 8 + w];
+    sp[16 * SP_NS + w] = now;
+  }
+}
+__device__ __forceinline__ void sp_skip() {
+  if ((threadIdx.x & 63) == 0) sp_base()[16 * SP_NS + (threadIdx.x >> 6)] = cycles();
+}
+#else
+__device__ __forceinline__ void sp_arrive(int) {}
+__device__ __forceinline__ void sp_depart(int) {}
+__device__ __forceinline__ void sp_skip() {}
+#endif
 
 // spin (one thread) until the counter reaches target (modulo 2^32); false on timeout or
 // another block's error
@@ -304,50 +349,6 @@ template <bool BF, bool E4, int N, int WHERE>
 __device__ __forceinline__ float dot(const uint8_t* ent, int64_t start, int n, const float* x) {
   return rest<BF, E4, N, WHERE>(ent, start, n, x, chunk<BF, E4, N, WHERE>(ent, start, n, 0, x, 0.0f));
 }
-// R rows at once (chunk's rules): the first N entries of every row, then N more of every row
-// while any row of this thread has more. Each round loads all rows' entries, then all their x
-// values, so a round is two LDS round trips. Entry reads run up to the longest row's length
-// past a shorter row's start: the tables sit inside the 64 KB hot region, followed by other
-// LDS arrays.
-template <bool BF, bool E4, int N, int R>
-__device__ __forceinline__ void dots_round(const uint8_t* ent, const int (&st)[R],
-                                           const int (&n)[R], int k0, const float* x,
-                                           float (&s)[R]) {
-  int i[R][N];
-  float w[R][N], xv[R][N];
-#pragma unroll
-  for (int r = 0; r < R; r++)
-#pragma unroll
-    for (int j = 0; j < N; j++) Ent<E4>::at(ent, st[r] + k0 + j, i[r][j], w[r][j]);
-#pragma unroll
-  for (int r = 0; r < R; r++)
-#pragma unroll
-    for (int j = 0; j < N; j++) {
-      i[r][j] &= OFF_MASK;
-      w[r][j] = k0 + j < n[r] ? w[r][j] : 0.0f;
-    }
-#pragma unroll
-  for (int r = 0; r < R; r++)
-#pragma unroll
-    for (int j = 0; j < N; j++) xv[r][j] = at_b(x, i[r][j]);
-#pragma unroll
-  for (int r = 0; r < R; r++)
-#pragma unroll
-    for (int j = 0; j < N; j++) s[r] = acc<BF>(s[r], xv[r][j], w[r][j]);
-}
-template <bool BF, bool E4, int N, int R>
-__device__ __forceinline__ void dots(const uint8_t* ent, const int (&st)[R], const int (&n)[R],
-                                     const float* x, float (&s)[R]) {
-  int m = 0;
-#pragma unroll
-  for (int r = 0; r < R; r++) {
-    s[r] = 0.0f;
-    m = n[r] > m ? n[r] : m;
-  }
-  dots_round<BF, E4, N, R>(ent, st, n, 0, x, s);
-  for (int k0 = N; k0 < m; k0 += N) dots_round<BF, E4, N, R>(ent, st, n, k0, x, s);
-}
-
 // A wave's tree sum: lane 0 ends with the sum that __shfl_down at offsets 32, 16, ..., 1
 // leaves there (lane l adds lane l + off). Offsets 32 and 16 by gfx950's permlane swaps, 8..1
 // by DPP row shifts; no LDS round trips.
@@ -372,16 +373,20 @@ __device__ __forceinline__ float wave_tree(float s) {
 // in order), combined within each wave at offsets 32..1, the 8 wave totals at offsets 4, 2, 1.
 // All threads call; all get the sum. In two halves, so a caller can put LDS writes between
 // the halves' barriers (the second orders them).
-__device__ __forceinline__ void sum512_begin(float s, float* wsum) {
+__device__ __forceinline__ void sum512_begin(float s, float* wsum, int sp = -1) {
   s = wave_tree(s);
   if ((threadIdx.x & 63) == 0) wsum[threadIdx.x >> 6] = s;
+  if (sp >= 0) sp_arrive(sp);
   lds_barrier();
+  if (sp >= 0) sp_depart(sp);
 }
-__device__ __forceinline__ float sum512_end(const float* wsum) {
+__device__ __forceinline__ float sum512_end(const float* wsum, int sp = -1) {
   float w[NW];
 #pragma unroll
   for (int i = 0; i < NW; i++) w[i] = wsum[i];
+  if (sp >= 0) sp_arrive(sp);
   lds_barrier();
+  if (sp >= 0) sp_depart(sp);
 #pragma unroll
   for (int off = NW / 2; off >= 1; off >>= 1)
 #pragma unroll
@@ -401,16 +406,6 @@ __device__ __forceinline__ float sum64(float s) {
 }
 
 // ---------------------------------------------------------------------------------------------
-template <bool E4>
-__device__ __forceinline__ float w1_at(const uint8_t* hot, int off, int c) {
-  if constexpr (E4) {
-    const float w = bf16f(reinterpret_cast<const uint16_t*>(hot + off)[c]);
-    return 1.0f + w;
-  } else {
-    return reinterpret_cast<const float*>(hot + off)[c];
-  }
-}
-
 // a conv state value (model dtype) as float
 template <bool BF>
 __device__ __forceinline__ float conv_at(const void* cs, int64_t i) {
@@ -481,7 +476,6 @@ __device__ __forceinline__ float rdot(const uint8_t* ent, int64_t start, int n, 
 // ---------------------------------------------------------------------------------------------
 // The chain workgroup. Its LDS arrays are addressed from the dynamic shared array itself, so
 // every access is a ds_read/ds_write.
-extern __shared__ __align__(16) uint8_t smem[];
 #define LF(off) reinterpret_cast<float*>(smem + (off))
 #define LI(off) reinterpret_cast<int*>(smem + (off))
 
@@ -489,107 +483,320 @@ extern __shared__ __align__(16) uint8_t smem[];
 __device__ __forceinline__ float norm_r(float ss, int H, float eps) {
   return rsqrt_(ss / (float)H + eps);
 }
-// The residual rows of thread t: 4t..4t+3 and 2048+4t..2048+4t+3 (two 16-byte words of each
-// hidden-sized LDS array). Rows >= H hold +0, and +0 terms leave each lane's sum unchanged.
+// The residual rows of thread t: 4t..4t+3 and 2048+4t..2048+4t+3, held in the thread's registers
+// (ha, hb) and mirrored in LDS for the gates. Rows >= H hold +0, and +0 terms leave each lane's
+// sum unchanged.
+// (acc: s + x * x rounded once as the oracle's s + D32(x * x); for bf16 models x * x is exact)
+template <bool BF>
 __device__ __forceinline__ float sq_terms(const v4f& a, const v4f& b) {
   float s = 0.0f;
-  s = s + a.x * a.x;
-  s = s + a.y * a.y;
-  s = s + a.z * a.z;
-  s = s + a.w * a.w;
-  s = s + b.x * b.x;
-  s = s + b.y * b.y;
-  s = s + b.z * b.z;
-  s = s + b.w * b.w;
+  s = acc<BF>(s, a.x, a.x);
+  s = acc<BF>(s, a.y, a.y);
+  s = acc<BF>(s, a.z, a.z);
+  s = acc<BF>(s, a.w, a.w);
+  s = acc<BF>(s, b.x, b.x);
+  s = acc<BF>(s, b.y, b.y);
+  s = acc<BF>(s, b.z, b.z);
+  s = acc<BF>(s, b.w, b.w);
   return s;
 }
-__device__ __forceinline__ float hidden_ss() {
-  const v4f* h4 = reinterpret_cast<const v4f*>(smem + L_H);
-  const v4f a = h4[threadIdx.x], b = h4[NT + threadIdx.x];
-  return sum512(sq_terms(a, b), LF(L_WSUM));
+// the sum of squares of the residual, whole (two barriers; wave totals in buffer 2)
+template <bool BF>
+__device__ __forceinline__ float hidden_ss(const v4f& ha, const v4f& hb) {
+  return sum512(sq_terms<BF>(ha, hb), LF(L_WSUM) + 16);
+}
+// the second half of the sum of squares begun in stage C2 (buffer par; the buffers alternate
+// by layer, so no barrier is needed after the reads)
+__device__ __forceinline__ float sum512_take(const float* wsum) {
+  float w[NW];
+#pragma unroll
+  for (int i = 0; i < NW; i++) w[i] = wsum[i];
+#pragma unroll
+  for (int off = NW / 2; off >= 1; off >>= 1)
+#pragma unroll
+    for (int i = 0; i < off; i++) w[i] = w[i] + w[i + off];
+  return w[0];
 }
 
-// The layer table in LDS: each layer's hot blob address and its 16-byte words
+// The layer table in LDS: each layer's per-thread table and the offset of its gate tables in
+// the resident gate section
 struct LtEnt {
-  const uint8_t* hot;
-  int32_t n16, pad;
+  const uint8_t* ptt;
+  int32_t goff, pad;
 };
+// The parameters the chain reads at every layer, read once into registers (a read of the
+// parameter block, in LDS, would cost an LDS round trip per use)
+struct ChainK {
+  int H, nl, nk, nv, R;
+  float* ring;
+  float* rring;
+  bool prof;
+};
+__device__ __forceinline__ float* ring_k(const ChainK& k, int step, int L) {
+  return k.ring + ((size_t)(step & 3) * k.nl + L) * MAXH;
+}
+__device__ __forceinline__ float* rr_k(const ChainK& k, int step, int L) {
+  return k.rring + (size_t)(step & 3) * k.nl + L;
+}
+// bf16 rounding of two values by one conversion (v_cvt_pk_bf16_f32), widened back to f32
+typedef float v2f __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ v2f rd2(v2f v) {
+  typedef __bf16 bf2 __attribute__((ext_vector_type(2)));
+  const uint32_t u = __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf2));
+  return v2f{__uint_as_float(u << 16), __uint_as_float(u & 0xffff0000u)};
+}
+template <bool BF>
+__device__ __forceinline__ v4f rd4(v4f v) {
+  if constexpr (BF) {
+    const v2f a = rd2(v2f{v.x, v.y}), b = rd2(v2f{v.z, v.w});
+    return v4f{a.x, a.y, b.x, b.y};
+  }
+  return v;
+}
 
-// stage layer L's hot blob: global -> registers (fetch, one layer ahead) -> LDS (stage); eight
-// 16-byte words per thread, kept in named registers
-static_assert(LXM_HOT_MAX == 16 * NT * 8, "the prefetch holds 8 words per thread");
-typedef uint32_t v4u __attribute__((ext_vector_type(4)));
-struct Pf {
-  v4u w0, w1, w2, w3, w4, w5, w6, w7;
+// The per-thread table's slot layout (linuxformer_amd/chain.py packs it). ESZ slots per entry:
+// e4 one (byte offset | bf16 << 16), else two (byte offset, float bits). Three regions, in 16-byte
+// words, each prefetched into its own registers right after its last use in a layer, in the
+// order the next layer uses them: RA = w1 + meta A (stages A and B), RU = the unit passes (stage
+// B), RB = meta B + the down passes (stage C1).
+// meta A: +0 the P0 unit's act index (bits 0-11, valid bit 15) and the P1 unit's (16-27, valid
+// bit 31); +1 the lane's long unit (0-15, 0xffff = none); +2 (equal across the wave) G0 (0-3),
+// G1 (4-7), shared columns in P0 (8) and P1 (9), any long unit (10).
+// meta B: +0..+2 the down passes' rows, 16 bits each (0xffff = none); +3 the lane's long row
+// (0-15, 0xffff = none), the wave's down passes present (16-23) and any long row (24).
+template <bool E4>
+struct PT;
+template <>
+struct PT<true> {
+  static constexpr int ESZ = 1, W1 = 0, MA = 8, U0 = 12, U1 = 18, MB = 44, D = 48, WORDS = 16;
+  static constexpr int G0MAX = 3, G1MAX = 13, ND = 6;
+  __host__ __device__ static constexpr int dlen(int q) {
+    return q < 3 ? 1 : q == 3 ? 2 : q == 4 ? 4 : 6;
+  }
+  __host__ __device__ static constexpr int doff(int q) {
+    return q < 3 ? q : q == 3 ? 3 : q == 4 ? 5 : 9;
+  }
 };
-__device__ __forceinline__ Pf fetch(int L) {
-  const LtEnt le = reinterpret_cast<const LtEnt*>(smem + L_LT)[L];
-  const GAS v4u* src = gp(reinterpret_cast<const v4u*>(le.hot));
-  const int t = threadIdx.x, n16 = le.n16;
-  // words past the blob: a duplicate of word 0 (staged, never read as a table)
-#define PF_LD(k) src[t + (k) * NT < n16 ? t + (k) * NT : 0]
-  Pf r;
-  r.w0 = PF_LD(0);
-  r.w1 = PF_LD(1);
-  r.w2 = PF_LD(2);
-  r.w3 = PF_LD(3);
-  r.w4 = PF_LD(4);
-  r.w5 = PF_LD(5);
-  r.w6 = PF_LD(6);
-  r.w7 = PF_LD(7);
-#undef PF_LD
+template <>
+struct PT<false> {
+  static constexpr int ESZ = 2, W1 = 0, MA = 8, U0 = 12, U1 = 20, MB = 36, D = 40, WORDS = 13;
+  static constexpr int G0MAX = 2, G1MAX = 4, ND = 4;
+  __host__ __device__ static constexpr int dlen(int q) { return q < 2 ? 1 : 2; }
+  __host__ __device__ static constexpr int doff(int q) { return q < 2 ? q : q == 2 ? 2 : 4; }
+};
+static_assert(PT<false>::WORDS <= LXM_PT_WORDS && PT<true>::WORDS <= LXM_PT_WORDS, "words");
+
+typedef uint32_t v4u __attribute__((ext_vector_type(4)));
+// words A .. A + N - 1 of this thread's part of a per-thread table
+template <int A, int N>
+struct Words {
+  v4u w[N];
+  __device__ __forceinline__ uint32_t slot(int s) const { return w[(s >> 2) - A][s & 3]; }
+  // every word live up to here: the register allocator may not reuse a loaded word's unused
+  // slots before its consumer, which would make the next layer wait for the load in flight
+  __device__ __forceinline__ void keep() const {
+#pragma unroll
+    for (int k = 0; k < N; k++) asm volatile("" ::"v"(w[k]));
+  }
+};
+template <int A, int N>
+__device__ __forceinline__ Words<A, N> fetch_words(const uint8_t* ptt) {
+  const GAS v4u* src = gp(reinterpret_cast<const v4u*>(ptt)) + threadIdx.x;
+  Words<A, N> r;
+#pragma unroll
+  for (int k = 0; k < N; k++) r.w[k] = src[(A + k) * NT];
   return r;
 }
-__device__ __forceinline__ void stage(const Pf& r) {
-  v4u* dst = reinterpret_cast<v4u*>(smem + L_HOT) + threadIdx.x;
-  dst[0 * NT] = r.w0;
-  dst[1 * NT] = r.w1;
-  dst[2 * NT] = r.w2;
-  dst[3 * NT] = r.w3;
-  dst[4 * NT] = r.w4;
-  dst[5 * NT] = r.w5;
-  dst[6 * NT] = r.w6;
-  dst[7 * NT] = r.w7;
+template <bool E4>
+struct Regions {
+  using F = PT<E4>;
+  static constexpr int RAA = 0, RAN = F::U0 / 4, RUA = F::U0 / 4, RUN = F::MB / 4 - F::U0 / 4,
+                       RBA = F::MB / 4, RBN = F::WORDS - F::MB / 4;
+  static_assert(F::MA % 4 == 0 && F::U0 % 4 == 0 && F::MB % 4 == 0 && F::D == F::MB + 4, "words");
+  using RA = Words<RAA, RAN>;
+  using RU = Words<RUA, RUN>;
+  using RB = Words<RBA, RBN>;
+};
+// entry s of a region: its byte offset and weight
+template <bool E4, class W>
+__device__ __forceinline__ void ent_of(const W& r, int s, int& off, float& w) {
+  if constexpr (E4) {
+    const uint32_t e = r.slot(s);
+    off = (int)(e & 0xffffu);
+    w = __uint_as_float(e & 0xffff0000u);
+  } else {
+    off = (int)r.slot(s);
+    w = __uint_as_float(r.slot(s + 1));
+  }
+}
+#define ACT_MASK (4 * LXM_MAXU - 4)
+
+// the MLP norm's weights 1 + w of the thread's rows (fp32: the packer forms 1 + w as
+// (1.0 + weight.float()) does)
+template <bool E4>
+__device__ __forceinline__ void w1_of(const typename Regions<E4>::RA& r1, v4f& wa, v4f& wb) {
+  wa = __builtin_bit_cast(v4f, r1.w[0]);
+  wb = __builtin_bit_cast(v4f, r1.w[1]);
 }
 
 // silu and the MLP product for one unit (Qwen3_5MLP :715): D(D(silu(D(g))) * D(u))
 template <bool BF>
 __device__ __forceinline__ float swiglu(float gs, float us) {
   const float g = rd<BF>(gs), up = rd<BF>(us);
-  const float sg = g == 0.0f ? g : silu(g);  // silu(+-0) = +-0 / 2 = +-0
+  const float sg = g == 0.0f ? g : silu_rd<BF>(g);  // silu(+-0) = +-0 / 2 = +-0
   return rd<BF>(rd<BF>(sg) * up);
 }
 
-// The MLP's gate and up rows of every unit: act[u]. Units 2t and 2t + 1 on thread t (the packer
-// orders units by row length, so a wave's rows are about equally long), their rows' rounds
-// issued together.
+template <bool BF>
+__device__ __forceinline__ v4f norm4(const v4f& h, float r, const v4f& w) {
+  return rd4<BF>(v4f{(h.x * r) * w.x, (h.y * r) * w.y, (h.z * r) * w.z, (h.w * r) * w.w});
+}
+
+// Stage A: the MLP norm's input D((h * r) * (1 + w)) (transformers qwen3_5 :729-734) of the
+// thread's rows into xm, down_proj's row sums cleared, and with ring the layer input h and its
+// norm factor r to the ring (the GDN norm's output, the same expression with its own weights,
+// is formed where it is read). Rows past H compute from +0; nothing reads them.
 template <bool BF, bool E4>
-__device__ __forceinline__ void mlp_units(const lxm_hot& hd, const uint8_t* hot) {
+__device__ __forceinline__ void stage_a(const ChainK& k, const typename Regions<E4>::RA& r1,
+                                        const v4f& ha, const v4f& hb, float r, int L, int step,
+                                        bool ring) {
   const int t = threadIdx.x;
+  v4f wa, wb;
+  w1_of<E4>(r1, wa, wb);
+  v4f* xm4 = reinterpret_cast<v4f*>(smem + L_XM);
+  xm4[t] = norm4<BF>(ha, r, wa);
+  xm4[NT + t] = norm4<BF>(hb, r, wb);
+  v4f* d4 = reinterpret_cast<v4f*>(smem + L_DSUM);
+  d4[t] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+  d4[NT + t] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+  if (ring) {
+    float* rg = ring_k(k, step, L);
+    st4_rlx(rg, 4 * t, ha);
+    st4_rlx(rg, 2048 + 4 * t, hb);
+    if (t == 0) st_rlxf(rr_k(k, step, L), r);
+  }
+}
+
+// A unit pass: each lane's unit (gate row and up row, entries interleaved from slot base) over
+// xm, padded to the wave's G entries, then act[u] = swiglu. Gathers first, then the sums (each
+// row in entry order from +0; a padding entry adds +0).
+template <bool BF, bool E4, int GMAX, class RU>
+__device__ __forceinline__ float unit_pass(const RU& ru, int base, int G, bool shared) {
+  constexpr int ESZ = PT<E4>::ESZ;
   const float* xm = LF(L_XM);
+  float x[GMAX], y[GMAX];
+#pragma unroll
+  for (int j = 0; j < GMAX; j++) {
+    if (j < G) {
+      int o;
+      float w;
+      ent_of<E4>(ru, base + 2 * ESZ * j, o, w);
+      x[j] = at_b(xm, o & OFF_MASK);
+      if (!shared) {
+        ent_of<E4>(ru, base + 2 * ESZ * j + ESZ, o, w);
+        y[j] = at_b(xm, o & OFF_MASK);
+      } else {
+        y[j] = x[j];
+      }
+    }
+  }
+  float g = 0.0f, u = 0.0f;
+#pragma unroll
+  for (int j = 0; j < GMAX; j++) {
+    if (j < G) {
+      int o;
+      float wg, wu;
+      ent_of<E4>(ru, base + 2 * ESZ * j, o, wg);
+      ent_of<E4>(ru, base + 2 * ESZ * j + ESZ, o, wu);
+      g = acc<BF>(g, x[j], wg);
+      u = acc<BF>(u, y[j], wu);
+    }
+  }
+  return swiglu<BF>(g, u);
+}
+
+// Stage B's units: passes P0 and P1 of the thread, then its long unit (entries in global memory)
+template <bool BF, bool E4>
+__device__ __forceinline__ void units(const uint8_t* gt, const typename Regions<E4>::RA& r1,
+                                      const typename Regions<E4>::RU& ru) {
+  using F = PT<E4>;
+  const uint32_t m0 = r1.slot(F::MA + 0);
+  const uint32_t m2 = __builtin_amdgcn_readfirstlane(r1.slot(F::MA + 2));
   float* act = LF(L_ACT);
-  const uint32_t* um = reinterpret_cast<const uint32_t*>(hot + hd.unit);
-  const uint8_t* gu = hot + hd.gu_ent;
-  for (int u = 2 * t; u < hd.n_units; u += 2 * NT) {
-    const int u2 = u + 1;
-    const bool two = u2 < hd.n_units;
-    const uint32_t m1 = um[u], m2 = um[two ? u2 : u];
-    const int s1 = (int)(m1 & 0xffffu), g1 = (int)((m1 >> 16) & 255), n1 = (int)(m1 >> 24);
-    const int s2 = (int)(m2 & 0xffffu);
-    const int g2 = two ? (int)((m2 >> 16) & 255) : 0, n2 = two ? (int)(m2 >> 24) : 0;
-    const int st[4] = {s1, s1 + g1, s2, s2 + g2}, n[4] = {g1, n1, g2, n2};
-    float v[4];
-    dots<BF, E4, 4, 4>(gu, st, n, xm, v);
-    act[u] = swiglu<BF>(v[0], v[1]);
-    if (two) act[u2] = swiglu<BF>(v[2], v[3]);
+  const float a0 = unit_pass<BF, E4, F::G0MAX>(ru, F::U0, (int)(m2 & 15u), (m2 & 256u) != 0);
+  const float a1 = unit_pass<BF, E4, F::G1MAX>(ru, F::U1, (int)((m2 >> 4) & 15u), (m2 & 512u) != 0);
+  if (m0 & 0x8000u) act[m0 & 0xfffu] = a0;
+  if (m0 & 0x80000000u) act[(m0 >> 16) & 0xfffu] = a1;
+  ru.keep();
+  r1.keep();
+  if (m2 & 1024u) {
+    const uint32_t li = r1.slot(F::MA + 1) & 0xffffu;
+    if (li != 0xffffu) {  // a long unit: its rows from the layer's resident long tables
+      const lxm_gate& hd = *reinterpret_cast<const lxm_gate*>(gt);
+      const lxm_longu lu = reinterpret_cast<const lxm_longu*>(gt + hd.long_u)[li];
+      const float* xm = LF(L_XM);
+      const float g = dot<BF, E4, 4, 0>(gt + hd.long_ent, lu.gs, lu.gn, xm);
+      const float u = dot<BF, E4, 4, 0>(gt + hd.long_ent, lu.us, lu.un, xm);
+      act[lu.act] = swiglu<BF>(g, u);
+    }
+  }
+}
+
+// Stage C1: down_proj's rows, each lane one row per pass (entries in the model's unit order, from
+// +0), the sum to dsum[row]; then the lane's long row
+template <bool BF, bool E4>
+__device__ __forceinline__ void down_rows(const uint8_t* gt, const typename Regions<E4>::RB& rdw) {
+  using F = PT<E4>;
+  constexpr int ESZ = F::ESZ;
+  const int t = threadIdx.x;
+  const uint32_t mb3 = rdw.slot(F::MB + 3);
+  const uint32_t m2 = __builtin_amdgcn_readfirstlane(mb3);
+  const uint32_t mask = (m2 >> 16) & 255u;
+  const float* act = LF(L_ACT);
+  float x[F::ND][8];
+#pragma unroll
+  for (int q = 0; q < F::ND; q++) {
+    if (mask & (1u << q)) {
+#pragma unroll
+      for (int j = 0; j < F::dlen(q); j++) {
+        int o;
+        float w;
+        ent_of<E4>(rdw, F::D + ESZ * (F::doff(q) + j), o, w);
+        x[q][j] = at_b(act, o & ACT_MASK);
+      }
+    }
+  }
+#pragma unroll
+  for (int q = 0; q < F::ND; q++) {
+    if (mask & (1u << q)) {
+      float s = 0.0f;
+#pragma unroll
+      for (int j = 0; j < F::dlen(q); j++) {
+        int o;
+        float w;
+        ent_of<E4>(rdw, F::D + ESZ * (F::doff(q) + j), o, w);
+        s = acc<BF>(s, x[q][j], w);
+      }
+      const uint32_t row = (rdw.slot(F::MB + q / 2) >> (16 * (q & 1))) & 0xffffu;
+      const int addr = row != 0xffffu ? L_DSUM + 4 * (int)row : L_DUMMY + 4 * t;
+      *reinterpret_cast<float*>(smem + addr) = s;
+    }
+  }
+  rdw.keep();
+  if (m2 & (1u << 24)) {
+    const uint32_t li = mb3 & 0xffffu;
+    if (li != 0xffffu) {  // a long row: its entries from the layer's resident long tables
+      const lxm_gate& hd = *reinterpret_cast<const lxm_gate*>(gt);
+      const lxm_longr lr = reinterpret_cast<const lxm_longr*>(gt + hd.long_r)[li];
+      LF(L_DSUM)[lr.row] = dot<BF, E4, 4, 0>(gt + hd.long_ent, lr.start, lr.len, act);
+    }
   }
 }
 
 // The gates: the live query/key channels' projections, conv windows (history in LDS) and silu
 // (causal_conv1d_update :199-216), and the decays g = -exp(A_log) softplus(a + dt_bias) (:499).
 // Flags per key head: 1 query nonzero, 2 key nonzero, 4 a decay exp(g) != 1; F_ANY and F_OUT
-// directly. Items run on the threads from the top down (the units take them from the bottom
-// up).
+// directly. Items run on the threads from the top down.
 // a gate row's dot product with the GDN norm's output D((h * r) * (1 + w_in)), formed per entry
 // (w1e: the norm weight at each entry's column); slots past the row add nothing
 template <bool BF, bool E4>
@@ -615,16 +822,16 @@ __device__ __forceinline__ float ndot(const uint8_t* ent, int start, int n, floa
 }
 
 template <bool BF, bool E4>
-__device__ __forceinline__ void gates(const lxm_params& p, const lxm_hot& hd, const uint8_t* hot,
-                                      float r) {
+__device__ __forceinline__ void gates(const ChainK& k, const uint8_t* gt, float r) {
+  const lxm_gate& hd = *reinterpret_cast<const lxm_gate*>(gt);
   const int tt = NT - 1 - (int)threadIdx.x;
-  const uint8_t* w1in = hot + hd.ent_w1;
+  const uint8_t* w1in = gt + hd.ent_w1;
   float* hist = LF(L_HIST);
   float* qkcur = LF(L_QKCUR);
   float* ev = LF(L_EV);
   int* flags = LI(L_FLAGS);
-  const lxm_qkc* qk = reinterpret_cast<const lxm_qkc*>(hot + hd.qk);
-  const uint8_t* ent = hot + hd.ent;
+  const lxm_qkc* qk = reinterpret_cast<const lxm_qkc*>(gt + hd.qk);
+  const uint8_t* ent = gt + hd.ent;
   for (int j = tt; j < hd.n_qk; j += NT) {
     const lxm_qkc c = qk[j];
     float* hs = hist + 3 * (hd.qk_base + j);
@@ -639,7 +846,7 @@ __device__ __forceinline__ void gates(const lxm_params& p, const lxm_hot& hd, co
     hs[1] = h2;
     hs[2] = P;
     const float yr = rd<BF>(y);
-    const float v = yr == 0.0f ? yr : rd<BF>(silu(yr));
+    const float v = yr == 0.0f ? yr : rd<BF>(silu_rd<BF>(yr));
     qkcur[j] = v;
     if (v != 0.0f) {
       const bool isk = (c.slot & 256) != 0;
@@ -648,7 +855,7 @@ __device__ __forceinline__ void gates(const lxm_params& p, const lxm_hot& hd, co
       if (!isk) atomicOr(&flags[F_OUT], 1);
     }
   }
-  const lxm_dec* dc = reinterpret_cast<const lxm_dec*>(hot + hd.dec);
+  const lxm_dec* dc = reinterpret_cast<const lxm_dec*>(gt + hd.dec);
   for (int j = ((tt - hd.n_qk) % NT + NT) % NT; j < hd.n_dec; j += NT) {
     const lxm_dec d = dc[j];
     const float a = rd<BF>(ndot<BF, E4>(ent, d.start, d.len, r, w1in));
@@ -662,49 +869,17 @@ __device__ __forceinline__ void gates(const lxm_params& p, const lxm_hot& hd, co
     }
     ev[d.vh] = e;
     if (e != 1.0f) {
-      atomicOr(&flags[F_KH + d.vh / (p.nv / p.nk)], 4);
+      atomicOr(&flags[F_KH + d.vh / k.R], 4);
       atomicOr(&flags[F_ANY], 1);
     }
   }
 }
 
-// stage A's norm: r = rsqrt(mean(h^2) + eps) (transformers qwen3_5 :727, mean = sum / n); the
-// MLP's input D((h * r) * (1 + w)) (:729-734) for every row; with gdn, h and r to the ring (the
-// GDN norm's output, the same expression with its own weights, is formed where it is read).
-// Rows past H compute from +0 and weight 1; nothing reads them.
-// four norm weights 1 + w of rows c..c+3 (c a multiple of 4; the table covers MAXH rows)
-template <bool E4>
-__device__ __forceinline__ v4f w1x4(const uint8_t* hot, int off, int c) {
-  if constexpr (E4) {
-    typedef uint16_t v4h __attribute__((ext_vector_type(4)));
-    const v4h b = reinterpret_cast<const v4h*>(hot + off)[c >> 2];
-    return v4f{1.0f + bf16f(b.x), 1.0f + bf16f(b.y), 1.0f + bf16f(b.z), 1.0f + bf16f(b.w)};
-  } else {
-    return reinterpret_cast<const v4f*>(hot + off)[c >> 2];
-  }
-}
-template <bool BF>
-__device__ __forceinline__ v4f norm4(const v4f& h, float r, const v4f& w) {
-  return v4f{rd<BF>((h.x * r) * w.x), rd<BF>((h.y * r) * w.y), rd<BF>((h.z * r) * w.z),
-             rd<BF>((h.w * r) * w.w)};
-}
-template <bool BF, bool E4>
-__device__ __forceinline__ void norms(const lxm_params& p, const lxm_hot& hd, const uint8_t* hot,
-                                      int L, int step, float r, bool gdn) {
-  const int t = threadIdx.x, H = p.hidden;
-  const v4f* h4 = reinterpret_cast<const v4f*>(smem + L_H);
-  v4f* xm4 = reinterpret_cast<v4f*>(smem + L_XM);
-  const int c0 = 4 * t, c1 = 2048 + 4 * t;
-  const v4f ha = h4[t], hb = h4[NT + t];
-  const v4f pa = w1x4<E4>(hot, hd.w1_post, c0), pb = w1x4<E4>(hot, hd.w1_post, c1);
-  xm4[t] = norm4<BF>(ha, r, pa);
-  xm4[NT + t] = norm4<BF>(hb, r, pb);
-  if (gdn) {
-    float* ring = ring_at(p, step, L);
-    st4_rlx(ring, c0, ha);
-    st4_rlx(ring, c1, hb);
-    if (t == 0) st_rlxf(rr_at(p, step, L), r);
-  }
+// 16 bytes from global memory at agent scope (a buffer load with the sc1 policy)
+__device__ __forceinline__ v4f ld4_rlx(const float* base, int idx) {
+  const __amdgpu_buffer_rsrc_t r =
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(base), 0, 0x7fffffff, 0x00020000);
+  return __builtin_bit_cast(v4f, __builtin_amdgcn_raw_buffer_load_b128(r, idx * 4, 0, 16));
 }
 
 // A GDN event for layer L (the chain's side): publish the value heads' tasks (bit 0 the key
@@ -712,9 +887,10 @@ __device__ __forceinline__ void norms(const lxm_params& p, const lxm_hot& hd, co
 // query/key channel values; post the event; wait for every helper; add out_proj's rows
 // (already rounded) to the residual when a query was live. Returns false on an error.
 template <bool BF, bool E4>
-__device__ bool gdn_event(const lxm_params& p, int L, uint32_t& seq, uint32_t& target) {
-  const int t = threadIdx.x, H = p.hidden;
-  const lxm_hot& hd = *reinterpret_cast<const lxm_hot*>(smem + L_HOT);
+__device__ bool gdn_event(const lxm_params& p, int L, const uint8_t* gt, uint32_t& seq,
+                          uint32_t& target, v4f& ha, v4f& hb) {
+  const int t = threadIdx.x;
+  const lxm_gate& hd = *reinterpret_cast<const lxm_gate*>(gt);
   int* flags = LI(L_FLAGS);
   const float* ev = LF(L_EV);
   const bool out = flags[F_OUT] != 0;
@@ -734,144 +910,185 @@ __device__ bool gdn_event(const lxm_params& p, int L, uint32_t& seq, uint32_t& t
   if (t == 0) flags[F_OK] = spin_sum_ge(p.sync + S_CALL, target, p.err, 4);
   __syncthreads();
   if (!flags[F_OK]) return false;
-  if (out) {
-    float* h = LF(L_H);
-    float xo[8];
-#pragma unroll
-    for (int k = 0; k < 8; k++) {
-      const int i = t + k * NT;
-      xo[k] = i < H ? ld_rlxf(p.xo + i) : 0.0f;
-    }
-#pragma unroll
-    for (int k = 0; k < 8; k++) {
-      const int i = t + k * NT;
-      if (i < H) h[i] = rd<BF>(h[i] + xo[k]);
-    }
+  if (out) {  // (rows past H: xo holds +0 there, and so does h)
+    const v4f xa = ld4_rlx(p.xo, 4 * t), xb = ld4_rlx(p.xo, 2048 + 4 * t);
+    ha = v4f{rd<BF>(ha.x + xa.x), rd<BF>(ha.y + xa.y), rd<BF>(ha.z + xa.z), rd<BF>(ha.w + xa.w)};
+    hb = v4f{rd<BF>(hb.x + xb.x), rd<BF>(hb.y + xb.y), rd<BF>(hb.z + xb.z), rd<BF>(hb.w + xb.w)};
+    v4f* h4 = reinterpret_cast<v4f*>(smem + L_H);
+    h4[t] = ha;
+    h4[NT + t] = hb;
   }
   __syncthreads();
   return true;
 }
 
 // One layer. ss: the sum of squares of h on entry. Ends inside the sum of squares of its output
-// (sum512_begin): the caller finishes it. False on an error.
+// (sum512_begin into wave-total buffer par): the caller takes it. False on an error.
 template <bool BF, bool E4>
-__device__ __forceinline__ bool layer(const lxm_params& p, int L, int step, float ss,
-                                      uint32_t& seq, uint32_t& target) {
-  const int t = threadIdx.x, H = p.hidden;
-  const uint8_t* hot = smem + L_HOT;
-  const lxm_hot hd = *reinterpret_cast<const lxm_hot*>(hot);
-  float* h = LF(L_H);
-  float* act = LF(L_ACT);
+__device__ __forceinline__ bool layer(const lxm_params& p, const ChainK& k, int L, int step,
+                                      float ss, int par,
+                                      v4f& ha, v4f& hb, typename Regions<E4>::RA& r1,
+                                      typename Regions<E4>::RU& ru, typename Regions<E4>::RB& rdw,
+                                      const uint8_t* ptt_next, uint32_t& seq, uint32_t& target) {
+  using RG = Regions<E4>;
+  const int t = threadIdx.x, H = k.H;
+  const LtEnt le = reinterpret_cast<const LtEnt*>(smem + L_LT)[L];
+  const uint8_t* gt = smem + L_GATES + le.goff;
+  const lxm_gate& hd = *reinterpret_cast<const lxm_gate*>(gt);
   float* ev = LF(L_EV);
   int* flags = LI(L_FLAGS);
   uint64_t* pa = reinterpret_cast<uint64_t*>(smem + L_PROF);
-  // ---- stage A: both norms (the GDN's input_layernorm :764 and the MLP's
+  // ---- stage A: both norms' factor (the GDN's input_layernorm :764 and the MLP's
   // post_attention_layernorm :789 read the same h when the GDN leaves it alone)
   const float r = norm_r(ss, H, hd.eps);
-  norms<BF, E4>(p, hd, hot, L, step, r, true);
-  if (t < p.nk) flags[F_KH + t] = 0;
-  if (t < p.nv) ev[t] = 1.0f;
+  stage_a<BF, E4>(k, r1, ha, hb, r, L, step, true);
+  if (t < k.nk) flags[F_KH + t] = 0;
+  if (t < k.nv) ev[t] = 1.0f;
   if (t < 2) flags[F_ANY + t] = 0;
+  sp_arrive(0);
   lds_barrier();
+  sp_depart(0);
   uint64_t c0 = 0;
-  if (PROF_ON && t == 0) {
+  if (k.prof && t == 0) {
     c0 = cycles();
     pa[2] += c0 - pa[15];
   }
   // ---- stage B: the gates and, speculatively (the GDN leaves h alone on most steps), the MLP
-  mlp_units<BF, E4>(hd, hot);
-  gates<BF, E4>(p, hd, hot, r);
+  units<BF, E4>(gt, r1, ru);
+  gates<BF, E4>(k, gt, r);
+  sp_arrive(1);
   lds_barrier();
-  if (PROF_ON && t == 0) {
+  sp_depart(1);
+  if (k.prof && t == 0) {
     const uint64_t c1 = cycles();
     pa[3] += c1 - c0;
     c0 = c1;
   }
   if (flags[F_ANY]) {
-    if (!gdn_event<BF, E4>(p, L, seq, target)) return false;
+    if (!gdn_event<BF, E4>(p, L, gt, seq, target, ha, hb)) return false;
     if (flags[F_OUT]) {  // h may have changed: the MLP again, on the new h
-      ss = hidden_ss();
-      norms<BF, E4>(p, hd, hot, L, step, norm_r(ss, H, hd.eps), false);
+      ss = hidden_ss<BF>(ha, hb);
+      stage_a<BF, E4>(k, r1, ha, hb, norm_r(ss, H, hd.eps), L, step, false);
       lds_barrier();
-      mlp_units<BF, E4>(hd, hot);
+      units<BF, E4>(gt, r1, ru);
       lds_barrier();
     }
-    if (PROF_ON && t == 0) {
+    if (k.prof && t == 0) {
       const uint64_t c1 = cycles();
       pa[4] += c1 - c0;
       pa[16] += 1;
       c0 = c1;
     }
+    sp_skip();
   }
-  // ---- stage C: down_proj by residual row (units ascending), the residual add on every row
-  // (:791), and this thread's terms of the next sum of squares (rows past H stay +0)
-  {
-    // the row pointers are padded to LXM_MAXH + 8 entries (rows past H have none)
-    typedef uint16_t v4h __attribute__((ext_vector_type(4)));
-    const uint16_t* dp = reinterpret_cast<const uint16_t*>(hot + hd.down_ptr);
-    const uint8_t* de = hot + hd.down_ent;
-    v4f* h4 = reinterpret_cast<v4f*>(smem + L_H);
-    const v4h pa4 = reinterpret_cast<const v4h*>(dp)[t], pb4 = reinterpret_cast<const v4h*>(dp + 2048)[t];
-    const int ea = dp[4 * t + 4], eb = dp[2048 + 4 * t + 4];
-    const int st[8] = {pa4.x, pa4.y, pa4.z, pa4.w, pb4.x, pb4.y, pb4.z, pb4.w};
-    const int n[8] = {pa4.y - pa4.x, pa4.z - pa4.y, pa4.w - pa4.z, ea - pa4.w,
-                      pb4.y - pb4.x, pb4.z - pb4.y, pb4.w - pb4.z, eb - pb4.w};
-    const v4f ha = h4[t], hb = h4[NT + t];
-    float d[8];
-    dots<BF, E4, 2, 8>(de, st, n, act, d);
-    const v4f na = v4f{rd<BF>(ha.x + rd<BF>(d[0])), rd<BF>(ha.y + rd<BF>(d[1])),
-                       rd<BF>(ha.z + rd<BF>(d[2])), rd<BF>(ha.w + rd<BF>(d[3]))};
-    const v4f nb = v4f{rd<BF>(hb.x + rd<BF>(d[4])), rd<BF>(hb.y + rd<BF>(d[5])),
-                       rd<BF>(hb.z + rd<BF>(d[6])), rd<BF>(hb.w + rd<BF>(d[7]))};
-    h4[t] = na;
-    h4[NT + t] = nb;
-    sum512_begin(sq_terms(na, nb), LF(L_WSUM));
-  }
-  if (PROF_ON && t == 0) {
+  // the next layer's RA and unit passes into the registers this layer's have left
+  r1 = fetch_words<RG::RAA, RG::RAN>(ptt_next);
+  ru = fetch_words<RG::RUA, RG::RUN>(ptt_next);
+  // ---- stage C1: down_proj by residual row (units in the model's order) into dsum
+  down_rows<BF, E4>(gt, rdw);
+  sp_arrive(2);
+  lds_barrier();
+  sp_depart(2);
+  if (k.prof && t == 0) {
     const uint64_t c1 = cycles();
     pa[5] += c1 - c0;
+    c0 = c1;
+  }
+  rdw = fetch_words<RG::RBA, RG::RBN>(ptt_next);
+  // ---- stage C2: the residual add on the thread's rows (:791), the LDS copy, and this
+  // thread's terms of the next sum of squares (rows past H stay +0)
+  {
+    const v4f* d4 = reinterpret_cast<const v4f*>(smem + L_DSUM);
+    const v4f da = d4[t], db = d4[NT + t];
+    const v4f ra = rd4<BF>(da), rb = rd4<BF>(db);
+    ha = rd4<BF>(v4f{ha.x + ra.x, ha.y + ra.y, ha.z + ra.z, ha.w + ra.w});
+    hb = rd4<BF>(v4f{hb.x + rb.x, hb.y + rb.y, hb.z + rb.z, hb.w + rb.w});
+    v4f* h4 = reinterpret_cast<v4f*>(smem + L_H);
+    h4[t] = ha;
+    h4[NT + t] = hb;
+    sum512_begin(sq_terms<BF>(ha, hb), LF(L_WSUM) + 8 * par, 3);
+  }
+  if (k.prof && t == 0) {
+    const uint64_t c1 = cycles();
+    pa[1] += c1 - c0;
     pa[15] = c1;
   }
   return true;
 }
 
+// the residual rows of this thread to the trace (a test aid)
+__device__ __forceinline__ void trace_rows(float* tr, int H, const v4f& ha, const v4f& hb) {
+  const int t = threadIdx.x;
+#pragma unroll
+  for (int k = 0; k < 4; k++) {
+    if (4 * t + k < H) tr[4 * t + k] = ha[k];
+    if (2048 + 4 * t + k < H) tr[2048 + 4 * t + k] = hb[k];
+  }
+}
+
 // ---------------------------------------------------------------------------------------------
-template <bool BF, bool E4>
-__device__ void run_chain(const lxm_params& p) {
-  const int t = threadIdx.x, H = p.hidden;
+template <bool BF, bool E4, bool TR>
+__device__ void run_chain(const lxm_params& pg) {
+  using RG = Regions<E4>;
+  const int t = threadIdx.x;
+  // the parameter block in LDS: read there at every layer, it costs an LDS read, where the
+  // compiler would reload it from global memory through the scalar cache (it does not keep the
+  // block in scalar registers across the layer loop)
+  static_assert(sizeof(lxm_params) <= 512 && sizeof(lxm_params) % 4 == 0, "params in LDS");
+  for (int k = t; k < (int)(sizeof(lxm_params) / 4); k += NT)
+    reinterpret_cast<uint32_t*>(smem + L_PARAMS)[k] = gp(reinterpret_cast<const uint32_t*>(&pg))[k];
+  __syncthreads();
+  const lxm_params& p = *reinterpret_cast<const lxm_params*>(smem + L_PARAMS);
+  const ChainK k{p.hidden, p.n_layers, p.nk, p.nv, p.nv / p.nk, p.ring, p.rring, p.prof != nullptr};
+  const int H = k.H;
   int* flags = LI(L_FLAGS);
   float* h = LF(L_H);
   float* hist = LF(L_HIST);
   LtEnt* lt = reinterpret_cast<LtEnt*>(smem + L_LT);
   // every LDS word starts finite (zero): gathers may read slots no table names
-  for (int k = t; k < L_CHAIN_END / 16; k += NT) reinterpret_cast<v4u*>(smem)[k] = v4u{0, 0, 0, 0};
+  for (int k = t; k < L_CHAIN_END / 16; k += NT)
+    if (k < L_PARAMS / 16 || k >= L_GATES / 16) reinterpret_cast<v4u*>(smem)[k] = v4u{0, 0, 0, 0};
+  __syncthreads();
+  // the gate section, resident for the launch (the packer pads it to whole 16-byte words)
+  {
+    const GAS v4u* src = gp(reinterpret_cast<const v4u*>(p.gates));
+    v4u* dst = reinterpret_cast<v4u*>(smem + L_GATES);
+    for (int k = t; k < p.gate_bytes / 16; k += NT) dst[k] = src[k];
+  }
+  const int64_t gsec = p.gates - p.blob;
+  for (int L = t; L < p.n_layers; L += NT) {
+    const lxm_layer ly = ldg(p.layers + L);
+    lt[L].ptt = p.blob + ly.ptt;
+    lt[L].goff = (int32_t)(ly.gate - gsec);
+  }
   __syncthreads();
   // the live query/key channels' windows from the conv state (positions 1..3)
   for (int L = 0; L < p.n_layers; L++) {
-    const lxm_hot* hd = reinterpret_cast<const lxm_hot*>(p.blob + p.layers[L].hot);
-    const lxm_qkc* qk = reinterpret_cast<const lxm_qkc*>(p.blob + p.layers[L].hot + hd->qk);
-    for (int j = t; j < hd->n_qk; j += NT)
+    const uint8_t* gt = smem + L_GATES + lt[L].goff;
+    const lxm_gate& hd = *reinterpret_cast<const lxm_gate*>(gt);
+    const lxm_qkc* qk = reinterpret_cast<const lxm_qkc*>(gt + hd.qk);
+    for (int j = t; j < hd.n_qk; j += NT)
       for (int s = 0; s < 3; s++)
-        hist[3 * (hd->qk_base + j) + s] = conv_at<BF>(p.conv[L], (int64_t)qk[j].chan * 4 + 1 + s);
+        hist[3 * (hd.qk_base + j) + s] = conv_at<BF>(p.conv[L], (int64_t)qk[j].chan * 4 + 1 + s);
   }
-  for (int L = t; L < p.n_layers; L += NT) {
-    const uint8_t* hb = p.blob + p.layers[L].hot;
-    lt[L].hot = hb;
-    lt[L].n16 = reinterpret_cast<const lxm_hot*>(hb)->size / 16;
-  }
-  __syncthreads();  // the layer table, before any thread's fetch reads it
-  stage(fetch(0));
-  Pf pf = fetch(p.n_layers > 1 ? 1 : 0);  // always one layer ahead of the staged one
   uint64_t* pa = reinterpret_cast<uint64_t*>(smem + L_PROF);
   if (t < 32) pa[t] = 0;
   __syncthreads();
+  // the first layer's tables; then always one layer ahead
+  typename RG::RA r1 = fetch_words<RG::RAA, RG::RAN>(lt[0].ptt);
+  typename RG::RU ru = fetch_words<RG::RUA, RG::RUN>(lt[0].ptt);
+  typename RG::RB rdw = fetch_words<RG::RBA, RG::RBN>(lt[0].ptt);
+  // the final norm's weights of this thread's rows (padded to MAXH)
+  const v4f wfa = *reinterpret_cast<const v4f*>(p.w1_final + 4 * t);
+  const v4f wfb = *reinterpret_cast<const v4f*>(p.w1_final + 2048 + 4 * t);
   int tok = p.forced[0];
   uint32_t seq = 0, target = 0;
   const uint32_t nh = (uint32_t)(p.n_blocks - 1);
+  int par = 0;
   for (int i = 0; i < p.n_tokens; i++) {
     if (tok < 0 || tok >= p.vocab) tok = 0;  // the host checks forced tokens; preds are in range
     if (t == 0 && p.inputs) p.inputs[i] = tok;
-    if (PROF_ON && t == 0) pa[15] = cycles();
+    if (k.prof && t == 0) pa[15] = cycles();
     // the input's embedding row (the rows past it are +0 already, and stay so)
     for (int c = t; c < H; c += NT) h[c] = 0.0f;
     lds_barrier();
@@ -885,39 +1102,30 @@ __device__ void run_chain(const lxm_params& p) {
       }
     }
     lds_barrier();
-    float ss = hidden_ss();
-    if (PROF_ON && t == 0) {
+    v4f ha = reinterpret_cast<const v4f*>(h)[t], hb = reinterpret_cast<const v4f*>(h)[NT + t];
+    float ss = hidden_ss<BF>(ha, hb);
+    if (k.prof && t == 0) {
       const uint64_t c = cycles();
       pa[0] += c - pa[15];
       pa[15] = c;
     }
-    for (int L = 0; L < p.n_layers; L++) {
-      if (!layer<BF, E4>(p, L, i, ss, seq, target)) return;
-      // the next layer's tables into LDS between the two barriers of the sum of squares (stage
-      // C's reads of this layer's tables are before the first)
-      if (p.trace) {
-        float* tr = p.trace + ((size_t)i * p.n_layers + L) * H;
-        for (int c = t; c < H; c += NT) tr[c] = h[c];
-      }
-      stage(pf);
-      ss = sum512_end(LF(L_WSUM));
-      int L2 = L + 2;
-      while (L2 >= p.n_layers) L2 -= p.n_layers;
-      pf = fetch(L2);
-      if (PROF_ON && t == 0) {
-        const uint64_t c = cycles();
-        pa[1] += c - pa[15];
-        pa[15] = c;
-      }
+    sp_skip();
+    for (int L = 0; L < k.nl; L++) {
+      const int Ln = L + 1 < k.nl ? L + 1 : 0;
+      if (!layer<BF, E4>(p, k, L, i, ss, par, ha, hb, r1, ru, rdw, lt[Ln].ptt, seq, target)) return;
+      if constexpr (TR) trace_rows(p.trace + ((size_t)i * k.nl + L) * H, H, ha, hb);
+      ss = sum512_take(LF(L_WSUM) + 8 * par);
+      par ^= 1;
     }
     // the final norm (lx/lx/hf.py:179-184: model.norm then the tied head), to the helpers
     {
       const float r = norm_r(ss, H, p.rms_eps);
-      for (int c = t; c < H; c += NT) st_rlxf(p.hn + c, rd<BF>((h[c] * r) * p.w1_final[c]));
+      st4_rlx(p.hn, 4 * t, norm4<BF>(ha, r, wfa));
+      st4_rlx(p.hn, 2048 + 4 * t, norm4<BF>(hb, r, wfb));
     }
     drain();
     __syncthreads();
-    if (PROF_ON && t == 0) {
+    if (k.prof && t == 0) {
       const uint64_t c = cycles();
       pa[6] += c - pa[15];
       pa[15] = c;
@@ -938,7 +1146,7 @@ __device__ void run_chain(const lxm_params& p) {
       }
       flags[F_OK] = ok;
       flags[F_TOK] = pred;
-      if (PROF_ON) {
+      if (k.prof) {
         const uint64_t c = cycles();
         pa[7] += c - pa[15];
         pa[15] = c;
@@ -949,7 +1157,10 @@ __device__ void run_chain(const lxm_params& p) {
     if (!flags[F_OK]) return;
     tok = i + 1 < p.n_forced ? p.forced[i + 1] : flags[F_TOK];
   }
-  if (PROF_ON && t < 32) p.prof[t] = pa[t];
+  if (k.prof && t < 32) p.prof[t] = pa[t];
+#ifdef LXM_SUBPROF
+  if (k.prof && t < 16 * SP_NS) p.prof[32 + 4 * p.n_blocks + t] = sp_base()[t];
+#endif
   // every ring write visible to the other blocks, then let them write the conv windows
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
   __syncthreads();
@@ -1014,8 +1225,8 @@ __device__ void gdn_head(const lxm_params& p, int L, int step, int vh, bool out,
   const float e = ld_rlxf(p.mb_e + vh);
   const bool live = (tf & 1) != 0, dec = (tf & 4) != 0;
   const lxm_layer ly = ldg(p.layers + L);
-  const uint8_t* hot = p.blob + ly.hot;
-  const lxm_hot hd = ldg(reinterpret_cast<const lxm_hot*>(hot));
+  const uint8_t* gtab = p.blob + ly.gate;
+  const lxm_gate hd = ldg(reinterpret_cast<const lxm_gate*>(gtab));
   // this key head's dense query and key
   if (t < KD) {
     qd[t] = 0.0f;
@@ -1023,7 +1234,7 @@ __device__ void gdn_head(const lxm_params& p, int L, int step, int vh, bool out,
   }
   __syncthreads();
   if (live) {
-    const lxm_qkc* qk = reinterpret_cast<const lxm_qkc*>(hot + hd.qk);
+    const lxm_qkc* qk = reinterpret_cast<const lxm_qkc*>(gtab + hd.qk);
     for (int j = t; j < hd.n_qk; j += NT) {
       const int sl = gp(&qk[j].slot)[0];
       if ((sl >> 9) == kh) ((sl & 256) ? kd : qd)[sl & 255] = ld_rlxf(p.mb_qk + j);
@@ -1357,10 +1568,12 @@ __device__ void write_windows(const lxm_params& p) {
   }
 }
 
-template <bool BF, bool E4>
+// TR: the launch records the trace (every layer's residual; a test aid), which the production
+// instantiation leaves out of the layer loop
+template <bool BF, bool E4, bool TR>
 __global__ void __launch_bounds__(NT, 1) lxm_decode(const lxm_params* __restrict__ pp) {
   const lxm_params& p = *pp;
-  if (blockIdx.x == 0) run_chain<BF, E4>(p);
+  if (blockIdx.x == 0) run_chain<BF, E4, TR>(p);
   else run_helper<BF, E4>(p);
   __syncthreads();
   if (__hip_atomic_load(gp(p.err), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) return;
@@ -1381,6 +1594,7 @@ __global__ void k_elem(int fn, const float* x, float* y, long n) {
     case 3: r = softplus(v); break;
     case 4: r = rsqrt_(v); break;
     case 5: r = cr_log1p(v); break;
+    case 7: r = silu_bf16(bf16r(v)); break;
     default: r = bf16r(v); break;
   }
   y[i] = r;
@@ -1417,9 +1631,13 @@ int lxm_run(const lxm_params* p_host, const lxm_params* p_dev, int n_blocks, int
             void* stream) {
   const lxm_params* pd = p_dev;
   void* args[] = {&pd};
-  const void* fn = p_host->bf16 ? (const void*)lxm_decode<true, true>
-                   : p_host->e4 ? (const void*)lxm_decode<false, true>
-                                : (const void*)lxm_decode<false, false>;
+  const bool tr = p_host->trace != nullptr;
+  const void* fn = p_host->bf16 ? (tr ? (const void*)lxm_decode<true, true, true>
+                                      : (const void*)lxm_decode<true, true, false>)
+                   : p_host->e4 ? (tr ? (const void*)lxm_decode<false, true, true>
+                                      : (const void*)lxm_decode<false, true, false>)
+                                : (tr ? (const void*)lxm_decode<false, false, true>
+                                      : (const void*)lxm_decode<false, false, false>);
   hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, lds_bytes);
   if (e != hipSuccess) return (int)e;
   e = hipLaunchCooperativeKernel(fn, dim3(n_blocks), dim3(NT), args, (unsigned)lds_bytes,
@@ -1431,10 +1649,10 @@ int lxm_max_blocks(int lds_bytes) {
   int dev = 0, cus = 0, n = 0;
   if (hipGetDevice(&dev) != hipSuccess) return 0;
   if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return 0;
-  if (hipFuncSetAttribute((const void*)lxm_decode<true, true>,
+  if (hipFuncSetAttribute((const void*)lxm_decode<true, true, false>,
                           hipFuncAttributeMaxDynamicSharedMemorySize, lds_bytes) != hipSuccess)
     return 0;
-  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, lxm_decode<true, true>, NT, lds_bytes) !=
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, lxm_decode<true, true, false>, NT, lds_bytes) !=
       hipSuccess)
     return 0;
   return n * cus;

@@ -99,6 +99,29 @@ __device__ __forceinline__ float cr_log1p(float y) {
 
 __device__ __forceinline__ float silu(float x) { return x / (1.0f + cr_exp(-x)); }
 __device__ __forceinline__ float sigmoid(float x) { return 1.0f / (1.0f + cr_exp(-x)); }
+
+// bf16r(silu(g)) for a bf16 value g (every MLP unit and conv output rounds silu's result to
+// bf16 at once), equal bit for bit to the exact sequence above. A fast evaluation first:
+// exp(-g) = 2^(-g*log2 e) with log2 e split in two (LH keeps 15 significant bits, so g * LH is
+// exact for g's 8), each power by the hardware's exp2, then g * rcp(1 + e); its result lies
+// within a few units in the last place of the exact sequence's. Where it lies within 64 units
+// of a bf16 rounding boundary (low half 0x8000), or |g| >= 64, the exact sequence decides (for
+// g >= 64, 1 + exp(-g) rounds to 1 and silu(g) = g). Tested on every bf16 input.
+__device__ __forceinline__ float silu_bf16(float g) {
+  if (g >= 64.0f) return bf16r(g);
+  if (!(g > -64.0f)) return bf16r(silu(g));
+  const float LH = __uint_as_float(0x3fb8aa00u), LL = __uint_as_float(0x36eca570u);
+  const float e = __builtin_amdgcn_exp2f(g * -LH) * __builtin_amdgcn_exp2f(g * -LL);
+  const float q = g * __builtin_amdgcn_rcpf(1.0f + e);
+  if ((fbits(q) & 0xffffu) - 0x7fc0u < 0x80u) return bf16r(silu(g));
+  return bf16r(q);
+}
+// silu rounded to the model dtype (bf16: the fast path above; fp32: the exact sequence)
+template <bool BF>
+__device__ __forceinline__ float silu_rd(float g) {
+  if constexpr (BF) return silu_bf16(g);
+  else return silu(g);
+}
 __device__ __forceinline__ float softplus(float x) { return x > 20.0f ? x : cr_log1p(cr_exp(x)); }
 __device__ __forceinline__ float rsqrt_(float x) { return 1.0f / __builtin_sqrtf(x); }
 

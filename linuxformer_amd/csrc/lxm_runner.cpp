@@ -8,7 +8,7 @@
 //
 // The dump's manifest lists each lxm_params pointer field with the file holding its device
 // buffer ("buf"), a zeroed buffer size ("zero"), or a list of files whose device copies form a
-// pointer array ("ptrs", the per-layer states). Every launch continues the stream from the last
+// pointer array ("ptrs", the per-layer states), or a pointer into another buffer ("sub"). Every launch continues the stream from the last
 // prediction of the one before. Prints one JSON line: tokens, per-launch kernel milliseconds
 // (hipEvent), tok/s, the last prediction.
 #include <dlfcn.h>
@@ -106,6 +106,7 @@ int main(int argc, char** argv) {
   memcpy(&p, pb.data(), sizeof p);
   std::map<std::string, void**> field = {
       {"layers", (void**)&p.layers},     {"blob", (void**)&p.blob},
+      {"gates", (void**)&p.gates},
       {"rec", (void**)&p.rec},           {"conv", (void**)&p.conv},
       {"emb_ptr", (void**)&p.emb_ptr},   {"emb_ent", (void**)&p.emb_ent},
       {"w1_final", (void**)&p.w1_final}, {"head_rows", (void**)&p.head_rows},
@@ -142,6 +143,11 @@ int main(int argc, char** argv) {
       CK(hipMemset(d, 0, n));
       zeroed.push_back({d, n});
       *field.at(name) = d;
+    } else if (kind == "sub") {  // a pointer into another buffer: sub <field> <base field> <offset>
+      std::string base;
+      size_t off;
+      ss >> base >> off;
+      *field.at(name) = (char*)*field.at(base) + off;
     } else if (kind == "ptrs") {
       int n;
       ss >> n;

@@ -7,10 +7,11 @@ the same cache tensors updated in place, the same predictions.
     preds = m.run(forced, n)   # n steps: inputs forced[0..], then each step's own prediction
 
 The packer here turns the model's sparse tensors (from ``Fast``) into one byte blob of tables the
-kernel reads: per layer a "hot" blob (norm weights, MLP rows, the gates' query/key/decay rows)
-that the chain workgroup streams into LDS one layer ahead, and "cold" tables (value rows, z,
-beta, out_proj by residual row, per key head) read only when a head is active; the head's rows
-split over the helper workgroups, each staging its own in LDS.
+kernel reads: per layer a per-thread table (norm weights, MLP rows, down rows; chain.py) that
+the chain workgroup prefetches into its registers one layer ahead, the gates' tables (the live
+query/key channels and decays, resident in the chain's LDS), and "cold" tables (value rows, z,
+beta, out_proj by residual row) read only when a head is active; the head's rows split over the
+helper workgroups, each staging its own in LDS.
 """
 
 from __future__ import annotations
@@ -20,19 +21,19 @@ import ctypes
 import numpy as np
 import torch
 
-from . import mk_build
+from . import chain, mk_build
 
 NT, MAXH, KD, VD, RMAX = 512, 4096, 256, 128, 8
-MAXU, MAXQK, MAXQKL, MAXDEC, HOT_MAX, NSYNC, OUT_MAX = 2048, 1024, 512, 512, 65536, 1024, 1024
+MAXU, MAXQK, MAXQKL, MAXDEC, GATE_MAX, NSYNC, OUT_MAX = 2048, 1024, 512, 512, 65536, 1024, 1024
 OUT_HELPERS, OUT_ROWS = 64, 64
 
 I32, I64, F32, PTR = ctypes.c_int32, ctypes.c_int64, ctypes.c_float, ctypes.c_void_p
 
 
-class Hot(ctypes.Structure):
-    _fields_ = [(n, I32) for n in ("n_units", "n_qk", "n_dec", "qk_base", "ent_w1", "w1_post",
-                                   "unit", "gu_ent", "down_ptr", "down_ent", "qk", "dec", "ent",
-                                   "size")] + [("eps", F32), ("geps", F32)]
+class Gate(ctypes.Structure):
+    _fields_ = [(n, I32) for n in ("n_qk", "n_dec", "qk_base", "qk", "dec", "ent", "ent_w1",
+                                   "size")] + [("eps", F32), ("geps", F32)] + \
+        [(n, I32) for n in ("long_u", "long_r", "long_ent", "n_long_u", "n_long_r", "pad")]
 
 
 class QkC(ctypes.Structure):
@@ -49,24 +50,25 @@ class Chan(ctypes.Structure):
 
 
 class LayerDesc(ctypes.Structure):
-    _fields_ = [(n, I64) for n in ("hot", "chan", "qkv_ent", "b_row", "b_ent", "z_row", "z_ent",
-                                   "out_ptr", "out_ent", "gnorm", "w1_in")]
+    _fields_ = [(n, I64) for n in ("ptt", "gate")] + \
+        [(n, I64) for n in ("chan", "qkv_ent", "b_row", "b_ent", "z_row", "z_ent", "out_ptr",
+                            "out_ent", "gnorm", "w1_in")]
 
 
 class Params(ctypes.Structure):
     _fields_ = [(n, I32) for n in ("hidden", "n_layers", "nk", "kd", "nv", "vd", "n_conv",
                                    "vocab", "bf16", "n_blocks")] + \
-        [("rms_eps", F32), ("head_lds", I32), ("e4", I32), ("pad1", I32)] + \
-        [(n, PTR) for n in ("layers", "blob", "rec", "conv", "emb_ptr", "emb_ent", "w1_final",
-                            "head_rows", "head_ptr", "head_ent", "forced")] + \
+        [("rms_eps", F32), ("head_lds", I32), ("e4", I32), ("gate_bytes", I32)] + \
+        [(n, PTR) for n in ("layers", "blob", "gates", "rec", "conv", "emb_ptr", "emb_ent",
+                            "w1_final", "head_rows", "head_ptr", "head_ent", "forced")] + \
         [("n_forced", I32), ("n_tokens", I32)] + \
         [(n, PTR) for n in ("preds", "inputs", "trace", "ring", "rring", "hn", "sync", "keys", "err",
                             "prof", "mb_task", "mb_e", "mb_qk", "ybuf", "xo")] + \
         [("n_qk_total", I32), ("pad", I32)]
 
 
-assert ctypes.sizeof(Hot) == 64 and ctypes.sizeof(QkC) == 32 and ctypes.sizeof(Dec) == 32
-assert ctypes.sizeof(Chan) == 24 and ctypes.sizeof(LayerDesc) == 88
+assert ctypes.sizeof(Gate) == 64 and ctypes.sizeof(QkC) == 32 and ctypes.sizeof(Dec) == 32
+assert ctypes.sizeof(Chan) == 24 and ctypes.sizeof(LayerDesc) == 96
 
 
 def _bf16_bits(v: np.ndarray) -> np.ndarray:
@@ -173,7 +175,8 @@ class Mega:
 
     def __init__(self, fast, model=None, cache=None, offset: int = 0, ncta: int | None = None,
                  subprof: bool = False, spec: bool = True, pair_layers=None, device=None):
-        self.lib = mk_build.load()
+        self.lib = mk_build.load(subprof)
+        self.subprof = subprof
         self.fast, self.model, self.cache, self.offset = fast, model, cache, offset
         sm = fast.sm
         d = sm.dims
@@ -198,33 +201,23 @@ class Mega:
         descs = (LayerDesc * d.n_layers)()
         H, R, C = d.hidden, d.nv // d.nk, d.n_conv
         qk_total = 0
-        self.stats = {"layers": d.n_layers, "hot_bytes": [], "units": [], "qk": [], "dec": []}
+        self.stats = {"layers": d.n_layers, "units": [], "qk": [], "dec": [], "chain": []}
         self.unit_order = []  # per layer: the model's unit index of each packed unit
+        cf = chain.fmt(self.e4)
+        gate_blobs, gate_off = [], 0
+        ptts, longs = [], []
         for L, ly in enumerate(sm.layers):
-            # ---- live MLP units (gate row, up row and down column nonzero; lx/lx/fast.py:242-248)
+            # ---- live MLP units (gate row, up row and down column nonzero; lx/lx/fast.py:242-248),
+            # in the model's order (the act index of a unit is its position here)
             g, u, dn = _Csr(ly.gate_proj), _Csr(ly.up_proj), _Csr(ly.down_proj.transpose())
             gc = np.diff(g.ptr)
             uc = np.diff(u.ptr)
             dc = np.diff(dn.ptr)
             units = np.nonzero((gc > 0) & (uc > 0) & (dc > 0))[0]
             assert len(units) <= MAXU, f"layer {L}: {len(units)} live MLP units > {MAXU}"
-            # by row length, longest first (stable): a wave's units have rows of about one length,
-            # so the kernel's 4-entry rounds over a thread's rows rarely run for a few long ones,
-            # and the shortest rows share the top wave with the gates
-            units = units[np.argsort(-np.maximum(gc[units], uc[units]), kind="stable")]
             self.unit_order.append(units)
             uidx = np.full(d.inter, -1, np.int64)
             uidx[units] = np.arange(len(units))
-            gu_parts, meta, pos = [], [], 0
-            for uu in units:
-                c1, v1 = g.row(uu)
-                c2, v2 = u.row(uu)
-                assert len(c1) < 256 and len(c2) < 256
-                meta.append(pos | (len(c1) << 16) | (len(c2) << 24))
-                gu_parts.append(pk.ent(c1, v1))
-                gu_parts.append(pk.ent(c2, v2))
-                pos += len(c1) + len(c2)
-            assert pos < 1 << 16
             # down_proj by residual row over the live units, in the model's unit order (the sum's
             # order), each entry naming the unit's packed index
             dcoo = ly.down_proj
@@ -234,7 +227,10 @@ class Mega:
             drows, dunits, dvals = drows[order], dunits[order], dvals[order]
             dptr = np.zeros(H + 1, np.int64)
             np.cumsum(np.bincount(drows, minlength=H), out=dptr[1:])
-            assert dptr[-1] < 1 << 16
+            ct = chain.pack_layer(
+                cf, H, units, [g.row(k) for k in units], [u.row(k) for k in units],
+                [(dunits[dptr[r]:dptr[r + 1]], dvals[dptr[r]:dptr[r + 1]]) for r in range(H)],
+                np.asarray(ly.post_attention_layernorm, np.float32))
             # ---- the gates: live query/key channels (nonzero conv taps) and decaying heads
             qkv = _Csr(ly.in_proj_qkv)
             taps = np.asarray(ly.conv1d, np.float32)
@@ -266,34 +262,29 @@ class Mega:
                 ent_w1.append(w1in[cols])
                 epos += len(cols)
             assert len(decs) <= MAXDEC
-            # ---- the hot blob
-            hb = _Blob()
-            hb.add(bytes(64))
-            # the MLP norm's weights, padded with 0 (1 + w = 1) to MAXH rows
-            wpost = np.zeros(MAXH, np.float32)
-            wpost[:H] = ly.post_attention_layernorm
-            o_w1post = hb.add(pk.w1(wpost))
-            o_unit = hb.add(np.asarray(meta, np.uint32).tobytes())
-            o_gu = hb.add(b"".join(gu_parts))
-            # padded to MAXH + 8 rows (the kernel reads four rows' pointers at once)
-            dpad = np.full(MAXH + 8, dptr[-1], np.int64)
-            dpad[:H + 1] = dptr
-            o_dptr = hb.add(dpad.astype(np.uint16).tobytes())
-            o_dent = hb.add(pk.ent(dunits, dvals))
-            o_qk = hb.add(b"".join(bytes(q) for q in qks))
-            o_dec = hb.add(b"".join(bytes(x) for x in decs))
-            o_ent = hb.add(b"".join(ent_parts))
+            gb = _Blob()
+            gb.add(bytes(64))
+            o_qk = gb.add(b"".join(bytes(q) for q in qks))
+            o_dec = gb.add(b"".join(bytes(x) for x in decs))
+            o_ent = gb.add(b"".join(ent_parts) + bytes(4 * pk.esz))
             # the GDN norm's weight at each of those entries' columns
-            o_entw = hb.add(pk.w1(np.concatenate(ent_w1)) if ent_w1 else b"")
-            hot = Hot(n_units=len(units), n_qk=len(qks), n_dec=len(decs), qk_base=qk_total,
-                      ent_w1=o_entw, w1_post=o_w1post, unit=o_unit, gu_ent=o_gu, down_ptr=o_dptr,
-                      down_ent=o_dent, qk=o_qk, dec=o_dec, ent=o_ent, size=hb.n,
-                      eps=d.rms_eps, geps=d.geps)
-            hb.parts[0] = bytes(hot)
-            assert hb.n <= HOT_MAX, f"layer {L}: resident tables {hb.n} B > {HOT_MAX}"
+            o_entw = gb.add((pk.w1(np.concatenate(ent_w1)) if ent_w1 else b"") + bytes(16))
+            # the chain's long units and rows (too long for its register passes)
+            o_lu = gb.add(ct.long_u)
+            o_lr = gb.add(ct.long_r)
+            o_le = gb.add(ct.long_ent)
+            gate = Gate(n_qk=len(qks), n_dec=len(decs), qk_base=qk_total, qk=o_qk, dec=o_dec,
+                        ent=o_ent, ent_w1=o_entw, size=gb.n, eps=d.rms_eps, geps=d.geps,
+                        long_u=o_lu, long_r=o_lr, long_ent=o_le, n_long_u=len(ct.long_u) // 32,
+                        n_long_r=len(ct.long_r) // 16)
+            gb.parts[0] = bytes(gate)
+            gate_blobs.append(gb.bytes())
+            descs[L].gate = gate_off  # (made absolute below)
+            gate_off += gb.n
             qk_total += len(qks)
+            ptts.append(ct)
+            self.stats["chain"].append(ct.stats)
             desc = descs[L]
-            desc.hot = blob.add(hb.bytes())
             # ---- cold tables
             chans = np.zeros(C, dtype=[("start", "<i4"), ("len", "<i4"), ("taps", "<f4", (4,))])
             chans["start"] = qkv.ptr[:-1]
@@ -319,12 +310,19 @@ class Mega:
             desc.out_ent = blob.add(pk.ent(oc.cols, oc.vals, scale=1))
             desc.gnorm = blob.add(np.asarray(ly.norm, np.float32).tobytes())
             desc.w1_in = blob.add(pk.w1(ly.input_layernorm))
-            self.stats["hot_bytes"].append(hb.n)
             self.stats["units"].append(len(units))
             self.stats["qk"].append(len(qks))
             self.stats["dec"].append(len(decs))
         assert qk_total <= MAXQK, f"{qk_total} live query/key channels > {MAXQK}"
-        blob.add(bytes(HOT_MAX))  # padding past the last table
+        assert gate_off <= GATE_MAX, f"the gate tables ({gate_off} B) exceed {GATE_MAX} B of LDS"
+        self.gate_bytes = gate_off
+        gsec = blob.add(b"".join(gate_blobs))
+        self.gate_sec = gsec
+        for L, ct in enumerate(ptts):
+            desc = descs[L]
+            desc.gate += gsec
+            desc.ptt = blob.add(ct.ptt)
+        blob.add(bytes(4096))  # padding past the last table
         self.blob = torch.frombuffer(bytearray(blob.bytes()), dtype=torch.uint8).to(dev)
         self.layers_d = torch.frombuffer(bytearray(bytes(descs)), dtype=torch.uint8).to(dev)
         self.n_qk_total = qk_total
@@ -334,7 +332,9 @@ class Mega:
         self.emb_ent = torch.frombuffer(bytearray(pk.ent(emb.cols, emb.vals)),
                                         dtype=torch.uint8).to(dev)
         w1f = (np.float32(1.0) + np.asarray(sm.norm, np.float32)).astype(np.float32)
-        self.w1_final = torch.from_numpy(w1f).to(dev)
+        w1pad = np.ones(MAXH, np.float32)  # the chain reads every thread's rows (<= MAXH)
+        w1pad[:H] = w1f
+        self.w1_final = torch.from_numpy(w1pad).to(dev)
         hcols = np.nonzero(w1f != 0)[0]  # a column whose (1 + w) is 0 adds only zeros
         hmask = np.zeros(H, bool)
         hmask[hcols] = True
@@ -380,14 +380,17 @@ class Mega:
                            "blob_bytes": int(self.blob.numel()), "qk_total": qk_total,
                            "head_nnz": int(hptr[-1]), "vocab": V})
 
-    PHASES = ("embedding", "layer staging (+trace)", "norms (stage A)",
+    PHASES = ("embedding", "residual + sums (stage C2, +trace)", "norms (stage A)",
               "gates + MLP units (stage B)", "GDN events + MLP redo",
-              "down_proj + next norm (stage C)", "final norm + publish", "head argmax wait")
+              "down_proj rows (stage C1)", "final norm + publish", "head argmax wait")
     HELPER = ("wait", "head rows", "value head", "out_proj rows")
+
+    SUB_STAGES = ("stage A (norms)", "stage B (units + gates)", "stage C1 (down rows)",
+                  "stage C2 (residual + sums)")
 
     @property
     def prof_size(self) -> int:
-        return 32 + 4 * self.ncta
+        return 32 + 4 * self.ncta + (16 * len(self.SUB_STAGES) if self.subprof else 0)
 
     def phase_report(self, prof: torch.Tensor) -> dict:
         """prof counters -> cycles per token of each chain phase, and the helpers' mean (and
@@ -401,6 +404,13 @@ class Mega:
             out[f"helper {name}"] = round(sum(v) / len(v) / n, 1)
             out[f"helper {name} max"] = round(max(v) / n, 1)
         out["tokens"] = n
+        if self.subprof:
+            base = 32 + 4 * self.ncta
+            for s, name in enumerate(self.SUB_STAGES):
+                busy = [round(c[base + 16 * s + w] / n / self.dims.n_layers) for w in range(8)]
+                wait = [round(c[base + 16 * s + 8 + w] / n / self.dims.n_layers) for w in range(8)]
+                out[f"per layer, {name}: busy by wave"] = busy
+                out[f"per layer, {name}: wait by wave"] = wait
         return out
 
     def _bufs(self) -> dict:
@@ -451,7 +461,8 @@ class Mega:
         p = Params(hidden=d.hidden, n_layers=d.n_layers, nk=d.nk, kd=KD, nv=d.nv, vd=VD,
                    n_conv=d.n_conv, vocab=self.vocab, bf16=int(self.bf), n_blocks=self.ncta,
                    rms_eps=d.rms_eps, head_lds=self.head_lds, e4=int(self.e4), n_forced=1,
-                   n_tokens=n, n_qk_total=self.n_qk_total)
+                   n_tokens=n, n_qk_total=self.n_qk_total, gate_bytes=self.gate_bytes)
+        lines.append(f"sub gates blob {self.gate_sec}")
         with open(os.path.join(path, "params.bin"), "wb") as f:
             f.write(bytes(p))
         with open(os.path.join(path, "manifest.txt"), "w") as f:
@@ -507,7 +518,8 @@ class Mega:
         p = Params(hidden=d.hidden, n_layers=d.n_layers, nk=d.nk, kd=KD, nv=d.nv, vd=VD,
                    n_conv=d.n_conv, vocab=self.vocab, bf16=int(self.bf), n_blocks=self.ncta,
                    rms_eps=d.rms_eps, head_lds=self.head_lds, e4=int(self.e4),
-                   layers=self.layers_d.data_ptr(), blob=self.blob.data_ptr(),
+                   gate_bytes=self.gate_bytes, layers=self.layers_d.data_ptr(),
+                   blob=self.blob.data_ptr(), gates=self.blob.data_ptr() + self.gate_sec,
                    rec=rs.data_ptr(), conv=cs.data_ptr(), emb_ptr=self.emb_ptr.data_ptr(),
                    emb_ent=self.emb_ent.data_ptr(), w1_final=self.w1_final.data_ptr(),
                    head_rows=self.head_rows.data_ptr(), head_ptr=self.head_ptr.data_ptr(),

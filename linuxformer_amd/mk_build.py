@@ -12,6 +12,8 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
 LIBDIR = os.path.join(HERE, "_lib")
 LIB = os.path.join(LIBDIR, "liblxm.so")
+# the same kernel with the per-wave sub-phase counters (-DLXM_SUBPROF; lx.mega's MK_SUBPROF build)
+LIB_SUBPROF = os.path.join(LIBDIR, "liblxm_subprof.so")
 RUNNER = os.path.join(LIBDIR, "lxm_runner")
 SOURCES = ["lxm_decode.hip"]
 HEADERS = ["lxm_math.h", os.path.join("..", "..", "include", "lxm.h")]
@@ -27,17 +29,26 @@ def hipcc() -> str:
     return "hipcc"
 
 
-def build(verbose: bool = False) -> str:
-    """Compile the library for gfx950 (always compiles)."""
-    os.makedirs(LIBDIR, exist_ok=True)
-    tmp = LIB + ".tmp"
-    cmd = [hipcc(), *FLAGS, "-o", tmp, *[os.path.join(CSRC, s) for s in SOURCES]]
+def _compile(out: str, extra: list, verbose: bool) -> None:
+    tmp = out + ".tmp"
+    cmd = [hipcc(), *FLAGS, *extra, "-o", tmp, *[os.path.join(CSRC, s) for s in SOURCES]]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         raise RuntimeError(f"hipcc failed ({r.returncode}):\n{r.stderr[-4000:]}")
     if verbose and r.stderr:
         print(r.stderr)
-    os.replace(tmp, LIB)
+    os.replace(tmp, out)
+
+
+def build(verbose: bool = False) -> str:
+    """Compile the library (and its sub-phase profiling twin) for gfx950 (always compiles)."""
+    os.makedirs(LIBDIR, exist_ok=True)
+    from concurrent.futures import ThreadPoolExecutor
+
+    with ThreadPoolExecutor(2) as ex:
+        for f in [ex.submit(_compile, LIB, [], verbose),
+                  ex.submit(_compile, LIB_SUBPROF, ["-DLXM_SUBPROF"], verbose)]:
+            f.result()
     # the runner has a kernel of its own (the copy that calibrates the byte counters): gfx950
     r = subprocess.run([hipcc(), "--offload-arch=gfx950", "-O2", "-std=c++17", "-Xclang",
                         "-target-feature", "-Xclang", "-packed-fp32-ops", "-o", RUNNER + ".tmp",
@@ -48,17 +59,18 @@ def build(verbose: bool = False) -> str:
     return LIB
 
 
-_lib = None
+_libs = {}
 
 
-def load() -> ctypes.CDLL:
-    """The built library (ctypes). Raises if it has not been built."""
-    global _lib
-    if _lib is None:
-        if not os.path.exists(LIB):
-            raise RuntimeError(f"{LIB} is missing: run linuxformer_amd.mk_build.build() (or "
+def load(subprof: bool = False) -> ctypes.CDLL:
+    """The built library (ctypes), or its sub-phase profiling twin. Raises if it has not been
+    built."""
+    path = LIB_SUBPROF if subprof else LIB
+    if path not in _libs:
+        if not os.path.exists(path):
+            raise RuntimeError(f"{path} is missing: run linuxformer_amd.mk_build.build() (or "
                                "__graft_entry__.build()) first")
-        lib = ctypes.CDLL(LIB)
+        lib = ctypes.CDLL(path)
         P, I = ctypes.c_void_p, ctypes.c_int
         lib.lxm_run.argtypes = [P, P, I, I, P]
         lib.lxm_run.restype = I
@@ -71,8 +83,10 @@ def load() -> ctypes.CDLL:
         lib.lxm_t_elem.restype = I
         lib.lxm_t_sum.argtypes = [I, P, I, I, P, P]
         lib.lxm_t_sum.restype = I
-        _lib = lib
-    return _lib
+        lib.lxm_helper_lds.argtypes = [I]
+        lib.lxm_helper_lds.restype = I
+        _libs[path] = lib
+    return _libs[path]
 
 
 EXPORTS = ("lxm_run", "lxm_lds_base", "lxm_helper_lds", "lxm_max_blocks", "lxm_max_lds",

@@ -106,6 +106,25 @@ def test_device_math_matches_oracle(cuda):
         assert same.all(), (fn, int((~same).sum()))
 
 
+def test_device_silu_bf16_fast_path_is_exact(cuda):
+    """The decode's fast silu for bf16 models (hardware exp2 and reciprocal; the exact sequence
+    near a bf16 rounding boundary and for |x| >= 64) equals bf16(silu(x)) of the oracle on every
+    one of the 65,536 bf16 inputs: the whole input space, so the equality is complete."""
+    from oracle import oracle as ox
+
+    lib = mk_build.load()
+    x = (np.arange(65536, dtype=np.uint32) << 16).view(np.float32)
+    st = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    xd = torch.from_numpy(x).to(cuda)
+    yd = torch.empty_like(xd)
+    assert lib.lxm_t_elem(7, ctypes.c_void_p(xd.data_ptr()), ctypes.c_void_p(yd.data_ptr()),
+                          x.size, st) == 0
+    y = yd.cpu().numpy()
+    ref = ox.elem("bf16", ox.elem("silu", x))
+    same = (bits(y) == bits(ref)) | (np.isnan(y) & np.isnan(ref))
+    assert same.all(), int((~same).sum())
+
+
 @pytest.mark.parametrize("kind,n", [(0, 3572), (0, 192), (1, 128), (1, 256)])
 def test_device_sums_match_oracle(cuda, kind, n):
     from oracle import oracle as ox

@@ -11,7 +11,7 @@ import sys
 import numpy as np
 import pytest
 
-from linuxformer_amd import fast, mega, mk_build, synth
+from linuxformer_amd import chain, fast, mega, mk_build, synth
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 
@@ -58,27 +58,32 @@ def test_config2_shape_and_gates():
 
 
 class _FakeLib:
-    """The library calls the packer makes, answered as an MI355X would (no GPU needed)."""
+    """The library calls the packer makes, answered as an MI355X would (no GPU needed): LDS
+    sizes from the built library itself (pure functions), the device's shape from MI355X."""
+
+    def __init__(self, real):
+        self.real = real
 
     def lxm_device_cus(self):
         return 256
 
     def lxm_lds_base(self):
-        return 141_000
+        return self.real.lxm_lds_base()
 
     def lxm_max_lds(self):
         return 163_840
 
     def lxm_helper_lds(self, head_lds):
-        return head_lds + 43_856
+        return self.real.lxm_helper_lds(head_lds)
 
     def lxm_max_blocks(self, lds):
-        return 256
+        return 256 if lds <= 163_840 else 0
 
 
 @pytest.fixture
-def packed(monkeypatch):
-    monkeypatch.setattr(mk_build, "_lib", _FakeLib())
+def packed(monkeypatch, native_lib):
+    fake = _FakeLib(native_lib)
+    monkeypatch.setattr(mk_build, "load", lambda subprof=False: fake)
 
     def make(spec):
         m = synth.build(spec)
@@ -93,60 +98,146 @@ def _ent(blob: bytes, off: int, i: int, scale: int = 4):
     return (w & 0xffff) // scale, np.uint32((w >> 16) << 16).view(np.float32)
 
 
+def _slot_ent(S, s):
+    """Entry at slot s of one lane's e4 slots: (index, value)."""
+    w = int(S[s])
+    assert (w & 0xffff) % 4 == 0
+    return (w & 0xffff) // 4, float(np.uint32((w >> 16) << 16).view(np.float32))
+
+
+def _chain_rows(mg, m, L, blob, desc):
+    """The chain tables of layer L decoded as the kernel reads them: {act index: (gate entries,
+    up entries)} and {row: down entries}, each an ordered list of (index, value) without the
+    padding, plus the checks on the padding and on the wave-uniform bounds."""
+    f = chain.fmt(mg.e4)
+    assert f.e4
+    S = chain.decode_ptt(f, blob[desc.ptt:desc.ptt + 16 * f.WORDS * chain.NT])
+    g = mega.Gate.from_buffer_copy(blob[desc.gate:desc.gate + 64])
+    a_u, a_r, a_e = desc.gate + g.long_u, desc.gate + g.long_r, desc.gate + g.long_ent
+    lu = np.frombuffer(blob[a_u:a_u + 32 * g.n_long_u], np.int32).reshape(-1, 8)
+    lr = np.frombuffer(blob[a_r:a_r + 16 * g.n_long_r], np.int32).reshape(-1, 4)
+    units, rows = {}, {}
+
+    def trim(lst, n):  # entries past the row's own are padding: index 0, value 0
+        assert all(e == (0, 0.0) for e in lst[n:])
+        return lst[:n]
+
+    for lane in range(chain.NT):
+        m0, m1, m2 = (int(x) for x in S[lane, f.MA:f.MA + 3])
+        wave = S[(lane // 64) * 64:(lane // 64 + 1) * 64, f.MA + 2]
+        assert (wave == m2).all()
+        mb3 = int(S[lane, f.MB + 3])
+        wave = S[(lane // 64) * 64:(lane // 64 + 1) * 64, f.MB + 3]
+        assert ((wave >> 16) == (mb3 >> 16)).all()
+        for p, base in ((0, f.U0), (1, f.U1)):
+            if not (m0 >> (16 * p)) & 0x8000:
+                continue
+            k = (m0 >> (16 * p)) & 0xfff
+            G = (m2 >> (4 * p)) & 15
+            gl = [_slot_ent(S[lane], base + 2 * j) for j in range(G)]
+            ul = [_slot_ent(S[lane], base + 2 * j + 1) for j in range(G)]
+            ng = len(m.layers[L].gate_proj.cols[m.layers[L].gate_proj.rows == mg.unit_order[L][k]])
+            nu = len(m.layers[L].up_proj.cols[m.layers[L].up_proj.rows == mg.unit_order[L][k]])
+            if (m2 >> (8 + p)) & 1:  # shared columns
+                assert [c for c, _ in gl] == [c for c, _ in ul]
+            assert k not in units
+            units[k] = (trim(gl, ng), trim(ul, nu))
+        mask = (mb3 >> 16) & 255
+        for q, ln in enumerate(f.DLEN):
+            row = (int(S[lane, f.MB + q // 2]) >> (16 * (q & 1))) & 0xffff
+            if row == 0xffff:
+                continue
+            assert mask & (1 << q)
+            ents = [_slot_ent(S[lane], f.D + f.doff[q] + j) for j in range(ln)]
+            n = len(m.layers[L].down_proj.cols[m.layers[L].down_proj.rows == row])
+            assert row not in rows
+            rows[row] = [e for e in ents if e != (0, 0.0)]
+        li, ri = m1 & 0xffff, mb3 & 0xffff
+        if li != 0xffff:
+            assert (m2 >> 10) & 1
+            k, gs, gn, us, un = (int(x) for x in lu[li][:5])
+            units[k] = ([_ent(blob, a_e, gs + j) for j in range(gn)],
+                        [_ent(blob, a_e, us + j) for j in range(un)])
+            units[k] = tuple([(int(c), float(v)) for c, v in r] for r in units[k])
+        if ri != 0xffff:
+            assert (mb3 >> 24) & 1
+            row, st, n = (int(x) for x in lr[ri][:3])
+            rows[row] = [(int(c), float(v)) for c, v in
+                         (_ent(blob, a_e, st + j) for j in range(n))]
+    return S, units, rows
+
+
 def test_packer_tables_decode_to_the_model(packed):
     """Every packed MLP row, down row, gate row and head row decodes back to the model's
-    tensors: same columns, same values, same order (ascending), nothing dropped."""
-    m, mg = packed(synth.small())
-    blob = bytes(mg.blob.numpy())
-    descs = (mega.LayerDesc * m.dims.n_layers).from_buffer_copy(bytes(mg.layers_d.numpy()))
-    for L, ly in enumerate(m.layers):
-        base = descs[L].hot
-        hot = mega.Hot.from_buffer_copy(blob[base:base + 64])
-        assert hot.size <= mega.HOT_MAX
-        units = mg.unit_order[L]  # the live units (lx/lx/fast.py:242-248), by row length
-        assert sorted(units.tolist()) == sorted(np.asarray(fast.Fast(m).dec[L]["units"]).tolist())
-        assert hot.n_units == len(units)
-        meta = np.frombuffer(blob[base + hot.unit:base + hot.unit + 4 * hot.n_units], np.uint32)
-        for j, u in enumerate(units):
-            st, ng, nu = int(meta[j] & 0xffff), int((meta[j] >> 16) & 255), int(meta[j] >> 24)
-            for rows, k0, cnt in ((ly.gate_proj, st, ng), (ly.up_proj, st + ng, nu)):
-                sel = rows.rows == u
-                got = [_ent(blob, base + hot.gu_ent, k0 + k) for k in range(cnt)]
-                assert [c for c, _ in got] == rows.cols[sel].tolist()
-                assert [float(v) for _, v in got] == rows.vals[sel].tolist()
-        # down rows: units ascending, all of a row's live terms
-        dptr = np.frombuffer(blob[base + hot.down_ptr:base + hot.down_ptr + 2 * (m.dims.hidden + 1)], np.uint16)
-        uidx = {int(u): j for j, u in enumerate(units)}
-        dn = ly.down_proj
-        for i in range(m.dims.hidden):
-            want = [(uidx[int(c)], float(v)) for c, v in zip(dn.cols[dn.rows == i], dn.vals[dn.rows == i])
-                    if int(c) in uidx]
-            got = [_ent(blob, base + hot.down_ent, k) for k in range(dptr[i], dptr[i + 1])]
-            assert [(int(c), float(v)) for c, v in got] == want
-        # out_proj by residual row over every value dim, ascending
-        oc = ly.out_proj
-        optr = np.frombuffer(blob[descs[L].out_ptr:descs[L].out_ptr + 4 * (m.dims.hidden + 1)], np.int32)
-        for i in range(m.dims.hidden):
-            sel = oc.rows == i
-            order = np.argsort(oc.cols[sel], kind="stable")
-            want = list(zip(oc.cols[sel][order].tolist(), oc.vals[sel][order].tolist()))
-            got = [_ent(blob, descs[L].out_ent, k, 1) for k in range(optr[i], optr[i + 1])]
-            assert [(int(c), float(v)) for c, v in got] == want
-    # head: rows x columns with a nonzero final weight
-    hptr = mg.head_ptr.numpy()
-    hent = bytes(mg.head_ent.numpy())
-    w1 = 1.0 + m.norm
-    E = m.embed
-    for v in (0, 7, m.dims.vocab - 1):
-        want = [(int(c), float(x)) for c, x in zip(E.cols[E.rows == v], E.vals[E.rows == v]) if w1[c] != 0]
-        got = [_ent(hent, 0, k) for k in range(hptr[v], hptr[v + 1])]
-        assert [(int(c), float(x)) for c, x in got] == want
+    tensors: same columns, same values, same order (ascending), nothing dropped; every table
+    slot past a row is padding that adds +0."""
+    for spec in (synth.small(), synth.config1()):
+        m, mg = packed(spec)
+        blob = bytes(mg.blob.numpy())
+        descs = (mega.LayerDesc * m.dims.n_layers).from_buffer_copy(bytes(mg.layers_d.numpy()))
+        H = m.dims.hidden
+        for L, ly in enumerate(m.layers):
+            S, units, rows = _chain_rows(mg, m, L, blob, descs[L])
+            order = mg.unit_order[L]  # the live units (lx/lx/fast.py:242-248), model order
+            assert order.tolist() == np.asarray(fast.Fast(m).dec[L]["units"]).tolist()
+            assert sorted(units) == list(range(len(order)))
+            for k, u in enumerate(order):
+                for coo, got in ((ly.gate_proj, units[k][0]), (ly.up_proj, units[k][1])):
+                    sel = coo.rows == u
+                    assert [c for c, _ in got] == coo.cols[sel].tolist()
+                    assert [v for _, v in got] == coo.vals[sel].tolist()
+            # down rows: live units in the model's order, all of a row's live terms
+            uidx = {int(u): j for j, u in enumerate(order)}
+            dn = ly.down_proj
+            for i in range(H):
+                want = [(uidx[int(c)], float(v)) for c, v in
+                        zip(dn.cols[dn.rows == i], dn.vals[dn.rows == i]) if int(c) in uidx]
+                assert rows.get(i, []) == want, (L, i)
+            # the MLP norm's weights of each thread's rows
+            f = chain.fmt(mg.e4)
+            w = np.zeros(4096, np.float32)
+            w[:H] = ly.post_attention_layernorm
+            for t in (0, 1, 300, 511):
+                rr = [4 * t + k for k in range(4)] + [2048 + 4 * t + k for k in range(4)]
+                got = S[t, f.W1:f.W1 + 8].astype(np.uint32).view(np.float32)
+                assert got.tolist() == (np.float32(1.0) + w[rr]).tolist()
+            # the gate tables: live query/key channels and their rows, in column order
+            gate = mega.Gate.from_buffer_copy(blob[descs[L].gate:descs[L].gate + 64])
+            qk = (mega.QkC * gate.n_qk).from_buffer_copy(
+                blob[descs[L].gate + gate.qk:descs[L].gate + gate.qk + 32 * gate.n_qk])
+            qkv = ly.in_proj_qkv
+            live = np.nonzero((np.asarray(ly.conv1d)[:2 * m.dims.nk * 256] != 0).any(1))[0]
+            assert [q.chan for q in qk] == live.tolist()
+            for q in qk:
+                sel = qkv.rows == q.chan
+                got = [_ent(blob, descs[L].gate + gate.ent, q.start + k) for k in range(q.len)]
+                assert [(int(c), float(v)) for c, v in got] == \
+                    list(zip(qkv.cols[sel].tolist(), qkv.vals[sel].tolist()))
+            # out_proj by residual row over every value dim, ascending
+            oc = ly.out_proj
+            optr = np.frombuffer(blob[descs[L].out_ptr:descs[L].out_ptr + 4 * (H + 1)], np.int32)
+            for i in range(0, H, 7):
+                sel = oc.rows == i
+                o2 = np.argsort(oc.cols[sel], kind="stable")
+                want = list(zip(oc.cols[sel][o2].tolist(), oc.vals[sel][o2].tolist()))
+                got = [_ent(blob, descs[L].out_ent, k, 1) for k in range(optr[i], optr[i + 1])]
+                assert [(int(c), float(v)) for c, v in got] == want
+        # head: rows x columns with a nonzero final weight
+        hptr = mg.head_ptr.numpy()
+        hent = bytes(mg.head_ent.numpy())
+        w1 = 1.0 + m.norm
+        E = m.embed
+        for v in (0, 7, m.dims.vocab - 1):
+            want = [(int(c), float(x)) for c, x in zip(E.cols[E.rows == v], E.vals[E.rows == v])
+                    if w1[c] != 0]
+            got = [_ent(hent, 0, k) for k in range(hptr[v], hptr[v + 1])]
+            assert [(int(c), float(x)) for c, x in got] == want
 
 
 def test_packer_fits_every_config(packed):
     for spec in (synth.config1(), synth.config2()):
         m, mg = packed(spec)
-        assert max(mg.stats["hot_bytes"]) <= mega.HOT_MAX
+        assert mg.gate_bytes <= mega.GATE_MAX
         assert mg.stats["qk_total"] <= mega.MAXQK
         assert mg.lds <= 163_840
         assert mg.e4  # every packed value is exact in bf16: 4-byte entries
