@@ -136,16 +136,27 @@ def pack_layer(f: Fmt, H: int, units, gate_rows, up_rows, down_rows, w_post) -> 
     meta0 = np.zeros(NT, np.uint64)
     G = np.zeros((2, NW), np.int64)
     sh = np.ones((2, NW), bool)
-    for p, (lst, base, gmax) in enumerate(((p0, f.U0, f.G0MAX), (p1, f.U1, f.G1MAX))):
-        for lane, k in enumerate(lst):
+    # lanes: P1 from lane 0 (wave 0 takes its longest units); P0 longest first over waves 1..5,
+    # then the lightest on wave 0 (the longest P1) and the top two waves (the gates)
+    lanes0 = list(range(64, NT - 128)) + list(range(64)) + list(range(NT - 128, NT))
+    p0 = sorted(p0, key=lambda k: -m[k])
+    placed = ((p0, lanes0, f.U0), (p1, list(range(NT)), f.U1))
+    for p, (lst, lanes, base) in enumerate(placed):
+        for k, lane in zip(lst, lanes):
             wv = lane // 64
             G[p, wv] = max(G[p, wv], m[k])
             sh[p, wv] &= bool(shared[k])
+    for p, (lst, lanes, base) in enumerate(placed):
+        for k, lane in zip(lst, lanes):
+            wv = lane // 64
             meta0[lane] |= np.uint64((k | 0x8000) << (16 * p))
             for j, (c, v) in enumerate(zip(*gate_rows[k])):
                 S[lane, base + 2 * esz * j:base + 2 * esz * j + esz] = _slots_of(f, 4 * c, v)
+            # (a wave whose pass shares columns reads the up slots as bare weights: offset 0)
+            bare = f.e4 and sh[p, wv]
             for j, (c, v) in enumerate(zip(*up_rows[k])):
-                S[lane, base + 2 * esz * j + esz:base + 2 * esz * (j + 1)] = _slots_of(f, 4 * c, v)
+                S[lane, base + 2 * esz * j + esz:base + 2 * esz * (j + 1)] = \
+                    _slots_of(f, 0 if bare else 4 * c, v)
     assert n < 1 << 12
     S[:, f.MA + 0] = meta0
 
@@ -168,11 +179,13 @@ def pack_layer(f: Fmt, H: int, units, gate_rows, up_rows, down_rows, w_post) -> 
             continue
         q = qs[0]
         place[int(r)] = (q, free[q].pop(0))
-    rowf = np.full((NT, 6), NONE16, np.uint64)
+    # where each pass's sum goes: the byte offset from dsum of its row, else of the lane's dummy
+    # slot (the kernel's L_DUMMY follows dsum's 4096 rows)
+    rowf = np.tile((4 * 4096 + 4 * np.arange(NT, dtype=np.uint64))[:, None], (1, 6))
     dmask = np.zeros(NW, np.int64)
     doff = f.doff
     for r, (q, lane) in place.items():
-        rowf[lane, q] = r
+        rowf[lane, q] = 4 * r
         dmask[lane // 64] |= 1 << q
         for j, (a, v) in enumerate(zip(*down_rows[r])):
             s0 = f.D + esz * (doff[q] + j)

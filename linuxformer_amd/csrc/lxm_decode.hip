@@ -56,6 +56,7 @@ static_assert(MAXH == 8 * NT, "eight residual rows per thread cover any hidden s
 #define L_H (L_XM + 4 * MAXH)         // float[MAXH]: the residual (the gates gather from it)
 #define L_DSUM (L_H + 4 * MAXH)       // float[MAXH]: down_proj's row sums
 #define L_DUMMY (L_DSUM + 4 * MAXH)   // float[NT]: where a lane with no row in a pass writes
+static_assert(L_DUMMY - L_DSUM + 4 * NT <= 65536, "down write offsets in 16 bits");
 #define L_HIST (L_DUMMY + 4 * NT)     // the live q/k channels' conv history, 3 per channel
 #define L_QKCUR (L_HIST + 4 * 3 * LXM_MAXQK)
 #define L_EV (L_QKCUR + 4 * LXM_MAXQKL)
@@ -562,8 +563,12 @@ __device__ __forceinline__ v4f rd4(v4f v) {
 // meta A: +0 the P0 unit's act index (bits 0-11, valid bit 15) and the P1 unit's (16-27, valid
 // bit 31); +1 the lane's long unit (0-15, 0xffff = none); +2 (equal across the wave) G0 (0-3),
 // G1 (4-7), shared columns in P0 (8) and P1 (9), any long unit (10).
-// meta B: +0..+2 the down passes' rows, 16 bits each (0xffff = none); +3 the lane's long row
-// (0-15, 0xffff = none), the wave's down passes present (16-23) and any long row (24).
+// meta B: +0..+2 where each down pass's sum goes, 16 bits each: the byte offset from dsum of its
+// row (4 row), or of the lane's dummy slot (L_DUMMY - L_DSUM + 4 lane) when it has none; +3 the
+// lane's long row (0-15, 0xffff = none), the wave's down passes present (16-23) and any long
+// row (24).
+// A shared-column unit pass's up slots hold the weight alone (its offset bits 0), so the weight
+// needs no mask.
 template <bool E4>
 struct PT;
 template <>
@@ -707,7 +712,8 @@ __device__ __forceinline__ float unit_pass(const RU& ru, int base, int G, bool s
       int o;
       float wg, wu;
       ent_of<E4>(ru, base + 2 * ESZ * j, o, wg);
-      ent_of<E4>(ru, base + 2 * ESZ * j + ESZ, o, wu);
+      if (E4 && shared) wu = __uint_as_float(ru.slot(base + 2 * j + 1));
+      else ent_of<E4>(ru, base + 2 * ESZ * j + ESZ, o, wu);
       g = acc<BF>(g, x[j], wg);
       u = acc<BF>(u, y[j], wu);
     }
@@ -777,9 +783,8 @@ __device__ __forceinline__ void down_rows(const uint8_t* gt, const typename Regi
         ent_of<E4>(rdw, F::D + ESZ * (F::doff(q) + j), o, w);
         s = acc<BF>(s, x[q][j], w);
       }
-      const uint32_t row = (rdw.slot(F::MB + q / 2) >> (16 * (q & 1))) & 0xffffu;
-      const int addr = row != 0xffffu ? L_DSUM + 4 * (int)row : L_DUMMY + 4 * t;
-      *reinterpret_cast<float*>(smem + addr) = s;
+      const uint32_t wo = (rdw.slot(F::MB + q / 2) >> (16 * (q & 1))) & 0xffffu;
+      *reinterpret_cast<float*>(smem + L_DSUM + wo) = s;
     }
   }
   rdw.keep();
@@ -796,7 +801,8 @@ __device__ __forceinline__ void down_rows(const uint8_t* gt, const typename Regi
 // The gates: the live query/key channels' projections, conv windows (history in LDS) and silu
 // (causal_conv1d_update :199-216), and the decays g = -exp(A_log) softplus(a + dt_bias) (:499).
 // Flags per key head: 1 query nonzero, 2 key nonzero, 4 a decay exp(g) != 1; F_ANY and F_OUT
-// directly. Items run on the threads from the top down.
+// directly. Items run on the threads from the top down: the query/key channels on the top
+// wave(s), the decays on the wave(s) below.
 // a gate row's dot product with the GDN norm's output D((h * r) * (1 + w_in)), formed per entry
 // (w1e: the norm weight at each entry's column); slots past the row add nothing
 template <bool BF, bool E4>
@@ -855,8 +861,10 @@ __device__ __forceinline__ void gates(const ChainK& k, const uint8_t* gt, float 
       if (!isk) atomicOr(&flags[F_OUT], 1);
     }
   }
+  // the decays on the wave(s) below the query/key channels' (a wave runs one kind of gate)
   const lxm_dec* dc = reinterpret_cast<const lxm_dec*>(gt + hd.dec);
-  for (int j = ((tt - hd.n_qk) % NT + NT) % NT; j < hd.n_dec; j += NT) {
+  const int tq = ((hd.n_qk + 63) >> 6) << 6;
+  for (int j = ((tt - tq) % NT + NT) % NT; j < hd.n_dec; j += NT) {
     const lxm_dec d = dc[j];
     const float a = rd<BF>(ndot<BF, E4>(ent, d.start, d.len, r, w1in));
     const float x = a + d.dt_bias;

@@ -136,6 +136,9 @@ def _chain_rows(mg, m, L, blob, desc):
             G = (m2 >> (4 * p)) & 15
             gl = [_slot_ent(S[lane], base + 2 * j) for j in range(G)]
             ul = [_slot_ent(S[lane], base + 2 * j + 1) for j in range(G)]
+            if (m2 >> (8 + p)) & 1:  # shared columns: the up slots hold bare weights
+                assert all(c == 0 for c, _ in ul)
+                ul = [(gl[j][0] if ul[j] != (0, 0.0) else 0, ul[j][1]) for j in range(G)]
             ng = len(m.layers[L].gate_proj.cols[m.layers[L].gate_proj.rows == mg.unit_order[L][k]])
             nu = len(m.layers[L].up_proj.cols[m.layers[L].up_proj.rows == mg.unit_order[L][k]])
             if (m2 >> (8 + p)) & 1:  # shared columns
@@ -144,9 +147,11 @@ def _chain_rows(mg, m, L, blob, desc):
             units[k] = (trim(gl, ng), trim(ul, nu))
         mask = (mb3 >> 16) & 255
         for q, ln in enumerate(f.DLEN):
-            row = (int(S[lane, f.MB + q // 2]) >> (16 * (q & 1))) & 0xffff
-            if row == 0xffff:
+            wo = (int(S[lane, f.MB + q // 2]) >> (16 * (q & 1))) & 0xffff
+            if wo == 4 * 4096 + 4 * lane:  # the lane's dummy slot: no row in this pass
                 continue
+            assert wo % 4 == 0 and wo < 4 * m.dims.hidden
+            row = wo // 4
             assert mask & (1 << q)
             ents = [_slot_ent(S[lane], f.D + f.doff[q] + j) for j in range(ln)]
             n = len(m.layers[L].down_proj.cols[m.layers[L].down_proj.rows == row])
