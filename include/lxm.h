@@ -40,7 +40,7 @@ extern "C" {
    into the thread's registers one layer ahead. Slots (uint32) in a fixed layout: the MLP norm's
    weights of the thread's residual rows (4t..4t+3, 2048+4t..2048+4t+3), meta words, two unit
    passes (gate/up entries interleaved) and down-row passes; see the kernel's PT<E4>. */
-#define LXM_PT_WORDS 16
+#define LXM_PT_WORDS 15
 
 /* One layer's gate tables: the live query/key channels and the decaying value heads, and the
    long units and rows of the chain's per-thread table (resident in the chain's LDS for a launch;
@@ -89,6 +89,8 @@ typedef struct lxm_row { int32_t start, len; } lxm_row;
 /* One layer: byte offsets into the packed blob. */
 typedef struct lxm_layer {
   int64_t ptt;             /* the chain's per-thread table */
+  int64_t pt_words;        /* byte w: the words of its unit region (low nibble) and down region
+                              (high nibble) wave w loads (the rest of its slots are unused) */
   int64_t gate;            /* lxm_gate + its tables (inside the gate section) */
   int64_t chan;            /* lxm_chan[n_conv] */
   int64_t qkv_ent;         /* entries (column) */

@@ -6,7 +6,7 @@ the chain never stages tables through LDS: thread t reads words t, NT + t, 2 NT 
 layer's *per-thread table*, i.e. a wave reads 1 KB runs. A thread's words are slots (uint32) in a
 fixed layout, the same for every layer:
 
-    w1     1 + the MLP norm's weights (fp32) of the thread's rows 4t..4t+3, 2048+4t..2048+4t+3
+    w1     the MLP norm's weights of the thread's residual rows 4t..4t+3, 2048+4t..2048+4t+3
     meta A its units' act indices, its long unit, the wave's unit pass bounds
     P0, P1 two unit passes: a unit whose gate and up rows have at most G0MAX (P0) or G1MAX (P1)
            entries, entry j of the gate row and of the up row interleaved (gate j, up j, ...),
@@ -63,7 +63,7 @@ class Fmt:
         return tuple(int(x) for x in np.concatenate([[0], np.cumsum(self.DLEN)[:-1]]))
 
 
-FMT_E4 = Fmt(True, W1=0, MA=8, U0=12, U1=18, MB=44, D=48, WORDS=16, G0MAX=3, G1MAX=13,
+FMT_E4 = Fmt(True, W1=0, MA=4, U0=8, U1=14, MB=40, D=44, WORDS=15, G0MAX=3, G1MAX=13,
              DLEN=(1, 1, 1, 2, 4, 6))
 FMT_E8 = Fmt(False, W1=0, MA=8, U0=12, U1=20, MB=36, D=40, WORDS=13, G0MAX=2, G1MAX=4,
              DLEN=(1, 1, 2, 2))
@@ -96,6 +96,7 @@ def _slots_of(f: Fmt, off: int, val: float) -> list:
 @dataclass
 class LayerTables:
     ptt: bytes          # WORDS x NT 16-byte words, word j of thread t at (j * NT + t) * 16
+    wave_words: int     # byte w: the RU words (low nibble) and RB words (high nibble) wave w loads
     long_u: bytes       # lxm_longu[n]
     long_r: bytes       # lxm_longr[n]
     long_ent: bytes     # their entries (unit: byte offsets into xm; row: into act)
@@ -118,8 +119,12 @@ def pack_layer(f: Fmt, H: int, units, gate_rows, up_rows, down_rows, w_post) -> 
     rows = np.concatenate([4 * np.arange(NT)[:, None] + np.arange(4)[None],
                            2048 + 4 * np.arange(NT)[:, None] + np.arange(4)[None]], 1)
     wt = w[rows]  # (NT, 8)
-    # 1 + w in fp32, as (1.0 + weight.float()) forms it (IEEE binary32 addition)
-    S[:, f.W1:f.W1 + 8] = (np.float32(1.0) + wt).astype(np.float32).view(np.uint32)
+    if f.e4:  # the raw weights' bf16 bits, two per slot (the kernel forms 1 + w in fp32)
+        b = _bf16_bits(wt).astype(np.uint64)
+        for k in range(4):
+            S[:, f.W1 + k] = b[:, 2 * k] | (b[:, 2 * k + 1] << 16)
+    else:  # 1 + w in fp32, as (1.0 + weight.float()) forms it
+        S[:, f.W1:f.W1 + 8] = (np.float32(1.0) + wt).astype(np.float32).view(np.uint32)
 
     # ---- units: passes P0 (rows <= G0MAX) and P1 (<= G1MAX), the rest long
     n = len(units)
@@ -235,6 +240,23 @@ def pack_layer(f: Fmt, H: int, units, gate_rows, up_rows, down_rows, w_post) -> 
         wb = (int(dmask[wv]) << 16) | (int(anyr[wv]) << 24)
         S[wv * 64:(wv + 1) * 64, f.MB + 3] = long_r_idx[wv * 64:(wv + 1) * 64] | np.uint64(wb)
 
+    # ---- the words each wave loads of the unit and down regions (its passes' last slots)
+    ru_a, rb_a = f.U0 // 4, f.MB // 4
+    wave_words = 0
+    for wv in range(NW):
+        last_u = -1
+        if G[1, wv]:
+            last_u = f.U1 + 2 * esz * int(G[1, wv]) - 1
+        elif G[0, wv]:
+            last_u = f.U0 + 2 * esz * int(G[0, wv]) - 1
+        nu = 0 if last_u < 0 else last_u // 4 - ru_a + 1
+        last_d = f.MB + 3
+        for q in range(nq):
+            if dmask[wv] >> q & 1:
+                last_d = max(last_d, f.D + esz * (doff[q] + f.DLEN[q]) - 1)
+        nb = last_d // 4 - rb_a + 1
+        assert nu <= (f.MB - f.U0) // 4 < 16 and nb <= f.WORDS - rb_a < 16
+        wave_words |= (nu | (nb << 4)) << (8 * wv)
     assert S.max() < 1 << 32
     # thread-interleaved words: word j of thread t at (j * NT + t)
     words = S.astype(np.uint32).reshape(NT, f.WORDS, 4).transpose(1, 0, 2)
@@ -244,7 +266,10 @@ def pack_layer(f: Fmt, H: int, units, gate_rows, up_rows, down_rows, w_post) -> 
              "unit_fill": round(used_g / max(slots_g, 1), 3), "G": G.tolist(),
              "down_mask": dmask.tolist()}
     ent_arr = np.array(ents, np.uint32).reshape(-1) if ents else np.zeros(0, np.uint32)
-    return LayerTables(ptt=words.tobytes(),
+    # 16-byte words a thread loads per layer, averaged over the waves
+    stats["words_per_thread"] = sum(f.U0 // 4 + ((wave_words >> (8 * w)) & 15) +
+                                    ((wave_words >> (8 * w + 4)) & 15) for w in range(NW)) / NW
+    return LayerTables(ptt=words.tobytes(), wave_words=wave_words,
                        long_u=b"".join(x.tobytes() for x in lu),
                        long_r=b"".join(x.tobytes() for x in lr),
                        long_ent=ent_arr.tobytes(), stats=stats)

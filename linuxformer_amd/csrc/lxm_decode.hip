@@ -64,7 +64,7 @@ static_assert(L_DUMMY - L_DSUM + 4 * NT <= 65536, "down write offsets in 16 bits
 #define L_FLAGS (L_WSUM + 4 * 32)
 #define L_PROF (L_FLAGS + 4 * 256)
 #define L_LT (L_PROF + 8 * 32)        // the layer table (LtEnt[64])
-#define L_PARAMS (L_LT + 16 * 64)     // the chain's copy of the parameter block
+#define L_PARAMS (L_LT + 32 * 64)     // the chain's copy of the parameter block
 #define L_GATES (L_PARAMS + 512)      // the gate section, resident for the launch
 #define L_SUBP (L_GATES + LXM_GATE_MAX + 64)  // (gate gathers read up to 4 entries past a row)
 #ifdef LXM_SUBPROF
@@ -524,7 +524,13 @@ __device__ __forceinline__ float sum512_take(const float* wsum) {
 struct LtEnt {
   const uint8_t* ptt;
   int32_t goff, pad;
+  uint8_t words[8];  // per wave: the words of RU (low nibble) and RB (high nibble) it loads
+  int32_t pad2[2];
 };
+// the words wave w of this thread loads of a layer's RU and RB regions
+__device__ __forceinline__ uint32_t wave_words(const LtEnt* le) {
+  return __builtin_amdgcn_readfirstlane((uint32_t)le->words[threadIdx.x >> 6]);
+}
 // The parameters the chain reads at every layer, read once into registers (a read of the
 // parameter block, in LDS, would cost an LDS round trip per use)
 struct ChainK {
@@ -573,7 +579,7 @@ template <bool E4>
 struct PT;
 template <>
 struct PT<true> {
-  static constexpr int ESZ = 1, W1 = 0, MA = 8, U0 = 12, U1 = 18, MB = 44, D = 48, WORDS = 16;
+  static constexpr int ESZ = 1, W1 = 0, MA = 4, U0 = 8, U1 = 14, MB = 40, D = 44, WORDS = 15;
   static constexpr int G0MAX = 3, G1MAX = 13, ND = 6;
   __host__ __device__ static constexpr int dlen(int q) {
     return q < 3 ? 1 : q == 3 ? 2 : q == 4 ? 4 : 6;
@@ -604,12 +610,17 @@ struct Words {
     for (int k = 0; k < N; k++) asm volatile("" ::"v"(w[k]));
   }
 };
+// (the first n of them: a wave loads only the words its passes use, n equal across the wave;
+// the others stay unused)
 template <int A, int N>
-__device__ __forceinline__ Words<A, N> fetch_words(const uint8_t* ptt) {
+__device__ __forceinline__ Words<A, N> fetch_words(const uint8_t* ptt, int n = N) {
   const GAS v4u* src = gp(reinterpret_cast<const v4u*>(ptt)) + threadIdx.x;
   Words<A, N> r;
 #pragma unroll
-  for (int k = 0; k < N; k++) r.w[k] = src[(A + k) * NT];
+  for (int k = 0; k < N; k++) {
+    if (k < n) r.w[k] = src[(A + k) * NT];
+    else r.w[k] = v4u{0, 0, 0, 0};
+  }
   return r;
 }
 template <bool E4>
@@ -636,12 +647,20 @@ __device__ __forceinline__ void ent_of(const W& r, int s, int& off, float& w) {
 }
 #define ACT_MASK (4 * LXM_MAXU - 4)
 
-// the MLP norm's weights 1 + w of the thread's rows (fp32: the packer forms 1 + w as
-// (1.0 + weight.float()) does)
+// the MLP norm's weights 1 + w of the thread's rows: e4 the raw weights' bf16 bits (1 + w formed
+// in fp32, as (1.0 + weight.float()) does), else 1 + w as fp32
 template <bool E4>
 __device__ __forceinline__ void w1_of(const typename Regions<E4>::RA& r1, v4f& wa, v4f& wb) {
-  wa = __builtin_bit_cast(v4f, r1.w[0]);
-  wb = __builtin_bit_cast(v4f, r1.w[1]);
+  if constexpr (E4) {
+    const v4u s = r1.w[0];
+    wa = v4f{1.0f + __uint_as_float(s.x << 16), 1.0f + __uint_as_float(s.x & 0xffff0000u),
+             1.0f + __uint_as_float(s.y << 16), 1.0f + __uint_as_float(s.y & 0xffff0000u)};
+    wb = v4f{1.0f + __uint_as_float(s.z << 16), 1.0f + __uint_as_float(s.z & 0xffff0000u),
+             1.0f + __uint_as_float(s.w << 16), 1.0f + __uint_as_float(s.w & 0xffff0000u)};
+  } else {
+    wa = __builtin_bit_cast(v4f, r1.w[0]);
+    wb = __builtin_bit_cast(v4f, r1.w[1]);
+  }
 }
 
 // silu and the MLP product for one unit (Qwen3_5MLP :715): D(D(silu(D(g))) * D(u))
@@ -937,7 +956,7 @@ __device__ __forceinline__ bool layer(const lxm_params& p, const ChainK& k, int 
                                       float ss, int par,
                                       v4f& ha, v4f& hb, typename Regions<E4>::RA& r1,
                                       typename Regions<E4>::RU& ru, typename Regions<E4>::RB& rdw,
-                                      const uint8_t* ptt_next, uint32_t& seq, uint32_t& target) {
+                                      const LtEnt* lnext, uint32_t& seq, uint32_t& target) {
   using RG = Regions<E4>;
   const int t = threadIdx.x, H = k.H;
   const LtEnt le = reinterpret_cast<const LtEnt*>(smem + L_LT)[L];
@@ -990,8 +1009,10 @@ __device__ __forceinline__ bool layer(const lxm_params& p, const ChainK& k, int 
     sp_skip();
   }
   // the next layer's RA and unit passes into the registers this layer's have left
+  const uint8_t* ptt_next = lnext->ptt;
+  const uint32_t nwords = wave_words(lnext);
   r1 = fetch_words<RG::RAA, RG::RAN>(ptt_next);
-  ru = fetch_words<RG::RUA, RG::RUN>(ptt_next);
+  ru = fetch_words<RG::RUA, RG::RUN>(ptt_next, (int)(nwords & 15u));
   // ---- stage C1: down_proj by residual row (units in the model's order) into dsum
   down_rows<BF, E4>(gt, rdw);
   sp_arrive(2);
@@ -1002,7 +1023,7 @@ __device__ __forceinline__ bool layer(const lxm_params& p, const ChainK& k, int 
     pa[5] += c1 - c0;
     c0 = c1;
   }
-  rdw = fetch_words<RG::RBA, RG::RBN>(ptt_next);
+  rdw = fetch_words<RG::RBA, RG::RBN>(ptt_next, (int)(nwords >> 4));
   // ---- stage C2: the residual add on the thread's rows (:791), the LDS copy, and this
   // thread's terms of the next sum of squares (rows past H stay +0)
   {
@@ -1068,6 +1089,7 @@ __device__ void run_chain(const lxm_params& pg) {
     const lxm_layer ly = ldg(p.layers + L);
     lt[L].ptt = p.blob + ly.ptt;
     lt[L].goff = (int32_t)(ly.gate - gsec);
+    *reinterpret_cast<int64_t*>(lt[L].words) = ly.pt_words;
   }
   __syncthreads();
   // the live query/key channels' windows from the conv state (positions 1..3)
@@ -1084,8 +1106,8 @@ __device__ void run_chain(const lxm_params& pg) {
   __syncthreads();
   // the first layer's tables; then always one layer ahead
   typename RG::RA r1 = fetch_words<RG::RAA, RG::RAN>(lt[0].ptt);
-  typename RG::RU ru = fetch_words<RG::RUA, RG::RUN>(lt[0].ptt);
-  typename RG::RB rdw = fetch_words<RG::RBA, RG::RBN>(lt[0].ptt);
+  typename RG::RU ru = fetch_words<RG::RUA, RG::RUN>(lt[0].ptt, (int)(wave_words(lt) & 15u));
+  typename RG::RB rdw = fetch_words<RG::RBA, RG::RBN>(lt[0].ptt, (int)(wave_words(lt) >> 4));
   // the final norm's weights of this thread's rows (padded to MAXH)
   const v4f wfa = *reinterpret_cast<const v4f*>(p.w1_final + 4 * t);
   const v4f wfb = *reinterpret_cast<const v4f*>(p.w1_final + 2048 + 4 * t);
@@ -1120,7 +1142,7 @@ __device__ void run_chain(const lxm_params& pg) {
     sp_skip();
     for (int L = 0; L < k.nl; L++) {
       const int Ln = L + 1 < k.nl ? L + 1 : 0;
-      if (!layer<BF, E4>(p, k, L, i, ss, par, ha, hb, r1, ru, rdw, lt[Ln].ptt, seq, target)) return;
+      if (!layer<BF, E4>(p, k, L, i, ss, par, ha, hb, r1, ru, rdw, lt + Ln, seq, target)) return;
       if constexpr (TR) trace_rows(p.trace + ((size_t)i * k.nl + L) * H, H, ha, hb);
       ss = sum512_take(LF(L_WSUM) + 8 * par);
       par ^= 1;

@@ -50,7 +50,7 @@ class Chan(ctypes.Structure):
 
 
 class LayerDesc(ctypes.Structure):
-    _fields_ = [(n, I64) for n in ("ptt", "gate")] + \
+    _fields_ = [(n, I64) for n in ("ptt", "pt_words", "gate")] + \
         [(n, I64) for n in ("chan", "qkv_ent", "b_row", "b_ent", "z_row", "z_ent", "out_ptr",
                             "out_ent", "gnorm", "w1_in")]
 
@@ -68,7 +68,7 @@ class Params(ctypes.Structure):
 
 
 assert ctypes.sizeof(Gate) == 64 and ctypes.sizeof(QkC) == 32 and ctypes.sizeof(Dec) == 32
-assert ctypes.sizeof(Chan) == 24 and ctypes.sizeof(LayerDesc) == 96
+assert ctypes.sizeof(Chan) == 24 and ctypes.sizeof(LayerDesc) == 104
 
 
 def _bf16_bits(v: np.ndarray) -> np.ndarray:
@@ -322,6 +322,7 @@ class Mega:
             desc = descs[L]
             desc.gate += gsec
             desc.ptt = blob.add(ct.ptt)
+            desc.pt_words = ct.wave_words
         blob.add(bytes(4096))  # padding past the last table
         self.blob = torch.frombuffer(bytearray(blob.bytes()), dtype=torch.uint8).to(dev)
         self.layers_d = torch.frombuffer(bytearray(bytes(descs)), dtype=torch.uint8).to(dev)

@@ -204,8 +204,17 @@ def test_packer_tables_decode_to_the_model(packed):
             w[:H] = ly.post_attention_layernorm
             for t in (0, 1, 300, 511):
                 rr = [4 * t + k for k in range(4)] + [2048 + 4 * t + k for k in range(4)]
-                got = S[t, f.W1:f.W1 + 8].astype(np.uint32).view(np.float32)
-                assert got.tolist() == (np.float32(1.0) + w[rr]).tolist()
+                bits16 = [(int(S[t, f.W1 + k // 2]) >> (16 * (k % 2))) & 0xffff for k in range(8)]
+                assert [np.uint32(b << 16).view(np.float32) for b in bits16] == w[rr].tolist()
+            # each wave loads every word its passes read
+            ww = int(descs[L].pt_words)
+            for wv in range(8):
+                nu, nb = (ww >> (8 * wv)) & 15, (ww >> (8 * wv + 4)) & 15
+                lanes = S[64 * wv:64 * wv + 64]
+                used_u = np.nonzero(lanes[:, f.U0:f.MB].any(0))[0]
+                used_b = np.nonzero(lanes[:, f.MB:].any(0))[0]
+                assert len(used_u) == 0 or used_u.max() // 4 < nu
+                assert used_b.max() // 4 < nb
             # the gate tables: live query/key channels and their rows, in column order
             gate = mega.Gate.from_buffer_copy(blob[descs[L].gate:descs[L].gate + 64])
             qk = (mega.QkC * gate.n_qk).from_buffer_copy(
