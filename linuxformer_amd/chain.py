@@ -64,7 +64,7 @@ class Fmt:
 
 
 FMT_E4 = Fmt(True, W1=0, MA=4, U0=8, U1=14, MB=40, D=44, WORDS=15, G0MAX=3, G1MAX=13,
-             DLEN=(1, 1, 1, 2, 4, 6))
+             DLEN=(1, 1, 2, 1, 4, 6))
 FMT_E8 = Fmt(False, W1=0, MA=8, U0=12, U1=20, MB=36, D=40, WORDS=13, G0MAX=2, G1MAX=4,
              DLEN=(1, 1, 2, 2))
 NONE16 = 0xFFFF

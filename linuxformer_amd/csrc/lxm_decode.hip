@@ -420,8 +420,9 @@ __device__ __forceinline__ void conv_put(void* cs, int64_t i, float v) {
 }
 
 // The ring of the last four steps' layer inputs (the residual before the GDN's norm): slot
-// (step & 3), layer L, MAXH floats each, and each entry's norm factor r (rring). The GDN norm's
-// output of a step is D((h * r) * (1 + w_in)) from them.
+// (step & 3), layer L, MAXH floats each (bf16 models: MAXH bf16 values, the residual being
+// bf16-exact there), and each entry's norm factor r (rring). The GDN norm's output of a step is
+// D((h * r) * (1 + w_in)) from them.
 __device__ __forceinline__ float* ring_at(const lxm_params& p, int step, int L) {
   return p.ring + ((size_t)(step & 3) * p.n_layers + L) * MAXH;
 }
@@ -435,6 +436,17 @@ __device__ __forceinline__ void st4_rlx(float* base, int idx, v4f v) {
   typedef uint32_t v4u_ __attribute__((ext_vector_type(4)));
   __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(v4u_, v), r, idx * 4, 0, 16);
 }
+typedef uint32_t v2u __attribute__((ext_vector_type(2)));
+// 8 bytes to global memory at agent scope (idx in 32-bit words)
+__device__ __forceinline__ void st2_rlx(float* base, int idx, v2u v) {
+  const __amdgpu_buffer_rsrc_t r = __builtin_amdgcn_make_buffer_rsrc(base, 0, 0x7fffffff, 0x00020000);
+  __builtin_amdgcn_raw_buffer_store_b64(v, r, idx * 4, 0, 16);
+}
+// four bf16-exact floats as their bf16 bits, two per word (low half first)
+__device__ __forceinline__ v2u pack_bf16(const v4f& v) {
+  return v2u{(__float_as_uint(v.x) >> 16) | (__float_as_uint(v.y) & 0xffff0000u),
+             (__float_as_uint(v.z) >> 16) | (__float_as_uint(v.w) & 0xffff0000u)};
+}
 // one norm weight 1 + w of column c from a layer's w1 table (LDS or global)
 template <bool E4, bool GLOBAL>
 __device__ __forceinline__ float w1_one(const uint8_t* tab, int c) {
@@ -444,6 +456,16 @@ __device__ __forceinline__ float w1_one(const uint8_t* tab, int c) {
     return 1.0f + bf16f(b);
   } else {
     return GLOBAL ? gp(reinterpret_cast<const float*>(tab))[c] : reinterpret_cast<const float*>(tab)[c];
+  }
+}
+// the ring value at byte offset off of a float vector (agent-scope load)
+template <bool BF>
+__device__ __forceinline__ float ring_val(const float* hs, int off) {
+  if constexpr (BF) {
+    const uint32_t w = ld_rlx(reinterpret_cast<const uint32_t*>(hs) + (off >> 3));
+    return __uint_as_float((off & 4) ? (w & 0xffff0000u) : (w << 16));
+  } else {
+    return ld_rlxf(reinterpret_cast<const float*>(reinterpret_cast<const uint8_t*>(hs) + off));
   }
 }
 // A row's dot product (entries in global memory, chunk's rules) with the GDN norm's output of
@@ -463,7 +485,7 @@ __device__ __forceinline__ float rdot(const uint8_t* ent, int64_t start, int n, 
     }
 #pragma unroll
     for (int j = 0; j < 4; j++) {
-      hv[j] = ld_rlxf(reinterpret_cast<const float*>(reinterpret_cast<const uint8_t*>(hs) + i[j]));
+      hv[j] = ring_val<BF>(hs, i[j]);
       wi[j] = w1_one<E4, true>(w1in, i[j] >> 2);
     }
     // (a slot past the row may name a column past the weights: its term is dropped, not
@@ -581,11 +603,12 @@ template <>
 struct PT<true> {
   static constexpr int ESZ = 1, W1 = 0, MA = 4, U0 = 8, U1 = 14, MB = 40, D = 44, WORDS = 15;
   static constexpr int G0MAX = 3, G1MAX = 13, ND = 6;
+  // (the passes every wave uses first: a wave loads the words up to its last pass)
   __host__ __device__ static constexpr int dlen(int q) {
-    return q < 3 ? 1 : q == 3 ? 2 : q == 4 ? 4 : 6;
+    return q == 2 ? 2 : q == 4 ? 4 : q == 5 ? 6 : 1;
   }
   __host__ __device__ static constexpr int doff(int q) {
-    return q < 3 ? q : q == 3 ? 3 : q == 4 ? 5 : 9;
+    return q == 0 ? 0 : q == 1 ? 1 : q == 2 ? 2 : q == 3 ? 4 : q == 4 ? 5 : 9;
   }
 };
 template <>
@@ -695,61 +718,97 @@ __device__ __forceinline__ void stage_a(const ChainK& k, const typename Regions<
   d4[NT + t] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
   if (ring) {
     float* rg = ring_k(k, step, L);
-    st4_rlx(rg, 4 * t, ha);
-    st4_rlx(rg, 2048 + 4 * t, hb);
+    if constexpr (BF) {  // four bf16 values in 8 bytes
+      st2_rlx(rg, 2 * t, pack_bf16(ha));
+      st2_rlx(rg, 1024 + 2 * t, pack_bf16(hb));
+    } else {
+      st4_rlx(rg, 4 * t, ha);
+      st4_rlx(rg, 2048 + 4 * t, hb);
+    }
     if (t == 0) st_rlxf(rr_k(k, step, L), r);
   }
 }
 
 // A unit pass: each lane's unit (gate row and up row, entries interleaved from slot base) over
-// xm, padded to the wave's G entries, then act[u] = swiglu. Gathers first, then the sums (each
-// row in entry order from +0; a padding entry adds +0).
-template <bool BF, bool E4, int GMAX, class RU>
-__device__ __forceinline__ float unit_pass(const RU& ru, int base, int G, bool shared) {
+// xm, padded to the wave's G entries, then act[u] = swiglu. Straight-line code for each G (equal
+// across the wave, dispatched at run time): every gather of both passes first, then the sums
+// (each row in entry order from +0; a padding entry adds +0), so the gathers' latencies overlap.
+// (the gathered values travel as vector values, which stay in registers)
+template <int GM>
+struct PV {
+  typedef float T __attribute__((ext_vector_type(GM <= 4 ? 4 : 16)));
+  T x, y;
+};
+template <bool E4, int G, bool SH, int GM, class RU>
+__device__ __forceinline__ PV<GM> pass_gather(const RU& ru, int base) {
   constexpr int ESZ = PT<E4>::ESZ;
   const float* xm = LF(L_XM);
-  float x[GMAX], y[GMAX];
+  PV<GM> v;
 #pragma unroll
-  for (int j = 0; j < GMAX; j++) {
-    if (j < G) {
-      int o;
-      float w;
-      ent_of<E4>(ru, base + 2 * ESZ * j, o, w);
-      x[j] = at_b(xm, o & OFF_MASK);
-      if (!shared) {
-        ent_of<E4>(ru, base + 2 * ESZ * j + ESZ, o, w);
-        y[j] = at_b(xm, o & OFF_MASK);
-      } else {
-        y[j] = x[j];
-      }
+  for (int j = 0; j < G; j++) {
+    int o;
+    float w;
+    ent_of<E4>(ru, base + 2 * ESZ * j, o, w);
+    v.x[j] = at_b(xm, o & OFF_MASK);
+    if constexpr (!SH) {
+      ent_of<E4>(ru, base + 2 * ESZ * j + ESZ, o, w);
+      v.y[j] = at_b(xm, o & OFF_MASK);
     }
   }
+  return v;
+}
+template <bool BF, bool E4, int G, bool SH, int GM, class RU>
+__device__ __forceinline__ v2f pass_sum(const RU& ru, int base, const PV<GM>& v) {
+  constexpr int ESZ = PT<E4>::ESZ;
   float g = 0.0f, u = 0.0f;
 #pragma unroll
-  for (int j = 0; j < GMAX; j++) {
-    if (j < G) {
-      int o;
-      float wg, wu;
-      ent_of<E4>(ru, base + 2 * ESZ * j, o, wg);
-      if (E4 && shared) wu = __uint_as_float(ru.slot(base + 2 * j + 1));
-      else ent_of<E4>(ru, base + 2 * ESZ * j + ESZ, o, wu);
-      g = acc<BF>(g, x[j], wg);
-      u = acc<BF>(u, y[j], wu);
-    }
+  for (int j = 0; j < G; j++) {
+    int o;
+    float wg, wu;
+    ent_of<E4>(ru, base + 2 * ESZ * j, o, wg);
+    if constexpr (E4 && SH) wu = __uint_as_float(ru.slot(base + 2 * j + 1));
+    else ent_of<E4>(ru, base + 2 * ESZ * j + ESZ, o, wu);
+    g = acc<BF>(g, v.x[j], wg);
+    u = acc<BF>(u, SH ? v.x[j] : v.y[j], wu);
   }
-  return swiglu<BF>(g, u);
+  return v2f{g, u};
+}
+template <bool E4, int N, int GM, class RU>
+__device__ __forceinline__ PV<GM> gather_g(const RU& ru, int base, int G, bool sh) {
+  if constexpr (N >= 1) {
+    if (G == N) return sh ? pass_gather<E4, N, true, GM>(ru, base) : pass_gather<E4, N, false, GM>(ru, base);
+    return gather_g<E4, N - 1, GM>(ru, base, G, sh);
+  } else {
+    PV<GM> v;
+    return v;
+  }
+}
+template <bool BF, bool E4, int N, int GM, class RU>
+__device__ __forceinline__ v2f sum_g(const RU& ru, int base, int G, bool sh, const PV<GM>& v) {
+  if constexpr (N >= 1) {
+    if (G == N)
+      return sh ? pass_sum<BF, E4, N, true, GM>(ru, base, v) : pass_sum<BF, E4, N, false, GM>(ru, base, v);
+    return sum_g<BF, E4, N - 1, GM>(ru, base, G, sh, v);
+  } else {
+    return v2f{0.0f, 0.0f};
+  }
 }
 
-// Stage B's units: passes P0 and P1 of the thread, then its long unit (entries in global memory)
+// Stage B's units: passes P0 and P1 of the thread, then its long unit (entries in LDS)
 template <bool BF, bool E4>
 __device__ __forceinline__ void units(const uint8_t* gt, const typename Regions<E4>::RA& r1,
                                       const typename Regions<E4>::RU& ru) {
   using F = PT<E4>;
   const uint32_t m0 = r1.slot(F::MA + 0);
   const uint32_t m2 = __builtin_amdgcn_readfirstlane(r1.slot(F::MA + 2));
+  const int G0 = (int)(m2 & 15u), G1 = (int)((m2 >> 4) & 15u);
+  const bool sh0 = (m2 & 256u) != 0, sh1 = (m2 & 512u) != 0;
   float* act = LF(L_ACT);
-  const float a0 = unit_pass<BF, E4, F::G0MAX>(ru, F::U0, (int)(m2 & 15u), (m2 & 256u) != 0);
-  const float a1 = unit_pass<BF, E4, F::G1MAX>(ru, F::U1, (int)((m2 >> 4) & 15u), (m2 & 512u) != 0);
+  const PV<F::G0MAX> v0 = gather_g<E4, F::G0MAX, F::G0MAX>(ru, F::U0, G0, sh0);
+  const PV<F::G1MAX> v1 = gather_g<E4, F::G1MAX, F::G1MAX>(ru, F::U1, G1, sh1);
+  const v2f s0 = sum_g<BF, E4, F::G0MAX, F::G0MAX>(ru, F::U0, G0, sh0, v0);
+  const v2f s1 = sum_g<BF, E4, F::G1MAX, F::G1MAX>(ru, F::U1, G1, sh1, v1);
+  const float a0 = swiglu<BF>(s0.x, s0.y), a1 = swiglu<BF>(s1.x, s1.y);
   if (m0 & 0x8000u) act[m0 & 0xfffu] = a0;
   if (m0 & 0x80000000u) act[(m0 >> 16) & 0xfffu] = a1;
   ru.keep();
