@@ -850,19 +850,27 @@ __device__ __forceinline__ void down_rows(const uint8_t* gt, const typename Regi
       }
     }
   }
+  // every pass's sum first, then the writes (an LDS write between the sums would make each
+  // later sum wait for it: LDS reads and writes share one counter)
+  float sum[F::ND];
 #pragma unroll
   for (int q = 0; q < F::ND; q++) {
+    sum[q] = 0.0f;
     if (mask & (1u << q)) {
-      float s = 0.0f;
 #pragma unroll
       for (int j = 0; j < F::dlen(q); j++) {
         int o;
         float w;
         ent_of<E4>(rdw, F::D + ESZ * (F::doff(q) + j), o, w);
-        s = acc<BF>(s, x[q][j], w);
+        sum[q] = acc<BF>(sum[q], x[q][j], w);
       }
+    }
+  }
+#pragma unroll
+  for (int q = 0; q < F::ND; q++) {
+    if (mask & (1u << q)) {
       const uint32_t wo = (rdw.slot(F::MB + q / 2) >> (16 * (q & 1))) & 0xffffu;
-      *reinterpret_cast<float*>(smem + L_DSUM + wo) = s;
+      *reinterpret_cast<float*>(smem + L_DSUM + wo) = sum[q];
     }
   }
   rdw.keep();
