@@ -887,8 +887,7 @@ __device__ __forceinline__ void down_rows(const uint8_t* gt, const typename Regi
 // The gates: the live query/key channels' projections, conv windows (history in LDS) and silu
 // (causal_conv1d_update :199-216), and the decays g = -exp(A_log) softplus(a + dt_bias) (:499).
 // Flags per key head: 1 query nonzero, 2 key nonzero, 4 a decay exp(g) != 1; F_ANY and F_OUT
-// directly. Items run on the threads from the top down: the query/key channels on the top
-// wave(s), the decays on the wave(s) below.
+// directly.
 // a gate row's dot product with the GDN norm's output D((h * r) * (1 + w_in)), formed per entry
 // (w1e: the norm weight at each entry's column); slots past the row add nothing
 template <bool BF, bool E4>
@@ -913,57 +912,113 @@ __device__ __forceinline__ float ndot(const uint8_t* ent, int start, int n, floa
   return s;
 }
 
+// One gate item per lane: query/key channel j on thread NT - 1 - j (the top wave(s)), decay j on
+// the wave(s) below them (the packer keeps ceil(n_qk / 64) * 64 + n_dec <= NT). Its loads (item,
+// history, the row's entries and the residual at their columns) need no norm factor, so they are
+// issued at the start of stage A (gate_load) and overlap its work; stage B forms the norm output
+// per entry and the rest (gate_compute). Rows of more than four entries take ndot in stage B.
+struct GateLd {
+  v4f hv, w, we;  // the residual, weight and norm weight 1 + w_in of each entry
+  v4f tp;         // query/key: the conv taps; decay: dt_bias, A_log
+  float h0, h1, h2;          // query/key: the conv history
+  int kind, j, len, start, info;  // kind 0 none, 1 query/key, 2 decay; info: slot, or vh
+};
 template <bool BF, bool E4>
-__device__ __forceinline__ void gates(const ChainK& k, const uint8_t* gt, float r) {
+__device__ __forceinline__ GateLd gate_load(const uint8_t* gt) {
   const lxm_gate& hd = *reinterpret_cast<const lxm_gate*>(gt);
   const int tt = NT - 1 - (int)threadIdx.x;
-  const uint8_t* w1in = gt + hd.ent_w1;
-  float* hist = LF(L_HIST);
-  float* qkcur = LF(L_QKCUR);
-  float* ev = LF(L_EV);
+  const int nq = hd.n_qk, tq = ((nq + 63) >> 6) << 6;
+  GateLd g;
+  g.kind = 0;
+  g.len = 0;
+  if (tt < nq) {
+    const lxm_qkc c = reinterpret_cast<const lxm_qkc*>(gt + hd.qk)[tt];
+    const float* hs = LF(L_HIST) + 3 * (hd.qk_base + tt);
+    g.kind = 1;
+    g.j = tt;
+    g.len = c.len;
+    g.start = c.start;
+    g.info = c.slot;
+    g.tp = v4f{c.taps[0], c.taps[1], c.taps[2], c.taps[3]};
+    g.h0 = hs[0];
+    g.h1 = hs[1];
+    g.h2 = hs[2];
+  } else if (tt >= tq && tt - tq < hd.n_dec) {
+    const lxm_dec d = reinterpret_cast<const lxm_dec*>(gt + hd.dec)[tt - tq];
+    g.kind = 2;
+    g.j = tt - tq;
+    g.len = d.len;
+    g.start = d.start;
+    g.info = d.vh;
+    g.tp = v4f{d.dt_bias, d.A_log, 0.0f, 0.0f};
+  }
+  if (g.kind != 0 && g.len <= 4) {
+    const uint8_t* ent = gt + hd.ent;
+    const uint8_t* w1e = gt + hd.ent_w1;
+    const float* h = LF(L_H);
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+      int i;
+      float w;
+      Ent<E4>::at(ent, g.start + e, i, w);
+      g.w[e] = w;
+      g.we[e] = w1_one<E4, false>(w1e, g.start + e);
+      g.hv[e] = at_b(h, i & OFF_MASK);
+    }
+  }
+  return g;
+}
+// the row's dot product with the GDN norm's output D((h * r) * (1 + w_in)), in entry order from
+// +0: from the loaded entries, or by ndot for a longer row
+template <bool BF, bool E4>
+__device__ __forceinline__ float gate_dot(const uint8_t* gt, const GateLd& g, float r) {
+  if (g.len <= 4) {
+    float s = 0.0f;
+#pragma unroll
+    for (int e = 0; e < 4; e++) s = e < g.len ? acc<BF>(s, rd<BF>((g.hv[e] * r) * g.we[e]), g.w[e]) : s;
+    return s;
+  }
+  const lxm_gate& hd = *reinterpret_cast<const lxm_gate*>(gt);
+  return ndot<BF, E4>(gt + hd.ent, g.start, g.len, r, gt + hd.ent_w1);
+}
+template <bool BF, bool E4>
+__device__ __forceinline__ void gate_compute(const ChainK& k, const uint8_t* gt, const GateLd& g,
+                                             float r) {
   int* flags = LI(L_FLAGS);
-  const lxm_qkc* qk = reinterpret_cast<const lxm_qkc*>(gt + hd.qk);
-  const uint8_t* ent = gt + hd.ent;
-  for (int j = tt; j < hd.n_qk; j += NT) {
-    const lxm_qkc c = qk[j];
-    float* hs = hist + 3 * (hd.qk_base + j);
-    const float h0 = hs[0], h1 = hs[1], h2 = hs[2];
-    const float P = rd<BF>(ndot<BF, E4>(ent, c.start, c.len, r, w1in));
+  if (g.kind == 1) {
+    const lxm_gate& hd = *reinterpret_cast<const lxm_gate*>(gt);
+    const float P = rd<BF>(gate_dot<BF, E4>(gt, g, r));
     float y = 0.0f;
-    y = y + c.taps[0] * h0;
-    y = y + c.taps[1] * h1;
-    y = y + c.taps[2] * h2;
-    y = y + c.taps[3] * P;
-    hs[0] = h1;
-    hs[1] = h2;
+    y = y + g.tp[0] * g.h0;
+    y = y + g.tp[1] * g.h1;
+    y = y + g.tp[2] * g.h2;
+    y = y + g.tp[3] * P;
+    float* hs = LF(L_HIST) + 3 * (hd.qk_base + g.j);
+    hs[0] = g.h1;
+    hs[1] = g.h2;
     hs[2] = P;
     const float yr = rd<BF>(y);
     const float v = yr == 0.0f ? yr : rd<BF>(silu_rd<BF>(yr));
-    qkcur[j] = v;
+    LF(L_QKCUR)[g.j] = v;
     if (v != 0.0f) {
-      const bool isk = (c.slot & 256) != 0;
-      atomicOr(&flags[F_KH + (c.slot >> 9)], isk ? 2 : 1);
+      const bool isk = (g.info & 256) != 0;
+      atomicOr(&flags[F_KH + (g.info >> 9)], isk ? 2 : 1);
       atomicOr(&flags[F_ANY], 1);
       if (!isk) atomicOr(&flags[F_OUT], 1);
     }
-  }
-  // the decays on the wave(s) below the query/key channels' (a wave runs one kind of gate)
-  const lxm_dec* dc = reinterpret_cast<const lxm_dec*>(gt + hd.dec);
-  const int tq = ((hd.n_qk + 63) >> 6) << 6;
-  for (int j = ((tt - tq) % NT + NT) % NT; j < hd.n_dec; j += NT) {
-    const lxm_dec d = dc[j];
-    const float a = rd<BF>(ndot<BF, E4>(ent, d.start, d.len, r, w1in));
-    const float x = a + d.dt_bias;
+  } else if (g.kind == 2) {
+    const float a = rd<BF>(gate_dot<BF, E4>(gt, g, r));
+    const float x = a + g.tp[0];
     float e;
-    if (x < -104.0f && d.A_log <= 88.0f) {
+    if (x < -104.0f && g.tp[1] <= 88.0f) {
       e = 1.0f;  // exp(x) rounds to 0, so softplus is 0 and g = -exp(A_log) * 0 = -0
     } else {
-      const float g = (-cr_exp(d.A_log)) * softplus(x);
-      e = cr_exp(g);
+      const float gg = (-cr_exp(g.tp[1])) * softplus(x);
+      e = cr_exp(gg);
     }
-    ev[d.vh] = e;
+    LF(L_EV)[g.info] = e;
     if (e != 1.0f) {
-      atomicOr(&flags[F_KH + d.vh / k.R], 4);
+      atomicOr(&flags[F_KH + g.info / k.R], 4);
       atomicOr(&flags[F_ANY], 1);
     }
   }
@@ -1034,6 +1089,7 @@ __device__ __forceinline__ bool layer(const lxm_params& p, const ChainK& k, int 
   uint64_t* pa = reinterpret_cast<uint64_t*>(smem + L_PROF);
   // ---- stage A: both norms' factor (the GDN's input_layernorm :764 and the MLP's
   // post_attention_layernorm :789 read the same h when the GDN leaves it alone)
+  const GateLd gl = gate_load<BF, E4>(gt);
   const float r = norm_r(ss, H, hd.eps);
   stage_a<BF, E4>(k, r1, ha, hb, r, L, step, true);
   if (t < k.nk) flags[F_KH + t] = 0;
@@ -1049,7 +1105,7 @@ __device__ __forceinline__ bool layer(const lxm_params& p, const ChainK& k, int 
   }
   // ---- stage B: the gates and, speculatively (the GDN leaves h alone on most steps), the MLP
   units<BF, E4>(gt, r1, ru);
-  gates<BF, E4>(k, gt, r);
+  gate_compute<BF, E4>(k, gt, gl, r);
   sp_arrive(1);
   lds_barrier();
   sp_depart(1);

@@ -262,6 +262,8 @@ class Mega:
                 ent_w1.append(w1in[cols])
                 epos += len(cols)
             assert len(decs) <= MAXDEC
+            # one gate item per chain lane: the channels on the top waves, the decays below them
+            assert -(-len(qks) // 64) * 64 + len(decs) <= NT, f"layer {L}: too many gate items"
             gb = _Blob()
             gb.add(bytes(64))
             o_qk = gb.add(b"".join(bytes(q) for q in qks))
