@@ -297,13 +297,6 @@ struct Ent<false> {
   }
 };
 
-// s + x * w, rounded once as the oracle's s + D(x * w): for bf16 models x and w are bf16
-// values, whose product is exact in fp32, so one fused op gives the same bits
-template <bool BF>
-__device__ __forceinline__ float acc(float s, float x, float w) {
-  if constexpr (BF) return __builtin_fmaf(x, w, s);
-  else return s + x * w;
-}
 // the float at byte offset off of vector x
 __device__ __forceinline__ float at_b(const float* x, int off) {
   return *reinterpret_cast<const float*>(reinterpret_cast<const uint8_t*>(x) + off);
@@ -350,25 +343,6 @@ template <bool BF, bool E4, int N, int WHERE>
 __device__ __forceinline__ float dot(const uint8_t* ent, int64_t start, int n, const float* x) {
   return rest<BF, E4, N, WHERE>(ent, start, n, x, chunk<BF, E4, N, WHERE>(ent, start, n, 0, x, 0.0f));
 }
-// A wave's tree sum: lane 0 ends with the sum that __shfl_down at offsets 32, 16, ..., 1
-// leaves there (lane l adds lane l + off). Offsets 32 and 16 by gfx950's permlane swaps, 8..1
-// by DPP row shifts; no LDS round trips.
-template <int CTRL>
-__device__ __forceinline__ float dpp_f(float x) {
-  return __builtin_bit_cast(
-      float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), CTRL, 0xf, 0xf, true));
-}
-__device__ __forceinline__ float wave_tree(float s) {
-  const uint32_t u = __float_as_uint(s);
-  s = s + __uint_as_float(__builtin_amdgcn_permlane32_swap(u, u, false, false)[1]);
-  const uint32_t v = __float_as_uint(s);
-  s = s + __uint_as_float(__builtin_amdgcn_permlane16_swap(v, v, false, false)[1]);
-  s = s + dpp_f<0x108>(s);  // row_shl:8
-  s = s + dpp_f<0x104>(s);
-  s = s + dpp_f<0x102>(s);
-  s = s + dpp_f<0x101>(s);
-  return s;
-}
 
 // the 512-lane hidden sum: lane t's partial (its elements 4t..4t+3, then 2048+4t..2048+4t+3,
 // in order), combined within each wave at offsets 32..1, the 8 wave totals at offsets 4, 2, 1.
@@ -399,12 +373,6 @@ __device__ __forceinline__ float sum512(float s, float* wsum) {
   return sum512_end(wsum);
 }
 
-// the 64-lane head sum over one wave: lane l's partial (elements l, l + 64, ...), offsets
-// 32..1; every lane gets the sum
-__device__ __forceinline__ float sum64(float s) {
-  return __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(
-                                       __builtin_bit_cast(int, wave_tree(s))));
-}
 
 // ---------------------------------------------------------------------------------------------
 // a conv state value (model dtype) as float

@@ -1,0 +1,908 @@
+// The verified-mode forward of the chip layers on MI355X (gfx950): lx.fast's Fast.forward,
+// Fast.layer, Fast.head_argmax and Fast.decode (lx/lx/fast.py:252-361, :544-550, :365-540).
+//
+// T known positions go through each layer together. Everything a position needs from its own
+// residual (norms, the MLP, which key heads its query/key projections reach, its decays) is
+// token-parallel and runs over tiles of 4 positions held column-major in LDS (one 16-byte read
+// gives a column for all four), with each layer's sparse rows read from L2 and reused by every
+// tile. Only the delta rule's state carries from one position to the next, and only positions
+// whose query, key or decay is live for a head change that state (lx/lx/fast.py:8-19: an idle
+// head keeps its state and outputs 0): those candidates are compacted in order, their inputs
+// (q, k, v, z, beta, the decay) computed in parallel, and one workgroup per value head then runs
+// the recurrence over them with the head's 256x128 state in registers. The gated norm and
+// out_proj go back to the candidates' residuals in parallel.
+//
+// Semantics: every position sees exactly the stock decode step (transformers' Qwen3_5 decoder
+// layer with causal_conv1d_update and torch_recurrent_gated_delta_rule, in lx/lx/hf.py's chip
+// view) with the rounding contract of the decode kernel, so T positions leave the same
+// residuals, predictions, conv windows and recurrent states as T forced decode steps, bit for bit.
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/lxm_prefill.h"
+#include "lxm_math.h"
+
+using namespace lxm;
+
+#define NT 512
+#define NW (NT / 64)
+#define TT LXM_PF_TT
+#define KD 256
+#define VD 128
+#define MAXH LXM_MAXH
+static_assert(TT == 4, "a residual column of a tile is one 16-byte vector");
+static_assert(NT == KD + 2 * VD, "the delta kernel loads k/q, v and z with one thread each");
+
+typedef float v4f __attribute__((ext_vector_type(4)));
+typedef uint32_t v2u __attribute__((ext_vector_type(2)));
+
+template <class T>
+__device__ __forceinline__ const T* tab(const uint8_t* blob, int64_t off) {
+  return reinterpret_cast<const T*>(blob + off);
+}
+
+// ---------------------------------------------------------------------------------------------
+// The residual tiles in HBM, in the model dtype: column c of tile b at (b * H + c) * 4.
+template <bool BF>
+__device__ __forceinline__ v4f ld_col(const void* h, int64_t b, int H, int c) {
+  if constexpr (BF) {
+    const v2u u = reinterpret_cast<const v2u*>(h)[b * H + c];
+    return v4f{bitsf(u.x << 16), bitsf(u.x & 0xffff0000u), bitsf(u.y << 16), bitsf(u.y & 0xffff0000u)};
+  } else {
+    return reinterpret_cast<const v4f*>(h)[b * H + c];
+  }
+}
+// (values exact in the model dtype: bf16 keeps the upper half of each float)
+template <bool BF>
+__device__ __forceinline__ void st_col(void* h, int64_t b, int H, int c, v4f v) {
+  if constexpr (BF) {
+    v2u u;
+    u.x = (fbits(v.x) >> 16) | (fbits(v.y) & 0xffff0000u);
+    u.y = (fbits(v.z) >> 16) | (fbits(v.w) & 0xffff0000u);
+    reinterpret_cast<v2u*>(h)[b * H + c] = u;
+  } else {
+    reinterpret_cast<v4f*>(h)[b * H + c] = v;
+  }
+}
+__device__ __forceinline__ int64_t el_idx(int H, int t, int c) {
+  return ((int64_t)(t / TT) * H + c) * TT + t % TT;
+}
+template <bool BF>
+__device__ __forceinline__ float ld_el(const void* h, int H, int t, int c) {
+  if constexpr (BF) return bf16f(reinterpret_cast<const uint16_t*>(h)[el_idx(H, t, c)]);
+  else return reinterpret_cast<const float*>(h)[el_idx(H, t, c)];
+}
+template <bool BF>
+__device__ __forceinline__ void st_el(void* h, int H, int t, int c, float v) {
+  if constexpr (BF) reinterpret_cast<uint16_t*>(h)[el_idx(H, t, c)] = (uint16_t)(fbits(v) >> 16);
+  else reinterpret_cast<float*>(h)[el_idx(H, t, c)] = v;
+}
+// a conv window value (model dtype)
+template <bool BF>
+__device__ __forceinline__ float conv_ld(const void* cs, int64_t i) {
+  if constexpr (BF) return bf16f(reinterpret_cast<const uint16_t*>(cs)[i]);
+  else return reinterpret_cast<const float*>(cs)[i];
+}
+template <bool BF>
+__device__ __forceinline__ void conv_st(void* cs, int64_t i, float v) {
+  if constexpr (BF) reinterpret_cast<uint16_t*>(cs)[i] = (uint16_t)(fbits(v) >> 16);
+  else reinterpret_cast<float*>(cs)[i] = v;
+}
+
+// ---------------------------------------------------------------------------------------------
+// Arithmetic on the four positions of a column, one IEEE op per position.
+template <bool BF>
+__device__ __forceinline__ v4f acc4(v4f s, v4f x, float w) {
+  return v4f{acc<BF>(s.x, x.x, w), acc<BF>(s.y, x.y, w), acc<BF>(s.z, x.z, w), acc<BF>(s.w, x.w, w)};
+}
+template <bool BF>
+__device__ __forceinline__ v4f rd4(v4f v) {
+  return v4f{rd<BF>(v.x), rd<BF>(v.y), rd<BF>(v.z), rd<BF>(v.w)};
+}
+// D((h * r) * w1) per position: the RMSNorm's output (TF:720-737)
+template <bool BF>
+__device__ __forceinline__ v4f norm4(v4f h, v4f r, float w1) {
+  return v4f{rd<BF>((h.x * r.x) * w1), rd<BF>((h.y * r.y) * w1), rd<BF>((h.z * r.z) * w1),
+             rd<BF>((h.w * r.w) * w1)};
+}
+__device__ __forceinline__ float norm_r(float ss, int H, float eps) {
+  return rsqrt_(ss / (float)H + eps);
+}
+
+// A sparse row's dot product with a column-major tile vector x in LDS (entry offsets 16 x
+// column), for the four positions at once: the terms in entry order from +0, each rounded once
+// (the oracle's CSR rows: ascending columns; its zero-x skips change no bits, a sum from +0 is
+// never -0). Entries load four at a time (every table is followed by four padding entries);
+// the terms past the row's end are not added.
+template <bool BF>
+__device__ __forceinline__ v4f dot4(const lxm_pf_ent* __restrict__ e, int n, const uint8_t* x) {
+  v4f s = {0.0f, 0.0f, 0.0f, 0.0f};
+  for (int k0 = 0; k0 < n; k0 += 4) {
+    lxm_pf_ent en[4];
+#pragma unroll
+    for (int j = 0; j < 4; j++) en[j] = e[k0 + j];
+    v4f xv[4];
+#pragma unroll
+    for (int j = 0; j < 4; j++) xv[j] = *reinterpret_cast<const v4f*>(x + en[j].off);
+#pragma unroll
+    for (int j = 0; j < 4; j++)
+      if (k0 + j < n) s = acc4<BF>(s, xv[j], en[j].w);
+  }
+  return s;
+}
+// the same for one float per entry at x + off (a flat vector, or one position's lane of a tile)
+template <bool BF>
+__device__ __forceinline__ float dot1(const lxm_pf_ent* __restrict__ e, int n, const uint8_t* x) {
+  float s = 0.0f;
+  for (int k0 = 0; k0 < n; k0 += 4) {
+    lxm_pf_ent en[4];
+#pragma unroll
+    for (int j = 0; j < 4; j++) en[j] = e[k0 + j];
+    float xv[4];
+#pragma unroll
+    for (int j = 0; j < 4; j++) xv[j] = *reinterpret_cast<const float*>(x + en[j].off);
+#pragma unroll
+    for (int j = 0; j < 4; j++)
+      if (k0 + j < n) s = acc<BF>(s, xv[j], en[j].w);
+  }
+  return s;
+}
+
+// The 512-lane hidden sum of x * x for the four positions of a tile (the decode's order: thread
+// t adds its columns 4t..4t+3, then 2048+4t..2048+4t+3; waves at offsets 32..1; the 8 wave
+// totals at offsets 4, 2, 1). With plus0, each column also becomes x + 0 (the residual add of a
+// row with no term: -0 becomes +0). Every thread gets the sums. wsum: 8 vectors of LDS, not
+// reused before the next barrier.
+template <bool BF>
+__device__ __forceinline__ v4f hsum(v4f* HV, v4f* wsum, bool plus0) {
+  const int t = threadIdx.x;
+  v4f s = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+  for (int half = 0; half < 2; half++)
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      const int c = half * 2048 + 4 * t + i;
+      v4f x = HV[c];
+      if (plus0) {
+        x = v4f{x.x + 0.0f, x.y + 0.0f, x.z + 0.0f, x.w + 0.0f};
+        HV[c] = x;
+      }
+      s = v4f{acc<BF>(s.x, x.x, x.x), acc<BF>(s.y, x.y, x.y), acc<BF>(s.z, x.z, x.z),
+              acc<BF>(s.w, x.w, x.w)};
+    }
+  s = v4f{wave_tree(s.x), wave_tree(s.y), wave_tree(s.z), wave_tree(s.w)};
+  if ((t & 63) == 0) wsum[t >> 6] = s;
+  __syncthreads();
+  v4f w[NW];
+#pragma unroll
+  for (int i = 0; i < NW; i++) w[i] = wsum[i];
+#pragma unroll
+  for (int off = NW / 2; off >= 1; off >>= 1)
+#pragma unroll
+    for (int i = 0; i < off; i++) w[i] = w[i] + w[i + off];
+  return w[0];
+}
+
+// ---------------------------------------------------------------------------------------------
+// The tile kernel: one workgroup per tile of 4 positions. Lm >= 0: layer Lm's MLP
+// (post_attention_layernorm, SwiGLU, down_proj, residual add; TF:704-717, :781-793) on the
+// residual as the previous steps left it, stored back. Then Ln >= 0: layer Ln's input norm
+// factor r1 per position, and which of the layer's key slots have a nonzero query/key projection
+// at each position, and whether a decay can act (bit 31); or Ln == -2: the final norm into hn.
+// LDS: 512 bytes of sums and masks, the residual (4,096 columns), the norm's output (then the
+// MLP units' outputs).
+#define X_HV 512
+#define X_XM (X_HV + 16 * MAXH)
+template <bool BF>
+__global__ __launch_bounds__(NT) void pf_tile(const lxm_pf_params* __restrict__ pp, int Lm, int Ln) {
+  extern __shared__ __align__(16) uint8_t sm[];
+  const lxm_pf_params& p = *pp;
+  const int t = threadIdx.x, H = p.hidden;
+  const int64_t b = blockIdx.x;
+  uint32_t* smask = reinterpret_cast<uint32_t*>(sm);
+  v4f* wsA = reinterpret_cast<v4f*>(sm + 64);
+  v4f* wsB = reinterpret_cast<v4f*>(sm + 192);
+  v4f* HV = reinterpret_cast<v4f*>(sm + X_HV);
+  v4f* XM = reinterpret_cast<v4f*>(sm + X_XM);
+  const uint8_t* xm = sm + X_XM;
+  if (t < TT) smask[t] = 0;
+  for (int c = t; c < MAXH; c += NT) HV[c] = c < H ? ld_col<BF>(p.h, b, H, c) : v4f{0.0f, 0.0f, 0.0f, 0.0f};
+  __syncthreads();
+  if (Lm >= 0) {
+    const lxm_pf_layer& ly = p.layers[Lm];
+    const lxm_pf_ent* ent = tab<lxm_pf_ent>(p.blob, ly.ent);
+    const v4f ss = hsum<BF>(HV, wsA, false);
+    const v4f r = {norm_r(ss.x, H, ly.eps), norm_r(ss.y, H, ly.eps), norm_r(ss.z, H, ly.eps),
+                   norm_r(ss.w, H, ly.eps)};
+    const float* w1 = tab<float>(p.blob, ly.w1_post);
+    for (int c = t; c < H; c += NT) XM[c] = norm4<BF>(HV[c], r, w1[c]);
+    __syncthreads();
+    // units: act = D(D(silu(D(gate . x))) * D(up . x))
+    const lxm_pf_unit* un = tab<lxm_pf_unit>(p.blob, ly.units);
+    v4f a[LXM_PF_UPT];
+#pragma unroll
+    for (int i = 0; i < LXM_PF_UPT; i++) {
+      const int u = t + i * NT;
+      if (u < ly.n_units) {
+        const lxm_pf_unit q = un[u];
+        const v4f g = rd4<BF>(dot4<BF>(ent + q.gs, q.gn, xm));
+        const v4f v = rd4<BF>(dot4<BF>(ent + q.us, q.un, xm));
+        a[i] = v4f{rd<BF>(silu_rd<BF>(g.x) * v.x), rd<BF>(silu_rd<BF>(g.y) * v.y),
+                   rd<BF>(silu_rd<BF>(g.z) * v.z), rd<BF>(silu_rd<BF>(g.w) * v.w)};
+      }
+    }
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < LXM_PF_UPT; i++)
+      if (t + i * NT < ly.n_units) XM[t + i * NT] = a[i];
+    __syncthreads();
+    // down_proj rows over the units (entries 16 x unit position), added to the residual
+    const lxm_pf_drow* dr = tab<lxm_pf_drow>(p.blob, ly.drows);
+    for (int i = t; i < ly.n_drows; i += NT) {
+      const lxm_pf_drow d = dr[i];
+      const v4f s = rd4<BF>(dot4<BF>(ent + d.start, d.len, xm));
+      HV[d.row] = rd4<BF>(HV[d.row] + s);
+    }
+    __syncthreads();
+  }
+  if (Ln >= 0) {
+    const lxm_pf_layer& ly = p.layers[Ln];
+    const lxm_pf_ent* ent = tab<lxm_pf_ent>(p.blob, ly.ent);
+    const v4f ss = hsum<BF>(HV, wsB, Lm >= 0);
+    const v4f r = {norm_r(ss.x, H, ly.eps), norm_r(ss.y, H, ly.eps), norm_r(ss.z, H, ly.eps),
+                   norm_r(ss.w, H, ly.eps)};
+    if (t < TT && b * TT + t < p.T) p.r1[b * TT + t] = t == 0 ? r.x : t == 1 ? r.y : t == 2 ? r.z : r.w;
+    const float* w1 = tab<float>(p.blob, ly.w1_in);
+    for (int c = t; c < H; c += NT) XM[c] = norm4<BF>(HV[c], r, w1[c]);
+    __syncthreads();
+    // query/key projections of the live key heads' channels: which slots are nonzero
+    const lxm_pf_qk* qk = tab<lxm_pf_qk>(p.blob, ly.qk);
+    for (int i = t; i < ly.n_qk; i += NT) {
+      const lxm_pf_qk q = qk[i];
+      const v4f P = rd4<BF>(dot4<BF>(ent + q.start, q.len, xm));
+      const uint32_t bit = 1u << q.kslot;
+      if (P.x != 0.0f) atomicOr(smask + 0, bit);
+      if (P.y != 0.0f) atomicOr(smask + 1, bit);
+      if (P.z != 0.0f) atomicOr(smask + 2, bit);
+      if (P.w != 0.0f) atomicOr(smask + 3, bit);
+    }
+    // decays: g = -exp(A_log) * softplus(a + dt_bias) (:499); a step decays when exp(g) != 1
+    const lxm_pf_dec* dc = tab<lxm_pf_dec>(p.blob, ly.dec);
+    for (int i = t; i < ly.n_dec; i += NT) {
+      const lxm_pf_dec d = dc[i];
+      const v4f a = d.len ? rd4<BF>(dot4<BF>(ent + d.start, d.len, xm)) : v4f{0.0f, 0.0f, 0.0f, 0.0f};
+      const float na = -cr_exp(d.A_log);
+#pragma unroll
+      for (int k = 0; k < TT; k++)
+        if (cr_exp(na * softplus(a[k] + d.dt_bias)) != 1.0f) atomicOr(smask + k, 0x80000000u);
+    }
+    __syncthreads();
+    if (t < TT && b * TT + t < p.T) p.mask[b * TT + t] = smask[t];
+  } else if (Ln == -2) {
+    const v4f ss = hsum<BF>(HV, wsB, Lm >= 0);
+    const v4f r = {norm_r(ss.x, H, p.rms_eps), norm_r(ss.y, H, p.rms_eps),
+                   norm_r(ss.z, H, p.rms_eps), norm_r(ss.w, H, p.rms_eps)};
+    for (int c = t; c < H; c += NT) st_col<BF>(p.hn, b, H, c, norm4<BF>(HV[c], r, p.w1_final[c]));
+  } else if (Lm >= 0) {
+    for (int c = t; c < H; c += NT) HV[c] = HV[c] + v4f{0.0f, 0.0f, 0.0f, 0.0f};
+  }
+  if (Lm >= 0)
+    for (int c = t; c < H; c += NT) st_col<BF>(p.h, b, H, c, HV[c]);
+}
+
+// ---------------------------------------------------------------------------------------------
+// The candidates of layer L, in position order: positions whose query/key channels of some live
+// key head can be nonzero (a nonzero projection within the earliest tap's reach, or a window
+// from before the call), or that decay. One workgroup of 1,024 threads; each thread takes 32
+// consecutive positions per round.
+#define C_NT 1024
+#define C_PER 32
+__global__ __launch_bounds__(C_NT) void pf_compact(const lxm_pf_params* __restrict__ pp, int L) {
+  __shared__ int wtot[C_NT / 64];
+  __shared__ int base_s;
+  const lxm_pf_params& p = *pp;
+  const lxm_pf_layer& ly = p.layers[L];
+  const int t = threadIdx.x, T = p.T, reach = ly.reach;
+  const uint32_t allk = ly.n_ks >= 32 ? 0xffffffffu : ((1u << ly.n_ks) - 1u);
+  if (t == 0) base_s = 0;
+  __syncthreads();
+  for (int r0 = 0; r0 < T; r0 += C_NT * C_PER) {
+    const int t0 = r0 + t * C_PER;
+    uint32_t m[C_PER + 3];
+#pragma unroll
+    for (int i = 0; i < C_PER + 3; i++) {
+      const int tp = t0 - 3 + i;
+      m[i] = (tp >= 0 && tp < T) ? p.mask[tp] : 0u;
+    }
+    int n = 0;
+    uint32_t cm[C_PER];
+#pragma unroll
+    for (int i = 0; i < C_PER; i++) {
+      const int tp = t0 + i;
+      uint32_t kb = m[i + 3] & 0xffffu;
+      if (reach >= 1) kb |= m[i + 2] & 0xffffu;
+      if (reach >= 2) kb |= m[i + 1] & 0xffffu;
+      if (reach >= 3) kb |= m[i] & 0xffffu;
+      if (tp < reach) kb |= allk;
+      kb |= m[i + 3] & 0x80000000u;
+      cm[i] = tp < T ? kb : 0u;
+      n += cm[i] != 0u;
+    }
+    // exclusive scan of n over the workgroup
+    int incl = n;
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+      const int y = __shfl_up(incl, off);
+      if ((t & 63) >= off) incl += y;
+    }
+    if ((t & 63) == 63) wtot[t >> 6] = incl;
+    __syncthreads();
+    int wbase = 0, all = 0;
+    for (int w = 0; w < C_NT / 64; w++) {
+      if (w < (t >> 6)) wbase += wtot[w];
+      all += wtot[w];
+    }
+    int o = base_s + wbase + incl - n;
+#pragma unroll
+    for (int i = 0; i < C_PER; i++)
+      if (cm[i] != 0u) {
+        p.cand[o] = t0 + i;
+        p.cmask[o] = cm[i];
+        o++;
+      }
+    __syncthreads();
+    if (t == 0) base_s += all;
+    __syncthreads();
+  }
+  if (t == 0) p.count[L] = base_s;
+}
+
+// ---------------------------------------------------------------------------------------------
+// Candidate records. Offsets inside one (see lxm_pf_layer): header {tok, live slots}, qn, kn, v,
+// z, beta, e, proc.
+struct RecOff {
+  int q, k, v, z, b, e, pr;
+  __device__ RecOff(int nks, int nvs) {
+    q = 16;
+    k = q + 1024 * nks;
+    v = k + 1024 * nks;
+    z = v + 512 * nvs;
+    b = z + 512 * nvs;
+    e = b + 4 * nvs;
+    pr = e + 4 * nvs;
+  }
+};
+
+// The conv output of a channel at position tok: the window [x(tok-3) .. x(tok)] from the
+// projections P (lane s: position tok - s) or, before the call's first position, the window the
+// cache held (TF:199-216: silu(D(sum of taps * window)), rounded to the model dtype).
+template <bool BF>
+__device__ __forceinline__ float conv_y(const v4f P, const float* taps, int tok, const void* cs,
+                                        int64_t chan) {
+  float y = 0.0f;
+#pragma unroll
+  for (int k = 0; k < 4; k++) {
+    if (taps[k] == 0.0f) continue;
+    const int s = 3 - k;
+    const float x = tok - s >= 0 ? P[s] : conv_ld<BF>(cs, chan * 4 + 4 + (tok - s));
+    y = acc<BF>(y, taps[k], x);
+  }
+  return silu_rd<BF>(rd<BF>(y));
+}
+
+// One workgroup per candidate (grid-stride): the input norm's output at positions tok..tok-3
+// (lanes 0..3 of a tile-shaped vector in LDS), the query/key conv outputs of its key slots,
+// which slots are live, their l2norms; for the live slots' value heads the value channels' conv
+// outputs, the in_proj_z rows and beta; every slot's decay factor exp(g). LDS: the normed input
+// (64 KB), q/k per key slot (32 KB), the live word.
+#define A_QK (16 * MAXH)
+#define A_MISC (A_QK + 4 * LXM_PF_MAXKS * 2 * KD)
+template <bool BF>
+__global__ __launch_bounds__(NT) void pf_act(const lxm_pf_params* __restrict__ pp, int L) {
+  extern __shared__ __align__(16) uint8_t sm[];
+  const lxm_pf_params& p = *pp;
+  const lxm_pf_layer& ly = p.layers[L];
+  const int t = threadIdx.x, H = p.hidden, lane = t & 63, wv = t >> 6;
+  v4f* XN = reinterpret_cast<v4f*>(sm);
+  float* QK = reinterpret_cast<float*>(sm + A_QK);
+  uint32_t* live_s = reinterpret_cast<uint32_t*>(sm + A_MISC);
+  const lxm_pf_ent* ent = tab<lxm_pf_ent>(p.blob, ly.ent);
+  const float* w1 = tab<float>(p.blob, ly.w1_in);
+  const void* cs = p.conv[L];
+  const RecOff ro(ly.n_ks, ly.n_vs);
+  const int count = p.count[L];
+  for (int j = blockIdx.x; j < count; j += gridDim.x) {
+    const int tok = p.cand[j];
+    const uint32_t cm = p.cmask[j];
+    uint8_t* rec = p.recs + (int64_t)j * ly.rec_bytes;
+    float rr[4];
+#pragma unroll
+    for (int s = 0; s < 4; s++) rr[s] = tok - s >= 0 ? p.r1[tok - s] : 0.0f;
+    for (int c = t; c < H; c += NT) {
+      v4f x;
+#pragma unroll
+      for (int s = 0; s < 4; s++) x[s] = tok - s >= 0 ? rd<BF>((ld_el<BF>(p.h, H, tok - s, c) * rr[s]) * w1[c]) : 0.0f;
+      XN[c] = x;
+    }
+    for (int i = t; i < ly.n_ks * 2 * KD; i += NT) QK[i] = 0.0f;
+    if (t == 0) *live_s = 0u;
+    __syncthreads();
+    // the query/key conv outputs of the slots to evaluate
+    const lxm_pf_qk* qk = tab<lxm_pf_qk>(p.blob, ly.qk);
+    for (int i = t; i < ly.n_qk; i += NT) {
+      const lxm_pf_qk q = qk[i];
+      if (!((cm >> q.kslot) & 1u)) continue;
+      const v4f P = rd4<BF>(dot4<BF>(ent + q.start, q.len, sm));
+      QK[q.kslot * 2 * KD + q.pos] = conv_y<BF>(P, q.taps, tok, cs, q.chan);
+    }
+    __syncthreads();
+    // live slots (a nonzero query or key) and the l2norms (TF:242-245, :352-353): one wave per
+    // (slot, query | key); D(x * D(rsqrt(D(D(sum64 D(x*x)) + 1e-6)))), the query times 1/16
+    for (int task = wv; task < 2 * ly.n_ks; task += NW) {
+      const int slot = task >> 1, isk = task & 1;
+      if (!((cm >> slot) & 1u)) continue;
+      const float* x = QK + slot * 2 * KD + isk * KD;
+      float xs[4], s = 0.0f;
+      bool nz = false;
+#pragma unroll
+      for (int i = 0; i < 4; i++) {
+        xs[i] = x[lane + 64 * i];
+        nz |= xs[i] != 0.0f;
+        s = s + rd<BF>(xs[i] * xs[i]);
+      }
+      if (__ballot(nz) != 0ull && lane == 0) atomicOr(live_s, 1u << slot);
+      s = rd<BF>(sum64(s));
+      const float inv = rd<BF>(rsqrt_(rd<BF>(s + 1e-6f)));
+      float* o = reinterpret_cast<float*>(rec + (isk ? ro.k : ro.q)) + slot * KD;
+#pragma unroll
+      for (int i = 0; i < 4; i++) {
+        float v = rd<BF>(xs[i] * inv);
+        if (!isk) v = v * 0.0625f;
+        o[lane + 64 * i] = v;
+      }
+    }
+    __syncthreads();
+    const uint32_t live = *live_s;
+    const lxm_pf_vs* vs = tab<lxm_pf_vs>(p.blob, ly.vs);
+    const lxm_pf_vc* vc = tab<lxm_pf_vc>(p.blob, ly.vc);
+    const lxm_row* zr = tab<lxm_row>(p.blob, ly.zrow);
+    float* rv = reinterpret_cast<float*>(rec + ro.v);
+    float* rz = reinterpret_cast<float*>(rec + ro.z);
+    for (int i = t; i < ly.n_vs * VD; i += NT) {
+      const lxm_pf_vs sv = vs[i >> 7];
+      if (sv.kslot < 0 || !((live >> sv.kslot) & 1u)) continue;
+      const lxm_pf_vc c = vc[i];
+      const v4f P = rd4<BF>(dot4<BF>(ent + c.start, c.len, sm));
+      const int64_t chan = 2 * (int64_t)p.nk * KD + (int64_t)sv.vh * VD + (i & 127);
+      rv[i] = conv_y<BF>(P, c.taps, tok, cs, chan);
+      const lxm_row z = zr[i];
+      rz[i] = rd<BF>(dot1<BF>(ent + z.start, z.len, sm));
+    }
+    const lxm_row* br = tab<lxm_row>(p.blob, ly.brow);
+    const lxm_pf_dec* dc = tab<lxm_pf_dec>(p.blob, ly.dec);
+    for (int i = t; i < ly.n_vs; i += NT) {
+      const lxm_pf_vs sv = vs[i];
+      float e = 1.0f;
+      if (sv.dslot >= 0) {
+        const lxm_pf_dec d = dc[sv.dslot];
+        const float a = d.len ? rd<BF>(dot1<BF>(ent + d.start, d.len, sm)) : 0.0f;
+        e = cr_exp((-cr_exp(d.A_log)) * softplus(a + d.dt_bias));
+      }
+      reinterpret_cast<float*>(rec + ro.e)[i] = e;
+      if (sv.kslot >= 0 && ((live >> sv.kslot) & 1u)) {
+        const lxm_row bb = br[i];
+        reinterpret_cast<float*>(rec + ro.b)[i] = rd<BF>(sigmoid(rd<BF>(dot1<BF>(ent + bb.start, bb.len, sm))));
+      }
+    }
+    if (t == 0) {
+      reinterpret_cast<int32_t*>(rec)[0] = tok;
+      reinterpret_cast<uint32_t*>(rec)[1] = live;
+    }
+    __syncthreads();
+  }
+}
+
+// ---------------------------------------------------------------------------------------------
+// The conv windows the call leaves (causal_conv1d_update's state after the last position: each
+// channel's last 4 projections, TF:199-216), for every channel of layer L. Runs while p->h holds
+// the layer's input and after pf_act has read the windows the call started from.
+template <bool BF>
+__global__ __launch_bounds__(256) void pf_tail(const lxm_pf_params* __restrict__ pp, int L) {
+  const lxm_pf_params& p = *pp;
+  const lxm_pf_layer& ly = p.layers[L];
+  const int c = blockIdx.x * 256 + threadIdx.x, H = p.hidden, T = p.T;
+  if (c >= p.n_conv) return;
+  const lxm_pf_ent* ent = tab<lxm_pf_ent>(p.blob, ly.ent);
+  const float* w1 = tab<float>(p.blob, ly.w1_in);
+  const lxm_row row = tab<lxm_row>(p.blob, ly.cc)[c];
+  void* cs = p.conv[L];
+  float win[4];
+#pragma unroll
+  for (int j = 0; j < 4; j++) {
+    const int tp = T - 4 + j;
+    if (tp >= 0) {
+      const float r = p.r1[tp];
+      float s = 0.0f;
+      for (int k = 0; k < row.len; k++) {
+        const lxm_pf_ent e = ent[row.start + k];
+        const int col = e.off >> 4;
+        s = acc<BF>(s, rd<BF>((ld_el<BF>(p.h, H, tp, col) * r) * w1[col]), e.w);
+      }
+      win[j] = rd<BF>(s);
+    } else {
+      win[j] = conv_ld<BF>(cs, (int64_t)c * 4 + j + T);
+    }
+  }
+#pragma unroll
+  for (int j = 0; j < 4; j++) conv_st<BF>(cs, (int64_t)c * 4 + j, win[j]);
+}
+
+// ---------------------------------------------------------------------------------------------
+// The recurrence of one value-head slot over the layer's candidates, in position order
+// (torch_recurrent_gated_delta_rule, TF:330-380, one token at a time): S <- S * exp(g) when
+// exp(g) != 1; with a live query or key kv = S^T k, delta = (v - kv) beta, S += k delta^T,
+// o = D(S^T q), then the gated norm (TF:168-184) y = D(D(w * D(o * r)) * silu(z)) into the
+// record (over z). The state tile stays in registers: thread (cg, rb) holds columns 4cg..4cg+3 of
+// rows 16rb..16rb+15, one of ATen's 16-row cascade blocks (torch .sum(-2) on the CPU).
+template <bool BF>
+__global__ __launch_bounds__(NT) void pf_delta(const lxm_pf_params* __restrict__ pp, int L) {
+  __shared__ __align__(16) float kn[KD], qn[KD], vb[VD], zb[VD], dl[VD], ob[VD];
+  __shared__ __align__(16) float bs[16 * VD];
+  __shared__ float beta_s;
+  const lxm_pf_params& p = *pp;
+  const lxm_pf_layer& ly = p.layers[L];
+  const int t = threadIdx.x, vslot = blockIdx.x, lane = t & 63;
+  const lxm_pf_vs sv = tab<lxm_pf_vs>(p.blob, ly.vs)[vslot];
+  const RecOff ro(ly.n_ks, ly.n_vs);
+  const float* gw = tab<float>(p.blob, ly.gnorm);
+  const int count = p.count[L];
+  const int cg = t & 31, rb = t >> 5;
+  v4f* S4 = reinterpret_cast<v4f*>(p.rec[L] + (size_t)sv.vh * KD * VD);
+  v4f s[16];
+#pragma unroll
+  for (int i = 0; i < 16; i++) s[i] = S4[(rb * 16 + i) * (VD / 4) + cg];
+  bool wrote = false;
+  for (int j = 0; j < count; j++) {
+    uint8_t* rec = p.recs + (int64_t)j * ly.rec_bytes;
+    const uint32_t livem = reinterpret_cast<const uint32_t*>(rec)[1];
+    const float e = reinterpret_cast<const float*>(rec + ro.e)[vslot];
+    const bool live = sv.kslot >= 0 && ((livem >> sv.kslot) & 1u);
+    int proc = 0;
+    if (live || e != 1.0f) {
+      wrote = true;
+      if (e != 1.0f) {
+#pragma unroll
+        for (int i = 0; i < 16; i++) s[i] = s[i] * e;
+      }
+      proc = 1;
+      if (live) {
+        proc = 2;
+        if (t < KD) {
+          kn[t] = reinterpret_cast<const float*>(rec + ro.k)[sv.kslot * KD + t];
+          qn[t] = reinterpret_cast<const float*>(rec + ro.q)[sv.kslot * KD + t];
+        } else if (t < KD + VD) {
+          vb[t - KD] = reinterpret_cast<const float*>(rec + ro.v)[vslot * VD + t - KD];
+        } else {
+          zb[t - KD - VD] = reinterpret_cast<const float*>(rec + ro.z)[vslot * VD + t - KD - VD];
+        }
+        if (t == 0) beta_s = reinterpret_cast<const float*>(rec + ro.b)[vslot];
+        __syncthreads();
+        v4f a = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int i = 0; i < 16; i++) {
+          const float f = kn[rb * 16 + i];
+          if (f != 0.0f) a = v4f{a.x + s[i].x * f, a.y + s[i].y * f, a.z + s[i].z * f, a.w + s[i].w * f};
+        }
+        reinterpret_cast<v4f*>(bs + rb * VD)[cg] = a;
+        __syncthreads();
+        if (t < VD) {
+          float kv = 0.0f;
+#pragma unroll
+          for (int q = 0; q < 16; q++) kv = kv + bs[q * VD + t];
+          dl[t] = (vb[t] - kv) * beta_s;
+        }
+        __syncthreads();
+        const v4f d = reinterpret_cast<const v4f*>(dl)[cg];
+        v4f o = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int i = 0; i < 16; i++) {
+          const float f = kn[rb * 16 + i];
+          if (f != 0.0f) s[i] = v4f{s[i].x + f * d.x, s[i].y + f * d.y, s[i].z + f * d.z, s[i].w + f * d.w};
+          const float g = qn[rb * 16 + i];
+          if (g != 0.0f) o = v4f{o.x + s[i].x * g, o.y + s[i].y * g, o.z + s[i].z * g, o.w + s[i].w * g};
+        }
+        reinterpret_cast<v4f*>(bs + rb * VD)[cg] = o;
+        __syncthreads();
+        if (t < VD) {
+          float q = 0.0f;
+#pragma unroll
+          for (int b = 0; b < 16; b++) q = q + bs[b * VD + t];
+          ob[t] = rd<BF>(q);
+        }
+        __syncthreads();
+        if (t < 64) {
+          float ss = 0.0f;
+          for (int k = lane; k < VD; k += 64) ss = ss + ob[k] * ob[k];
+          ss = sum64(ss);
+          const float rr = rsqrt_(ss / (float)VD + ly.geps);
+          float* y = reinterpret_cast<float*>(rec + ro.z) + vslot * VD;
+          for (int k = lane; k < VD; k += 64) {
+            const float t1 = rd<BF>(ob[k] * rr);
+            const float t2 = rd<BF>(gw[k] * t1);
+            y[k] = rd<BF>(t2 * silu(zb[k]));
+          }
+        }
+        __syncthreads();
+      }
+    }
+    if (t == 0) reinterpret_cast<int32_t*>(rec + ro.pr)[vslot] = proc;
+  }
+  if (wrote) {
+#pragma unroll
+    for (int i = 0; i < 16; i++) S4[(rb * 16 + i) * (VD / 4) + cg] = s[i];
+  }
+}
+
+// ---------------------------------------------------------------------------------------------
+// out_proj and the residual add at each candidate with a live head (TF:541-543, :777-779):
+// per residual row the terms over every value dim in ascending order, rounded once
+// (lx/lx/fast.py:349-361), then h = D(h + that). Heads that did not run add nothing (their
+// output is exactly 0 and the oracle skips zero inputs). One workgroup per candidate.
+template <bool BF>
+__global__ __launch_bounds__(NT) void pf_out(const lxm_pf_params* __restrict__ pp, int L) {
+  extern __shared__ __align__(16) uint8_t sm[];
+  __shared__ int any_s;
+  const lxm_pf_params& p = *pp;
+  const lxm_pf_layer& ly = p.layers[L];
+  const int t = threadIdx.x, H = p.hidden;
+  float* ON = reinterpret_cast<float*>(sm);
+  const RecOff ro(ly.n_ks, ly.n_vs);
+  const lxm_pf_drow* orows = tab<lxm_pf_drow>(p.blob, ly.orows);
+  const lxm_pf_ent* ent = tab<lxm_pf_ent>(p.blob, ly.ent);
+  const int count = p.count[L];
+  for (int j = blockIdx.x; j < count; j += gridDim.x) {
+    const uint8_t* rec = p.recs + (int64_t)j * ly.rec_bytes;
+    const int tok = reinterpret_cast<const int32_t*>(rec)[0];
+    const int32_t* pr = reinterpret_cast<const int32_t*>(rec + ro.pr);
+    const float* y = reinterpret_cast<const float*>(rec + ro.z);
+    if (t == 0) any_s = 0;
+    __syncthreads();
+    for (int i = t; i < ly.n_vs * VD; i += NT) {
+      const bool on = pr[i >> 7] == 2;
+      ON[i] = on ? y[i] : 0.0f;
+      if (on && (i & 127) == 0) any_s = 1;
+    }
+    __syncthreads();
+    if (any_s) {
+      for (int i = t; i < ly.n_orows; i += NT) {
+        const lxm_pf_drow r = orows[i];
+        const float o = rd<BF>(dot1<BF>(ent + r.start, r.len, sm));
+        st_el<BF>(p.h, H, tok, r.row, rd<BF>(ld_el<BF>(p.h, H, tok, r.row) + o));
+      }
+    }
+    __syncthreads();
+  }
+}
+
+// ---------------------------------------------------------------------------------------------
+// The head (lx/lx/hf.py:179-184): logits D(hn . row) over the tied embedding rows, the first
+// maximum per position. Workgroup (tile, slice): slice = the XCD the workgroup lands on, so each
+// XCD's L2 keeps one eighth of the head. A thread takes rows in ascending order and keeps the
+// first strict maximum; NaN logits (which compare false) are tracked apart and, where one
+// occurred, the thread finds its first NaN row. The thread keys (value, lower index, NaN above
+// everything: torch.argmax) fold into p->keys by 64-bit atomic max.
+__device__ __forceinline__ unsigned long long kmax(unsigned long long a, unsigned long long b) {
+  return a > b ? a : b;
+}
+__device__ __forceinline__ unsigned long long wave_kmax(unsigned long long k) {
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) k = kmax(k, __shfl_xor(k, off));
+  return k;
+}
+template <bool BF>
+__global__ __launch_bounds__(NT) void pf_head(const lxm_pf_params* __restrict__ pp) {
+  extern __shared__ __align__(16) uint8_t sm[];
+  const lxm_pf_params& p = *pp;
+  const int t = threadIdx.x, H = p.hidden;
+  const int slice = blockIdx.x % LXM_PF_SLICES;
+  const int64_t b = blockIdx.x / LXM_PF_SLICES;
+  v4f* HN = reinterpret_cast<v4f*>(sm);
+  for (int c = t; c < H; c += NT) HN[c] = ld_col<BF>(p.hn, b, H, c);
+  __syncthreads();
+  const int r0 = p.head_slice[slice], r1 = p.head_slice[slice + 1];
+  float best[TT];
+  int bidx[TT];
+  bool nan_any = false;
+#pragma unroll
+  for (int k = 0; k < TT; k++) {
+    best[k] = 0.0f;
+    bidx[k] = -1;
+  }
+  for (int r = r0 + t; r < r1; r += NT) {
+    const int64_t e0 = p.head_ptr[r], e1 = p.head_ptr[r + 1];
+    const v4f s = rd4<BF>(dot4<BF>(p.head_ent + e0, (int)(e1 - e0), sm));
+#pragma unroll
+    for (int k = 0; k < TT; k++) {
+      const float v = s[k];
+      nan_any |= v != v;
+      if (bidx[k] < 0 || v > best[k]) {
+        best[k] = v;
+        bidx[k] = r;
+      }
+    }
+  }
+  unsigned long long key[TT];
+#pragma unroll
+  for (int k = 0; k < TT; k++) key[k] = bidx[k] < 0 ? 0ull : argmax_key(best[k], bidx[k]);
+  if (nan_any) {  // rare: the first NaN row of each position, which outranks every number
+    for (int r = r0 + t; r < r1; r += NT) {
+      const int64_t e0 = p.head_ptr[r], e1 = p.head_ptr[r + 1];
+      const v4f s = rd4<BF>(dot4<BF>(p.head_ent + e0, (int)(e1 - e0), sm));
+#pragma unroll
+      for (int k = 0; k < TT; k++)
+        if (s[k] != s[k]) key[k] = kmax(key[k], argmax_key(s[k], r));
+    }
+  }
+#pragma unroll
+  for (int k = 0; k < TT; k++) {
+    const unsigned long long w = wave_kmax(key[k]);
+    if ((t & 63) == 0 && b * TT + k < p.T && w != 0ull) atomicMax(p.keys + b * TT + k, w);
+  }
+}
+
+__global__ void pf_fill_keys(const lxm_pf_params* __restrict__ pp) {
+  const int i = blockIdx.x * 256 + threadIdx.x;
+  if (i < pp->T) pp->keys[i] = 0ull;
+}
+__global__ void pf_preds(const lxm_pf_params* __restrict__ pp) {
+  const int i = blockIdx.x * 256 + threadIdx.x;
+  if (i < pp->T) pp->preds[i] = argmax_idx(pp->keys[i]);
+}
+
+// ---------------------------------------------------------------------------------------------
+// The embedding rows of the positions' tokens into the residual tiles (one workgroup per tile).
+template <bool BF>
+__global__ __launch_bounds__(NT) void pf_embed(const lxm_pf_params* __restrict__ pp) {
+  extern __shared__ __align__(16) uint8_t sm[];
+  const lxm_pf_params& p = *pp;
+  const int t = threadIdx.x, H = p.hidden;
+  const int64_t b = blockIdx.x;
+  float* HV = reinterpret_cast<float*>(sm);
+  for (int i = t; i < H * TT; i += NT) HV[i] = 0.0f;
+  __syncthreads();
+#pragma unroll
+  for (int k = 0; k < TT; k++) {
+    const int64_t pos = b * TT + k;
+    if (pos >= p.T) continue;
+    const int tok = p.tokens[pos];
+    if (tok < 0 || tok >= p.vocab) {
+      if (t == 0) *p.err = 1;
+      continue;
+    }
+    const int64_t e0 = p.emb_ptr[tok], e1 = p.emb_ptr[tok + 1];
+    for (int64_t e = e0 + t; e < e1; e += NT) {
+      const lxm_pf_ent en = p.emb_ent[e];
+      HV[en.off * TT + k] = en.w;
+    }
+  }
+  __syncthreads();
+  for (int c = t; c < H; c += NT) st_col<BF>(p.h, b, H, c, reinterpret_cast<const v4f*>(HV)[c]);
+}
+
+// row-major (T, H) <-> tiles, one element per thread
+template <bool BF>
+__global__ void pf_tiles_k(const void* x, void* y, int T, int H, int dir) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= (int64_t)T * H) return;
+  const int t = (int)(i / H), c = (int)(i % H);
+  const int64_t j = el_idx(H, t, c);
+  const int64_t from = dir == 0 ? i : j, to = dir == 0 ? j : i;
+  if constexpr (BF) reinterpret_cast<uint16_t*>(y)[to] = reinterpret_cast<const uint16_t*>(x)[from];
+  else reinterpret_cast<float*>(y)[to] = reinterpret_cast<const float*>(x)[from];
+}
+
+// ---------------------------------------------------------------------------------------------
+// Host side.
+static int tile_lds(int n_units_max) {
+  const int cols = n_units_max > MAXH ? n_units_max : MAXH;
+  return X_XM + 16 * cols;
+}
+#define ACT_LDS (A_MISC + 16)
+#define ACT_GRID 1024
+#define OUT_GRID 1024
+
+// Dynamic LDS above 64 KB needs the kernel's attribute raised first (to the bytes it launches with).
+static hipError_t lds_attr(const void* k, int bytes) {
+  return hipFuncSetAttribute(k, hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
+}
+
+template <bool BF>
+static hipError_t run_layers(const lxm_pf_params* ph, const lxm_pf_params* pd, int l0, int l1,
+                             hipStream_t st) {
+  const int ntiles = ph->ntiles;
+  int umax = 0;
+  for (int L = l0; L < l1; L++) umax = ph->layers_host[L].n_units > umax ? ph->layers_host[L].n_units : umax;
+  const int xl = tile_lds(umax);
+  hipError_t e = lds_attr((const void*)pf_tile<BF>, xl);
+  if (e == hipSuccess) e = lds_attr((const void*)pf_act<BF>, ACT_LDS);
+  if (e == hipSuccess) e = lds_attr((const void*)pf_out<BF>, 4 * VD * LXM_PF_MAXVS + 16);
+  if (e != hipSuccess) return e;
+  for (int L = l0; L < l1; L++) {
+    const lxm_pf_layer& ly = ph->layers_host[L];
+    hipLaunchKernelGGL(pf_tile<BF>, dim3(ntiles), dim3(NT), xl, st, pd, L == l0 ? -1 : L - 1, L);
+    hipLaunchKernelGGL(pf_compact, dim3(1), dim3(C_NT), 0, st, pd, L);
+    hipLaunchKernelGGL(pf_act<BF>, dim3(ACT_GRID), dim3(NT), ACT_LDS, st, pd, L);
+    hipLaunchKernelGGL(pf_tail<BF>, dim3((ph->n_conv + 255) / 256), dim3(256), 0, st, pd, L);
+    if (ly.n_vs > 0) hipLaunchKernelGGL(pf_delta<BF>, dim3(ly.n_vs), dim3(NT), 0, st, pd, L);
+    if (ly.n_vs > 0)
+      hipLaunchKernelGGL(pf_out<BF>, dim3(OUT_GRID), dim3(NT), 4 * VD * ly.n_vs + 16, st, pd, L);
+  }
+  hipLaunchKernelGGL(pf_tile<BF>, dim3(ntiles), dim3(NT), xl, st, pd, l1 - 1, -1);
+  return hipGetLastError();
+}
+
+template <bool BF>
+static hipError_t run_head(const lxm_pf_params* ph, const lxm_pf_params* pd, hipStream_t st) {
+  const int ntiles = ph->ntiles, T = ph->T;
+  hipError_t e = lds_attr((const void*)pf_tile<BF>, tile_lds(0));
+  if (e == hipSuccess) e = lds_attr((const void*)pf_head<BF>, 16 * ph->hidden + 64);
+  if (e != hipSuccess) return e;
+  hipLaunchKernelGGL(pf_fill_keys, dim3((T + 255) / 256), dim3(256), 0, st, pd);
+  hipLaunchKernelGGL(pf_tile<BF>, dim3(ntiles), dim3(NT), tile_lds(0), st, pd, -1, -2);
+  hipLaunchKernelGGL(pf_head<BF>, dim3(ntiles * LXM_PF_SLICES), dim3(NT), 16 * ph->hidden + 64, st, pd);
+  hipLaunchKernelGGL(pf_preds, dim3((T + 255) / 256), dim3(256), 0, st, pd);
+  return hipGetLastError();
+}
+
+static bool ok_params(const lxm_pf_params* ph) {
+  return ph && ph->hidden > 0 && ph->hidden <= MAXH && ph->T > 0 &&
+         ph->ntiles == (ph->T + TT - 1) / TT && ph->layers_host;
+}
+
+extern "C" {
+
+int lxm_pf_layers(const lxm_pf_params* ph, const lxm_pf_params* pd, int l0, int l1, void* stream) {
+  if (!ok_params(ph) || l0 < 0 || l1 > ph->n_layers || l0 >= l1) return (int)hipErrorInvalidValue;
+  for (int L = l0; L < l1; L++) {
+    const lxm_pf_layer& ly = ph->layers_host[L];
+    if (ly.n_units > LXM_PF_UPT * NT || ly.n_ks > LXM_PF_MAXKS || ly.n_vs > LXM_PF_MAXVS ||
+        ly.rec_bytes > ph->max_rec)
+      return (int)hipErrorInvalidValue;
+  }
+  hipStream_t st = (hipStream_t)stream;
+  return (int)(ph->bf16 ? run_layers<true>(ph, pd, l0, l1, st) : run_layers<false>(ph, pd, l0, l1, st));
+}
+
+int lxm_pf_head(const lxm_pf_params* ph, const lxm_pf_params* pd, void* stream) {
+  if (!ok_params(ph)) return (int)hipErrorInvalidValue;
+  hipStream_t st = (hipStream_t)stream;
+  return (int)(ph->bf16 ? run_head<true>(ph, pd, st) : run_head<false>(ph, pd, st));
+}
+
+int lxm_pf_embed(const lxm_pf_params* ph, const lxm_pf_params* pd, void* stream) {
+  if (!ok_params(ph)) return (int)hipErrorInvalidValue;
+  hipStream_t st = (hipStream_t)stream;
+  const int lds = 16 * ph->hidden;
+  hipError_t e = lds_attr(ph->bf16 ? (const void*)pf_embed<true> : (const void*)pf_embed<false>, lds);
+  if (e != hipSuccess) return (int)e;
+  if (ph->bf16) hipLaunchKernelGGL(pf_embed<true>, dim3(ph->ntiles), dim3(NT), lds, st, pd);
+  else hipLaunchKernelGGL(pf_embed<false>, dim3(ph->ntiles), dim3(NT), lds, st, pd);
+  return (int)hipGetLastError();
+}
+
+int lxm_pf_tiles(const lxm_pf_params* ph, const void* x, void* y, int dir, void* stream) {
+  if (!ok_params(ph) || (dir != 0 && dir != 1)) return (int)hipErrorInvalidValue;
+  const int64_t n = (int64_t)ph->T * ph->hidden;
+  hipStream_t st = (hipStream_t)stream;
+  const dim3 g((unsigned)((n + 255) / 256));
+  if (ph->bf16) hipLaunchKernelGGL(pf_tiles_k<true>, g, dim3(256), 0, st, x, y, ph->T, ph->hidden, dir);
+  else hipLaunchKernelGGL(pf_tiles_k<false>, g, dim3(256), 0, st, x, y, ph->T, ph->hidden, dir);
+  return (int)hipGetLastError();
+}
+
+int lxm_pf_lds(int hidden, int n_units) {
+  (void)hidden;
+  return tile_lds(n_units);
+}
+
+}  // extern "C"

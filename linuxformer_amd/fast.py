@@ -65,6 +65,64 @@ class Fast:
                 "decays": np.unique(ly.in_proj_a.rows),
                 "out_rows": np.unique(ly.out_proj.rows)}
 
+    # ---- verified mode: the native prefill (linuxformer_amd/prefill.py)
+    def prefill(self, device="cuda"):
+        """The packed prefill tables on device (built once per device)."""
+        from .prefill import Prefill
+
+        dev = torch.device(device)
+        if dev.type == "cuda" and dev.index is None:
+            dev = torch.device("cuda", torch.cuda.current_device())
+        if getattr(self, "_pf", None) is None or self._pf.dev != dev:
+            self._pf = Prefill(self, dev)
+        return self._pf
+
+    def _dtype(self):
+        return torch.bfloat16 if self.sm.dims.dtype == "bf16" else torch.float32
+
+    @torch.no_grad()
+    def forward(self, h: torch.Tensor, cache) -> torch.Tensor:
+        """h (1, T, hidden) -> (1, T, hidden), updating the cache's conv and recurrent states
+        (lx/lx/fast.py:252-258). Each position sees exactly the stock decode step."""
+        assert h.dim() == 3 and h.shape[0] == 1 and h.shape[2] == self.sm.dims.hidden
+        pf = self.prefill(h.device)
+        T = h.shape[1]
+        pf.to_tiles(h[0].to(self._dtype()))
+        pf.layers(T, cache)
+        return pf.from_tiles(T)[None]
+
+    @torch.no_grad()
+    def layer(self, L: int, h: torch.Tensor, cache) -> None:
+        """One chip layer on h (T, hidden), in place (lx/lx/fast.py:260-269)."""
+        assert h.dim() == 2 and h.shape[1] == self.sm.dims.hidden and h.dtype == self._dtype()
+        pf = self.prefill(h.device)
+        T = h.shape[0]
+        pf.to_tiles(h)
+        pf.layers(T, cache, L, L + 1)
+        h.copy_(pf.from_tiles(T))
+
+    @torch.no_grad()
+    def head_argmax(self, h: torch.Tensor, block: int | None = None) -> torch.Tensor:
+        """The final norm and the tied head's first maximum at each position of h (T, hidden)
+        or (1, T, hidden): int64 (T,) (lx/lx/fast.py:544-550; block sizes are the kernel's
+        own)."""
+        x = h.reshape(-1, self.sm.dims.hidden).to(self._dtype())
+        pf = self.prefill(h.device)
+        pf.to_tiles(x)
+        return pf.head(x.shape[0]).to(torch.int64).clone()
+
+    @torch.no_grad()
+    def decode(self, h: torch.Tensor, cache) -> torch.Tensor:
+        """One decode step of every chip layer on h (1, 1, hidden) (lx/lx/fast.py:365-540):
+        the forward of a single position."""
+        return self.forward(h, cache)
+
+    @torch.no_grad()
+    def verify(self, tokens, cache) -> torch.Tensor:
+        """Verified mode end to end: the tokens' embedding rows, every layer, the head; returns
+        each position's prediction (int32, on the device; prediction i is for token i + 1)."""
+        return self.prefill().verify(tokens, cache)
+
     def embed_rows(self, offset: int = 0) -> Rows:
         """The embedding rows of chip tokens offset .. offset + vocab (all columns)."""
         lo, hi = self.head_range

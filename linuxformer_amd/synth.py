@@ -129,7 +129,7 @@ class SparseModel:
 
 @dataclass
 class Spec:
-    """A synthetic stack: shapes, density, gates and seeds (2 and 5)."""
+    """A synthetic stack: shapes, density, gates and seeds (2, 3 and 5)."""
     name: str
     dims: Dims
     seed: int = 0
@@ -160,6 +160,16 @@ def config2(seed: int = 2) -> Spec:
     gates exactly one layer (1/37 = 2.7 % of layer-steps, BASELINE's "about 2 %")."""
     return Spec("c2", Dims(hidden=3572, n_layers=37, vocab=459_982, dtype="bf16"), seed=seed,
                 state="normal", n_steps=262_144, p_gate=1.0 / 37)
+
+
+def config3(seed: int = 2) -> Spec:
+    """verified mode (the prefill) over config 2's stack, 65,536 seeded
+    uniform token ids per call. A token gates a layer with probability 0.35 % (0.13 gates per
+    token over the 37 layers), so a live key head (a quarter of them) is active in a 64-token
+    chunk with probability 1 - (1 - 0.0035)^64 = 20 %: 5 % of (key head, chunk) pairs, as the
+    config states."""
+    s = config2(seed)
+    return replace(s, name="c3", p_gate=0.0035, n_steps=65_536)
 
 
 def config5(seed: int = 2) -> Spec:
@@ -319,6 +329,12 @@ def init_state(model: SparseModel, kind: str | None = None, seed: int | None = N
         for L in range(d.n_layers):
             rec[L] = _rng(seed, L, _STATE).standard_normal((d.nv, d.kd, d.vd), np.float32)
     return conv, rec
+
+
+def tokens(spec: Spec, n: int | None = None, seed: int = 0) -> np.ndarray:
+    """n seeded uniform token ids over the vocabulary (config 3's verified-mode input)."""
+    n = spec.n_steps if n is None else n
+    return _rng(spec.seed, 1 + seed, _START).integers(0, spec.dims.vocab, n).astype(np.int64)
 
 
 def start_token(spec: Spec) -> int:

@@ -1,0 +1,191 @@
+"""Parity of the HIP verified-mode forward (the prefill: Fast.forward / layer / head_argmax /
+decode) with the oracle, on an MI355X, through the C ABI.
+
+Each position sees exactly the stock decode step, so a prefill over T positions must leave what
+T forced decode steps of the oracle leave: every position's prediction, every layer's residual
+at every position, the conv windows and the recurrent states, compared bit for bit. At full
+config-3 size the prefill is checked against the decode kernel driven by the same tokens (two
+independent GPU paths of the same semantics).
+"""
+
+import numpy as np
+import pytest
+import torch
+
+from linuxformer_amd import fast, mega, mk_build, synth
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def cuda():
+    assert torch.cuda.is_available(), "the gpu tests need an MI355X"
+    mk_build.load()  # the native library, never a fallback
+    return torch.device("cuda", 0)
+
+
+def _specs():
+    return {"small": synth.small(), "small_fp32": synth.small(dtype="fp32", seed=3),
+            "c1": synth.config1(), "c2": synth.config2(), "c3": synth.config3(),
+            "c5": synth.config5()}
+
+
+_MODELS = {}
+
+
+def model(name):
+    if name not in _MODELS:
+        spec = _specs()[name]
+        m = synth.build(spec)
+        conv0, rec0 = synth.init_state(m)
+        _MODELS[name] = (spec, m, conv0, rec0, fast.Fast(m))
+    return _MODELS[name]
+
+
+def bits(a):
+    return np.ascontiguousarray(a, np.float32).view(np.uint32)
+
+
+def check(name, tokens, conv0=None, per_layer=True):
+    """The prefill over tokens from the model's initial state against the oracle's forced
+    decode of the same tokens, bit for bit."""
+    from oracle import oracle as ox
+
+    spec, m, c0, r0, f = model(name)
+    conv0 = c0 if conv0 is None else conv0
+    tokens = [int(x) for x in tokens]
+    T, d = len(tokens), m.dims
+    print(f"[gpu-test] prefill {name}: T={T} per_layer={per_layer}", flush=True)
+    cache = fast.StateCache(conv0, r0, d.dtype, "cuda")
+    pf = f.prefill("cuda")
+    if per_layer:
+        pf.embed(tokens)
+        traces = []
+        for L in range(d.n_layers):
+            pf.layers(T, cache, L, L + 1)
+            traces.append(pf.from_tiles(T).float().cpu().numpy())
+        preds = pf.head(T).cpu().numpy()
+    else:
+        preds = f.verify(tokens, cache).cpu().numpy()
+    om = ox.OracleModel(m)
+    c, r = conv0.copy(), r0.copy()
+    po, _, tro = om.decode(c, r, tokens, T, trace=per_layer)
+    if per_layer:
+        for L in range(d.n_layers):
+            same = bits(traces[L]) == bits(tro[:, L])
+            assert same.all(), (L, np.argwhere(~same)[:5].tolist())
+    assert preds.tolist() == po.tolist()
+    assert (bits(cache.conv_numpy()) == bits(c)).all()
+    assert (bits(cache.rec_numpy()) == bits(r)).all()
+    return preds
+
+
+def _toks(name, T, seed=0):
+    spec = _specs()[name]
+    return synth.tokens(spec, T, seed)
+
+
+def test_prefill_small(cuda):
+    check("small", _toks("small", 37))
+
+
+def test_prefill_small_fp32(cuda):
+    check("small_fp32", _toks("small_fp32", 30))
+
+
+def test_prefill_config1(cuda):
+    """BASELINE config 1's layer (fp32): 256 positions, a quarter of them gated."""
+    check("c1", _toks("c1", 256))
+
+
+def test_prefill_config2(cuda):
+    """The 37-layer bf16 stack from its N(0,1) state: 48 positions, every layer's residual."""
+    check("c2", _toks("c2", 48))
+
+
+def test_prefill_config5(cuda):
+    """Half of the layer-steps gated: 16 positions."""
+    check("c5", _toks("c5", 16))
+
+
+def test_prefill_short_from_live_windows(cuda):
+    """1, 2, 3 and 5 positions from nonzero windows on every channel: the first positions'
+    convs read the windows the cache held, and short calls shift them."""
+    spec, m, c0, r0, f = model("small")
+    rng = np.random.default_rng(11)
+    conv0 = synth._round(rng.standard_normal(c0.shape).astype(np.float32), "bf16")
+    for T in (1, 2, 3, 5):
+        check("small", _toks("small", T, seed=T), conv0=conv0)
+
+
+def test_prefill_calls_continue(cuda):
+    """Two calls (10, then 27 positions) leave the states of one call of 37 and the same
+    predictions."""
+    from oracle import oracle as ox
+
+    spec, m, c0, r0, f = model("small")
+    toks = [int(x) for x in _toks("small", 37, seed=4)]
+    cache = fast.StateCache(c0, r0, m.dims.dtype, "cuda")
+    p1 = f.verify(toks[:10], cache).cpu().numpy().tolist()
+    p2 = f.verify(toks[10:], cache).cpu().numpy().tolist()
+    c, r = c0.copy(), r0.copy()
+    po, _, _ = ox.OracleModel(m).decode(c, r, toks, 37)
+    assert p1 + p2 == po.tolist()
+    assert (bits(cache.conv_numpy()) == bits(c)).all()
+    assert (bits(cache.rec_numpy()) == bits(r)).all()
+
+
+def test_fast_api_forward_decode_head(cuda):
+    """The reference's Fast API on residual tensors: forward (1, T, hidden), decode (1, 1,
+    hidden), head_argmax (int64) agree with the oracle's layer steps and head."""
+    from oracle import oracle as ox
+
+    spec, m, c0, r0, f = model("small")
+    d = m.dims
+    toks = [int(x) for x in _toks("small", 9, seed=2)]
+    emb = m.embed.dense()[toks]  # exact in bf16
+    h = torch.from_numpy(emb).to("cuda", torch.bfloat16)[None]
+    cache = fast.StateCache(c0, r0, d.dtype, "cuda")
+    out = f.forward(h[:, :8], cache)
+    out1 = f.decode(h[:, 8:], cache)
+    hs = torch.cat([out, out1], 1)[0]
+    preds = f.head_argmax(hs)
+    om = ox.OracleModel(m)
+    c, r = c0.copy(), r0.copy()
+    want = np.zeros((9, d.hidden), np.float32)
+    for i in range(9):
+        x = emb[i].astype(np.float32).copy()
+        for L in range(d.n_layers):
+            om.layer_step(L, x, c[L], r[L])
+        want[i] = x
+    assert (bits(hs.float().cpu().numpy()) == bits(want)).all()
+    assert preds.dtype == torch.int64
+    assert preds.cpu().numpy().tolist() == om.head(want).tolist()
+    assert (bits(cache.rec_numpy()) == bits(r)).all()
+
+
+def test_prefill_token_out_of_range(cuda):
+    spec, m, c0, r0, f = model("small")
+    cache = fast.StateCache(c0, r0, m.dims.dtype, "cuda")
+    with pytest.raises(ValueError):
+        f.verify([0, m.dims.vocab], cache)
+
+
+def test_config3_full_matches_decode_kernel(cuda):
+    """BASELINE config 3 at full size: 65,536 uniform tokens through the 37-layer stack. The
+    prefill's predictions and final states equal those of the decode kernel forced through
+    the same tokens (65,536 steps), bit for bit."""
+    spec, m, c0, r0, f = model("c3")
+    toks = _toks("c3", 65_536)
+    print("[gpu-test] c3 prefill 65,536", flush=True)
+    cache = fast.StateCache(c0, r0, "bf16", "cuda")
+    preds = f.verify(toks, cache).cpu().numpy()
+    conv_p, rec_p = cache.conv_numpy(), cache.rec_numpy()
+    del cache
+    print("[gpu-test] c3 decode kernel 65,536", flush=True)
+    cache2 = fast.StateCache(c0, r0, "bf16", "cuda")
+    mg = mega.Mega(f, m, cache2, 0)
+    want = mg.run(toks.tolist(), len(toks))
+    assert preds.tolist() == want
+    assert (bits(cache2.conv_numpy()) == bits(conv_p)).all()
+    assert (bits(cache2.rec_numpy()) == bits(rec_p)).all()
