@@ -127,8 +127,9 @@ int lxm_pf_embed(const lxm_pf_params* p_host, const lxm_pf_params* p_dev, void* 
 /* Layout conversion: dir 0 (T, hidden) row-major -> tiles (p->h), dir 1 tiles -> row-major. x is
    in the model dtype. */
 int lxm_pf_tiles(const lxm_pf_params* p_host, const void* x, void* y, int dir, void* stream);
-/* LDS bytes the tile kernel needs (it is launched with them; the device allows lxm_max_lds()). */
-int lxm_pf_lds(int hidden, int n_units);
+/* LDS bytes the tile kernel needs for a model dtype (bf16 != 0) and a layer's MLP units (it is
+   launched with them; the device allows lxm_max_lds()). */
+int lxm_pf_lds(int bf16, int n_units);
 
 #ifdef __cplusplus
 }

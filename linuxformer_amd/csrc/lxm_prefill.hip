@@ -114,7 +114,33 @@ __device__ __forceinline__ float norm_r(float ss, int H, float eps) {
 // (the oracle's CSR rows: ascending columns; its zero-x skips change no bits, a sum from +0 is
 // never -0). Entries load four at a time (every table is followed by four padding entries);
 // the terms past the row's end are not added.
-template <bool BF>
+// LDS tile vectors: a column of the 4 positions per slot, fp32 (16 bytes), or bf16 (8 bytes;
+// HALF) where every value kept there is exact in bf16. at(): by a table offset (16 x column).
+template <bool HALF>
+struct TV {
+  static constexpr int B = HALF ? 8 : 16;
+  static __device__ __forceinline__ v4f at(const uint8_t* v, int off) {
+    if constexpr (HALF) {
+      const v2u u = *reinterpret_cast<const v2u*>(v + (off >> 1));
+      return v4f{bitsf(u.x << 16), bitsf(u.x & 0xffff0000u), bitsf(u.y << 16), bitsf(u.y & 0xffff0000u)};
+    } else {
+      return *reinterpret_cast<const v4f*>(v + off);
+    }
+  }
+  static __device__ __forceinline__ v4f get(const uint8_t* v, int c) { return at(v, 16 * c); }
+  static __device__ __forceinline__ void put(uint8_t* v, int c, v4f x) {
+    if constexpr (HALF) {
+      v2u u;
+      u.x = (fbits(x.x) >> 16) | (fbits(x.y) & 0xffff0000u);
+      u.y = (fbits(x.z) >> 16) | (fbits(x.w) & 0xffff0000u);
+      *reinterpret_cast<v2u*>(v + B * c) = u;
+    } else {
+      *reinterpret_cast<v4f*>(v + B * c) = x;
+    }
+  }
+};
+
+template <bool BF, bool HALF = false>
 __device__ __forceinline__ v4f dot4(const lxm_pf_ent* __restrict__ e, int n, const uint8_t* x) {
   v4f s = {0.0f, 0.0f, 0.0f, 0.0f};
   for (int k0 = 0; k0 < n; k0 += 4) {
@@ -123,7 +149,7 @@ __device__ __forceinline__ v4f dot4(const lxm_pf_ent* __restrict__ e, int n, con
     for (int j = 0; j < 4; j++) en[j] = e[k0 + j];
     v4f xv[4];
 #pragma unroll
-    for (int j = 0; j < 4; j++) xv[j] = *reinterpret_cast<const v4f*>(x + en[j].off);
+    for (int j = 0; j < 4; j++) xv[j] = TV<HALF>::at(x, en[j].off);
 #pragma unroll
     for (int j = 0; j < 4; j++)
       if (k0 + j < n) s = acc4<BF>(s, xv[j], en[j].w);
@@ -150,11 +176,11 @@ __device__ __forceinline__ float dot1(const lxm_pf_ent* __restrict__ e, int n, c
 
 // The 512-lane hidden sum of x * x for the four positions of a tile (the decode's order: thread
 // t adds its columns 4t..4t+3, then 2048+4t..2048+4t+3; waves at offsets 32..1; the 8 wave
-// totals at offsets 4, 2, 1). With plus0, each column also becomes x + 0 (the residual add of a
-// row with no term: -0 becomes +0). Every thread gets the sums. wsum: 8 vectors of LDS, not
-// reused before the next barrier.
-template <bool BF>
-__device__ __forceinline__ v4f hsum(v4f* HV, v4f* wsum, bool plus0) {
+// totals at offsets 4, 2, 1; columns >= H are +0 and add nothing). With plus0, each column also
+// becomes x + 0 (the residual add of a row with no term: -0 becomes +0). Every thread gets the
+// sums. wsum: 8 vectors of LDS, not reused before the next barrier.
+template <bool BF, bool HALF>
+__device__ __forceinline__ v4f hsum(uint8_t* HV, int H, v4f* wsum, bool plus0) {
   const int t = threadIdx.x;
   v4f s = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
@@ -162,10 +188,11 @@ __device__ __forceinline__ v4f hsum(v4f* HV, v4f* wsum, bool plus0) {
 #pragma unroll
     for (int i = 0; i < 4; i++) {
       const int c = half * 2048 + 4 * t + i;
-      v4f x = HV[c];
+      if (c >= H) continue;
+      v4f x = TV<HALF>::get(HV, c);
       if (plus0) {
         x = v4f{x.x + 0.0f, x.y + 0.0f, x.z + 0.0f, x.w + 0.0f};
-        HV[c] = x;
+        TV<HALF>::put(HV, c, x);
       }
       s = v4f{acc<BF>(s.x, x.x, x.x), acc<BF>(s.y, x.y, x.y), acc<BF>(s.z, x.z, x.z),
               acc<BF>(s.w, x.w, x.w)};
@@ -190,32 +217,59 @@ __device__ __forceinline__ v4f hsum(v4f* HV, v4f* wsum, bool plus0) {
 // factor r1 per position, and which of the layer's key slots have a nonzero query/key projection
 // at each position, and whether a decay can act (bit 31); or Ln == -2: the final norm into hn.
 // LDS: 512 bytes of sums and masks, the residual (4,096 columns), the norm's output (then the
-// MLP units' outputs).
+// MLP units' outputs), as tile vectors in the model dtype (bf16 models: 66 KB, two workgroups
+// per CU).
 #define X_HV 512
-#define X_XM (X_HV + 16 * MAXH)
+// A residual tile from HBM (model dtype) into LDS tile vectors (bf16 if HALF): every thread's
+// columns (t, t + 512, ...) loaded at once.
+template <bool BF, bool HALF>
+__device__ __forceinline__ void load_tile(const void* h, int64_t b, int H, uint8_t* HV) {
+  const int t = threadIdx.x;
+  v4f x[MAXH / NT];
+#pragma unroll
+  for (int k = 0; k < MAXH / NT; k++)
+    x[k] = t + k * NT < H ? ld_col<BF>(h, b, H, t + k * NT) : v4f{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+  for (int k = 0; k < MAXH / NT; k++)
+    if (t + k * NT < H) TV<HALF>::put(HV, t + k * NT, x[k]);
+}
+// XM = D((HV * r) * w1) for every column, the weights loaded at once
+template <bool BF>
+__device__ __forceinline__ void norm_tile(const uint8_t* HV, uint8_t* XM, int H, v4f r,
+                                          const float* w1) {
+  const int t = threadIdx.x;
+  float w[MAXH / NT];
+#pragma unroll
+  for (int k = 0; k < MAXH / NT; k++) w[k] = t + k * NT < H ? w1[t + k * NT] : 0.0f;
+#pragma unroll
+  for (int k = 0; k < MAXH / NT; k++)
+    if (t + k * NT < H) TV<BF>::put(XM, t + k * NT, norm4<BF>(TV<BF>::get(HV, t + k * NT), r, w[k]));
+}
+
+template <bool BF>
+__host__ __device__ constexpr int x_xm() { return X_HV + TV<BF>::B * MAXH; }
 template <bool BF>
 __global__ __launch_bounds__(NT) void pf_tile(const lxm_pf_params* __restrict__ pp, int Lm, int Ln) {
   extern __shared__ __align__(16) uint8_t sm[];
+  using V = TV<BF>;
   const lxm_pf_params& p = *pp;
   const int t = threadIdx.x, H = p.hidden;
   const int64_t b = blockIdx.x;
   uint32_t* smask = reinterpret_cast<uint32_t*>(sm);
   v4f* wsA = reinterpret_cast<v4f*>(sm + 64);
   v4f* wsB = reinterpret_cast<v4f*>(sm + 192);
-  v4f* HV = reinterpret_cast<v4f*>(sm + X_HV);
-  v4f* XM = reinterpret_cast<v4f*>(sm + X_XM);
-  const uint8_t* xm = sm + X_XM;
+  uint8_t* HV = sm + X_HV;
+  uint8_t* XM = sm + x_xm<BF>();
   if (t < TT) smask[t] = 0;
-  for (int c = t; c < MAXH; c += NT) HV[c] = c < H ? ld_col<BF>(p.h, b, H, c) : v4f{0.0f, 0.0f, 0.0f, 0.0f};
+  load_tile<BF, BF>(p.h, b, H, HV);
   __syncthreads();
   if (Lm >= 0) {
     const lxm_pf_layer& ly = p.layers[Lm];
     const lxm_pf_ent* ent = tab<lxm_pf_ent>(p.blob, ly.ent);
-    const v4f ss = hsum<BF>(HV, wsA, false);
+    const v4f ss = hsum<BF, BF>(HV, H, wsA, false);
     const v4f r = {norm_r(ss.x, H, ly.eps), norm_r(ss.y, H, ly.eps), norm_r(ss.z, H, ly.eps),
                    norm_r(ss.w, H, ly.eps)};
-    const float* w1 = tab<float>(p.blob, ly.w1_post);
-    for (int c = t; c < H; c += NT) XM[c] = norm4<BF>(HV[c], r, w1[c]);
+    norm_tile<BF>(HV, XM, H, r, tab<float>(p.blob, ly.w1_post));
     __syncthreads();
     // units: act = D(D(silu(D(gate . x))) * D(up . x))
     const lxm_pf_unit* un = tab<lxm_pf_unit>(p.blob, ly.units);
@@ -225,8 +279,8 @@ __global__ __launch_bounds__(NT) void pf_tile(const lxm_pf_params* __restrict__ 
       const int u = t + i * NT;
       if (u < ly.n_units) {
         const lxm_pf_unit q = un[u];
-        const v4f g = rd4<BF>(dot4<BF>(ent + q.gs, q.gn, xm));
-        const v4f v = rd4<BF>(dot4<BF>(ent + q.us, q.un, xm));
+        const v4f g = rd4<BF>(dot4<BF, BF>(ent + q.gs, q.gn, XM));
+        const v4f v = rd4<BF>(dot4<BF, BF>(ent + q.us, q.un, XM));
         a[i] = v4f{rd<BF>(silu_rd<BF>(g.x) * v.x), rd<BF>(silu_rd<BF>(g.y) * v.y),
                    rd<BF>(silu_rd<BF>(g.z) * v.z), rd<BF>(silu_rd<BF>(g.w) * v.w)};
       }
@@ -234,32 +288,31 @@ __global__ __launch_bounds__(NT) void pf_tile(const lxm_pf_params* __restrict__ 
     __syncthreads();
 #pragma unroll
     for (int i = 0; i < LXM_PF_UPT; i++)
-      if (t + i * NT < ly.n_units) XM[t + i * NT] = a[i];
+      if (t + i * NT < ly.n_units) V::put(XM, t + i * NT, a[i]);
     __syncthreads();
     // down_proj rows over the units (entries 16 x unit position), added to the residual
     const lxm_pf_drow* dr = tab<lxm_pf_drow>(p.blob, ly.drows);
     for (int i = t; i < ly.n_drows; i += NT) {
       const lxm_pf_drow d = dr[i];
-      const v4f s = rd4<BF>(dot4<BF>(ent + d.start, d.len, xm));
-      HV[d.row] = rd4<BF>(HV[d.row] + s);
+      const v4f s = rd4<BF>(dot4<BF, BF>(ent + d.start, d.len, XM));
+      V::put(HV, d.row, rd4<BF>(V::get(HV, d.row) + s));
     }
     __syncthreads();
   }
   if (Ln >= 0) {
     const lxm_pf_layer& ly = p.layers[Ln];
     const lxm_pf_ent* ent = tab<lxm_pf_ent>(p.blob, ly.ent);
-    const v4f ss = hsum<BF>(HV, wsB, Lm >= 0);
+    const v4f ss = hsum<BF, BF>(HV, H, wsB, Lm >= 0);
     const v4f r = {norm_r(ss.x, H, ly.eps), norm_r(ss.y, H, ly.eps), norm_r(ss.z, H, ly.eps),
                    norm_r(ss.w, H, ly.eps)};
     if (t < TT && b * TT + t < p.T) p.r1[b * TT + t] = t == 0 ? r.x : t == 1 ? r.y : t == 2 ? r.z : r.w;
-    const float* w1 = tab<float>(p.blob, ly.w1_in);
-    for (int c = t; c < H; c += NT) XM[c] = norm4<BF>(HV[c], r, w1[c]);
+    norm_tile<BF>(HV, XM, H, r, tab<float>(p.blob, ly.w1_in));
     __syncthreads();
     // query/key projections of the live key heads' channels: which slots are nonzero
     const lxm_pf_qk* qk = tab<lxm_pf_qk>(p.blob, ly.qk);
     for (int i = t; i < ly.n_qk; i += NT) {
       const lxm_pf_qk q = qk[i];
-      const v4f P = rd4<BF>(dot4<BF>(ent + q.start, q.len, xm));
+      const v4f P = rd4<BF>(dot4<BF, BF>(ent + q.start, q.len, XM));
       const uint32_t bit = 1u << q.kslot;
       if (P.x != 0.0f) atomicOr(smask + 0, bit);
       if (P.y != 0.0f) atomicOr(smask + 1, bit);
@@ -270,7 +323,7 @@ __global__ __launch_bounds__(NT) void pf_tile(const lxm_pf_params* __restrict__ 
     const lxm_pf_dec* dc = tab<lxm_pf_dec>(p.blob, ly.dec);
     for (int i = t; i < ly.n_dec; i += NT) {
       const lxm_pf_dec d = dc[i];
-      const v4f a = d.len ? rd4<BF>(dot4<BF>(ent + d.start, d.len, xm)) : v4f{0.0f, 0.0f, 0.0f, 0.0f};
+      const v4f a = d.len ? rd4<BF>(dot4<BF, BF>(ent + d.start, d.len, XM)) : v4f{0.0f, 0.0f, 0.0f, 0.0f};
       const float na = -cr_exp(d.A_log);
 #pragma unroll
       for (int k = 0; k < TT; k++)
@@ -279,15 +332,20 @@ __global__ __launch_bounds__(NT) void pf_tile(const lxm_pf_params* __restrict__ 
     __syncthreads();
     if (t < TT && b * TT + t < p.T) p.mask[b * TT + t] = smask[t];
   } else if (Ln == -2) {
-    const v4f ss = hsum<BF>(HV, wsB, Lm >= 0);
+    const v4f ss = hsum<BF, BF>(HV, H, wsB, Lm >= 0);
     const v4f r = {norm_r(ss.x, H, p.rms_eps), norm_r(ss.y, H, p.rms_eps),
                    norm_r(ss.z, H, p.rms_eps), norm_r(ss.w, H, p.rms_eps)};
-    for (int c = t; c < H; c += NT) st_col<BF>(p.hn, b, H, c, norm4<BF>(HV[c], r, p.w1_final[c]));
+    float w[MAXH / NT];
+#pragma unroll
+    for (int k = 0; k < MAXH / NT; k++) w[k] = t + k * NT < H ? p.w1_final[t + k * NT] : 0.0f;
+#pragma unroll
+    for (int k = 0; k < MAXH / NT; k++)
+      if (t + k * NT < H) st_col<BF>(p.hn, b, H, t + k * NT, norm4<BF>(V::get(HV, t + k * NT), r, w[k]));
   } else if (Lm >= 0) {
-    for (int c = t; c < H; c += NT) HV[c] = HV[c] + v4f{0.0f, 0.0f, 0.0f, 0.0f};
+    for (int c = t; c < H; c += NT) V::put(HV, c, V::get(HV, c) + v4f{0.0f, 0.0f, 0.0f, 0.0f});
   }
   if (Lm >= 0)
-    for (int c = t; c < H; c += NT) st_col<BF>(p.h, b, H, c, HV[c]);
+    for (int c = t; c < H; c += NT) st_col<BF>(p.h, b, H, c, V::get(HV, c));
 }
 
 // ---------------------------------------------------------------------------------------------
@@ -544,6 +602,34 @@ __global__ __launch_bounds__(256) void pf_tail(const lxm_pf_params* __restrict__
 // o = D(S^T q), then the gated norm (TF:168-184) y = D(D(w * D(o * r)) * silu(z)) into the
 // record (over z). The state tile stays in registers: thread (cg, rb) holds columns 4cg..4cg+3 of
 // rows 16rb..16rb+15, one of ATen's 16-row cascade blocks (torch .sum(-2) on the CPU).
+// A candidate's inputs as one thread of the delta kernel holds them (loaded one candidate ahead):
+// the header word, the slot's decay factor, and the thread's share of k and q (threads < 256),
+// v (256..383) or z (384..511), and beta (thread 0).
+struct DeltaIn {
+  uint32_t live;
+  float e, a, b, beta;
+};
+__device__ __forceinline__ DeltaIn delta_in(const uint8_t* rec, const RecOff& ro, int vslot,
+                                            int kslot) {
+  const int t = threadIdx.x;
+  DeltaIn d;
+  d.live = reinterpret_cast<const uint32_t*>(rec)[1];
+  d.e = reinterpret_cast<const float*>(rec + ro.e)[vslot];
+  d.a = d.b = d.beta = 0.0f;
+  if (kslot >= 0) {
+    if (t < KD) {
+      d.a = reinterpret_cast<const float*>(rec + ro.k)[kslot * KD + t];
+      d.b = reinterpret_cast<const float*>(rec + ro.q)[kslot * KD + t];
+    } else if (t < KD + VD) {
+      d.a = reinterpret_cast<const float*>(rec + ro.v)[vslot * VD + t - KD];
+    } else {
+      d.a = reinterpret_cast<const float*>(rec + ro.z)[vslot * VD + t - KD - VD];
+    }
+    if (t == 0) d.beta = reinterpret_cast<const float*>(rec + ro.b)[vslot];
+  }
+  return d;
+}
+
 template <bool BF>
 __global__ __launch_bounds__(NT) void pf_delta(const lxm_pf_params* __restrict__ pp, int L) {
   __shared__ __align__(16) float kn[KD], qn[KD], vb[VD], zb[VD], dl[VD], ob[VD];
@@ -552,21 +638,28 @@ __global__ __launch_bounds__(NT) void pf_delta(const lxm_pf_params* __restrict__
   const lxm_pf_params& p = *pp;
   const lxm_pf_layer& ly = p.layers[L];
   const int t = threadIdx.x, vslot = blockIdx.x, lane = t & 63;
+  // everything the loop needs in registers: its stores to the records could alias p and ly
   const lxm_pf_vs sv = tab<lxm_pf_vs>(p.blob, ly.vs)[vslot];
   const RecOff ro(ly.n_ks, ly.n_vs);
-  const float* gw = tab<float>(p.blob, ly.gnorm);
+  const float* gwp = tab<float>(p.blob, ly.gnorm);
+  const float gw0 = gwp[lane], gw1 = gwp[lane + 64], geps = ly.geps;
   const int count = p.count[L];
+  const int64_t rec_b = ly.rec_bytes;
+  uint8_t* const recs = p.recs;
   const int cg = t & 31, rb = t >> 5;
   v4f* S4 = reinterpret_cast<v4f*>(p.rec[L] + (size_t)sv.vh * KD * VD);
   v4f s[16];
 #pragma unroll
   for (int i = 0; i < 16; i++) s[i] = S4[(rb * 16 + i) * (VD / 4) + cg];
   bool wrote = false;
+  DeltaIn nx = {};
+  if (count > 0) nx = delta_in(recs, ro, vslot, sv.kslot);
   for (int j = 0; j < count; j++) {
-    uint8_t* rec = p.recs + (int64_t)j * ly.rec_bytes;
-    const uint32_t livem = reinterpret_cast<const uint32_t*>(rec)[1];
-    const float e = reinterpret_cast<const float*>(rec + ro.e)[vslot];
-    const bool live = sv.kslot >= 0 && ((livem >> sv.kslot) & 1u);
+    uint8_t* rec = recs + (int64_t)j * rec_b;
+    const DeltaIn cur = nx;
+    if (j + 1 < count) nx = delta_in(rec + rec_b, ro, vslot, sv.kslot);
+    const bool live = sv.kslot >= 0 && ((cur.live >> sv.kslot) & 1u);
+    const float e = cur.e;
     int proc = 0;
     if (live || e != 1.0f) {
       wrote = true;
@@ -578,14 +671,14 @@ __global__ __launch_bounds__(NT) void pf_delta(const lxm_pf_params* __restrict__
       if (live) {
         proc = 2;
         if (t < KD) {
-          kn[t] = reinterpret_cast<const float*>(rec + ro.k)[sv.kslot * KD + t];
-          qn[t] = reinterpret_cast<const float*>(rec + ro.q)[sv.kslot * KD + t];
+          kn[t] = cur.a;
+          qn[t] = cur.b;
         } else if (t < KD + VD) {
-          vb[t - KD] = reinterpret_cast<const float*>(rec + ro.v)[vslot * VD + t - KD];
+          vb[t - KD] = cur.a;
         } else {
-          zb[t - KD - VD] = reinterpret_cast<const float*>(rec + ro.z)[vslot * VD + t - KD - VD];
+          zb[t - KD - VD] = cur.a;
         }
-        if (t == 0) beta_s = reinterpret_cast<const float*>(rec + ro.b)[vslot];
+        if (t == 0) beta_s = cur.beta;
         __syncthreads();
         v4f a = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
@@ -624,13 +717,10 @@ __global__ __launch_bounds__(NT) void pf_delta(const lxm_pf_params* __restrict__
           float ss = 0.0f;
           for (int k = lane; k < VD; k += 64) ss = ss + ob[k] * ob[k];
           ss = sum64(ss);
-          const float rr = rsqrt_(ss / (float)VD + ly.geps);
+          const float rr = rsqrt_(ss / (float)VD + geps);
           float* y = reinterpret_cast<float*>(rec + ro.z) + vslot * VD;
-          for (int k = lane; k < VD; k += 64) {
-            const float t1 = rd<BF>(ob[k] * rr);
-            const float t2 = rd<BF>(gw[k] * t1);
-            y[k] = rd<BF>(t2 * silu(zb[k]));
-          }
+          y[lane] = rd<BF>(rd<BF>(gw0 * rd<BF>(ob[lane] * rr)) * silu(zb[lane]));
+          y[lane + 64] = rd<BF>(rd<BF>(gw1 * rd<BF>(ob[lane + 64] * rr)) * silu(zb[lane + 64]));
         }
         __syncthreads();
       }
@@ -706,8 +796,7 @@ __global__ __launch_bounds__(NT) void pf_head(const lxm_pf_params* __restrict__ 
   const int t = threadIdx.x, H = p.hidden;
   const int slice = blockIdx.x % LXM_PF_SLICES;
   const int64_t b = blockIdx.x / LXM_PF_SLICES;
-  v4f* HN = reinterpret_cast<v4f*>(sm);
-  for (int c = t; c < H; c += NT) HN[c] = ld_col<BF>(p.hn, b, H, c);
+  load_tile<BF, false>(p.hn, b, H, sm);
   __syncthreads();
   const int r0 = p.head_slice[slice], r1 = p.head_slice[slice + 1];
   float best[TT];
@@ -803,9 +892,10 @@ __global__ void pf_tiles_k(const void* x, void* y, int T, int H, int dir) {
 
 // ---------------------------------------------------------------------------------------------
 // Host side.
+template <bool BF>
 static int tile_lds(int n_units_max) {
   const int cols = n_units_max > MAXH ? n_units_max : MAXH;
-  return X_XM + 16 * cols;
+  return x_xm<BF>() + TV<BF>::B * cols;
 }
 #define ACT_LDS (A_MISC + 16)
 #define ACT_GRID 1024
@@ -822,7 +912,7 @@ static hipError_t run_layers(const lxm_pf_params* ph, const lxm_pf_params* pd, i
   const int ntiles = ph->ntiles;
   int umax = 0;
   for (int L = l0; L < l1; L++) umax = ph->layers_host[L].n_units > umax ? ph->layers_host[L].n_units : umax;
-  const int xl = tile_lds(umax);
+  const int xl = tile_lds<BF>(umax);
   hipError_t e = lds_attr((const void*)pf_tile<BF>, xl);
   if (e == hipSuccess) e = lds_attr((const void*)pf_act<BF>, ACT_LDS);
   if (e == hipSuccess) e = lds_attr((const void*)pf_out<BF>, 4 * VD * LXM_PF_MAXVS + 16);
@@ -844,11 +934,11 @@ static hipError_t run_layers(const lxm_pf_params* ph, const lxm_pf_params* pd, i
 template <bool BF>
 static hipError_t run_head(const lxm_pf_params* ph, const lxm_pf_params* pd, hipStream_t st) {
   const int ntiles = ph->ntiles, T = ph->T;
-  hipError_t e = lds_attr((const void*)pf_tile<BF>, tile_lds(0));
+  hipError_t e = lds_attr((const void*)pf_tile<BF>, tile_lds<BF>(0));
   if (e == hipSuccess) e = lds_attr((const void*)pf_head<BF>, 16 * ph->hidden + 64);
   if (e != hipSuccess) return e;
   hipLaunchKernelGGL(pf_fill_keys, dim3((T + 255) / 256), dim3(256), 0, st, pd);
-  hipLaunchKernelGGL(pf_tile<BF>, dim3(ntiles), dim3(NT), tile_lds(0), st, pd, -1, -2);
+  hipLaunchKernelGGL(pf_tile<BF>, dim3(ntiles), dim3(NT), tile_lds<BF>(0), st, pd, -1, -2);
   hipLaunchKernelGGL(pf_head<BF>, dim3(ntiles * LXM_PF_SLICES), dim3(NT), 16 * ph->hidden + 64, st, pd);
   hipLaunchKernelGGL(pf_preds, dim3((T + 255) / 256), dim3(256), 0, st, pd);
   return hipGetLastError();
@@ -900,9 +990,8 @@ int lxm_pf_tiles(const lxm_pf_params* ph, const void* x, void* y, int dir, void*
   return (int)hipGetLastError();
 }
 
-int lxm_pf_lds(int hidden, int n_units) {
-  (void)hidden;
-  return tile_lds(n_units);
+int lxm_pf_lds(int bf16, int n_units) {
+  return bf16 ? tile_lds<true>(n_units) : tile_lds<false>(n_units);
 }
 
 }  // extern "C"

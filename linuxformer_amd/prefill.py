@@ -313,7 +313,7 @@ class Prefill:
 
     # ------------------------------------------------------------------------------------------
     def lds_ok(self) -> bool:
-        return self.lib.lxm_pf_lds(self.dims.hidden, self.umax) <= 160 * 1024
+        return self.lib.lxm_pf_lds(int(self.bf), self.umax) <= 160 * 1024
 
     def _buffers(self, T: int) -> None:
         if self._T == T:
