@@ -1,12 +1,20 @@
-"""Benchmark: greedy decode tok/s of the 37-layer synthetic sparse chip stack on one MI355X.
+"""Benchmark: greedy decode tok/s of the 37-layer synthetic sparse chip stack on one MI355X, and
+verified-prefill tok/s of the same stack (BASELINE's two metrics).
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--tokens T] [--config c2]
+                    [--legs decode,prefill] [--pf-calls N] [--pf-tokens T]
 
-A step is one launch of the persistent decode kernel over one chunk of T tokens (default
-262,144), continuing the same greedy stream launch after launch, as
-lx/tools/mega_boot.py runs the boot in 262,144-token launches. The model is the seeded synthetic
-stack (synth.config2: 37 layers, hidden 3572, bf16, 0.08 % density, N(0,1) state); it is built
-and packed on the host, then every input is resident in HBM before the timed region.
+Decode (the headline `value`): a step is one launch of the persistent decode kernel over one
+chunk of T tokens (default 262,144), continuing the same greedy stream launch
+after launch, as lx/tools/mega_boot.py runs the boot in 262,144-token launches. The model is the
+seeded synthetic stack (synth.config2: 37 layers, hidden 3572, bf16, 0.08 % density, N(0,1)
+state); it is built and packed on the host, then every input is resident in HBM before the
+timed region.
+
+Verified prefill (`verified_prefill`): BASELINE config 3, calls of 65,536 seeded uniform tokens
+through the same stack (synth.config3: 0.35 % of token-layers gated, 5 % of (key head, 64-token
+chunk) pairs active), each call embedding, running all 37 layers and taking every position's
+argmax (lx.fast's verified mode), timed with HIP events on the stream.
 
 One JSON line on stdout (the driver's contract); everything else goes to stderr.
 """
@@ -22,7 +30,7 @@ import time
 HERE = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, HERE)
 
-METRIC = "greedy decode tok/s, 37-layer sparse chip stack, 1 MI355X"
+METRIC = "greedy decode tok/s, 37-layer sparse chip stack, 1 MI355X; verified prefill tok/s"
 HBM_PEAK_GBS = 8000.0
 
 
@@ -82,6 +90,73 @@ def cpu_baseline(model, conv0, rec0, start: int, n: int):
     return n / dt, preds
 
 
+def prefill_leg(calls: int, T: int, cpu_tokens: int) -> dict:
+    """verified-mode calls of T seeded uniform tokens; tok/s over the timed
+    calls (HIP events around each call on the current stream, inputs resident)."""
+    import numpy as np
+    import torch
+
+    from linuxformer_amd import fast, synth
+
+    spec = synth.config3()
+    t0 = time.time()
+    model = synth.build(spec)
+    conv0, rec0 = synth.init_state(model)
+    f = fast.Fast(model)
+    dev = torch.device("cuda", 0)
+    cache = fast.StateCache(conv0, rec0, model.dims.dtype, dev)
+    pf = f.prefill(dev)
+    d = model.dims
+    log(f"[bench] c3: built and packed in {time.time() - t0:.1f}s; {json.dumps({k: v for k, v in pf.stats.items() if not isinstance(v, list)})}")
+    stream = torch.cuda.current_stream(dev)
+    first = synth.tokens(spec, T, 0)
+    p0 = pf.verify(first, cache).cpu().numpy()  # warm-up call (and the parity sample below)
+    cand = pf.count.cpu().numpy()[:d.n_layers].astype(np.int64)
+    ms = []
+    for k in range(calls):
+        toks = synth.tokens(spec, T, 1 + k)
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        e0.record(stream)
+        pf.verify(toks, cache)
+        e1.record(stream)
+        torch.cuda.synchronize()
+        ms.append(e0.elapsed_time(e1))
+        log(f"[bench] verified-prefill call {k + 1}/{calls}: {T} tokens in {ms[-1]:.2f} ms")
+    call_ms = sum(ms) / len(ms)
+    # algorithmic bytes per position: the residual read and written per layer (bf16), the head's
+    # normed input, and each value-head slot's state read and written once per layer per call
+    slots = sum(int(pf.layers_h[L].n_vs) for L in range(d.n_layers))
+    esz = 2 if d.dtype == "bf16" else 4
+    b_pos = d.n_layers * 2 * esz * d.hidden + 2 * esz * d.hidden + 2 * 4 * 256 * 128 * slots / T
+    achieved = b_pos * T / (call_ms * 1e-3) / 1e9
+    out = {"metric": "verified prefill tok/s, 37-layer sparse chip stack, 1 MI355X",
+           "value": round(T / (call_ms * 1e-3), 1), "unit": "tok/s", "calls": calls,
+           "ms_per_call": round(call_ms, 3), "tokens_per_call": T,
+           "config": {"workload": f"c3: verified mode over the c2 stack, {T} seeded uniform tokens "
+                                  f"per call, p_gate {spec.p_gate}",
+                      "candidates_per_layer": round(float(cand.mean()), 1),
+                      "value_head_slots": slots},
+           "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS,
+                        "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 5),
+                        "bytes_per_position": round(b_pos)}}
+    if cpu_tokens > 0:
+        from oracle import oracle as ox
+
+        ox.build()
+        om = ox.OracleModel(model)
+        c, r = conv0.copy(), rec0.copy()
+        t = time.perf_counter()
+        po, _, _ = om.decode(c, r, [int(x) for x in first[:cpu_tokens]], cpu_tokens)
+        dt = time.perf_counter() - t
+        out["cpu_baseline"] = {"value": round(cpu_tokens / dt, 2), "unit": "tok/s", "cores": 1,
+                               "kind": "port", "sample": f"the first {cpu_tokens} positions of "
+                               "the warm-up call (C oracle's forced decode, one thread)"}
+        out["check"] = {"oracle_positions": cpu_tokens,
+                        "preds_match": bool(po.tolist() == p0[:cpu_tokens].tolist())}
+    return out
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -91,11 +166,20 @@ def main() -> int:
     ap.add_argument("--warmup-tokens", type=int, default=4096)
     ap.add_argument("--config", default="c2", choices=["c1", "c2", "c5", "small"])
     ap.add_argument("--cpu-tokens", type=int, default=256, help="CPU baseline sample (0: skip)")
+    ap.add_argument("--legs", default="decode,prefill", help="decode, prefill or both")
+    ap.add_argument("--pf-calls", type=int, default=5)
+    ap.add_argument("--pf-tokens", type=int, default=65_536)
+    ap.add_argument("--pf-cpu-tokens", type=int, default=48)
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: the decode is one sequential chain per stream and this "
               f"build runs on a single MI355X (asked for --gpus {args.gpus}).", file=sys.stderr)
         return 2
+
+    legs = set(args.legs.split(","))
+    if "decode" not in legs:
+        print(json.dumps(prefill_leg(args.pf_calls, args.pf_tokens, args.pf_cpu_tokens)), flush=True)
+        return 0
 
     import numpy as np
     import torch
@@ -174,6 +258,10 @@ def main() -> int:
                                "sample": f"first {args.cpu_tokens} tokens of the {spec.name} stream "
                                          f"(C oracle, one thread)"}
         out["check"] = {"oracle_tokens": m, "preds_match": match}
+    if "prefill" in legs:
+        del mg, cache
+        torch.cuda.empty_cache()
+        out["verified_prefill"] = prefill_leg(args.pf_calls, args.pf_tokens, args.pf_cpu_tokens)
     print(json.dumps(out), flush=True)
     return 0
 
