@@ -151,17 +151,26 @@ def pack_layer(f: Fmt, H: int, units, gate_rows, up_rows, down_rows, w_post) -> 
             wv = lane // 64
             G[p, wv] = max(G[p, wv], m[k])
             sh[p, wv] &= bool(shared[k])
+    # "fly": every unit pass of the layer shares its columns (and no unit is long, 4-byte
+    # entries): the kernel forms the MLP norm's output per gathered column from the residual,
+    # D((h * r) * (1 + w)), instead of writing it for every row first; the up slot's free low
+    # half then carries the column's raw norm weight w (bf16 bits)
+    fly = bool(f.e4 and sh.all() and len(p0) + len(p1) == n)
+    wbits = _bf16_bits(np.asarray(w_post, np.float32)) if fly else None
     for p, (lst, lanes, base) in enumerate(placed):
         for k, lane in zip(lst, lanes):
             wv = lane // 64
             meta0[lane] |= np.uint64((k | 0x8000) << (16 * p))
             for j, (c, v) in enumerate(zip(*gate_rows[k])):
                 S[lane, base + 2 * esz * j:base + 2 * esz * j + esz] = _slots_of(f, 4 * c, v)
-            # (a wave whose pass shares columns reads the up slots as bare weights: offset 0)
+            # (a wave whose pass shares columns reads the up slots as bare weights: offset 0,
+            # or in a fly layer the column's norm weight)
             bare = f.e4 and sh[p, wv]
             for j, (c, v) in enumerate(zip(*up_rows[k])):
-                S[lane, base + 2 * esz * j + esz:base + 2 * esz * (j + 1)] = \
-                    _slots_of(f, 0 if bare else 4 * c, v)
+                sl = _slots_of(f, 0 if bare else 4 * c, v)
+                if fly:
+                    sl = [int(sl[0]) | int(wbits[c])]
+                S[lane, base + 2 * esz * j + esz:base + 2 * esz * (j + 1)] = sl
     assert n < 1 << 12
     S[:, f.MA + 0] = meta0
 
@@ -235,7 +244,7 @@ def pack_layer(f: Fmt, H: int, units, gate_rows, up_rows, down_rows, w_post) -> 
     # ---- the wave-uniform words (meta A +2; meta B +3 above its lane's long row)
     for wv in range(NW):
         wa = (int(G[0, wv]) | (int(G[1, wv]) << 4) | (int(sh[0, wv]) << 8) |
-              (int(sh[1, wv]) << 9) | (int(anyu[wv]) << 10))
+              (int(sh[1, wv]) << 9) | (int(anyu[wv]) << 10) | (int(fly) << 11))
         S[wv * 64:(wv + 1) * 64, f.MA + 2] = wa
         wb = (int(dmask[wv]) << 16) | (int(anyr[wv]) << 24)
         S[wv * 64:(wv + 1) * 64, f.MB + 3] = long_r_idx[wv * 64:(wv + 1) * 64] | np.uint64(wb)
@@ -264,7 +273,7 @@ def pack_layer(f: Fmt, H: int, units, gate_rows, up_rows, down_rows, w_post) -> 
     slots_g = sum(2 * int(G[p, wv]) * 64 for p in range(2) for wv in range(NW))
     stats = {"p0": len(p0), "p1": len(p1), "long_units": len(longu), "long_rows": len(longr),
              "unit_fill": round(used_g / max(slots_g, 1), 3), "G": G.tolist(),
-             "down_mask": dmask.tolist()}
+             "down_mask": dmask.tolist(), "fly": fly}
     ent_arr = np.array(ents, np.uint32).reshape(-1) if ents else np.zeros(0, np.uint32)
     # 16-byte words a thread loads per layer, averaged over the waves
     stats["words_per_thread"] = sum(f.U0 // 4 + ((wave_words >> (8 * w)) & 15) +

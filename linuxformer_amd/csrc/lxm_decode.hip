@@ -399,15 +399,23 @@ __device__ __forceinline__ float* rr_at(const lxm_params& p, int step, int L) {
 }
 // 16 bytes to global memory at agent scope (a buffer store with the sc1 policy: written through
 // to the coherence point, like the relaxed atomic stores)
+// a pointer the whole wave shares, in scalar registers (a buffer resource built from it is
+// uniform: no waterfall loop around the store)
+__device__ __forceinline__ float* wave_ptr(float* q) {
+  const uint64_t u = reinterpret_cast<uint64_t>(q);
+  const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)u);
+  const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(u >> 32));
+  return reinterpret_cast<float*>(((uint64_t)hi << 32) | lo);
+}
 __device__ __forceinline__ void st4_rlx(float* base, int idx, v4f v) {
-  const __amdgpu_buffer_rsrc_t r = __builtin_amdgcn_make_buffer_rsrc(base, 0, 0x7fffffff, 0x00020000);
+  const __amdgpu_buffer_rsrc_t r = __builtin_amdgcn_make_buffer_rsrc(wave_ptr(base), 0, 0x7fffffff, 0x00020000);
   typedef uint32_t v4u_ __attribute__((ext_vector_type(4)));
   __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(v4u_, v), r, idx * 4, 0, 16);
 }
 typedef uint32_t v2u __attribute__((ext_vector_type(2)));
 // 8 bytes to global memory at agent scope (idx in 32-bit words)
 __device__ __forceinline__ void st2_rlx(float* base, int idx, v2u v) {
-  const __amdgpu_buffer_rsrc_t r = __builtin_amdgcn_make_buffer_rsrc(base, 0, 0x7fffffff, 0x00020000);
+  const __amdgpu_buffer_rsrc_t r = __builtin_amdgcn_make_buffer_rsrc(wave_ptr(base), 0, 0x7fffffff, 0x00020000);
   __builtin_amdgcn_raw_buffer_store_b64(v, r, idx * 4, 0, 16);
 }
 // four bf16-exact floats as their bf16 bits, two per word (low half first)
@@ -674,13 +682,15 @@ __device__ __forceinline__ v4f norm4(const v4f& h, float r, const v4f& w) {
 template <bool BF, bool E4>
 __device__ __forceinline__ void stage_a(const ChainK& k, const typename Regions<E4>::RA& r1,
                                         const v4f& ha, const v4f& hb, float r, int L, int step,
-                                        bool ring) {
+                                        bool ring, bool fly) {
   const int t = threadIdx.x;
-  v4f wa, wb;
-  w1_of<E4>(r1, wa, wb);
-  v4f* xm4 = reinterpret_cast<v4f*>(smem + L_XM);
-  xm4[t] = norm4<BF>(ha, r, wa);
-  xm4[NT + t] = norm4<BF>(hb, r, wb);
+  if (!fly) {  // (a FLY layer's unit passes form these themselves)
+    v4f wa, wb;
+    w1_of<E4>(r1, wa, wb);
+    v4f* xm4 = reinterpret_cast<v4f*>(smem + L_XM);
+    xm4[t] = norm4<BF>(ha, r, wa);
+    xm4[NT + t] = norm4<BF>(hb, r, wb);
+  }
   v4f* d4 = reinterpret_cast<v4f*>(smem + L_DSUM);
   d4[t] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
   d4[NT + t] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
@@ -707,10 +717,13 @@ struct PV {
   typedef float T __attribute__((ext_vector_type(GM <= 4 ? 4 : 16)));
   T x, y;
 };
-template <bool E4, int G, bool SH, int GM, class RU>
+// FLY: the layer's passes all share columns and gather the residual h itself; pass_sum forms the
+// MLP norm's output D((h * r) * (1 + w)) of each column, w from the up slot's low half (the rows
+// of a FLY layer are never written to xm). Otherwise the passes gather xm.
+template <bool E4, int G, bool SH, int GM, bool FLY, class RU>
 __device__ __forceinline__ PV<GM> pass_gather(const RU& ru, int base) {
   constexpr int ESZ = PT<E4>::ESZ;
-  const float* xm = LF(L_XM);
+  const float* xm = FLY ? LF(L_H) : LF(L_XM);
   PV<GM> v;
 #pragma unroll
   for (int j = 0; j < G; j++) {
@@ -725,8 +738,8 @@ __device__ __forceinline__ PV<GM> pass_gather(const RU& ru, int base) {
   }
   return v;
 }
-template <bool BF, bool E4, int G, bool SH, int GM, class RU>
-__device__ __forceinline__ v2f pass_sum(const RU& ru, int base, const PV<GM>& v) {
+template <bool BF, bool E4, int G, bool SH, int GM, bool FLY, class RU>
+__device__ __forceinline__ v2f pass_sum(const RU& ru, int base, const PV<GM>& v, float r) {
   constexpr int ESZ = PT<E4>::ESZ;
   float g = 0.0f, u = 0.0f;
 #pragma unroll
@@ -734,48 +747,69 @@ __device__ __forceinline__ v2f pass_sum(const RU& ru, int base, const PV<GM>& v)
     int o;
     float wg, wu;
     ent_of<E4>(ru, base + 2 * ESZ * j, o, wg);
-    if constexpr (E4 && SH) wu = __uint_as_float(ru.slot(base + 2 * j + 1));
-    else ent_of<E4>(ru, base + 2 * ESZ * j + ESZ, o, wu);
-    g = acc<BF>(g, v.x[j], wg);
-    u = acc<BF>(u, SH ? v.x[j] : v.y[j], wu);
+    if constexpr (FLY) {
+      const uint32_t us = ru.slot(base + 2 * j + 1);
+      wu = __uint_as_float(us & 0xffff0000u);
+      const float x = rd<BF>((v.x[j] * r) * (1.0f + __uint_as_float(us << 16)));
+      g = acc<BF>(g, x, wg);
+      u = acc<BF>(u, x, wu);
+    } else {
+      if constexpr (E4 && SH) wu = __uint_as_float(ru.slot(base + 2 * j + 1));
+      else ent_of<E4>(ru, base + 2 * ESZ * j + ESZ, o, wu);
+      g = acc<BF>(g, v.x[j], wg);
+      u = acc<BF>(u, SH ? v.x[j] : v.y[j], wu);
+    }
   }
   return v2f{g, u};
 }
-template <bool E4, int N, int GM, class RU>
+template <bool E4, int N, int GM, bool FLY, class RU>
 __device__ __forceinline__ PV<GM> gather_g(const RU& ru, int base, int G, bool sh) {
   if constexpr (N >= 1) {
-    if (G == N) return sh ? pass_gather<E4, N, true, GM>(ru, base) : pass_gather<E4, N, false, GM>(ru, base);
-    return gather_g<E4, N - 1, GM>(ru, base, G, sh);
+    if (G == N) {
+      if constexpr (FLY) return pass_gather<E4, N, true, GM, true>(ru, base);
+      else return sh ? pass_gather<E4, N, true, GM, false>(ru, base) : pass_gather<E4, N, false, GM, false>(ru, base);
+    }
+    return gather_g<E4, N - 1, GM, FLY>(ru, base, G, sh);
   } else {
     PV<GM> v;
     return v;
   }
 }
-template <bool BF, bool E4, int N, int GM, class RU>
-__device__ __forceinline__ v2f sum_g(const RU& ru, int base, int G, bool sh, const PV<GM>& v) {
+template <bool BF, bool E4, int N, int GM, bool FLY, class RU>
+__device__ __forceinline__ v2f sum_g(const RU& ru, int base, int G, bool sh, const PV<GM>& v, float r) {
   if constexpr (N >= 1) {
-    if (G == N)
-      return sh ? pass_sum<BF, E4, N, true, GM>(ru, base, v) : pass_sum<BF, E4, N, false, GM>(ru, base, v);
-    return sum_g<BF, E4, N - 1, GM>(ru, base, G, sh, v);
+    if (G == N) {
+      if constexpr (FLY) return pass_sum<BF, E4, N, true, GM, true>(ru, base, v, r);
+      else return sh ? pass_sum<BF, E4, N, true, GM, false>(ru, base, v, r) : pass_sum<BF, E4, N, false, GM, false>(ru, base, v, r);
+    }
+    return sum_g<BF, E4, N - 1, GM, FLY>(ru, base, G, sh, v, r);
   } else {
     return v2f{0.0f, 0.0f};
   }
 }
 
-// Stage B's units: passes P0 and P1 of the thread, then its long unit (entries in LDS)
-template <bool BF, bool E4>
+// whether a layer's unit passes form the MLP norm's output themselves (its wave-uniform word)
+template <bool E4>
+__device__ __forceinline__ bool fly_of(const typename Regions<E4>::RA& r1) {
+  if constexpr (E4) return (__builtin_amdgcn_readfirstlane(r1.slot(PT<E4>::MA + 2)) & 2048u) != 0;
+  else return false;
+}
+
+// Stage B's units: passes P0 and P1 of the thread, then its long unit (entries in LDS). r: the
+// norm factor (FLY layers form each gathered column's norm output).
+template <bool BF, bool E4, bool FLY>
 __device__ __forceinline__ void units(const uint8_t* gt, const typename Regions<E4>::RA& r1,
-                                      const typename Regions<E4>::RU& ru) {
+                                      const typename Regions<E4>::RU& ru, float r) {
   using F = PT<E4>;
   const uint32_t m0 = r1.slot(F::MA + 0);
   const uint32_t m2 = __builtin_amdgcn_readfirstlane(r1.slot(F::MA + 2));
   const int G0 = (int)(m2 & 15u), G1 = (int)((m2 >> 4) & 15u);
   const bool sh0 = (m2 & 256u) != 0, sh1 = (m2 & 512u) != 0;
   float* act = LF(L_ACT);
-  const PV<F::G0MAX> v0 = gather_g<E4, F::G0MAX, F::G0MAX>(ru, F::U0, G0, sh0);
-  const PV<F::G1MAX> v1 = gather_g<E4, F::G1MAX, F::G1MAX>(ru, F::U1, G1, sh1);
-  const v2f s0 = sum_g<BF, E4, F::G0MAX, F::G0MAX>(ru, F::U0, G0, sh0, v0);
-  const v2f s1 = sum_g<BF, E4, F::G1MAX, F::G1MAX>(ru, F::U1, G1, sh1, v1);
+  const PV<F::G0MAX> v0 = gather_g<E4, F::G0MAX, F::G0MAX, FLY>(ru, F::U0, G0, sh0);
+  const PV<F::G1MAX> v1 = gather_g<E4, F::G1MAX, F::G1MAX, FLY>(ru, F::U1, G1, sh1);
+  const v2f s0 = sum_g<BF, E4, F::G0MAX, F::G0MAX, FLY>(ru, F::U0, G0, sh0, v0, r);
+  const v2f s1 = sum_g<BF, E4, F::G1MAX, F::G1MAX, FLY>(ru, F::U1, G1, sh1, v1, r);
   const float a0 = swiglu<BF>(s0.x, s0.y), a1 = swiglu<BF>(s1.x, s1.y);
   if (m0 & 0x8000u) act[m0 & 0xfffu] = a0;
   if (m0 & 0x80000000u) act[(m0 >> 16) & 0xfffu] = a1;
@@ -1039,6 +1073,17 @@ __device__ bool gdn_event(const lxm_params& p, int L, const uint8_t* gt, uint32_
   return true;
 }
 
+// The gate flags and decay factors a layer's stage B writes, cleared beforehand (in the previous
+// layer's stage C2, and before the first token): live key heads, each value head's exp(g), and
+// whether any gate opened / any query was live.
+__device__ __forceinline__ void clear_gate_flags(const ChainK& k) {
+  const int t = threadIdx.x;
+  int* flags = LI(L_FLAGS);
+  if (t < k.nk) flags[F_KH + t] = 0;
+  if (t < k.nv) LF(L_EV)[t] = 1.0f;
+  if (t < 2) flags[F_ANY + t] = 0;
+}
+
 // One layer. ss: the sum of squares of h on entry. Ends inside the sum of squares of its output
 // (sum512_begin into wave-total buffer par): the caller takes it. False on an error.
 template <bool BF, bool E4>
@@ -1059,20 +1104,22 @@ __device__ __forceinline__ bool layer(const lxm_params& p, const ChainK& k, int 
   // post_attention_layernorm :789 read the same h when the GDN leaves it alone)
   const GateLd gl = gate_load<BF, E4>(gt);
   const float r = norm_r(ss, H, hd.eps);
-  stage_a<BF, E4>(k, r1, ha, hb, r, L, step, true);
-  if (t < k.nk) flags[F_KH + t] = 0;
-  if (t < k.nv) ev[t] = 1.0f;
-  if (t < 2) flags[F_ANY + t] = 0;
-  sp_arrive(0);
-  lds_barrier();
-  sp_depart(0);
+  const bool fly = fly_of<E4>(r1);
+  stage_a<BF, E4>(k, r1, ha, hb, r, L, step, true, fly);
+  if (!fly) {  // (a FLY layer writes no norm output: nothing for stage B to wait for)
+    sp_arrive(0);
+    lds_barrier();
+    sp_depart(0);
+  }
   uint64_t c0 = 0;
   if (k.prof && t == 0) {
     c0 = cycles();
     pa[2] += c0 - pa[15];
   }
   // ---- stage B: the gates and, speculatively (the GDN leaves h alone on most steps), the MLP
-  units<BF, E4>(gt, r1, ru);
+  // (the gate flags were cleared in the previous layer's stage C2)
+  if (fly) units<BF, E4, true>(gt, r1, ru, r);
+  else units<BF, E4, false>(gt, r1, ru, r);
   gate_compute<BF, E4>(k, gt, gl, r);
   sp_arrive(1);
   lds_barrier();
@@ -1086,9 +1133,11 @@ __device__ __forceinline__ bool layer(const lxm_params& p, const ChainK& k, int 
     if (!gdn_event<BF, E4>(p, L, gt, seq, target, ha, hb)) return false;
     if (flags[F_OUT]) {  // h may have changed: the MLP again, on the new h
       ss = hidden_ss<BF>(ha, hb);
-      stage_a<BF, E4>(k, r1, ha, hb, norm_r(ss, H, hd.eps), L, step, false);
+      const float r2 = norm_r(ss, H, hd.eps);
+      stage_a<BF, E4>(k, r1, ha, hb, r2, L, step, false, fly);
       lds_barrier();
-      units<BF, E4>(gt, r1, ru);
+      if (fly) units<BF, E4, true>(gt, r1, ru, r2);
+      else units<BF, E4, false>(gt, r1, ru, r2);
       lds_barrier();
     }
     if (k.prof && t == 0) {
@@ -1126,6 +1175,7 @@ __device__ __forceinline__ bool layer(const lxm_params& p, const ChainK& k, int 
     v4f* h4 = reinterpret_cast<v4f*>(smem + L_H);
     h4[t] = ha;
     h4[NT + t] = hb;
+    clear_gate_flags(k);  // for the next layer's gates (this layer's flags are read by now)
     sum512_begin(sq_terms<BF>(ha, hb), LF(L_WSUM) + 8 * par, 3);
   }
   if (k.prof && t == 0) {
@@ -1194,6 +1244,7 @@ __device__ void run_chain(const lxm_params& pg) {
   }
   uint64_t* pa = reinterpret_cast<uint64_t*>(smem + L_PROF);
   if (t < 32) pa[t] = 0;
+  clear_gate_flags(k);
   __syncthreads();
   // the first layer's tables; then always one layer ahead
   typename RG::RA r1 = fetch_words<RG::RAA, RG::RAN>(lt[0].ptt);
