@@ -1,0 +1,74 @@
+/* linuxformer on MI355X: greedy decode of the dense padded text-view stack,
+ * C ABI.
+ *
+ * The dense counterpart of lxm_run for stacks whose projections are dense (lx/lx/merge.py:82-120
+ * pads the text layers' key heads from 128 to 256 dims and keeps 2 of every 8 value heads): one
+ * decode step of every layer and the head per call, each layer as a few HBM-bound row kernels
+ * (one wave per row: 64 lanes, each summing one 64th of the row's entries in order from +0, the
+ * 64 sums combined by a pairwise tree at offsets 32..1; the oracle's dense order) around the
+ * delta rule of the live value heads. The step counter, the fed-back token and the predictions
+ * stay on the device, so a caller may capture one call in a graph and replay it per token. The
+ * reference has no C entry point for this path (it decodes dense stacks with torch ops,
+ * lx/lx/fast.py:365-540): the roles mirror lxm_run's. All buffers belong to the caller.
+ *
+ * Layouts (bf16 = uint16 bits): a projection set's rows are contiguous, row r's entries (every
+ * live column, ascending) at r x K. Value heads of a key head kh: kh x 8 + r, live for
+ * r < rl (their state and windows change); the other heads and the zero-padded key dims must
+ * hold zero state and windows (they then stay zero, as the stock layer leaves them).
+ */
+#ifndef LXM_DENSE_H
+#define LXM_DENSE_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct lxm_dn_layer {
+  const uint16_t* proj;    /* rows: q (nk x kl), k (nk x kl), v (nk x rl x 128), z (nk x rl x 128),
+                              b (nk x rl), a (nk x rl); each of hidden entries */
+  const uint16_t* conv_qk; /* (2, nk, kl, 4): the live query/key channels' taps */
+  const uint16_t* conv_v;  /* (nk, rl, 128, 4) */
+  const float* A_log;      /* (nv) */
+  const float* dt_bias;    /* (nv) */
+  const float* gnorm;      /* (128): the gated norm's weight */
+  const float* ln_in;      /* (hidden): input_layernorm's raw weight w (the kernels form 1 + w) */
+  const float* ln_post;    /* (hidden) */
+  const uint16_t* out;     /* (hidden, nk x rl x 128): out_proj over the live value dims */
+  const uint16_t* gate;    /* (inter, hidden) */
+  const uint16_t* up;      /* (inter, hidden) */
+  const uint16_t* down;    /* (hidden, inter) */
+  float* rec;              /* (nv, 256, 128): the layer's recurrent state (in place) */
+  uint16_t* conv;          /* (n_conv, 4) bf16: the layer's conv windows (in place) */
+} lxm_dn_layer;
+
+typedef struct lxm_dn_params {
+  int32_t hidden, n_layers, nk, kl, nv, rl, inter, vocab, n_conv;
+  float rms_eps, geps;
+  int32_t n_forced, n_steps, pad;
+  const lxm_dn_layer* layers; /* device, n_layers */
+  const lxm_dn_layer* layers_host; /* the same in host memory (the launcher's weight pointers) */
+  const uint16_t* embed;      /* (vocab, hidden): the embedding, tied to the head */
+  const float* w_final;       /* (hidden): the final norm's raw weight */
+  const int32_t* forced;      /* (n_forced): step i's input is forced[i], else the last prediction */
+  int32_t* preds;             /* (n_steps) */
+  int32_t* step;              /* (1): the next step's index (advanced by each call) */
+  int32_t* tok;               /* (1): the last prediction */
+  float* h;                   /* (hidden): the residual */
+  float* xn;                  /* (hidden + inter): a norm's output, then the MLP's act at +hidden */
+  float* P;                   /* (rows of proj): the projections */
+  float* on;                  /* (nk x rl x 128): the live heads' gated-norm outputs */
+  unsigned long long* keys;   /* (1): the head's argmax key */
+  int32_t* err;               /* (1): 1 a forced token out of range */
+} lxm_dn_params;
+
+/* One greedy step (embedding, every layer, the head's first maximum, the token fed back) on
+   stream. p_host: the block in host memory (launch shapes); p_dev: the same bytes on the
+   device. Returns a hipError_t. */
+int lxm_dn_step(const lxm_dn_params* p_host, const lxm_dn_params* p_dev, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

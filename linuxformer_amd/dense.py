@@ -1,0 +1,150 @@
+"""Greedy decode of the dense padded text-view stack on the native dense
+kernels (csrc/lxm_dense.hip, C ABI include/lxm_dense.h).
+
+    dd = DenseDecode(model, cache)            # model: synth.DenseModel on the GPU
+    preds = dd.run(forced, n)                 # lx.mega's run semantics: step i's input is
+                                              # forced[i] (i < len(forced)), else pred[i - 1]
+
+Every step (embedding, 24 layers, the head's argmax, the token fed back) is one call of
+lxm_dn_step; the step counter and the fed-back token live on the device, so ``run`` can capture a
+step in a graph once and replay it per token. The cache holds the states in transformers'
+layout (conv (1, n_conv, 4) bf16, recurrent (1, nv, 256, 128) fp32) and is updated in place.
+"""
+
+from __future__ import annotations
+
+import ctypes
+
+import torch
+
+from . import mk_build
+
+P64 = ctypes.c_void_p
+
+
+class DnLayer(ctypes.Structure):
+    _fields_ = [(n, P64) for n in ("proj", "conv_qk", "conv_v", "A_log", "dt_bias", "gnorm",
+                                   "ln_in", "ln_post", "out", "gate", "up", "down", "rec",
+                                   "conv")]
+
+
+class DnParams(ctypes.Structure):
+    _fields_ = [(n, ctypes.c_int32) for n in ("hidden", "n_layers", "nk", "kl", "nv", "rl",
+                                              "inter", "vocab", "n_conv")] + \
+        [("rms_eps", ctypes.c_float), ("geps", ctypes.c_float)] + \
+        [(n, ctypes.c_int32) for n in ("n_forced", "n_steps", "pad")] + \
+        [(n, P64) for n in ("layers", "layers_host", "embed", "w_final", "forced", "preds", "step",
+                            "tok", "h", "xn", "P", "on", "keys", "err")]
+
+
+class DenseDecode:
+    """The packed weights of a DenseModel and the decode driver over a cache."""
+
+    def __init__(self, model, cache, max_steps: int = 1 << 16):
+        self.model, self.cache = model, cache
+        sp, d = model.spec, model.dims
+        self.spec, self.dims = sp, d
+        self.dev = model.embed.device
+        self.lib = mk_build.load()
+        H, nk, kl, rl, I = sp.hidden, sp.nk, sp.kd_live, sp.r_live, sp.inter
+        R = d.nv // d.nk
+        self.nproj = 2 * nk * kl + 2 * nk * rl * 128 + 2 * nk * rl
+        self._keep = []
+        self.layers_h = (DnLayer * d.n_layers)()
+        for L, ly in enumerate(model.layers):
+            proj = torch.cat([ly["qk"][0].reshape(-1, H), ly["qk"][1].reshape(-1, H),
+                              ly["v"].reshape(-1, H), ly["z"].reshape(-1, H),
+                              ly["b"].reshape(-1, H), ly["a"].reshape(-1, H)]).contiguous()
+            assert proj.shape[0] == self.nproj
+            tens = dict(proj=proj, conv_qk=ly["conv_qk"].contiguous(),
+                        conv_v=ly["conv_v"].contiguous(), A_log=ly["A_log"].contiguous(),
+                        dt_bias=ly["dt_bias"].contiguous(), gnorm=ly["norm"].contiguous(),
+                        ln_in=ly["ln_in"].contiguous(), ln_post=ly["ln_post"].contiguous(),
+                        out=ly["out"].reshape(H, -1).contiguous(), gate=ly["gate"].contiguous(),
+                        up=ly["up"].contiguous(), down=ly["down"].contiguous())
+            self._keep.append(tens)
+            cl = cache.layers[L]
+            rec, conv = cl.recurrent_states[0], cl.conv_states[0]
+            assert rec.dtype == torch.float32 and rec.is_contiguous() and rec.device == self.dev
+            assert conv.dtype == torch.bfloat16 and conv.is_contiguous() and conv.device == self.dev
+            # the zero value heads and the zero-padded key dims must hold zero state and windows
+            # (the kernels leave them alone; the stock layer keeps them zero)
+            rv = rec[0].view(nk, R, 256, 128)
+            cv = conv[0]
+            assert not rv[:, rl:].any() and not rv[:, :rl, kl:].any(), "dead heads' state != 0"
+            qk = cv[:2 * nk * 256].view(2, nk, 256, 4)
+            vv = cv[2 * nk * 256:].view(nk, R, 128, 4)
+            assert not qk[:, :, kl:].any() and not vv[:, rl:].any(), "dead channels' windows != 0"
+            lay = self.layers_h[L]
+            for k, t in tens.items():
+                setattr(lay, k, t.data_ptr())
+            lay.rec, lay.conv = rec.data_ptr(), conv.data_ptr()
+        self.layers_d = torch.frombuffer(bytearray(bytes(self.layers_h)), dtype=torch.uint8).to(self.dev)
+        dev = self.dev
+        self.h = torch.zeros(H, dtype=torch.float32, device=dev)
+        self.xn = torch.zeros(H + I, dtype=torch.float32, device=dev)
+        self.P = torch.zeros(self.nproj, dtype=torch.float32, device=dev)
+        self.on = torch.zeros(nk * rl * 128, dtype=torch.float32, device=dev)
+        self.keys = torch.zeros(1, dtype=torch.int64, device=dev)
+        self.step = torch.zeros(1, dtype=torch.int32, device=dev)
+        self.tok = torch.zeros(1, dtype=torch.int32, device=dev)
+        self.err = torch.zeros(1, dtype=torch.int32, device=dev)
+        self.preds = torch.zeros(max_steps, dtype=torch.int32, device=dev)
+        self.forced = torch.zeros(max_steps, dtype=torch.int32, device=dev)
+        self.max_steps = max_steps
+        self.graph = None
+
+    def _params(self, n_forced: int):
+        sp, d = self.spec, self.dims
+        p = DnParams(hidden=sp.hidden, n_layers=d.n_layers, nk=sp.nk, kl=sp.kd_live, nv=d.nv,
+                     rl=sp.r_live, inter=sp.inter, vocab=sp.vocab, n_conv=d.n_conv,
+                     rms_eps=sp.rms_eps, geps=sp.gated_eps, n_forced=n_forced,
+                     n_steps=self.max_steps, layers=self.layers_d.data_ptr(),
+                     layers_host=ctypes.cast(self.layers_h, P64).value,
+                     embed=self.model.embed.data_ptr(), w_final=self.model.norm.data_ptr(),
+                     forced=self.forced.data_ptr(), preds=self.preds.data_ptr(),
+                     step=self.step.data_ptr(), tok=self.tok.data_ptr(), h=self.h.data_ptr(),
+                     xn=self.xn.data_ptr(), P=self.P.data_ptr(), on=self.on.data_ptr(),
+                     keys=self.keys.data_ptr(), err=self.err.data_ptr())
+        pd = torch.frombuffer(bytearray(bytes(p)), dtype=torch.uint8).to(self.dev)
+        return p, pd
+
+    def _step(self) -> None:
+        st = ctypes.c_void_p(torch.cuda.current_stream(self.dev).cuda_stream)
+        e = self.lib.lxm_dn_step(ctypes.byref(self._p), ctypes.c_void_p(self._pd.data_ptr()), st)
+        if e:
+            raise RuntimeError(f"dense decode launch failed: hipError {e}")
+
+    @torch.no_grad()
+    def run(self, forced, n: int, graph: bool = True) -> list:
+        """n greedy steps from the cache's states (updated in place); step i's input is forced[i]
+        for i < len(forced), else step i - 1's prediction. Returns the n predictions. graph: the
+        first step runs eagerly, one step is captured (capturing runs nothing) and replayed for
+        the others; the step reads its index and input from device memory."""
+        f = torch.as_tensor(forced, dtype=torch.int64)
+        if len(f) == 0 or n < 1 or n > self.max_steps or len(f) > self.max_steps:
+            raise ValueError("forced tokens and steps: 1 .. max_steps")
+        if int(f.min()) < 0 or int(f.max()) >= self.spec.vocab:
+            raise ValueError("forced token out of range")
+        self.forced[:len(f)].copy_(f.to(torch.int32))
+        self.step.zero_()
+        self.err.zero_()
+        if getattr(self, "_nf", None) != len(f):
+            self._p, self._pd = self._params(len(f))
+            self._nf, self.graph = len(f), None
+        self._step()
+        if graph and n > 1:
+            if self.graph is None:
+                g = torch.cuda.CUDAGraph()
+                with torch.cuda.graph(g):
+                    self._step()
+                self.graph = g
+            for _ in range(n - 1):
+                self.graph.replay()
+        else:
+            for _ in range(n - 1):
+                self._step()
+        torch.cuda.synchronize(self.dev)
+        if int(self.err.item()):
+            raise RuntimeError("dense decode: a forced token out of range")
+        return self.preds[:n].cpu().tolist()

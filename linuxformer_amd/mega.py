@@ -21,7 +21,7 @@ import ctypes
 import numpy as np
 import torch
 
-from . import chain, mk_build
+from . import synth, chain, mk_build
 
 NT, MAXH, KD, VD, RMAX = 512, 4096, 256, 128, 8
 MAXU, MAXQK, MAXQKL, MAXDEC, GATE_MAX, NSYNC, OUT_MAX = 2048, 1024, 512, 512, 65536, 1024, 1024
@@ -179,6 +179,8 @@ class Mega:
         self.subprof = subprof
         self.fast, self.model, self.cache, self.offset = fast, model, cache, offset
         sm = fast.sm
+        if synth.has_dense_order(sm):
+            raise ValueError("a dense-order stack (config 4) runs on linuxformer_amd.dense")
         d = sm.dims
         self.dims = d
         dev = torch.device(device) if device is not None else torch.device("cuda")

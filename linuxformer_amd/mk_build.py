@@ -15,9 +15,10 @@ LIB = os.path.join(LIBDIR, "liblxm.so")
 # the same kernel with the per-wave sub-phase counters (-DLXM_SUBPROF; lx.mega's MK_SUBPROF build)
 LIB_SUBPROF = os.path.join(LIBDIR, "liblxm_subprof.so")
 RUNNER = os.path.join(LIBDIR, "lxm_runner")
-SOURCES = ["lxm_decode.hip", "lxm_prefill.hip"]
+SOURCES = ["lxm_decode.hip", "lxm_prefill.hip", "lxm_dense.hip"]
 HEADERS = ["lxm_math.h", os.path.join("..", "..", "include", "lxm.h"),
-           os.path.join("..", "..", "include", "lxm_prefill.h")]
+           os.path.join("..", "..", "include", "lxm_prefill.h"),
+           os.path.join("..", "..", "include", "lxm_dense.h")]
 # -ffp-contract=off: no a*b+c is fused (the rounding contract); packed fp32 ops disabled
 FLAGS = ["--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC", "-shared", "-ffp-contract=off",
          "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops"]
@@ -95,10 +96,12 @@ def load(subprof: bool = False) -> ctypes.CDLL:
         lib.lxm_pf_tiles.restype = I
         lib.lxm_pf_lds.argtypes = [I, I]
         lib.lxm_pf_lds.restype = I
+        lib.lxm_dn_step.argtypes = [P, P, P]
+        lib.lxm_dn_step.restype = I
         _libs[path] = lib
     return _libs[path]
 
 
 EXPORTS = ("lxm_run", "lxm_lds_base", "lxm_helper_lds", "lxm_max_blocks", "lxm_max_lds",
            "lxm_last_error", "lxm_device_cus", "lxm_t_elem", "lxm_t_sum", "lxm_pf_layers",
-           "lxm_pf_head", "lxm_pf_embed", "lxm_pf_tiles", "lxm_pf_lds")
+           "lxm_pf_head", "lxm_pf_embed", "lxm_pf_tiles", "lxm_pf_lds", "lxm_dn_step")

@@ -15,7 +15,7 @@ import ctypes
 import numpy as np
 import torch
 
-from . import mk_build
+from . import mk_build, synth
 
 TT, KD, VD, NT = 4, 256, 128, 512
 MAXKS, MAXVS, UPT, SLICES = 16, 128, 4, 8
@@ -268,6 +268,8 @@ class Prefill:
     def __init__(self, fast, device="cuda", offset: int = 0):
         self.fast = fast
         sm = fast.sm
+        if synth.has_dense_order(sm):
+            raise ValueError("a dense-order stack (config 4) runs on linuxformer_amd.dense")
         d = self.dims = sm.dims
         self.dev = torch.device(device)
         self.bf = d.dtype == "bf16"

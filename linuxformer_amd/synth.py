@@ -43,6 +43,7 @@ class Coo:
     rows: np.ndarray
     cols: np.ndarray
     vals: np.ndarray
+    blocks: int = 0  # 64: a dense matrix, rows summed in the dense order (every live column kept)
 
     @staticmethod
     def build(shape, rows, cols, vals) -> "Coo":
@@ -461,3 +462,192 @@ def from_hf(m, n_chip: int | None = None) -> SparseModel:
             gate_proj=coo(lay.mlp.gate_proj.weight), up_proj=coo(lay.mlp.up_proj.weight),
             down_proj=coo(lay.mlp.down_proj.weight)))
     return SparseModel(d, layers, coo(m.lm_head.weight), f(m.model.norm.weight))
+
+
+# ---------------------------------------------------------------------------------------------
+# the dense padded text-view stack (lx/lx/merge.py:82-120's layout): key heads
+# of dim 256 whose upper 128 dims are zero, 8 value heads per key head of which 2 are live and 6
+# zero, bf16 N(0, 0.02) weights on the live blocks. Its projections are dense, so they are summed
+# in the dense order (64 groups of a row's entries, then a pairwise tree; the oracle's `blocks`).
+
+
+@dataclass
+class DenseSpec:
+    name: str
+    hidden: int
+    n_layers: int
+    nk: int = 16
+    kd_live: int = 128      # live dims of each 256-dim key head (the rest zero-padded)
+    nv: int = 128
+    r_live: int = 2         # live value heads of each key head (the first r_live of its 8)
+    inter: int = 9216
+    vocab: int = 248_320
+    seed: int = 4
+    std: float = 0.02
+    rms_eps: float = 1e-6
+    gated_eps: float = 5e-7
+    n_prefill: int = 8192
+    n_steps: int = 4096
+
+    def dims(self) -> Dims:
+        return Dims(hidden=self.hidden, n_layers=self.n_layers, nk=self.nk, kd=256, nv=self.nv,
+                    vd=128, conv=4, inter=self.inter, vocab=self.vocab, dtype="bf16",
+                    rms_eps=self.rms_eps, gated_eps=self.gated_eps)
+
+
+def config4(seed: int = 4) -> DenseSpec:
+    """24 layers, hidden 2560, 16 key heads (256, zero-padded from 128), 128
+    value heads (2 live + 6 zero per key head), SwiGLU 9216, gated-norm eps 5e-7, vocabulary
+    248,320; an 8,192-token prefill of seeded uniform ids, then 4,096 greedy steps."""
+    return DenseSpec("c4", hidden=2560, n_layers=24, seed=seed)
+
+
+def config4_small(seed: int = 5) -> DenseSpec:
+    """Config 4's structure at a size the oracle runs in seconds (the parity tests)."""
+    return DenseSpec("c4s", hidden=256, n_layers=2, nk=2, nv=16, inter=512, vocab=1024,
+                     seed=seed, n_prefill=24, n_steps=16)
+
+
+@dataclass
+class DenseModel:
+    """Config 4's tensors on a device: bf16 weights of the live blocks only (the zero-padded
+    rows and columns are implicit), float32 small parameters (values exact in bf16)."""
+    spec: DenseSpec
+    dims: Dims
+    layers: list          # dicts of tensors, see build_dense
+    embed: object         # (vocab, hidden) bf16, tied to the head
+    norm: object          # (hidden,) float32 final norm weight
+
+
+def build_dense(spec: DenseSpec, device="cpu") -> DenseModel:
+    """The seeded dense stack on device (torch generators seeded per (layer, tensor))."""
+    import torch
+
+    d = spec.dims()
+    H, nk, kl, rl, I = spec.hidden, spec.nk, spec.kd_live, spec.r_live, spec.inter
+    dev = torch.device(device)
+
+    def gen(L, c):
+        return torch.Generator(device=dev).manual_seed(spec.seed * 1_000_003 + L * 101 + c)
+
+    def w(L, c, *shape, std=None):
+        x = torch.randn(*shape, generator=gen(L, c), device=dev, dtype=torch.float32)
+        return (x * (spec.std if std is None else std)).to(torch.bfloat16)
+
+    def small(x):
+        return x.to(torch.bfloat16).to(torch.float32)
+
+    layers = []
+    for L in range(spec.n_layers):
+        g = gen(L, 50)
+        A = torch.rand(d.nv, generator=g, device=dev) * 15.0 + 1.0
+        dt = torch.exp(torch.rand(d.nv, generator=g, device=dev) * (np.log(0.1) - np.log(0.001))
+                       + np.log(0.001))
+        layers.append({
+            "qk": w(L, 0, 2, nk, kl, H),              # query / key rows of the live dims
+            "v": w(L, 1, nk, rl, 128, H),             # value rows of the live value heads
+            "z": w(L, 2, nk, rl, 128, H),
+            "b": w(L, 3, nk, rl, H),
+            "a": w(L, 4, nk, rl, H),
+            "conv_qk": w(L, 5, 2, nk, kl, 4),
+            "conv_v": w(L, 6, nk, rl, 128, 4),
+            "A_log": small(torch.log(A)),
+            "dt_bias": small(torch.log(torch.expm1(dt))),
+            "norm": small(1.0 + w(L, 7, 128).float()),
+            "ln_in": small(w(L, 8, H).float()),
+            "ln_post": small(w(L, 9, H).float()),
+            "out": w(L, 10, H, nk, rl, 128),          # out_proj over the live value dims
+            "gate": w(L, 11, I, H),
+            "up": w(L, 12, I, H),
+            "down": w(L, 13, H, I),
+        })
+    embed = w(999, 14, spec.vocab, H)
+    norm = small(w(999, 15, H).float())
+    return DenseModel(spec, d, layers, embed, norm)
+
+
+def dense_to(dm: DenseModel, device) -> DenseModel:
+    """The same model with every tensor on device."""
+    return DenseModel(dm.spec, dm.dims, [{k: v.to(device) for k, v in ly.items()} for ly in dm.layers],
+                      dm.embed.to(device), dm.norm.to(device))
+
+
+def dense_state(dm: DenseModel, seed: int | None = None):
+    """Initial (conv, rec) for a dense stack as float32 numpy arrays in the padded layout: zero,
+    or (seed) N(0, 1) recurrent rows and N(0, 0.02) windows (bf16-exact) on the live heads'
+    dims only (the dead heads and padded dims stay zero, as the stock layer keeps them)."""
+    sp, d = dm.spec, dm.dims
+    R = d.nv // d.nk
+    conv = np.zeros((d.n_layers, d.n_conv, 4), np.float32)
+    rec = np.zeros((d.n_layers, d.nv, 256, 128), np.float32)
+    if seed is None:
+        return conv, rec
+    rng = np.random.default_rng(seed)
+    for kh in range(sp.nk):
+        for r in range(sp.r_live):
+            vh = kh * R + r
+            rec[:, vh, :sp.kd_live] = rng.standard_normal((d.n_layers, sp.kd_live, 128))
+            ch = 2 * sp.nk * 256 + vh * 128
+            conv[:, ch:ch + 128] = _round(0.02 * rng.standard_normal((d.n_layers, 128, 4)), "bf16")
+        for part in (0, 1):
+            ch = part * sp.nk * 256 + kh * 256
+            conv[:, ch:ch + sp.kd_live] = _round(0.02 * rng.standard_normal((d.n_layers, sp.kd_live, 4)), "bf16")
+    return conv, rec
+
+
+def to_sparse(dm: DenseModel) -> SparseModel:
+    """The dense stack as the padded checkpoint tensors in coordinate form, dense matrices marked
+    (blocks = 64, every live column kept): the oracle's input. Small stacks only."""
+    sp, d = dm.spec, dm.dims
+    H, nk, kl, rl, R = sp.hidden, sp.nk, sp.kd_live, sp.r_live, d.nv // d.nk
+    C = d.n_conv
+
+    def np32(t):
+        return t.float().cpu().numpy()
+
+    def coo_rows(shape, rows, mat, cols):
+        rows = np.asarray(rows, np.int64)
+        cols = np.asarray(cols, np.int64)
+        rr = np.repeat(rows, len(cols))
+        cc = np.tile(cols, len(rows))
+        order = np.lexsort((cc, rr))
+        return Coo(tuple(shape), rr[order], cc[order], np.asarray(mat, np.float32).reshape(-1)[order],
+                   blocks=64)
+
+    layers = []
+    allH = np.arange(H)
+    vh_live = np.array([kh * R + r for kh in range(nk) for r in range(rl)], np.int64)
+    for ly in dm.layers:
+        qk = np32(ly["qk"])          # (2, nk, kl, H)
+        qrows = np.array([kh * 256 + i for kh in range(nk) for i in range(kl)], np.int64)
+        krows = nk * 256 + qrows
+        vrows = 2 * nk * 256 + (vh_live[:, None] * 128 + np.arange(128)[None]).reshape(-1)
+        qkv = coo_rows((C, H), np.concatenate([qrows, krows, vrows]),
+                       np.concatenate([qk[0].reshape(-1, H), qk[1].reshape(-1, H),
+                                       np32(ly["v"]).reshape(-1, H)]), allH)
+        conv = np.zeros((C, 4), np.float32)
+        conv[qrows] = np32(ly["conv_qk"])[0].reshape(-1, 4)
+        conv[krows] = np32(ly["conv_qk"])[1].reshape(-1, 4)
+        conv[vrows] = np32(ly["conv_v"]).reshape(-1, 4)
+        zrows = (vh_live[:, None] * 128 + np.arange(128)[None]).reshape(-1)
+        z = coo_rows((d.nv * 128, H), zrows, np32(ly["z"]).reshape(-1, H), allH)
+        b = coo_rows((d.nv, H), vh_live, np32(ly["b"]).reshape(-1, H), allH)
+        a = coo_rows((d.nv, H), vh_live, np32(ly["a"]).reshape(-1, H), allH)
+        out = coo_rows((H, d.nv * 128), allH, np32(ly["out"]).reshape(H, -1), zrows)
+        layers.append(Layer(
+            in_proj_qkv=qkv, in_proj_z=z, in_proj_b=b, in_proj_a=a, out_proj=out, conv1d=conv,
+            A_log=np32(ly["A_log"]), dt_bias=np32(ly["dt_bias"]), norm=np32(ly["norm"]),
+            input_layernorm=np32(ly["ln_in"]), post_attention_layernorm=np32(ly["ln_post"]),
+            gate_proj=coo_rows((d.inter, H), np.arange(d.inter), np32(ly["gate"]), allH),
+            up_proj=coo_rows((d.inter, H), np.arange(d.inter), np32(ly["up"]), allH),
+            down_proj=coo_rows((H, d.inter), allH, np32(ly["down"]), np.arange(d.inter))))
+    embed = coo_rows((d.vocab, H), np.arange(d.vocab), np32(dm.embed), allH)
+    return SparseModel(d, layers, embed, np32(dm.norm), meta={"dense_spec": sp})
+
+
+def has_dense_order(model) -> bool:
+    """Whether any matrix of a SparseModel is marked dense (only the dense path sums those)."""
+    cs = [model.embed] + [getattr(ly, n) for ly in model.layers for n in (
+        "in_proj_qkv", "in_proj_z", "in_proj_b", "in_proj_a", "out_proj", "gate_proj", "up_proj",
+        "down_proj")]
+    return any(getattr(c, "blocks", 0) for c in cs)

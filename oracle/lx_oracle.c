@@ -33,10 +33,17 @@
  *     of 16, each block summed in order from +0, the block sums added in order from +0 (this
  *     order does not depend on the CPU's vector width, and torch's sum matches it bit for bit);
  *   - sums over a hidden vector (RMSNorm's sum of squares) use 512 lanes: lane l adds
- *     x[l], x[l + 512], ... in order from +0; the lanes of each group of 64 are combined by a
+ *     x[4l..4l+3], then x[2048+4l..2048+4l+3], in order from +0; the lanes of each group of 64
+ *     are combined by a
  *     pairwise tree at offsets 32, 16, 8, 4, 2, 1 (lane i takes i + off); the 8 group totals by
  *     a tree at offsets 4, 2, 1. Sums over a head (128 or 256 values) use one group of 64 lanes.
  *     Means divide the sum by the count (ATen's CPU mean is sum().div_(n)).
+ *   - a matrix marked dense (blocks = 64; the dense padded text-view stack, whose projections a
+ *     GPU sums across a wave) sums each row's stored entries (every live column, zeros included;
+ *     a multiple of 64) in 64 equal consecutive groups, each in order from +0, and combines the
+ *     64 group sums by the pairwise tree at offsets 32, 16, 8, 4, 2, 1. The stock forward's dense
+ *     GEMV order (oneDNN, cuBLAS) is a library choice with no canonical form; this one is fixed
+ *     here and shared with the dense kernels.
  */
 #include <math.h>
 #include <stdint.h>
@@ -203,6 +210,8 @@ typedef struct { /* CSR: row r's entries ptr[r] .. ptr[r + 1] - 1, columns ascen
   const int64_t* ptr;
   const int32_t* col;
   const float* val;
+  int blocks;      /* 0: each row summed in order; 64: the dense order (entries per row % 64 == 0) */
+  int pad;
 } ox_csr;
 
 typedef struct {
@@ -261,17 +270,36 @@ static void ws_free(ox_ws* w) {
   for (size_t i = 0; i < sizeof(ps) / sizeof(ps[0]); i++) free(ps[i]);
 }
 
-/* out[r] = D(sum over row r's entries of x[col] * w), ascending columns, from +0 */
-static void csr_mv(const ox_csr* m, const float* x, float* out) {
-  for (int r = 0; r < m->nrows; r++) {
+/* sum over row r's entries of x[col] * w (unrounded): ascending columns from +0, or for a dense
+   matrix per group of n / 64 consecutive entries, then the group sums' pairwise tree (lane i
+   takes i + off) */
+static float row_dot(const ox_csr* m, int r, const float* x) {
+  if (!m->blocks) {
     float s = 0.0f;
     for (int64_t e = m->ptr[r]; e < m->ptr[r + 1]; e++) {
       float xv = x[m->col[e]];
       if (xv == 0.0f) continue;
       s = s + xv * m->val[e];
     }
-    out[r] = D(s);
+    return s;
   }
+  float p[64] = {0};
+  const int64_t e0 = m->ptr[r], n = m->ptr[r + 1] - e0, g = n / 64;
+  if (n % 64) abort(); /* the packer keeps every live column of a dense row */
+  for (int64_t e = e0; e < e0 + n; e++) {
+    float xv = x[m->col[e]];
+    if (xv == 0.0f) continue;
+    const int b = (int)((e - e0) / g);
+    p[b] = p[b] + xv * m->val[e];
+  }
+  for (int off = 32; off >= 1; off >>= 1)
+    for (int i = 0; i < off; i++) p[i] = p[i] + p[i + off];
+  return p[0];
+}
+
+/* out[r] = D(row r . x) */
+static void csr_mv(const ox_csr* m, const float* x, float* out) {
+  for (int r = 0; r < m->nrows; r++) out[r] = D(row_dot(m, r, x));
 }
 
 /* Qwen3_5RMSNorm(h) (TF:720-737): r = rsqrt(mean(h^2) + eps); xn = D((h * r) * (1 + w)) */
@@ -403,17 +431,8 @@ static void layer_step(const ox_model* m, int L, float* h, float* cs, float* S, 
     float ss = ox_sum_64(w->sq, vd);
     float rr = ox_rsqrt(ss / (float)vd + d->gated_eps);
     float zrow[256];
-    for (int j = 0; j < vd; j++) { /* in_proj_z rows of this head */
-      const ox_csr* zm = &ly->z;
-      int row = vh * vd + j;
-      float s = 0.0f;
-      for (int64_t e2 = zm->ptr[row]; e2 < zm->ptr[row + 1]; e2++) {
-        float xv = w->xn[zm->col[e2]];
-        if (xv == 0.0f) continue;
-        s = s + xv * zm->val[e2];
-      }
-      zrow[j] = D(s);
-    }
+    for (int j = 0; j < vd; j++) /* in_proj_z rows of this head */
+      zrow[j] = D(row_dot(&ly->z, vh * vd + j, w->xn));
     for (int j = 0; j < vd; j++) {
       float t1 = D(o[j] * rr);
       float t2 = D(ly->gnorm[j] * t1);

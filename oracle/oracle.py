@@ -30,7 +30,8 @@ class Dims(ctypes.Structure):
 
 
 class Csr(ctypes.Structure):
-    _fields_ = [("nrows", I32), ("ncols", I32), ("ptr", PTR), ("col", PTR), ("val", PTR)]
+    _fields_ = [("nrows", I32), ("ncols", I32), ("ptr", PTR), ("col", PTR), ("val", PTR),
+                ("blocks", I32), ("pad", I32)]
 
 
 class Layer(ctypes.Structure):
@@ -138,12 +139,16 @@ class OracleModel:
 
     def _csr(self, coo) -> Csr:
         rows = np.asarray(coo.rows, np.int64)
-        order = np.lexsort((coo.cols, rows))
+        order = np.lexsort((coo.cols, rows))  # (dense matrices keep their explicit zeros)
         rows, cols, vals = rows[order], np.asarray(coo.cols)[order], np.asarray(coo.vals)[order]
         ptr = np.zeros(coo.shape[0] + 1, np.int64)
         np.cumsum(np.bincount(rows, minlength=coo.shape[0]), out=ptr[1:])
+        blocks = int(getattr(coo, "blocks", 0))
+        assert blocks in (0, 64)
+        if blocks:  # every stored row: a multiple of 64 entries (the oracle aborts otherwise)
+            assert (np.diff(ptr) % 64 == 0).all(), "a dense row needs a multiple of 64 entries"
         return Csr(nrows=coo.shape[0], ncols=coo.shape[1], ptr=self._arr(ptr, np.int64),
-                   col=self._arr(cols, np.int32), val=self._arr(vals))
+                   col=self._arr(cols, np.int32), val=self._arr(vals), blocks=blocks)
 
     def decode(self, conv: np.ndarray, rec: np.ndarray, forced, n: int, trace: bool = False):
         """n greedy steps from forced tokens, conv/rec (float32 numpy, updated in place).

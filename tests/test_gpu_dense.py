@@ -1,0 +1,84 @@
+"""Parity of the HIP dense decode (BASELINE config 4's structure) with the oracle on an MI355X,
+through the C ABI: predictions and final states bit for bit. The dense projections are summed in
+the dense order the oracle restates for matrices marked dense (64 groups of a row's entries in
+order from +0, then the pairwise tree); everything else follows the stock decode as in the
+sparse paths. Sizes: config 4's layout scaled down (hidden 256, 2 layers) so the oracle runs in
+seconds; the full config is measured by bench.py (--legs dense).
+"""
+
+import numpy as np
+import pytest
+import torch
+
+from linuxformer_amd import dense, fast, mk_build, synth
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def cuda():
+    assert torch.cuda.is_available(), "the gpu tests need an MI355X"
+    mk_build.load()
+    return torch.device("cuda", 0)
+
+
+_M = {}
+
+
+def model():
+    if "m" not in _M:
+        spec = synth.config4_small()
+        dm_cpu = synth.build_dense(spec, "cpu")
+        _M["m"] = (spec, dm_cpu, synth.to_sparse(dm_cpu))
+    return _M["m"]
+
+
+def bits(a):
+    return np.ascontiguousarray(a, np.float32).view(np.uint32)
+
+
+def check(n_forced, n, seed=None, graph=True):
+    from oracle import oracle as ox
+
+    spec, dm_cpu, sm = model()
+    conv0, rec0 = synth.dense_state(dm_cpu, seed)
+    forced = [int(x) for x in np.random.default_rng(7 + n_forced).integers(0, spec.vocab, n_forced)]
+    print(f"[gpu-test] dense c4s: forced={n_forced} n={n} seed={seed} graph={graph}", flush=True)
+    dm = synth.dense_to(dm_cpu, "cuda")
+    cache = fast.StateCache(conv0, rec0, "bf16", "cuda")
+    dd = dense.DenseDecode(dm, cache)
+    preds = dd.run(forced, n, graph=graph)
+    c, r = conv0.copy(), rec0.copy()
+    po, _, _ = ox.OracleModel(sm).decode(c, r, forced, n)
+    assert preds == po.tolist()
+    assert (bits(cache.conv_numpy()) == bits(c)).all()
+    assert (bits(cache.rec_numpy()) == bits(r)).all()
+    return preds
+
+
+def test_dense_small_greedy(cuda):
+    check(1, 24)
+
+
+def test_dense_small_forced_then_greedy(cuda):
+    """A forced prefix (the config's prefill, scaled down), then greedy steps."""
+    check(16, 32)
+
+
+def test_dense_small_live_state_eager(cuda):
+    """From N(0, 1) states and nonzero windows on the live heads, eager steps (no graph)."""
+    check(4, 12, seed=3, graph=False)
+
+
+def test_dense_small_live_state_graph(cuda):
+    check(4, 12, seed=3, graph=True)
+
+
+def test_dense_rejects_dead_state(cuda):
+    """A nonzero state on a dead value head would not stay zero as the kernels assume."""
+    spec, dm_cpu, sm = model()
+    conv0, rec0 = synth.dense_state(dm_cpu)
+    rec0[0, 2, 0, 0] = 1.0  # value head 2 of key head 0: dead (r_live = 2)
+    cache = fast.StateCache(conv0, rec0, "bf16", "cuda")
+    with pytest.raises(AssertionError):
+        dense.DenseDecode(synth.dense_to(dm_cpu, "cuda"), cache)

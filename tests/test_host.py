@@ -258,9 +258,8 @@ def test_packer_fits_every_config(packed):
 
 
 def test_c_abi_exports_every_declared_symbol(native_lib):
-    """The library loads and exports each entry point include/lxm.h and include/lxm_prefill.h
-    declare (no GPU call)."""
-    hdr = "".join(open(os.path.join(ROOT, "include", h)).read() for h in ("lxm.h", "lxm_prefill.h"))
+    """The library loads and exports each entry point include/*.h declares (no GPU call)."""
+    hdr = "".join(open(os.path.join(ROOT, "include", h)).read() for h in ("lxm.h", "lxm_prefill.h", "lxm_dense.h"))
     names = re.findall(r"^int (lxm_\w+)\(", hdr, re.M)
     assert len(names) >= 8
     lib = ctypes.CDLL(mk_build.LIB)
