@@ -11,8 +11,10 @@
  * reference has no C entry point for this path (it decodes dense stacks with torch ops,
  * lx/lx/fast.py:365-540): the roles mirror lxm_run's. All buffers belong to the caller.
  *
- * Layouts (bf16 = uint16 bits): a projection set's rows are contiguous, row r's entries (every
- * live column, ascending) at r x K. Value heads of a key head kh: kh x 8 + r, live for
+ * Layouts (bf16 = uint16 bits): a projection set's rows are contiguous, row r's K entries (every
+ * live column, ascending) at r x K, interleaved for the wave that reads them: with G = K / 64
+ * entries per lane and G >= 8, entries 8q..8q+7 of lane l's G at (q x 64 + l) x 8 within the row
+ * (G = 4: plain order). The embedding rows (the head's) likewise. Value heads of a key head kh: kh x 8 + r, live for
  * r < rl (their state and windows change); the other heads and the zero-padded key dims must
  * hold zero state and windows (they then stay zero, as the stock layer leaves them).
  */

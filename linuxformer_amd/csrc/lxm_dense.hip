@@ -63,7 +63,13 @@ __global__ __launch_bounds__(NT) void dn_embed(const lxm_dn_params* __restrict__
     tok = 0;
   }
   const uint16_t* e = p.embed + (int64_t)tok * p.hidden;
-  for (int c = threadIdx.x; c < p.hidden; c += NT) p.h[c] = bf16f(e[c]);
+  const int G = p.hidden / 64;
+  for (int c = threadIdx.x; c < p.hidden; c += NT) {
+    // entry c is lane c / G's entry c % G (interleaved in 8-entry chunks when G >= 8)
+    const int l = c / G, k = c % G;
+    const int at = G < 8 ? c : ((k >> 3) * 64 + l) * 8 + (k & 7);
+    p.h[c] = bf16f(e[at]);
+  }
   if (threadIdx.x == 0) *p.keys = 0ull;
 }
 
@@ -84,22 +90,30 @@ __global__ __launch_bounds__(NT) void dn_norm(const lxm_dn_params* __restrict__ 
 // bf16 pairs for every row the wave takes.
 template <int G>
 struct XChunk {
+  static_assert(G % 4 == 0, "16-byte input loads");
   uint32_t v[G / 2];
+  // x[lane G .. lane G + G), bf16-exact values
   __device__ __forceinline__ void load(const float* x, int lane) {
+    const v4f* src = reinterpret_cast<const v4f*>(x + lane * G);
+    v4f a[G / 4];
 #pragma unroll
-    for (int k = 0; k < G / 2; k++) {
-      const float a = x[lane * G + 2 * k], b = x[lane * G + 2 * k + 1];
-      v[k] = (fbits(a) >> 16) | (fbits(b) & 0xffff0000u);
+    for (int k = 0; k < G / 4; k++) a[k] = src[k];
+#pragma unroll
+    for (int k = 0; k < G / 4; k++) {
+      v[2 * k] = (fbits(a[k].x) >> 16) | (fbits(a[k].y) & 0xffff0000u);
+      v[2 * k + 1] = (fbits(a[k].z) >> 16) | (fbits(a[k].w) & 0xffff0000u);
     }
   }
 };
-// the lane's sum of its G entries of row w (bf16), in order from +0
+// The lane's sum of its G entries of row w (bf16), in order from +0. A row is stored in 16-byte
+// chunks lane-interleaved: chunk q (entries 8q..8q+7) of lane l at (q * 64 + l) * 16 bytes, so each
+// of the wave's loads reads 1 KB in one piece (G = 4: lane l's 8 bytes at l * 8).
 template <int G>
 __device__ __forceinline__ float lane_dot(const uint16_t* w, int lane, const XChunk<G>& x) {
   static_assert(G % 8 == 0 || G == 4, "16-byte weight loads (or 8)");
-  const uint16_t* src = w + (int64_t)lane * G;
   float s = 0.0f;
   if constexpr (G == 4) {
+    const uint16_t* src = w + (int64_t)lane * G;
     const uint2 u = *reinterpret_cast<const uint2*>(src);
     const uint32_t wv[2] = {u.x, u.y};
 #pragma unroll
@@ -110,7 +124,7 @@ __device__ __forceinline__ float lane_dot(const uint16_t* w, int lane, const XCh
   } else {
     v4u wv[G / 8];
 #pragma unroll
-    for (int q = 0; q < G / 8; q++) wv[q] = reinterpret_cast<const v4u*>(src)[q];
+    for (int q = 0; q < G / 8; q++) wv[q] = reinterpret_cast<const v4u*>(w)[q * 64 + lane];
 #pragma unroll
     for (int q = 0; q < G / 8; q++)
 #pragma unroll
@@ -233,6 +247,12 @@ __global__ __launch_bounds__(NT) void dn_gdn(const lxm_dn_params* __restrict__ p
   const int R = p.nv / nk, vh = kh * R + rr;
   const int nq = nk * kl, nvr = nk * rl * VD;
   const float* P = p.P;
+  // the state tile first (its loads overlap the inputs' work below)
+  const int cg = t & 31, rb = t >> 5;
+  v4f* S4 = reinterpret_cast<v4f*>(ly.rec + (size_t)vh * KD * VD);
+  v4f s[16];
+#pragma unroll
+  for (int i = 0; i < 16; i++) s[i] = S4[(rb * 16 + i) * (VD / 4) + cg];
   // rows of P: q [0, nq), k [nq, 2nq), v [2nq, 2nq + nvr), z [.., + nvr), b [.., + nk rl), a
   if (t < KD) {
     float q = 0.0f, k = 0.0f;
@@ -282,11 +302,6 @@ __global__ __launch_bounds__(NT) void dn_gdn(const lxm_dn_params* __restrict__ p
   __syncthreads();
   const float beta = misc[0], e = misc[1];
   const bool live = misc[2] != 0.0f || misc[3] != 0.0f;
-  const int cg = t & 31, rb = t >> 5;
-  v4f* S4 = reinterpret_cast<v4f*>(ly.rec + (size_t)vh * KD * VD);
-  v4f s[16];
-#pragma unroll
-  for (int i = 0; i < 16; i++) s[i] = S4[(rb * 16 + i) * (VD / 4) + cg];
   if (e != 1.0f) {
 #pragma unroll
     for (int i = 0; i < 16; i++) s[i] = s[i] * e;

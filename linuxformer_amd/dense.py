@@ -37,6 +37,17 @@ class DnParams(ctypes.Structure):
                             "tok", "h", "xn", "P", "on", "keys", "err")]
 
 
+def interleave(w):
+    """Rows (n, K) bf16 in the kernels' order: each lane's K / 64 entries in 8-entry chunks,
+    chunk q of lane l at (q * 64 + l) * 8 (K / 64 = 4: unchanged)."""
+    n, K = w.shape
+    G = K // 64
+    assert K % 64 == 0 and (G == 4 or G % 8 == 0), K
+    if G == 4:
+        return w.contiguous()
+    return w.reshape(n, 64, G // 8, 8).transpose(1, 2).contiguous().reshape(n, K)
+
+
 class DenseDecode:
     """The packed weights of a DenseModel and the decode driver over a cache."""
 
@@ -56,12 +67,12 @@ class DenseDecode:
                               ly["v"].reshape(-1, H), ly["z"].reshape(-1, H),
                               ly["b"].reshape(-1, H), ly["a"].reshape(-1, H)]).contiguous()
             assert proj.shape[0] == self.nproj
-            tens = dict(proj=proj, conv_qk=ly["conv_qk"].contiguous(),
+            tens = dict(proj=interleave(proj), conv_qk=ly["conv_qk"].contiguous(),
                         conv_v=ly["conv_v"].contiguous(), A_log=ly["A_log"].contiguous(),
                         dt_bias=ly["dt_bias"].contiguous(), gnorm=ly["norm"].contiguous(),
                         ln_in=ly["ln_in"].contiguous(), ln_post=ly["ln_post"].contiguous(),
-                        out=ly["out"].reshape(H, -1).contiguous(), gate=ly["gate"].contiguous(),
-                        up=ly["up"].contiguous(), down=ly["down"].contiguous())
+                        out=interleave(ly["out"].reshape(H, -1)), gate=interleave(ly["gate"]),
+                        up=interleave(ly["up"]), down=interleave(ly["down"]))
             self._keep.append(tens)
             cl = cache.layers[L]
             rec, conv = cl.recurrent_states[0], cl.conv_states[0]
@@ -80,6 +91,7 @@ class DenseDecode:
                 setattr(lay, k, t.data_ptr())
             lay.rec, lay.conv = rec.data_ptr(), conv.data_ptr()
         self.layers_d = torch.frombuffer(bytearray(bytes(self.layers_h)), dtype=torch.uint8).to(self.dev)
+        self.embed = interleave(model.embed)  # (the head's rows, and the embedding through it)
         dev = self.dev
         self.h = torch.zeros(H, dtype=torch.float32, device=dev)
         self.xn = torch.zeros(H + I, dtype=torch.float32, device=dev)
@@ -101,7 +113,7 @@ class DenseDecode:
                      rms_eps=sp.rms_eps, geps=sp.gated_eps, n_forced=n_forced,
                      n_steps=self.max_steps, layers=self.layers_d.data_ptr(),
                      layers_host=ctypes.cast(self.layers_h, P64).value,
-                     embed=self.model.embed.data_ptr(), w_final=self.model.norm.data_ptr(),
+                     embed=self.embed.data_ptr(), w_final=self.model.norm.data_ptr(),
                      forced=self.forced.data_ptr(), preds=self.preds.data_ptr(),
                      step=self.step.data_ptr(), tok=self.tok.data_ptr(), h=self.h.data_ptr(),
                      xn=self.xn.data_ptr(), P=self.P.data_ptr(), on=self.on.data_ptr(),

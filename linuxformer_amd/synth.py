@@ -508,6 +508,12 @@ def config4_small(seed: int = 5) -> DenseSpec:
                      seed=seed, n_prefill=24, n_steps=16)
 
 
+def config4_mid(seed: int = 6) -> DenseSpec:
+    """One layer of config 4 at its full widths (hidden 2560, 16 key heads, SwiGLU 9216) with a
+    small vocabulary: the parity tests' check of the full row lengths."""
+    return DenseSpec("c4m", hidden=2560, n_layers=1, vocab=4096, seed=seed, n_prefill=8, n_steps=8)
+
+
 @dataclass
 class DenseModel:
     """Config 4's tensors on a device: bf16 weights of the live blocks only (the zero-padded

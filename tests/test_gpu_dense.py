@@ -25,25 +25,26 @@ def cuda():
 _M = {}
 
 
-def model():
-    if "m" not in _M:
-        spec = synth.config4_small()
+def model(name="small"):
+    if name not in _M:
+        spec = synth.config4_small() if name == "small" else synth.config4_mid()
         dm_cpu = synth.build_dense(spec, "cpu")
-        _M["m"] = (spec, dm_cpu, synth.to_sparse(dm_cpu))
-    return _M["m"]
+        _M[name] = (spec, dm_cpu, synth.to_sparse(dm_cpu))
+    return _M[name]
 
 
 def bits(a):
     return np.ascontiguousarray(a, np.float32).view(np.uint32)
 
 
-def check(n_forced, n, seed=None, graph=True):
+def check(n_forced, n, seed=None, graph=True, name="small"):
     from oracle import oracle as ox
 
-    spec, dm_cpu, sm = model()
+    spec, dm_cpu, sm = model(name)
     conv0, rec0 = synth.dense_state(dm_cpu, seed)
     forced = [int(x) for x in np.random.default_rng(7 + n_forced).integers(0, spec.vocab, n_forced)]
-    print(f"[gpu-test] dense c4s: forced={n_forced} n={n} seed={seed} graph={graph}", flush=True)
+    print(f"[gpu-test] dense {spec.name}: forced={n_forced} n={n} seed={seed} graph={graph}",
+          flush=True)
     dm = synth.dense_to(dm_cpu, "cuda")
     cache = fast.StateCache(conv0, rec0, "bf16", "cuda")
     dd = dense.DenseDecode(dm, cache)
@@ -72,6 +73,12 @@ def test_dense_small_live_state_eager(cuda):
 
 def test_dense_small_live_state_graph(cuda):
     check(4, 12, seed=3, graph=True)
+
+
+def test_dense_full_widths(cuda):
+    """Config 4's full row lengths (hidden 2560: 40 entries per lane; SwiGLU 9216: 144; 16 key
+    heads x 2 live value heads: 4096 out_proj entries, 64) over one layer, from live states."""
+    check(3, 6, seed=5, name="mid")
 
 
 def test_dense_rejects_dead_state(cuda):
