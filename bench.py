@@ -2,7 +2,7 @@
 verified-prefill tok/s of the same stack (BASELINE's two metrics).
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--tokens T] [--config c2]
-                    [--legs decode,prefill] [--pf-calls N] [--pf-tokens T]
+                    [--legs decode,prefill[,dense]] [--pf-calls N] [--pf-tokens T]
 
 Decode (the headline `value`): a step is one launch of the persistent decode kernel over one
 chunk of T tokens (default 262,144), continuing the same greedy stream launch
@@ -15,6 +15,10 @@ Verified prefill (`verified_prefill`): BASELINE config 3, calls of 65,536 seeded
 through the same stack (synth.config3: 0.35 % of token-layers gated, 5 % of (key head, 64-token
 chunk) pairs active), each call embedding, running all 37 layers and taking every position's
 argmax (lx.fast's verified mode), timed with HIP events on the stream.
+
+Dense decode (`dense_decode`, with --legs ...,dense): BASELINE config 4, the dense padded
+text-view stack (synth.config4: 24 layers, hidden 2560, SwiGLU 9216); an 8,192-step forced
+prefix of seeded uniform ids, then 4,096 greedy steps timed.
 
 One JSON line on stdout (the driver's contract); everything else goes to stderr.
 """
@@ -157,6 +161,118 @@ def prefill_leg(calls: int, T: int, cpu_tokens: int) -> dict:
     return out
 
 
+def dense_cpu_tok_s(dm, n: int) -> float:
+    """The dense stack's decode step restated with torch's eager ops in float32 on the host cores
+    (weights copied from the GPU once; the stock forward's structure, not its bit order): tok/s
+    over n greedy steps from a zero state. A reported baseline only."""
+    import numpy as np
+    import torch
+    import torch.nn.functional as F
+
+    sp, d = dm.spec, dm.dims
+    H, nk, kl, rl = sp.hidden, sp.nk, sp.kd_live, sp.r_live
+    torch.set_num_threads(os.cpu_count() or 1)
+    L = [{k: v.float().cpu() for k, v in ly.items()} for ly in dm.layers]
+    E = dm.embed.float().cpu()
+    wf = dm.norm.float().cpu()
+    S = [torch.zeros(nk * rl, 256, 128) for _ in L]
+    win = [torch.zeros(2 * nk * kl + nk * rl * 128, 4) for _ in L]
+
+    def rms(x, w, eps):
+        return (x * torch.rsqrt(x.pow(2).mean() + eps)) * (1.0 + w)
+
+    tok = 0
+    t = time.perf_counter()
+    for _ in range(n):
+        h = E[tok].clone()
+        for i, ly in enumerate(L):
+            x = rms(h, ly["ln_in"], sp.rms_eps)
+            qk = ly["qk"].reshape(-1, H) @ x
+            v = ly["v"].reshape(-1, H) @ x
+            z = (ly["z"].reshape(-1, H) @ x).view(nk * rl, 128)
+            b = ly["b"].reshape(-1, H) @ x
+            a = ly["a"].reshape(-1, H) @ x
+            P = torch.cat([qk, v])
+            win[i] = torch.cat([win[i][:, 1:], P[:, None]], 1)
+            taps = torch.cat([ly["conv_qk"].reshape(-1, 4), ly["conv_v"].reshape(-1, 4)])
+            y = F.silu((win[i] * taps).sum(1))
+            q = F.normalize(y[:nk * kl].view(nk, kl), dim=-1).repeat_interleave(rl, 0) / 16.0
+            k = F.normalize(y[nk * kl:2 * nk * kl].view(nk, kl), dim=-1).repeat_interleave(rl, 0)
+            vv = y[2 * nk * kl:].view(nk * rl, 128)
+            R = d.nv // nk
+            vh = torch.tensor([kh * R + r for kh in range(nk) for r in range(rl)])
+            g = torch.exp(-torch.exp(ly["A_log"][vh]) * F.softplus(a + ly["dt_bias"][vh]))
+            St = S[i][:, :kl] * g[:, None, None]
+            kv = (St * k[:, :, None]).sum(1)
+            St = St + k[:, :, None] * ((vv - kv) * torch.sigmoid(b)[:, None])[:, None, :]
+            S[i][:, :kl] = St
+            o = (St * q[:, :, None]).sum(1)
+            on = (o * torch.rsqrt(o.pow(2).mean(-1, keepdim=True) + sp.gated_eps)) * ly["norm"] * F.silu(z)
+            h = h + ly["out"].reshape(H, -1) @ on.reshape(-1)
+            xm = rms(h, ly["ln_post"], sp.rms_eps)
+            h = h + ly["down"] @ (F.silu(ly["gate"] @ xm) * (ly["up"] @ xm))
+        tok = int(torch.argmax(E @ rms(h, wf, sp.rms_eps)))
+    return n / (time.perf_counter() - t)
+
+
+def dense_leg(n_prefill: int, n_steps: int, cpu_tokens: int) -> dict:
+    """the dense padded text-view stack; n_prefill seeded uniform forced steps
+    from a zero state, then n_steps greedy steps, timed (HIP events on the stream)."""
+    import numpy as np
+    import torch
+
+    from linuxformer_amd import dense, fast, synth
+
+    spec = synth.config4()
+    t0 = time.time()
+    dm = synth.build_dense(spec, "cuda")
+    d = dm.dims
+    conv0 = np.zeros((d.n_layers, d.n_conv, 4), np.float32)
+    rec0 = np.zeros((d.n_layers, d.nv, 256, 128), np.float32)
+    cache = fast.StateCache(conv0, rec0, "bf16", torch.device("cuda", 0))
+    dd = dense.DenseDecode(dm, cache, max_steps=max(n_prefill, n_steps) + 1)
+    torch.cuda.synchronize()
+    log(f"[bench] c4: built in {time.time() - t0:.1f}s")
+    toks = np.random.default_rng(spec.seed).integers(0, spec.vocab, n_prefill).tolist()
+    t = time.perf_counter()
+    p1 = dd.run(toks, n_prefill)
+    pre_s = time.perf_counter() - t
+    log(f"[bench] c4: prefill of {n_prefill} forced steps in {pre_s:.2f}s")
+    stream = torch.cuda.current_stream()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    p2 = dd.run([p1[-1]], n_steps)
+    e1.record(stream)
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1)
+    H, I, nk, kl, rl = spec.hidden, spec.inter, spec.nk, spec.kd_live, spec.r_live
+    nvr = nk * rl * 128
+    w_layer = 2 * ((2 * nk * kl + 2 * nvr + 2 * nk * rl) * H + H * nvr + 3 * I * H)
+    state = 2 * nk * rl * 256 * 128 * 4
+    b_tok = d.n_layers * (w_layer + state) + 2 * spec.vocab * H
+    pad_layer = 2 * ((2 * nk * 256 + 2 * d.nv * 128 + 2 * d.nv) * H + H * d.nv * 128 + 3 * I * H)
+    achieved = b_tok * n_steps / (ms * 1e-3) / 1e9
+    out = {"metric": "dense padded decode tok/s, 24-layer text-view stack, 1 MI355X",
+           "value": round(n_steps / (ms * 1e-3), 1), "unit": "tok/s",
+           "ms_per_token": round(ms / n_steps, 4), "steps": n_steps,
+           "prefill": {"forced_steps": n_prefill, "s": round(pre_s, 2),
+                       "tok_s": round(n_prefill / pre_s, 1)},
+           "config": {"workload": "c4: 24 layers, hidden 2560, 16 key heads (256, 128 live), 128 "
+                                  "value heads (2 live per key head), SwiGLU 9216, vocab 248,320, "
+                                  "bf16 N(0, 0.02); zero state"},
+           "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS,
+                        "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
+                        "bytes_per_token": b_tok,
+                        "padded_bytes_per_token": d.n_layers * (pad_layer + state) + 2 * spec.vocab * H},
+           "distinct_predictions": len(set(p2))}
+    if cpu_tokens > 0:
+        out["cpu_baseline"] = {"value": round(dense_cpu_tok_s(dm, cpu_tokens), 3), "unit": "tok/s",
+                               "cores": os.cpu_count(), "kind": "port",
+                               "sample": f"{cpu_tokens} greedy steps from a zero state, torch eager "
+                                         "float32 on the host"}
+    return out
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -170,6 +286,9 @@ def main() -> int:
     ap.add_argument("--pf-calls", type=int, default=5)
     ap.add_argument("--pf-tokens", type=int, default=65_536)
     ap.add_argument("--pf-cpu-tokens", type=int, default=48)
+    ap.add_argument("--dn-prefill", type=int, default=8192)
+    ap.add_argument("--dn-steps", type=int, default=4096)
+    ap.add_argument("--dn-cpu-tokens", type=int, default=4)
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: the decode is one sequential chain per stream and this "
@@ -178,7 +297,12 @@ def main() -> int:
 
     legs = set(args.legs.split(","))
     if "decode" not in legs:
-        print(json.dumps(prefill_leg(args.pf_calls, args.pf_tokens, args.pf_cpu_tokens)), flush=True)
+        out = {}
+        if "prefill" in legs:
+            out["verified_prefill"] = prefill_leg(args.pf_calls, args.pf_tokens, args.pf_cpu_tokens)
+        if "dense" in legs:
+            out["dense_decode"] = dense_leg(args.dn_prefill, args.dn_steps, args.dn_cpu_tokens)
+        print(json.dumps(out), flush=True)
         return 0
 
     import numpy as np
@@ -262,6 +386,9 @@ def main() -> int:
         del mg, cache
         torch.cuda.empty_cache()
         out["verified_prefill"] = prefill_leg(args.pf_calls, args.pf_tokens, args.pf_cpu_tokens)
+    if "dense" in legs:
+        torch.cuda.empty_cache()
+        out["dense_decode"] = dense_leg(args.dn_prefill, args.dn_steps, args.dn_cpu_tokens)
     print(json.dumps(out), flush=True)
     return 0
 
