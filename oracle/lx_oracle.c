@@ -297,6 +297,18 @@ static float row_dot(const ox_csr* m, int r, const float* x) {
   return p[0];
 }
 
+/* test export: x . w over n terms in a row's order (blocks 0: in order; 64: the dense order) */
+float ox_row_dot(int blocks, int n, const float* x, const float* w) {
+  int64_t ptr[2] = {0, n};
+  int32_t* col = malloc(sizeof(int32_t) * (n ? n : 1));
+  if (!col) abort();
+  for (int i = 0; i < n; i++) col[i] = i;
+  ox_csr m = {1, n, ptr, col, w, blocks, 0};
+  float r = row_dot(&m, 0, x);
+  free(col);
+  return r;
+}
+
 /* out[r] = D(row r . x) */
 static void csr_mv(const ox_csr* m, const float* x, float* out) {
   for (int r = 0; r < m->nrows; r++) out[r] = D(row_dot(m, r, x));

@@ -71,6 +71,8 @@ def lib():
         _lib.ox_layer_step.argtypes = [PTR, I32, PTR, PTR, PTR]
         _lib.ox_head.argtypes = [PTR, PTR, I32, PTR, PTR]
         _lib.ox_rec_step.argtypes = [I32, I32, I32] + [PTR] * 7
+        _lib.ox_row_dot.restype = F32
+        _lib.ox_row_dot.argtypes = [I32, I32, PTR, PTR]
     return _lib
 
 
@@ -93,6 +95,12 @@ def sum_h(x) -> np.float32:
 def sum_64(x) -> np.float32:
     x = np.ascontiguousarray(x, np.float32)
     return np.float32(lib().ox_sum_64(_p(x), len(x)))
+
+
+def row_dot(x, w, dense: bool) -> np.float32:
+    """x . w in a row's order: in order from +0, or (dense) the dense order."""
+    x, w = np.ascontiguousarray(x, np.float32), np.ascontiguousarray(w, np.float32)
+    return np.float32(lib().ox_row_dot(64 if dense else 0, len(x), _p(x), _p(w)))
 
 
 def rec_step(q, k, v, g, beta, S, bf16: bool):

@@ -243,3 +243,28 @@ def test_recurrent_step_generic_inputs(oracle_lib, dtype):
     assert np.abs(S - S_t).max() <= 1e-6 * np.abs(S_t).max()
     if dtype == "bf16":
         assert (S[same_e] == S_t[same_e]).all()
+
+
+def test_dense_order_sums_exact_integers(oracle_lib):
+    """Small integers: every order gives the exact sum, so a dropped, doubled or misplaced term
+    (a wrong group bound) shows."""
+    ox = oracle_lib
+    rng = np.random.default_rng(0)
+    for n in (64, 2560, 9216):
+        x = rng.integers(-8, 9, n).astype(np.float32)
+        w = rng.integers(-8, 9, n).astype(np.float32)
+        exact = float(np.dot(x.astype(np.int64), w.astype(np.int64)))
+        assert float(ox.row_dot(x, w, dense=True)) == exact
+        assert float(ox.row_dot(x, w, dense=False)) == exact
+
+
+def test_dense_order_is_the_group_tree(oracle_lib):
+    """Terms 1, 2^24, 1 in groups 0, 1 and 32 of a 64-entry row: the tree adds group 32 to group
+    0 first (1 + 1 = 2), then group 1 last: 2 + 2^24 = 16777218, exact; in order, 1 + 2^24
+    rounds to 2^24 and so does + 1. Both values follow from the definitions by hand."""
+    ox = oracle_lib
+    x = np.zeros(64, np.float32)
+    w = np.ones(64, np.float32)
+    x[0], x[1], x[32] = 1.0, 2.0 ** 24, 1.0
+    assert float(ox.row_dot(x, w, dense=True)) == 16777218.0
+    assert float(ox.row_dot(x, w, dense=False)) == 16777216.0
