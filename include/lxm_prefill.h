@@ -59,8 +59,8 @@ typedef struct lxm_pf_vc {   /* a value channel of a slot: in_proj_qkv row and c
 
 /* One layer's tables: byte offsets into the plan's blob; entry starts index the layer's
    lxm_pf_ent array at `ent`. A candidate record (one per position the layer may touch) holds
-   {tok, live key slots, 2 x pad}, qn[n_ks][256], kn[n_ks][256], v[n_vs][128], z[n_vs][128]
-   (then the gated norm's output), beta[n_vs], e[n_vs], proc[n_vs] (int), padded to 16 bytes:
+   {tok, live key slots, 2 x pad}, qn[n_ks][256], kn[n_ks][256], v[n_vs][128] (then the delta
+   rule's output o), z[n_vs][128], beta[n_vs], e[n_vs], proc[n_vs] (int), padded to 16 bytes:
    rec_bytes. */
 typedef struct lxm_pf_layer {
   int64_t ent;       /* lxm_pf_ent[] */

@@ -10,7 +10,7 @@
 // head keeps its state and outputs 0): those candidates are compacted in order, their inputs
 // (q, k, v, z, beta, the decay) computed in parallel, and one workgroup per value head then runs
 // the recurrence over them with the head's 256x128 state in registers. The gated norm and
-// out_proj go back to the candidates' residuals in parallel.
+// out_proj run per candidate again, in parallel.
 //
 // Semantics: every position sees exactly the stock decode step (transformers' Qwen3_5 decoder
 // layer with causal_conv1d_update and torch_recurrent_gated_delta_rule, in lx/lx/hf.py's chip
@@ -31,7 +31,7 @@ using namespace lxm;
 #define VD 128
 #define MAXH LXM_MAXH
 static_assert(TT == 4, "a residual column of a tile is one 16-byte vector");
-static_assert(NT == KD + 2 * VD, "the delta kernel loads k/q, v and z with one thread each");
+static_assert(NT >= KD + VD, "the delta kernel loads k/q and v with one thread each");
 
 typedef float v4f __attribute__((ext_vector_type(4)));
 typedef uint32_t v2u __attribute__((ext_vector_type(2)));
@@ -599,12 +599,11 @@ __global__ __launch_bounds__(256) void pf_tail(const lxm_pf_params* __restrict__
 // The recurrence of one value-head slot over the layer's candidates, in position order
 // (torch_recurrent_gated_delta_rule, TF:330-380, one token at a time): S <- S * exp(g) when
 // exp(g) != 1; with a live query or key kv = S^T k, delta = (v - kv) beta, S += k delta^T,
-// o = D(S^T q), then the gated norm (TF:168-184) y = D(D(w * D(o * r)) * silu(z)) into the
-// record (over z). The state tile stays in registers: thread (cg, rb) holds columns 4cg..4cg+3 of
+// o = D(S^T q) into the record (over v, which this step has read). The state tile stays in registers: thread (cg, rb) holds columns 4cg..4cg+3 of
 // rows 16rb..16rb+15, one of ATen's 16-row cascade blocks (torch .sum(-2) on the CPU).
 // A candidate's inputs as one thread of the delta kernel holds them (loaded one candidate ahead):
-// the header word, the slot's decay factor, and the thread's share of k and q (threads < 256),
-// v (256..383) or z (384..511), and beta (thread 0).
+// the header word, the slot's decay factor, and the thread's share of k and q (threads < 256) or
+// v (256..383), and beta (thread 0).
 struct DeltaIn {
   uint32_t live;
   float e, a, b, beta;
@@ -622,8 +621,6 @@ __device__ __forceinline__ DeltaIn delta_in(const uint8_t* rec, const RecOff& ro
       d.b = reinterpret_cast<const float*>(rec + ro.q)[kslot * KD + t];
     } else if (t < KD + VD) {
       d.a = reinterpret_cast<const float*>(rec + ro.v)[vslot * VD + t - KD];
-    } else {
-      d.a = reinterpret_cast<const float*>(rec + ro.z)[vslot * VD + t - KD - VD];
     }
     if (t == 0) d.beta = reinterpret_cast<const float*>(rec + ro.b)[vslot];
   }
@@ -632,17 +629,15 @@ __device__ __forceinline__ DeltaIn delta_in(const uint8_t* rec, const RecOff& ro
 
 template <bool BF>
 __global__ __launch_bounds__(NT) void pf_delta(const lxm_pf_params* __restrict__ pp, int L) {
-  __shared__ __align__(16) float kn[KD], qn[KD], vb[VD], zb[VD], dl[VD], ob[VD];
+  __shared__ __align__(16) float kn[KD], qn[KD], vb[VD], dl[VD];
   __shared__ __align__(16) float bs[16 * VD];
   __shared__ float beta_s;
   const lxm_pf_params& p = *pp;
   const lxm_pf_layer& ly = p.layers[L];
-  const int t = threadIdx.x, vslot = blockIdx.x, lane = t & 63;
+  const int t = threadIdx.x, vslot = blockIdx.x;
   // everything the loop needs in registers: its stores to the records could alias p and ly
   const lxm_pf_vs sv = tab<lxm_pf_vs>(p.blob, ly.vs)[vslot];
   const RecOff ro(ly.n_ks, ly.n_vs);
-  const float* gwp = tab<float>(p.blob, ly.gnorm);
-  const float gw0 = gwp[lane], gw1 = gwp[lane + 64], geps = ly.geps;
   const int count = p.count[L];
   const int64_t rec_b = ly.rec_bytes;
   uint8_t* const recs = p.recs;
@@ -675,16 +670,22 @@ __global__ __launch_bounds__(NT) void pf_delta(const lxm_pf_params* __restrict__
           qn[t] = cur.b;
         } else if (t < KD + VD) {
           vb[t - KD] = cur.a;
-        } else {
-          zb[t - KD - VD] = cur.a;
         }
         if (t == 0) beta_s = cur.beta;
         __syncthreads();
+        // the thread's 16 rows of k and q at once (one LDS wait), then the cascade blocks'
+        // sums; a zero factor adds nothing (the oracle skips it; a sum from +0 is never -0)
+        float kr[16], qr[16];
+#pragma unroll
+        for (int i = 0; i < 16; i++) {
+          kr[i] = kn[rb * 16 + i];
+          qr[i] = qn[rb * 16 + i];
+        }
         v4f a = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
         for (int i = 0; i < 16; i++) {
-          const float f = kn[rb * 16 + i];
-          if (f != 0.0f) a = v4f{a.x + s[i].x * f, a.y + s[i].y * f, a.z + s[i].z * f, a.w + s[i].w * f};
+          const v4f m = v4f{a.x + s[i].x * kr[i], a.y + s[i].y * kr[i], a.z + s[i].z * kr[i], a.w + s[i].w * kr[i]};
+          a = kr[i] != 0.0f ? m : a;
         }
         reinterpret_cast<v4f*>(bs + rb * VD)[cg] = a;
         __syncthreads();
@@ -699,30 +700,22 @@ __global__ __launch_bounds__(NT) void pf_delta(const lxm_pf_params* __restrict__
         v4f o = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
         for (int i = 0; i < 16; i++) {
-          const float f = kn[rb * 16 + i];
-          if (f != 0.0f) s[i] = v4f{s[i].x + f * d.x, s[i].y + f * d.y, s[i].z + f * d.z, s[i].w + f * d.w};
-          const float g = qn[rb * 16 + i];
-          if (g != 0.0f) o = v4f{o.x + s[i].x * g, o.y + s[i].y * g, o.z + s[i].z * g, o.w + s[i].w * g};
+          // (the update keeps rows with a zero key factor exactly as they are: -0 stays -0)
+          const v4f u = v4f{s[i].x + kr[i] * d.x, s[i].y + kr[i] * d.y, s[i].z + kr[i] * d.z, s[i].w + kr[i] * d.w};
+          s[i] = kr[i] != 0.0f ? u : s[i];
+          const v4f m = v4f{o.x + s[i].x * qr[i], o.y + s[i].y * qr[i], o.z + s[i].z * qr[i], o.w + s[i].w * qr[i]};
+          o = qr[i] != 0.0f ? m : o;
         }
         reinterpret_cast<v4f*>(bs + rb * VD)[cg] = o;
         __syncthreads();
+        // o = D(the block sums in order), into the record (over v: read at this step's start);
+        // the gated norm is pf_out's
         if (t < VD) {
           float q = 0.0f;
 #pragma unroll
           for (int b = 0; b < 16; b++) q = q + bs[b * VD + t];
-          ob[t] = rd<BF>(q);
+          reinterpret_cast<float*>(rec + ro.v)[vslot * VD + t] = rd<BF>(q);
         }
-        __syncthreads();
-        if (t < 64) {
-          float ss = 0.0f;
-          for (int k = lane; k < VD; k += 64) ss = ss + ob[k] * ob[k];
-          ss = sum64(ss);
-          const float rr = rsqrt_(ss / (float)VD + geps);
-          float* y = reinterpret_cast<float*>(rec + ro.z) + vslot * VD;
-          y[lane] = rd<BF>(rd<BF>(gw0 * rd<BF>(ob[lane] * rr)) * silu(zb[lane]));
-          y[lane + 64] = rd<BF>(rd<BF>(gw1 * rd<BF>(ob[lane + 64] * rr)) * silu(zb[lane + 64]));
-        }
-        __syncthreads();
       }
     }
     if (t == 0) reinterpret_cast<int32_t*>(rec + ro.pr)[vslot] = proc;
@@ -734,40 +727,57 @@ __global__ __launch_bounds__(NT) void pf_delta(const lxm_pf_params* __restrict__
 }
 
 // ---------------------------------------------------------------------------------------------
-// out_proj and the residual add at each candidate with a live head (TF:541-543, :777-779):
-// per residual row the terms over every value dim in ascending order, rounded once
-// (lx/lx/fast.py:349-361), then h = D(h + that). Heads that did not run add nothing (their
-// output is exactly 0 and the oracle skips zero inputs). One workgroup per candidate.
+// The gated norm of each head that ran (TF:168-184): y = D(D(w * D(o * r)) * silu(z)), r =
+// rsqrt(mean(o^2) + eps) with the squares summed per lane (dims lane, lane + 64) and then by the
+// pairwise tree, one wave per head. Then out_proj and the residual add at the candidate
+// (TF:541-543, :777-779): per residual row the terms over every value dim in ascending order,
+// rounded once (lx/lx/fast.py:349-361), then h = D(h + that). Heads that did not run add nothing
+// (their output is exactly 0 and the oracle skips zero inputs). One workgroup per candidate.
 template <bool BF>
 __global__ __launch_bounds__(NT) void pf_out(const lxm_pf_params* __restrict__ pp, int L) {
   extern __shared__ __align__(16) uint8_t sm[];
   __shared__ int any_s;
   const lxm_pf_params& p = *pp;
   const lxm_pf_layer& ly = p.layers[L];
-  const int t = threadIdx.x, H = p.hidden;
+  const int t = threadIdx.x, H = p.hidden, lane = t & 63, wv = t >> 6;
   float* ON = reinterpret_cast<float*>(sm);
   const RecOff ro(ly.n_ks, ly.n_vs);
   const lxm_pf_drow* orows = tab<lxm_pf_drow>(p.blob, ly.orows);
   const lxm_pf_ent* ent = tab<lxm_pf_ent>(p.blob, ly.ent);
-  const int count = p.count[L];
+  const float* gwp = tab<float>(p.blob, ly.gnorm);
+  const float gw0 = gwp[lane], gw1 = gwp[lane + 64], geps = ly.geps;
+  const int count = p.count[L], n_vs = ly.n_vs;
   for (int j = blockIdx.x; j < count; j += gridDim.x) {
     const uint8_t* rec = p.recs + (int64_t)j * ly.rec_bytes;
     const int tok = reinterpret_cast<const int32_t*>(rec)[0];
     const int32_t* pr = reinterpret_cast<const int32_t*>(rec + ro.pr);
-    const float* y = reinterpret_cast<const float*>(rec + ro.z);
+    const float* o = reinterpret_cast<const float*>(rec + ro.v);
+    const float* z = reinterpret_cast<const float*>(rec + ro.z);
     if (t == 0) any_s = 0;
     __syncthreads();
-    for (int i = t; i < ly.n_vs * VD; i += NT) {
-      const bool on = pr[i >> 7] == 2;
-      ON[i] = on ? y[i] : 0.0f;
-      if (on && (i & 127) == 0) any_s = 1;
+    for (int v = wv; v < n_vs; v += NT / 64) {
+      float y0 = 0.0f, y1 = 0.0f;
+      if (pr[v] == 2) {
+        const float o0 = o[v * VD + lane], o1 = o[v * VD + lane + 64];
+        const float z0 = z[v * VD + lane], z1 = z[v * VD + lane + 64];
+        float ss = 0.0f;
+        ss = ss + o0 * o0;
+        ss = ss + o1 * o1;
+        ss = sum64(ss);
+        const float rr = rsqrt_(ss / (float)VD + geps);
+        y0 = rd<BF>(rd<BF>(gw0 * rd<BF>(o0 * rr)) * silu(z0));
+        y1 = rd<BF>(rd<BF>(gw1 * rd<BF>(o1 * rr)) * silu(z1));
+        if (lane == 0) any_s = 1;
+      }
+      ON[v * VD + lane] = y0;
+      ON[v * VD + lane + 64] = y1;
     }
     __syncthreads();
     if (any_s) {
       for (int i = t; i < ly.n_orows; i += NT) {
         const lxm_pf_drow r = orows[i];
-        const float o = rd<BF>(dot1<BF>(ent + r.start, r.len, sm));
-        st_el<BF>(p.h, H, tok, r.row, rd<BF>(ld_el<BF>(p.h, H, tok, r.row) + o));
+        const float y = rd<BF>(dot1<BF>(ent + r.start, r.len, sm));
+        st_el<BF>(p.h, H, tok, r.row, rd<BF>(ld_el<BF>(p.h, H, tok, r.row) + y));
       }
     }
     __syncthreads();
