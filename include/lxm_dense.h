@@ -58,9 +58,11 @@ typedef struct lxm_dn_params {
   int32_t* step;              /* (1): the next step's index (advanced by each call) */
   int32_t* tok;               /* (1): the last prediction */
   float* h;                   /* (hidden): the residual */
-  float* xn;                  /* (hidden + inter): a norm's output, then the MLP's act at +hidden */
+  float* xn;                  /* (hidden + inter): the MLP's act at +hidden (the norms are formed
+                                 inside the kernels that read them) */
   float* P;                   /* (rows of proj): the projections */
-  float* on;                  /* (nk x rl x 128): the live heads' gated-norm outputs */
+  float* on;                  /* (nk x rl x 128): the live heads' delta-rule outputs o (the out_proj
+                                 kernel forms the gated norm); nk x rl <= 32 */
   unsigned long long* keys;   /* (1): the head's argmax key */
   int32_t* err;               /* (1): 1 a forced token out of range */
 } lxm_dn_params;

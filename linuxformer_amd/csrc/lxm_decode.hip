@@ -158,14 +158,6 @@ __device__ __forceinline__ void drain() {
 }
 __device__ __forceinline__ uint64_t wall() { return __builtin_amdgcn_s_memrealtime(); }
 
-// a workgroup barrier ordering LDS only: global loads in flight (the next layer's tables)
-// stay in flight across it
-__device__ __forceinline__ void lds_barrier() {
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
-  __builtin_amdgcn_s_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
-}
-
 extern __shared__ __align__(16) uint8_t smem[];
 
 // In-kernel phase counters (lx/csrc/mega.cu's prof buffer and MK_SUBPROF checkpoints): with

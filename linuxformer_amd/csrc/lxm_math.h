@@ -133,6 +133,14 @@ __device__ __forceinline__ float acc(float s, float x, float w) {
   else return s + x * w;
 }
 
+// a workgroup barrier ordering LDS only: global loads in flight (the next tables or weight rows)
+// stay in flight across it
+__device__ __forceinline__ void lds_barrier() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
 // A wave's tree sum: lane 0 ends with the sum that __shfl_down at offsets 32, 16, ..., 1
 // leaves there (lane l adds lane l + off). Offsets 32 and 16 by gfx950's permlane swaps, 8..1
 // by DPP row shifts; no LDS round trips.
