@@ -245,6 +245,14 @@ def dense_leg(n_prefill: int, n_steps: int, cpu_tokens: int) -> dict:
     e1.record(stream)
     torch.cuda.synchronize()
     ms = e0.elapsed_time(e1)
+    # the same steps as one persistent launch (lxm_dn_run), timed the same way
+    n_per = max(1, n_steps // 4)
+    e2, e3 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e2.record(stream)
+    dd.run([p2[-1]], n_per, mode="persistent")
+    e3.record(stream)
+    torch.cuda.synchronize()
+    ms_per = e2.elapsed_time(e3)
     H, I, nk, kl, rl = spec.hidden, spec.inter, spec.nk, spec.kd_live, spec.r_live
     nvr = nk * rl * 128
     w_layer = 2 * ((2 * nk * kl + 2 * nvr + 2 * nk * rl) * H + H * nvr + 3 * I * H)
@@ -264,7 +272,9 @@ def dense_leg(n_prefill: int, n_steps: int, cpu_tokens: int) -> dict:
                         "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
                         "bytes_per_token": b_tok,
                         "padded_bytes_per_token": d.n_layers * (pad_layer + state) + 2 * spec.vocab * H},
-           "distinct_predictions": len(set(p2))}
+           "distinct_predictions": len(set(p2)),
+           "persistent": {"steps": n_per, "tok_s": round(n_per / (ms_per * 1e-3), 1),
+                          "note": "lxm_dn_run, continuing from the greedy run's states"}}
     if cpu_tokens > 0:
         out["cpu_baseline"] = {"value": round(dense_cpu_tok_s(dm, cpu_tokens), 3), "unit": "tok/s",
                                "cores": os.cpu_count(), "kind": "port",

@@ -63,14 +63,25 @@ typedef struct lxm_dn_params {
   float* P;                   /* (rows of proj): the projections */
   float* on;                  /* (nk x rl x 128): the live heads' delta-rule outputs o (the out_proj
                                  kernel forms the gated norm); nk x rl <= 32 */
-  unsigned long long* keys;   /* (1): the head's argmax key */
-  int32_t* err;               /* (1): 1 a forced token out of range */
+  unsigned long long* keys;   /* (2): the head's argmax key (lxm_dn_run alternates between the two
+                                 by step parity; both zero before a run) */
+  int32_t* err;               /* (1): 1 a forced token out of range, 2 a wait of lxm_dn_run timed out */
+  uint32_t* sync;             /* (256): lxm_dn_run's barrier counters, zero before each run */
 } lxm_dn_params;
 
 /* One greedy step (embedding, every layer, the head's first maximum, the token fed back) on
-   stream. p_host: the block in host memory (launch shapes); p_dev: the same bytes on the
-   device. Returns a hipError_t. */
+   stream, as five kernels per layer (a caller may capture one call in a graph and replay it).
+   p_host: the block in host memory (launch shapes); p_dev: the same bytes on the device.
+   Returns a hipError_t. */
 int lxm_dn_step(const lxm_dn_params* p_host, const lxm_dn_params* p_dev, void* stream);
+
+/* n greedy steps in one cooperative launch of one workgroup per CU (the same results as n calls
+   of lxm_dn_step): the layers' phases are separated by grid barriers, each wave requesting its
+   first weight rows of the next phase before it waits. Before the call: sync[0..255] = 0, keys[0..1] =
+   0, *err = 0; afterwards *err != 0 reports a bad forced token (1) or a timed-out wait (2). Needs
+   nk x rl x 4 <= the device's CUs and (hidden, live value dims, inter) = (2560, 4096, 9216) or
+   (256, 512, 512). Returns a hipError_t. */
+int lxm_dn_run(const lxm_dn_params* p_host, const lxm_dn_params* p_dev, int n, void* stream);
 
 #ifdef __cplusplus
 }

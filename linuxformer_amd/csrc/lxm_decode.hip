@@ -36,6 +36,7 @@
 
 #include "../../include/lxm.h"
 #include "lxm_math.h"
+#include "lxm_sync.h"
 
 using namespace lxm;
 
@@ -45,7 +46,6 @@ using namespace lxm;
 #define KD LXM_KD
 #define VD LXM_VD
 #define RMAX LXM_RMAX
-#define TIMEOUT_TICKS 300000000ull  // 3 s of the 100 MHz wall clock
 static_assert(MAXH == 8 * NT, "eight residual rows per thread cover any hidden size");
 
 // ---------------------------------------------------------------------------------------------
@@ -110,54 +110,6 @@ static_assert(L_H + 4 * MAXH <= 65536, "gathered vectors below 64 KB");
 #define EV_GDN 1u
 #define EV_OUT 2u
 
-#define GAS __attribute__((address_space(1)))
-template <class T>
-__device__ __forceinline__ GAS T* gp(T* q) {
-  return (GAS T*)q;
-}
-template <class T>
-__device__ __forceinline__ const GAS T* gp(const T* q) {
-  return (const GAS T*)q;
-}
-
-// a struct from global memory through global loads (a generic copy would be flat loads)
-template <class T>
-__device__ __forceinline__ T ldg(const T* q) {
-  static_assert(sizeof(T) % 4 == 0, "whole words");
-  T r;
-  const GAS uint32_t* src = gp(reinterpret_cast<const uint32_t*>(q));
-  uint32_t* dst = reinterpret_cast<uint32_t*>(&r);
-#pragma unroll
-  for (int i = 0; i < (int)(sizeof(T) / 4); i++) dst[i] = src[i];
-  return r;
-}
-typedef float v4f __attribute__((ext_vector_type(4)));
-
-// agent-scope relaxed atomics: sc1 loads and stores on gfx950, coherent across the XCDs
-__device__ __forceinline__ uint32_t ld_rlx(const uint32_t* p) {
-  return __hip_atomic_load(gp(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ void st_rlx(uint32_t* p, uint32_t v) {
-  __hip_atomic_store(gp(p), v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ float ld_rlxf(const float* p) {
-  return __hip_atomic_load(gp(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ void st_rlxf(float* p, float v) {
-  __hip_atomic_store(gp(p), v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ void add_rlx(uint32_t* p, uint32_t v) {
-  __hip_atomic_fetch_add(gp(p), v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-// every earlier memory op of this wave has completed (its stores are visible at agent scope
-// when they were agent-scope atomics)
-__device__ __forceinline__ void drain() {
-  __atomic_signal_fence(__ATOMIC_SEQ_CST);
-  __builtin_amdgcn_s_waitcnt(0);
-  __atomic_signal_fence(__ATOMIC_SEQ_CST);
-}
-__device__ __forceinline__ uint64_t wall() { return __builtin_amdgcn_s_memrealtime(); }
-
 extern __shared__ __align__(16) uint8_t smem[];
 
 // In-kernel phase counters (lx/csrc/mega.cu's prof buffer and MK_SUBPROF checkpoints): with
@@ -207,20 +159,6 @@ __device__ __forceinline__ void sp_depart(int) {}
 __device__ __forceinline__ void sp_skip() {}
 #endif
 
-// spin (one thread) until the counter reaches target (modulo 2^32); false on timeout or
-// another block's error
-__device__ bool spin_ge(const uint32_t* p, uint32_t target, int32_t* err, int code) {
-  const uint64_t t0 = wall();
-  while ((int32_t)(ld_rlx(p) - target) < 0) {
-    __builtin_amdgcn_s_sleep(2);
-    if (__hip_atomic_load(gp(err), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) return false;
-    if (wall() - t0 > TIMEOUT_TICKS) {
-      __hip_atomic_fetch_max(gp(err), code, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      return false;
-    }
-  }
-  return true;
-}
 // spin (one thread) until the sum of a counter's NGRP copies reaches target (modulo 2^32)
 __device__ bool spin_sum_ge(const uint32_t* p, uint32_t target, int32_t* err, int code) {
   const uint64_t t0 = wall();
@@ -391,14 +329,6 @@ __device__ __forceinline__ float* rr_at(const lxm_params& p, int step, int L) {
 }
 // 16 bytes to global memory at agent scope (a buffer store with the sc1 policy: written through
 // to the coherence point, like the relaxed atomic stores)
-// a pointer the whole wave shares, in scalar registers (a buffer resource built from it is
-// uniform: no waterfall loop around the store)
-__device__ __forceinline__ float* wave_ptr(float* q) {
-  const uint64_t u = reinterpret_cast<uint64_t>(q);
-  const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)u);
-  const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(u >> 32));
-  return reinterpret_cast<float*>(((uint64_t)hi << 32) | lo);
-}
 __device__ __forceinline__ void st4_rlx(float* base, int idx, v4f v) {
   const __amdgpu_buffer_rsrc_t r = __builtin_amdgcn_make_buffer_rsrc(wave_ptr(base), 0, 0x7fffffff, 0x00020000);
   typedef uint32_t v4u_ __attribute__((ext_vector_type(4)));
@@ -1018,12 +948,6 @@ __device__ __forceinline__ void gate_compute(const ChainK& k, const uint8_t* gt,
   }
 }
 
-// 16 bytes from global memory at agent scope (a buffer load with the sc1 policy)
-__device__ __forceinline__ v4f ld4_rlx(const float* base, int idx) {
-  const __amdgpu_buffer_rsrc_t r =
-      __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(base), 0, 0x7fffffff, 0x00020000);
-  return __builtin_bit_cast(v4f, __builtin_amdgcn_raw_buffer_load_b128(r, idx * 4, 0, 16));
-}
 
 // A GDN event for layer L (the chain's side): publish the value heads' tasks (bit 0 the key
 // head's query or key is live, bit 2 the head decays), their decays and the layer's live

@@ -10,12 +10,18 @@
 // to bf16 once. The oracle restates exactly this order for dense matrices. The delta rule keeps
 // the stock decode's (ATen's 16-row cascade for the state's row sums), as the sparse paths do.
 // (Qwen3_5 decoder layer: transformers/models/qwen3_5/modeling_qwen3_5.py:168-545, :704-793.)
+//
+// Two drivers share the phase bodies below: lxm_dn_step (one step as five kernels per layer, for
+// a caller that captures it in a graph) and lxm_dn_run (n steps in one persistent launch: one
+// workgroup per CU, the phases separated by grid barriers; the vectors that cross workgroups
+// move through agent-scope loads and stores, and each wave requests its first weight rows of the
+// next phase before it waits).
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
-
 #include "../../include/lxm_dense.h"
 #include "lxm_math.h"
+#include "lxm_sync.h"
 
 using namespace lxm;
 
@@ -23,21 +29,77 @@ using namespace lxm;
 #define NW (NT / 64)
 #define KD 256
 #define VD 128
-typedef float v4f __attribute__((ext_vector_type(4)));
 typedef uint32_t v4u __attribute__((ext_vector_type(4)));
+
+// The thread index, opaque to the compiler: values computed from it stay where they are used
+// instead of being hoisted out of the persistent run's step and layer loops (where they would
+// hold registers across every phase).
+__device__ __forceinline__ int tid() {
+  int t = threadIdx.x;
+  asm volatile("" : "+v"(t));
+  return t;
+}
+// the wave's index in the workgroup, in a scalar register
+__device__ __forceinline__ int wave_id() { return __builtin_amdgcn_readfirstlane(tid() >> 6); }
+
+// Vector accesses: COH = the data crosses workgroups inside one launch (agent-scope, coherent
+// across the XCDs); otherwise plain (a kernel boundary orders them).
+template <bool COH>
+__device__ __forceinline__ float ldf(const float* p) {
+  if constexpr (COH) return ld_rlxf(p);
+  else return *p;
+}
+template <bool COH>
+__device__ __forceinline__ void stf(float* p, float v) {
+  if constexpr (COH) st_rlxf(p, v);
+  else *p = v;
+}
+// 16 bytes at base[idx] (base uniform over the wave)
+template <bool COH>
+__device__ __forceinline__ v4f ldf4(const float* base, int idx) {
+  if constexpr (COH) return ld4_rlx(wave_ptr(const_cast<float*>(base)), idx);
+  else return *reinterpret_cast<const v4f*>(base + idx);
+}
+// a channel's window (4 bf16 values, 8 bytes)
+template <bool COH>
+__device__ __forceinline__ uint64_t ldw(const uint16_t* w) {
+  if constexpr (COH) {
+    return __hip_atomic_load(gp(reinterpret_cast<const uint64_t*>(w)), __ATOMIC_RELAXED,
+                             __HIP_MEMORY_SCOPE_AGENT);
+  } else {
+    return *reinterpret_cast<const uint64_t*>(w);
+  }
+}
+template <bool COH>
+__device__ __forceinline__ void stw(uint16_t* w, uint64_t v) {
+  if constexpr (COH) {
+    __hip_atomic_store(gp(reinterpret_cast<uint64_t*>(w)), v, __ATOMIC_RELAXED,
+                       __HIP_MEMORY_SCOPE_AGENT);
+  } else {
+    *reinterpret_cast<uint64_t*>(w) = v;
+  }
+}
+// causal_conv1d_update's shift: [x(t-2), x(t-1), P] behind the oldest (tap k at bits 16k)
+__device__ __forceinline__ uint64_t shifted(uint64_t w, float p) {
+  return (w >> 16) | ((uint64_t)(fbits(p) >> 16) << 48);
+}
 
 // ---------------------------------------------------------------------------------------------
 // The 512-lane hidden sum of x * x over n <= 4096 values (thread t: its values 4t..4t+3, then
 // 2048+4t..2048+4t+3; waves at offsets 32..1; the 8 wave totals at offsets 4, 2, 1).
+template <bool COH>
 __device__ __forceinline__ float hidden_sum(const float* x, int n, float* wsum) {
-  const int t = threadIdx.x;
+  const int t = tid();
   float s = 0.0f;
 #pragma unroll
   for (int half = 0; half < 2; half++)
 #pragma unroll
     for (int i = 0; i < 4; i++) {
       const int c = half * 2048 + 4 * t + i;
-      if (c < n) s = acc<true>(s, x[c], x[c]);
+      if (c < n) {
+        const float v = ldf<COH>(x + c);
+        s = acc<true>(s, v, v);
+      }
     }
   s = wave_tree(s);
   if ((t & 63) == 0) wsum[t >> 6] = s;
@@ -45,6 +107,7 @@ __device__ __forceinline__ float hidden_sum(const float* x, int n, float* wsum) 
   float w[NW];
 #pragma unroll
   for (int i = 0; i < NW; i++) w[i] = wsum[i];
+  lds_barrier();  // (wsum is free again)
 #pragma unroll
   for (int off = NW / 2; off >= 1; off >>= 1)
 #pragma unroll
@@ -59,24 +122,25 @@ __global__ __launch_bounds__(NT) void dn_embed(const lxm_dn_params* __restrict__
   const int step = *p.step;
   int tok = step < p.n_forced ? p.forced[step] : *p.tok;
   if (tok < 0 || tok >= p.vocab) {
-    if (threadIdx.x == 0) *p.err = 1;
+    if (tid() == 0) *p.err = 1;
     tok = 0;
   }
   const uint16_t* e = p.embed + (int64_t)tok * p.hidden;
   const int G = p.hidden / 64;
-  for (int c = threadIdx.x; c < p.hidden; c += NT) {
+  for (int c = tid(); c < p.hidden; c += NT) {
     // entry c is lane c / G's entry c % G (interleaved in 8-entry chunks when G >= 8)
     const int l = c / G, k = c % G;
     const int at = G < 8 ? c : ((k >> 3) * 64 + l) * 8 + (k & 7);
     p.h[c] = bf16f(e[at]);
   }
-  if (threadIdx.x == 0) *p.keys = 0ull;
+  if (tid() == 0) *p.keys = 0ull;
 }
 
 // The RMSNorm factor r = rsqrt(mean(h^2) + eps) of TF:720-737, computed by every workgroup that
 // consumes the norm (the sum in the 512-lane order above); x[c] = D((h[c] * r) * (1 + w[c])).
+template <bool COH>
 __device__ __forceinline__ float norm_factor(const float* h, int H, float eps, float* wsum) {
-  return rsqrt_(hidden_sum(h, H, wsum) / (float)H + eps);
+  return rsqrt_(hidden_sum<COH>(h, H, wsum) / (float)H + eps);
 }
 __device__ __forceinline__ float norm_el(float h, float r, float w) {
   return bf16r((h * r) * (1.0f + w));
@@ -113,38 +177,67 @@ struct XRegs {
   static_assert(G % 4 == 0, "16-byte input loads");
   uint32_t v[G / 2 < 4 ? 4 : G / 2];
   // x[lane G .. lane G + G)
+  // (in pieces of 16 values: the unpacked floats would crowd out the weights in flight)
+  template <bool COH>
   __device__ __forceinline__ void load(const float* x, int lane) {
     if constexpr (G == 4) v[2] = v[3] = 0u;
-    const v4f* src = reinterpret_cast<const v4f*>(x + lane * G);
-    v4f a[G / 4];
+    constexpr int PC = G / 4 < 4 ? G / 4 : 4;
 #pragma unroll
-    for (int k = 0; k < G / 4; k++) a[k] = src[k];
+    for (int k0 = 0; k0 < G / 4; k0 += PC) {
+      v4f a[PC];
 #pragma unroll
-    for (int k = 0; k < G / 4; k++) {
-      v[2 * k] = pack2(a[k].x, a[k].y);
-      v[2 * k + 1] = pack2(a[k].z, a[k].w);
+      for (int k = 0; k < PC; k++) a[k] = ldf4<COH>(x, lane * G + 4 * (k0 + k));
+#pragma unroll
+      for (int k = 0; k < PC; k++) {
+        v[2 * (k0 + k)] = pack2(a[k].x, a[k].y);
+        v[2 * (k0 + k) + 1] = pack2(a[k].z, a[k].w);
+      }
+      __atomic_signal_fence(__ATOMIC_SEQ_CST);
     }
   }
-  // the norm's output over the lane's entries: D((h * r) * (1 + w))
+  // the norm's output over the lane's entries: D((h * r) * (1 + w)) (in pieces, as load)
+  template <bool COH>
   __device__ __forceinline__ void load_norm(const float* h, const float* nw, float r, int lane) {
     if constexpr (G == 4) v[2] = v[3] = 0u;
-    const v4f* hs = reinterpret_cast<const v4f*>(h + lane * G);
     const v4f* ws = reinterpret_cast<const v4f*>(nw + lane * G);
-    v4f a[G / 4], b[G / 4];
+    constexpr int PC = G / 4 < 4 ? G / 4 : 4;
 #pragma unroll
-    for (int k = 0; k < G / 4; k++) {
-      a[k] = hs[k];
-      b[k] = ws[k];
-    }
+    for (int k0 = 0; k0 < G / 4; k0 += PC) {
+      v4f a[PC], b[PC];
 #pragma unroll
-    for (int k = 0; k < G / 4; k++) {
-      v[2 * k] = pack2(norm_el(a[k].x, r, b[k].x), norm_el(a[k].y, r, b[k].y));
-      v[2 * k + 1] = pack2(norm_el(a[k].z, r, b[k].z), norm_el(a[k].w, r, b[k].w));
+      for (int k = 0; k < PC; k++) {
+        a[k] = ldf4<COH>(h, lane * G + 4 * (k0 + k));
+        b[k] = ws[k0 + k];
+      }
+#pragma unroll
+      for (int k = 0; k < PC; k++) {
+        v[2 * (k0 + k)] = pack2(norm_el(a[k].x, r, b[k].x), norm_el(a[k].y, r, b[k].y));
+        v[2 * (k0 + k) + 1] = pack2(norm_el(a[k].z, r, b[k].z), norm_el(a[k].w, r, b[k].w));
+      }
+      __atomic_signal_fence(__ATOMIC_SEQ_CST);
     }
   }
   __device__ __forceinline__ v4u chunk(int q) const {
     return v4u{v[4 * q], v[4 * q + 1], v[4 * q + 2], v[4 * q + 3]};
   }
+};
+// The same input staged in LDS in the weights' interleaved order (chunk q of lane l at q * 64 +
+// l), for the longest rows: the registers then hold the weights in flight instead.
+template <int G>
+struct XLds {
+  static_assert(G % 8 == 0, "16-byte chunks");
+  const v4u* xs;
+  int lane;
+  // every thread of the workgroup: x (64 G values) into xs
+  template <bool COH>
+  __device__ __forceinline__ static void stage(v4u* xs, const float* x) {
+    for (int c8 = tid(); c8 < 8 * G; c8 += blockDim.x) {
+      const int l = c8 / (G / 8), q = c8 % (G / 8);
+      const v4f a = ldf4<COH>(x, 8 * c8), b = ldf4<COH>(x, 8 * c8 + 4);
+      xs[q * 64 + l] = v4u{pack2(a.x, a.y), pack2(a.z, a.w), pack2(b.x, b.y), pack2(b.z, b.w)};
+    }
+  }
+  __device__ __forceinline__ v4u chunk(int q) const { return xs[q * 64 + lane]; }
 };
 // The lane's sum of its G entries, in order from +0 (bf16 x bf16 products are exact in fp32:
 // one fused op per term)
@@ -169,86 +262,59 @@ __device__ __forceinline__ float row_dot(const WRow<G>& r, const X& x) {
   return wave_tree(lane_dot<G>(r, x));
 }
 
-// Rows: out[r] = D(row . x) (MODE 0) or out[r] = D(out[r] + D(row . x)) (MODE 1, the residual).
-// XS 0: x from a vector; 1: x = the RMSNorm of h with weight nw (hidden H; every workgroup forms
-// it). NTB threads per workgroup. Each wave requests its first row before it forms x.
-template <int G, int MODE, int XS, int NTB>
-__global__ __launch_bounds__(NTB) void dn_rows(const uint16_t* __restrict__ W, int nrows,
-                                               const float* __restrict__ x,
-                                               const float* __restrict__ nw, float eps, int H,
-                                               float* out) {
-  static_assert(XS != 1 || NTB == NT, "the norm's 512-lane sum");
-  constexpr int NWB = NTB / 64;
-  const int lane = threadIdx.x & 63;
-  const int wv = blockIdx.x * NWB + (threadIdx.x >> 6), nwv = gridDim.x * NWB;
-  WRow<G> cur;
-  if (wv < nrows) cur.load(W, wv, lane);
-  XRegs<G> xc;
-  if constexpr (XS == 1) {
-    __shared__ float wsum[NW];
-    xc.load_norm(x, nw, norm_factor(x, H, eps, wsum), lane);
-  } else {
-    xc.load(x, lane);
-  }
-  for (int r = wv; r < nrows; r += nwv) {
-    if (r != wv) cur.load(W, r, lane);
-    const float s = row_dot<G>(cur, xc);
+// A wave's rows: w0, then in round j >= 1 row j nw + (w0 + rot) % nw (rot 0: w0 + j nw), so a
+// phase's rows past the first nw go to the waves rot places on (cur holds row w0, requested
+// earlier). MODE 0 out[r] = D(row . x); MODE 1 out[r] = D(out[r] + D(row . x)) (the residual).
+__device__ __forceinline__ int round_row(int w0, int j, int nw, int rot) {
+  return j == 0 ? w0 : j * nw + (w0 + rot) % nw;
+}
+template <int G, int MODE, bool COH, class X>
+__device__ __forceinline__ void rows_run(const uint16_t* W, int nrows, const X& xc, WRow<G>& cur,
+                                         int w0, int nw, float* out, int rot = 0) {
+  const int lane = tid() & 63;
+  for (int j = 0;; j++) {
+    const int r = round_row(w0, j, nw, rot);
+    if (r >= nrows) break;
+    if (j) cur.load(W, r, lane);
+    const float s = row_dot<G, X>(cur, xc);
     if (lane == 0) {
-      if constexpr (MODE == 0) out[r] = bf16r(s);
-      else out[r] = bf16r(out[r] + bf16r(s));
+      if constexpr (MODE == 0) stf<COH>(out + r, bf16r(s));
+      else stf<COH>(out + r, bf16r(ldf<COH>(out + r) + bf16r(s)));
     }
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);  // (the next row's loads stay after this one's sums)
   }
 }
-
-// SwiGLU over the post norm of h: unit u's gate and up rows, act[u] = D(D(silu(D(g))) * D(u))
-// (TF:704-717)
-template <int G>
-__global__ __launch_bounds__(NT) void dn_units(const uint16_t* __restrict__ Wg,
-                                               const uint16_t* __restrict__ Wu, int nunits,
-                                               const float* __restrict__ h,
-                                               const float* __restrict__ nw, float eps, int H,
-                                               float* act) {
-  __shared__ float wsum[NW];
-  const int lane = threadIdx.x & 63;
-  const int wv = blockIdx.x * NW + (threadIdx.x >> 6), nwv = gridDim.x * NW;
-  WRow<G> cg, cu;
-  if (wv < nunits) {
-    cg.load(Wg, wv, lane);
-    cu.load(Wu, wv, lane);
-  }
-  XRegs<G> xc;
-  xc.load_norm(h, nw, norm_factor(h, H, eps, wsum), lane);
-  for (int u = wv; u < nunits; u += nwv) {
-    if (u != wv) {
+// SwiGLU units, dealt as rows_run deals rows (cg / cu hold unit w0's gate and up rows): act[u]
+// = D(D(silu(D(g))) * D(u)) (TF:704-717)
+template <int G, bool COH>
+__device__ __forceinline__ void units_run(const uint16_t* Wg, const uint16_t* Wu, int nunits,
+                                          const XRegs<G>& xc, WRow<G>& cg, WRow<G>& cu, int w0,
+                                          int nw, float* act, int rot = 0) {
+  const int lane = tid() & 63;
+  for (int j = 0;; j++) {
+    const int u = round_row(w0, j, nw, rot);
+    if (u >= nunits) break;
+    if (j) {
       cg.load(Wg, u, lane);
       cu.load(Wu, u, lane);
     }
     const float g = row_dot<G>(cg, xc);
     const float v = row_dot<G>(cu, xc);
-    if (lane == 0) act[u] = bf16r(silu_bf16(bf16r(g)) * bf16r(v));
+    if (lane == 0) stf<COH>(act + u, bf16r(silu_bf16(bf16r(g)) * bf16r(v)));
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
   }
 }
-
-// The head over the final norm of h: logits D(row . x) over the vocabulary, the first maximum
-// (ties to the lower index, NaN above everything: torch.argmax) folded into *keys by 64-bit
-// atomic max. Each wave takes rows in ascending order and keeps its first strict maximum (and
-// its first NaN apart).
+// The head's rows r = w0, w0 + nw, ...: logits D(row . x), the wave's first maximum (ties to the
+// lower index, NaN above everything: torch.argmax) folded into *keys by 64-bit atomic max. Each
+// wave takes rows in ascending order and keeps its first strict maximum (and its first NaN apart).
 template <int G>
-__global__ __launch_bounds__(NT) void dn_head(const uint16_t* __restrict__ W, int nrows,
-                                              const float* __restrict__ h,
-                                              const float* __restrict__ nw, float eps, int H,
-                                              unsigned long long* keys) {
-  __shared__ float wsum[NW];
-  const int lane = threadIdx.x & 63;
-  const int wv = blockIdx.x * NW + (threadIdx.x >> 6), nwv = gridDim.x * NW;
-  WRow<G> cur;
-  if (wv < nrows) cur.load(W, wv, lane);
-  XRegs<G> xc;
-  xc.load_norm(h, nw, norm_factor(h, H, eps, wsum), lane);
+__device__ __forceinline__ void head_run(const uint16_t* W, int nrows, const XRegs<G>& xc,
+                                         WRow<G>& cur, int w0, int nw, unsigned long long* keys) {
+  const int lane = tid() & 63;
   float best = 0.0f;
   int bidx = -1, nanr = -1;
-  for (int r = wv; r < nrows; r += nwv) {
-    if (r != wv) cur.load(W, r, lane);
+  for (int r = w0; r < nrows; r += nw) {
+    if (r != w0) cur.load(W, r, lane);
     const float v = bf16r(row_dot<G>(cur, xc));
     if (v != v) {
       if (nanr < 0) nanr = r;
@@ -256,6 +322,7 @@ __global__ __launch_bounds__(NT) void dn_head(const uint16_t* __restrict__ W, in
       best = v;
       bidx = r;
     }
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
   }
   if (lane == 0) {
     unsigned long long k = bidx < 0 ? 0ull : argmax_key(best, bidx);
@@ -267,10 +334,70 @@ __global__ __launch_bounds__(NT) void dn_head(const uint16_t* __restrict__ W, in
   }
 }
 
+// Rows: out[r] = D(row . x) (MODE 0) or out[r] = D(out[r] + D(row . x)) (MODE 1, the residual).
+// XS 0: x from a vector; 1: x = the RMSNorm of h with weight nw (hidden H; every workgroup forms
+// it). NTB threads per workgroup. Each wave requests its first row before it forms x.
+template <int G, int MODE, int XS, int NTB>
+__global__ __launch_bounds__(NTB) void dn_rows(const uint16_t* __restrict__ W, int nrows,
+                                               const float* __restrict__ x,
+                                               const float* __restrict__ nw, float eps, int H,
+                                               float* out) {
+  static_assert(XS != 1 || NTB == NT, "the norm's 512-lane sum");
+  constexpr int NWB = NTB / 64;
+  const int lane = tid() & 63;
+  const int wv = blockIdx.x * NWB + (tid() >> 6), nwv = gridDim.x * NWB;
+  WRow<G> cur;
+  if (wv < nrows) cur.load(W, wv, lane);
+  XRegs<G> xc;
+  if constexpr (XS == 1) {
+    __shared__ float wsum[NW];
+    xc.template load_norm<false>(x, nw, norm_factor<false>(x, H, eps, wsum), lane);
+  } else {
+    xc.template load<false>(x, lane);
+  }
+  rows_run<G, MODE, false>(W, nrows, xc, cur, wv, nwv, out);
+}
+
+// SwiGLU over the post norm of h
+template <int G>
+__global__ __launch_bounds__(NT) void dn_units(const uint16_t* __restrict__ Wg,
+                                               const uint16_t* __restrict__ Wu, int nunits,
+                                               const float* __restrict__ h,
+                                               const float* __restrict__ nw, float eps, int H,
+                                               float* act) {
+  __shared__ float wsum[NW];
+  const int lane = tid() & 63;
+  const int wv = blockIdx.x * NW + (tid() >> 6), nwv = gridDim.x * NW;
+  WRow<G> cg, cu;
+  if (wv < nunits) {
+    cg.load(Wg, wv, lane);
+    cu.load(Wu, wv, lane);
+  }
+  XRegs<G> xc;
+  xc.template load_norm<false>(h, nw, norm_factor<false>(h, H, eps, wsum), lane);
+  units_run<G, false>(Wg, Wu, nunits, xc, cg, cu, wv, nwv, act);
+}
+
+// The head over the final norm of h
+template <int G>
+__global__ __launch_bounds__(NT) void dn_head(const uint16_t* __restrict__ W, int nrows,
+                                              const float* __restrict__ h,
+                                              const float* __restrict__ nw, float eps, int H,
+                                              unsigned long long* keys) {
+  __shared__ float wsum[NW];
+  const int lane = tid() & 63;
+  const int wv = blockIdx.x * NW + (tid() >> 6), nwv = gridDim.x * NW;
+  WRow<G> cur;
+  if (wv < nrows) cur.load(W, wv, lane);
+  XRegs<G> xc;
+  xc.template load_norm<false>(h, nw, norm_factor<false>(h, H, eps, wsum), lane);
+  head_run<G>(W, nrows, xc, cur, wv, nwv, keys);
+}
+
 // the prediction, fed back; the step advanced
 __global__ void dn_next(const lxm_dn_params* __restrict__ pp) {
   const lxm_dn_params& p = *pp;
-  if (threadIdx.x == 0) {
+  if (tid() == 0) {
     const int step = *p.step;
     const int pred = argmax_idx(*p.keys);
     if (step < p.n_steps) p.preds[step] = pred;
@@ -287,7 +414,7 @@ __global__ void dn_next(const lxm_dn_params* __restrict__ pp) {
 // g = -exp(A_log) softplus(a + dt_bias) (:497-499), the recurrent step (TF:330-380) on its
 // 256 x 32 tile in registers (thread = one column of one of ATen's 16-row cascade blocks), and
 // o = D(S^T q) into on (0 for a head without a live query or key: the oracle's proc 1). The
-// gated norm and the query/key windows' shift belong to the out_proj kernel.
+// gated norm and the query/key windows' shift belong to the out_proj phase.
 #define QC 4
 #define QW (VD / QC)
 static_assert(NT == 16 * QW && NT >= KD + QW, "dn_gdn: one thread per (16-row block, column)");
@@ -302,66 +429,73 @@ struct DnGdn {
   float* on;
   int nk, kl, rl, R;
 };
-__device__ __forceinline__ float conv_y(const uint16_t* cs, int64_t chan, const uint16_t* taps, float P) {
+struct GdnLds {
+  float qd[KD], kd[KD], qn[KD], kn[KD], vb[QW], dl[QW], bs[16 * QW];
+  float misc[4];
+};
+__device__ __forceinline__ float conv_y(uint64_t win, const uint16_t* taps, float P) {
   float y = 0.0f;
 #pragma unroll
   for (int k = 0; k < 4; k++) {
-    const float x = k < 3 ? bf16f(cs[chan * 4 + k + 1]) : P;
+    const float x = k < 3 ? bf16f((uint32_t)(win >> (16 * (k + 1))) & 0xffffu) : P;
     y = __builtin_fmaf(bf16f(taps[k]), x, y);
   }
   return silu_bf16(bf16r(y));
 }
-__global__ __launch_bounds__(NT) void dn_gdn(DnGdn g) {
-  __shared__ __align__(16) float qd[KD], kd_[KD], qn[KD], kn[KD], vb[QW], dl[QW];
-  __shared__ __align__(16) float bs[16 * QW];
-  __shared__ float misc[4];
-  const int t = threadIdx.x, lane = t & 63, wv = t >> 6;
+// the thread's 16 state values: column c0 + t % 32 of rows 16 (t / 32) .. + 15 of value head vh
+__device__ __forceinline__ float* gdn_tile(const DnGdn& g, int blk) {
+  const int t = tid(), vslot = blk / QC, c0 = (blk % QC) * QW;
+  const int vh = (vslot / g.rl) * g.R + vslot % g.rl;
+  return g.rec + (size_t)vh * KD * VD + c0 + t % QW + (t / QW) * 16 * VD;
+}
+template <bool COH>
+__device__ __forceinline__ void gdn_load(const DnGdn& g, int blk, float (&s)[16]) {
+  const float* S = gdn_tile(g, blk);
+#pragma unroll
+  for (int i = 0; i < 16; i++) s[i] = ldf<COH>(S + i * VD);
+}
+template <bool COH>
+__device__ __forceinline__ void gdn_body(const DnGdn& g, int blk, float (&s)[16], GdnLds& l) {
+  const int t = tid(), lane = t & 63, wv = t >> 6;
   const int nk = g.nk, kl = g.kl, rl = g.rl;
-  const int vslot = blockIdx.x / QC, c0 = (blockIdx.x % QC) * QW;
+  const int vslot = blk / QC, c0 = (blk % QC) * QW;
   const int kh = vslot / rl, vh = kh * g.R + vslot % rl;
   const int nq = nk * kl, nvr = nk * rl * VD;
   const float* P = g.P;
-  // the state tile first (its loads overlap the inputs' work below): column c0 + c of rows
-  // 16 rb .. 16 rb + 15
   const int c = t % QW, rb = t / QW;
-  float* S = g.rec + (size_t)vh * KD * VD + c0 + c;
-  float s[16];
-#pragma unroll
-  for (int i = 0; i < 16; i++) s[i] = S[(rb * 16 + i) * VD];
   // rows of P: q [0, nq), k [nq, 2nq), v [2nq, 2nq + nvr), z [.., + nvr), b [.., + nk rl), a
   if (t < KD) {
     float q = 0.0f, k = 0.0f;
     if (t < kl) {
       const int64_t cq = (int64_t)kh * KD + t, ck = (int64_t)nk * KD + kh * KD + t;
-      q = conv_y(g.conv, cq, g.conv_qk + ((int64_t)kh * kl + t) * 4, P[kh * kl + t]);
-      k = conv_y(g.conv, ck, g.conv_qk + ((int64_t)(nk + kh) * kl + t) * 4, P[nq + kh * kl + t]);
+      q = conv_y(ldw<COH>(g.conv + cq * 4), g.conv_qk + ((int64_t)kh * kl + t) * 4,
+                 ldf<COH>(P + kh * kl + t));
+      k = conv_y(ldw<COH>(g.conv + ck * 4), g.conv_qk + ((int64_t)(nk + kh) * kl + t) * 4,
+                 ldf<COH>(P + nq + kh * kl + t));
     }
-    qd[t] = q;
-    kd_[t] = k;
+    l.qd[t] = q;
+    l.kd[t] = k;
   } else if (t < KD + QW) {
     // the workgroup's value channels: no other workgroup reads their windows, so they advance
-    // here (causal_conv1d_update's shift: [x(t-2), x(t-1), P] behind the oldest)
+    // here (causal_conv1d_update's shift)
     const int d = c0 + t - KD;
-    const int64_t ch = 2 * (int64_t)nk * KD + (int64_t)vh * VD + d;
-    const float pv = P[2 * nq + vslot * VD + d];
-    vb[t - KD] = conv_y(g.conv, ch, g.conv_v + ((int64_t)vslot * VD + d) * 4, pv);
-    uint16_t* w = g.conv + ch * 4;
-    const uint16_t w1 = w[1], w2 = w[2], w3 = w[3];
-    w[0] = w1;
-    w[1] = w2;
-    w[2] = w3;
-    w[3] = (uint16_t)(fbits(pv) >> 16);
+    uint16_t* w = g.conv + (2 * (int64_t)nk * KD + (int64_t)vh * VD + d) * 4;
+    const float pv = ldf<COH>(P + 2 * nq + vslot * VD + d);
+    const uint64_t win = ldw<COH>(w);
+    l.vb[t - KD] = conv_y(win, g.conv_v + ((int64_t)vslot * VD + d) * 4, pv);
+    stw<COH>(w, shifted(win, pv));
   }
   if (t == 0) {
-    const float b = P[2 * nq + 2 * nvr + vslot], a = P[2 * nq + 2 * nvr + nk * rl + vslot];
-    misc[0] = bf16r(sigmoid(b));
-    misc[1] = cr_exp((-cr_exp(g.A_log[vh])) * softplus(a + g.dt_bias[vh]));
+    const float b = ldf<COH>(P + 2 * nq + 2 * nvr + vslot);
+    const float a = ldf<COH>(P + 2 * nq + 2 * nvr + nk * rl + vslot);
+    l.misc[0] = bf16r(sigmoid(b));
+    l.misc[1] = cr_exp((-cr_exp(g.A_log[vh])) * softplus(a + g.dt_bias[vh]));
   }
-  __syncthreads();
+  lds_barrier();
   // l2norm of the query (wave 0) and key (wave 1) in the model dtype; live: any nonzero
   if (wv < 2) {
-    const float* x = wv ? kd_ : qd;
-    float* o = wv ? kn : qn;
+    const float* x = wv ? l.kd : l.qd;
+    float* o = wv ? l.kn : l.qn;
     float xs[4], ss = 0.0f;
     bool nz = false;
 #pragma unroll
@@ -370,7 +504,7 @@ __global__ __launch_bounds__(NT) void dn_gdn(DnGdn g) {
       nz |= xs[i] != 0.0f;
       ss = ss + bf16r(xs[i] * xs[i]);
     }
-    if (lane == 0) misc[2 + wv] = __ballot(nz) != 0ull ? 1.0f : 0.0f;
+    if (lane == 0) l.misc[2 + wv] = __ballot(nz) != 0ull ? 1.0f : 0.0f;
     ss = bf16r(sum64(ss));
     const float inv = bf16r(rsqrt_(bf16r(ss + 1e-6f)));
 #pragma unroll
@@ -380,35 +514,31 @@ __global__ __launch_bounds__(NT) void dn_gdn(DnGdn g) {
       o[lane + 64 * i] = v;
     }
   }
-  __syncthreads();
-  const float beta = misc[0], e = misc[1];
-  const bool live = misc[2] != 0.0f || misc[3] != 0.0f;
+  lds_barrier();
+  const float beta = l.misc[0], e = l.misc[1];
+  const bool live = l.misc[2] != 0.0f || l.misc[3] != 0.0f;
   if (e != 1.0f) {
 #pragma unroll
     for (int i = 0; i < 16; i++) s[i] = s[i] * e;
   }
   float* o_out = g.on + vslot * VD + c0;
   if (live) {
-    float kr[16], qr[16];
-#pragma unroll
-    for (int i = 0; i < 16; i++) {
-      kr[i] = kn[rb * 16 + i];
-      qr[i] = qn[rb * 16 + i];
-    }
+    const float* kr = l.kn + rb * 16;
+    const float* qr = l.qn + rb * 16;
     // kv = S^T k: the block's rows in order (a zero factor adds nothing), then the 16 blocks
     float a = 0.0f;
 #pragma unroll
     for (int i = 0; i < 16; i++) a = kr[i] != 0.0f ? a + s[i] * kr[i] : a;
-    bs[rb * QW + c] = a;
-    __syncthreads();
+    l.bs[rb * QW + c] = a;
+    lds_barrier();
     if (t < QW) {
       float kv = 0.0f;
 #pragma unroll
-      for (int q = 0; q < 16; q++) kv = kv + bs[q * QW + t];
-      dl[t] = (vb[t] - kv) * beta;
+      for (int q = 0; q < 16; q++) kv = kv + l.bs[q * QW + t];
+      l.dl[t] = (l.vb[t] - kv) * beta;
     }
-    __syncthreads();
-    const float d = dl[c];
+    lds_barrier();
+    const float d = l.dl[c];
     float o = 0.0f;
 #pragma unroll
     for (int i = 0; i < 16; i++) {
@@ -416,19 +546,27 @@ __global__ __launch_bounds__(NT) void dn_gdn(DnGdn g) {
       s[i] = kr[i] != 0.0f ? s[i] + kr[i] * d : s[i];
       o = qr[i] != 0.0f ? o + s[i] * qr[i] : o;
     }
-    bs[rb * QW + c] = o;
-    __syncthreads();
+    l.bs[rb * QW + c] = o;
+    lds_barrier();
     if (t < QW) {
       float q = 0.0f;
 #pragma unroll
-      for (int b = 0; b < 16; b++) q = q + bs[b * QW + t];
-      o_out[t] = bf16r(q);
+      for (int b = 0; b < 16; b++) q = q + l.bs[b * QW + t];
+      stf<COH>(o_out + t, bf16r(q));
     }
   } else if (t < QW) {
-    o_out[t] = 0.0f;
+    stf<COH>(o_out + t, 0.0f);
   }
+  float* S = gdn_tile(g, blk);
 #pragma unroll
-  for (int i = 0; i < 16; i++) S[(rb * 16 + i) * VD] = s[i];
+  for (int i = 0; i < 16; i++) stf<COH>(S + i * VD, s[i]);
+  lds_barrier();  // (the scratch is free for the next use)
+}
+__global__ __launch_bounds__(NT) void dn_gdn(DnGdn g) {
+  __shared__ GdnLds l;
+  float s[16];
+  gdn_load<false>(g, blockIdx.x, s);  // the state tile first: its loads overlap the inputs' work
+  gdn_body<false>(g, blockIdx.x, s, l);
 }
 
 // ---------------------------------------------------------------------------------------------
@@ -437,7 +575,7 @@ __global__ __launch_bounds__(NT) void dn_gdn(DnGdn g) {
 // squares summed per lane over dims lane, lane + 64 and then by the pairwise tree; one wave per
 // head) into LDS, then h[r] = D(h[r] + D(row . y)) for its rows. Then the workgroups advance the
 // windows of the live query/key channels (every key head's live dims), which the delta rule has
-// read (causal_conv1d_update's shift: [x(t-2), x(t-1), P] behind the oldest).
+// read (causal_conv1d_update's shift).
 struct DnOut {
   const uint16_t* W;  // (hidden, nh x 128), interleaved
   int nrows, nh;
@@ -450,15 +588,10 @@ struct DnOut {
   const float* P;
   int nk, kl;
 };
-template <int G, int NTB>
-__global__ __launch_bounds__(NTB) void dn_out(DnOut a) {
-  static_assert(G * 64 <= 4096, "dn_out: at most 32 value heads");
-  constexpr int NWB = NTB / 64;
-  __shared__ __align__(16) float ys[G * 64];
-  const int t = threadIdx.x, lane = t & 63, wvl = t >> 6;
-  const int wv = blockIdx.x * NWB + wvl, nwv = gridDim.x * NWB;
-  WRow<G> cur;
-  if (wv < a.nrows) cur.load(a.W, wv, lane);
+// the gated norm of every live head into ys (nh x 128), the NWB waves taking heads in turn
+template <int NWB, bool COH>
+__device__ __forceinline__ void gated_norm(const DnOut& a, float* ys) {
+  const int lane = tid() & 63, wvl = tid() >> 6;
   // the wave's heads wvl, wvl + NWB, ...: every input requested first, then the norms
   constexpr int HPW = (4096 / VD + NWB - 1) / NWB;
   const float g0 = a.gw[lane], g1 = a.gw[lane + 64];
@@ -467,10 +600,10 @@ __global__ __launch_bounds__(NTB) void dn_out(DnOut a) {
   for (int j = 0; j < HPW; j++) {
     const int hh = wvl + j * NWB;
     if (hh < a.nh) {
-      o[j][0] = a.on[hh * VD + lane];
-      o[j][1] = a.on[hh * VD + lane + 64];
-      z[j][0] = a.z[hh * VD + lane];
-      z[j][1] = a.z[hh * VD + lane + 64];
+      o[j][0] = ldf<COH>(a.on + hh * VD + lane);
+      o[j][1] = ldf<COH>(a.on + hh * VD + lane + 64);
+      z[j][0] = ldf<COH>(a.z + hh * VD + lane);
+      z[j][1] = ldf<COH>(a.z + hh * VD + lane + 64);
     }
   }
 #pragma unroll
@@ -486,25 +619,228 @@ __global__ __launch_bounds__(NTB) void dn_out(DnOut a) {
       ys[hh * VD + lane + 64] = bf16r(bf16r(g1 * bf16r(o[j][1] * rr)) * silu(z[j][1]));
     }
   }
-  lds_barrier();
-  XRegs<G> xc;
-  xc.load(ys, lane);
-  for (int r = wv; r < a.nrows; r += nwv) {
-    if (r != wv) cur.load(a.W, r, lane);
-    const float s = row_dot<G>(cur, xc);
-    if (lane == 0) a.h[r] = bf16r(a.h[r] + bf16r(s));
-  }
-  // the query/key windows, spread over the workgroups (channel i: workgroup i % grid)
+}
+// the query/key windows, spread over the workgroups (channel i: workgroup i % nblk)
+template <bool COH>
+__device__ __forceinline__ void qk_windows(const DnOut& a, int blk, int nblk, int ntb) {
   const int nq = a.nk * a.kl;
-  for (int i = blockIdx.x + gridDim.x * t; i < 2 * nq; i += gridDim.x * NTB) {
+  for (int i = blk + nblk * tid(); i < 2 * nq; i += nblk * ntb) {
     const int part = i / nq, j = i % nq, kh = j / a.kl, d = j % a.kl;
     uint16_t* w = a.conv + ((int64_t)part * a.nk * KD + kh * KD + d) * 4;
-    const uint16_t w1 = w[1], w2 = w[2], w3 = w[3];
-    w[0] = w1;
-    w[1] = w2;
-    w[2] = w3;
-    w[3] = (uint16_t)(fbits(a.P[i]) >> 16);
+    stw<COH>(w, shifted(ldw<COH>(w), ldf<COH>(a.P + i)));
   }
+}
+template <int G, int NTB>
+__global__ __launch_bounds__(NTB) void dn_out(DnOut a) {
+  static_assert(G * 64 <= 4096, "dn_out: at most 32 value heads");
+  constexpr int NWB = NTB / 64;
+  __shared__ __align__(16) float ys[G * 64];
+  const int lane = tid() & 63;
+  const int wv = blockIdx.x * NWB + (tid() >> 6), nwv = gridDim.x * NWB;
+  WRow<G> cur;
+  if (wv < a.nrows) cur.load(a.W, wv, lane);
+  gated_norm<NWB, false>(a, ys);
+  lds_barrier();
+  XRegs<G> xc;
+  xc.template load<false>(ys, lane);
+  rows_run<G, 1, false>(a.W, a.nrows, xc, cur, wv, nwv, a.h);
+  qk_windows<false>(a, blockIdx.x, gridDim.x, NTB);
+}
+
+// ---------------------------------------------------------------------------------------------
+// The persistent run: n steps in one launch of one workgroup per CU. Per step: the embedding,
+// per layer five phases (projections over the input norm; the delta rule in nk x rl x QC
+// workgroups; the gated norm, out_proj and the query/key windows; SwiGLU over the post norm;
+// down_proj), the head over the final norm, then every workgroup reads the argmax key. A phase
+// ends at a grid barrier: each wave drains its stores (agent-scope, coherent across the XCDs),
+// the workgroup arrives on a monotone counter, requests its waves' first rows of the next phase,
+// and waits for the count (a wave past a phase's last row requests the last row, unused). The
+// rows past the first round go where the previous phase left the least work: out_proj's to the
+// upper half of the waves (the lower half ran the delta rule), SwiGLU's to the lower half,
+// down_proj's to the upper half, the projections' to the lower half. The
+// head's keys alternate between two slots by step parity (the other slot is cleared for the next
+// step). Every wait gives up after 3 s with the error word set (code 2), and so do the other
+// workgroups on seeing it.
+// The counter has 8 copies 128 bytes apart (workgroup b adds to copy b % 8, the XCD it lands on
+// when workgroups are dealt round-robin), so at most 32 workgroups' atomics meet on one line; a
+// waiter polls the sum. (One shared counter measured 3.9 us per barrier of 256 workgroups on
+// MI355X, eight copies 1.6 us.)
+#define BAR_COPIES 8
+struct Bar {
+  uint32_t* ctr;
+  int32_t* err;
+  uint32_t target;
+  int nblk;
+  int* flag;  // LDS
+  __device__ __forceinline__ void arrive() {
+    drain();
+    lds_barrier();
+    target += (uint32_t)nblk;
+    if (tid() == 0) add_rlx(ctr + 32 * (blockIdx.x % BAR_COPIES), 1u);
+  }
+  __device__ __forceinline__ bool wait() {
+    if (tid() == 0) {
+      const uint64_t t0 = wall();
+      int ok = 1;
+      for (;;) {
+        uint32_t v[BAR_COPIES], sum = 0;
+#pragma unroll
+        for (int g = 0; g < BAR_COPIES; g++) v[g] = ld_rlx(ctr + 32 * g);
+#pragma unroll
+        for (int g = 0; g < BAR_COPIES; g++) sum += v[g];
+        if ((int32_t)(sum - target) >= 0) break;
+        __builtin_amdgcn_s_sleep(1);
+        if (__hip_atomic_load(gp(err), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) {
+          ok = 0;
+          break;
+        }
+        if (wall() - t0 > TIMEOUT_TICKS) {
+          __hip_atomic_fetch_max(gp(err), 2, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          ok = 0;
+          break;
+        }
+      }
+      *flag = ok;
+    }
+    lds_barrier();
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    const bool ok = *flag != 0;
+    lds_barrier();  // (flag is free again)
+    return ok;
+  }
+};
+
+template <int GH, int GV, int GI>
+__global__ __launch_bounds__(NT, 1) void dn_run(const lxm_dn_params* __restrict__ pp, int n_run) {
+  static_assert(GV * 64 <= 4096, "at most 32 live value heads");
+  __shared__ float wsum[NW];
+  __shared__ __align__(16) float ys[GV * 64];
+  __shared__ GdnLds gl;
+  __shared__ v4u xd[8 * GI];
+  __shared__ int flag;
+  const lxm_dn_params& p = *pp;  // (scalar loads: the block never changes)
+  // (the thread's LANE and the wave's global index come from tid() at each use: see tid())
+  const int b = blockIdx.x, nb = gridDim.x, nwv = nb * NW;
+#define LANE (tid() & 63)
+#define GW (b * NW + wave_id())
+  const int H = p.hidden, I = p.inter, nk = p.nk, kl = p.kl, rl = p.rl, R = p.nv / nk;
+  const int nq = nk * kl, nvr = nk * rl * VD, nproj = 2 * nq + 2 * nvr + 2 * nk * rl;
+  const int ngdn = nk * rl * QC;
+  const float eps = p.rms_eps;
+  float* const act = p.xn + H;
+  Bar bar{p.sync, p.err, 0u, nb, &flag};
+  const int step0 = *p.step;
+  int tok = *p.tok;
+  for (int si = 0; si < n_run; si++) {
+    const int step = step0 + si;
+    // the input and its embedding row into h
+    if (step < p.n_forced) tok = p.forced[step];
+    if (tok < 0 || tok >= p.vocab) {
+      if (b == 0 && tid() == 0)
+        __hip_atomic_fetch_max(gp(p.err), 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      tok = 0;
+    }
+    {
+      const uint16_t* e = p.embed + (int64_t)tok * H;
+      for (int c = b * NT + tid(); c < H; c += nb * NT) {
+        const int l = c / GH, k = c % GH;
+        const int at = GH < 8 ? c : ((k >> 3) * 64 + l) * 8 + (k & 7);
+        stf<true>(p.h + c, bf16f(e[at]));
+      }
+    }
+    bar.arrive();
+    WRow<GH> rp;
+    rp.load(p.layers[0].proj, min(GW, nproj - 1), LANE);
+    if (!bar.wait()) return;
+    for (int L = 0; L < p.n_layers; L++) {
+      const lxm_dn_layer& ly = p.layers[L];
+      const DnGdn g{ly.conv_qk, ly.conv_v, ly.A_log, ly.dt_bias, ly.rec, ly.conv, p.P, p.on,
+                    nk, kl, rl, R};
+      const DnOut o{ly.out, H, nk * rl, p.on, p.P + 2 * nq + nvr, ly.gnorm, p.geps, p.h,
+                    ly.conv, p.P, nk, kl};
+      // projections over the input norm
+      {
+        XRegs<GH> xc;
+        xc.template load_norm<true>(p.h, ly.ln_in, norm_factor<true>(p.h, H, eps, wsum), LANE);
+        rows_run<GH, 0, true>(ly.proj, nproj, xc, rp, GW, nwv, p.P, 0);
+      }
+      bar.arrive();
+      // the delta rule; the other workgroups request their first out_proj rows meanwhile (two
+      // paths, so the rows' registers are not held across the delta rule)
+      WRow<GV> ro;
+      if (b < ngdn) {
+        float s[16];
+        gdn_load<true>(g, b, s);
+        if (!bar.wait()) return;
+        gdn_body<true>(g, b, s, gl);
+        bar.arrive();
+        ro.load(ly.out, min(GW, H - 1), LANE);
+        if (!bar.wait()) return;
+      } else {
+        ro.load(ly.out, min(GW, H - 1), LANE);
+        if (!bar.wait()) return;
+        bar.arrive();
+        if (!bar.wait()) return;
+      }
+      // the gated norm, out_proj, the query/key windows
+      {
+        gated_norm<NW, true>(o, ys);
+        lds_barrier();
+        XRegs<GV> xc;
+        xc.template load<false>(ys, LANE);
+        rows_run<GV, 1, true>(ly.out, H, xc, ro, GW, nwv, p.h, nwv / 2);
+        qk_windows<true>(o, b, nb, NT);
+      }
+      bar.arrive();
+      WRow<GH> ug, uu;
+      ug.load(ly.gate, min(GW, I - 1), LANE);
+      uu.load(ly.up, min(GW, I - 1), LANE);
+      if (!bar.wait()) return;
+      // SwiGLU over the post norm
+      {
+        XRegs<GH> xc;
+        xc.template load_norm<true>(p.h, ly.ln_post, norm_factor<true>(p.h, H, eps, wsum), LANE);
+        units_run<GH, true>(ly.gate, ly.up, I, xc, ug, uu, GW, nwv, act, 0);
+      }
+      bar.arrive();
+      WRow<GI> rdn;
+      rdn.load(ly.down, min(GW, H - 1), LANE);
+      if (!bar.wait()) return;
+      // down_proj (its input staged in LDS)
+      {
+        XLds<GI>::template stage<true>(xd, act);
+        lds_barrier();
+        const XLds<GI> xc{xd, LANE};
+        rows_run<GI, 1, true>(ly.down, H, xc, rdn, GW, nwv, p.h, nwv / 2);
+        lds_barrier();  // (xd is free again)
+      }
+      bar.arrive();
+      if (L + 1 < p.n_layers) rp.load(p.layers[L + 1].proj, min(GW, nproj - 1), LANE);
+      else rp.load(p.embed, min(GW, p.vocab - 1), LANE);
+      if (!bar.wait()) return;
+    }
+    // the head over the final norm; the argmax key of this step's parity
+    unsigned long long* key = p.keys + (step & 1);
+    {
+      XRegs<GH> xc;
+      xc.template load_norm<true>(p.h, p.w_final, norm_factor<true>(p.h, H, eps, wsum), LANE);
+      head_run<GH>(p.embed, p.vocab, xc, rp, GW, nwv, key);
+    }
+    bar.arrive();
+    if (!bar.wait()) return;
+    tok = argmax_idx(__hip_atomic_load(gp(key), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+    if (b == 0 && tid() == 0) {
+      if (step < p.n_steps) p.preds[step] = tok;
+      __hip_atomic_store(gp(p.keys + ((step + 1) & 1)), 0ull, __ATOMIC_RELAXED,
+                         __HIP_MEMORY_SCOPE_AGENT);
+    }
+  }
+  if (b == 0 && tid() == 0) {
+    *p.step = step0 + n_run;
+    *p.tok = tok;
+  }
+#undef LANE
+#undef GW
 }
 
 // ---------------------------------------------------------------------------------------------
@@ -537,7 +873,7 @@ static void launch_rows(const uint16_t* W, int nrows, const float* x, const floa
   hipLaunchKernelGGL((dn_rows<G, MODE, XS, NTB>), dim3(grid_for(nrows, NTB, NTB == NTL ? CAP_L : CAP_W)),
                      dim3(NTB), 0, st, W, nrows, x, nw, eps, H, out);
 }
-// the residual's rows: x from a vector (in LDS for the longest rows)
+// the residual's rows: x from a vector
 static bool res_rows(int K, const uint16_t* W, int nrows, const float* x, float* out,
                      hipStream_t st) {
   switch (g_of(K)) {
@@ -595,10 +931,14 @@ static bool out_proj(int K, const DnOut& a, hipStream_t st) {
   }
 }
 
+static bool dims_ok(const lxm_dn_params* ph) {
+  return ph && ph->hidden > 0 && ph->hidden <= 4096 && ph->kl > 0 && ph->kl <= KD && ph->nk > 0 &&
+         ph->nv % ph->nk == 0 && ph->rl > 0 && ph->nk * ph->rl <= 32 && ph->layers &&
+         ph->layers_host;
+}
+
 extern "C" int lxm_dn_step(const lxm_dn_params* ph, const lxm_dn_params* pd, void* stream) {
-  if (!ph || ph->hidden <= 0 || ph->hidden > 4096 || ph->kl > KD || ph->nv % ph->nk ||
-      ph->nk * ph->rl > 32 || !ph->layers || !ph->layers_host)
-    return (int)hipErrorInvalidValue;
+  if (!dims_ok(ph)) return (int)hipErrorInvalidValue;
   hipStream_t st = (hipStream_t)stream;
   const int H = ph->hidden, I = ph->inter, nk = ph->nk, kl = ph->kl, rl = ph->rl;
   const int nq = nk * kl, nvr = nk * rl * VD, nproj = 2 * nq + 2 * nvr + 2 * nk * rl;
@@ -621,4 +961,27 @@ extern "C" int lxm_dn_step(const lxm_dn_params* ph, const lxm_dn_params* pd, voi
   if (!head(H, ph->embed, ph->vocab, ph->h, ph->w_final, eps, ph->keys, st)) return (int)hipErrorInvalidValue;
   hipLaunchKernelGGL(dn_next, dim3(1), dim3(64), 0, st, pd);
   return (int)hipGetLastError();
+}
+
+// the persistent run's instances: (hidden, live value dims, inter) / 64
+template <int GH, int GV, int GI>
+static int launch_run(const lxm_dn_params* pd, int n, int nblk, hipStream_t st) {
+  void* args[] = {(void*)&pd, (void*)&n};
+  return (int)hipLaunchCooperativeKernel((const void*)dn_run<GH, GV, GI>, dim3(nblk), dim3(NT),
+                                         args, 0, st);
+}
+
+extern "C" int lxm_dn_run(const lxm_dn_params* ph, const lxm_dn_params* pd, int n, void* stream) {
+  if (!dims_ok(ph) || !ph->sync || n < 1) return (int)hipErrorInvalidValue;
+  int dev = 0, n_cus = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e == hipSuccess) e = hipDeviceGetAttribute(&n_cus, hipDeviceAttributeMultiprocessorCount, dev);
+  if (e != hipSuccess) return (int)e;
+  // one workgroup per CU; the delta rule's tiles need nk x rl x QC of them
+  if (n_cus < ph->nk * ph->rl * QC) return (int)hipErrorInvalidConfiguration;
+  hipStream_t st = (hipStream_t)stream;
+  const int gh = g_of(ph->hidden), gv = g_of(ph->nk * ph->rl * VD), gi = g_of(ph->inter);
+  if (gh == 40 && gv == 64 && gi == 144) return launch_run<40, 64, 144>(pd, n, n_cus, st);
+  if (gh == 4 && gv == 8 && gi == 8) return launch_run<4, 8, 8>(pd, n, n_cus, st);
+  return (int)hipErrorInvalidValue;
 }

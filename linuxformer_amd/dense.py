@@ -5,10 +5,12 @@ kernels (csrc/lxm_dense.hip, C ABI include/lxm_dense.h).
     preds = dd.run(forced, n)                 # lx.mega's run semantics: step i's input is
                                               # forced[i] (i < len(forced)), else pred[i - 1]
 
-Every step (embedding, 24 layers, the head's argmax, the token fed back) is one call of
-lxm_dn_step; the step counter and the fed-back token live on the device, so ``run`` can capture a
-step in a graph once and replay it per token. The cache holds the states in transformers'
-layout (conv (1, n_conv, 4) bf16, recurrent (1, nv, 256, 128) fp32) and is updated in place.
+By default ``run`` calls lxm_dn_step per step (embedding, 24 layers, the head's argmax, the token
+fed back), whose step counter and fed-back token live on the device, so it captures a step in a
+graph once and replays it per token; mode "persistent" makes all n steps in one launch
+(lxm_dn_run: one workgroup per CU, grid barriers between the layers' phases). The cache
+holds the states in transformers' layout (conv (1, n_conv, 4) bf16, recurrent (1, nv, 256, 128)
+fp32) and is updated in place.
 """
 
 from __future__ import annotations
@@ -34,7 +36,7 @@ class DnParams(ctypes.Structure):
         [("rms_eps", ctypes.c_float), ("geps", ctypes.c_float)] + \
         [(n, ctypes.c_int32) for n in ("n_forced", "n_steps", "pad")] + \
         [(n, P64) for n in ("layers", "layers_host", "embed", "w_final", "forced", "preds", "step",
-                            "tok", "h", "xn", "P", "on", "keys", "err")]
+                            "tok", "h", "xn", "P", "on", "keys", "err", "sync")]
 
 
 def interleave(w):
@@ -97,7 +99,8 @@ class DenseDecode:
         self.xn = torch.zeros(H + I, dtype=torch.float32, device=dev)
         self.P = torch.zeros(self.nproj, dtype=torch.float32, device=dev)
         self.on = torch.zeros(nk * rl * 128, dtype=torch.float32, device=dev)
-        self.keys = torch.zeros(1, dtype=torch.int64, device=dev)
+        self.keys = torch.zeros(2, dtype=torch.int64, device=dev)
+        self.sync = torch.zeros(256, dtype=torch.int32, device=dev)
         self.step = torch.zeros(1, dtype=torch.int32, device=dev)
         self.tok = torch.zeros(1, dtype=torch.int32, device=dev)
         self.err = torch.zeros(1, dtype=torch.int32, device=dev)
@@ -117,7 +120,8 @@ class DenseDecode:
                      forced=self.forced.data_ptr(), preds=self.preds.data_ptr(),
                      step=self.step.data_ptr(), tok=self.tok.data_ptr(), h=self.h.data_ptr(),
                      xn=self.xn.data_ptr(), P=self.P.data_ptr(), on=self.on.data_ptr(),
-                     keys=self.keys.data_ptr(), err=self.err.data_ptr())
+                     keys=self.keys.data_ptr(), err=self.err.data_ptr(),
+                     sync=self.sync.data_ptr())
         pd = torch.frombuffer(bytearray(bytes(p)), dtype=torch.uint8).to(self.dev)
         return p, pd
 
@@ -128,35 +132,50 @@ class DenseDecode:
             raise RuntimeError(f"dense decode launch failed: hipError {e}")
 
     @torch.no_grad()
-    def run(self, forced, n: int, graph: bool = True) -> list:
+    def run(self, forced, n: int, graph: bool = True, mode: str = "steps") -> list:
         """n greedy steps from the cache's states (updated in place); step i's input is forced[i]
-        for i < len(forced), else step i - 1's prediction. Returns the n predictions. graph: the
-        first step runs eagerly, one step is captured (capturing runs nothing) and replayed for
-        the others; the step reads its index and input from device memory."""
+        for i < len(forced), else step i - 1's prediction. Returns the n predictions. mode
+        "steps": lxm_dn_step per step (graph: the first step eagerly, one step captured
+        (capturing runs nothing) and replayed for the others; the step reads its index and input
+        from device memory); "persistent": one launch of lxm_dn_run for all n steps (the same
+        results; for callers that cannot capture graphs)."""
         f = torch.as_tensor(forced, dtype=torch.int64)
         if len(f) == 0 or n < 1 or n > self.max_steps or len(f) > self.max_steps:
             raise ValueError("forced tokens and steps: 1 .. max_steps")
         if int(f.min()) < 0 or int(f.max()) >= self.spec.vocab:
             raise ValueError("forced token out of range")
+        if mode not in ("persistent", "steps"):
+            raise ValueError(f"mode: persistent or steps, not {mode!r}")
         self.forced[:len(f)].copy_(f.to(torch.int32))
         self.step.zero_()
         self.err.zero_()
+        self.keys.zero_()
+        self.sync.zero_()
         if getattr(self, "_nf", None) != len(f):
             self._p, self._pd = self._params(len(f))
             self._nf, self.graph = len(f), None
-        self._step()
-        if graph and n > 1:
-            if self.graph is None:
-                g = torch.cuda.CUDAGraph()
-                with torch.cuda.graph(g):
-                    self._step()
-                self.graph = g
-            for _ in range(n - 1):
-                self.graph.replay()
+        if mode == "persistent":
+            st = ctypes.c_void_p(torch.cuda.current_stream(self.dev).cuda_stream)
+            e = self.lib.lxm_dn_run(ctypes.byref(self._p), ctypes.c_void_p(self._pd.data_ptr()), n, st)
+            if e:
+                raise RuntimeError(f"dense decode launch failed: hipError {e}")
         else:
-            for _ in range(n - 1):
-                self._step()
+            self._step()
+            if graph and n > 1:
+                if self.graph is None:
+                    g = torch.cuda.CUDAGraph()
+                    with torch.cuda.graph(g):
+                        self._step()
+                    self.graph = g
+                for _ in range(n - 1):
+                    self.graph.replay()
+            else:
+                for _ in range(n - 1):
+                    self._step()
         torch.cuda.synchronize(self.dev)
-        if int(self.err.item()):
+        err = int(self.err.item())
+        if err == 1:
             raise RuntimeError("dense decode: a forced token out of range")
+        if err:
+            raise RuntimeError(f"dense decode: a wait timed out (error {err})")
         return self.preds[:n].cpu().tolist()

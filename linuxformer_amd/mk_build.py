@@ -98,10 +98,12 @@ def load(subprof: bool = False) -> ctypes.CDLL:
         lib.lxm_pf_lds.restype = I
         lib.lxm_dn_step.argtypes = [P, P, P]
         lib.lxm_dn_step.restype = I
+        lib.lxm_dn_run.argtypes = [P, P, I, P]
+        lib.lxm_dn_run.restype = I
         _libs[path] = lib
     return _libs[path]
 
 
 EXPORTS = ("lxm_run", "lxm_lds_base", "lxm_helper_lds", "lxm_max_blocks", "lxm_max_lds",
            "lxm_last_error", "lxm_device_cus", "lxm_t_elem", "lxm_t_sum", "lxm_pf_layers",
-           "lxm_pf_head", "lxm_pf_embed", "lxm_pf_tiles", "lxm_pf_lds", "lxm_dn_step")
+           "lxm_pf_head", "lxm_pf_embed", "lxm_pf_tiles", "lxm_pf_lds", "lxm_dn_step", "lxm_dn_run")

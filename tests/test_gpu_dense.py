@@ -1,5 +1,6 @@
 """Parity of the HIP dense decode (BASELINE config 4's structure) with the oracle on an MI355X,
-through the C ABI: predictions and final states bit for bit. The dense projections are summed in
+through the C ABI (the persistent run, lxm_dn_run, and the per-step kernels, lxm_dn_step):
+predictions and final states bit for bit. The dense projections are summed in
 the dense order the oracle restates for matrices marked dense (64 groups of a row's entries in
 order from +0, then the pairwise tree); everything else follows the stock decode as in the
 sparse paths. Sizes: config 4's layout scaled down (hidden 256, 2 layers) so the oracle runs in
@@ -37,18 +38,18 @@ def bits(a):
     return np.ascontiguousarray(a, np.float32).view(np.uint32)
 
 
-def check(n_forced, n, seed=None, graph=True, name="small"):
+def check(n_forced, n, seed=None, graph=True, name="small", mode="persistent"):
     from oracle import oracle as ox
 
     spec, dm_cpu, sm = model(name)
     conv0, rec0 = synth.dense_state(dm_cpu, seed)
     forced = [int(x) for x in np.random.default_rng(7 + n_forced).integers(0, spec.vocab, n_forced)]
-    print(f"[gpu-test] dense {spec.name}: forced={n_forced} n={n} seed={seed} graph={graph}",
-          flush=True)
+    print(f"[gpu-test] dense {spec.name}: forced={n_forced} n={n} seed={seed} mode={mode} "
+          f"graph={graph}", flush=True)
     dm = synth.dense_to(dm_cpu, "cuda")
     cache = fast.StateCache(conv0, rec0, "bf16", "cuda")
     dd = dense.DenseDecode(dm, cache)
-    preds = dd.run(forced, n, graph=graph)
+    preds = dd.run(forced, n, graph=graph, mode=mode)
     c, r = conv0.copy(), rec0.copy()
     po, _, _ = ox.OracleModel(sm).decode(c, r, forced, n)
     assert preds == po.tolist()
@@ -57,28 +58,38 @@ def check(n_forced, n, seed=None, graph=True, name="small"):
     return preds
 
 
-def test_dense_small_greedy(cuda):
-    check(1, 24)
+MODES = ["persistent", "steps"]
 
 
-def test_dense_small_forced_then_greedy(cuda):
+@pytest.mark.parametrize("mode", MODES)
+def test_dense_small_greedy(cuda, mode):
+    check(1, 24, mode=mode)
+
+
+@pytest.mark.parametrize("mode", MODES)
+def test_dense_small_forced_then_greedy(cuda, mode):
     """A forced prefix (the config's prefill, scaled down), then greedy steps."""
-    check(16, 32)
+    check(16, 32, mode=mode)
 
 
 def test_dense_small_live_state_eager(cuda):
     """From N(0, 1) states and nonzero windows on the live heads, eager steps (no graph)."""
-    check(4, 12, seed=3, graph=False)
+    check(4, 12, seed=3, graph=False, mode="steps")
 
 
 def test_dense_small_live_state_graph(cuda):
-    check(4, 12, seed=3, graph=True)
+    check(4, 12, seed=3, graph=True, mode="steps")
 
 
-def test_dense_full_widths(cuda):
+def test_dense_small_live_state_persistent(cuda):
+    check(4, 12, seed=3)
+
+
+@pytest.mark.parametrize("mode", MODES)
+def test_dense_full_widths(cuda, mode):
     """Config 4's full row lengths (hidden 2560: 40 entries per lane; SwiGLU 9216: 144; 16 key
     heads x 2 live value heads: 4096 out_proj entries, 64) over one layer, from live states."""
-    check(3, 6, seed=5, name="mid")
+    check(3, 6, seed=5, name="mid", mode=mode)
 
 
 def test_dense_rejects_dead_state(cuda):
