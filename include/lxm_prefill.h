@@ -77,6 +77,9 @@ typedef struct lxm_pf_layer {
   int64_t orows;     /* lxm_pf_drow[n_orows]: out_proj rows, entries 4 x (vslot * 128 + dim) */
   int64_t cc;        /* lxm_row[n_conv]: every conv channel's in_proj_qkv row (the windows) */
   int64_t gnorm;     /* float[128]: the gated norm's weight */
+  int64_t entn;      /* float[] parallel to ent: for entries over a norm's output (the MLP units',
+                        the query/key channels', the decays'), the norm weight 1 + w of the entry's
+                        column, which the tile kernel applies as it gathers; else 0 */
   int32_t n_units, n_drows, n_qk, n_dec, n_ks, n_vs, n_orows, rec_bytes;
   int32_t kh[LXM_PF_MAXKS]; /* key head of each key slot */
   float eps, geps;
@@ -127,9 +130,9 @@ int lxm_pf_embed(const lxm_pf_params* p_host, const lxm_pf_params* p_dev, void* 
 /* Layout conversion: dir 0 (T, hidden) row-major -> tiles (p->h), dir 1 tiles -> row-major. x is
    in the model dtype. */
 int lxm_pf_tiles(const lxm_pf_params* p_host, const void* x, void* y, int dir, void* stream);
-/* LDS bytes the tile kernel needs for a model dtype (bf16 != 0) and a layer's MLP units (it is
-   launched with them; the device allows lxm_max_lds()). */
-int lxm_pf_lds(int bf16, int n_units);
+/* LDS bytes the tile kernel needs for a model dtype (bf16 != 0), the hidden size and a layer's
+   MLP units (it is launched with them; the device allows lxm_max_lds()). */
+int lxm_pf_lds(int bf16, int hidden, int n_units);
 
 #ifdef __cplusplus
 }

@@ -156,6 +156,29 @@ __device__ __forceinline__ v4f dot4(const lxm_pf_ent* __restrict__ e, int n, con
   }
   return s;
 }
+// The same over the RMSNorm of a tile: each gathered column x becomes D((x * r) * w1) (norm4),
+// w1 the column's norm weight from the table parallel to the entries.
+template <bool BF, bool HALF>
+__device__ __forceinline__ v4f dot4n(const lxm_pf_ent* __restrict__ e, const float* __restrict__ en,
+                                     int n, const uint8_t* x, v4f r) {
+  v4f s = {0.0f, 0.0f, 0.0f, 0.0f};
+  for (int k0 = 0; k0 < n; k0 += 4) {
+    lxm_pf_ent ee[4];
+    float nw[4];
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+      ee[j] = e[k0 + j];
+      nw[j] = en[k0 + j];
+    }
+    v4f xv[4];
+#pragma unroll
+    for (int j = 0; j < 4; j++) xv[j] = TV<HALF>::at(x, ee[j].off);
+#pragma unroll
+    for (int j = 0; j < 4; j++)
+      if (k0 + j < n) s = acc4<BF>(s, norm4<BF>(xv[j], r, nw[j]), ee[j].w);
+  }
+  return s;
+}
 // the same for one float per entry at x + off (a flat vector, or one position's lane of a tile)
 template <bool BF>
 __device__ __forceinline__ float dot1(const lxm_pf_ent* __restrict__ e, int n, const uint8_t* x) {
@@ -216,9 +239,10 @@ __device__ __forceinline__ v4f hsum(uint8_t* HV, int H, v4f* wsum, bool plus0) {
 // residual as the previous steps left it, stored back. Then Ln >= 0: layer Ln's input norm
 // factor r1 per position, and which of the layer's key slots have a nonzero query/key projection
 // at each position, and whether a decay can act (bit 31); or Ln == -2: the final norm into hn.
-// LDS: 512 bytes of sums and masks, the residual (4,096 columns), the norm's output (then the
-// MLP units' outputs), as tile vectors in the model dtype (bf16 models: 66 KB, two workgroups
-// per CU).
+// The norms' outputs are formed as the entries gather (each entry carries its column's norm
+// weight), so LDS holds 512 bytes of sums and masks, the residual (hidden columns) and the MLP
+// units' outputs, as tile vectors in the model dtype (bf16, hidden 3,572, 1,024 units: 37 KB,
+// four workgroups per CU).
 #define X_HV 512
 // A residual tile from HBM (model dtype) into LDS tile vectors (bf16 if HALF): every thread's
 // columns (t, t + 512, ...) loaded at once.
@@ -233,21 +257,8 @@ __device__ __forceinline__ void load_tile(const void* h, int64_t b, int H, uint8
   for (int k = 0; k < MAXH / NT; k++)
     if (t + k * NT < H) TV<HALF>::put(HV, t + k * NT, x[k]);
 }
-// XM = D((HV * r) * w1) for every column, the weights loaded at once
 template <bool BF>
-__device__ __forceinline__ void norm_tile(const uint8_t* HV, uint8_t* XM, int H, v4f r,
-                                          const float* w1) {
-  const int t = threadIdx.x;
-  float w[MAXH / NT];
-#pragma unroll
-  for (int k = 0; k < MAXH / NT; k++) w[k] = t + k * NT < H ? w1[t + k * NT] : 0.0f;
-#pragma unroll
-  for (int k = 0; k < MAXH / NT; k++)
-    if (t + k * NT < H) TV<BF>::put(XM, t + k * NT, norm4<BF>(TV<BF>::get(HV, t + k * NT), r, w[k]));
-}
-
-template <bool BF>
-__host__ __device__ constexpr int x_xm() { return X_HV + TV<BF>::B * MAXH; }
+__host__ __device__ constexpr int x_xm(int H) { return X_HV + ((TV<BF>::B * H + 15) & ~15); }
 template <bool BF>
 __global__ __launch_bounds__(NT) void pf_tile(const lxm_pf_params* __restrict__ pp, int Lm, int Ln) {
   extern __shared__ __align__(16) uint8_t sm[];
@@ -259,19 +270,19 @@ __global__ __launch_bounds__(NT) void pf_tile(const lxm_pf_params* __restrict__ 
   v4f* wsA = reinterpret_cast<v4f*>(sm + 64);
   v4f* wsB = reinterpret_cast<v4f*>(sm + 192);
   uint8_t* HV = sm + X_HV;
-  uint8_t* XM = sm + x_xm<BF>();
+  uint8_t* XM = sm + x_xm<BF>(H);
   if (t < TT) smask[t] = 0;
   load_tile<BF, BF>(p.h, b, H, HV);
   __syncthreads();
   if (Lm >= 0) {
     const lxm_pf_layer& ly = p.layers[Lm];
     const lxm_pf_ent* ent = tab<lxm_pf_ent>(p.blob, ly.ent);
+    const float* entn = tab<float>(p.blob, ly.entn);
     const v4f ss = hsum<BF, BF>(HV, H, wsA, false);
     const v4f r = {norm_r(ss.x, H, ly.eps), norm_r(ss.y, H, ly.eps), norm_r(ss.z, H, ly.eps),
                    norm_r(ss.w, H, ly.eps)};
-    norm_tile<BF>(HV, XM, H, r, tab<float>(p.blob, ly.w1_post));
-    __syncthreads();
-    // units: act = D(D(silu(D(gate . x))) * D(up . x))
+    // units over the post norm (formed as the entries gather): act = D(D(silu(D(gate . x))) *
+    // D(up . x))
     const lxm_pf_unit* un = tab<lxm_pf_unit>(p.blob, ly.units);
     v4f a[LXM_PF_UPT];
 #pragma unroll
@@ -279,13 +290,12 @@ __global__ __launch_bounds__(NT) void pf_tile(const lxm_pf_params* __restrict__ 
       const int u = t + i * NT;
       if (u < ly.n_units) {
         const lxm_pf_unit q = un[u];
-        const v4f g = rd4<BF>(dot4<BF, BF>(ent + q.gs, q.gn, XM));
-        const v4f v = rd4<BF>(dot4<BF, BF>(ent + q.us, q.un, XM));
+        const v4f g = rd4<BF>(dot4n<BF, BF>(ent + q.gs, entn + q.gs, q.gn, HV, r));
+        const v4f v = rd4<BF>(dot4n<BF, BF>(ent + q.us, entn + q.us, q.un, HV, r));
         a[i] = v4f{rd<BF>(silu_rd<BF>(g.x) * v.x), rd<BF>(silu_rd<BF>(g.y) * v.y),
                    rd<BF>(silu_rd<BF>(g.z) * v.z), rd<BF>(silu_rd<BF>(g.w) * v.w)};
       }
     }
-    __syncthreads();
 #pragma unroll
     for (int i = 0; i < LXM_PF_UPT; i++)
       if (t + i * NT < ly.n_units) V::put(XM, t + i * NT, a[i]);
@@ -302,17 +312,17 @@ __global__ __launch_bounds__(NT) void pf_tile(const lxm_pf_params* __restrict__ 
   if (Ln >= 0) {
     const lxm_pf_layer& ly = p.layers[Ln];
     const lxm_pf_ent* ent = tab<lxm_pf_ent>(p.blob, ly.ent);
+    const float* entn = tab<float>(p.blob, ly.entn);
     const v4f ss = hsum<BF, BF>(HV, H, wsB, Lm >= 0);
     const v4f r = {norm_r(ss.x, H, ly.eps), norm_r(ss.y, H, ly.eps), norm_r(ss.z, H, ly.eps),
                    norm_r(ss.w, H, ly.eps)};
     if (t < TT && b * TT + t < p.T) p.r1[b * TT + t] = t == 0 ? r.x : t == 1 ? r.y : t == 2 ? r.z : r.w;
-    norm_tile<BF>(HV, XM, H, r, tab<float>(p.blob, ly.w1_in));
-    __syncthreads();
-    // query/key projections of the live key heads' channels: which slots are nonzero
+    // query/key projections of the live key heads' channels over the input norm (formed as the
+    // entries gather): which slots are nonzero
     const lxm_pf_qk* qk = tab<lxm_pf_qk>(p.blob, ly.qk);
     for (int i = t; i < ly.n_qk; i += NT) {
       const lxm_pf_qk q = qk[i];
-      const v4f P = rd4<BF>(dot4<BF, BF>(ent + q.start, q.len, XM));
+      const v4f P = rd4<BF>(dot4n<BF, BF>(ent + q.start, entn + q.start, q.len, HV, r));
       const uint32_t bit = 1u << q.kslot;
       if (P.x != 0.0f) atomicOr(smask + 0, bit);
       if (P.y != 0.0f) atomicOr(smask + 1, bit);
@@ -323,7 +333,8 @@ __global__ __launch_bounds__(NT) void pf_tile(const lxm_pf_params* __restrict__ 
     const lxm_pf_dec* dc = tab<lxm_pf_dec>(p.blob, ly.dec);
     for (int i = t; i < ly.n_dec; i += NT) {
       const lxm_pf_dec d = dc[i];
-      const v4f a = d.len ? rd4<BF>(dot4<BF, BF>(ent + d.start, d.len, XM)) : v4f{0.0f, 0.0f, 0.0f, 0.0f};
+      const v4f a = d.len ? rd4<BF>(dot4n<BF, BF>(ent + d.start, entn + d.start, d.len, HV, r))
+                          : v4f{0.0f, 0.0f, 0.0f, 0.0f};
       const float na = -cr_exp(d.A_log);
 #pragma unroll
       for (int k = 0; k < TT; k++)
@@ -903,9 +914,8 @@ __global__ void pf_tiles_k(const void* x, void* y, int T, int H, int dir) {
 // ---------------------------------------------------------------------------------------------
 // Host side.
 template <bool BF>
-static int tile_lds(int n_units_max) {
-  const int cols = n_units_max > MAXH ? n_units_max : MAXH;
-  return x_xm<BF>() + TV<BF>::B * cols;
+static int tile_lds(int H, int n_units_max) {
+  return x_xm<BF>(H) + TV<BF>::B * (n_units_max > 0 ? n_units_max : 1);
 }
 #define ACT_LDS (A_MISC + 16)
 #define ACT_GRID 1024
@@ -922,7 +932,7 @@ static hipError_t run_layers(const lxm_pf_params* ph, const lxm_pf_params* pd, i
   const int ntiles = ph->ntiles;
   int umax = 0;
   for (int L = l0; L < l1; L++) umax = ph->layers_host[L].n_units > umax ? ph->layers_host[L].n_units : umax;
-  const int xl = tile_lds<BF>(umax);
+  const int xl = tile_lds<BF>(ph->hidden, umax);
   hipError_t e = lds_attr((const void*)pf_tile<BF>, xl);
   if (e == hipSuccess) e = lds_attr((const void*)pf_act<BF>, ACT_LDS);
   if (e == hipSuccess) e = lds_attr((const void*)pf_out<BF>, 4 * VD * LXM_PF_MAXVS + 16);
@@ -944,11 +954,11 @@ static hipError_t run_layers(const lxm_pf_params* ph, const lxm_pf_params* pd, i
 template <bool BF>
 static hipError_t run_head(const lxm_pf_params* ph, const lxm_pf_params* pd, hipStream_t st) {
   const int ntiles = ph->ntiles, T = ph->T;
-  hipError_t e = lds_attr((const void*)pf_tile<BF>, tile_lds<BF>(0));
+  hipError_t e = lds_attr((const void*)pf_tile<BF>, tile_lds<BF>(ph->hidden, 0));
   if (e == hipSuccess) e = lds_attr((const void*)pf_head<BF>, 16 * ph->hidden + 64);
   if (e != hipSuccess) return e;
   hipLaunchKernelGGL(pf_fill_keys, dim3((T + 255) / 256), dim3(256), 0, st, pd);
-  hipLaunchKernelGGL(pf_tile<BF>, dim3(ntiles), dim3(NT), tile_lds<BF>(0), st, pd, -1, -2);
+  hipLaunchKernelGGL(pf_tile<BF>, dim3(ntiles), dim3(NT), tile_lds<BF>(ph->hidden, 0), st, pd, -1, -2);
   hipLaunchKernelGGL(pf_head<BF>, dim3(ntiles * LXM_PF_SLICES), dim3(NT), 16 * ph->hidden + 64, st, pd);
   hipLaunchKernelGGL(pf_preds, dim3((T + 255) / 256), dim3(256), 0, st, pd);
   return hipGetLastError();
@@ -1000,8 +1010,8 @@ int lxm_pf_tiles(const lxm_pf_params* ph, const void* x, void* y, int dir, void*
   return (int)hipGetLastError();
 }
 
-int lxm_pf_lds(int bf16, int n_units) {
-  return bf16 ? tile_lds<true>(n_units) : tile_lds<false>(n_units);
+int lxm_pf_lds(int bf16, int hidden, int n_units) {
+  return bf16 ? tile_lds<true>(hidden, n_units) : tile_lds<false>(hidden, n_units);
 }
 
 }  // extern "C"

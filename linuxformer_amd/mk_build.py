@@ -94,7 +94,7 @@ def load(subprof: bool = False) -> ctypes.CDLL:
         lib.lxm_pf_layers.restype = I
         lib.lxm_pf_tiles.argtypes = [P, P, P, I, P]
         lib.lxm_pf_tiles.restype = I
-        lib.lxm_pf_lds.argtypes = [I, I]
+        lib.lxm_pf_lds.argtypes = [I, I, I]
         lib.lxm_pf_lds.restype = I
         lib.lxm_dn_step.argtypes = [P, P, P]
         lib.lxm_dn_step.restype = I

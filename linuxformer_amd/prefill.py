@@ -26,7 +26,7 @@ ENT = np.dtype([("off", "<i4"), ("w", "<f4")])
 class PfLayer(ctypes.Structure):
     _fields_ = [(n, ctypes.c_int64) for n in ("ent", "w1_in", "w1_post", "units", "drows", "qk",
                                               "dec", "vs", "vc", "zrow", "brow", "orows", "cc",
-                                              "gnorm")] + \
+                                              "gnorm", "entn")] + \
         [(n, ctypes.c_int32) for n in ("n_units", "n_drows", "n_qk", "n_dec", "n_ks", "n_vs",
                                        "n_orows", "rec_bytes")] + \
         [("kh", ctypes.c_int32 * MAXKS), ("eps", ctypes.c_float), ("geps", ctypes.c_float),
@@ -69,13 +69,18 @@ class _Ents:
     """One layer's entry array, built row group by row group."""
 
     def __init__(self):
-        self.offs, self.ws, self.n = [], [], 0
+        self.offs, self.ws, self.nws, self.n = [], [], [], 0
 
-    def add(self, offs, ws) -> int:
+    def add(self, offs, ws, nw=None) -> int:
+        """Entries (16 x column, weight); nw: the norm weight of each entry's column when the
+        row reads a norm's output (applied as the tile kernel gathers), else 0."""
         start = self.n
         self.offs.append(np.asarray(offs, np.int64))
         self.ws.append(np.asarray(ws, np.float32))
-        self.n += len(self.offs[-1])
+        k = len(self.offs[-1])
+        self.nws.append(np.zeros(k, np.float32) if nw is None else np.asarray(nw, np.float32))
+        assert len(self.nws[-1]) == k
+        self.n += k
         return start
 
     def pad(self) -> None:
@@ -89,6 +94,13 @@ class _Ents:
             e["off"][:self.n] = np.concatenate(self.offs)
             e["w"][:self.n] = np.concatenate(self.ws)
         return e
+
+    def norms(self) -> np.ndarray:
+        """The entries' norm weights, padded like array()."""
+        n = np.zeros(self.n + 4, np.float32)
+        if self.n:
+            n[:self.n] = np.concatenate(self.nws)
+        return n
 
 
 class _Csr:
@@ -130,6 +142,8 @@ def pack_layer(sm, fast, L: int, blob: _Blob) -> PfLayer:
     pl = PfLayer()
     # ---- MLP: live units sorted by length (thread-strided, similar lengths per wave)
     g, u = _Csr(ly.gate_proj), _Csr(ly.up_proj)
+    w1_in = np.float32(1.0) + np.asarray(ly.input_layernorm, np.float32)
+    w1_post = np.float32(1.0) + np.asarray(ly.post_attention_layernorm, np.float32)
     units = np.asarray(dec_info["units"], np.int64)
     assert len(units) <= UPT * NT, f"layer {L}: {len(units)} MLP units > {UPT * NT}"
     glen = g.ptr[units + 1] - g.ptr[units]
@@ -141,9 +155,9 @@ def pack_layer(sm, fast, L: int, blob: _Blob) -> PfLayer:
     ut = np.zeros((len(units), 4), np.int32)
     for i, un in enumerate(units):
         c, v = g.row(un)
-        ut[i, 0], ut[i, 1] = E.add(16 * c, v), len(c)
+        ut[i, 0], ut[i, 1] = E.add(16 * c, v, w1_post[c]), len(c)
         c, v = u.row(un)
-        ut[i, 2], ut[i, 3] = E.add(16 * c, v), len(c)
+        ut[i, 2], ut[i, 3] = E.add(16 * c, v, w1_post[c]), len(c)
     E.pad()
     # down_proj rows over the live units, entries in ascending unit order (16 x position)
     dcoo = ly.down_proj
@@ -176,7 +190,7 @@ def pack_layer(sm, fast, L: int, blob: _Blob) -> PfLayer:
                     continue
                 reach = max(reach, 3 - int(np.nonzero(tp)[0][0]))
                 c, v = qkv.row(ch)
-                qk_rows.append((ch, s, part * KD + i, E.add(16 * c, v), len(c), tp))
+                qk_rows.append((ch, s, part * KD + i, E.add(16 * c, v, w1_in[c]), len(c), tp))
     qkt = np.zeros(len(qk_rows), np.dtype([("chan", "<i4"), ("kslot", "<i4"), ("pos", "<i4"),
                                            ("start", "<i4"), ("len", "<i4"), ("pad", "<i4", 3),
                                            ("taps", "<f4", 4)]))
@@ -200,7 +214,8 @@ def pack_layer(sm, fast, L: int, blob: _Blob) -> PfLayer:
                                            ("pad", "<i4", 3)]))
     for i, vh in enumerate(decays):
         c, v = acsr.row(vh)
-        dect[i] = (vslot[vh], E.add(16 * c, v), len(c), ly.dt_bias[vh], ly.A_log[vh], (0, 0, 0))
+        dect[i] = (vslot[vh], E.add(16 * c, v, w1_in[c]), len(c), ly.dt_bias[vh], ly.A_log[vh],
+                   (0, 0, 0))
     zcsr, bcsr = _Csr(ly.in_proj_z), _Csr(ly.in_proj_b)
     vct = np.zeros(len(slots) * VD, np.dtype([("start", "<i4"), ("len", "<i4"), ("taps", "<f4", 4)]))
     zt = np.zeros((len(slots) * VD, 2), np.int32)
@@ -240,8 +255,9 @@ def pack_layer(sm, fast, L: int, blob: _Blob) -> PfLayer:
     ents = E.array()
     assert len(ents) < 2 ** 31
     pl.ent = blob.add(ents)
-    pl.w1_in = blob.add(np.float32(1.0) + np.asarray(ly.input_layernorm, np.float32))
-    pl.w1_post = blob.add(np.float32(1.0) + np.asarray(ly.post_attention_layernorm, np.float32))
+    pl.entn = blob.add(E.norms())
+    pl.w1_in = blob.add(w1_in)
+    pl.w1_post = blob.add(w1_post)
     pl.units = blob.add(ut)
     pl.drows = blob.add(dt)
     pl.qk = blob.add(qkt)
@@ -315,7 +331,7 @@ class Prefill:
 
     # ------------------------------------------------------------------------------------------
     def lds_ok(self) -> bool:
-        return self.lib.lxm_pf_lds(int(self.bf), self.umax) <= 160 * 1024
+        return self.lib.lxm_pf_lds(int(self.bf), self.dims.hidden, self.umax) <= 160 * 1024
 
     def _buffers(self, T: int) -> None:
         if self._T == T:
