@@ -612,7 +612,7 @@ __global__ __launch_bounds__(256) void pf_tail(const lxm_pf_params* __restrict__
 // exp(g) != 1; with a live query or key kv = S^T k, delta = (v - kv) beta, S += k delta^T,
 // o = D(S^T q) into the record (over v, which this step has read). The state tile stays in registers: thread (cg, rb) holds columns 4cg..4cg+3 of
 // rows 16rb..16rb+15, one of ATen's 16-row cascade blocks (torch .sum(-2) on the CPU).
-// A candidate's inputs as one thread of the delta kernel holds them (loaded one candidate ahead):
+// A candidate's inputs as one thread of the delta kernel holds them (loaded three candidates ahead):
 // the header word, the slot's decay factor, and the thread's share of k and q (threads < 256) or
 // v (256..383), and beta (thread 0).
 struct DeltaIn {
@@ -658,12 +658,17 @@ __global__ __launch_bounds__(NT) void pf_delta(const lxm_pf_params* __restrict__
 #pragma unroll
   for (int i = 0; i < 16; i++) s[i] = S4[(rb * 16 + i) * (VD / 4) + cg];
   bool wrote = false;
-  DeltaIn nx = {};
-  if (count > 0) nx = delta_in(recs, ro, vslot, sv.kslot);
+  // the inputs of the next three candidates in flight (a step takes about one load's latency)
+  DeltaIn n1 = {}, n2 = {}, n3 = {};
+  if (count > 0) n1 = delta_in(recs, ro, vslot, sv.kslot);
+  if (count > 1) n2 = delta_in(recs + rec_b, ro, vslot, sv.kslot);
+  if (count > 2) n3 = delta_in(recs + 2 * rec_b, ro, vslot, sv.kslot);
   for (int j = 0; j < count; j++) {
     uint8_t* rec = recs + (int64_t)j * rec_b;
-    const DeltaIn cur = nx;
-    if (j + 1 < count) nx = delta_in(rec + rec_b, ro, vslot, sv.kslot);
+    const DeltaIn cur = n1;
+    n1 = n2;
+    n2 = n3;
+    if (j + 3 < count) n3 = delta_in(rec + 3 * rec_b, ro, vslot, sv.kslot);
     const bool live = sv.kslot >= 0 && ((cur.live >> sv.kslot) & 1u);
     const float e = cur.e;
     int proc = 0;
