@@ -66,15 +66,16 @@ def survey_bytes_per_token(model, f_out: float) -> float:
     return tot
 
 
-def measured_traffic(config: str):
-    """HBM bytes per decoded token of the decode kernel, from the committed rocprofv3 counter
-    summary (profiles/pmc_lxm_decode_<config>.txt: FETCH_SIZE and WRITE_SIZE per dispatch,
-    each scaled by the same counter's reading for a plain copy of known size), or None."""
-    path = os.path.join(HERE, "profiles", f"pmc_lxm_decode_{config}.txt")
+def measured_traffic(config: str, kind: str = "decode", key: str = "hbm_bytes_per_token"):
+    """HBM bytes per unit (a decoded token, a prefill position) of a path, from the committed
+    rocprofv3 counter summary (profiles/pmc_lxm_<kind>_<config>.txt: FETCH_SIZE and WRITE_SIZE
+    per dispatch, each scaled by the same counter's reading for a plain copy of known size), or
+    None."""
+    path = os.path.join(HERE, "profiles", f"pmc_lxm_{kind}_{config}.txt")
     if not os.path.exists(path):
         return None
     for line in open(path):
-        if line.startswith("hbm_bytes_per_token:"):
+        if line.startswith(key + ":"):
             return float(line.split(":", 1)[1])
     return None
 
@@ -134,6 +135,7 @@ def prefill_leg(calls: int, T: int, cpu_tokens: int) -> dict:
     esz = 2 if d.dtype == "bf16" else 4
     b_pos = d.n_layers * 2 * esz * d.hidden + 2 * esz * d.hidden + 2 * 4 * 256 * 128 * slots / T
     achieved = b_pos * T / (call_ms * 1e-3) / 1e9
+    t_pos = measured_traffic("c3", "prefill", "hbm_bytes_per_position")
     out = {"metric": "verified prefill tok/s, 37-layer sparse chip stack, 1 MI355X",
            "value": round(T / (call_ms * 1e-3), 1), "unit": "tok/s", "calls": calls,
            "ms_per_call": round(call_ms, 3), "tokens_per_call": T,
@@ -143,7 +145,8 @@ def prefill_leg(calls: int, T: int, cpu_tokens: int) -> dict:
                       "value_head_slots": slots},
            "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS,
                         "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 5),
-                        "bytes_per_position": round(b_pos)}}
+                        "bytes_per_position": round(b_pos),
+                        "traffic": None if t_pos is None else round(t_pos * T)}}
     if cpu_tokens > 0:
         from oracle import oracle as ox
 
@@ -215,7 +218,8 @@ def dense_cpu_tok_s(dm, n: int) -> float:
     return n / (time.perf_counter() - t)
 
 
-def dense_leg(n_prefill: int, n_steps: int, cpu_tokens: int) -> dict:
+def dense_leg(n_prefill: int, n_steps: int, cpu_tokens: int, graph: bool = True,
+              persistent: bool = True) -> dict:
     """the dense padded text-view stack; n_prefill seeded uniform forced steps
     from a zero state, then n_steps greedy steps, timed (HIP events on the stream)."""
     import numpy as np
@@ -235,24 +239,26 @@ def dense_leg(n_prefill: int, n_steps: int, cpu_tokens: int) -> dict:
     log(f"[bench] c4: built in {time.time() - t0:.1f}s")
     toks = np.random.default_rng(spec.seed).integers(0, spec.vocab, n_prefill).tolist()
     t = time.perf_counter()
-    p1 = dd.run(toks, n_prefill)
+    p1 = dd.run(toks, n_prefill, graph=graph)
     pre_s = time.perf_counter() - t
     log(f"[bench] c4: prefill of {n_prefill} forced steps in {pre_s:.2f}s")
     stream = torch.cuda.current_stream()
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     e0.record(stream)
-    p2 = dd.run([p1[-1]], n_steps)
+    p2 = dd.run([p1[-1]], n_steps, graph=graph)
     e1.record(stream)
     torch.cuda.synchronize()
     ms = e0.elapsed_time(e1)
     # the same steps as one persistent launch (lxm_dn_run), timed the same way
     n_per = max(1, n_steps // 4)
-    e2, e3 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    e2.record(stream)
-    dd.run([p2[-1]], n_per, mode="persistent")
-    e3.record(stream)
-    torch.cuda.synchronize()
-    ms_per = e2.elapsed_time(e3)
+    ms_per = None
+    if persistent:
+        e2, e3 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e2.record(stream)
+        dd.run([p2[-1]], n_per, mode="persistent")
+        e3.record(stream)
+        torch.cuda.synchronize()
+        ms_per = e2.elapsed_time(e3)
     H, I, nk, kl, rl = spec.hidden, spec.inter, spec.nk, spec.kd_live, spec.r_live
     nvr = nk * rl * 128
     w_layer = 2 * ((2 * nk * kl + 2 * nvr + 2 * nk * rl) * H + H * nvr + 3 * I * H)
@@ -260,6 +266,7 @@ def dense_leg(n_prefill: int, n_steps: int, cpu_tokens: int) -> dict:
     b_tok = d.n_layers * (w_layer + state) + 2 * spec.vocab * H
     pad_layer = 2 * ((2 * nk * 256 + 2 * d.nv * 128 + 2 * d.nv) * H + H * d.nv * 128 + 3 * I * H)
     achieved = b_tok * n_steps / (ms * 1e-3) / 1e9
+    t_tok = measured_traffic("c4", "dense")
     out = {"metric": "dense padded decode tok/s, 24-layer text-view stack, 1 MI355X",
            "value": round(n_steps / (ms * 1e-3), 1), "unit": "tok/s",
            "ms_per_token": round(ms / n_steps, 4), "steps": n_steps,
@@ -271,9 +278,11 @@ def dense_leg(n_prefill: int, n_steps: int, cpu_tokens: int) -> dict:
            "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS,
                         "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
                         "bytes_per_token": b_tok,
+                        "traffic": None if t_tok is None else round(t_tok * n_steps),
                         "padded_bytes_per_token": d.n_layers * (pad_layer + state) + 2 * spec.vocab * H},
            "distinct_predictions": len(set(p2)),
-           "persistent": {"steps": n_per, "tok_s": round(n_per / (ms_per * 1e-3), 1),
+           "persistent": None if ms_per is None else
+                         {"steps": n_per, "tok_s": round(n_per / (ms_per * 1e-3), 1),
                           "note": "lxm_dn_run, continuing from the greedy run's states"}}
     if cpu_tokens > 0:
         out["cpu_baseline"] = {"value": round(dense_cpu_tok_s(dm, cpu_tokens), 3), "unit": "tok/s",
@@ -299,6 +308,10 @@ def main() -> int:
     ap.add_argument("--dn-prefill", type=int, default=8192)
     ap.add_argument("--dn-steps", type=int, default=4096)
     ap.add_argument("--dn-cpu-tokens", type=int, default=4)
+    ap.add_argument("--dn-graph", type=int, default=1,
+                    help="1: the dense steps replayed from a captured graph; 0: launched eagerly")
+    ap.add_argument("--dn-persistent", type=int, default=1,
+                    help="1: also time the persistent run (lxm_dn_run); 0: skip it")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: the decode is one sequential chain per stream and this "
@@ -311,7 +324,8 @@ def main() -> int:
         if "prefill" in legs:
             out["verified_prefill"] = prefill_leg(args.pf_calls, args.pf_tokens, args.pf_cpu_tokens)
         if "dense" in legs:
-            out["dense_decode"] = dense_leg(args.dn_prefill, args.dn_steps, args.dn_cpu_tokens)
+            out["dense_decode"] = dense_leg(args.dn_prefill, args.dn_steps, args.dn_cpu_tokens,
+                                            bool(args.dn_graph), bool(args.dn_persistent))
         print(json.dumps(out), flush=True)
         return 0
 
@@ -398,7 +412,8 @@ def main() -> int:
         out["verified_prefill"] = prefill_leg(args.pf_calls, args.pf_tokens, args.pf_cpu_tokens)
     if "dense" in legs:
         torch.cuda.empty_cache()
-        out["dense_decode"] = dense_leg(args.dn_prefill, args.dn_steps, args.dn_cpu_tokens)
+        out["dense_decode"] = dense_leg(args.dn_prefill, args.dn_steps, args.dn_cpu_tokens,
+                                        bool(args.dn_graph), bool(args.dn_persistent))
     print(json.dumps(out), flush=True)
     return 0
 
