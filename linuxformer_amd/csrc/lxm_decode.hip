@@ -1266,7 +1266,14 @@ __device__ void head_rows(const lxm_params& p, int step, const int32_t* lptr, co
   const int t = threadIdx.x, H = p.hidden;
   float* hn = reinterpret_cast<float*>(hx + HX_X);
   unsigned long long* wk = reinterpret_cast<unsigned long long*>(hx + HX_BS);
-  for (int c = t; c < H; c += NT) hn[c] = ld_rlxf(p.hn + c);
+  {  // the thread's columns requested together (one round trip, not one per column)
+    float v[MAXH / NT];
+#pragma unroll
+    for (int k = 0; k < MAXH / NT; k++) v[k] = t + k * NT < H ? ld_rlxf(p.hn + t + k * NT) : 0.0f;
+#pragma unroll
+    for (int k = 0; k < MAXH / NT; k++)
+      if (t + k * NT < H) hn[t + k * NT] = v[k];
+  }
   __syncthreads();
   unsigned long long best = 0;
   for (int k = t; k < nr; k += NT) {
@@ -1393,7 +1400,8 @@ __device__ void gdn_head(const lxm_params& p, int L, int step, int vh, bool out,
   const float beta = __uint_as_float((uint32_t)misc[2]);
   // The state tile: thread (cg, rb) holds columns 4cg..4cg+3 of rows 16rb..16rb+15, i.e. one
   // of ATen's 16-row cascade blocks (torch .sum(-2) on the CPU: blocks of 16 rows, each from +0
-  // in order, the block sums from +0 in order; only rows with a nonzero factor add terms).
+  // in order, the block sums from +0 in order; only rows with a nonzero factor add terms). Only
+  // those rows are read: the whole tile (128 KB) streamed into one CU was measured slower.
   {
     const int cg = t & 31, rb = t >> 5;
     GAS v4f* S4 = gp(reinterpret_cast<v4f*>(p.rec[L] + (size_t)vh * KD * VD));
