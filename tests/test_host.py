@@ -272,3 +272,45 @@ def test_bench_refuses_more_than_one_gpu():
     r = subprocess.run([sys.executable, os.path.join(ROOT, "bench.py"), "--gpus", "2"],
                        capture_output=True, text=True, timeout=120)
     assert r.returncode == 2 and "one GPU" in r.stderr
+
+
+@pytest.mark.parametrize("name", ["small", "tiny"])
+def test_prefill_entries_carry_their_norm_weights(name):
+    """The prefill packer (host only): every entry of an MLP unit's gate/up row carries the
+    post-attention norm weight 1 + w of its column, every entry of a query/key row and of a decay
+    row the input norm's; other entries carry 0. The tile kernel forms D((x r) w1) from them as
+    it gathers, so a wrong weight here would change the units' and the gates' inputs. (tiny:
+    random norm weights on every column, where the two norms differ everywhere.)"""
+    from linuxformer_amd import fast, prefill
+
+    m = synth.build(synth.small()) if name == "small" else synth.tiny_dense(3, "bf16")
+    f = fast.Fast(m)
+    for L in range(m.dims.n_layers):
+        ly = m.layers[L]
+        blob = prefill._Blob()
+        pl = prefill.pack_layer(m, f, L, blob)
+        raw = blob.bytes()
+
+        def arr(off, dtype, n):
+            return np.frombuffer(raw, dtype=dtype, count=n, offset=off)
+
+        n_ent = (pl.entn - pl.ent) // prefill.ENT.itemsize  # ent is followed by entn
+        ent = arr(pl.ent, prefill.ENT, n_ent)
+        entn = arr(pl.entn, np.float32, n_ent)
+        w1_in = np.float32(1.0) + np.asarray(ly.input_layernorm, np.float32)
+        w1_post = np.float32(1.0) + np.asarray(ly.post_attention_layernorm, np.float32)
+        want = np.zeros(n_ent, np.float32)
+        units = arr(pl.units, np.int32, 4 * pl.n_units).reshape(-1, 4)
+        for gs, gn, us, un in units:
+            for a, n in ((gs, gn), (us, un)):
+                want[a:a + n] = w1_post[ent["off"][a:a + n] // 16]
+        qk = arr(pl.qk, np.dtype([("chan", "<i4"), ("kslot", "<i4"), ("pos", "<i4"),
+                                  ("start", "<i4"), ("len", "<i4"), ("pad", "<i4", 3),
+                                  ("taps", "<f4", 4)]), pl.n_qk)
+        dec = arr(pl.dec, np.dtype([("vslot", "<i4"), ("start", "<i4"), ("len", "<i4"),
+                                    ("dt_bias", "<f4"), ("A_log", "<f4"), ("pad", "<i4", 3)]),
+                  pl.n_dec)
+        for a, n in list(zip(qk["start"], qk["len"])) + list(zip(dec["start"], dec["len"])):
+            want[a:a + n] = w1_in[ent["off"][a:a + n] // 16]
+        assert pl.n_units > 0 and pl.n_qk > 0
+        assert (entn.view(np.uint32) == want.view(np.uint32)).all(), L
