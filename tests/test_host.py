@@ -314,3 +314,14 @@ def test_prefill_entries_carry_their_norm_weights(name):
             want[a:a + n] = w1_in[ent["off"][a:a + n] // 16]
         assert pl.n_units > 0 and pl.n_qk > 0
         assert (entn.view(np.uint32) == want.view(np.uint32)).all(), L
+
+
+def test_alone_rejects_bad_launch_sizes():
+    from linuxformer_amd import alone
+
+    with pytest.raises(ValueError):
+        alone.run_alone(None, [[1]], final=lambda t: True, done=lambda s, b: True,
+                        first_launch=0)
+    with pytest.raises(ValueError):
+        alone.run_alone(None, [[1]], final=lambda t: True, done=lambda s, b: True,
+                        first_launch=64, max_launch=32)
