@@ -219,9 +219,10 @@ def dense_cpu_tok_s(dm, n: int) -> float:
 
 
 def dense_leg(n_prefill: int, n_steps: int, cpu_tokens: int, graph: bool = True,
-              persistent: bool = True) -> dict:
-    """the dense padded text-view stack; n_prefill seeded uniform forced steps
-    from a zero state, then n_steps greedy steps, timed (HIP events on the stream)."""
+              persistent: bool = True, batched: bool = True) -> dict:
+    """the dense padded text-view stack; a prompt of n_prefill seeded uniform
+    tokens from a zero state (batched: lxm_dn_prefill over all but the last, then one step;
+    else n_prefill forced steps), then n_steps greedy steps, timed (HIP events on the stream)."""
     import numpy as np
     import torch
 
@@ -239,9 +240,14 @@ def dense_leg(n_prefill: int, n_steps: int, cpu_tokens: int, graph: bool = True,
     log(f"[bench] c4: built in {time.time() - t0:.1f}s")
     toks = np.random.default_rng(spec.seed).integers(0, spec.vocab, n_prefill).tolist()
     t = time.perf_counter()
-    p1 = dd.run(toks, n_prefill, graph=graph)
+    if batched:
+        dd.prefill(toks[:-1])  # lxm_dn_prefill: the same states as forced steps, bit for bit
+        p1 = dd.run(toks[-1:], 1, graph=graph)
+    else:
+        p1 = dd.run(toks, n_prefill, graph=graph)
     pre_s = time.perf_counter() - t
-    log(f"[bench] c4: prefill of {n_prefill} forced steps in {pre_s:.2f}s")
+    log(f"[bench] c4: prefill of {n_prefill} tokens in {pre_s:.2f}s "
+        f"({'batched, then one step' if batched else 'forced steps'})")
     stream = torch.cuda.current_stream()
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     e0.record(stream)
@@ -270,8 +276,10 @@ def dense_leg(n_prefill: int, n_steps: int, cpu_tokens: int, graph: bool = True,
     out = {"metric": "dense padded decode tok/s, 24-layer text-view stack, 1 MI355X",
            "value": round(n_steps / (ms * 1e-3), 1), "unit": "tok/s",
            "ms_per_token": round(ms / n_steps, 4), "steps": n_steps,
-           "prefill": {"forced_steps": n_prefill, "s": round(pre_s, 2),
-                       "tok_s": round(n_prefill / pre_s, 1)},
+           "prefill": {"tokens": n_prefill, "s": round(pre_s, 2),
+                       "tok_s": round(n_prefill / pre_s, 1),
+                       "mode": "lxm_dn_prefill (batches of 16) + one step" if batched
+                               else "forced steps"},
            "config": {"workload": "c4: 24 layers, hidden 2560, 16 key heads (256, 128 live), 128 "
                                   "value heads (2 live per key head), SwiGLU 9216, vocab 248,320, "
                                   "bf16 N(0, 0.02); zero state"},
@@ -310,6 +318,8 @@ def main() -> int:
     ap.add_argument("--dn-cpu-tokens", type=int, default=4)
     ap.add_argument("--dn-graph", type=int, default=1,
                     help="1: the dense steps replayed from a captured graph; 0: launched eagerly")
+    ap.add_argument("--dn-batched", type=int, default=1,
+                    help="config 4's prompt through lxm_dn_prefill (0: as forced steps)")
     ap.add_argument("--dn-persistent", type=int, default=1,
                     help="1: also time the persistent run (lxm_dn_run); 0: skip it")
     args = ap.parse_args()
@@ -325,7 +335,7 @@ def main() -> int:
             out["verified_prefill"] = prefill_leg(args.pf_calls, args.pf_tokens, args.pf_cpu_tokens)
         if "dense" in legs:
             out["dense_decode"] = dense_leg(args.dn_prefill, args.dn_steps, args.dn_cpu_tokens,
-                                            bool(args.dn_graph), bool(args.dn_persistent))
+                                            bool(args.dn_graph), bool(args.dn_persistent), bool(args.dn_batched))
         print(json.dumps(out), flush=True)
         return 0
 
@@ -413,7 +423,7 @@ def main() -> int:
     if "dense" in legs:
         torch.cuda.empty_cache()
         out["dense_decode"] = dense_leg(args.dn_prefill, args.dn_steps, args.dn_cpu_tokens,
-                                        bool(args.dn_graph), bool(args.dn_persistent))
+                                        bool(args.dn_graph), bool(args.dn_persistent), bool(args.dn_batched))
     print(json.dumps(out), flush=True)
     return 0
 

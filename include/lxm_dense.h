@@ -83,6 +83,31 @@ int lxm_dn_step(const lxm_dn_params* p_host, const lxm_dn_params* p_dev, void* s
    (256, 512, 512). Returns a hipError_t. */
 int lxm_dn_run(const lxm_dn_params* p_host, const lxm_dn_params* p_dev, int n, void* stream);
 
+/* The batched prefill's buffers (device, caller-owned; PB = LXM_DN_PB tokens per batch). */
+#define LXM_DN_PB 16
+typedef struct lxm_dn_pbuf {
+  float* h;    /* (PB, hidden): the batch's residuals */
+  float* xn;   /* (PB, hidden): a norm's output, in the weights' interleaved order */
+  float* P;    /* (PB, rows of proj): the projections */
+  float* qk;   /* (PB, nk, 2, 256): the normed query (times 1/16) and key */
+  float* v;    /* (PB, nk x rl x 128): the values after the conv */
+  float* g;    /* (PB, nk x rl, 2): beta and exp(g) */
+  float* live; /* (PB, nk, 2): 1 where the query / key has a nonzero element */
+  float* o;    /* (PB, nk x rl x 128): the delta rule's outputs */
+  float* ys;   /* (PB, nk x rl x 128): the gated norm's output, interleaved */
+  float* act;  /* (PB, inter): SwiGLU's output, interleaved */
+} lxm_dn_pbuf;
+
+/* T forced tokens (device int32) through every layer without the head, in batches of LXM_DN_PB:
+   the states and windows afterwards are those T calls of lxm_dn_step with these forced tokens
+   leave, bit for bit (each weight row is read once per batch; every sum keeps the step's
+   order). The stock generate's prefill role (the prompt before the first prediction, here with
+   the decode's per-token arithmetic); a caller then steps from the next token. A token out of
+   range sets *err = 1 (row 0 is used). Supports (hidden, live value dims, inter) = (2560, 4096,
+   9216) or (256, 512, 512). Returns a hipError_t. */
+int lxm_dn_prefill(const lxm_dn_params* p_host, const int32_t* tokens, int T,
+                   const lxm_dn_pbuf* buf, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -844,6 +844,375 @@ __global__ __launch_bounds__(NT, 1) void dn_run(const lxm_dn_params* __restrict_
 }
 
 // ---------------------------------------------------------------------------------------------
+// The batched prefill (lxm_dn_prefill): T forced tokens through every layer in batches of up to
+// PB tokens, without the head, leaving the states and windows that T calls of lxm_dn_step leave,
+// bit for bit. Per batch and layer: every token's input norm (pb_norm); the projections
+// (pb_rows: each weight row read once per batch; lane l sums its 64th of the row for every token
+// in the step's order, and the 64 lane sums of every (row, token) go through the step's pairwise
+// tree, spread over the lanes); every token's conv, l2norms, beta and decay (pb_prep: token t's
+// window is the previous tokens' projections); the delta rule token by token (pb_gdn); the
+// windows' advance (pb_win); the gated norm (pb_gnorm), out_proj, the post norm, SwiGLU and
+// down_proj (pb_rows). The row kernels' inputs are stored in their weights' interleaved order.
+#define PB LXM_DN_PB
+#define PBT 256  // threads of the row kernels: 4 waves
+
+// position of element c of a row of K = 64 G entries in the interleaved order
+__device__ __forceinline__ int il(int c, int G) {
+  if (G < 8) return c;
+  const int l = c / G, k = c % G;
+  return ((k >> 3) * 64 + l) * 8 + (k & 7);
+}
+
+// V values per lane, each to be summed over the wave by the pairwise tree at offsets 32..1:
+// after the call lane l holds the sums of values l V / 64 .. + max(1, V / 64) - 1 (in v[0..]).
+// At offset o a lane keeps half of its values (the upper half where lane & o) and adds its
+// partner's partial sums of them: the same pairs as the tree's (lane l + lane l + o), since
+// fp32 addition is commutative.
+template <int V, int S>
+__device__ __forceinline__ void tree_scatter(float (&v)[V], int lane) {
+  if constexpr (S < 6) {
+    constexpr int o = 32 >> S, C = V >> S;
+    if constexpr (C >= 2) {
+      const bool up = (lane & o) != 0;
+#pragma unroll
+      for (int i = 0; i < C / 2; i++) {
+        const float send = up ? v[i] : v[i + C / 2];
+        const float keep = up ? v[i + C / 2] : v[i];
+        v[i] = keep + __shfl_xor(send, o);
+      }
+    } else {
+      v[0] = v[0] + __shfl_xor(v[0], o);
+    }
+    tree_scatter<V, S + 1>(v, lane);
+  }
+}
+
+// Rows for a batch of n <= PB tokens: the wave's R rows (MODE 2: R / 2 SwiGLU units, gate rows
+// from W and up rows from W2) over X (n x 64 G, interleaved), staged in LDS one 8-entry chunk per
+// lane at a time. MODE 0: out[b ldo + r] = D(s); 1: out[b ldo + r] = D(out + D(s)) (the
+// residual); 2: out[b ldo + il(u, og)] = D(D(silu(D(g))) * D(u)).
+template <int G, int R, int MODE>
+__global__ __launch_bounds__(PBT) void pb_rows(const uint16_t* __restrict__ W,
+                                               const uint16_t* __restrict__ W2, int nrows,
+                                               const float* __restrict__ X, int n, float* out,
+                                               int ldo, int og) {
+  constexpr int CH = G == 4 ? 4 : 8, NC = G / CH, K = 64 * G, V = R * PB;
+  constexpr int RU = MODE == 2 ? R / 2 : R;  // distinct row indices per wave
+  static_assert(MODE != 2 || (R % 2 == 0 && V == 128), "units: gate and up rows 32 lanes apart");
+  __shared__ v4f xlo[PB * 64];
+  __shared__ v4f xhi[CH == 8 ? PB * 64 : 1];
+  const int lane = tid() & 63;
+  const int wv = blockIdx.x * (PBT / 64) + (tid() >> 6);
+  const uint16_t* rp[R];
+#pragma unroll
+  for (int i = 0; i < R; i++) {
+    int r = wv * RU + i % RU;
+    r = r < nrows ? r : nrows - 1;  // (rows past the end load the last row, unused)
+    rp[i] = (MODE == 2 && i >= RU ? W2 : W) + (int64_t)r * K;
+  }
+  float acc[R][PB];
+#pragma unroll
+  for (int i = 0; i < R; i++)
+#pragma unroll
+    for (int b = 0; b < PB; b++) acc[i][b] = 0.0f;
+  for (int q = 0; q < NC; q++) {
+    v4u w[R];
+#pragma unroll
+    for (int i = 0; i < R; i++) {
+      if constexpr (CH == 8) {
+        w[i] = reinterpret_cast<const v4u*>(rp[i])[q * 64 + lane];
+      } else {
+        const uint2 u = reinterpret_cast<const uint2*>(rp[i])[lane];
+        w[i] = v4u{u.x, u.y, 0u, 0u};
+      }
+    }
+    lds_barrier();  // (the previous chunk's reads are done)
+    for (int idx = tid(); idx < PB * 64; idx += PBT) {
+      const int b = idx >> 6, l = idx & 63;
+      v4f lo = {0.0f, 0.0f, 0.0f, 0.0f}, hi = lo;
+      if (b < n) {
+        const float* src = X + (int64_t)b * K + (int64_t)(q * 64 + l) * CH;
+        lo = *reinterpret_cast<const v4f*>(src);
+        if constexpr (CH == 8) hi = *reinterpret_cast<const v4f*>(src + 4);
+      }
+      xlo[idx] = lo;
+      if constexpr (CH == 8) xhi[idx] = hi;
+    }
+    lds_barrier();
+#pragma unroll
+    for (int b = 0; b < PB; b++) {
+      const v4f lo = xlo[b * 64 + lane];
+      v4f hi = {0.0f, 0.0f, 0.0f, 0.0f};
+      if constexpr (CH == 8) hi = xhi[b * 64 + lane];
+      const float x[8] = {lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
+#pragma unroll
+      for (int i = 0; i < R; i++)
+#pragma unroll
+        for (int k = 0; k < CH / 2; k++) {
+          const uint32_t ww = w[i][k];
+          acc[i][b] = __builtin_fmaf(bitsf(ww << 16), x[2 * k], acc[i][b]);
+          acc[i][b] = __builtin_fmaf(bitsf(ww & 0xffff0000u), x[2 * k + 1], acc[i][b]);
+        }
+    }
+  }
+  float v[V];
+#pragma unroll
+  for (int i = 0; i < R; i++)
+#pragma unroll
+    for (int b = 0; b < PB; b++) v[i * PB + b] = acc[i][b];
+  tree_scatter<V, 0>(v, lane);
+  // (V < 64: 64 / V lanes hold each sum; the first of them stores it)
+  constexpr int PER = V >= 64 ? V / 64 : 1;
+  if (V < 64 && lane % (V < 64 ? 64 / V : 1) != 0) return;
+#pragma unroll
+  for (int j = 0; j < PER; j++) {
+    const int vi = (lane * V) / 64 + j;
+    const int i = vi / PB, b = vi % PB;
+    if constexpr (MODE == 2) {
+      const float u = __shfl_xor(v[j], 32);  // (the up row's sum, 32 lanes on)
+      const int unit = wv * RU + i;
+      if (lane < 32 && unit < nrows && b < n)
+        out[(int64_t)b * ldo + il(unit, og)] = bf16r(silu_bf16(bf16r(v[j])) * bf16r(u));
+    } else {
+      const int r = wv * RU + i;
+      if (r < nrows && b < n) {
+        float* o = out + (int64_t)b * ldo + r;
+        if constexpr (MODE == 0) *o = bf16r(v[j]);
+        else *o = bf16r(*o + bf16r(v[j]));
+      }
+    }
+  }
+}
+
+// every token's embedding row into its residual
+__global__ __launch_bounds__(PBT) void pb_embed(const uint16_t* __restrict__ embed,
+                                                const int32_t* __restrict__ tokens, int H,
+                                                int vocab, float* h, int32_t* err) {
+  const int b = blockIdx.x;
+  int tok = tokens[b];
+  if (tok < 0 || tok >= vocab) {
+    if (tid() == 0) *err = 1;
+    tok = 0;
+  }
+  const uint16_t* e = embed + (int64_t)tok * H;
+  const int G = H / 64;
+  for (int c = tid(); c < H; c += PBT) h[(int64_t)b * H + c] = bf16f(e[il(c, G)]);
+}
+
+// every token's RMSNorm (the step's factor and elements) into xn, interleaved for G = gx
+__global__ __launch_bounds__(NT) void pb_norm(const float* __restrict__ h,
+                                              const float* __restrict__ nw, float eps, int H,
+                                              int gx, float* xn) {
+  __shared__ float wsum[NW];
+  const int b = blockIdx.x;
+  const float* hb = h + (int64_t)b * H;
+  const float r = norm_factor<false>(hb, H, eps, wsum);
+  for (int c = tid(); c < H; c += NT) xn[(int64_t)b * H + il(c, gx)] = norm_el(hb[c], r, nw[c]);
+}
+
+struct PbGdn {
+  const uint16_t* conv_qk;  // (2, nk, kl, 4)
+  const uint16_t* conv_v;   // (nk, rl, 128, 4)
+  const float* A_log;
+  const float* dt_bias;
+  float* rec;
+  uint16_t* conv;
+  const float* P;           // (n, nproj)
+  float* qk;                // (n, nk, 2, 256)
+  float* v;                 // (n, nvr)
+  float* g;                 // (n, nk rl, 2)
+  float* live;              // (n, nk, 2)
+  float* o;                 // (n, nvr)
+  int nk, kl, rl, R, nproj, n;
+};
+// conv_y for token b of the batch: the window [x(b-3), x(b-2), x(b-1)] is the batch's earlier
+// projections (row ch of P) or, before the batch, the stored window's newest values
+__device__ __forceinline__ float conv_b(uint64_t win, const uint16_t* taps, const float* P,
+                                        int nproj, int ch, int b) {
+  float y = 0.0f;
+#pragma unroll
+  for (int k = 0; k < 4; k++) {
+    const int idx = b - 3 + k;
+    const float x = idx >= 0 ? P[(int64_t)idx * nproj + ch]
+                             : bf16f((uint32_t)(win >> (16 * (idx + 4))) & 0xffffu);
+    y = __builtin_fmaf(bf16f(taps[k]), x, y);
+  }
+  return silu_bf16(bf16r(y));
+}
+// one workgroup per (token, key head): the query and key (conv, l2norm in the model dtype, the
+// query times 1/16, and whether any element is nonzero), the key head's value channels, and its
+// value heads' beta and exp(g), as the step's delta-rule kernel forms them
+__global__ __launch_bounds__(KD) void pb_prep(PbGdn a) {
+  __shared__ float qd[KD], kd[KD];
+  const int b = blockIdx.x, kh = blockIdx.y, t = tid(), lane = t & 63, wv = t >> 6;
+  const int nk = a.nk, kl = a.kl, rl = a.rl, nq = nk * kl, nvr = nk * rl * VD;
+  float q = 0.0f, k = 0.0f;
+  if (t < kl) {
+    const int64_t cq = (int64_t)kh * KD + t, ck = (int64_t)nk * KD + kh * KD + t;
+    q = conv_b(ldw<false>(a.conv + cq * 4), a.conv_qk + ((int64_t)kh * kl + t) * 4, a.P, a.nproj,
+               kh * kl + t, b);
+    k = conv_b(ldw<false>(a.conv + ck * 4), a.conv_qk + ((int64_t)(nk + kh) * kl + t) * 4, a.P,
+               a.nproj, nq + kh * kl + t, b);
+  }
+  qd[t] = q;
+  kd[t] = k;
+  for (int c = t; c < rl * VD; c += KD) {
+    const int vslot = kh * rl + c / VD, d = c % VD, vh = kh * a.R + c / VD;
+    const uint64_t win = ldw<false>(a.conv + (2 * (int64_t)nk * KD + (int64_t)vh * VD + d) * 4);
+    a.v[(int64_t)b * nvr + vslot * VD + d] =
+        conv_b(win, a.conv_v + ((int64_t)vslot * VD + d) * 4, a.P, a.nproj, 2 * nq + vslot * VD + d, b);
+  }
+  if (t < rl) {
+    const int vslot = kh * rl + t, vh = kh * a.R + t;
+    const float* Pb = a.P + (int64_t)b * a.nproj;
+    const float bb = Pb[2 * nq + 2 * nvr + vslot], aa = Pb[2 * nq + 2 * nvr + nk * rl + vslot];
+    float* g = a.g + ((int64_t)b * nk * rl + vslot) * 2;
+    g[0] = bf16r(sigmoid(bb));
+    g[1] = cr_exp((-cr_exp(a.A_log[vh])) * softplus(aa + a.dt_bias[vh]));
+  }
+  lds_barrier();
+  if (wv < 2) {
+    const float* x = wv ? kd : qd;
+    float* o = a.qk + (((int64_t)b * nk + kh) * 2 + wv) * KD;
+    float xs[4], ss = 0.0f;
+    bool nz = false;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      xs[i] = x[lane + 64 * i];
+      nz |= xs[i] != 0.0f;
+      ss = ss + bf16r(xs[i] * xs[i]);
+    }
+    const bool any = __ballot(nz) != 0ull;
+    ss = bf16r(sum64(ss));
+    const float inv = bf16r(rsqrt_(bf16r(ss + 1e-6f)));
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      float v = bf16r(xs[i] * inv);
+      if (!wv) v = v * 0.0625f;
+      o[lane + 64 * i] = v;
+    }
+    if (lane == 0) a.live[((int64_t)b * nk + kh) * 2 + wv] = any ? 1.0f : 0.0f;
+  }
+}
+// the delta rule of one live value head's 32 state columns (nk x rl x QC workgroups, as the
+// step's) over the batch's tokens in order, the tile in registers throughout
+struct PbLds {
+  float qk[PB][2][KD];
+  float vb[PB][QW], bg[PB][2], lv[PB];
+  float bsk[16 * QW], bso[16 * QW], dl[QW];
+};
+__global__ __launch_bounds__(NT) void pb_gdn(PbGdn a) {
+  __shared__ PbLds l;
+  const int t = tid(), blk = blockIdx.x;
+  const int nk = a.nk, rl = a.rl, nvr = nk * rl * VD, n = a.n;
+  const int vslot = blk / QC, c0 = (blk % QC) * QW, kh = vslot / rl, vh = kh * a.R + vslot % rl;
+  const int c = t % QW, rb = t / QW;
+  float* S = a.rec + (size_t)vh * KD * VD + c0 + c + rb * 16 * VD;
+  float s[16];
+#pragma unroll
+  for (int i = 0; i < 16; i++) s[i] = S[i * VD];
+  for (int i = t; i < n * 2 * KD; i += NT) {
+    const int b = i / (2 * KD), j = i % (2 * KD);
+    (&l.qk[b][0][0])[j] = a.qk[((int64_t)b * nk + kh) * 2 * KD + j];
+  }
+  for (int i = t; i < n * QW; i += NT) {
+    const int b = i / QW, j = i % QW;
+    l.vb[b][j] = a.v[(int64_t)b * nvr + vslot * VD + c0 + j];
+  }
+  if (t < n) {
+    const float* g = a.g + ((int64_t)t * nk * rl + vslot) * 2;
+    l.bg[t][0] = g[0];
+    l.bg[t][1] = g[1];
+    const float* lv = a.live + ((int64_t)t * nk + kh) * 2;
+    l.lv[t] = lv[0] != 0.0f || lv[1] != 0.0f ? 1.0f : 0.0f;
+  }
+  lds_barrier();
+  for (int b = 0; b < n; b++) {
+    const float beta = l.bg[b][0], e = l.bg[b][1];
+    if (e != 1.0f) {
+#pragma unroll
+      for (int i = 0; i < 16; i++) s[i] = s[i] * e;
+    }
+    float* o_out = a.o + (int64_t)b * nvr + vslot * VD + c0;
+    if (l.lv[b] != 0.0f) {
+      const float* kr = &l.qk[b][1][rb * 16];
+      const float* qr = &l.qk[b][0][rb * 16];
+      float acc = 0.0f;
+#pragma unroll
+      for (int i = 0; i < 16; i++) acc = kr[i] != 0.0f ? acc + s[i] * kr[i] : acc;
+      l.bsk[rb * QW + c] = acc;
+      lds_barrier();
+      if (t < QW) {
+        float kv = 0.0f;
+#pragma unroll
+        for (int q = 0; q < 16; q++) kv = kv + l.bsk[q * QW + t];
+        l.dl[t] = (l.vb[b][t] - kv) * beta;
+      }
+      lds_barrier();
+      const float d = l.dl[c];
+      float o = 0.0f;
+#pragma unroll
+      for (int i = 0; i < 16; i++) {
+        s[i] = kr[i] != 0.0f ? s[i] + kr[i] * d : s[i];
+        o = qr[i] != 0.0f ? o + s[i] * qr[i] : o;
+      }
+      l.bso[rb * QW + c] = o;
+      lds_barrier();
+      if (t < QW) {
+        float q = 0.0f;
+#pragma unroll
+        for (int j = 0; j < 16; j++) q = q + l.bso[j * QW + t];
+        o_out[t] = bf16r(q);
+      }
+    } else if (t < QW) {
+      o_out[t] = 0.0f;
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < 16; i++) S[i * VD] = s[i];
+}
+// every live channel's window after the batch: its last 4 inputs (the step's shift, n times)
+__global__ void pb_win(uint16_t* conv, const float* __restrict__ P, int nproj, int n, int nk,
+                       int kl, int rl, int R) {
+  const int nq = nk * kl, nch = 2 * nq + nk * rl * VD;
+  for (int i = blockIdx.x * blockDim.x + tid(); i < nch; i += gridDim.x * blockDim.x) {
+    int64_t wch;
+    if (i < 2 * nq) {
+      const int part = i / nq, j = i % nq, kh = j / kl, d = j % kl;
+      wch = (int64_t)part * nk * KD + kh * KD + d;
+    } else {
+      const int j = i - 2 * nq, vslot = j / VD, d = j % VD;
+      const int vh = (vslot / rl) * R + vslot % rl;
+      wch = 2 * (int64_t)nk * KD + (int64_t)vh * VD + d;
+    }
+    uint64_t* w = reinterpret_cast<uint64_t*>(conv + wch * 4);
+    const uint64_t old = *w;
+    uint64_t nw = 0;
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+      const int idx = n - 4 + j;
+      const uint64_t v = idx >= 0 ? (uint64_t)(fbits(P[(int64_t)idx * nproj + i]) >> 16)
+                                  : (old >> (16 * (idx + 4))) & 0xffffu;
+      nw |= v << (16 * j);
+    }
+    *w = nw;
+  }
+}
+// every token's gated norm of the live heads (the step's, 4 waves) into ys, interleaved for G = gv
+__global__ __launch_bounds__(PBT) void pb_gnorm(const float* __restrict__ o,
+                                                const float* __restrict__ P, int nproj, int zoff,
+                                                const float* __restrict__ gw, float geps, int nh,
+                                                int gv, float* ys) {
+  __shared__ float y[4096];
+  const int b = blockIdx.x, nvr = nh * VD;
+  const DnOut d{nullptr, 0, nh, o + (int64_t)b * nvr, P + (int64_t)b * nproj + zoff, gw, geps,
+                nullptr, nullptr, nullptr, 0, 0};
+  gated_norm<PBT / 64, false>(d, y);
+  lds_barrier();
+  for (int c = tid(); c < nvr; c += PBT) ys[(int64_t)b * nvr + il(c, gv)] = y[c];
+}
+
+// ---------------------------------------------------------------------------------------------
 // Host side. Launch shapes (measured on MI355X over these matrices): the hidden rows (out_proj,
 // down_proj: few long rows) in 4-wave workgroups, one per CU, each wave taking rows in turn;
 // the wide sets (projections, SwiGLU units, the head) in 8-wave workgroups, two per CU.
@@ -984,4 +1353,55 @@ extern "C" int lxm_dn_run(const lxm_dn_params* ph, const lxm_dn_params* pd, int 
   if (gh == 40 && gv == 64 && gi == 144) return launch_run<40, 64, 144>(pd, n, n_cus, st);
   if (gh == 4 && gv == 8 && gi == 8) return launch_run<4, 8, 8>(pd, n, n_cus, st);
   return (int)hipErrorInvalidValue;
+}
+
+// the batched prefill's row kernels: R rows per wave (MODE 2: R / 2 units), 4 waves per workgroup
+template <int G, int R, int MODE>
+static void launch_pb(const uint16_t* W, const uint16_t* W2, int nrows, const float* X, int n,
+                      float* out, int ldo, int og, hipStream_t st) {
+  const int per = (PBT / 64) * (MODE == 2 ? R / 2 : R);
+  hipLaunchKernelGGL((pb_rows<G, R, MODE>), dim3((nrows + per - 1) / per), dim3(PBT), 0, st, W, W2,
+                     nrows, X, n, out, ldo, og);
+}
+// (G of the hidden rows, live value dims, inter) = (40, 64, 144) or (4, 8, 8)
+template <int GH, int GV, int GI>
+static void pb_layer(const lxm_dn_params* ph, const lxm_dn_layer& ly, const lxm_dn_pbuf* pb, int n,
+                     hipStream_t st) {
+  const int H = ph->hidden, I = ph->inter, nk = ph->nk, kl = ph->kl, rl = ph->rl, R = ph->nv / nk;
+  const int nq = nk * kl, nvr = nk * rl * VD, nproj = 2 * nq + 2 * nvr + 2 * nk * rl;
+  const float eps = ph->rms_eps;
+  hipLaunchKernelGGL(pb_norm, dim3(n), dim3(NT), 0, st, pb->h, ly.ln_in, eps, H, GH, pb->xn);
+  launch_pb<GH, 8, 0>(ly.proj, nullptr, nproj, pb->xn, n, pb->P, nproj, 0, st);
+  const PbGdn g{ly.conv_qk, ly.conv_v, ly.A_log, ly.dt_bias, ly.rec, ly.conv, pb->P, pb->qk,
+                pb->v, pb->g, pb->live, pb->o, nk, kl, rl, R, nproj, n};
+  hipLaunchKernelGGL(pb_prep, dim3(n, nk), dim3(KD), 0, st, g);
+  hipLaunchKernelGGL(pb_gdn, dim3(nk * rl * QC), dim3(NT), 0, st, g);
+  const int nch = 2 * nq + nvr;
+  hipLaunchKernelGGL(pb_win, dim3((nch + 255) / 256), dim3(256), 0, st, ly.conv, pb->P, nproj, n,
+                     nk, kl, rl, R);
+  hipLaunchKernelGGL(pb_gnorm, dim3(n), dim3(PBT), 0, st, pb->o, pb->P, nproj, 2 * nq + nvr,
+                     ly.gnorm, ph->geps, nk * rl, GV, pb->ys);
+  launch_pb<GV, 2, 1>(ly.out, nullptr, H, pb->ys, n, pb->h, H, 0, st);
+  hipLaunchKernelGGL(pb_norm, dim3(n), dim3(NT), 0, st, pb->h, ly.ln_post, eps, H, GH, pb->xn);
+  launch_pb<GH, 8, 2>(ly.gate, ly.up, I, pb->xn, n, pb->act, I, GI, st);
+  launch_pb<GI, 2, 1>(ly.down, nullptr, H, pb->act, n, pb->h, H, 0, st);
+}
+
+extern "C" int lxm_dn_prefill(const lxm_dn_params* ph, const int32_t* tokens, int T,
+                              const lxm_dn_pbuf* pb, void* stream) {
+  if (!dims_ok(ph) || !pb || !tokens || T < 0) return (int)hipErrorInvalidValue;
+  const int gh = g_of(ph->hidden), gv = g_of(ph->nk * ph->rl * VD), gi = g_of(ph->inter);
+  const bool full = gh == 40 && gv == 64 && gi == 144, small = gh == 4 && gv == 8 && gi == 8;
+  if (!full && !small) return (int)hipErrorInvalidValue;
+  hipStream_t st = (hipStream_t)stream;
+  for (int b0 = 0; b0 < T; b0 += PB) {
+    const int n = T - b0 < PB ? T - b0 : PB;
+    hipLaunchKernelGGL(pb_embed, dim3(n), dim3(PBT), 0, st, ph->embed, tokens + b0, ph->hidden,
+                       ph->vocab, pb->h, ph->err);
+    for (int L = 0; L < ph->n_layers; L++) {
+      if (full) pb_layer<40, 64, 144>(ph, ph->layers_host[L], pb, n, st);
+      else pb_layer<4, 8, 8>(ph, ph->layers_host[L], pb, n, st);
+    }
+  }
+  return (int)hipGetLastError();
 }

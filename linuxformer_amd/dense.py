@@ -4,6 +4,8 @@ kernels (csrc/lxm_dense.hip, C ABI include/lxm_dense.h).
     dd = DenseDecode(model, cache)            # model: synth.DenseModel on the GPU
     preds = dd.run(forced, n)                 # lx.mega's run semantics: step i's input is
                                               # forced[i] (i < len(forced)), else pred[i - 1]
+    dd.prefill(prompt[:-1]); dd.run(prompt[-1:], n)   # the same states and predictions from the
+                                              # last prompt token on, the prompt in batches
 
 By default ``run`` calls lxm_dn_step per step (embedding, 24 layers, the head's argmax, the token
 fed back), whose step counter and fed-back token live on the device, so it captures a step in a
@@ -28,6 +30,13 @@ class DnLayer(ctypes.Structure):
     _fields_ = [(n, P64) for n in ("proj", "conv_qk", "conv_v", "A_log", "dt_bias", "gnorm",
                                    "ln_in", "ln_post", "out", "gate", "up", "down", "rec",
                                    "conv")]
+
+
+class DnPbuf(ctypes.Structure):
+    _fields_ = [(n, P64) for n in ("h", "xn", "P", "qk", "v", "g", "live", "o", "ys", "act")]
+
+
+PB = 16  # tokens per prefill batch (LXM_DN_PB)
 
 
 class DnParams(ctypes.Structure):
@@ -108,6 +117,7 @@ class DenseDecode:
         self.forced = torch.zeros(max_steps, dtype=torch.int32, device=dev)
         self.max_steps = max_steps
         self.graph = None
+        self._pb = None
 
     def _params(self, n_forced: int):
         sp, d = self.spec, self.dims
@@ -124,6 +134,43 @@ class DenseDecode:
                      sync=self.sync.data_ptr())
         pd = torch.frombuffer(bytearray(bytes(p)), dtype=torch.uint8).to(self.dev)
         return p, pd
+
+    def _pbuf(self):
+        """The batched prefill's buffers (allocated on first use)."""
+        if self._pb is None:
+            sp, d = self.spec, self.dims
+            H, nk, rl, I = sp.hidden, sp.nk, sp.r_live, sp.inter
+            nvr = nk * rl * 128
+            sizes = dict(h=H, xn=H, P=self.nproj, qk=nk * 2 * 256, v=nvr, g=nk * rl * 2,
+                         live=nk * 2, o=nvr, ys=nvr, act=I)
+            self._pb_t = {k: torch.zeros(PB * n, dtype=torch.float32, device=self.dev)
+                          for k, n in sizes.items()}
+            self._pb = DnPbuf(**{k: t.data_ptr() for k, t in self._pb_t.items()})
+        return self._pb
+
+    @torch.no_grad()
+    def prefill(self, tokens) -> None:
+        """The tokens through every layer without the head (lxm_dn_prefill, batches of PB tokens,
+        each weight row read once per batch): the cache's states and windows afterwards are those
+        of len(tokens) forced steps of run(), bit for bit; no predictions are made. A caller then
+        steps from the next token: run([next], n)."""
+        t = torch.as_tensor(tokens, dtype=torch.int64)
+        if t.numel() == 0:
+            return
+        if int(t.min()) < 0 or int(t.max()) >= self.spec.vocab:
+            raise ValueError("prefill token out of range")
+        pb = self._pbuf()
+        tok = t.to(torch.int32).to(self.dev)
+        self.err.zero_()
+        p, _ = self._params(1)
+        st = ctypes.c_void_p(torch.cuda.current_stream(self.dev).cuda_stream)
+        e = self.lib.lxm_dn_prefill(ctypes.byref(p), ctypes.c_void_p(tok.data_ptr()), int(t.numel()),
+                                    ctypes.byref(pb), st)
+        if e:
+            raise RuntimeError(f"dense prefill launch failed: hipError {e}")
+        torch.cuda.synchronize(self.dev)
+        if int(self.err.item()):
+            raise RuntimeError("dense prefill: a token out of range")
 
     def _step(self) -> None:
         st = ctypes.c_void_p(torch.cuda.current_stream(self.dev).cuda_stream)

@@ -100,10 +100,13 @@ def load(subprof: bool = False) -> ctypes.CDLL:
         lib.lxm_dn_step.restype = I
         lib.lxm_dn_run.argtypes = [P, P, I, P]
         lib.lxm_dn_run.restype = I
+        lib.lxm_dn_prefill.argtypes = [P, P, I, P, P]
+        lib.lxm_dn_prefill.restype = I
         _libs[path] = lib
     return _libs[path]
 
 
 EXPORTS = ("lxm_run", "lxm_lds_base", "lxm_helper_lds", "lxm_max_blocks", "lxm_max_lds",
            "lxm_last_error", "lxm_device_cus", "lxm_t_elem", "lxm_t_sum", "lxm_pf_layers",
-           "lxm_pf_head", "lxm_pf_embed", "lxm_pf_tiles", "lxm_pf_lds", "lxm_dn_step", "lxm_dn_run")
+           "lxm_pf_head", "lxm_pf_embed", "lxm_pf_tiles", "lxm_pf_lds", "lxm_dn_step", "lxm_dn_run",
+           "lxm_dn_prefill")

@@ -1,6 +1,6 @@
 """Parity of the HIP dense decode (BASELINE config 4's structure) with the oracle on an MI355X,
-through the C ABI (the persistent run, lxm_dn_run, and the per-step kernels, lxm_dn_step):
-predictions and final states bit for bit. The dense projections are summed in
+through the C ABI (the persistent run, lxm_dn_run, the per-step kernels, lxm_dn_step, and the
+batched prefill, lxm_dn_prefill, followed by steps): predictions and final states bit for bit. The dense projections are summed in
 the dense order the oracle restates for matrices marked dense (64 groups of a row's entries in
 order from +0, then the pairwise tree); everything else follows the stock decode as in the
 sparse paths. Sizes: config 4's layout scaled down (hidden 256, 2 layers) so the oracle runs in
@@ -90,6 +90,45 @@ def test_dense_full_widths(cuda, mode):
     """Config 4's full row lengths (hidden 2560: 40 entries per lane; SwiGLU 9216: 144; 16 key
     heads x 2 live value heads: 4096 out_proj entries, 64) over one layer, from live states."""
     check(3, 6, seed=5, name="mid", mode=mode)
+
+
+def check_prefill(T, n, seed=None, name="small"):
+    """lxm_dn_prefill over T - 1 forced tokens, then n steps from the last one: the predictions
+    and states of T - 1 + n steps of the oracle with the same T forced tokens."""
+    from oracle import oracle as ox
+
+    spec, dm_cpu, sm = model(name)
+    conv0, rec0 = synth.dense_state(dm_cpu, seed)
+    toks = [int(x) for x in np.random.default_rng(11 + T).integers(0, spec.vocab, T)]
+    print(f"[gpu-test] dense prefill {spec.name}: T={T} n={n} seed={seed}", flush=True)
+    dm = synth.dense_to(dm_cpu, "cuda")
+    cache = fast.StateCache(conv0, rec0, "bf16", "cuda")
+    dd = dense.DenseDecode(dm, cache)
+    dd.prefill(toks[:-1])
+    preds = dd.run(toks[-1:], n)
+    c, r = conv0.copy(), rec0.copy()
+    po, _, _ = ox.OracleModel(sm).decode(c, r, toks, T - 1 + n)
+    assert preds == po.tolist()[T - 1:]
+    assert (bits(cache.conv_numpy()) == bits(c)).all()
+    assert (bits(cache.rec_numpy()) == bits(r)).all()
+
+
+@pytest.mark.parametrize("T,seed", [(40, None), (3, 3), (34, 3)])
+def test_dense_prefill_small(cuda, T, seed):
+    """Batches of 16 (the last one partial), a prompt shorter than the conv window, live states."""
+    check_prefill(T, 6, seed=seed)
+
+
+def test_dense_prefill_full_widths(cuda):
+    check_prefill(21, 3, seed=5, name="mid")
+
+
+def test_dense_prefill_rejects_bad_token(cuda):
+    spec, dm_cpu, _ = model()
+    conv0, rec0 = synth.dense_state(dm_cpu)
+    dd = dense.DenseDecode(synth.dense_to(dm_cpu, "cuda"), fast.StateCache(conv0, rec0, "bf16", "cuda"))
+    with pytest.raises(ValueError, match="out of range"):
+        dd.prefill([1, spec.vocab])
 
 
 def test_dense_rejects_dead_state(cuda):
