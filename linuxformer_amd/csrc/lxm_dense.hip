@@ -850,9 +850,10 @@ __global__ __launch_bounds__(NT, 1) void dn_run(const lxm_dn_params* __restrict_
 // (pb_rows: each weight row read once per batch; lane l sums its 64th of the row for every token
 // in the step's order, and the 64 lane sums of every (row, token) go through the step's pairwise
 // tree, spread over the lanes); every token's conv, l2norms, beta and decay (pb_prep: token t's
-// window is the previous tokens' projections); the delta rule token by token (pb_gdn); the
-// windows' advance (pb_win); the gated norm (pb_gnorm), out_proj, the post norm, SwiGLU and
-// down_proj (pb_rows). The row kernels' inputs are stored in their weights' interleaved order.
+// window is the previous tokens' projections); the delta rule token by token (pb_gdn); the gated
+// norm and the windows' advance (pb_gnorm); out_proj (pb_hrows), the post norm, SwiGLU (pb_rows)
+// and down_proj (pb_hrows). The row kernels' inputs are stored in their weights' interleaved
+// order.
 #define PB LXM_DN_PB
 #define PBT 256  // threads of the row kernels: 4 waves
 
@@ -981,6 +982,82 @@ __global__ __launch_bounds__(PBT) void pb_rows(const uint16_t* __restrict__ W,
         else *o = bf16r(*o + bf16r(v[j]));
       }
     }
+  }
+}
+
+// Long rows (out_proj, down_proj: few rows of many entries) for a batch of PB tokens: the
+// workgroup's 4 waves share R rows, wave w taking tokens w BW .. w BW + BW - 1 (BW = PB / 4), each
+// wave reading its tokens' inputs straight from X (no LDS, no barriers: the rows are too few to
+// share a staged input among many waves). Sums and MODEs as pb_rows (0 and 1).
+template <int G, int R, int MODE>
+__global__ __launch_bounds__(PBT) void pb_hrows(const uint16_t* __restrict__ W, int nrows,
+                                                const float* __restrict__ X, int n, float* out,
+                                                int ldo) {
+  constexpr int CH = G == 4 ? 4 : 8, NC = G / CH, K = 64 * G, BW = PB / (PBT / 64), V = R * BW;
+  static_assert(V <= 64 && 64 % V == 0, "one sum per lane group");
+  const int lane = tid() & 63, wvl = tid() >> 6;
+  const int r0 = blockIdx.x * R, b0 = wvl * BW;
+  const uint16_t* rp[R];
+#pragma unroll
+  for (int i = 0; i < R; i++) {
+    const int r = r0 + i < nrows ? r0 + i : nrows - 1;
+    rp[i] = W + (int64_t)r * K;
+  }
+  const float* xp[BW];
+#pragma unroll
+  for (int b = 0; b < BW; b++) {
+    const int bb = b0 + b < n ? b0 + b : n - 1;  // (tokens past n read token n - 1, unused)
+    xp[b] = X + (int64_t)bb * K;
+  }
+  float acc[R][BW];
+#pragma unroll
+  for (int i = 0; i < R; i++)
+#pragma unroll
+    for (int b = 0; b < BW; b++) acc[i][b] = 0.0f;
+  for (int q = 0; q < NC; q++) {
+    v4u w[R];
+    float x[BW][8];
+#pragma unroll
+    for (int i = 0; i < R; i++) {
+      if constexpr (CH == 8) {
+        w[i] = reinterpret_cast<const v4u*>(rp[i])[q * 64 + lane];
+      } else {
+        const uint2 u = reinterpret_cast<const uint2*>(rp[i])[lane];
+        w[i] = v4u{u.x, u.y, 0u, 0u};
+      }
+    }
+#pragma unroll
+    for (int b = 0; b < BW; b++) {
+      const float* src = xp[b] + (int64_t)(q * 64 + lane) * CH;
+      const v4f lo = *reinterpret_cast<const v4f*>(src);
+      v4f hi = {0.0f, 0.0f, 0.0f, 0.0f};
+      if constexpr (CH == 8) hi = *reinterpret_cast<const v4f*>(src + 4);
+      x[b][0] = lo.x; x[b][1] = lo.y; x[b][2] = lo.z; x[b][3] = lo.w;
+      x[b][4] = hi.x; x[b][5] = hi.y; x[b][6] = hi.z; x[b][7] = hi.w;
+    }
+#pragma unroll
+    for (int b = 0; b < BW; b++)
+#pragma unroll
+      for (int i = 0; i < R; i++)
+#pragma unroll
+        for (int k = 0; k < CH / 2; k++) {
+          const uint32_t ww = w[i][k];
+          acc[i][b] = __builtin_fmaf(bitsf(ww << 16), x[b][2 * k], acc[i][b]);
+          acc[i][b] = __builtin_fmaf(bitsf(ww & 0xffff0000u), x[b][2 * k + 1], acc[i][b]);
+        }
+  }
+  float v[V];
+#pragma unroll
+  for (int i = 0; i < R; i++)
+#pragma unroll
+    for (int b = 0; b < BW; b++) v[i * BW + b] = acc[i][b];
+  tree_scatter<V, 0>(v, lane);
+  if (lane % (64 / V) != 0) return;  // (64 / V lanes hold each sum; the first stores it)
+  const int vi = (lane * V) / 64, i = vi / BW, b = b0 + vi % BW, r = r0 + i;
+  if (r < nrows && b < n) {
+    float* o = out + (int64_t)b * ldo + r;
+    if constexpr (MODE == 0) *o = bf16r(v[0]);
+    else *o = bf16r(*o + bf16r(v[0]));
   }
 }
 
@@ -1171,11 +1248,12 @@ __global__ __launch_bounds__(NT) void pb_gdn(PbGdn a) {
 #pragma unroll
   for (int i = 0; i < 16; i++) S[i * VD] = s[i];
 }
-// every live channel's window after the batch: its last 4 inputs (the step's shift, n times)
-__global__ void pb_win(uint16_t* conv, const float* __restrict__ P, int nproj, int n, int nk,
-                       int kl, int rl, int R) {
+// every live channel's window after the batch: its last 4 inputs (the step's shift, n times);
+// thread i0 of ni takes channels i0, i0 + ni, ...
+__device__ __forceinline__ void win_after(uint16_t* conv, const float* __restrict__ P, int nproj,
+                                          int n, int nk, int kl, int rl, int R, int i0, int ni) {
   const int nq = nk * kl, nch = 2 * nq + nk * rl * VD;
-  for (int i = blockIdx.x * blockDim.x + tid(); i < nch; i += gridDim.x * blockDim.x) {
+  for (int i = i0; i < nch; i += ni) {
     int64_t wch;
     if (i < 2 * nq) {
       const int part = i / nq, j = i % nq, kh = j / kl, d = j % kl;
@@ -1198,11 +1276,13 @@ __global__ void pb_win(uint16_t* conv, const float* __restrict__ P, int nproj, i
     *w = nw;
   }
 }
-// every token's gated norm of the live heads (the step's, 4 waves) into ys, interleaved for G = gv
+// every token's gated norm of the live heads (the step's, 4 waves) into ys, interleaved for G =
+// gv; then (the delta rule having read them) the windows' advance
 __global__ __launch_bounds__(PBT) void pb_gnorm(const float* __restrict__ o,
                                                 const float* __restrict__ P, int nproj, int zoff,
                                                 const float* __restrict__ gw, float geps, int nh,
-                                                int gv, float* ys) {
+                                                int gv, float* ys, uint16_t* conv, int n, int nk,
+                                                int kl, int rl, int R) {
   __shared__ float y[4096];
   const int b = blockIdx.x, nvr = nh * VD;
   const DnOut d{nullptr, 0, nh, o + (int64_t)b * nvr, P + (int64_t)b * nproj + zoff, gw, geps,
@@ -1210,6 +1290,7 @@ __global__ __launch_bounds__(PBT) void pb_gnorm(const float* __restrict__ o,
   gated_norm<PBT / 64, false>(d, y);
   lds_barrier();
   for (int c = tid(); c < nvr; c += PBT) ys[(int64_t)b * nvr + il(c, gv)] = y[c];
+  win_after(conv, P, nproj, n, nk, kl, rl, R, blockIdx.x * PBT + tid(), gridDim.x * PBT);
 }
 
 // ---------------------------------------------------------------------------------------------
@@ -1363,6 +1444,14 @@ static void launch_pb(const uint16_t* W, const uint16_t* W2, int nrows, const fl
   hipLaunchKernelGGL((pb_rows<G, R, MODE>), dim3((nrows + per - 1) / per), dim3(PBT), 0, st, W, W2,
                      nrows, X, n, out, ldo, og);
 }
+// the residual's long rows: 8 rows per workgroup, the batch's tokens split over its 4 waves
+template <int G>
+static void launch_hrows(const uint16_t* W, int nrows, const float* X, int n, float* out, int ldo,
+                         hipStream_t st) {
+  constexpr int R = 8;
+  hipLaunchKernelGGL((pb_hrows<G, R, 1>), dim3((nrows + R - 1) / R), dim3(PBT), 0, st, W, nrows, X,
+                     n, out, ldo);
+}
 // (G of the hidden rows, live value dims, inter) = (40, 64, 144) or (4, 8, 8)
 template <int GH, int GV, int GI>
 static void pb_layer(const lxm_dn_params* ph, const lxm_dn_layer& ly, const lxm_dn_pbuf* pb, int n,
@@ -1376,15 +1465,12 @@ static void pb_layer(const lxm_dn_params* ph, const lxm_dn_layer& ly, const lxm_
                 pb->v, pb->g, pb->live, pb->o, nk, kl, rl, R, nproj, n};
   hipLaunchKernelGGL(pb_prep, dim3(n, nk), dim3(KD), 0, st, g);
   hipLaunchKernelGGL(pb_gdn, dim3(nk * rl * QC), dim3(NT), 0, st, g);
-  const int nch = 2 * nq + nvr;
-  hipLaunchKernelGGL(pb_win, dim3((nch + 255) / 256), dim3(256), 0, st, ly.conv, pb->P, nproj, n,
-                     nk, kl, rl, R);
   hipLaunchKernelGGL(pb_gnorm, dim3(n), dim3(PBT), 0, st, pb->o, pb->P, nproj, 2 * nq + nvr,
-                     ly.gnorm, ph->geps, nk * rl, GV, pb->ys);
-  launch_pb<GV, 2, 1>(ly.out, nullptr, H, pb->ys, n, pb->h, H, 0, st);
+                     ly.gnorm, ph->geps, nk * rl, GV, pb->ys, ly.conv, n, nk, kl, rl, R);
+  launch_hrows<GV>(ly.out, H, pb->ys, n, pb->h, H, st);
   hipLaunchKernelGGL(pb_norm, dim3(n), dim3(NT), 0, st, pb->h, ly.ln_post, eps, H, GH, pb->xn);
   launch_pb<GH, 8, 2>(ly.gate, ly.up, I, pb->xn, n, pb->act, I, GI, st);
-  launch_pb<GI, 2, 1>(ly.down, nullptr, H, pb->act, n, pb->h, H, 0, st);
+  launch_hrows<GI>(ly.down, H, pb->act, n, pb->h, H, st);
 }
 
 extern "C" int lxm_dn_prefill(const lxm_dn_params* ph, const int32_t* tokens, int T,
