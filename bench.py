@@ -2,7 +2,7 @@
 verified-prefill tok/s of the same stack (BASELINE's two metrics).
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--tokens T] [--config c2]
-                    [--legs decode,prefill[,dense]] [--pf-calls N] [--pf-tokens T]
+                    [--legs decode,prefill,dense] [--pf-calls N] [--pf-tokens T]
 
 Decode (the headline `value`): a step is one launch of the persistent decode kernel over one
 chunk of T tokens (default 262,144), continuing the same greedy stream launch
@@ -16,9 +16,9 @@ through the same stack (synth.config3: 0.35 % of token-layers gated, 5 % of (key
 chunk) pairs active), each call embedding, running all 37 layers and taking every position's
 argmax (lx.fast's verified mode), timed with HIP events on the stream.
 
-Dense decode (`dense_decode`, with --legs ...,dense): BASELINE config 4, the dense padded
-text-view stack (synth.config4: 24 layers, hidden 2560, SwiGLU 9216); an 8,192-step forced
-prefix of seeded uniform ids, then 4,096 greedy steps timed.
+Dense decode (`dense_decode`): BASELINE config 4, the dense padded text-view stack
+(synth.config4: 24 layers, hidden 2560, SwiGLU 9216); an 8,192-token prompt of seeded uniform ids
+(the batched prefill, then one step), then 4,096 greedy steps timed.
 
 One JSON line on stdout (the driver's contract); everything else goes to stderr.
 """
@@ -127,7 +127,9 @@ def prefill_leg(calls: int, T: int, cpu_tokens: int) -> dict:
         e1.record(stream)
         torch.cuda.synchronize()
         ms.append(e0.elapsed_time(e1))
-        log(f"[bench] verified-prefill call {k + 1}/{calls}: {T} tokens in {ms[-1]:.2f} ms")
+        nc = int(pf.count[:d.n_layers].sum())
+        log(f"[bench] verified-prefill call {k + 1}/{calls}: {T} tokens in {ms[-1]:.2f} ms "
+            f"({nc} candidate positions over the layers)")
     call_ms = sum(ms) / len(ms)
     # algorithmic bytes per position: the residual read and written per layer (bf16), the head's
     # normed input, and each value-head slot's state read and written once per layer per call
@@ -309,7 +311,8 @@ def main() -> int:
     ap.add_argument("--warmup-tokens", type=int, default=4096)
     ap.add_argument("--config", default="c2", choices=["c1", "c2", "c5", "small"])
     ap.add_argument("--cpu-tokens", type=int, default=256, help="CPU baseline sample (0: skip)")
-    ap.add_argument("--legs", default="decode,prefill", help="decode, prefill or both")
+    ap.add_argument("--legs", default="decode,prefill,dense",
+                    help="comma-separated: decode (config 2), prefill (config 3), dense (config 4)")
     ap.add_argument("--pf-calls", type=int, default=5)
     ap.add_argument("--pf-tokens", type=int, default=65_536)
     ap.add_argument("--pf-cpu-tokens", type=int, default=48)
