@@ -95,6 +95,23 @@ def cpu_baseline(model, conv0, rec0, start: int, n: int):
     return n / dt, preds
 
 
+# The fastest grid-wide synchronisation measured on MI355X: 256 workgroups (one per CU) arriving
+# on eight per-XCD counter copies whose sum the waiters poll, 1.6 us per barrier.
+T_BAR_US = 1.6
+
+
+def latency_roofline(n_layers: int, us_per_token: float) -> dict:
+    """The decode's latency term: a token's dependent chain is two phases per layer (the GDN, then
+    the MLP that reads its residual) and the head, and with the rarely-writing GDN phases paired
+    with their MLP about n_layers + 1 grid-wide synchronisations; at the measured barrier cost
+    that bounds a design that syncs the grid per phase. This kernel runs the chain on one
+    workgroup instead and syncs across workgroups only for the head and GDN events."""
+    p = n_layers + 1
+    t = p * T_BAR_US
+    return {"dependent_syncs_per_token": p, "t_bar_us": T_BAR_US, "t_roof_us": round(t, 1),
+            "t_measured_us": round(us_per_token, 2), "frac": round(t / us_per_token, 4)}
+
+
 def prefill_leg(calls: int, T: int, cpu_tokens: int) -> dict:
     """verified-mode calls of T seeded uniform tokens; tok/s over the timed
     calls (HIP events around each call on the current stream, inputs resident)."""
@@ -410,6 +427,7 @@ def main() -> int:
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 5),
                      "traffic": None if t_tok is None else round(t_tok * args.tokens),
                      "bytes_per_token": round(b_tok), "kernel_ms_per_launch": round(kern_ms, 3)},
+        "latency_roofline": latency_roofline(d.n_layers, kern_ms * 1e3 / args.tokens),
     }
     if args.cpu_tokens > 0:
         cps, cpreds = cpu_baseline(model, conv0, rec0, start, args.cpu_tokens)
