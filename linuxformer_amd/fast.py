@@ -19,6 +19,28 @@ import torch
 from . import synth
 
 
+# the chip layers' projection modules (the weights Fast packs from)
+PROJ = ("in_proj_qkv", "in_proj_z", "in_proj_b", "in_proj_a", "out_proj", "gate_proj", "up_proj",
+        "down_proj")
+
+
+def place_lean(model, n_chip: int, dev) -> None:
+    """lx.fast.place_lean (lx/lx/fast.py:33-46): a transformers model moved to dev except its
+    first n_chip layers' projections (the chip's 0.08 %-dense weights, which Fast packs and the
+    device never needs in full); build Fast from the model first, then Fast.to(dev)."""
+    kept = []
+    for layer in model.model.layers[:n_chip]:
+        for mod in layer.modules():
+            for name in PROJ:
+                lin = getattr(mod, name, None)
+                if isinstance(lin, torch.nn.Linear):
+                    kept.append((lin, lin.weight))
+                    lin.weight = None  # (a None parameter is skipped by Module.to)
+    model.to(dev)
+    for lin, w in kept:
+        lin.weight = w
+
+
 class Rows:
     """CSR rows (ptr, cols, vals) of a Coo's row range."""
 
@@ -48,6 +70,37 @@ class Fast:
         w1 = np.float32(1.0) + np.asarray(self.sm.norm, np.float32)
         self.head_cols = np.nonzero(w1 != 0)[0]
         self.dec = [self._live(L) for L in range(self.n_chip)]
+
+    lean = False       # lx.fast's flags (lx/lx/fast.py:388-397): the projections are not on the
+    head_block = None  # device (place_lean); the head's row block (the kernel picks its own)
+
+    def to(self, dev) -> "Fast":
+        """Fast.to (lx/lx/fast.py:399-418): everything Fast needs on dev (the packed tables of
+        the verified-mode kernels, built from host memory), so the model's own projections may
+        stay on the host (place_lean)."""
+        self.prefill(dev)
+        return self
+
+    def init_cache(self, cache, dev) -> None:
+        """Fast.init_cache (lx/lx/fast.py:420-430): the chip layers' states as the stock forward
+        of one zero token leaves them, all zero (conv windows in the model dtype, recurrent states
+        float32). cache: a transformers DynamicCache or a StateCache."""
+        d = self.sm.dims
+        conv = torch.zeros(1, d.n_conv, 1, dtype=self._dtype(), device=dev)
+        rec = torch.zeros(1, d.nv, d.kd, d.vd, dtype=torch.float32, device=dev)
+        for L in range(self.n_chip):
+            if hasattr(cache, "update_conv_state"):
+                cache.update_conv_state(conv, L, conv_kernel_size=d.conv)
+                ly = cache.layers[L]
+                if hasattr(ly, "update_recurrent_state"):
+                    ly.update_recurrent_state(rec.clone())
+                else:
+                    cache.update_recurrent_state(rec.clone(), L)
+            else:
+                ly = cache.layers[L]
+                ly.conv_states[0] = torch.zeros(1, d.n_conv, d.conv, dtype=self._dtype(),
+                                                device=dev)
+                ly.recurrent_states[0] = rec.clone()
 
     def _live(self, L: int) -> dict:
         """A layer's live parts (lx/lx/fast.py:187-248): key heads with a live query or key

@@ -146,6 +146,7 @@ def test_fast_api_forward_decode_head(cuda):
     emb = m.embed.dense()[toks]  # exact in bf16
     h = torch.from_numpy(emb).to("cuda", torch.bfloat16)[None]
     cache = fast.StateCache(c0, r0, d.dtype, "cuda")
+    assert f.to("cuda") is f  # (the tables on the device; the calls below use them)
     out = f.forward(h[:, :8], cache)
     out1 = f.decode(h[:, 8:], cache)
     hs = torch.cat([out, out1], 1)[0]
