@@ -7,8 +7,10 @@
  * are a few native entry points over caller-owned buffers. Semantics: each position sees
  * exactly the stock decode step (the recurrent delta rule, token by token), so a verified
  * prefill of T tokens leaves the predictions and the states that T forced decode steps leave,
- * bit for bit; on the chip's exact-regime values this is also what the stock chunked forward
- * computes. All buffers belong to the caller; the library allocates nothing. Every entry
+ * bit for bit. (The reference runs fla's chunked rule here and relies on the circuit's values
+ * being exact in fp32 for the two to agree, lx/lx/fast.py:17-20; on general values the chunked
+ * and recurrent forms round apart, and this library keeps the decode's.) All buffers belong to
+ * the caller; the library allocates nothing. Every entry
  * point returns a hipError_t (0 on success).
  *
  * The residual stream lives in HBM as tiles of LXM_PF_TT tokens: element (t, c) of a (T, hidden)
