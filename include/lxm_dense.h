@@ -87,15 +87,15 @@ int lxm_dn_run(const lxm_dn_params* p_host, const lxm_dn_params* p_dev, int n, v
 #define LXM_DN_PB 16
 typedef struct lxm_dn_pbuf {
   float* h;    /* (PB, hidden): the batch's residuals */
-  float* xn;   /* (PB, hidden): a norm's output, in the weights' interleaved order */
+  uint16_t* xn; /* (PB, hidden) bf16: a norm's output, in the weights' interleaved order */
   float* P;    /* (PB, rows of proj): the projections */
   float* qk;   /* (PB, nk, 2, 256): the normed query (times 1/16) and key */
   float* v;    /* (PB, nk x rl x 128): the values after the conv */
   float* g;    /* (PB, nk x rl, 2): beta and exp(g) */
   float* live; /* (PB, nk, 2): 1 where the query / key has a nonzero element */
   float* o;    /* (PB, nk x rl x 128): the delta rule's outputs */
-  float* ys;   /* (PB, nk x rl x 128): the gated norm's output, interleaved */
-  float* act;  /* (PB, inter): SwiGLU's output, interleaved */
+  uint16_t* ys;  /* (PB, nk x rl x 128) bf16: the gated norm's output, interleaved */
+  uint16_t* act; /* (PB, inter) bf16: SwiGLU's output, interleaved */
 } lxm_dn_pbuf;
 
 /* T forced tokens (device int32) through every layer without the head, in batches of LXM_DN_PB:

@@ -888,20 +888,45 @@ __device__ __forceinline__ void tree_scatter(float (&v)[V], int lane) {
   }
 }
 
+// A chunk (CH = 8 or 4 bf16 values) of an interleaved bf16 row as 16 bytes
+template <int CH>
+__device__ __forceinline__ v4u chunk_bf(const uint16_t* row, int q, int lane) {
+  if constexpr (CH == 8) {
+    return reinterpret_cast<const v4u*>(row)[q * 64 + lane];
+  } else {
+    const uint2 u = reinterpret_cast<const uint2*>(row)[lane];
+    return v4u{u.x, u.y, 0u, 0u};
+  }
+}
+// acc += the chunk's products in entry order (bf16 x bf16 products are exact in fp32)
+template <int CH>
+__device__ __forceinline__ float chunk_dot(v4u w, v4u x, float acc) {
+#pragma unroll
+  for (int k = 0; k < CH / 2; k++) {
+    acc = __builtin_fmaf(bitsf(w[k] << 16), bitsf(x[k] << 16), acc);
+    acc = __builtin_fmaf(bitsf(w[k] & 0xffff0000u), bitsf(x[k] & 0xffff0000u), acc);
+  }
+  return acc;
+}
+__device__ __forceinline__ uint16_t bf16_bits(float v) { return (uint16_t)(fbits(v) >> 16); }
+
 // Rows for a batch of n <= PB tokens: the wave's R rows (MODE 2: R / 2 SwiGLU units, gate rows
-// from W and up rows from W2) over X (n x 64 G, interleaved), staged in LDS one 8-entry chunk per
-// lane at a time. MODE 0: out[b ldo + r] = D(s); 1: out[b ldo + r] = D(out + D(s)) (the
-// residual); 2: out[b ldo + il(u, og)] = D(D(silu(D(g))) * D(u)).
+// from W and up rows from W2) over X (n x 64 G bf16, interleaved). The batch's inputs are staged
+// in LDS one chunk per lane at a time, double-buffered: each thread loads its share of chunk q + 1
+// into registers before chunk q's sums and stores it to LDS after them, so a chunk costs one
+// barrier and its loads overlap the arithmetic. MODE 0: out[b ldo + r] = D(s) (float); 1:
+// out[b ldo + r] = D(out + D(s)) (float, the residual); 2: out[b ldo + il(u, og)] =
+// D(D(silu(D(g))) * D(u)) (bf16).
 template <int G, int R, int MODE>
 __global__ __launch_bounds__(PBT) void pb_rows(const uint16_t* __restrict__ W,
                                                const uint16_t* __restrict__ W2, int nrows,
-                                               const float* __restrict__ X, int n, float* out,
+                                               const uint16_t* __restrict__ X, int n, void* out,
                                                int ldo, int og) {
   constexpr int CH = G == 4 ? 4 : 8, NC = G / CH, K = 64 * G, V = R * PB;
   constexpr int RU = MODE == 2 ? R / 2 : R;  // distinct row indices per wave
+  constexpr int SPT = PB * 64 / PBT;         // staged chunks per thread
   static_assert(MODE != 2 || (R % 2 == 0 && V == 128), "units: gate and up rows 32 lanes apart");
-  __shared__ v4f xlo[PB * 64];
-  __shared__ v4f xhi[CH == 8 ? PB * 64 : 1];
+  __shared__ v4u xs[2][PB * 64];
   const int lane = tid() & 63;
   const int wv = blockIdx.x * (PBT / 64) + (tid() >> 6);
   const uint16_t* rp[R];
@@ -911,49 +936,37 @@ __global__ __launch_bounds__(PBT) void pb_rows(const uint16_t* __restrict__ W,
     r = r < nrows ? r : nrows - 1;  // (rows past the end load the last row, unused)
     rp[i] = (MODE == 2 && i >= RU ? W2 : W) + (int64_t)r * K;
   }
+  // thread t stages (token, lane) = idx / 64, idx % 64 for idx = t + j PBT; tokens past n: zero
+  auto fetch = [&](int q, v4u (&st)[SPT]) {
+#pragma unroll
+    for (int j = 0; j < SPT; j++) {
+      const int idx = tid() + j * PBT, b = idx >> 6;
+      st[j] = b < n ? chunk_bf<CH>(X + (int64_t)b * K, q, idx & 63) : v4u{0u, 0u, 0u, 0u};
+    }
+  };
   float acc[R][PB];
 #pragma unroll
   for (int i = 0; i < R; i++)
 #pragma unroll
     for (int b = 0; b < PB; b++) acc[i][b] = 0.0f;
+  v4u st[SPT];
+  fetch(0, st);
   for (int q = 0; q < NC; q++) {
     v4u w[R];
 #pragma unroll
-    for (int i = 0; i < R; i++) {
-      if constexpr (CH == 8) {
-        w[i] = reinterpret_cast<const v4u*>(rp[i])[q * 64 + lane];
-      } else {
-        const uint2 u = reinterpret_cast<const uint2*>(rp[i])[lane];
-        w[i] = v4u{u.x, u.y, 0u, 0u};
-      }
-    }
-    lds_barrier();  // (the previous chunk's reads are done)
-    for (int idx = tid(); idx < PB * 64; idx += PBT) {
-      const int b = idx >> 6, l = idx & 63;
-      v4f lo = {0.0f, 0.0f, 0.0f, 0.0f}, hi = lo;
-      if (b < n) {
-        const float* src = X + (int64_t)b * K + (int64_t)(q * 64 + l) * CH;
-        lo = *reinterpret_cast<const v4f*>(src);
-        if constexpr (CH == 8) hi = *reinterpret_cast<const v4f*>(src + 4);
-      }
-      xlo[idx] = lo;
-      if constexpr (CH == 8) xhi[idx] = hi;
-    }
+    for (int i = 0; i < R; i++) w[i] = chunk_bf<CH>(rp[i], q, lane);
+    v4u* buf = xs[q & 1];
+#pragma unroll
+    for (int j = 0; j < SPT; j++) buf[tid() + j * PBT] = st[j];
+    // (every thread's share of chunk q is in; the buffer written next was last read two
+    // chunks ago, before this barrier)
     lds_barrier();
+    if (q + 1 < NC) fetch(q + 1, st);
 #pragma unroll
     for (int b = 0; b < PB; b++) {
-      const v4f lo = xlo[b * 64 + lane];
-      v4f hi = {0.0f, 0.0f, 0.0f, 0.0f};
-      if constexpr (CH == 8) hi = xhi[b * 64 + lane];
-      const float x[8] = {lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
+      const v4u xx = buf[b * 64 + lane];
 #pragma unroll
-      for (int i = 0; i < R; i++)
-#pragma unroll
-        for (int k = 0; k < CH / 2; k++) {
-          const uint32_t ww = w[i][k];
-          acc[i][b] = __builtin_fmaf(bitsf(ww << 16), x[2 * k], acc[i][b]);
-          acc[i][b] = __builtin_fmaf(bitsf(ww & 0xffff0000u), x[2 * k + 1], acc[i][b]);
-        }
+      for (int i = 0; i < R; i++) acc[i][b] = chunk_dot<CH>(w[i], xx, acc[i][b]);
     }
   }
   float v[V];
@@ -973,11 +986,12 @@ __global__ __launch_bounds__(PBT) void pb_rows(const uint16_t* __restrict__ W,
       const float u = __shfl_xor(v[j], 32);  // (the up row's sum, 32 lanes on)
       const int unit = wv * RU + i;
       if (lane < 32 && unit < nrows && b < n)
-        out[(int64_t)b * ldo + il(unit, og)] = bf16r(silu_bf16(bf16r(v[j])) * bf16r(u));
+        static_cast<uint16_t*>(out)[(int64_t)b * ldo + il(unit, og)] =
+            bf16_bits(bf16r(silu_bf16(bf16r(v[j])) * bf16r(u)));
     } else {
       const int r = wv * RU + i;
       if (r < nrows && b < n) {
-        float* o = out + (int64_t)b * ldo + r;
+        float* o = static_cast<float*>(out) + (int64_t)b * ldo + r;
         if constexpr (MODE == 0) *o = bf16r(v[j]);
         else *o = bf16r(*o + bf16r(v[j]));
       }
@@ -987,11 +1001,12 @@ __global__ __launch_bounds__(PBT) void pb_rows(const uint16_t* __restrict__ W,
 
 // Long rows (out_proj, down_proj: few rows of many entries) for a batch of PB tokens: the
 // workgroup's 4 waves share R rows, wave w taking tokens w BW .. w BW + BW - 1 (BW = PB / 4), each
-// wave reading its tokens' inputs straight from X (no LDS, no barriers: the rows are too few to
-// share a staged input among many waves). Sums and MODEs as pb_rows (0 and 1).
+// wave reading its tokens' inputs straight from X (bf16; no LDS, no barriers: the rows are too
+// few to share a staged input among many waves), the next chunk's loads issued before this
+// chunk's sums. Sums and MODEs as pb_rows (0 and 1).
 template <int G, int R, int MODE>
 __global__ __launch_bounds__(PBT) void pb_hrows(const uint16_t* __restrict__ W, int nrows,
-                                                const float* __restrict__ X, int n, float* out,
+                                                const uint16_t* __restrict__ X, int n, float* out,
                                                 int ldo) {
   constexpr int CH = G == 4 ? 4 : 8, NC = G / CH, K = 64 * G, BW = PB / (PBT / 64), V = R * BW;
   static_assert(V <= 64 && 64 % V == 0, "one sum per lane group");
@@ -1003,7 +1018,7 @@ __global__ __launch_bounds__(PBT) void pb_hrows(const uint16_t* __restrict__ W, 
     const int r = r0 + i < nrows ? r0 + i : nrows - 1;
     rp[i] = W + (int64_t)r * K;
   }
-  const float* xp[BW];
+  const uint16_t* xp[BW];
 #pragma unroll
   for (int b = 0; b < BW; b++) {
     const int bb = b0 + b < n ? b0 + b : n - 1;  // (tokens past n read token n - 1, unused)
@@ -1014,37 +1029,26 @@ __global__ __launch_bounds__(PBT) void pb_hrows(const uint16_t* __restrict__ W, 
   for (int i = 0; i < R; i++)
 #pragma unroll
     for (int b = 0; b < BW; b++) acc[i][b] = 0.0f;
+  v4u w[R], x[BW];
+#pragma unroll
+  for (int i = 0; i < R; i++) w[i] = chunk_bf<CH>(rp[i], 0, lane);
+#pragma unroll
+  for (int b = 0; b < BW; b++) x[b] = chunk_bf<CH>(xp[b], 0, lane);
   for (int q = 0; q < NC; q++) {
-    v4u w[R];
-    float x[BW][8];
+    v4u wn[R], xn[BW];
+    const int qn = q + 1 < NC ? q + 1 : q;  // (the last chunk reloads itself, unused)
 #pragma unroll
-    for (int i = 0; i < R; i++) {
-      if constexpr (CH == 8) {
-        w[i] = reinterpret_cast<const v4u*>(rp[i])[q * 64 + lane];
-      } else {
-        const uint2 u = reinterpret_cast<const uint2*>(rp[i])[lane];
-        w[i] = v4u{u.x, u.y, 0u, 0u};
-      }
-    }
+    for (int i = 0; i < R; i++) wn[i] = chunk_bf<CH>(rp[i], qn, lane);
 #pragma unroll
-    for (int b = 0; b < BW; b++) {
-      const float* src = xp[b] + (int64_t)(q * 64 + lane) * CH;
-      const v4f lo = *reinterpret_cast<const v4f*>(src);
-      v4f hi = {0.0f, 0.0f, 0.0f, 0.0f};
-      if constexpr (CH == 8) hi = *reinterpret_cast<const v4f*>(src + 4);
-      x[b][0] = lo.x; x[b][1] = lo.y; x[b][2] = lo.z; x[b][3] = lo.w;
-      x[b][4] = hi.x; x[b][5] = hi.y; x[b][6] = hi.z; x[b][7] = hi.w;
-    }
+    for (int b = 0; b < BW; b++) xn[b] = chunk_bf<CH>(xp[b], qn, lane);
 #pragma unroll
     for (int b = 0; b < BW; b++)
 #pragma unroll
-      for (int i = 0; i < R; i++)
+      for (int i = 0; i < R; i++) acc[i][b] = chunk_dot<CH>(w[i], x[b], acc[i][b]);
 #pragma unroll
-        for (int k = 0; k < CH / 2; k++) {
-          const uint32_t ww = w[i][k];
-          acc[i][b] = __builtin_fmaf(bitsf(ww << 16), x[b][2 * k], acc[i][b]);
-          acc[i][b] = __builtin_fmaf(bitsf(ww & 0xffff0000u), x[b][2 * k + 1], acc[i][b]);
-        }
+    for (int i = 0; i < R; i++) w[i] = wn[i];
+#pragma unroll
+    for (int b = 0; b < BW; b++) x[b] = xn[b];
   }
   float v[V];
 #pragma unroll
@@ -1076,15 +1080,16 @@ __global__ __launch_bounds__(PBT) void pb_embed(const uint16_t* __restrict__ emb
   for (int c = tid(); c < H; c += PBT) h[(int64_t)b * H + c] = bf16f(e[il(c, G)]);
 }
 
-// every token's RMSNorm (the step's factor and elements) into xn, interleaved for G = gx
+// every token's RMSNorm (the step's factor and elements) into xn (bf16), interleaved for G = gx
 __global__ __launch_bounds__(NT) void pb_norm(const float* __restrict__ h,
                                               const float* __restrict__ nw, float eps, int H,
-                                              int gx, float* xn) {
+                                              int gx, uint16_t* xn) {
   __shared__ float wsum[NW];
   const int b = blockIdx.x;
   const float* hb = h + (int64_t)b * H;
   const float r = norm_factor<false>(hb, H, eps, wsum);
-  for (int c = tid(); c < H; c += NT) xn[(int64_t)b * H + il(c, gx)] = norm_el(hb[c], r, nw[c]);
+  for (int c = tid(); c < H; c += NT)
+    xn[(int64_t)b * H + il(c, gx)] = bf16_bits(norm_el(hb[c], r, nw[c]));
 }
 
 struct PbGdn {
@@ -1281,7 +1286,7 @@ __device__ __forceinline__ void win_after(uint16_t* conv, const float* __restric
 __global__ __launch_bounds__(PBT) void pb_gnorm(const float* __restrict__ o,
                                                 const float* __restrict__ P, int nproj, int zoff,
                                                 const float* __restrict__ gw, float geps, int nh,
-                                                int gv, float* ys, uint16_t* conv, int n, int nk,
+                                                int gv, uint16_t* ys, uint16_t* conv, int n, int nk,
                                                 int kl, int rl, int R) {
   __shared__ float y[4096];
   const int b = blockIdx.x, nvr = nh * VD;
@@ -1289,7 +1294,7 @@ __global__ __launch_bounds__(PBT) void pb_gnorm(const float* __restrict__ o,
                 nullptr, nullptr, nullptr, 0, 0};
   gated_norm<PBT / 64, false>(d, y);
   lds_barrier();
-  for (int c = tid(); c < nvr; c += PBT) ys[(int64_t)b * nvr + il(c, gv)] = y[c];
+  for (int c = tid(); c < nvr; c += PBT) ys[(int64_t)b * nvr + il(c, gv)] = bf16_bits(y[c]);
   win_after(conv, P, nproj, n, nk, kl, rl, R, blockIdx.x * PBT + tid(), gridDim.x * PBT);
 }
 
@@ -1438,15 +1443,15 @@ extern "C" int lxm_dn_run(const lxm_dn_params* ph, const lxm_dn_params* pd, int 
 
 // the batched prefill's row kernels: R rows per wave (MODE 2: R / 2 units), 4 waves per workgroup
 template <int G, int R, int MODE>
-static void launch_pb(const uint16_t* W, const uint16_t* W2, int nrows, const float* X, int n,
-                      float* out, int ldo, int og, hipStream_t st) {
+static void launch_pb(const uint16_t* W, const uint16_t* W2, int nrows, const uint16_t* X, int n,
+                      void* out, int ldo, int og, hipStream_t st) {
   const int per = (PBT / 64) * (MODE == 2 ? R / 2 : R);
   hipLaunchKernelGGL((pb_rows<G, R, MODE>), dim3((nrows + per - 1) / per), dim3(PBT), 0, st, W, W2,
                      nrows, X, n, out, ldo, og);
 }
 // the residual's long rows: 8 rows per workgroup, the batch's tokens split over its 4 waves
 template <int G>
-static void launch_hrows(const uint16_t* W, int nrows, const float* X, int n, float* out, int ldo,
+static void launch_hrows(const uint16_t* W, int nrows, const uint16_t* X, int n, float* out, int ldo,
                          hipStream_t st) {
   constexpr int R = 8;
   hipLaunchKernelGGL((pb_hrows<G, R, 1>), dim3((nrows + R - 1) / R), dim3(PBT), 0, st, W, nrows, X,

@@ -143,7 +143,9 @@ class DenseDecode:
             nvr = nk * rl * 128
             sizes = dict(h=H, xn=H, P=self.nproj, qk=nk * 2 * 256, v=nvr, g=nk * rl * 2,
                          live=nk * 2, o=nvr, ys=nvr, act=I)
-            self._pb_t = {k: torch.zeros(PB * n, dtype=torch.float32, device=self.dev)
+            bf = ("xn", "ys", "act")  # (the row kernels' inputs, bf16)
+            self._pb_t = {k: torch.zeros(PB * n, device=self.dev,
+                                         dtype=torch.bfloat16 if k in bf else torch.float32)
                           for k, n in sizes.items()}
             self._pb = DnPbuf(**{k: t.data_ptr() for k, t in self._pb_t.items()})
         return self._pb
