@@ -427,7 +427,7 @@ def main() -> int:
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 5),
                      "traffic": None if t_tok is None else round(t_tok * args.tokens),
                      "bytes_per_token": round(b_tok), "kernel_ms_per_launch": round(kern_ms, 3)},
-        "latency_roofline": latency_roofline(d.n_layers, kern_ms * 1e3 / args.tokens),
+        "latency_roofline": latency_roofline(model.dims.n_layers, kern_ms * 1e3 / args.tokens),
     }
     if args.cpu_tokens > 0:
         cps, cpreds = cpu_baseline(model, conv0, rec0, start, args.cpu_tokens)
