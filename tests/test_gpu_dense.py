@@ -123,6 +123,39 @@ def test_dense_prefill_full_widths(cuda):
     check_prefill(21, 3, seed=5, name="mid")
 
 
+def test_dense_prefill_equals_steps_config4(cuda):
+    """At config 4's full size (24 layers, hidden 2560, vocabulary 248,320): a 40-token prompt
+    through lxm_dn_prefill and one step leaves the prediction and every state and window that
+    40 forced steps leave, bit for bit (two native paths, each pinned to the oracle above on the
+    scaled-down stacks)."""
+    spec = synth.config4()
+    dm = synth.build_dense(spec, "cuda")
+    d = dm.dims
+    toks = [int(x) for x in np.random.default_rng(9).integers(0, spec.vocab, 40)]
+    print(f"[gpu-test] dense prefill config 4 full size: T={len(toks)}", flush=True)
+    out = []
+    for batched in (False, True):
+        conv0 = np.zeros((d.n_layers, d.n_conv, 4), np.float32)
+        rec0 = np.zeros((d.n_layers, d.nv, 256, 128), np.float32)
+        cache = fast.StateCache(conv0, rec0, "bf16", "cuda")
+        dd = dense.DenseDecode(dm, cache, max_steps=64)
+        if batched:
+            dd.prefill(toks[:-1])
+            p = dd.run(toks[-1:], 1)
+        else:
+            p = dd.run(toks, len(toks))[-1:]
+        out.append((p, [l.conv_states[0].clone() for l in cache.layers],
+                    [l.recurrent_states[0].clone() for l in cache.layers]))
+        del dd, cache
+    (p0, c0, r0), (p1, c1, r1) = out
+    assert p0 == p1
+    for a, b in zip(c0, c1):
+        assert torch.equal(a.view(torch.int16), b.view(torch.int16))
+    for a, b in zip(r0, r1):
+        assert torch.equal(a.view(torch.int32), b.view(torch.int32))
+    assert any(bool(r.any()) for r in r1)  # (the prompt moved the live states)
+
+
 def test_dense_prefill_rejects_bad_token(cuda):
     spec, dm_cpu, _ = model()
     conv0, rec0 = synth.dense_state(dm_cpu)
