@@ -925,7 +925,8 @@ __global__ __launch_bounds__(PBT) void pb_rows(const uint16_t* __restrict__ W,
   constexpr int CH = G == 4 ? 4 : 8, NC = G / CH, K = 64 * G, V = R * PB;
   constexpr int RU = MODE == 2 ? R / 2 : R;  // distinct row indices per wave
   constexpr int SPT = PB * 64 / PBT;         // staged chunks per thread
-  static_assert(MODE != 2 || (R % 2 == 0 && V == 128), "units: gate and up rows 32 lanes apart");
+  static_assert(MODE != 2 || (R % 2 == 0 && (V == 128 || V == 64)),
+                "units: gate and up sums 32 lanes apart");
   __shared__ v4u xs[2][PB * 64];
   const int lane = tid() & 63;
   const int wv = blockIdx.x * (PBT / 64) + (tid() >> 6);
@@ -1474,7 +1475,9 @@ static void pb_layer(const lxm_dn_params* ph, const lxm_dn_layer& ly, const lxm_
                      ly.gnorm, ph->geps, nk * rl, GV, pb->ys, ly.conv, n, nk, kl, rl, R);
   launch_hrows<GV>(ly.out, H, pb->ys, n, pb->h, H, st);
   hipLaunchKernelGGL(pb_norm, dim3(n), dim3(NT), 0, st, pb->h, ly.ln_post, eps, H, GH, pb->xn);
-  launch_pb<GH, 8, 2>(ly.gate, ly.up, I, pb->xn, n, pb->act, I, GI, st);
+  // (SwiGLU: 2 units per wave, 1,152 workgroups at 3 per CU; with 4 units per wave its 576
+  // workgroups took two rounds of 512, 44 us against 34)
+  launch_pb<GH, 4, 2>(ly.gate, ly.up, I, pb->xn, n, pb->act, I, GI, st);
   launch_hrows<GI>(ly.down, H, pb->act, n, pb->h, H, st);
 }
 
