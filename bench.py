@@ -36,6 +36,7 @@ sys.path.insert(0, HERE)
 
 METRIC = "greedy decode tok/s, 37-layer sparse chip stack, 1 MI355X; verified prefill tok/s"
 HBM_PEAK_GBS = 8000.0
+FP32_PEAK_TFLOPS = 157.3  # MI355X's published fp32 peak
 
 
 def log(*a):
@@ -295,13 +296,22 @@ def dense_leg(n_prefill: int, n_steps: int, cpu_tokens: int, graph: bool = True,
     pad_layer = 2 * ((2 * nk * 256 + 2 * d.nv * 128 + 2 * d.nv) * H + H * d.nv * 128 + 3 * I * H)
     achieved = b_tok * n_steps / (ms * 1e-3) / 1e9
     t_tok = measured_traffic("c4", "dense")
+    # fused multiply-adds per prompt token: every live weight of every layer once
+    fma_tok = d.n_layers * ((2 * nk * kl + 2 * nvr + 2 * nk * rl) * H + H * nvr + 3 * I * H)
     out = {"metric": "dense padded decode tok/s, 24-layer text-view stack, 1 MI355X",
            "value": round(n_steps / (ms * 1e-3), 1), "unit": "tok/s",
            "ms_per_token": round(ms / n_steps, 4), "steps": n_steps,
            "prefill": {"tokens": n_prefill, "s": round(pre_s, 2),
                        "tok_s": round(n_prefill / pre_s, 1),
                        "mode": "lxm_dn_prefill (batches of 16) + one step" if batched
-                               else "forced steps"},
+                               else "forced steps",
+                       # the prompt's row sums are fp32 fused ops on the VALU (bf16 x bf16
+                       # products, summed in the decode's order); packed fp32 is not used, so
+                       # the vector rate available is half the published fp32 peak
+                       "roofline": {"bound": "valu", "achieved": round(2 * fma_tok * n_prefill / pre_s / 1e12, 2),
+                                    "peak": FP32_PEAK_TFLOPS, "unit": "TFLOP/s",
+                                    "frac": round(2 * fma_tok * n_prefill / pre_s / 1e12 / FP32_PEAK_TFLOPS, 4),
+                                    "flops_per_token": 2 * fma_tok}},
            "config": {"workload": "c4: 24 layers, hidden 2560, 16 key heads (256, 128 live), 128 "
                                   "value heads (2 live per key head), SwiGLU 9216, vocab 248,320, "
                                   "bf16 N(0, 0.02); zero state"},
