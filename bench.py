@@ -1,15 +1,20 @@
 """Benchmark: greedy decode tok/s of the 37-layer synthetic sparse chip stack on one MI355X, and
 verified-prefill tok/s of the same stack (BASELINE's two metrics).
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--tokens T] [--config c2]
-                    [--legs decode,prefill,dense] [--pf-calls N] [--pf-tokens T]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--chunk T] [--config c2]
+                    [--legs decode,prefill,dense] [--cpu-seconds S] ...
 
-Decode (the headline `value`): a step is one launch of the persistent decode kernel over one
-chunk of T tokens (default 262,144), continuing the same greedy stream launch
-after launch, as lx/tools/mega_boot.py runs the boot in 262,144-token launches. The model is the
-seeded synthetic stack (synth.config2: 37 layers, hidden 3572, bf16, 0.08 % density, N(0,1)
-state); it is built and packed on the host, then every input is resident in HBM before the
-timed region.
+Decode (the headline `value`): the workload is one greedy chunk of T = 262,144 tokens (BASELINE
+config 2) from the config's start token and initial state, as lx/tools/mega_boot.py runs the
+boot in 262,144-token launches. A step is one launch of the persistent decode kernel over the
+next T/K tokens of that chunk (the sizes differ by at most one token and add up to T), each
+launch continuing the stream where the previous one stopped; K steps are the whole chunk. The W
+warm-up launches (T/K tokens each) run first, then the initial state is restored, so the timed
+chunk is exactly the one tests/golden/c2_chunk.json hashes (its prediction stream and final
+states, from the CPU oracle). The model is the seeded synthetic stack (synth.config2: 37 layers,
+hidden 3572, bf16, 0.08 % density, N(0,1) state), built and packed on the host; every input is
+resident in HBM before the timed region. Also reported: the same kernel on a forced stream of
+seeded uniform tokens (the greedy stream of this synthetic stack visits few distinct tokens).
 
 Verified prefill (`verified_prefill`): BASELINE config 3, calls of 65,536 seeded uniform tokens
 through the same stack (synth.config3: 0.35 % of token-layers gated, 5 % of (key head, 64-token
@@ -20,12 +25,17 @@ Dense decode (`dense_decode`): BASELINE config 4, the dense padded text-view sta
 (synth.config4: 24 layers, hidden 2560, SwiGLU 9216); an 8,192-token prompt of seeded uniform ids
 (the batched prefill, then one step), then 4,096 greedy steps timed.
 
+CPU baselines (reported beside, never the target): the stock forward, i.e. transformers'
+Qwen3_5 decoder layers on dense tensors in torch eager mode on every host thread torch uses
+(oracle/stock.py), on a bounded sample of each workload (about --cpu-seconds of work).
+
 One JSON line on stdout (the driver's contract); everything else goes to stderr.
 """
 
 from __future__ import annotations
 
 import argparse
+import hashlib
 import json
 import os
 import sys
@@ -37,10 +47,18 @@ sys.path.insert(0, HERE)
 METRIC = "greedy decode tok/s, 37-layer sparse chip stack, 1 MI355X; verified prefill tok/s"
 HBM_PEAK_GBS = 8000.0
 FP32_PEAK_TFLOPS = 157.3  # MI355X's published fp32 peak
+CHUNK_GOLDEN = os.path.join(HERE, "tests", "golden", "c2_chunk.json")
 
 
 def log(*a):
     print(*a, file=sys.stderr, flush=True)
+
+
+def split_chunk(total: int, steps: int) -> list:
+    """The chunk's tokens dealt to `steps` launches: sizes differing by at most one, summing to
+    total (the first total % steps launches take one more)."""
+    q, r = divmod(total, steps)
+    return [q + (1 if k < r else 0) for k in range(steps)]
 
 
 def survey_bytes_per_token(model, f_out: float) -> float:
@@ -81,39 +99,258 @@ def measured_traffic(config: str, kind: str = "decode", key: str = "hbm_bytes_pe
     return None
 
 
-def cpu_baseline(model, conv0, rec0, start: int, n: int):
-    """The C oracle (a single-threaded port of the stock decode) on the first n tokens."""
+def gates_per_token(model, inputs) -> float:
+    """GDN events per token: the gate columns each step's input embedding row sets (a layer-step
+    runs the delta rule exactly when its input carries that layer's gate; synth's write gates)."""
+    import numpy as np
+
+    d = model.dims
+    hng = d.hidden - d.n_layers
+    e = model.embed
+    g = np.bincount(e.rows[e.cols >= hng], minlength=d.vocab)
+    return float(g[np.asarray(inputs, np.int64)].mean())
+
+
+def sync_costs(n_blocks: int) -> dict:
+    """The grid barrier and the cross-workgroup round trip, measured on this GPU with the decode's
+    own primitives (lxm_t_sync), microseconds."""
+    import ctypes
+
+    import torch
+
+    from linuxformer_amd import mk_build
+
+    lib = mk_build.load()
+    dev = torch.device("cuda", 0)
+    out = {}
+    for name, kind, far in (("grid_barrier_us", 0, 0), ("round_trip_other_xcd_us", 1, 1),
+                            ("round_trip_same_xcd_us", 1, 8)):
+        words = torch.zeros(320, dtype=torch.int32, device=dev)
+        err = torch.zeros(1, dtype=torch.int32, device=dev)
+        res = torch.zeros(1, dtype=torch.float32, device=dev)
+        st = ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream)
+        e = lib.lxm_t_sync(kind, 2000, n_blocks, far, ctypes.c_void_p(words.data_ptr()),
+                           ctypes.c_void_p(err.data_ptr()), ctypes.c_void_p(res.data_ptr()), st)
+        if e:
+            raise RuntimeError(f"lxm_t_sync failed: hipError {e}")
+        torch.cuda.synchronize()
+        if int(err.item()):
+            raise RuntimeError(f"lxm_t_sync({kind}): a wait timed out")
+        out[name] = round(float(res.item()), 3)
+    out["n_blocks"] = n_blocks
+    return out
+
+
+def state_sha(cache) -> tuple:
+    """sha256 of the final conv windows and recurrent states as float32, layer after layer (the
+    bytes of the stacked (L, C, 4) and (L, nv, 256, 128) arrays)."""
+    hc, hr = hashlib.sha256(), hashlib.sha256()
+    for ly in cache.layers:
+        hc.update(ly.conv_states[0][0].float().cpu().numpy().tobytes())
+        hr.update(ly.recurrent_states[0][0].cpu().numpy().tobytes())
+    return hc.hexdigest(), hr.hexdigest()
+
+
+def cpu_threads() -> int:
+    import torch
+
+    return torch.get_num_threads()
+
+
+def stock_decode_baseline(hf, conv0, rec0, start: int, max_steps: int, budget_s: float):
+    """The stock decode (transformers' layers, torch eager, bf16, every thread torch uses) from
+    the chunk's start: steps until max_steps or budget_s of wall time, after one untimed step
+    (page-in). Returns (tok/s, steps, predictions)."""
+    from oracle import stock
+
+    cache = stock.make_cache(hf, conv0, rec0)
+    emb = hf.model.embed_tokens.weight
+    outs = stock.chip_forward(hf, emb[start][None, None], cache)  # warm-up (first touch)
+    cache = stock.make_cache(hf, conv0, rec0)
+    tok, preds = start, []
+    t0 = time.perf_counter()
+    while len(preds) < max_steps:
+        outs = stock.chip_forward(hf, emb[tok][None, None], cache)
+        tok = int(stock.head_argmax(hf, outs[-1][0])[0])
+        preds.append(tok)
+        if time.perf_counter() - t0 > budget_s:
+            break
+    dt = time.perf_counter() - t0
+    return len(preds) / dt, len(preds), preds
+
+
+def oracle_check(model, conv0, rec0, start: int, n: int):
+    """The C oracle's first n predictions of the chunk (the checker)."""
     from oracle import oracle as ox
 
     ox.build()
     om = ox.OracleModel(model)
     c, r = conv0.copy(), rec0.copy()
-    om.decode(c, r, [start], 2)  # warm-up (page-in)
-    c, r = conv0.copy(), rec0.copy()
-    t = time.perf_counter()
     preds, _, _ = om.decode(c, r, [start], n)
-    dt = time.perf_counter() - t
-    return n / dt, preds
+    return preds.tolist()
 
 
-# The fastest grid-wide synchronisation measured on MI355X: 256 workgroups (one per CU) arriving
-# on eight per-XCD counter copies whose sum the waiters poll, 1.6 us per barrier.
-T_BAR_US = 1.6
+def decode_leg(args, dev, hf_holder: dict) -> dict:
+    import numpy as np
+    import torch
+
+    from linuxformer_amd import fast, mega, synth
+
+    spec = {"c1": synth.config1(), "c2": synth.config2(), "c5": synth.config5(),
+            "small": synth.small()}[args.config]
+    t0 = time.time()
+    model = synth.build(spec)
+    conv0, rec0 = synth.init_state(model)
+    start = synth.start_token(spec)
+    f = fast.Fast(model)
+    cache = fast.StateCache(conv0, rec0, model.dims.dtype, dev)
+    mg = mega.Mega(f, model, cache, 0)
+    torch.cuda.synchronize()
+    log(f"[bench] {spec.name}: built and packed in {time.time() - t0:.1f}s; "
+        f"{json.dumps({k: v for k, v in mg.stats.items() if not isinstance(v, list)})}")
+    chunk = args.chunk
+    sizes = split_chunk(chunk, args.steps)
+    saved = [(ly.conv_states[0].clone(), ly.recurrent_states[0].clone()) for ly in cache.layers]
+    stream = torch.cuda.current_stream(dev)
+
+    tok = start
+    for w in range(args.warmup):
+        preds = mg.run([tok], sizes[0])
+        tok = preds[-1]
+        log(f"[bench] warm-up launch {w + 1}/{args.warmup}: {sizes[0]} tokens")
+    for ly, (c, r) in zip(cache.layers, saved):  # the timed chunk starts from the initial state
+        ly.conv_states[0].copy_(c)
+        ly.recurrent_states[0].copy_(r)
+    torch.cuda.synchronize()
+
+    stream_preds, evs = [], []
+    tok = start
+    torch.cuda.synchronize()
+    t_start = time.perf_counter()
+    for k, n in enumerate(sizes):
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        preds = mg.run([tok], n)
+        e1.record(stream)
+        evs.append((e0, e1))
+        stream_preds += preds
+        tok = preds[-1]
+        log(f"[bench] step {k + 1}/{len(sizes)}: {n} tokens, {len(stream_preds)} of {chunk}")
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t_start
+    launch_ms = [a.elapsed_time(b) for a, b in evs]
+    kern_ms = sum(launch_ms) / len(launch_ms)
+    value = chunk / wall
+
+    stream_sha = hashlib.sha256(np.asarray(stream_preds, "<i4").tobytes()).hexdigest()
+    conv_sha, rec_sha = state_sha(cache)
+    inputs = [start] + stream_preds[:-1]
+    ev_tok = gates_per_token(model, inputs)
+    gold = None
+    if os.path.exists(CHUNK_GOLDEN):
+        g = json.load(open(CHUNK_GOLDEN))
+        if g.get("config") == spec.name and g.get("chunk") == chunk and g.get("start") == start:
+            gold = g
+    log(f"[bench] chunk of {chunk} tokens in {wall:.2f}s; stream sha256 {stream_sha[:16]}..., "
+        f"{len(set(stream_preds))} distinct predictions")
+
+    # the same kernel on a forced stream of seeded uniform tokens (every step's input given)
+    n_f = args.forced_tokens
+    forced_out = None
+    if n_f > 0:
+        toks = synth.tokens(spec, n_f, 77).tolist()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        mg.run(toks, n_f)
+        e1.record(stream)
+        torch.cuda.synchronize()
+        ms_f = e0.elapsed_time(e1)
+        forced_out = {"tokens": n_f, "tok_s": round(n_f / (ms_f * 1e-3), 1),
+                      "distinct_inputs": len(set(toks)),
+                      "gdn_events_per_token": round(gates_per_token(model, toks), 4),
+                      "note": "one launch, every step's input forced (seeded uniform ids), "
+                              "continuing from the chunk's final state"}
+        log(f"[bench] forced stream: {n_f} tokens at {forced_out['tok_s']} tok/s")
+
+    sync = sync_costs(mg.ncta)
+    log(f"[bench] sync costs: {sync}")
+    us_tok = kern_ms * 1e3 / (chunk / len(sizes))
+    rt = sync["round_trip_other_xcd_us"]
+    n_rt = 1.0 + 2.0 * ev_tok
+
+    b_tok = survey_bytes_per_token(model, spec.p_gate)
+    achieved = b_tok * (chunk / len(sizes)) / (kern_ms * 1e-3) / 1e9
+    t_tok = measured_traffic(spec.name)
+    out = {
+        "metric": METRIC, "value": round(value, 1), "unit": "tok/s", "n_gpus": 1,
+        "steps": len(sizes), "warmup": args.warmup,
+        "ms_per_step": round(wall * 1e3 / len(sizes), 3),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "bf16" if model.dims.dtype == "bf16" else "fp32",
+        "data": "synthetic (seeded config stack, random weights and state; no checkpoint)",
+        "config": {"workload": f"{spec.name}: one {chunk}-token greedy chunk of the "
+                               f"{model.dims.n_layers}-layer synthetic sparse chip stack (hidden "
+                               f"{model.dims.hidden}, vocab {model.dims.vocab}) at batch 1, split "
+                               f"over {len(sizes)} launches continuing one stream",
+                   "chunk_tokens": chunk, "tokens_per_step": sizes, "batch": 1,
+                   "p_gate": spec.p_gate, "density": spec.density,
+                   "parallelism": f"single GPU (one chain workgroup + {mg.ncta - 1} helper "
+                                  "workgroups)"},
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 5),
+                     "traffic": None if t_tok is None else round(t_tok * chunk / len(sizes)),
+                     "bytes_per_token": round(b_tok),
+                     "kernel_ms_per_launch": round(kern_ms, 3),
+                     "launch_ms": [round(x, 2) for x in launch_ms]},
+        # the decode is latency-bound: one cross-XCD round trip per token for the head and two per
+        # GDN event (chain -> value-head helpers -> out_proj helpers -> chain), measured live
+        "latency_roofline": {"round_trip_us": rt, "round_trips_per_token": round(n_rt, 4),
+                             "gdn_events_per_token": round(ev_tok, 4),
+                             "t_sync_us": round(n_rt * rt, 2),
+                             "t_measured_us": round(us_tok, 2),
+                             "frac": round(n_rt * rt / us_tok, 4), "sync": sync},
+        "check": {"stream_sha256": stream_sha, "conv_sha256": conv_sha, "rec_sha256": rec_sha,
+                  "distinct_predictions": len(set(stream_preds)),
+                  "matches_oracle_chunk": None if gold is None else bool(
+                      gold["stream_sha256"] == stream_sha and gold["conv_sha256"] == conv_sha
+                      and gold["rec_sha256"] == rec_sha)},
+        "forced_input": forced_out,
+    }
+    if args.oracle_tokens > 0:
+        want = oracle_check(model, conv0, rec0, start, args.oracle_tokens)
+        out["check"]["oracle_prefix_tokens"] = len(want)
+        out["check"]["oracle_prefix_match"] = want == stream_preds[:len(want)]
+    del mg, cache, saved
+    torch.cuda.empty_cache()
+    if args.cpu_seconds > 0:
+        from linuxformer_amd import synth as sy
+
+        t = time.time()
+        hf = sy.to_hf(model)
+        hf_holder["hf"] = hf
+        hf_holder["conv0"], hf_holder["rec0"] = conv0, rec0
+        log(f"[bench] stock model (dense, bf16) built in {time.time() - t:.1f}s")
+        tps, n, cp = stock_decode_baseline(hf, conv0, rec0, start, 64, args.cpu_seconds)
+        out["cpu_baseline"] = {
+            "value": round(tps, 3), "unit": "tok/s", "cores": cpu_threads(), "kind": "port",
+            "impl": "torch-eager",
+            "sample": f"the chunk's first {n} greedy steps through the stock forward "
+                      f"(transformers {_tf_version()} Qwen3_5 decoder layers on dense bf16 "
+                      "tensors, torch eager, lx/lx/hf.py:169-184's chip view), "
+                      f"{cpu_threads()} host threads"}
+        out["check"]["stock_prefix_match"] = cp == stream_preds[:n]
+        log(f"[bench] CPU stock decode: {tps:.3f} tok/s over {n} steps")
+    return out
 
 
-def latency_roofline(n_layers: int, us_per_token: float) -> dict:
-    """The decode's latency term: a token's dependent chain is two phases per layer (the GDN, then
-    the MLP that reads its residual) and the head, and with the rarely-writing GDN phases paired
-    with their MLP about n_layers + 1 grid-wide synchronisations; at the measured barrier cost
-    that bounds a design that syncs the grid per phase. This kernel runs the chain on one
-    workgroup instead and syncs across workgroups only for the head and GDN events."""
-    p = n_layers + 1
-    t = p * T_BAR_US
-    return {"dependent_syncs_per_token": p, "t_bar_us": T_BAR_US, "t_roof_us": round(t, 1),
-            "t_measured_us": round(us_per_token, 2), "frac": round(t / us_per_token, 4)}
+def _tf_version() -> str:
+    import transformers
+
+    return transformers.__version__
 
 
-def prefill_leg(calls: int, T: int, cpu_tokens: int) -> dict:
+def prefill_leg(args, dev, hf_holder: dict) -> dict:
     """verified-mode calls of T seeded uniform tokens; tok/s over the timed
     calls (HIP events around each call on the current stream, inputs resident)."""
     import numpy as np
@@ -121,16 +358,17 @@ def prefill_leg(calls: int, T: int, cpu_tokens: int) -> dict:
 
     from linuxformer_amd import fast, synth
 
+    calls, T = args.pf_calls, args.pf_tokens
     spec = synth.config3()
     t0 = time.time()
     model = synth.build(spec)
     conv0, rec0 = synth.init_state(model)
     f = fast.Fast(model)
-    dev = torch.device("cuda", 0)
     cache = fast.StateCache(conv0, rec0, model.dims.dtype, dev)
     pf = f.prefill(dev)
     d = model.dims
-    log(f"[bench] c3: built and packed in {time.time() - t0:.1f}s; {json.dumps({k: v for k, v in pf.stats.items() if not isinstance(v, list)})}")
+    log(f"[bench] c3: built and packed in {time.time() - t0:.1f}s; "
+        f"{json.dumps({k: v for k, v in pf.stats.items() if not isinstance(v, list)})}")
     stream = torch.cuda.current_stream(dev)
     first = synth.tokens(spec, T, 0)
     p0 = pf.verify(first, cache).cpu().numpy()  # warm-up calls (the first is the parity sample)
@@ -170,20 +408,33 @@ def prefill_leg(calls: int, T: int, cpu_tokens: int) -> dict:
                         "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 5),
                         "bytes_per_position": round(b_pos),
                         "traffic": None if t_pos is None else round(t_pos * T)}}
-    if cpu_tokens > 0:
-        from oracle import oracle as ox
+    del pf, cache
+    torch.cuda.empty_cache()
+    n_cpu = args.pf_cpu_tokens
+    if n_cpu > 0 and args.cpu_seconds > 0:
+        from linuxformer_amd import synth as sy
+        from oracle import stock
 
-        ox.build()
-        om = ox.OracleModel(model)
-        c, r = conv0.copy(), rec0.copy()
+        hf = hf_holder.get("hf")
+        if hf is None:
+            hf = sy.to_hf(model)
+            hf_holder["hf"] = hf
+        else:  # config 3 shares config 2's layers; only the embedding's gate columns differ
+            stock.set_embedding(hf, model.embed)
+        stock.prefill(hf, conv0, rec0, first[:8])  # warm-up (first touch)
         t = time.perf_counter()
-        po, _, _ = om.decode(c, r, [int(x) for x in first[:cpu_tokens]], cpu_tokens)
+        pc, _, _ = stock.prefill(hf, conv0, rec0, first[:n_cpu])
         dt = time.perf_counter() - t
-        out["cpu_baseline"] = {"value": round(cpu_tokens / dt, 2), "unit": "tok/s", "cores": 1,
-                               "kind": "port", "sample": f"the first {cpu_tokens} positions of "
-                               "the warm-up call (C oracle's forced decode, one thread)"}
-        out["check"] = {"oracle_positions": cpu_tokens,
-                        "preds_match": bool(po.tolist() == p0[:cpu_tokens].tolist())}
+        agree = float((pc == p0[:n_cpu]).mean())
+        out["cpu_baseline"] = {
+            "value": round(n_cpu / dt, 2), "unit": "tok/s", "cores": cpu_threads(),
+            "kind": "port", "impl": "torch-eager",
+            "sample": f"one call over the first {n_cpu} positions of the warm-up call's tokens: "
+                      f"the stock forward's T > 1 path (transformers {_tf_version()} "
+                      "Qwen3_5 layers, torch_chunk_gated_delta_rule, dense bf16, torch eager), "
+                      f"{cpu_threads()} host threads"}
+        out["check"] = {"stock_positions": n_cpu, "stock_argmax_agreement": agree}
+        log(f"[bench] CPU stock prefill: {n_cpu / dt:.2f} tok/s; argmax agreement {agree:.4f}")
     return out
 
 
@@ -191,18 +442,18 @@ def dense_cpu_tok_s(dm, n: int) -> float:
     """The dense stack's decode step restated with torch's eager ops in float32 on the host cores
     (weights copied from the GPU once; the stock forward's structure, not its bit order): tok/s
     over n greedy steps from a zero state. A reported baseline only."""
-    import numpy as np
     import torch
     import torch.nn.functional as F
 
     sp, d = dm.spec, dm.dims
     H, nk, kl, rl = sp.hidden, sp.nk, sp.kd_live, sp.r_live
-    torch.set_num_threads(os.cpu_count() or 1)
     L = [{k: v.float().cpu() for k, v in ly.items()} for ly in dm.layers]
     E = dm.embed.float().cpu()
     wf = dm.norm.float().cpu()
     S = [torch.zeros(nk * rl, 256, 128) for _ in L]
     win = [torch.zeros(2 * nk * kl + nk * rl * 128, 4) for _ in L]
+    R = d.nv // nk
+    vh = torch.tensor([kh * R + r for kh in range(nk) for r in range(rl)])
 
     def rms(x, w, eps):
         return (x * torch.rsqrt(x.pow(2).mean() + eps)) * (1.0 + w)
@@ -225,8 +476,6 @@ def dense_cpu_tok_s(dm, n: int) -> float:
             q = F.normalize(y[:nk * kl].view(nk, kl), dim=-1).repeat_interleave(rl, 0) / 16.0
             k = F.normalize(y[nk * kl:2 * nk * kl].view(nk, kl), dim=-1).repeat_interleave(rl, 0)
             vv = y[2 * nk * kl:].view(nk * rl, 128)
-            R = d.nv // nk
-            vh = torch.tensor([kh * R + r for kh in range(nk) for r in range(rl)])
             g = torch.exp(-torch.exp(ly["A_log"][vh]) * F.softplus(a + ly["dt_bias"][vh]))
             St = S[i][:, :kl] * g[:, None, None]
             kv = (St * k[:, :, None]).sum(1)
@@ -241,8 +490,7 @@ def dense_cpu_tok_s(dm, n: int) -> float:
     return n / (time.perf_counter() - t)
 
 
-def dense_leg(n_prefill: int, n_steps: int, cpu_tokens: int, graph: bool = True,
-              persistent: bool = True, batched: bool = True) -> dict:
+def dense_leg(args, dev) -> dict:
     """the dense padded text-view stack; a prompt of n_prefill seeded uniform
     tokens from a zero state (batched: lxm_dn_prefill over all but the last, then one step;
     else n_prefill forced steps), then n_steps greedy steps, timed (HIP events on the stream)."""
@@ -251,26 +499,26 @@ def dense_leg(n_prefill: int, n_steps: int, cpu_tokens: int, graph: bool = True,
 
     from linuxformer_amd import dense, fast, synth
 
+    n_prefill, n_steps, graph = args.dn_prefill, args.dn_steps, bool(args.dn_graph)
     spec = synth.config4()
     t0 = time.time()
     dm = synth.build_dense(spec, "cuda")
     d = dm.dims
     conv0 = np.zeros((d.n_layers, d.n_conv, 4), np.float32)
     rec0 = np.zeros((d.n_layers, d.nv, 256, 128), np.float32)
-    cache = fast.StateCache(conv0, rec0, "bf16", torch.device("cuda", 0))
+    cache = fast.StateCache(conv0, rec0, "bf16", dev)
     dd = dense.DenseDecode(dm, cache, max_steps=max(n_prefill, n_steps) + 1)
     torch.cuda.synchronize()
     log(f"[bench] c4: built in {time.time() - t0:.1f}s")
     toks = np.random.default_rng(spec.seed).integers(0, spec.vocab, n_prefill).tolist()
     t = time.perf_counter()
-    if batched:
+    if args.dn_batched:
         dd.prefill(toks[:-1])  # lxm_dn_prefill: the same states as forced steps, bit for bit
         p1 = dd.run(toks[-1:], 1, graph=graph)
     else:
         p1 = dd.run(toks, n_prefill, graph=graph)
     pre_s = time.perf_counter() - t
-    log(f"[bench] c4: prefill of {n_prefill} tokens in {pre_s:.2f}s "
-        f"({'batched, then one step' if batched else 'forced steps'})")
+    log(f"[bench] c4: prefill of {n_prefill} tokens in {pre_s:.2f}s")
     stream = torch.cuda.current_stream()
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     e0.record(stream)
@@ -278,10 +526,9 @@ def dense_leg(n_prefill: int, n_steps: int, cpu_tokens: int, graph: bool = True,
     e1.record(stream)
     torch.cuda.synchronize()
     ms = e0.elapsed_time(e1)
-    # the same steps as one persistent launch (lxm_dn_run), timed the same way
     n_per = max(1, n_steps // 4)
     ms_per = None
-    if persistent:
+    if args.dn_persistent:
         e2, e3 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         e2.record(stream)
         dd.run([p2[-1]], n_per, mode="persistent")
@@ -298,19 +545,22 @@ def dense_leg(n_prefill: int, n_steps: int, cpu_tokens: int, graph: bool = True,
     t_tok = measured_traffic("c4", "dense")
     # fused multiply-adds per prompt token: every live weight of every layer once
     fma_tok = d.n_layers * ((2 * nk * kl + 2 * nvr + 2 * nk * rl) * H + H * nvr + 3 * I * H)
+    pf_rate = 2 * fma_tok * n_prefill / pre_s / 1e12
     out = {"metric": "dense padded decode tok/s, 24-layer text-view stack, 1 MI355X",
            "value": round(n_steps / (ms * 1e-3), 1), "unit": "tok/s",
            "ms_per_token": round(ms / n_steps, 4), "steps": n_steps,
            "prefill": {"tokens": n_prefill, "s": round(pre_s, 2),
                        "tok_s": round(n_prefill / pre_s, 1),
-                       "mode": "lxm_dn_prefill (batches of 16) + one step" if batched
+                       "mode": "lxm_dn_prefill (batches of 16) + one step" if args.dn_batched
                                else "forced steps",
                        # the prompt's row sums are fp32 fused ops on the VALU (bf16 x bf16
                        # products, summed in the decode's order); packed fp32 is not used, so
                        # the vector rate available is half the published fp32 peak
-                       "roofline": {"bound": "valu", "achieved": round(2 * fma_tok * n_prefill / pre_s / 1e12, 2),
-                                    "peak": FP32_PEAK_TFLOPS, "unit": "TFLOP/s",
-                                    "frac": round(2 * fma_tok * n_prefill / pre_s / 1e12 / FP32_PEAK_TFLOPS, 4),
+                       "roofline": {"bound": "valu", "achieved": round(pf_rate, 2),
+                                    "peak": FP32_PEAK_TFLOPS / 2, "unit": "TFLOP/s",
+                                    "frac": round(pf_rate / (FP32_PEAK_TFLOPS / 2), 4),
+                                    "peak_note": "half of the published 157.3 TFLOP/s fp32 peak: "
+                                                 "no packed fp32 ops",
                                     "flops_per_token": 2 * fma_tok}},
            "config": {"workload": "c4: 24 layers, hidden 2560, 16 key heads (256, 128 live), 128 "
                                   "value heads (2 live per key head), SwiGLU 9216, vocab 248,320, "
@@ -324,28 +574,33 @@ def dense_leg(n_prefill: int, n_steps: int, cpu_tokens: int, graph: bool = True,
            "persistent": None if ms_per is None else
                          {"steps": n_per, "tok_s": round(n_per / (ms_per * 1e-3), 1),
                           "note": "lxm_dn_run, continuing from the greedy run's states"}}
-    if cpu_tokens > 0:
-        out["cpu_baseline"] = {"value": round(dense_cpu_tok_s(dm, cpu_tokens), 3), "unit": "tok/s",
-                               "cores": os.cpu_count(), "kind": "port",
-                               "sample": f"{cpu_tokens} greedy steps from a zero state, torch eager "
-                                         "float32 on the host"}
+    if args.dn_cpu_tokens > 0 and args.cpu_seconds > 0:
+        out["cpu_baseline"] = {"value": round(dense_cpu_tok_s(dm, args.dn_cpu_tokens), 3),
+                               "unit": "tok/s", "cores": cpu_threads(), "kind": "port",
+                               "impl": "torch-eager",
+                               "sample": f"{args.dn_cpu_tokens} greedy steps from a zero state, "
+                                         "the stock layer's ops in torch eager float32"}
     return out
 
 
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=1)
-    ap.add_argument("--warmup", type=int, default=1)
-    ap.add_argument("--tokens", type=int, default=262_144)
-    ap.add_argument("--warmup-tokens", type=int, default=4096)
+    ap.add_argument("--steps", type=int, default=20, help="launches the chunk is split over")
+    ap.add_argument("--warmup", type=int, default=5, help="untimed launches of chunk/steps tokens")
+    ap.add_argument("--chunk", type=int, default=262_144, help="tokens of the timed greedy chunk")
     ap.add_argument("--config", default="c2", choices=["c1", "c2", "c5", "small"])
-    ap.add_argument("--cpu-tokens", type=int, default=256, help="CPU baseline sample (0: skip)")
+    ap.add_argument("--forced-tokens", type=int, default=16_384,
+                    help="tokens of the forced-input launch (0: skip)")
+    ap.add_argument("--oracle-tokens", type=int, default=256,
+                    help="chunk prefix checked against the C oracle (0: skip)")
+    ap.add_argument("--cpu-seconds", type=float, default=15.0,
+                    help="wall time of each CPU baseline's sample (0: skip the baselines)")
     ap.add_argument("--legs", default="decode,prefill,dense",
                     help="comma-separated: decode (config 2), prefill (config 3), dense (config 4)")
     ap.add_argument("--pf-calls", type=int, default=5)
     ap.add_argument("--pf-tokens", type=int, default=65_536)
-    ap.add_argument("--pf-cpu-tokens", type=int, default=48)
+    ap.add_argument("--pf-cpu-tokens", type=int, default=256)
     ap.add_argument("--dn-prefill", type=int, default=8192)
     ap.add_argument("--dn-steps", type=int, default=4096)
     ap.add_argument("--dn-cpu-tokens", type=int, default=4)
@@ -360,104 +615,25 @@ def main() -> int:
         print(f"bench.py measures one GPU: the decode is one sequential chain per stream and this "
               f"build runs on a single MI355X (asked for --gpus {args.gpus}).", file=sys.stderr)
         return 2
+    if args.steps < 1 or args.warmup < 0 or args.chunk < args.steps:
+        print("bench.py: need steps >= 1, warmup >= 0 and chunk >= steps", file=sys.stderr)
+        return 2
 
-    legs = set(args.legs.split(","))
-    if "decode" not in legs:
-        out = {}
-        if "prefill" in legs:
-            out["verified_prefill"] = prefill_leg(args.pf_calls, args.pf_tokens, args.pf_cpu_tokens)
-        if "dense" in legs:
-            out["dense_decode"] = dense_leg(args.dn_prefill, args.dn_steps, args.dn_cpu_tokens,
-                                            bool(args.dn_graph), bool(args.dn_persistent), bool(args.dn_batched))
-        print(json.dumps(out), flush=True)
-        return 0
-
-    import numpy as np
     import torch
 
-    from linuxformer_amd import fast, mega, synth
-
-    spec = {"c1": synth.config1(), "c2": synth.config2(), "c5": synth.config5(),
-            "small": synth.small()}[args.config]
-    t0 = time.time()
-    model = synth.build(spec)
-    conv0, rec0 = synth.init_state(model)
-    start = synth.start_token(spec)
-    f = fast.Fast(model)
+    torch.set_grad_enabled(False)
     dev = torch.device("cuda", 0)
-    cache = fast.StateCache(conv0, rec0, model.dims.dtype, dev)
-    mg = mega.Mega(f, model, cache, 0)
-    torch.cuda.synchronize()
-    log(f"[bench] {spec.name}: built and packed in {time.time() - t0:.1f}s; "
-        f"{json.dumps({k: v for k, v in mg.stats.items() if not isinstance(v, list)})}")
-
-    stream = torch.cuda.current_stream(dev)
-    # warm-up launches continue the stream from the start token; their first predictions are
-    # checked against the CPU oracle below
-    tok = start
-    first_preds = None
-    for w in range(args.warmup):
-        preds = mg.run([tok], args.warmup_tokens)
-        if first_preds is None:
-            first_preds = preds
-        tok = preds[-1]
-        log(f"[bench] warm-up launch {w + 1}/{args.warmup}: {args.warmup_tokens} tokens")
-    torch.cuda.synchronize()
-    # timed: K launches of T tokens, events on the launch stream around each
-    evs = []
-    t_start = time.perf_counter()
-    for k in range(args.steps):
-        e0 = torch.cuda.Event(enable_timing=True)
-        e1 = torch.cuda.Event(enable_timing=True)
-        e0.record(stream)
-        preds = mg.run([tok], args.tokens)
-        e1.record(stream)
-        evs.append((e0, e1))
-        tok = preds[-1]
-        log(f"[bench] timed launch {k + 1}/{args.steps}: {args.tokens} tokens, "
-            f"distinct predictions {len(set(preds))}")
-    torch.cuda.synchronize()
-    wall = time.perf_counter() - t_start
-    kern_ms = sum(a.elapsed_time(b) for a, b in evs) / len(evs)
-    n_tok = args.steps * args.tokens
-    value = n_tok / wall
-    # roofline: SURVEY 8(d)'s algorithmic bytes per token x tokens per launch / launch time
-    b_tok = survey_bytes_per_token(model, spec.p_gate)
-    achieved = b_tok * args.tokens / (kern_ms * 1e-3) / 1e9
-    t_tok = measured_traffic(spec.name)
-    out = {
-        "metric": METRIC, "value": round(value, 1), "unit": "tok/s", "n_gpus": 1,
-        "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(wall * 1e3 / args.steps, 3),
-        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16" if model.dims.dtype == "bf16" else "fp32",
-        "data": "synthetic (seeded config stack, random weights and state; no checkpoint)",
-        "config": {"workload": f"{spec.name}: {model.dims.n_layers}-layer synthetic sparse chip stack, "
-                               f"hidden {model.dims.hidden}, vocab {model.dims.vocab}, greedy decode "
-                               f"chunks of {args.tokens} tokens at batch 1",
-                   "tokens_per_step": args.tokens, "batch": 1, "p_gate": spec.p_gate,
-                   "density": spec.density, "parallelism": "single GPU (one chain workgroup + "
-                   f"{mg.ncta - 1} head workgroups)"},
-        "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS,
-                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 5),
-                     "traffic": None if t_tok is None else round(t_tok * args.tokens),
-                     "bytes_per_token": round(b_tok), "kernel_ms_per_launch": round(kern_ms, 3)},
-        "latency_roofline": latency_roofline(model.dims.n_layers, kern_ms * 1e3 / args.tokens),
-    }
-    if args.cpu_tokens > 0:
-        cps, cpreds = cpu_baseline(model, conv0, rec0, start, args.cpu_tokens)
-        m = min(len(cpreds), len(first_preds or []))
-        match = bool(m > 0 and list(cpreds[:m]) == list(first_preds[:m]))
-        out["cpu_baseline"] = {"value": round(cps, 2), "unit": "tok/s", "cores": 1, "kind": "port",
-                               "sample": f"first {args.cpu_tokens} tokens of the {spec.name} stream "
-                                         f"(C oracle, one thread)"}
-        out["check"] = {"oracle_tokens": m, "preds_match": match}
+    legs = set(args.legs.split(","))
+    t_all = time.time()
+    hf_holder: dict = {}
+    out = decode_leg(args, dev, hf_holder) if "decode" in legs else {}
     if "prefill" in legs:
-        del mg, cache
-        torch.cuda.empty_cache()
-        out["verified_prefill"] = prefill_leg(args.pf_calls, args.pf_tokens, args.pf_cpu_tokens)
+        out["verified_prefill"] = prefill_leg(args, dev, hf_holder)
+    hf_holder.clear()
     if "dense" in legs:
         torch.cuda.empty_cache()
-        out["dense_decode"] = dense_leg(args.dn_prefill, args.dn_steps, args.dn_cpu_tokens,
-                                        bool(args.dn_graph), bool(args.dn_persistent), bool(args.dn_batched))
+        out["dense_decode"] = dense_leg(args, dev)
+    log(f"[bench] total {time.time() - t_all:.1f}s")
     print(json.dumps(out), flush=True)
     return 0
 

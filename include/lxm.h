@@ -167,6 +167,16 @@ int lxm_t_elem(int fn, const float* x, float* y, long n, void* stream);
    values (x row-major); out (rows). */
 int lxm_t_sum(int kind, const float* x, int n, int rows, float* out, void* stream);
 
+/* Cross-workgroup synchronisation costs, measured with the decode's own primitives (agent-scope
+   words, one polling thread per workgroup, bounded spins): kind 0, a grid barrier over n_blocks
+   workgroups on 8 per-XCD counter copies; kind 1, a round trip between workgroup 0 and workgroup
+   far (1: another XCD, 8: the same one). n_iter timed operations after a first; *out_us (device)
+   gets microseconds per operation, or -1 when a wait timed out (then *err is nonzero). words
+   (device, at least 320 uint32) and err (device) must be zero at launch. The role of the
+   reference's barrier profile counters (lx/csrc/mega.cu:732-737); a cooperative launch. */
+int lxm_t_sync(int kind, int n_iter, int n_blocks, int far, uint32_t* words, int32_t* err,
+               float* out_us, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

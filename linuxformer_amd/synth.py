@@ -381,8 +381,9 @@ def _round(x: np.ndarray, dtype: str) -> np.ndarray:
 
 
 def to_hf(model: SparseModel, dev: str = "cpu"):
-    """The model as a stock transformers Qwen3_5ForCausalLM (dense tensors; small models only):
-    n_layers linear-attention layers, the tied head, the final norm."""
+    """The model as a stock transformers Qwen3_5ForCausalLM (dense tensors: config 2's stack
+    takes 16 GB in bf16 plus 3.3 GB of tied embedding): n_layers linear-attention layers, the
+    tied head, the final norm."""
     import torch
     from transformers import Qwen3_5ForCausalLM, Qwen3_5TextConfig
 
@@ -401,24 +402,31 @@ def to_hf(model: SparseModel, dev: str = "cpu"):
         m = Qwen3_5ForCausalLM(cfg)
     sd = {}
     t = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(dt)  # noqa: E731
+
+    def dense(coo):  # scattered straight into a zeroed tensor of the model dtype
+        w = torch.zeros(coo.shape, dtype=dt)
+        if coo.nnz:
+            w[torch.from_numpy(coo.rows), torch.from_numpy(coo.cols)] = t(coo.vals)
+        return w
+
     for L, lay in enumerate(model.layers):
         p = f"model.layers.{L}."
         ga = p + "linear_attn."
-        sd[ga + "in_proj_qkv.weight"] = t(lay.in_proj_qkv.dense())
-        sd[ga + "in_proj_z.weight"] = t(lay.in_proj_z.dense())
-        sd[ga + "in_proj_b.weight"] = t(lay.in_proj_b.dense())
-        sd[ga + "in_proj_a.weight"] = t(lay.in_proj_a.dense())
-        sd[ga + "out_proj.weight"] = t(lay.out_proj.dense())
+        sd[ga + "in_proj_qkv.weight"] = dense(lay.in_proj_qkv)
+        sd[ga + "in_proj_z.weight"] = dense(lay.in_proj_z)
+        sd[ga + "in_proj_b.weight"] = dense(lay.in_proj_b)
+        sd[ga + "in_proj_a.weight"] = dense(lay.in_proj_a)
+        sd[ga + "out_proj.weight"] = dense(lay.out_proj)
         sd[ga + "conv1d.weight"] = t(lay.conv1d[:, None, :])
         sd[ga + "A_log"] = t(lay.A_log)
         sd[ga + "dt_bias"] = t(lay.dt_bias)
         sd[ga + "norm.weight"] = t(lay.norm)
         sd[p + "input_layernorm.weight"] = t(lay.input_layernorm)
         sd[p + "post_attention_layernorm.weight"] = t(lay.post_attention_layernorm)
-        sd[p + "mlp.gate_proj.weight"] = t(lay.gate_proj.dense())
-        sd[p + "mlp.up_proj.weight"] = t(lay.up_proj.dense())
-        sd[p + "mlp.down_proj.weight"] = t(lay.down_proj.dense())
-    sd["model.embed_tokens.weight"] = t(model.embed.dense())
+        sd[p + "mlp.gate_proj.weight"] = dense(lay.gate_proj)
+        sd[p + "mlp.up_proj.weight"] = dense(lay.up_proj)
+        sd[p + "mlp.down_proj.weight"] = dense(lay.down_proj)
+    sd["model.embed_tokens.weight"] = dense(model.embed)
     sd["model.norm.weight"] = t(model.norm)
     missing, unexpected = m.load_state_dict(sd, strict=False, assign=True)
     assert not unexpected and set(missing) <= {"lm_head.weight"}, (missing[:4], unexpected[:4])

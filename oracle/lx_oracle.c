@@ -309,8 +309,10 @@ float ox_row_dot(int blocks, int n, const float* x, const float* w) {
   return r;
 }
 
-/* out[r] = D(row r . x) */
+/* out[r] = D(row r . x); rows are independent, so they are spread over the host's threads (each
+   row's own sum keeps its order) */
 static void csr_mv(const ox_csr* m, const float* x, float* out) {
+#pragma omp parallel for schedule(static) if (m->nrows >= 2048)
   for (int r = 0; r < m->nrows; r++) out[r] = D(row_dot(m, r, x));
 }
 
@@ -357,11 +359,13 @@ static int rec_heads(const ox_dims* d, const float* qall, const float* kall, con
                      const float* g, const float* betas, float* S, ox_ws* w) {
   const int kd = d->kd, vd = d->vd, nk = d->nk, nv = d->nv, R = nv / nk;
   int any = 0;
+  int klive[64];
   for (int kh = 0; kh < nk; kh++) {
     const float* q = qall + (size_t)kh * kd;
     const float* k = kall + (size_t)kh * kd;
     int live = 0;
     for (int i = 0; i < kd; i++) live |= (q[i] != 0.0f) | (k[i] != 0.0f);
+    klive[kh] = live;
     float* qn = w->qn + (size_t)kh * kd;
     float* kn = w->kn + (size_t)kh * kd;
     if (live) {
@@ -369,32 +373,36 @@ static int rec_heads(const ox_dims* d, const float* qall, const float* kall, con
       l2norm_D(k, kd, w->sq, kn);
       for (int i = 0; i < kd; i++) qn[i] = qn[i] * 0.0625f; /* 1 / sqrt(256) */
     }
-    for (int r = 0; r < R; r++) {
-      const int vh = kh * R + r;
-      float* Sv = S + (size_t)vh * kd * vd;
-      float* o = w->o + (size_t)vh * vd;
-      const float e = ox_expf(g[vh]);
-      w->proc[vh] = live || e != 1.0f;
-      for (int j = 0; j < vd; j++) o[j] = 0.0f;
-      if (!w->proc[vh]) continue;
-      if (e != 1.0f)
-        for (size_t i = 0; i < (size_t)kd * vd; i++) Sv[i] = Sv[i] * e;
-      if (!live) continue; /* q = 0: output exactly 0 */
-      const float* v = vall + (size_t)vh * vd;
-      const float beta = betas[vh];
-      for (int j = 0; j < vd; j++) {
-        float s = row_sum(Sv + j, vd, kn, kd);
-        w->kv[j] = s;
-        w->delta[j] = (v[j] - s) * beta;
-      }
-      for (int i = 0; i < kd; i++) {
-        if (kn[i] == 0.0f) continue;
-        for (int j = 0; j < vd; j++) Sv[(size_t)i * vd + j] = Sv[(size_t)i * vd + j] + kn[i] * w->delta[j];
-      }
-      for (int j = 0; j < vd; j++) o[j] = D(row_sum(Sv + j, vd, qn, kd));
-      w->proc[vh] = 2;
-      any = 1;
+  }
+  /* value heads are independent: each owns its state tile, output and flag */
+#pragma omp parallel for schedule(dynamic) reduction(| : any) if (nv >= 16)
+  for (int vh = 0; vh < nv; vh++) {
+    const int kh = vh / R, live = klive[kh];
+    const float* qn = w->qn + (size_t)kh * kd;
+    const float* kn = w->kn + (size_t)kh * kd;
+    float* Sv = S + (size_t)vh * kd * vd;
+    float* o = w->o + (size_t)vh * vd;
+    float delta[256];
+    const float e = ox_expf(g[vh]);
+    w->proc[vh] = live || e != 1.0f;
+    for (int j = 0; j < vd; j++) o[j] = 0.0f;
+    if (!w->proc[vh]) continue;
+    if (e != 1.0f)
+      for (size_t i = 0; i < (size_t)kd * vd; i++) Sv[i] = Sv[i] * e;
+    if (!live) continue; /* q = 0: output exactly 0 */
+    const float* v = vall + (size_t)vh * vd;
+    const float beta = betas[vh];
+    for (int j = 0; j < vd; j++) {
+      float s = row_sum(Sv + j, vd, kn, kd);
+      delta[j] = (v[j] - s) * beta;
     }
+    for (int i = 0; i < kd; i++) {
+      if (kn[i] == 0.0f) continue;
+      for (int j = 0; j < vd; j++) Sv[(size_t)i * vd + j] = Sv[(size_t)i * vd + j] + kn[i] * delta[j];
+    }
+    for (int j = 0; j < vd; j++) o[j] = D(row_sum(Sv + j, vd, qn, kd));
+    w->proc[vh] = 2;
+    any = 1;
   }
   return any;
 }
@@ -414,14 +422,21 @@ static void layer_step(const ox_model* m, int L, float* h, float* cs, float* S, 
   csr_mv(&ly->b, w->xn, w->b);
   csr_mv(&ly->a, w->xn, w->a);
   /* causal_conv1d_update (TF:199-216): window <- [window[1:], P]; y = silu(D(sum w_i x_i)) */
+#pragma omp parallel for schedule(static) if (C >= 2048)
   for (int c = 0; c < C; c++) {
     float* win = cs + (size_t)c * K;
+    if (w->P[c] == 0.0f) { /* a zero window stays zero and gives +0 (a sum from +0 of zeros) */
+      int zero = 1;
+      for (int i = 0; i < K; i++) zero &= win[i] == 0.0f;
+      if (zero) { w->y[c] = 0.0f; continue; }
+    }
     for (int i = 0; i + 1 < K; i++) win[i] = win[i + 1];
     win[K - 1] = w->P[c];
     const float* tw = ly->conv_w + (size_t)c * K;
     float s = 0.0f;
     for (int i = 0; i < K; i++) s = s + tw[i] * win[i];
-    w->y[c] = D(ox_silu(D(s)));
+    const float ds = D(s);
+    w->y[c] = D(ds == 0.0f ? ds : ox_silu(ds)); /* silu(+-0) = +-0: skips the exp */
   }
   for (int v = 0; v < nv; v++) {
     w->beta[v] = D(ox_sigmoid(w->b[v]));
@@ -463,7 +478,10 @@ static void layer_step(const ox_model* m, int L, float* h, float* cs, float* S, 
   rms_norm(h, H, d->rms_eps, ly->ln_post, hsq, w->xn);
   csr_mv(&ly->gate, w->xn, w->gt);
   csr_mv(&ly->up, w->xn, w->up);
-  for (int u = 0; u < d->inter; u++) w->act[u] = D(D(ox_silu(w->gt[u])) * w->up[u]);
+  for (int u = 0; u < d->inter; u++) {
+    const float gt = w->gt[u];
+    w->act[u] = D(D(gt == 0.0f ? gt : ox_silu(gt)) * w->up[u]); /* silu(+-0) = +-0 */
+  }
   csr_mv(&ly->down, w->act, w->out);
   for (int i = 0; i < H; i++) h[i] = D(h[i] + w->out[i]);
 }

@@ -1,4 +1,6 @@
-"""The stock forward (the reference semantics), run with transformers' own modules on the CPU.
+"""TEST INFRASTRUCTURE ONLY: the stock forward (the reference semantics), run with transformers'
+own modules on the CPU. It writes the golden vectors (tests/golden/make_golden.py) and is the CPU
+baseline bench.py times; the product never imports it.
 
 lx/lx/hf.py:169-184 defines it: the chip layers as stock Qwen3_5DecoderLayers with no positions
 or masks ("chip view"), carrying a DynamicCache; the head is the final norm and the tied
@@ -66,3 +68,32 @@ def decode(m, conv0, rec0, forced, n: int):
     conv = np.stack([cache.layers[k].conv_states[0][0].float().numpy() for k in range(L)])
     rec = np.stack([cache.layers[k].recurrent_states[0][0].float().numpy() for k in range(L)])
     return np.array(preds, np.int32), np.stack(trace), conv, rec
+
+
+@torch.no_grad()
+def prefill(m, conv0, rec0, tokens):
+    """The stock forward over T tokens at once (transformers' T > 1 path: causal_conv1d_fn over
+    the cached window and the new inputs, torch_chunk_gated_delta_rule in chunks of 64 from the
+    cached state; modeling_qwen3_5.py:249-327, :454-525), then every position's argmax, as
+    lx.fast's verified mode compares (lx/lx/fast.py:252-361). Returns (preds (T,), final conv,
+    final rec)."""
+    cache = make_cache(m, conv0, rec0)
+    emb = m.model.embed_tokens.weight
+    h = emb[torch.as_tensor(np.asarray(tokens, np.int64))][None]
+    outs = chip_forward(m, h, cache)
+    preds = head_argmax(m, outs[-1][0]).numpy().astype(np.int32)
+    L = m.config.num_hidden_layers
+    conv = np.stack([cache.layers[k].conv_states[0][0].float().numpy() for k in range(L)])
+    rec = np.stack([cache.layers[k].recurrent_states[0][0].float().numpy() for k in range(L)])
+    return preds, conv, rec
+
+
+def set_embedding(m, coo) -> None:
+    """Replace the tied embedding/head rows with a coordinate tensor's values (configs 2 and 3
+    share their layers and differ only in the embedding's gate columns)."""
+    w = m.model.embed_tokens.weight
+    with torch.no_grad():
+        w.zero_()
+        if coo.nnz:
+            w[torch.from_numpy(coo.rows), torch.from_numpy(coo.cols)] = \
+                torch.from_numpy(coo.vals).to(w.dtype)

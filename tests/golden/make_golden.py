@@ -2,7 +2,7 @@
 
 The stock forward is transformers 5.15.0's Qwen3_5 decoder layers (torch fallbacks; neither
 fla nor the hub kernels are installed) in lx/lx/hf.py's chip view, run token by token on the CPU
-by tests/stock.py; the reference pins 5.19.0 (requirements.txt:4), whose qwen3_5 code path for
+by oracle/stock.py; the reference pins 5.19.0 (requirements.txt:4), whose qwen3_5 code path for
 these ops is the same. Nothing of the reference repository is imported.
 
     python tests/golden/make_golden.py      # rewrites tests/golden/*.npz
@@ -26,7 +26,7 @@ sys.path.insert(0, os.path.dirname(os.path.dirname(HERE)))
 sys.path.insert(0, os.path.dirname(HERE))
 
 from linuxformer_amd import synth  # noqa: E402
-import stock  # noqa: E402
+from oracle import stock  # noqa: E402
 
 CASES = {
     # name: (spec builder, steps, keep full traces)

@@ -147,7 +147,7 @@ def test_layer_step_matches_stock_decoder_layer(oracle_lib):
     3.8e-6) -- and the state and conv window within 1e-6. (The sparse, chip-shaped config 1 is
     bit-identical: test_oracle_matches_stock_fp32; the delta rule alone is bit-identical:
     test_recurrent_step_bit_exact.)"""
-    import stock
+    from oracle import stock
 
     torch.set_grad_enabled(False)
     m = synth.tiny_dense(seed=11, dtype="fp32")
