@@ -167,6 +167,21 @@ int lxm_t_elem(int fn, const float* x, float* y, long n, void* stream);
    values (x row-major); out (rows). */
 int lxm_t_sum(int kind, const float* x, int n, int rows, float* out, void* stream);
 
+/* No counterpart in the reference: lxm_run for callers that cannot allocate device memory (code
+   under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc). The run buffers
+   (ring, rring, hn, sync, keys, mb_task, mb_e, mb_qk, ybuf, xo) and the parameter block's device
+   copy come from a static array of LXM_SCRATCH_BYTES per GPU (held until the process ends); the
+   corresponding fields of *p_host are ignored, everything else (tables, states, forced, preds,
+   inputs, trace, prof) and err (zeroed by this call) are the caller's, as for lxm_run. Allocates
+   nothing; clears what must start at zero with a kernel on the stream (no memset). Limits:
+   n_layers <= LXM_SCRATCH_MAXL, nv <= LXM_SCRATCH_MAXNV (hipErrorInvalidValue beyond them, and
+   for a missing err). Calls on one GPU share its array: calls that overlap in time on one GPU
+   race, so issue them on one stream (or wait between them). */
+#define LXM_SCRATCH_MAXL 64
+#define LXM_SCRATCH_MAXNV 256
+#define LXM_SCRATCH_BYTES 4368128
+int lxm_run_noalloc(const lxm_params* p_host, int n_blocks, int lds_bytes, void* stream);
+
 /* Cross-workgroup synchronisation costs, measured with the decode's own primitives (agent-scope
    words, one polling thread per workgroup, bounded spins): kind 0, a grid barrier over n_blocks
    workgroups on 8 per-XCD counter copies; kind 1, a round trip between workgroup 0 and workgroup

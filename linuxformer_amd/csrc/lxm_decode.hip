@@ -34,6 +34,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <mutex>
+
 #include "../../include/lxm.h"
 #include "lxm_math.h"
 #include "lxm_sync.h"
@@ -1717,6 +1719,75 @@ __global__ void __launch_bounds__(NT) k_sum(int kind, const float* x, int n, flo
 }
 
 // ---------------------------------------------------------------------------------------------
+// The no-allocation launch's per-device scratch: the parameter block's device copy and every run
+// buffer, at fixed 256-byte-aligned offsets (each GPU holds its own copy of the array).
+#define SC_PARAMS 0
+#define SC_SYNC 512
+#define SC_KEYS (SC_SYNC + 4 * LXM_NSYNC)
+#define SC_HN (SC_KEYS + 256)
+#define SC_XO (SC_HN + 4 * MAXH)
+#define SC_MBQK (SC_XO + 4 * MAXH)
+#define SC_MBTASK (SC_MBQK + 4 * LXM_MAXQKL)
+#define SC_MBE (SC_MBTASK + 4 * LXM_SCRATCH_MAXNV)
+#define SC_YBUF (SC_MBE + 4 * LXM_SCRATCH_MAXNV)
+#define SC_RRING (SC_YBUF + 4 * LXM_SCRATCH_MAXNV * VD)
+#define SC_RING (SC_RRING + 4 * 4 * LXM_SCRATCH_MAXL)
+#define SC_END (SC_RING + 4 * 4 * LXM_SCRATCH_MAXL * MAXH)
+static_assert(sizeof(lxm_params) <= SC_SYNC, "the parameter block fits its slot");
+static_assert(SC_END == LXM_SCRATCH_BYTES, "LXM_SCRATCH_BYTES matches the layout");
+static_assert(SC_KEYS % 256 == 0 && SC_RING % 256 == 0 && SC_YBUF % 256 == 0, "aligned slots");
+
+static __device__ __align__(256) uint8_t scratch[LXM_SCRATCH_BYTES];
+
+// the parameter block into the scratch's slot, and the words that must start at zero cleared:
+// the sync area, the head keys and the caller's error word
+__global__ void __launch_bounds__(256) k_noalloc_prep(lxm_params p, uint8_t* sc) {
+  if (threadIdx.x == 0) *reinterpret_cast<lxm_params*>(sc + SC_PARAMS) = p;
+  uint32_t* sync = reinterpret_cast<uint32_t*>(sc + SC_SYNC);
+  for (int i = threadIdx.x; i < LXM_NSYNC; i += blockDim.x) sync[i] = 0u;
+  if (threadIdx.x < 2) reinterpret_cast<unsigned long long*>(sc + SC_KEYS)[threadIdx.x] = 0ull;
+  if (threadIdx.x == 0) *p.err = 0;
+}
+
+static const void* decode_fn(const lxm_params* p) {
+  const bool tr = p->trace != nullptr;
+  return p->bf16 ? (tr ? (const void*)lxm_decode<true, true, true>
+                       : (const void*)lxm_decode<true, true, false>)
+         : p->e4 ? (tr ? (const void*)lxm_decode<false, true, true>
+                       : (const void*)lxm_decode<false, true, false>)
+                 : (tr ? (const void*)lxm_decode<false, false, true>
+                       : (const void*)lxm_decode<false, false, false>);
+}
+
+static hipError_t launch_decode(const void* fn, const lxm_params* pd, int n_blocks, int lds_bytes,
+                                hipStream_t stream) {
+  void* args[] = {&pd};
+  hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, lds_bytes);
+  if (e != hipSuccess) return e;
+  return hipLaunchCooperativeKernel(fn, dim3(n_blocks), dim3(NT), args, (unsigned)lds_bytes, stream);
+}
+
+#define SC_MAX_DEVICES 64
+static std::mutex g_scratch_mu;
+static uint8_t* g_scratch[SC_MAX_DEVICES];  // the scratch's device address, per device
+
+// the current device's scratch address (hipGetSymbolAddress once per device, with it current)
+static hipError_t scratch_ptr(uint8_t** out) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return e;
+  if (dev < 0 || dev >= SC_MAX_DEVICES) return hipErrorInvalidDevice;
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch[dev]) {
+    void* ptr = nullptr;
+    e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return e;
+    g_scratch[dev] = static_cast<uint8_t*>(ptr);
+  }
+  *out = g_scratch[dev];
+  return hipSuccess;
+}
+
 extern "C" {
 
 int lxm_lds_base(void) { return L_CHAIN_END; }
@@ -1725,20 +1796,32 @@ int lxm_helper_lds(int head_lds) { return HX_END + head_lds + 256; }  // (reads 
 
 int lxm_run(const lxm_params* p_host, const lxm_params* p_dev, int n_blocks, int lds_bytes,
             void* stream) {
-  const lxm_params* pd = p_dev;
-  void* args[] = {&pd};
-  const bool tr = p_host->trace != nullptr;
-  const void* fn = p_host->bf16 ? (tr ? (const void*)lxm_decode<true, true, true>
-                                      : (const void*)lxm_decode<true, true, false>)
-                   : p_host->e4 ? (tr ? (const void*)lxm_decode<false, true, true>
-                                      : (const void*)lxm_decode<false, true, false>)
-                                : (tr ? (const void*)lxm_decode<false, false, true>
-                                      : (const void*)lxm_decode<false, false, false>);
-  hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, lds_bytes);
+  return (int)launch_decode(decode_fn(p_host), p_dev, n_blocks, lds_bytes, (hipStream_t)stream);
+}
+
+int lxm_run_noalloc(const lxm_params* p_host, int n_blocks, int lds_bytes, void* stream) {
+  if (!p_host || !p_host->err || p_host->n_layers < 1 || p_host->n_layers > LXM_SCRATCH_MAXL ||
+      p_host->nv < 1 || p_host->nv > LXM_SCRATCH_MAXNV || p_host->hidden > MAXH)
+    return (int)hipErrorInvalidValue;
+  uint8_t* sc = nullptr;
+  hipError_t e = scratch_ptr(&sc);
   if (e != hipSuccess) return (int)e;
-  e = hipLaunchCooperativeKernel(fn, dim3(n_blocks), dim3(NT), args, (unsigned)lds_bytes,
-                                 (hipStream_t)stream);
-  return (int)e;
+  lxm_params p = *p_host;
+  p.ring = reinterpret_cast<float*>(sc + SC_RING);
+  p.rring = reinterpret_cast<float*>(sc + SC_RRING);
+  p.hn = reinterpret_cast<float*>(sc + SC_HN);
+  p.sync = reinterpret_cast<uint32_t*>(sc + SC_SYNC);
+  p.keys = reinterpret_cast<unsigned long long*>(sc + SC_KEYS);
+  p.mb_task = reinterpret_cast<uint32_t*>(sc + SC_MBTASK);
+  p.mb_e = reinterpret_cast<float*>(sc + SC_MBE);
+  p.mb_qk = reinterpret_cast<float*>(sc + SC_MBQK);
+  p.ybuf = reinterpret_cast<float*>(sc + SC_YBUF);
+  p.xo = reinterpret_cast<float*>(sc + SC_XO);
+  hipLaunchKernelGGL(k_noalloc_prep, dim3(1), dim3(256), 0, (hipStream_t)stream, p, sc);
+  e = hipGetLastError();
+  if (e != hipSuccess) return (int)e;
+  return (int)launch_decode(decode_fn(&p), reinterpret_cast<const lxm_params*>(sc + SC_PARAMS),
+                            n_blocks, lds_bytes, (hipStream_t)stream);
 }
 
 int lxm_max_blocks(int lds_bytes) {

@@ -493,6 +493,24 @@ class Mega:
     def sync_bitmaps(self) -> None:
         """lx.mega's nonzero-row bitmaps are not used: decays scale the whole state tile."""
 
+    def _params(self, rs, cs, ft, n_forced: int, n: int, preds, inputs=None, trace=None,
+                prof=None, bufs: dict | None = None) -> Params:
+        d = self.dims
+        return Params(hidden=d.hidden, n_layers=d.n_layers, nk=d.nk, kd=KD, nv=d.nv, vd=VD,
+                      n_conv=d.n_conv, vocab=self.vocab, bf16=int(self.bf), n_blocks=self.ncta,
+                      rms_eps=d.rms_eps, head_lds=self.head_lds, e4=int(self.e4),
+                      gate_bytes=self.gate_bytes, layers=self.layers_d.data_ptr(),
+                      blob=self.blob.data_ptr(), gates=self.blob.data_ptr() + self.gate_sec,
+                      rec=rs.data_ptr(), conv=cs.data_ptr(), emb_ptr=self.emb_ptr.data_ptr(),
+                      emb_ent=self.emb_ent.data_ptr(), w1_final=self.w1_final.data_ptr(),
+                      head_rows=self.head_rows.data_ptr(), head_ptr=self.head_ptr.data_ptr(),
+                      head_ent=self.head_ent.data_ptr(), forced=ft.data_ptr(), n_forced=n_forced,
+                      n_tokens=n, preds=preds.data_ptr(),
+                      inputs=inputs.data_ptr() if inputs is not None else None,
+                      trace=trace.data_ptr() if trace is not None else None,
+                      prof=prof.data_ptr() if prof is not None else None,
+                      n_qk_total=self.n_qk_total, **(bufs or {}))
+
     @torch.no_grad()
     def run(self, forced, n: int, dbg=None, dbg_tok: int = 0, dbg_items=None, prof=None,
             inputs: torch.Tensor | None = None, trace: torch.Tensor | None = None) -> list:
@@ -520,20 +538,7 @@ class Mega:
         self.sync.zero_()
         self.keys.zero_()
         self.err.zero_()
-        p = Params(hidden=d.hidden, n_layers=d.n_layers, nk=d.nk, kd=KD, nv=d.nv, vd=VD,
-                   n_conv=d.n_conv, vocab=self.vocab, bf16=int(self.bf), n_blocks=self.ncta,
-                   rms_eps=d.rms_eps, head_lds=self.head_lds, e4=int(self.e4),
-                   gate_bytes=self.gate_bytes, layers=self.layers_d.data_ptr(),
-                   blob=self.blob.data_ptr(), gates=self.blob.data_ptr() + self.gate_sec,
-                   rec=rs.data_ptr(), conv=cs.data_ptr(), emb_ptr=self.emb_ptr.data_ptr(),
-                   emb_ent=self.emb_ent.data_ptr(), w1_final=self.w1_final.data_ptr(),
-                   head_rows=self.head_rows.data_ptr(), head_ptr=self.head_ptr.data_ptr(),
-                   head_ent=self.head_ent.data_ptr(), forced=ft.data_ptr(), n_forced=len(f),
-                   n_tokens=n, preds=preds.data_ptr(),
-                   inputs=inputs.data_ptr() if inputs is not None else None,
-                   trace=trace.data_ptr() if trace is not None else None,
-                   prof=prof.data_ptr() if prof is not None else None,
-                   n_qk_total=self.n_qk_total, **self._bufs())
+        p = self._params(rs, cs, ft, len(f), n, preds, inputs, trace, prof, self._bufs())
         pd = torch.frombuffer(bytearray(bytes(p)), dtype=torch.uint8).to(self.dev)
         self._keep = (rs, cs, ft, pd)
         st = ctypes.c_void_p(torch.cuda.current_stream(self.dev).cuda_stream)
@@ -549,3 +554,31 @@ class Mega:
         if err:
             raise RuntimeError(f"mega failed: a grid wait timed out (code {err})")
         return out
+
+    def run_noalloc(self, forced: torch.Tensor, n: int, preds: torch.Tensor, err: torch.Tensor,
+                    inputs: torch.Tensor | None = None) -> None:
+        """``run`` through lxm_run_noalloc, for callers that cannot allocate device memory: the
+        forced tokens (int32, device), the predictions (int32, device, >= n) and the error word
+        (int32, device, 1; nonzero after the run when a wait timed out) are the caller's; the
+        run buffers are the library's static per-device scratch. Asynchronous on the current
+        stream (nothing here allocates or synchronizes); calls that overlap on one GPU race."""
+        for t in (forced, preds, err):
+            assert t.dtype == torch.int32 and t.device == self.dev and t.is_contiguous()
+        assert forced.numel() >= 1 and n >= 1 and preds.numel() >= n and err.numel() >= 1
+        if inputs is not None:
+            assert inputs.dtype == torch.int32 and inputs.numel() >= n and inputs.device == self.dev
+        rs, cs = self._state_ptrs_cached()
+        p = self._params(rs, cs, forced, forced.numel(), n, preds, inputs)
+        p.err = err.data_ptr()
+        st = ctypes.c_void_p(torch.cuda.current_stream(self.dev).cuda_stream)
+        e = self.lib.lxm_run_noalloc(ctypes.byref(p), self.ncta, self.lds, st)
+        if e:
+            raise RuntimeError(f"mega launch failed: hipError {e}")
+
+    def _state_ptrs_cached(self):
+        """The state pointer arrays, built once (the cache's tensors stay where they are)."""
+        key = tuple(self.cache.layers[L].recurrent_states[0].data_ptr() for L in range(self.dims.n_layers))
+        if getattr(self, "_ptrs_key", None) != key:
+            self._ptrs = self._state_ptrs()
+            self._ptrs_key = key
+        return self._ptrs

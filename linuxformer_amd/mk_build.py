@@ -76,6 +76,8 @@ def load(subprof: bool = False) -> ctypes.CDLL:
         P, I = ctypes.c_void_p, ctypes.c_int
         lib.lxm_run.argtypes = [P, P, I, I, P]
         lib.lxm_run.restype = I
+        lib.lxm_run_noalloc.argtypes = [P, I, I, P]
+        lib.lxm_run_noalloc.restype = I
         for n in ("lxm_lds_base", "lxm_max_lds", "lxm_last_error", "lxm_device_cus"):
             getattr(lib, n).restype = I
             getattr(lib, n).argtypes = []
@@ -111,4 +113,4 @@ def load(subprof: bool = False) -> ctypes.CDLL:
 EXPORTS = ("lxm_run", "lxm_lds_base", "lxm_helper_lds", "lxm_max_blocks", "lxm_max_lds",
            "lxm_last_error", "lxm_device_cus", "lxm_t_elem", "lxm_t_sum", "lxm_pf_layers",
            "lxm_pf_head", "lxm_pf_embed", "lxm_pf_tiles", "lxm_pf_lds", "lxm_dn_step", "lxm_dn_run",
-           "lxm_dn_prefill", "lxm_t_sync")
+           "lxm_dn_prefill", "lxm_t_sync", "lxm_run_noalloc")
