@@ -518,7 +518,12 @@ class Mega:
         Returns the n predictions (chip token ids). inputs (n,) int32: each step's input as the
         kernel embedded it. trace (n, n_layers, hidden) float32: the residual after each
         layer of each step. prof (``prof_size``) int64: phase cycle counters (see
-        ``phase_report``)."""
+        ``phase_report``). lx.mega's item dumps (dbg, dbg_items: its per-item shared-memory
+        layout) have no counterpart in this kernel and raise; ``trace`` records every layer's
+        residual instead."""
+        if dbg is not None or dbg_items is not None:
+            raise NotImplementedError("Mega.run: dbg/dbg_items dump lx.mega's per-item shared "
+                                      "memory, which this kernel does not have; use trace=")
         assert len(forced) >= 1 and n >= 1
         f = np.asarray(forced, np.int64)
         if f.min() < 0 or f.max() >= self.vocab:

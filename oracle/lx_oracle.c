@@ -65,6 +65,14 @@ static inline float bf16r(float x) {
 static int g_bf16 = 1; /* model dtype of the current call */
 static inline float D(float x) { return g_bf16 ? bf16r(x) : x; }
 
+/* The flush mode (off by default; never the contract the kernels follow): bf16 matrix products
+   treat denormal inputs as zero and flush denormal sums to zero, as oneDNN's bf16 GEMM does on
+   CPUs with AMX / AVX512-BF16 (the stock forward's F.linear on such hosts). It lets the tests
+   show that this flushing is the only difference between the contract and the stock forward. */
+static int g_flush = 0;
+void ox_set_flush(int on) { g_flush = on; }
+static inline int tiny(float x) { return x != 0.0f && fabsf(x) < 0x1p-126f; }
+
 static inline double pow2i(int k) { /* 2^k, -1022 <= k <= 1023 */
   uint64_t u = (uint64_t)(k + 1023) << 52;
   double d; memcpy(&d, &u, 8); return d;
@@ -276,6 +284,15 @@ static void ws_free(ox_ws* w) {
 static float row_dot(const ox_csr* m, int r, const float* x) {
   if (!m->blocks) {
     float s = 0.0f;
+    if (g_flush && g_bf16) {
+      for (int64_t e = m->ptr[r]; e < m->ptr[r + 1]; e++) {
+        float xv = x[m->col[e]];
+        if (xv == 0.0f || tiny(xv)) continue;
+        s = s + xv * m->val[e];
+        if (tiny(s)) s = copysignf(0.0f, s);
+      }
+      return s;
+    }
     for (int64_t e = m->ptr[r]; e < m->ptr[r + 1]; e++) {
       float xv = x[m->col[e]];
       if (xv == 0.0f) continue;
@@ -407,6 +424,31 @@ static int rec_heads(const ox_dims* d, const float* qall, const float* kall, con
   return any;
 }
 
+/* channels c0 .. c1 - 1 of causal_conv1d_update: each window shifts in P[c]; y[c] is formed
+   unless live (non-null) marks the channel's key head idle (channels (c - c0) / per of a key
+   head) */
+static void conv_channels(const ox_layer* ly, float* cs, ox_ws* w, int c0, int c1,
+                          const int* live, int K, int per) {
+#pragma omp parallel for schedule(static) if (c1 - c0 >= 2048)
+  for (int c = c0; c < c1; c++) {
+    float* win = cs + (size_t)c * K;
+    if (fbits(w->P[c]) == 0u) { /* a window of +0s stays so and gives +0 (a sum of zeros from
+                                   +0); a -0 (a tiny negative rounded) must still shift */
+      uint32_t any = 0u;
+      for (int i = 0; i < K; i++) any |= fbits(win[i]);
+      if (!any) { w->y[c] = 0.0f; continue; }
+    }
+    for (int i = 0; i + 1 < K; i++) win[i] = win[i + 1];
+    win[K - 1] = w->P[c];
+    if (live && !live[(c - c0) / per]) { w->y[c] = 0.0f; continue; }
+    const float* tw = ly->conv_w + (size_t)c * K;
+    float s = 0.0f;
+    for (int i = 0; i < K; i++) s = s + tw[i] * win[i];
+    const float ds = D(s);
+    w->y[c] = D(ds == 0.0f ? ds : ox_silu(ds)); /* silu(+-0) = +-0: skips the exp */
+  }
+}
+
 /* one chip layer's decode step on the residual h (TF:753-793), updating its conv window cs
    (n_conv, conv) and recurrent state S (nv, kd, vd) in place */
 static void layer_step(const ox_model* m, int L, float* h, float* cs, float* S, ox_ws* w,
@@ -421,23 +463,19 @@ static void layer_step(const ox_model* m, int L, float* h, float* cs, float* S, 
   csr_mv(&ly->qkv, w->xn, w->P);
   csr_mv(&ly->b, w->xn, w->b);
   csr_mv(&ly->a, w->xn, w->a);
-  /* causal_conv1d_update (TF:199-216): window <- [window[1:], P]; y = silu(D(sum w_i x_i)) */
-#pragma omp parallel for schedule(static) if (C >= 2048)
-  for (int c = 0; c < C; c++) {
-    float* win = cs + (size_t)c * K;
-    if (w->P[c] == 0.0f) { /* a zero window stays zero and gives +0 (a sum from +0 of zeros) */
-      int zero = 1;
-      for (int i = 0; i < K; i++) zero &= win[i] == 0.0f;
-      if (zero) { w->y[c] = 0.0f; continue; }
-    }
-    for (int i = 0; i + 1 < K; i++) win[i] = win[i + 1];
-    win[K - 1] = w->P[c];
-    const float* tw = ly->conv_w + (size_t)c * K;
-    float s = 0.0f;
-    for (int i = 0; i < K; i++) s = s + tw[i] * win[i];
-    const float ds = D(s);
-    w->y[c] = D(ds == 0.0f ? ds : ox_silu(ds)); /* silu(+-0) = +-0: skips the exp */
+  /* causal_conv1d_update (TF:199-216): window <- [window[1:], P]; y = silu(D(sum w_i x_i)).
+     Every window shifts; a value channel's output is formed only under a key head whose query
+     or key is nonzero (the delta rule reads no other head's values) */
+  const int QK = 2 * nk * kd;
+  conv_channels(ly, cs, w, 0, QK, NULL, K, kd * (nv / nk));
+  int vlive[64];
+  for (int kh = 0; kh < nk; kh++) {
+    int live = 0;
+    for (int i = 0; i < kd; i++)
+      live |= (w->y[(size_t)kh * kd + i] != 0.0f) | (w->y[(size_t)(nk + kh) * kd + i] != 0.0f);
+    vlive[kh] = live;
   }
+  conv_channels(ly, cs, w, QK, C, vlive, K, vd * (nv / nk));
   for (int v = 0; v < nv; v++) {
     w->beta[v] = D(ox_sigmoid(w->b[v]));
     float sp = ox_softplus(w->a[v] + ly->dt_bias[v]);

@@ -71,9 +71,17 @@ def lib():
         _lib.ox_layer_step.argtypes = [PTR, I32, PTR, PTR, PTR]
         _lib.ox_head.argtypes = [PTR, PTR, I32, PTR, PTR]
         _lib.ox_rec_step.argtypes = [I32, I32, I32] + [PTR] * 7
+        _lib.ox_set_flush.argtypes = [I32]
         _lib.ox_row_dot.restype = F32
         _lib.ox_row_dot.argtypes = [I32, I32, PTR, PTR]
     return _lib
+
+
+def set_flush(on: bool) -> None:
+    """Model oneDNN's bf16 GEMM on AMX hosts (denormal inputs and sums flushed to zero) in the
+    bf16 matrix products: only for showing that this is all that separates the contract from the
+    stock forward on such a host. Off by default."""
+    lib().ox_set_flush(int(bool(on)))
 
 
 def _p(a: np.ndarray):

@@ -5,7 +5,7 @@ fla nor the hub kernels are installed) in lx/lx/hf.py's chip view, run token by 
 by oracle/stock.py; the reference pins 5.19.0 (requirements.txt:4), whose qwen3_5 code path for
 these ops is the same. Nothing of the reference repository is imported.
 
-    python tests/golden/make_golden.py      # rewrites tests/golden/*.npz
+    python tests/golden/make_golden.py [names]     # rewrites tests/golden/<name>.npz
 
 Each fixture holds the inputs' seeds and shapes (rebuilt by linuxformer_amd.synth), the greedy
 stream, every step's per-layer residual (float32) or a hash of it, and the final states' hashes
@@ -17,6 +17,7 @@ from __future__ import annotations
 import hashlib
 import os
 import sys
+from dataclasses import replace
 
 import numpy as np
 import torch
@@ -26,11 +27,20 @@ sys.path.insert(0, os.path.dirname(os.path.dirname(HERE)))
 sys.path.insert(0, os.path.dirname(HERE))
 
 from linuxformer_amd import synth  # noqa: E402
+from oracle import oracle as ox  # noqa: E402
 from oracle import stock  # noqa: E402
+
+def c2_cut():
+    """Config 2's layer shape (hidden 3572, 16 key x 128 value heads, SwiGLU 1024, bf16, N(0,1)
+    state) cut to 3 layers and a 4,096-token vocabulary; every token gates one of the 3 layers."""
+    s = synth.config2()
+    return replace(s, name="c2s", dims=replace(s.dims, n_layers=3, vocab=4096), p_gate=1.0 / 3)
+
 
 CASES = {
     # name: (spec builder, steps, keep full traces)
-    "c1_64": (lambda: synth.config1(), 64, False),
+    "c1_256": (lambda: synth.config1(), 256, False),
+    "c2s_bf16_64": (c2_cut, 64, False),
     "small_bf16_32": (lambda: synth.small(), 32, True),
     "small_fp32_32": (lambda: synth.small(dtype="fp32", seed=3), 32, True),
     "tiny_fp32_8": (lambda: "tiny_fp32", 8, True),
@@ -40,6 +50,15 @@ CASES = {
 
 def sha(a: np.ndarray) -> str:
     return hashlib.sha256(np.ascontiguousarray(a, np.float32).tobytes()).hexdigest()
+
+
+def sha_state(a: np.ndarray) -> str:
+    """sha256 of recurrent-state values with the sign of zero made +0 (x + 0): states are equal
+    when every element compares equal, as the reference compares them (x.ne(y),
+    lx/tests/check_mega.py:34-36). The stock update S + k (x) delta on every head turns some -0
+    entries of a fully decayed head into +0 on later steps, which skipping idle heads (the
+    reference's own design, lx/lx/fast.py:8-19) does not."""
+    return sha(np.ascontiguousarray(a, np.float32) + np.float32(0.0))
 
 
 def model_of(name):
@@ -58,20 +77,35 @@ def model_of(name):
 
 def main():
     torch.set_grad_enabled(False)
-    for name, (_, n, full) in CASES.items():
+    names = sys.argv[1:] or list(CASES)
+    for name in names:
+        _, n, full = CASES[name]
         m, conv0, rec0, start = model_of(name)
         hf = synth.to_hf(m)
         preds, trace, conv, rec = stock.decode(hf, conv0, rec0, [start], n)
         rng = np.random.default_rng(0)
         ridx = rng.integers(0, rec.size, 4096)
         out = {"preds": preds, "start": np.int64(start), "n": np.int64(n),
-               "conv_sha": sha(conv), "rec_sha": sha(rec), "rec_idx": ridx,
+               "conv_sha": sha(conv), "rec_sha": sha_state(rec), "rec_idx": ridx,
                "rec_sample": rec.reshape(-1)[ridx], "trace_sha": sha(trace),
                "conv_sample": conv.reshape(-1)[rng.integers(0, conv.size, 4096)],
                "conv_idx": rng.integers(0, conv.size, 4096)}
         out["conv_sample"] = conv.reshape(-1)[out["conv_idx"]]
         if full:
             out["trace"] = trace
+        if m.dims.dtype == "bf16" and not full:
+            # the contract (IEEE, no flushing) against the stock trace: the elements that differ
+            # (oneDNN's bf16 GEMM flushes denormals on this host; the oracle's flush mode models it)
+            ox.build()
+            om = ox.OracleModel(m)
+            ox.set_flush(False)
+            c, r = conv0.copy(), rec0.copy()
+            _, _, tr = om.decode(c, r, [start], n, trace=True)
+            diff = tr.view(np.uint32) != np.ascontiguousarray(trace, np.float32).view(np.uint32)
+            out["contract_diff"] = np.int64(diff.sum())
+            out["contract_diff_max_abs"] = np.float32(
+                max(np.abs(tr[diff]).max(initial=0), np.abs(trace[diff]).max(initial=0)))
+            out["host_cpu_capability"] = torch.backends.cpu.get_cpu_capability()
         path = os.path.join(HERE, name + ".npz")
         np.savez_compressed(path, **out)
         print(name, os.path.getsize(path), "bytes", preds.tolist()[:8])
