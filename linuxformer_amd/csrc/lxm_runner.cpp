@@ -2,7 +2,7 @@
 // of liblxm.so, without Python: the binding a foreign host (C, Go via cgo, ...) would use, and the
 // process rocprofv3 profiles.
 //
-//   lxm_runner <dump dir> <launches> [tokens per launch]
+//   lxm_runner <dump dir> <launches> [tokens per launch, at most the dumped count]
 //   lxm_runner --copy <MiB>     (one plain device copy kernel of that size: the calibration run
 //                                for the HBM byte counters FETCH_SIZE and WRITE_SIZE)
 //
@@ -43,10 +43,18 @@ static std::vector<char> slurp(const std::string& path) {
   return std::vector<char>((std::istreambuf_iterator<char>(f)), std::istreambuf_iterator<char>());
 }
 
+static std::vector<void*> g_allocs;  // every device buffer the runner made, freed at the end
+
+static void* dev_alloc(size_t n) {
+  void* d = nullptr;
+  CK(hipMalloc(&d, n));
+  g_allocs.push_back(d);
+  return d;
+}
+
 static void* upload(const std::string& path, size_t* n = nullptr) {
   std::vector<char> b = slurp(path);
-  void* d = nullptr;
-  CK(hipMalloc(&d, b.size() + 256));
+  void* d = dev_alloc(b.size() + 256);
   CK(hipMemcpy(d, b.data(), b.size(), hipMemcpyHostToDevice));
   if (n) *n = b.size();
   return d;
@@ -122,10 +130,37 @@ int main(int argc, char** argv) {
       {"xo", (void**)&p.xo}};
   for (auto& kv : field) *kv.second = nullptr;
   int n_blocks = 0, lds = 0;
-  std::ifstream mf(dir + "/manifest.txt");
-  std::string line;
-  std::vector<std::pair<void*, size_t>> zeroed;
-  while (std::getline(mf, line)) {
+  std::vector<std::string> manifest;
+  {
+    std::ifstream mf(dir + "/manifest.txt");
+    for (std::string l; std::getline(mf, l);) manifest.push_back(l);
+  }
+  std::map<std::string, size_t> zero_bytes;  // the size of each zeroed buffer, by field
+  for (const std::string& line : manifest) {
+    std::istringstream ss(line);
+    std::string kind, name;
+    size_t n = 0;
+    if ((ss >> kind >> name) && kind == "zero" && (ss >> n)) zero_bytes[name] = n;
+  }
+  {
+    // the launch writes n_tokens predictions (and inputs / a trace when the dump has them):
+    // refuse a count its buffers cannot hold, before anything touches the GPU
+    const long n = argc > 3 ? atol(argv[3]) : (long)p.n_tokens;
+    const size_t per_trace = (size_t)p.n_layers * p.hidden * 4;
+    auto holds = [&](const char* f, size_t need) {
+      return zero_bytes.count(f) && need <= zero_bytes.at(f);
+    };
+    const bool fits = n >= 1 && holds("preds", (size_t)n * 4) &&
+                      (!zero_bytes.count("inputs") || holds("inputs", (size_t)n * 4)) &&
+                      (!zero_bytes.count("trace") || holds("trace", (size_t)n * per_trace));
+    if (!fits) {
+      fprintf(stderr, "tokens %ld: the dump's buffers hold %zu predictions (dump again with more)\n",
+              n, zero_bytes.count("preds") ? zero_bytes.at("preds") / 4 : (size_t)0);
+      return 2;
+    }
+    p.n_tokens = (int)n;
+  }
+  for (const std::string& line : manifest) {
     std::istringstream ss(line);
     std::string kind, name;
     ss >> kind >> name;
@@ -138,10 +173,8 @@ int main(int argc, char** argv) {
     } else if (kind == "zero") {
       size_t n;
       ss >> n;
-      void* d;
-      CK(hipMalloc(&d, n));
+      void* d = dev_alloc(n);
       CK(hipMemset(d, 0, n));
-      zeroed.push_back({d, n});
       *field.at(name) = d;
     } else if (kind == "sub") {  // a pointer into another buffer: sub <field> <base field> <offset>
       std::string base;
@@ -157,17 +190,14 @@ int main(int argc, char** argv) {
         ss >> file;
         ptrs[i] = upload(dir + "/" + file);
       }
-      void* d;
-      CK(hipMalloc(&d, sizeof(void*) * n));
+      void* d = dev_alloc(sizeof(void*) * n);
       CK(hipMemcpy(d, ptrs.data(), sizeof(void*) * n, hipMemcpyHostToDevice));
       *field.at(name) = d;
     }
   }
-  if (argc > 3) p.n_tokens = atoi(argv[3]);
   int* forced_d = (int*)p.forced;
   int* preds_d = p.preds;
-  lxm_params* pd;
-  CK(hipMalloc(&pd, sizeof p));
+  lxm_params* pd = (lxm_params*)dev_alloc(sizeof p);
   hipStream_t st;
   CK(hipStreamCreate(&st));
   hipEvent_t e0, e1;
@@ -211,5 +241,15 @@ int main(int argc, char** argv) {
   for (size_t i = 0; i < ms.size(); i++) printf("%s%.3f", i ? ", " : "", ms[i]);
   printf("], \"tok_per_s\": %.1f, \"last_pred\": %d}\n", p.n_tokens * launches / (tot * 1e-3), tok);
   fflush(stdout);
+  // teardown in dependency order, while the runtime is up: the stream's work, the events and the
+  // stream, every device buffer, then the library (its code object unregisters before exit)
+  CK(hipStreamSynchronize(st));
+  CK(hipEventDestroy(e0));
+  CK(hipEventDestroy(e1));
+  CK(hipStreamDestroy(st));
+  for (void* d : g_allocs) CK(hipFree(d));
+  g_allocs.clear();
+  CK(hipDeviceSynchronize());
+  dlclose(h);
   return 0;
 }

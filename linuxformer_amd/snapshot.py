@@ -10,11 +10,17 @@ scalars and the proposer's fields, in the reference's formats (lx/lx/session.py:
 are tensors (this package's ``fast.StateCache``, transformers' cache): conv (1, C, 4) in the
 model dtype, recurrent (1, nv, 256, 128) float32, stored as they are.
 
-.safetensors, the pickle-free form (session.py:258-292): tensors ``conv.{L}`` and
-``recurrent.{L}``, each byte field of the proposer as a uint8 tensor ``ref.{field}``, and every
-other field as JSON under the metadata key ``"lx.session"``: ``{"next", "last", "n", "waiting",
-"ref": {the proposer's other fields}, "bytes": {field: "bytes" | "bytearray"}}``. A file the
-reference wrote loads here, and one written here loads in the reference's ``load_safe``.
+.safetensors, the pickle-free form (the reference's save_safe / load_safe, session.py:258-292):
+
+    tensor ``conv.{L}``           conv window of layer L, (1, C, 4), the model dtype
+    tensor ``recurrent.{L}``      recurrent state of layer L, (1, nv, 256, 128), float32
+    tensor ``ref.{name}``         a bytes / bytearray field of the proposer, uint8 (1-D)
+    metadata ``"lx.session"``     JSON: {"next", "last", "n", "waiting": the session's scalars,
+                                  "ref": the proposer's other fields, "bytes": {name: "bytes" |
+                                  "bytearray"} for the ref.{name} tensors}
+
+for L = 0 .. n-1. A file the reference wrote loads here, and one written here loads in the
+reference's load_safe.
 
 .pt: the same dict through ``torch.save``, the proposer as a plain dict of its fields (this
 package has no ``lx.ref.Machine``), loaded with ``weights_only=True`` (bytes and bytearray
@@ -26,9 +32,11 @@ pickles a ``Machine`` object; loading it would run code from the file, so it is 
 from __future__ import annotations
 
 import json
+import re
 from pathlib import Path
 from types import SimpleNamespace
 
+import numpy as np
 import torch
 
 KEY = "lx.session"
@@ -106,27 +114,36 @@ def load(path) -> dict:
     return d
 
 
+_LAYER_KEY = re.compile(r"^(conv|recurrent)\.(\d+)$")
+
+
+def _byte_tensor(v) -> torch.Tensor:
+    """A bytes-like value as a 1-D uint8 tensor (owning its memory; empty for b"")."""
+    return torch.from_numpy(np.frombuffer(bytes(v), dtype=np.uint8).copy())
+
+
 def _save_safe(d: dict, path: Path) -> None:
-    """session.py:258-275's layout."""
+    """The .safetensors layout (the module docstring's table): states as conv.L / recurrent.L,
+    byte-valued proposer fields as ref.NAME uint8 tensors, the rest as JSON metadata."""
     from safetensors.torch import save_file
 
-    t, ref, kinds = {}, {}, {}
+    tensors = {}
     for L, (cs, rs) in enumerate(d["state"]):
-        t[f"conv.{L}"], t[f"recurrent.{L}"] = cs.contiguous(), rs.contiguous()
-    for k, v in d["ref"].items():
-        if isinstance(v, (bytes, bytearray)):
-            t[f"ref.{k}"] = torch.frombuffer(bytearray(v), dtype=torch.uint8).clone() if v \
-                else torch.zeros(0, dtype=torch.uint8)
-            kinds[k] = type(v).__name__
-        else:
-            ref[k] = v
-    meta = {k: d[k] for k in SCALARS}
-    meta.update(ref=ref, bytes=kinds)
-    save_file(t, str(path), metadata={KEY: json.dumps(meta)})
+        tensors[f"conv.{L}"] = cs.contiguous()
+        tensors[f"recurrent.{L}"] = rs.contiguous()
+    fields = d["ref"]
+    byte_kind = {k: type(v).__name__ for k, v in fields.items()
+                 if isinstance(v, (bytes, bytearray))}
+    tensors.update({f"ref.{k}": _byte_tensor(fields[k]) for k in byte_kind})
+    meta = {"next": d["next"], "last": d["last"], "n": d["n"], "waiting": d["waiting"],
+            "ref": {k: v for k, v in fields.items() if k not in byte_kind},
+            "bytes": byte_kind}
+    save_file(tensors, str(path), metadata={KEY: json.dumps(meta)})
 
 
 def _load_safe(path: Path) -> dict:
-    """session.py:278-292's reading."""
+    """Read the .safetensors layout back; the layers are the conv.L / recurrent.L pairs, which
+    must number 0 .. n-1 with both halves present."""
     from safetensors import safe_open
 
     with safe_open(str(path), "pt") as f:
@@ -134,11 +151,21 @@ def _load_safe(path: Path) -> dict:
         if KEY not in md:
             raise ValueError(f"{path}: no {KEY!r} metadata: not a session snapshot")
         meta = json.loads(md[KEY])
-        t = {k: f.get_tensor(k) for k in f.keys()}
-    ref = dict(meta.pop("ref", {}))
-    for k, kind in meta.pop("bytes", {}).items():
-        b = t[f"ref.{k}"].numpy().tobytes()
-        ref[k] = bytearray(b) if kind == "bytearray" else b
-    n = sum(k.startswith("conv.") for k in t)
-    state = [(t[f"conv.{L}"], t[f"recurrent.{L}"]) for L in range(n)]
-    return dict(meta, ref=SimpleNamespace(**ref), state=state)
+        keys = list(f.keys())
+        layers: dict = {}
+        for k in keys:
+            hit = _LAYER_KEY.match(k)
+            if hit:
+                layers.setdefault(int(hit.group(2)), {})[hit.group(1)] = f.get_tensor(k)
+        kinds = meta.get("bytes", {})
+        fields = dict(meta.get("ref", {}))
+        for name, kind in kinds.items():
+            raw = f.get_tensor(f"ref.{name}").numpy().tobytes()
+            fields[name] = bytearray(raw) if kind == "bytearray" else raw
+    if sorted(layers) != list(range(len(layers))) or \
+            any(set(v) != {"conv", "recurrent"} for v in layers.values()):
+        raise ValueError(f"{path}: the conv.L / recurrent.L tensors do not form layers 0..n-1")
+    out = {k: meta.get(k) for k in SCALARS}
+    out["state"] = [(layers[L]["conv"], layers[L]["recurrent"]) for L in range(len(layers))]
+    out["ref"] = SimpleNamespace(**fields)
+    return out

@@ -325,3 +325,24 @@ def test_alone_rejects_bad_launch_sizes():
     with pytest.raises(ValueError):
         alone.run_alone(None, [[1]], final=lambda t: True, done=lambda s, b: True,
                         first_launch=64, max_launch=32)
+
+
+def test_runner_refuses_more_tokens_than_the_dump_holds(tmp_path, native_lib):
+    """lxm_runner checks the token count against the dumped prediction buffer (and inputs and
+    trace) before it touches the GPU: a launch of more tokens would write past them."""
+    from linuxformer_amd import mega
+
+    if not os.path.exists(mk_build.RUNNER):
+        mk_build.build()
+    p = mega.Params(hidden=64, n_layers=2, n_tokens=10)
+    (tmp_path / "params.bin").write_bytes(bytes(p))
+    (tmp_path / "lib.txt").write_text(mk_build.LIB + "\n")
+    (tmp_path / "manifest.txt").write_text("launch x 256 1024\nzero preds 40\nzero inputs 40\n")
+    for n, ok in (("11", False), ("0", False)):
+        r = subprocess.run([mk_build.RUNNER, str(tmp_path), "1", n], capture_output=True,
+                           text=True, timeout=60)
+        assert r.returncode == 2 and "hold 10 predictions" in r.stderr, (n, r.stderr)
+    (tmp_path / "manifest.txt").write_text("launch x 256 1024\nzero preds 8\n")
+    r = subprocess.run([mk_build.RUNNER, str(tmp_path), "1"], capture_output=True, text=True,
+                       timeout=60)  # the dumped count itself (10) exceeds a 2-token buffer
+    assert r.returncode == 2 and "hold 2 predictions" in r.stderr, r.stderr
