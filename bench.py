@@ -586,7 +586,7 @@ def dense_leg(args, dev) -> dict:
     return out
 
 
-def main() -> int:
+def make_parser() -> argparse.ArgumentParser:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20, help="launches the chunk is split over")
@@ -613,7 +613,11 @@ def main() -> int:
                     help="config 4's prompt through lxm_dn_prefill (0: as forced steps)")
     ap.add_argument("--dn-persistent", type=int, default=1,
                     help="1: also time the persistent run (lxm_dn_run); 0: skip it")
-    args = ap.parse_args()
+    return ap
+
+
+def main() -> int:
+    args = make_parser().parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: the decode is one sequential chain per stream and this "
               f"build runs on a single MI355X (asked for --gpus {args.gpus}).", file=sys.stderr)
