@@ -276,6 +276,10 @@ def decode_leg(args, dev, hf_holder: dict) -> dict:
                               "continuing from the chunk's final state"}
         log(f"[bench] forced stream: {n_f} tokens at {forced_out['tok_s']} tok/s")
 
+    session_out = None
+    if args.session_tokens > 0:
+        session_out = session_leg(args, dev, f, model, conv0, rec0, start, stream_preds)
+
     sync = sync_costs(mg.ncta)
     log(f"[bench] sync costs: {sync}")
     us_tok = kern_ms * 1e3 / (chunk / len(sizes))
@@ -319,6 +323,7 @@ def decode_leg(args, dev, hf_holder: dict) -> dict:
                       gold["stream_sha256"] == stream_sha and gold["conv_sha256"] == conv_sha
                       and gold["rec_sha256"] == rec_sha)},
         "forced_input": forced_out,
+        "session_decode": session_out,
     }
     if args.oracle_tokens > 0:
         want = oracle_check(model, conv0, rec0, start, args.oracle_tokens)
@@ -345,6 +350,39 @@ def decode_leg(args, dev, hf_holder: dict) -> dict:
         out["check"]["stock_prefix_match"] = cp == stream_preds[:n]
         log(f"[bench] CPU stock decode: {tps:.3f} tok/s over {n} steps")
     return out
+
+
+def session_leg(args, dev, f, model, conv0, rec0, start: int, stream_preds) -> dict:
+    """The non-mega decode (linuxformer_amd.session.Session, lx/lx/session.py:148-225) on the same
+    stack from the same start and initial state: graph replays of run_k single-token steps of
+    the verified-mode kernels, each step's prediction fed back on the GPU; tok/s over
+    --session-tokens tokens after one warm-up replay, and whether its stream equals the
+    persistent kernel's (the reference's figures: 80.8 tok/s stock, 552.9 tok/s lx.fast with
+    idle-skip, lx/results/summary.md:80-82)."""
+    import torch
+
+    from linuxformer_amd import fast
+    from linuxformer_amd.session import Session
+
+    n = args.session_tokens
+    cache = fast.StateCache(conv0, rec0, model.dims.dtype, dev)
+    s = Session(f, cache)
+    p0 = s.step(start)
+    out = s.free(s.run_k)  # captures the run graph, and is its first replay
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    out += s.free(n)
+    torch.cuda.synchronize()
+    dt = time.perf_counter() - t0
+    got = [p0] + out[1:] + [s.next]
+    same = got[:len(stream_preds)] == stream_preds[:len(got)]
+    res = {"tokens": n, "tok_s": round(n / dt, 1), "run_k": s.run_k,
+           "matches_persistent_stream": bool(same),
+           "note": "Session.free: graphs of run_k single-token steps (lxm_pf_embed, lxm_pf_layers "
+                   "at T = 1, lxm_pf_head), predictions fed back on the GPU"}
+    log(f"[bench] session decode: {res['tok_s']} tok/s over {n} tokens; stream equal: {same}")
+    del s, cache
+    return res
 
 
 def _tf_version() -> str:
@@ -595,6 +633,8 @@ def make_parser() -> argparse.ArgumentParser:
     ap.add_argument("--config", default="c2", choices=["c1", "c2", "c5", "small"])
     ap.add_argument("--forced-tokens", type=int, default=16_384,
                     help="tokens of the forced-input launch (0: skip)")
+    ap.add_argument("--session-tokens", type=int, default=2048,
+                    help="tokens of the graph-replayed non-mega decode (0: skip)")
     ap.add_argument("--oracle-tokens", type=int, default=256,
                     help="chunk prefix checked against the C oracle (0: skip)")
     ap.add_argument("--cpu-seconds", type=float, default=15.0,

@@ -278,6 +278,30 @@ def pack_layer(sm, fast, L: int, blob: _Blob) -> PfLayer:
     return pl
 
 
+class PfBuffers:
+    """The run buffers of T positions (device, caller-owned; include/lxm_prefill.h)."""
+
+    NAMES = ("tokens", "h", "hn", "r1", "mask", "cand", "cmask", "count", "recs", "keys",
+             "preds", "err")
+
+    def __init__(self, dims, max_rec: int, T: int, dev):
+        nt = (T + TT - 1) // TT
+        dt = torch.bfloat16 if dims.dtype == "bf16" else torch.float32
+        self.T = T
+        self.h = torch.zeros(nt * dims.hidden * TT, dtype=dt, device=dev)
+        self.hn = torch.zeros_like(self.h)
+        self.r1 = torch.zeros(T, dtype=torch.float32, device=dev)
+        self.mask = torch.zeros(T, dtype=torch.int32, device=dev)
+        self.cand = torch.zeros(T, dtype=torch.int32, device=dev)
+        self.cmask = torch.zeros(T, dtype=torch.int32, device=dev)
+        self.count = torch.zeros(dims.n_layers + 1, dtype=torch.int32, device=dev)
+        self.recs = torch.zeros(T * max_rec, dtype=torch.uint8, device=dev)
+        self.keys = torch.zeros(T, dtype=torch.int64, device=dev)
+        self.preds = torch.zeros(T, dtype=torch.int32, device=dev)
+        self.tokens = torch.zeros(T, dtype=torch.int32, device=dev)
+        self.err = torch.zeros(1, dtype=torch.int32, device=dev)
+
+
 class Prefill:
     """The packed tables of a Fast's layers and head on one device, and the drivers."""
 
@@ -333,24 +357,17 @@ class Prefill:
     def lds_ok(self) -> bool:
         return self.lib.lxm_pf_lds(int(self.bf), self.dims.hidden, self.umax) <= 160 * 1024
 
+    def buffers(self, T: int) -> "PfBuffers":
+        """A new set of run buffers for T positions (a caller that captures the launches in a
+        graph keeps its own set, which later calls of other sizes never reallocate)."""
+        return PfBuffers(self.dims, self.max_rec, T, self.dev)
+
     def _buffers(self, T: int) -> None:
         if self._T == T:
             return
-        d, dev = self.dims, self.dev
-        nt = (T + TT - 1) // TT
-        dt = torch.bfloat16 if self.bf else torch.float32
-        self.h = torch.zeros(nt * d.hidden * TT, dtype=dt, device=dev)
-        self.hn = torch.zeros_like(self.h)
-        self.r1 = torch.zeros(T, dtype=torch.float32, device=dev)
-        self.mask = torch.zeros(T, dtype=torch.int32, device=dev)
-        self.cand = torch.zeros(T, dtype=torch.int32, device=dev)
-        self.cmask = torch.zeros(T, dtype=torch.int32, device=dev)
-        self.count = torch.zeros(d.n_layers + 1, dtype=torch.int32, device=dev)
-        self.recs = torch.zeros(T * self.max_rec, dtype=torch.uint8, device=dev)
-        self.keys = torch.zeros(T, dtype=torch.int64, device=dev)
-        self.preds = torch.zeros(T, dtype=torch.int32, device=dev)
-        self.tokens = torch.zeros(T, dtype=torch.int32, device=dev)
-        self.err = torch.zeros(1, dtype=torch.int32, device=dev)
+        self.buf = self.buffers(T)
+        for name in PfBuffers.NAMES:
+            setattr(self, name, getattr(self.buf, name))
         self._T = T
 
     def _state_ptrs(self, cache):
@@ -368,9 +385,19 @@ class Prefill:
         return (torch.tensor(rs, dtype=torch.int64, device=self.dev),
                 torch.tensor(cs, dtype=torch.int64, device=self.dev))
 
-    def params(self, T: int, cache=None):
-        """The parameter block for T positions (host struct, device copy)."""
-        self._buffers(T)
+    def params(self, T: int, cache=None, buf: "PfBuffers | None" = None):
+        """The parameter block for T positions (host struct, device copy) over buf (default: the
+        Prefill's own buffers for T)."""
+        p, pd, keep = self.bind(T, cache, buf)
+        self._keep = keep
+        return p, pd
+
+    def bind(self, T: int, cache=None, buf: "PfBuffers | None" = None):
+        """(host block, device block, tensors the blocks point into that the caller keeps)."""
+        if buf is None:
+            self._buffers(T)
+            buf = self.buf
+        assert buf.T == T
         d = self.dims
         rs, cs = self._state_ptrs(cache) if cache is not None else (None, None)
         p = PfParams(hidden=d.hidden, n_layers=d.n_layers, nk=d.nk, nv=d.nv, n_conv=d.n_conv,
@@ -384,14 +411,9 @@ class Prefill:
                      w1_final=self.w1_final.data_ptr(), emb_ptr=self.emb_ptr.data_ptr(),
                      emb_ent=self.emb_ent.data_ptr(), head_slice=self.head_slice.data_ptr(),
                      head_ptr=self.head_ptr.data_ptr(), head_ent=self.head_ent.data_ptr(),
-                     tokens=self.tokens.data_ptr(), h=self.h.data_ptr(), hn=self.hn.data_ptr(),
-                     r1=self.r1.data_ptr(), mask=self.mask.data_ptr(), cand=self.cand.data_ptr(),
-                     cmask=self.cmask.data_ptr(), count=self.count.data_ptr(),
-                     recs=self.recs.data_ptr(), keys=self.keys.data_ptr(),
-                     preds=self.preds.data_ptr(), err=self.err.data_ptr())
+                     **{n: getattr(buf, n).data_ptr() for n in PfBuffers.NAMES})
         pd = torch.frombuffer(bytearray(bytes(p)), dtype=torch.uint8).to(self.dev)
-        self._keep = (rs, cs, pd)
-        return p, pd
+        return p, pd, (rs, cs, pd, buf)
 
     def _stream(self):
         return ctypes.c_void_p(torch.cuda.current_stream(self.dev).cuda_stream)

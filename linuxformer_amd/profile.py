@@ -1,0 +1,58 @@
+"""In-kernel cycle counters of the decode kernel (lx.mega's prof buffer and MK_SUBPROF build):
+
+    python -m linuxformer_amd.profile --config c2 --tokens 4096 [--subprof]
+
+Runs one launch of --tokens greedy steps from the config's start token and initial state with
+the phase counters on, and prints one JSON object: cycles per token of each chain phase
+(embedding, stage A, stage B, GDN events, stage C1, stage C2, final norm, head wait), the
+helpers' mean and max cycles per token in each of their parts, and with --subprof (the library
+built with -DLXM_SUBPROF) each chain wave's busy and waiting cycles per layer in each stage.
+The counters are the chain's own clock cycle counter; `clock_mhz` is the chain's cycles per token
+over the launch's wall time per token (the launch's set-up included)."""
+
+from __future__ import annotations
+
+import argparse
+import json
+import sys
+import time
+
+import torch
+
+from . import fast, mega, synth
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--config", default="c2", choices=["c1", "c2", "c5", "small"])
+    ap.add_argument("--tokens", type=int, default=4096)
+    ap.add_argument("--subprof", action="store_true")
+    a = ap.parse_args()
+    spec = {"c1": synth.config1(), "c2": synth.config2(), "c5": synth.config5(),
+            "small": synth.small()}[a.config]
+    m = synth.build(spec)
+    conv0, rec0 = synth.init_state(m)
+    dev = torch.device("cuda", 0)
+    cache = fast.StateCache(conv0, rec0, m.dims.dtype, dev)
+    mg = mega.Mega(fast.Fast(m), m, cache, 0, subprof=a.subprof)
+    start = synth.start_token(spec)
+    mg.run([start], 256)  # warm-up (first touch of the tables)
+    prof = torch.zeros(mg.prof_size, dtype=torch.int64, device=dev)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    mg.run([start], a.tokens, prof=prof)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    rep = mg.phase_report(prof)
+    chain = sum(v for k, v in rep.items() if k in mega.Mega.PHASES)
+    rep["chain cycles per token"] = round(chain, 1)
+    rep["us per token"] = round(wall * 1e6 / a.tokens, 2)
+    rep["clock_mhz"] = round(chain / (wall * 1e6 / a.tokens), 1)
+    rep["config"] = spec.name
+    rep["subprof"] = a.subprof
+    print(json.dumps(rep))
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())
