@@ -15,10 +15,11 @@ LIB = os.path.join(LIBDIR, "liblxm.so")
 # the same kernel with the per-wave sub-phase counters (-DLXM_SUBPROF; lx.mega's MK_SUBPROF build)
 LIB_SUBPROF = os.path.join(LIBDIR, "liblxm_subprof.so")
 RUNNER = os.path.join(LIBDIR, "lxm_runner")
-SOURCES = ["lxm_decode.hip", "lxm_prefill.hip", "lxm_dense.hip", "lxm_probe.hip"]
+SOURCES = ["lxm_decode.hip", "lxm_prefill.hip", "lxm_dense.hip", "lxm_chunk.hip", "lxm_probe.hip"]
 HEADERS = ["lxm_math.h", os.path.join("..", "..", "include", "lxm.h"),
            os.path.join("..", "..", "include", "lxm_prefill.h"),
-           os.path.join("..", "..", "include", "lxm_dense.h")]
+           os.path.join("..", "..", "include", "lxm_dense.h"),
+           os.path.join("..", "..", "include", "lxm_chunk.h")]
 # -ffp-contract=off: no a*b+c is fused (the rounding contract); packed fp32 ops disabled
 FLAGS = ["--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC", "-shared", "-ffp-contract=off",
          "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops"]
@@ -104,6 +105,8 @@ def load(subprof: bool = False) -> ctypes.CDLL:
         lib.lxm_dn_run.restype = I
         lib.lxm_dn_prefill.argtypes = [P, P, I, P, P]
         lib.lxm_dn_prefill.restype = I
+        lib.lxm_gdn_chunk.argtypes = [P, P]
+        lib.lxm_gdn_chunk.restype = I
         lib.lxm_t_sync.argtypes = [I, I, I, I, P, P, P, P]
         lib.lxm_t_sync.restype = I
         _libs[path] = lib
@@ -113,4 +116,4 @@ def load(subprof: bool = False) -> ctypes.CDLL:
 EXPORTS = ("lxm_run", "lxm_lds_base", "lxm_helper_lds", "lxm_max_blocks", "lxm_max_lds",
            "lxm_last_error", "lxm_device_cus", "lxm_t_elem", "lxm_t_sum", "lxm_pf_layers",
            "lxm_pf_head", "lxm_pf_embed", "lxm_pf_tiles", "lxm_pf_lds", "lxm_dn_step", "lxm_dn_run",
-           "lxm_dn_prefill", "lxm_t_sync", "lxm_run_noalloc")
+           "lxm_dn_prefill", "lxm_t_sync", "lxm_run_noalloc", "lxm_gdn_chunk")

@@ -622,3 +622,133 @@ void ox_rec_step(int nk, int nv, int bf16, const float* q, const float* k, const
   memcpy(o, w.o, 4 * (size_t)nv * 128);
   ws_free(&w);
 }
+
+/* ---------------------------------------------------------------------------------------------
+   torch_chunk_gated_delta_rule (TF:249-327), the stock forward's T > 1 delta rule, for one value
+   head over positions 0 .. T - 1 in chunks of C from position 0 (the sequence padded with zero
+   positions to a multiple of C, as F.pad does): everything in fp32 (the function casts its
+   inputs to float32). q, k (T, K) are the l2-normed query and key (use_qk_l2norm_in_kernel is
+   applied by the caller, in the model dtype), v (T, V), g (T) the log decays, beta (T); S (K, V)
+   the initial state, overwritten with the final state; o (T, V) the fp32 outputs (the caller
+   casts them to the model dtype). The matrix products sum in index order from +0; the
+   cumulative sum of g accumulates in binary64 and rounds each prefix (ATen's CPU cumsum for
+   float). Returns 0, or -1 if C > 64 or K, V > 256. */
+int ox_chunk_gdr(int T, int K, int V, int C, const float* q, const float* k, const float* v,
+                 const float* g, const float* beta, float* S, float* o) {
+  if (C > 64 || C < 1 || K > 256 || V > 256) return -1;
+  const float scale = (float)(1.0 / sqrt((double)K));
+  float* A = xalloc(4 * 64 * 64);      /* attn, then (I - A)^-1 form */
+  float* Dm = xalloc(4 * 64 * 64);     /* decay_mask */
+  float* A2 = xalloc(4 * 64 * 64);     /* (q k^T) * decay_mask */
+  float* U = xalloc(4 * (size_t)64 * V);  /* value = attn @ v_beta */
+  float* W = xalloc(4 * (size_t)64 * K);  /* k_cumdecay = attn @ (k_beta exp(gc)) */
+  float* kb = xalloc(4 * (size_t)64 * K); /* k_beta, then k_beta exp(gc) */
+  float* vb = xalloc(4 * (size_t)64 * V); /* v_beta */
+  float* qs = xalloc(4 * (size_t)64 * K); /* q * scale */
+  float* vn = xalloc(4 * (size_t)64 * V); /* v_new */
+  float* Sn = xalloc(4 * (size_t)K * V);
+  float gc[64], row[64];
+  for (int c0 = 0; c0 < T; c0 += C) {
+    const int n = T - c0 < C ? T - c0 : C; /* live positions; the rest are the zero padding */
+    /* the chunk's inputs, padded with zeros to C positions */
+    double acc = 0.0;
+    for (int i = 0; i < C; i++) {
+      const int t = c0 + i;
+      const float gi = i < n ? g[t] : 0.0f, bi = i < n ? beta[t] : 0.0f;
+      acc += (double)gi;
+      gc[i] = (float)acc;
+      for (int d = 0; d < K; d++) {
+        const float qi = i < n ? q[(size_t)t * K + d] : 0.0f, ki = i < n ? k[(size_t)t * K + d] : 0.0f;
+        qs[i * K + d] = qi * scale;
+        kb[i * K + d] = ki * bi;
+      }
+      for (int d = 0; d < V; d++) vb[i * V + d] = (i < n ? v[(size_t)t * V + d] : 0.0f) * bi;
+    }
+    /* decay_mask = exp(tril(gc_i - gc_j)), zero above the diagonal */
+    for (int i = 0; i < C; i++)
+      for (int j = 0; j < C; j++) Dm[i * 64 + j] = j <= i ? ox_expf(gc[i] - gc[j]) : 0.0f;
+    /* attn = -((k_beta @ k^T) * decay_mask), zero on and above the diagonal */
+    for (int i = 0; i < C; i++)
+      for (int j = 0; j < C; j++) {
+        if (j >= i) { A[i * 64 + j] = 0.0f; continue; }
+        float s = 0.0f;
+        for (int d = 0; d < K; d++) {
+          const float kj = c0 + j < T ? k[(size_t)(c0 + j) * K + d] : 0.0f;
+          s = s + kb[i * K + d] * kj;
+        }
+        A[i * 64 + j] = -(s * Dm[i * 64 + j]);
+      }
+    /* row i += row i (before the update) @ attn[:i, :i] (rows < i already updated) */
+    for (int i = 1; i < C; i++) {
+      for (int j = 0; j < i; j++) row[j] = A[i * 64 + j];
+      for (int j = 0; j < i; j++) {
+        float s = 0.0f;
+        for (int m = 0; m < i; m++) s = s + row[m] * A[m * 64 + j];
+        A[i * 64 + j] = row[j] + s;
+      }
+    }
+    for (int i = 0; i < C; i++) A[i * 64 + i] = A[i * 64 + i] + 1.0f;
+    /* value = attn @ v_beta; k_cumdecay = attn @ (k_beta * exp(gc)) */
+    for (int i = 0; i < C; i++) {
+      const float e = ox_expf(gc[i]);
+      for (int d = 0; d < K; d++) kb[i * K + d] = kb[i * K + d] * e;
+    }
+    for (int i = 0; i < C; i++) {
+      for (int d = 0; d < V; d++) {
+        float s = 0.0f;
+        for (int m = 0; m < C; m++) s = s + A[i * 64 + m] * vb[m * V + d];
+        U[i * V + d] = s;
+      }
+      for (int d = 0; d < K; d++) {
+        float s = 0.0f;
+        for (int m = 0; m < C; m++) s = s + A[i * 64 + m] * kb[m * K + d];
+        W[i * K + d] = s;
+      }
+    }
+    /* attn2 = (q @ k^T) * decay_mask (zero above the diagonal) */
+    for (int i = 0; i < C; i++)
+      for (int j = 0; j < C; j++) {
+        float s = 0.0f;
+        for (int d = 0; d < K; d++) {
+          const float kj = c0 + j < T ? k[(size_t)(c0 + j) * K + d] : 0.0f;
+          s = s + qs[i * K + d] * kj;
+        }
+        A2[i * 64 + j] = s * Dm[i * 64 + j];
+      }
+    /* v_new = value - k_cumdecay @ S; o = (q exp(gc)) @ S + attn2 @ v_new */
+    for (int i = 0; i < C; i++) {
+      const float e = ox_expf(gc[i]);
+      for (int d = 0; d < V; d++) {
+        float s = 0.0f;
+        for (int m = 0; m < K; m++) s = s + W[i * K + m] * S[(size_t)m * V + d];
+        vn[i * V + d] = U[i * V + d] - s;
+      }
+      for (int d = 0; d < V; d++) {
+        float s = 0.0f;
+        for (int m = 0; m < K; m++) s = s + (qs[i * K + m] * e) * S[(size_t)m * V + d];
+        if (i < n) o[(size_t)(c0 + i) * V + d] = s;
+      }
+    }
+    for (int i = 0; i < n; i++)
+      for (int d = 0; d < V; d++) {
+        float s = 0.0f;
+        for (int m = 0; m < C; m++) s = s + A2[i * 64 + m] * vn[m * V + d];
+        o[(size_t)(c0 + i) * V + d] = o[(size_t)(c0 + i) * V + d] + s;
+      }
+    /* S = S * exp(gc[-1]) + (k * exp(gc[-1] - gc))^T @ v_new */
+    const float el = ox_expf(gc[C - 1]);
+    for (int i = 0; i < C; i++) row[i] = ox_expf(gc[C - 1] - gc[i]);
+    for (int m = 0; m < K; m++)
+      for (int d = 0; d < V; d++) {
+        float s = 0.0f;
+        for (int i = 0; i < C; i++) {
+          const float ki = c0 + i < T ? k[(size_t)(c0 + i) * K + m] : 0.0f;
+          s = s + (ki * row[i]) * vn[i * V + d];
+        }
+        Sn[(size_t)m * V + d] = S[(size_t)m * V + d] * el + s;
+      }
+    memcpy(S, Sn, 4 * (size_t)K * V);
+  }
+  free(A); free(Dm); free(A2); free(U); free(W); free(kb); free(vb); free(qs); free(vn); free(Sn);
+  return 0;
+}

@@ -122,6 +122,20 @@ def rec_step(q, k, v, g, beta, S, bf16: bool):
     return o
 
 
+def chunk_gdr(q, k, v, g, beta, S, C: int = 64):
+    """torch_chunk_gated_delta_rule for one value head (q, k (T, K) l2-normed; v (T, V); g, beta
+    (T)); S (K, V) float32 updated in place to the final state. Returns o (T, V) float32."""
+    q, k, v, g, beta = (np.ascontiguousarray(a, np.float32) for a in (q, k, v, g, beta))
+    assert S.dtype == np.float32 and S.flags.c_contiguous
+    T, K = q.shape
+    V = v.shape[1]
+    o = np.zeros((T, V), np.float32)
+    rc = lib().ox_chunk_gdr(T, K, V, C, _p(q), _p(k), _p(v), _p(g), _p(beta), _p(S), _p(o))
+    if rc:
+        raise ValueError("chunk_gdr: unsupported sizes")
+    return o
+
+
 class OracleModel:
     """A SparseModel's tensors in the oracle's C layout (owns every array it points to)."""
 

@@ -75,10 +75,66 @@ def model_of(name):
     return m, conv0, rec0, synth.start_token(spec)
 
 
+def chunk_inputs(T: int, seed: int, exact: bool = False):
+    """One value head's delta-rule inputs over T positions: query and key l2-normed over 128 live
+    dims of 256 (the padded key heads), values, log decays and betas, and an initial state.
+    exact: the chip's exact regime (one-hot keys and queries, beta in {0, 1}, no decay, small
+    dyadic values), where every product and sum is exact."""
+    rng = np.random.default_rng(seed)
+    K, V, KL = 256, 128, 128
+    if exact:
+        q = np.zeros((T, K), np.float32)
+        k = np.zeros((T, K), np.float32)
+        q[np.arange(T), rng.integers(0, KL, T)] = 1.0
+        k[np.arange(T), rng.integers(0, KL, T)] = 1.0
+        v = rng.integers(-8, 9, (T, V)).astype(np.float32) / 4
+        g = np.zeros(T, np.float32)
+        beta = rng.integers(0, 2, T).astype(np.float32)
+        S0 = rng.integers(-8, 9, (K, V)).astype(np.float32) / 8
+        S0[KL:] = 0.0
+        return q, k, v, g, beta, S0
+
+    def unit(x):
+        return (x / np.sqrt((x.astype(np.float64) ** 2).sum(-1, keepdims=True))).astype(np.float32)
+
+    q = np.zeros((T, K), np.float32)
+    k = np.zeros((T, K), np.float32)
+    q[:, :KL] = unit(rng.standard_normal((T, KL)))
+    k[:, :KL] = unit(rng.standard_normal((T, KL)))
+    v = rng.standard_normal((T, V)).astype(np.float32)
+    g = (-0.5 * rng.random(T)).astype(np.float32)
+    beta = rng.random(T).astype(np.float32)
+    S0 = np.zeros((K, V), np.float32)
+    S0[:KL] = rng.standard_normal((KL, V))
+    return q, k, v, g, beta, S0
+
+
+def write_chunk(name: str, T: int, seed: int) -> None:
+    """transformers' torch_chunk_gated_delta_rule (chunk 64, float32, the initial state given,
+    use_qk_l2norm_in_kernel off: the inputs are normed already) on chunk_inputs(T, seed)."""
+    from transformers.models.qwen3_5.modeling_qwen3_5 import torch_chunk_gated_delta_rule
+
+    q, k, v, g, beta, S0 = chunk_inputs(T, seed)
+    t = [torch.from_numpy(a)[None, :, None] for a in (q, k, v, g, beta)]
+    o, S = torch_chunk_gated_delta_rule(*t, chunk_size=64, initial_state=torch.from_numpy(S0)[None, None],
+                                        output_final_state=True, use_qk_l2norm_in_kernel=False)
+    out = {"q": q[:, :128], "k": k[:, :128], "v": v, "g": g, "beta": beta, "S0": S0[:128],
+           "o": o[0, :, 0].numpy(), "S": S[0, 0, :128].numpy(), "T": np.int64(T)}
+    path = os.path.join(HERE, name + ".npz")
+    np.savez_compressed(path, **out)
+    print(name, os.path.getsize(path), "bytes")
+
+
+CHUNK_CASES = {"chunk_fp32_100": (100, 11)}
+
+
 def main():
     torch.set_grad_enabled(False)
-    names = sys.argv[1:] or list(CASES)
+    names = sys.argv[1:] or list(CASES) + list(CHUNK_CASES)
     for name in names:
+        if name in CHUNK_CASES:
+            write_chunk(name, *CHUNK_CASES[name])
+            continue
         _, n, full = CASES[name]
         m, conv0, rec0, start = model_of(name)
         hf = synth.to_hf(m)

@@ -259,7 +259,9 @@ def test_packer_fits_every_config(packed):
 
 def test_c_abi_exports_every_declared_symbol(native_lib):
     """The library loads and exports each entry point include/*.h declares (no GPU call)."""
-    hdr = "".join(open(os.path.join(ROOT, "include", h)).read() for h in ("lxm.h", "lxm_prefill.h", "lxm_dense.h"))
+    hdrs = sorted(f for f in os.listdir(os.path.join(ROOT, "include")) if f.endswith(".h"))
+    assert {"lxm.h", "lxm_prefill.h", "lxm_dense.h", "lxm_chunk.h"} <= set(hdrs)
+    hdr = "".join(open(os.path.join(ROOT, "include", h)).read() for h in hdrs)
     names = re.findall(r"^int (lxm_\w+)\(", hdr, re.M)
     assert len(names) >= 8
     lib = ctypes.CDLL(mk_build.LIB)

@@ -328,3 +328,57 @@ def test_dense_order_is_the_group_tree(oracle_lib):
     x[0], x[1], x[32] = 1.0, 2.0 ** 24, 1.0
     assert float(ox.row_dot(x, w, dense=True)) == 16777218.0
     assert float(ox.row_dot(x, w, dense=False)) == 16777216.0
+
+
+def _chunk_fixture():
+    g = _load("chunk_fp32_100")
+    pad = lambda a, n: np.concatenate([a, np.zeros((a.shape[0], n - a.shape[1]), np.float32)], 1)
+    q, k = pad(g["q"], 256), pad(g["k"], 256)
+    S0 = np.zeros((256, 128), np.float32)
+    S0[:128] = g["S0"]
+    return g, q, k, S0
+
+
+def test_chunk_form_matches_stock_chunk(oracle_lib):
+    """The oracle's chunked delta rule against transformers' torch_chunk_gated_delta_rule (chunk
+    64, float32) on one value head over 100 positions (a full chunk and a padded one): outputs and
+    final state within 1e-6 of the largest magnitude (the matrix products' orders are MKL's)."""
+    g, q, k, S0 = _chunk_fixture()
+    S = S0.copy()
+    o = oracle_lib.chunk_gdr(q, k, g["v"], g["g"], g["beta"], S, 64)
+    assert np.abs(o - g["o"]).max() <= 1e-6 * np.abs(g["o"]).max()
+    assert np.abs(S[:128] - g["S"]).max() <= 1e-6 * np.abs(g["S"]).max()
+    assert not S[128:].any()
+
+
+def test_chunk_form_planted_mistakes_fail(oracle_lib):
+    """What the fixture comparison catches: a dropped decay (g = 0), a dropped beta, and the
+    recurrent form itself differ from the stock chunk output by far more than its tolerance."""
+    g, q, k, S0 = _chunk_fixture()
+    ref = g["o"]
+    tol = 1e-6 * np.abs(ref).max()
+    o1 = oracle_lib.chunk_gdr(q, k, g["v"], np.zeros_like(g["g"]), g["beta"], S0.copy(), 64)
+    o2 = oracle_lib.chunk_gdr(q, k, g["v"], g["g"], np.ones_like(g["beta"]), S0.copy(), 64)
+    assert np.abs(o1 - ref).max() > 1e3 * tol and np.abs(o2 - ref).max() > 1e3 * tol
+
+
+@pytest.mark.parametrize("C", [64, 16])
+def test_chunk_form_exact_regime_equals_recurrent(oracle_lib, C):
+    """In the chip's exact regime (one-hot keys and queries, beta in {0, 1}, no decay, dyadic
+    values) every product and sum is exact, so the chunked form (any chunk size) equals the
+    delta rule's recurrence S <- S + k (x) (v - S^T k) beta, o = S^T q / 16, run position by
+    position, bit for bit (outputs and final state)."""
+    from golden.make_golden import chunk_inputs
+
+    q, k, v, g, beta, S0 = chunk_inputs(150, 4, exact=True)
+    S = S0.copy()
+    o = oracle_lib.chunk_gdr(q, k, v, g, beta, S, C)
+    Sr = S0.astype(np.float64)
+    orr = np.zeros(o.shape, np.float64)
+    for t in range(len(q)):
+        Sr = Sr * np.exp(float(g[t]))
+        Sr = Sr + np.outer(k[t], (v[t] - Sr.T @ k[t]) * beta[t])
+        orr[t] = Sr.T @ (q[t] / 16.0)
+    assert (o.astype(np.float64) == orr).all()
+    assert (S.astype(np.float64) == Sr).all()
+    assert np.abs(orr).max() > 0 and (beta == 1).any() and (beta == 0).any()
