@@ -576,6 +576,25 @@ def dense_leg(args, dev) -> dict:
         e3.record(stream)
         torch.cuda.synchronize()
         ms_per = e2.elapsed_time(e3)
+    chunked = None
+    if args.dn_chunked:
+        # the stock forward's prompt (T > 1 path): the delta rule in chunks of 64 on the matrix
+        # cores, from the same zero state (the decode above continues from the batched prompt)
+        c2 = fast.StateCache(conv0, rec0, "bf16", dev)
+        dd2 = dense.DenseDecode(dm, c2, max_steps=2)
+        dd2.prefill(toks[:64], mode="chunked")  # warm-up (one chunk)
+        c2 = fast.StateCache(conv0, rec0, "bf16", dev)
+        dd2 = dense.DenseDecode(dm, c2, max_steps=2)
+        torch.cuda.synchronize()
+        t = time.perf_counter()
+        dd2.prefill(toks[:-1], mode="chunked")
+        pc = dd2.run(toks[-1:], 1, graph=False)
+        ch_s = time.perf_counter() - t
+        chunked = {"tokens": n_prefill, "s": round(ch_s, 3), "tok_s": round(n_prefill / ch_s, 1),
+                   "first_prediction_equal": bool(pc[0] == p1[-1]),
+                   "mode": "lxm_dn_prefill_chunked (chunks of 64, lxm_gdn_chunk on MFMA) + one step"}
+        log(f"[bench] c4: chunked prompt of {n_prefill} tokens in {ch_s:.2f}s")
+        del dd2, c2
     H, I, nk, kl, rl = spec.hidden, spec.inter, spec.nk, spec.kd_live, spec.r_live
     nvr = nk * rl * 128
     w_layer = 2 * ((2 * nk * kl + 2 * nvr + 2 * nk * rl) * H + H * nvr + 3 * I * H)
@@ -612,6 +631,7 @@ def dense_leg(args, dev) -> dict:
                         "traffic": None if t_tok is None else round(t_tok * n_steps),
                         "padded_bytes_per_token": d.n_layers * (pad_layer + state) + 2 * spec.vocab * H},
            "distinct_predictions": len(set(p2)),
+           "prefill_chunked": chunked,
            "persistent": None if ms_per is None else
                          {"steps": n_per, "tok_s": round(n_per / (ms_per * 1e-3), 1),
                           "note": "lxm_dn_run, continuing from the greedy run's states"}}
@@ -651,6 +671,8 @@ def make_parser() -> argparse.ArgumentParser:
                     help="1: the dense steps replayed from a captured graph; 0: launched eagerly")
     ap.add_argument("--dn-batched", type=int, default=1,
                     help="config 4's prompt through lxm_dn_prefill (0: as forced steps)")
+    ap.add_argument("--dn-chunked", type=int, default=1,
+                    help="1: also time the prompt through lxm_dn_prefill_chunked; 0: skip it")
     ap.add_argument("--dn-persistent", type=int, default=1,
                     help="1: also time the persistent run (lxm_dn_run); 0: skip it")
     return ap

@@ -96,6 +96,7 @@ typedef struct lxm_dn_pbuf {
   float* o;    /* (PB, nk x rl x 128): the delta rule's outputs */
   uint16_t* ys;  /* (PB, nk x rl x 128) bf16: the gated norm's output, interleaved */
   uint16_t* act; /* (PB, inter) bf16: SwiGLU's output, interleaved */
+  float* gl;     /* (PB, nk x rl): the log decays (lxm_dn_prefill_chunked only; else unused) */
 } lxm_dn_pbuf;
 
 /* T forced tokens (device int32) through every layer without the head, in batches of LXM_DN_PB:
@@ -107,6 +108,19 @@ typedef struct lxm_dn_pbuf {
    9216) or (256, 512, 512). Returns a hipError_t. */
 int lxm_dn_prefill(const lxm_dn_params* p_host, const int32_t* tokens, int T,
                    const lxm_dn_pbuf* buf, void* stream);
+
+/* The stock forward's prompt (transformers' T > 1 path, Qwen3_5GatedDeltaNet.forward :517-529:
+   torch_chunk_gated_delta_rule, chunks of 64 from the prompt's first token) for T forced tokens
+   through every layer without the head: each chunk of LXM_CHUNK (64) tokens goes through every
+   layer, its delta rule as one call of lxm_gdn_chunk (include/lxm_chunk.h; MFMA), the row
+   kernels on its LXM_DN_PB-token slices. The projections, norms, conv, MLP and out_proj are
+   those of lxm_dn_prefill bit for bit on the same inputs; the delta rule's outputs and states
+   are the chunked form's (equal to the recurrent step's up to the order of fp32 sums).
+   buf's arrays hold LXM_CHUNK tokens (the sizes above with PB = 64) and buf->gl is set. The
+   predictions a caller then takes from steps are the stock generate's after a T-token prompt.
+   Returns a hipError_t. */
+int lxm_dn_prefill_chunked(const lxm_dn_params* p_host, const int32_t* tokens, int T,
+                           const lxm_dn_pbuf* buf, void* stream);
 
 #ifdef __cplusplus
 }

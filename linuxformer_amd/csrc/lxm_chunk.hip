@@ -1,7 +1,7 @@
 // The stock forward's chunked delta rule (torch_chunk_gated_delta_rule, transformers qwen3_5
 // :249-327) for one chunk of <= 64 positions, on MI355X's matrix cores.
 //
-// One workgroup (4 waves) per (value head, 32 state columns). Everything a chunk needs sits in
+// One workgroup (8 waves) per (value head, 32 state columns). Everything a chunk needs sits in
 // LDS as fp32 (the keys and queries over the live key dims, the state's 32 columns, the values
 // times beta), and every matrix product is a sequence of v_mfma_f32_16x16x4_f32 (a 16 x 16 tile
 // += 16 x 4 times 4 x 16; lane l supplies A[l % 16][l / 16] and B[l / 16][l % 16] and holds
@@ -25,7 +25,8 @@ using namespace lxm;
 
 namespace {
 
-constexpr int CT = 256;       // threads per workgroup (4 waves)
+constexpr int CT = 512;       // threads per workgroup (8 waves: two per SIMD)
+constexpr int NWV = CT / 64;
 constexpr int C = 64;         // positions per chunk
 constexpr int KL = 128;       // live key dims at most
 constexpr int VD = 128;
@@ -67,8 +68,38 @@ struct Lane {
   }
 };
 
-// dispatch of one of the four waves' rows of a 16 x 16 output tile
 __device__ __forceinline__ int wave() { return __builtin_amdgcn_readfirstlane(threadIdx.x >> 6); }
+
+// acc += A B over k blocks kb0 .. kb1 - 1 of 16 (k = 16 kb + 4 j + a_k): fa(k) and fb(k) give
+// this lane's A and B elements. Each block's 8 operands are read before the previous block's 4
+// MFMAs issue, so the LDS reads overlap the matrix core.
+template <class FA, class FB>
+__device__ __forceinline__ v4f tile_mm(int kb0, int kb1, const Lane& ln, FA fa, FB fb, v4f acc) {
+  if (kb0 >= kb1) return acc;
+  float a[4], b[4];
+#pragma unroll
+  for (int j = 0; j < 4; j++) {
+    a[j] = fa(16 * kb0 + 4 * j + ln.a_k);
+    b[j] = fb(16 * kb0 + 4 * j + ln.a_k);
+  }
+  for (int kb = kb0; kb < kb1; kb++) {
+    float an[4], bn[4];
+    const int kn = kb + 1 < kb1 ? kb + 1 : kb;  // (the last block reads its own operands again)
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+      an[j] = fa(16 * kn + 4 * j + ln.a_k);
+      bn[j] = fb(16 * kn + 4 * j + ln.a_k);
+    }
+#pragma unroll
+    for (int j = 0; j < 4; j++) acc = mfma4(a[j], b[j], acc);
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+      a[j] = an[j];
+      b[j] = bn[j];
+    }
+  }
+  return acc;
+}
 
 }  // namespace
 
@@ -79,17 +110,19 @@ __global__ __launch_bounds__(CT) void lxm_chunk_k(lxm_chunk_io io) {
   const int n = io.n, kl = io.kl, kh = h / io.rl;
   const Lane ln;
   float* Sg = io.S + ((size_t)kh * io.rfull + h % io.rl) * 256 * VD;
+  constexpr int NKB = KL / 16;  // k blocks over the key dims (zeros past kl add nothing)
 
-  // ---- inputs into LDS (zero past n positions and kl dims)
-  for (int idx = t; idx < C * KL; idx += CT) {
-    const int i = idx / KL, d = idx % KL;
-    float kv = 0.0f, qv = 0.0f;
+  // ---- inputs into LDS (zero past n positions and kl dims), four values per load
+  for (int idx = t; idx < C * KL / 4; idx += CT) {
+    const int i = idx / (KL / 4), d = 4 * (idx % (KL / 4));
+    v4f kv = {0.0f, 0.0f, 0.0f, 0.0f}, qv = kv;
     if (i < n && d < kl) {
-      kv = io.k[(int64_t)i * io.qk_ts + (int64_t)kh * io.qk_hs + d];
-      qv = io.q[(int64_t)i * io.qk_ts + (int64_t)kh * io.qk_hs + d];
+      const int64_t o = (int64_t)i * io.qk_ts + (int64_t)kh * io.qk_hs + d;
+      kv = *reinterpret_cast<const v4f*>(io.k + o);
+      qv = *reinterpret_cast<const v4f*>(io.q + o);
     }
-    l.k[i][d] = kv;
-    l.qw[i][d] = qv;
+    *reinterpret_cast<v4f*>(&l.k[i][d]) = kv;
+    *reinterpret_cast<v4f*>(&l.qw[i][d]) = qv;
   }
   if (t < C) {
     float b = 0.0f, g = 0.0f;
@@ -100,9 +133,11 @@ __global__ __launch_bounds__(CT) void lxm_chunk_k(lxm_chunk_io io) {
     l.beta[t] = b;
     l.gc[t] = g;
   }
-  for (int idx = t; idx < KL * VT; idx += CT) {
-    const int d = idx / VT, c = idx % VT;
-    l.s[d][c] = d < kl ? Sg[(size_t)d * VD + c0 + c] : 0.0f;
+  for (int idx = t; idx < KL * VT / 4; idx += CT) {
+    const int d = idx / (VT / 4), c = 4 * (idx % (VT / 4));
+    v4f sv = {0.0f, 0.0f, 0.0f, 0.0f};
+    if (d < kl) sv = *reinterpret_cast<const v4f*>(Sg + (size_t)d * VD + c0 + c);
+    *reinterpret_cast<v4f*>(&l.s[d][c]) = sv;
   }
   __syncthreads();
   if (t == 0) {  // cumsum of g: binary64 accumulation, each prefix rounded (ATen's CPU cumsum)
@@ -112,9 +147,12 @@ __global__ __launch_bounds__(CT) void lxm_chunk_k(lxm_chunk_io io) {
       l.gc[i] = (float)acc;
     }
   }
-  for (int idx = t; idx < C * VT; idx += CT) {
-    const int i = idx / VT, c = idx % VT;
-    l.vb[i][c] = (i < n ? io.v[(int64_t)i * io.v_ts + (int64_t)h * VD + c0 + c] : 0.0f) * l.beta[i];
+  for (int idx = t; idx < C * VT / 4; idx += CT) {
+    const int i = idx / (VT / 4), c = 4 * (idx % (VT / 4));
+    v4f vv = {0.0f, 0.0f, 0.0f, 0.0f};
+    if (i < n) vv = *reinterpret_cast<const v4f*>(io.v + (int64_t)i * io.v_ts + (int64_t)h * VD + c0 + c);
+    const float b = l.beta[i];
+    *reinterpret_cast<v4f*>(&l.vb[i][c]) = v4f{vv.x * b, vv.y * b, vv.z * b, vv.w * b};
   }
   __syncthreads();
   if (t < C) {
@@ -125,45 +163,72 @@ __global__ __launch_bounds__(CT) void lxm_chunk_k(lxm_chunk_io io) {
   }
   __syncthreads();
 
-  // ---- A2 = (q k^T) * Gamma and L = (k beta k^T) * Gamma (strictly lower): wave w takes row
-  // block w, column blocks 0..w (the rest are zero); O1 = (q exp(gc)) S on the wave's row block
-  v4f o1[VT / 16];
+  // ---- A2 = (q k^T) * Gamma and L = (k beta k^T) * Gamma (strictly lower) on the 10 tiles on
+  // or below the diagonal, dealt to the waves (tile p: row block ti, column block tj <= ti);
+  // O1 = (q exp(gc)) S: wave w takes row block w % 4, column tile w / 4
+  for (int p = w; p < 10; p += NWV) {
+    const int ti = p < 1 ? 0 : p < 3 ? 1 : p < 6 ? 2 : 3;
+    const int tj = p - ti * (ti + 1) / 2;
+    const int ia = 16 * ti + ln.a_i, jb = 16 * tj + ln.a_i;
+    const float bi = l.beta[ia];
+    v4f aq = {0.0f, 0.0f, 0.0f, 0.0f}, ak = aq;
+    float qa[4], ka[4], kb[4];
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+      qa[j] = l.qw[ia][4 * j + ln.a_k];
+      ka[j] = l.k[ia][4 * j + ln.a_k] * bi;
+      kb[j] = l.k[jb][4 * j + ln.a_k];
+    }
+    for (int d0 = 0; d0 < KL; d0 += 16) {
+      float qn[4], kn[4], bn[4];
+      const int dn = d0 + 16 < KL ? d0 + 16 : d0;
+#pragma unroll
+      for (int j = 0; j < 4; j++) {
+        qn[j] = l.qw[ia][dn + 4 * j + ln.a_k];
+        kn[j] = l.k[ia][dn + 4 * j + ln.a_k] * bi;
+        bn[j] = l.k[jb][dn + 4 * j + ln.a_k];
+      }
+#pragma unroll
+      for (int j = 0; j < 4; j++) {
+        aq = mfma4(qa[j], kb[j], aq);
+        ak = mfma4(ka[j], kb[j], ak);
+      }
+#pragma unroll
+      for (int j = 0; j < 4; j++) {
+        qa[j] = qn[j];
+        ka[j] = kn[j];
+        kb[j] = bn[j];
+      }
+    }
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+      const int i = 16 * ti + ln.d_i + r, j = 16 * tj + ln.d_j;
+      const float gm = j <= i ? cr_exp(l.gc[i] - l.gc[j]) : 0.0f;
+      l.a2[i][j] = aq[r] * gm;
+      l.lp[i][j] = j < i ? ak[r] * gm : 0.0f;
+    }
+  }
+  // the six tiles above the diagonal are zero in both
+  for (int idx = t; idx < 6 * 256; idx += CT) {
+    const int p = idx / 256, e = idx % 256;
+    const int ti = p < 3 ? 0 : p < 5 ? 1 : 2, tj = p < 3 ? p + 1 : p < 5 ? p - 1 : 3;
+    l.a2[16 * ti + e / 16][16 * tj + e % 16] = 0.0f;
+    l.lp[16 * ti + e / 16][16 * tj + e % 16] = 0.0f;
+  }
+  const int ob = w & 3, oc = w >> 2;  // this wave's output tile of the (64, 32) products
+  v4f o1 = {0.0f, 0.0f, 0.0f, 0.0f};
   {
-    const int ti = w;
-    for (int tj = 0; tj < 4; tj++) {
-      v4f aq = {0.0f, 0.0f, 0.0f, 0.0f}, ak = {0.0f, 0.0f, 0.0f, 0.0f};
-      if (tj <= ti) {
-        const int ia = 16 * ti + ln.a_i, jb = 16 * tj + ln.a_i;
-        const float bi = l.beta[ia];
-        for (int d0 = 0; d0 < kl; d0 += 4) {
-          const float kb = l.k[jb][d0 + ln.a_k];  // B[d][j] = k[j][d]
-          aq = mfma4(l.qw[ia][d0 + ln.a_k], kb, aq);
-          ak = mfma4(l.k[ia][d0 + ln.a_k] * bi, kb, ak);
-        }
-      }
-#pragma unroll
-      for (int r = 0; r < 4; r++) {
-        const int i = 16 * ti + ln.d_i + r, j = 16 * tj + ln.d_j;
-        const float gm = j <= i ? cr_exp(l.gc[i] - l.gc[j]) : 0.0f;
-        l.a2[i][j] = aq[r] * gm;
-        l.lp[i][j] = j < i ? ak[r] * gm : 0.0f;
-      }
-    }
-#pragma unroll
-    for (int tc = 0; tc < VT / 16; tc++) {
-      v4f a = {0.0f, 0.0f, 0.0f, 0.0f};
-      const int ia = 16 * ti + ln.a_i;
-      const float e = l.eg[ia];
-      for (int d0 = 0; d0 < kl; d0 += 4)
-        a = mfma4(l.qw[ia][d0 + ln.a_k] * e, l.s[d0 + ln.a_k][16 * tc + ln.a_i], a);
-      o1[tc] = a;
-    }
+    const int ia = 16 * ob + ln.a_i;
+    const float e = l.eg[ia];
+    o1 = tile_mm(0, NKB, ln, [&](int k) { return l.qw[ia][k] * e; },
+                 [&](int k) { return l.s[k][16 * oc + ln.a_i]; }, o1);
   }
   __syncthreads();
 
-  // ---- T = (I + L)^-1: diagonal block w by forward substitution on wave w (lanes 0..15 are
-  // the columns: T[i][j] = -sum_{m=j}^{i-1} L[i][m] T[m][j], T[i][i] = 1)
-  {
+  // ---- T = (I + L)^-1: diagonal block w (waves 0..3) by forward substitution (lanes 0..15
+  // are the columns: T[i][j] = -sum_{m=j}^{i-1} L[i][m] T[m][j], T[i][i] = 1); blocks above
+  // the diagonal are zero
+  if (w < 4) {
     const int b0 = 16 * w, j = t & 63;
     if (j < 16) l.tt[b0][b0 + j] = j == 0 ? 1.0f : 0.0f;
     __builtin_amdgcn_wave_barrier();
@@ -175,10 +240,12 @@ __global__ __launch_bounds__(CT) void lxm_chunk_k(lxm_chunk_io io) {
       }
       __builtin_amdgcn_wave_barrier();
     }
-    // the blocks above the diagonal are zero
-    if (j < 16)
-      for (int jb = w + 1; jb < 4; jb++)
-        for (int i = 0; i < 16; i++) l.tt[b0 + i][16 * jb + j] = 0.0f;
+  } else {
+    for (int idx = t - 256; idx < 6 * 256; idx += 256) {
+      const int p = idx / 256, e = idx % 256;
+      const int ti = p < 3 ? 0 : p < 5 ? 1 : 2, tj = p < 3 ? p + 1 : p < 5 ? p - 1 : 3;
+      l.tt[16 * ti + e / 16][16 * tj + e % 16] = 0.0f;
+    }
   }
   __syncthreads();
   // block rows 1..3: T_ij = -T_ii P, P = sum_{k=j}^{i-1} L_ik T_kj; block (i, j) on wave j
@@ -186,92 +253,73 @@ __global__ __launch_bounds__(CT) void lxm_chunk_k(lxm_chunk_io io) {
     if (w < bi) {
       const int bj = w;
       v4f p = {0.0f, 0.0f, 0.0f, 0.0f};
-      for (int bk = bj; bk < bi; bk++)
-        for (int m0 = 0; m0 < 16; m0 += 4)
-          p = mfma4(l.lp[16 * bi + ln.a_i][16 * bk + m0 + ln.a_k],
-                    l.tt[16 * bk + m0 + ln.a_k][16 * bj + ln.a_i], p);
+      p = tile_mm(bj, bi, ln, [&](int k) { return l.lp[16 * bi + ln.a_i][k]; },
+                  [&](int k) { return l.tt[k][16 * bj + ln.a_i]; }, p);
 #pragma unroll
       for (int r = 0; r < 4; r++) l.pt[w][ln.d_i + r][ln.d_j] = p[r];
       __builtin_amdgcn_wave_barrier();
       v4f q = {0.0f, 0.0f, 0.0f, 0.0f};
-      for (int m0 = 0; m0 < 16; m0 += 4)
-        q = mfma4(l.tt[16 * bi + ln.a_i][16 * bi + m0 + ln.a_k], l.pt[w][m0 + ln.a_k][ln.a_i], q);
+      q = tile_mm(0, 1, ln, [&](int k) { return l.tt[16 * bi + ln.a_i][16 * bi + k]; },
+                  [&](int k) { return l.pt[w][k][ln.a_i]; }, q);
 #pragma unroll
       for (int r = 0; r < 4; r++) l.tt[16 * bi + ln.d_i + r][16 * bj + ln.d_j] = -q[r];
     }
     __syncthreads();
   }
 
-  // ---- W = T (k beta exp(gc)) into qw (the queries are no longer read): wave w takes column
-  // blocks 2w, 2w + 1 of every row block (T is lower triangular: k blocks <= the row block)
+  // ---- W = T (k beta exp(gc)) into qw (the queries are no longer read): the 32 tiles (4 row
+  // blocks x 8 column blocks) dealt to the waves; T is lower triangular (k blocks <= the row's)
+  for (int p = w; p < 32; p += NWV) {
+    const int ti = p & 3, tc = p >> 2;
+    v4f a = {0.0f, 0.0f, 0.0f, 0.0f};
+    a = tile_mm(0, ti + 1, ln, [&](int k) { return l.tt[16 * ti + ln.a_i][k]; },
+                [&](int k) { return (l.k[k][16 * tc + ln.a_i] * l.beta[k]) * l.eg[k]; }, a);
 #pragma unroll
-  for (int cb = 0; cb < 2; cb++) {
-    const int tc = 2 * w + cb;
-    if (16 * tc >= kl) continue;
-    for (int ti = 0; ti < 4; ti++) {
-      v4f a = {0.0f, 0.0f, 0.0f, 0.0f};
-      for (int m0 = 0; m0 < 16 * (ti + 1); m0 += 4) {
-        const int m = m0 + ln.a_k;
-        a = mfma4(l.tt[16 * ti + ln.a_i][m], (l.k[m][16 * tc + ln.a_i] * l.beta[m]) * l.eg[m], a);
-      }
-#pragma unroll
-      for (int r = 0; r < 4; r++) l.qw[16 * ti + ln.d_i + r][16 * tc + ln.d_j] = a[r];
-    }
+    for (int r = 0; r < 4; r++) l.qw[16 * ti + ln.d_i + r][16 * tc + ln.d_j] = a[r];
   }
   __syncthreads();
 
-  // ---- v_new = T (v beta) - W S on the wave's row block, into lp (L is no longer read)
+  // ---- v_new = T (v beta) - W S on the wave's output tile, into lp (L was last read by the
+  // block stages, before the barriers above)
   {
-    const int ti = w;
+    v4f u = {0.0f, 0.0f, 0.0f, 0.0f}, vp = u;
+    u = tile_mm(0, ob + 1, ln, [&](int k) { return l.tt[16 * ob + ln.a_i][k]; },
+                [&](int k) { return l.vb[k][16 * oc + ln.a_i]; }, u);
+    vp = tile_mm(0, NKB, ln, [&](int k) { return l.qw[16 * ob + ln.a_i][k]; },
+                 [&](int k) { return l.s[k][16 * oc + ln.a_i]; }, vp);
 #pragma unroll
-    for (int tc = 0; tc < VT / 16; tc++) {
-      v4f u = {0.0f, 0.0f, 0.0f, 0.0f}, vp = {0.0f, 0.0f, 0.0f, 0.0f};
-      for (int m0 = 0; m0 < 16 * (ti + 1); m0 += 4)
-        u = mfma4(l.tt[16 * ti + ln.a_i][m0 + ln.a_k], l.vb[m0 + ln.a_k][16 * tc + ln.a_i], u);
-      for (int d0 = 0; d0 < kl; d0 += 4)
-        vp = mfma4(l.qw[16 * ti + ln.a_i][d0 + ln.a_k], l.s[d0 + ln.a_k][16 * tc + ln.a_i], vp);
-#pragma unroll
-      for (int r = 0; r < 4; r++) l.lp[16 * ti + ln.d_i + r][16 * tc + ln.d_j] = u[r] - vp[r];
-    }
+    for (int r = 0; r < 4; r++) l.lp[16 * ob + ln.d_i + r][16 * oc + ln.d_j] = u[r] - vp[r];
   }
   __syncthreads();
 
-  // ---- o = O1 + A2 v_new on the wave's row block (A2 is lower triangular)
+  // ---- o = O1 + A2 v_new on the wave's output tile (A2 is lower triangular)
   {
-    const int ti = w;
+    v4f a = {0.0f, 0.0f, 0.0f, 0.0f};
+    a = tile_mm(0, ob + 1, ln, [&](int k) { return l.a2[16 * ob + ln.a_i][k]; },
+                [&](int k) { return l.lp[k][16 * oc + ln.a_i]; }, a);
 #pragma unroll
-    for (int tc = 0; tc < VT / 16; tc++) {
-      v4f a = {0.0f, 0.0f, 0.0f, 0.0f};
-      for (int m0 = 0; m0 < 16 * (ti + 1); m0 += 4)
-        a = mfma4(l.a2[16 * ti + ln.a_i][m0 + ln.a_k], l.lp[m0 + ln.a_k][16 * tc + ln.a_i], a);
-#pragma unroll
-      for (int r = 0; r < 4; r++) {
-        const int i = 16 * ti + ln.d_i + r, c = 16 * tc + ln.d_j;
-        if (i < n) {
-          const float v = o1[tc][r] + a[r];
-          io.o[(int64_t)i * io.o_ts + (int64_t)h * VD + c0 + c] = io.o_bf16 ? bf16r(v) : v;
-        }
+    for (int r = 0; r < 4; r++) {
+      const int i = 16 * ob + ln.d_i + r, c = 16 * oc + ln.d_j;
+      if (i < n) {
+        const float v = o1[r] + a[r];
+        io.o[(int64_t)i * io.o_ts + (int64_t)h * VD + c0 + c] = io.o_bf16 ? bf16r(v) : v;
       }
     }
   }
-  // ---- S <- S exp(g_last) + (k f)^T v_new: rows d of the state (kl of them), wave w takes
-  // row blocks w, w + 4 (only those below kl)
+  // ---- S <- S exp(g_last) + (k f)^T v_new: the state's 16 tiles (8 row blocks x 2 column
+  // tiles) dealt to the waves (row blocks past kl skipped)
   {
     const float el = l.misc[0];
-    for (int rb = w; rb < KL / 16; rb += 4) {
+    for (int p = w; p < 2 * KL / 16; p += NWV) {
+      const int rb = p >> 1, tc = p & 1;
       if (16 * rb >= kl) continue;
+      v4f a = {0.0f, 0.0f, 0.0f, 0.0f};
+      a = tile_mm(0, C / 16, ln, [&](int m) { return l.k[m][16 * rb + ln.a_i] * l.f[m]; },
+                  [&](int m) { return l.lp[m][16 * tc + ln.a_i]; }, a);
 #pragma unroll
-      for (int tc = 0; tc < VT / 16; tc++) {
-        v4f a = {0.0f, 0.0f, 0.0f, 0.0f};
-        for (int m0 = 0; m0 < C; m0 += 4) {
-          const int m = m0 + ln.a_k;
-          a = mfma4(l.k[m][16 * rb + ln.a_i] * l.f[m], l.lp[m][16 * tc + ln.a_i], a);
-        }
-#pragma unroll
-        for (int r = 0; r < 4; r++) {
-          const int d = 16 * rb + ln.d_i + r, c = 16 * tc + ln.d_j;
-          Sg[(size_t)d * VD + c0 + c] = l.s[d][c] * el + a[r];
-        }
+      for (int r = 0; r < 4; r++) {
+        const int d = 16 * rb + ln.d_i + r, c = 16 * tc + ln.d_j;
+        Sg[(size_t)d * VD + c0 + c] = l.s[d][c] * el + a[r];
       }
     }
   }

@@ -19,6 +19,7 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include "../../include/lxm_chunk.h"
 #include "../../include/lxm_dense.h"
 #include "lxm_math.h"
 #include "lxm_sync.h"
@@ -1107,6 +1108,7 @@ struct PbGdn {
   float* live;              // (n, nk, 2)
   float* o;                 // (n, nvr)
   int nk, kl, rl, R, nproj, n;
+  float* gl;                // (n, nk rl): the log decays g (the chunked form's input), or null
 };
 // conv_y for token b of the batch: the window [x(b-3), x(b-2), x(b-1)] is the batch's earlier
 // projections (row ch of P) or, before the batch, the stored window's newest values
@@ -1151,7 +1153,9 @@ __global__ __launch_bounds__(KD) void pb_prep(PbGdn a) {
     const float bb = Pb[2 * nq + 2 * nvr + vslot], aa = Pb[2 * nq + 2 * nvr + nk * rl + vslot];
     float* g = a.g + ((int64_t)b * nk * rl + vslot) * 2;
     g[0] = bf16r(sigmoid(bb));
-    g[1] = cr_exp((-cr_exp(a.A_log[vh])) * softplus(aa + a.dt_bias[vh]));
+    const float gg = (-cr_exp(a.A_log[vh])) * softplus(aa + a.dt_bias[vh]);
+    g[1] = cr_exp(gg);
+    if (a.gl) a.gl[(int64_t)b * nk * rl + vslot] = gg;
   }
   lds_barrier();
   if (wv < 2) {
@@ -1468,7 +1472,7 @@ static void pb_layer(const lxm_dn_params* ph, const lxm_dn_layer& ly, const lxm_
   hipLaunchKernelGGL(pb_norm, dim3(n), dim3(NT), 0, st, pb->h, ly.ln_in, eps, H, GH, pb->xn);
   launch_pb<GH, 8, 0>(ly.proj, nullptr, nproj, pb->xn, n, pb->P, nproj, 0, st);
   const PbGdn g{ly.conv_qk, ly.conv_v, ly.A_log, ly.dt_bias, ly.rec, ly.conv, pb->P, pb->qk,
-                pb->v, pb->g, pb->live, pb->o, nk, kl, rl, R, nproj, n};
+                pb->v, pb->g, pb->live, pb->o, nk, kl, rl, R, nproj, n, nullptr};
   hipLaunchKernelGGL(pb_prep, dim3(n, nk), dim3(KD), 0, st, g);
   hipLaunchKernelGGL(pb_gdn, dim3(nk * rl * QC), dim3(NT), 0, st, g);
   hipLaunchKernelGGL(pb_gnorm, dim3(n), dim3(PBT), 0, st, pb->o, pb->P, nproj, 2 * nq + nvr,
@@ -1495,6 +1499,82 @@ extern "C" int lxm_dn_prefill(const lxm_dn_params* ph, const int32_t* tokens, in
     for (int L = 0; L < ph->n_layers; L++) {
       if (full) pb_layer<40, 64, 144>(ph, ph->layers_host[L], pb, n, st);
       else pb_layer<4, 8, 8>(ph, ph->layers_host[L], pb, n, st);
+    }
+  }
+  return (int)hipGetLastError();
+}
+
+// The stock forward's prompt (the T > 1 path: Qwen3_5GatedDeltaNet.forward :517-529 calls
+// torch_chunk_gated_delta_rule): super-batches of up to LXM_CHUNK tokens, each a chunk of the
+// chunked delta rule (lxm_gdn_chunk, MFMA), the row kernels run on its PB-token slices. Every
+// other sum keeps the step's order; the delta rule's outputs and states are the chunked form's.
+template <int GH, int GV, int GI>
+static hipError_t pc_layer(const lxm_dn_params* ph, const lxm_dn_layer& ly, const lxm_dn_pbuf* pb,
+                           int n, hipStream_t st) {
+  const int H = ph->hidden, I = ph->inter, nk = ph->nk, kl = ph->kl, rl = ph->rl, R = ph->nv / nk;
+  const int nq = nk * kl, nvr = nk * rl * VD, nproj = 2 * nq + 2 * nvr + 2 * nk * rl;
+  const float eps = ph->rms_eps;
+  hipLaunchKernelGGL(pb_norm, dim3(n), dim3(NT), 0, st, pb->h, ly.ln_in, eps, H, GH, pb->xn);
+  for (int s = 0; s < n; s += PB)
+    launch_pb<GH, 8, 0>(ly.proj, nullptr, nproj, pb->xn + (int64_t)s * H, n - s < PB ? n - s : PB,
+                        pb->P + (int64_t)s * nproj, nproj, 0, st);
+  const PbGdn g{ly.conv_qk, ly.conv_v, ly.A_log, ly.dt_bias, ly.rec, ly.conv, pb->P, pb->qk,
+                pb->v, pb->g, pb->live, pb->o, nk, kl, rl, R, nproj, n, pb->gl};
+  hipLaunchKernelGGL(pb_prep, dim3(n, nk), dim3(KD), 0, st, g);
+  lxm_chunk_io io;
+  io.q = pb->qk;
+  io.k = pb->qk + KD;
+  io.v = pb->v;
+  io.beta = pb->g;
+  io.g = pb->gl;
+  io.S = ly.rec;
+  io.o = pb->o;
+  io.qk_ts = (int64_t)nk * 2 * KD;
+  io.qk_hs = 2 * KD;
+  io.v_ts = nvr;
+  io.g_ts = 2 * (int64_t)nk * rl;
+  io.g_hs = 2;
+  io.gl_ts = (int64_t)nk * rl;
+  io.o_ts = nvr;
+  io.n = n;
+  io.n_slots = nk * rl;
+  io.rl = rl;
+  io.rfull = R;
+  io.kl = kl;
+  io.o_bf16 = 1;
+  const int e = lxm_gdn_chunk(&io, st);
+  if (e) return (hipError_t)e;
+  hipLaunchKernelGGL(pb_gnorm, dim3(n), dim3(PBT), 0, st, pb->o, pb->P, nproj, 2 * nq + nvr,
+                     ly.gnorm, ph->geps, nk * rl, GV, pb->ys, ly.conv, n, nk, kl, rl, R);
+  for (int s = 0; s < n; s += PB)
+    launch_hrows<GV>(ly.out, H, pb->ys + (int64_t)s * nvr, n - s < PB ? n - s : PB,
+                     pb->h + (int64_t)s * H, H, st);
+  hipLaunchKernelGGL(pb_norm, dim3(n), dim3(NT), 0, st, pb->h, ly.ln_post, eps, H, GH, pb->xn);
+  for (int s = 0; s < n; s += PB)
+    launch_pb<GH, 4, 2>(ly.gate, ly.up, I, pb->xn + (int64_t)s * H, n - s < PB ? n - s : PB,
+                        pb->act + (int64_t)s * I, I, GI, st);
+  for (int s = 0; s < n; s += PB)
+    launch_hrows<GI>(ly.down, H, pb->act + (int64_t)s * I, n - s < PB ? n - s : PB,
+                     pb->h + (int64_t)s * H, H, st);
+  return hipGetLastError();
+}
+
+extern "C" int lxm_dn_prefill_chunked(const lxm_dn_params* ph, const int32_t* tokens, int T,
+                                      const lxm_dn_pbuf* pb, void* stream) {
+  if (!dims_ok(ph) || !pb || !pb->gl || !tokens || T < 0 || ph->kl > 128 || ph->kl % 16)
+    return (int)hipErrorInvalidValue;
+  const int gh = g_of(ph->hidden), gv = g_of(ph->nk * ph->rl * VD), gi = g_of(ph->inter);
+  const bool full = gh == 40 && gv == 64 && gi == 144, small = gh == 4 && gv == 8 && gi == 8;
+  if (!full && !small) return (int)hipErrorInvalidValue;
+  hipStream_t st = (hipStream_t)stream;
+  for (int b0 = 0; b0 < T; b0 += LXM_CHUNK) {
+    const int n = T - b0 < LXM_CHUNK ? T - b0 : LXM_CHUNK;
+    hipLaunchKernelGGL(pb_embed, dim3(n), dim3(PBT), 0, st, ph->embed, tokens + b0, ph->hidden,
+                       ph->vocab, pb->h, ph->err);
+    for (int L = 0; L < ph->n_layers; L++) {
+      const hipError_t e = full ? pc_layer<40, 64, 144>(ph, ph->layers_host[L], pb, n, st)
+                                : pc_layer<4, 8, 8>(ph, ph->layers_host[L], pb, n, st);
+      if (e != hipSuccess) return (int)e;
     }
   }
   return (int)hipGetLastError();

@@ -33,10 +33,11 @@ class DnLayer(ctypes.Structure):
 
 
 class DnPbuf(ctypes.Structure):
-    _fields_ = [(n, P64) for n in ("h", "xn", "P", "qk", "v", "g", "live", "o", "ys", "act")]
+    _fields_ = [(n, P64) for n in ("h", "xn", "P", "qk", "v", "g", "live", "o", "ys", "act", "gl")]
 
 
 PB = 16  # tokens per prefill batch (LXM_DN_PB)
+CHUNK = 64  # tokens per chunk of the chunked prompt (LXM_CHUNK)
 
 
 class DnParams(ctypes.Structure):
@@ -135,39 +136,52 @@ class DenseDecode:
         pd = torch.frombuffer(bytearray(bytes(p)), dtype=torch.uint8).to(self.dev)
         return p, pd
 
-    def _pbuf(self):
-        """The batched prefill's buffers (allocated on first use)."""
-        if self._pb is None:
-            sp, d = self.spec, self.dims
+    def _pbuf(self, chunked: bool = False):
+        """The prompt's buffers (allocated on first use): PB tokens for the batched prefill,
+        CHUNK tokens (and the log decays) for the chunked one."""
+        key = "_pbc" if chunked else "_pb"
+        if getattr(self, key, None) is None:
+            sp = self.spec
             H, nk, rl, I = sp.hidden, sp.nk, sp.r_live, sp.inter
             nvr = nk * rl * 128
             sizes = dict(h=H, xn=H, P=self.nproj, qk=nk * 2 * 256, v=nvr, g=nk * rl * 2,
                          live=nk * 2, o=nvr, ys=nvr, act=I)
+            if chunked:
+                sizes["gl"] = nk * rl
             bf = ("xn", "ys", "act")  # (the row kernels' inputs, bf16)
-            self._pb_t = {k: torch.zeros(PB * n, device=self.dev,
-                                         dtype=torch.bfloat16 if k in bf else torch.float32)
-                          for k, n in sizes.items()}
-            self._pb = DnPbuf(**{k: t.data_ptr() for k, t in self._pb_t.items()})
-        return self._pb
+            nt = CHUNK if chunked else PB
+            ts = {k: torch.zeros(nt * n, device=self.dev,
+                                 dtype=torch.bfloat16 if k in bf else torch.float32)
+                  for k, n in sizes.items()}
+            setattr(self, key + "_t", ts)
+            setattr(self, key, DnPbuf(**{k: t.data_ptr() for k, t in ts.items()}))
+        return getattr(self, key)
 
-    @torch.no_grad()
-    def prefill(self, tokens) -> None:
-        """The tokens through every layer without the head (lxm_dn_prefill, batches of PB tokens,
-        each weight row read once per batch): the cache's states and windows afterwards are those
-        of len(tokens) forced steps of run(), bit for bit; no predictions are made. A caller then
-        steps from the next token: run([next], n)."""
+    def prefill(self, tokens, mode: str = "batched") -> None:
+        """The tokens through every layer without the head; no predictions are made. A caller
+        then steps from the next token: run([next], n).
+
+        mode "batched" (lxm_dn_prefill: batches of PB tokens, each weight row read once per
+        batch): the cache's states and windows afterwards are those of len(tokens) forced steps
+        of run(), bit for bit. mode "chunked" (lxm_dn_prefill_chunked): the stock forward's
+        T > 1 path, the delta rule in chunks of 64 on the matrix cores
+        (torch_chunk_gated_delta_rule); every other sum as in "batched", the delta rule's outputs
+        and states those of the chunked form."""
+        if mode not in ("batched", "chunked"):
+            raise ValueError(f"prefill mode {mode!r}: 'batched' or 'chunked'")
         t = torch.as_tensor(tokens, dtype=torch.int64)
         if t.numel() == 0:
             return
         if int(t.min()) < 0 or int(t.max()) >= self.spec.vocab:
             raise ValueError("prefill token out of range")
-        pb = self._pbuf()
+        chunked = mode == "chunked"
+        pb = self._pbuf(chunked)
         tok = t.to(torch.int32).to(self.dev)
         self.err.zero_()
         p, _ = self._params(1)
         st = ctypes.c_void_p(torch.cuda.current_stream(self.dev).cuda_stream)
-        e = self.lib.lxm_dn_prefill(ctypes.byref(p), ctypes.c_void_p(tok.data_ptr()), int(t.numel()),
-                                    ctypes.byref(pb), st)
+        fn = self.lib.lxm_dn_prefill_chunked if chunked else self.lib.lxm_dn_prefill
+        e = fn(ctypes.byref(p), ctypes.c_void_p(tok.data_ptr()), int(t.numel()), ctypes.byref(pb), st)
         if e:
             raise RuntimeError(f"dense prefill launch failed: hipError {e}")
         torch.cuda.synchronize(self.dev)

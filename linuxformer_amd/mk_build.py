@@ -105,6 +105,8 @@ def load(subprof: bool = False) -> ctypes.CDLL:
         lib.lxm_dn_run.restype = I
         lib.lxm_dn_prefill.argtypes = [P, P, I, P, P]
         lib.lxm_dn_prefill.restype = I
+        lib.lxm_dn_prefill_chunked.argtypes = [P, P, I, P, P]
+        lib.lxm_dn_prefill_chunked.restype = I
         lib.lxm_gdn_chunk.argtypes = [P, P]
         lib.lxm_gdn_chunk.restype = I
         lib.lxm_t_sync.argtypes = [I, I, I, I, P, P, P, P]
@@ -116,4 +118,5 @@ def load(subprof: bool = False) -> ctypes.CDLL:
 EXPORTS = ("lxm_run", "lxm_lds_base", "lxm_helper_lds", "lxm_max_blocks", "lxm_max_lds",
            "lxm_last_error", "lxm_device_cus", "lxm_t_elem", "lxm_t_sum", "lxm_pf_layers",
            "lxm_pf_head", "lxm_pf_embed", "lxm_pf_tiles", "lxm_pf_lds", "lxm_dn_step", "lxm_dn_run",
-           "lxm_dn_prefill", "lxm_t_sync", "lxm_run_noalloc", "lxm_gdn_chunk")
+           "lxm_dn_prefill", "lxm_t_sync", "lxm_run_noalloc", "lxm_gdn_chunk",
+           "lxm_dn_prefill_chunked")

@@ -1,6 +1,7 @@
 """In-kernel cycle counters of the decode kernel (lx.mega's prof buffer and MK_SUBPROF build):
 
     python -m linuxformer_amd.profile --config c2 --tokens 4096 [--subprof]
+    python -m linuxformer_amd.profile --config c4 --tokens 1024 [--mode chunked|batched]
 
 Runs one launch of --tokens greedy steps from the config's start token and initial state with
 the phase counters on, and prints one JSON object: cycles per token of each chain phase
@@ -8,7 +9,11 @@ the phase counters on, and prints one JSON object: cycles per token of each chai
 helpers' mean and max cycles per token in each of their parts, and with --subprof (the library
 built with -DLXM_SUBPROF) each chain wave's busy and waiting cycles per layer in each stage.
 The counters are the chain's own clock cycle counter; `clock_mhz` is the chain's cycles per token
-over the launch's wall time per token (the launch's set-up included)."""
+over the launch's wall time per token (the launch's set-up included).
+
+--config c4 runs only config 4's prompt (--tokens seeded uniform ids from a zero state) through
+DenseDecode.prefill in the given mode, once to warm up and once timed: the process to put under
+rocprofv3 for the prompt's kernels (few enough dispatches for counter collection)."""
 
 from __future__ import annotations
 
@@ -24,10 +29,13 @@ from . import fast, mega, synth
 
 def main() -> int:
     ap = argparse.ArgumentParser()
-    ap.add_argument("--config", default="c2", choices=["c1", "c2", "c5", "small"])
+    ap.add_argument("--config", default="c2", choices=["c1", "c2", "c5", "small", "c4"])
     ap.add_argument("--tokens", type=int, default=4096)
     ap.add_argument("--subprof", action="store_true")
+    ap.add_argument("--mode", default="chunked", choices=["chunked", "batched"])
     a = ap.parse_args()
+    if a.config == "c4":
+        return dense_prompt(a.tokens, a.mode)
     spec = {"c1": synth.config1(), "c2": synth.config2(), "c5": synth.config5(),
             "small": synth.small()}[a.config]
     m = synth.build(spec)
@@ -51,6 +59,33 @@ def main() -> int:
     rep["config"] = spec.name
     rep["subprof"] = a.subprof
     print(json.dumps(rep))
+    return 0
+
+
+def dense_prompt(n: int, mode: str) -> int:
+    import numpy as np
+
+    from . import dense
+
+    spec = synth.config4()
+    dev = torch.device("cuda", 0)
+    dm = synth.build_dense(spec, "cuda")
+    d = dm.dims
+    toks = np.random.default_rng(spec.seed).integers(0, spec.vocab, n).tolist()
+    times = []
+    for _ in range(2):
+        conv0 = np.zeros((d.n_layers, d.n_conv, 4), np.float32)
+        rec0 = np.zeros((d.n_layers, d.nv, 256, 128), np.float32)
+        cache = fast.StateCache(conv0, rec0, "bf16", dev)
+        dd = dense.DenseDecode(dm, cache, max_steps=2)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        dd.prefill(toks, mode=mode)
+        torch.cuda.synchronize()
+        times.append(time.perf_counter() - t0)
+        del dd, cache
+    print(json.dumps({"config": "c4", "mode": mode, "tokens": n, "s": [round(x, 4) for x in times],
+                      "tok_s": round(n / times[-1], 1)}))
     return 0
 
 

@@ -752,3 +752,114 @@ int ox_chunk_gdr(int T, int K, int V, int C, const float* q, const float* k, con
   free(A); free(Dm); free(A2); free(U); free(W); free(kb); free(vb); free(qs); free(vn); free(Sn);
   return 0;
 }
+
+/* The stock forward over T tokens at once (transformers' T > 1 path, Qwen3_5GatedDeltaNet.forward
+   TF:454-543 with causal_conv1d_fn over the cached window and torch_chunk_gated_delta_rule in
+   chunks of C from the cached state), layer after layer, without the head: each position's norms,
+   projections, conv, l2norms, gated norm, out_proj and MLP are the decode step's; the delta rule
+   is ox_chunk_gdr per value head over the T positions, its fp32 outputs cast to the model dtype.
+   conv (n_layers, n_conv, conv) and rec (n_layers, nv, kd, vd) are updated in place; h (T, hidden)
+   holds the embedding rows on entry and the last layer's outputs on return; trace (optional,
+   T x n_layers x hidden) gets every layer's output. */
+void ox_prefill_chunked(const ox_model* m, float* conv, float* rec, float* h, int T, int C,
+                        float* trace) {
+  const ox_dims* d = &m->d;
+  g_bf16 = d->bf16;
+  const int H = d->hidden, K = d->conv, kd = d->kd, vd = d->vd, nk = d->nk, nv = d->nv;
+  const int R = nv / nk, NC = 2 * nk * kd + nv * vd, QK = 2 * nk * kd;
+  ox_ws w;
+  ws_init(&w, d);
+  float* hsq = xalloc(4 * (size_t)H);
+  float* XN = xalloc(4 * (size_t)T * H);          /* the input norm's output per position */
+  float* Y = xalloc(4 * (size_t)T * NC);          /* conv outputs */
+  float* Qn = xalloc(4 * (size_t)T * nk * kd);    /* l2-normed queries and keys, per key head */
+  float* Kn = xalloc(4 * (size_t)T * nk * kd);
+  float* G = xalloc(4 * (size_t)T * nv);
+  float* Bt = xalloc(4 * (size_t)T * nv);
+  float* O = xalloc(4 * (size_t)T * nv * vd);     /* the delta rule's outputs (model dtype) */
+  float* qh = xalloc(4 * (size_t)T * kd);
+  float* kh_ = xalloc(4 * (size_t)T * kd);
+  float* vh_ = xalloc(4 * (size_t)T * vd);
+  float* gh = xalloc(4 * (size_t)T);
+  float* bh = xalloc(4 * (size_t)T);
+  float* oh = xalloc(4 * (size_t)T * vd);
+  for (int L = 0; L < d->n_layers; L++) {
+    const ox_layer* ly = &m->layers[L];
+    float* cs = conv + (size_t)L * NC * K;
+    float* S = rec + (size_t)L * nv * kd * vd;
+    /* per position: norm, projections, conv (the windows shift in position order), gates */
+    for (int t = 0; t < T; t++) {
+      float* ht = h + (size_t)t * H;
+      rms_norm(ht, H, d->rms_eps, ly->ln_in, hsq, XN + (size_t)t * H);
+      csr_mv(&ly->qkv, XN + (size_t)t * H, w.P);
+      csr_mv(&ly->b, XN + (size_t)t * H, w.b);
+      csr_mv(&ly->a, XN + (size_t)t * H, w.a);
+      conv_channels(ly, cs, &w, 0, NC, NULL, K, 1);
+      memcpy(Y + (size_t)t * NC, w.y, 4 * (size_t)NC);
+      for (int v = 0; v < nv; v++) {
+        Bt[(size_t)t * nv + v] = D(ox_sigmoid(w.b[v]));
+        G[(size_t)t * nv + v] = (-ox_expf(ly->A_log[v])) * ox_softplus(w.a[v] + ly->dt_bias[v]);
+      }
+      for (int k = 0; k < nk; k++) { /* l2norm in the model dtype (zero stays zero) */
+        l2norm_D(w.y + (size_t)k * kd, kd, w.sq, Qn + ((size_t)t * nk + k) * kd);
+        l2norm_D(w.y + (size_t)(nk + k) * kd, kd, w.sq, Kn + ((size_t)t * nk + k) * kd);
+      }
+    }
+    /* the chunked delta rule per value head over the T positions */
+    for (int v = 0; v < nv; v++) {
+      const int k = v / R;
+      for (int t = 0; t < T; t++) {
+        memcpy(qh + (size_t)t * kd, Qn + ((size_t)t * nk + k) * kd, 4 * (size_t)kd);
+        memcpy(kh_ + (size_t)t * kd, Kn + ((size_t)t * nk + k) * kd, 4 * (size_t)kd);
+        memcpy(vh_ + (size_t)t * vd, Y + (size_t)t * NC + QK + (size_t)v * vd, 4 * (size_t)vd);
+        gh[t] = G[(size_t)t * nv + v];
+        bh[t] = Bt[(size_t)t * nv + v];
+      }
+      ox_chunk_gdr(T, kd, vd, C, qh, kh_, vh_, gh, bh, S + (size_t)v * kd * vd, oh);
+      for (int t = 0; t < T; t++)
+        for (int j = 0; j < vd; j++) O[((size_t)t * nv + v) * vd + j] = D(oh[(size_t)t * vd + j]);
+    }
+    /* per position: gated norm, out_proj, residual; the MLP */
+    for (int t = 0; t < T; t++) {
+      float* ht = h + (size_t)t * H;
+      const float* xn = XN + (size_t)t * H;
+      for (int v = 0; v < nv; v++) {
+        const float* o = O + ((size_t)t * nv + v) * vd;
+        float* on = w.on + (size_t)v * vd;
+        for (int j = 0; j < vd; j++) w.sq[j] = o[j] * o[j];
+        float ss = ox_sum_64(w.sq, vd);
+        float rr = ox_rsqrt(ss / (float)vd + d->gated_eps);
+        for (int j = 0; j < vd; j++) {
+          float zj = D(row_dot(&ly->z, v * vd + j, xn));
+          float t1 = D(o[j] * rr);
+          float t2 = D(ly->gnorm[j] * t1);
+          on[j] = D(t2 * ox_silu(zj));
+        }
+      }
+      csr_mv(&ly->out, w.on, w.out);
+      for (int i = 0; i < H; i++) ht[i] = D(ht[i] + w.out[i]);
+      rms_norm(ht, H, d->rms_eps, ly->ln_post, hsq, w.xn);
+      csr_mv(&ly->gate, w.xn, w.gt);
+      csr_mv(&ly->up, w.xn, w.up);
+      for (int u = 0; u < d->inter; u++) {
+        const float gt = w.gt[u];
+        w.act[u] = D(D(gt == 0.0f ? gt : ox_silu(gt)) * w.up[u]);
+      }
+      csr_mv(&ly->down, w.act, w.out);
+      for (int i = 0; i < H; i++) ht[i] = D(ht[i] + w.out[i]);
+      if (trace) memcpy(trace + ((size_t)t * d->n_layers + L) * H, ht, 4 * (size_t)H);
+    }
+  }
+  void* ps[] = {hsq, XN, Y, Qn, Kn, G, Bt, O, qh, kh_, vh_, gh, bh, oh};
+  for (size_t i = 0; i < sizeof(ps) / sizeof(ps[0]); i++) free(ps[i]);
+  ws_free(&w);
+}
+
+/* The embedding rows of tokens (T) into h (T, hidden); 0, or -1 on a token out of range. */
+int ox_embed(const ox_model* m, const int* tokens, int T, float* h) {
+  for (int t = 0; t < T; t++) {
+    if (tokens[t] < 0 || tokens[t] >= m->d.vocab) return -1;
+    embed_row(m, tokens[t], h + (size_t)t * m->d.hidden);
+  }
+  return 0;
+}

@@ -196,6 +196,24 @@ class OracleModel:
             raise ValueError("oracle: token id out of range")
         return preds, inputs, tr
 
+    def prefill_chunked(self, conv: np.ndarray, rec: np.ndarray, tokens, C: int = 64,
+                        trace: bool = False):
+        """The stock forward's T > 1 path over tokens (ox_prefill_chunked): conv/rec (float32
+        numpy) updated in place. Returns (every position's argmax, the last layer's outputs
+        (T, hidden), trace (T, n_layers, hidden) or None)."""
+        d = self.model.dims
+        assert conv.dtype == np.float32 and conv.flags.c_contiguous
+        assert rec.dtype == np.float32 and rec.flags.c_contiguous
+        t = np.ascontiguousarray(tokens, np.int32)
+        T = len(t)
+        h = np.zeros((T, d.hidden), np.float32)
+        if lib().ox_embed(ctypes.byref(self.c), _p(t), T, _p(h)):
+            raise ValueError("oracle: token id out of range")
+        tr = np.zeros((T, d.n_layers, d.hidden), np.float32) if trace else None
+        lib().ox_prefill_chunked(ctypes.byref(self.c), _p(conv), _p(rec), _p(h), T, C,
+                                 _p(tr) if trace else None)
+        return self.head(h), h, tr
+
     def layer_step(self, L: int, h: np.ndarray, conv_L: np.ndarray, rec_L: np.ndarray):
         """One layer's decode step on residual h (float32, updated in place)."""
         lib().ox_layer_step(ctypes.byref(self.c), L, _p(h), _p(conv_L), _p(rec_L))

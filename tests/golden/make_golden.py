@@ -128,12 +128,44 @@ def write_chunk(name: str, T: int, seed: int) -> None:
 CHUNK_CASES = {"chunk_fp32_100": (100, 11)}
 
 
+def write_prefill(name: str, base: str, T: int) -> None:
+    """The stock forward over T tokens at once (transformers' T > 1 path: causal_conv1d_fn and
+    torch_chunk_gated_delta_rule from the cached state) on the stack of fixture `base`: every
+    layer's output at every position, the argmax at every position, samples of the final states
+    (with their indices and the states' largest magnitudes)."""
+    m, conv0, rec0, _ = model_of(base)
+    hf = synth.to_hf(m)
+    toks = np.random.default_rng(3).integers(0, m.dims.vocab, T).astype(np.int64)
+    cache = stock.make_cache(hf, conv0, rec0)
+    h = hf.model.embed_tokens.weight[torch.from_numpy(toks)][None]
+    outs = stock.chip_forward(hf, h, cache)
+    trace = torch.stack([o[0].float() for o in outs], 1).numpy()
+    preds = stock.head_argmax(hf, outs[-1][0]).numpy().astype(np.int32)
+    L = m.dims.n_layers
+    conv = np.stack([cache.layers[k].conv_states[0][0].float().numpy() for k in range(L)])
+    rec = np.stack([cache.layers[k].recurrent_states[0][0].float().numpy() for k in range(L)])
+    rng = np.random.default_rng(1)
+    ridx = rng.integers(0, rec.size, 8192)
+    out = {"tokens": toks, "preds": preds, "trace": trace, "base": base, "conv": conv,
+           "rec_idx": ridx, "rec_sample": rec.reshape(-1)[ridx], "rec_max": np.float32(np.abs(rec).max()),
+           "rec_sha": sha_state(rec), "trace_sha": sha(trace)}
+    path = os.path.join(HERE, name + ".npz")
+    np.savez_compressed(path, **out)
+    print(name, os.path.getsize(path), "bytes", preds.tolist()[:8])
+
+
+PREFILL_CASES = {"small_fp32_pf100": ("small_fp32_32", 100), "small_bf16_pf100": ("small_bf16_32", 100)}
+
+
 def main():
     torch.set_grad_enabled(False)
-    names = sys.argv[1:] or list(CASES) + list(CHUNK_CASES)
+    names = sys.argv[1:] or list(CASES) + list(CHUNK_CASES) + list(PREFILL_CASES)
     for name in names:
         if name in CHUNK_CASES:
             write_chunk(name, *CHUNK_CASES[name])
+            continue
+        if name in PREFILL_CASES:
+            write_prefill(name, *PREFILL_CASES[name])
             continue
         _, n, full = CASES[name]
         m, conv0, rec0, start = model_of(name)

@@ -172,3 +172,78 @@ def test_dense_rejects_dead_state(cuda):
     cache = fast.StateCache(conv0, rec0, "bf16", "cuda")
     with pytest.raises(AssertionError):
         dense.DenseDecode(synth.dense_to(dm_cpu, "cuda"), cache)
+
+
+def check_prefill_chunked(T, n, seed=None, name="small"):
+    """lxm_dn_prefill_chunked over T - 1 tokens (the stock T > 1 path: chunks of 64, the delta
+    rule on the matrix cores), then n steps from the last token, against the oracle's restatement
+    of the same (ox_prefill_chunked, then ox_decode). The chunked delta rule sums in its own order
+    (MFMA tiles), so its outputs match the oracle's to about 1e-6 before they round to bf16: a
+    rare output rounds the other way and moves the residual by one bf16 step, which the later
+    layers carry. Bounds: the first layer's recurrent states (its inputs are the embeddings, so
+    only the delta rule's own arithmetic differs) within 1e-6 of each head's largest magnitude
+    (measured <= 2e-7; the oracle's recurrent and chunked forms differ by up to 9e-7); later
+    layers within 5e-3 (measured <= 9e-4; the oracle's two forms differ by up to 1.3e-3 there);
+    at least 99 % of the conv windows' values bit for bit (measured: all) and the rest within
+    2^-6 relative; the same greedy predictions."""
+    from oracle import oracle as ox
+
+    spec, dm_cpu, sm = model(name)
+    conv0, rec0 = synth.dense_state(dm_cpu, seed)
+    toks = [int(x) for x in np.random.default_rng(23 + T).integers(0, spec.vocab, T)]
+    print(f"[gpu-test] dense chunked prefill {spec.name}: T={T} n={n} seed={seed}", flush=True)
+    dm = synth.dense_to(dm_cpu, "cuda")
+    cache = fast.StateCache(conv0, rec0, "bf16", "cuda")
+    dd = dense.DenseDecode(dm, cache)
+    dd.prefill(toks[:-1], mode="chunked")
+    gc_, gr = cache.conv_numpy().copy(), cache.rec_numpy().copy()
+    preds = dd.run(toks[-1:], n)
+    om = ox.OracleModel(sm)
+    c, r = conv0.copy(), rec0.copy()
+    om.prefill_chunked(c, r, toks[:-1])
+    diff = bits(gc_) != bits(c)
+    assert diff.mean() <= 0.01, diff.mean()
+    assert (np.abs(gc_ - c) <= 2.0 ** -6 * np.abs(c)).all()
+    for L in range(r.shape[0]):
+        bound = 1e-6 if L == 0 else 5e-3
+        for h in range(r.shape[1]):
+            ref = np.abs(r[L, h]).max()
+            assert np.abs(gr[L, h] - r[L, h]).max() <= bound * max(ref, 1e-30), (L, h)
+    po, _, _ = om.decode(c, r, toks[-1:], n)
+    assert preds == po.tolist()
+    # the prompt moved the live heads' states (the chunked path ran)
+    assert not np.array_equal(gr, rec0)
+    return gr
+
+
+@pytest.mark.parametrize("T,seed", [(150, None), (66, 3), (20, 3)])
+def test_dense_prefill_chunked_small(cuda, T, seed):
+    """Chunks of 64 with a ragged last one, exactly one chunk plus a token, a prompt shorter than
+    one chunk; from zero and from live states."""
+    check_prefill_chunked(T, 6, seed=seed)
+
+
+def test_dense_prefill_chunked_full_widths(cuda):
+    check_prefill_chunked(70, 3, seed=5, name="mid")
+
+
+def test_dense_prefill_chunked_close_to_batched(cuda):
+    """The chunked and the batched (recurrent, bit-exact to forced steps) prompts on the same
+    tokens: the same states up to rounding: the first layer within 2e-6 of each head's largest
+    magnitude (the two forms' own arithmetic), the later ones within 5e-3 (rare bf16 outputs
+    rounding the other way, carried)."""
+    spec, dm_cpu, sm = model("small")
+    conv0, rec0 = synth.dense_state(dm_cpu, 3)
+    toks = [int(x) for x in np.random.default_rng(5).integers(0, spec.vocab, 100)]
+    dm = synth.dense_to(dm_cpu, "cuda")
+    out = []
+    for mode in ("batched", "chunked"):
+        cache = fast.StateCache(conv0, rec0, "bf16", "cuda")
+        dense.DenseDecode(dm, cache).prefill(toks, mode=mode)
+        out.append(cache.rec_numpy())
+    a, b = out
+    for L in range(a.shape[0]):
+        bound = 2e-6 if L == 0 else 5e-3
+        for h in range(a.shape[1]):
+            assert np.abs(a[L, h] - b[L, h]).max() <= bound * max(np.abs(a[L, h]).max(), 1e-30)
+    assert not np.array_equal(a, b)  # different forms, different roundings

@@ -382,3 +382,51 @@ def test_chunk_form_exact_regime_equals_recurrent(oracle_lib, C):
     assert (o.astype(np.float64) == orr).all()
     assert (S.astype(np.float64) == Sr).all()
     assert np.abs(orr).max() > 0 and (beta == 1).any() and (beta == 0).any()
+
+
+@pytest.mark.parametrize("name,tol", [("small_fp32_pf100", 1e-6), ("small_bf16_pf100", 0.0)])
+def test_oracle_prefill_chunked_matches_stock_T_gt_1(oracle_lib, name, tol):
+    """The oracle's restatement of the stock T > 1 forward (ox_prefill_chunked: the decode step's
+    arithmetic per position, the delta rule as torch_chunk_gated_delta_rule per value head)
+    against transformers' own forward over the same 100 tokens at once: the same argmax at every
+    position; every layer's output within tol of its row's largest magnitude (fp32: 1e-6; the
+    bf16 stack: bit for bit); final recurrent states within 1e-6 of their largest magnitude; the
+    final conv windows (the last projections) within 2e-6 of each window's largest magnitude in
+    fp32 (oneDNN's GEMM sums in its own order), and in bf16 bit for bit except values below
+    2^-40 (2 of 24,576: the host's flushing of denormal products)."""
+    from golden.make_golden import model_of
+
+    g = _load(name)
+    m, conv0, rec0, _ = model_of(str(g["base"]))
+    om = oracle_lib.OracleModel(m)
+    c, r = conv0.copy(), rec0.copy()
+    preds, _, tr = om.prefill_chunked(c, r, g["tokens"], trace=True)
+    assert preds.tolist() == g["preds"].tolist()
+    ref = g["trace"]
+    rel = np.abs(tr - ref).max(-1) / np.maximum(np.abs(ref).max(-1), 1e-30)
+    assert rel.max() <= tol, rel.max()
+    assert np.abs(r.reshape(-1)[g["rec_idx"]] - g["rec_sample"]).max() <= 1e-6 * float(g["rec_max"])
+    cr = g["conv"]
+    if tol:
+        crel = np.abs(c - cr).max(-1) / np.maximum(np.abs(cr).max(-1), 1e-30)
+        assert crel.max() <= 2e-6, crel.max()
+    else:
+        diff = bits(c) != bits(cr)
+        assert diff.sum() <= 4
+        assert np.maximum(np.abs(c[diff]), np.abs(cr[diff])).max(initial=0.0) < 2.0 ** -40
+
+
+def test_oracle_prefill_chunked_differs_from_forced_decode(oracle_lib):
+    """The two forms are different restatements: on the fp32 stack the chunked prefill's final
+    states differ from those of the same tokens as forced decode steps (by rounding only)."""
+    from golden.make_golden import model_of
+
+    g = _load("small_fp32_pf100")
+    m, conv0, rec0, _ = model_of(str(g["base"]))
+    om = oracle_lib.OracleModel(m)
+    c1, r1 = conv0.copy(), rec0.copy()
+    om.prefill_chunked(c1, r1, g["tokens"])
+    c2, r2 = conv0.copy(), rec0.copy()
+    om.decode(c2, r2, g["tokens"], len(g["tokens"]))
+    d = np.abs(r1 - r2).max() / np.abs(r2).max()
+    assert 0 < d < 1e-5
