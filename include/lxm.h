@@ -30,7 +30,9 @@ extern "C" {
 #define LXM_MAXQKL 512      /* live query/key channels of one layer */
 #define LXM_MAXDEC 512      /* decaying value heads of one layer */
 #define LXM_GATE_MAX 65536  /* bytes of the gate section (resident in the chain's LDS) */
-#define LXM_NSYNC 1024      /* uint32 words of the sync area */
+#define LXM_NSYNC 19456     /* uint32 words of the sync area (event words, per-writer stamps) */
+#define LXM_MAXBLOCKS 256   /* workgroups of a launch, at most (the chain and 255 helpers) */
+#define LXM_MAXVOCAB 524288 /* vocabulary rows, at most (a token index fits 19 bits) */
 #define LXM_OUT_MAX 1024    /* out_proj entries of the rows one helper workgroup computes */
 #define LXM_OUT_HELPERS 64  /* helper workgroups that compute out_proj's rows */
 #define LXM_OUT_ROWS 64     /* out_proj rows one of them computes, at most */
@@ -128,7 +130,7 @@ typedef struct lxm_params {
   float* rring;            /* (4, n_layers): their norm factors r */
   float* hn;               /* (hidden): the head's normed input, chain -> helpers */
   uint32_t* sync;          /* LXM_NSYNC words, zero at launch */
-  unsigned long long* keys;/* (2), zero at launch */
+  unsigned long long* keys;/* (2): reserved (the head's keys travel in the sync area) */
   int32_t* err;            /* (1), zero at launch; nonzero: a spin timed out (1..) */
   unsigned long long* prof; /* null, or 32 + 4 x n_blocks counters (phase cycles, see the kernel) */
   uint32_t* mb_task;       /* (nv): a GDN event's task per value head, chain -> helpers */
@@ -179,7 +181,7 @@ int lxm_t_sum(int kind, const float* x, int n, int rows, float* out, void* strea
    race, so issue them on one stream (or wait between them). */
 #define LXM_SCRATCH_MAXL 64
 #define LXM_SCRATCH_MAXNV 256
-#define LXM_SCRATCH_BYTES 4368128
+#define LXM_SCRATCH_BYTES 4441856
 int lxm_run_noalloc(const lxm_params* p_host, int n_blocks, int lds_bytes, void* stream);
 
 /* Cross-workgroup synchronisation costs, measured with the decode's own primitives (agent-scope

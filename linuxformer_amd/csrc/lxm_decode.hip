@@ -21,7 +21,8 @@
 //     rule, gated norm and output; then every helper computes a slice of out_proj's rows from
 //     all heads' outputs. The chain adds the rows to the residual.
 //   Cross-block data moves through agent-scope atomic loads and stores (sc1 on gfx950) and
-//   two monotone counters; a counter's target is known to every party, so nothing is reset.
+//   per-writer stamps (each workgroup stores the number of the event it has finished on a line of
+//   its own; the waiting workgroup reads all the lines at once), so nothing is reset.
 // * Gates instead of speculation: the chain computes, for each layer, the query/key channels'
 //   conv outputs and the decays first (a few rows), so it knows exactly whether the layer's
 //   delta rule runs and whether it can change the residual; the MLP is computed alongside and
@@ -81,7 +82,10 @@ static_assert(L_H + 4 * MAXH <= 65536, "gathered vectors below 64 KB");
 #define F_OUT 1
 #define F_OK 4
 #define F_TOK 8
+#define F_STOP 12
 #define F_KH 16
+#define F_KEYW 192  // 8 uint64: the head keys' wave maxima (key heads: nk <= F_KEYW - F_KH)
+static_assert((L_FLAGS + 4 * F_KEYW) % 8 == 0 && F_KEYW + 16 <= 256, "the key words in the flags");
 
 // LDS layout of a helper workgroup, before its head tables (p.head_lds bytes, from HX_END)
 #define HX_X 0                        // hidden: the head's normed input
@@ -100,15 +104,23 @@ static_assert(L_H + 4 * MAXH <= 65536, "gathered vectors below 64 KB");
 #define HX_OY (HX_OE + 8 * LXM_OUT_MAX)  // the head outputs each entry reads
 #define HX_END (HX_OY + 4 * LXM_OUT_MAX + 64)  // (reads run up to 3 slots past the end)
 
-// sync words (uint32 indices into p.sync). The event word and both counters have one copy per
-// group of helpers (group = block index mod 8, the XCD a block lands on when blocks are dealt
-// round-robin), each on its own 128-byte line, so at most 32 workgroups poll or count on one
-// line; a counter's value is the sum of its 8 copies.
+// sync words (uint32 indices into p.sync). The event word has one copy per group of helpers
+// (group = block index mod 8, the XCD a block lands on when blocks are dealt round-robin), each
+// on its own 128-byte line, so at most 32 workgroups poll one line. Completion travels as
+// stamps: every writer owns its own 128-byte line and stores the number of the event it has
+// finished (plain agent-scope stores, no atomics: counters that many workgroups add to
+// serialise at the coherence point), and the waiting workgroup reads all the lines at once, one
+// per thread, in one round trip per poll.
 #define NGRP 8
 #define S_EV 0       // + 32 g: seq << 8 | layer << 2 | out << 1 | kind (0 head, 1 gdn)
-#define S_CALL 256   // + 32 g: helpers done with an event (each helper, each event)
-#define S_CVH 512    // + 32 g: value-head helpers done with a GDN event's heads
 #define S_DONE 768
+#define S_OWN 1024   // + 32 vh: the number of GDN events whose output value head vh has stored
+#define S_XO (S_OWN + 32 * LXM_SCRATCH_MAXNV)  // + 32 j: the seq whose out_proj rows helper 1 + j stored
+#define S_KEY (S_XO + 32 * LXM_OUT_HELPERS)    // + 32 b (a uint64): helper b's head key, stamped
+#define S_END (S_KEY + 32 * LXM_MAXBLOCKS)
+static_assert(S_END == LXM_NSYNC, "LXM_NSYNC matches the layout");
+#define SEQ_MASK 0xffffffu   // an event's seq as its word carries it
+#define KEY_STAMP 0x1fffu    // the head key's stamp bits (the seq's low 13 bits)
 #define EV_GDN 1u
 #define EV_OUT 2u
 
@@ -131,7 +143,16 @@ __device__ __forceinline__ uint64_t cycles() { return __builtin_readcyclecounter
 // the stage's closing barrier (busy) and the cycles it then waits in the barrier (wait). The
 // counters follow the helpers' in p.prof: [32 + 4 n_blocks + 16 s + w] busy, [.. + 8 + w] wait.
 // GDN events, the embedding and the head are outside every stage (their time is skipped).
+// The same build also timestamps every GDN event on the 100 MHz wall clock (comparable across
+// workgroups): after the subprof slots, [0] the chain's sum of post times, [1] the sum of the
+// times it saw every helper done, [2] the number of events; then per helper b at 4 + 4 b: the
+// sums of the times it saw the event, had its value head's output stored (owners), saw every
+// head's output (out_proj helpers) and had its out_proj rows stored; then per helper b at
+// 4 + 4 n_blocks + 8 b: its value head's step, the sums of the times from its start to its
+// checkpoints (0 query/key in, 1 values/z/beta in, 2 state tile computed, 3 state stored, 4
+// output stored), the number of steps, the sum of whole steps that decayed, their number.
 #define SP_NS 4
+#define SP_EV (16 * SP_NS)
 #ifdef LXM_SUBPROF
 __device__ __forceinline__ uint64_t* sp_base() { return reinterpret_cast<uint64_t*>(smem + L_SUBP); }
 __device__ __forceinline__ void sp_arrive(int s) {
@@ -161,24 +182,6 @@ __device__ __forceinline__ void sp_depart(int) {}
 __device__ __forceinline__ void sp_skip() {}
 #endif
 
-// spin (one thread) until the sum of a counter's NGRP copies reaches target (modulo 2^32)
-__device__ bool spin_sum_ge(const uint32_t* p, uint32_t target, int32_t* err, int code) {
-  const uint64_t t0 = wall();
-  for (;;) {
-    uint32_t v[NGRP], sum = 0;
-#pragma unroll
-    for (int g = 0; g < NGRP; g++) v[g] = ld_rlx(p + 32 * g);
-#pragma unroll
-    for (int g = 0; g < NGRP; g++) sum += v[g];
-    if ((int32_t)(sum - target) >= 0) return true;
-    __builtin_amdgcn_s_sleep(2);
-    if (__hip_atomic_load(gp(err), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) return false;
-    if (wall() - t0 > TIMEOUT_TICKS) {
-      __hip_atomic_fetch_max(gp(err), code, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      return false;
-    }
-  }
-}
 // spin (one thread) until the word differs from last; 0 on timeout or another block's error
 __device__ bool spin_ne(const uint32_t* p, uint32_t last, uint32_t* out, int32_t* err, int code) {
   const uint64_t t0 = wall();
@@ -192,6 +195,75 @@ __device__ bool spin_ne(const uint32_t* p, uint32_t last, uint32_t* out, int32_t
     }
   }
   *out = v;
+  return true;
+}
+
+// The workgroup waits until every thread t < n sees the word base[32 t] equal to want, reading
+// all of them in each poll (one round trip for the lot); thread 0 watches the error word and the
+// time limit. All threads call; all return the same: false on an error or a timeout. stop: an
+// int in the caller's LDS.
+__device__ bool wait_stamps(const uint32_t* base, int n, uint32_t want, int32_t* err, int code,
+                            int* stop) {
+  const int t = threadIdx.x;
+  const uint64_t t0 = wall();
+  for (;;) {
+    const uint32_t v = t < n ? ld_rlx(base + 32 * t) : want;
+    int32_t e = 0;
+    if (t == 0) {
+      e = __hip_atomic_load(gp(err), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if (!e && wall() - t0 > TIMEOUT_TICKS) {
+        __hip_atomic_fetch_max(gp(err), code, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        e = code;
+      }
+      *stop = e != 0;
+    }
+    const int all = __syncthreads_and(v == want);
+    if (*stop) return false;
+    if (all) return true;
+    __builtin_amdgcn_s_sleep(1);
+  }
+}
+
+// The same for the head's keys: helper b = 1 .. n stores at S_KEY + 32 b a uint64 whose low 13
+// bits are the HEAD event's stamp; the workgroup waits for every stamp, then takes the largest
+// key (every valid key carries the same stamp, so the maximum is the maximum of the keys
+// themselves). Returns false on an error or a timeout; *best: the maximum.
+__device__ bool wait_keys(const uint32_t* sync, int n, uint32_t stamp, int32_t* err, int code,
+                          int* stop, unsigned long long* wk, unsigned long long* best) {
+  const int t = threadIdx.x;
+  const uint64_t t0 = wall();
+  unsigned long long k = 0;
+  for (;;) {
+    bool ok = true;
+    if (t >= 1 && t <= n) {
+      k = __hip_atomic_load(gp(reinterpret_cast<const unsigned long long*>(sync + S_KEY + 32 * t)),
+                            __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      ok = (uint32_t)(k & KEY_STAMP) == stamp;
+    }
+    int32_t e = 0;
+    if (t == 0) {
+      e = __hip_atomic_load(gp(err), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if (!e && wall() - t0 > TIMEOUT_TICKS) {
+        __hip_atomic_fetch_max(gp(err), code, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        e = code;
+      }
+      *stop = e != 0;
+    }
+    const int all = __syncthreads_and(ok);
+    if (*stop) return false;
+    if (all) break;
+    __builtin_amdgcn_s_sleep(1);
+  }
+  for (int off = 32; off >= 1; off >>= 1) {
+    const unsigned long long o = __shfl_xor(k, off, 64);
+    k = o > k ? o : k;
+  }
+  if ((t & 63) == 0) wk[t >> 6] = k;
+  __syncthreads();
+  unsigned long long m = wk[0];
+  for (int w = 1; w < NT / 64; w++) m = wk[w] > m ? wk[w] : m;
+  *best = m;
+  __syncthreads();
   return true;
 }
 
@@ -953,11 +1025,13 @@ __device__ __forceinline__ void gate_compute(const ChainK& k, const uint8_t* gt,
 
 // A GDN event for layer L (the chain's side): publish the value heads' tasks (bit 0 the key
 // head's query or key is live, bit 2 the head decays), their decays and the layer's live
-// query/key channel values; post the event; wait for every helper; add out_proj's rows
-// (already rounded) to the residual when a query was live. Returns false on an error.
+// query/key channel values; post the event; wait until the helpers have done it: with a live
+// query, until every out_proj helper has stored its rows (each had waited for every value
+// head's output), which the chain then adds to the residual (already rounded); without, until
+// every value head has stored its state. Returns false on an error.
 template <bool BF, bool E4>
 __device__ bool gdn_event(const lxm_params& p, int L, const uint8_t* gt, uint32_t& seq,
-                          uint32_t& target, v4f& ha, v4f& hb) {
+                          v4f& ha, v4f& hb) {
   const int t = threadIdx.x;
   const lxm_gate& hd = *reinterpret_cast<const lxm_gate*>(gt);
   int* flags = LI(L_FLAGS);
@@ -975,10 +1049,21 @@ __device__ bool gdn_event(const lxm_params& p, int L, const uint8_t* gt, uint32_
   seq++;
   if (t < NGRP)
     st_rlx(p.sync + S_EV + 32 * t, (seq << 8) | ((uint32_t)L << 2) | (out ? EV_OUT : 0u) | EV_GDN);
-  target += (uint32_t)(p.n_blocks - 1);
-  if (t == 0) flags[F_OK] = spin_sum_ge(p.sync + S_CALL, target, p.err, 4);
-  __syncthreads();
-  if (!flags[F_OK]) return false;
+#ifdef LXM_SUBPROF
+  const uint64_t tpost = wall();
+#endif
+  const int no = p.n_blocks - 1 < LXM_OUT_HELPERS ? p.n_blocks - 1 : LXM_OUT_HELPERS;
+  const bool ok = wait_stamps(p.sync + (out ? S_XO : S_OWN), out ? no : p.nv, seq & SEQ_MASK,
+                             p.err, 4, &flags[F_STOP]);
+#ifdef LXM_SUBPROF
+  if (t == 0 && p.prof) {
+    uint64_t* evs = reinterpret_cast<uint64_t*>(p.prof) + 32 + 4 * p.n_blocks + SP_EV;
+    evs[0] += tpost;
+    evs[1] += wall();
+    evs[2] += 1;
+  }
+#endif
+  if (!ok) return false;
   if (out) {  // (rows past H: xo holds +0 there, and so does h)
     const v4f xa = ld4_rlx(p.xo, 4 * t), xb = ld4_rlx(p.xo, 2048 + 4 * t);
     ha = v4f{rd<BF>(ha.x + xa.x), rd<BF>(ha.y + xa.y), rd<BF>(ha.z + xa.z), rd<BF>(ha.w + xa.w)};
@@ -1009,7 +1094,7 @@ __device__ __forceinline__ bool layer(const lxm_params& p, const ChainK& k, int 
                                       float ss, int par,
                                       v4f& ha, v4f& hb, typename Regions<E4>::RA& r1,
                                       typename Regions<E4>::RU& ru, typename Regions<E4>::RB& rdw,
-                                      const LtEnt* lnext, uint32_t& seq, uint32_t& target) {
+                                      const LtEnt* lnext, uint32_t& seq) {
   using RG = Regions<E4>;
   const int t = threadIdx.x, H = k.H;
   const LtEnt le = reinterpret_cast<const LtEnt*>(smem + L_LT)[L];
@@ -1048,7 +1133,7 @@ __device__ __forceinline__ bool layer(const lxm_params& p, const ChainK& k, int 
     c0 = c1;
   }
   if (flags[F_ANY]) {
-    if (!gdn_event<BF, E4>(p, L, gt, seq, target, ha, hb)) return false;
+    if (!gdn_event<BF, E4>(p, L, gt, seq, ha, hb)) return false;
     if (flags[F_OUT]) {  // h may have changed: the MLP again, on the new h
       ss = hidden_ss<BF>(ha, hb);
       const float r2 = norm_r(ss, H, hd.eps);
@@ -1172,7 +1257,7 @@ __device__ void run_chain(const lxm_params& pg) {
   const v4f wfa = *reinterpret_cast<const v4f*>(p.w1_final + 4 * t);
   const v4f wfb = *reinterpret_cast<const v4f*>(p.w1_final + 2048 + 4 * t);
   int tok = p.forced[0];
-  uint32_t seq = 0, target = 0;
+  uint32_t seq = 0;
   const uint32_t nh = (uint32_t)(p.n_blocks - 1);
   int par = 0;
   for (int i = 0; i < p.n_tokens; i++) {
@@ -1202,7 +1287,7 @@ __device__ void run_chain(const lxm_params& pg) {
     sp_skip();
     for (int L = 0; L < k.nl; L++) {
       const int Ln = L + 1 < k.nl ? L + 1 : 0;
-      if (!layer<BF, E4>(p, k, L, i, ss, par, ha, hb, r1, ru, rdw, lt + Ln, seq, target)) return;
+      if (!layer<BF, E4>(p, k, L, i, ss, par, ha, hb, r1, ru, rdw, lt + Ln, seq)) return;
       if constexpr (TR) trace_rows(p.trace + ((size_t)i * k.nl + L) * H, H, ha, hb);
       ss = sum512_take(LF(L_WSUM) + 8 * par);
       par ^= 1;
@@ -1221,26 +1306,25 @@ __device__ void run_chain(const lxm_params& pg) {
       pa[15] = c;
     }
     seq++;
-    target += nh;
     if (t < NGRP) st_rlx(p.sync + S_EV + 32 * t, seq << 8);
-    if (t == 0) {
-      bool ok = spin_sum_ge(p.sync + S_CALL, target, p.err, 1);
-      int pred = 0;
-      if (ok) {
-        const unsigned long long key = __hip_atomic_load(gp(p.keys + (i & 1)), __ATOMIC_RELAXED,
-                                                         __HIP_MEMORY_SCOPE_AGENT);
-        pred = argmax_idx(key);
-        __hip_atomic_store(gp(p.keys + ((i + 1) & 1)), 0ull, __ATOMIC_RELAXED,
-                           __HIP_MEMORY_SCOPE_AGENT);
-        p.preds[i] = pred;
-      }
-      flags[F_OK] = ok;
-      flags[F_TOK] = pred;
-      if (k.prof) {
-        const uint64_t c = cycles();
-        pa[7] += c - pa[15];
-        pa[15] = c;
-        pa[17] += 1;
+    {  // every helper's stamped key, then the first maximum
+      unsigned long long best = 0;
+      const bool ok = wait_keys(p.sync, (int)nh, seq & KEY_STAMP, p.err, 1, &flags[F_STOP],
+                                reinterpret_cast<unsigned long long*>(flags + F_KEYW), &best);
+      if (t == 0) {
+        int pred = 0;
+        if (ok) {
+          pred = argmax_idx19(best);
+          p.preds[i] = pred;
+        }
+        flags[F_OK] = ok;
+        flags[F_TOK] = pred;
+        if (k.prof) {
+          const uint64_t c = cycles();
+          pa[7] += c - pa[15];
+          pa[15] = c;
+          pa[17] += 1;
+        }
       }
     }
     __syncthreads();
@@ -1260,11 +1344,11 @@ __device__ void run_chain(const lxm_params& pg) {
 // ---------------------------------------------------------------------------------------------
 // The helpers.
 
-// HEAD: this helper's vocabulary rows against the final normed residual; its best key into the
-// token's atomicMax slot.
+// HEAD: this helper's vocabulary rows against the final normed residual; its best key, stamped
+// with the event's low bits, into its own slot (the chain reads every slot).
 template <bool BF, bool E4>
-__device__ void head_rows(const lxm_params& p, int step, const int32_t* lptr, const uint8_t* lent,
-                          int r0, int nr, uint8_t* hx) {
+__device__ void head_rows(const lxm_params& p, uint32_t stamp, const int32_t* lptr,
+                          const uint8_t* lent, int r0, int nr, uint8_t* hx) {
   const int t = threadIdx.x, H = p.hidden;
   float* hn = reinterpret_cast<float*>(hx + HX_X);
   unsigned long long* wk = reinterpret_cast<unsigned long long*>(hx + HX_BS);
@@ -1280,7 +1364,7 @@ __device__ void head_rows(const lxm_params& p, int step, const int32_t* lptr, co
   unsigned long long best = 0;
   for (int k = t; k < nr; k += NT) {
     const float v = rd<BF>(dot<BF, E4, 4, 0>(lent, lptr[k], lptr[k + 1] - lptr[k], hn));
-    const unsigned long long key = argmax_key(v, r0 + k);
+    const unsigned long long key = argmax_key19(v, r0 + k);
     best = key > best ? key : best;
   }
   for (int off = 32; off >= 1; off >>= 1) {
@@ -1291,8 +1375,8 @@ __device__ void head_rows(const lxm_params& p, int step, const int32_t* lptr, co
   __syncthreads();
   if (t == 0) {
     for (int w = 1; w < NW; w++) best = wk[w] > best ? wk[w] : best;
-    __hip_atomic_fetch_max(gp(p.keys + (step & 1)), best, __ATOMIC_RELAXED,
-                           __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_store(gp(reinterpret_cast<unsigned long long*>(p.sync + S_KEY + 32 * blockIdx.x)),
+                       best | stamp, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
 }
 
@@ -1314,6 +1398,16 @@ __device__ void gdn_head(const lxm_params& p, int L, int step, int vh, bool out,
   float* bs = reinterpret_cast<float*>(hx + HX_BS);
   int* misc = reinterpret_cast<int*>(hx + HX_MISC);
   float* y = p.ybuf + (size_t)vh * VD;
+#ifdef LXM_SUBPROF
+  // (the profiling build: wall-clock checkpoints of this step, summed per helper in LDS and
+  // written out at the launch's end)
+  uint64_t* gpr = p.prof ? reinterpret_cast<uint64_t*>(hx + HX_MISC + 64) : nullptr;
+  const uint64_t g0 = wall();
+#define GH_MARK(k) \
+  if (gpr && t == 0) gpr[k] += wall() - g0
+#else
+#define GH_MARK(k)
+#endif
   const uint32_t tf = ld_rlx(p.mb_task + vh);
   if (tf == 0) {  // the step leaves this head alone: state unchanged, output exactly 0
     if (out && t < VD) st_rlxf(y + t, 0.0f);
@@ -1324,6 +1418,12 @@ __device__ void gdn_head(const lxm_params& p, int L, int step, int vh, bool out,
   const lxm_layer ly = ldg(p.layers + L);
   const uint8_t* gtab = p.blob + ly.gate;
   const lxm_gate hd = ldg(reinterpret_cast<const lxm_gate*>(gtab));
+#ifdef LXM_SUBPROF
+  if (gpr && t == 0) {
+    gpr[5] += 1;
+    if (dec) gpr[7] += 1;
+  }
+#endif
   // this key head's dense query and key
   if (t < KD) {
     qd[t] = 0.0f;
@@ -1338,6 +1438,7 @@ __device__ void gdn_head(const lxm_params& p, int L, int step, int vh, bool out,
     }
   }
   __syncthreads();
+  GH_MARK(0);
   // l2norm in the model dtype: D(x * D(rsqrt(D(D(sum D(x*x)) + 1e-6)))); the query scaled by
   // 1/sqrt(256) in fp32 (:352-353). Without a live query or key both stay 0.
   if (wv < 2) {
@@ -1398,6 +1499,7 @@ __device__ void gdn_head(const lxm_params& p, int L, int step, int vh, bool out,
     }
   }
   __syncthreads();
+  GH_MARK(1);
   const int nq = misc[0], nk = misc[1];
   const float beta = __uint_as_float((uint32_t)misc[2]);
   // The state tile: thread (cg, rb) holds columns 4cg..4cg+3 of rows 16rb..16rb+15, i.e. one
@@ -1456,11 +1558,7 @@ __device__ void gdn_head(const lxm_params& p, int L, int step, int vh, bool out,
         }
       }
     }
-#pragma unroll
-    for (int i = 0; i < 16; i++) {
-      const int r = rb * 16 + i;
-      if (dec || kn[r] != 0.0f) S4[r * (VD / 4) + cg] = s[i];
-    }
+    GH_MARK(2);
     if (nq > 0) {
       v4f a = v4f{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
@@ -1483,7 +1581,15 @@ __device__ void gdn_head(const lxm_params& p, int L, int step, int vh, bool out,
         ob[t] = rd<BF>(o);
       }
     }
+    // the state's written rows, after the barriers above (a barrier waits for earlier stores);
+    // the caller's drain waits for them
+#pragma unroll
+    for (int i = 0; i < 16; i++) {
+      const int r = rb * 16 + i;
+      if (dec || kn[r] != 0.0f) S4[r * (VD / 4) + cg] = s[i];
+    }
   }
+  GH_MARK(3);
   if (!out) return;
   __syncthreads();
   // the gated norm on this value head (one wave), gate z: y = D(D(w * D(o * r)) * silu(z))
@@ -1503,17 +1609,22 @@ __device__ void gdn_head(const lxm_params& p, int L, int step, int vh, bool out,
       for (int j = lane; j < VD; j += 64) st_rlxf(y + j, 0.0f);
     }
   }
+  GH_MARK(4);
+#ifdef LXM_SUBPROF
+  if (gpr && t == 0 && dec) gpr[6] += wall() - g0;
+#endif
 }
+#undef GH_MARK
 
 // GDN, second part: out_proj rows ra..rb (all value heads' outputs, ascending dims, from +0),
-// rounded once, to p.xo.
+// rounded once, to p.xo. out_prep reads the rows' static tables into LDS (before the wait for
+// the heads' outputs); out_rows then reads the outputs the entries name and sums.
 template <bool BF, bool E4>
-__device__ void out_rows(const lxm_params& p, int L, int ra, int rb, uint8_t* hx) {
+__device__ int out_prep(const lxm_params& p, int L, int ra, int rb, uint8_t* hx) {
   const int t = threadIdx.x;
   int* op = reinterpret_cast<int*>(hx + HX_OP);
   uint8_t* oe = hx + HX_OE;
-  float* oy = reinterpret_cast<float*>(hx + HX_OY);
-  const lxm_layer ly = p.layers[L];
+  const lxm_layer ly = ldg(p.layers + L);
   const GAS int32_t* gptr = gp(reinterpret_cast<const int32_t*>(p.blob + ly.out_ptr));
   const int e0 = gptr[ra], ne = gptr[rb] - e0;  // the packer keeps ne <= LXM_OUT_MAX
   if (t <= rb - ra) op[t] = gptr[ra + t] - e0;
@@ -1523,9 +1634,22 @@ __device__ void out_rows(const lxm_params& p, int L, int ra, int rb, uint8_t* hx
     Ent<E4>::gat(p.blob + ly.out_ent, e0 + k, d, w);
     if constexpr (E4) reinterpret_cast<uint32_t*>(oe)[k] = (uint32_t)d | (__float_as_uint(w) & 0xffff0000u);
     else reinterpret_cast<uint2*>(oe)[k] = make_uint2((uint32_t)d, __float_as_uint(w));
+  }
+  return ne;
+}
+template <bool BF, bool E4>
+__device__ void out_rows(const lxm_params& p, int ra, int rb, int ne, uint8_t* hx) {
+  const int t = threadIdx.x;
+  int* op = reinterpret_cast<int*>(hx + HX_OP);
+  uint8_t* oe = hx + HX_OE;
+  float* oy = reinterpret_cast<float*>(hx + HX_OY);
+  for (int k = t; k < ne; k += NT) {
+    int d;
+    float w;
+    Ent<E4>::at(oe, k, d, w);
     oy[k] = ld_rlxf(p.ybuf + d);
   }
-  __syncthreads();
+  lds_barrier();
   if (t < rb - ra) {
     // the row's entries in order, four at a time (slots past the row weigh 0; oy is finite)
     const int a = op[t], n = op[t + 1] - a;
@@ -1578,7 +1702,11 @@ __device__ void run_helper(const lxm_params& p) {
   const int grp = b % NGRP;
   __syncthreads();
   uint64_t pr[4] = {0, 0, 0, 0};
-  uint32_t last = 0, ngdn = 0;
+#ifdef LXM_SUBPROF
+  if (t < 8) reinterpret_cast<uint64_t*>(hx + HX_MISC + 64)[t] = 0;
+  __syncthreads();
+#endif
+  uint32_t last = 0;
   int step = 0;
   while (step < p.n_tokens) {
     const uint64_t w0 = PROF_ON ? cycles() : 0;
@@ -1597,38 +1725,61 @@ __device__ void run_helper(const lxm_params& p) {
       pr[0] += w1 - w0;
     }
     if (!(w & EV_GDN)) {
-      head_rows<BF, E4>(p, step, lptr, lent, r0, nr, hx);
+      head_rows<BF, E4>(p, (w >> 8) & KEY_STAMP, lptr, lent, r0, nr, hx);
       if (PROF_ON) pr[1] += cycles() - w1;
       step++;
     } else {
+      // (a helper that is neither a value-head owner nor an out_proj helper has nothing to do,
+      // and may even miss a GDN event: only HEAD events need every helper)
       const int L = (int)((w >> 2) & 63);
       const bool out = (w & EV_OUT) != 0;
-      ngdn++;
+      const uint32_t seq = (w >> 8) & SEQ_MASK;
+#ifdef LXM_SUBPROF
+      uint64_t* evh = PROF_ON ? reinterpret_cast<uint64_t*>(p.prof) + 32 + 4 * p.n_blocks + SP_EV + 4 + 4 * b
+                              : nullptr;
+      if (evh && t == 0) evh[0] += wall();
+#endif
       if (owner) {
         gdn_head<BF, E4>(p, L, step, vh, out, hx);
         drain();
         __syncthreads();
-        if (t == 0) add_rlx(p.sync + S_CVH + 32 * grp, 1u);
+#ifdef LXM_SUBPROF
+        if (evh && t == 0) evh[1] += wall();
+#endif
+        if (t == 0) st_rlx(p.sync + S_OWN + 32 * vh, seq);
       }
       uint64_t w2 = 0;
       if (PROF_ON) {
         w2 = cycles();
         pr[2] += w2 - w1;
       }
-      if (out && rb > ra) {  // only the helpers with out_proj rows wait for every head
-        if (t == 0) misc[5] = spin_sum_ge(p.sync + S_CVH, (uint32_t)p.nv * ngdn, p.err, 5);
-        __syncthreads();
-        if (!misc[5]) return;
-        out_rows<BF, E4>(p, L, ra, rb, hx);
+      if (out && b <= no) {  // the out_proj helpers: every value head's output, then the rows
+        if (rb > ra) {
+          const int ne = out_prep<BF, E4>(p, L, ra, rb, hx);
+          if (!wait_stamps(p.sync + S_OWN, p.nv, seq, p.err, 5, &misc[6])) return;
+#ifdef LXM_SUBPROF
+          if (evh && t == 0) evh[2] += wall();
+#endif
+          out_rows<BF, E4>(p, ra, rb, ne, hx);
+          drain();
+          __syncthreads();
+        }
+#ifdef LXM_SUBPROF
+        if (evh && t == 0) evh[3] += wall();
+#endif
+        if (t == 0) st_rlx(p.sync + S_XO + 32 * (b - 1), seq);
       }
       if (PROF_ON) pr[3] += cycles() - w2;
     }
-    drain();
-    __syncthreads();
-    if (t == 0) add_rlx(p.sync + S_CALL + 32 * grp, 1u);
   }
   if (PROF_ON && t == 0)
     for (int k = 0; k < 4; k++) p.prof[32 + 4 * b + k] = pr[k];
+#ifdef LXM_SUBPROF
+  if (PROF_ON && t == 0)
+    for (int k = 0; k < 8; k++)
+      reinterpret_cast<uint64_t*>(p.prof)[32 + 8 * p.n_blocks + SP_EV + 4 + 8 * b + k] =
+          reinterpret_cast<const uint64_t*>(hx + HX_MISC + 64)[k];
+#endif
   if (t == 0) misc[5] = spin_ge(p.sync + S_DONE, 1u, p.err, 3);
   __syncthreads();
   if (misc[5]) __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
@@ -1794,14 +1945,22 @@ int lxm_lds_base(void) { return L_CHAIN_END; }
 
 int lxm_helper_lds(int head_lds) { return HX_END + head_lds + 256; }  // (reads past the tables)
 
+// the shapes the sync area and the stamped keys hold
+static bool launch_ok(const lxm_params* p, int n_blocks) {
+  return p && n_blocks >= 2 && n_blocks <= LXM_MAXBLOCKS && p->n_blocks == n_blocks &&
+         p->vocab <= LXM_MAXVOCAB && p->nv >= 1 && p->nv <= LXM_SCRATCH_MAXNV && p->nk >= 1 &&
+         p->nk <= F_KEYW - F_KH;
+}
+
 int lxm_run(const lxm_params* p_host, const lxm_params* p_dev, int n_blocks, int lds_bytes,
             void* stream) {
+  if (!launch_ok(p_host, n_blocks)) return (int)hipErrorInvalidValue;
   return (int)launch_decode(decode_fn(p_host), p_dev, n_blocks, lds_bytes, (hipStream_t)stream);
 }
 
 int lxm_run_noalloc(const lxm_params* p_host, int n_blocks, int lds_bytes, void* stream) {
-  if (!p_host || !p_host->err || p_host->n_layers < 1 || p_host->n_layers > LXM_SCRATCH_MAXL ||
-      p_host->nv < 1 || p_host->nv > LXM_SCRATCH_MAXNV || p_host->hidden > MAXH)
+  if (!launch_ok(p_host, n_blocks) || !p_host->err || p_host->n_layers < 1 ||
+      p_host->n_layers > LXM_SCRATCH_MAXL || p_host->hidden > MAXH)
     return (int)hipErrorInvalidValue;
   uint8_t* sc = nullptr;
   hipError_t e = scratch_ptr(&sc);

@@ -183,5 +183,14 @@ __device__ __forceinline__ unsigned long long argmax_key(float v, int idx) {
 __device__ __forceinline__ int argmax_idx(unsigned long long key) {
   return (int)(0xffffffffu - (uint32_t)(key & 0xffffffffull));
 }
+// the same order with the index in 19 bits (bits 13..31) and the low 13 bits free for a stamp:
+// (value, lower index) for indices below 2^19
+__device__ __forceinline__ unsigned long long argmax_key19(float v, int idx) {
+  const unsigned long long k = argmax_key(v, 0);
+  return (k & 0xffffffff00000000ull) | ((unsigned long long)(0x7ffffu - (uint32_t)idx) << 13);
+}
+__device__ __forceinline__ int argmax_idx19(unsigned long long key) {
+  return (int)(0x7ffffu - (uint32_t)((key >> 13) & 0x7ffffu));
+}
 
 }  // namespace lxm

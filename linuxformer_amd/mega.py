@@ -24,7 +24,7 @@ import torch
 from . import synth, chain, mk_build
 
 NT, MAXH, KD, VD, RMAX = 512, 4096, 256, 128, 8
-MAXU, MAXQK, MAXQKL, MAXDEC, GATE_MAX, NSYNC, OUT_MAX = 2048, 1024, 512, 512, 65536, 1024, 1024
+MAXU, MAXQK, MAXQKL, MAXDEC, GATE_MAX, NSYNC, OUT_MAX = 2048, 1024, 512, 512, 65536, 19456, 1024
 OUT_HELPERS, OUT_ROWS = 64, 64
 
 I32, I64, F32, PTR = ctypes.c_int32, ctypes.c_int64, ctypes.c_float, ctypes.c_void_p
@@ -190,6 +190,7 @@ class Mega:
         cus = int(self.lib.lxm_device_cus())
         self.ncta = ncta or cus
         assert self.ncta >= 2, "the decode needs the chain workgroup and at least one helper"
+        assert self.ncta <= 256, "at most 256 workgroups (the sync area's per-helper stamps)"
         nh = self.ncta - 1
         assert d.nv <= nh, "each value head needs its own helper workgroup"
         assert -(-d.hidden // min(nh, OUT_HELPERS)) <= OUT_ROWS, "too many out_proj rows per helper"
@@ -369,6 +370,8 @@ class Mega:
         assert self.lds <= maxlds, (self.lds, maxlds)
         assert int(self.lib.lxm_max_blocks(self.lds)) >= self.ncta, "the grid is not co-resident"
         self.vocab = V
+        assert V <= 1 << 19, "at most 2^19 vocabulary rows (the head keys carry a 19-bit index)"
+        assert d.nv <= 256 and d.nk <= 176, "value heads <= 256, key heads <= 176"
         # ---- run buffers (the library allocates nothing)
         self.ring = torch.zeros(4 * d.n_layers * MAXH, dtype=torch.float32, device=dev)
         self.rring = torch.zeros(4 * d.n_layers, dtype=torch.float32, device=dev)
@@ -395,7 +398,8 @@ class Mega:
 
     @property
     def prof_size(self) -> int:
-        return 32 + 4 * self.ncta + (16 * len(self.SUB_STAGES) if self.subprof else 0)
+        return 32 + 4 * self.ncta + (16 * len(self.SUB_STAGES) + 4 + 12 * self.ncta
+                                     if self.subprof else 0)
 
     def phase_report(self, prof: torch.Tensor) -> dict:
         """prof counters -> cycles per token of each chain phase, and the helpers' mean (and
@@ -416,6 +420,35 @@ class Mega:
                 wait = [round(c[base + 16 * s + 8 + w] / n / self.dims.n_layers) for w in range(8)]
                 out[f"per layer, {name}: busy by wave"] = busy
                 out[f"per layer, {name}: wait by wave"] = wait
+            ev = base + 16 * len(self.SUB_STAGES)
+            ne = c[ev + 2]
+            if ne:
+                post = c[ev] / ne  # mean wall-clock ticks (10 ns) of the events' posts
+                us = lambda x: round((x / ne - post) / 100.0, 3)  # noqa: E731
+                seen = [us(c[ev + 4 + 4 * b]) for b in range(1, self.ncta)]
+                own = [us(c[ev + 4 + 4 * b + 1]) for b in range(1, min(self.ncta, self.dims.nv + 1))]
+                outs = [b for b in range(1, self.ncta) if c[ev + 4 + 4 * b + 2]]
+                cvh = [us(c[ev + 4 + 4 * b + 2]) for b in outs]
+                odone = [us(c[ev + 4 + 4 * b + 3]) for b in outs]
+                out["GDN event timeline (us after the post, mean over events)"] = {
+                    "events": ne, "helpers saw it (mean, max)": [round(sum(seen) / len(seen), 3), max(seen)],
+                    "value head stored (mean, max)": [round(sum(own) / len(own), 3), max(own)] if own else None,
+                    "out_proj helpers saw every head (mean, max)": [round(sum(cvh) / len(cvh), 3), max(cvh)] if cvh else None,
+                    "out_proj rows stored (mean, max)": [round(sum(odone) / len(odone), 3), max(odone)] if odone else None,
+                    "chain saw every helper": us(c[ev + 1])}
+                gb = ev + 4 + 4 * self.ncta
+                rows = []
+                for b in range(1, min(self.ncta, self.dims.nv + 1)):
+                    g = c[gb + 8 * b: gb + 8 * b + 8]
+                    if g[5]:
+                        rows.append([round(g[k] / g[5] / 100.0, 2) for k in range(5)] +
+                                    [g[5], round(g[6] / max(g[7], 1) / 100.0, 2), g[7]])
+                if rows:
+                    worst = max(rows, key=lambda r: r[4])
+                    out["value head step (us from its start: q/k in, v/z/beta in, tile computed, "
+                        "state stored, output stored; steps; mean decaying step; decaying steps)"] = {
+                        "mean over heads": [round(sum(r[k] for r in rows) / len(rows), 2) for k in range(8)],
+                        "slowest head": worst}
         return out
 
     def _bufs(self) -> dict:

@@ -190,3 +190,22 @@ def test_config3_full_matches_decode_kernel(cuda):
     assert preds.tolist() == want
     assert (bits(cache2.conv_numpy()) == bits(conv_p)).all()
     assert (bits(cache2.rec_numpy()) == bits(rec_p)).all()
+
+
+def test_verify_matches_stock_T_gt_1_forward(cuda):
+    """Verified mode against the stock forward it names, transformers' T > 1 path (one forward
+    over all 100 tokens: causal_conv1d_fn and torch_chunk_gated_delta_rule from the cached
+    state; the committed fixture tests/golden/small_bf16_pf100.npz): the same argmax at every
+    position, and final recurrent states within 1e-6 of their largest magnitude (the chunked
+    and recurrent forms round apart by ~3e-7 there)."""
+    from golden.make_golden import model_of
+
+    g = dict(np.load(__import__("os").path.join(__import__("os").path.dirname(__file__), "golden",
+                                                "small_bf16_pf100.npz")))
+    m, conv0, rec0, _ = model_of(str(g["base"]))
+    print("[gpu-test] verify vs stock T>1: small_bf16_pf100", flush=True)
+    cache = fast.StateCache(conv0, rec0, m.dims.dtype, "cuda")
+    got = fast.Fast(m).verify([int(t) for t in g["tokens"]], cache).cpu().numpy()
+    assert got.tolist() == g["preds"].tolist()
+    r = cache.rec_numpy()
+    assert np.abs(r.reshape(-1)[g["rec_idx"]] - g["rec_sample"]).max() <= 1e-6 * float(g["rec_max"])
