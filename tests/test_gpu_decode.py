@@ -217,3 +217,35 @@ def test_config2_long_run_properties(cuda):
         touched.update(int(v) for v in f.dec[L]["decays"])
         idle = [v for v in range(m.dims.nv) if v not in touched]
         assert idle and (bits(rec[L][idle]) == bits(r0[L][idle])).all()
+
+
+def test_config2_whole_chunk_equals_oracle(cuda):
+    """BASELINE config 2's whole 262,144-token greedy chunk from its start token and initial
+    state, in four launches continuing one stream: the prediction stream and the final conv
+    windows and recurrent states hash to what the CPU oracle's run of the same chunk hashes
+    (tests/golden/c2_chunk.json, written by tests/golden/make_chunk.py; the reference pins its
+    boot the same way: lx/tools/mega_boot.py:74-75, lx/results/mega_boot.json's stream_sha256)."""
+    import hashlib
+    import json
+    import os
+
+    g = json.load(open(os.path.join(os.path.dirname(__file__), "golden", "c2_chunk.json")))
+    spec, m, conv0, rec0 = model("c2")
+    assert g["config"] == spec.name and g["start"] == synth.start_token(spec)
+    print(f"[gpu-test] c2 whole chunk: {g['chunk']} tokens", flush=True)
+    cache = fast.StateCache(conv0, rec0, m.dims.dtype, "cuda")
+    mg = mega.Mega(fast.Fast(m), m, cache, 0)
+    preds, tok = [], g["start"]
+    n = g["chunk"] // 4
+    for _ in range(4):
+        preds += mg.run([tok], n)
+        tok = preds[-1]
+        print(f"[gpu-test] c2 whole chunk: {len(preds)} tokens", flush=True)
+    assert preds[:256] == g["first_preds"] and preds[-16:] == g["last_preds"]
+    assert hashlib.sha256(np.asarray(preds, "<i4").tobytes()).hexdigest() == g["stream_sha256"]
+    hc, hr = hashlib.sha256(), hashlib.sha256()
+    for ly in cache.layers:
+        hc.update(ly.conv_states[0][0].float().cpu().numpy().tobytes())
+        hr.update((ly.recurrent_states[0][0].cpu().numpy() + np.float32(0.0)).tobytes())
+    assert hc.hexdigest() == g["conv_sha256"]
+    assert hr.hexdigest() == g["rec_sha256"]
