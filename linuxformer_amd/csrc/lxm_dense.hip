@@ -160,14 +160,17 @@ struct WRow {
   static_assert(G % 8 == 0 || G == 4, "16-byte weight loads (or 8)");
   static constexpr int N = G == 4 ? 1 : G / 8;
   v4u w[N];
+  // (global loads: a flat load would also count against the LDS counter, and an LDS barrier
+  // would then wait for the rows in flight)
   __device__ __forceinline__ void load(const uint16_t* W, int r, int lane) {
     const uint16_t* row = W + (int64_t)r * 64 * G;
     if constexpr (G == 4) {
-      const uint2 u = reinterpret_cast<const uint2*>(row)[lane];
+      typedef uint32_t v2u __attribute__((ext_vector_type(2)));
+      const v2u u = gp(reinterpret_cast<const v2u*>(row))[lane];
       w[0] = v4u{u.x, u.y, 0u, 0u};
     } else {
 #pragma unroll
-      for (int q = 0; q < N; q++) w[q] = reinterpret_cast<const v4u*>(row)[q * 64 + lane];
+      for (int q = 0; q < N; q++) w[q] = gp(reinterpret_cast<const v4u*>(row))[q * 64 + lane];
     }
   }
 };
@@ -589,8 +592,9 @@ struct DnOut {
   const float* P;
   int nk, kl;
 };
-// the gated norm of every live head into ys (nh x 128), the NWB waves taking heads in turn
-template <int NWB, bool COH>
+// the gated norm of every live head into ys (nh x 128), the NWB waves taking heads in turn (SZ:
+// a.z holds silu(z) already, fp32, as the persistent run's projections store it)
+template <int NWB, bool COH, bool SZ = false>
 __device__ __forceinline__ void gated_norm(const DnOut& a, float* ys) {
   const int lane = tid() & 63, wvl = tid() >> 6;
   // the wave's heads wvl, wvl + NWB, ...: every input requested first, then the norms
@@ -616,8 +620,9 @@ __device__ __forceinline__ void gated_norm(const DnOut& a, float* ys) {
       ss = ss + o[j][1] * o[j][1];
       ss = sum64(ss);
       const float rr = rsqrt_(ss / (float)VD + a.geps);
-      ys[hh * VD + lane] = bf16r(bf16r(g0 * bf16r(o[j][0] * rr)) * silu(z[j][0]));
-      ys[hh * VD + lane + 64] = bf16r(bf16r(g1 * bf16r(o[j][1] * rr)) * silu(z[j][1]));
+      const float s0 = SZ ? z[j][0] : silu(z[j][0]), s1 = SZ ? z[j][1] : silu(z[j][1]);
+      ys[hh * VD + lane] = bf16r(bf16r(g0 * bf16r(o[j][0] * rr)) * s0);
+      ys[hh * VD + lane + 64] = bf16r(bf16r(g1 * bf16r(o[j][1] * rr)) * s1);
     }
   }
 }
@@ -649,19 +654,33 @@ __global__ __launch_bounds__(NTB) void dn_out(DnOut a) {
 }
 
 // ---------------------------------------------------------------------------------------------
-// The persistent run: n steps in one launch of one workgroup per CU. Per step: the embedding,
-// per layer five phases (projections over the input norm; the delta rule in nk x rl x QC
-// workgroups; the gated norm, out_proj and the query/key windows; SwiGLU over the post norm;
-// down_proj), the head over the final norm, then every workgroup reads the argmax key. A phase
-// ends at a grid barrier: each wave drains its stores (agent-scope, coherent across the XCDs),
-// the workgroup arrives on a monotone counter, requests its waves' first rows of the next phase,
-// and waits for the count (a wave past a phase's last row requests the last row, unused). The
-// rows past the first round go where the previous phase left the least work: out_proj's to the
-// upper half of the waves (the lower half ran the delta rule), SwiGLU's to the lower half,
-// down_proj's to the upper half, the projections' to the lower half. The
-// head's keys alternate between two slots by step parity (the other slot is cleared for the next
-// step). Every wait gives up after 3 s with the error word set (code 2), and so do the other
-// workgroups on seeing it.
+// The persistent run: n steps in one launch of one workgroup per CU. Per step, per layer five
+// phases (the projections over the input norm; the delta rule in nk x rl x QC workgroups; the
+// gated norm, out_proj and the query/key windows; SwiGLU over the post norm; down_proj), then
+// the head over the final norm. A phase ends at a grid barrier: each wave drains its stores
+// (agent-scope, coherent across the XCDs) and the workgroup arrives on a monotone counter.
+//
+// Each workgroup's wave 0 is its control wave: it holds no weight rows. It polls the barriers
+// and stages each row phase's input in LDS: h and the norm's weight (every wave then forms the
+// norm from LDS in the 512-lane order), or down_proj's input and the residual. Waves 1-7 stream
+// the weight rows: right after a phase's arrival each requests its rows of the next phase (the
+// first D; each later one as the row before it in its slot has been summed), which then stream
+// from HBM while the barrier and the input complete. A vector memory counter counts every load
+// of a wave in order, so a wave with rows in flight must not load anything else it has to wait
+// for: the stream waves read their inputs and residuals from LDS only, and the layer tables
+// come through scalar loads. The delta rule runs on all 8 waves of its workgroups; out_proj's
+// rows go to the stream waves of the other workgroups, which request them before the delta rule
+// (they have landed when its gated norm, formed by all 8 waves, is ready). The projections store
+// silu(z) for the gated norm's z rows; SwiGLU stores its bf16 outputs in down_proj's interleaved
+// input order.
+// (Measured on MI355X: a CU's vector memory requests are served in order, so the control wave's
+// polls and input loads wait behind the rows its CU requested at the arrival; a phase boundary
+// costs about that burst's time at the CU's share of HBM bandwidth, 4-11 us.)
+//
+// The step's embedding row becomes h through LDS in the control wave (workgroup 0 also writes
+// it to h for the residual). The head's keys alternate between two slots by step parity (the
+// other slot is cleared for the next step). Every wait gives up after 3 s with the error word set
+// (code 2), and so do the other workgroups on seeing it.
 // The counter has 8 copies 128 bytes apart (workgroup b adds to copy b % 8, the XCD it lands on
 // when workgroups are dealt round-robin), so at most 32 workgroups' atomics meet on one line; a
 // waiter polls the sum. (One shared counter measured 3.9 us per barrier of 256 workgroups on
@@ -711,137 +730,511 @@ struct Bar {
   }
 };
 
+// h (n values, written by other workgroups) into LDS: thread t copies the values of its share
+// of the 512-lane order (4t..4t+3, 2048 + 4t..)
+__device__ __forceinline__ void stage_h(const float* h, int n, float* hs) {
+  const int t = tid();
+#pragma unroll
+  for (int half = 0; half < 2; half++) {
+    const int c = half * 2048 + 4 * t;
+    if (c < n) *reinterpret_cast<v4f*>(hs + c) = ldf4<true>(h, c);
+  }
+}
+
+// A stream wave's weight rows of one phase in flight: round j's row (round_row) in slot j % D.
+// The first D are requested by prefetch (right after the arrival ahead of the phase), each later
+// one when the row before it in its slot has been summed. prefetch fills every slot (a slot past
+// the wave's last row requests its first row again, a cache hit), so no slot's old contents stay
+// live from one phase to the next.
+__device__ __forceinline__ int slot_row(int w0, int s, int nw, int rot, int n) {
+  const int r = round_row(w0, s, nw, rot);
+  return r < n ? r : min(w0, n - 1);
+}
+template <int G, int D>
+struct RowSet {
+  WRow<G> w[D];
+  __device__ __forceinline__ void prefetch(const uint16_t* W, int nrows, int w0, int nw, int rot) {
+#pragma unroll
+    for (int s = 0; s < D; s++) w[s].load(W, slot_row(w0, s, nw, rot, nrows), tid() & 63);
+  }
+};
+// the number of rows round_row deals to the wave w0 (of nw) out of nrows
+__device__ __forceinline__ int rows_of(int w0, int nw, int rot, int nrows) {
+  return w0 < nrows ? 1 + (nrows - (w0 + rot) % nw - 1) / nw : 0;
+}
+// A wave's n rows in rounds of D slots: while a round is not the last, each slot's row is summed
+// and the slot then requests its row D rounds on (clamped to the wave's last row: the last full
+// round's surplus requests hit the cache); the last round sums the rows left, with no requests.
+// emit(s, r): row r's sum (lane 0 holds it) from slot s.
+template <int D, class Dot, class Load, class Emit>
+__device__ __forceinline__ void pipe(int n, int w0, int nw, int rot, Dot&& dot, Load&& load,
+                                     Emit&& emit) {
+  int j0 = 0;
+  for (; j0 + D < n; j0 += D) {
+#pragma unroll
+    for (int s = 0; s < D; s++) {
+      const int r = round_row(w0, j0 + s, nw, rot);
+      dot(s, r);
+      // (the slot's next row is requested after its sums have read it: one copy per slot)
+      __builtin_amdgcn_sched_barrier(0);
+      load(s, round_row(w0, min(j0 + s + D, n - 1), nw, rot));
+      emit(s, r);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  }
+#pragma unroll
+  for (int s = 0; s < D; s++) {
+    if (j0 + s < n) {
+      const int r = round_row(w0, j0 + s, nw, rot);
+      dot(s, r);
+      emit(s, r);
+    }
+  }
+}
+// the wave's rows: MODE 0 out[r] = D(row . x); MODE 1 out[r] = D(hs[r] + D(row . x)), hs the
+// staged residual; MODE 2 as 0, silu of it for the rows [zlo, zhi) (the gated norm's z)
+template <int G, int D, int MODE, class X>
+__device__ __forceinline__ void pipe_rows(RowSet<G, D>& rs, const uint16_t* W, int nrows,
+                                          const X& xc, int w0, int nw, int rot, float* out,
+                                          const float* hs, int zlo = 0, int zhi = 0) {
+  float v = 0.0f;
+  pipe<D>(
+      rows_of(w0, nw, rot, nrows), w0, nw, rot, [&](int s, int r) { v = row_dot<G>(rs.w[s], xc); },
+      [&](int s, int r) { rs.w[s].load(W, r, tid() & 63); },
+      [&](int s, int r) {
+        if ((tid() & 63) == 0) {
+          if constexpr (MODE == 1) {
+            stf<true>(out + r, bf16r(hs[r] + bf16r(v)));
+          } else {
+            const float y = bf16r(v);
+            stf<true>(out + r, MODE == 2 && r >= zlo && r < zhi ? silu(y) : y);
+          }
+        }
+      });
+}
+// SwiGLU units the same way (gate and up rows of unit u in slot j % D): act[u] =
+// D(D(silu(D(g))) * D(u)) (TF:704-717), stored as bf16 at act16[pos(u)]: down_proj's interleaved
+// input order (GI entries per lane)
+template <int G, int D>
+struct UnitSet {
+  WRow<G> g[D], u[D];
+  __device__ __forceinline__ void prefetch(const uint16_t* Wg, const uint16_t* Wu, int n, int w0,
+                                           int nw, int rot) {
+#pragma unroll
+    for (int s = 0; s < D; s++) {
+      const int r = slot_row(w0, s, nw, rot, n);
+      g[s].load(Wg, r, tid() & 63);
+      u[s].load(Wu, r, tid() & 63);
+    }
+  }
+};
+// entry c of a row whose lanes hold G entries each, in the interleaved order: its halfword
+__device__ __forceinline__ int il_pos(int c, int G) {
+  const int l = c / G, k = c % G;
+  return ((k >> 3) * 64 + l) * 8 + (k & 7);
+}
+template <int G, int GI, int D>
+__device__ __forceinline__ void pipe_units(UnitSet<G, D>& us, const uint16_t* Wg,
+                                           const uint16_t* Wu, int n, const XRegs<G>& xc, int w0,
+                                           int nw, int rot, uint16_t* act16) {
+  float g = 0.0f, v = 0.0f;
+  pipe<D>(
+      rows_of(w0, nw, rot, n), w0, nw, rot,
+      [&](int s, int r) {
+        g = row_dot<G>(us.g[s], xc);
+        v = row_dot<G>(us.u[s], xc);
+      },
+      [&](int s, int r) {
+        us.g[s].load(Wg, r, tid() & 63);
+        us.u[s].load(Wu, r, tid() & 63);
+      },
+      [&](int s, int r) {
+        if ((tid() & 63) == 0) {
+          const float a = bf16r(silu_bf16(bf16r(g)) * bf16r(v));
+          __hip_atomic_store(gp(act16 + il_pos(r, GI)), (uint16_t)(fbits(a) >> 16),
+                             __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+      });
+}
+// The head's rows w0, w0 + nw, ... (slot j % D): logits D(row . x), the wave's first maximum
+// (ties to the lower index, NaN above everything: torch.argmax) folded into *keys by 64-bit
+// atomic max.
+template <int G, int D>
+__device__ __forceinline__ void pipe_head(RowSet<G, D>& rs, const uint16_t* W, int nrows,
+                                          const XRegs<G>& xc, int w0, int nw,
+                                          unsigned long long* keys) {
+  float best = 0.0f, v = 0.0f;
+  int bidx = -1, nanr = -1;
+  pipe<D>(
+      rows_of(w0, nw, 0, nrows), w0, nw, 0,
+      [&](int s, int r) { v = bf16r(row_dot<G>(rs.w[s], xc)); },
+      [&](int s, int r) { rs.w[s].load(W, r, tid() & 63); },
+      [&](int s, int r) {
+        if (v != v) {
+          if (nanr < 0) nanr = r;
+        } else if (bidx < 0 || v > best) {
+          best = v;
+          bidx = r;
+        }
+      });
+  if ((tid() & 63) == 0) {
+    unsigned long long k = bidx < 0 ? 0ull : argmax_key(best, bidx);
+    if (nanr >= 0) {
+      const unsigned long long kn = argmax_key(__builtin_nanf(""), nanr);
+      k = kn > k ? kn : k;
+    }
+    if (k) atomicMax(keys, k);
+  }
+}
+
+// a layer's table through scalar loads (it never changes during a run; vector or flat loads
+// would wait for every weight row the wave has in flight). Field by field: a struct copy is
+// lowered to flat loads.
+__device__ __forceinline__ lxm_dn_layer layer_of(const lxm_dn_layer* t, int L) {
+  const __attribute__((address_space(4))) lxm_dn_layer* q =
+      (const __attribute__((address_space(4))) lxm_dn_layer*)t + L;
+  lxm_dn_layer y;
+  y.proj = q->proj;
+  y.conv_qk = q->conv_qk;
+  y.conv_v = q->conv_v;
+  y.A_log = q->A_log;
+  y.dt_bias = q->dt_bias;
+  y.gnorm = q->gnorm;
+  y.ln_in = q->ln_in;
+  y.ln_post = q->ln_post;
+  y.out = q->out;
+  y.gate = q->gate;
+  y.up = q->up;
+  y.down = q->down;
+  y.rec = q->rec;
+  y.conv = q->conv;
+  return y;
+}
+
+// The control wave's share of a hidden vector of n <= 4096 values in the 512-lane order: lane l,
+// slot m < M holds the 4 values at 256 m + 4 l (thread t = 64 (m % 8) + l's values 4t.. for
+// m < 8, its values 2048 + 4t.. for m >= 8).
+template <int M>
+struct HVec {
+  v4f v[M];
+  // from a vector other workgroups write (agent scope)
+  __device__ __forceinline__ void load_coh(const float* x, int n) {
+#pragma unroll
+    for (int m = 0; m < M; m++) {
+      const int c = 256 * m + 4 * (tid() & 63);
+      v[m] = c < n ? ldf4<true>(x, c) : v4f{0.0f, 0.0f, 0.0f, 0.0f};
+    }
+  }
+  // from a constant vector (a norm's weight)
+  __device__ __forceinline__ void load(const float* x, int n) {
+#pragma unroll
+    for (int m = 0; m < M; m++) {
+      const int c = 256 * m + 4 * (tid() & 63);
+      v[m] = c < n ? *gp(reinterpret_cast<const v4f*>(x + c)) : v4f{0.0f, 0.0f, 0.0f, 0.0f};
+    }
+  }
+  __device__ __forceinline__ void load_lds(const float* hs, int n) {
+#pragma unroll
+    for (int m = 0; m < M; m++) {
+      const int c = 256 * m + 4 * (tid() & 63);
+      v[m] = c < n ? *reinterpret_cast<const v4f*>(hs + c) : v4f{0.0f, 0.0f, 0.0f, 0.0f};
+    }
+  }
+  __device__ __forceinline__ void store_lds(float* hs, int n) const {
+#pragma unroll
+    for (int m = 0; m < M; m++) {
+      const int c = 256 * m + 4 * (tid() & 63);
+      if (c < n) *reinterpret_cast<v4f*>(hs + c) = v[m];
+    }
+  }
+};
+// rows in flight per stream wave: the projections' and the head's (GH entries per lane),
+// out_proj's, SwiGLU's units, down_proj's
+#define D_P 3
+#define D_O 2
+#define D_U 2
+#define D_D 2
+
+// the shared memory of the persistent run
 template <int GH, int GV, int GI>
-__global__ __launch_bounds__(NT, 1) void dn_run(const lxm_dn_params* __restrict__ pp, int n_run) {
-  static_assert(GV * 64 <= 4096, "at most 32 live value heads");
-  __shared__ float wsum[NW];
-  __shared__ __align__(16) float ys[GV * 64];
-  __shared__ GdnLds gl;
-  __shared__ v4u xd[8 * GI];
-  __shared__ int flag;
-  const lxm_dn_params& p = *pp;  // (scalar loads: the block never changes)
-  // (the thread's LANE and the wave's global index come from tid() at each use: see tid())
-  const int b = blockIdx.x, nb = gridDim.x, nwv = nb * NW;
-#define LANE (tid() & 63)
-#define GW (b * NW + wave_id())
-  const int H = p.hidden, I = p.inter, nk = p.nk, kl = p.kl, rl = p.rl, R = p.nv / nk;
-  const int nq = nk * kl, nvr = nk * rl * VD, nproj = 2 * nq + 2 * nvr + 2 * nk * rl;
-  const int ngdn = nk * rl * QC;
-  const float eps = p.rms_eps;
-  float* const act = p.xn + H;
-  Bar bar{p.sync, p.err, 0u, nb, &flag};
-  const int step0 = *p.step;
+struct RunLds {
+  float hs[4096];                 // a staged hidden vector (a norm's input, the residual)
+  float ws[4096];                 // a staged norm weight
+  float wsum[NW];
+  float ys[GV * 64];              // the gated norm's output
+  v4u xd[8 * GI];                 // down_proj's bf16 input, interleaved
+  GdnLds gl;
+  int flag;
+};
+
+// The run's shared state (scalar)
+struct RunCtx {
+  const lxm_dn_params* pp;
+  int H, I, nk, kl, rl, R, nq, nvr, nproj, ngdn, nL, nit, step0;
+  float eps;
+};
+__device__ __forceinline__ RunCtx run_ctx(const lxm_dn_params* pp, int n_run) {
+  const lxm_dn_params& p = *pp;
+  RunCtx c;
+  c.pp = pp;
+  c.H = p.hidden;
+  c.I = p.inter;
+  c.nk = p.nk;
+  c.kl = p.kl;
+  c.rl = p.rl;
+  c.R = p.nv / p.nk;
+  c.nq = c.nk * c.kl;
+  c.nvr = c.nk * c.rl * VD;
+  c.nproj = 2 * c.nq + 2 * c.nvr + 2 * c.nk * c.rl;
+  c.ngdn = c.nk * c.rl * QC;
+  c.nL = p.n_layers;
+  c.nit = n_run * (c.nL + 1);
+  c.step0 = *p.step;
+  c.eps = p.rms_eps;
+  return c;
+}
+__device__ __forceinline__ DnGdn gdn_of(const lxm_dn_params& p, const lxm_dn_layer& ly,
+                                        const RunCtx& c) {
+  return DnGdn{ly.conv_qk, ly.conv_v, ly.A_log, ly.dt_bias, ly.rec, ly.conv, p.P, p.on,
+               c.nk, c.kl, c.rl, c.R};
+}
+__device__ __forceinline__ DnOut out_of(const lxm_dn_params& p, const lxm_dn_layer& ly,
+                                        const RunCtx& c) {
+  return DnOut{ly.out, c.H, c.nk * c.rl, p.on, p.P + 2 * c.nq + c.nvr, ly.gnorm, p.geps, p.h,
+               ly.conv, p.P, c.nk, c.kl};
+}
+// the delta rule phase (both roles; all 8 waves of the delta rule's workgroups)
+template <int GH, int GV, int GI>
+__device__ __forceinline__ bool gdn_phase(const lxm_dn_params& p, const lxm_dn_layer& ly,
+                                          const RunCtx& c, Bar& bar, RunLds<GH, GV, GI>& sm) {
+  const DnGdn g = gdn_of(p, ly, c);
+  float s[16];
+  gdn_load<true>(g, blockIdx.x, s);
+  if (!bar.wait()) return false;
+  gdn_body<true>(g, blockIdx.x, s, sm.gl);
+  bar.arrive();
+  return bar.wait();
+}
+
+// The control wave's loop (wave 0)
+template <int GH, int GV, int GI>
+__device__ __forceinline__ void run_ctl(const lxm_dn_params* pp, int n_run,
+                                        RunLds<GH, GV, GI>& sm) {
+  constexpr int M = (64 * GH + 255) / 256;
+  const lxm_dn_params& p = *pp;
+  const RunCtx c = run_ctx(pp, n_run);
+  const int b = blockIdx.x, nb = gridDim.x;
+  Bar bar{p.sync, p.err, 0u, nb, &sm.flag};
+  uint16_t* const act16 = reinterpret_cast<uint16_t*>(p.xn + c.H);
   int tok = *p.tok;
-  for (int si = 0; si < n_run; si++) {
-    const int step = step0 + si;
-    // the input and its embedding row into h
-    if (step < p.n_forced) tok = p.forced[step];
-    if (tok < 0 || tok >= p.vocab) {
-      if (b == 0 && tid() == 0)
-        __hip_atomic_fetch_max(gp(p.err), 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      tok = 0;
+  HVec<M> w;  // the next norm's weight (staged in LDS)
+  w.load(layer_of(p.layers, 0).ln_in, c.H);
+  w.store_lds(sm.ws, c.H);
+  for (int it = 0; it < c.nit; it++) {
+    const int si = it / (c.nL + 1), L = it % (c.nL + 1), step = c.step0 + si;
+    HVec<M> h;
+    if (L == 0) {
+      // the input; its embedding row as h, through LDS (workgroup 0 writes h)
+      if (step < p.n_forced) tok = p.forced[step];
+      if (tok < 0 || tok >= p.vocab) {
+        if (b == 0 && tid() == 0)
+          __hip_atomic_fetch_max(gp(p.err), 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        tok = 0;
+      }
+      const uint16_t* e = p.embed + (int64_t)tok * c.H;
+      for (int j = tid() & 63; j < c.H / 8; j += 64) {
+        // stored chunk j: entries 8 (j / 64) .. of lane j % 64 (GH >= 8), or entries 8j.. (GH 4)
+        const v4u u = *gp(reinterpret_cast<const v4u*>(e) + j);
+        const int c0 = GH < 8 ? 8 * j : (j % 64) * GH + 8 * (j / 64);
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+          sm.hs[c0 + 2 * i] = bf16f(u[i] & 0xffffu);
+          sm.hs[c0 + 2 * i + 1] = bf16f(u[i] >> 16);
+        }
+      }
+      if (b == 0) {
+        h.load_lds(sm.hs, c.H);
+        for (int m = 0; m < M; m++) {
+          const int c0 = 256 * m + 4 * (tid() & 63);
+          if (c0 < c.H)
+#pragma unroll
+            for (int i = 0; i < 4; i++) stf<true>(p.h + c0 + i, h.v[m][i]);
+        }
+      }
+    } else {
+      h.load_coh(p.h, c.H);
+      h.store_lds(sm.hs, c.H);
     }
-    {
-      const uint16_t* e = p.embed + (int64_t)tok * H;
-      for (int c = b * NT + tid(); c < H; c += nb * NT) {
-        const int l = c / GH, k = c % GH;
-        const int at = GH < 8 ? c : ((k >> 3) * 64 + l) * 8 + (k & 7);
-        stf<true>(p.h + c, bf16f(e[at]));
-      }
-    }
-    bar.arrive();
-    WRow<GH> rp;
-    rp.load(p.layers[0].proj, min(GW, nproj - 1), LANE);
-    if (!bar.wait()) return;
-    for (int L = 0; L < p.n_layers; L++) {
-      const lxm_dn_layer& ly = p.layers[L];
-      const DnGdn g{ly.conv_qk, ly.conv_v, ly.A_log, ly.dt_bias, ly.rec, ly.conv, p.P, p.on,
-                    nk, kl, rl, R};
-      const DnOut o{ly.out, H, nk * rl, p.on, p.P + 2 * nq + nvr, ly.gnorm, p.geps, p.h,
-                    ly.conv, p.P, nk, kl};
-      // projections over the input norm
-      {
-        XRegs<GH> xc;
-        xc.template load_norm<true>(p.h, ly.ln_in, norm_factor<true>(p.h, H, eps, wsum), LANE);
-        rows_run<GH, 0, true>(ly.proj, nproj, xc, rp, GW, nwv, p.P, 0);
-      }
-      bar.arrive();
-      // the delta rule; the other workgroups request their first out_proj rows meanwhile (two
-      // paths, so the rows' registers are not held across the delta rule)
-      WRow<GV> ro;
-      if (b < ngdn) {
-        float s[16];
-        gdn_load<true>(g, b, s);
-        if (!bar.wait()) return;
-        gdn_body<true>(g, b, s, gl);
-        bar.arrive();
-        ro.load(ly.out, min(GW, H - 1), LANE);
-        if (!bar.wait()) return;
-      } else {
-        ro.load(ly.out, min(GW, H - 1), LANE);
-        if (!bar.wait()) return;
-        bar.arrive();
-        if (!bar.wait()) return;
-      }
-      // the gated norm, out_proj, the query/key windows
-      {
-        gated_norm<NW, true>(o, ys);
-        lds_barrier();
-        XRegs<GV> xc;
-        xc.template load<false>(ys, LANE);
-        rows_run<GV, 1, true>(ly.out, H, xc, ro, GW, nwv, p.h, nwv / 2);
-        qk_windows<true>(o, b, nb, NT);
-      }
-      bar.arrive();
-      WRow<GH> ug, uu;
-      ug.load(ly.gate, min(GW, I - 1), LANE);
-      uu.load(ly.up, min(GW, I - 1), LANE);
-      if (!bar.wait()) return;
-      // SwiGLU over the post norm
-      {
-        XRegs<GH> xc;
-        xc.template load_norm<true>(p.h, ly.ln_post, norm_factor<true>(p.h, H, eps, wsum), LANE);
-        units_run<GH, true>(ly.gate, ly.up, I, xc, ug, uu, GW, nwv, act, 0);
-      }
-      bar.arrive();
-      WRow<GI> rdn;
-      rdn.load(ly.down, min(GW, H - 1), LANE);
-      if (!bar.wait()) return;
-      // down_proj (its input staged in LDS)
-      {
-        XLds<GI>::template stage<true>(xd, act);
-        lds_barrier();
-        const XLds<GI> xc{xd, LANE};
-        rows_run<GI, 1, true>(ly.down, H, xc, rdn, GW, nwv, p.h, nwv / 2);
-        lds_barrier();  // (xd is free again)
-      }
-      bar.arrive();
-      if (L + 1 < p.n_layers) rp.load(p.layers[L + 1].proj, min(GW, nproj - 1), LANE);
-      else rp.load(p.embed, min(GW, p.vocab - 1), LANE);
-      if (!bar.wait()) return;
-    }
-    // the head over the final norm; the argmax key of this step's parity
     unsigned long long* key = p.keys + (step & 1);
-    {
-      XRegs<GH> xc;
-      xc.template load_norm<true>(p.h, p.w_final, norm_factor<true>(p.h, H, eps, wsum), LANE);
-      head_run<GH>(p.embed, p.vocab, xc, rp, GW, nwv, key);
+    // the first phase's input: the input norm (a layer) or the final norm (the head), formed by
+    // every wave from LDS
+    lds_barrier();
+    (void)norm_factor<false>(sm.hs, c.H, c.eps, sm.wsum);
+    if (L < c.nL) {
+      const lxm_dn_layer ly = layer_of(p.layers, L);
+      bar.arrive();
+      if (b < c.ngdn) {
+        if (!gdn_phase<GH, GV, GI>(p, ly, c, bar, sm)) return;
+      } else {
+        if (!bar.wait()) return;
+        bar.arrive();
+        if (!bar.wait()) return;
+      }
+      // out_proj's phase: the gated norm and the residual (the rows' workgroups), the windows
+      const DnOut o = out_of(p, ly, c);
+      if (b >= c.ngdn) {
+        gated_norm<NW, true, true>(o, sm.ys);
+        stage_h(p.h, c.H, sm.hs);
+      }
+      lds_barrier();
+      qk_windows<true>(o, b, nb, NT);
+      bar.arrive();
+      w.load(ly.ln_post, c.H);
+      w.store_lds(sm.ws, c.H);
+      if (!bar.wait()) return;
+      // SwiGLU's input: the post norm
+      h.load_coh(p.h, c.H);
+      h.store_lds(sm.hs, c.H);
+      lds_barrier();
+      (void)norm_factor<false>(sm.hs, c.H, c.eps, sm.wsum);
+      bar.arrive();
+      if (!bar.wait()) return;
+      // down_proj's input and the residual
+      for (int j = tid() & 63; j < c.I / 8; j += 64)
+        sm.xd[j] = __builtin_bit_cast(v4u, ldf4<true>(reinterpret_cast<const float*>(act16), 4 * j));
+      h.load_coh(p.h, c.H);
+      h.store_lds(sm.hs, c.H);
+      lds_barrier();
+    } else {
+      lds_barrier();  // (the stream waves' head rows)
     }
     bar.arrive();
+    {
+      const bool head = L + 1 == c.nL;
+      const int Ln = L + 1 > c.nL ? 0 : L + 1;
+      w.load(head ? p.w_final : layer_of(p.layers, Ln).ln_in, c.H);
+      w.store_lds(sm.ws, c.H);
+    }
     if (!bar.wait()) return;
-    tok = argmax_idx(__hip_atomic_load(gp(key), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
-    if (b == 0 && tid() == 0) {
-      if (step < p.n_steps) p.preds[step] = tok;
-      __hip_atomic_store(gp(p.keys + ((step + 1) & 1)), 0ull, __ATOMIC_RELAXED,
-                         __HIP_MEMORY_SCOPE_AGENT);
+    if (L == c.nL) {
+      tok = argmax_idx(__hip_atomic_load(gp(key), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+      if (b == 0 && tid() == 0) {
+        if (step < p.n_steps) p.preds[step] = tok;
+        __hip_atomic_store(gp(p.keys + ((step + 1) & 1)), 0ull, __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_AGENT);
+      }
     }
   }
   if (b == 0 && tid() == 0) {
-    *p.step = step0 + n_run;
+    *p.step = c.step0 + n_run;
     *p.tok = tok;
   }
-#undef LANE
-#undef GW
+}
+
+// A stream wave's loop (waves 1-7)
+template <int GH, int GV, int GI>
+__device__ __forceinline__ void run_stream(const lxm_dn_params* pp, int n_run,
+                                           RunLds<GH, GV, GI>& sm) {
+  const lxm_dn_params& p = *pp;
+  const RunCtx c = run_ctx(pp, n_run);
+  const int b = blockIdx.x, nb = gridDim.x;
+  Bar bar{p.sync, p.err, 0u, nb, &sm.flag};
+  uint16_t* const act16 = reinterpret_cast<uint16_t*>(p.xn + c.H);
+  // stream wave index (waves 1-7 of every workgroup); out_proj's waves (outside the delta rule's
+  // workgroups)
+#define SW (b * (NW - 1) + wave_id() - 1)
+#define OW ((b - c.ngdn) * (NW - 1) + wave_id() - 1)
+  const int nsw = nb * (NW - 1), now = (nb - c.ngdn) * (NW - 1);
+  const int zlo = 2 * c.nq + c.nvr, zhi = 2 * c.nq + 2 * c.nvr;
+  RowSet<GH, D_P> rp;  // the item's first rows (a layer's projections, the head's)
+  rp.prefetch(layer_of(p.layers, 0).proj, c.nproj, SW, nsw, 0);
+  for (int it = 0; it < c.nit; it++) {
+    const int si = it / (c.nL + 1), L = it % (c.nL + 1), step = c.step0 + si;
+    unsigned long long* key = p.keys + (step & 1);
+    lds_barrier();  // (the control wave's h and weight)
+    const float rn = norm_factor<false>(sm.hs, c.H, c.eps, sm.wsum);
+    if (L < c.nL) {
+      const lxm_dn_layer ly = layer_of(p.layers, L);
+      // the projections (silu of the gated norm's z rows)
+      {
+        XRegs<GH> xc;
+        xc.template load_norm<false>(sm.hs, sm.ws, rn, tid() & 63);
+        pipe_rows<GH, D_P, 2>(rp, ly.proj, c.nproj, xc, SW, nsw, 0, p.P, sm.hs, zlo, zhi);
+      }
+      bar.arrive();
+      RowSet<GV, D_O> ro;
+      if (b < c.ngdn) {
+        if (!gdn_phase<GH, GV, GI>(p, ly, c, bar, sm)) return;
+      } else {
+        ro.prefetch(ly.out, c.H, OW, now, 0);
+        if (!bar.wait()) return;
+        bar.arrive();
+        if (!bar.wait()) return;
+      }
+      // out_proj (outside the delta rule's workgroups)
+      const DnOut o = out_of(p, ly, c);
+      if (b >= c.ngdn) {
+        gated_norm<NW, true, true>(o, sm.ys);
+        stage_h(p.h, c.H, sm.hs);
+      }
+      lds_barrier();
+      if (b >= c.ngdn) {
+        XRegs<GV> xc;
+        xc.template load<false>(sm.ys, tid() & 63);
+        pipe_rows<GV, D_O, 1>(ro, ly.out, c.H, xc, OW, now, 0, p.h, sm.hs);
+      }
+      qk_windows<true>(o, b, nb, NT);
+      bar.arrive();
+      UnitSet<GH, D_U> us;
+      us.prefetch(ly.gate, ly.up, c.I, SW, nsw, 0);
+      if (!bar.wait()) return;
+      // SwiGLU
+      lds_barrier();  // (the control wave's h and weight)
+      {
+        XRegs<GH> xc;
+        xc.template load_norm<false>(sm.hs, sm.ws, norm_factor<false>(sm.hs, c.H, c.eps, sm.wsum),
+                                     tid() & 63);
+        pipe_units<GH, GI, D_U>(us, ly.gate, ly.up, c.I, xc, SW, nsw, 0, act16);
+      }
+      bar.arrive();
+      RowSet<GI, D_D> rdn;
+      rdn.prefetch(ly.down, c.H, SW, nsw, 0);
+      if (!bar.wait()) return;
+      // down_proj
+      lds_barrier();  // (the control wave's input and residual)
+      {
+        const XLds<GI> xc{sm.xd, tid() & 63};
+        pipe_rows<GI, D_D, 1>(rdn, ly.down, c.H, xc, SW, nsw, 0, p.h, sm.hs);
+      }
+    } else {
+      // the head over the final norm; the argmax key of this step's parity
+      XRegs<GH> xc;
+      xc.template load_norm<false>(sm.hs, sm.ws, rn, tid() & 63);
+      pipe_head<GH, D_P>(rp, p.embed, p.vocab, xc, SW, nsw, key);
+      lds_barrier();
+    }
+    bar.arrive();
+    // the next item's first rows: the next layer's projections, or the head's (after the last
+    // item every slot requests the head's row 0, a cache hit: a request on every path, so the
+    // old rows' registers are free during the item)
+    {
+      const bool head = L + 1 == c.nL, last = it + 1 == c.nit;
+      const int Ln = L + 1 > c.nL ? 0 : L + 1;
+      rp.prefetch(head || last ? p.embed : layer_of(p.layers, Ln).proj,
+                  last ? 1 : head ? p.vocab : c.nproj, SW, nsw, 0);
+    }
+    if (!bar.wait()) return;
+  }
+#undef SW
+#undef OW
+}
+
+template <int GH, int GV, int GI>
+__global__ __launch_bounds__(NT, 1) void dn_run(const lxm_dn_params* __restrict__ pp, int n_run) {
+  static_assert(GV * 64 <= 4096, "at most 32 live value heads");
+  __shared__ RunLds<GH, GV, GI> sm;
+  if (wave_id() == 0) run_ctl<GH, GV, GI>(pp, n_run, sm);
+  else run_stream<GH, GV, GI>(pp, n_run, sm);
 }
 
 // ---------------------------------------------------------------------------------------------
