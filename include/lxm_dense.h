@@ -67,6 +67,11 @@ typedef struct lxm_dn_params {
                                  by step parity; both zero before a run) */
   int32_t* err;               /* (1): 1 a forced token out of range, 2 a wait of lxm_dn_run timed out */
   uint32_t* sync;             /* (256): lxm_dn_run's barrier counters, zero before each run */
+  unsigned long long* prof;   /* null, or (the sub-phase profiling build only) lxm_dn_run's phase
+                                 clock: per workgroup b at prof + 32 b, for each phase k (the
+                                 projections, the delta rule, out_proj, SwiGLU, down_proj, the
+                                 head) 3 sums over the run of 100 MHz wall-clock ticks: input
+                                 staged, rows summed, barrier passed */
 } lxm_dn_params;
 
 /* One greedy step (embedding, every layer, the head's first maximum, the token fed back) on

@@ -691,10 +691,14 @@ struct Bar {
   int32_t* err;
   uint32_t target;
   int nblk;
-  int* flag;  // LDS
+  int* flag;        // LDS
+  uint64_t* tarr;   // LDS: the arrival's time (the sub-phase profiling build), or null
   __device__ __forceinline__ void arrive() {
     drain();
     lds_barrier();
+#ifdef LXM_SUBPROF
+    if (tid() == 0) *tarr = wall();
+#endif
     target += (uint32_t)nblk;
     if (tid() == 0) add_rlx(ctr + 32 * (blockIdx.x % BAR_COPIES), 1u);
   }
@@ -955,6 +959,43 @@ struct HVec {
 #define D_U 2
 #define D_D 2
 
+// The persistent run's phase clock (the sub-phase profiling build, LXM_SUBPROF): thread 0 (the
+// control wave's lane 0) stamps each phase's start (the barrier before it passed), its input
+// staged (dp_x) and every wave's rows summed (the arrival, in Bar::arrive); dp_phase(k) closes
+// phase k and adds its three spans to the workgroup's sums, written to p.prof at the end.
+#define DP_NPH 6
+struct DnProf {
+  uint64_t acc[DP_NPH][3];
+  uint64_t t[3];  // start, input staged, arrival
+};
+template <class S>
+__device__ __forceinline__ void dp_x(S& sm) {
+#ifdef LXM_SUBPROF
+  if (tid() == 0) sm.dp.t[1] = wall();
+#endif
+}
+template <class S>
+__device__ __forceinline__ void dp_phase(S& sm, int k) {
+#ifdef LXM_SUBPROF
+  if (tid() == 0) {
+    DnProf& d = sm.dp;
+    const uint64_t w = wall();
+    d.acc[k][0] += d.t[1] - d.t[0];
+    d.acc[k][1] += d.t[2] - d.t[1];
+    d.acc[k][2] += w - d.t[2];
+    d.t[0] = d.t[1] = w;
+  }
+#endif
+}
+template <class S>
+__device__ __forceinline__ uint64_t* dp_tarr(S& sm) {
+#ifdef LXM_SUBPROF
+  return &sm.dp.t[2];
+#else
+  return nullptr;
+#endif
+}
+
 // the shared memory of the persistent run
 template <int GH, int GV, int GI>
 struct RunLds {
@@ -965,6 +1006,9 @@ struct RunLds {
   v4u xd[8 * GI];                 // down_proj's bf16 input, interleaved
   GdnLds gl;
   int flag;
+#ifdef LXM_SUBPROF
+  DnProf dp;
+#endif
 };
 
 // The run's shared state (scalar)
@@ -1011,9 +1055,12 @@ __device__ __forceinline__ bool gdn_phase(const lxm_dn_params& p, const lxm_dn_l
   float s[16];
   gdn_load<true>(g, blockIdx.x, s);
   if (!bar.wait()) return false;
+  dp_phase(sm, 0);
   gdn_body<true>(g, blockIdx.x, s, sm.gl);
   bar.arrive();
-  return bar.wait();
+  if (!bar.wait()) return false;
+  dp_phase(sm, 1);
+  return true;
 }
 
 // The control wave's loop (wave 0)
@@ -1024,12 +1071,16 @@ __device__ __forceinline__ void run_ctl(const lxm_dn_params* pp, int n_run,
   const lxm_dn_params& p = *pp;
   const RunCtx c = run_ctx(pp, n_run);
   const int b = blockIdx.x, nb = gridDim.x;
-  Bar bar{p.sync, p.err, 0u, nb, &sm.flag};
+  Bar bar{p.sync, p.err, 0u, nb, &sm.flag, dp_tarr(sm)};
   uint16_t* const act16 = reinterpret_cast<uint16_t*>(p.xn + c.H);
   int tok = *p.tok;
   HVec<M> w;  // the next norm's weight (staged in LDS)
   w.load(layer_of(p.layers, 0).ln_in, c.H);
   w.store_lds(sm.ws, c.H);
+#ifdef LXM_SUBPROF
+  if (tid() < DP_NPH * 3) sm.dp.acc[tid() / 3][tid() % 3] = 0;
+  if (tid() == 0) sm.dp.t[0] = sm.dp.t[1] = sm.dp.t[2] = wall();
+#endif
   for (int it = 0; it < c.nit; it++) {
     const int si = it / (c.nL + 1), L = it % (c.nL + 1), step = c.step0 + si;
     HVec<M> h;
@@ -1070,6 +1121,7 @@ __device__ __forceinline__ void run_ctl(const lxm_dn_params* pp, int n_run,
     // every wave from LDS
     lds_barrier();
     (void)norm_factor<false>(sm.hs, c.H, c.eps, sm.wsum);
+    dp_x(sm);
     if (L < c.nL) {
       const lxm_dn_layer ly = layer_of(p.layers, L);
       bar.arrive();
@@ -1077,8 +1129,10 @@ __device__ __forceinline__ void run_ctl(const lxm_dn_params* pp, int n_run,
         if (!gdn_phase<GH, GV, GI>(p, ly, c, bar, sm)) return;
       } else {
         if (!bar.wait()) return;
+        dp_phase(sm, 0);
         bar.arrive();
         if (!bar.wait()) return;
+        dp_phase(sm, 1);
       }
       // out_proj's phase: the gated norm and the residual (the rows' workgroups), the windows
       const DnOut o = out_of(p, ly, c);
@@ -1087,24 +1141,29 @@ __device__ __forceinline__ void run_ctl(const lxm_dn_params* pp, int n_run,
         stage_h(p.h, c.H, sm.hs);
       }
       lds_barrier();
+      dp_x(sm);
       qk_windows<true>(o, b, nb, NT);
       bar.arrive();
       w.load(ly.ln_post, c.H);
       w.store_lds(sm.ws, c.H);
       if (!bar.wait()) return;
+      dp_phase(sm, 2);
       // SwiGLU's input: the post norm
       h.load_coh(p.h, c.H);
       h.store_lds(sm.hs, c.H);
       lds_barrier();
       (void)norm_factor<false>(sm.hs, c.H, c.eps, sm.wsum);
+      dp_x(sm);
       bar.arrive();
       if (!bar.wait()) return;
+      dp_phase(sm, 3);
       // down_proj's input and the residual
       for (int j = tid() & 63; j < c.I / 8; j += 64)
         sm.xd[j] = __builtin_bit_cast(v4u, ldf4<true>(reinterpret_cast<const float*>(act16), 4 * j));
       h.load_coh(p.h, c.H);
       h.store_lds(sm.hs, c.H);
       lds_barrier();
+      dp_x(sm);
     } else {
       lds_barrier();  // (the stream waves' head rows)
     }
@@ -1116,6 +1175,7 @@ __device__ __forceinline__ void run_ctl(const lxm_dn_params* pp, int n_run,
       w.store_lds(sm.ws, c.H);
     }
     if (!bar.wait()) return;
+    dp_phase(sm, L < c.nL ? 4 : 5);
     if (L == c.nL) {
       tok = argmax_idx(__hip_atomic_load(gp(key), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
       if (b == 0 && tid() == 0) {
@@ -1125,6 +1185,9 @@ __device__ __forceinline__ void run_ctl(const lxm_dn_params* pp, int n_run,
       }
     }
   }
+#ifdef LXM_SUBPROF
+  if (p.prof && tid() < DP_NPH * 3) p.prof[32 * b + tid()] = sm.dp.acc[tid() / 3][tid() % 3];
+#endif
   if (b == 0 && tid() == 0) {
     *p.step = c.step0 + n_run;
     *p.tok = tok;
@@ -1138,7 +1201,7 @@ __device__ __forceinline__ void run_stream(const lxm_dn_params* pp, int n_run,
   const lxm_dn_params& p = *pp;
   const RunCtx c = run_ctx(pp, n_run);
   const int b = blockIdx.x, nb = gridDim.x;
-  Bar bar{p.sync, p.err, 0u, nb, &sm.flag};
+  Bar bar{p.sync, p.err, 0u, nb, &sm.flag, dp_tarr(sm)};
   uint16_t* const act16 = reinterpret_cast<uint16_t*>(p.xn + c.H);
   // stream wave index (waves 1-7 of every workgroup); out_proj's waves (outside the delta rule's
   // workgroups)

@@ -46,7 +46,7 @@ class DnParams(ctypes.Structure):
         [("rms_eps", ctypes.c_float), ("geps", ctypes.c_float)] + \
         [(n, ctypes.c_int32) for n in ("n_forced", "n_steps", "pad")] + \
         [(n, P64) for n in ("layers", "layers_host", "embed", "w_final", "forced", "preds", "step",
-                            "tok", "h", "xn", "P", "on", "keys", "err", "sync")]
+                            "tok", "h", "xn", "P", "on", "keys", "err", "sync", "prof")]
 
 
 def interleave(w):
@@ -63,12 +63,12 @@ def interleave(w):
 class DenseDecode:
     """The packed weights of a DenseModel and the decode driver over a cache."""
 
-    def __init__(self, model, cache, max_steps: int = 1 << 16):
+    def __init__(self, model, cache, max_steps: int = 1 << 16, subprof: bool = False):
         self.model, self.cache = model, cache
         sp, d = model.spec, model.dims
         self.spec, self.dims = sp, d
         self.dev = model.embed.device
-        self.lib = mk_build.load()
+        self.lib = mk_build.load(subprof)  # (subprof: the build with the phase clocks)
         H, nk, kl, rl, I = sp.hidden, sp.nk, sp.kd_live, sp.r_live, sp.inter
         R = d.nv // d.nk
         self.nproj = 2 * nk * kl + 2 * nk * rl * 128 + 2 * nk * rl
@@ -120,7 +120,7 @@ class DenseDecode:
         self.graph = None
         self._pb = None
 
-    def _params(self, n_forced: int):
+    def _params(self, n_forced: int, prof: int = 0):
         sp, d = self.spec, self.dims
         p = DnParams(hidden=sp.hidden, n_layers=d.n_layers, nk=sp.nk, kl=sp.kd_live, nv=d.nv,
                      rl=sp.r_live, inter=sp.inter, vocab=sp.vocab, n_conv=d.n_conv,
@@ -132,7 +132,7 @@ class DenseDecode:
                      step=self.step.data_ptr(), tok=self.tok.data_ptr(), h=self.h.data_ptr(),
                      xn=self.xn.data_ptr(), P=self.P.data_ptr(), on=self.on.data_ptr(),
                      keys=self.keys.data_ptr(), err=self.err.data_ptr(),
-                     sync=self.sync.data_ptr())
+                     sync=self.sync.data_ptr(), prof=prof)
         pd = torch.frombuffer(bytearray(bytes(p)), dtype=torch.uint8).to(self.dev)
         return p, pd
 
@@ -195,13 +195,15 @@ class DenseDecode:
             raise RuntimeError(f"dense decode launch failed: hipError {e}")
 
     @torch.no_grad()
-    def run(self, forced, n: int, graph: bool = True, mode: str = "steps") -> list:
+    def run(self, forced, n: int, graph: bool = True, mode: str = "steps", prof=None) -> list:
         """n greedy steps from the cache's states (updated in place); step i's input is forced[i]
         for i < len(forced), else step i - 1's prediction. Returns the n predictions. mode
         "steps": lxm_dn_step per step (graph: the first step eagerly, one step captured
         (capturing runs nothing) and replayed for the others; the step reads its index and input
         from device memory); "persistent": one launch of lxm_dn_run for all n steps (the same
-        results; for callers that cannot capture graphs)."""
+        results; for callers that cannot capture graphs). prof: with a DenseDecode built with
+        subprof=True and mode "persistent", an int64 tensor of 32 x (workgroups) that receives
+        the run's phase clock (include/lxm_dense.h)."""
         f = torch.as_tensor(forced, dtype=torch.int64)
         if len(f) == 0 or n < 1 or n > self.max_steps or len(f) > self.max_steps:
             raise ValueError("forced tokens and steps: 1 .. max_steps")
@@ -214,9 +216,15 @@ class DenseDecode:
         self.err.zero_()
         self.keys.zero_()
         self.sync.zero_()
-        if getattr(self, "_nf", None) != len(f):
-            self._p, self._pd = self._params(len(f))
-            self._nf, self.graph = len(f), None
+        if prof is not None:
+            ncu = torch.cuda.get_device_properties(self.dev).multi_processor_count
+            if prof.dtype != torch.int64 or not prof.is_cuda or prof.numel() < 32 * ncu:
+                raise ValueError("prof: an int64 device tensor of at least 32 x (the device's "
+                                 "CUs) entries")
+        pp = 0 if prof is None else prof.data_ptr()
+        if getattr(self, "_nf", None) != len(f) or getattr(self, "_pp", 0) != pp:
+            self._p, self._pd = self._params(len(f), pp)
+            self._nf, self._pp, self.graph = len(f), pp, None
         if mode == "persistent":
             st = ctypes.c_void_p(torch.cuda.current_stream(self.dev).cuda_stream)
             e = self.lib.lxm_dn_run(ctypes.byref(self._p), ctypes.c_void_p(self._pd.data_ptr()), n, st)
