@@ -917,7 +917,7 @@ __device__ __forceinline__ float ndot(const uint8_t* ent, int start, int n, floa
 // per entry and the rest (gate_compute). Rows of more than four entries take ndot in stage B.
 struct GateLd {
   v4f hv, w, we;  // the residual, weight and norm weight 1 + w_in of each entry
-  v4f tp;         // query/key: the conv taps; decay: dt_bias, A_log
+  v4f tp;         // query/key: the conv taps; decay: dt_bias, -exp(A_log)
   float h0, h1, h2;          // query/key: the conv history
   int kind, j, len, start, info;  // kind 0 none, 1 query/key, 2 decay; info: slot, or vh
 };
@@ -1008,10 +1008,10 @@ __device__ __forceinline__ void gate_compute(const ChainK& k, const uint8_t* gt,
     const float a = rd<BF>(gate_dot<BF, E4>(gt, g, r));
     const float x = a + g.tp[0];
     float e;
-    if (x < -104.0f && g.tp[1] <= 88.0f) {
+    if (x < -104.0f && g.tp[1] > -__builtin_inff()) {
       e = 1.0f;  // exp(x) rounds to 0, so softplus is 0 and g = -exp(A_log) * 0 = -0
     } else {
-      const float gg = (-cr_exp(g.tp[1])) * softplus(x);
+      const float gg = g.tp[1] * softplus(x);
       e = cr_exp(gg);
     }
     LF(L_EV)[g.info] = e;
@@ -1236,14 +1236,18 @@ __device__ void run_chain(const lxm_params& pg) {
     *reinterpret_cast<int64_t*>(lt[L].words) = ly.pt_words;
   }
   __syncthreads();
-  // the live query/key channels' windows from the conv state (positions 1..3)
+  // the live query/key channels' windows from the conv state (positions 1..3); each decay's
+  // -exp(A_log), a constant of its value head, formed once here in the LDS copy (the gates read
+  // it in A_log's place: the same cr_exp a step would evaluate)
   for (int L = 0; L < p.n_layers; L++) {
-    const uint8_t* gt = smem + L_GATES + lt[L].goff;
+    uint8_t* gt = smem + L_GATES + lt[L].goff;
     const lxm_gate& hd = *reinterpret_cast<const lxm_gate*>(gt);
     const lxm_qkc* qk = reinterpret_cast<const lxm_qkc*>(gt + hd.qk);
     for (int j = t; j < hd.n_qk; j += NT)
       for (int s = 0; s < 3; s++)
         hist[3 * (hd.qk_base + j) + s] = conv_at<BF>(p.conv[L], (int64_t)qk[j].chan * 4 + 1 + s);
+    lxm_dec* dec = reinterpret_cast<lxm_dec*>(gt + hd.dec);
+    for (int j = t; j < hd.n_dec; j += NT) dec[j].A_log = -cr_exp(dec[j].A_log);
   }
   uint64_t* pa = reinterpret_cast<uint64_t*>(smem + L_PROF);
   if (t < 32) pa[t] = 0;
