@@ -276,6 +276,23 @@ def decode_leg(args, dev, hf_holder: dict) -> dict:
                               "continuing from the chunk's final state"}
         log(f"[bench] forced stream: {n_f} tokens at {forced_out['tok_s']} tok/s")
 
+    # the chain's own counters on the chunk's first tokens, from the initial state again: GDN
+    # events and MLP redos (the MLP run again after an event with a live query) per token
+    n_c = min(4096, chunk)
+    for ly, (c, r) in zip(cache.layers, saved):
+        ly.conv_states[0].copy_(c)
+        ly.recurrent_states[0].copy_(r)
+    prof = torch.zeros(mg.prof_size, dtype=torch.int64, device=dev)
+    counted = mg.run([start], n_c, prof=prof)
+    rep = mg.phase_report(prof)
+    gdn_out = {"tokens": n_c, "events_per_token": rep["GDN events per token"],
+               "mlp_redos_per_token": rep["MLP redos per token"],
+               "stream_equal": counted == stream_preds[:n_c],
+               "note": "the chain's counters on the chunk's first tokens (a second launch from "
+                       "the initial state)"}
+    log(f"[bench] GDN events {gdn_out['events_per_token']}/token, MLP redos "
+        f"{gdn_out['mlp_redos_per_token']}/token")
+
     session_out = None
     if args.session_tokens > 0:
         session_out = session_leg(args, dev, f, model, conv0, rec0, start, stream_preds)
@@ -323,6 +340,7 @@ def decode_leg(args, dev, hf_holder: dict) -> dict:
                       gold["stream_sha256"] == stream_sha and gold["conv_sha256"] == conv_sha
                       and gold["rec_sha256"] == rec_sha)},
         "forced_input": forced_out,
+        "gdn_events": gdn_out,
         "session_decode": session_out,
     }
     if args.oracle_tokens > 0:

@@ -1135,6 +1135,7 @@ __device__ __forceinline__ bool layer(const lxm_params& p, const ChainK& k, int 
   if (flags[F_ANY]) {
     if (!gdn_event<BF, E4>(p, L, gt, seq, ha, hb)) return false;
     if (flags[F_OUT]) {  // h may have changed: the MLP again, on the new h
+      if (k.prof && t == 0) pa[18] += 1;  // (the MLP redos)
       ss = hidden_ss<BF>(ha, hb);
       const float r2 = norm_r(ss, H, hd.eps);
       stage_a<BF, E4>(k, r1, ha, hb, r2, L, step, false, fly);

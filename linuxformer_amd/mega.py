@@ -408,6 +408,7 @@ class Mega:
         n = max(c[17], 1)
         out = {name: round(c[k] / n, 1) for k, name in enumerate(self.PHASES)}
         out["GDN events per token"] = round(c[16] / n, 3)
+        out["MLP redos per token"] = round(c[18] / n, 3)  # (events with a live query)
         for k, name in enumerate(self.HELPER):
             v = [c[32 + 4 * b + k] for b in range(1, self.ncta)]
             out[f"helper {name}"] = round(sum(v) / len(v) / n, 1)
