@@ -81,6 +81,32 @@ def test_dense_small_live_state_graph(cuda):
     check(4, 12, seed=3, graph=True, mode="steps")
 
 
+def test_dense_persistent_phase_clock(cuda):
+    """The profiling build's persistent run (its phase clock on) predicts what the oracle does and
+    fills the clock: every workgroup's six phases, each use counted in ticks."""
+    from oracle import oracle as ox
+
+    spec, dm_cpu, sm = model("small")
+    conv0, rec0 = synth.dense_state(dm_cpu, 3)
+    forced = [int(x) for x in np.random.default_rng(11).integers(0, spec.vocab, 3)]
+    print(f"[gpu-test] dense {spec.name}: persistent run with the phase clock", flush=True)
+    dm = synth.dense_to(dm_cpu, "cuda")
+    cache = fast.StateCache(conv0, rec0, "bf16", "cuda")
+    dd = dense.DenseDecode(dm, cache, subprof=True)
+    ncu = torch.cuda.get_device_properties(0).multi_processor_count
+    prof = torch.zeros(32 * ncu, dtype=torch.int64, device="cuda")
+    preds = dd.run(forced, 10, mode="persistent", prof=prof)
+    c, r = conv0.copy(), rec0.copy()
+    po, _, _ = ox.OracleModel(sm).decode(c, r, forced, 10)
+    assert preds == po.tolist()
+    assert (bits(cache.rec_numpy()) == bits(r)).all()
+    acc = prof.view(ncu, 32)[:, :18].cpu().numpy().reshape(ncu, 6, 3)
+    assert (acc[:, :, 1:].sum(axis=2) > 0).all()  # every phase's rows and barrier took time
+    assert (acc >= 0).all() and (acc[:, 5, 1] > 0).all()  # the head's rows on every workgroup
+    with pytest.raises(ValueError):
+        dd.run(forced, 2, mode="persistent", prof=prof[:16])
+
+
 def test_dense_small_live_state_persistent(cuda):
     check(4, 12, seed=3)
 
