@@ -81,8 +81,9 @@ typedef struct lxm_dn_params {
 int lxm_dn_step(const lxm_dn_params* p_host, const lxm_dn_params* p_dev, void* stream);
 
 /* n greedy steps in one cooperative launch of one workgroup per CU (the same results as n calls
-   of lxm_dn_step): the layers' phases are separated by grid barriers, each wave requesting its
-   first weight rows of the next phase before it waits. Before the call: sync[0..255] = 0, keys[0..1] =
+   of lxm_dn_step): the layers' phases are separated by grid barriers; in each workgroup a control
+   wave polls them and stages each phase's input in LDS while seven stream waves hold their next
+   phase's weight rows in flight. Before the call: sync[0..255] = 0, keys[0..1] =
    0, *err = 0; afterwards *err != 0 reports a bad forced token (1) or a timed-out wait (2). Needs
    nk x rl x 4 <= the device's CUs and (hidden, live value dims, inter) = (2560, 4096, 9216) or
    (256, 512, 512). Returns a hipError_t. */

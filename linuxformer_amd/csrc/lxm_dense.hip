@@ -11,11 +11,12 @@
 // the stock decode's (ATen's 16-row cascade for the state's row sums), as the sparse paths do.
 // (Qwen3_5 decoder layer: transformers/models/qwen3_5/modeling_qwen3_5.py:168-545, :704-793.)
 //
-// Two drivers share the phase bodies below: lxm_dn_step (one step as five kernels per layer, for
-// a caller that captures it in a graph) and lxm_dn_run (n steps in one persistent launch: one
-// workgroup per CU, the phases separated by grid barriers; the vectors that cross workgroups
-// move through agent-scope loads and stores, and each wave requests its first weight rows of the
-// next phase before it waits).
+// Two drivers share the row sums and the delta rule below: lxm_dn_step (one step as five kernels
+// per layer, for a caller that captures it in a graph) and lxm_dn_run (n steps in one persistent
+// launch: one workgroup per CU, the phases separated by grid barriers; the vectors that cross
+// workgroups move through agent-scope loads and stores; a control wave per workgroup polls the
+// barriers and stages each phase's input while seven stream waves hold the next phase's weight
+// rows in flight).
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
