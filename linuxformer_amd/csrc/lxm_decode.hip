@@ -102,7 +102,8 @@ static_assert((L_FLAGS + 4 * F_KEYW) % 8 == 0 && F_KEYW + 16 <= 256, "the key wo
 #define HX_OP (HX_MISC + 256)         // out_proj: the helper's row pointers (LXM_OUT_ROWS + 1)
 #define HX_OE (HX_OP + 4 * (LXM_OUT_ROWS + 4))  // its entries (LXM_OUT_MAX, 8 bytes at most)
 #define HX_OY (HX_OE + 8 * LXM_OUT_MAX)  // the head outputs each entry reads
-#define HX_END (HX_OY + 4 * LXM_OUT_MAX + 64)  // (reads run up to 3 slots past the end)
+#define HX_LT (HX_OY + 4 * LXM_OUT_MAX + 64)  // (reads run up to 3 slots past the end)
+#define HX_END (HX_LT + 64 * (int)sizeof(lxm_layer))  // the layer table, resident for the launch
 
 // sync words (uint32 indices into p.sync). The event word has one copy per group of helpers
 // (group = block index mod 8, the XCD a block lands on when blocks are dealt round-robin), each
@@ -1420,7 +1421,19 @@ __device__ void gdn_head(const lxm_params& p, int L, int step, int vh, bool out,
   }
   const float e = ld_rlxf(p.mb_e + vh);
   const bool live = (tf & 1) != 0, dec = (tf & 4) != 0;
-  const lxm_layer ly = ldg(p.layers + L);
+  const lxm_layer ly = reinterpret_cast<const lxm_layer*>(hx + HX_LT)[L];
+  // the value channels', z rows' and beta row's descriptors, requested first (they do not
+  // depend on the step's data)
+  lxm_chan ch{};
+  lxm_row zr{}, br{};
+  if (live) {
+    if (t < VD)
+      ch = ldg(reinterpret_cast<const lxm_chan*>(p.blob + ly.chan) + 2 * p.nk * KD + vh * VD + t);
+    else if (t < 2 * VD)
+      zr = ldg(reinterpret_cast<const lxm_row*>(p.blob + ly.z_row) + vh * VD + t - VD);
+    else if (t == 2 * VD)
+      br = ldg(reinterpret_cast<const lxm_row*>(p.blob + ly.b_row) + vh);
+  }
   const uint8_t* gtab = p.blob + ly.gate;
   const lxm_gate hd = ldg(reinterpret_cast<const lxm_gate*>(gtab));
 #ifdef LXM_SUBPROF
@@ -1475,7 +1488,6 @@ __device__ void gdn_head(const lxm_params& p, int L, int step, int vh, bool out,
     const float r0 = ld_rlxf(rr_at(p, step, L));
     if (t < VD) {
       const int chan = 2 * p.nk * KD + vh * VD + t;
-      const lxm_chan ch = ldg(reinterpret_cast<const lxm_chan*>(p.blob + ly.chan) + chan);
       float win[4];
       win[3] = rd<BF>(rdot<BF, E4>(qent, ch.start, ch.len, h0, r0, w1in));
 #pragma unroll
@@ -1495,10 +1507,8 @@ __device__ void gdn_head(const lxm_params& p, int L, int step, int vh, bool out,
       vb[t] = rd<BF>(silu(rd<BF>(yv)));
     } else if (t < 2 * VD) {
       const int j = t - VD;
-      const lxm_row zr = ldg(reinterpret_cast<const lxm_row*>(p.blob + ly.z_row) + vh * VD + j);
       zb[j] = rd<BF>(rdot<BF, E4>(p.blob + ly.z_ent, zr.start, zr.len, h0, r0, w1in));
     } else if (t == 2 * VD) {
-      const lxm_row br = ldg(reinterpret_cast<const lxm_row*>(p.blob + ly.b_row) + vh);
       const float b = rd<BF>(rdot<BF, E4>(p.blob + ly.b_ent, br.start, br.len, h0, r0, w1in));
       misc[2] = (int)__float_as_uint(rd<BF>(sigmoid(b)));
     }
@@ -1629,7 +1639,7 @@ __device__ int out_prep(const lxm_params& p, int L, int ra, int rb, uint8_t* hx)
   const int t = threadIdx.x;
   int* op = reinterpret_cast<int*>(hx + HX_OP);
   uint8_t* oe = hx + HX_OE;
-  const lxm_layer ly = ldg(p.layers + L);
+  const lxm_layer ly = reinterpret_cast<const lxm_layer*>(hx + HX_LT)[L];
   const GAS int32_t* gptr = gp(reinterpret_cast<const int32_t*>(p.blob + ly.out_ptr));
   const int e0 = gptr[ra], ne = gptr[rb] - e0;  // the packer keeps ne <= LXM_OUT_MAX
   if (t <= rb - ra) op[t] = gptr[ra + t] - e0;
@@ -1692,6 +1702,9 @@ __device__ void run_helper(const lxm_params& p) {
     reinterpret_cast<v4u*>(lds)[k] = v4u{0, 0, 0, 0};
   __syncthreads();
   for (int k = t; k <= nr; k += NT) lptr[k] = (int32_t)(p.head_ptr[r0 + k] - e0);
+  // the layer table (an event then reads its layer's offsets from LDS, not from global memory)
+  for (int L = t; L < p.n_layers; L += NT)
+    reinterpret_cast<lxm_layer*>(hx + HX_LT)[L] = ldg(p.layers + L);
   {
     const uint32_t* src = p.head_ent + e0 * (Ent<E4>::SZ / 4);
     uint32_t* dst = reinterpret_cast<uint32_t*>(lent);
