@@ -1442,43 +1442,41 @@ __device__ void gdn_head(const lxm_params& p, int L, int step, int vh, bool out,
     if (dec) gpr[7] += 1;
   }
 #endif
-  // this key head's dense query and key
-  if (t < KD) {
-    qd[t] = 0.0f;
-    kd[t] = 0.0f;
-  }
-  __syncthreads();
-  if (live) {
-    const lxm_qkc* qk = reinterpret_cast<const lxm_qkc*>(gtab + hd.qk);
-    for (int j = t; j < hd.n_qk; j += NT) {
-      const int sl = gp(&qk[j].slot)[0];
-      if ((sl >> 9) == kh) ((sl & 256) ? kd : qd)[sl & 255] = ld_rlxf(p.mb_qk + j);
-    }
-  }
-  __syncthreads();
-  GH_MARK(0);
-  // l2norm in the model dtype: D(x * D(rsqrt(D(D(sum D(x*x)) + 1e-6)))); the query scaled by
-  // 1/sqrt(256) in fp32 (:352-353). Without a live query or key both stay 0.
-  if (wv < 2) {
-    const float* x = wv ? kd : qd;
-    float* o = wv ? kn : qn;
+  // This key head's dense query (wave NW - 2) and key (wave NW - 1), each gathered and then
+  // l2-normed in the model dtype by its own wave, D(x * D(rsqrt(D(D(sum D(x*x)) + 1e-6)))), the
+  // query scaled by 1/sqrt(256) in fp32 (:352-353), while waves 0-4 form the value channels, the
+  // z rows and beta below. Without a live query or key both stay 0.
+  if (wv >= NW - 2) {
+    const bool isk = wv == NW - 1;
+    float* x = isk ? kd : qd;
+    float* o = isk ? kn : qn;
     int n = 0;
     if (live) {
+      for (int i = lane; i < KD; i += 64) x[i] = 0.0f;
+      __atomic_signal_fence(__ATOMIC_SEQ_CST);
+      const lxm_qkc* qk = reinterpret_cast<const lxm_qkc*>(gtab + hd.qk);
+      for (int j = lane; j < hd.n_qk; j += 64) {
+        const int sl = gp(&qk[j].slot)[0];
+        if ((sl >> 9) == kh && ((sl & 256) != 0) == isk) x[sl & 255] = ld_rlxf(p.mb_qk + j);
+      }
+      // (one wave's LDS accesses run in order: its reads below see its writes above)
+      __atomic_signal_fence(__ATOMIC_SEQ_CST);
       float s = 0.0f;
       for (int i = lane; i < KD; i += 64) s = s + rd<BF>(x[i] * x[i]);
       s = rd<BF>(sum64(s));
       const float inv = rd<BF>(rsqrt_(rd<BF>(s + 1e-6f)));
       for (int b = 0; b < KD; b += 64) {
         float v = rd<BF>(x[b + lane] * inv);
-        if (!wv) v = v * 0.0625f;
+        if (!isk) v = v * 0.0625f;
         o[b + lane] = v;
         n += __popcll(__ballot(v != 0.0f));
       }
     } else {
       for (int b = 0; b < KD; b += 64) o[b + lane] = 0.0f;
     }
-    if (lane == 0) misc[wv] = n;
+    if (lane == 0) misc[isk ? 1 : 0] = n;
   }
+  GH_MARK(0);
   // the value channels' conv outputs (the window's earlier inputs from the ring, or from the
   // conv state before this launch), the in_proj_z rows and beta = sigmoid(b) (:497)
   if (live) {
