@@ -136,7 +136,9 @@ typedef struct lxm_params {
   uint32_t* mb_task;       /* (nv): a GDN event's task per value head, chain -> helpers */
   float* mb_e;             /* (nv): its decay factor exp(g) */
   float* mb_qk;            /* (LXM_MAXQKL): the layer's live query/key channel values */
-  float* ybuf;             /* (nv, vd): each value head's gated-norm output */
+  unsigned long long* ybuf; /* (nv, vd), zero at launch: each value head's gated-norm output,
+                              a stamped word (the value's fp32 bits low, the GDN event's
+                              sequence number high) */
   float* xo;               /* (LXM_MAXH): out_proj's rows, rounded, helpers -> chain */
   int32_t n_qk_total, pad;
 } lxm_params;
@@ -147,6 +149,8 @@ typedef struct lxm_params {
    reads its parameters from there). Returns a hipError_t. */
 int lxm_run(const lxm_params* p_host, const lxm_params* p_dev, int n_blocks, int lds_bytes,
             void* stream);
+/* (A launch numbers its events, at most n_tokens x (n_layers + 1), below 2^24: longer launches
+   are refused with hipErrorInvalidValue.) */
 /* mk_smem_base (mega.cu:865): LDS bytes the kernel needs besides the staged head tables. */
 int lxm_lds_base(void);
 /* LDS bytes a helper workgroup needs with head_lds bytes of head tables (the launch's LDS is
@@ -181,7 +185,7 @@ int lxm_t_sum(int kind, const float* x, int n, int rows, float* out, void* strea
    race, so issue them on one stream (or wait between them). */
 #define LXM_SCRATCH_MAXL 64
 #define LXM_SCRATCH_MAXNV 256
-#define LXM_SCRATCH_BYTES 4441856
+#define LXM_SCRATCH_BYTES 4572928
 int lxm_run_noalloc(const lxm_params* p_host, int n_blocks, int lds_bytes, void* stream);
 
 /* Cross-workgroup synchronisation costs, measured with the decode's own primitives (agent-scope

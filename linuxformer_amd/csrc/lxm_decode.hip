@@ -225,6 +225,54 @@ __device__ bool wait_stamps(const uint32_t* base, int n, uint32_t want, int32_t*
   }
 }
 
+// Stamped words (8 bytes: a 32-bit value low, the GDN event's sequence number high), written
+// and read whole at agent scope: a reader that sees the event's number in a word sees its value,
+// with no separate completion flag.
+__device__ __forceinline__ uint64_t ld64_rlx(const unsigned long long* p) {
+  return __hip_atomic_load(gp(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void st64_rlx(unsigned long long* p, uint32_t stamp, float v) {
+  __hip_atomic_store(gp(p), ((unsigned long long)stamp << 32) | fbits(v), __ATOMIC_RELAXED,
+                     __HIP_MEMORY_SCOPE_AGENT);
+}
+// Every thread's words base[idx[i]] (idx[i] < 0: none): waits until all the workgroup's words
+// carry the stamp want; v[i] their values (0 for none). False on an error or a timeout (code).
+template <int N>
+__device__ bool wait_words(const unsigned long long* base, const int (&idx)[N], uint32_t want,
+                           int32_t* err, int code, int* stop, float (&v)[N]) {
+  const int t = threadIdx.x;
+  const uint64_t t0 = wall();
+  bool mine = false;
+#pragma unroll
+  for (int i = 0; i < N; i++) v[i] = 0.0f;
+  for (;;) {
+    if (!mine) {
+      bool ok = true;
+#pragma unroll
+      for (int i = 0; i < N; i++) {
+        if (idx[i] >= 0) {
+          const uint64_t w = ld64_rlx(base + idx[i]);
+          v[i] = __uint_as_float((uint32_t)w);
+          ok = ok && (uint32_t)(w >> 32) == want;
+        }
+      }
+      mine = ok;
+    }
+    if (t == 0) {
+      int32_t e = __hip_atomic_load(gp(err), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if (!e && wall() - t0 > TIMEOUT_TICKS) {
+        __hip_atomic_fetch_max(gp(err), code, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        e = code;
+      }
+      *stop = e != 0;
+    }
+    const int all = __syncthreads_and(mine);
+    if (*stop) return false;
+    if (all) return true;
+    __builtin_amdgcn_s_sleep(1);
+  }
+}
+
 // The same for the head's keys: helper b = 1 .. n stores at S_KEY + 32 b a uint64 whose low 13
 // bits are the HEAD event's stamp; the workgroup waits for every stamp, then takes the largest
 // key (every valid key carries the same stamp, so the maximum is the maximum of the keys
@@ -1390,7 +1438,8 @@ __device__ void head_rows(const lxm_params& p, uint32_t stamp, const int32_t* lp
 // :330-380 with l2norm :242-245 in the model dtype, Qwen3_5RMSNormGated :168-184), by the
 // head's owner. Writes the head's gated-norm output (zeros when it has none) to p.ybuf.
 template <bool BF, bool E4>
-__device__ void gdn_head(const lxm_params& p, int L, int step, int vh, bool out, uint8_t* hx) {
+__device__ void gdn_head(const lxm_params& p, int L, int step, int vh, bool out, uint32_t seq,
+                         uint8_t* hx) {
   const int t = threadIdx.x, H = p.hidden, R = p.nv / p.nk, kh = vh / R;
   const int wv = t >> 6, lane = t & 63;
   float* qd = reinterpret_cast<float*>(hx + HX_QD);
@@ -1403,7 +1452,7 @@ __device__ void gdn_head(const lxm_params& p, int L, int step, int vh, bool out,
   float* dl = reinterpret_cast<float*>(hx + HX_DL);
   float* bs = reinterpret_cast<float*>(hx + HX_BS);
   int* misc = reinterpret_cast<int*>(hx + HX_MISC);
-  float* y = p.ybuf + (size_t)vh * VD;
+  unsigned long long* y = p.ybuf + (size_t)vh * VD;  // (stamped with seq)
 #ifdef LXM_SUBPROF
   // (the profiling build: wall-clock checkpoints of this step, summed per helper in LDS and
   // written out at the launch's end)
@@ -1416,7 +1465,7 @@ __device__ void gdn_head(const lxm_params& p, int L, int step, int vh, bool out,
 #endif
   const uint32_t tf = ld_rlx(p.mb_task + vh);
   if (tf == 0) {  // the step leaves this head alone: state unchanged, output exactly 0
-    if (out && t < VD) st_rlxf(y + t, 0.0f);
+    if (out && t < VD) st64_rlx(y + t, seq, 0.0f);
     return;
   }
   const float e = ld_rlxf(p.mb_e + vh);
@@ -1616,10 +1665,10 @@ __device__ void gdn_head(const lxm_params& p, int L, int step, int vh, bool out,
       for (int j = lane; j < VD; j += 64) {
         const float t1 = rd<BF>(ob[j] * rr);
         const float t2 = rd<BF>(gp(gw)[j] * t1);
-        st_rlxf(y + j, rd<BF>(t2 * silu(zb[j])));
+        st64_rlx(y + j, seq, rd<BF>(t2 * silu(zb[j])));
       }
     } else {  // no live query: o = 0, and so is every term the head gives out_proj
-      for (int j = lane; j < VD; j += 64) st_rlxf(y + j, 0.0f);
+      for (int j = lane; j < VD; j += 64) st64_rlx(y + j, seq, 0.0f);
     }
   }
   GH_MARK(4);
@@ -1651,16 +1700,31 @@ __device__ int out_prep(const lxm_params& p, int L, int ra, int rb, uint8_t* hx)
   return ne;
 }
 template <bool BF, bool E4>
-__device__ void out_rows(const lxm_params& p, int ra, int rb, int ne, uint8_t* hx) {
+__device__ bool out_rows(const lxm_params& p, int ra, int rb, int ne, uint32_t seq, uint8_t* hx) {
   const int t = threadIdx.x;
   int* op = reinterpret_cast<int*>(hx + HX_OP);
   uint8_t* oe = hx + HX_OE;
   float* oy = reinterpret_cast<float*>(hx + HX_OY);
-  for (int k = t; k < ne; k += NT) {
-    int d;
-    float w;
-    Ent<E4>::at(oe, k, d, w);
-    oy[k] = ld_rlxf(p.ybuf + d);
+  int* misc = reinterpret_cast<int*>(hx + HX_MISC);
+  static_assert(LXM_OUT_MAX <= 2 * NT, "two entries per thread");
+  {  // the head outputs the entries name, once every one carries this event's stamp
+    int idx[2];
+    float yv[2];
+#pragma unroll
+    for (int i = 0; i < 2; i++) {
+      const int k = t + i * NT;
+      idx[i] = -1;
+      if (k < ne) {
+        int d;
+        float w;
+        Ent<E4>::at(oe, k, d, w);
+        idx[i] = d;
+      }
+    }
+    if (!wait_words<2>(p.ybuf, idx, seq, p.err, 5, &misc[6], yv)) return false;
+#pragma unroll
+    for (int i = 0; i < 2; i++)
+      if (t + i * NT < ne) oy[t + i * NT] = yv[i];
   }
   lds_barrier();
   if (t < rb - ra) {
@@ -1681,6 +1745,7 @@ __device__ void out_rows(const lxm_params& p, int ra, int rb, int ne, uint8_t* h
     }
     st_rlxf(p.xo + ra + t, rd<BF>(s));
   }
+  return true;
 }
 
 template <bool BF, bool E4>
@@ -1756,30 +1821,34 @@ __device__ void run_helper(const lxm_params& p) {
       if (evh && t == 0) evh[0] += wall();
 #endif
       if (owner) {
-        gdn_head<BF, E4>(p, L, step, vh, out, hx);
-        drain();
-        __syncthreads();
+        // (its output goes out as stamped words; without a live query the chain waits for
+        // every head's state instead, so the head then drains and stamps it)
+        gdn_head<BF, E4>(p, L, step, vh, out, seq, hx);
+        if (!out) {
+          drain();
+          __syncthreads();
+          if (t == 0) st_rlx(p.sync + S_OWN + 32 * vh, seq);
+        }
 #ifdef LXM_SUBPROF
         if (evh && t == 0) evh[1] += wall();
 #endif
-        if (t == 0) st_rlx(p.sync + S_OWN + 32 * vh, seq);
       }
       uint64_t w2 = 0;
       if (PROF_ON) {
         w2 = cycles();
         pr[2] += w2 - w1;
       }
-      if (out && b <= no) {  // the out_proj helpers: every value head's output, then the rows
-        if (rb > ra) {
-          const int ne = out_prep<BF, E4>(p, L, ra, rb, hx);
-          if (!wait_stamps(p.sync + S_OWN, p.nv, seq, p.err, 5, &misc[6])) return;
+      if (out && b <= no && rb > ra) {  // the out_proj helpers: their rows, as stamped words,
+        // from every value head's stamped output
+        const int ne = out_prep<BF, E4>(p, L, ra, rb, hx);
+        if (!out_rows<BF, E4>(p, ra, rb, ne, seq, hx)) return;
 #ifdef LXM_SUBPROF
-          if (evh && t == 0) evh[2] += wall();
+        if (evh && t == 0) evh[2] += wall();
 #endif
-          out_rows<BF, E4>(p, ra, rb, ne, hx);
-          drain();
-          __syncthreads();
-        }
+        drain();
+        __syncthreads();
+      }
+      if (out && b <= no) {
 #ifdef LXM_SUBPROF
         if (evh && t == 0) evh[3] += wall();
 #endif
@@ -1897,7 +1966,7 @@ __global__ void __launch_bounds__(NT) k_sum(int kind, const float* x, int n, flo
 #define SC_MBTASK (SC_MBQK + 4 * LXM_MAXQKL)
 #define SC_MBE (SC_MBTASK + 4 * LXM_SCRATCH_MAXNV)
 #define SC_YBUF (SC_MBE + 4 * LXM_SCRATCH_MAXNV)
-#define SC_RRING (SC_YBUF + 4 * LXM_SCRATCH_MAXNV * VD)
+#define SC_RRING (SC_YBUF + 8 * LXM_SCRATCH_MAXNV * VD)
 #define SC_RING (SC_RRING + 4 * 4 * LXM_SCRATCH_MAXL)
 #define SC_END (SC_RING + 4 * 4 * LXM_SCRATCH_MAXL * MAXH)
 static_assert(sizeof(lxm_params) <= SC_SYNC, "the parameter block fits its slot");
@@ -1907,11 +1976,12 @@ static_assert(SC_KEYS % 256 == 0 && SC_RING % 256 == 0 && SC_YBUF % 256 == 0, "a
 static __device__ __align__(256) uint8_t scratch[LXM_SCRATCH_BYTES];
 
 // the parameter block into the scratch's slot, and the words that must start at zero cleared:
-// the sync area, the head keys and the caller's error word
+// the sync area, the head keys, the value heads' stamped outputs and the caller's error word
 __global__ void __launch_bounds__(256) k_noalloc_prep(lxm_params p, uint8_t* sc) {
   if (threadIdx.x == 0) *reinterpret_cast<lxm_params*>(sc + SC_PARAMS) = p;
   uint32_t* sync = reinterpret_cast<uint32_t*>(sc + SC_SYNC);
   for (int i = threadIdx.x; i < LXM_NSYNC; i += blockDim.x) sync[i] = 0u;
+  for (int i = threadIdx.x; i < p.nv * VD; i += blockDim.x) p.ybuf[i] = 0ull;
   if (threadIdx.x < 2) reinterpret_cast<unsigned long long*>(sc + SC_KEYS)[threadIdx.x] = 0ull;
   if (threadIdx.x == 0) *p.err = 0;
 }
@@ -1964,6 +2034,7 @@ int lxm_helper_lds(int head_lds) { return HX_END + head_lds + 256; }  // (reads 
 // the shapes the sync area and the stamped keys hold
 static bool launch_ok(const lxm_params* p, int n_blocks) {
   return p && n_blocks >= 2 && n_blocks <= LXM_MAXBLOCKS && p->n_blocks == n_blocks &&
+         p->n_tokens >= 0 && (int64_t)p->n_tokens * (p->n_layers + 1) < (int64_t)SEQ_MASK &&
          p->vocab <= LXM_MAXVOCAB && p->nv >= 1 && p->nv <= LXM_SCRATCH_MAXNV && p->nk >= 1 &&
          p->nk <= F_KEYW - F_KH;
 }
@@ -1990,7 +2061,7 @@ int lxm_run_noalloc(const lxm_params* p_host, int n_blocks, int lds_bytes, void*
   p.mb_task = reinterpret_cast<uint32_t*>(sc + SC_MBTASK);
   p.mb_e = reinterpret_cast<float*>(sc + SC_MBE);
   p.mb_qk = reinterpret_cast<float*>(sc + SC_MBQK);
-  p.ybuf = reinterpret_cast<float*>(sc + SC_YBUF);
+  p.ybuf = reinterpret_cast<unsigned long long*>(sc + SC_YBUF);
   p.xo = reinterpret_cast<float*>(sc + SC_XO);
   hipLaunchKernelGGL(k_noalloc_prep, dim3(1), dim3(256), 0, (hipStream_t)stream, p, sc);
   e = hipGetLastError();

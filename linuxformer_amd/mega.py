@@ -378,7 +378,8 @@ class Mega:
         self.mb_task = torch.zeros(d.nv, dtype=torch.int32, device=dev)
         self.mb_e = torch.zeros(d.nv, dtype=torch.float32, device=dev)
         self.mb_qk = torch.zeros(MAXQKL, dtype=torch.float32, device=dev)
-        self.ybuf = torch.zeros(d.nv * VD, dtype=torch.float32, device=dev)
+        # stamped words (a float low, the event's number high), zeroed for every launch
+        self.ybuf = torch.zeros(d.nv * VD, dtype=torch.int64, device=dev)
         self.xo = torch.zeros(MAXH, dtype=torch.float32, device=dev)
         self.hn = torch.zeros(MAXH, dtype=torch.float32, device=dev)
         self.sync = torch.zeros(NSYNC, dtype=torch.int32, device=dev)
@@ -434,7 +435,7 @@ class Mega:
                 out["GDN event timeline (us after the post, mean over events)"] = {
                     "events": ne, "helpers saw it (mean, max)": [round(sum(seen) / len(seen), 3), max(seen)],
                     "value head stored (mean, max)": [round(sum(own) / len(own), 3), max(own)] if own else None,
-                    "out_proj helpers saw every head (mean, max)": [round(sum(cvh) / len(cvh), 3), max(cvh)] if cvh else None,
+                    "out_proj helpers had every head and their rows (mean, max)": [round(sum(cvh) / len(cvh), 3), max(cvh)] if cvh else None,
                     "out_proj rows stored (mean, max)": [round(sum(odone) / len(odone), 3), max(odone)] if odone else None,
                     "chain saw every helper": us(c[ev + 1])}
                 gb = ev + 4 + 4 * self.ncta
@@ -493,7 +494,7 @@ class Mega:
                              ("hn", self.hn.numel() * 4), ("sync", NSYNC * 4), ("keys", 16),
                              ("err", 4), ("mb_task", self.mb_task.numel() * 4),
                              ("mb_e", self.mb_e.numel() * 4), ("mb_qk", self.mb_qk.numel() * 4),
-                             ("ybuf", self.ybuf.numel() * 4), ("xo", self.xo.numel() * 4)):
+                             ("ybuf", self.ybuf.numel() * 8), ("xo", self.xo.numel() * 4)):
             lines.append(f"zero {name} {nbytes}")
         if prof:
             lines.append(f"zero prof {8 * self.prof_size}")
@@ -562,6 +563,7 @@ class Mega:
         f = np.asarray(forced, np.int64)
         if f.min() < 0 or f.max() >= self.vocab:
             raise ValueError("forced token out of range")
+        self._check_events(n)
         d = self.dims
         rs, cs = self._state_ptrs()
         ft = torch.tensor(f.astype(np.int32), device=self.dev)
@@ -577,6 +579,7 @@ class Mega:
         self.sync.zero_()
         self.keys.zero_()
         self.err.zero_()
+        self.ybuf.zero_()
         p = self._params(rs, cs, ft, len(f), n, preds, inputs, trace, prof, self._bufs())
         pd = torch.frombuffer(bytearray(bytes(p)), dtype=torch.uint8).to(self.dev)
         self._keep = (rs, cs, ft, pd)
@@ -604,6 +607,7 @@ class Mega:
         for t in (forced, preds, err):
             assert t.dtype == torch.int32 and t.device == self.dev and t.is_contiguous()
         assert forced.numel() >= 1 and n >= 1 and preds.numel() >= n and err.numel() >= 1
+        self._check_events(n)
         if inputs is not None:
             assert inputs.dtype == torch.int32 and inputs.numel() >= n and inputs.device == self.dev
         rs, cs = self._state_ptrs_cached()
@@ -613,6 +617,13 @@ class Mega:
         e = self.lib.lxm_run_noalloc(ctypes.byref(p), self.ncta, self.lds, st)
         if e:
             raise RuntimeError(f"mega launch failed: hipError {e}")
+
+    def _check_events(self, n: int) -> None:
+        """A launch numbers its events (n_layers + 1 per token) in 24 bits, as the stamped
+        words carry them."""
+        if n * (self.dims.n_layers + 1) >= 1 << 24:
+            raise ValueError(f"{n} tokens: at most {((1 << 24) - 1) // (self.dims.n_layers + 1)} "
+                             "per launch")
 
     def _state_ptrs_cached(self):
         """The state pointer arrays, built once (the cache's tensors stay where they are)."""
