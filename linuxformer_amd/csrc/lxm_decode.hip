@@ -1643,8 +1643,33 @@ __device__ void gdn_head(const lxm_params& p, int L, int step, int vh, bool out,
         ob[t] = rd<BF>(o);
       }
     }
-    // the state's written rows, after the barriers above (a barrier waits for earlier stores);
-    // the caller's drain waits for them
+    if (out) {
+      __syncthreads();
+      // the gated norm on this value head (one wave), gate z: y = D(D(w * D(o * r)) * silu(z)),
+      // issued before any wave stores the state's rows, so that the output does not queue
+      // behind them in the CU's memory pipeline
+      if (wv == 0) {
+        const float* gw = reinterpret_cast<const float*>(p.blob + ly.gnorm);
+        if (nq > 0) {
+          float sq = 0.0f;
+          for (int j = lane; j < VD; j += 64) sq = sq + ob[j] * ob[j];
+          sq = sum64(sq);
+          const float rr = rsqrt_(sq / (float)VD + hd.geps);
+          for (int j = lane; j < VD; j += 64) {
+            const float t1 = rd<BF>(ob[j] * rr);
+            const float t2 = rd<BF>(gp(gw)[j] * t1);
+            st64_rlx(y + j, seq, rd<BF>(t2 * silu(zb[j])));
+          }
+        } else {  // no live query: o = 0, and so is every term the head gives out_proj
+          for (int j = lane; j < VD; j += 64) st64_rlx(y + j, seq, 0.0f);
+        }
+      }
+      GH_MARK(4);
+      __syncthreads();
+    }
+    // the state's written rows (each thread stores the blocks it alone reads at the next step,
+    // so its own later loads see them; a drain before the head's completion stamp covers them
+    // where the chain waits for the states)
 #pragma unroll
     for (int i = 0; i < 16; i++) {
       const int r = rb * 16 + i;
@@ -1652,26 +1677,6 @@ __device__ void gdn_head(const lxm_params& p, int L, int step, int vh, bool out,
     }
   }
   GH_MARK(3);
-  if (!out) return;
-  __syncthreads();
-  // the gated norm on this value head (one wave), gate z: y = D(D(w * D(o * r)) * silu(z))
-  if (wv == 0) {
-    const float* gw = reinterpret_cast<const float*>(p.blob + ly.gnorm);
-    if (nq > 0) {
-      float s = 0.0f;
-      for (int j = lane; j < VD; j += 64) s = s + ob[j] * ob[j];
-      s = sum64(s);
-      const float rr = rsqrt_(s / (float)VD + hd.geps);
-      for (int j = lane; j < VD; j += 64) {
-        const float t1 = rd<BF>(ob[j] * rr);
-        const float t2 = rd<BF>(gp(gw)[j] * t1);
-        st64_rlx(y + j, seq, rd<BF>(t2 * silu(zb[j])));
-      }
-    } else {  // no live query: o = 0, and so is every term the head gives out_proj
-      for (int j = lane; j < VD; j += 64) st64_rlx(y + j, seq, 0.0f);
-    }
-  }
-  GH_MARK(4);
 #ifdef LXM_SUBPROF
   if (gpr && t == 0 && dec) gpr[6] += wall() - g0;
 #endif
