@@ -610,17 +610,23 @@ __global__ __launch_bounds__(256) void pf_tail(const lxm_pf_params* __restrict__
 // The recurrence of one value-head slot over the layer's candidates, in position order
 // (torch_recurrent_gated_delta_rule, TF:330-380, one token at a time): S <- S * exp(g) when
 // exp(g) != 1; with a live query or key kv = S^T k, delta = (v - kv) beta, S += k delta^T,
-// o = D(S^T q) into the record (over v, which this step has read). The state tile stays in registers: thread (cg, rb) holds columns 4cg..4cg+3 of
-// rows 16rb..16rb+15, one of ATen's 16-row cascade blocks (torch .sum(-2) on the CPU).
+// o = D(S^T q) into the record (over v, which this step has read). A slot's 128 state columns
+// are split over DQ workgroups of DW columns (no sum crosses columns, so each column's sums are
+// those of the whole tile, and a step's arithmetic is spread over four CUs). The state tile
+// stays in registers: thread (c, rb) holds column c0 + c of rows 16rb..16rb+15, one of ATen's
+// 16-row cascade blocks (torch .sum(-2) on the CPU).
+#define DQ 4
+#define DW (VD / DQ)
+static_assert(NT == 16 * DW, "16 row blocks of DW columns");
 // A candidate's inputs as one thread of the delta kernel holds them (loaded three candidates ahead):
 // the header word, the slot's decay factor, and the thread's share of k and q (threads < 256) or
-// v (256..383), and beta (thread 0).
+// of the workgroup's DW values of v (256..256 + DW - 1), and beta (thread 0).
 struct DeltaIn {
   uint32_t live;
   float e, a, b, beta;
 };
 __device__ __forceinline__ DeltaIn delta_in(const uint8_t* rec, const RecOff& ro, int vslot,
-                                            int kslot) {
+                                            int kslot, int c0) {
   const int t = threadIdx.x;
   DeltaIn d;
   d.live = reinterpret_cast<const uint32_t*>(rec)[1];
@@ -630,8 +636,8 @@ __device__ __forceinline__ DeltaIn delta_in(const uint8_t* rec, const RecOff& ro
     if (t < KD) {
       d.a = reinterpret_cast<const float*>(rec + ro.k)[kslot * KD + t];
       d.b = reinterpret_cast<const float*>(rec + ro.q)[kslot * KD + t];
-    } else if (t < KD + VD) {
-      d.a = reinterpret_cast<const float*>(rec + ro.v)[vslot * VD + t - KD];
+    } else if (t < KD + DW) {
+      d.a = reinterpret_cast<const float*>(rec + ro.v)[vslot * VD + c0 + t - KD];
     }
     if (t == 0) d.beta = reinterpret_cast<const float*>(rec + ro.b)[vslot];
   }
@@ -640,35 +646,35 @@ __device__ __forceinline__ DeltaIn delta_in(const uint8_t* rec, const RecOff& ro
 
 template <bool BF>
 __global__ __launch_bounds__(NT) void pf_delta(const lxm_pf_params* __restrict__ pp, int L) {
-  __shared__ __align__(16) float kn[KD], qn[KD], vb[VD], dl[VD];
-  __shared__ __align__(16) float bs[16 * VD];
+  __shared__ __align__(16) float kn[KD], qn[KD], vb[DW], dl[DW];
+  __shared__ __align__(16) float bs[16 * DW];
   __shared__ float beta_s;
   const lxm_pf_params& p = *pp;
   const lxm_pf_layer& ly = p.layers[L];
-  const int t = threadIdx.x, vslot = blockIdx.x;
+  const int t = threadIdx.x, vslot = blockIdx.x / DQ, c0 = (blockIdx.x % DQ) * DW;
   // everything the loop needs in registers: its stores to the records could alias p and ly
   const lxm_pf_vs sv = tab<lxm_pf_vs>(p.blob, ly.vs)[vslot];
   const RecOff ro(ly.n_ks, ly.n_vs);
   const int count = p.count[L];
   const int64_t rec_b = ly.rec_bytes;
   uint8_t* const recs = p.recs;
-  const int cg = t & 31, rb = t >> 5;
-  v4f* S4 = reinterpret_cast<v4f*>(p.rec[L] + (size_t)sv.vh * KD * VD);
-  v4f s[16];
+  const int c = t % DW, rb = t / DW;
+  float* S = p.rec[L] + (size_t)sv.vh * KD * VD + c0 + c;
+  float s[16];
 #pragma unroll
-  for (int i = 0; i < 16; i++) s[i] = S4[(rb * 16 + i) * (VD / 4) + cg];
+  for (int i = 0; i < 16; i++) s[i] = S[(rb * 16 + i) * VD];
   bool wrote = false;
-  // the inputs of the next three candidates in flight (a step takes about one load's latency)
+  // the inputs of the next three candidates in flight
   DeltaIn n1 = {}, n2 = {}, n3 = {};
-  if (count > 0) n1 = delta_in(recs, ro, vslot, sv.kslot);
-  if (count > 1) n2 = delta_in(recs + rec_b, ro, vslot, sv.kslot);
-  if (count > 2) n3 = delta_in(recs + 2 * rec_b, ro, vslot, sv.kslot);
+  if (count > 0) n1 = delta_in(recs, ro, vslot, sv.kslot, c0);
+  if (count > 1) n2 = delta_in(recs + rec_b, ro, vslot, sv.kslot, c0);
+  if (count > 2) n3 = delta_in(recs + 2 * rec_b, ro, vslot, sv.kslot, c0);
   for (int j = 0; j < count; j++) {
     uint8_t* rec = recs + (int64_t)j * rec_b;
     const DeltaIn cur = n1;
     n1 = n2;
     n2 = n3;
-    if (j + 3 < count) n3 = delta_in(rec + 3 * rec_b, ro, vslot, sv.kslot);
+    if (j + 3 < count) n3 = delta_in(rec + 3 * rec_b, ro, vslot, sv.kslot, c0);
     const bool live = sv.kslot >= 0 && ((cur.live >> sv.kslot) & 1u);
     const float e = cur.e;
     int proc = 0;
@@ -684,7 +690,7 @@ __global__ __launch_bounds__(NT) void pf_delta(const lxm_pf_params* __restrict__
         if (t < KD) {
           kn[t] = cur.a;
           qn[t] = cur.b;
-        } else if (t < KD + VD) {
+        } else if (t < KD + DW) {
           vb[t - KD] = cur.a;
         }
         if (t == 0) beta_s = cur.beta;
@@ -697,50 +703,47 @@ __global__ __launch_bounds__(NT) void pf_delta(const lxm_pf_params* __restrict__
           kr[i] = kn[rb * 16 + i];
           qr[i] = qn[rb * 16 + i];
         }
-        v4f a = {0.0f, 0.0f, 0.0f, 0.0f};
+        float a = 0.0f;
 #pragma unroll
-        for (int i = 0; i < 16; i++) {
-          const v4f m = v4f{a.x + s[i].x * kr[i], a.y + s[i].y * kr[i], a.z + s[i].z * kr[i], a.w + s[i].w * kr[i]};
-          a = kr[i] != 0.0f ? m : a;
-        }
-        reinterpret_cast<v4f*>(bs + rb * VD)[cg] = a;
+        for (int i = 0; i < 16; i++) a = kr[i] != 0.0f ? a + s[i] * kr[i] : a;
+        bs[rb * DW + c] = a;
         __syncthreads();
-        if (t < VD) {
+        if (t < DW) {
           float kv = 0.0f;
 #pragma unroll
-          for (int q = 0; q < 16; q++) kv = kv + bs[q * VD + t];
+          for (int q = 0; q < 16; q++) kv = kv + bs[q * DW + t];
           dl[t] = (vb[t] - kv) * beta_s;
         }
         __syncthreads();
-        const v4f d = reinterpret_cast<const v4f*>(dl)[cg];
-        v4f o = {0.0f, 0.0f, 0.0f, 0.0f};
+        const float d = dl[c];
+        float o = 0.0f;
 #pragma unroll
         for (int i = 0; i < 16; i++) {
           // (the update keeps rows with a zero key factor exactly as they are: -0 stays -0)
-          const v4f u = v4f{s[i].x + kr[i] * d.x, s[i].y + kr[i] * d.y, s[i].z + kr[i] * d.z, s[i].w + kr[i] * d.w};
-          s[i] = kr[i] != 0.0f ? u : s[i];
-          const v4f m = v4f{o.x + s[i].x * qr[i], o.y + s[i].y * qr[i], o.z + s[i].z * qr[i], o.w + s[i].w * qr[i]};
-          o = qr[i] != 0.0f ? m : o;
+          s[i] = kr[i] != 0.0f ? s[i] + kr[i] * d : s[i];
+          o = qr[i] != 0.0f ? o + s[i] * qr[i] : o;
         }
-        reinterpret_cast<v4f*>(bs + rb * VD)[cg] = o;
+        bs[rb * DW + c] = o;  // (the kv sums read bs before the barrier above)
         __syncthreads();
         // o = D(the block sums in order), into the record (over v: read at this step's start);
         // the gated norm is pf_out's
-        if (t < VD) {
+        if (t < DW) {
           float q = 0.0f;
 #pragma unroll
-          for (int b = 0; b < 16; b++) q = q + bs[b * VD + t];
-          reinterpret_cast<float*>(rec + ro.v)[vslot * VD + t] = rd<BF>(q);
+          for (int b = 0; b < 16; b++) q = q + bs[b * DW + t];
+          reinterpret_cast<float*>(rec + ro.v)[vslot * VD + c0 + t] = rd<BF>(q);
         }
       }
     }
-    if (t == 0) reinterpret_cast<int32_t*>(rec + ro.pr)[vslot] = proc;
+    if (t == 0 && c0 == 0) reinterpret_cast<int32_t*>(rec + ro.pr)[vslot] = proc;
   }
   if (wrote) {
 #pragma unroll
-    for (int i = 0; i < 16; i++) S4[(rb * 16 + i) * (VD / 4) + cg] = s[i];
+    for (int i = 0; i < 16; i++) S[(rb * 16 + i) * VD] = s[i];
   }
 }
+#undef DQ
+#undef DW
 
 // ---------------------------------------------------------------------------------------------
 // The gated norm of each head that ran (TF:168-184): y = D(D(w * D(o * r)) * silu(z)), r =
@@ -948,7 +951,8 @@ static hipError_t run_layers(const lxm_pf_params* ph, const lxm_pf_params* pd, i
     hipLaunchKernelGGL(pf_compact, dim3(1), dim3(C_NT), 0, st, pd, L);
     hipLaunchKernelGGL(pf_act<BF>, dim3(ACT_GRID), dim3(NT), ACT_LDS, st, pd, L);
     hipLaunchKernelGGL(pf_tail<BF>, dim3((ph->n_conv + 255) / 256), dim3(256), 0, st, pd, L);
-    if (ly.n_vs > 0) hipLaunchKernelGGL(pf_delta<BF>, dim3(ly.n_vs), dim3(NT), 0, st, pd, L);
+    // (four workgroups per value-head slot, 32 state columns each)
+    if (ly.n_vs > 0) hipLaunchKernelGGL(pf_delta<BF>, dim3(4 * ly.n_vs), dim3(NT), 0, st, pd, L);
     if (ly.n_vs > 0)
       hipLaunchKernelGGL(pf_out<BF>, dim3(OUT_GRID), dim3(NT), 4 * VD * ly.n_vs + 16, st, pd, L);
   }
