@@ -612,18 +612,22 @@ __global__ __launch_bounds__(256) void pf_tail(const lxm_pf_params* __restrict__
 // exp(g) != 1; with a live query or key kv = S^T k, delta = (v - kv) beta, S += k delta^T,
 // o = D(S^T q) into the record (over v, which this step has read). A slot's 128 state columns
 // are split over DQ workgroups of DW columns (no sum crosses columns, so each column's sums are
-// those of the whole tile, and a step's arithmetic is spread over four CUs). The state tile
+// those of the whole tile, and a step's arithmetic is spread over DQ CUs; 8 and 16 workgroups
+// of 16 and 8 columns measured the same as 4). The state tile
 // stays in registers: thread (c, rb) holds column c0 + c of rows 16rb..16rb+15, one of ATen's
 // 16-row cascade blocks (torch .sum(-2) on the CPU).
-#define DQ 4
+#define PF_DQ 4
+#define DQ PF_DQ
 #define DW (VD / DQ)
-static_assert(NT == 16 * DW, "16 row blocks of DW columns");
+#define NTD (16 * DW)
+static_assert(NTD >= KD || NTD * 2 == KD, "k and q: one or two per thread");
 // A candidate's inputs as one thread of the delta kernel holds them (loaded three candidates ahead):
-// the header word, the slot's decay factor, and the thread's share of k and q (threads < 256) or
-// of the workgroup's DW values of v (256..256 + DW - 1), and beta (thread 0).
+// the header word, the slot's decay factor, the thread's share of k and q, of the workgroup's DW
+// values of v (threads VT .. VT + DW - 1), and beta (thread 0).
+#define VT (NTD >= KD + DW ? KD : 0)
 struct DeltaIn {
   uint32_t live;
-  float e, a, b, beta;
+  float e, k, q, k2, q2, v, beta;
 };
 __device__ __forceinline__ DeltaIn delta_in(const uint8_t* rec, const RecOff& ro, int vslot,
                                             int kslot, int c0) {
@@ -631,21 +635,26 @@ __device__ __forceinline__ DeltaIn delta_in(const uint8_t* rec, const RecOff& ro
   DeltaIn d;
   d.live = reinterpret_cast<const uint32_t*>(rec)[1];
   d.e = reinterpret_cast<const float*>(rec + ro.e)[vslot];
-  d.a = d.b = d.beta = 0.0f;
+  d.k = d.q = d.k2 = d.q2 = d.v = d.beta = 0.0f;
   if (kslot >= 0) {
+    const float* kk = reinterpret_cast<const float*>(rec + ro.k) + kslot * KD;
+    const float* qq = reinterpret_cast<const float*>(rec + ro.q) + kslot * KD;
     if (t < KD) {
-      d.a = reinterpret_cast<const float*>(rec + ro.k)[kslot * KD + t];
-      d.b = reinterpret_cast<const float*>(rec + ro.q)[kslot * KD + t];
-    } else if (t < KD + DW) {
-      d.a = reinterpret_cast<const float*>(rec + ro.v)[vslot * VD + c0 + t - KD];
+      d.k = kk[t];
+      d.q = qq[t];
     }
+    if (NTD < KD) {
+      d.k2 = kk[NTD + t];
+      d.q2 = qq[NTD + t];
+    }
+    if (t >= VT && t < VT + DW) d.v = reinterpret_cast<const float*>(rec + ro.v)[vslot * VD + c0 + t - VT];
     if (t == 0) d.beta = reinterpret_cast<const float*>(rec + ro.b)[vslot];
   }
   return d;
 }
 
 template <bool BF>
-__global__ __launch_bounds__(NT) void pf_delta(const lxm_pf_params* __restrict__ pp, int L) {
+__global__ __launch_bounds__(NTD) void pf_delta(const lxm_pf_params* __restrict__ pp, int L) {
   __shared__ __align__(16) float kn[KD], qn[KD], vb[DW], dl[DW];
   __shared__ __align__(16) float bs[16 * DW];
   __shared__ float beta_s;
@@ -688,11 +697,14 @@ __global__ __launch_bounds__(NT) void pf_delta(const lxm_pf_params* __restrict__
       if (live) {
         proc = 2;
         if (t < KD) {
-          kn[t] = cur.a;
-          qn[t] = cur.b;
-        } else if (t < KD + DW) {
-          vb[t - KD] = cur.a;
+          kn[t] = cur.k;
+          qn[t] = cur.q;
         }
+        if (NTD < KD) {
+          kn[NTD + t] = cur.k2;
+          qn[NTD + t] = cur.q2;
+        }
+        if (t >= VT && t < VT + DW) vb[t - VT] = cur.v;
         if (t == 0) beta_s = cur.beta;
         __syncthreads();
         // the thread's 16 rows of k and q at once (one LDS wait), then the cascade blocks'
@@ -744,6 +756,8 @@ __global__ __launch_bounds__(NT) void pf_delta(const lxm_pf_params* __restrict__
 }
 #undef DQ
 #undef DW
+#undef NTD
+#undef VT
 
 // ---------------------------------------------------------------------------------------------
 // The gated norm of each head that ran (TF:168-184): y = D(D(w * D(o * r)) * silu(z)), r =
@@ -951,8 +965,9 @@ static hipError_t run_layers(const lxm_pf_params* ph, const lxm_pf_params* pd, i
     hipLaunchKernelGGL(pf_compact, dim3(1), dim3(C_NT), 0, st, pd, L);
     hipLaunchKernelGGL(pf_act<BF>, dim3(ACT_GRID), dim3(NT), ACT_LDS, st, pd, L);
     hipLaunchKernelGGL(pf_tail<BF>, dim3((ph->n_conv + 255) / 256), dim3(256), 0, st, pd, L);
-    // (four workgroups per value-head slot, 32 state columns each)
-    if (ly.n_vs > 0) hipLaunchKernelGGL(pf_delta<BF>, dim3(4 * ly.n_vs), dim3(NT), 0, st, pd, L);
+    // (PF_DQ workgroups per value-head slot, 128 / PF_DQ state columns each)
+    if (ly.n_vs > 0)
+      hipLaunchKernelGGL(pf_delta<BF>, dim3(PF_DQ * ly.n_vs), dim3(16 * VD / PF_DQ), 0, st, pd, L);
     if (ly.n_vs > 0)
       hipLaunchKernelGGL(pf_out<BF>, dim3(OUT_GRID), dim3(NT), 4 * VD * ly.n_vs + 16, st, pd, L);
   }
