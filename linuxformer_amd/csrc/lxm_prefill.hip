@@ -337,8 +337,13 @@ __global__ __launch_bounds__(NT) void pf_tile(const lxm_pf_params* __restrict__ 
                           : v4f{0.0f, 0.0f, 0.0f, 0.0f};
       const float na = -cr_exp(d.A_log);
 #pragma unroll
-      for (int k = 0; k < TT; k++)
-        if (cr_exp(na * softplus(a[k] + d.dt_bias)) != 1.0f) atomicOr(smask + k, 0x80000000u);
+      for (int k = 0; k < TT; k++) {
+        // (x < -104: exp(x) rounds to 0, so softplus(x) is 0 and, na being finite, exp(na * 0)
+        // is 1 without evaluating it)
+        const float x = a[k] + d.dt_bias;
+        if (x < -104.0f && na > -__builtin_inff()) continue;
+        if (cr_exp(na * softplus(x)) != 1.0f) atomicOr(smask + k, 0x80000000u);
+      }
     }
     __syncthreads();
     if (t < TT && b * TT + t < p.T) p.mask[b * TT + t] = smask[t];
@@ -555,7 +560,9 @@ __global__ __launch_bounds__(NT) void pf_act(const lxm_pf_params* __restrict__ p
       if (sv.dslot >= 0) {
         const lxm_pf_dec d = dc[sv.dslot];
         const float a = d.len ? rd<BF>(dot1<BF>(ent + d.start, d.len, sm)) : 0.0f;
-        e = cr_exp((-cr_exp(d.A_log)) * softplus(a + d.dt_bias));
+        const float na = -cr_exp(d.A_log), x = a + d.dt_bias;
+        // (x < -104: softplus(x) is 0, and exp(na * 0) is 1 for a finite na)
+        if (!(x < -104.0f && na > -__builtin_inff())) e = cr_exp(na * softplus(x));
       }
       reinterpret_cast<float*>(rec + ro.e)[i] = e;
       if (sv.kslot >= 0 && ((live >> sv.kslot) & 1u)) {
