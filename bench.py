@@ -436,7 +436,9 @@ def prefill_leg(args, dev, hf_holder: dict) -> dict:
     torch.cuda.synchronize()
     ms = []
     for k in range(calls):
-        toks = synth.tokens(spec, T, 1 + k)
+        # the call's tokens resident on the device before the timed region (the kernel checks
+        # their range into the error word)
+        toks = torch.from_numpy(np.asarray(synth.tokens(spec, T, 1 + k), np.int32)).to(dev)
         e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         torch.cuda.synchronize()
         e0.record(stream)
@@ -444,6 +446,8 @@ def prefill_leg(args, dev, hf_holder: dict) -> dict:
         e1.record(stream)
         torch.cuda.synchronize()
         ms.append(e0.elapsed_time(e1))
+        if int(pf.err.item()):
+            raise RuntimeError("verified prefill: a token out of range")
         nc = int(pf.count[:d.n_layers].sum())
         log(f"[bench] verified-prefill call {k + 1}/{calls}: {T} tokens in {ms[-1]:.2f} ms "
             f"({nc} candidate positions over the layers)")

@@ -26,6 +26,13 @@ __device__ __forceinline__ uint32_t fbits(float x) { return __float_as_uint(x); 
 // from finite inputs in the decode)
 __device__ __forceinline__ float bf16r(float x) { return (float)(__bf16)x; }
 __device__ __forceinline__ float bf16f(uint32_t hi16) { return bitsf(hi16 << 16); }
+// the same for two values by one conversion (one v_cvt_pk_bf16_f32 for the pair)
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ f32x2 bf16r2(f32x2 v) {
+  typedef __bf16 bf2 __attribute__((ext_vector_type(2)));
+  const uint32_t u = __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf2));
+  return f32x2{bitsf(u << 16), bitsf(u & 0xffff0000u)};
+}
 
 // the model dtype's rounding
 template <bool BF>

@@ -95,15 +95,19 @@ template <bool BF>
 __device__ __forceinline__ v4f acc4(v4f s, v4f x, float w) {
   return v4f{acc<BF>(s.x, x.x, w), acc<BF>(s.y, x.y, w), acc<BF>(s.z, x.z, w), acc<BF>(s.w, x.w, w)};
 }
+// (bf16: the four roundings as two paired conversions)
 template <bool BF>
 __device__ __forceinline__ v4f rd4(v4f v) {
-  return v4f{rd<BF>(v.x), rd<BF>(v.y), rd<BF>(v.z), rd<BF>(v.w)};
+  if constexpr (BF) {
+    const f32x2 a = bf16r2(f32x2{v.x, v.y}), b = bf16r2(f32x2{v.z, v.w});
+    return v4f{a.x, a.y, b.x, b.y};
+  }
+  return v;
 }
 // D((h * r) * w1) per position: the RMSNorm's output (TF:720-737)
 template <bool BF>
 __device__ __forceinline__ v4f norm4(v4f h, v4f r, float w1) {
-  return v4f{rd<BF>((h.x * r.x) * w1), rd<BF>((h.y * r.y) * w1), rd<BF>((h.z * r.z) * w1),
-             rd<BF>((h.w * r.w) * w1)};
+  return rd4<BF>(v4f{(h.x * r.x) * w1, (h.y * r.y) * w1, (h.z * r.z) * w1, (h.w * r.w) * w1});
 }
 __device__ __forceinline__ float norm_r(float ss, int H, float eps) {
   return rsqrt_(ss / (float)H + eps);

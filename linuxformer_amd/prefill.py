@@ -371,6 +371,17 @@ class Prefill:
         self._T = T
 
     def _state_ptrs(self, cache):
+        """The cache's state pointer arrays on the device (kept per set of pointers: the cache's
+        tensors stay where they are, so later calls copy nothing to the device)."""
+        key = tuple((cache.layers[L].recurrent_states[0].data_ptr(),
+                     cache.layers[L].conv_states[0].data_ptr()) for L in range(self.dims.n_layers))
+        memo = self.__dict__.setdefault("_ptrs_memo", {})
+        if key not in memo:
+            memo.clear()
+            memo[key] = self._state_ptrs_new(cache)
+        return memo[key]
+
+    def _state_ptrs_new(self, cache):
         rs, cs = [], []
         d = self.dims
         for L in range(d.n_layers):
@@ -393,13 +404,26 @@ class Prefill:
         return p, pd
 
     def bind(self, T: int, cache=None, buf: "PfBuffers | None" = None):
-        """(host block, device block, tensors the blocks point into that the caller keeps)."""
+        """(host block, device block, tensors the blocks point into that the caller keeps). The
+        blocks are kept per (T, buffers, state pointers): a repeated call copies nothing."""
         if buf is None:
             self._buffers(T)
             buf = self.buf
         assert buf.T == T
-        d = self.dims
         rs, cs = self._state_ptrs(cache) if cache is not None else (None, None)
+        # (kept with the buffers, which it points into, by the addresses of the state arrays it
+        # points to: the arrays at those addresses are the current ones)
+        key = None if rs is None else (rs.data_ptr(), cs.data_ptr())
+        memo = buf.__dict__.setdefault("_bind_memo", {})
+        if key not in memo:
+            if len(memo) > 8:
+                memo.clear()
+            memo[key] = self._bind_new(T, buf, rs, cs)
+        p, pd = memo[key]
+        return p, pd, (rs, cs, pd, buf)
+
+    def _bind_new(self, T: int, buf: "PfBuffers", rs, cs):
+        d = self.dims
         p = PfParams(hidden=d.hidden, n_layers=d.n_layers, nk=d.nk, nv=d.nv, n_conv=d.n_conv,
                      vocab=self.vocab, bf16=int(self.bf), T=T, ntiles=(T + TT - 1) // TT,
                      max_rec=self.max_rec, rms_eps=d.rms_eps,
@@ -413,7 +437,7 @@ class Prefill:
                      head_ptr=self.head_ptr.data_ptr(), head_ent=self.head_ent.data_ptr(),
                      **{n: getattr(buf, n).data_ptr() for n in PfBuffers.NAMES})
         pd = torch.frombuffer(bytearray(bytes(p)), dtype=torch.uint8).to(self.dev)
-        return p, pd, (rs, cs, pd, buf)
+        return p, pd
 
     def _stream(self):
         return ctypes.c_void_p(torch.cuda.current_stream(self.dev).cuda_stream)
@@ -444,7 +468,19 @@ class Prefill:
         return out
 
     def embed(self, tokens) -> int:
-        """The tokens' embedding rows into the residual tiles. Returns T."""
+        """The tokens' embedding rows into the residual tiles. Returns T. Tokens already on the
+        device (an int32 tensor) are copied there and range-checked by the kernel, which sets the
+        error word (``err``, nonzero after the call when a token was out of range; nothing
+        synchronizes); host tokens are checked here and raise."""
+        if isinstance(tokens, torch.Tensor) and tokens.device == self.dev:
+            if tokens.dtype != torch.int32 or tokens.numel() == 0:
+                raise ValueError("device tokens: a non-empty int32 tensor")
+            T = int(tokens.numel())
+            p, pd = self.params(T)
+            self.tokens.copy_(tokens.reshape(-1))
+            self._check(self.lib.lxm_pf_embed(ctypes.byref(p), ctypes.c_void_p(pd.data_ptr()),
+                                              self._stream()), "prefill embed")
+            return T
         t = torch.as_tensor(tokens, dtype=torch.int64)
         T = int(t.numel())
         if T == 0:

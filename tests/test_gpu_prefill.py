@@ -172,6 +172,34 @@ def test_prefill_token_out_of_range(cuda):
         f.verify([0, m.dims.vocab], cache)
 
 
+def test_prefill_device_tokens_and_caches(cuda):
+    """Tokens already on the device give the host path's predictions and states; a call on
+    another cache and size in between (the parameter blocks are kept per buffers and state
+    arrays) changes nothing; a device token out of range sets the error word, with no raise."""
+    spec, m, c0, r0, f = model("small")
+    toks = np.asarray(_toks("small", 40), np.int32)
+    print("[gpu-test] prefill device tokens", flush=True)
+    ca = fast.StateCache(c0, r0, m.dims.dtype, "cuda")
+    want = f.verify([int(x) for x in toks], ca).cpu().numpy()
+    want_conv, want_rec = ca.conv_numpy(), ca.rec_numpy()
+    pf = f.prefill("cuda")
+    td = torch.from_numpy(toks).to("cuda")
+    cb = fast.StateCache(c0, r0, m.dims.dtype, "cuda")
+    pb = pf.verify(td, cb).cpu().numpy()
+    cc = fast.StateCache(c0, r0, m.dims.dtype, "cuda")
+    pf.verify([int(x) for x in toks[:7]], ca)
+    pc = pf.verify(td, cc).cpu().numpy()
+    assert pb.tolist() == want.tolist() and pc.tolist() == want.tolist()
+    for cx in (cb, cc):
+        assert (bits(cx.conv_numpy()) == bits(want_conv)).all()
+        assert (bits(cx.rec_numpy()) == bits(want_rec)).all()
+    assert int(pf.err.item()) == 0
+    bad = torch.tensor([0, m.dims.vocab], dtype=torch.int32, device="cuda")
+    pf.verify(bad, fast.StateCache(c0, r0, m.dims.dtype, "cuda"))
+    assert int(pf.err.item()) != 0
+    pf.err.zero_()
+
+
 def test_config3_full_matches_decode_kernel(cuda):
     """BASELINE config 3 at full size: 65,536 uniform tokens through the 37-layer stack. The
     prefill's predictions and final states equal those of the decode kernel forced through
