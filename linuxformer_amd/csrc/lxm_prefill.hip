@@ -40,6 +40,20 @@ template <class T>
 __device__ __forceinline__ const T* tab(const uint8_t* blob, int64_t off) {
   return reinterpret_cast<const T*>(blob + off);
 }
+// a table item (whole words) from global memory by global loads (a generic pointer's flat loads
+// would also count against the LDS counter, so every wait on a table entry would also wait for
+// the LDS reads in flight, and the reverse)
+#define GAS __attribute__((address_space(1)))
+template <class T>
+__device__ __forceinline__ T gld(const T* q) {
+  static_assert(sizeof(T) % 4 == 0, "whole words");
+  T r;
+  const GAS uint32_t* src = (const GAS uint32_t*)q;
+  uint32_t* dst = reinterpret_cast<uint32_t*>(&r);
+#pragma unroll
+  for (int i = 0; i < (int)(sizeof(T) / 4); i++) dst[i] = src[i];
+  return r;
+}
 
 // ---------------------------------------------------------------------------------------------
 // The residual tiles in HBM, in the model dtype: column c of tile b at (b * H + c) * 4.
@@ -150,7 +164,7 @@ __device__ __forceinline__ v4f dot4(const lxm_pf_ent* __restrict__ e, int n, con
   for (int k0 = 0; k0 < n; k0 += 4) {
     lxm_pf_ent en[4];
 #pragma unroll
-    for (int j = 0; j < 4; j++) en[j] = e[k0 + j];
+    for (int j = 0; j < 4; j++) en[j] = gld(e + k0 + j);
     v4f xv[4];
 #pragma unroll
     for (int j = 0; j < 4; j++) xv[j] = TV<HALF>::at(x, en[j].off);
@@ -171,8 +185,8 @@ __device__ __forceinline__ v4f dot4n(const lxm_pf_ent* __restrict__ e, const flo
     float nw[4];
 #pragma unroll
     for (int j = 0; j < 4; j++) {
-      ee[j] = e[k0 + j];
-      nw[j] = en[k0 + j];
+      ee[j] = gld(e + k0 + j);
+      nw[j] = gld(en + k0 + j);
     }
     v4f xv[4];
 #pragma unroll
@@ -190,7 +204,7 @@ __device__ __forceinline__ float dot1(const lxm_pf_ent* __restrict__ e, int n, c
   for (int k0 = 0; k0 < n; k0 += 4) {
     lxm_pf_ent en[4];
 #pragma unroll
-    for (int j = 0; j < 4; j++) en[j] = e[k0 + j];
+    for (int j = 0; j < 4; j++) en[j] = gld(e + k0 + j);
     float xv[4];
 #pragma unroll
     for (int j = 0; j < 4; j++) xv[j] = *reinterpret_cast<const float*>(x + en[j].off);
@@ -293,7 +307,7 @@ __global__ __launch_bounds__(NT) void pf_tile(const lxm_pf_params* __restrict__ 
     for (int i = 0; i < LXM_PF_UPT; i++) {
       const int u = t + i * NT;
       if (u < ly.n_units) {
-        const lxm_pf_unit q = un[u];
+        const lxm_pf_unit q = gld(un + u);
         const v4f g = rd4<BF>(dot4n<BF, BF>(ent + q.gs, entn + q.gs, q.gn, HV, r));
         const v4f v = rd4<BF>(dot4n<BF, BF>(ent + q.us, entn + q.us, q.un, HV, r));
         a[i] = v4f{rd<BF>(silu_rd<BF>(g.x) * v.x), rd<BF>(silu_rd<BF>(g.y) * v.y),
@@ -307,7 +321,7 @@ __global__ __launch_bounds__(NT) void pf_tile(const lxm_pf_params* __restrict__ 
     // down_proj rows over the units (entries 16 x unit position), added to the residual
     const lxm_pf_drow* dr = tab<lxm_pf_drow>(p.blob, ly.drows);
     for (int i = t; i < ly.n_drows; i += NT) {
-      const lxm_pf_drow d = dr[i];
+      const lxm_pf_drow d = gld(dr + i);
       const v4f s = rd4<BF>(dot4<BF, BF>(ent + d.start, d.len, XM));
       V::put(HV, d.row, rd4<BF>(V::get(HV, d.row) + s));
     }
@@ -325,7 +339,7 @@ __global__ __launch_bounds__(NT) void pf_tile(const lxm_pf_params* __restrict__ 
     // entries gather): which slots are nonzero
     const lxm_pf_qk* qk = tab<lxm_pf_qk>(p.blob, ly.qk);
     for (int i = t; i < ly.n_qk; i += NT) {
-      const lxm_pf_qk q = qk[i];
+      const lxm_pf_qk q = gld(qk + i);
       const v4f P = rd4<BF>(dot4n<BF, BF>(ent + q.start, entn + q.start, q.len, HV, r));
       const uint32_t bit = 1u << q.kslot;
       if (P.x != 0.0f) atomicOr(smask + 0, bit);
@@ -336,7 +350,7 @@ __global__ __launch_bounds__(NT) void pf_tile(const lxm_pf_params* __restrict__ 
     // decays: g = -exp(A_log) * softplus(a + dt_bias) (:499); a step decays when exp(g) != 1
     const lxm_pf_dec* dc = tab<lxm_pf_dec>(p.blob, ly.dec);
     for (int i = t; i < ly.n_dec; i += NT) {
-      const lxm_pf_dec d = dc[i];
+      const lxm_pf_dec d = gld(dc + i);
       const v4f a = d.len ? rd4<BF>(dot4n<BF, BF>(ent + d.start, entn + d.start, d.len, HV, r))
                           : v4f{0.0f, 0.0f, 0.0f, 0.0f};
       const float na = -cr_exp(d.A_log);
@@ -508,7 +522,7 @@ __global__ __launch_bounds__(NT) void pf_act(const lxm_pf_params* __restrict__ p
     // the query/key conv outputs of the slots to evaluate
     const lxm_pf_qk* qk = tab<lxm_pf_qk>(p.blob, ly.qk);
     for (int i = t; i < ly.n_qk; i += NT) {
-      const lxm_pf_qk q = qk[i];
+      const lxm_pf_qk q = gld(qk + i);
       if (!((cm >> q.kslot) & 1u)) continue;
       const v4f P = rd4<BF>(dot4<BF>(ent + q.start, q.len, sm));
       QK[q.kslot * 2 * KD + q.pos] = conv_y<BF>(P, q.taps, tok, cs, q.chan);
@@ -853,22 +867,27 @@ __global__ __launch_bounds__(NT) void pf_head(const lxm_pf_params* __restrict__ 
   load_tile<BF, false>(p.hn, b, H, sm);
   __syncthreads();
   const int r0 = p.head_slice[slice], r1 = p.head_slice[slice + 1];
+  const int64_t* hptr = p.head_ptr;
+  const lxm_pf_ent* hent = p.head_ent;
+  // each position's first strict maximum over the thread's rows: from -inf, so a row is taken
+  // when it is above every earlier one; a thread whose rows are all -inf keeps its first row
+  // (with a NaN row the NaN pass below decides, as NaN outranks every number)
   float best[TT];
   int bidx[TT];
   bool nan_any = false;
 #pragma unroll
   for (int k = 0; k < TT; k++) {
-    best[k] = 0.0f;
-    bidx[k] = -1;
+    best[k] = -__builtin_inff();
+    bidx[k] = r0 + t;
   }
   for (int r = r0 + t; r < r1; r += NT) {
-    const int64_t e0 = p.head_ptr[r], e1 = p.head_ptr[r + 1];
-    const v4f s = rd4<BF>(dot4<BF>(p.head_ent + e0, (int)(e1 - e0), sm));
+    const int64_t e0 = gld(hptr + r), e1 = gld(hptr + r + 1);
+    const v4f s = rd4<BF>(dot4<BF>(hent + e0, (int)(e1 - e0), sm));
 #pragma unroll
     for (int k = 0; k < TT; k++) {
       const float v = s[k];
       nan_any |= v != v;
-      if (bidx[k] < 0 || v > best[k]) {
+      if (v > best[k]) {
         best[k] = v;
         bidx[k] = r;
       }
@@ -876,11 +895,11 @@ __global__ __launch_bounds__(NT) void pf_head(const lxm_pf_params* __restrict__ 
   }
   unsigned long long key[TT];
 #pragma unroll
-  for (int k = 0; k < TT; k++) key[k] = bidx[k] < 0 ? 0ull : argmax_key(best[k], bidx[k]);
+  for (int k = 0; k < TT; k++) key[k] = r0 + t < r1 ? argmax_key(best[k], bidx[k]) : 0ull;
   if (nan_any) {  // rare: the first NaN row of each position, which outranks every number
     for (int r = r0 + t; r < r1; r += NT) {
-      const int64_t e0 = p.head_ptr[r], e1 = p.head_ptr[r + 1];
-      const v4f s = rd4<BF>(dot4<BF>(p.head_ent + e0, (int)(e1 - e0), sm));
+      const int64_t e0 = gld(hptr + r), e1 = gld(hptr + r + 1);
+      const v4f s = rd4<BF>(dot4<BF>(hent + e0, (int)(e1 - e0), sm));
 #pragma unroll
       for (int k = 0; k < TT; k++)
         if (s[k] != s[k]) key[k] = kmax(key[k], argmax_key(s[k], r));
