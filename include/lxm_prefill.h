@@ -103,8 +103,9 @@ typedef struct lxm_pf_params {
   const int64_t* emb_ptr;      /* (vocab + 1): the embedding rows */
   const lxm_pf_ent* emb_ent;   /* off = column, w = value */
   const int32_t* head_slice;   /* (LXM_PF_SLICES + 1): head row ranges, one per XCD */
-  const int64_t* head_ptr;     /* (vocab + 1): head rows (columns with nonzero final weight) */
-  const lxm_pf_ent* head_ent;  /* off = 16 x column */
+  const int64_t* head_ptr;     /* (vocab + 1): head rows (columns with nonzero final weight),
+                                  each padded to a multiple of 4 entries */
+  const lxm_pf_ent* head_ent;  /* off = 16 x column; padding: off = 16 x hidden, w = 0 */
   const int32_t* tokens;       /* (T): the positions' token ids (embedding) */
   void* h;                     /* (ntiles, hidden, TT) model dtype: the residual stream */
   void* hn;                    /* same layout: the head's normed input */

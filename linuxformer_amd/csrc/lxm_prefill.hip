@@ -197,6 +197,23 @@ __device__ __forceinline__ v4f dot4n(const lxm_pf_ent* __restrict__ e, const flo
   }
   return s;
 }
+// dot4 over a row padded to a multiple of 4 entries (padding: weight 0 at a column holding +0),
+// so every entry adds its term with no test
+template <bool BF>
+__device__ __forceinline__ v4f dot4p(const lxm_pf_ent* __restrict__ e, int n, const uint8_t* x) {
+  v4f s = {0.0f, 0.0f, 0.0f, 0.0f};
+  for (int k0 = 0; k0 < n; k0 += 4) {
+    lxm_pf_ent en[4];
+#pragma unroll
+    for (int j = 0; j < 4; j++) en[j] = gld(e + k0 + j);
+    v4f xv[4];
+#pragma unroll
+    for (int j = 0; j < 4; j++) xv[j] = TV<false>::at(x, en[j].off);
+#pragma unroll
+    for (int j = 0; j < 4; j++) s = acc4<BF>(s, xv[j], en[j].w);
+  }
+  return s;
+}
 // the same for one float per entry at x + off (a flat vector, or one position's lane of a tile)
 template <bool BF>
 __device__ __forceinline__ float dot1(const lxm_pf_ent* __restrict__ e, int n, const uint8_t* x) {
@@ -865,6 +882,7 @@ __global__ __launch_bounds__(NT) void pf_head(const lxm_pf_params* __restrict__ 
   const int slice = blockIdx.x % LXM_PF_SLICES;
   const int64_t b = blockIdx.x / LXM_PF_SLICES;
   load_tile<BF, false>(p.hn, b, H, sm);
+  if (t == 0) reinterpret_cast<v4f*>(sm)[H] = v4f{0.0f, 0.0f, 0.0f, 0.0f};  // the padding's column
   __syncthreads();
   const int r0 = p.head_slice[slice], r1 = p.head_slice[slice + 1];
   const int64_t* hptr = p.head_ptr;
@@ -882,7 +900,7 @@ __global__ __launch_bounds__(NT) void pf_head(const lxm_pf_params* __restrict__ 
   }
   for (int r = r0 + t; r < r1; r += NT) {
     const int64_t e0 = gld(hptr + r), e1 = gld(hptr + r + 1);
-    const v4f s = rd4<BF>(dot4<BF>(hent + e0, (int)(e1 - e0), sm));
+    const v4f s = rd4<BF>(dot4p<BF>(hent + e0, (int)(e1 - e0), sm));
 #pragma unroll
     for (int k = 0; k < TT; k++) {
       const float v = s[k];
@@ -899,7 +917,7 @@ __global__ __launch_bounds__(NT) void pf_head(const lxm_pf_params* __restrict__ 
   if (nan_any) {  // rare: the first NaN row of each position, which outranks every number
     for (int r = r0 + t; r < r1; r += NT) {
       const int64_t e0 = gld(hptr + r), e1 = gld(hptr + r + 1);
-      const v4f s = rd4<BF>(dot4<BF>(hent + e0, (int)(e1 - e0), sm));
+      const v4f s = rd4<BF>(dot4p<BF>(hent + e0, (int)(e1 - e0), sm));
 #pragma unroll
       for (int k = 0; k < TT; k++)
         if (s[k] != s[k]) key[k] = kmax(key[k], argmax_key(s[k], r));

@@ -333,11 +333,18 @@ class Prefill:
         w1f = np.float32(1.0) + np.asarray(sm.norm, np.float32)
         keep = w1f[er.cols] != 0
         rows = np.repeat(np.arange(er.n), np.diff(er.ptr))[keep]
+        # each head row padded to a multiple of 4 entries by entries of weight 0 at column hidden
+        # (the head kernel's zero column): a row's sum then takes its entries four at a time
+        # with no test (adding +0 to a sum from +0 changes no bits: such a sum is never -0)
+        cnt = np.bincount(rows, minlength=er.n)
+        plen = (cnt + 3) // 4 * 4
         hptr = np.zeros(er.n + 1, np.int64)
-        np.cumsum(np.bincount(rows, minlength=er.n), out=hptr[1:])
-        hent = np.zeros(int(keep.sum()) + 4, ENT)
-        hent["off"][:-4] = 16 * er.cols[keep]
-        hent["w"][:-4] = er.vals[keep]
+        np.cumsum(plen, out=hptr[1:])
+        hent = np.zeros(int(hptr[-1]) + 4, ENT)
+        hent["off"][:] = 16 * d.hidden
+        pos = hptr[rows] + (np.arange(len(rows)) - np.repeat(np.cumsum(cnt) - cnt, cnt))
+        hent["off"][pos] = 16 * er.cols[keep]
+        hent["w"][pos] = er.vals[keep]
         # slices of about equal work (rows + entries), one per XCD
         work = np.cumsum(np.diff(hptr) + 2)
         tot = work[-1] if len(work) else 0
