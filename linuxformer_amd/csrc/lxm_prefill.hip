@@ -698,7 +698,7 @@ __device__ __forceinline__ DeltaIn delta_in(const uint8_t* rec, const RecOff& ro
 template <bool BF>
 __global__ __launch_bounds__(NTD) void pf_delta(const lxm_pf_params* __restrict__ pp, int L) {
   __shared__ __align__(16) float kn[KD], qn[KD], vb[DW], dl[DW];
-  __shared__ __align__(16) float bs[16 * DW];
+  __shared__ __align__(16) float bs[16 * DW], bo[16 * DW];  // the kv and the o block sums
   __shared__ float beta_s;
   const lxm_pf_params& p = *pp;
   const lxm_pf_layer& ly = p.layers[L];
@@ -715,6 +715,9 @@ __global__ __launch_bounds__(NTD) void pf_delta(const lxm_pf_params* __restrict_
 #pragma unroll
   for (int i = 0; i < 16; i++) s[i] = S[(rb * 16 + i) * VD];
   bool wrote = false;
+  // a live step's o block sums stay in bo until the next live step's first barrier (or the
+  // loop's end), where they are summed into the record they belong to: three barriers a step
+  float* o_rec = nullptr;
   // the inputs of the next three candidates in flight
   DeltaIn n1 = {}, n2 = {}, n3 = {};
   if (count > 0) n1 = delta_in(recs, ro, vslot, sv.kslot, c0);
@@ -749,6 +752,15 @@ __global__ __launch_bounds__(NTD) void pf_delta(const lxm_pf_params* __restrict_
         if (t >= VT && t < VT + DW) vb[t - VT] = cur.v;
         if (t == 0) beta_s = cur.beta;
         __syncthreads();
+        if (o_rec) {  // the previous live step's o = D(the block sums in order)
+          if (t < DW) {
+            float q = 0.0f;
+#pragma unroll
+            for (int b = 0; b < 16; b++) q = q + bo[b * DW + t];
+            o_rec[t] = rd<BF>(q);
+          }
+          o_rec = nullptr;
+        }
         // the thread's 16 rows of k and q at once (one LDS wait), then the cascade blocks'
         // sums; a zero factor adds nothing (the oracle skips it; a sum from +0 is never -0)
         float kr[16], qr[16];
@@ -777,19 +789,22 @@ __global__ __launch_bounds__(NTD) void pf_delta(const lxm_pf_params* __restrict_
           s[i] = kr[i] != 0.0f ? s[i] + kr[i] * d : s[i];
           o = qr[i] != 0.0f ? o + s[i] * qr[i] : o;
         }
-        bs[rb * DW + c] = o;  // (the kv sums read bs before the barrier above)
-        __syncthreads();
-        // o = D(the block sums in order), into the record (over v: read at this step's start);
-        // the gated norm is pf_out's
-        if (t < DW) {
-          float q = 0.0f;
-#pragma unroll
-          for (int b = 0; b < 16; b++) q = q + bs[b * DW + t];
-          reinterpret_cast<float*>(rec + ro.v)[vslot * VD + c0 + t] = rd<BF>(q);
-        }
+        // (the previous step's o sums read bo before this step's first barrier)
+        bo[rb * DW + c] = o;
+        // o goes into the record over v (read at this step's start); the gated norm is pf_out's
+        o_rec = reinterpret_cast<float*>(rec + ro.v) + vslot * VD + c0;
       }
     }
     if (t == 0 && c0 == 0) reinterpret_cast<int32_t*>(rec + ro.pr)[vslot] = proc;
+  }
+  if (o_rec) {
+    __syncthreads();
+    if (t < DW) {
+      float q = 0.0f;
+#pragma unroll
+      for (int b = 0; b < 16; b++) q = q + bo[b * DW + t];
+      o_rec[t] = rd<BF>(q);
+    }
   }
   if (wrote) {
 #pragma unroll
