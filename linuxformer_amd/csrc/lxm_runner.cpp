@@ -207,9 +207,11 @@ int main(int argc, char** argv) {
   int tok = 0;
   CK(hipMemcpy(&tok, forced_d, 4, hipMemcpyDeviceToHost));
   for (int k = 0; k < launches; k++) {
-    // sync words, keys and the error flag start at zero; the stream continues from `tok`
+    // sync words, keys, the value heads' stamped outputs and the error flag start at zero; the
+    // stream continues from `tok`
     CK(hipMemsetAsync(p.sync, 0, LXM_NSYNC * 4, st));
     CK(hipMemsetAsync(p.keys, 0, 16, st));
+    CK(hipMemsetAsync(p.ybuf, 0, (size_t)p.nv * p.vd * 8, st));
     CK(hipMemsetAsync(p.err, 0, 4, st));
     CK(hipMemcpyAsync(forced_d, &tok, 4, hipMemcpyHostToDevice, st));
     p.n_forced = 1;
