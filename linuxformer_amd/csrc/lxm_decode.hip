@@ -1554,7 +1554,9 @@ __device__ void gdn_head(const lxm_params& p, int L, int step, int vh, bool out,
       vb[t] = rd<BF>(silu(rd<BF>(yv)));
     } else if (t < 2 * VD) {
       const int j = t - VD;
-      zb[j] = rd<BF>(rdot<BF, E4>(p.blob + ly.z_ent, zr.start, zr.len, h0, r0, w1in));
+      // (silu of the gate, for the gated norm: formed here, beside the value channels' longer
+      // windows, rather than on the output's path)
+      zb[j] = silu(rd<BF>(rdot<BF, E4>(p.blob + ly.z_ent, zr.start, zr.len, h0, r0, w1in)));
     } else if (t == 2 * VD) {
       const float b = rd<BF>(rdot<BF, E4>(p.blob + ly.b_ent, br.start, br.len, h0, r0, w1in));
       misc[2] = (int)__float_as_uint(rd<BF>(sigmoid(b)));
@@ -1658,7 +1660,7 @@ __device__ void gdn_head(const lxm_params& p, int L, int step, int vh, bool out,
           for (int j = lane; j < VD; j += 64) {
             const float t1 = rd<BF>(ob[j] * rr);
             const float t2 = rd<BF>(gp(gw)[j] * t1);
-            st64_rlx(y + j, seq, rd<BF>(t2 * silu(zb[j])));
+            st64_rlx(y + j, seq, rd<BF>(t2 * zb[j]));
           }
         } else {  // no live query: o = 0, and so is every term the head gives out_proj
           for (int j = lane; j < VD; j += 64) st64_rlx(y + j, seq, 0.0f);
