@@ -95,9 +95,9 @@ static_assert((L_FLAGS + 4 * F_KEYW) % 8 == 0 && F_KEYW + 16 <= 256, "the key wo
 #define HX_KN (HX_QN + 4 * KD)
 #define HX_V (HX_KN + 4 * KD)         // value channels' conv outputs
 #define HX_Z (HX_V + 4 * VD)          // in_proj_z rows
-#define HX_O (HX_Z + 4 * VD)          // the head's output o
-#define HX_DL (HX_O + 4 * VD)         // delta = (v - kv) beta
-#define HX_BS (HX_DL + 4 * VD)        // per row block (16 rows) partial sums, [16][VD]
+#define HX_DL (HX_Z + 4 * VD)         // delta = (v - kv) beta
+#define HX_GW (HX_DL + 4 * VD)        // the gated norm's weight
+#define HX_BS (HX_GW + 4 * VD)        // per row block (16 rows) partial sums, [16][VD]
 #define HX_MISC (HX_BS + 4 * 16 * VD) // ints: [0] nq, [1] nk, [2] beta bits, [4] event, [5] ok
 #define HX_OP (HX_MISC + 256)         // out_proj: the helper's row pointers (LXM_OUT_ROWS + 1)
 #define HX_OE (HX_OP + 4 * (LXM_OUT_ROWS + 4))  // its entries (LXM_OUT_MAX, 8 bytes at most)
@@ -1448,7 +1448,7 @@ __device__ void gdn_head(const lxm_params& p, int L, int step, int vh, bool out,
   float* kn = reinterpret_cast<float*>(hx + HX_KN);
   float* vb = reinterpret_cast<float*>(hx + HX_V);
   float* zb = reinterpret_cast<float*>(hx + HX_Z);
-  float* ob = reinterpret_cast<float*>(hx + HX_O);
+  float* gwl = reinterpret_cast<float*>(hx + HX_GW);
   float* dl = reinterpret_cast<float*>(hx + HX_DL);
   float* bs = reinterpret_cast<float*>(hx + HX_BS);
   int* misc = reinterpret_cast<int*>(hx + HX_MISC);
@@ -1556,7 +1556,10 @@ __device__ void gdn_head(const lxm_params& p, int L, int step, int vh, bool out,
       const int j = t - VD;
       // (silu of the gate, for the gated norm: formed here, beside the value channels' longer
       // windows, rather than on the output's path)
+      // (and the gated norm's weight into LDS: not a global load on the output's path)
+      const float w = gp(reinterpret_cast<const float*>(p.blob + ly.gnorm))[j];
       zb[j] = silu(rd<BF>(rdot<BF, E4>(p.blob + ly.z_ent, zr.start, zr.len, h0, r0, w1in)));
+      gwl[j] = w;
     } else if (t == 2 * VD) {
       const float b = rd<BF>(rdot<BF, E4>(p.blob + ly.b_ent, br.start, br.len, h0, r0, w1in));
       misc[2] = (int)__float_as_uint(rd<BF>(sigmoid(b)));
@@ -1638,34 +1641,37 @@ __device__ void gdn_head(const lxm_params& p, int L, int step, int vh, bool out,
       __syncthreads();  // the kv sums above have read bs
       reinterpret_cast<v4f*>(bs + rb * VD)[cg] = a;
       __syncthreads();
-      if (t < VD) {
-        float o = 0.0f;
-#pragma unroll
-        for (int b = 0; b < 16; b++) o = o + bs[b * VD + t];
-        ob[t] = rd<BF>(o);
-      }
-    }
-    if (out) {
-      __syncthreads();
-      // the gated norm on this value head (one wave), gate z: y = D(D(w * D(o * r)) * silu(z)),
-      // issued before any wave stores the state's rows, so that the output does not queue
-      // behind them in the CU's memory pipeline
+      // (a live query makes the event's output live, so out holds here.) One wave forms o for
+      // dims lane and lane + 64 (the block sums in order), then the gated norm on this value
+      // head, gate z: y = D(D(w * D(o * r)) * silu(z)), issued before any wave stores the
+      // state's rows, so that the output does not queue behind them in the CU's memory pipeline
       if (wv == 0) {
-        const float* gw = reinterpret_cast<const float*>(p.blob + ly.gnorm);
-        if (nq > 0) {
-          float sq = 0.0f;
-          for (int j = lane; j < VD; j += 64) sq = sq + ob[j] * ob[j];
-          sq = sum64(sq);
-          const float rr = rsqrt_(sq / (float)VD + hd.geps);
-          for (int j = lane; j < VD; j += 64) {
-            const float t1 = rd<BF>(ob[j] * rr);
-            const float t2 = rd<BF>(gp(gw)[j] * t1);
-            st64_rlx(y + j, seq, rd<BF>(t2 * zb[j]));
-          }
-        } else {  // no live query: o = 0, and so is every term the head gives out_proj
-          for (int j = lane; j < VD; j += 64) st64_rlx(y + j, seq, 0.0f);
+        float ov[2];
+#pragma unroll
+        for (int h = 0; h < 2; h++) {
+          float o = 0.0f;
+#pragma unroll
+          for (int b = 0; b < 16; b++) o = o + bs[b * VD + lane + 64 * h];
+          ov[h] = rd<BF>(o);
+        }
+        float sq = 0.0f;
+#pragma unroll
+        for (int h = 0; h < 2; h++) sq = sq + ov[h] * ov[h];
+        sq = sum64(sq);
+        const float rr = rsqrt_(sq / (float)VD + hd.geps);
+#pragma unroll
+        for (int h = 0; h < 2; h++) {
+          const int j = lane + 64 * h;
+          const float t1 = rd<BF>(ov[h] * rr);
+          const float t2 = rd<BF>(gwl[j] * t1);
+          st64_rlx(y + j, seq, rd<BF>(t2 * zb[j]));
         }
       }
+      GH_MARK(4);
+      __syncthreads();
+    } else if (out) {  // no live query: o = 0, and so is every term the head gives out_proj
+      if (wv == 0)
+        for (int j = lane; j < VD; j += 64) st64_rlx(y + j, seq, 0.0f);
       GH_MARK(4);
       __syncthreads();
     }
