@@ -184,19 +184,23 @@ __device__ __forceinline__ void sp_skip() {}
 #endif
 
 // spin (one thread) until the word differs from last; 0 on timeout or another block's error
+// (the word and the error word are requested together: one round trip a poll)
 __device__ bool spin_ne(const uint32_t* p, uint32_t last, uint32_t* out, int32_t* err, int code) {
   const uint64_t t0 = wall();
-  uint32_t v;
-  while ((v = ld_rlx(p)) == last) {
-    __builtin_amdgcn_s_sleep(2);
-    if (__hip_atomic_load(gp(err), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) return false;
+  for (;;) {
+    const uint32_t v = ld_rlx(p);
+    const int32_t e = __hip_atomic_load(gp(err), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (v != last) {
+      *out = v;
+      return true;
+    }
+    if (e) return false;
     if (wall() - t0 > TIMEOUT_TICKS) {
       __hip_atomic_fetch_max(gp(err), code, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       return false;
     }
+    __builtin_amdgcn_s_sleep(1);
   }
-  *out = v;
-  return true;
 }
 
 // The workgroup waits until every thread t < n sees the word base[32 t] equal to want, reading
