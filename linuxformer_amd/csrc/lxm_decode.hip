@@ -520,6 +520,42 @@ __device__ __forceinline__ float rdot(const uint8_t* ent, int64_t start, int n, 
   }
   return s;
 }
+// rdot over up to four steps' inputs at once, for a conv channel's window: window k (on[k], the
+// same across the thread's calls) reads ring hs[k] with norm factor r[k]. Each sum keeps rdot's
+// order; the entries and norm weights are read once, and every window's ring values are
+// requested together (only for the windows that are on).
+template <bool BF, bool E4>
+__device__ __forceinline__ void rdot4(const uint8_t* ent, int64_t start, int n,
+                                      const float* const (&hs)[4], const float (&r)[4],
+                                      const bool (&on)[4], const uint8_t* w1in, float (&out)[4]) {
+#pragma unroll
+  for (int k = 0; k < 4; k++) out[k] = 0.0f;
+  for (int k0 = 0; k0 < n; k0 += 4) {
+    int i[4];
+    float w[4], wi[4], hv[4][4];
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+      Ent<E4>::gat(ent, start + k0 + j, i[j], w[j]);
+      i[j] &= OFF_MASK;
+      wi[j] = w1_one<E4, true>(w1in, i[j] >> 2);
+    }
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+      if (on[k]) {
+#pragma unroll
+        for (int j = 0; j < 4; j++) hv[k][j] = ring_val<BF>(hs[k], i[j]);
+      } else {
+#pragma unroll
+        for (int j = 0; j < 4; j++) hv[k][j] = 0.0f;
+      }
+    }
+#pragma unroll
+    for (int k = 0; k < 4; k++)
+#pragma unroll
+      for (int j = 0; j < 4; j++)
+        if (on[k] && k0 + j < n) out[k] = acc<BF>(out[k], rd<BF>((hv[k][j] * r[k]) * wi[j]), w[j]);
+  }
+}
 
 // ---------------------------------------------------------------------------------------------
 // The chain workgroup. Its LDS arrays are addressed from the dynamic shared array itself, so
@@ -1538,24 +1574,35 @@ __device__ void gdn_head(const lxm_params& p, int L, int step, int vh, bool out,
     const float* h0 = ring_at(p, step, L);
     const float r0 = ld_rlxf(rr_at(p, step, L));
     if (t < VD) {
+      // window k = 3 - s holds step - s's input: from the ring (one pass over the channel's
+      // entries for every such step), or from the conv state before this launch
       const int chan = 2 * p.nk * KD + vh * VD + t;
-      float win[4];
-      win[3] = rd<BF>(rdot<BF, E4>(qent, ch.start, ch.len, h0, r0, w1in));
+      const float* hs[4];
+      float rs[4], win[4], sm[4];
+      bool on[4];
 #pragma unroll
-      for (int s = 1; s <= 3; s++) {
-        win[3 - s] = 0.0f;
-        if (ch.taps[3 - s] == 0.0f) continue;
-        if (step - s >= 0)
-          win[3 - s] = rd<BF>(rdot<BF, E4>(qent, ch.start, ch.len, ring_at(p, step - s, L),
-                                            ld_rlxf(rr_at(p, step - s, L)), w1in));
-        else
-          win[3 - s] = conv_at<BF>(p.conv[L], (int64_t)chan * 4 + 4 - (s - step));
+      for (int k = 0; k < 4; k++) {
+        const int s = 3 - k;
+        on[k] = s == 0 || (ch.taps[k] != 0.0f && step - s >= 0);
+        hs[k] = ring_at(p, step - s, L);
+        rs[k] = r0;
+        win[k] = 0.0f;
       }
+#pragma unroll
+      for (int k = 0; k < 3; k++) {
+        const int s = 3 - k;
+        if (on[k]) rs[k] = ld_rlxf(rr_at(p, step - s, L));
+        else if (ch.taps[k] != 0.0f) win[k] = conv_at<BF>(p.conv[L], (int64_t)chan * 4 + 4 - (s - step));
+      }
+      rdot4<BF, E4>(qent, ch.start, ch.len, hs, rs, on, w1in, sm);
+#pragma unroll
+      for (int k = 0; k < 4; k++)
+        if (on[k]) win[k] = rd<BF>(sm[k]);
       float yv = 0.0f;
 #pragma unroll
       for (int k = 0; k < 4; k++)
         if (ch.taps[k] != 0.0f) yv = yv + ch.taps[k] * win[k];
-      vb[t] = rd<BF>(silu(rd<BF>(yv)));
+      vb[t] = silu_rd<BF>(rd<BF>(yv));  // (bf16: the fast exact path, as the chain's units)
     } else if (t < 2 * VD) {
       const int j = t - VD;
       // (silu of the gate, for the gated norm: formed here, beside the value channels' longer
