@@ -57,13 +57,14 @@ __device__ __forceinline__ T gld(const T* q) {
 
 // ---------------------------------------------------------------------------------------------
 // The residual tiles in HBM, in the model dtype: column c of tile b at (b * H + c) * 4.
+// (global loads and stores: generic ones would be flat and also count against the LDS counter)
 template <bool BF>
 __device__ __forceinline__ v4f ld_col(const void* h, int64_t b, int H, int c) {
   if constexpr (BF) {
-    const v2u u = reinterpret_cast<const v2u*>(h)[b * H + c];
+    const v2u u = ((const __attribute__((address_space(1))) v2u*)h)[b * H + c];
     return v4f{bitsf(u.x << 16), bitsf(u.x & 0xffff0000u), bitsf(u.y << 16), bitsf(u.y & 0xffff0000u)};
   } else {
-    return reinterpret_cast<const v4f*>(h)[b * H + c];
+    return ((const __attribute__((address_space(1))) v4f*)h)[b * H + c];
   }
 }
 // (values exact in the model dtype: bf16 keeps the upper half of each float)
@@ -73,9 +74,9 @@ __device__ __forceinline__ void st_col(void* h, int64_t b, int H, int c, v4f v) 
     v2u u;
     u.x = (fbits(v.x) >> 16) | (fbits(v.y) & 0xffff0000u);
     u.y = (fbits(v.z) >> 16) | (fbits(v.w) & 0xffff0000u);
-    reinterpret_cast<v2u*>(h)[b * H + c] = u;
+    ((__attribute__((address_space(1))) v2u*)h)[b * H + c] = u;
   } else {
-    reinterpret_cast<v4f*>(h)[b * H + c] = v;
+    ((__attribute__((address_space(1))) v4f*)h)[b * H + c] = v;
   }
 }
 __device__ __forceinline__ int64_t el_idx(int H, int t, int c) {
