@@ -103,7 +103,8 @@ static_assert((L_FLAGS + 4 * F_KEYW) % 8 == 0 && F_KEYW + 16 <= 256, "the key wo
 #define HX_OE (HX_OP + 4 * (LXM_OUT_ROWS + 4))  // its entries (LXM_OUT_MAX, 8 bytes at most)
 #define HX_OY (HX_OE + 8 * LXM_OUT_MAX)  // the head outputs each entry reads
 #define HX_LT (HX_OY + 4 * LXM_OUT_MAX + 64)  // (reads run up to 3 slots past the end)
-#define HX_END (HX_LT + 64 * (int)sizeof(lxm_layer))  // the layer table, resident for the launch
+#define HX_PARAMS (HX_LT + 64 * (int)sizeof(lxm_layer))  // the layer table, resident for the launch
+#define HX_END (HX_PARAMS + 512)      // the helper's copy of the parameter block
 
 // sync words (uint32 indices into p.sync). The event word has one copy per group of helpers
 // (group = block index mod 8, the XCD a block lands on when blocks are dealt round-robin), each
@@ -1813,11 +1814,11 @@ __device__ bool out_rows(const lxm_params& p, int ra, int rb, int ne, uint32_t s
 }
 
 template <bool BF, bool E4>
-__device__ void run_helper(const lxm_params& p) {
+__device__ void run_helper(const lxm_params& pg) {
   uint8_t* lds = smem;
-  const int t = threadIdx.x, H = p.hidden, b = blockIdx.x, nh = p.n_blocks - 1;
-  const int r0 = p.head_rows[b], r1 = p.head_rows[b + 1], nr = r1 - r0;
-  const int64_t e0 = p.head_ptr[r0], ne = p.head_ptr[r1] - e0;
+  const int t = threadIdx.x, b = blockIdx.x;
+  const int r0 = pg.head_rows[b], r1 = pg.head_rows[b + 1], nr = r1 - r0;
+  const int64_t e0 = pg.head_ptr[r0], ne = pg.head_ptr[r1] - e0;
   // the scratch regions first (constant offsets: the head's normed input at 0), the head
   // tables after them
   uint8_t* hx = lds;
@@ -1825,9 +1826,17 @@ __device__ void run_helper(const lxm_params& p) {
   uint8_t* lent = lds + HX_END + (((size_t)(nr + 1) * 4 + 15) & ~(size_t)15);
   int* misc = reinterpret_cast<int*>(hx + HX_MISC);
   // every LDS word starts finite (zero): gathers may read slots no table names
-  for (int k = t; k < (HX_END + p.head_lds + 256) / 16; k += NT)
+  for (int k = t; k < (HX_END + pg.head_lds + 256) / 16; k += NT)
     reinterpret_cast<v4u*>(lds)[k] = v4u{0, 0, 0, 0};
   __syncthreads();
+  // the parameter block into LDS: the event path reads its pointers by ds_reads, not by flat
+  // loads from global memory (which would also wait on the vector memory counter)
+  static_assert(sizeof(lxm_params) <= 512 && sizeof(lxm_params) % 4 == 0, "params in LDS");
+  for (int k = t; k < (int)(sizeof(lxm_params) / 4); k += NT)
+    reinterpret_cast<uint32_t*>(hx + HX_PARAMS)[k] = gp(reinterpret_cast<const uint32_t*>(&pg))[k];
+  __syncthreads();
+  const lxm_params& p = *reinterpret_cast<const lxm_params*>(hx + HX_PARAMS);
+  const int H = p.hidden, nh = p.n_blocks - 1;
   for (int k = t; k <= nr; k += NT) lptr[k] = (int32_t)(p.head_ptr[r0 + k] - e0);
   // the layer table (an event then reads its layer's offsets from LDS, not from global memory)
   for (int L = t; L < p.n_layers; L += NT)
@@ -1870,7 +1879,9 @@ __device__ void run_helper(const lxm_params& p) {
       pr[0] += w1 - w0;
     }
     if (!(w & EV_GDN)) {
-      head_rows<BF, E4>(p, (w >> 8) & KEY_STAMP, lptr, lent, r0, nr, hx);
+      // (the head's rows read the parameter block from global memory: the LDS copy, read
+      // between the row tables' LDS reads, measured slower there)
+      head_rows<BF, E4>(pg, (w >> 8) & KEY_STAMP, lptr, lent, r0, nr, hx);
       if (PROF_ON) pr[1] += cycles() - w1;
       step++;
     } else {
