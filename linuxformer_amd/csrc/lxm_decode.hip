@@ -1512,6 +1512,9 @@ __device__ void gdn_head(const lxm_params& p, int L, int step, int vh, bool out,
   const float e = ld_rlxf(p.mb_e + vh);
   const bool live = (tf & 1) != 0, dec = (tf & 4) != 0;
   const lxm_layer ly = reinterpret_cast<const lxm_layer*>(hx + HX_LT)[L];
+  // the layer's state pointer requested at the start (a global load; it is used after the
+  // value channels, on the step's path)
+  float* const recL = gp(p.rec)[L];
   // the value channels', z rows' and beta row's descriptors, requested first (they do not
   // depend on the step's data)
   lxm_chan ch{};
@@ -1627,7 +1630,7 @@ __device__ void gdn_head(const lxm_params& p, int L, int step, int vh, bool out,
   // those rows are read: the whole tile (128 KB) streamed into one CU was measured slower.
   {
     const int cg = t & 31, rb = t >> 5;
-    GAS v4f* S4 = gp(reinterpret_cast<v4f*>(p.rec[L] + (size_t)vh * KD * VD));
+    GAS v4f* S4 = gp(reinterpret_cast<v4f*>(recL + (size_t)vh * KD * VD));
     v4f s[16];
 #pragma unroll
     for (int i = 0; i < 16; i++) {
