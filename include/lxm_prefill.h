@@ -104,7 +104,8 @@ typedef struct lxm_pf_params {
   const lxm_pf_ent* emb_ent;   /* off = column, w = value */
   const int32_t* head_slice;   /* (LXM_PF_SLICES + 1): head row ranges, one per XCD */
   const int64_t* head_ptr;     /* (vocab + 1): head rows (columns with nonzero final weight),
-                                  each padded to a multiple of 4 entries */
+                                  each padded to a multiple of 4 entries and to at least 4;
+                                  fewer than 2^31 entries in all */
   const lxm_pf_ent* head_ent;  /* off = 16 x column; padding: off = 16 x hidden, w = 0 */
   const int32_t* tokens;       /* (T): the positions' token ids (embedding) */
   void* h;                     /* (ntiles, hidden, TT) model dtype: the residual stream */
@@ -117,7 +118,8 @@ typedef struct lxm_pf_params {
   uint8_t* recs;               /* (T x max_rec): candidate records */
   unsigned long long* keys;    /* (T): argmax keys */
   int32_t* preds;              /* (T) */
-  int32_t* err;                /* (1): 1 a token id out of range */
+  int32_t* err;                /* (1): 1 a token id out of range; 2 the head kernel's LDS tile
+                                  not at LDS address 0 (a build fault) */
 } lxm_pf_params;
 
 /* Fast.forward / Fast.layer (fast.py:252-269): layers [l0, l1) over the T positions of p->h, in

@@ -198,20 +198,43 @@ __device__ __forceinline__ v4f dot4n(const lxm_pf_ent* __restrict__ e, const flo
   }
   return s;
 }
-// dot4 over a row padded to a multiple of 4 entries (padding: weight 0 at a column holding +0),
-// so every entry adds its term with no test
+// The head's rows over a tile at LDS address 0: an entry's column offset is its LDS address (no
+// base added per entry).
+typedef const __attribute__((address_space(3))) v4f* lds_v4f;
 template <bool BF>
-__device__ __forceinline__ v4f dot4p(const lxm_pf_ent* __restrict__ e, int n, const uint8_t* x) {
-  v4f s = {0.0f, 0.0f, 0.0f, 0.0f};
-  for (int k0 = 0; k0 < n; k0 += 4) {
+__device__ __forceinline__ v4f sum4z(v4f s, const lxm_pf_ent (&en)[4]) {
+  v4f xv[4];
+#pragma unroll
+  for (int j = 0; j < 4; j++) xv[j] = *(lds_v4f)(size_t)(uint32_t)en[j].off;
+#pragma unroll
+  for (int j = 0; j < 4; j++) s = acc4<BF>(s, xv[j], en[j].w);
+  return s;
+}
+// a head row: its first entry's index, its length (a multiple of 4, at least 4), and its first
+// four entries
+struct HRow {
+  uint32_t e0;
+  int n;
+  lxm_pf_ent g[4];
+};
+// row r's bounds and first four entries
+__device__ __forceinline__ void hrow_req(const int64_t* hptr, const lxm_pf_ent* hent, int r,
+                                         HRow& h) {
+  const int64_t e0 = gld(hptr + r), e1 = gld(hptr + r + 1);
+  h.e0 = (uint32_t)e0;
+  h.n = (int)(e1 - e0);
+#pragma unroll
+  for (int j = 0; j < 4; j++) h.g[j] = gld(hent + e0 + j);
+}
+// the row's sums for the tile's four positions, entries in ascending order from +0
+template <bool BF>
+__device__ __forceinline__ v4f hrow_sum(const lxm_pf_ent* hent, const HRow& h) {
+  v4f s = sum4z<BF>(v4f{0.0f, 0.0f, 0.0f, 0.0f}, h.g);
+  for (int k0 = 4; k0 < h.n; k0 += 4) {
     lxm_pf_ent en[4];
 #pragma unroll
-    for (int j = 0; j < 4; j++) en[j] = gld(e + k0 + j);
-    v4f xv[4];
-#pragma unroll
-    for (int j = 0; j < 4; j++) xv[j] = TV<false>::at(x, en[j].off);
-#pragma unroll
-    for (int j = 0; j < 4; j++) s = acc4<BF>(s, xv[j], en[j].w);
+    for (int j = 0; j < 4; j++) en[j] = gld(hent + h.e0 + k0 + j);
+    s = sum4z<BF>(s, en);
   }
   return s;
 }
@@ -897,6 +920,11 @@ __global__ __launch_bounds__(NT) void pf_head(const lxm_pf_params* __restrict__ 
   const int t = threadIdx.x, H = p.hidden;
   const int slice = blockIdx.x % LXM_PF_SLICES;
   const int64_t b = blockIdx.x / LXM_PF_SLICES;
+  // the tile's columns are read at LDS address 16 x column (sum4z): the tile must start at 0
+  if ((uint32_t)(size_t)(const __attribute__((address_space(3))) uint8_t*)sm != 0u) {
+    if (t == 0) *p.err = 2;
+    return;
+  }
   load_tile<BF, false>(p.hn, b, H, sm);
   if (t == 0) reinterpret_cast<v4f*>(sm)[H] = v4f{0.0f, 0.0f, 0.0f, 0.0f};  // the padding's column
   __syncthreads();
@@ -915,8 +943,9 @@ __global__ __launch_bounds__(NT) void pf_head(const lxm_pf_params* __restrict__ 
     bidx[k] = r0 + t;
   }
   for (int r = r0 + t; r < r1; r += NT) {
-    const int64_t e0 = gld(hptr + r), e1 = gld(hptr + r + 1);
-    const v4f s = rd4<BF>(dot4p<BF>(hent + e0, (int)(e1 - e0), sm));
+    HRow h;
+    hrow_req(hptr, hent, r, h);
+    const v4f s = rd4<BF>(hrow_sum<BF>(hent, h));
 #pragma unroll
     for (int k = 0; k < TT; k++) {
       const float v = s[k];
@@ -932,8 +961,9 @@ __global__ __launch_bounds__(NT) void pf_head(const lxm_pf_params* __restrict__ 
   for (int k = 0; k < TT; k++) key[k] = r0 + t < r1 ? argmax_key(best[k], bidx[k]) : 0ull;
   if (nan_any) {  // rare: the first NaN row of each position, which outranks every number
     for (int r = r0 + t; r < r1; r += NT) {
-      const int64_t e0 = gld(hptr + r), e1 = gld(hptr + r + 1);
-      const v4f s = rd4<BF>(dot4p<BF>(hent + e0, (int)(e1 - e0), sm));
+      HRow h;
+      hrow_req(hptr, hent, r, h);
+      const v4f s = rd4<BF>(hrow_sum<BF>(hent, h));
 #pragma unroll
       for (int k = 0; k < TT; k++)
         if (s[k] != s[k]) key[k] = kmax(key[k], argmax_key(s[k], r));

@@ -302,6 +302,34 @@ class PfBuffers:
         self.err = torch.zeros(1, dtype=torch.int32, device=dev)
 
 
+def head_table(er, w1f: np.ndarray, hidden: int):
+    """The tied head's rows for pf_head: the embedding rows' entries at columns whose final-norm
+    factor (1 + weight) is nonzero, as (slices, row pointers, entries). Entries: off = 16 x
+    column, w = value; each row padded to a multiple of 4 entries, and to at least 4, by entries
+    of weight 0 at column hidden (the head kernel's zero column): a row's sum then takes its
+    entries four at a time with no test, its first four always its own (adding +0 to a sum from
+    +0 changes no bits: such a sum is never -0; an empty row's logit stays +0). Slices: row
+    ranges of about equal work (rows + entries), one per XCD."""
+    keep = w1f[er.cols] != 0
+    rows = np.repeat(np.arange(er.n), np.diff(er.ptr))[keep]
+    cnt = np.bincount(rows, minlength=er.n)
+    plen = np.maximum(4, (cnt + 3) // 4 * 4)
+    hptr = np.zeros(er.n + 1, np.int64)
+    np.cumsum(plen, out=hptr[1:])
+    if int(hptr[-1]) + 4 >= 2**31:  # the head kernel reads the bounds' low 32-bit words
+        raise ValueError("head table: more than 2^31 entries")
+    hent = np.zeros(int(hptr[-1]) + 4, ENT)
+    hent["off"][:] = 16 * hidden
+    pos = hptr[rows] + (np.arange(len(rows)) - np.repeat(np.cumsum(cnt) - cnt, cnt))
+    hent["off"][pos] = 16 * er.cols[keep]
+    hent["w"][pos] = er.vals[keep]
+    work = np.cumsum(np.diff(hptr) + 2)
+    tot = work[-1] if len(work) else 0
+    sl = [0] + [int(np.searchsorted(work, tot * k / SLICES)) for k in range(1, SLICES)] + [er.n]
+    sl = np.maximum.accumulate(np.asarray(sl, np.int64))
+    return sl, hptr, hent
+
+
 class Prefill:
     """The packed tables of a Fast's layers and head on one device, and the drivers."""
 
@@ -331,25 +359,7 @@ class Prefill:
         self.emb_ptr = torch.from_numpy(er.ptr.astype(np.int64)).to(self.dev)
         self.emb_ent = torch.from_numpy(ent.view(np.uint8)).to(self.dev)
         w1f = np.float32(1.0) + np.asarray(sm.norm, np.float32)
-        keep = w1f[er.cols] != 0
-        rows = np.repeat(np.arange(er.n), np.diff(er.ptr))[keep]
-        # each head row padded to a multiple of 4 entries by entries of weight 0 at column hidden
-        # (the head kernel's zero column): a row's sum then takes its entries four at a time
-        # with no test (adding +0 to a sum from +0 changes no bits: such a sum is never -0)
-        cnt = np.bincount(rows, minlength=er.n)
-        plen = (cnt + 3) // 4 * 4
-        hptr = np.zeros(er.n + 1, np.int64)
-        np.cumsum(plen, out=hptr[1:])
-        hent = np.zeros(int(hptr[-1]) + 4, ENT)
-        hent["off"][:] = 16 * d.hidden
-        pos = hptr[rows] + (np.arange(len(rows)) - np.repeat(np.cumsum(cnt) - cnt, cnt))
-        hent["off"][pos] = 16 * er.cols[keep]
-        hent["w"][pos] = er.vals[keep]
-        # slices of about equal work (rows + entries), one per XCD
-        work = np.cumsum(np.diff(hptr) + 2)
-        tot = work[-1] if len(work) else 0
-        sl = [0] + [int(np.searchsorted(work, tot * k / SLICES)) for k in range(1, SLICES)] + [er.n]
-        sl = np.maximum.accumulate(np.asarray(sl, np.int64))
+        sl, hptr, hent = head_table(er, w1f, d.hidden)
         self.head_slice = torch.from_numpy(sl.astype(np.int32)).to(self.dev)
         self.head_ptr = torch.from_numpy(hptr).to(self.dev)
         self.head_ent = torch.from_numpy(hent.view(np.uint8)).to(self.dev)

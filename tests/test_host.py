@@ -348,3 +348,34 @@ def test_runner_refuses_more_tokens_than_the_dump_holds(tmp_path, native_lib):
     r = subprocess.run([mk_build.RUNNER, str(tmp_path), "1"], capture_output=True, text=True,
                        timeout=60)  # the dumped count itself (10) exceeds a 2-token buffer
     assert r.returncode == 2 and "hold 2 predictions" in r.stderr, r.stderr
+
+
+def test_prefill_head_table_rows():
+    """pf_head's table (host only): each row holds its kept entries (columns whose final-norm
+    factor is nonzero) in column order, then zero-weight entries at column hidden up to a multiple
+    of 4 and at least 4 (an empty row too); the slices cover the rows in order."""
+    from types import SimpleNamespace
+    from linuxformer_amd import prefill
+    hidden = 12
+    rows = [[], [(1, 0.5)], [(0, 1.0), (3, -2.0), (5, 0.25), (7, 4.0), (9, -1.0)], [(4, 3.0)],
+            [(2, 1.5), (6, 2.5), (8, -0.5), (10, 0.75)]]
+    ptr = np.cumsum([0] + [len(r) for r in rows]).astype(np.int64)
+    cols = np.asarray([c for r in rows for c, _ in r], np.int64)
+    vals = np.asarray([v for r in rows for _, v in r], np.float32)
+    er = SimpleNamespace(n=len(rows), ptr=ptr, cols=cols, vals=vals)
+    w1f = np.ones(hidden, np.float32)
+    w1f[4] = 0.0  # a column the final norm zeroes: dropped from every row
+    w1f[9] = 0.0
+    sl, hptr, hent = prefill.head_table(er, w1f, hidden)
+    assert hptr[0] == 0 and len(hptr) == len(rows) + 1
+    assert len(hent) == hptr[-1] + 4
+    for i, r in enumerate(rows):
+        kept = [(c, v) for c, v in r if w1f[c] != 0]
+        e = hent[hptr[i]:hptr[i + 1]]
+        n = len(e)
+        assert n >= 4 and n % 4 == 0 and n - len(kept) < 4 + (4 if not kept else 0)
+        assert [(int(o) // 16, float(w)) for o, w in e[:len(kept)]] == [(c, v) for c, v in kept]
+        assert (e["off"][len(kept):] == 16 * hidden).all() and (e["w"][len(kept):] == 0).all()
+    assert (hent["off"][hptr[-1]:] == 16 * hidden).all() and (hent["w"][hptr[-1]:] == 0).all()
+    assert sl[0] == 0 and sl[-1] == len(rows) and (np.diff(sl) >= 0).all()
+    assert len(sl) == prefill.SLICES + 1
