@@ -146,6 +146,16 @@ struct TV {
       return *reinterpret_cast<const v4f*>(v + off);
     }
   }
+  // the same for a tile vector at LDS byte address base (the kernel's dynamic LDS at address 0):
+  // the address formed from the entry's offset alone (a constant base folds into the read)
+  static __device__ __forceinline__ v4f at_lds(uint32_t base, int off) {
+    if constexpr (HALF) {
+      const v2u u = *(const __attribute__((address_space(3))) v2u*)(size_t)(base + ((uint32_t)off >> 1));
+      return v4f{bitsf(u.x << 16), bitsf(u.x & 0xffff0000u), bitsf(u.y << 16), bitsf(u.y & 0xffff0000u)};
+    } else {
+      return *(const __attribute__((address_space(3))) v4f*)(size_t)(base + (uint32_t)off);
+    }
+  }
   static __device__ __forceinline__ v4f get(const uint8_t* v, int c) { return at(v, 16 * c); }
   static __device__ __forceinline__ void put(uint8_t* v, int c, v4f x) {
     if constexpr (HALF) {
@@ -159,7 +169,11 @@ struct TV {
   }
 };
 
-template <bool BF, bool HALF = false>
+// the tile kernel's residual tile: LDS byte address (after 512 bytes of sums and masks)
+#define X_HV 512
+// (PAD: the row is padded to a multiple of 4 entries at a column holding +0, weight 0, so every
+// entry of its last group adds its term with no test)
+template <bool BF, bool HALF = false, bool PAD = false>
 __device__ __forceinline__ v4f dot4(const lxm_pf_ent* __restrict__ e, int n, const uint8_t* x) {
   v4f s = {0.0f, 0.0f, 0.0f, 0.0f};
   for (int k0 = 0; k0 < n; k0 += 4) {
@@ -171,13 +185,14 @@ __device__ __forceinline__ v4f dot4(const lxm_pf_ent* __restrict__ e, int n, con
     for (int j = 0; j < 4; j++) xv[j] = TV<HALF>::at(x, en[j].off);
 #pragma unroll
     for (int j = 0; j < 4; j++)
-      if (k0 + j < n) s = acc4<BF>(s, xv[j], en[j].w);
+      if (PAD || k0 + j < n) s = acc4<BF>(s, xv[j], en[j].w);
   }
   return s;
 }
 // The same over the RMSNorm of a tile: each gathered column x becomes D((x * r) * w1) (norm4),
 // w1 the column's norm weight from the table parallel to the entries.
-template <bool BF, bool HALF>
+// (PAD: padded rows as for dot4, and x the tile kernel's residual tile at LDS address X_HV)
+template <bool BF, bool HALF, bool PAD = false>
 __device__ __forceinline__ v4f dot4n(const lxm_pf_ent* __restrict__ e, const float* __restrict__ en,
                                      int n, const uint8_t* x, v4f r) {
   v4f s = {0.0f, 0.0f, 0.0f, 0.0f};
@@ -191,10 +206,10 @@ __device__ __forceinline__ v4f dot4n(const lxm_pf_ent* __restrict__ e, const flo
     }
     v4f xv[4];
 #pragma unroll
-    for (int j = 0; j < 4; j++) xv[j] = TV<HALF>::at(x, ee[j].off);
+    for (int j = 0; j < 4; j++) xv[j] = PAD ? TV<HALF>::at_lds(X_HV, ee[j].off) : TV<HALF>::at(x, ee[j].off);
 #pragma unroll
     for (int j = 0; j < 4; j++)
-      if (k0 + j < n) s = acc4<BF>(s, norm4<BF>(xv[j], r, nw[j]), ee[j].w);
+      if (PAD || k0 + j < n) s = acc4<BF>(s, norm4<BF>(xv[j], r, nw[j]), ee[j].w);
   }
   return s;
 }
@@ -301,8 +316,8 @@ __device__ __forceinline__ v4f hsum(uint8_t* HV, int H, v4f* wsum, bool plus0) {
 // The norms' outputs are formed as the entries gather (each entry carries its column's norm
 // weight), so LDS holds 512 bytes of sums and masks, the residual (hidden columns) and the MLP
 // units' outputs, as tile vectors in the model dtype (bf16, hidden 3,572, 1,024 units: 37 KB,
-// four workgroups per CU).
-#define X_HV 512
+// four workgroups per CU), each followed by a column of zeros that the rows' padding entries
+// read (rows padded to multiples of 4 entries, summed with no per-entry test).
 // A residual tile from HBM (model dtype) into LDS tile vectors (bf16 if HALF): every thread's
 // columns (t, t + 512, ...) loaded at once.
 template <bool BF, bool HALF>
@@ -317,7 +332,7 @@ __device__ __forceinline__ void load_tile(const void* h, int64_t b, int H, uint8
     if (t + k * NT < H) TV<HALF>::put(HV, t + k * NT, x[k]);
 }
 template <bool BF>
-__host__ __device__ constexpr int x_xm(int H) { return X_HV + ((TV<BF>::B * H + 15) & ~15); }
+__host__ __device__ constexpr int x_xm(int H) { return X_HV + ((TV<BF>::B * (H + 1) + 15) & ~15); }
 template <bool BF>
 __global__ __launch_bounds__(NT) void pf_tile(const lxm_pf_params* __restrict__ pp, int Lm, int Ln) {
   extern __shared__ __align__(16) uint8_t sm[];
@@ -330,7 +345,13 @@ __global__ __launch_bounds__(NT) void pf_tile(const lxm_pf_params* __restrict__ 
   v4f* wsB = reinterpret_cast<v4f*>(sm + 192);
   uint8_t* HV = sm + X_HV;
   uint8_t* XM = sm + x_xm<BF>(H);
+  // the residual tile is read at LDS address X_HV + offset (dot4n): the LDS must start at 0
+  if ((uint32_t)(size_t)(const __attribute__((address_space(3))) uint8_t*)sm != 0u) {
+    if (t == 0) *p.err = 2;
+    return;
+  }
   if (t < TT) smask[t] = 0;
+  if (t == 0) V::put(HV, H, v4f{0.0f, 0.0f, 0.0f, 0.0f});  // the padding entries' zero column
   load_tile<BF, BF>(p.h, b, H, HV);
   __syncthreads();
   if (Lm >= 0) {
@@ -349,8 +370,8 @@ __global__ __launch_bounds__(NT) void pf_tile(const lxm_pf_params* __restrict__ 
       const int u = t + i * NT;
       if (u < ly.n_units) {
         const lxm_pf_unit q = gld(un + u);
-        const v4f g = rd4<BF>(dot4n<BF, BF>(ent + q.gs, entn + q.gs, q.gn, HV, r));
-        const v4f v = rd4<BF>(dot4n<BF, BF>(ent + q.us, entn + q.us, q.un, HV, r));
+        const v4f g = rd4<BF>(dot4n<BF, BF, true>(ent + q.gs, entn + q.gs, q.gn, HV, r));
+        const v4f v = rd4<BF>(dot4n<BF, BF, true>(ent + q.us, entn + q.us, q.un, HV, r));
         a[i] = v4f{rd<BF>(silu_rd<BF>(g.x) * v.x), rd<BF>(silu_rd<BF>(g.y) * v.y),
                    rd<BF>(silu_rd<BF>(g.z) * v.z), rd<BF>(silu_rd<BF>(g.w) * v.w)};
       }
@@ -358,12 +379,13 @@ __global__ __launch_bounds__(NT) void pf_tile(const lxm_pf_params* __restrict__ 
 #pragma unroll
     for (int i = 0; i < LXM_PF_UPT; i++)
       if (t + i * NT < ly.n_units) V::put(XM, t + i * NT, a[i]);
+    if (t == 0) V::put(XM, ly.n_units, v4f{0.0f, 0.0f, 0.0f, 0.0f});  // the down rows' zero column
     __syncthreads();
     // down_proj rows over the units (entries 16 x unit position), added to the residual
     const lxm_pf_drow* dr = tab<lxm_pf_drow>(p.blob, ly.drows);
     for (int i = t; i < ly.n_drows; i += NT) {
       const lxm_pf_drow d = gld(dr + i);
-      const v4f s = rd4<BF>(dot4<BF, BF>(ent + d.start, d.len, XM));
+      const v4f s = rd4<BF>(dot4<BF, BF, true>(ent + d.start, d.len, XM));
       V::put(HV, d.row, rd4<BF>(V::get(HV, d.row) + s));
     }
     __syncthreads();
@@ -381,7 +403,7 @@ __global__ __launch_bounds__(NT) void pf_tile(const lxm_pf_params* __restrict__ 
     const lxm_pf_qk* qk = tab<lxm_pf_qk>(p.blob, ly.qk);
     for (int i = t; i < ly.n_qk; i += NT) {
       const lxm_pf_qk q = gld(qk + i);
-      const v4f P = rd4<BF>(dot4n<BF, BF>(ent + q.start, entn + q.start, q.len, HV, r));
+      const v4f P = rd4<BF>(dot4n<BF, BF, true>(ent + q.start, entn + q.start, q.len, HV, r));
       const uint32_t bit = 1u << q.kslot;
       if (P.x != 0.0f) atomicOr(smask + 0, bit);
       if (P.y != 0.0f) atomicOr(smask + 1, bit);
@@ -392,7 +414,7 @@ __global__ __launch_bounds__(NT) void pf_tile(const lxm_pf_params* __restrict__ 
     const lxm_pf_dec* dc = tab<lxm_pf_dec>(p.blob, ly.dec);
     for (int i = t; i < ly.n_dec; i += NT) {
       const lxm_pf_dec d = gld(dc + i);
-      const v4f a = d.len ? rd4<BF>(dot4n<BF, BF>(ent + d.start, entn + d.start, d.len, HV, r))
+      const v4f a = d.len ? rd4<BF>(dot4n<BF, BF, true>(ent + d.start, entn + d.start, d.len, HV, r))
                           : v4f{0.0f, 0.0f, 0.0f, 0.0f};
       const float na = -cr_exp(d.A_log);
 #pragma unroll
@@ -1031,7 +1053,7 @@ __global__ void pf_tiles_k(const void* x, void* y, int T, int H, int dir) {
 // Host side.
 template <bool BF>
 static int tile_lds(int H, int n_units_max) {
-  return x_xm<BF>(H) + TV<BF>::B * (n_units_max > 0 ? n_units_max : 1);
+  return x_xm<BF>(H) + TV<BF>::B * (n_units_max + 1);
 }
 #define ACT_LDS (A_MISC + 16)
 #define ACT_GRID 1024

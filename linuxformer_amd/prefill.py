@@ -83,6 +83,18 @@ class _Ents:
         self.n += k
         return start
 
+    def add4(self, offs, ws, nw, zero: int) -> int:
+        """add() for a row that the tile kernel sums four entries at a time with no test: padded
+        to a multiple of 4 by entries (off = zero, w = 0, norm weight 0), zero being 16 x a
+        column that holds +0 (adding +0 x 0 to a sum from +0 changes no bits: such a sum is
+        never -0). The row's length stays its own."""
+        offs, ws = np.asarray(offs, np.int64), np.asarray(ws, np.float32)
+        p = (-len(offs)) % 4
+        nw = np.zeros(len(offs), np.float32) if nw is None else np.asarray(nw, np.float32)
+        return self.add(np.concatenate([offs, np.full(p, zero, np.int64)]),
+                        np.concatenate([ws, np.zeros(p, np.float32)]),
+                        np.concatenate([nw, np.zeros(p, np.float32)]))
+
     def pad(self) -> None:
         """Four entries (off 0, w 0) closing a group: a row's last load of four entries reads
         its own group or these, never a table of another vector."""
@@ -140,7 +152,9 @@ def pack_layer(sm, fast, L: int, blob: _Blob) -> PfLayer:
     dec_info = fast.dec[L]
     E = _Ents()
     pl = PfLayer()
-    # ---- MLP: live units sorted by length (thread-strided, similar lengths per wave)
+    # ---- MLP: live units sorted by length (thread-strided, similar lengths per wave); the tile
+    # kernel's rows (units, down_proj, query/key channels, decays) padded to multiples of 4 at a
+    # zero column (column hidden of the residual tile, column n_units of the units' outputs)
     g, u = _Csr(ly.gate_proj), _Csr(ly.up_proj)
     w1_in = np.float32(1.0) + np.asarray(ly.input_layernorm, np.float32)
     w1_post = np.float32(1.0) + np.asarray(ly.post_attention_layernorm, np.float32)
@@ -155,9 +169,9 @@ def pack_layer(sm, fast, L: int, blob: _Blob) -> PfLayer:
     ut = np.zeros((len(units), 4), np.int32)
     for i, un in enumerate(units):
         c, v = g.row(un)
-        ut[i, 0], ut[i, 1] = E.add(16 * c, v, w1_post[c]), len(c)
+        ut[i, 0], ut[i, 1] = E.add4(16 * c, v, w1_post[c], 16 * H), len(c)
         c, v = u.row(un)
-        ut[i, 2], ut[i, 3] = E.add(16 * c, v, w1_post[c]), len(c)
+        ut[i, 2], ut[i, 3] = E.add4(16 * c, v, w1_post[c], 16 * H), len(c)
     E.pad()
     # down_proj rows over the live units, entries in ascending unit order (16 x position)
     dcoo = ly.down_proj
@@ -171,7 +185,8 @@ def pack_layer(sm, fast, L: int, blob: _Blob) -> PfLayer:
     dt = np.zeros((len(rows_u), 4), np.int32)
     for i, k in enumerate(dorder):
         a, n = rstart_src[k], rcount[k]
-        dt[i] = (rows_u[k], E.add(16 * dcols[a:a + n], dvals[a:a + n]), n, 0)
+        dt[i] = (rows_u[k], E.add4(16 * dcols[a:a + n], dvals[a:a + n], None, 16 * len(units)),
+                 n, 0)
     E.pad()
     # ---- gates: live key heads' query/key channels with a nonzero tap
     qkv = _Csr(ly.in_proj_qkv)
@@ -190,7 +205,8 @@ def pack_layer(sm, fast, L: int, blob: _Blob) -> PfLayer:
                     continue
                 reach = max(reach, 3 - int(np.nonzero(tp)[0][0]))
                 c, v = qkv.row(ch)
-                qk_rows.append((ch, s, part * KD + i, E.add(16 * c, v, w1_in[c]), len(c), tp))
+                qk_rows.append((ch, s, part * KD + i, E.add4(16 * c, v, w1_in[c], 16 * H), len(c),
+                                tp))
     qkt = np.zeros(len(qk_rows), np.dtype([("chan", "<i4"), ("kslot", "<i4"), ("pos", "<i4"),
                                            ("start", "<i4"), ("len", "<i4"), ("pad", "<i4", 3),
                                            ("taps", "<f4", 4)]))
@@ -214,8 +230,8 @@ def pack_layer(sm, fast, L: int, blob: _Blob) -> PfLayer:
                                            ("pad", "<i4", 3)]))
     for i, vh in enumerate(decays):
         c, v = acsr.row(vh)
-        dect[i] = (vslot[vh], E.add(16 * c, v, w1_in[c]), len(c), ly.dt_bias[vh], ly.A_log[vh],
-                   (0, 0, 0))
+        dect[i] = (vslot[vh], E.add4(16 * c, v, w1_in[c], 16 * H), len(c), ly.dt_bias[vh],
+                   ly.A_log[vh], (0, 0, 0))
     zcsr, bcsr = _Csr(ly.in_proj_z), _Csr(ly.in_proj_b)
     vct = np.zeros(len(slots) * VD, np.dtype([("start", "<i4"), ("len", "<i4"), ("taps", "<f4", 4)]))
     zt = np.zeros((len(slots) * VD, 2), np.int32)
