@@ -459,15 +459,34 @@ __global__ __launch_bounds__(C_NT) void pf_compact(const lxm_pf_params* __restri
   const lxm_pf_layer& ly = p.layers[L];
   const int t = threadIdx.x, T = p.T, reach = ly.reach;
   const uint32_t allk = ly.n_ks >= 32 ? 0xffffffffu : ((1u << ly.n_ks) - 1u);
+  const bool vec = (reinterpret_cast<uintptr_t>(p.mask) & 15u) == 0;
   if (t == 0) base_s = 0;
   __syncthreads();
   for (int r0 = 0; r0 < T; r0 += C_NT * C_PER) {
     const int t0 = r0 + t * C_PER;
     uint32_t m[C_PER + 3];
+    // m[3 + i]: the mask of position t0 + i, by eight 16-byte loads where the thread's 32 lie
+    // inside T and the array is 16-byte aligned (a lane's run is one 128-byte line); m[0..2]: the
+    // three before t0, from the lane below (its last three), lane 0 reading its own
+    if (vec && t0 + C_PER <= T) {
+      const uint4* src = reinterpret_cast<const uint4*>(p.mask + t0);
 #pragma unroll
-    for (int i = 0; i < C_PER + 3; i++) {
+      for (int j = 0; j < C_PER / 4; j++) {
+        const uint4 v = gld(src + j);
+        m[3 + 4 * j] = v.x;
+        m[4 + 4 * j] = v.y;
+        m[5 + 4 * j] = v.z;
+        m[6 + 4 * j] = v.w;
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < C_PER; i++) m[3 + i] = t0 + i < T ? p.mask[t0 + i] : 0u;
+    }
+#pragma unroll
+    for (int i = 0; i < 3; i++) {
+      const uint32_t below = __shfl_up(m[C_PER + i], 1);
       const int tp = t0 - 3 + i;
-      m[i] = (tp >= 0 && tp < T) ? p.mask[tp] : 0u;
+      m[i] = (t & 63) ? below : (tp >= 0 && tp < T) ? p.mask[tp] : 0u;
     }
     int n = 0;
     uint32_t cm[C_PER];
