@@ -592,10 +592,20 @@ __global__ __launch_bounds__(NT) void pf_act(const lxm_pf_params* __restrict__ p
     float rr[4];
 #pragma unroll
     for (int s = 0; s < 4; s++) rr[s] = tok - s >= 0 ? p.r1[tok - s] : 0.0f;
+    // positions tok - s, s = 0..3: lane l0 - s of tile tok / 4 for s <= l0, else lane l0 - s + 4 of
+    // the tile before (tok / 4 and l0 the same for the whole workgroup), read as columns
+    const int64_t b0 = tok >> 2;
+    const int l0 = tok & 3;
     for (int c = t; c < H; c += NT) {
+      const v4f c0 = ld_col<BF>(p.h, b0, H, c);
+      const v4f c1 = l0 < 3 && b0 > 0 ? ld_col<BF>(p.h, b0 - 1, H, c) : v4f{0.0f, 0.0f, 0.0f, 0.0f};
+      const float w = w1[c];
       v4f x;
 #pragma unroll
-      for (int s = 0; s < 4; s++) x[s] = tok - s >= 0 ? rd<BF>((ld_el<BF>(p.h, H, tok - s, c) * rr[s]) * w1[c]) : 0.0f;
+      for (int s = 0; s < 4; s++) {
+        const float h = s <= l0 ? c0[l0 - s] : c1[l0 - s + 4];
+        x[s] = tok - s >= 0 ? rd<BF>((h * rr[s]) * w) : 0.0f;
+      }
       XN[c] = x;
     }
     for (int i = t; i < ly.n_ks * 2 * KD; i += NT) QK[i] = 0.0f;
