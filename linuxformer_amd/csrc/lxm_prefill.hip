@@ -702,23 +702,33 @@ __global__ __launch_bounds__(256) void pf_tail(const lxm_pf_params* __restrict__
   const float* w1 = tab<float>(p.blob, ly.w1_in);
   const lxm_row row = tab<lxm_row>(p.blob, ly.cc)[c];
   void* cs = p.conv[L];
-  float win[4];
+  // one pass over the channel's entries forms the four window sums (each in entry order); the
+  // positions T-4..T-1 are lanes of the last tile and the one before it, read as columns
+  const int64_t b0 = (T - 1) >> 2;
+  const int l0 = (T - 1) & 3;
+  float r[4], s[4];
 #pragma unroll
   for (int j = 0; j < 4; j++) {
-    const int tp = T - 4 + j;
-    if (tp >= 0) {
-      const float r = p.r1[tp];
-      float s = 0.0f;
-      for (int k = 0; k < row.len; k++) {
-        const lxm_pf_ent e = ent[row.start + k];
-        const int col = e.off >> 4;
-        s = acc<BF>(s, rd<BF>((ld_el<BF>(p.h, H, tp, col) * r) * w1[col]), e.w);
-      }
-      win[j] = rd<BF>(s);
-    } else {
-      win[j] = conv_ld<BF>(cs, (int64_t)c * 4 + j + T);
+    r[j] = T - 4 + j >= 0 ? p.r1[T - 4 + j] : 0.0f;
+    s[j] = 0.0f;
+  }
+  for (int k = 0; k < row.len; k++) {
+    const lxm_pf_ent e = ent[row.start + k];
+    const int col = e.off >> 4;
+    const float w = w1[col];
+    const v4f c0 = ld_col<BF>(p.h, b0, H, col);
+    const v4f c1 = l0 < 3 && b0 > 0 ? ld_col<BF>(p.h, b0 - 1, H, col) : v4f{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+      const int d = 3 - j;  // position T-1-d
+      const float h = d <= l0 ? c0[l0 - d] : c1[l0 - d + 4];
+      if (T - 4 + j >= 0) s[j] = acc<BF>(s[j], rd<BF>((h * r[j]) * w), e.w);
     }
   }
+  float win[4];
+#pragma unroll
+  for (int j = 0; j < 4; j++)
+    win[j] = T - 4 + j >= 0 ? rd<BF>(s[j]) : conv_ld<BF>(cs, (int64_t)c * 4 + j + T);
 #pragma unroll
   for (int j = 0; j < 4; j++) conv_st<BF>(cs, (int64_t)c * 4 + j, win[j]);
 }
