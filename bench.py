@@ -141,6 +141,37 @@ def sync_costs(n_blocks: int) -> dict:
     return out
 
 
+def latency_roofline(sync: dict, ev_tok: float, us_tok: float) -> dict:
+    """The decode's synchronisation floor per token: one-way cross-XCD hops, 2 for the head
+    (chain -> helpers -> chain) and 3 per GDN event (chain -> value-head owners -> out_proj
+    helpers -> chain), each half of the round trip measured live (lxm_t_sync)."""
+    rt = sync["round_trip_other_xcd_us"]
+    hops = 2.0 + 3.0 * ev_tok
+    t = hops * rt / 2.0
+    return {"round_trip_us": rt, "hops_per_token": round(hops, 4),
+            "round_trips_per_token": round(hops / 2.0, 4), "gdn_events_per_token": round(ev_tok, 4),
+            "t_sync_us": round(t, 2), "t_measured_us": round(us_tok, 2),
+            "frac": round(t / us_tok, 4), "sync": sync}
+
+
+def restore(cache, saved) -> None:
+    for ly, (c, r) in zip(cache.layers, saved):
+        ly.conv_states[0].copy_(c)
+        ly.recurrent_states[0].copy_(r)
+
+
+def chain_counters(mg, start: int, n: int) -> dict:
+    """The chain's own counters over one launch of n greedy tokens from start: GDN events and MLP
+    redos (the MLP run again after an event with a live query) per token."""
+    import torch
+
+    prof = torch.zeros(mg.prof_size, dtype=torch.int64, device=mg.dev)
+    preds = mg.run([start], n, prof=prof)
+    rep = mg.phase_report(prof)
+    return {"tokens": n, "events_per_token": rep["GDN events per token"],
+            "mlp_redos_per_token": rep["MLP redos per token"], "preds": preds}
+
+
 def state_sha(cache) -> tuple:
     """sha256 of the final conv windows and recurrent states as float32, layer after layer (the
     bytes of the stacked (L, C, 4) and (L, nv, 256, 128) arrays; every zero of the states made
@@ -221,9 +252,7 @@ def decode_leg(args, dev, hf_holder: dict) -> dict:
         preds = mg.run([tok], sizes[0])
         tok = preds[-1]
         log(f"[bench] warm-up launch {w + 1}/{args.warmup}: {sizes[0]} tokens")
-    for ly, (c, r) in zip(cache.layers, saved):  # the timed chunk starts from the initial state
-        ly.conv_states[0].copy_(c)
-        ly.recurrent_states[0].copy_(r)
+    restore(cache, saved)  # the timed chunk starts from the initial state
     torch.cuda.synchronize()
 
     stream_preds, evs = [], []
@@ -276,20 +305,13 @@ def decode_leg(args, dev, hf_holder: dict) -> dict:
                               "continuing from the chunk's final state"}
         log(f"[bench] forced stream: {n_f} tokens at {forced_out['tok_s']} tok/s")
 
-    # the chain's own counters on the chunk's first tokens, from the initial state again: GDN
-    # events and MLP redos (the MLP run again after an event with a live query) per token
+    # the chain's own counters on the chunk's first tokens, from the initial state again
     n_c = min(4096, chunk)
-    for ly, (c, r) in zip(cache.layers, saved):
-        ly.conv_states[0].copy_(c)
-        ly.recurrent_states[0].copy_(r)
-    prof = torch.zeros(mg.prof_size, dtype=torch.int64, device=dev)
-    counted = mg.run([start], n_c, prof=prof)
-    rep = mg.phase_report(prof)
-    gdn_out = {"tokens": n_c, "events_per_token": rep["GDN events per token"],
-               "mlp_redos_per_token": rep["MLP redos per token"],
-               "stream_equal": counted == stream_preds[:n_c],
-               "note": "the chain's counters on the chunk's first tokens (a second launch from "
-                       "the initial state)"}
+    restore(cache, saved)
+    gdn_out = chain_counters(mg, start, n_c)
+    gdn_out["stream_equal"] = gdn_out.pop("preds") == stream_preds[:n_c]
+    gdn_out["note"] = ("the chain's counters on the chunk's first tokens (a second launch from the "
+                       "initial state)")
     log(f"[bench] GDN events {gdn_out['events_per_token']}/token, MLP redos "
         f"{gdn_out['mlp_redos_per_token']}/token")
 
@@ -298,10 +320,10 @@ def decode_leg(args, dev, hf_holder: dict) -> dict:
         session_out = session_leg(args, dev, f, model, conv0, rec0, start, stream_preds)
 
     sync = sync_costs(mg.ncta)
+    hf_holder["sync"] = sync
     log(f"[bench] sync costs: {sync}")
     us_tok = kern_ms * 1e3 / (chunk / len(sizes))
-    rt = sync["round_trip_other_xcd_us"]
-    n_rt = 1.0 + 2.0 * ev_tok
+    lat = latency_roofline(sync, ev_tok, us_tok)
 
     b_tok = survey_bytes_per_token(model, spec.p_gate)
     achieved = b_tok * (chunk / len(sizes)) / (kern_ms * 1e-3) / 1e9
@@ -327,13 +349,7 @@ def decode_leg(args, dev, hf_holder: dict) -> dict:
                      "bytes_per_token": round(b_tok),
                      "kernel_ms_per_launch": round(kern_ms, 3),
                      "launch_ms": [round(x, 2) for x in launch_ms]},
-        # the decode is latency-bound: one cross-XCD round trip per token for the head and two per
-        # GDN event (chain -> value-head helpers -> out_proj helpers -> chain), measured live
-        "latency_roofline": {"round_trip_us": rt, "round_trips_per_token": round(n_rt, 4),
-                             "gdn_events_per_token": round(ev_tok, 4),
-                             "t_sync_us": round(n_rt * rt, 2),
-                             "t_measured_us": round(us_tok, 2),
-                             "frac": round(n_rt * rt / us_tok, 4), "sync": sync},
+        "latency_roofline": lat,
         "check": {"stream_sha256": stream_sha, "conv_sha256": conv_sha, "rec_sha256": rec_sha,
                   "distinct_predictions": len(set(stream_preds)),
                   "matches_oracle_chunk": None if gold is None else bool(
@@ -349,6 +365,7 @@ def decode_leg(args, dev, hf_holder: dict) -> dict:
         out["check"]["oracle_prefix_match"] = want == stream_preds[:len(want)]
     del mg, cache, saved
     torch.cuda.empty_cache()
+    hf_holder["model"] = model
     if args.cpu_seconds > 0:
         from linuxformer_amd import synth as sy
 
@@ -359,8 +376,8 @@ def decode_leg(args, dev, hf_holder: dict) -> dict:
         log(f"[bench] stock model (dense, bf16) built in {time.time() - t:.1f}s")
         tps, n, cp = stock_decode_baseline(hf, conv0, rec0, start, 64, args.cpu_seconds)
         out["cpu_baseline"] = {
-            "value": round(tps, 3), "unit": "tok/s", "cores": cpu_threads(), "kind": "port",
-            "impl": "torch-eager",
+            "value": round(tps, 3), "unit": "tok/s", "cores": cpu_threads(),
+            "kind": "reference", "impl": "transformers-modules, torch eager",
             "sample": f"the chunk's first {n} greedy steps through the stock forward "
                       f"(transformers {_tf_version()} Qwen3_5 decoder layers on dense bf16 "
                       "tensors, torch eager, lx/lx/hf.py:169-184's chip view), "
@@ -401,6 +418,171 @@ def session_leg(args, dev, f, model, conv0, rec0, start: int, stream_preds) -> d
     log(f"[bench] session decode: {res['tok_s']} tok/s over {n} tokens; stream equal: {same}")
     del s, cache
     return res
+
+
+def stress_leg(args, dev, hf_holder: dict) -> dict:
+    """config 2's stack with write gates on for half of the layer-steps, 65,536
+    greedy tokens from the config's start token and initial state, as --c5-steps launches
+    continuing one stream after one warm-up launch (the state restored after it). Reported next
+    to config 2: tok/s, GDN events and MLP redos per token (the redo counts; lx/lx/mega.py:495-504
+    reports the reference's), the rooflines, the stream and final states against the CPU
+    oracle's run of the same tokens (tests/golden/c5_run.json), and the stock forward on the
+    host over the first steps."""
+    import numpy as np
+    import torch
+
+    from linuxformer_amd import fast, mega, synth
+
+    spec = synth.config5()
+    t0 = time.time()
+    base = hf_holder.get("model")
+    model = synth.build(spec, layers=base.layers if base is not None else None)
+    conv0, rec0 = synth.init_state(model)
+    start = synth.start_token(spec)
+    f = fast.Fast(model)
+    cache = fast.StateCache(conv0, rec0, model.dims.dtype, dev)
+    mg = mega.Mega(f, model, cache, 0)
+    torch.cuda.synchronize()
+    log(f"[bench] c5: built and packed in {time.time() - t0:.1f}s")
+    n_tok = args.c5_tokens
+    sizes = split_chunk(n_tok, args.c5_steps)
+    saved = [(ly.conv_states[0].clone(), ly.recurrent_states[0].clone()) for ly in cache.layers]
+    mg.run([start], sizes[0])  # warm-up launch
+    restore(cache, saved)
+    stream = torch.cuda.current_stream(dev)
+    torch.cuda.synchronize()
+    preds, evs, tok = [], [], start
+    t_start = time.perf_counter()
+    for k, n in enumerate(sizes):
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        p = mg.run([tok], n)
+        e1.record(stream)
+        evs.append((e0, e1))
+        preds += p
+        tok = p[-1]
+        log(f"[bench] c5 step {k + 1}/{len(sizes)}: {n} tokens, {len(preds)} of {n_tok}")
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t_start
+    launch_ms = [a.elapsed_time(b) for a, b in evs]
+    kern_ms = sum(launch_ms) / len(launch_ms)
+    stream_sha = hashlib.sha256(np.asarray(preds, "<i4").tobytes()).hexdigest()
+    conv_sha, rec_sha = state_sha(cache)
+    gold = None
+    path = os.path.join(HERE, "tests", "golden", "c5_run.json")
+    if os.path.exists(path):
+        g = json.load(open(path))
+        if g.get("config") == spec.name and g.get("chunk") == n_tok and g.get("start") == start:
+            gold = g
+    inputs = [start] + preds[:-1]
+    ev_tok = gates_per_token(model, inputs)
+    restore(cache, saved)
+    n_c = min(args.c5_count_tokens, n_tok)
+    counted = chain_counters(mg, start, n_c)
+    counted["stream_equal"] = counted.pop("preds") == preds[:n_c]
+    sync = hf_holder.get("sync") or sync_costs(mg.ncta)
+    us_tok = kern_ms * 1e3 / (n_tok / len(sizes))
+    b_tok = survey_bytes_per_token(model, spec.p_gate)
+    achieved = b_tok * (n_tok / len(sizes)) / (kern_ms * 1e-3) / 1e9
+    out = {"metric": "greedy decode tok/s, config 5 (config 2's stack, 50 % of layer-steps gated)",
+           "value": round(n_tok / wall, 1), "unit": "tok/s", "steps": len(sizes),
+           "ms_per_step": round(wall * 1e3 / len(sizes), 3),
+           "config": {"workload": f"c5: {n_tok} greedy tokens of the 37-layer synthetic stack with "
+                                  f"write gates on {spec.p_gate:.0%} of layer-steps, batch 1, "
+                                  f"{len(sizes)} launches continuing one stream",
+                      "tokens": n_tok, "tokens_per_step": sizes, "p_gate": spec.p_gate},
+           "gdn_events_per_token": round(ev_tok, 4),
+           "redo": counted,
+           "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS,
+                        "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 5),
+                        "traffic": None, "bytes_per_token": round(b_tok),
+                        "kernel_ms_per_launch": round(kern_ms, 3)},
+           "latency_roofline": latency_roofline(sync, ev_tok, us_tok),
+           "check": {"stream_sha256": stream_sha, "conv_sha256": conv_sha, "rec_sha256": rec_sha,
+                     "distinct_predictions": len(set(preds)),
+                     "matches_oracle": None if gold is None else bool(
+                         gold["stream_sha256"] == stream_sha and gold["conv_sha256"] == conv_sha
+                         and gold["rec_sha256"] == rec_sha)}}
+    log(f"[bench] c5: {out['value']} tok/s, {ev_tok:.2f} GDN events/token, matches oracle: "
+        f"{out['check']['matches_oracle']}")
+    del mg, cache, saved
+    torch.cuda.empty_cache()
+    hf = hf_holder.get("hf")
+    if hf is not None and args.cpu_seconds > 0:
+        from oracle import stock
+
+        stock.set_embedding(hf, model.embed)
+        tps, n, cp = stock_decode_baseline(hf, conv0, rec0, start, 64, args.cpu_seconds)
+        out["cpu_baseline"] = {
+            "value": round(tps, 3), "unit": "tok/s", "cores": cpu_threads(),
+            "kind": "reference", "impl": "transformers-modules, torch eager",
+            "sample": f"the run's first {n} greedy steps through the stock forward (transformers "
+                      f"{_tf_version()} Qwen3_5 decoder layers on dense bf16 tensors, torch eager), "
+                      f"{cpu_threads()} host threads"}
+        out["check"]["stock_prefix_match"] = cp == preds[:n]
+        log(f"[bench] c5 CPU stock decode: {tps:.3f} tok/s over {n} steps")
+    return out
+
+
+def plumbing_leg(args, dev) -> dict:
+    """the one chip-shaped fp32 layer, 256 greedy steps from the config's
+    start token and zero state, one launch per run; --c1-runs timed runs from the same initial
+    state (restored between them, untimed). Predictions and final states against the stock
+    forward's run of the same steps (tests/golden/c1_256.npz, transformers' own modules); the
+    stock forward on the host over all 256 steps as the CPU baseline."""
+    import numpy as np
+    import torch
+
+    from linuxformer_amd import fast, mega, synth
+
+    spec = synth.config1()
+    model = synth.build(spec)
+    conv0, rec0 = synth.init_state(model)
+    start = synth.start_token(spec)
+    f = fast.Fast(model)
+    cache = fast.StateCache(conv0, rec0, model.dims.dtype, dev)
+    mg = mega.Mega(f, model, cache, 0)
+    n = spec.n_steps
+    saved = [(ly.conv_states[0].clone(), ly.recurrent_states[0].clone()) for ly in cache.layers]
+    mg.run([start], n)  # warm-up
+    stream = torch.cuda.current_stream(dev)
+    ms, preds = [], None
+    for _ in range(args.c1_runs):
+        restore(cache, saved)
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        e0.record(stream)
+        preds = mg.run([start], n)
+        e1.record(stream)
+        torch.cuda.synchronize()
+        ms.append(e0.elapsed_time(e1))
+    conv_sha, rec_sha = state_sha(cache)
+    g = np.load(os.path.join(HERE, "tests", "golden", "c1_256.npz"))
+    same = bool(int(g["start"]) == start and g["preds"].tolist() == preds
+                and str(g["conv_sha"]) == conv_sha and str(g["rec_sha"]) == rec_sha)
+    call_ms = sum(ms) / len(ms)
+    out = {"metric": "greedy decode tok/s, config 1 (one chip-shaped fp32 layer)",
+           "value": round(n / (call_ms * 1e-3), 1), "unit": "tok/s", "runs": len(ms),
+           "ms_per_run": round(call_ms, 3), "dtype": "fp32",
+           "config": {"workload": f"c1: {n} greedy steps of one fp32 layer (hidden "
+                                  f"{model.dims.hidden}, 16 key x 128 value heads, SwiGLU 1024, "
+                                  f"vocab {model.dims.vocab}) from a zero state, one launch"},
+           "check": {"matches_stock_golden": same, "distinct_predictions": len(set(preds))}}
+    log(f"[bench] c1: {out['value']} tok/s ({call_ms:.3f} ms per {n} steps); stock golden: {same}")
+    del mg, cache, saved
+    if args.cpu_seconds > 0:
+        from linuxformer_amd import synth as sy
+
+        hf = sy.to_hf(model)
+        tps, m, cp = stock_decode_baseline(hf, conv0, rec0, start, n, args.cpu_seconds)
+        out["cpu_baseline"] = {
+            "value": round(tps, 3), "unit": "tok/s", "cores": cpu_threads(),
+            "kind": "reference", "impl": "transformers-modules, torch eager",
+            "sample": f"{m} greedy steps through the stock forward (transformers {_tf_version()} "
+                      f"Qwen3_5 decoder layer, fp32, torch eager), {cpu_threads()} host threads"}
+        out["check"]["stock_prefix_match"] = cp == preds[:m]
+        log(f"[bench] c1 CPU stock decode: {tps:.2f} tok/s over {m} steps")
+    return out
 
 
 def _tf_version() -> str:
@@ -491,7 +673,7 @@ def prefill_leg(args, dev, hf_holder: dict) -> dict:
         agree = float((pc == p0[:n_cpu]).mean())
         out["cpu_baseline"] = {
             "value": round(n_cpu / dt, 2), "unit": "tok/s", "cores": cpu_threads(),
-            "kind": "port", "impl": "torch-eager",
+            "kind": "reference", "impl": "transformers-modules, torch eager",
             "sample": f"one call over the first {n_cpu} positions of the warm-up call's tokens: "
                       f"the stock forward's T > 1 path (transformers {_tf_version()} "
                       "Qwen3_5 layers, torch_chunk_gated_delta_rule, dense bf16, torch eager), "
@@ -690,8 +872,14 @@ def make_parser() -> argparse.ArgumentParser:
                     help="chunk prefix checked against the C oracle (0: skip)")
     ap.add_argument("--cpu-seconds", type=float, default=15.0,
                     help="wall time of each CPU baseline's sample (0: skip the baselines)")
-    ap.add_argument("--legs", default="decode,prefill,dense",
-                    help="comma-separated: decode (config 2), prefill (config 3), dense (config 4)")
+    ap.add_argument("--legs", default="decode,stress,plumbing,prefill,dense",
+                    help="comma-separated: decode (config 2), stress (config 5), plumbing "
+                         "(config 1), prefill (config 3), dense (config 4)")
+    ap.add_argument("--c5-tokens", type=int, default=65_536)
+    ap.add_argument("--c5-steps", type=int, default=8, help="launches config 5's run is split over")
+    ap.add_argument("--c5-count-tokens", type=int, default=2048,
+                    help="tokens of config 5's counter launch (GDN events, MLP redos)")
+    ap.add_argument("--c1-runs", type=int, default=5)
     ap.add_argument("--pf-calls", type=int, default=5)
     ap.add_argument("--pf-tokens", type=int, default=65_536)
     ap.add_argument("--pf-cpu-tokens", type=int, default=256)
@@ -727,6 +915,10 @@ def main() -> int:
     t_all = time.time()
     hf_holder: dict = {}
     out = decode_leg(args, dev, hf_holder) if "decode" in legs else {}
+    if "stress" in legs:
+        out["c5"] = stress_leg(args, dev, hf_holder)
+    if "plumbing" in legs:
+        out["c1"] = plumbing_leg(args, dev)
     if "prefill" in legs:
         out["verified_prefill"] = prefill_leg(args, dev, hf_holder)
     hf_holder.clear()

@@ -173,8 +173,9 @@ int lxm_t_elem(int fn, const float* x, float* y, long n, void* stream);
    values (x row-major); out (rows). */
 int lxm_t_sum(int kind, const float* x, int n, int rows, float* out, void* stream);
 
-/* No counterpart in the reference: lxm_run for callers that cannot allocate device memory (code
-   under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc). The run buffers
+/* No counterpart in the reference: lxm_run for callers that cannot allocate device memory (tight
+   serving loops, harnesses that forbid hipMalloc). It is a cooperative launch, which is not
+   recorded into a captured HIP graph here; no test captures it. The run buffers
    (ring, rring, hn, sync, keys, mb_task, mb_e, mb_qk, ybuf, xo) and the parameter block's device
    copy come from a static array of LXM_SCRATCH_BYTES per GPU (held until the process ends); the
    corresponding fields of *p_host are ignored, everything else (tables, states, forced, preds,

@@ -37,12 +37,16 @@ typedef struct lxm_chunk_io {
   int32_t n_slots; /* value heads (slots) */
   int32_t rl;      /* slots per key head (slot h reads key head h / rl) */
   int32_t rfull;   /* state heads per key head (>= rl) */
-  int32_t kl;      /* live key dims, <= 128: q, k dims and S rows from kl on are zero */
+  int32_t kl;      /* live key dims, a multiple of 16, <= 128: q and k dims from kl on are
+                      zero, and so must be S's rows from kl on (the kernel neither reads nor
+                      decays them) */
   int32_t o_bf16;  /* 1: o rounded to bf16 (the stock casts the output to the model dtype) */
 } lxm_chunk_io;
 
-/* One chunk of every slot on stream (one workgroup per slot and 32 state columns). Returns a
-   hipError_t (hipErrorInvalidValue for sizes outside the limits above). */
+/* One chunk of every slot on stream (one workgroup per slot and 32 state columns). q, k, v and S
+   are read 16 bytes at a time: each must be 16-byte aligned and qk_ts, qk_hs and v_ts multiples of
+   4. Returns a hipError_t (hipErrorInvalidValue for sizes outside the limits above or a misaligned
+   pointer or stride). */
 int lxm_gdn_chunk(const lxm_chunk_io* io, void* stream);
 
 #ifdef __cplusplus

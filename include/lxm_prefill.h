@@ -119,7 +119,10 @@ typedef struct lxm_pf_params {
   unsigned long long* keys;    /* (T): argmax keys */
   int32_t* preds;              /* (T) */
   int32_t* err;                /* (1): 1 a token id out of range; 2 the head kernel's LDS tile
-                                  not at LDS address 0 (a build fault) */
+                                  not at LDS address 0 (a build fault). Sticky: the kernels only
+                                  set it, the caller zeroes it before a call (Prefill.embed does).
+                                  A bad token's position is embedded as zeros and the layers
+                                  still run, so the cache has changed when err reads 1. */
 } lxm_pf_params;
 
 /* Fast.forward / Fast.layer (fast.py:252-269): layers [l0, l1) over the T positions of p->h, in

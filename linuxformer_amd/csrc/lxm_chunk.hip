@@ -325,9 +325,16 @@ __global__ __launch_bounds__(CT) void lxm_chunk_k(lxm_chunk_io io) {
   }
 }
 
+// q, k, v and S are read four floats at a time: their pointers 16-byte aligned, and the strides
+// between those reads multiples of 4 floats
+static bool al16(const void* p) { return ((uintptr_t)p & 15) == 0; }
+
 extern "C" int lxm_gdn_chunk(const lxm_chunk_io* io, void* stream) {
   if (!io || io->n < 1 || io->n > C || io->kl < 1 || io->kl > KL || io->kl % 16 != 0 ||
       io->n_slots < 1 || io->rl < 1 || io->rfull < io->rl)
+    return (int)hipErrorInvalidValue;
+  if (!al16(io->q) || !al16(io->k) || !al16(io->v) || !al16(io->S) || io->qk_ts % 4 != 0 ||
+      io->qk_hs % 4 != 0 || io->v_ts % 4 != 0)
     return (int)hipErrorInvalidValue;
   const int lds = (int)sizeof(ChunkLds);
   hipError_t e = hipFuncSetAttribute((const void*)lxm_chunk_k,

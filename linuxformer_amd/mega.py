@@ -626,8 +626,11 @@ class Mega:
                              "per launch")
 
     def _state_ptrs_cached(self):
-        """The state pointer arrays, built once (the cache's tensors stay where they are)."""
-        key = tuple(self.cache.layers[L].recurrent_states[0].data_ptr() for L in range(self.dims.n_layers))
+        """The state pointer arrays, built once per set of state tensors (keyed by every layer's
+        recurrent and conv pointers; a new set goes through _state_ptrs' checks)."""
+        key = tuple((self.cache.layers[L].recurrent_states[0].data_ptr(),
+                     self.cache.layers[L].conv_states[0].data_ptr())
+                    for L in range(self.dims.n_layers))
         if getattr(self, "_ptrs_key", None) != key:
             self._ptrs = self._state_ptrs()
             self._ptrs_key = key

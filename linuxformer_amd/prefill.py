@@ -503,13 +503,15 @@ class Prefill:
     def embed(self, tokens) -> int:
         """The tokens' embedding rows into the residual tiles. Returns T. Tokens already on the
         device (an int32 tensor) are copied there and range-checked by the kernel, which sets the
-        error word (``err``, nonzero after the call when a token was out of range; nothing
-        synchronizes); host tokens are checked here and raise."""
+        error word (``err``, zeroed here at the start of every call, nonzero after it when a
+        token was out of range; nothing synchronizes; the layers still run on such a call and
+        change the cache); host tokens are checked here and raise."""
         if isinstance(tokens, torch.Tensor) and tokens.device == self.dev:
             if tokens.dtype != torch.int32 or tokens.numel() == 0:
                 raise ValueError("device tokens: a non-empty int32 tensor")
             T = int(tokens.numel())
             p, pd = self.params(T)
+            self.err.zero_()
             self.tokens.copy_(tokens.reshape(-1))
             self._check(self.lib.lxm_pf_embed(ctypes.byref(p), ctypes.c_void_p(pd.data_ptr()),
                                               self._stream()), "prefill embed")
@@ -522,6 +524,7 @@ class Prefill:
         if lo < 0 or hi >= self.vocab:
             raise ValueError("token out of range")
         p, pd = self.params(T)
+        self.err.zero_()
         self.tokens.copy_(t.to(torch.int32).reshape(-1))
         self._check(self.lib.lxm_pf_embed(ctypes.byref(p), ctypes.c_void_p(pd.data_ptr()),
                                           self._stream()), "prefill embed")

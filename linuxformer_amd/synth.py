@@ -272,12 +272,17 @@ def _layer(spec: Spec, L: int) -> Layer:
     return lay
 
 
-def build(spec: Spec) -> SparseModel:
-    """The seeded stack of ``spec`` (weights only; see ``init_state`` for the caches)."""
+def build(spec: Spec, layers: list | None = None) -> SparseModel:
+    """The seeded stack of ``spec`` (weights only; see ``init_state`` for the caches). ``layers``:
+    the layers of a stack built from a spec that differs from this one only in p_gate (configs
+    2, 3 and 5), reused as they are (a layer does not depend on p_gate; only the embedding's
+    gate columns do)."""
     d, s = spec.dims, spec.seed
     H, V = d.hidden, d.vocab
     assert d.nv % d.nk == 0 and H > d.n_layers
-    layers = [_layer(spec, L) for L in range(d.n_layers)]
+    if layers is None:
+        layers = [_layer(spec, L) for L in range(d.n_layers)]
+    assert len(layers) == d.n_layers
     # embedding: emb_nnz distinct non-gate columns per row, plus each layer's gate at p_gate
     re = _rng(s, 0, _EMB)
     hng = H - d.n_layers

@@ -1,7 +1,9 @@
-"""Write tests/golden/c2_chunk.json: the CPU oracle's run of BASELINE config 2's whole greedy chunk.
+"""Write tests/golden/c2_chunk.json (or c5_run.json): the CPU oracle's run of a whole greedy chunk.
 
-One 262,144-token greedy chunk of the 37-layer synthetic stack (linuxformer_amd.synth.config2)
-from its start token and initial state, decoded by the C oracle (oracle/lx_oracle.c, the stock
+Config 2: one 262,144-token greedy chunk of the 37-layer synthetic stack
+(linuxformer_amd.synth.config2); config 5 (--config c5): the same stack with half of the
+layer-steps gated, 65,536 greedy tokens (BASELINE config 5's run). Each starts from its config's
+start token and initial state and is decoded by the C oracle (oracle/lx_oracle.c, the stock
 decode restated). The fixture holds the sha256 of the prediction stream (int32, little-endian),
 of the final conv windows and of the final recurrent states (float32, the stacked (L, C, 4) and
 (L, nv, 256, 128) arrays; the states with every zero made +0), and the stream's first
@@ -9,9 +11,9 @@ predictions. The GPU test and bench.py compare
 the decode kernel's chunk against it (the reference pins its boot the same way:
 lx/tools/mega_boot.py:74-75, lx/results/mega_boot.json's stream_sha256).
 
-    OMP_NUM_THREADS=8 python tests/golden/make_chunk.py [--chunk N] [--ckpt DIR]
+    OMP_NUM_THREADS=8 python tests/golden/make_chunk.py [--config c2|c5] [--chunk N] [--ckpt DIR]
 
-About 1-2 hours on 8 host threads. With --ckpt the run saves its progress every piece and resumes
+About 1-2 hours on 8 host threads for config 2, about 35 minutes for config 5. With --ckpt the run saves its progress every piece and resumes
 from it.
 """
 
@@ -35,13 +37,18 @@ from oracle import oracle as ox  # noqa: E402
 
 def main() -> int:
     ap = argparse.ArgumentParser()
-    ap.add_argument("--chunk", type=int, default=262_144)
+    ap.add_argument("--config", choices=("c2", "c5"), default="c2")
+    ap.add_argument("--chunk", type=int, default=None, help="tokens (default: the config's run)")
     ap.add_argument("--piece", type=int, default=4096)
     ap.add_argument("--ckpt", default=None, help="directory for resumable progress")
-    ap.add_argument("--out", default=os.path.join(HERE, "c2_chunk.json"))
+    ap.add_argument("--out", default=None)
     args = ap.parse_args()
 
-    spec = synth.config2()
+    spec = synth.config2() if args.config == "c2" else synth.config5()
+    if args.chunk is None:
+        args.chunk = spec.n_steps
+    if args.out is None:
+        args.out = os.path.join(HERE, "c2_chunk.json" if args.config == "c2" else "c5_run.json")
     model = synth.build(spec)
     conv, rec = synth.init_state(model)
     start = synth.start_token(spec)

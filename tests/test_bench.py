@@ -25,7 +25,9 @@ def test_defaults_are_the_driver_workload():
     a = bench.make_parser().parse_args(["--gpus", "1", "--steps", "20", "--warmup", "5"])
     assert a.config == "c2" and a.chunk == 262_144
     assert sum(bench.split_chunk(a.chunk, a.steps)) == 262_144
-    assert set(a.legs.split(",")) == {"decode", "prefill", "dense"}
+    assert set(a.legs.split(",")) == {"decode", "stress", "plumbing", "prefill", "dense"}
+    # config 5's run: 65,536 greedy tokens; config 1: 256 steps
+    assert a.c5_tokens == 65_536 and sum(bench.split_chunk(a.c5_tokens, a.c5_steps)) == 65_536
     d = bench.make_parser().parse_args([])
     assert (d.gpus, d.steps, d.warmup) == (1, 20, 5)
 
@@ -36,3 +38,11 @@ def test_more_than_one_gpu_is_refused():
     assert r.returncode == 2
     assert "one GPU" in r.stderr
     assert r.stdout == ""
+
+
+def test_latency_roofline_counts_hops():
+    """Two one-way hops per token for the head, three per GDN event, each half a round trip."""
+    sync = {"round_trip_other_xcd_us": 1.0}
+    r = bench.latency_roofline(sync, 1.0, 100.0)
+    assert r["hops_per_token"] == 5.0 and r["round_trips_per_token"] == 2.5
+    assert r["t_sync_us"] == 2.5 and r["frac"] == 0.025

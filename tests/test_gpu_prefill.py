@@ -197,7 +197,12 @@ def test_prefill_device_tokens_and_caches(cuda):
     bad = torch.tensor([0, m.dims.vocab], dtype=torch.int32, device="cuda")
     pf.verify(bad, fast.StateCache(c0, r0, m.dims.dtype, "cuda"))
     assert int(pf.err.item()) != 0
-    pf.err.zero_()
+    # a good call after the bad one: the error word starts from zero again, the results are whole
+    cd = fast.StateCache(c0, r0, m.dims.dtype, "cuda")
+    pd = pf.verify(td, cd).cpu().numpy()
+    assert int(pf.err.item()) == 0
+    assert pd.tolist() == want.tolist()
+    assert (bits(cd.rec_numpy()) == bits(want_rec)).all()
 
 
 def test_config3_full_matches_decode_kernel(cuda):
