@@ -36,6 +36,7 @@ extern "C" {
 #define LXM_OUT_MAX 1024    /* out_proj entries of the rows one helper workgroup computes */
 #define LXM_OUT_HELPERS 64  /* helper workgroups that compute out_proj's rows */
 #define LXM_OUT_ROWS 64     /* out_proj rows one of them computes, at most */
+#define LXM_HEAD_DENSE 32   /* dense head columns (2-bit coded), at most */
 
 /* The chain workgroup's per-thread table of one layer (packed by linuxformer_amd/chain.py):
    LXM_PT_WORDS x LXM_NT 16-byte words, word j of thread t at (j * LXM_NT + t) * 16, prefetched
@@ -107,7 +108,11 @@ typedef struct lxm_layer {
 typedef struct lxm_params {
   int32_t hidden, n_layers, nk, kd, nv, vd, n_conv, vocab, bf16, n_blocks;
   float rms_eps;
-  int32_t head_lds;        /* bytes of head tables a helper workgroup stages */
+  int32_t head_lds;        /* bytes of head tables a helper workgroup stages: its rows' pointers
+                              (rows + 1 int32), their entries, and with dense columns (n_hd > 0)
+                              the rows' code words (8 bytes each), a column-rank byte per hidden
+                              column, the dense columns, their inputs and their tables (768
+                              bytes); each part from a 16-byte boundary */
   int32_t e4;              /* the entry format (above) */
   int32_t gate_bytes;      /* bytes of the gate section (every layer's lxm_gate tables) */
   const lxm_layer* layers; /* device, n_layers */
@@ -140,7 +145,18 @@ typedef struct lxm_params {
                               a stamped word (the value's fp32 bits low, the GDN event's
                               sequence number high) */
   float* xo;               /* (LXM_MAXH): out_proj's rows, rounded, helpers -> chain */
-  int32_t n_qk_total, pad;
+  int32_t n_qk_total;
+  /* Dense head columns (the reference keeps its head's all-nonzero columns as 2-bit codes,
+     lx/csrc/mega.cu:96-101, :551-563; lx/lx/mega.py:354-376): n_hd <= LXM_HEAD_DENSE columns,
+     head_dcol (ascending hidden indices), each with a table of 4 values head_dtab[4 j + c]
+     (bf16-exact for e4 models), and per vocabulary row one word head_code (column j's code at
+     bits 2j, 2j + 1). head_ptr / head_ent then hold only the other columns. A row's logit adds
+     its terms in ascending column order, the dense ones merged in, from +0 (a code whose value
+     is 0 adds nothing). n_hd 0: the pointers may be null. */
+  int32_t n_hd;
+  const int32_t* head_dcol;
+  const float* head_dtab;
+  const unsigned long long* head_code;
 } lxm_params;
 
 /* mk_run (lx/csrc/mega.cu:867-874): launch the persistent decode, cooperatively, n_blocks

@@ -1441,10 +1441,54 @@ __device__ void run_chain(const lxm_params& pg) {
 
 // HEAD: this helper's vocabulary rows against the final normed residual; its best key, stamped
 // with the event's low bits, into its own slot (the chain reads every slot).
+// The dense head columns' tables in a helper's LDS (after its rows' entries): the rows' code
+// words, a byte per hidden column (how many dense columns lie below it), the dense columns, their
+// inputs at the current event, their 4-value tables.
+struct HeadDense {
+  const unsigned long long* code;
+  const uint8_t* rank;
+  const int32_t* dcol;
+  float* xd;
+  const float* tab;
+};
+__host__ __device__ inline int a16(int64_t n) { return (int)((n + 15) & ~(int64_t)15); }
+__device__ inline HeadDense head_dense(uint8_t* base, int nr, int H) {
+  uint8_t* rk = base + a16(8 * (int64_t)nr);
+  uint8_t* dc = rk + a16(H);
+  return {reinterpret_cast<const unsigned long long*>(base), rk,
+          reinterpret_cast<const int32_t*>(dc), reinterpret_cast<float*>(dc + 128),
+          reinterpret_cast<const float*>(dc + 256)};
+}
+
+// One head row with dense columns: its sparse entries (columns outside the dense set, ascending)
+// and its dense columns' coded values, merged in ascending column order, from +0.
+template <bool BF, bool E4>
+__device__ __forceinline__ float dense_row(const uint8_t* lent, int a, int n, const float* hn,
+                                           const HeadDense& hd, unsigned long long cw, int nd) {
+  float s = 0.0f;
+  int j = 0;
+  for (int e = 0; e < n; e++) {
+    int i;
+    float w;
+    Ent<E4>::at(lent, a + e, i, w);
+    i &= OFF_MASK;
+    for (const int nb = hd.rank[i >> 2]; j < nb; j++) {
+      const float wd = hd.tab[4 * j + (int)((cw >> (2 * j)) & 3ull)];
+      s = wd != 0.0f ? acc<BF>(s, hd.xd[j], wd) : s;
+    }
+    s = acc<BF>(s, at_b(hn, i), w);
+  }
+  for (; j < nd; j++) {
+    const float wd = hd.tab[4 * j + (int)((cw >> (2 * j)) & 3ull)];
+    s = wd != 0.0f ? acc<BF>(s, hd.xd[j], wd) : s;
+  }
+  return s;
+}
+
 template <bool BF, bool E4>
 __device__ void head_rows(const lxm_params& p, uint32_t stamp, const int32_t* lptr,
-                          const uint8_t* lent, int r0, int nr, uint8_t* hx) {
-  const int t = threadIdx.x, H = p.hidden;
+                          const uint8_t* lent, int r0, int nr, uint8_t* hx, const HeadDense& hd) {
+  const int t = threadIdx.x, H = p.hidden, nd = p.n_hd;
   float* hn = reinterpret_cast<float*>(hx + HX_X);
   unsigned long long* wk = reinterpret_cast<unsigned long long*>(hx + HX_BS);
   {  // the thread's columns requested together (one round trip, not one per column)
@@ -1457,10 +1501,21 @@ __device__ void head_rows(const lxm_params& p, uint32_t stamp, const int32_t* lp
   }
   __syncthreads();
   unsigned long long best = 0;
-  for (int k = t; k < nr; k += NT) {
-    const float v = rd<BF>(dot<BF, E4, 4, 0>(lent, lptr[k], lptr[k + 1] - lptr[k], hn));
-    const unsigned long long key = argmax_key19(v, r0 + k);
-    best = key > best ? key : best;
+  if (nd == 0) {
+    for (int k = t; k < nr; k += NT) {
+      const float v = rd<BF>(dot<BF, E4, 4, 0>(lent, lptr[k], lptr[k + 1] - lptr[k], hn));
+      const unsigned long long key = argmax_key19(v, r0 + k);
+      best = key > best ? key : best;
+    }
+  } else {
+    if (t < nd) hd.xd[t] = hn[hd.dcol[t]];
+    __syncthreads();
+    for (int k = t; k < nr; k += NT) {
+      const float v = rd<BF>(dense_row<BF, E4>(lent, lptr[k], lptr[k + 1] - lptr[k], hn, hd,
+                                               hd.code[k], nd));
+      const unsigned long long key = argmax_key19(v, r0 + k);
+      best = key > best ? key : best;
+    }
   }
   for (int off = 32; off >= 1; off >>= 1) {
     const unsigned long long o = __shfl_xor(best, off, 64);
@@ -1849,6 +1904,23 @@ __device__ void run_helper(const lxm_params& pg) {
     uint32_t* dst = reinterpret_cast<uint32_t*>(lent);
     for (int64_t k = t; k < ne * (Ent<E4>::SZ / 4); k += NT) dst[k] = src[k];
   }
+  // the dense head columns' tables (after the entries; none without dense columns)
+  uint8_t* ldense = lent + a16(ne * Ent<E4>::SZ);
+  const HeadDense hd = head_dense(ldense, nr, H);
+  if (p.n_hd > 0) {
+    unsigned long long* code = const_cast<unsigned long long*>(hd.code);
+    for (int k = t; k < nr; k += NT) code[k] = p.head_code[r0 + k];
+    int32_t* dcol = const_cast<int32_t*>(hd.dcol);
+    float* tab = const_cast<float*>(hd.tab);
+    if (t < p.n_hd) dcol[t] = p.head_dcol[t];
+    if (t < 4 * p.n_hd) tab[t] = p.head_dtab[t];
+    uint8_t* rank = const_cast<uint8_t*>(hd.rank);
+    for (int c = t; c < H; c += NT) {
+      int nb = 0;
+      for (int j = 0; j < p.n_hd; j++) nb += p.head_dcol[j] < c ? 1 : 0;
+      rank[c] = (uint8_t)nb;
+    }
+  }
   // out_proj rows of this helper: an even split of the residual rows over the first
   // LXM_OUT_HELPERS helpers
   const int no = nh < LXM_OUT_HELPERS ? nh : LXM_OUT_HELPERS;
@@ -1884,7 +1956,7 @@ __device__ void run_helper(const lxm_params& pg) {
     if (!(w & EV_GDN)) {
       // (the head's rows read the parameter block from global memory: the LDS copy, read
       // between the row tables' LDS reads, measured slower there)
-      head_rows<BF, E4>(pg, (w >> 8) & KEY_STAMP, lptr, lent, r0, nr, hx);
+      head_rows<BF, E4>(pg, (w >> 8) & KEY_STAMP, lptr, lent, r0, nr, hx, hd);
       if (PROF_ON) pr[1] += cycles() - w1;
       step++;
     } else {
@@ -2114,7 +2186,8 @@ static bool launch_ok(const lxm_params* p, int n_blocks) {
   return p && n_blocks >= 2 && n_blocks <= LXM_MAXBLOCKS && p->n_blocks == n_blocks &&
          p->n_tokens >= 0 && (int64_t)p->n_tokens * (p->n_layers + 1) < (int64_t)SEQ_MASK &&
          p->vocab <= LXM_MAXVOCAB && p->nv >= 1 && p->nv <= LXM_SCRATCH_MAXNV && p->nk >= 1 &&
-         p->nk <= F_KEYW - F_KH;
+         p->nk <= F_KEYW - F_KH && p->n_hd >= 0 && p->n_hd <= LXM_HEAD_DENSE &&
+         (p->n_hd == 0 || (p->head_dcol && p->head_dtab && p->head_code));
 }
 
 int lxm_run(const lxm_params* p_host, const lxm_params* p_dev, int n_blocks, int lds_bytes,

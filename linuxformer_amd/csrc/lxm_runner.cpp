@@ -127,7 +127,8 @@ int main(int argc, char** argv) {
       {"err", (void**)&p.err},           {"prof", (void**)&p.prof},
       {"mb_task", (void**)&p.mb_task},   {"mb_e", (void**)&p.mb_e},
       {"mb_qk", (void**)&p.mb_qk},       {"ybuf", (void**)&p.ybuf},
-      {"xo", (void**)&p.xo}};
+      {"xo", (void**)&p.xo},             {"head_dcol", (void**)&p.head_dcol},
+      {"head_dtab", (void**)&p.head_dtab}, {"head_code", (void**)&p.head_code}};
   for (auto& kv : field) *kv.second = nullptr;
   int n_blocks = 0, lds = 0;
   std::vector<std::string> manifest;

@@ -58,14 +58,24 @@ class Fast:
 
     def __init__(self, model, n_chip: int | None = None, rows: slice | None = None):
         self.model = model
-        self.sm = model if isinstance(model, synth.SparseModel) else synth.from_hf(model, n_chip)
+        if isinstance(model, synth.SparseModel):
+            self.sm, self.row0 = model, 0
+        else:
+            # only the chip's rows of the head are read (lx/lx/fast.py:183's lm_head.weight[rows]):
+            # the coordinate model's embedding holds rows row0 .. row0 + vocab of the model's
+            self.sm = synth.from_hf(model, n_chip, rows)
+            self.row0 = int(self.sm.meta.get("row0", 0))
         d = self.sm.dims
         self.n_chip = d.n_layers
         self.nk, self.nv, self.kd, self.vd = d.nk, d.nv, d.kd, d.vd
         self.r = d.nv // d.nk
         self.rows = rows
+        n_all = self.row0 + d.vocab  # rows of the model's embedding this Fast can see
         lo = 0 if rows is None else (rows.start or 0)
-        hi = d.vocab if rows is None or rows.stop is None else rows.stop
+        hi = n_all if rows is None or rows.stop is None else rows.stop
+        if (rows is not None and rows.step not in (None, 1)) or not self.row0 <= lo < hi <= n_all:
+            raise ValueError(f"rows {rows}: not a range of the embedding's rows "
+                             f"{self.row0} .. {n_all}")
         self.head_range = (lo, hi)
         w1 = np.float32(1.0) + np.asarray(self.sm.norm, np.float32)
         self.head_cols = np.nonzero(w1 != 0)[0]
@@ -176,11 +186,15 @@ class Fast:
         each position's prediction (int32, on the device; prediction i is for token i + 1)."""
         return self.prefill().verify(tokens, cache)
 
-    def embed_rows(self, offset: int = 0) -> Rows:
-        """The embedding rows of chip tokens offset .. offset + vocab (all columns)."""
+    def embed_rows(self, offset: int | None = None) -> Rows:
+        """The chip tokens' embedding rows (all columns): the head's rows (``rows``, or every row),
+        which are also the inputs' rows, chip token t at row offset + t (lx/csrc/mega.cu:647-651's
+        embed[tok + offset]); a given offset must be where those rows start."""
         lo, hi = self.head_range
-        return Rows(self.sm.embed, offset + lo if self.rows is None else lo,
-                    (offset + hi) if self.rows is None else hi)
+        if offset is not None and offset != lo:
+            raise ValueError(f"offset {offset}: the chip's rows start at {lo} (Fast's rows="
+                             f"{self.rows}); the tied head and the inputs share them")
+        return Rows(self.sm.embed, lo - self.row0, hi - self.row0)
 
 
 class _CacheLayer:

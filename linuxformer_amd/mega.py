@@ -64,7 +64,8 @@ class Params(ctypes.Structure):
         [("n_forced", I32), ("n_tokens", I32)] + \
         [(n, PTR) for n in ("preds", "inputs", "trace", "ring", "rring", "hn", "sync", "keys", "err",
                             "prof", "mb_task", "mb_e", "mb_qk", "ybuf", "xo")] + \
-        [("n_qk_total", I32), ("pad", I32)]
+        [("n_qk_total", I32), ("n_hd", I32)] + \
+        [(n, PTR) for n in ("head_dcol", "head_dtab", "head_code")]
 
 
 assert ctypes.sizeof(Gate) == 64 and ctypes.sizeof(QkC) == 32 and ctypes.sizeof(Dec) == 32
@@ -162,6 +163,297 @@ class Packer:
         return (np.float32(1.0) + w).astype(np.float32).tobytes()
 
 
+class PackError(ValueError):
+    """A model the decode kernel's tables cannot hold; the message names the limit."""
+
+
+def _cap(ok: bool, msg: str) -> None:
+    if not ok:
+        raise PackError(msg)
+
+
+MAX_LDS_MI355X = 163_840  # LDS bytes one workgroup may use on gfx950 (160 KB per CU)
+HEAD_DENSE = 32           # dense head columns, at most (LXM_HEAD_DENSE)
+
+
+def head_dense_columns(rows, cols, vals, n_rows: int, hidden: int):
+    """The head columns kept as 2-bit codes (the reference's dense head columns,
+    lx/lx/mega.py:354-376, lx/csrc/mega.cu:96-101): a column nonzero in at least half of the
+    rows with at most 4 distinct values (zero counted where the column has one), the fullest
+    first, at most HEAD_DENSE of them. Returns (columns ascending, (n, 4) float32 tables: each
+    column's values ascending, padded with the first)."""
+    cnt = np.bincount(cols, minlength=hidden)
+    cand = np.nonzero(2 * cnt >= max(n_rows, 1))[0]
+    if len(cand) == 0:
+        return np.zeros(0, np.int64), np.zeros((0, 4), np.float32)
+    sel = np.isin(cols, cand)
+    c_s, v_s = cols[sel], vals[sel]
+    order = np.argsort(c_s, kind="stable")
+    c_s, v_s = c_s[order], v_s[order]
+    bounds = np.searchsorted(c_s, cand), np.searchsorted(c_s, cand, side="right")
+    picked = []
+    for k in np.argsort(-cnt[cand], kind="stable"):
+        c = int(cand[k])
+        v = np.unique(v_s[bounds[0][k]:bounds[1][k]].astype(np.float32))
+        if cnt[c] < n_rows:
+            v = np.unique(np.concatenate([v, np.zeros(1, np.float32)]))
+        if len(v) <= 4:
+            picked.append((c, v))
+        if len(picked) == HEAD_DENSE:
+            break
+    picked.sort()
+    tabs = np.zeros((len(picked), 4), np.float32)
+    for j, (_, v) in enumerate(picked):
+        tabs[j, :len(v)] = v
+        tabs[j, len(v):] = v[0]
+    return np.array([c for c, _ in picked], np.int64), tabs
+
+
+class Plan:
+    """The decode's packed tables and launch sizes, built on the host (``pack``); ``Mega``
+    uploads them. ``check(max_lds)`` raises PackError naming a limit the plan breaks."""
+
+    def check(self, max_lds: int = MAX_LDS_MI355X) -> "Plan":
+        _cap(self.lds <= max_lds,
+             f"a workgroup needs {self.lds} B of LDS (chain {self.lds_chain}, helper "
+             f"{self.lds_helper} with {self.head_lds} B of head tables) > {max_lds}")
+        return self
+
+    def summary(self) -> dict:
+        return {k: v for k, v in self.stats.items() if not isinstance(v, list)}
+
+
+def pack(fast, offset: int = 0, ncta: int = 256, lib=None) -> Plan:
+    """Pack ``fast``'s chip layers for the decode kernel on ncta workgroups (the chain and
+    ncta - 1 helpers). Host work only: the tables as bytes and arrays, the LDS each workgroup
+    needs (lib: the native library, for its LDS constants). Raises PackError when the model
+    breaks one of the kernel's limits (include/lxm.h)."""
+    lib = lib or mk_build.load()
+    sm = fast.sm
+    if synth.has_dense_order(sm):
+        raise ValueError("a dense-order stack (config 4) runs on linuxformer_amd.dense")
+    d = sm.dims
+    pl = Plan()
+    pl.dims, pl.ncta = d, ncta
+    _cap(ncta >= 2, "the decode needs the chain workgroup and at least one helper")
+    _cap(ncta <= 256, "at most 256 workgroups (the sync area's per-helper stamps)")
+    nh = ncta - 1
+    _cap(d.nv <= nh, f"{d.nv} value heads: each needs its own helper workgroup ({nh})")
+    _cap(-(-d.hidden // min(nh, OUT_HELPERS)) <= OUT_ROWS, "too many out_proj rows per helper")
+    _cap(d.kd == KD and d.vd == VD and d.conv == 4, "key dim 256, value dim 128, conv 4")
+    _cap(d.nv % d.nk == 0 and d.nv // d.nk <= RMAX, f"at most {RMAX} value heads per key head")
+    _cap(d.hidden <= MAXH, f"hidden {d.hidden} > {MAXH} (LXM_MAXH)")
+    _cap(d.nv <= 256 and d.nk <= 64 and d.n_layers <= 64,
+         "at most 256 value heads, 64 key heads and 64 layers")
+    pl.bf = d.dtype == "bf16"
+    pl.e4 = model_e4(sm)
+    pk = Packer(pl.e4)
+    blob = _Blob()
+    descs = (LayerDesc * d.n_layers)()
+    H, R, C = d.hidden, d.nv // d.nk, d.n_conv
+    qk_total = 0
+    pl.stats = {"layers": d.n_layers, "units": [], "qk": [], "dec": [], "chain": []}
+    pl.unit_order = []  # per layer: the model's unit index of each packed unit
+    cf = chain.fmt(pl.e4)
+    gate_blobs, gate_off = [], 0
+    ptts, longs = [], []
+    for L, ly in enumerate(sm.layers):
+        # ---- live MLP units (gate row, up row and down column nonzero; lx/lx/fast.py:242-248),
+        # in the model's order (the act index of a unit is its position here)
+        g, u, dn = _Csr(ly.gate_proj), _Csr(ly.up_proj), _Csr(ly.down_proj.transpose())
+        gc = np.diff(g.ptr)
+        uc = np.diff(u.ptr)
+        dc = np.diff(dn.ptr)
+        units = np.nonzero((gc > 0) & (uc > 0) & (dc > 0))[0]
+        _cap(len(units) <= MAXU, f"layer {L}: {len(units)} live MLP units > {MAXU} (LXM_MAXU)")
+        pl.unit_order.append(units)
+        uidx = np.full(d.inter, -1, np.int64)
+        uidx[units] = np.arange(len(units))
+        # down_proj by residual row over the live units, in the model's unit order (the sum's
+        # order), each entry naming the unit's packed index
+        dcoo = ly.down_proj
+        keep = uidx[dcoo.cols] >= 0
+        drows, dunits, dvals = dcoo.rows[keep], uidx[dcoo.cols[keep]], dcoo.vals[keep]
+        order = np.lexsort((dcoo.cols[keep], drows))
+        drows, dunits, dvals = drows[order], dunits[order], dvals[order]
+        dptr = np.zeros(H + 1, np.int64)
+        np.cumsum(np.bincount(drows, minlength=H), out=dptr[1:])
+        ct = chain.pack_layer(
+            cf, H, units, [g.row(k) for k in units], [u.row(k) for k in units],
+            [(dunits[dptr[r]:dptr[r + 1]], dvals[dptr[r]:dptr[r + 1]]) for r in range(H)],
+            np.asarray(ly.post_attention_layernorm, np.float32))
+        # ---- the gates: live query/key channels (nonzero conv taps) and decaying heads
+        qkv = _Csr(ly.in_proj_qkv)
+        taps = np.asarray(ly.conv1d, np.float32)
+        ent_parts, ent_w1, epos = [], [], 0
+        qks = []
+        w1in = np.asarray(ly.input_layernorm, np.float32)
+        for c in np.nonzero((taps[:2 * d.nk * KD] != 0).any(1))[0]:
+            kh, rem = divmod(int(c) % (d.nk * KD), KD)
+            isk = int(c) >= d.nk * KD
+            cols, vals = qkv.row(c)
+            q = QkC(slot=kh * 512 + (256 if isk else 0) + rem, chan=int(c), start=epos,
+                    len=len(cols))
+            q.taps[:] = [float(x) for x in taps[c]]
+            qks.append(q)
+            ent_parts.append(pk.ent(cols, vals))
+            ent_w1.append(w1in[cols])
+            epos += len(cols)
+        _cap(len(qks) <= MAXQKL, f"layer {L}: {len(qks)} live query/key channels > {MAXQKL} (LXM_MAXQKL)")
+        acsr = _Csr(ly.in_proj_a)
+        decs = []
+        for vh in range(d.nv):
+            cols, vals = acsr.row(vh)
+            # softplus(dt_bias) is exactly 0 only when exp(dt_bias) underflows (< -103.97)
+            if len(cols) == 0 and not float(ly.dt_bias[vh]) > -103.9:
+                continue
+            decs.append(Dec(vh=vh, start=epos, len=len(cols), dt_bias=float(ly.dt_bias[vh]),
+                            A_log=float(ly.A_log[vh])))
+            ent_parts.append(pk.ent(cols, vals))
+            ent_w1.append(w1in[cols])
+            epos += len(cols)
+        _cap(len(decs) <= MAXDEC, f"layer {L}: {len(decs)} decaying value heads > {MAXDEC} (LXM_MAXDEC)")
+        # one gate item per chain lane: the channels on the top waves, the decays below them
+        _cap(-(-len(qks) // 64) * 64 + len(decs) <= NT, f"layer {L}: {len(qks)} query/key channels and {len(decs)} decays exceed the chain's {NT} gate lanes")
+        gb = _Blob()
+        gb.add(bytes(64))
+        o_qk = gb.add(b"".join(bytes(q) for q in qks))
+        o_dec = gb.add(b"".join(bytes(x) for x in decs))
+        o_ent = gb.add(b"".join(ent_parts) + bytes(4 * pk.esz))
+        # the GDN norm's weight at each of those entries' columns
+        o_entw = gb.add((pk.w1(np.concatenate(ent_w1)) if ent_w1 else b"") + bytes(16))
+        # the chain's long units and rows (too long for its register passes)
+        o_lu = gb.add(ct.long_u)
+        o_lr = gb.add(ct.long_r)
+        o_le = gb.add(ct.long_ent)
+        gate = Gate(n_qk=len(qks), n_dec=len(decs), qk_base=qk_total, qk=o_qk, dec=o_dec,
+                    ent=o_ent, ent_w1=o_entw, size=gb.n, eps=d.rms_eps, geps=d.geps,
+                    long_u=o_lu, long_r=o_lr, long_ent=o_le, n_long_u=len(ct.long_u) // 32,
+                    n_long_r=len(ct.long_r) // 16)
+        gb.parts[0] = bytes(gate)
+        gate_blobs.append(gb.bytes())
+        descs[L].gate = gate_off  # (made absolute below)
+        gate_off += gb.n
+        qk_total += len(qks)
+        ptts.append(ct)
+        pl.stats["chain"].append(ct.stats)
+        desc = descs[L]
+        # ---- cold tables
+        chans = np.zeros(C, dtype=[("start", "<i4"), ("len", "<i4"), ("taps", "<f4", (4,))])
+        chans["start"] = qkv.ptr[:-1]
+        chans["len"] = np.diff(qkv.ptr)
+        chans["taps"] = taps
+        desc.chan = blob.add(chans.tobytes())
+        desc.qkv_ent = blob.add(pk.ent(qkv.cols, qkv.vals))
+        b = _Csr(ly.in_proj_b)
+        desc.b_row = blob.add(np.stack([b.ptr[:-1], np.diff(b.ptr)], 1).astype(np.int32).tobytes())
+        desc.b_ent = blob.add(pk.ent(b.cols, b.vals))
+        z = _Csr(ly.in_proj_z)
+        desc.z_row = blob.add(np.stack([z.ptr[:-1], np.diff(z.ptr)], 1).astype(np.int32).tobytes())
+        desc.z_ent = blob.add(pk.ent(z.cols, z.vals))
+        # out_proj by residual row over all value dims (vh * vd + j), ascending; each
+        # helper workgroup stages the entries of its slice of rows
+        oc = _Csr(ly.out_proj)
+        optr = oc.ptr
+        rp = -(-H // min(nh, OUT_HELPERS))
+        for r0 in range(0, H, rp):
+            n_e = int(optr[min(r0 + rp, H)] - optr[r0])
+            _cap(n_e <= OUT_MAX, f"layer {L}: {n_e} out_proj entries in {rp} rows > {OUT_MAX} (LXM_OUT_MAX)")
+        desc.out_ptr = blob.add(optr.astype(np.int32).tobytes())
+        desc.out_ent = blob.add(pk.ent(oc.cols, oc.vals, scale=1))
+        desc.gnorm = blob.add(np.asarray(ly.norm, np.float32).tobytes())
+        desc.w1_in = blob.add(pk.w1(ly.input_layernorm))
+        pl.stats["units"].append(len(units))
+        pl.stats["qk"].append(len(qks))
+        pl.stats["dec"].append(len(decs))
+    _cap(qk_total <= MAXQK, f"{qk_total} live query/key channels > {MAXQK} (LXM_MAXQK)")
+    _cap(gate_off <= GATE_MAX, f"the gate tables ({gate_off} B) exceed {GATE_MAX} B of the chain's LDS (LXM_GATE_MAX)")
+    pl.gate_bytes = gate_off
+    gsec = blob.add(b"".join(gate_blobs))
+    pl.gate_sec = gsec
+    for L, ct in enumerate(ptts):
+        desc = descs[L]
+        desc.gate += gsec
+        desc.ptt = blob.add(ct.ptt)
+        desc.pt_words = ct.wave_words
+    blob.add(bytes(4096))  # padding past the last table
+    pl.blob = blob.bytes()
+    pl.layers = bytes(descs)
+    pl.n_qk_total = qk_total
+    # ---- embedding (the chip's rows, all columns) and the head
+    emb = fast.embed_rows(offset)
+    V = emb.n
+    _cap(V <= 1 << 19, f"{V} vocabulary rows > 2^19 (the head keys carry a 19-bit index)")
+    pl.emb_ptr = emb.ptr.astype(np.int64)
+    pl.emb_ent = pk.ent(emb.cols, emb.vals)
+    w1f = (np.float32(1.0) + np.asarray(sm.norm, np.float32)).astype(np.float32)
+    w1pad = np.ones(MAXH, np.float32)  # the chain reads every thread's rows (<= MAXH)
+    w1pad[:H] = w1f
+    pl.w1_final = w1pad
+    hmask = w1f != 0  # a column whose (1 + w) is 0 adds only zeros
+    keep = hmask[emb.cols]
+    hrows = np.repeat(np.arange(V), np.diff(emb.ptr))[keep]
+    hcols, hvals = emb.cols[keep], emb.vals[keep]
+    # dense columns as 2-bit codes per row; the other columns as entries
+    dcols, dtabs = head_dense_columns(hrows, hcols, hvals, V, H)
+    nd = len(dcols)
+    code = np.zeros(V, np.uint64)
+    if nd:
+        jof = np.full(H, -1, np.int64)
+        jof[dcols] = np.arange(nd)
+        isd = jof[hcols] >= 0
+        for j in range(nd):
+            zc = int(np.nonzero(dtabs[j] == 0.0)[0][0]) if (dtabs[j] == 0.0).any() else 0
+            code |= np.uint64(zc) << np.uint64(2 * j)  # rows with no entry there: the zero's code
+        r_d, j_d, v_d = hrows[isd], jof[hcols[isd]], hvals[isd].astype(np.float32)
+        c_d = np.zeros(len(r_d), np.uint64)
+        for j in range(nd):
+            m = j_d == j
+            c_d[m] = np.searchsorted(dtabs[j], v_d[m]).astype(np.uint64)
+            assert np.all(dtabs[j][c_d[m].astype(np.int64)] == v_d[m])
+        # clear each coded column's default, then set its code
+        clear = np.zeros(len(r_d), np.uint64)
+        for j in range(nd):
+            clear[j_d == j] = np.uint64(3) << np.uint64(2 * j)
+        np.bitwise_and.at(code, r_d, ~clear)
+        np.bitwise_or.at(code, r_d, c_d << (2 * j_d).astype(np.uint64))
+        hrows, hcols, hvals = hrows[~isd], hcols[~isd], hvals[~isd]
+    hptr = np.zeros(V + 1, np.int64)
+    np.cumsum(np.bincount(hrows, minlength=V), out=hptr[1:])
+    pl.head_ptr = hptr
+    pl.head_ent = pk.ent(hcols, hvals) + bytes(16)
+    pl.n_hd = nd
+    pl.head_dcol = np.zeros(HEAD_DENSE, np.int32)
+    pl.head_dcol[:nd] = dcols
+    pl.head_dtab = np.zeros(4 * HEAD_DENSE, np.float32)
+    pl.head_dtab[:4 * nd] = dtabs.reshape(-1)
+    if pl.e4 and nd:
+        _bf16_bits(dtabs)  # (the e4 kernel's coded values are bf16-exact, as the entries)
+    pl.head_code = code if nd else np.zeros(1, np.uint64)
+    # block 0 is the chain (no head rows); helper b covers cuts[b - 1] .. cuts[b]
+    cuts = np.linspace(0, V, nh + 1).round().astype(np.int64)
+    bounds = np.concatenate([[0], cuts])
+    pl.head_rows = bounds.astype(np.int32)
+    a16 = lambda n: (int(n) + 15) // 16 * 16  # noqa: E731
+    need = 0
+    for b in range(1, ncta):
+        r0, r1 = bounds[b], bounds[b + 1]
+        ne = hptr[r1] - hptr[r0]
+        nb = a16((r1 - r0 + 1) * 4) + a16(ne * pk.esz)
+        if nd:
+            nb += a16(8 * (r1 - r0)) + a16(H) + 768
+        need = max(need, nb)
+    pl.head_lds = a16(need)
+    pl.lds_chain = int(lib.lxm_lds_base())
+    pl.lds_helper = int(lib.lxm_helper_lds(pl.head_lds))
+    pl.lds = (max(pl.lds_chain, pl.lds_helper) + 255) // 256 * 256
+    pl.vocab = V
+    pl.stats.update({"ctas": ncta, "lds": pl.lds, "head_lds": pl.head_lds,
+                     "blob_bytes": len(pl.blob), "qk_total": qk_total,
+                     "head_nnz": int(hptr[-1]), "head_dense_cols": nd, "vocab": V})
+    return pl
+
+
 class Mega:
     """lx.mega.Mega (lx/lx/mega.py:198-574) on MI355X.
 
@@ -178,200 +470,36 @@ class Mega:
         self.lib = mk_build.load(subprof)
         self.subprof = subprof
         self.fast, self.model, self.cache, self.offset = fast, model, cache, offset
-        sm = fast.sm
-        if synth.has_dense_order(sm):
-            raise ValueError("a dense-order stack (config 4) runs on linuxformer_amd.dense")
-        d = sm.dims
-        self.dims = d
         dev = torch.device(device) if device is not None else torch.device("cuda")
         if dev.type == "cuda" and dev.index is None:
             dev = torch.device("cuda", torch.cuda.current_device())
         self.dev = dev
-        cus = int(self.lib.lxm_device_cus())
-        self.ncta = ncta or cus
-        assert self.ncta >= 2, "the decode needs the chain workgroup and at least one helper"
-        assert self.ncta <= 256, "at most 256 workgroups (the sync area's per-helper stamps)"
-        nh = self.ncta - 1
-        assert d.nv <= nh, "each value head needs its own helper workgroup"
-        assert -(-d.hidden // min(nh, OUT_HELPERS)) <= OUT_ROWS, "too many out_proj rows per helper"
-        assert d.kd == KD and d.vd == VD and d.conv == 4, "key dim 256, value dim 128, conv 4"
-        assert d.nv % d.nk == 0 and d.nv // d.nk <= RMAX and d.hidden <= MAXH
-        assert d.nv <= 256 and d.nk <= 64 and d.n_layers <= 64
-        self.bf = d.dtype == "bf16"
-        self.e4 = model_e4(sm)
-        pk = Packer(self.e4)
-        blob = _Blob()
-        descs = (LayerDesc * d.n_layers)()
-        H, R, C = d.hidden, d.nv // d.nk, d.n_conv
-        qk_total = 0
-        self.stats = {"layers": d.n_layers, "units": [], "qk": [], "dec": [], "chain": []}
-        self.unit_order = []  # per layer: the model's unit index of each packed unit
-        cf = chain.fmt(self.e4)
-        gate_blobs, gate_off = [], 0
-        ptts, longs = [], []
-        for L, ly in enumerate(sm.layers):
-            # ---- live MLP units (gate row, up row and down column nonzero; lx/lx/fast.py:242-248),
-            # in the model's order (the act index of a unit is its position here)
-            g, u, dn = _Csr(ly.gate_proj), _Csr(ly.up_proj), _Csr(ly.down_proj.transpose())
-            gc = np.diff(g.ptr)
-            uc = np.diff(u.ptr)
-            dc = np.diff(dn.ptr)
-            units = np.nonzero((gc > 0) & (uc > 0) & (dc > 0))[0]
-            assert len(units) <= MAXU, f"layer {L}: {len(units)} live MLP units > {MAXU}"
-            self.unit_order.append(units)
-            uidx = np.full(d.inter, -1, np.int64)
-            uidx[units] = np.arange(len(units))
-            # down_proj by residual row over the live units, in the model's unit order (the sum's
-            # order), each entry naming the unit's packed index
-            dcoo = ly.down_proj
-            keep = uidx[dcoo.cols] >= 0
-            drows, dunits, dvals = dcoo.rows[keep], uidx[dcoo.cols[keep]], dcoo.vals[keep]
-            order = np.lexsort((dcoo.cols[keep], drows))
-            drows, dunits, dvals = drows[order], dunits[order], dvals[order]
-            dptr = np.zeros(H + 1, np.int64)
-            np.cumsum(np.bincount(drows, minlength=H), out=dptr[1:])
-            ct = chain.pack_layer(
-                cf, H, units, [g.row(k) for k in units], [u.row(k) for k in units],
-                [(dunits[dptr[r]:dptr[r + 1]], dvals[dptr[r]:dptr[r + 1]]) for r in range(H)],
-                np.asarray(ly.post_attention_layernorm, np.float32))
-            # ---- the gates: live query/key channels (nonzero conv taps) and decaying heads
-            qkv = _Csr(ly.in_proj_qkv)
-            taps = np.asarray(ly.conv1d, np.float32)
-            ent_parts, ent_w1, epos = [], [], 0
-            qks = []
-            w1in = np.asarray(ly.input_layernorm, np.float32)
-            for c in np.nonzero((taps[:2 * d.nk * KD] != 0).any(1))[0]:
-                kh, rem = divmod(int(c) % (d.nk * KD), KD)
-                isk = int(c) >= d.nk * KD
-                cols, vals = qkv.row(c)
-                q = QkC(slot=kh * 512 + (256 if isk else 0) + rem, chan=int(c), start=epos,
-                        len=len(cols))
-                q.taps[:] = [float(x) for x in taps[c]]
-                qks.append(q)
-                ent_parts.append(pk.ent(cols, vals))
-                ent_w1.append(w1in[cols])
-                epos += len(cols)
-            assert len(qks) <= MAXQKL, f"layer {L}: {len(qks)} live query/key channels"
-            acsr = _Csr(ly.in_proj_a)
-            decs = []
-            for vh in range(d.nv):
-                cols, vals = acsr.row(vh)
-                # softplus(dt_bias) is exactly 0 only when exp(dt_bias) underflows (< -103.97)
-                if len(cols) == 0 and not float(ly.dt_bias[vh]) > -103.9:
-                    continue
-                decs.append(Dec(vh=vh, start=epos, len=len(cols), dt_bias=float(ly.dt_bias[vh]),
-                                A_log=float(ly.A_log[vh])))
-                ent_parts.append(pk.ent(cols, vals))
-                ent_w1.append(w1in[cols])
-                epos += len(cols)
-            assert len(decs) <= MAXDEC
-            # one gate item per chain lane: the channels on the top waves, the decays below them
-            assert -(-len(qks) // 64) * 64 + len(decs) <= NT, f"layer {L}: too many gate items"
-            gb = _Blob()
-            gb.add(bytes(64))
-            o_qk = gb.add(b"".join(bytes(q) for q in qks))
-            o_dec = gb.add(b"".join(bytes(x) for x in decs))
-            o_ent = gb.add(b"".join(ent_parts) + bytes(4 * pk.esz))
-            # the GDN norm's weight at each of those entries' columns
-            o_entw = gb.add((pk.w1(np.concatenate(ent_w1)) if ent_w1 else b"") + bytes(16))
-            # the chain's long units and rows (too long for its register passes)
-            o_lu = gb.add(ct.long_u)
-            o_lr = gb.add(ct.long_r)
-            o_le = gb.add(ct.long_ent)
-            gate = Gate(n_qk=len(qks), n_dec=len(decs), qk_base=qk_total, qk=o_qk, dec=o_dec,
-                        ent=o_ent, ent_w1=o_entw, size=gb.n, eps=d.rms_eps, geps=d.geps,
-                        long_u=o_lu, long_r=o_lr, long_ent=o_le, n_long_u=len(ct.long_u) // 32,
-                        n_long_r=len(ct.long_r) // 16)
-            gb.parts[0] = bytes(gate)
-            gate_blobs.append(gb.bytes())
-            descs[L].gate = gate_off  # (made absolute below)
-            gate_off += gb.n
-            qk_total += len(qks)
-            ptts.append(ct)
-            self.stats["chain"].append(ct.stats)
-            desc = descs[L]
-            # ---- cold tables
-            chans = np.zeros(C, dtype=[("start", "<i4"), ("len", "<i4"), ("taps", "<f4", (4,))])
-            chans["start"] = qkv.ptr[:-1]
-            chans["len"] = np.diff(qkv.ptr)
-            chans["taps"] = taps
-            desc.chan = blob.add(chans.tobytes())
-            desc.qkv_ent = blob.add(pk.ent(qkv.cols, qkv.vals))
-            b = _Csr(ly.in_proj_b)
-            desc.b_row = blob.add(np.stack([b.ptr[:-1], np.diff(b.ptr)], 1).astype(np.int32).tobytes())
-            desc.b_ent = blob.add(pk.ent(b.cols, b.vals))
-            z = _Csr(ly.in_proj_z)
-            desc.z_row = blob.add(np.stack([z.ptr[:-1], np.diff(z.ptr)], 1).astype(np.int32).tobytes())
-            desc.z_ent = blob.add(pk.ent(z.cols, z.vals))
-            # out_proj by residual row over all value dims (vh * vd + j), ascending; each
-            # helper workgroup stages the entries of its slice of rows
-            oc = _Csr(ly.out_proj)
-            optr = oc.ptr
-            rp = -(-H // min(nh, OUT_HELPERS))
-            for r0 in range(0, H, rp):
-                n_e = int(optr[min(r0 + rp, H)] - optr[r0])
-                assert n_e <= OUT_MAX, f"layer {L}: {n_e} out_proj entries in {rp} rows > {OUT_MAX}"
-            desc.out_ptr = blob.add(optr.astype(np.int32).tobytes())
-            desc.out_ent = blob.add(pk.ent(oc.cols, oc.vals, scale=1))
-            desc.gnorm = blob.add(np.asarray(ly.norm, np.float32).tobytes())
-            desc.w1_in = blob.add(pk.w1(ly.input_layernorm))
-            self.stats["units"].append(len(units))
-            self.stats["qk"].append(len(qks))
-            self.stats["dec"].append(len(decs))
-        assert qk_total <= MAXQK, f"{qk_total} live query/key channels > {MAXQK}"
-        assert gate_off <= GATE_MAX, f"the gate tables ({gate_off} B) exceed {GATE_MAX} B of LDS"
-        self.gate_bytes = gate_off
-        gsec = blob.add(b"".join(gate_blobs))
-        self.gate_sec = gsec
-        for L, ct in enumerate(ptts):
-            desc = descs[L]
-            desc.gate += gsec
-            desc.ptt = blob.add(ct.ptt)
-            desc.pt_words = ct.wave_words
-        blob.add(bytes(4096))  # padding past the last table
-        self.blob = torch.frombuffer(bytearray(blob.bytes()), dtype=torch.uint8).to(dev)
-        self.layers_d = torch.frombuffer(bytearray(bytes(descs)), dtype=torch.uint8).to(dev)
-        self.n_qk_total = qk_total
-        # ---- embedding (rows offset .. offset + vocab, all columns) and the head
-        emb = fast.embed_rows(offset)
-        self.emb_ptr = torch.from_numpy(emb.ptr).to(dev)
-        self.emb_ent = torch.frombuffer(bytearray(pk.ent(emb.cols, emb.vals)),
-                                        dtype=torch.uint8).to(dev)
-        w1f = (np.float32(1.0) + np.asarray(sm.norm, np.float32)).astype(np.float32)
-        w1pad = np.ones(MAXH, np.float32)  # the chain reads every thread's rows (<= MAXH)
-        w1pad[:H] = w1f
-        self.w1_final = torch.from_numpy(w1pad).to(dev)
-        hcols = np.nonzero(w1f != 0)[0]  # a column whose (1 + w) is 0 adds only zeros
-        hmask = np.zeros(H, bool)
-        hmask[hcols] = True
-        keep = hmask[emb.cols]
-        hrows = np.repeat(np.arange(emb.n), np.diff(emb.ptr))[keep]
-        hptr = np.zeros(emb.n + 1, np.int64)
-        np.cumsum(np.bincount(hrows, minlength=emb.n), out=hptr[1:])
-        self.head_ptr = torch.from_numpy(hptr).to(dev)
-        self.head_ent = torch.frombuffer(bytearray(pk.ent(emb.cols[keep], emb.vals[keep]) + bytes(16)),
-                                         dtype=torch.uint8).to(dev)
-        V = emb.n
-        # block 0 is the chain (no head rows); helper b covers cuts[b - 1] .. cuts[b]
-        cuts = np.linspace(0, V, nh + 1).round().astype(np.int64)
-        bounds = np.concatenate([[0], cuts])
-        self.head_rows = torch.from_numpy(bounds.astype(np.int32)).to(dev)
-        need = 0
-        for b in range(1, self.ncta):
-            r0, r1 = bounds[b], bounds[b + 1]
-            ne = hptr[r1] - hptr[r0]
-            need = max(need, ((r1 - r0 + 1) * 4 + 15) // 16 * 16 + ne * pk.esz)
-        self.head_lds = int((need + 15) // 16 * 16)
-        base = int(self.lib.lxm_lds_base())
-        self.lds = max(base, int(self.lib.lxm_helper_lds(self.head_lds)))
-        self.lds = (self.lds + 255) // 256 * 256
-        self.smem = self.lds  # lx.mega.Mega's name for the launch's dynamic shared memory
-        maxlds = int(self.lib.lxm_max_lds())
-        assert self.lds <= maxlds, (self.lds, maxlds)
-        assert int(self.lib.lxm_max_blocks(self.lds)) >= self.ncta, "the grid is not co-resident"
-        self.vocab = V
-        assert V <= 1 << 19, "at most 2^19 vocabulary rows (the head keys carry a 19-bit index)"
-        assert d.nv <= 256 and d.nk <= 176, "value heads <= 256, key heads <= 176"
+        pl = pack(fast, offset, ncta or int(self.lib.lxm_device_cus()), self.lib)
+        pl.check(int(self.lib.lxm_max_lds()))
+        if int(self.lib.lxm_max_blocks(pl.lds)) < pl.ncta:
+            raise PackError("the grid is not co-resident")
+        self.plan = pl
+        d = self.dims = pl.dims
+        self.ncta, self.bf, self.e4 = pl.ncta, pl.bf, pl.e4
+        self.lds = self.smem = pl.lds  # (smem: lx.mega.Mega's name for the launch's LDS)
+        self.head_lds, self.gate_bytes, self.gate_sec = pl.head_lds, pl.gate_bytes, pl.gate_sec
+        self.n_qk_total, self.vocab, self.n_hd = pl.n_qk_total, pl.vocab, pl.n_hd
+        self.unit_order, self.stats = pl.unit_order, pl.stats
+
+        def up(b, dtype=torch.uint8):
+            return torch.frombuffer(bytearray(b), dtype=torch.uint8).view(dtype).to(dev)
+
+        self.blob = up(pl.blob)
+        self.layers_d = up(pl.layers)
+        self.emb_ptr = torch.from_numpy(pl.emb_ptr).to(dev)
+        self.emb_ent = up(pl.emb_ent)
+        self.w1_final = torch.from_numpy(pl.w1_final).to(dev)
+        self.head_ptr = torch.from_numpy(pl.head_ptr).to(dev)
+        self.head_ent = up(pl.head_ent)
+        self.head_rows = torch.from_numpy(pl.head_rows).to(dev)
+        self.head_dcol = torch.from_numpy(pl.head_dcol).to(dev)
+        self.head_dtab = torch.from_numpy(pl.head_dtab).to(dev)
+        self.head_code = torch.from_numpy(pl.head_code.view(np.int64)).to(dev)
         # ---- run buffers (the library allocates nothing)
         self.ring = torch.zeros(4 * d.n_layers * MAXH, dtype=torch.float32, device=dev)
         self.rring = torch.zeros(4 * d.n_layers, dtype=torch.float32, device=dev)
@@ -385,9 +513,6 @@ class Mega:
         self.sync = torch.zeros(NSYNC, dtype=torch.int32, device=dev)
         self.keys = torch.zeros(2, dtype=torch.int64, device=dev)
         self.err = torch.zeros(1, dtype=torch.int32, device=dev)
-        self.stats.update({"ctas": self.ncta, "lds": self.lds, "head_lds": self.head_lds,
-                           "blob_bytes": int(self.blob.numel()), "qk_total": qk_total,
-                           "head_nnz": int(hptr[-1]), "vocab": V})
 
     PHASES = ("embedding", "residual + sums (stage C2, +trace)", "norms (stage A)",
               "gates + MLP units (stage B)", "GDN events + MLP redo",
@@ -477,7 +602,7 @@ class Mega:
             lines.append(f"buf {name} {fn}")
 
         for name in ("layers_d", "blob", "emb_ptr", "emb_ent", "w1_final", "head_rows",
-                     "head_ptr", "head_ent"):
+                     "head_ptr", "head_ent", "head_dcol", "head_dtab", "head_code"):
             buf({"layers_d": "layers"}.get(name, name), getattr(self, name))
         buf("forced", torch.tensor([int(forced[0])], dtype=torch.int32))
         for field, attr in (("rec", "recurrent_states"), ("conv", "conv_states")):
@@ -501,7 +626,8 @@ class Mega:
         p = Params(hidden=d.hidden, n_layers=d.n_layers, nk=d.nk, kd=KD, nv=d.nv, vd=VD,
                    n_conv=d.n_conv, vocab=self.vocab, bf16=int(self.bf), n_blocks=self.ncta,
                    rms_eps=d.rms_eps, head_lds=self.head_lds, e4=int(self.e4), n_forced=1,
-                   n_tokens=n, n_qk_total=self.n_qk_total, gate_bytes=self.gate_bytes)
+                   n_tokens=n, n_qk_total=self.n_qk_total, gate_bytes=self.gate_bytes,
+                   n_hd=self.n_hd)
         lines.append(f"sub gates blob {self.gate_sec}")
         with open(os.path.join(path, "params.bin"), "wb") as f:
             f.write(bytes(p))
@@ -544,7 +670,9 @@ class Mega:
                       inputs=inputs.data_ptr() if inputs is not None else None,
                       trace=trace.data_ptr() if trace is not None else None,
                       prof=prof.data_ptr() if prof is not None else None,
-                      n_qk_total=self.n_qk_total, **(bufs or {}))
+                      n_qk_total=self.n_qk_total, n_hd=self.n_hd,
+                      head_dcol=self.head_dcol.data_ptr(), head_dtab=self.head_dtab.data_ptr(),
+                      head_code=self.head_code.data_ptr(), **(bufs or {}))
 
     @torch.no_grad()
     def run(self, forced, n: int, dbg=None, dbg_tok: int = 0, dbg_items=None, prof=None,

@@ -349,7 +349,7 @@ def head_table(er, w1f: np.ndarray, hidden: int):
 class Prefill:
     """The packed tables of a Fast's layers and head on one device, and the drivers."""
 
-    def __init__(self, fast, device="cuda", offset: int = 0):
+    def __init__(self, fast, device="cuda", offset: int | None = None):
         self.fast = fast
         sm = fast.sm
         if synth.has_dense_order(sm):

@@ -32,7 +32,8 @@ import numpy as np
 VALS = np.array([-2.0, -1.0, -0.5, 0.5, 1.0, 2.0], dtype=np.float32)
 
 # component ids for per-(layer, component) seeds
-_QKV, _Z, _B, _A, _OUT, _CONV, _GATE, _UP, _DOWN, _LIVE, _EMB, _GEMB, _FN, _STATE, _START = range(15)
+_QKV, _Z, _B, _A, _OUT, _CONV, _GATE, _UP, _DOWN, _LIVE, _EMB, _GEMB, _FN, _STATE, _START, \
+    _HD, _MERGE = range(17)
 
 
 @dataclass
@@ -146,6 +147,11 @@ class Spec:
     emb_nnz: int = 3  # nonzeros per embedding row outside the gate columns
     state: str = "normal"  # initial recurrent state: "normal" (N(0,1)) or "zero"
     n_steps: int = 256
+    # dense head columns (the real chip's head has 31: every row nonzero, few distinct values,
+    # lx/results/mega_boot.json's head_dense): this many seeded non-gate columns of the tied
+    # embedding get a value on (almost) every row, from 4 values per column (the last column
+    # from {0, +-1/2, 1}, so it holds zeros too)
+    head_dense: int = 0
 
 
 def config1(seed: int = 1) -> Spec:
@@ -301,14 +307,45 @@ def build(spec: Spec, layers: list | None = None) -> SparseModel:
     on = np.arange(d.n_layers)[None, :] < k[:, None]
     gr = np.repeat(np.arange(V), on.sum(1))
     gc = hng + order[on]
-    embed = Coo.build((V, H), np.concatenate([rows, gr]), np.concatenate([cols.reshape(-1), gc]),
-                      np.concatenate([vals, rg.choice(VALS, size=len(gr))]))
+    rows, cols = np.concatenate([rows, gr]), np.concatenate([cols.reshape(-1), gc])
+    vals = np.concatenate([vals, rg.choice(VALS, size=len(gr))])
+    if spec.head_dense:
+        rd = _rng(s, 0, _HD)
+        dcols = rd.choice(hng, size=spec.head_dense, replace=False)
+        keep = ~np.isin(cols, dcols)
+        rows, cols, vals = rows[keep], cols[keep], vals[keep]
+        for j, c in enumerate(dcols):
+            tab = [-1.0, -0.5, 0.5, 1.0] if j + 1 < len(dcols) else [0.0, -0.5, 0.5, 1.0]
+            rows = np.concatenate([rows, np.arange(V)])
+            cols = np.concatenate([cols, np.full(V, c)])
+            vals = np.concatenate([vals, rd.choice(np.asarray(tab, np.float32), size=V)])
+    embed = Coo.build((V, H), rows, cols, vals)
     # final norm: weight 0 or -2 (1 + w = +-1) outside the gates, -1 on them (the head ignores
     # the gates)
     rf = _rng(s, 0, _FN)
     norm = np.where(rf.random(H) < 0.5, -2.0, 0.0).astype(np.float32)
     norm[hng:] = -1.0
     return SparseModel(d, layers, embed, norm, meta={"spec": spec})
+
+
+def merged(model: SparseModel, offset: int, seed: int = 0) -> SparseModel:
+    """The chip stack inside a larger vocabulary, as the reference's merged model holds it
+    (lx/lx/merge.py; lx/lx/linux.py:108-109): ``offset`` seeded rows of other tokens (a few
+    nonzeros each) before the chip's embedding rows, so chip token t is row offset + t.
+    ``Fast(m, rows=slice(offset, offset + vocab))`` and ``Mega(..., offset)`` select the chip's
+    rows again; the layers are the chip's."""
+    d = model.dims
+    r = _rng(seed, 0, _MERGE)
+    k = 4
+    xc = np.stack([r.choice(d.hidden, size=k, replace=False) for _ in range(offset)]) if offset \
+        else np.zeros((0, k), np.int64)
+    xr = np.repeat(np.arange(offset), k)
+    e = model.embed
+    emb = Coo.build((offset + d.vocab, d.hidden), np.concatenate([xr, e.rows + offset]),
+                    np.concatenate([xc.reshape(-1), e.cols]),
+                    np.concatenate([r.choice(VALS, size=offset * k), e.vals]))
+    return SparseModel(replace(d, vocab=offset + d.vocab), model.layers, emb, model.norm,
+                       meta={**model.meta, "merged_offset": offset})
 
 
 def _distinct_cols(rng, V: int, n: int, k: int) -> np.ndarray:
@@ -441,17 +478,43 @@ def to_hf(model: SparseModel, dev: str = "cpu"):
     return m.to(device=dev, dtype=dt).eval()
 
 
-def from_hf(m, n_chip: int | None = None) -> SparseModel:
-    """A transformers Qwen3_5 chip model's tensors (its first n_chip layers) in coordinate form."""
+def _coo_rows(w, lo: int, hi: int, block: int = 32768) -> Coo:
+    """Rows lo .. hi of a weight tensor in coordinate form, a block of rows at a time (the rows
+    are never densified in float32 all at once)."""
+    rs, cs, vs = [], [], []
+    for a in range(lo, hi, block):
+        x = w[a:min(a + block, hi)].detach().float().cpu().numpy()
+        r, c = np.nonzero(x)
+        rs.append(r.astype(np.int64) + (a - lo))
+        cs.append(c.astype(np.int64))
+        vs.append(x[r, c])
+    cat = lambda z, t: np.concatenate(z) if z else np.zeros(0, t)  # noqa: E731
+    return Coo((hi - lo, w.shape[1]), cat(rs, np.int64), cat(cs, np.int64), cat(vs, np.float32))
+
+
+def from_hf(m, n_chip: int | None = None, rows: slice | None = None) -> SparseModel:
+    """A transformers Qwen3_5 chip model's tensors (its first n_chip layers) in coordinate form.
+    rows: the head's rows (lx/lx/fast.py:183, the merged model's chip tokens); only those rows of
+    the tied embedding are read, and the result's embedding holds them (meta "row0": the first
+    one's index in the model)."""
     import torch
 
     cfg = m.config
     n = n_chip if n_chip is not None else cfg.num_hidden_layers
     dtype = "bf16" if m.dtype == torch.bfloat16 else "fp32"
+    w = m.lm_head.weight
+    lo = 0 if rows is None else (rows.start or 0)
+    hi = w.shape[0] if rows is None or rows.stop is None else min(rows.stop, w.shape[0])
+    e = m.model.embed_tokens.weight
+    if e.data_ptr() != w.data_ptr() and not all(
+            torch.equal(e[a:min(a + 65536, hi)], w[a:min(a + 65536, hi)])
+            for a in range(lo, hi, 65536)):
+        raise ValueError("the chip path reads one tied table for its inputs and its head: "
+                         "lm_head and embed_tokens differ on the chip's rows")
     d = Dims(hidden=cfg.hidden_size, n_layers=n, nk=cfg.linear_num_key_heads,
              kd=cfg.linear_key_head_dim, nv=cfg.linear_num_value_heads,
              vd=cfg.linear_value_head_dim, conv=cfg.linear_conv_kernel_dim,
-             inter=cfg.intermediate_size, vocab=m.lm_head.weight.shape[0], dtype=dtype,
+             inter=cfg.intermediate_size, vocab=hi - lo, dtype=dtype,
              rms_eps=cfg.rms_norm_eps,
              gated_eps=float(m.model.layers[0].linear_attn.norm.variance_epsilon) if n else None)
 
@@ -474,7 +537,8 @@ def from_hf(m, n_chip: int | None = None) -> SparseModel:
             post_attention_layernorm=f(lay.post_attention_layernorm.weight),
             gate_proj=coo(lay.mlp.gate_proj.weight), up_proj=coo(lay.mlp.up_proj.weight),
             down_proj=coo(lay.mlp.down_proj.weight)))
-    return SparseModel(d, layers, coo(m.lm_head.weight), f(m.model.norm.weight))
+    return SparseModel(d, layers, _coo_rows(w, lo, hi), f(m.model.norm.weight),
+                       meta={"row0": lo})
 
 
 # ---------------------------------------------------------------------------------------------

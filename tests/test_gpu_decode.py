@@ -25,7 +25,11 @@ def cuda():
 
 
 def _specs():
+    import dataclasses
+
     return {"small": synth.small(), "small_fp32": synth.small(dtype="fp32", seed=3),
+            "small_hd": dataclasses.replace(synth.small(seed=11), head_dense=5),
+            "small_hd_fp32": dataclasses.replace(synth.small(dtype="fp32", seed=12), head_dense=3),
             "c1": synth.config1(), "c2": synth.config2(), "c5": synth.config5()}
 
 
@@ -45,17 +49,27 @@ def bits(a):
     return np.ascontiguousarray(a, np.float32).view(np.uint32)
 
 
-def check(name, n, forced=None, launches=None, conv0=None, trace=True):
-    """Run the kernel and the oracle from the same state; compare everything bit for bit."""
+def check(name, n, forced=None, launches=None, conv0=None, trace=True, merged=None):
+    """Run the kernel and the oracle from the same state; compare everything bit for bit.
+    merged (offset, via): the chip's rows at offset in a larger embedding (synth.merged), the
+    kernel built through Fast(rows=...) and Mega(offset) from the coordinate model (via "coo")
+    or from a transformers model of it (via "hf"); the oracle runs the chip-only model."""
     from oracle import oracle as ox
 
     spec, m, c0, r0 = model(name)
     conv0 = c0 if conv0 is None else conv0
     print(f"[gpu-test] {name}: n={n} forced={None if forced is None else len(forced)} "
-          f"launches={launches}", flush=True)
+          f"launches={launches} merged={merged}", flush=True)
     forced = [synth.start_token(spec)] if forced is None else list(forced)
     cache = fast.StateCache(conv0, r0, m.dims.dtype, "cuda")
-    mg = mega.Mega(fast.Fast(m), m, cache, 0)
+    if merged is None:
+        mg = mega.Mega(fast.Fast(m), m, cache, 0)
+    else:
+        off, via = merged
+        mm = synth.merged(m, off)
+        src = mm if via == "coo" else synth.to_hf(mm)
+        f = fast.Fast(src, m.dims.n_layers, slice(off, off + m.dims.vocab))
+        mg = mega.Mega(f, src, cache, off)
     d = m.dims
     tr = torch.zeros(n, d.n_layers, d.hidden, device="cuda") if trace else None
     inp = torch.zeros(n, dtype=torch.int32, device="cuda")
@@ -169,6 +183,43 @@ def test_config2(cuda):
 def test_config5(cuda):
     """BASELINE config 5 (half of the layer-steps gated): 8 steps."""
     check("c5", 8)
+
+
+def test_dense_head_columns(cuda):
+    """A head with dense columns (every row nonzero there; 2-bit codes in the helpers' LDS, the
+    reference's head_dense), one with zeros: bf16 and fp32 stacks."""
+    spec, m, _, _ = model("small_hd")
+    assert mega.pack(fast.Fast(m), 0, 256).n_hd == 5
+    check("small_hd", 48)
+    check("small_hd_fp32", 40)
+
+
+@pytest.mark.parametrize("via", ["coo", "hf"])
+def test_merged_model_offset(cuda, via):
+    """The merged model's call path (lx/lx/linux.py:108-109, :222): Fast(model, n_chip,
+    rows=slice(offset, offset + VOCAB)) and Mega(fast, model, cache, offset), here with 300 rows
+    of other tokens before the chip's; the inputs are chip token ids."""
+    check("small_hd", 40, merged=(300, via), launches=[17, 23])
+
+
+def test_merged_model_verified_mode(cuda):
+    """Verified mode (Fast.verify) through the merged model's Fast (transformers model, rows)
+    against the oracle's forced decode of the chip-only model."""
+    from oracle import oracle as ox
+
+    spec, m, c0, r0 = model("small_hd")
+    off = 300
+    hf = synth.to_hf(synth.merged(m, off))
+    f = fast.Fast(hf, m.dims.n_layers, slice(off, off + m.dims.vocab))
+    toks = [int(t) for t in synth.tokens(spec, 29, 3)]
+    print("[gpu-test] merged verified mode: 29 tokens", flush=True)
+    cache = fast.StateCache(c0, r0, m.dims.dtype, "cuda")
+    got = f.verify(toks, cache).cpu().numpy().tolist()
+    c, r = c0.copy(), r0.copy()
+    want, _, _ = ox.OracleModel(m).decode(c, r, toks, len(toks))
+    assert got == want.tolist()
+    assert (bits(cache.conv_numpy()) == bits(c)).all()
+    assert (bits(cache.rec_numpy()) == bits(r)).all()
 
 
 def test_launches_continue_the_stream(cuda):

@@ -379,3 +379,101 @@ def test_prefill_head_table_rows():
     assert (hent["off"][hptr[-1]:] == 16 * hidden).all() and (hent["w"][hptr[-1]:] == 0).all()
     assert sl[0] == 0 and sl[-1] == len(rows) and (np.diff(sl) >= 0).all()
     assert len(sl) == prefill.SLICES + 1
+
+
+def _head_dense_back(pl, H):
+    """The packed head (entries plus coded dense columns) as a dense (vocab, hidden) array."""
+    V = pl.vocab
+    out = np.zeros((V, H), np.float32)
+    ent = np.frombuffer(pl.head_ent, np.uint32)[:pl.head_ptr[-1]]
+    rows = np.repeat(np.arange(V), np.diff(pl.head_ptr))
+    out[rows, (ent & 0xffff) // 4] = ((ent >> 16) << 16).view(np.float32)
+    for j in range(pl.n_hd):
+        codes = ((pl.head_code >> np.uint64(2 * j)) & np.uint64(3)).astype(np.int64)
+        out[:, pl.head_dcol[j]] = pl.head_dtab[4 * j + codes]
+    return out
+
+
+def test_dense_head_columns_decode_to_the_model(native_lib):
+    """A head with dense columns (every row nonzero there, 4 values; one column with zeros): the
+    coded columns and the remaining entries decode back to the tied head's rows exactly, and the
+    coded columns are exactly the dense ones."""
+    import dataclasses
+
+    m = synth.build(dataclasses.replace(synth.small(), head_dense=5))
+    pl = mega.pack(fast.Fast(m), 0, 256, native_lib)
+    assert pl.n_hd == 5
+    w1 = 1.0 + m.norm
+    want = m.embed.dense() * (w1 != 0)[None]
+    assert np.array_equal(_head_dense_back(pl, m.dims.hidden), want)
+    cnt = (want != 0).sum(0)
+    assert set(pl.head_dcol[:5].tolist()) == set(np.nonzero(cnt * 2 >= m.dims.vocab)[0].tolist())
+    assert (np.diff(pl.head_dcol[:5]) > 0).all()
+    # without dense columns nothing is coded
+    pl0 = mega.pack(fast.Fast(synth.build(synth.small())), 0, 256, native_lib)
+    assert pl0.n_hd == 0 and pl0.summary()["head_dense_cols"] == 0
+
+
+def test_merged_layout_packs_the_chip_rows(native_lib):
+    """The chip inside a larger vocabulary (lx/lx/linux.py:108-109's rows = slice(offset,
+    offset + VOCAB), Mega's offset): the packed tables equal the chip-only model's, through the
+    coordinate model and through a transformers model (only the chip's rows of its head read);
+    an offset that is not where the rows start is refused."""
+    m = synth.build(synth.small())
+    off = 300
+    mm = synth.merged(m, off)
+    want = mega.pack(fast.Fast(m), 0, 256, native_lib)
+    rows = slice(off, off + m.dims.vocab)
+    f = fast.Fast(mm, rows=rows)
+    got = mega.pack(f, off, 256, native_lib)
+    hf = synth.to_hf(mm)
+    fh = fast.Fast(hf, m.dims.n_layers, rows)
+    assert fh.sm.embed.shape == (m.dims.vocab, m.dims.hidden)  # only the chip's rows were read
+    via_hf = mega.pack(fh, off, 256, native_lib)
+    for pl in (got, via_hf):
+        assert pl.blob == want.blob and pl.emb_ent == want.emb_ent and pl.head_ent == want.head_ent
+        assert np.array_equal(pl.emb_ptr, want.emb_ptr) and np.array_equal(pl.head_ptr, want.head_ptr)
+        assert pl.vocab == m.dims.vocab
+    with pytest.raises(ValueError, match="offset"):
+        mega.pack(f, 0, 256, native_lib)
+    with pytest.raises(ValueError, match="offset"):
+        mega.pack(fast.Fast(m), 5, 256, native_lib)
+    # the verified-mode tables read the same rows
+    pf_rows = f.embed_rows()
+    assert pf_rows.n == m.dims.vocab and np.array_equal(pf_rows.cols, fast.Fast(m).embed_rows().cols)
+
+
+def test_real_chip_sizes(native_lib):
+    """The reference's real chip against the decode kernel's limits, from its published table
+    statistics (lx/results/mega_boot.json: 459,982 head rows, 31 dense head columns, 4,133,751
+    other head nonzeros; fast_boot.json: hidden 2560, 37 layers, up to 8,102 live MLP units in
+    one layer). The head now fits a helper's LDS (its dense columns as 2-bit codes, not 14.3M
+    entries), and the packer names the limit the MLP units break (LXM_MAXU)."""
+    import dataclasses
+
+    d = synth.Dims(hidden=2560, n_layers=1, vocab=459_982, inter=1024)
+    spec = dataclasses.replace(synth.small(), dims=d, emb_nnz=9, head_dense=31, density=0.0008,
+                               p_live=0.25, p_decay=0.25, p_tap=0.1)
+    m = synth.build(spec)
+    e = m.embed
+    dense_cols = np.nonzero(np.bincount(e.cols, minlength=d.hidden) == d.vocab)[0]
+    assert len(dense_cols) >= 30
+    pl = mega.pack(fast.Fast(m), 0, 256, native_lib).check()
+    assert pl.n_hd == 31
+    assert abs(pl.summary()["head_nnz"] - 4_133_751) / 4_133_751 < 0.02  # the other columns
+    # (about 140 KB a helper: 89 KB of head tables, 14 KB of them the codes; the same rows as
+    # 4-byte entries would need ~290 KB)
+    assert pl.lds <= mega.MAX_LDS_MI355X and pl.lds_helper <= mega.MAX_LDS_MI355X
+    # a layer with the real chip's largest live-unit count
+    ly = m.layers[0]
+    rng = np.random.default_rng(0)
+    U, d2 = 8102, dataclasses.replace(d, inter=9216)
+    cols = np.stack([rng.choice(d.hidden - 1, 3, replace=False) for _ in range(U)]).reshape(-1)
+    gate = synth.Coo.build((d2.inter, d.hidden), np.repeat(np.arange(U), 3), cols,
+                           np.ones(3 * U, np.float32))
+    down = synth.Coo.build((d.hidden, d2.inter), rng.integers(0, d.hidden - 1, U), np.arange(U),
+                           np.ones(U, np.float32))
+    big = dataclasses.replace(ly, gate_proj=gate, up_proj=gate, down_proj=down)
+    m2 = synth.SparseModel(d2, [big], m.embed, m.norm, meta=m.meta)
+    with pytest.raises(mega.PackError, match="LXM_MAXU"):
+        mega.pack(fast.Fast(m2), 0, 256, native_lib)
