@@ -129,6 +129,7 @@ def sync_costs(n_blocks: int) -> dict:
         err = torch.zeros(1, dtype=torch.int32, device=dev)
         res = torch.zeros(1, dtype=torch.float32, device=dev)
         st = ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream)
+        mk_build.note_cooperative()
         e = lib.lxm_t_sync(kind, 2000, n_blocks, far, ctypes.c_void_p(words.data_ptr()),
                            ctypes.c_void_p(err.data_ptr()), ctypes.c_void_p(res.data_ptr()), st)
         if e:
@@ -674,7 +675,8 @@ def prefill_leg(args, dev, hf_holder: dict) -> dict:
         out["cpu_baseline"] = {
             "value": round(n_cpu / dt, 2), "unit": "tok/s", "cores": cpu_threads(),
             "kind": "reference", "impl": "transformers-modules, torch eager",
-            "sample": f"one call over the first {n_cpu} positions of the warm-up call's tokens: "
+            "sample": f"one call over the first {n_cpu} positions of the warm-up call's tokens "
+                      "(bounded: BASELINE.md's 4,096-position call would take many minutes): "
                       f"the stock forward's T > 1 path (transformers {_tf_version()} "
                       "Qwen3_5 layers, torch_chunk_gated_delta_rule, dense bf16, torch eager), "
                       f"{cpu_threads()} host threads"}
@@ -683,56 +685,28 @@ def prefill_leg(args, dev, hf_holder: dict) -> dict:
     return out
 
 
-def dense_cpu_tok_s(dm, n: int) -> float:
-    """The dense stack's decode step restated with torch's eager ops in float32 on the host cores
-    (weights copied from the GPU once; the stock forward's structure, not its bit order): tok/s
-    over n greedy steps from a zero state. A reported baseline only."""
-    import torch
-    import torch.nn.functional as F
+def dense_cpu_stock(dm, toks, n_prompt: int, max_steps: int, budget_s: float) -> dict:
+    """Config 4's CPU baseline: the stock forward (transformers' Qwen3_5 layers, torch eager,
+    bf16) on the padded model (synth.dense_to_hf) on the host cores, as BASELINE.md's plan asks: a
+    prompt through the stock T > 1 path, then greedy steps (one token at a time) until max_steps
+    or budget_s of wall time. Returns the prompt's and the steps' rates and their sizes."""
+    import numpy as np
 
-    sp, d = dm.spec, dm.dims
-    H, nk, kl, rl = sp.hidden, sp.nk, sp.kd_live, sp.r_live
-    L = [{k: v.float().cpu() for k, v in ly.items()} for ly in dm.layers]
-    E = dm.embed.float().cpu()
-    wf = dm.norm.float().cpu()
-    S = [torch.zeros(nk * rl, 256, 128) for _ in L]
-    win = [torch.zeros(2 * nk * kl + nk * rl * 128, 4) for _ in L]
-    R = d.nv // nk
-    vh = torch.tensor([kh * R + r for kh in range(nk) for r in range(rl)])
+    from linuxformer_amd import synth
+    from oracle import stock
 
-    def rms(x, w, eps):
-        return (x * torch.rsqrt(x.pow(2).mean() + eps)) * (1.0 + w)
-
-    tok = 0
+    hf = synth.dense_to_hf(dm)
+    d = dm.dims
+    conv0 = np.zeros((d.n_layers, d.n_conv, 4), np.float32)
+    rec0 = np.zeros((d.n_layers, d.nv, 256, 128), np.float32)
+    stock.prefill(hf, conv0, rec0, toks[:8])  # warm-up (page-in)
     t = time.perf_counter()
-    for _ in range(n):
-        h = E[tok].clone()
-        for i, ly in enumerate(L):
-            x = rms(h, ly["ln_in"], sp.rms_eps)
-            qk = ly["qk"].reshape(-1, H) @ x
-            v = ly["v"].reshape(-1, H) @ x
-            z = (ly["z"].reshape(-1, H) @ x).view(nk * rl, 128)
-            b = ly["b"].reshape(-1, H) @ x
-            a = ly["a"].reshape(-1, H) @ x
-            P = torch.cat([qk, v])
-            win[i] = torch.cat([win[i][:, 1:], P[:, None]], 1)
-            taps = torch.cat([ly["conv_qk"].reshape(-1, 4), ly["conv_v"].reshape(-1, 4)])
-            y = F.silu((win[i] * taps).sum(1))
-            q = F.normalize(y[:nk * kl].view(nk, kl), dim=-1).repeat_interleave(rl, 0) / 16.0
-            k = F.normalize(y[nk * kl:2 * nk * kl].view(nk, kl), dim=-1).repeat_interleave(rl, 0)
-            vv = y[2 * nk * kl:].view(nk * rl, 128)
-            g = torch.exp(-torch.exp(ly["A_log"][vh]) * F.softplus(a + ly["dt_bias"][vh]))
-            St = S[i][:, :kl] * g[:, None, None]
-            kv = (St * k[:, :, None]).sum(1)
-            St = St + k[:, :, None] * ((vv - kv) * torch.sigmoid(b)[:, None])[:, None, :]
-            S[i][:, :kl] = St
-            o = (St * q[:, :, None]).sum(1)
-            on = (o * torch.rsqrt(o.pow(2).mean(-1, keepdim=True) + sp.gated_eps)) * ly["norm"] * F.silu(z)
-            h = h + ly["out"].reshape(H, -1) @ on.reshape(-1)
-            xm = rms(h, ly["ln_post"], sp.rms_eps)
-            h = h + ly["down"] @ (F.silu(ly["gate"] @ xm) * (ly["up"] @ xm))
-        tok = int(torch.argmax(E @ rms(h, wf, sp.rms_eps)))
-    return n / (time.perf_counter() - t)
+    pc, conv, rec = stock.prefill(hf, conv0, rec0, toks[:n_prompt])
+    pre_s = time.perf_counter() - t
+    tps, n, _ = stock_decode_baseline(hf, conv, rec, int(pc[-1]), max_steps, budget_s)
+    del hf
+    return {"prompt_tokens": n_prompt, "prompt_tok_s": round(n_prompt / pre_s, 2),
+            "steps": n, "tok_s": round(tps, 3)}
 
 
 def dense_leg(args, dev) -> dict:
@@ -849,11 +823,15 @@ def dense_leg(args, dev) -> dict:
                          {"steps": n_per, "tok_s": round(n_per / (ms_per * 1e-3), 1),
                           "note": "lxm_dn_run, continuing from the greedy run's states"}}
     if args.dn_cpu_tokens > 0 and args.cpu_seconds > 0:
-        out["cpu_baseline"] = {"value": round(dense_cpu_tok_s(dm, args.dn_cpu_tokens), 3),
-                               "unit": "tok/s", "cores": cpu_threads(), "kind": "port",
-                               "impl": "torch-eager",
-                               "sample": f"{args.dn_cpu_tokens} greedy steps from a zero state, "
-                                         "the stock layer's ops in torch eager float32"}
+        cb = dense_cpu_stock(dm, toks, args.dn_cpu_prompt, args.dn_cpu_tokens, args.cpu_seconds)
+        out["cpu_baseline"] = {
+            "value": cb["tok_s"], "unit": "tok/s", "cores": cpu_threads(), "kind": "reference",
+            "impl": "transformers-modules, torch eager",
+            "prefill_tok_s": cb["prompt_tok_s"],
+            "sample": f"the stock forward on the padded model (transformers {_tf_version()} Qwen3_5 "
+                      f"layers, bf16, torch eager, {cpu_threads()} host threads): a "
+                      f"{cb['prompt_tokens']}-token prompt of the run's tokens through the T > 1 "
+                      f"path (not 8,192: bounded), then {cb['steps']} greedy steps"}
     return out
 
 
@@ -882,10 +860,17 @@ def make_parser() -> argparse.ArgumentParser:
     ap.add_argument("--c1-runs", type=int, default=5)
     ap.add_argument("--pf-calls", type=int, default=5)
     ap.add_argument("--pf-tokens", type=int, default=65_536)
-    ap.add_argument("--pf-cpu-tokens", type=int, default=256)
+    ap.add_argument("--pf-cpu-tokens", type=int, default=512,
+                    help="positions of config 3's CPU baseline call (BASELINE.md plans 4,096; the "
+                         "stock T > 1 forward grows faster than linearly on the host: 512 "
+                         "positions took 35 s and 1,024 took 147 s on 8 threads, so a bounded "
+                         "sample is 512)")
     ap.add_argument("--dn-prefill", type=int, default=8192)
     ap.add_argument("--dn-steps", type=int, default=4096)
-    ap.add_argument("--dn-cpu-tokens", type=int, default=4)
+    ap.add_argument("--dn-cpu-tokens", type=int, default=256,
+                    help="greedy steps of config 4's CPU baseline, at most (--cpu-seconds bounds)")
+    ap.add_argument("--dn-cpu-prompt", type=int, default=256,
+                    help="prompt tokens of config 4's CPU baseline (the stock T > 1 path)")
     ap.add_argument("--dn-graph", type=int, default=1,
                     help="1: the dense steps replayed from a captured graph; 0: launched eagerly")
     ap.add_argument("--dn-batched", type=int, default=1,

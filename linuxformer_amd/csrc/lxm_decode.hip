@@ -117,7 +117,7 @@ static_assert((L_FLAGS + 4 * F_KEYW) % 8 == 0 && F_KEYW + 16 <= 256, "the key wo
 #define S_EV 0       // + 32 g: seq << 8 | layer << 2 | out << 1 | kind (0 head, 1 gdn)
 #define S_DONE 768
 #define S_OWN 1024   // + 32 vh: the number of GDN events whose output value head vh has stored
-#define S_XO (S_OWN + 32 * LXM_SCRATCH_MAXNV)  // + 32 j: the seq whose out_proj rows helper 1 + j stored
+#define S_XO (S_OWN + 32 * LXM_SCRATCH_MAXNV)  // + 32 j: the seq whose out_proj rows helper j stored
 #define S_KEY (S_XO + 32 * LXM_OUT_HELPERS)    // + 32 b (a uint64): helper b's head key, stamped
 #define S_END (S_KEY + 32 * LXM_MAXBLOCKS)
 static_assert(S_END == LXM_NSYNC, "LXM_NSYNC matches the layout");
@@ -1921,11 +1921,15 @@ __device__ void run_helper(const lxm_params& pg) {
       rank[c] = (uint8_t)nb;
     }
   }
-  // out_proj rows of this helper: an even split of the residual rows over the first
-  // LXM_OUT_HELPERS helpers
+  // out_proj rows of this helper: an even split of the residual rows over LXM_OUT_HELPERS
+  // helpers (fewer on a smaller grid): the helpers after the value heads' owners when enough
+  // remain, so that every out_proj helper reads its tables and polls the heads' outputs while
+  // the heads work (an owner would start only after its own head's step); else the first ones
   const int no = nh < LXM_OUT_HELPERS ? nh : LXM_OUT_HELPERS;
   const int rp = (H + no - 1) / no;
-  const int ra = (b - 1) * rp < H ? (b - 1) * rp : H, rb = ra + rp < H ? ra + rp : H;
+  const int ob = b - 1 - (nh - p.nv >= no ? p.nv : 0);  // out_proj index (helper ob of no)
+  const bool oh = ob >= 0 && ob < no;
+  const int ra = oh && ob * rp < H ? ob * rp : H, rb = ra + rp < H ? ra + rp : H;
   const int vh = b - 1;
   const bool owner = vh < p.nv;
   const int grp = b % NGRP;
@@ -1988,7 +1992,7 @@ __device__ void run_helper(const lxm_params& pg) {
         w2 = cycles();
         pr[2] += w2 - w1;
       }
-      if (out && b <= no && rb > ra) {  // the out_proj helpers: their rows, as stamped words,
+      if (out && oh && rb > ra) {  // the out_proj helpers: their rows, as stamped words,
         // from every value head's stamped output
         const int ne = out_prep<BF, E4>(p, L, ra, rb, hx);
         if (!out_rows<BF, E4>(p, ra, rb, ne, seq, hx)) return;
@@ -1998,11 +2002,11 @@ __device__ void run_helper(const lxm_params& pg) {
         drain();
         __syncthreads();
       }
-      if (out && b <= no) {
+      if (out && oh) {
 #ifdef LXM_SUBPROF
         if (evh && t == 0) evh[3] += wall();
 #endif
-        if (t == 0) st_rlx(p.sync + S_XO + 32 * (b - 1), seq);
+        if (t == 0) st_rlx(p.sync + S_XO + 32 * ob, seq);
       }
       if (PROF_ON) pr[3] += cycles() - w2;
     }

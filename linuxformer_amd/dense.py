@@ -227,6 +227,7 @@ class DenseDecode:
             self._nf, self._pp, self.graph = len(f), pp, None
         if mode == "persistent":
             st = ctypes.c_void_p(torch.cuda.current_stream(self.dev).cuda_stream)
+            mk_build.note_cooperative()
             e = self.lib.lxm_dn_run(ctypes.byref(self._p), ctypes.c_void_p(self._pd.data_ptr()), n, st)
             if e:
                 raise RuntimeError(f"dense decode launch failed: hipError {e}")

@@ -712,6 +712,7 @@ class Mega:
         pd = torch.frombuffer(bytearray(bytes(p)), dtype=torch.uint8).to(self.dev)
         self._keep = (rs, cs, ft, pd)
         st = ctypes.c_void_p(torch.cuda.current_stream(self.dev).cuda_stream)
+        mk_build.note_cooperative()
         e = self.lib.lxm_run(ctypes.byref(p), ctypes.c_void_p(pd.data_ptr()), self.ncta,
                              self.lds, st)
         if e:
@@ -742,6 +743,7 @@ class Mega:
         p = self._params(rs, cs, forced, forced.numel(), n, preds, inputs)
         p.err = err.data_ptr()
         st = ctypes.c_void_p(torch.cuda.current_stream(self.dev).cuda_stream)
+        mk_build.note_cooperative()
         e = self.lib.lxm_run_noalloc(ctypes.byref(p), self.ncta, self.lds, st)
         if e:
             raise RuntimeError(f"mega launch failed: hipError {e}")

@@ -63,6 +63,15 @@ def build(verbose: bool = False) -> str:
 
 
 _libs = {}
+# cooperative launches this process has made (lxm_run, lxm_run_noalloc, lxm_dn_run, lxm_t_sync):
+# on the GPU boxes a cooperative launch from another process is refused (hipErrorIllegalState)
+# while one that has made them holds the device
+cooperative_launches = 0
+
+
+def note_cooperative() -> None:
+    global cooperative_launches
+    cooperative_launches += 1
 
 
 def load(subprof: bool = False) -> ctypes.CDLL:

@@ -475,7 +475,11 @@ def to_hf(model: SparseModel, dev: str = "cpu"):
     m.tie_weights()
     from transformers.models.qwen3_5 import modeling_qwen3_5 as q
     m.model.rotary_emb = q.Qwen3_5TextRotaryEmbedding(config=cfg)
-    return m.to(device=dev, dtype=dt).eval()
+    m = m.to(device=dev, dtype=dt).eval()
+    if d.gated_eps is not None:  # (the gated norm's own eps, where the stack has one)
+        for layer in m.model.layers:
+            layer.linear_attn.norm.variance_epsilon = d.gated_eps
+    return m
 
 
 def _coo_rows(w, lo: int, hi: int, block: int = 32768) -> Coo:
@@ -726,6 +730,72 @@ def to_sparse(dm: DenseModel) -> SparseModel:
             down_proj=coo_rows((H, d.inter), allH, np32(ly["down"]), np.arange(d.inter))))
     embed = coo_rows((d.vocab, H), np.arange(d.vocab), np32(dm.embed), allH)
     return SparseModel(d, layers, embed, np32(dm.norm), meta={"dense_spec": sp})
+
+
+def dense_to_hf(dm: DenseModel):
+    """Config 4's stack as the stock transformers Qwen3_5ForCausalLM on the host, in its padded
+    layout (lx/lx/merge.py:82-120: 256-dim key heads with zero upper dims, 8 value heads per key
+    head of which the first r_live are live; zeros everywhere else), bf16, the gated norm's eps
+    set to the spec's. The CPU baseline's model: the reference's stock forward runs it as is."""
+    import torch
+    from transformers import Qwen3_5ForCausalLM, Qwen3_5TextConfig
+
+    sp, d = dm.spec, dm.dims
+    H, nk, kl, rl, R = sp.hidden, sp.nk, sp.kd_live, sp.r_live, d.nv // d.nk
+    cfg = Qwen3_5TextConfig(
+        vocab_size=d.vocab, hidden_size=H, intermediate_size=d.inter,
+        num_hidden_layers=d.n_layers, layer_types=["linear_attention"] * d.n_layers,
+        linear_key_head_dim=256, linear_value_head_dim=128, linear_num_key_heads=nk,
+        linear_num_value_heads=d.nv, linear_conv_kernel_dim=4, rms_norm_eps=sp.rms_eps,
+        tie_word_embeddings=True, hidden_act="silu", num_attention_heads=4,
+        num_key_value_heads=1, head_dim=64,
+        rope_parameters={"rope_type": "default", "rope_theta": 10000.0,
+                         "partial_rotary_factor": 0.25})
+    with torch.device("meta"):
+        m = Qwen3_5ForCausalLM(cfg)
+    bf, cpu = torch.bfloat16, lambda x: x.detach().to("cpu")  # noqa: E731
+    vh = torch.tensor([kh * R + r for kh in range(nk) for r in range(rl)])
+    vdims = (vh[:, None] * 128 + torch.arange(128)[None]).reshape(-1)
+    qrows = torch.tensor([kh * 256 + i for kh in range(nk) for i in range(kl)])
+    sd = {}
+    for L, ly in enumerate(dm.layers):
+        p, ga = f"model.layers.{L}.", f"model.layers.{L}.linear_attn."
+        C = 2 * nk * 256 + d.nv * 128
+        qkv = torch.zeros(C, H, dtype=bf)
+        qk = cpu(ly["qk"]).reshape(2, nk * kl, H)
+        qkv[qrows], qkv[nk * 256 + qrows] = qk[0], qk[1]
+        qkv[2 * nk * 256 + vdims] = cpu(ly["v"]).reshape(-1, H)
+        conv = torch.zeros(C, 1, 4, dtype=bf)
+        cqk = cpu(ly["conv_qk"]).reshape(2, nk * kl, 4)
+        conv[qrows, 0], conv[nk * 256 + qrows, 0] = cqk[0], cqk[1]
+        conv[2 * nk * 256 + vdims, 0] = cpu(ly["conv_v"]).reshape(-1, 4)
+        z = torch.zeros(d.nv * 128, H, dtype=bf)
+        z[vdims] = cpu(ly["z"]).reshape(-1, H)
+        ba = {k: torch.zeros(d.nv, H, dtype=bf) for k in ("b", "a")}
+        for k in ba:
+            ba[k][vh] = cpu(ly[k]).reshape(-1, H)
+        out = torch.zeros(H, d.nv * 128, dtype=bf)
+        out[:, vdims] = cpu(ly["out"]).reshape(H, -1)
+        sd.update({ga + "in_proj_qkv.weight": qkv, ga + "in_proj_z.weight": z,
+                   ga + "in_proj_b.weight": ba["b"], ga + "in_proj_a.weight": ba["a"],
+                   ga + "out_proj.weight": out, ga + "conv1d.weight": conv,
+                   ga + "A_log": cpu(ly["A_log"]).to(bf), ga + "dt_bias": cpu(ly["dt_bias"]).to(bf),
+                   ga + "norm.weight": cpu(ly["norm"]).to(bf),
+                   p + "input_layernorm.weight": cpu(ly["ln_in"]).to(bf),
+                   p + "post_attention_layernorm.weight": cpu(ly["ln_post"]).to(bf),
+                   p + "mlp.gate_proj.weight": cpu(ly["gate"]), p + "mlp.up_proj.weight": cpu(ly["up"]),
+                   p + "mlp.down_proj.weight": cpu(ly["down"])})
+    sd["model.embed_tokens.weight"] = cpu(dm.embed)
+    sd["model.norm.weight"] = cpu(dm.norm).to(bf)
+    missing, unexpected = m.load_state_dict(sd, strict=False, assign=True)
+    assert not unexpected and set(missing) <= {"lm_head.weight"}, (missing[:4], unexpected[:4])
+    m.tie_weights()
+    from transformers.models.qwen3_5 import modeling_qwen3_5 as q
+    m.model.rotary_emb = q.Qwen3_5TextRotaryEmbedding(config=cfg)
+    m = m.to(dtype=bf).eval()
+    for layer in m.model.layers:
+        layer.linear_attn.norm.variance_epsilon = sp.gated_eps
+    return m
 
 
 def has_dense_order(model) -> bool:

@@ -39,7 +39,9 @@ _MODELS = {}
 def model(name):
     if name not in _MODELS:
         spec = _specs()[name]
-        m = synth.build(spec)
+        # (configs 2 and 5 share their layers: only the embedding's gate columns differ)
+        other = {"c2": "c5", "c5": "c2"}.get(name)
+        m = synth.build(spec, layers=_MODELS[other][1].layers if other in _MODELS else None)
         conv0, rec0 = synth.init_state(m)
         _MODELS[name] = (spec, m, conv0, rec0)
     return _MODELS[name]
@@ -270,20 +272,23 @@ def test_config2_long_run_properties(cuda):
         assert idle and (bits(rec[L][idle]) == bits(r0[L][idle])).all()
 
 
-def test_config2_whole_chunk_equals_oracle(cuda):
-    """BASELINE config 2's whole 262,144-token greedy chunk from its start token and initial
-    state, in four launches continuing one stream: the prediction stream and the final conv
-    windows and recurrent states hash to what the CPU oracle's run of the same chunk hashes
-    (tests/golden/c2_chunk.json, written by tests/golden/make_chunk.py; the reference pins its
-    boot the same way: lx/tools/mega_boot.py:74-75, lx/results/mega_boot.json's stream_sha256)."""
+@pytest.mark.parametrize("name,golden", [("c2", "c2_chunk.json"), ("c5", "c5_run.json")])
+def test_whole_run_equals_oracle(cuda, name, golden):
+    """BASELINE config 2's whole 262,144-token greedy chunk, and config 5's 65,536-token run
+    (half of the layer-steps gated: long chains of GDN events and MLP redos), each from its start
+    token and initial state, in four launches continuing one stream: the prediction stream and
+    the final conv windows and recurrent states hash to what the CPU oracle's run of the same
+    tokens hashes (tests/golden/c2_chunk.json and c5_run.json, written by
+    tests/golden/make_chunk.py; the reference pins its boot the same way:
+    lx/tools/mega_boot.py:74-75, lx/results/mega_boot.json's stream_sha256)."""
     import hashlib
     import json
     import os
 
-    g = json.load(open(os.path.join(os.path.dirname(__file__), "golden", "c2_chunk.json")))
-    spec, m, conv0, rec0 = model("c2")
+    g = json.load(open(os.path.join(os.path.dirname(__file__), "golden", golden)))
+    spec, m, conv0, rec0 = model(name)
     assert g["config"] == spec.name and g["start"] == synth.start_token(spec)
-    print(f"[gpu-test] c2 whole chunk: {g['chunk']} tokens", flush=True)
+    print(f"[gpu-test] {name} whole run: {g['chunk']} tokens", flush=True)
     cache = fast.StateCache(conv0, rec0, m.dims.dtype, "cuda")
     mg = mega.Mega(fast.Fast(m), m, cache, 0)
     preds, tok = [], g["start"]
@@ -291,7 +296,7 @@ def test_config2_whole_chunk_equals_oracle(cuda):
     for _ in range(4):
         preds += mg.run([tok], n)
         tok = preds[-1]
-        print(f"[gpu-test] c2 whole chunk: {len(preds)} tokens", flush=True)
+        print(f"[gpu-test] {name} whole run: {len(preds)} tokens", flush=True)
     assert preds[:256] == g["first_preds"] and preds[-16:] == g["last_preds"]
     assert hashlib.sha256(np.asarray(preds, "<i4").tobytes()).hexdigest() == g["stream_sha256"]
     hc, hr = hashlib.sha256(), hashlib.sha256()
