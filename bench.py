@@ -163,14 +163,36 @@ def restore(cache, saved) -> None:
 
 def chain_counters(mg, start: int, n: int) -> dict:
     """The chain's own counters over one launch of n greedy tokens from start: GDN events and MLP
-    redos (the MLP run again after an event with a live query) per token."""
+    redos (the MLP run again after an event with a live query) per token, and where the chain's
+    time goes (``chain``: its clock cycles per token by phase over the launch's wall time)."""
     import torch
 
     prof = torch.zeros(mg.prof_size, dtype=torch.int64, device=mg.dev)
+    stream = torch.cuda.current_stream(mg.dev)
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
     preds = mg.run([start], n, prof=prof)
+    e1.record(stream)
+    torch.cuda.synchronize()
+    us_tok = e0.elapsed_time(e1) * 1e3 / n
     rep = mg.phase_report(prof)
+    cyc = {k: rep[k] for k in mg.PHASES}
+    tot = sum(cyc.values())
+    mhz = tot / us_tok
+    stages = sum(v for k, v in cyc.items() if k not in ("GDN events + MLP redo", "head argmax wait"))
+    chain = {
+        "bound": "instruction issue of the chain workgroup's one CU (the token is one dependent "
+                 "chain of 37 layers; the layer stages run on one CU, the HBM and "
+                 "synchronisation floors are far below)",
+        "clock_mhz": round(mhz, 1), "us_per_token": round(us_tok, 2),
+        "layer_stages_us": round(stages / mhz, 2),
+        "gdn_events_us": round(cyc["GDN events + MLP redo"] / mhz, 2),
+        "head_wait_us": round(cyc["head argmax wait"] / mhz, 2),
+        "layer_stages_share": round(stages / tot, 4),
+        "cycles_per_layer": round(stages / mg.dims.n_layers, 1),
+        "cycles_per_token_by_phase": cyc}
     return {"tokens": n, "events_per_token": rep["GDN events per token"],
-            "mlp_redos_per_token": rep["MLP redos per token"], "preds": preds}
+            "mlp_redos_per_token": rep["MLP redos per token"], "preds": preds, "chain": chain}
 
 
 def state_sha(cache) -> tuple:
@@ -310,6 +332,7 @@ def decode_leg(args, dev, hf_holder: dict) -> dict:
     n_c = min(4096, chunk)
     restore(cache, saved)
     gdn_out = chain_counters(mg, start, n_c)
+    chain_roof = gdn_out.pop("chain")
     gdn_out["stream_equal"] = gdn_out.pop("preds") == stream_preds[:n_c]
     gdn_out["note"] = ("the chain's counters on the chunk's first tokens (a second launch from the "
                        "initial state)")
@@ -351,6 +374,8 @@ def decode_leg(args, dev, hf_holder: dict) -> dict:
                      "kernel_ms_per_launch": round(kern_ms, 3),
                      "launch_ms": [round(x, 2) for x in launch_ms]},
         "latency_roofline": lat,
+        # the binding resource: the chain's own cycle counters on the first tokens
+        "chain_roofline": chain_roof,
         "check": {"stream_sha256": stream_sha, "conv_sha256": conv_sha, "rec_sha256": rec_sha,
                   "distinct_predictions": len(set(stream_preds)),
                   "matches_oracle_chunk": None if gold is None else bool(
@@ -480,6 +505,7 @@ def stress_leg(args, dev, hf_holder: dict) -> dict:
     restore(cache, saved)
     n_c = min(args.c5_count_tokens, n_tok)
     counted = chain_counters(mg, start, n_c)
+    chain_roof = counted.pop("chain")
     counted["stream_equal"] = counted.pop("preds") == preds[:n_c]
     sync = hf_holder.get("sync") or sync_costs(mg.ncta)
     us_tok = kern_ms * 1e3 / (n_tok / len(sizes))
@@ -499,6 +525,7 @@ def stress_leg(args, dev, hf_holder: dict) -> dict:
                         "traffic": None, "bytes_per_token": round(b_tok),
                         "kernel_ms_per_launch": round(kern_ms, 3)},
            "latency_roofline": latency_roofline(sync, ev_tok, us_tok),
+           "chain_roofline": chain_roof,
            "check": {"stream_sha256": stream_sha, "conv_sha256": conv_sha, "rec_sha256": rec_sha,
                      "distinct_predictions": len(set(preds)),
                      "matches_oracle": None if gold is None else bool(

@@ -157,15 +157,58 @@ def write_prefill(name: str, base: str, T: int) -> None:
 PREFILL_CASES = {"small_fp32_pf100": ("small_fp32_32", 100), "small_bf16_pf100": ("small_bf16_32", 100)}
 
 
+def write_prefill_c3(name: str, T: int) -> None:
+    """The stock forward's T > 1 path over the first T tokens of config 3's first verified-mode
+    call (bench.py's warm-up call), on the 37-layer stack at its full shape: the argmax at every
+    position; each layer's largest output magnitude and its outputs at 4,096 seeded (position,
+    column) samples (bf16 bits: the layers' outputs are bf16); samples of the final states with
+    their largest magnitudes. The full trace (37 x T x 3572) is too large to commit."""
+    spec = synth.config3()
+    m = synth.build(spec)
+    conv0, rec0 = synth.init_state(m)
+    hf = synth.to_hf(m)
+    toks = synth.tokens(spec, 65_536, 0)[:T].astype(np.int64)
+    cache = stock.make_cache(hf, conv0, rec0)
+    h = hf.model.embed_tokens.weight[torch.from_numpy(toks)][None]
+    outs = stock.chip_forward(hf, h, cache)
+    trace = torch.stack([o[0].float() for o in outs], 1).numpy()  # (T, L, hidden)
+    preds = stock.head_argmax(hf, outs[-1][0]).numpy().astype(np.int32)
+    L, H = m.dims.n_layers, m.dims.hidden
+    conv = np.stack([cache.layers[k].conv_states[0][0].float().numpy() for k in range(L)])
+    rec = np.stack([cache.layers[k].recurrent_states[0][0].float().numpy() for k in range(L)])
+    rng = np.random.default_rng(5)
+    pos, col = rng.integers(0, T, 4096), rng.integers(0, H, 4096)
+    samp = trace[pos, :, col]  # (4096, L)
+    assert np.all((samp.view(np.uint32) & 0xffff) == 0)
+    ridx, cidx = rng.integers(0, rec.size, 8192), rng.integers(0, conv.size, 8192)
+    out = {"tokens": toks, "preds": preds, "pos": pos, "col": col,
+           "trace_bf16": (samp.T.copy().view(np.uint32) >> 16).astype(np.uint16),
+           "layer_max": np.abs(trace).max(axis=(0, 2)).astype(np.float32),
+           "rec_idx": ridx, "rec_sample": rec.reshape(-1)[ridx],
+           "rec_max": np.float32(np.abs(rec).max()), "conv_idx": cidx,
+           "conv_sample": conv.reshape(-1)[cidx], "conv_max": np.float32(np.abs(conv).max()),
+           "trace_sha": sha(trace), "transformers": __import__("transformers").__version__}
+    path = os.path.join(HERE, name + ".npz")
+    np.savez_compressed(path, **out)
+    print(name, os.path.getsize(path), "bytes", preds.tolist()[:8])
+
+
+PREFILL_C3_CASES = {"c3_pf64": 64}
+
+
 def main():
     torch.set_grad_enabled(False)
-    names = sys.argv[1:] or list(CASES) + list(CHUNK_CASES) + list(PREFILL_CASES)
+    names = sys.argv[1:] or list(CASES) + list(CHUNK_CASES) + list(PREFILL_CASES) + \
+        list(PREFILL_C3_CASES)
     for name in names:
         if name in CHUNK_CASES:
             write_chunk(name, *CHUNK_CASES[name])
             continue
         if name in PREFILL_CASES:
             write_prefill(name, *PREFILL_CASES[name])
+            continue
+        if name in PREFILL_C3_CASES:
+            write_prefill_c3(name, PREFILL_C3_CASES[name])
             continue
         _, n, full = CASES[name]
         m, conv0, rec0, start = model_of(name)

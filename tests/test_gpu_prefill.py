@@ -242,3 +242,25 @@ def test_verify_matches_stock_T_gt_1_forward(cuda):
     assert got.tolist() == g["preds"].tolist()
     r = cache.rec_numpy()
     assert np.abs(r.reshape(-1)[g["rec_idx"]] - g["rec_sample"]).max() <= 1e-6 * float(g["rec_max"])
+
+
+def test_config3_shape_matches_stock_T_gt_1_forward(cuda):
+    """Verified mode at config 3's full shape (37 layers, hidden 3,572, the c3 stack and its
+    N(0,1) state) over the first 64 tokens of bench.py's first call, layer by layer, against the
+    stock T > 1 forward (transformers' own modules; tests/golden/c3_pf64.npz)."""
+    from c3_check import check_against_stock_c3, c3_stock_fixture
+
+    g = c3_stock_fixture()
+    spec, m, c0, r0, f = model("c3")
+    tokens = [int(x) for x in g["tokens"]]
+    T = len(tokens)
+    print(f"[gpu-test] c3 shape vs stock T>1: T={T}", flush=True)
+    cache = fast.StateCache(c0, r0, m.dims.dtype, "cuda")
+    pf = f.prefill("cuda")
+    pf.embed(tokens)
+    traces = []
+    for L in range(m.dims.n_layers):
+        pf.layers(T, cache, L, L + 1)
+        traces.append(pf.from_tiles(T).float().cpu().numpy())
+    preds = pf.head(T).cpu().numpy()
+    check_against_stock_c3(traces, preds, cache.conv_numpy(), cache.rec_numpy(), g)

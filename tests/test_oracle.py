@@ -430,3 +430,29 @@ def test_oracle_prefill_chunked_differs_from_forced_decode(oracle_lib):
     om.decode(c2, r2, g["tokens"], len(g["tokens"]))
     d = np.abs(r1 - r2).max() / np.abs(r2).max()
     assert 0 < d < 1e-5
+
+
+def test_decode_form_within_stock_T_gt_1_at_config3_shape(oracle_lib):
+    """The oracle's decode form (what the verified-mode kernels compute, bit for bit) against
+    the stock T > 1 forward at config 3's full shape over 64 tokens (tests/golden/c3_pf64.npz):
+    the bounds the GPU test applies to the kernel (test_gpu_prefill.py) hold here; a decay left
+    out of one layer (its dt_bias moved) breaks them."""
+    import c3_check as gpf
+
+    ox = oracle_lib
+    g = gpf.c3_stock_fixture()
+    spec = synth.config3()
+    m = synth.build(spec)
+    conv0, rec0 = synth.init_state(m)
+    om = ox.OracleModel(m)
+    c, r = conv0.copy(), rec0.copy()
+    toks = [int(x) for x in g["tokens"]]
+    preds, _, tr = om.decode(c, r, toks, len(toks), trace=True)
+    gpf.check_against_stock_c3([tr[:, L] for L in range(m.dims.n_layers)], preds, c, r, g)
+    # a planted mistake: the recurrent states left undecayed where a decay acts
+    m.layers[5].dt_bias[:] = 0.0
+    om = ox.OracleModel(m)
+    c, r = conv0.copy(), rec0.copy()
+    preds, _, tr = om.decode(c, r, toks, len(toks), trace=True)
+    with pytest.raises(AssertionError):
+        gpf.check_against_stock_c3([tr[:, L] for L in range(m.dims.n_layers)], preds, c, r, g)
