@@ -103,9 +103,11 @@ typedef struct lxm_pf_params {
   const int64_t* emb_ptr;      /* (vocab + 1): the embedding rows */
   const lxm_pf_ent* emb_ent;   /* off = column, w = value */
   const int32_t* head_slice;   /* (LXM_PF_SLICES + 1): head row ranges, one per XCD */
-  const int64_t* head_ptr;     /* (vocab + 1): head rows (columns with nonzero final weight),
-                                  each padded to a multiple of 4 entries and to at least 4;
-                                  fewer than 2^31 entries in all */
+  const int32_t* head_more;    /* (vocab, 2): the head's rows (columns with nonzero final
+                                  weight): row r's first 4 entries at head_ent[4 r ..] (padded);
+                                  the rest of a longer row at head_ent[head_more[2 r] ..], a
+                                  multiple of 4 entries (padded), head_more[2 r + 1] of them
+                                  ((0, 0): none); fewer than 2^31 entries in all */
   const lxm_pf_ent* head_ent;  /* off = 16 x column; padding: off = 16 x hidden, w = 0 */
   const int32_t* tokens;       /* (T): the positions' token ids (embedding) */
   void* h;                     /* (ntiles, hidden, TT) model dtype: the residual stream */

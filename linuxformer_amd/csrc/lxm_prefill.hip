@@ -225,27 +225,27 @@ __device__ __forceinline__ v4f sum4z(v4f s, const lxm_pf_ent (&en)[4]) {
   for (int j = 0; j < 4; j++) s = acc4<BF>(s, xv[j], en[j].w);
   return s;
 }
-// a head row: its first entry's index, its length (a multiple of 4, at least 4), and its first
-// four entries
+// a head row: its first four entries (at 4 r: no row pointer to wait for), and where the rest
+// of a longer row sits (start, count: a multiple of 4; 0 for a row of at most four)
 struct HRow {
   uint32_t e0;
   int n;
   lxm_pf_ent g[4];
 };
-// row r's bounds and first four entries
-__device__ __forceinline__ void hrow_req(const int64_t* hptr, const lxm_pf_ent* hent, int r,
+__device__ __forceinline__ void hrow_req(const int32_t* hmore, const lxm_pf_ent* hent, int r,
                                          HRow& h) {
-  const int64_t e0 = gld(hptr + r), e1 = gld(hptr + r + 1);
-  h.e0 = (uint32_t)e0;
-  h.n = (int)(e1 - e0);
+  typedef int32_t v2i __attribute__((ext_vector_type(2)));
+  const v2i m = gld(reinterpret_cast<const v2i*>(hmore) + r);
+  h.e0 = (uint32_t)m.x;
+  h.n = m.y;
 #pragma unroll
-  for (int j = 0; j < 4; j++) h.g[j] = gld(hent + e0 + j);
+  for (int j = 0; j < 4; j++) h.g[j] = gld(hent + 4 * (uint32_t)r + j);
 }
 // the row's sums for the tile's four positions, entries in ascending order from +0
 template <bool BF>
 __device__ __forceinline__ v4f hrow_sum(const lxm_pf_ent* hent, const HRow& h) {
   v4f s = sum4z<BF>(v4f{0.0f, 0.0f, 0.0f, 0.0f}, h.g);
-  for (int k0 = 4; k0 < h.n; k0 += 4) {
+  for (int k0 = 0; k0 < h.n; k0 += 4) {
     lxm_pf_ent en[4];
 #pragma unroll
     for (int j = 0; j < 4; j++) en[j] = gld(hent + h.e0 + k0 + j);
@@ -990,7 +990,7 @@ __global__ __launch_bounds__(NT) void pf_head(const lxm_pf_params* __restrict__ 
   if (t == 0) reinterpret_cast<v4f*>(sm)[H] = v4f{0.0f, 0.0f, 0.0f, 0.0f};  // the padding's column
   __syncthreads();
   const int r0 = p.head_slice[slice], r1 = p.head_slice[slice + 1];
-  const int64_t* hptr = p.head_ptr;
+  const int32_t* hmore = p.head_more;
   const lxm_pf_ent* hent = p.head_ent;
   // each position's first strict maximum over the thread's rows: from -inf, so a row is taken
   // when it is above every earlier one; a thread whose rows are all -inf keeps its first row
@@ -1005,7 +1005,7 @@ __global__ __launch_bounds__(NT) void pf_head(const lxm_pf_params* __restrict__ 
   }
   for (int r = r0 + t; r < r1; r += NT) {
     HRow h;
-    hrow_req(hptr, hent, r, h);
+    hrow_req(hmore, hent, r, h);
     const v4f s = rd4<BF>(hrow_sum<BF>(hent, h));
 #pragma unroll
     for (int k = 0; k < TT; k++) {
@@ -1023,7 +1023,7 @@ __global__ __launch_bounds__(NT) void pf_head(const lxm_pf_params* __restrict__ 
   if (nan_any) {  // rare: the first NaN row of each position, which outranks every number
     for (int r = r0 + t; r < r1; r += NT) {
       HRow h;
-      hrow_req(hptr, hent, r, h);
+      hrow_req(hmore, hent, r, h);
       const v4f s = rd4<BF>(hrow_sum<BF>(hent, h));
 #pragma unroll
       for (int k = 0; k < TT; k++)

@@ -38,7 +38,7 @@ class PfParams(ctypes.Structure):
                                               "bf16", "T", "ntiles", "max_rec")] + \
         [("rms_eps", ctypes.c_float), ("pad0", ctypes.c_int32)] + \
         [(n, ctypes.c_void_p) for n in ("layers", "layers_host", "blob", "rec", "conv", "w1_final",
-                                        "emb_ptr", "emb_ent", "head_slice", "head_ptr", "head_ent",
+                                        "emb_ptr", "emb_ent", "head_slice", "head_more", "head_ent",
                                         "tokens", "h", "hn", "r1", "mask", "cand", "cmask", "count",
                                         "recs", "keys", "preds", "err")]
 
@@ -320,30 +320,38 @@ class PfBuffers:
 
 def head_table(er, w1f: np.ndarray, hidden: int):
     """The tied head's rows for pf_head: the embedding rows' entries at columns whose final-norm
-    factor (1 + weight) is nonzero, as (slices, row pointers, entries). Entries: off = 16 x
-    column, w = value; each row padded to a multiple of 4 entries, and to at least 4, by entries
-    of weight 0 at column hidden (the head kernel's zero column): a row's sum then takes its
-    entries four at a time with no test, its first four always its own (adding +0 to a sum from
-    +0 changes no bits: such a sum is never -0; an empty row's logit stays +0). Slices: row
-    ranges of about equal work (rows + entries), one per XCD."""
+    factor (1 + weight) is nonzero, as (slices, more, entries). Entries: off = 16 x column, w =
+    value. Row r's first four entries sit at 4 r (a row's place is its index: no row pointer to
+    wait for), padded by entries of weight 0 at column hidden (the head kernel's zero column);
+    the rest of a longer row, padded the same way to a multiple of 4, sits after the 4 x vocab
+    first entries at more[r] = (start, count), (0, 0) for a row of at most four. A row's sum
+    takes its entries four at a time with no test (adding +0 to a sum from +0 changes no bits:
+    such a sum is never -0; an empty row's logit stays +0). Slices: row ranges of about equal
+    work (rows + entries), one per XCD."""
     keep = w1f[er.cols] != 0
     rows = np.repeat(np.arange(er.n), np.diff(er.ptr))[keep]
+    cols, vals = er.cols[keep], er.vals[keep]
     cnt = np.bincount(rows, minlength=er.n)
-    plen = np.maximum(4, (cnt + 3) // 4 * 4)
-    hptr = np.zeros(er.n + 1, np.int64)
-    np.cumsum(plen, out=hptr[1:])
-    if int(hptr[-1]) + 4 >= 2**31:  # the head kernel reads the bounds' low 32-bit words
+    rank = np.arange(len(rows)) - np.repeat(np.cumsum(cnt) - cnt, cnt)  # entry's place in its row
+    extra = np.maximum(0, (cnt - 4 + 3) // 4 * 4)  # the rest of each row, padded
+    start = 4 * er.n + np.concatenate([[0], np.cumsum(extra)[:-1]]) if er.n else np.zeros(0, np.int64)
+    total = 4 * er.n + int(extra.sum())
+    if total + 4 >= 2**31:  # the head kernel indexes entries with 32-bit words
         raise ValueError("head table: more than 2^31 entries")
-    hent = np.zeros(int(hptr[-1]) + 4, ENT)
+    hent = np.zeros(total + 4, ENT)
     hent["off"][:] = 16 * hidden
-    pos = hptr[rows] + (np.arange(len(rows)) - np.repeat(np.cumsum(cnt) - cnt, cnt))
-    hent["off"][pos] = 16 * er.cols[keep]
-    hent["w"][pos] = er.vals[keep]
-    work = np.cumsum(np.diff(hptr) + 2)
+    first = rank < 4
+    pos = np.where(first, 4 * rows + rank, start[rows] + rank - 4)
+    hent["off"][pos] = 16 * cols
+    hent["w"][pos] = vals
+    more = np.zeros((er.n, 2), np.int32)
+    more[:, 0] = np.where(extra > 0, start, 0)
+    more[:, 1] = extra
+    work = np.cumsum(4 + extra + 2)
     tot = work[-1] if len(work) else 0
     sl = [0] + [int(np.searchsorted(work, tot * k / SLICES)) for k in range(1, SLICES)] + [er.n]
     sl = np.maximum.accumulate(np.asarray(sl, np.int64))
-    return sl, hptr, hent
+    return sl, more, hent
 
 
 class Prefill:
@@ -375,9 +383,9 @@ class Prefill:
         self.emb_ptr = torch.from_numpy(er.ptr.astype(np.int64)).to(self.dev)
         self.emb_ent = torch.from_numpy(ent.view(np.uint8)).to(self.dev)
         w1f = np.float32(1.0) + np.asarray(sm.norm, np.float32)
-        sl, hptr, hent = head_table(er, w1f, d.hidden)
+        sl, more, hent = head_table(er, w1f, d.hidden)
         self.head_slice = torch.from_numpy(sl.astype(np.int32)).to(self.dev)
-        self.head_ptr = torch.from_numpy(hptr).to(self.dev)
+        self.head_more = torch.from_numpy(more).to(self.dev)
         self.head_ent = torch.from_numpy(hent.view(np.uint8)).to(self.dev)
         self.w1_final = torch.from_numpy(w1f).to(self.dev)
         self._T = None
@@ -467,7 +475,7 @@ class Prefill:
                      conv=cs.data_ptr() if cs is not None else None,
                      w1_final=self.w1_final.data_ptr(), emb_ptr=self.emb_ptr.data_ptr(),
                      emb_ent=self.emb_ent.data_ptr(), head_slice=self.head_slice.data_ptr(),
-                     head_ptr=self.head_ptr.data_ptr(), head_ent=self.head_ent.data_ptr(),
+                     head_more=self.head_more.data_ptr(), head_ent=self.head_ent.data_ptr(),
                      **{n: getattr(buf, n).data_ptr() for n in PfBuffers.NAMES})
         pd = torch.frombuffer(bytearray(bytes(p)), dtype=torch.uint8).to(self.dev)
         return p, pd

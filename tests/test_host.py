@@ -352,8 +352,9 @@ def test_runner_refuses_more_tokens_than_the_dump_holds(tmp_path, native_lib):
 
 def test_prefill_head_table_rows():
     """pf_head's table (host only): each row holds its kept entries (columns whose final-norm
-    factor is nonzero) in column order, then zero-weight entries at column hidden up to a multiple
-    of 4 and at least 4 (an empty row too); the slices cover the rows in order."""
+    factor is nonzero) in column order, its first four at 4 x row and the rest of a longer row at
+    its (start, count), then zero-weight entries at column hidden up to a multiple of 4 and at
+    least 4 (an empty row too); the slices cover the rows in order."""
     from types import SimpleNamespace
     from linuxformer_amd import prefill
     hidden = 12
@@ -366,17 +367,19 @@ def test_prefill_head_table_rows():
     w1f = np.ones(hidden, np.float32)
     w1f[4] = 0.0  # a column the final norm zeroes: dropped from every row
     w1f[9] = 0.0
-    sl, hptr, hent = prefill.head_table(er, w1f, hidden)
-    assert hptr[0] == 0 and len(hptr) == len(rows) + 1
-    assert len(hent) == hptr[-1] + 4
+    sl, more, hent = prefill.head_table(er, w1f, hidden)
+    assert more.shape == (len(rows), 2)
+    n_all = 4 * len(rows) + int(more[:, 1].sum())
+    assert len(hent) == n_all + 4
     for i, r in enumerate(rows):
         kept = [(c, v) for c, v in r if w1f[c] != 0]
-        e = hent[hptr[i]:hptr[i + 1]]
-        n = len(e)
-        assert n >= 4 and n % 4 == 0 and n - len(kept) < 4 + (4 if not kept else 0)
+        s, n = int(more[i, 0]), int(more[i, 1])
+        e = np.concatenate([hent[4 * i:4 * i + 4], hent[s:s + n]])  # the row as the kernel reads it
+        assert n % 4 == 0 and (n == 0) == (len(kept) <= 4) and len(e) - len(kept) < 4 + (4 if not kept else 0)
+        assert n == 0 or s >= 4 * len(rows)
         assert [(int(o) // 16, float(w)) for o, w in e[:len(kept)]] == [(c, v) for c, v in kept]
         assert (e["off"][len(kept):] == 16 * hidden).all() and (e["w"][len(kept):] == 0).all()
-    assert (hent["off"][hptr[-1]:] == 16 * hidden).all() and (hent["w"][hptr[-1]:] == 0).all()
+    assert (hent["off"][n_all:] == 16 * hidden).all() and (hent["w"][n_all:] == 0).all()
     assert sl[0] == 0 and sl[-1] == len(rows) and (np.diff(sl) >= 0).all()
     assert len(sl) == prefill.SLICES + 1
 
