@@ -1003,17 +1003,26 @@ __global__ __launch_bounds__(NT) void pf_head(const lxm_pf_params* __restrict__ 
     best[k] = -__builtin_inff();
     bidx[k] = r0 + t;
   }
-  for (int r = r0 + t; r < r1; r += NT) {
-    HRow h;
-    hrow_req(hmore, hent, r, h);
-    const v4f s = rd4<BF>(hrow_sum<BF>(hent, h));
+  for (int r = r0 + t; r < r1; r += 2 * NT) {
+    // two rows a step (r and r + NT, each coalesced across the wave), their entries requested
+    // together; rows taken in ascending order (the first strict maximum)
+    const int r2 = r + NT < r1 ? r + NT : r;
+    HRow h1, h2;
+    hrow_req(hmore, hent, r, h1);
+    hrow_req(hmore, hent, r2, h2);
+    const v4f s1 = rd4<BF>(hrow_sum<BF>(hent, h1));
+    const v4f s2 = rd4<BF>(hrow_sum<BF>(hent, h2));
 #pragma unroll
     for (int k = 0; k < TT; k++) {
-      const float v = s[k];
-      nan_any |= v != v;
+      const float v = s1[k], w = s2[k];
+      nan_any |= (v != v) | (w != w);
       if (v > best[k]) {
         best[k] = v;
         bidx[k] = r;
+      }
+      if (w > best[k]) {
+        best[k] = w;
+        bidx[k] = r2;
       }
     }
   }
