@@ -511,6 +511,7 @@ def stress_leg(args, dev, hf_holder: dict) -> dict:
     us_tok = kern_ms * 1e3 / (n_tok / len(sizes))
     b_tok = survey_bytes_per_token(model, spec.p_gate)
     achieved = b_tok * (n_tok / len(sizes)) / (kern_ms * 1e-3) / 1e9
+    t_tok = measured_traffic(spec.name)
     out = {"metric": "greedy decode tok/s, config 5 (config 2's stack, 50 % of layer-steps gated)",
            "value": round(n_tok / wall, 1), "unit": "tok/s", "steps": len(sizes),
            "ms_per_step": round(wall * 1e3 / len(sizes), 3),
@@ -522,7 +523,8 @@ def stress_leg(args, dev, hf_holder: dict) -> dict:
            "redo": counted,
            "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS,
                         "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 5),
-                        "traffic": None, "bytes_per_token": round(b_tok),
+                        "traffic": None if t_tok is None else round(t_tok * n_tok / len(sizes)),
+                        "bytes_per_token": round(b_tok),
                         "kernel_ms_per_launch": round(kern_ms, 3)},
            "latency_roofline": latency_roofline(sync, ev_tok, us_tok),
            "chain_roofline": chain_roof,
