@@ -127,6 +127,19 @@ __device__ __forceinline__ v4f norm4(v4f h, v4f r, float w1) {
 __device__ __forceinline__ float norm_r(float ss, int H, float eps) {
   return rsqrt_(ss / (float)H + eps);
 }
+// The four positions' factors from their sums of squares (equal in every lane): lane k
+// evaluates position k & 3's, and every lane reads positions 0-3 back from lanes 0-3, so a wave
+// evaluates the IEEE divide and square root sequence once instead of four times. Every lane of
+// the wave must be active.
+__device__ __forceinline__ v4f norm_r4(v4f ss, int H, float eps) {
+  const int k = threadIdx.x & 3;
+  const float s = k == 0 ? ss.x : k == 1 ? ss.y : k == 2 ? ss.z : ss.w;
+  const int u = __float_as_int(norm_r(s, H, eps));
+  return v4f{__int_as_float(__builtin_amdgcn_readlane(u, 0)),
+             __int_as_float(__builtin_amdgcn_readlane(u, 1)),
+             __int_as_float(__builtin_amdgcn_readlane(u, 2)),
+             __int_as_float(__builtin_amdgcn_readlane(u, 3))};
+}
 
 // A sparse row's dot product with a column-major tile vector x in LDS (entry offsets 16 x
 // column), for the four positions at once: the terms in entry order from +0, each rounded once
@@ -359,8 +372,7 @@ __global__ __launch_bounds__(NT) void pf_tile(const lxm_pf_params* __restrict__ 
     const lxm_pf_ent* ent = tab<lxm_pf_ent>(p.blob, ly.ent);
     const float* entn = tab<float>(p.blob, ly.entn);
     const v4f ss = hsum<BF, BF>(HV, H, wsA, false);
-    const v4f r = {norm_r(ss.x, H, ly.eps), norm_r(ss.y, H, ly.eps), norm_r(ss.z, H, ly.eps),
-                   norm_r(ss.w, H, ly.eps)};
+    const v4f r = norm_r4(ss, H, ly.eps);
     // units over the post norm (formed as the entries gather): act = D(D(silu(D(gate . x))) *
     // D(up . x))
     const lxm_pf_unit* un = tab<lxm_pf_unit>(p.blob, ly.units);
@@ -395,8 +407,7 @@ __global__ __launch_bounds__(NT) void pf_tile(const lxm_pf_params* __restrict__ 
     const lxm_pf_ent* ent = tab<lxm_pf_ent>(p.blob, ly.ent);
     const float* entn = tab<float>(p.blob, ly.entn);
     const v4f ss = hsum<BF, BF>(HV, H, wsB, Lm >= 0);
-    const v4f r = {norm_r(ss.x, H, ly.eps), norm_r(ss.y, H, ly.eps), norm_r(ss.z, H, ly.eps),
-                   norm_r(ss.w, H, ly.eps)};
+    const v4f r = norm_r4(ss, H, ly.eps);
     if (t < TT && b * TT + t < p.T) p.r1[b * TT + t] = t == 0 ? r.x : t == 1 ? r.y : t == 2 ? r.z : r.w;
     // query/key projections of the live key heads' channels over the input norm (formed as the
     // entries gather): which slots are nonzero
@@ -430,8 +441,7 @@ __global__ __launch_bounds__(NT) void pf_tile(const lxm_pf_params* __restrict__ 
     if (t < TT && b * TT + t < p.T) p.mask[b * TT + t] = smask[t];
   } else if (Ln == -2) {
     const v4f ss = hsum<BF, BF>(HV, H, wsB, Lm >= 0);
-    const v4f r = {norm_r(ss.x, H, p.rms_eps), norm_r(ss.y, H, p.rms_eps),
-                   norm_r(ss.z, H, p.rms_eps), norm_r(ss.w, H, p.rms_eps)};
+    const v4f r = norm_r4(ss, H, p.rms_eps);
     float w[MAXH / NT];
 #pragma unroll
     for (int k = 0; k < MAXH / NT; k++) w[k] = t + k * NT < H ? p.w1_final[t + k * NT] : 0.0f;
