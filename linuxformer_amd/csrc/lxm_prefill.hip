@@ -328,9 +328,11 @@ __device__ __forceinline__ v4f hsum(uint8_t* HV, int H, v4f* wsum, bool plus0) {
 // at each position, and whether a decay can act (bit 31); or Ln == -2: the final norm into hn.
 // The norms' outputs are formed as the entries gather (each entry carries its column's norm
 // weight), so LDS holds 512 bytes of sums and masks, the residual (hidden columns) and the MLP
-// units' outputs, as tile vectors in the model dtype (bf16, hidden 3,572, 1,024 units: 37 KB,
-// four workgroups per CU), each followed by a column of zeros that the rows' padding entries
-// read (rows padded to multiples of 4 entries, summed with no per-entry test).
+// units' outputs, as tile vectors in the model dtype (bf16, hidden 3,572, 1,024 units: 37 KB),
+// each followed by a column of zeros that the rows' padding entries read (rows padded to
+// multiples of 4 entries, summed with no per-entry test). At most 64 VGPRs (eight waves per
+// SIMD): four workgroups per CU, as many as that LDS allows (69 VGPRs held three); each unit's
+// output goes to LDS as soon as it is formed, so no unit's result is held in registers.
 // A residual tile from HBM (model dtype) into LDS tile vectors (bf16 if HALF): every thread's
 // columns (t, t + 512, ...) loaded at once.
 template <bool BF, bool HALF>
@@ -347,7 +349,7 @@ __device__ __forceinline__ void load_tile(const void* h, int64_t b, int H, uint8
 template <bool BF>
 __host__ __device__ constexpr int x_xm(int H) { return X_HV + ((TV<BF>::B * (H + 1) + 15) & ~15); }
 template <bool BF>
-__global__ __launch_bounds__(NT) void pf_tile(const lxm_pf_params* __restrict__ pp, int Lm, int Ln) {
+__global__ __launch_bounds__(NT, 8) void pf_tile(const lxm_pf_params* __restrict__ pp, int Lm, int Ln) {
   extern __shared__ __align__(16) uint8_t sm[];
   using V = TV<BF>;
   const lxm_pf_params& p = *pp;
@@ -376,21 +378,13 @@ __global__ __launch_bounds__(NT) void pf_tile(const lxm_pf_params* __restrict__ 
     // units over the post norm (formed as the entries gather): act = D(D(silu(D(gate . x))) *
     // D(up . x))
     const lxm_pf_unit* un = tab<lxm_pf_unit>(p.blob, ly.units);
-    v4f a[LXM_PF_UPT];
-#pragma unroll
-    for (int i = 0; i < LXM_PF_UPT; i++) {
-      const int u = t + i * NT;
-      if (u < ly.n_units) {
-        const lxm_pf_unit q = gld(un + u);
-        const v4f g = rd4<BF>(dot4n<BF, BF, true>(ent + q.gs, entn + q.gs, q.gn, HV, r));
-        const v4f v = rd4<BF>(dot4n<BF, BF, true>(ent + q.us, entn + q.us, q.un, HV, r));
-        a[i] = v4f{rd<BF>(silu_rd<BF>(g.x) * v.x), rd<BF>(silu_rd<BF>(g.y) * v.y),
-                   rd<BF>(silu_rd<BF>(g.z) * v.z), rd<BF>(silu_rd<BF>(g.w) * v.w)};
-      }
+    for (int u = t; u < ly.n_units; u += NT) {
+      const lxm_pf_unit q = gld(un + u);
+      const v4f g = rd4<BF>(dot4n<BF, BF, true>(ent + q.gs, entn + q.gs, q.gn, HV, r));
+      const v4f v = rd4<BF>(dot4n<BF, BF, true>(ent + q.us, entn + q.us, q.un, HV, r));
+      V::put(XM, u, v4f{rd<BF>(silu_rd<BF>(g.x) * v.x), rd<BF>(silu_rd<BF>(g.y) * v.y),
+                        rd<BF>(silu_rd<BF>(g.z) * v.z), rd<BF>(silu_rd<BF>(g.w) * v.w)});
     }
-#pragma unroll
-    for (int i = 0; i < LXM_PF_UPT; i++)
-      if (t + i * NT < ly.n_units) V::put(XM, t + i * NT, a[i]);
     if (t == 0) V::put(XM, ly.n_units, v4f{0.0f, 0.0f, 0.0f, 0.0f});  // the down rows' zero column
     __syncthreads();
     // down_proj rows over the units (entries 16 x unit position), added to the residual
