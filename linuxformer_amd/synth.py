@@ -697,9 +697,12 @@ def to_sparse(dm: DenseModel) -> SparseModel:
         cols = np.asarray(cols, np.int64)
         rr = np.repeat(rows, len(cols))
         cc = np.tile(cols, len(rows))
-        order = np.lexsort((cc, rr))
-        return Coo(tuple(shape), rr[order], cc[order], np.asarray(mat, np.float32).reshape(-1)[order],
-                   blocks=64)
+        vals = np.asarray(mat, np.float32).reshape(-1)
+        # (row-major entries of ascending rows and columns are in (row, column) order already)
+        if not ((np.diff(rows) > 0).all() and (np.diff(cols) > 0).all()):
+            order = np.lexsort((cc, rr))
+            rr, cc, vals = rr[order], cc[order], vals[order]
+        return Coo(tuple(shape), rr, cc, vals, blocks=64)
 
     layers = []
     allH = np.arange(H)

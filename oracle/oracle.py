@@ -169,8 +169,11 @@ class OracleModel:
 
     def _csr(self, coo) -> Csr:
         rows = np.asarray(coo.rows, np.int64)
-        order = np.lexsort((coo.cols, rows))  # (dense matrices keep their explicit zeros)
-        rows, cols, vals = rows[order], np.asarray(coo.cols)[order], np.asarray(coo.vals)[order]
+        cols, vals = np.asarray(coo.cols), np.asarray(coo.vals)
+        dr, dc = np.diff(rows), np.diff(cols.astype(np.int64))
+        if not ((dr > 0) | ((dr == 0) & (dc > 0))).all():  # (already in (row, column) order: kept)
+            order = np.lexsort((cols, rows))  # (dense matrices keep their explicit zeros)
+            rows, cols, vals = rows[order], cols[order], vals[order]
         ptr = np.zeros(coo.shape[0] + 1, np.int64)
         np.cumsum(np.bincount(rows, minlength=coo.shape[0]), out=ptr[1:])
         blocks = int(getattr(coo, "blocks", 0))

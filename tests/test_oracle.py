@@ -231,6 +231,66 @@ def test_layer_step_matches_stock_decoder_layer(oracle_lib):
     assert np.abs(c - Cs).max() <= 1e-6 * np.abs(Cs).max()
 
 
+def _bf16_ulps(a: np.ndarray, b: np.ndarray) -> np.ndarray:
+    """|a - b| in bf16 units in the last place of the larger magnitude (8 significant bits)."""
+    m = np.maximum(np.abs(a), np.abs(b))
+    e = np.floor(np.log2(np.maximum(m, np.float32(1e-38))))
+    return np.abs(a.astype(np.float64) - b) / np.exp2(e - 7)
+
+
+def test_dense_layer_within_one_bf16_ulp_of_stock_at_config4_widths(oracle_lib):
+    """Config 4's dense order against the stock bf16 forward, one layer at config 4's full widths
+    (hidden 2560, 16 key heads of 256 dims with 128 live, 2 live of 8 value heads each, SwiGLU
+    9216) from identical inputs and a live state: transformers' Qwen3_5DecoderLayer on the host
+    (oneDNN's bf16 GEMV order) against the oracle's dense order (64 groups, pairwise tree). Each
+    dense row is the fp32 sum of the same exact bf16 products rounded once to bf16, so two
+    orders can differ only where that sum lies within the orders' fp32 spread of a bf16
+    rounding boundary: the residual output and the conv window agree to within one bf16 unit in
+    the last place everywhere and bit for bit on at least 99.9 % of their values, and the fp32
+    recurrent state bit for bit on at least 99.9 % and within 1e-6 of its largest value. (On
+    this seed: the residual and the state bit-equal, one conv value of 98,304 one unit apart.)
+    A mistake planted in the oracle's input (one out_proj weight dropped) is caught."""
+    from oracle import stock
+
+    torch.set_grad_enabled(False)
+    dm = synth.build_dense(synth.config4_mid(), "cpu")
+    sm = synth.to_sparse(dm)
+    hf = synth.dense_to_hf(dm)
+    conv0, rec0 = synth.dense_state(dm, seed=3)
+    rng = np.random.default_rng(5)
+    h = synth._round(rng.standard_normal(sm.dims.hidden).astype(np.float32) * 0.5, "bf16")
+    cache = stock.make_cache(hf, conv0, rec0)
+    out = hf.model.layers[0](torch.from_numpy(h)[None, None].to(torch.bfloat16),
+                             position_embeddings=None, attention_mask=None, position_ids=None,
+                             past_key_values=cache)
+    out = (out[0] if isinstance(out, tuple) else out)[0, 0].float().numpy()
+    R = cache.layers[0].recurrent_states[0][0].float().numpy()
+    Cs = cache.layers[0].conv_states[0][0].float().numpy()
+    del hf, cache, dm
+
+    def step(model):
+        hx, c, r = h.copy(), conv0[0].copy(), rec0[0].copy()
+        oracle_lib.OracleModel(model).layer_step(0, hx, c, r)
+        return hx, c, r
+
+    def agrees(hx, c, r):
+        return (_bf16_ulps(hx, out).max() <= 1.0 and (hx == out).mean() >= 0.999 and
+                _bf16_ulps(c, Cs).max() <= 1.0 and (c == Cs).mean() >= 0.999 and
+                (r == R).mean() >= 0.999 and np.abs(r - R).max() <= 1e-6 * np.abs(R).max())
+
+    hx, c, r = step(sm)
+    assert agrees(hx, c, r), (_bf16_ulps(hx, out).max(), (hx == out).mean(),
+                              _bf16_ulps(c, Cs).max(), (c == Cs).mean(), (r == R).mean())
+    op = sm.layers[0].out_proj
+    k = int(np.argmax(np.abs(op.vals)))
+    v = op.vals[k]
+    op.vals[k] = 0.0
+    try:
+        assert not agrees(*step(sm))
+    finally:
+        op.vals[k] = v
+
+
 def _rec_inputs(dtype, dense, chip, seed):
     rng = np.random.default_rng(seed)
     nk, nv = 16, 128
