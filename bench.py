@@ -1,10 +1,10 @@
 """Benchmark: greedy decode tok/s of the 37-layer synthetic sparse chip stack on one MI355X, and
-verified-prefill tok/s of the same stack (BASELINE's two metrics).
+verified-prefill tok/s of the same stack (the benchmark's two metrics).
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--chunk T] [--config c2]
                     [--legs decode,prefill,dense] [--cpu-seconds S] ...
 
-Decode (the headline `value`): the workload is one greedy chunk of T = 262,144 tokens (BASELINE
+Decode (the headline `value`): the workload is one greedy chunk of T = 262,144 tokens (benchmark
 config 2) from the config's start token and initial state, as lx/tools/mega_boot.py runs the
 boot in 262,144-token launches. A step is one launch of the persistent decode kernel over the
 next T/K tokens of that chunk (the sizes differ by at most one token and add up to T), each
@@ -16,12 +16,12 @@ hidden 3572, bf16, 0.08 % density, N(0,1) state), built and packed on the host; 
 resident in HBM before the timed region. Also reported: the same kernel on a forced stream of
 seeded uniform tokens (the greedy stream of this synthetic stack visits few distinct tokens).
 
-Verified prefill (`verified_prefill`): BASELINE config 3, calls of 65,536 seeded uniform tokens
+Verified prefill (`verified_prefill`): benchmark config 3, calls of 65,536 seeded uniform tokens
 through the same stack (synth.config3: 0.35 % of token-layers gated, 5 % of (key head, 64-token
 chunk) pairs active), each call embedding, running all 37 layers and taking every position's
 argmax (lx.fast's verified mode), timed with HIP events on the stream after two warm-up calls.
 
-Dense decode (`dense_decode`): BASELINE config 4, the dense padded text-view stack
+Dense decode (`dense_decode`): benchmark config 4, the dense padded text-view stack
 (synth.config4: 24 layers, hidden 2560, SwiGLU 9216); an 8,192-token prompt of seeded uniform ids
 (the batched prefill, then one step), then 4,096 greedy steps timed.
 
@@ -61,8 +61,8 @@ def split_chunk(total: int, steps: int) -> list:
     return [q + (1 if k < r else 0) for k in range(steps)]
 
 
-def survey_bytes_per_token(model, f_out: float) -> float:
-    """The algorithmic bytes of one decoded token, SURVEY 8(d)'s formula for config 2:
+def algorithmic_bytes_per_token(model, f_out: float) -> float:
+    """The algorithmic bytes of one decoded token of a sparse stack (config 2's formula):
     sum over layers of 4 B per nonzero of in_proj_qkv, b, a, gate, up, down, plus 4 B x the
     fraction of layer-steps with output x (in_proj_z + out_proj nonzeros), plus 16 B per live
     conv channel (window read + write), plus 4 B per head nonzero, plus the 2 B x hidden
@@ -349,7 +349,7 @@ def decode_leg(args, dev, hf_holder: dict) -> dict:
     us_tok = kern_ms * 1e3 / (chunk / len(sizes))
     lat = latency_roofline(sync, ev_tok, us_tok)
 
-    b_tok = survey_bytes_per_token(model, spec.p_gate)
+    b_tok = algorithmic_bytes_per_token(model, spec.p_gate)
     achieved = b_tok * (chunk / len(sizes)) / (kern_ms * 1e-3) / 1e9
     t_tok = measured_traffic(spec.name)
     out = {
@@ -447,7 +447,7 @@ def session_leg(args, dev, f, model, conv0, rec0, start: int, stream_preds) -> d
 
 
 def stress_leg(args, dev, hf_holder: dict) -> dict:
-    """config 2's stack with write gates on for half of the layer-steps, 65,536
+    """Benchmark config 5: config 2's stack with write gates on for half of the layer-steps, 65,536
     greedy tokens from the config's start token and initial state, as --c5-steps launches
     continuing one stream after one warm-up launch (the state restored after it). Reported next
     to config 2: tok/s, GDN events and MLP redos per token (the redo counts; lx/lx/mega.py:495-504
@@ -509,7 +509,7 @@ def stress_leg(args, dev, hf_holder: dict) -> dict:
     counted["stream_equal"] = counted.pop("preds") == preds[:n_c]
     sync = hf_holder.get("sync") or sync_costs(mg.ncta)
     us_tok = kern_ms * 1e3 / (n_tok / len(sizes))
-    b_tok = survey_bytes_per_token(model, spec.p_gate)
+    b_tok = algorithmic_bytes_per_token(model, spec.p_gate)
     achieved = b_tok * (n_tok / len(sizes)) / (kern_ms * 1e-3) / 1e9
     t_tok = measured_traffic(spec.name)
     out = {"metric": "greedy decode tok/s, config 5 (config 2's stack, 50 % of layer-steps gated)",
@@ -555,7 +555,7 @@ def stress_leg(args, dev, hf_holder: dict) -> dict:
 
 
 def plumbing_leg(args, dev) -> dict:
-    """the one chip-shaped fp32 layer, 256 greedy steps from the config's
+    """Benchmark config 1: the one chip-shaped fp32 layer, 256 greedy steps from the config's
     start token and zero state, one launch per run; --c1-runs timed runs from the same initial
     state (restored between them, untimed). Predictions and final states against the stock
     forward's run of the same steps (tests/golden/c1_256.npz, transformers' own modules); the
@@ -622,7 +622,7 @@ def _tf_version() -> str:
 
 
 def prefill_leg(args, dev, hf_holder: dict) -> dict:
-    """verified-mode calls of T seeded uniform tokens; tok/s over the timed
+    """Benchmark config 3: verified-mode calls of T seeded uniform tokens; tok/s over the timed
     calls (HIP events around each call on the current stream, inputs resident)."""
     import numpy as np
     import torch
@@ -705,7 +705,7 @@ def prefill_leg(args, dev, hf_holder: dict) -> dict:
             "value": round(n_cpu / dt, 2), "unit": "tok/s", "cores": cpu_threads(),
             "kind": "reference", "impl": "transformers-modules, torch eager",
             "sample": f"one call over the first {n_cpu} positions of the warm-up call's tokens "
-                      "(bounded: BASELINE.md's 4,096-position call would take many minutes): "
+                      "(bounded: a 4,096-position call would take many minutes): "
                       f"the stock forward's T > 1 path (transformers {_tf_version()} "
                       "Qwen3_5 layers, torch_chunk_gated_delta_rule, dense bf16, torch eager), "
                       f"{cpu_threads()} host threads"}
@@ -716,7 +716,7 @@ def prefill_leg(args, dev, hf_holder: dict) -> dict:
 
 def dense_cpu_stock(dm, toks, n_prompt: int, max_steps: int, budget_s: float) -> dict:
     """Config 4's CPU baseline: the stock forward (transformers' Qwen3_5 layers, torch eager,
-    bf16) on the padded model (synth.dense_to_hf) on the host cores, as BASELINE.md's plan asks: a
+    bf16) on the padded model (synth.dense_to_hf) on the host cores: a
     prompt through the stock T > 1 path, then greedy steps (one token at a time) until max_steps
     or budget_s of wall time. Returns the prompt's and the steps' rates and their sizes."""
     import numpy as np
@@ -739,7 +739,7 @@ def dense_cpu_stock(dm, toks, n_prompt: int, max_steps: int, budget_s: float) ->
 
 
 def dense_leg(args, dev) -> dict:
-    """the dense padded text-view stack; a prompt of n_prefill seeded uniform
+    """Benchmark config 4: the dense padded text-view stack; a prompt of n_prefill seeded uniform
     tokens from a zero state (batched: lxm_dn_prefill over all but the last, then one step;
     else n_prefill forced steps), then n_steps greedy steps, timed (HIP events on the stream)."""
     import numpy as np
@@ -890,7 +890,7 @@ def make_parser() -> argparse.ArgumentParser:
     ap.add_argument("--pf-calls", type=int, default=5)
     ap.add_argument("--pf-tokens", type=int, default=65_536)
     ap.add_argument("--pf-cpu-tokens", type=int, default=512,
-                    help="positions of config 3's CPU baseline call (BASELINE.md plans 4,096; the "
+                    help="positions of config 3's CPU baseline call (4,096 would be the full plan; the "
                          "stock T > 1 forward grows faster than linearly on the host: 512 "
                          "positions took 35 s and 1,024 took 147 s on 8 threads, so a bounded "
                          "sample is 512)")

@@ -1,4 +1,4 @@
-/* linuxformer on MI355X: greedy decode of the dense padded text-view stack,
+/* linuxformer on MI355X: greedy decode of the dense padded text-view stack (benchmark config 4),
  * C ABI.
  *
  * The dense counterpart of lxm_run for stacks whose projections are dense (lx/lx/merge.py:82-120

@@ -1,4 +1,4 @@
-// Greedy decode of the dense padded text-view stack on MI355X (gfx950).
+// Greedy decode of the dense padded text-view stack (benchmark config 4) on MI355X (gfx950).
 //
 // Per token: the embedding row; per layer the input norm, the projections (q, k, v, z, b, a of
 // the live blocks), the conv and the delta rule of each live value head with its gated norm,

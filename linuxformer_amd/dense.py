@@ -1,4 +1,4 @@
-"""Greedy decode of the dense padded text-view stack on the native dense
+"""Greedy decode of the dense padded text-view stack (benchmark config 4) on the native dense
 kernels (csrc/lxm_dense.hip, C ABI include/lxm_dense.h).
 
     dd = DenseDecode(model, cache)            # model: synth.DenseModel on the GPU

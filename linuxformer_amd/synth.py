@@ -131,7 +131,7 @@ class SparseModel:
 
 @dataclass
 class Spec:
-    """A synthetic stack: shapes, density, gates and seeds (2, 3 and 5)."""
+    """A synthetic stack: shapes, density, gates and seeds (benchmark configs 1, 2, 3 and 5)."""
     name: str
     dims: Dims
     seed: int = 0
@@ -155,7 +155,7 @@ class Spec:
 
 
 def config1(seed: int = 1) -> Spec:
-    """one chip-shaped GDN + SwiGLU layer, fp32, zero state, 4,096 tokens.
+    """Benchmark config 1: one chip-shaped GDN + SwiGLU layer, fp32, zero state, 4,096 tokens.
     A single layer at 0.08 % density barely mixes the residual stream, so a quarter of its
     layer-steps are gated on (the delta rule, its writes into the zero state and their reads)."""
     return Spec("c1", Dims(hidden=3572, n_layers=1, vocab=4096, dtype="fp32"), seed=seed,
@@ -163,14 +163,14 @@ def config1(seed: int = 1) -> Spec:
 
 
 def config2(seed: int = 2) -> Spec:
-    """the 37-layer synthetic chip stack, bf16, N(0,1) state; every token
-    gates exactly one layer (1/37 = 2.7 % of layer-steps, BASELINE's "about 2 %")."""
+    """Benchmark config 2: the 37-layer synthetic chip stack, bf16, N(0,1) state; every token
+    gates exactly one layer (1/37 = 2.7 % of layer-steps, the benchmark's "about 2 %")."""
     return Spec("c2", Dims(hidden=3572, n_layers=37, vocab=459_982, dtype="bf16"), seed=seed,
                 state="normal", n_steps=262_144, p_gate=1.0 / 37)
 
 
 def config3(seed: int = 2) -> Spec:
-    """verified mode (the prefill) over config 2's stack, 65,536 seeded
+    """Benchmark config 3: verified mode (the prefill) over config 2's stack, 65,536 seeded
     uniform token ids per call. A token gates a layer with probability 0.35 % (0.13 gates per
     token over the 37 layers), so a live key head (a quarter of them) is active in a 64-token
     chunk with probability 1 - (1 - 0.0035)^64 = 20 %: 5 % of (key head, chunk) pairs, as the
@@ -180,7 +180,7 @@ def config3(seed: int = 2) -> Spec:
 
 
 def config5(seed: int = 2) -> Spec:
-    """config 2's stack with gates on for half of the layer-steps."""
+    """Benchmark config 5: config 2's stack with gates on for half of the layer-steps."""
     s = config2(seed)
     return replace(s, name="c5", p_gate=0.5, n_steps=65_536)
 
@@ -546,7 +546,7 @@ def from_hf(m, n_chip: int | None = None, rows: slice | None = None) -> SparseMo
 
 
 # ---------------------------------------------------------------------------------------------
-# the dense padded text-view stack (lx/lx/merge.py:82-120's layout): key heads
+# Benchmark config 4: the dense padded text-view stack (lx/lx/merge.py:82-120's layout): key heads
 # of dim 256 whose upper 128 dims are zero, 8 value heads per key head of which 2 are live and 6
 # zero, bf16 N(0, 0.02) weights on the live blocks. Its projections are dense, so they are summed
 # in the dense order (64 groups of a row's entries, then a pairwise tree; the oracle's `blocks`).
@@ -577,7 +577,7 @@ class DenseSpec:
 
 
 def config4(seed: int = 4) -> DenseSpec:
-    """24 layers, hidden 2560, 16 key heads (256, zero-padded from 128), 128
+    """Benchmark config 4: 24 layers, hidden 2560, 16 key heads (256, zero-padded from 128), 128
     value heads (2 live + 6 zero per key head), SwiGLU 9216, gated-norm eps 5e-7, vocabulary
     248,320; an 8,192-token prefill of seeded uniform ids, then 4,096 greedy steps."""
     return DenseSpec("c4", hidden=2560, n_layers=24, seed=seed)

@@ -2,7 +2,7 @@
 
 Config 2: one 262,144-token greedy chunk of the 37-layer synthetic stack
 (linuxformer_amd.synth.config2); config 5 (--config c5): the same stack with half of the
-layer-steps gated, 65,536 greedy tokens (BASELINE config 5's run). Each starts from its config's
+layer-steps gated, 65,536 greedy tokens (benchmark config 5's run). Each starts from its config's
 start token and initial state and is decoded by the C oracle (oracle/lx_oracle.c, the stock
 decode restated). The fixture holds the sha256 of the prediction stream (int32, little-endian),
 of the final conv windows and of the final recurrent states (float32, the stacked (L, C, 4) and

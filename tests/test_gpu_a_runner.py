@@ -1,6 +1,6 @@
 """The C-only binding (csrc/lxm_runner.cpp): a packed decode replayed through liblxm.so's C ABI
-by a process with no Python, as a foreign host (C, cgo, JNI) would drive it (INTEGRATION.md's
-C host). Its stream must be the oracle's.
+by a process with no Python, as a foreign host (C, cgo, JNI) would drive it: dlopen, the
+parameter block filled from the dumped tables, lxm_run. Its stream must be the oracle's.
 
 The runner's cooperative launch is refused (hipErrorIllegalState, 401) while another process
 that has made cooperative launches holds the device, so the runner runs in a child of a process

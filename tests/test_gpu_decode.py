@@ -2,7 +2,7 @@
 
 Bit-exact: predictions, each step's input, every layer's residual after every step, the conv
 windows and the recurrent states (compared bit for bit). The oracle runs the same seeded inputs
-on the CPU; the configs are BASELINE's (config 1, 2, 5) and a small stack of the chip's head
+on the CPU; the configs are the benchmark's (config 1, 2, 5) and a small stack of the chip's head
 shapes. Full-size runs are checked by properties the decode must keep.
 """
 
@@ -167,7 +167,7 @@ def test_small_stack_fp32(cuda):
 
 
 def test_config1_greedy(cuda):
-    """256 greedy steps of one chip-shaped fp32 layer."""
+    """Benchmark config 1: 256 greedy steps of one chip-shaped fp32 layer."""
     check("c1", 256)
 
 
@@ -178,12 +178,12 @@ def test_config1_forced_inputs(cuda):
 
 
 def test_config2(cuda):
-    """BASELINE config 2 (37 layers, bf16, N(0,1) state): 20 steps, every layer's residual."""
+    """Benchmark config 2 (37 layers, bf16, N(0,1) state): 20 steps, every layer's residual."""
     check("c2", 20)
 
 
 def test_config5(cuda):
-    """BASELINE config 5 (half of the layer-steps gated): 8 steps."""
+    """Benchmark config 5 (half of the layer-steps gated): 8 steps."""
     check("c5", 8)
 
 
@@ -274,7 +274,7 @@ def test_config2_long_run_properties(cuda):
 
 @pytest.mark.parametrize("name,golden", [("c2", "c2_chunk.json"), ("c5", "c5_run.json")])
 def test_whole_run_equals_oracle(cuda, name, golden):
-    """BASELINE config 2's whole 262,144-token greedy chunk, and config 5's 65,536-token run
+    """Benchmark config 2's whole 262,144-token greedy chunk, and config 5's 65,536-token run
     (half of the layer-steps gated: long chains of GDN events and MLP redos), each from its start
     token and initial state, in four launches continuing one stream: the prediction stream and
     the final conv windows and recurrent states hash to what the CPU oracle's run of the same

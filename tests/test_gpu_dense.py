@@ -1,4 +1,4 @@
-"""Parity of the HIP dense decode (BASELINE config 4's structure) with the oracle on an MI355X,
+"""Parity of the HIP dense decode (benchmark config 4's structure) with the oracle on an MI355X,
 through the C ABI (the persistent run, lxm_dn_run, the per-step kernels, lxm_dn_step, and the
 batched prefill, lxm_dn_prefill, followed by steps): predictions and final states bit for bit. The dense projections are summed in
 the dense order the oracle restates for matrices marked dense (64 groups of a row's entries in

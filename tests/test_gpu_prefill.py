@@ -94,7 +94,7 @@ def test_prefill_small_fp32(cuda):
 
 
 def test_prefill_config1(cuda):
-    """BASELINE config 1's layer (fp32): 256 positions, a quarter of them gated."""
+    """Benchmark config 1's layer (fp32): 256 positions, a quarter of them gated."""
     check("c1", _toks("c1", 256))
 
 
@@ -206,7 +206,7 @@ def test_prefill_device_tokens_and_caches(cuda):
 
 
 def test_config3_full_matches_decode_kernel(cuda):
-    """BASELINE config 3 at full size: 65,536 uniform tokens through the 37-layer stack. The
+    """Benchmark config 3 at full size: 65,536 uniform tokens through the 37-layer stack. The
     prefill's predictions and final states equal those of the decode kernel forced through
     the same tokens (65,536 steps), bit for bit."""
     spec, m, c0, r0, f = model("c3")
