@@ -741,169 +741,157 @@ __global__ __launch_bounds__(256) void pf_tail(const lxm_pf_params* __restrict__
 // The recurrence of one value-head slot over the layer's candidates, in position order
 // (torch_recurrent_gated_delta_rule, TF:330-380, one token at a time): S <- S * exp(g) when
 // exp(g) != 1; with a live query or key kv = S^T k, delta = (v - kv) beta, S += k delta^T,
-// o = D(S^T q) into the record (over v, which this step has read). A slot's 128 state columns
-// are split over DQ workgroups of DW columns (no sum crosses columns, so each column's sums are
-// those of the whole tile, and a step's arithmetic is spread over DQ CUs; 8 and 16 workgroups
-// of 16 and 8 columns measured the same as 4). The state tile
-// stays in registers: thread (c, rb) holds column c0 + c of rows 16rb..16rb+15, one of ATen's
-// 16-row cascade blocks (torch .sum(-2) on the CPU).
-#define PF_DQ 4
-#define DQ PF_DQ
-#define DW (VD / DQ)
-#define NTD (16 * DW)
-static_assert(NTD >= KD || NTD * 2 == KD, "k and q: one or two per thread");
-// A candidate's inputs as one thread of the delta kernel holds them (loaded three candidates ahead):
-// the header word, the slot's decay factor, the thread's share of k and q, of the workgroup's DW
-// values of v (threads VT .. VT + DW - 1), and beta (thread 0).
-#define VT (NTD >= KD + DW ? KD : 0)
+// o = D(S^T q) into the record (over v, which this step has read). One wave per DCW = 4 of the
+// slot's 128 state columns (DWS = 32 one-wave workgroups a slot): lane 16 c + b holds column
+// c0 + c of rows 16b..16b+15 in registers, one of ATen's 16-row cascade blocks (torch .sum(-2)
+// on the CPU: each block from +0 in row order, the block sums from +0 in block order). Both of a
+// step's sums over the 16 blocks stay in the wave: each lane's block sum goes to the wave's row
+// of LDS and every lane of the column reads the column's 16 back and adds them in block order
+// (a wave's LDS accesses run in order, so no barrier). No sum crosses columns, so each column's
+// sums are those of the whole tile.
+#define DCW 4
+#define DWS (VD / DCW)
+// A candidate's inputs as one lane holds them (loaded three candidates ahead): the header word,
+// the slot's decay factor, the lane's 16 rows of k and q, its column's v, and beta.
 struct DeltaIn {
   uint32_t live;
-  float e, k, q, k2, q2, v, beta;
+  float e, v, beta;
+  v4f k[4], q[4];
 };
 __device__ __forceinline__ DeltaIn delta_in(const uint8_t* rec, const RecOff& ro, int vslot,
-                                            int kslot, int c0) {
-  const int t = threadIdx.x;
+                                            int kslot, int col, int b) {
   DeltaIn d;
   d.live = reinterpret_cast<const uint32_t*>(rec)[1];
   d.e = reinterpret_cast<const float*>(rec + ro.e)[vslot];
-  d.k = d.q = d.k2 = d.q2 = d.v = d.beta = 0.0f;
+  d.v = d.beta = 0.0f;
+#pragma unroll
+  for (int j = 0; j < 4; j++) d.k[j] = d.q[j] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
   if (kslot >= 0) {
-    const float* kk = reinterpret_cast<const float*>(rec + ro.k) + kslot * KD;
-    const float* qq = reinterpret_cast<const float*>(rec + ro.q) + kslot * KD;
-    if (t < KD) {
-      d.k = kk[t];
-      d.q = qq[t];
+    // (the record's k and q rows start at 16-byte multiples: 16 + 1024 x slot)
+    const v4f* kk = reinterpret_cast<const v4f*>(rec + ro.k + 4 * KD * kslot) + 4 * b;
+    const v4f* qq = reinterpret_cast<const v4f*>(rec + ro.q + 4 * KD * kslot) + 4 * b;
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+      d.k[j] = kk[j];
+      d.q[j] = qq[j];
     }
-    if (NTD < KD) {
-      d.k2 = kk[NTD + t];
-      d.q2 = qq[NTD + t];
-    }
-    if (t >= VT && t < VT + DW) d.v = reinterpret_cast<const float*>(rec + ro.v)[vslot * VD + c0 + t - VT];
-    if (t == 0) d.beta = reinterpret_cast<const float*>(rec + ro.b)[vslot];
+    d.v = reinterpret_cast<const float*>(rec + ro.v)[vslot * VD + col];
+    d.beta = reinterpret_cast<const float*>(rec + ro.b)[vslot];
   }
   return d;
 }
+// the 16 block sums of this lane's column, from +0 in block order (every lane of the column
+// gets the same sum)
+__device__ __forceinline__ float col_sum16(float* red, int c, int b, float x) {
+  red[16 * c + b] = x;
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+  const v4f* r = reinterpret_cast<const v4f*>(red + 16 * c);
+  const v4f w0 = r[0], w1 = r[1], w2 = r[2], w3 = r[3];
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+  float q = 0.0f;
+  q = q + w0.x; q = q + w0.y; q = q + w0.z; q = q + w0.w;
+  q = q + w1.x; q = q + w1.y; q = q + w1.z; q = q + w1.w;
+  q = q + w2.x; q = q + w2.y; q = q + w2.z; q = q + w2.w;
+  q = q + w3.x; q = q + w3.y; q = q + w3.z; q = q + w3.w;
+  return q;
+}
+
+// One candidate's step for one lane (see pf_delta). (Skipping the row offsets where no lane of
+// the wave has a nonzero factor, by a wave-uniform branch per row, measured slower: the branches
+// cost more than the rows they save.)
+template <bool BF>
+__device__ __forceinline__ void delta_step(const DeltaIn& cur, float (&s)[16], float* red, int c,
+                                           int b, int kslot, uint8_t* rec, const RecOff& ro,
+                                           int vslot, int col, bool first, bool& wrote) {
+  const bool live = kslot >= 0 && ((cur.live >> kslot) & 1u);
+  const float e = cur.e;
+  int proc = 0;
+  if (live || e != 1.0f) {
+    wrote = true;
+    if (e != 1.0f) {
+#pragma unroll
+      for (int i = 0; i < 16; i++) s[i] = s[i] * e;
+    }
+    proc = 1;
+    if (live) {
+      proc = 2;
+      float kr[16], qr[16];
+#pragma unroll
+      for (int i = 0; i < 16; i++) {
+        kr[i] = cur.k[i >> 2][i & 3];
+        qr[i] = cur.q[i >> 2][i & 3];
+      }
+      // the block's sum; a zero factor adds nothing (the oracle skips it; a sum from +0 is
+      // never -0)
+      float a = 0.0f;
+#pragma unroll
+      for (int i = 0; i < 16; i++) a = kr[i] != 0.0f ? a + s[i] * kr[i] : a;
+      const float kv = col_sum16(red, c, b, a);
+      const float d = (cur.v - kv) * cur.beta;
+      float o = 0.0f;
+#pragma unroll
+      for (int i = 0; i < 16; i++) {
+        // (the update keeps rows with a zero key factor exactly as they are: -0 stays -0)
+        s[i] = kr[i] != 0.0f ? s[i] + kr[i] * d : s[i];
+        o = qr[i] != 0.0f ? o + s[i] * qr[i] : o;
+      }
+      const float q = col_sum16(red, c, b, o);
+      // o goes into the record over v (read three candidates ago); the gated norm is pf_out's
+      if (b == 0) reinterpret_cast<float*>(rec + ro.v)[vslot * VD + col] = rd<BF>(q);
+    }
+  }
+  if (first) reinterpret_cast<int32_t*>(rec + ro.pr)[vslot] = proc;
+}
 
 template <bool BF>
-__global__ __launch_bounds__(NTD) void pf_delta(const lxm_pf_params* __restrict__ pp, int L) {
-  __shared__ __align__(16) float kn[KD], qn[KD], vb[DW], dl[DW];
-  __shared__ __align__(16) float bs[16 * DW], bo[16 * DW];  // the kv and the o block sums
-  __shared__ float beta_s;
+__global__ __launch_bounds__(64) void pf_delta(const lxm_pf_params* __restrict__ pp, int L) {
+  __shared__ __align__(16) float red[DCW * 16];
   const lxm_pf_params& p = *pp;
   const lxm_pf_layer& ly = p.layers[L];
-  const int t = threadIdx.x, vslot = blockIdx.x / DQ, c0 = (blockIdx.x % DQ) * DW;
+  const int lane = threadIdx.x, c = lane >> 4, b = lane & 15;
+  const int vslot = blockIdx.x / DWS, c0 = (blockIdx.x % DWS) * DCW;
   // everything the loop needs in registers: its stores to the records could alias p and ly
   const lxm_pf_vs sv = tab<lxm_pf_vs>(p.blob, ly.vs)[vslot];
   const RecOff ro(ly.n_ks, ly.n_vs);
   const int count = p.count[L];
   const int64_t rec_b = ly.rec_bytes;
   uint8_t* const recs = p.recs;
-  const int c = t % DW, rb = t / DW;
-  float* S = p.rec[L] + (size_t)sv.vh * KD * VD + c0 + c;
+  const int col = c0 + c, ks = sv.kslot;
+  const bool first = lane == 0 && c0 == 0;
+  float* S = p.rec[L] + (size_t)sv.vh * KD * VD + col;
   float s[16];
 #pragma unroll
-  for (int i = 0; i < 16; i++) s[i] = S[(rb * 16 + i) * VD];
+  for (int i = 0; i < 16; i++) s[i] = S[(16 * b + i) * VD];
   bool wrote = false;
-  // a live step's o block sums stay in bo until the next live step's first barrier (or the
-  // loop's end), where they are summed into the record they belong to: three barriers a step
-  float* o_rec = nullptr;
-  // the inputs of the next three candidates in flight
-  DeltaIn n1 = {}, n2 = {}, n3 = {};
-  if (count > 0) n1 = delta_in(recs, ro, vslot, sv.kslot, c0);
-  if (count > 1) n2 = delta_in(recs + rec_b, ro, vslot, sv.kslot, c0);
-  if (count > 2) n3 = delta_in(recs + 2 * rec_b, ro, vslot, sv.kslot, c0);
-  for (int j = 0; j < count; j++) {
+  // the inputs of the next three candidates in flight, in three fixed buffers (the loop taken
+  // three candidates a round, so none is copied)
+  DeltaIn n0 = {}, n1 = {}, n2 = {};
+  if (count > 0) n0 = delta_in(recs, ro, vslot, ks, col, b);
+  if (count > 1) n1 = delta_in(recs + rec_b, ro, vslot, ks, col, b);
+  if (count > 2) n2 = delta_in(recs + 2 * rec_b, ro, vslot, ks, col, b);
+  for (int j = 0; j < count; j += 3) {
     uint8_t* rec = recs + (int64_t)j * rec_b;
-    const DeltaIn cur = n1;
-    n1 = n2;
-    n2 = n3;
-    if (j + 3 < count) n3 = delta_in(rec + 3 * rec_b, ro, vslot, sv.kslot, c0);
-    const bool live = sv.kslot >= 0 && ((cur.live >> sv.kslot) & 1u);
-    const float e = cur.e;
-    int proc = 0;
-    if (live || e != 1.0f) {
-      wrote = true;
-      if (e != 1.0f) {
-#pragma unroll
-        for (int i = 0; i < 16; i++) s[i] = s[i] * e;
-      }
-      proc = 1;
-      if (live) {
-        proc = 2;
-        if (t < KD) {
-          kn[t] = cur.k;
-          qn[t] = cur.q;
-        }
-        if (NTD < KD) {
-          kn[NTD + t] = cur.k2;
-          qn[NTD + t] = cur.q2;
-        }
-        if (t >= VT && t < VT + DW) vb[t - VT] = cur.v;
-        if (t == 0) beta_s = cur.beta;
-        __syncthreads();
-        if (o_rec) {  // the previous live step's o = D(the block sums in order)
-          if (t < DW) {
-            float q = 0.0f;
-#pragma unroll
-            for (int b = 0; b < 16; b++) q = q + bo[b * DW + t];
-            o_rec[t] = rd<BF>(q);
-          }
-          o_rec = nullptr;
-        }
-        // the thread's 16 rows of k and q at once (one LDS wait), then the cascade blocks'
-        // sums; a zero factor adds nothing (the oracle skips it; a sum from +0 is never -0)
-        float kr[16], qr[16];
-#pragma unroll
-        for (int i = 0; i < 16; i++) {
-          kr[i] = kn[rb * 16 + i];
-          qr[i] = qn[rb * 16 + i];
-        }
-        float a = 0.0f;
-#pragma unroll
-        for (int i = 0; i < 16; i++) a = kr[i] != 0.0f ? a + s[i] * kr[i] : a;
-        bs[rb * DW + c] = a;
-        __syncthreads();
-        if (t < DW) {
-          float kv = 0.0f;
-#pragma unroll
-          for (int q = 0; q < 16; q++) kv = kv + bs[q * DW + t];
-          dl[t] = (vb[t] - kv) * beta_s;
-        }
-        __syncthreads();
-        const float d = dl[c];
-        float o = 0.0f;
-#pragma unroll
-        for (int i = 0; i < 16; i++) {
-          // (the update keeps rows with a zero key factor exactly as they are: -0 stays -0)
-          s[i] = kr[i] != 0.0f ? s[i] + kr[i] * d : s[i];
-          o = qr[i] != 0.0f ? o + s[i] * qr[i] : o;
-        }
-        // (the previous step's o sums read bo before this step's first barrier)
-        bo[rb * DW + c] = o;
-        // o goes into the record over v (read at this step's start); the gated norm is pf_out's
-        o_rec = reinterpret_cast<float*>(rec + ro.v) + vslot * VD + c0;
-      }
+    {
+      const DeltaIn cur = n0;
+      if (j + 3 < count) n0 = delta_in(rec + 3 * rec_b, ro, vslot, ks, col, b);
+      delta_step<BF>(cur, s, red, c, b, ks, rec, ro, vslot, col, first, wrote);
     }
-    if (t == 0 && c0 == 0) reinterpret_cast<int32_t*>(rec + ro.pr)[vslot] = proc;
-  }
-  if (o_rec) {
-    __syncthreads();
-    if (t < DW) {
-      float q = 0.0f;
-#pragma unroll
-      for (int b = 0; b < 16; b++) q = q + bo[b * DW + t];
-      o_rec[t] = rd<BF>(q);
+    if (j + 1 < count) {
+      const DeltaIn cur = n1;
+      if (j + 4 < count) n1 = delta_in(rec + 4 * rec_b, ro, vslot, ks, col, b);
+      delta_step<BF>(cur, s, red, c, b, ks, rec + rec_b, ro, vslot, col, first, wrote);
+    }
+    if (j + 2 < count) {
+      const DeltaIn cur = n2;
+      if (j + 5 < count) n2 = delta_in(rec + 5 * rec_b, ro, vslot, ks, col, b);
+      delta_step<BF>(cur, s, red, c, b, ks, rec + 2 * rec_b, ro, vslot, col, first, wrote);
     }
   }
   if (wrote) {
 #pragma unroll
-    for (int i = 0; i < 16; i++) S[(rb * 16 + i) * VD] = s[i];
+    for (int i = 0; i < 16; i++) S[(16 * b + i) * VD] = s[i];
   }
 }
-#undef DQ
-#undef DW
-#undef NTD
-#undef VT
 
 // ---------------------------------------------------------------------------------------------
 // The gated norm of each head that ran (TF:168-184): y = D(D(w * D(o * r)) * silu(z)), r =
@@ -1133,9 +1121,9 @@ static hipError_t run_layers(const lxm_pf_params* ph, const lxm_pf_params* pd, i
     hipLaunchKernelGGL(pf_compact, dim3(1), dim3(C_NT), 0, st, pd, L);
     hipLaunchKernelGGL(pf_act<BF>, dim3(ACT_GRID), dim3(NT), ACT_LDS, st, pd, L);
     hipLaunchKernelGGL(pf_tail<BF>, dim3((ph->n_conv + 255) / 256), dim3(256), 0, st, pd, L);
-    // (PF_DQ workgroups per value-head slot, 128 / PF_DQ state columns each)
+    // (DWS one-wave workgroups per value-head slot, DCW state columns each)
     if (ly.n_vs > 0)
-      hipLaunchKernelGGL(pf_delta<BF>, dim3(PF_DQ * ly.n_vs), dim3(16 * VD / PF_DQ), 0, st, pd, L);
+      hipLaunchKernelGGL(pf_delta<BF>, dim3(DWS * ly.n_vs), dim3(64), 0, st, pd, L);
     if (ly.n_vs > 0)
       hipLaunchKernelGGL(pf_out<BF>, dim3(OUT_GRID), dim3(NT), 4 * VD * ly.n_vs + 16, st, pd, L);
   }
