@@ -752,31 +752,32 @@ __global__ __launch_bounds__(256) void pf_tail(const lxm_pf_params* __restrict__
 #define DCW 4
 #define DWS (VD / DCW)
 // A candidate's inputs as one lane holds them (loaded three candidates ahead): the header word,
-// the slot's decay factor, the lane's 16 rows of k and q, its column's v, and beta.
+// the slot's decay factor, its column's v, beta, and an eighth of the slot's k and q (lanes
+// 0-31 k, 32-63 q, 8 values each), which the step stages in the wave's LDS for every lane.
 struct DeltaIn {
   uint32_t live;
   float e, v, beta;
-  v4f k[4], q[4];
+  v4f kq[2];
 };
 __device__ __forceinline__ DeltaIn delta_in(const uint8_t* rec, const RecOff& ro, int vslot,
                                             int kslot, int col, int b) {
+  // (global loads: a generic pointer's flat loads would also count against the LDS counter, and
+  // every LDS wait of a step would then wait for the candidates in flight)
+  const GAS uint8_t* g = (const GAS uint8_t*)rec;
   DeltaIn d;
-  d.live = reinterpret_cast<const uint32_t*>(rec)[1];
-  d.e = reinterpret_cast<const float*>(rec + ro.e)[vslot];
+  d.live = ((const GAS uint32_t*)g)[1];
+  d.e = ((const GAS float*)(g + ro.e))[vslot];
   d.v = d.beta = 0.0f;
-#pragma unroll
-  for (int j = 0; j < 4; j++) d.k[j] = d.q[j] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+  d.kq[0] = d.kq[1] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
   if (kslot >= 0) {
     // (the record's k and q rows start at 16-byte multiples: 16 + 1024 x slot)
-    const v4f* kk = reinterpret_cast<const v4f*>(rec + ro.k + 4 * KD * kslot) + 4 * b;
-    const v4f* qq = reinterpret_cast<const v4f*>(rec + ro.q + 4 * KD * kslot) + 4 * b;
-#pragma unroll
-    for (int j = 0; j < 4; j++) {
-      d.k[j] = kk[j];
-      d.q[j] = qq[j];
-    }
-    d.v = reinterpret_cast<const float*>(rec + ro.v)[vslot * VD + col];
-    d.beta = reinterpret_cast<const float*>(rec + ro.b)[vslot];
+    const int lane = threadIdx.x;
+    const GAS v4f* kq = (const GAS v4f*)(g + (lane < 32 ? ro.k : ro.q) + 4 * KD * kslot) +
+                        2 * (lane & 31);
+    d.kq[0] = kq[0];
+    d.kq[1] = kq[1];
+    d.v = ((const GAS float*)(g + ro.v))[vslot * VD + col];
+    d.beta = ((const GAS float*)(g + ro.b))[vslot];
   }
   return d;
 }
@@ -800,9 +801,10 @@ __device__ __forceinline__ float col_sum16(float* red, int c, int b, float x) {
 // the wave has a nonzero factor, by a wave-uniform branch per row, measured slower: the branches
 // cost more than the rows they save.)
 template <bool BF>
-__device__ __forceinline__ void delta_step(const DeltaIn& cur, float (&s)[16], float* red, int c,
-                                           int b, int kslot, uint8_t* rec, const RecOff& ro,
-                                           int vslot, int col, bool first, bool& wrote) {
+__device__ __forceinline__ void delta_step(const DeltaIn& cur, float (&s)[16], float* red,
+                                           float* kqs, int c, int b, int kslot, uint8_t* rec,
+                                           const RecOff& ro, int vslot, int col, bool first,
+                                           bool& wrote) {
   const bool live = kslot >= 0 && ((cur.live >> kslot) & 1u);
   const float e = cur.e;
   int proc = 0;
@@ -815,12 +817,19 @@ __device__ __forceinline__ void delta_step(const DeltaIn& cur, float (&s)[16], f
     proc = 1;
     if (live) {
       proc = 2;
+      // k and q through the wave's LDS (lane l wrote values 8l..8l+7 of k, then of q)
+      v4f* kq4 = reinterpret_cast<v4f*>(kqs);
+      kq4[2 * threadIdx.x] = cur.kq[0];
+      kq4[2 * threadIdx.x + 1] = cur.kq[1];
+      __atomic_signal_fence(__ATOMIC_SEQ_CST);
       float kr[16], qr[16];
 #pragma unroll
-      for (int i = 0; i < 16; i++) {
-        kr[i] = cur.k[i >> 2][i & 3];
-        qr[i] = cur.q[i >> 2][i & 3];
+      for (int j = 0; j < 4; j++) {
+        const v4f kv4 = kq4[4 * b + j], qv4 = kq4[64 + 4 * b + j];
+        kr[4 * j] = kv4.x; kr[4 * j + 1] = kv4.y; kr[4 * j + 2] = kv4.z; kr[4 * j + 3] = kv4.w;
+        qr[4 * j] = qv4.x; qr[4 * j + 1] = qv4.y; qr[4 * j + 2] = qv4.z; qr[4 * j + 3] = qv4.w;
       }
+      __atomic_signal_fence(__ATOMIC_SEQ_CST);
       // the block's sum; a zero factor adds nothing (the oracle skips it; a sum from +0 is
       // never -0)
       float a = 0.0f;
@@ -837,15 +846,16 @@ __device__ __forceinline__ void delta_step(const DeltaIn& cur, float (&s)[16], f
       }
       const float q = col_sum16(red, c, b, o);
       // o goes into the record over v (read three candidates ago); the gated norm is pf_out's
-      if (b == 0) reinterpret_cast<float*>(rec + ro.v)[vslot * VD + col] = rd<BF>(q);
+      if (b == 0) ((GAS float*)((GAS uint8_t*)rec + ro.v))[vslot * VD + col] = rd<BF>(q);
     }
   }
-  if (first) reinterpret_cast<int32_t*>(rec + ro.pr)[vslot] = proc;
+  if (first) ((GAS int32_t*)((GAS uint8_t*)rec + ro.pr))[vslot] = proc;
 }
 
 template <bool BF>
 __global__ __launch_bounds__(64) void pf_delta(const lxm_pf_params* __restrict__ pp, int L) {
   __shared__ __align__(16) float red[DCW * 16];
+  __shared__ __align__(16) float kqs[2 * KD];  // a live step's k and q
   const lxm_pf_params& p = *pp;
   const lxm_pf_layer& ly = p.layers[L];
   const int lane = threadIdx.x, c = lane >> 4, b = lane & 15;
@@ -874,17 +884,17 @@ __global__ __launch_bounds__(64) void pf_delta(const lxm_pf_params* __restrict__
     {
       const DeltaIn cur = n0;
       if (j + 3 < count) n0 = delta_in(rec + 3 * rec_b, ro, vslot, ks, col, b);
-      delta_step<BF>(cur, s, red, c, b, ks, rec, ro, vslot, col, first, wrote);
+      delta_step<BF>(cur, s, red, kqs, c, b, ks, rec, ro, vslot, col, first, wrote);
     }
     if (j + 1 < count) {
       const DeltaIn cur = n1;
       if (j + 4 < count) n1 = delta_in(rec + 4 * rec_b, ro, vslot, ks, col, b);
-      delta_step<BF>(cur, s, red, c, b, ks, rec + rec_b, ro, vslot, col, first, wrote);
+      delta_step<BF>(cur, s, red, kqs, c, b, ks, rec + rec_b, ro, vslot, col, first, wrote);
     }
     if (j + 2 < count) {
       const DeltaIn cur = n2;
       if (j + 5 < count) n2 = delta_in(rec + 5 * rec_b, ro, vslot, ks, col, b);
-      delta_step<BF>(cur, s, red, c, b, ks, rec + 2 * rec_b, ro, vslot, col, first, wrote);
+      delta_step<BF>(cur, s, red, kqs, c, b, ks, rec + 2 * rec_b, ro, vslot, col, first, wrote);
     }
   }
   if (wrote) {
