@@ -93,7 +93,8 @@ typedef struct lxm_pf_params {
   int32_t T, ntiles;           /* positions; tiles = ceil(T / LXM_PF_TT) */
   int32_t max_rec;             /* bytes of the largest layer's record */
   float rms_eps;
-  int32_t pad0;
+  int32_t head_long;           /* 1: some head row has more than 4 entries (head_more is read); 0:
+                                  none (head_more is not read) */
   const lxm_pf_layer* layers;  /* device, n_layers */
   const lxm_pf_layer* layers_host; /* the same in host memory (the launcher's counts) */
   const uint8_t* blob;         /* device */

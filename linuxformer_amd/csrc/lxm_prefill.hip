@@ -245,12 +245,18 @@ struct HRow {
   int n;
   lxm_pf_ent g[4];
 };
+// (LONG false: no row of the table has more than four entries, and head_more is not read)
+template <bool LONG>
 __device__ __forceinline__ void hrow_req(const int32_t* hmore, const lxm_pf_ent* hent, int r,
                                          HRow& h) {
   typedef int32_t v2i __attribute__((ext_vector_type(2)));
-  const v2i m = gld(reinterpret_cast<const v2i*>(hmore) + r);
-  h.e0 = (uint32_t)m.x;
-  h.n = m.y;
+  h.e0 = 0;
+  h.n = 0;
+  if constexpr (LONG) {
+    const v2i m = gld(reinterpret_cast<const v2i*>(hmore) + r);
+    h.e0 = (uint32_t)m.x;
+    h.n = m.y;
+  }
 #pragma unroll
   for (int j = 0; j < 4; j++) h.g[j] = gld(hent + 4 * (uint32_t)r + j);
 }
@@ -389,9 +395,18 @@ __global__ __launch_bounds__(NT, 8) void pf_tile(const lxm_pf_params* __restrict
     __syncthreads();
     // down_proj rows over the units (entries 16 x unit position), added to the residual
     const lxm_pf_drow* dr = tab<lxm_pf_drow>(p.blob, ly.drows);
+    // (a row of one entry: its padding entries read the zero column with weight 0 and add +0 to
+    // a sum that is never -0, so the sum is its one term; the rows come longest first, so a
+    // wave's rows take one path or the other except at one boundary)
     for (int i = t; i < ly.n_drows; i += NT) {
       const lxm_pf_drow d = gld(dr + i);
-      const v4f s = rd4<BF>(dot4<BF, BF, true>(ent + d.start, d.len, XM));
+      v4f s;
+      if (d.len == 1) {
+        const lxm_pf_ent e = gld(ent + d.start);
+        s = rd4<BF>(acc4<BF>(v4f{0.0f, 0.0f, 0.0f, 0.0f}, V::at(XM, e.off), e.w));
+      } else {
+        s = rd4<BF>(dot4<BF, BF, true>(ent + d.start, d.len, XM));
+      }
       V::put(HV, d.row, rd4<BF>(V::get(HV, d.row) + s));
     }
     __syncthreads();
@@ -976,22 +991,10 @@ __device__ __forceinline__ unsigned long long wave_kmax(unsigned long long k) {
   for (int off = 32; off >= 1; off >>= 1) k = kmax(k, __shfl_xor(k, off));
   return k;
 }
-template <bool BF>
-__global__ __launch_bounds__(NT) void pf_head(const lxm_pf_params* __restrict__ pp) {
-  extern __shared__ __align__(16) uint8_t sm[];
-  const lxm_pf_params& p = *pp;
-  const int t = threadIdx.x, H = p.hidden;
-  const int slice = blockIdx.x % LXM_PF_SLICES;
-  const int64_t b = blockIdx.x / LXM_PF_SLICES;
-  // the tile's columns are read at LDS address 16 x column (sum4z): the tile must start at 0
-  if ((uint32_t)(size_t)(const __attribute__((address_space(3))) uint8_t*)sm != 0u) {
-    if (t == 0) *p.err = 2;
-    return;
-  }
-  load_tile<BF, false>(p.hn, b, H, sm);
-  if (t == 0) reinterpret_cast<v4f*>(sm)[H] = v4f{0.0f, 0.0f, 0.0f, 0.0f};  // the padding's column
-  __syncthreads();
-  const int r0 = p.head_slice[slice], r1 = p.head_slice[slice + 1];
+// The head's scan over rows r0..r1 of a slice for the tile at LDS address 0 (pf_head)
+template <bool BF, bool LONG>
+__device__ __forceinline__ void head_scan(const lxm_pf_params& p, int64_t b, int r0, int r1) {
+  const int t = threadIdx.x;
   const int32_t* hmore = p.head_more;
   const lxm_pf_ent* hent = p.head_ent;
   // each position's first strict maximum over the thread's rows: from -inf, so a row is taken
@@ -1010,8 +1013,8 @@ __global__ __launch_bounds__(NT) void pf_head(const lxm_pf_params* __restrict__ 
     // together; rows taken in ascending order (the first strict maximum)
     const int r2 = r + NT < r1 ? r + NT : r;
     HRow h1, h2;
-    hrow_req(hmore, hent, r, h1);
-    hrow_req(hmore, hent, r2, h2);
+    hrow_req<LONG>(hmore, hent, r, h1);
+    hrow_req<LONG>(hmore, hent, r2, h2);
     const v4f s1 = rd4<BF>(hrow_sum<BF>(hent, h1));
     const v4f s2 = rd4<BF>(hrow_sum<BF>(hent, h2));
 #pragma unroll
@@ -1034,7 +1037,7 @@ __global__ __launch_bounds__(NT) void pf_head(const lxm_pf_params* __restrict__ 
   if (nan_any) {  // rare: the first NaN row of each position, which outranks every number
     for (int r = r0 + t; r < r1; r += NT) {
       HRow h;
-      hrow_req(hmore, hent, r, h);
+      hrow_req<LONG>(hmore, hent, r, h);
       const v4f s = rd4<BF>(hrow_sum<BF>(hent, h));
 #pragma unroll
       for (int k = 0; k < TT; k++)
@@ -1046,6 +1049,26 @@ __global__ __launch_bounds__(NT) void pf_head(const lxm_pf_params* __restrict__ 
     const unsigned long long w = wave_kmax(key[k]);
     if ((t & 63) == 0 && b * TT + k < p.T && w != 0ull) atomicMax(p.keys + b * TT + k, w);
   }
+}
+
+template <bool BF>
+__global__ __launch_bounds__(NT) void pf_head(const lxm_pf_params* __restrict__ pp) {
+  extern __shared__ __align__(16) uint8_t sm[];
+  const lxm_pf_params& p = *pp;
+  const int t = threadIdx.x, H = p.hidden;
+  const int slice = blockIdx.x % LXM_PF_SLICES;
+  const int64_t b = blockIdx.x / LXM_PF_SLICES;
+  // the tile's columns are read at LDS address 16 x column (sum4z): the tile must start at 0
+  if ((uint32_t)(size_t)(const __attribute__((address_space(3))) uint8_t*)sm != 0u) {
+    if (t == 0) *p.err = 2;
+    return;
+  }
+  load_tile<BF, false>(p.hn, b, H, sm);
+  if (t == 0) reinterpret_cast<v4f*>(sm)[H] = v4f{0.0f, 0.0f, 0.0f, 0.0f};  // the padding's column
+  __syncthreads();
+  const int r0 = p.head_slice[slice], r1 = p.head_slice[slice + 1];
+  if (p.head_long) head_scan<BF, true>(p, b, r0, r1);
+  else head_scan<BF, false>(p, b, r0, r1);
 }
 
 __global__ void pf_fill_keys(const lxm_pf_params* __restrict__ pp) {

@@ -36,7 +36,7 @@ class PfLayer(ctypes.Structure):
 class PfParams(ctypes.Structure):
     _fields_ = [(n, ctypes.c_int32) for n in ("hidden", "n_layers", "nk", "nv", "n_conv", "vocab",
                                               "bf16", "T", "ntiles", "max_rec")] + \
-        [("rms_eps", ctypes.c_float), ("pad0", ctypes.c_int32)] + \
+        [("rms_eps", ctypes.c_float), ("head_long", ctypes.c_int32)] + \
         [(n, ctypes.c_void_p) for n in ("layers", "layers_host", "blob", "rec", "conv", "w1_final",
                                         "emb_ptr", "emb_ent", "head_slice", "head_more", "head_ent",
                                         "tokens", "h", "hn", "r1", "mask", "cand", "cmask", "count",
@@ -386,6 +386,7 @@ class Prefill:
         sl, more, hent = head_table(er, w1f, d.hidden)
         self.head_slice = torch.from_numpy(sl.astype(np.int32)).to(self.dev)
         self.head_more = torch.from_numpy(more).to(self.dev)
+        self.head_long = int((more[:, 1] > 0).any())  # (else the head kernel reads no head_more)
         self.head_ent = torch.from_numpy(hent.view(np.uint8)).to(self.dev)
         self.w1_final = torch.from_numpy(w1f).to(self.dev)
         self._T = None
@@ -467,7 +468,7 @@ class Prefill:
         d = self.dims
         p = PfParams(hidden=d.hidden, n_layers=d.n_layers, nk=d.nk, nv=d.nv, n_conv=d.n_conv,
                      vocab=self.vocab, bf16=int(self.bf), T=T, ntiles=(T + TT - 1) // TT,
-                     max_rec=self.max_rec, rms_eps=d.rms_eps,
+                     max_rec=self.max_rec, rms_eps=d.rms_eps, head_long=self.head_long,
                      layers=self.layers_d.data_ptr(),
                      layers_host=ctypes.cast(self.layers_h, ctypes.c_void_p).value,
                      blob=self.blob.data_ptr(),
