@@ -1008,26 +1008,30 @@ __device__ __forceinline__ void head_scan(const lxm_pf_params& p, int64_t b, int
     best[k] = -__builtin_inff();
     bidx[k] = r0 + t;
   }
-  for (int r = r0 + t; r < r1; r += 2 * NT) {
-    // two rows a step (r and r + NT, each coalesced across the wave), their entries requested
-    // together; rows taken in ascending order (the first strict maximum)
-    const int r2 = r + NT < r1 ? r + NT : r;
-    HRow h1, h2;
-    hrow_req<LONG>(hmore, hent, r, h1);
-    hrow_req<LONG>(hmore, hent, r2, h2);
-    const v4f s1 = rd4<BF>(hrow_sum<BF>(hent, h1));
-    const v4f s2 = rd4<BF>(hrow_sum<BF>(hent, h2));
+  for (int r = r0 + t; r < r1; r += 4 * NT) {
+    // four rows a step (r, r + NT, r + 2 NT, r + 3 NT, each coalesced across the wave), their
+    // entries requested together; rows taken in ascending order (the first strict maximum); a
+    // row past the slice is r again, which adds nothing (not above itself)
+    int rr[4];
+    HRow h[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      rr[i] = r + i * NT < r1 ? r + i * NT : r;
+      hrow_req<LONG>(hmore, hent, rr[i], h[i]);
+    }
+    v4f sv[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) sv[i] = rd4<BF>(hrow_sum<BF>(hent, h[i]));
 #pragma unroll
     for (int k = 0; k < TT; k++) {
-      const float v = s1[k], w = s2[k];
-      nan_any |= (v != v) | (w != w);
-      if (v > best[k]) {
-        best[k] = v;
-        bidx[k] = r;
-      }
-      if (w > best[k]) {
-        best[k] = w;
-        bidx[k] = r2;
+#pragma unroll
+      for (int i = 0; i < 4; i++) {
+        const float v = sv[i][k];
+        nan_any |= v != v;
+        if (v > best[k]) {
+          best[k] = v;
+          bidx[k] = rr[i];
+        }
       }
     }
   }
