@@ -874,7 +874,11 @@ __global__ __launch_bounds__(64) void pf_delta(const lxm_pf_params* __restrict__
   const lxm_pf_params& p = *pp;
   const lxm_pf_layer& ly = p.layers[L];
   const int lane = threadIdx.x, c = lane >> 4, b = lane & 15;
-  const int vslot = blockIdx.x / DWS, c0 = (blockIdx.x % DWS) * DCW;
+  // a slot's DWS workgroups on one XCD (workgroups are dealt to the 8 XCDs in turn): the slot's
+  // records are then fetched into one L2, and its columns' outputs merge in it
+  const int xcd = blockIdx.x & 7, jx = blockIdx.x >> 3;
+  const int vslot = xcd + 8 * (jx / DWS), c0 = (jx % DWS) * DCW;
+  if (vslot >= ly.n_vs) return;
   // everything the loop needs in registers: its stores to the records could alias p and ly
   const lxm_pf_vs sv = tab<lxm_pf_vs>(p.blob, ly.vs)[vslot];
   const RecOff ro(ly.n_ks, ly.n_vs);
@@ -1158,9 +1162,9 @@ static hipError_t run_layers(const lxm_pf_params* ph, const lxm_pf_params* pd, i
     hipLaunchKernelGGL(pf_compact, dim3(1), dim3(C_NT), 0, st, pd, L);
     hipLaunchKernelGGL(pf_act<BF>, dim3(ACT_GRID), dim3(NT), ACT_LDS, st, pd, L);
     hipLaunchKernelGGL(pf_tail<BF>, dim3((ph->n_conv + 255) / 256), dim3(256), 0, st, pd, L);
-    // (DWS one-wave workgroups per value-head slot, DCW state columns each)
+    // (DWS one-wave workgroups per value-head slot, DCW state columns each, a slot's on one XCD)
     if (ly.n_vs > 0)
-      hipLaunchKernelGGL(pf_delta<BF>, dim3(DWS * ly.n_vs), dim3(64), 0, st, pd, L);
+      hipLaunchKernelGGL(pf_delta<BF>, dim3(8 * DWS * ((ly.n_vs + 7) / 8)), dim3(64), 0, st, pd, L);
     if (ly.n_vs > 0)
       hipLaunchKernelGGL(pf_out<BF>, dim3(OUT_GRID), dim3(NT), 4 * VD * ly.n_vs + 16, st, pd, L);
   }
