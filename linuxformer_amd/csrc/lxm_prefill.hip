@@ -766,6 +766,7 @@ __global__ __launch_bounds__(256) void pf_tail(const lxm_pf_params* __restrict__
 // sums are those of the whole tile.
 #define DCW 4
 #define DWS (VD / DCW)
+#define KQ_Q (20 * KD / 16)  // the q half of a wave's k and q staging
 // A candidate's inputs as one lane holds them (loaded three candidates ahead): the header word,
 // the slot's decay factor, its column's v, beta, and an eighth of the slot's k and q (lanes
 // 0-31 k, 32-63 q, 8 values each), which the step stages in the wave's LDS for every lane.
@@ -832,15 +833,22 @@ __device__ __forceinline__ void delta_step(const DeltaIn& cur, float (&s)[16], f
     proc = 1;
     if (live) {
       proc = 2;
-      // k and q through the wave's LDS (lane l wrote values 8l..8l+7 of k, then of q)
-      v4f* kq4 = reinterpret_cast<v4f*>(kqs);
-      kq4[2 * threadIdx.x] = cur.kq[0];
-      kq4[2 * threadIdx.x + 1] = cur.kq[1];
+      // k and q through the wave's LDS: value v of k at 20 (v / 16) + v % 16, of q at KQ_Q plus
+      // the same (rows of 16 values 80 bytes apart, so the 16 rows a pass of 16 lanes reads lie
+      // on distinct bank groups; 64 bytes apart they shared four)
+      {
+        const int v0 = 8 * (threadIdx.x & 31);
+        v4f* dst = reinterpret_cast<v4f*>(kqs + (threadIdx.x < 32 ? 0 : KQ_Q) + 20 * (v0 >> 4) +
+                                          (v0 & 15));
+        dst[0] = cur.kq[0];
+        dst[1] = cur.kq[1];
+      }
       __atomic_signal_fence(__ATOMIC_SEQ_CST);
+      const v4f* kq4 = reinterpret_cast<const v4f*>(kqs + 20 * b);
       float kr[16], qr[16];
 #pragma unroll
       for (int j = 0; j < 4; j++) {
-        const v4f kv4 = kq4[4 * b + j], qv4 = kq4[64 + 4 * b + j];
+        const v4f kv4 = kq4[j], qv4 = kq4[KQ_Q / 4 + j];
         kr[4 * j] = kv4.x; kr[4 * j + 1] = kv4.y; kr[4 * j + 2] = kv4.z; kr[4 * j + 3] = kv4.w;
         qr[4 * j] = qv4.x; qr[4 * j + 1] = qv4.y; qr[4 * j + 2] = qv4.z; qr[4 * j + 3] = qv4.w;
       }
@@ -870,7 +878,7 @@ __device__ __forceinline__ void delta_step(const DeltaIn& cur, float (&s)[16], f
 template <bool BF>
 __global__ __launch_bounds__(64) void pf_delta(const lxm_pf_params* __restrict__ pp, int L) {
   __shared__ __align__(16) float red[DCW * 16];
-  __shared__ __align__(16) float kqs[2 * KD];  // a live step's k and q
+  __shared__ __align__(16) float kqs[2 * KQ_Q];  // a live step's k and q (rows of 20)
   const lxm_pf_params& p = *pp;
   const lxm_pf_layer& ly = p.layers[L];
   const int lane = threadIdx.x, c = lane >> 4, b = lane & 15;
