@@ -484,7 +484,22 @@ __device__ __forceinline__ float w1_one(const uint8_t* tab, int c) {
     return GLOBAL ? gp(reinterpret_cast<const float*>(tab))[c] : reinterpret_cast<const float*>(tab)[c];
   }
 }
-// the ring value at byte offset off of a float vector (agent-scope load)
+// The ring word holding the value at byte offset off of a ring row that is the same for every
+// lane of the wave (its base is taken from the first active lane), by an agent-scope buffer load
+// (sc1 policy), and the value from that word. The loads of a group of entries are all issued
+// before any value is taken from its word.
+template <bool BF>
+__device__ __forceinline__ uint32_t ring_word(const float* hs, int off) {
+  const __amdgpu_buffer_rsrc_t r =
+      __builtin_amdgcn_make_buffer_rsrc(wave_ptr(const_cast<float*>(hs)), 0, 0x7fffffff, 0x00020000);
+  return __builtin_amdgcn_raw_buffer_load_b32(r, BF ? (off >> 3) * 4 : off, 0, 16);
+}
+template <bool BF>
+__device__ __forceinline__ float ring_of(uint32_t w, int off) {
+  if constexpr (BF) return __uint_as_float((off & 4) ? (w & 0xffff0000u) : (w << 16));
+  else return __uint_as_float(w);
+}
+// the ring value at byte offset off of a ring row of this lane's own (agent-scope load)
 template <bool BF>
 __device__ __forceinline__ float ring_val(const float* hs, int off) {
   if constexpr (BF) {
@@ -496,8 +511,10 @@ __device__ __forceinline__ float ring_val(const float* hs, int off) {
 }
 // A row's dot product (entries in global memory, chunk's rules) with the GDN norm's output of
 // a step, formed per entry from the ring: x[c] = D((h[c] * r) * (1 + w_in[c])), h by agent-
-// scope loads. Only the columns the row names are read.
-template <bool BF, bool E4>
+// scope loads. Only the columns the row names are read. UNI: the ring row hs is the same for
+// every lane of the wave (a group's loads are then issued together); otherwise each lane reads
+// its own.
+template <bool BF, bool E4, bool UNI>
 __device__ __forceinline__ float rdot(const uint8_t* ent, int64_t start, int n, const float* hs,
                                       float r, const uint8_t* w1in) {
   float s = 0.0f;
@@ -509,10 +526,21 @@ __device__ __forceinline__ float rdot(const uint8_t* ent, int64_t start, int n, 
       Ent<E4>::gat(ent, start + k0 + j, i[j], w[j]);
       i[j] &= OFF_MASK;
     }
+    if constexpr (UNI) {
+      uint32_t u[4];
 #pragma unroll
-    for (int j = 0; j < 4; j++) {
-      hv[j] = ring_val<BF>(hs, i[j]);
-      wi[j] = w1_one<E4, true>(w1in, i[j] >> 2);
+      for (int j = 0; j < 4; j++) {
+        u[j] = ring_word<BF>(hs, i[j]);
+        wi[j] = w1_one<E4, true>(w1in, i[j] >> 2);
+      }
+#pragma unroll
+      for (int j = 0; j < 4; j++) hv[j] = ring_of<BF>(u[j], i[j]);
+    } else {
+#pragma unroll
+      for (int j = 0; j < 4; j++) {
+        hv[j] = ring_val<BF>(hs, i[j]);
+        wi[j] = w1_one<E4, true>(w1in, i[j] >> 2);
+      }
     }
     // (a slot past the row may name a column past the weights: its term is dropped, not
     // weighted by 0)
@@ -522,9 +550,9 @@ __device__ __forceinline__ float rdot(const uint8_t* ent, int64_t start, int n, 
   return s;
 }
 // rdot over up to four steps' inputs at once, for a conv channel's window: window k (on[k], the
-// same across the thread's calls) reads ring hs[k] with norm factor r[k]. Each sum keeps rdot's
-// order; the entries and norm weights are read once, and every window's ring values are
-// requested together (only for the windows that are on).
+// same across the thread's calls) reads ring hs[k] with norm factor r[k], each row the same for
+// every lane of the wave. Each sum keeps rdot's order; the entries and norm weights are read
+// once, and all four windows' ring words of a group of entries are requested together.
 template <bool BF, bool E4>
 __device__ __forceinline__ void rdot4(const uint8_t* ent, int64_t start, int n,
                                       const float* const (&hs)[4], const float (&r)[4],
@@ -540,16 +568,17 @@ __device__ __forceinline__ void rdot4(const uint8_t* ent, int64_t start, int n,
       i[j] &= OFF_MASK;
       wi[j] = w1_one<E4, true>(w1in, i[j] >> 2);
     }
+    // (every window's words are requested, on or not: the rows are in bounds for any step, and
+    // one wait then covers the group)
+    uint32_t u[4][4];
 #pragma unroll
-    for (int k = 0; k < 4; k++) {
-      if (on[k]) {
+    for (int k = 0; k < 4; k++)
 #pragma unroll
-        for (int j = 0; j < 4; j++) hv[k][j] = ring_val<BF>(hs[k], i[j]);
-      } else {
+      for (int j = 0; j < 4; j++) u[k][j] = ring_word<BF>(hs[k], i[j]);
 #pragma unroll
-        for (int j = 0; j < 4; j++) hv[k][j] = 0.0f;
-      }
-    }
+    for (int k = 0; k < 4; k++)
+#pragma unroll
+      for (int j = 0; j < 4; j++) hv[k][j] = on[k] ? ring_of<BF>(u[k][j], i[j]) : 0.0f;
 #pragma unroll
     for (int k = 0; k < 4; k++)
 #pragma unroll
@@ -1668,10 +1697,10 @@ __device__ void gdn_head(const lxm_params& p, int L, int step, int vh, bool out,
       // windows, rather than on the output's path)
       // (and the gated norm's weight into LDS: not a global load on the output's path)
       const float w = gp(reinterpret_cast<const float*>(p.blob + ly.gnorm))[j];
-      zb[j] = silu(rd<BF>(rdot<BF, E4>(p.blob + ly.z_ent, zr.start, zr.len, h0, r0, w1in)));
+      zb[j] = silu(rd<BF>(rdot<BF, E4, true>(p.blob + ly.z_ent, zr.start, zr.len, h0, r0, w1in)));
       gwl[j] = w;
     } else if (t == 2 * VD) {
-      const float b = rd<BF>(rdot<BF, E4>(p.blob + ly.b_ent, br.start, br.len, h0, r0, w1in));
+      const float b = rd<BF>(rdot<BF, E4, true>(p.blob + ly.b_ent, br.start, br.len, h0, r0, w1in));
       misc[2] = (int)__float_as_uint(rd<BF>(sigmoid(b)));
     }
   }
@@ -2044,8 +2073,9 @@ __device__ void write_windows(const lxm_params& p) {
       const int s = n - 4 + k;
       if (s >= 0) {
         // the channel's projection of step s's GDN norm output, formed per entry from the ring
+        // (the lanes of a wave can hold two layers' channels: each reads its own layer's row)
         const uint8_t* w1in = p.blob + ly.w1_in;
-        w[k] = rd<BF>(rdot<BF, E4>(p.blob + ly.qkv_ent, ch.start, ch.len, ring_at(p, s, L),
+        w[k] = rd<BF>(rdot<BF, E4, false>(p.blob + ly.qkv_ent, ch.start, ch.len, ring_at(p, s, L),
                                    ld_rlxf(rr_at(p, s, L)), w1in));
       } else {
         w[k] = conv_at<BF>(cs, (int64_t)c * 4 + 4 + s);
