@@ -1715,12 +1715,28 @@ __device__ void gdn_head(const lxm_params& p, int L, int step, int vh, bool out,
   {
     const int cg = t & 31, rb = t >> 5;
     GAS v4f* S4 = gp(reinterpret_cast<v4f*>(recL + (size_t)vh * KD * VD));
+    // (the block's rows with a nonzero key factor and with a nonzero query factor, as masks
+    // from 16-byte LDS reads, so that the rows' loads are issued back to back and the loops
+    // below branch on registers; each loop reads its factors four at a time)
+    const v4f* kn4 = reinterpret_cast<const v4f*>(kn + rb * 16);
+    const v4f* qn4 = reinterpret_cast<const v4f*>(qn + rb * 16);
+    uint32_t km = 0, qm = 0;
+#pragma unroll
+    for (int q = 0; q < 4; q++) {
+      const v4f a = kn4[q], b = qn4[q];
+#pragma unroll
+      for (int c = 0; c < 4; c++) {
+        km |= (uint32_t)(a[c] != 0.0f) << (4 * q + c);
+        qm |= (uint32_t)(b[c] != 0.0f) << (4 * q + c);
+      }
+    }
+    const uint32_t need = dec ? 0xffffu : (km | qm);
     v4f s[16];
 #pragma unroll
     for (int i = 0; i < 16; i++) {
       const int r = rb * 16 + i;
       s[i] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
-      if (dec || kn[r] != 0.0f || qn[r] != 0.0f) s[i] = S4[r * (VD / 4) + cg];
+      if ((need >> i) & 1) s[i] = S4[r * (VD / 4) + cg];
     }
     if (dec) {
 #pragma unroll
@@ -1733,10 +1749,13 @@ __device__ void gdn_head(const lxm_params& p, int L, int step, int vh, bool out,
     }
     if (nk > 0) {
       v4f a = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+      v4f kf[4];
+#pragma unroll
+      for (int q = 0; q < 4; q++) kf[q] = kn4[q];
 #pragma unroll
       for (int i = 0; i < 16; i++) {
-        const float f = kn[rb * 16 + i];
-        if (f != 0.0f) {
+        const float f = kf[i >> 2][i & 3];
+        if ((km >> i) & 1) {
           a.x = a.x + s[i].x * f;
           a.y = a.y + s[i].y * f;
           a.z = a.z + s[i].z * f;
@@ -1754,9 +1773,11 @@ __device__ void gdn_head(const lxm_params& p, int L, int step, int vh, bool out,
       __syncthreads();
       const v4f d = reinterpret_cast<const v4f*>(dl)[cg];
 #pragma unroll
+      for (int q = 0; q < 4; q++) kf[q] = kn4[q];
+#pragma unroll
       for (int i = 0; i < 16; i++) {
-        const float f = kn[rb * 16 + i];
-        if (f != 0.0f) {
+        const float f = kf[i >> 2][i & 3];
+        if ((km >> i) & 1) {
           s[i].x = s[i].x + f * d.x;
           s[i].y = s[i].y + f * d.y;
           s[i].z = s[i].z + f * d.z;
@@ -1767,10 +1788,13 @@ __device__ void gdn_head(const lxm_params& p, int L, int step, int vh, bool out,
     GH_MARK(2);
     if (nq > 0) {
       v4f a = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+      v4f qf[4];
+#pragma unroll
+      for (int q = 0; q < 4; q++) qf[q] = qn4[q];
 #pragma unroll
       for (int i = 0; i < 16; i++) {
-        const float f = qn[rb * 16 + i];
-        if (f != 0.0f) {
+        const float f = qf[i >> 2][i & 3];
+        if ((qm >> i) & 1) {
           a.x = a.x + s[i].x * f;
           a.y = a.y + s[i].y * f;
           a.z = a.z + s[i].z * f;
@@ -1817,10 +1841,11 @@ __device__ void gdn_head(const lxm_params& p, int L, int step, int vh, bool out,
     // the state's written rows (each thread stores the blocks it alone reads at the next step,
     // so its own later loads see them; a drain before the head's completion stamp covers them
     // where the chain waits for the states)
+    const uint32_t wrote = dec ? 0xffffu : km;
 #pragma unroll
     for (int i = 0; i < 16; i++) {
       const int r = rb * 16 + i;
-      if (dec || kn[r] != 0.0f) S4[r * (VD / 4) + cg] = s[i];
+      if ((wrote >> i) & 1) S4[r * (VD / 4) + cg] = s[i];
     }
   }
   GH_MARK(3);
