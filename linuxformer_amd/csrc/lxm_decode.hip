@@ -568,13 +568,21 @@ __device__ __forceinline__ void rdot4(const uint8_t* ent, int64_t start, int n,
       i[j] &= OFF_MASK;
       wi[j] = w1_one<E4, true>(w1in, i[j] >> 2);
     }
-    // (every window's words are requested, on or not: the rows are in bounds for any step, and
-    // one wait then covers the group)
+    // (an earlier window's words only where it is on; no word is looked at before all are
+    // requested, so one wait covers the group)
     uint32_t u[4][4];
 #pragma unroll
     for (int k = 0; k < 4; k++)
 #pragma unroll
-      for (int j = 0; j < 4; j++) u[k][j] = ring_word<BF>(hs[k], i[j]);
+      for (int j = 0; j < 4; j++) u[k][j] = 0u;
+#pragma unroll
+    for (int k = 0; k < 3; k++)
+      if (on[k]) {
+#pragma unroll
+        for (int j = 0; j < 4; j++) u[k][j] = ring_word<BF>(hs[k], i[j]);
+      }
+#pragma unroll
+    for (int j = 0; j < 4; j++) u[3][j] = ring_word<BF>(hs[3], i[j]);
 #pragma unroll
     for (int k = 0; k < 4; k++)
 #pragma unroll
