@@ -82,7 +82,6 @@ static_assert(L_H + 4 * MAXH <= 65536, "gathered vectors below 64 KB");
 #define F_OUT 1
 #define F_OK 4
 #define F_TOK 8
-#define F_STOP 12
 #define F_KH 16
 #define F_KEYW 192  // 8 uint64: the head keys' wave maxima (key heads: nk <= F_KEYW - F_KH)
 static_assert((L_FLAGS + 4 * F_KEYW) % 8 == 0 && F_KEYW + 16 <= 256, "the key words in the flags");
@@ -204,30 +203,32 @@ __device__ bool spin_ne(const uint32_t* p, uint32_t last, uint32_t* out, int32_t
   }
 }
 
-// The workgroup waits until every thread t < n sees the word base[32 t] equal to want, reading
-// all of them in each poll (one round trip for the lot); thread 0 watches the error word and the
-// time limit. All threads call; all return the same: false on an error or a timeout. stop: an
-// int in the caller's LDS.
-__device__ bool wait_stamps(const uint32_t* base, int n, uint32_t want, int32_t* err, int code,
-                            int* stop) {
+// The workgroup waits until every thread t < n sees the word base[32 t] equal to want. Each wave
+// holding a word spins on its own (one request of its words and of the error word a poll, its
+// own time limit), with no barrier between polls; the workgroup meets once, at the end. All
+// threads call; all return the same: false on an error or a timeout.
+__device__ bool wait_stamps(const uint32_t* base, int n, uint32_t want, int32_t* err, int code) {
   const int t = threadIdx.x;
-  const uint64_t t0 = wall();
-  for (;;) {
-    const uint32_t v = t < n ? ld_rlx(base + 32 * t) : want;
-    int32_t e = 0;
-    if (t == 0) {
-      e = __hip_atomic_load(gp(err), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      if (!e && wall() - t0 > TIMEOUT_TICKS) {
-        __hip_atomic_fetch_max(gp(err), code, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        e = code;
+  int bad = 0;
+  if (t - (t & 63) < n) {
+    const uint64_t t0 = wall();
+    for (;;) {
+      const uint32_t v = ld_rlx(base + 32 * (t < n ? t : 0));
+      const int32_t e = __hip_atomic_load(gp(err), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if (e != 0) {
+        bad = 1;
+        break;
       }
-      *stop = e != 0;
+      if (__all(t >= n || v == want)) break;
+      if (wall() - t0 > TIMEOUT_TICKS) {
+        __hip_atomic_fetch_max(gp(err), code, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        bad = 1;
+        break;
+      }
+      __builtin_amdgcn_s_sleep(1);
     }
-    const int all = __syncthreads_and(v == want);
-    if (*stop) return false;
-    if (all) return true;
-    __builtin_amdgcn_s_sleep(1);
   }
+  return __syncthreads_or(bad) == 0;
 }
 
 // Stamped words (8 bytes: a 32-bit value low, the GDN event's sequence number high), written
@@ -241,41 +242,39 @@ __device__ __forceinline__ void st64_rlx(unsigned long long* p, uint32_t stamp, 
                      __HIP_MEMORY_SCOPE_AGENT);
 }
 // Every thread's words base[idx[i]] (idx[i] < 0: none): waits until all the workgroup's words
-// carry the stamp want; v[i] their values (0 for none). False on an error or a timeout (code).
+// carry the stamp want; v[i] their values (0 for none). Each wave spins on its own words as
+// wait_stamps does. False on an error or a timeout (code).
 template <int N>
 __device__ bool wait_words(const unsigned long long* base, const int (&idx)[N], uint32_t want,
-                           int32_t* err, int code, int* stop, float (&v)[N]) {
-  const int t = threadIdx.x;
+                           int32_t* err, int code, float (&v)[N]) {
   const uint64_t t0 = wall();
-  bool mine = false;
-#pragma unroll
-  for (int i = 0; i < N; i++) v[i] = 0.0f;
+  int bad = 0;
   for (;;) {
-    if (!mine) {
-      bool ok = true;
+    // (every word is requested, a thread without one reading word 0, and the error word beside
+    // them, before any is looked at)
+    uint64_t w[N];
 #pragma unroll
-      for (int i = 0; i < N; i++) {
-        if (idx[i] >= 0) {
-          const uint64_t w = ld64_rlx(base + idx[i]);
-          v[i] = __uint_as_float((uint32_t)w);
-          ok = ok && (uint32_t)(w >> 32) == want;
-        }
-      }
-      mine = ok;
+    for (int i = 0; i < N; i++) w[i] = ld64_rlx(base + (idx[i] >= 0 ? idx[i] : 0));
+    const int32_t e = __hip_atomic_load(gp(err), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    bool mine = true;
+#pragma unroll
+    for (int i = 0; i < N; i++) {
+      v[i] = idx[i] >= 0 ? __uint_as_float((uint32_t)w[i]) : 0.0f;
+      mine = mine & ((idx[i] < 0) | ((uint32_t)(w[i] >> 32) == want));
     }
-    if (t == 0) {
-      int32_t e = __hip_atomic_load(gp(err), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      if (!e && wall() - t0 > TIMEOUT_TICKS) {
-        __hip_atomic_fetch_max(gp(err), code, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        e = code;
-      }
-      *stop = e != 0;
+    if (e != 0) {
+      bad = 1;
+      break;
     }
-    const int all = __syncthreads_and(mine);
-    if (*stop) return false;
-    if (all) return true;
+    if (__all(mine)) break;
+    if (wall() - t0 > TIMEOUT_TICKS) {
+      __hip_atomic_fetch_max(gp(err), code, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      bad = 1;
+      break;
+    }
     __builtin_amdgcn_s_sleep(1);
   }
+  return __syncthreads_or(bad) == 0;
 }
 
 // The same for the head's keys: helper b = 1 .. n stores at S_KEY + 32 b a uint64 whose low 13
@@ -283,31 +282,33 @@ __device__ bool wait_words(const unsigned long long* base, const int (&idx)[N], 
 // key (every valid key carries the same stamp, so the maximum is the maximum of the keys
 // themselves). Returns false on an error or a timeout; *best: the maximum.
 __device__ bool wait_keys(const uint32_t* sync, int n, uint32_t stamp, int32_t* err, int code,
-                          int* stop, unsigned long long* wk, unsigned long long* best) {
+                          unsigned long long* wk, unsigned long long* best) {
   const int t = threadIdx.x;
-  const uint64_t t0 = wall();
+  const bool has = t >= 1 && t <= n;
   unsigned long long k = 0;
-  for (;;) {
-    bool ok = true;
-    if (t >= 1 && t <= n) {
-      k = __hip_atomic_load(gp(reinterpret_cast<const unsigned long long*>(sync + S_KEY + 32 * t)),
-                            __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      ok = (uint32_t)(k & KEY_STAMP) == stamp;
-    }
-    int32_t e = 0;
-    if (t == 0) {
-      e = __hip_atomic_load(gp(err), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      if (!e && wall() - t0 > TIMEOUT_TICKS) {
-        __hip_atomic_fetch_max(gp(err), code, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        e = code;
+  int bad = 0;
+  if (t - (t & 63) <= n) {  // the waves holding a key spin on their own, as wait_stamps's do
+    const uint64_t t0 = wall();
+    for (;;) {
+      const unsigned long long k0 = __hip_atomic_load(
+          gp(reinterpret_cast<const unsigned long long*>(sync + S_KEY + 32 * (has ? t : 1))),
+          __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      const int32_t e = __hip_atomic_load(gp(err), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      k = has ? k0 : 0ull;
+      if (e != 0) {
+        bad = 1;
+        break;
       }
-      *stop = e != 0;
+      if (__all(!has || (uint32_t)(k & KEY_STAMP) == stamp)) break;
+      if (wall() - t0 > TIMEOUT_TICKS) {
+        __hip_atomic_fetch_max(gp(err), code, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        bad = 1;
+        break;
+      }
+      __builtin_amdgcn_s_sleep(1);
     }
-    const int all = __syncthreads_and(ok);
-    if (*stop) return false;
-    if (all) break;
-    __builtin_amdgcn_s_sleep(1);
   }
+  if (__syncthreads_or(bad)) return false;
   for (int off = 32; off >= 1; off >>= 1) {
     const unsigned long long o = __shfl_xor(k, off, 64);
     k = o > k ? o : k;
@@ -1181,7 +1182,7 @@ __device__ bool gdn_event(const lxm_params& p, int L, const uint8_t* gt, uint32_
 #endif
   const int no = p.n_blocks - 1 < LXM_OUT_HELPERS ? p.n_blocks - 1 : LXM_OUT_HELPERS;
   const bool ok = wait_stamps(p.sync + (out ? S_XO : S_OWN), out ? no : p.nv, seq & SEQ_MASK,
-                             p.err, 4, &flags[F_STOP]);
+                             p.err, 4);
 #ifdef LXM_SUBPROF
   if (t == 0 && p.prof) {
     uint64_t* evs = reinterpret_cast<uint64_t*>(p.prof) + 32 + 4 * p.n_blocks + SP_EV;
@@ -1441,7 +1442,7 @@ __device__ void run_chain(const lxm_params& pg) {
     if (t < NGRP) st_rlx(p.sync + S_EV + 32 * t, seq << 8);
     {  // every helper's stamped key, then the first maximum
       unsigned long long best = 0;
-      const bool ok = wait_keys(p.sync, (int)nh, seq & KEY_STAMP, p.err, 1, &flags[F_STOP],
+      const bool ok = wait_keys(p.sync, (int)nh, seq & KEY_STAMP, p.err, 1,
                                 reinterpret_cast<unsigned long long*>(flags + F_KEYW), &best);
       if (t == 0) {
         int pred = 0;
@@ -1906,7 +1907,7 @@ __device__ bool out_rows(const lxm_params& p, int ra, int rb, int ne, uint32_t s
         idx[i] = d;
       }
     }
-    if (!wait_words<2>(p.ybuf, idx, seq, p.err, 5, &misc[6], yv)) return false;
+    if (!wait_words<2>(p.ybuf, idx, seq, p.err, 5, yv)) return false;
 #pragma unroll
     for (int i = 0; i < 2; i++)
       if (t + i * NT < ne) oy[t + i * NT] = yv[i];
