@@ -299,16 +299,25 @@ template <bool BF, bool HALF>
 __device__ __forceinline__ v4f hsum(uint8_t* HV, int H, v4f* wsum, bool plus0) {
   const int t = threadIdx.x;
   v4f s = {0.0f, 0.0f, 0.0f, 0.0f};
+  // (every column read before any is summed: a column past H reads the tile's zero column H,
+  // whose +0 squares leave the sum, which starts at +0 and adds squares, unchanged)
+  v4f xs[8];
 #pragma unroll
   for (int half = 0; half < 2; half++)
 #pragma unroll
     for (int i = 0; i < 4; i++) {
       const int c = half * 2048 + 4 * t + i;
-      if (c >= H) continue;
-      v4f x = TV<HALF>::get(HV, c);
+      xs[4 * half + i] = TV<HALF>::get(HV, c < H ? c : H);
+    }
+#pragma unroll
+  for (int half = 0; half < 2; half++)
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      const int c = half * 2048 + 4 * t + i;
+      v4f x = xs[4 * half + i];
       if (plus0) {
         x = v4f{x.x + 0.0f, x.y + 0.0f, x.z + 0.0f, x.w + 0.0f};
-        TV<HALF>::put(HV, c, x);
+        if (c < H) TV<HALF>::put(HV, c, x);
       }
       s = v4f{acc<BF>(s.x, x.x, x.x), acc<BF>(s.y, x.y, x.y), acc<BF>(s.z, x.z, x.z),
               acc<BF>(s.w, x.w, x.w)};
@@ -344,10 +353,14 @@ __device__ __forceinline__ v4f hsum(uint8_t* HV, int H, v4f* wsum, bool plus0) {
 template <bool BF, bool HALF>
 __device__ __forceinline__ void load_tile(const void* h, int64_t b, int H, uint8_t* HV) {
   const int t = threadIdx.x;
+  // (every load is issued, a column past H reading column H - 1 of the same tile, before any
+  // value is looked at: a load under the column's test was waited on inside its branch)
   v4f x[MAXH / NT];
 #pragma unroll
-  for (int k = 0; k < MAXH / NT; k++)
-    x[k] = t + k * NT < H ? ld_col<BF>(h, b, H, t + k * NT) : v4f{0.0f, 0.0f, 0.0f, 0.0f};
+  for (int k = 0; k < MAXH / NT; k++) {
+    const int c = t + k * NT;
+    x[k] = ld_col<BF>(h, b, H, c < H ? c : H - 1);
+  }
 #pragma unroll
   for (int k = 0; k < MAXH / NT; k++)
     if (t + k * NT < H) TV<HALF>::put(HV, t + k * NT, x[k]);
