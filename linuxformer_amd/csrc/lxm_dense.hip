@@ -739,11 +739,12 @@ struct Bar {
 // of the 512-lane order (4t..4t+3, 2048 + 4t..)
 __device__ __forceinline__ void stage_h(const float* h, int n, float* hs) {
   const int t = tid();
-#pragma unroll
-  for (int half = 0; half < 2; half++) {
-    const int c = half * 2048 + 4 * t;
-    if (c < n) *reinterpret_cast<v4f*>(hs + c) = ldf4<true>(h, c);
-  }
+  // (both loads are issued before either value is stored, a column past n reading column 0: a
+  // load under its column test was waited on inside its branch)
+  const int c0 = 4 * t, c1 = 2048 + 4 * t;
+  const v4f a = ldf4<true>(h, c0 < n ? c0 : 0), b = ldf4<true>(h, c1 < n ? c1 : 0);
+  if (c0 < n) *reinterpret_cast<v4f*>(hs + c0) = a;
+  if (c1 < n) *reinterpret_cast<v4f*>(hs + c1) = b;
 }
 
 // A stream wave's weight rows of one phase in flight: round j's row (round_row) in slot j % D.
