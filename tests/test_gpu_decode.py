@@ -240,6 +240,56 @@ def test_short_launch_with_live_windows(cuda):
     check("small", 9, launches=[1, 1, 1, 6], conv0=conv0)
 
 
+def test_window_writer_waves_spanning_two_layers(cuda):
+    """The launch's last conv windows are written by waves whose lanes can hold two layers'
+    channels (the small stack's 6,144 channels over 256 workgroups: 24 a workgroup). Layer 1's
+    first 24 query rows here also read ordinary columns, so their windows differ from what
+    layer 0's ring rows would give: each lane has to read its own layer's rows. The test checks
+    that such a wave exists and that its layer-1 channels hold nonzero windows, then compares
+    the whole run with the oracle bit for bit."""
+    import dataclasses
+
+    from oracle import oracle as ox
+
+    spec, m0, c0, r0 = model("small")
+    d = m0.dims
+    q = m0.layers[1].in_proj_qkv
+    rng = np.random.default_rng(21)
+    have = set(zip(q.rows.tolist(), q.cols.tolist()))
+    rows, cols = [], []
+    for r in range(24):
+        for c in rng.choice(d.hidden - d.n_layers, size=3, replace=False):  # not a gate column
+            if (r, int(c)) not in have:
+                rows.append(r)
+                cols.append(int(c))
+    vals = rng.choice(np.array([0.5, -0.25, 0.75, -1.0], np.float32), size=len(rows))
+    q2 = synth.Coo.build(q.shape, np.concatenate([q.rows, rows]), np.concatenate([q.cols, cols]),
+                         np.concatenate([q.vals, vals]))
+    layers = list(m0.layers)
+    layers[1] = dataclasses.replace(layers[1], in_proj_qkv=q2)
+    m = dataclasses.replace(m0, layers=layers)
+    n = 64
+    print("[gpu-test] window writer across layers: small, n=64", flush=True)
+    cache = fast.StateCache(c0, r0, d.dtype, "cuda")
+    mg = mega.Mega(fast.Fast(m), m, cache, 0)
+    start = [synth.start_token(spec)]
+    preds = mg.run(start, n)
+    om = ox.OracleModel(m)
+    c, r = c0.copy(), r0.copy()
+    po, _, _ = om.decode(c, r, start, n)
+    # a wave whose lane 0 holds a layer-0 channel and whose later lanes hold layer-1 query
+    # channels with nonzero windows (the workgroups' channel ranges as the kernel deals them)
+    per = -(-(d.n_layers * d.n_conv) // mg.ncta)
+    b = d.n_conv // per
+    w0 = b * per + 64 * ((d.n_conv - b * per) // 64)
+    assert w0 < d.n_conv, "no wave spans layers 0 and 1"
+    hi = min(w0 + 64, (b + 1) * per) - d.n_conv
+    assert np.any(c[1, :hi] != 0), "the spanning wave's layer-1 windows are all zero"
+    assert preds == po.tolist()
+    assert (bits(cache.conv_numpy()) == bits(c)).all()
+    assert (bits(cache.rec_numpy()) == bits(r)).all()
+
+
 def test_forced_token_out_of_range(cuda):
     spec, m, c0, r0 = model("small")
     cache = fast.StateCache(c0, r0, m.dims.dtype, "cuda")
