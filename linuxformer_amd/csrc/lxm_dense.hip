@@ -1095,14 +1095,29 @@ __device__ __forceinline__ void run_ctl(const lxm_dn_params* pp, int n_run,
         tok = 0;
       }
       const uint16_t* e = p.embed + (int64_t)tok * c.H;
-      for (int j = tid() & 63; j < c.H / 8; j += 64) {
-        // stored chunk j: entries 8 (j / 64) .. of lane j % 64 (GH >= 8), or entries 8j.. (GH 4)
-        const v4u u = *gp(reinterpret_cast<const v4u*>(e) + j);
-        const int c0 = GH < 8 ? 8 * j : (j % 64) * GH + 8 * (j / 64);
+      // (a round's chunks all requested before any is stored: a load stored in its own
+      // iteration is waited for alone)
+      constexpr int EB = 8;
+      const int ne = c.H / 8;
+      for (int j0 = tid() & 63; j0 < ne; j0 += 64 * EB) {
+        v4u u[EB];
 #pragma unroll
-        for (int i = 0; i < 4; i++) {
-          sm.hs[c0 + 2 * i] = bf16f(u[i] & 0xffffu);
-          sm.hs[c0 + 2 * i + 1] = bf16f(u[i] >> 16);
+        for (int q = 0; q < EB; q++) {
+          const int j = j0 + 64 * q;
+          u[q] = *gp(reinterpret_cast<const v4u*>(e) + (j < ne ? j : j0));
+        }
+#pragma unroll
+        for (int q = 0; q < EB; q++) {
+          // stored chunk j: entries 8 (j / 64) .. of lane j % 64 (GH >= 8), or entries 8j.. (GH 4);
+          // a chunk past the end is chunk j0 again, stored again (unconditional stores keep the
+          // compiler from moving a load into a store's branch)
+          const int j = j0 + 64 * q < ne ? j0 + 64 * q : j0;
+          const int c0 = GH < 8 ? 8 * j : (j % 64) * GH + 8 * (j / 64);
+#pragma unroll
+          for (int i = 0; i < 4; i++) {
+            sm.hs[c0 + 2 * i] = bf16f(u[q][i] & 0xffffu);
+            sm.hs[c0 + 2 * i + 1] = bf16f(u[q][i] >> 16);
+          }
         }
       }
       if (b == 0) {
@@ -1159,10 +1174,26 @@ __device__ __forceinline__ void run_ctl(const lxm_dn_params* pp, int n_run,
       bar.arrive();
       if (!bar.wait()) return;
       dp_phase(sm, 3);
-      // down_proj's input and the residual
-      for (int j = tid() & 63; j < c.I / 8; j += 64)
-        sm.xd[j] = __builtin_bit_cast(v4u, ldf4<true>(reinterpret_cast<const float*>(act16), 4 * j));
+      // down_proj's input and the residual: the residual's loads and each round's chunks all
+      // requested before any is stored (a load stored in its own iteration is waited for alone)
       h.load_coh(p.h, c.H);
+      {
+        constexpr int XB = 9;
+        const int nx = c.I / 8;
+        for (int j0 = tid() & 63; j0 < nx; j0 += 64 * XB) {
+          v4u xr[XB];
+#pragma unroll
+          for (int q = 0; q < XB; q++) {
+            const int j = j0 + 64 * q;
+            xr[q] = __builtin_bit_cast(
+                v4u, ldf4<true>(reinterpret_cast<const float*>(act16), 4 * (j < nx ? j : j0)));
+          }
+          // (a chunk past the end is chunk j0 again, stored again: unconditional stores keep the
+          // compiler from moving a load into a store's branch)
+#pragma unroll
+          for (int q = 0; q < XB; q++) sm.xd[j0 + 64 * q < nx ? j0 + 64 * q : j0] = xr[q];
+        }
+      }
       h.store_lds(sm.hs, c.H);
       lds_barrier();
       dp_x(sm);
