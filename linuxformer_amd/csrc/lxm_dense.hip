@@ -438,12 +438,17 @@ struct GdnLds {
   float qd[KD], kd[KD], qn[KD], kn[KD], vb[QW], dl[QW], bs[16 * QW];
   float misc[4];
 };
-__device__ __forceinline__ float conv_y(uint64_t win, const uint16_t* taps, float P) {
+// (the channel's four bf16 taps as one 8-byte word, tap k in bits 16k.., requested by the caller
+// with the window and the input, so that the three loads are waited for together)
+__device__ __forceinline__ uint64_t taps_of(const uint16_t* taps) {
+  return *gp(reinterpret_cast<const uint64_t*>(taps));
+}
+__device__ __forceinline__ float conv_y(uint64_t win, uint64_t taps, float P) {
   float y = 0.0f;
 #pragma unroll
   for (int k = 0; k < 4; k++) {
     const float x = k < 3 ? bf16f((uint32_t)(win >> (16 * (k + 1))) & 0xffffu) : P;
-    y = __builtin_fmaf(bf16f(taps[k]), x, y);
+    y = __builtin_fmaf(bf16f((uint32_t)(taps >> (16 * k)) & 0xffffu), x, y);
   }
   return silu_bf16(bf16r(y));
 }
@@ -473,10 +478,12 @@ __device__ __forceinline__ void gdn_body(const DnGdn& g, int blk, float (&s)[16]
     float q = 0.0f, k = 0.0f;
     if (t < kl) {
       const int64_t cq = (int64_t)kh * KD + t, ck = (int64_t)nk * KD + kh * KD + t;
-      q = conv_y(ldw<COH>(g.conv + cq * 4), g.conv_qk + ((int64_t)kh * kl + t) * 4,
-                 ldf<COH>(P + kh * kl + t));
-      k = conv_y(ldw<COH>(g.conv + ck * 4), g.conv_qk + ((int64_t)(nk + kh) * kl + t) * 4,
-                 ldf<COH>(P + nq + kh * kl + t));
+      const uint64_t wq = ldw<COH>(g.conv + cq * 4), wk = ldw<COH>(g.conv + ck * 4);
+      const uint64_t tq = taps_of(g.conv_qk + ((int64_t)kh * kl + t) * 4);
+      const uint64_t tk = taps_of(g.conv_qk + ((int64_t)(nk + kh) * kl + t) * 4);
+      const float pq = ldf<COH>(P + kh * kl + t), pk = ldf<COH>(P + nq + kh * kl + t);
+      q = conv_y(wq, tq, pq);
+      k = conv_y(wk, tk, pk);
     }
     l.qd[t] = q;
     l.kd[t] = k;
@@ -487,14 +494,17 @@ __device__ __forceinline__ void gdn_body(const DnGdn& g, int blk, float (&s)[16]
     uint16_t* w = g.conv + (2 * (int64_t)nk * KD + (int64_t)vh * VD + d) * 4;
     const float pv = ldf<COH>(P + 2 * nq + vslot * VD + d);
     const uint64_t win = ldw<COH>(w);
-    l.vb[t - KD] = conv_y(win, g.conv_v + ((int64_t)vslot * VD + d) * 4, pv);
+    const uint64_t tv = taps_of(g.conv_v + ((int64_t)vslot * VD + d) * 4);
+    l.vb[t - KD] = conv_y(win, tv, pv);
     stw<COH>(w, shifted(win, pv));
   }
   if (t == 0) {
+    // (the four loads requested before any is used)
     const float b = ldf<COH>(P + 2 * nq + 2 * nvr + vslot);
     const float a = ldf<COH>(P + 2 * nq + 2 * nvr + nk * rl + vslot);
+    const float al = *gp(g.A_log + vh), dtb = *gp(g.dt_bias + vh);
     l.misc[0] = bf16r(sigmoid(b));
-    l.misc[1] = cr_exp((-cr_exp(g.A_log[vh])) * softplus(a + g.dt_bias[vh]));
+    l.misc[1] = cr_exp((-cr_exp(al)) * softplus(a + dtb));
   }
   lds_barrier();
   // l2norm of the query (wave 0) and key (wave 1) in the model dtype; live: any nonzero
